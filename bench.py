@@ -1,0 +1,203 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X quantized decode hot path (one GPU).
+
+Headline workload: the beam/ragged-batched int8 decode GEMV -- M = 3 packed
+rows (beam width 3), K = 2048, N = 8192, int8 weights with one fp16 scale per
+32-element group, activations quantized per row to int8 (absmax/127).  One
+step = one GEMV launch over one weight matrix; successive steps cycle through
+enough distinct weight copies (>= 300 MB) that the 256 MB Infinity Cache
+cannot hold them, so every step streams its weights from HBM.  The K timed
+steps are replayed as one HIP graph (no host launch overhead in the timed
+region) and timed with HIP events on the stream the kernels run on.
+
+Printed: one JSON line with the metric, a roofline object for the GEMV
+kernel (algorithmic bytes / average launch time vs 8 TB/s) and the CPU
+baseline (the oracle's restatement of the reference CPU MatMulRows, row-
+parallel over NEEDLE_THREADS host threads, on a bounded sample).
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes as C
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+import needle_cs_amd as N  # noqa: E402
+
+HBM_PEAK_GBS = 8000.0
+METRIC = "int8 decode GEMV GB/s (% HBM peak); beam-3 batched decode tokens/sec"
+
+
+def gemv_bytes(m: int, k: int, n: int) -> int:
+    """Algorithmic bytes of one int8/g32 GEMV: weights, fp16 scales, int8
+    activations + fp32 row scales, fp32 outputs."""
+    return n * k + n * (k // 32) * 2 + m * k + m * 4 + m * n * 4
+
+
+class GemvCase:
+    """Device-resident inputs of one GEMV shape: `copies` distinct weight
+    matrices, one activation batch, one output buffer."""
+
+    def __init__(self, m: int, k: int, n: int, seed: int, min_bytes: int = 300 << 20):
+        self.m, self.k, self.n = m, k, n
+        st = C.c_uint64(seed)
+        per = n * k + n * (k // 32) * 2
+        self.copies = max(2, -(-min_bytes // per))
+        self.weights = []
+        for _ in range(self.copies):
+            w = N.synth_int8(st, n * k).reshape(n, k)
+            s = N.synth_half_uniform(st, n * (k // 32), 0.002, 0.02).reshape(n, k // 32)
+            self.weights.append(N.Weights.int8(w, s))
+        self.host_w, self.host_s = w, s  # last copy, reused by the CPU baseline
+        x = N.synth_normal(st, m * k).reshape(m, k)
+        self.x = x
+        dx = N.DeviceBuffer.from_array(x)
+        self.dq = N.DeviceBuffer(m * k)
+        self.ds = N.DeviceBuffer(m * 4)
+        N.check(N.lib().nhip_quantize_rows_dev(dx.ptr, m, k, self.dq.ptr, self.ds.ptr, None))
+        self.dy = N.DeviceBuffer(m * n * 4)
+        self.bytes = gemv_bytes(m, k, n)
+
+    def launch(self, i: int) -> None:
+        w = self.weights[i % self.copies]
+        N.check(N.lib().nhip_matmul_i8_dev(w.handle, self.dq.ptr, self.ds.ptr, self.m, self.dy.ptr, self.n, 0,
+                                           self.n, None))
+
+    def time(self, steps: int, warmup: int) -> float:
+        """Average ms per launch over `steps` launches replayed as one graph."""
+        for i in range(warmup):
+            self.launch(i)
+        N.check(N.lib().nhip_device_sync())
+        with N.Graph.capture() as g:
+            for i in range(steps):
+                self.launch(i)
+        start, stop = N.Event(), N.Event()
+        N.check(N.lib().nhip_device_sync())
+        start.record()
+        g.launch()
+        stop.record()
+        ms = start.elapsed_ms(stop)
+        N.check(N.lib().nhip_device_sync())
+        g.close()
+        return ms / steps
+
+    def close(self) -> None:
+        for w in self.weights:
+            w.close()
+
+
+def physical_cores() -> int:
+    try:
+        import subprocess
+        out = subprocess.run(["lscpu", "-p=CORE,SOCKET"], capture_output=True, text=True).stdout
+        cores = {tuple(line.split(",")) for line in out.splitlines() if line and not line.startswith("#")}
+        return max(1, len(cores))
+    except Exception:
+        return max(1, (os.cpu_count() or 2) // 2)
+
+
+def cpu_baseline(case: GemvCase, budget_s: float) -> dict:
+    """The oracle's MatMulRows restatement (row-parallel as MatMulBatch.RunShard)
+    on the host cores, same shape, bounded to about `budget_s` seconds."""
+    from oracle import oracle as O  # the checker, timed here as the CPU baseline
+
+    threads = int(os.environ.get("NEEDLE_THREADS", "0")) or min(physical_cores(), int(os.environ.get("OMP_NUM_THREADS", "16") or 16))
+    threads = O.lib().or_baseline_start(threads)
+    m, k, n = case.m, case.k, case.n
+    st = C.c_uint64(0xC0FFEE)
+    copies = 4
+    ws = [N.synth_int8(st, n * k).reshape(n, k) for _ in range(copies)]
+    ss = [N.synth_half_uniform(st, n * (k // 32), 0.002, 0.02).reshape(n, k // 32) for _ in range(copies)]
+    q, qs = O.quantize_rows(case.x)
+    y = np.zeros((m, n), dtype=np.float32)
+    times = []
+    t_end = time.perf_counter() + budget_s
+    i = 0
+    while time.perf_counter() < t_end or i < 3:
+        t0 = time.perf_counter()
+        O.lib().or_baseline_matmul_i8(O.p(ws[i % copies]), O.p(ss[i % copies]), n, k, 32, O.p(q), O.p(qs), m,
+                                      O.p(y), n, 0, n)
+        times.append(time.perf_counter() - t0)
+        i += 1
+    O.lib().or_baseline_stop()
+    med = float(np.median(times))
+    return {"value": round(case.bytes / med / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+            "sample": f"{len(times)} GEMVs M={m} K={k} N={n} cycling {copies} weight copies in {sum(times):.1f} s "
+                      f"(median {med * 1e3:.2f} ms/GEMV); oracle restatement of Scalar.MatMulRows, row-parallel "
+                      f"over {threads} threads"}
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=2000)
+    ap.add_argument("--warmup", type=int, default=100)
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-secondary", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (got --gpus {args.gpus}); multi-GPU scaling is not part of this "
+              "build", file=sys.stderr)
+        return 2
+    N.check(N.lib().nhip_init(0))
+    print(f"# {N.lib().nhip_describe().decode()}", file=sys.stderr, flush=True)
+
+    main_case = GemvCase(3, 2048, 8192, seed=0x1001)
+    ms = main_case.time(args.steps, args.warmup)
+    gbs = main_case.bytes / (ms * 1e-3) / 1e9
+    print(f"# headline GEMV M=3 K=2048 N=8192: {ms * 1e3:.2f} us/launch, {gbs:.0f} GB/s", file=sys.stderr, flush=True)
+
+    secondary = []
+    if not args.no_secondary:
+        for (m, k, n) in [(16, 2048, 8192), (3, 2048, 2048), (16, 2048, 2048), (1, 1024, 4096)]:
+            case = GemvCase(m, k, n, seed=0x2000 + m + n)
+            t = case.time(max(200, args.steps // 2), args.warmup)
+            g = case.bytes / (t * 1e-3) / 1e9
+            secondary.append({"workload": f"int8 GEMV M={m} K={k} N={n}", "us_per_launch": round(t * 1e3, 3),
+                              "GB/s": round(g, 1), "frac_hbm_peak": round(g / HBM_PEAK_GBS, 4),
+                              "bytes_per_launch": case.bytes})
+            print(f"# GEMV M={m} K={k} N={n}: {t * 1e3:.2f} us/launch, {g:.0f} GB/s", file=sys.stderr, flush=True)
+            case.close()
+
+    cpu = None
+    if not args.no_cpu:
+        cpu = cpu_baseline(main_case, args.cpu_seconds)
+        print(f"# cpu baseline: {cpu['value']} GB/s on {cpu['cores']} threads", file=sys.stderr, flush=True)
+
+    line = {
+        "metric": METRIC,
+        "value": round(gbs, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 6),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8",
+        "data": "synthetic (seeded XorShift64: int8 U[-127,127] weights, fp16 U(0.002,0.02) group-32 scales, "
+                "N(0,1) activations quantized per row)",
+        "config": {"workload": "beam-batched int8 decode GEMV", "rows_M": 3, "K": 2048, "N": 8192,
+                   "group": 32, "weight_copies_cycled": main_case.copies,
+                   "bytes_per_step": main_case.bytes},
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None},
+        "cpu_baseline": cpu,
+        "secondary": secondary,
+    }
+    main_case.close()
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

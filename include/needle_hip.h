@@ -1,0 +1,227 @@
+/*
+ * needle_hip.h -- C ABI of libneedle_hip.so, the MI355X (gfx950) quantized
+ * decode hot path of needle-cs.
+ *
+ * Two groups of entry points:
+ *
+ *  1. Kernel-table entries.  Same signatures and semantics as the reference's
+ *     cdecl KernelTable slots (src/Needle/Kernels/KernelTable.cs:6-47, filled
+ *     by src/Needle/Kernels/Net10KernelExports.cs:118-150): host pointers,
+ *     synchronous, void (the reference has no error channel), rows outside
+ *     [rowStart,rowEnd) untouched, tokens == 0 or an empty range a no-op.
+ *     Weights are resolved to device-resident copies through a host-pointer ->
+ *     device-pointer cache filled on first use, so a model's weights cross
+ *     PCIe once.  A failure leaves the outputs untouched and sets
+ *     nhip_last_error().
+ *
+ *  2. Device-resident API (the performance path).  Weights are uploaded once
+ *     and stay in HBM; activations, outputs and KV caches are device pointers;
+ *     every call is asynchronous on the given stream (NULL = the library's
+ *     default stream) and returns 0 on success or a negative nhip_status.
+ *
+ * Every struct below matches the reference's C# sequential layout on x86-64
+ * (natural alignment, 8-byte pointers).
+ */
+#ifndef NEEDLE_HIP_H
+#define NEEDLE_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ------------------------------------------------------------ status ---- */
+
+typedef enum nhip_status {
+    NHIP_OK = 0,
+    NHIP_ERR_ARG = -1,      /* invalid argument (shape, range, null pointer) */
+    NHIP_ERR_HIP = -2,      /* a HIP runtime call failed */
+    NHIP_ERR_NODEV = -3,    /* no usable gfx950 device */
+    NHIP_ERR_FORMAT = -4,   /* malformed .cact archive */
+    NHIP_ERR_CAPACITY = -5, /* KV capacity or slot count exceeded */
+    NHIP_ERR_UNSUPPORTED = -6
+} nhip_status;
+
+/* Text of the last error on the calling thread ("" if none). */
+const char* nhip_last_error(void);
+/* Library and device description, e.g. "needle_hip 0.1 gfx950 (256 CUs)". */
+const char* nhip_describe(void);
+
+/* --------------------------------------------- reference struct layouts */
+
+/* src/Needle/Model.cs:36-42 (Codebook: 100 bytes) */
+typedef struct nhip_codebook {
+    float levels[16];
+    uint8_t bytes[32];
+    float byte_scale;
+} nhip_codebook;
+
+/* src/Needle/Model.cs:8-34 (Cq: codebook-quantized weight view, 40 bytes).
+ * indices: rows x (cols*bits/8) bytes; norms: fp16 [rows][cols/128]. */
+typedef struct nhip_cq {
+    const uint8_t* indices;
+    const uint16_t* norms;
+    const nhip_codebook* book;
+    int32_t rows, cols, bits;
+} nhip_cq;
+
+/* src/Needle/Quant.cs:11-28 (Activations, 40 bytes).  values: int8
+ * [tokens][cols] in planes order; scales/offsets: fp32 [tokens][stride],
+ * stride = roundup8(cols/128). */
+typedef struct nhip_activations {
+    int8_t* values;
+    float* scales;
+    float* offsets;
+    int32_t cols, groups, stride;
+} nhip_activations;
+
+/* src/Needle/Blocks.cs:11-27 (AttentionTile, 128 bytes) */
+typedef struct nhip_attn_tile {
+    const int8_t* queries;
+    const float* query_scales;
+    int32_t heads;
+    const int8_t* keys;
+    const float* key_scales;
+    const int8_t* values;
+    const float* value_scales;
+    int32_t key_stride, value_stride, scale_stride, first, count;
+    float* scores;
+    float* output;
+    float* probabilities;
+    int32_t probability_stride;
+    float* peaks;
+    float* sums;
+} nhip_attn_tile;
+
+/* ------------------------------------------------- kernel-table entries */
+
+/* Replaces slot 0, Quant.MatMulRows (src/Needle/Quant.cs:615-633; scalar
+ * semantics src/Needle/Scalar.cs:146-192).  Results are bit-identical to the
+ * reference's scalar kernel. */
+void nhip_matmul_rows(const nhip_cq* w, const nhip_activations* a, int32_t tokens, float* y,
+                      int32_t ldy, int32_t row_start, int32_t row_end);
+
+/* Replaces slot 1, Quant.Prepare (src/Needle/Quant.cs:439-502; scalar branch
+ * Quant.cs:473-488): per 128-group Walsh-Hadamard, int8 quantization,
+ * planes permutation and offsets 63*sum(q). */
+void nhip_prepare(float* x, int32_t tokens, int32_t cols, int32_t bits, const nhip_activations* a);
+
+/* Replaces slot 3, Attention.Run (src/Needle/Blocks.cs:65-84; scalar
+ * src/Needle/Scalar.cs:290-321).  With peaks/sums set, writes the
+ * un-normalised partial (output, peak, sum per head) as the position-split
+ * path expects (Blocks.cs:188-199, 950-958). */
+void nhip_attention_tile(const nhip_attn_tile* tile);
+
+/* Replaces slot 4, Attention.MergePartials (src/Needle/Blocks.cs:750-817). */
+void nhip_merge_partials(const float* partials, int32_t count, int32_t heads, float* output);
+
+/* Replaces slot 22, Quant.QuantizeInt8 (src/Needle/Quant.cs:103-132;
+ * scalar src/Needle/Scalar.cs:67-74).  Returns the scale. */
+float nhip_quantize_int8(const float* x, int32_t n, int8_t* destination);
+
+/* Mirror of Net10KernelExports.Fill (src/Needle/Kernels/Net10KernelExports.cs:118-150):
+ * writes this library's entries into a 27-slot KernelTable (slots 0, 1, 3, 4,
+ * 22; every other slot is set to NULL so the reference falls back to its own
+ * kernels).  Returns NHIP_ERR_ARG if count < 27 or table is NULL. */
+int32_t nhip_fill_kernel_table(void** table, int32_t count);
+
+/* ------------------------------------------------ runtime plumbing ------ */
+
+int32_t nhip_init(int32_t device);
+int32_t nhip_device_count(int32_t* count);
+int32_t nhip_malloc(void** ptr, size_t bytes);
+int32_t nhip_free(void* ptr);
+int32_t nhip_memcpy_htod(void* dst, const void* src, size_t bytes);
+int32_t nhip_memcpy_dtoh(void* dst, const void* src, size_t bytes);
+int32_t nhip_memcpy_dtod(void* dst, const void* src, size_t bytes, void* stream);
+int32_t nhip_memset(void* dst, int32_t value, size_t bytes);
+int32_t nhip_stream_create(void** stream);
+int32_t nhip_stream_destroy(void* stream);
+int32_t nhip_stream_sync(void* stream);
+int32_t nhip_device_sync(void);
+int32_t nhip_event_create(void** event);
+int32_t nhip_event_destroy(void* event);
+int32_t nhip_event_record(void* event, void* stream);
+int32_t nhip_event_elapsed_ms(void* start, void* stop, float* ms);
+
+/* HIP graphs: capture the device-resident calls issued on `stream` between
+ * begin and end into an executable graph, then replay it with one launch.
+ * The library records no memset nodes into captured work. */
+int32_t nhip_graph_begin(void* stream);
+int32_t nhip_graph_end(void* stream, void** graph_exec);
+int32_t nhip_graph_launch(void* graph_exec, void* stream);
+int32_t nhip_graph_destroy(void* graph_exec);
+
+/* --------------------------------------------- device-resident weights */
+
+typedef struct nhip_weights nhip_weights;
+
+/* Literal int8 format: int8 weights [rows][cols] row-major, one fp16 scale
+ * per 32 consecutive elements [rows][cols/32].  cols must be a multiple of
+ * 32.  Uploaded once and re-tiled in HBM for 1 KB coalesced loads. */
+int32_t nhip_weights_i8_create(const int8_t* w, const uint16_t* scales, int32_t rows,
+                               int32_t cols, nhip_weights** out);
+/* Same from device buffers (no host copy; the inputs may be freed after). */
+int32_t nhip_weights_i8_create_dev(const int8_t* d_w, const uint16_t* d_scales, int32_t rows,
+                                   int32_t cols, nhip_weights** out);
+/* Codebook format of .cact (Model.cs:257-267): indices + fp16 norms +
+ * codebook, host pointers, 2- or 4-bit, cols a multiple of 128. */
+int32_t nhip_weights_cq_create(const nhip_cq* w, nhip_weights** out);
+int32_t nhip_weights_destroy(nhip_weights* w);
+/* rows, cols, bits (8 for the literal format), HBM bytes held. */
+int32_t nhip_weights_info(const nhip_weights* w, int32_t* rows, int32_t* cols, int32_t* bits,
+                          size_t* device_bytes);
+
+/* ------------------------------------------------ device-resident ops -- */
+
+/* Per-row dynamic quantization (Scalar.QuantizeInt8 on each row):
+ * x fp32 [tokens][cols] -> q int8 [tokens][cols], scales fp32 [tokens]. */
+int32_t nhip_quantize_rows_dev(const float* d_x, int32_t tokens, int32_t cols, int8_t* d_q,
+                               float* d_scales, void* stream);
+
+/* Quant.Prepare on device (Quant.cs:473-488): x fp32 [tokens][cols] ->
+ * values int8 [tokens][cols] (planes order), scales/offsets fp32
+ * [tokens][stride]. */
+int32_t nhip_prepare_dev(const float* d_x, int32_t tokens, int32_t cols, int32_t bits,
+                         int8_t* d_values, float* d_scales, float* d_offsets, int32_t stride,
+                         void* stream);
+
+/* y[t*ldy+n] = sum_g (h(scale[n][g]) * qscale[t]) * dot_g(w[n], q[t]) for
+ * n in [row_start,row_end), t < tokens, in Scalar.MatMulRows' order
+ * (Scalar.cs:160-189).  Literal int8 weights. */
+int32_t nhip_matmul_i8_dev(const nhip_weights* w, const int8_t* d_q, const float* d_qscale,
+                           int32_t tokens, float* d_y, int32_t ldy, int32_t row_start,
+                           int32_t row_end, void* stream);
+
+/* Scalar.MatMulRows on device for codebook weights (Scalar.cs:146-192):
+ * activations as produced by nhip_prepare_dev. */
+int32_t nhip_matmul_cq_dev(const nhip_weights* w, const int8_t* d_values, const float* d_scales,
+                           const float* d_offsets, int32_t stride, int32_t tokens, float* d_y,
+                           int32_t ldy, int32_t row_start, int32_t row_end, void* stream);
+
+/* The int32 group sums D[t][n-row_start][g] (Scalar.cs:162-184) that the
+ * matmuls accumulate, for checking them bit-exactly.  Literal / codebook. */
+int32_t nhip_group_dots_i8_dev(const nhip_weights* w, const int8_t* d_q, int32_t tokens,
+                               int32_t row_start, int32_t row_end, int32_t* d_dots,
+                               void* stream);
+int32_t nhip_group_dots_cq_dev(const nhip_weights* w, const int8_t* d_values, int32_t tokens,
+                               int32_t row_start, int32_t row_end, int32_t* d_dots,
+                               void* stream);
+
+/* ------------------------------------------ synthetic workload inputs -- */
+
+/* Deterministic host-side generators for the benchmark workloads: one
+ * XorShift64 stream (tests/Needle.Tests/Conformance/Conformance.cs:10-38),
+ * 53-bit uniforms, N(0,1) by Box-Muller, fp16 by round-to-nearest-even.
+ * The state is updated in place. */
+void nhip_synth_normal(uint64_t* state, float* x, size_t n);
+void nhip_synth_uniform(uint64_t* state, float* x, size_t n, float lo, float hi);
+void nhip_synth_int8(uint64_t* state, int8_t* x, size_t n);
+void nhip_synth_half_uniform(uint64_t* state, uint16_t* x, size_t n, float lo, float hi);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,96 @@
+// common.hpp -- shared runtime helpers and exact device arithmetic for
+// libneedle_hip.so (gfx950).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <cstdio>
+#include <string>
+
+#include "../../include/needle_hip.h"
+
+namespace nhip {
+
+// ---------------------------------------------------------------- errors --
+
+void set_error(const char* fmt, ...) __attribute__((format(printf, 1, 2)));
+void clear_error();
+
+#define NHIP_CHECK_HIP(expr)                                                        \
+    do {                                                                            \
+        hipError_t nhip_e_ = (expr);                                                \
+        if (nhip_e_ != hipSuccess) {                                                \
+            ::nhip::set_error("%s failed: %s (%s:%d)", #expr,                       \
+                              hipGetErrorString(nhip_e_), __FILE__, __LINE__);      \
+            return NHIP_ERR_HIP;                                                    \
+        }                                                                           \
+    } while (0)
+
+#define NHIP_REQUIRE(cond, ...)                                                     \
+    do {                                                                            \
+        if (!(cond)) {                                                              \
+            ::nhip::set_error(__VA_ARGS__);                                         \
+            return NHIP_ERR_ARG;                                                    \
+        }                                                                           \
+    } while (0)
+
+// Initialises the device on first use (device 0 unless nhip_init chose one).
+int32_t ensure_device();
+hipStream_t default_stream();
+inline hipStream_t as_stream(void* s) { return s ? static_cast<hipStream_t>(s) : default_stream(); }
+
+// ------------------------------------------------------- device weights --
+
+enum class WeightFormat : int32_t { Int8G32 = 8, Cq2 = 2, Cq4 = 4 };
+
+// HBM-resident weight matrix.  `tiles` holds the weights re-tiled for the
+// matmul kernels: 16-row tiles, each a sequence of 1 KB blocks in which lane
+// l of a wave finds its 16 bytes at l*16 (see gemv.hip for the block map);
+// `norms` holds fp16 scales [rows_pad][groups_pad8].
+struct DeviceWeights {
+    WeightFormat format;
+    int32_t rows, cols, groups;
+    int32_t tiles_n;      // ceil(rows / 16)
+    int32_t blocks;       // 1 KB blocks per tile
+    int32_t groups_pad8;  // scale row stride (halves)
+    uint32_t table[4];    // codebook bytes 0..15 (Cq formats)
+    float byte_scale;     // codebook ByteScale (1 for the literal format)
+    uint8_t* tiles;
+    uint16_t* norms;
+    size_t device_bytes;
+};
+
+}  // namespace nhip
+
+struct nhip_weights : nhip::DeviceWeights {};
+
+namespace nhip {
+
+// ------------------------------------------------ exact device arithmetic --
+
+// Scalar.HalfToSingle (src/Needle/Scalar.cs:121-128): exact binary16 decode,
+// +0 for both zeros, and the reference's integer formula for exponent 31.
+__device__ __forceinline__ float ref_half_to_single(uint32_t half)
+{
+    const uint32_t mag = half & 0x7FFFu;
+    const uint32_t bits = ((mag << 13) + 0x38000000u) | ((half & 0x8000u) << 16);
+    float sub = static_cast<float>(static_cast<int32_t>(mag)) * 5.9604645e-8f;
+    sub = (half & 0x8000u) ? -sub : sub;
+    const float v = mag < 0x0400u ? sub : __uint_as_float(bits);
+    return mag == 0 ? 0.0f : v;
+}
+
+// Scalar.RoundEven (src/Needle/Scalar.cs:51-53).
+__device__ __forceinline__ float ref_round_even(float x)
+{
+    return (x + 12582912.0f) - 12582912.0f;
+}
+
+// MathF.Max for the non-NaN operands used here (+0 preferred over -0).
+__device__ __forceinline__ float ref_max(float a, float b)
+{
+    return a > b ? a : (b > a ? b : (__float_as_uint(a) == 0x80000000u ? b : a));
+}
+
+}  // namespace nhip

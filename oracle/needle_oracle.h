@@ -1,0 +1,192 @@
+/*
+ * needle_oracle.h -- CPU restatement of the needle-cs quantized decode path.
+ *
+ * TEST INFRASTRUCTURE ONLY.  This library is the parity checker for the HIP
+ * path: only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg
+ * may load it.  Nothing in the product (needle_cs_amd/, include/) links or
+ * calls it.
+ *
+ * Every function restates one reference function; the citation is given at
+ * the declaration.  Paths are relative to the reference repository root
+ * (IAFahim/needle-cs).  Where the reference has no counterpart (the literal
+ * int8/group-32 weight format, head dimension 64, the plain decoder used for
+ * the full decode loop), the function says so and names the reference
+ * function it generalises.
+ *
+ * Arithmetic rules: float is IEEE binary32, no contraction (built with
+ * -ffp-contract=off); explicit fmaf() only where the reference uses an FMA
+ * (Fma.MultiplyAdd / MultiplyAddNegated).
+ */
+#ifndef NEEDLE_ORACLE_H
+#define NEEDLE_ORACLE_H
+
+#include <stdint.h>
+#include <stddef.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- reference struct layouts (C# sequential layout == C natural layout) ---- */
+
+/* src/Needle/Model.cs:36-42 */
+typedef struct or_codebook {
+    float levels[16];
+    uint8_t bytes[32];
+    float byte_scale;
+} or_codebook;
+
+/* src/Needle/Model.cs:8-34; GroupSize 128 (Model.cs:10) */
+typedef struct or_cq {
+    const uint8_t* indices;
+    const uint16_t* norms;
+    const or_codebook* book;
+    int rows, cols, bits;
+} or_cq;
+
+/* src/Needle/Quant.cs:11-28 */
+typedef struct or_activations {
+    int8_t* values;
+    float* scales;
+    float* offsets;
+    int cols, groups, stride;
+} or_activations;
+
+/* src/Needle/Blocks.cs:11-27 */
+typedef struct or_attention_tile {
+    const int8_t* queries;
+    const float* query_scales;
+    int heads;
+    const int8_t* keys;
+    const float* key_scales;
+    const int8_t* values;
+    const float* value_scales;
+    int key_stride, value_stride, scale_stride, first, count;
+    float* scores;
+    float* output;
+    float* probabilities;
+    int probability_stride;
+    float* peaks;
+    float* sums;
+} or_attention_tile;
+
+/* ---- generators ---- */
+
+/* tests/Needle.Tests/Conformance/Conformance.cs:10-38 (XorShift64) */
+uint64_t or_xs_seed(uint64_t seed);
+uint64_t or_xs_next(uint64_t* state);
+int or_xs_next_int(uint64_t* state, int lo, int hi);
+float or_xs_next_float(uint64_t* state, float scale);
+/* tests/Needle.Tests/Conformance/Conformance.cs:42-68 */
+void or_fill_uniform(float* x, int n, uint64_t* state, float scale);
+void or_fill_edges(float* x, int n, uint64_t* state, float scale);
+/* tests/Needle.Tests/Conformance/Conformance.cs:70-101 */
+void or_fill_sbyte(int8_t* x, int n, uint64_t* state, int extremes);
+void or_fill_bytes(uint8_t* x, int n, uint64_t* state, int extremes);
+/* tests/Needle.Tests/Conformance/Conformance.cs:103-118 */
+uint16_t or_half_bits(float value);
+
+/* Synthetic workload distributions (no reference counterpart; the workload
+ * definition of the decode benchmarks): one XorShift64 stream, 53-bit
+ * uniforms u = (next >> 11) * 2^-53, N(0,1) by Box-Muller on (1-u1, u2),
+ * U(a,b) = a + (b-a)*u, int8 U[-127,127] = NextInt(-127,128), fp16 by RNE. */
+double or_synth_u53(uint64_t* state);
+void or_synth_normal(float* x, size_t n, uint64_t* state);
+void or_synth_uniform(float* x, size_t n, uint64_t* state, float lo, float hi);
+void or_synth_int8(int8_t* x, size_t n, uint64_t* state);
+void or_synth_half_uniform(uint16_t* x, size_t n, uint64_t* state, float lo, float hi);
+uint16_t or_single_to_half_rne(float f);
+
+/* ---- scalar kernels ---- */
+
+/* src/Needle/Scalar.cs:121-128 */
+float or_half_to_single(uint16_t half);
+/* src/Needle/Scalar.cs:113-119 */
+float or_half_to_single_upstream(uint16_t half);
+/* src/Needle/Model.cs:44-52 */
+void or_codebook_fill(or_codebook* book, const float* levels, int count);
+/* src/Needle/Scalar.cs:76-89 (128-element Walsh-Hadamard) */
+void or_hadamard(const float* source, float* p);
+/* src/Needle/Scalar.cs:55-60 */
+float or_abs_max(const float* x, int n);
+/* src/Needle/Scalar.cs:62-65 */
+void or_round_trip(float* x, int n, float inverse, float scale);
+/* src/Needle/Scalar.cs:67-74 */
+float or_quantize_int8(const float* x, int n, int8_t* destination);
+/* src/Needle/Scalar.cs:91-111 */
+void or_planes(const int8_t* quantized, int bits, int8_t* destination, int* sum);
+/* src/Needle/Quant.cs:473-488 (scalar branch of PrepareRange) */
+void or_prepare(const float* x, int tokens, int cols, int bits, const or_activations* a);
+/* src/Needle/Scalar.cs:130-144 */
+void or_decode_row(const or_cq* w, int row, float* destination);
+/* src/Needle/Scalar.cs:146-192 */
+void or_matmul_rows(const or_cq* w, const or_activations* a, int tokens, float* y, int ldy,
+                    int row_start, int row_end);
+/* Int32 group sums D[t][n][g] of Scalar.cs:162-184 (the accumulators the
+ * parity bar requires bit-exact), for rows [row_start,row_end). */
+void or_group_dots_cq(const or_cq* w, const or_activations* a, int tokens, int row_start,
+                      int row_end, int32_t* dots);
+
+/* Literal int8 format: int8 weights [rows][cols], one fp16 scale per
+ * `group` elements [rows][cols/group], activations quantized per row by
+ * or_quantize_int8 (one scale per token).  No reference counterpart: this is
+ * Scalar.MatMulRows (Scalar.cs:146-192) with the codebook replaced by the
+ * identity (Bytes[i] = i, ByteScale = 1), Cq.GroupSize = `group`, every
+ * group's activation scale equal to the row scale and zero offsets.  The
+ * epilogue keeps Scalar.cs:185-189's exact order. */
+void or_matmul_rows_i8(const int8_t* w, const uint16_t* scales, int rows, int cols, int group,
+                       const int8_t* q, const float* qscale, int tokens, float* y, int ldy,
+                       int row_start, int row_end);
+void or_group_dots_i8(const int8_t* w, int rows, int cols, int group, const int8_t* q,
+                      int tokens, int row_start, int row_end, int32_t* dots);
+/* Per-row activation quantization of the literal path: or_quantize_int8 over
+ * each of `tokens` rows of `cols` floats. */
+void or_quantize_rows(const float* x, int tokens, int cols, int8_t* q, float* scales);
+
+/* ---- softmax / exp / attention ---- */
+
+/* src/Needle/Ops.cs:16-31, one lane of the AVX polynomial exp. */
+float or_exp_poly(float x);
+/* src/Needle/Scalar.cs:220-231; use_poly selects or_exp_poly instead of
+ * libm expf (MathF.Exp). */
+void or_softmax(float* s, int n, int use_poly);
+/* src/Needle/Scalar.cs:290-312, generalised to qk_dim in {48, 64} and
+ * v_dim 64 (the reference hard-codes 48; Blocks.cs:45-46).  The score scale
+ * is 1/sqrt(qk_dim) rounded to float (0.14433756729740643f for 48, as
+ * Scalar.cs:50). */
+void or_attention_head(const int8_t* query, float query_scale, const int8_t* keys,
+                       const float* key_scales, const int8_t* values, const float* value_scales,
+                       int key_stride, int value_stride, int scale_stride, int first, int last,
+                       float* scores, float* output, float* probabilities, int qk_dim,
+                       int use_poly);
+/* One head's position-split partial: the un-normalised output
+ * sum_s (e_s * valueScale_s) * v_s with e_s = exp(score_s - peak), plus the
+ * peak and sum_s e_s (src/Needle/Blocks.cs:188-199 with Peaks set and
+ * ValuesFloat, Blocks.cs:415-435, restated with scalar operations). */
+void or_attention_partial(const int8_t* query, float query_scale, const int8_t* keys,
+                          const float* key_scales, const int8_t* values, const float* value_scales,
+                          int key_stride, int value_stride, int scale_stride, int first, int count,
+                          int qk_dim, int use_poly, float* output, float* peak, float* sum);
+/* src/Needle/Scalar.cs:314-321 */
+void or_attention_tile_run(const or_attention_tile* tile, int use_poly);
+/* src/Needle/Blocks.cs:750-817, the non-SIMD branch (count == 2 special
+ * case included).  Partial layout: PartialFloats = 6*64+16 floats per chunk,
+ * out [6][64], peaks at +384, sums at +392 (Blocks.cs:42-43,956-957). */
+void or_merge_partials(const float* partials, int count, int heads, float* output,
+                       int use_poly);
+/* tests/Needle.Tests/Conformance/KernelConformanceTests.cs:498-525 (double
+ * reference). */
+void or_merge_partials_double(const float* partials, int count, int heads, float* output);
+/* src/Needle/Blocks.cs:973-978 */
+void or_attention_span(int position, int window, int frames, int* first, int* count);
+
+/* src/Needle/Ops.cs:1086-1089 (first index of the maximum) */
+int or_argmax(const float* x, int n);
+/* src/Needle/Ops.cs:1092-1221, scalar branch (the double log-sum-exp) */
+void or_topk_log_softmax(const float* x, int n, int k, int* indices, float* log_probs,
+                         float* probs, int mask_special_023);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

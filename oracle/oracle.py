@@ -1,0 +1,194 @@
+"""ctypes binding of the oracle (libneedle_oracle.so).
+
+TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and
+bench.py's cpu_baseline leg, never by the product (needle_cs_amd/).
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "_build", "libneedle_oracle.so")
+
+
+class Codebook(C.Structure):
+    _fields_ = [("levels", C.c_float * 16), ("bytes", C.c_uint8 * 32), ("byte_scale", C.c_float)]
+
+
+class Cq(C.Structure):
+    _fields_ = [("indices", C.c_void_p), ("norms", C.c_void_p), ("book", C.POINTER(Codebook)),
+                ("rows", C.c_int), ("cols", C.c_int), ("bits", C.c_int)]
+
+
+class Activations(C.Structure):
+    _fields_ = [("values", C.c_void_p), ("scales", C.c_void_p), ("offsets", C.c_void_p),
+                ("cols", C.c_int), ("groups", C.c_int), ("stride", C.c_int)]
+
+
+class AttnTile(C.Structure):
+    _fields_ = [("queries", C.c_void_p), ("query_scales", C.c_void_p), ("heads", C.c_int),
+                ("keys", C.c_void_p), ("key_scales", C.c_void_p), ("values", C.c_void_p),
+                ("value_scales", C.c_void_p), ("key_stride", C.c_int), ("value_stride", C.c_int),
+                ("scale_stride", C.c_int), ("first", C.c_int), ("count", C.c_int),
+                ("scores", C.c_void_p), ("output", C.c_void_p), ("probabilities", C.c_void_p),
+                ("probability_stride", C.c_int), ("peaks", C.c_void_p), ("sums", C.c_void_p)]
+
+
+_u64p, _vp, _i, _f, _sz = C.POINTER(C.c_uint64), C.c_void_p, C.c_int, C.c_float, C.c_size_t
+_PROTOS = {
+    "or_xs_seed": (C.c_uint64, [C.c_uint64]),
+    "or_xs_next": (C.c_uint64, [_u64p]),
+    "or_xs_next_int": (_i, [_u64p, _i, _i]),
+    "or_xs_next_float": (_f, [_u64p, _f]),
+    "or_fill_uniform": (None, [_vp, _i, _u64p, _f]),
+    "or_fill_edges": (None, [_vp, _i, _u64p, _f]),
+    "or_fill_sbyte": (None, [_vp, _i, _u64p, _i]),
+    "or_fill_bytes": (None, [_vp, _i, _u64p, _i]),
+    "or_half_bits": (C.c_uint16, [_f]),
+    "or_synth_u53": (C.c_double, [_u64p]),
+    "or_synth_normal": (None, [_vp, _sz, _u64p]),
+    "or_synth_uniform": (None, [_vp, _sz, _u64p, _f, _f]),
+    "or_synth_int8": (None, [_vp, _sz, _u64p]),
+    "or_synth_half_uniform": (None, [_vp, _sz, _u64p, _f, _f]),
+    "or_single_to_half_rne": (C.c_uint16, [_f]),
+    "or_half_to_single": (_f, [C.c_uint16]),
+    "or_half_to_single_upstream": (_f, [C.c_uint16]),
+    "or_codebook_fill": (None, [C.POINTER(Codebook), _vp, _i]),
+    "or_hadamard": (None, [_vp, _vp]),
+    "or_abs_max": (_f, [_vp, _i]),
+    "or_round_trip": (None, [_vp, _i, _f, _f]),
+    "or_quantize_int8": (_f, [_vp, _i, _vp]),
+    "or_planes": (None, [_vp, _i, _vp, C.POINTER(_i)]),
+    "or_prepare": (None, [_vp, _i, _i, _i, C.POINTER(Activations)]),
+    "or_decode_row": (None, [C.POINTER(Cq), _i, _vp]),
+    "or_matmul_rows": (None, [C.POINTER(Cq), C.POINTER(Activations), _i, _vp, _i, _i, _i]),
+    "or_group_dots_cq": (None, [C.POINTER(Cq), C.POINTER(Activations), _i, _i, _i, _vp]),
+    "or_matmul_rows_i8": (None, [_vp, _vp, _i, _i, _i, _vp, _vp, _i, _vp, _i, _i, _i]),
+    "or_group_dots_i8": (None, [_vp, _i, _i, _i, _vp, _i, _i, _i, _vp]),
+    "or_quantize_rows": (None, [_vp, _i, _i, _vp, _vp]),
+    "or_exp_poly": (_f, [_f]),
+    "or_softmax": (None, [_vp, _i, _i]),
+    "or_attention_head": (None, [_vp, _f, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _vp, _vp, _vp, _i, _i]),
+    "or_attention_tile_run": (None, [C.POINTER(AttnTile), _i]),
+    "or_attention_partial": (None, [_vp, _f, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _i, _vp,
+                                    C.POINTER(_f), C.POINTER(_f)]),
+    "or_merge_partials": (None, [_vp, _i, _i, _vp, _i]),
+    "or_merge_partials_double": (None, [_vp, _i, _i, _vp]),
+    "or_attention_span": (None, [_i, _i, _i, C.POINTER(_i), C.POINTER(_i)]),
+    "or_argmax": (_i, [_vp, _i]),
+    "or_topk_log_softmax": (None, [_vp, _i, _i, _vp, _vp, _vp, _i]),
+    "or_baseline_start": (_i, [_i]),
+    "or_baseline_stop": (None, []),
+    "or_baseline_matmul_i8": (None, [_vp, _vp, _i, _i, _i, _vp, _vp, _i, _vp, _i, _i, _i]),
+}
+
+_LIB = None
+
+
+def lib() -> C.CDLL:
+    global _LIB
+    if _LIB is None:
+        if not os.path.exists(LIB_PATH):
+            from . import build as _build  # noqa: F401  (package-relative when imported as oracle.oracle)
+            _build.build()
+        handle = C.CDLL(LIB_PATH)
+        for name, (res, args) in _PROTOS.items():
+            fn = getattr(handle, name)
+            fn.restype = res
+            fn.argtypes = args
+        _LIB = handle
+    return _LIB
+
+
+def p(a: np.ndarray) -> int:
+    assert a.flags["C_CONTIGUOUS"]
+    return a.ctypes.data
+
+
+def state(seed: int) -> C.c_uint64:
+    return C.c_uint64(lib().or_xs_seed(seed))
+
+
+# ------------------------------------------------------------- helpers --
+
+def codebook(levels: np.ndarray, count: int) -> Codebook:
+    book = Codebook()
+    lv = np.zeros(16, dtype=np.float32)
+    lv[:count] = levels[:count]
+    lib().or_codebook_fill(C.byref(book), p(lv), count)
+    return book
+
+
+def activations(tokens: int, cols: int):
+    """Host buffers laid out as Quant.cs:33-41 (Activations(ref Arena, ...))."""
+    groups = cols // 128
+    stride = (groups + 7) & ~7
+    values = np.zeros(tokens * cols, dtype=np.int8)
+    scales = np.zeros(tokens * stride, dtype=np.float32)
+    offsets = np.zeros(tokens * stride, dtype=np.float32)
+    act = Activations(p(values), p(scales), p(offsets), cols, groups, stride)
+    return act, values, scales, offsets
+
+
+def prepare(x: np.ndarray, tokens: int, cols: int, bits: int):
+    act, values, scales, offsets = activations(tokens, cols)
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    lib().or_prepare(p(x), tokens, cols, bits, C.byref(act))
+    return act, values, scales, offsets
+
+
+def matmul_rows(cq: Cq, act: Activations, tokens: int, y: np.ndarray, ldy: int, r0: int, r1: int) -> None:
+    lib().or_matmul_rows(C.byref(cq), C.byref(act), tokens, p(y), ldy, r0, r1)
+
+
+def matmul_rows_i8(w, scales, q, qscale, tokens, y, ldy, r0, r1, group=32):
+    rows, cols = w.shape
+    lib().or_matmul_rows_i8(p(w), p(scales), rows, cols, group, p(q), p(qscale), tokens, p(y), ldy, r0, r1)
+
+
+def group_dots_i8(w, q, tokens, r0, r1, group=32):
+    rows, cols = w.shape
+    out = np.zeros((tokens, r1 - r0, cols // group), dtype=np.int32)
+    lib().or_group_dots_i8(p(w), rows, cols, group, p(q), tokens, r0, r1, p(out))
+    return out
+
+
+def group_dots_cq(cq: Cq, act: Activations, tokens: int, r0: int, r1: int):
+    out = np.zeros((tokens, r1 - r0, cq.cols // 128), dtype=np.int32)
+    lib().or_group_dots_cq(C.byref(cq), C.byref(act), tokens, r0, r1, p(out))
+    return out
+
+
+def quantize_rows(x: np.ndarray):
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    tokens, cols = x.shape
+    q = np.zeros((tokens, cols), dtype=np.int8)
+    s = np.zeros(tokens, dtype=np.float32)
+    lib().or_quantize_rows(p(x), tokens, cols, p(q), p(s))
+    return q, s
+
+
+def synth_normal(st: C.c_uint64, n: int) -> np.ndarray:
+    out = np.empty(n, dtype=np.float32)
+    lib().or_synth_normal(p(out), n, C.byref(st))
+    return out
+
+
+def synth_int8(st: C.c_uint64, n: int) -> np.ndarray:
+    out = np.empty(n, dtype=np.int8)
+    lib().or_synth_int8(p(out), n, C.byref(st))
+    return out
+
+
+def synth_half_uniform(st: C.c_uint64, n: int, lo: float, hi: float) -> np.ndarray:
+    out = np.empty(n, dtype=np.uint16)
+    lib().or_synth_half_uniform(p(out), n, C.byref(st), lo, hi)
+    return out
+
+
+def half_to_single_array(h: np.ndarray) -> np.ndarray:
+    f = lib().or_half_to_single
+    return np.array([f(int(v)) for v in h.ravel()], dtype=np.float32).reshape(h.shape)
