@@ -88,6 +88,8 @@ struct MatmulParams {
     int32_t* dots;
     int32_t tokens, cols, groups, blocks, groups_pad8, stride, ldy;
     int32_t row_start, row_end, tile_begin, tile_end;
+    int32_t gph;              // groups per phase (a multiple of Traits::GPB)
+    int32_t d_bytes;          // LDS bytes of the D buffer of one phase
     uint32_t t0, t1, t2, t3;  // codebook bytes 0..15
     float byte_scale;
 };
@@ -107,29 +109,62 @@ __device__ __forceinline__ uint32_t lut4(uint32_t idx, uint32_t t0, uint32_t t1,
     return (hi & mask) | (lo & ~mask);
 }
 
-// D_g for the group `h` (0/1) of the loaded block `w`.
+// The MFMA A operand(s) one lane supplies for one group: activation bytes of
+// token lane%16 at act_pos(slot, lane/16) inside the group.
 template <int F>
-__device__ __forceinline__ v4i group_dot(const u4& w, int h, const uint8_t* lds, int g, int lane,
-                                         const MatmulParams& p)
+struct Operand;
+template <>
+struct Operand<kI8> {
+    long a;
+};
+template <>
+struct Operand<kCq2> {
+    long a[4];
+};
+template <>
+struct Operand<kCq4> {
+    v4i a[2];
+};
+
+template <int F>
+__device__ __forceinline__ Operand<F> load_operand(const int8_t* qrow, int g, int kq)
+{
+    using T = Traits<F>;
+    Operand<F> o;
+    const int8_t* base = qrow + (size_t)g * T::GS;
+    if constexpr (F == kI8) {
+        o.a = qrow ? *reinterpret_cast<const long*>(base + act_pos<F>(0, kq)) : 0;
+    } else if constexpr (F == kCq2) {
+#pragma unroll
+        for (int s = 0; s < 4; s++) o.a[s] = qrow ? *reinterpret_cast<const long*>(base + act_pos<F>(s, kq)) : 0;
+    } else {
+#pragma unroll
+        for (int s = 0; s < 2; s++) {
+            const v4i zero = {0, 0, 0, 0};
+            o.a[s] = qrow ? *reinterpret_cast<const v4i*>(base + act_pos<F>(s, kq)) : zero;
+        }
+    }
+    return o;
+}
+
+// D_g for group `h` (0/1) of the loaded weight block `w`.
+template <int F>
+__device__ __forceinline__ v4i group_dot(const u4& w, int h, const Operand<F>& a, const MatmulParams& p)
 {
     v4i d = {0, 0, 0, 0};
     if constexpr (F == kI8) {
-        const long a = reinterpret_cast<const long*>(lds)[g * 64 + lane];
         const long b = h ? (long)(((uint64_t)w.w << 32) | w.z) : (long)(((uint64_t)w.y << 32) | w.x);
-        d = __builtin_amdgcn_mfma_i32_16x16x32_i8(a, b, d, 0, 0, 0);
+        d = __builtin_amdgcn_mfma_i32_16x16x32_i8(a.a, b, d, 0, 0, 0);
     } else if constexpr (F == kCq2) {
         const uint32_t x0 = h ? w.z : w.x;
         const uint32_t x1 = h ? w.w : w.y;
-        const long* la = reinterpret_cast<const long*>(lds) + (size_t)g * 4 * 64 + lane;
 #pragma unroll
         for (int pl = 0; pl < 4; pl++) {
             const uint32_t b0 = lut2((x0 >> (2 * pl)) & 0x03030303u, p.t0);
             const uint32_t b1 = lut2((x1 >> (2 * pl)) & 0x03030303u, p.t0);
-            const long b = (long)(((uint64_t)b1 << 32) | b0);
-            d = __builtin_amdgcn_mfma_i32_16x16x32_i8(la[pl * 64], b, d, 0, 0, 0);
+            d = __builtin_amdgcn_mfma_i32_16x16x32_i8(a.a[pl], (long)(((uint64_t)b1 << 32) | b0), d, 0, 0, 0);
         }
     } else {
-        const v4i* la = reinterpret_cast<const v4i*>(lds) + (size_t)g * 2 * 64 + lane;
 #pragma unroll
         for (int s = 0; s < 2; s++) {
             const int sh = 4 * s;
@@ -138,175 +173,166 @@ __device__ __forceinline__ v4i group_dot(const u4& w, int h, const uint8_t* lds,
             b.y = (int)lut4((w.y >> sh) & 0x0F0F0F0Fu, p.t0, p.t1, p.t2, p.t3);
             b.z = (int)lut4((w.z >> sh) & 0x0F0F0F0Fu, p.t0, p.t1, p.t2, p.t3);
             b.w = (int)lut4((w.w >> sh) & 0x0F0F0F0Fu, p.t0, p.t1, p.t2, p.t3);
-            d = __builtin_amdgcn_mfma_i32_16x16x64_i8(la[s * 64], b, d, 0, 0, 0);
+            d = __builtin_amdgcn_mfma_i32_16x16x64_i8(a.a[s], b, d, 0, 0, 0);
         }
     }
     return d;
 }
 
-// One wave per 16-row tile, 2 waves per block, blockIdx.y = 16-token block.
-// TI = token slots per lane (min(4, tokens)); CB = 1 KB blocks loaded per
-// chunk (all of a tile's blocks when K is small enough).
-template <int F, int TI, int CB, bool DOTS>
-__global__ __launch_bounds__(kThreads) void matmul_kernel(MatmulParams p)
+// One block per (16-row tile, 16-token block); S = blockDim.x/64 waves split
+// the tile's weight blocks.  Per phase of `gph` groups:
+//  1. group dots: every wave loads its share of activation operands (first)
+//     and 1 KB weight blocks (all in flight together), runs one MFMA chain per
+//     group and writes the int32 D_g of the valid tokens to LDS [g][t][row];
+//     the fp16 scales of its groups are decoded (Scalar.HalfToSingle) to LDS;
+//  2. epilogue: thread c owns the (token c/16, row c%16) accumulator and
+//     walks the phase's groups in ascending order:
+//         scaled = (hs * ByteScale) * scale[t][g]; acc += scaled * D_g;
+//         bias += scaled * offset[t][g]           (Cq formats)
+//         scaled = hs * scale[t];  acc += scaled * D_g          (int8)
+//     which is Scalar.MatMulRows' exact operation order (Scalar.cs:185-189);
+//     phases continue the same accumulators, so the order spans all of K.
+template <int F, int CB, bool DOTS>
+__global__ __launch_bounds__(512) void matmul_kernel(MatmulParams p)
 {
     using T = Traits<F>;
     extern __shared__ __align__(16) uint8_t lds[];
+    int32_t* dl = reinterpret_cast<int32_t*>(lds);
+    float* hl = reinterpret_cast<float*>(lds + p.d_bytes);
+    const int S = blockDim.x >> 6;
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
-    const int tile = p.tile_begin + blockIdx.x * kWavesPerBlock + wave;
+    const int tile = p.tile_begin + blockIdx.x;
     const int tb = blockIdx.y * 16;
-    const int ntok = min(16, p.tokens - tb);
+    const int M = min(16, p.tokens - tb);
     const int G = p.groups;
-
-    // Stage activations in per-lane operand order: entry e = (g, slot, lane).
-    {
-        const int entries = G * T::SLOTS * 64;
-        for (int e = threadIdx.x; e < entries; e += kThreads) {
-            const int g = e / (T::SLOTS * 64);
-            const int r = e - g * (T::SLOTS * 64);
-            const int slot = r >> 6;
-            const int el = r & 63;
-            const int t = el & 15;
-            const int kq = el >> 4;
-            const int8_t* src = p.q + (size_t)(tb + t) * p.cols + g * T::GS + act_pos<F>(slot, kq);
-            if constexpr (T::SLOT_BYTES == 8) {
-                uint2 v = make_uint2(0, 0);
-                if (t < ntok) v = *reinterpret_cast<const uint2*>(src);
-                reinterpret_cast<uint2*>(lds)[e] = v;
-            } else {
-                uint4 v = make_uint4(0, 0, 0, 0);
-                if (t < ntok) v = *reinterpret_cast<const uint4*>(src);
-                reinterpret_cast<uint4*>(lds)[e] = v;
-            }
-        }
-    }
-    float* sc_lds = reinterpret_cast<float*>(lds + (size_t)G * T::SLOTS * 64 * T::SLOT_BYTES);
-    float* off_lds = sc_lds + 16 * G;
-    if constexpr (F != kI8 && !DOTS) {
-        for (int e = threadIdx.x; e < 16 * G; e += kThreads) {
-            const int t = e / G;
-            const int g = e - t * G;
-            const bool ok = t < ntok;
-            sc_lds[e] = ok ? p.qscale[(size_t)(tb + t) * p.stride + g] : 0.0f;
-            off_lds[e] = ok ? p.offsets[(size_t)(tb + t) * p.stride + g] : 0.0f;
-        }
-    }
-    __syncthreads();
-    if (tile >= p.tile_end) return;
-
     const int r = lane & 15;
     const int kq = lane >> 4;
     const int n = tile * 16 + r;
-
-    float qs[TI];
-    float acc[TI];
-    float bias[TI];
-#pragma unroll
-    for (int i = 0; i < TI; i++) {
-        const int t = 4 * kq + i;
-        if constexpr (F == kI8 && !DOTS) qs[i] = t < ntok ? p.qscale[tb + t] : 0.0f;
-        acc[i] = 0.0f;
-        bias[i] = 0.0f;
-    }
-
+    const int8_t* qrow = r < M ? p.q + (size_t)(tb + r) * p.cols : nullptr;  // A operand token = lane % 16
     const u4* wbase = reinterpret_cast<const u4*>(p.tiles) + (size_t)tile * p.blocks * 64 + lane;
     const uint16_t* nrow = p.norms + (size_t)n * p.groups_pad8;
-    constexpr int GPC = CB * T::GPB;  // groups per chunk (multiple of 8)
 
-    for (int b0 = 0; b0 < p.blocks; b0 += CB) {
+    // epilogue ownership
+    const int ct = threadIdx.x >> 4;
+    const int cr = threadIdx.x & 15;
+    const bool chain = !DOTS && ct < M;
+    float acc = 0.0f, bias = 0.0f, qs = 0.0f;
+    if constexpr (F == kI8 && !DOTS)
+        if (chain) qs = p.qscale[tb + ct];
+
+    for (int p0 = 0; p0 < G; p0 += p.gph) {
+        const int gend = min(G, p0 + p.gph);
+        const int b_begin = p0 / T::GPB;
+        const int b_end = (gend + T::GPB - 1) / T::GPB;
+        const int per = (b_end - b_begin + S - 1) / S;
+        const int mb0 = b_begin + wave * per;
+        const int mb1 = min(b_end, mb0 + per);
+        const int g_first = mb0 * T::GPB;
+        const int g_last = min(gend, mb1 * T::GPB);  // exclusive
+
+        Operand<F> ops[CB * T::GPB];
+#pragma unroll
+        for (int c = 0; c < CB; c++)
+#pragma unroll
+            for (int h = 0; h < T::GPB; h++) {
+                const int g = (mb0 + c) * T::GPB + h;
+                if (g < g_last) ops[c * T::GPB + h] = load_operand<F>(qrow, g, kq);
+            }
         u4 w[CB];
 #pragma unroll
         for (int c = 0; c < CB; c++)
-            if (b0 + c < p.blocks) w[c] = __builtin_nontemporal_load(wbase + (size_t)(b0 + c) * 64);
-        const int g0 = b0 * T::GPB;
-        uint4 sv[GPC / 8];
+            if (mb0 + c < mb1) w[c] = __builtin_nontemporal_load(wbase + (size_t)(mb0 + c) * 64);
+        // this lane decodes the scales of groups g_first + 4j + kq
+        constexpr int HJ = (CB * T::GPB + 3) / 4;
+        uint16_t hraw[HJ];
+        if constexpr (!DOTS) {
 #pragma unroll
-        for (int j = 0; j < GPC / 8; j++)
-            if (g0 + 8 * j < p.groups_pad8) sv[j] = *reinterpret_cast<const uint4*>(nrow + g0 + 8 * j);
+            for (int j = 0; j < HJ; j++) {
+                const int g = g_first + 4 * j + kq;
+                hraw[j] = g < g_last ? nrow[g] : (uint16_t)0;
+            }
+        }
 #pragma unroll
         for (int c = 0; c < CB; c++) {
+            if (mb0 + c >= mb1) break;
 #pragma unroll
             for (int h = 0; h < T::GPB; h++) {
-                const int gl = c * T::GPB + h;  // group within chunk
-                const int g = g0 + gl;
-                if (g >= G) break;
-                const v4i d = group_dot<F>(w[c], h, lds, g, lane, p);
-                if constexpr (DOTS) {
+                const int g = (mb0 + c) * T::GPB + h;
+                if (g >= g_last) break;
+                const v4i d = group_dot<F>(w[c], h, ops[c * T::GPB + h], p);
 #pragma unroll
-                    for (int i = 0; i < TI; i++) {
-                        const int t = 4 * kq + i;
-                        if (t < ntok && n >= p.row_start && n < p.row_end)
-                            p.dots[((size_t)(tb + t) * (p.row_end - p.row_start) + (n - p.row_start)) * G + g] = d[i];
-                    }
-                } else {
-                    const uint4 s4 = sv[gl >> 3];
-                    const uint32_t word = ((gl & 7) < 4) ? (((gl & 7) < 2) ? s4.x : s4.y) : (((gl & 7) < 6) ? s4.z : s4.w);
-                    const float hs = ref_half_to_single((gl & 1) ? (word >> 16) : (word & 0xFFFFu));
-#pragma unroll
-                    for (int i = 0; i < TI; i++) {
-                        if constexpr (F == kI8) {
-                            const float scaled = hs * qs[i];
-                            acc[i] = acc[i] + scaled * static_cast<float>(d[i]);
+                for (int i = 0; i < 4; i++) {
+                    const int t = 4 * kq + i;
+                    if (t < M) {
+                        if constexpr (DOTS) {
+                            if (n >= p.row_start && n < p.row_end)
+                                p.dots[((size_t)(tb + t) * (p.row_end - p.row_start) + (n - p.row_start)) * G + g] =
+                                    d[i];
                         } else {
-                            const int t = 4 * kq + i;
-                            const float scaled = (hs * p.byte_scale) * sc_lds[t * G + g];
-                            acc[i] = acc[i] + scaled * static_cast<float>(d[i]);
-                            bias[i] = bias[i] + scaled * off_lds[t * G + g];
+                            dl[((g - p0) * M + t) * 16 + r] = d[i];
                         }
                     }
                 }
             }
         }
-    }
-    if constexpr (!DOTS) {
-        if (n >= p.row_start && n < p.row_end) {
+        if constexpr (DOTS) continue;
 #pragma unroll
-            for (int i = 0; i < TI; i++) {
-                const int t = 4 * kq + i;
-                if (t < ntok) p.y[(size_t)(tb + t) * p.ldy + n] = acc[i] - bias[i];
+        for (int j = 0; j < HJ; j++) {
+            const int g = g_first + 4 * j + kq;
+            if (g < g_last) hl[(g - p0) * 16 + r] = ref_half_to_single(hraw[j]);
+        }
+        __syncthreads();
+        if (chain) {
+            const float* sc_row = nullptr;
+            const float* off_row = nullptr;
+            if constexpr (F != kI8) {
+                sc_row = p.qscale + (size_t)(tb + ct) * p.stride;
+                off_row = p.offsets + (size_t)(tb + ct) * p.stride;
+            }
+            for (int g = p0; g < gend; g++) {
+                const float dv = static_cast<float>(dl[((g - p0) * M + ct) * 16 + cr]);
+                const float hs = hl[(g - p0) * 16 + cr];
+                if constexpr (F == kI8) {
+                    const float scaled = hs * qs;
+                    acc = acc + scaled * dv;
+                } else {
+                    const float scaled = (hs * p.byte_scale) * sc_row[g];
+                    acc = acc + scaled * dv;
+                    bias = bias + scaled * off_row[g];
+                }
             }
         }
+        __syncthreads();
+    }
+    if (chain) {
+        const int nc = tile * 16 + cr;
+        if (nc >= p.row_start && nc < p.row_end) p.y[(size_t)(tb + ct) * p.ldy + nc] = acc - bias;
     }
 }
 
-template <int F, int TI, int CB, bool DOTS>
-int32_t launch_tpl(const MatmulParams& p, size_t lds_bytes, hipStream_t stream)
+template <int F, int CB, bool DOTS>
+int32_t launch_tpl(const MatmulParams& p, int waves, size_t lds_bytes, hipStream_t stream)
 {
-    auto kernel = matmul_kernel<F, TI, CB, DOTS>;
-    static bool attr_set = false;
-    if (!attr_set) {
-        NHIP_CHECK_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024));
-        attr_set = true;
-    }
+    auto kernel = matmul_kernel<F, CB, DOTS>;
     const int tiles = p.tile_end - p.tile_begin;
-    dim3 grid((tiles + kWavesPerBlock - 1) / kWavesPerBlock, (p.tokens + 15) / 16);
-    hipLaunchKernelGGL(kernel, grid, dim3(kThreads), lds_bytes, stream, p);
+    dim3 grid(tiles, (p.tokens + 15) / 16);
+    hipLaunchKernelGGL(kernel, grid, dim3(64 * waves), lds_bytes, stream, p);
     NHIP_CHECK_HIP(hipGetLastError());
     return NHIP_OK;
 }
 
-template <int F, int TI, bool DOTS>
-int32_t launch_cb(const MatmulParams& p, size_t lds, hipStream_t s)
-{
-    if (p.blocks <= 8) return launch_tpl<F, TI, 8, DOTS>(p, lds, s);
-    if (p.blocks <= 16) return launch_tpl<F, TI, 16, DOTS>(p, lds, s);
-    return launch_tpl<F, TI, 32, DOTS>(p, lds, s);
-}
-
 template <int F, bool DOTS>
-int32_t launch_fmt(const MatmulParams& p, size_t lds, hipStream_t s)
+int32_t launch_fmt(const MatmulParams& p, int waves, size_t lds, hipStream_t s)
 {
-    switch (std::min(4, p.tokens)) {
-        case 1: return launch_cb<F, 1, DOTS>(p, lds, s);
-        case 2: return launch_cb<F, 2, DOTS>(p, lds, s);
-        case 3: return launch_cb<F, 3, DOTS>(p, lds, s);
-        default: return launch_cb<F, 4, DOTS>(p, lds, s);
-    }
+    using T = Traits<F>;
+    const int per = ((p.gph + T::GPB - 1) / T::GPB + waves - 1) / waves;
+    if (per <= 2) return launch_tpl<F, 2, DOTS>(p, waves, lds, s);
+    if (per <= 4) return launch_tpl<F, 4, DOTS>(p, waves, lds, s);
+    return launch_tpl<F, 8, DOTS>(p, waves, lds, s);
 }
 
-constexpr size_t kMaxLds = 160 * 1024;
+constexpr size_t kMaxLds = 64 * 1024 + 16 * 1024;
 
 int32_t run_matmul(const DeviceWeights* w, const int8_t* q, const float* scales, const float* offsets,
                    int32_t stride, int32_t tokens, float* y, int32_t ldy, int32_t row_start,
@@ -350,19 +376,30 @@ int32_t run_matmul(const DeviceWeights* w, const int8_t* q, const float* scales,
     p.t3 = w->table[3];
     p.byte_scale = w->byte_scale;
 
-    size_t lds = (size_t)w->cols * 16;  // 16 tokens x cols bytes of staged operands
-    if (cq) lds += (size_t)32 * w->groups * sizeof(float);
+    // Enough waves to cover the chip: 4 per tile, 8 when tiles are few.
+    const int tiles = p.tile_end - p.tile_begin;
+    const int waves = tiles * ((tokens + 15) / 16) >= 512 ? 4 : 8;
+    // Groups per phase: the int32 D buffer [gph][M][16] stays within 64 KB
+    // and no wave holds more than 8 weight blocks.
+    const int m = std::min(16, tokens);
+    const int gpb = w->format == WeightFormat::Cq4 ? 1 : 2;
+    int gph = std::min(std::min(w->groups, 1024 / m), 8 * waves * gpb);
+    gph -= gph % gpb;
+    if (gph < gpb) gph = gpb;
+    p.gph = gph;
+    p.d_bytes = gph * m * 64;
+    const size_t lds = (size_t)p.d_bytes + (size_t)gph * 64;
     if (lds > kMaxLds) {
-        set_error("cols %d needs %zu bytes of LDS (max %zu)", w->cols, lds, kMaxLds);
+        set_error("matmul needs %zu bytes of LDS (max %zu)", lds, kMaxLds);
         return NHIP_ERR_UNSUPPORTED;
     }
     switch (w->format) {
         case WeightFormat::Int8G32:
-            return dots ? launch_fmt<kI8, true>(p, lds, stream) : launch_fmt<kI8, false>(p, lds, stream);
+            return dots ? launch_fmt<kI8, true>(p, waves, lds, stream) : launch_fmt<kI8, false>(p, waves, lds, stream);
         case WeightFormat::Cq2:
-            return dots ? launch_fmt<kCq2, true>(p, lds, stream) : launch_fmt<kCq2, false>(p, lds, stream);
+            return dots ? launch_fmt<kCq2, true>(p, waves, lds, stream) : launch_fmt<kCq2, false>(p, waves, lds, stream);
         case WeightFormat::Cq4:
-            return dots ? launch_fmt<kCq4, true>(p, lds, stream) : launch_fmt<kCq4, false>(p, lds, stream);
+            return dots ? launch_fmt<kCq4, true>(p, waves, lds, stream) : launch_fmt<kCq4, false>(p, waves, lds, stream);
     }
     return NHIP_ERR_ARG;
 }
