@@ -59,6 +59,7 @@ struct DeviceWeights {
     uint8_t* tiles;
     uint16_t* norms;
     size_t device_bytes;
+    int32_t special_scales;  // some scale has binary16 exponent 31 (inf/NaN patterns)
 };
 
 }  // namespace nhip

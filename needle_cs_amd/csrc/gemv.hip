@@ -23,7 +23,9 @@
 // permutation-invariant in k, so the lane->k assignment only has to agree
 // between A (activations) and B (weights), which it does by construction.
 #include <algorithm>
+#include <cstdlib>
 #include <cstring>
+#include <type_traits>
 
 #include "common.hpp"
 
@@ -33,8 +35,7 @@ namespace {
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef unsigned int u4 __attribute__((ext_vector_type(4)));
 
-constexpr int kWavesPerBlock = 2;
-constexpr int kThreads = 64 * kWavesPerBlock;
+constexpr size_t kMaxLds = 64 * 1024;  // dynamic LDS per block
 
 enum Fmt { kI8 = 0, kCq2 = 1, kCq4 = 2 };
 
@@ -90,6 +91,8 @@ struct MatmulParams {
     int32_t row_start, row_end, tile_begin, tile_end;
     int32_t gph;              // groups per phase (a multiple of Traits::GPB)
     int32_t d_bytes;          // LDS bytes of the D buffer of one phase
+    int32_t ldd;              // LDS row stride (int32) of D and scales: roundup4(gph) + 4
+    int32_t st_bytes;         // int8 path: LDS bytes of the staged activation operands
     uint32_t t0, t1, t2, t3;  // codebook bytes 0..15
     float byte_scale;
 };
@@ -127,21 +130,26 @@ struct Operand<kCq4> {
 };
 
 template <int F>
-__device__ __forceinline__ Operand<F> load_operand(const int8_t* qrow, int g, int kq)
+__device__ __forceinline__ Operand<F> load_operand(const int8_t* qrow, bool valid, int g, int kq)
 {
     using T = Traits<F>;
     Operand<F> o;
     const int8_t* base = qrow + (size_t)g * T::GS;
     if constexpr (F == kI8) {
-        o.a = qrow ? *reinterpret_cast<const long*>(base + act_pos<F>(0, kq)) : 0;
+        const long v = *reinterpret_cast<const long*>(base + act_pos<F>(0, kq));
+        o.a = valid ? v : 0;
     } else if constexpr (F == kCq2) {
 #pragma unroll
-        for (int s = 0; s < 4; s++) o.a[s] = qrow ? *reinterpret_cast<const long*>(base + act_pos<F>(s, kq)) : 0;
+        for (int s = 0; s < 4; s++) {
+            const long v = *reinterpret_cast<const long*>(base + act_pos<F>(s, kq));
+            o.a[s] = valid ? v : 0;
+        }
     } else {
 #pragma unroll
         for (int s = 0; s < 2; s++) {
+            const v4i v = *reinterpret_cast<const v4i*>(base + act_pos<F>(s, kq));
             const v4i zero = {0, 0, 0, 0};
-            o.a[s] = qrow ? *reinterpret_cast<const v4i*>(base + act_pos<F>(s, kq)) : zero;
+            o.a[s] = valid ? v : zero;
         }
     }
     return o;
@@ -197,6 +205,10 @@ __global__ __launch_bounds__(512) void matmul_kernel(MatmulParams p)
 {
     using T = Traits<F>;
     extern __shared__ __align__(16) uint8_t lds[];
+    // D as [token][row][gph + 4] int32 and scales as [row][gph + 4] float: a
+    // chain reads 4 consecutive groups per 16-byte load, and the 16-byte row
+    // padding spreads the MFMA-side writes of 16 rows over distinct banks.
+    const int ld = p.ldd;
     int32_t* dl = reinterpret_cast<int32_t*>(lds);
     float* hl = reinterpret_cast<float*>(lds + p.d_bytes);
     const int S = blockDim.x >> 6;
@@ -209,17 +221,19 @@ __global__ __launch_bounds__(512) void matmul_kernel(MatmulParams p)
     const int r = lane & 15;
     const int kq = lane >> 4;
     const int n = tile * 16 + r;
-    const int8_t* qrow = r < M ? p.q + (size_t)(tb + r) * p.cols : nullptr;  // A operand token = lane % 16
+    // A operand token = lane % 16; lanes past the last token load token
+    // M-1's bytes (a valid address) and zero them.
+    const bool tok_ok = r < M;
+    const int8_t* qrow = p.q + (size_t)(tb + min(r, M - 1)) * p.cols;
     const u4* wbase = reinterpret_cast<const u4*>(p.tiles) + (size_t)tile * p.blocks * 64 + lane;
     const uint16_t* nrow = p.norms + (size_t)n * p.groups_pad8;
+    int32_t* dummy = reinterpret_cast<int32_t*>(lds + p.d_bytes + 16 * p.ldd * 4);  // sink for masked stores
 
-    // epilogue ownership
+    // epilogue ownership: thread c accumulates (token c/16, row c%16)
     const int ct = threadIdx.x >> 4;
     const int cr = threadIdx.x & 15;
     const bool chain = !DOTS && ct < M;
-    float acc = 0.0f, bias = 0.0f, qs = 0.0f;
-    if constexpr (F == kI8 && !DOTS)
-        if (chain) qs = p.qscale[tb + ct];
+    float acc = 0.0f, bias = 0.0f;
 
     for (int p0 = 0; p0 < G; p0 += p.gph) {
         const int gend = min(G, p0 + p.gph);
@@ -231,47 +245,46 @@ __global__ __launch_bounds__(512) void matmul_kernel(MatmulParams p)
         const int g_first = mb0 * T::GPB;
         const int g_last = min(gend, mb1 * T::GPB);  // exclusive
 
+        // Straight-line issue: operands, then every weight block, then the
+        // raw scales, all in flight before the first MFMA waits.  Blocks and
+        // groups past this wave's share are clamped to valid addresses and
+        // their results discarded.
         Operand<F> ops[CB * T::GPB];
 #pragma unroll
         for (int c = 0; c < CB; c++)
 #pragma unroll
             for (int h = 0; h < T::GPB; h++) {
-                const int g = (mb0 + c) * T::GPB + h;
-                if (g < g_last) ops[c * T::GPB + h] = load_operand<F>(qrow, g, kq);
+                const int g = min((mb0 + c) * T::GPB + h, G - 1);
+                ops[c * T::GPB + h] = load_operand<F>(qrow, tok_ok, g, kq);
             }
         u4 w[CB];
 #pragma unroll
-        for (int c = 0; c < CB; c++)
-            if (mb0 + c < mb1) w[c] = __builtin_nontemporal_load(wbase + (size_t)(mb0 + c) * 64);
-        // this lane decodes the scales of groups g_first + 4j + kq
+        for (int c = 0; c < CB; c++) w[c] = __builtin_nontemporal_load(wbase + (size_t)min(mb0 + c, b_end - 1) * 64);
         constexpr int HJ = (CB * T::GPB + 3) / 4;
         uint16_t hraw[HJ];
         if constexpr (!DOTS) {
 #pragma unroll
-            for (int j = 0; j < HJ; j++) {
-                const int g = g_first + 4 * j + kq;
-                hraw[j] = g < g_last ? nrow[g] : (uint16_t)0;
-            }
+            for (int j = 0; j < HJ; j++) hraw[j] = nrow[min(g_first + 4 * j + kq, G - 1)];
         }
+        // Keep every load above this point: the scheduler would otherwise sink
+        // weight loads between MFMAs and serialise memory round trips.
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int c = 0; c < CB; c++) {
-            if (mb0 + c >= mb1) break;
 #pragma unroll
             for (int h = 0; h < T::GPB; h++) {
                 const int g = (mb0 + c) * T::GPB + h;
-                if (g >= g_last) break;
+                const bool g_ok = g < g_last;
                 const v4i d = group_dot<F>(w[c], h, ops[c * T::GPB + h], p);
 #pragma unroll
                 for (int i = 0; i < 4; i++) {
                     const int t = 4 * kq + i;
-                    if (t < M) {
-                        if constexpr (DOTS) {
-                            if (n >= p.row_start && n < p.row_end)
-                                p.dots[((size_t)(tb + t) * (p.row_end - p.row_start) + (n - p.row_start)) * G + g] =
-                                    d[i];
-                        } else {
-                            dl[((g - p0) * M + t) * 16 + r] = d[i];
-                        }
+                    if constexpr (DOTS) {
+                        if (g_ok && t < M && n >= p.row_start && n < p.row_end)
+                            p.dots[((size_t)(tb + t) * (p.row_end - p.row_start) + (n - p.row_start)) * G + g] = d[i];
+                    } else {
+                        int32_t* dst = (g_ok && t < M) ? dl + (t * 16 + r) * ld + (g - p0) : dummy + lane;
+                        *dst = d[i];
                     }
                 }
             }
@@ -280,24 +293,59 @@ __global__ __launch_bounds__(512) void matmul_kernel(MatmulParams p)
 #pragma unroll
         for (int j = 0; j < HJ; j++) {
             const int g = g_first + 4 * j + kq;
-            if (g < g_last) hl[(g - p0) * 16 + r] = ref_half_to_single(hraw[j]);
+            float* dst = g < g_last ? hl + r * ld + (g - p0) : reinterpret_cast<float*>(dummy) + lane;
+            *dst = ref_half_to_single(hraw[j]);
         }
         __syncthreads();
         if (chain) {
+            float qs = 0.0f;
+            if constexpr (F == kI8) qs = p.qscale[tb + ct];
+            const int32_t* drow = dl + (ct * 16 + cr) * ld;
+            const float* hrow = hl + cr * ld;
             const float* sc_row = nullptr;
             const float* off_row = nullptr;
             if constexpr (F != kI8) {
-                sc_row = p.qscale + (size_t)(tb + ct) * p.stride;
-                off_row = p.offsets + (size_t)(tb + ct) * p.stride;
+                sc_row = p.qscale + (size_t)(tb + ct) * p.stride + p0;
+                off_row = p.offsets + (size_t)(tb + ct) * p.stride + p0;
             }
-            for (int g = p0; g < gend; g++) {
-                const float dv = static_cast<float>(dl[((g - p0) * M + ct) * 16 + cr]);
-                const float hs = hl[(g - p0) * 16 + cr];
+            const int cnt = gend - p0;
+            int g = 0;
+            for (; g + 8 <= cnt; g += 8) {
+                const v4i d0 = *reinterpret_cast<const v4i*>(drow + g);
+                const v4i d1 = *reinterpret_cast<const v4i*>(drow + g + 4);
+                const float4 h0 = *reinterpret_cast<const float4*>(hrow + g);
+                const float4 h1 = *reinterpret_cast<const float4*>(hrow + g + 4);
+                const float dv[8] = {(float)d0.x, (float)d0.y, (float)d0.z, (float)d0.w,
+                                     (float)d1.x, (float)d1.y, (float)d1.z, (float)d1.w};
+                const float hv[8] = {h0.x, h0.y, h0.z, h0.w, h1.x, h1.y, h1.z, h1.w};
                 if constexpr (F == kI8) {
-                    const float scaled = hs * qs;
+#pragma unroll
+                    for (int k = 0; k < 8; k++) {
+                        const float scaled = hv[k] * qs;
+                        acc = acc + scaled * dv[k];
+                    }
+                } else {
+                    const float4 s0 = *reinterpret_cast<const float4*>(sc_row + g);
+                    const float4 s1 = *reinterpret_cast<const float4*>(sc_row + g + 4);
+                    const float4 o0 = *reinterpret_cast<const float4*>(off_row + g);
+                    const float4 o1 = *reinterpret_cast<const float4*>(off_row + g + 4);
+                    const float sv[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
+                    const float ov[8] = {o0.x, o0.y, o0.z, o0.w, o1.x, o1.y, o1.z, o1.w};
+#pragma unroll
+                    for (int k = 0; k < 8; k++) {
+                        const float scaled = (hv[k] * p.byte_scale) * sv[k];
+                        acc = acc + scaled * dv[k];
+                        bias = bias + scaled * ov[k];
+                    }
+                }
+            }
+            for (; g < cnt; g++) {
+                const float dv = static_cast<float>(drow[g]);
+                if constexpr (F == kI8) {
+                    const float scaled = hrow[g] * qs;
                     acc = acc + scaled * dv;
                 } else {
-                    const float scaled = (hs * p.byte_scale) * sc_row[g];
+                    const float scaled = (hrow[g] * p.byte_scale) * sc_row[g];
                     acc = acc + scaled * dv;
                     bias = bias + scaled * off_row[g];
                 }
@@ -309,6 +357,421 @@ __global__ __launch_bounds__(512) void matmul_kernel(MatmulParams p)
         const int nc = tile * 16 + cr;
         if (nc >= p.row_start && nc < p.row_end) p.y[(size_t)(tb + ct) * p.ldy + nc] = acc - bias;
     }
+}
+
+// Literal int8 path.  Same phases and epilogue as matmul_kernel, but the
+// activation operands are staged once per block: the M token rows of the
+// phase's K range are read with coalesced 16-byte loads (issued before the
+// weight blocks) and written to LDS as [group][kq][token] 8-byte MFMA A
+// operands, so each wave issues one weight load per 1 KB block and no
+// scattered activation loads.
+template <int CB, int NS, bool DOTS>
+__global__ __launch_bounds__(512) void matmul_i8_kernel(MatmulParams p)
+{
+    extern __shared__ __align__(16) uint8_t lds[];
+    const int ld = p.ldd;
+    uint2* st = reinterpret_cast<uint2*>(lds);
+    float* pl = reinterpret_cast<float*>(lds + p.st_bytes);  // products [token][row][ld]
+    float* dummy = reinterpret_cast<float*>(lds + p.st_bytes + p.d_bytes);  // 256-float sink
+    const int S = blockDim.x >> 6;
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int tile = p.tile_begin + blockIdx.x;
+    const int tb = blockIdx.y * 16;
+    const int M = min(16, p.tokens - tb);
+    const int G = p.groups;
+    const int r = lane & 15;
+    const int kq = lane >> 4;
+    const int n = tile * 16 + r;
+    const int ra = min(r, M - 1);  // A operand token (lanes past M read a valid row and zero it)
+    const u4* wbase = reinterpret_cast<const u4*>(p.tiles) + (size_t)tile * p.blocks * 64 + lane;
+    const uint16_t* nrow = p.norms + (size_t)n * p.groups_pad8;
+    const int8_t* qblock = p.q + (size_t)tb * p.cols;
+
+    const int ct = threadIdx.x >> 4;
+    const int cr = threadIdx.x & 15;
+    const bool chain = !DOTS && ct < M;
+    float acc = 0.0f;
+
+    for (int p0 = 0; p0 < G; p0 += p.gph) {
+        const int gend = min(G, p0 + p.gph);
+        const int gcnt = gend - p0;
+        const int b_begin = p0 >> 1;
+        const int b_end = (gend + 1) >> 1;
+        const int per = (b_end - b_begin + S - 1) / S;
+        const int mb0 = b_begin + wave * per;
+        const int mb1 = min(b_end, mb0 + per);
+        const int g_first = mb0 * 2;
+        const int g_last = min(gend, mb1 * 2);
+
+        // 1. activation rows of this phase: unit u = (token, 16-byte offset)
+        const int units = M * gcnt * 2;
+        uint4 sv[NS];
+#pragma unroll
+        for (int j = 0; j < NS; j++) {
+            const int u = min((int)threadIdx.x + j * (int)blockDim.x, units - 1);
+            const int t = u / (2 * gcnt);
+            const int o = (u - t * 2 * gcnt) * 16;
+            sv[j] = *reinterpret_cast<const uint4*>(qblock + (size_t)t * p.cols + p0 * 32 + o);
+        }
+        // 2. raw scales (lane kq holds groups g_first+4j+kq), 3. weight
+        //    blocks -- scales first so that waiting for them does not wait
+        //    for the weights (loads complete in issue order)
+        constexpr int HJ = (CB * 2 + 3) / 4;
+        uint16_t hraw[HJ];
+        // activation scales of the four tokens this lane's MFMA results belong to
+        float qraw[4];
+        if constexpr (!DOTS) {
+#pragma unroll
+            for (int j = 0; j < HJ; j++) hraw[j] = nrow[min(g_first + 4 * j + kq, G - 1)];
+#pragma unroll
+            for (int i = 0; i < 4; i++) qraw[i] = p.qscale[tb + min(4 * kq + i, M - 1)];
+        }
+        u4 w[CB];
+#pragma unroll
+        for (int c = 0; c < CB; c++) w[c] = __builtin_nontemporal_load(wbase + (size_t)min(mb0 + c, b_end - 1) * 64);
+        __builtin_amdgcn_sched_barrier(0);
+        // 4. staged operands to LDS: bytes o..o+15 of a row are kq = (o%32)/8
+        //    and kq+1 of group o/32
+#pragma unroll
+        for (int j = 0; j < NS; j++) {
+            const int u = (int)threadIdx.x + j * (int)blockDim.x;
+            const int uc = min(u, units - 1);
+            const int t = uc / (2 * gcnt);
+            const int o = (uc - t * 2 * gcnt) * 16;
+            const int g = o >> 5;
+            const int k0 = (o & 31) >> 3;
+            uint2* d0 = u < units ? st + (g * 4 + k0) * M + t : reinterpret_cast<uint2*>(dummy) + lane;
+            uint2* d1 = u < units ? st + (g * 4 + k0 + 1) * M + t : reinterpret_cast<uint2*>(dummy) + 64 + lane;
+            *d0 = make_uint2(sv[j].x, sv[j].y);
+            *d1 = make_uint2(sv[j].z, sv[j].w);
+        }
+        float hsv[HJ];
+        if constexpr (!DOTS) {
+#pragma unroll
+            for (int j = 0; j < HJ; j++) hsv[j] = ref_half_to_single(hraw[j]);
+        }
+        __syncthreads();
+        // 5. all A operands from LDS, then all MFMAs (each waits only for its
+        //    own weight block), then the products of Scalar.cs:185-186
+        //      scaled = HalfToSingle(norm[n][g]) * ByteScale(1) * scale[t]
+        //      prod   = scaled * D_g      (rounded; added to acc in step 6)
+        long av[2 * CB];
+#pragma unroll
+        for (int k = 0; k < 2 * CB; k++) {
+            const int gl = min(g_first + k, gend - 1) - p0;
+            const long araw = *reinterpret_cast<const long*>(st + (gl * 4 + kq) * M + ra);
+            av[k] = r < M ? araw : 0;
+        }
+        v4i dv[2 * CB];
+#pragma unroll
+        for (int k = 0; k < 2 * CB; k++) {
+            const u4& wc = w[k >> 1];
+            const long b = (k & 1) ? (long)(((uint64_t)wc.w << 32) | wc.z) : (long)(((uint64_t)wc.y << 32) | wc.x);
+            const v4i zero = {0, 0, 0, 0};
+            dv[k] = __builtin_amdgcn_mfma_i32_16x16x32_i8(av[k], b, zero, 0, 0, 0);
+        }
+        if constexpr (DOTS) {
+#pragma unroll
+            for (int k = 0; k < 2 * CB; k++) {
+                const int g = g_first + k;
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const int t = 4 * kq + i;
+                    if (g < g_last && t < M && n >= p.row_start && n < p.row_end)
+                        p.dots[((size_t)(tb + t) * (p.row_end - p.row_start) + (n - p.row_start)) * G + g] = dv[k][i];
+                }
+            }
+        } else {
+            float qs[4];
+#pragma unroll
+            for (int i = 0; i < 4; i++) qs[i] = 4 * kq + i < M ? qraw[i] : 0.0f;
+            // scale of (row r, group g_first + k) sits in lane (k % 4) * 16 + r
+            float hk[2 * CB];
+#pragma unroll
+            for (int k = 0; k < 2 * CB; k++) hk[k] = __shfl(hsv[k >> 2], (k & 3) * 16 + r);
+#pragma unroll
+            for (int k = 0; k < 2 * CB; k++) {
+                const int g = g_first + k;
+                const bool g_ok = g < g_last;
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const int t = 4 * kq + i;
+                    const float scaled = hk[k] * qs[i];
+                    const float prod = scaled * static_cast<float>(dv[k][i]);
+                    float* dst = (g_ok && t < M) ? pl + (t * 16 + r) * ld + (g - p0) : dummy + 128 + lane;
+                    *dst = prod;
+                }
+            }
+        }
+        __syncthreads();
+        if constexpr (DOTS) continue;
+        // 6. each (token, row) accumulator adds its products in ascending g
+        if (chain) {
+            const float* prow = pl + (ct * 16 + cr) * ld;
+            int g = 0;
+            for (; g + 8 <= gcnt; g += 8) {
+                const float4 v0 = *reinterpret_cast<const float4*>(prow + g);
+                const float4 v1 = *reinterpret_cast<const float4*>(prow + g + 4);
+                acc = acc + v0.x;
+                acc = acc + v0.y;
+                acc = acc + v0.z;
+                acc = acc + v0.w;
+                acc = acc + v1.x;
+                acc = acc + v1.y;
+                acc = acc + v1.z;
+                acc = acc + v1.w;
+            }
+            for (; g < gcnt; g++) acc = acc + prow[g];
+        }
+        __syncthreads();
+    }
+    if (chain) {
+        const int nc = tile * 16 + cr;
+        if (nc >= p.row_start && nc < p.row_end) p.y[(size_t)(tb + ct) * p.ldy + nc] = acc;
+    }
+}
+
+// Decode path of the literal int8 format for M <= 4 tokens (beam rows).
+// Each of the S waves of a tile owns `per` weight blocks (2*per groups),
+// computes its products p_g = (hs * scale[t]) * D_g (Scalar.cs:185-186) and
+// leaves them in LDS as [t][r][g]; after one barrier the lanes (t, r) of wave
+// 0 add them in ascending group order, so each y[t][n] is exactly
+// (((0 + p_0) + p_1) + ... + p_{G-1}).  Preconditions (checked on the host):
+// every wave owns per == CB blocks with per % 4 == 0 (its scales are 16-byte
+// aligned in the padded scale rows).
+template <int CB, int TI, int NS, bool EXACT>
+__global__ __launch_bounds__(512) void matmul_i8_decode_kernel(MatmulParams p)
+{
+    extern __shared__ __align__(16) uint8_t lds[];
+    uint2* st = reinterpret_cast<uint2*>(lds);
+    float* pl = reinterpret_cast<float*>(lds + p.st_bytes);  // [t][r][GS]
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int tile = p.tile_begin + blockIdx.x;
+    const int M = p.tokens;  // <= 4 == TI
+    const int G = p.groups;
+    const int GS = p.ldd;    // product row stride (floats), multiple of 4
+    const int r = lane & 15;
+    const int kq = lane >> 4;
+    const int n = tile * 16 + r;
+    const int ra = min(r, M - 1);
+    const int mb0 = wave * CB;
+    const int g_first = mb0 * 2;
+    const u4* wbase = reinterpret_cast<const u4*>(p.tiles) + (size_t)tile * p.blocks * 64 + lane;
+    const uint16_t* nrow = p.norms + (size_t)n * p.groups_pad8 + g_first;
+
+    // 1. activation rows (all K): unit u = (token, 16-byte offset)
+    const int units = M * G * 2;
+    uint4 sv[NS];
+#pragma unroll
+    for (int j = 0; j < NS; j++) {
+        const int u = min((int)threadIdx.x + j * (int)blockDim.x, units - 1);
+        const int t = u / (2 * G);
+        const int o = (u - t * 2 * G) * 16;
+        sv[j] = *reinterpret_cast<const uint4*>(p.q + (size_t)t * p.cols + o);
+    }
+    // 2. activation scales, 3. this wave's weight scales (8 per 16-byte load),
+    // 4. its weight blocks -- in this order, all in flight together
+    float qraw[TI];
+#pragma unroll
+    for (int i = 0; i < TI; i++) qraw[i] = p.qscale[min(i, M - 1)];
+    constexpr int SJ = CB / 4;  // 16-byte scale loads covering 2*CB groups
+    uint4 sraw[SJ];
+#pragma unroll
+    for (int j = 0; j < SJ; j++) sraw[j] = *reinterpret_cast<const uint4*>(nrow + 8 * j);
+    u4 w[CB];
+#pragma unroll
+    for (int c = 0; c < CB; c++) w[c] = __builtin_nontemporal_load(wbase + (size_t)(mb0 + c) * 64);
+    __builtin_amdgcn_sched_barrier(0);
+    // 5. staged operands: bytes o..o+15 of a row are kq = (o%32)/8 and kq+1
+#pragma unroll
+    for (int j = 0; j < NS; j++) {
+        const int u = (int)threadIdx.x + j * (int)blockDim.x;
+        const int uc = min(u, units - 1);
+        const int t = uc / (2 * G);
+        const int o = (uc - t * 2 * G) * 16;
+        const int g = o >> 5;
+        const int k0 = (o & 31) >> 3;
+        if (u < units) {
+            st[(g * 4 + k0) * M + t] = make_uint2(sv[j].x, sv[j].y);
+            st[(g * 4 + k0 + 1) * M + t] = make_uint2(sv[j].z, sv[j].w);
+        }
+    }
+    __syncthreads();
+    long av[2 * CB];
+#pragma unroll
+    for (int k = 0; k < 2 * CB; k++) {
+        const int g = min(g_first + k, G - 1);
+        const long araw = *reinterpret_cast<const long*>(st + (g * 4 + kq) * M + ra);
+        av[k] = r < M ? araw : 0;
+    }
+    float qs[TI];
+#pragma unroll
+    for (int i = 0; i < TI; i++) qs[i] = i < M ? qraw[i] : 0.0f;
+    float pr[2 * CB][TI];
+#pragma unroll
+    for (int k = 0; k < 2 * CB; k++) {
+        const u4& wc = w[k >> 1];
+        const long b = (k & 1) ? (long)(((uint64_t)wc.w << 32) | wc.z) : (long)(((uint64_t)wc.y << 32) | wc.x);
+        const v4i zero = {0, 0, 0, 0};
+        const v4i d = __builtin_amdgcn_mfma_i32_16x16x32_i8(av[k], b, zero, 0, 0, 0);
+        const uint4 s4 = sraw[k >> 3];
+        const int kk = k & 7;
+        const uint32_t word = kk < 4 ? (kk < 2 ? s4.x : s4.y) : (kk < 6 ? s4.z : s4.w);
+        const uint32_t h = (kk & 1) ? (word >> 16) : (word & 0xFFFFu);
+        float hs;
+        if constexpr (EXACT) {
+            hs = ref_half_to_single(h);
+        } else {
+            // binary16 -> binary32 is exact; a -0 scale gives a +-0 product,
+            // which cannot change an accumulator that starts at +0.
+            hs = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(h)));
+        }
+#pragma unroll
+        for (int i = 0; i < TI; i++) pr[k][i] = (hs * qs[i]) * static_cast<float>(d[i]);
+    }
+    // lanes kq == 0 hold D rows 0..3 (the tokens); groups >= G are never read
+    if (kq == 0) {
+#pragma unroll
+        for (int i = 0; i < TI; i++) {
+            float4* dst = reinterpret_cast<float4*>(pl + (size_t)(i * 16 + r) * GS + g_first);
+#pragma unroll
+            for (int k4 = 0; k4 < 2 * CB; k4 += 4)
+                dst[k4 >> 2] = make_float4(pr[k4][i], pr[k4 + 1][i], pr[k4 + 2][i], pr[k4 + 3][i]);
+        }
+    }
+    __syncthreads();
+    if (threadIdx.x < M * 16) {
+        const int t = threadIdx.x >> 4;
+        const int rr = threadIdx.x & 15;
+        const int nn = tile * 16 + rr;
+        const float4* row = reinterpret_cast<const float4*>(pl + (size_t)(t * 16 + rr) * GS);
+        float acc = 0.0f;
+        int c = 0;
+        float4 v[4];
+        const int full = G >> 4;  // chunks of 16 groups
+        if (full > 0) {
+#pragma unroll
+            for (int j = 0; j < 4; j++) v[j] = row[j];
+        }
+        for (int ch = 0; ch < full; ch++) {
+            float4 nx[4];
+            const int nb = min(ch + 1, full - 1) * 4;
+#pragma unroll
+            for (int j = 0; j < 4; j++) nx[j] = row[nb + j];
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                acc = acc + v[j].x;
+                acc = acc + v[j].y;
+                acc = acc + v[j].z;
+                acc = acc + v[j].w;
+            }
+#pragma unroll
+            for (int j = 0; j < 4; j++) v[j] = nx[j];
+        }
+        c = full * 16;
+        const float* rowf = reinterpret_cast<const float*>(row);
+        for (; c < G; c++) acc = acc + rowf[c];
+        if (nn >= p.row_start && nn < p.row_end) p.y[(size_t)t * p.ldy + nn] = acc;
+    }
+}
+
+template <int CB, int TI, int NS, bool EXACT>
+int32_t launch_dec_tpl(const MatmulParams& p, int waves, size_t lds, hipStream_t stream)
+{
+    const int tiles = p.tile_end - p.tile_begin;
+    hipLaunchKernelGGL((matmul_i8_decode_kernel<CB, TI, NS, EXACT>), dim3(tiles), dim3(64 * waves), lds, stream, p);
+    NHIP_CHECK_HIP(hipGetLastError());
+    return NHIP_OK;
+}
+
+template <int CB, int TI, bool EXACT>
+int32_t launch_dec_ns(const MatmulParams& p, int waves, int ns, size_t lds, hipStream_t s)
+{
+    if (ns <= 1) return launch_dec_tpl<CB, TI, 1, EXACT>(p, waves, lds, s);
+    if (ns <= 2) return launch_dec_tpl<CB, TI, 2, EXACT>(p, waves, lds, s);
+    return launch_dec_tpl<CB, TI, 4, EXACT>(p, waves, lds, s);
+}
+
+template <int CB, bool EXACT>
+int32_t launch_dec_ti(const MatmulParams& p, int waves, int ns, size_t lds, hipStream_t s)
+{
+    switch (p.tokens) {
+        case 1: return launch_dec_ns<CB, 1, EXACT>(p, waves, ns, lds, s);
+        case 2: return launch_dec_ns<CB, 2, EXACT>(p, waves, ns, lds, s);
+        case 3: return launch_dec_ns<CB, 3, EXACT>(p, waves, ns, lds, s);
+        default: return launch_dec_ns<CB, 4, EXACT>(p, waves, ns, lds, s);
+    }
+}
+
+// Runs the decode kernel when its preconditions hold; returns 1 when it did
+// not apply (the caller falls back to the general kernel).
+int32_t try_i8_decode(const DeviceWeights* w, MatmulParams& p, hipStream_t stream)
+{
+    if (p.tokens > 4 || p.dots) return 1;
+    static const int waves_override = [] {
+        // tuning knob: 2, 4 or 8 waves per tile, or 1 to use the general kernel
+        const char* e = getenv("NHIP_DECODE_WAVES");
+        const int v = e ? atoi(e) : 0;
+        return (v == 1 || v == 2 || v == 4 || v == 8) ? v : 0;
+    }();
+    if (waves_override == 1) return 1;
+    int waves = 0;
+    const int cands[3] = {4, 8, 2};
+    for (int c : cands) {
+        if (waves_override && c != waves_override) continue;
+        if (w->blocks % c == 0 && (w->blocks / c == 4 || w->blocks / c == 8)) {
+            waves = c;
+            break;
+        }
+    }
+    if (!waves) return 1;
+    const int per = w->blocks / waves;
+    const int m = p.tokens;
+    p.st_bytes = (w->groups * 32 * m + 15) & ~15;
+    p.ldd = ((2 * w->blocks + 3) & ~3) + 4;  // product row stride: every group a wave writes
+    const size_t lds = (size_t)p.st_bytes + (size_t)m * 16 * p.ldd * sizeof(float);
+    if (lds > kMaxLds) return 1;
+    const int ns = (m * w->groups * 2 + 64 * waves - 1) / (64 * waves);
+    if (ns > 4) return 1;
+    int32_t rc;
+    // the kernel's CB must equal per (4 or 8)
+    if (per == 4)
+        rc = w->special_scales ? launch_dec_ti<4, true>(p, waves, ns, lds, stream)
+                               : launch_dec_ti<4, false>(p, waves, ns, lds, stream);
+    else
+        rc = w->special_scales ? launch_dec_ti<8, true>(p, waves, ns, lds, stream)
+                               : launch_dec_ti<8, false>(p, waves, ns, lds, stream);
+    return rc;
+}
+
+template <int CB, int NS, bool DOTS>
+int32_t launch_i8_tpl(const MatmulParams& p, int waves, size_t lds_bytes, hipStream_t stream)
+{
+    const int tiles = p.tile_end - p.tile_begin;
+    dim3 grid(tiles, (p.tokens + 15) / 16);
+    hipLaunchKernelGGL((matmul_i8_kernel<CB, NS, DOTS>), grid, dim3(64 * waves), lds_bytes, stream, p);
+    NHIP_CHECK_HIP(hipGetLastError());
+    return NHIP_OK;
+}
+
+template <int CB, bool DOTS>
+int32_t launch_i8_ns(const MatmulParams& p, int waves, int ns, size_t lds, hipStream_t s)
+{
+    if (ns <= 1) return launch_i8_tpl<CB, 1, DOTS>(p, waves, lds, s);
+    if (ns <= 2) return launch_i8_tpl<CB, 2, DOTS>(p, waves, lds, s);
+    if (ns <= 4) return launch_i8_tpl<CB, 4, DOTS>(p, waves, lds, s);
+    return launch_i8_tpl<CB, 8, DOTS>(p, waves, lds, s);
+}
+
+template <bool DOTS>
+int32_t launch_i8(const MatmulParams& p, int waves, int ns, size_t lds, hipStream_t s)
+{
+    const int per = ((p.gph + 1) / 2 + waves - 1) / waves;
+    if (per <= 2) return launch_i8_ns<2, DOTS>(p, waves, ns, lds, s);
+    if (per <= 4) return launch_i8_ns<4, DOTS>(p, waves, ns, lds, s);
+    return launch_i8_ns<8, DOTS>(p, waves, ns, lds, s);
 }
 
 template <int F, int CB, bool DOTS>
@@ -332,7 +795,6 @@ int32_t launch_fmt(const MatmulParams& p, int waves, size_t lds, hipStream_t s)
     return launch_tpl<F, 8, DOTS>(p, waves, lds, s);
 }
 
-constexpr size_t kMaxLds = 64 * 1024 + 16 * 1024;
 
 int32_t run_matmul(const DeviceWeights* w, const int8_t* q, const float* scales, const float* offsets,
                    int32_t stride, int32_t tokens, float* y, int32_t ldy, int32_t row_start,
@@ -376,26 +838,58 @@ int32_t run_matmul(const DeviceWeights* w, const int8_t* q, const float* scales,
     p.t3 = w->table[3];
     p.byte_scale = w->byte_scale;
 
-    // Enough waves to cover the chip: 4 per tile, 8 when tiles are few.
+    // Waves per 16-row tile (each loads 1/waves of the tile's weight blocks).
+    // NHIP_MATMUL_WAVES (4 or 8) overrides the default for tuning.
     const int tiles = p.tile_end - p.tile_begin;
-    const int waves = tiles * ((tokens + 15) / 16) >= 512 ? 4 : 8;
-    // Groups per phase: the int32 D buffer [gph][M][16] stays within 64 KB
-    // and no wave holds more than 8 weight blocks.
+    static const int waves_override = [] {
+        const char* e = getenv("NHIP_MATMUL_WAVES");
+        const int v = e ? atoi(e) : 0;
+        return (v == 4 || v == 8) ? v : 0;
+    }();
+    const int waves = waves_override ? waves_override : (tiles * ((tokens + 15) / 16) >= 512 ? 4 : 8);
     const int m = std::min(16, tokens);
+    if (w->format == WeightFormat::Int8G32) {
+        const int32_t drc = try_i8_decode(w, p, stream);
+        if (drc <= 0) return drc;
+        // LDS per phase: staged operands gph*32*m + products m*16*ldd*4 + a
+        // 1 KB sink, within 64 KB; no wave holds more than 8 weight blocks.
+        int gph = std::min(w->groups, 16 * waves);
+        auto need = [&](int g) {
+            const int ldd = ((g + 3) & ~3) + 4;
+            return (size_t)g * 32 * m + (size_t)m * 16 * ldd * 4 + 1024;
+        };
+        while (gph > 2 && need(gph) > kMaxLds) gph -= 2;
+        if (gph > 1 && gph % 2) gph -= 1;
+        p.gph = gph;
+        p.ldd = ((gph + 3) & ~3) + 4;
+        p.st_bytes = (gph * 32 * m + 15) & ~15;
+        p.d_bytes = m * 16 * p.ldd * 4;
+        const size_t lds = need(gph);
+        const int ns = (m * gph * 2 + 64 * waves - 1) / (64 * waves);
+        if (lds > kMaxLds || ns > 8) {
+            set_error("matmul needs %zu bytes of LDS (max %zu)", lds, kMaxLds);
+            return NHIP_ERR_UNSUPPORTED;
+        }
+        return dots ? launch_i8<true>(p, waves, ns, lds, stream) : launch_i8<false>(p, waves, ns, lds, stream);
+    }
+    // Codebook formats.  Groups per phase: the int32 D buffer [gph][M][16]
+    // plus the decoded scales [gph][16] stay within 64 KB of LDS, and no
+    // wave holds more than 8 weight blocks.
     const int gpb = w->format == WeightFormat::Cq4 ? 1 : 2;
-    int gph = std::min(std::min(w->groups, 1024 / m), 8 * waves * gpb);
+    int gph = std::min(std::min(w->groups, 1024 / (m + 1) - 12), 8 * waves * gpb);
     gph -= gph % gpb;
     if (gph < gpb) gph = gpb;
     p.gph = gph;
-    p.d_bytes = gph * m * 64;
-    const size_t lds = (size_t)p.d_bytes + (size_t)gph * 64;
+    p.ldd = ((gph + 3) & ~3) + 4;
+    p.d_bytes = m * 16 * p.ldd * 4;
+    const size_t lds = (size_t)p.d_bytes + (size_t)16 * p.ldd * 4 + 64 * 4;
     if (lds > kMaxLds) {
         set_error("matmul needs %zu bytes of LDS (max %zu)", lds, kMaxLds);
         return NHIP_ERR_UNSUPPORTED;
     }
     switch (w->format) {
         case WeightFormat::Int8G32:
-            return dots ? launch_fmt<kI8, true>(p, waves, lds, stream) : launch_fmt<kI8, false>(p, waves, lds, stream);
+            break;
         case WeightFormat::Cq2:
             return dots ? launch_fmt<kCq2, true>(p, waves, lds, stream) : launch_fmt<kCq2, false>(p, waves, lds, stream);
         case WeightFormat::Cq4:
@@ -444,13 +938,15 @@ __global__ void retile_kernel(const uint8_t* __restrict__ src, int rows, int row
 }
 
 __global__ void pad_norms_kernel(const uint16_t* __restrict__ src, int rows, int groups, int rows_pad,
-                                 int groups_pad8, uint16_t* __restrict__ dst)
+                                 int groups_pad8, uint16_t* __restrict__ dst, int* __restrict__ special)
 {
     const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= (size_t)rows_pad * groups_pad8) return;
     const int n = (int)(i / groups_pad8);
     const int g = (int)(i % groups_pad8);
-    dst[i] = (n < rows && g < groups) ? src[(size_t)n * groups + g] : (uint16_t)0;
+    const uint16_t h = (n < rows && g < groups) ? src[(size_t)n * groups + g] : (uint16_t)0;
+    dst[i] = h;
+    if ((h & 0x7C00u) == 0x7C00u) atomicOr(special, 1);
 }
 
 int32_t create_weights(WeightFormat fmt, const uint8_t* d_src, const uint16_t* d_norms, int32_t rows,
@@ -503,10 +999,18 @@ int32_t create_weights(WeightFormat fmt, const uint8_t* d_src, const uint16_t* d
                                w->blocks, units, reinterpret_cast<uint4*>(w->tiles));
             break;
     }
-    hipLaunchKernelGGL(pad_norms_kernel, dim3((unsigned)((norm_elems + 255) / 256)), dim3(256), 0, s, d_norms,
-                       rows, w->groups, w->tiles_n * 16, w->groups_pad8, w->norms);
-    e = hipGetLastError();
+    int* d_special = nullptr;
+    e = hipMalloc(&d_special, sizeof(int));
+    if (e == hipSuccess) e = hipMemsetAsync(d_special, 0, sizeof(int), s);
+    if (e == hipSuccess) {
+        hipLaunchKernelGGL(pad_norms_kernel, dim3((unsigned)((norm_elems + 255) / 256)), dim3(256), 0, s, d_norms,
+                           rows, w->groups, w->tiles_n * 16, w->groups_pad8, w->norms, d_special);
+        e = hipGetLastError();
+    }
+    int special = 0;
+    if (e == hipSuccess) e = hipMemcpyAsync(&special, d_special, sizeof(int), hipMemcpyDeviceToHost, s);
     if (e == hipSuccess) e = hipStreamSynchronize(s);
+    (void)hipFree(d_special);
     if (e != hipSuccess) {
         set_error("weight re-tiling failed: %s", hipGetErrorString(e));
         (void)hipFree(w->tiles);
@@ -514,6 +1018,7 @@ int32_t create_weights(WeightFormat fmt, const uint8_t* d_src, const uint16_t* d
         delete w;
         return NHIP_ERR_HIP;
     }
+    w->special_scales = special;
     *out = w;
     return NHIP_OK;
 }

@@ -275,3 +275,41 @@ def test_kernel_table_prepare_and_quantize(hip, orc):
     q = np.zeros(8, dtype=np.int8)
     scale = hip.lib().nhip_quantize_int8(g.ctypes.data, 8, q.ctypes.data)
     assert abs(scale - 0.03149606) <= 1e-6 and list(q) == [-127, 0, 127, 0, 0, 0, 0, 0]
+
+
+# ------------------------------------------ decode kernel (M <= 4) edges --
+
+@pytest.mark.parametrize("tokens", [1, 2, 3, 4])
+@pytest.mark.parametrize("r0,r1", [(0, 37), (5, 29), (16, 17)])
+def test_int8_decode_path_row_ranges(hip, orc, tokens, r0, r1):
+    """M <= 4 with K = 1024 and K = 4096 runs the chained decode kernel."""
+    for cols in (1024, 4096):
+        rows = 37
+        w, scales, x, q, qs = int8_case(orc, 4000 + tokens * 10 + r0 + cols, rows, cols, tokens)
+        weights = hip.Weights.int8(w, scales)
+        ldy = rows + 5
+        y = run_i8(hip, weights, q, qs, tokens, ldy, r0, r1)
+        want = np.full((tokens, ldy), SENTINEL, dtype=np.float32)
+        orc.matmul_rows_i8(w, scales, q, qs, tokens, want, ldy, r0, r1)
+        assert np.array_equal(y.view(np.uint32), want.view(np.uint32))
+
+
+@pytest.mark.parametrize("tokens", [3, 7])
+def test_int8_special_scale_patterns(hip, orc, tokens):
+    """Zero, negative-zero, subnormal and exponent-31 fp16 scales decode as
+    Scalar.HalfToSingle does (Scalar.cs:121-128), in both kernels."""
+    rows, cols = 64, 2048
+    w, scales, x, q, qs = int8_case(orc, 555 + tokens, rows, cols, tokens)
+    scales = scales.copy()
+    flat = scales.reshape(-1)
+    flat[::7] = 0x8000
+    flat[::11] = 0x0000
+    flat[::13] = 0x0001
+    flat[::17] = 0x83FF
+    flat[::19] = 0x7C00
+    flat[::23] = 0xFC01
+    weights = hip.Weights.int8(w, scales)
+    y = run_i8(hip, weights, q, qs, tokens, rows, 0, rows)
+    want = np.zeros((tokens, rows), dtype=np.float32)
+    orc.matmul_rows_i8(w, scales, q, qs, tokens, want, rows, 0, rows)
+    assert np.array_equal(y.view(np.uint32), want.view(np.uint32))
