@@ -35,6 +35,22 @@ HBM_PEAK_GBS = 8000.0
 METRIC = "int8 decode GEMV GB/s (% HBM peak); beam-3 batched decode tokens/sec"
 
 
+PROFILE = os.path.join(ROOT, "profiles", "gemv_i8_decode_m3_k2048_n8192.txt")
+
+
+def measured_traffic() -> int | None:
+    """HBM bytes per launch of the headline GEMV kernel, from the committed
+    rocprofv3 FETCH_SIZE/WRITE_SIZE summary (copy-kernel calibrated)."""
+    try:
+        with open(PROFILE) as f:
+            for line in f:
+                if line.startswith("traffic_bytes_per_launch:"):
+                    return int(line.split(":")[1])
+    except OSError:
+        pass
+    return None
+
+
 def gemv_bytes(m: int, k: int, n: int) -> int:
     """Algorithmic bytes of one int8/g32 GEMV: weights, fp16 scales, int8
     activations + fp32 row scales, fp32 outputs."""
@@ -134,6 +150,25 @@ def cpu_baseline(case: GemvCase, budget_s: float) -> dict:
                       f"over {threads} threads"}
 
 
+def pmc_run(case: GemvCase, launches: int) -> int:
+    """Eager launches for hardware-counter runs (one dispatch each): first a
+    plain 64 MiB device-to-device copy kernel (nhip_copy_dev), whose
+    FETCH_SIZE/WRITE_SIZE calibrate the counters, then `launches` headline
+    GEMVs cycling the weight copies so that each reads its weights from HBM."""
+    nbytes = 64 << 20
+    src, dst = N.DeviceBuffer(nbytes), N.DeviceBuffer(nbytes)
+    src.zero()
+    for _ in range(3):
+        N.check(N.lib().nhip_copy_dev(dst.ptr, src.ptr, nbytes, None))
+    N.check(N.lib().nhip_device_sync())
+    for i in range(launches):
+        case.launch(i)
+    N.check(N.lib().nhip_device_sync())
+    print(f"# pmc run: 3 copies of {nbytes} B, {launches} GEMVs of {case.bytes} algorithmic bytes", file=sys.stderr)
+    case.close()
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -142,6 +177,9 @@ def main() -> int:
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-secondary", action="store_true")
+    ap.add_argument("--pmc-run", type=int, default=0, metavar="LAUNCHES",
+                    help="counter-collection mode: a 64 MiB device copy (the calibration kernel of known size), "
+                         "then LAUNCHES eager headline GEMVs; prints no JSON line")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (got --gpus {args.gpus}); multi-GPU scaling is not part of this "
@@ -151,6 +189,8 @@ def main() -> int:
     print(f"# {N.lib().nhip_describe().decode()}", file=sys.stderr, flush=True)
 
     main_case = GemvCase(3, 2048, 8192, seed=0x1001)
+    if args.pmc_run:
+        return pmc_run(main_case, args.pmc_run)
     ms = main_case.time(args.steps, args.warmup)
     gbs = main_case.bytes / (ms * 1e-3) / 1e9
     print(f"# headline GEMV M=3 K=2048 N=8192: {ms * 1e3:.2f} us/launch, {gbs:.0f} GB/s", file=sys.stderr, flush=True)
@@ -190,7 +230,7 @@ def main() -> int:
                    "group": 32, "weight_copies_cycled": main_case.copies,
                    "bytes_per_step": main_case.bytes},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None},
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": measured_traffic()},
         "cpu_baseline": cpu,
         "secondary": secondary,
     }

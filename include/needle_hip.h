@@ -136,6 +136,9 @@ int32_t nhip_free(void* ptr);
 int32_t nhip_memcpy_htod(void* dst, const void* src, size_t bytes);
 int32_t nhip_memcpy_dtoh(void* dst, const void* src, size_t bytes);
 int32_t nhip_memcpy_dtod(void* dst, const void* src, size_t bytes, void* stream);
+/* Device-to-device copy by a kernel on `stream` (NULL = the library stream);
+ * asynchronous and capturable in a graph.  Used for KV-slot copies. */
+int32_t nhip_copy_dev(void* dst, const void* src, size_t bytes, void* stream);
 int32_t nhip_memset(void* dst, int32_t value, size_t bytes);
 int32_t nhip_stream_create(void** stream);
 int32_t nhip_stream_destroy(void* stream);

@@ -72,6 +72,7 @@ _PROTOS = {
     "nhip_memcpy_htod": (_i32, [_vp, _vp, _sz]),
     "nhip_memcpy_dtoh": (_i32, [_vp, _vp, _sz]),
     "nhip_memcpy_dtod": (_i32, [_vp, _vp, _sz, _vp]),
+    "nhip_copy_dev": (_i32, [_vp, _vp, _sz, _vp]),
     "nhip_memset": (_i32, [_vp, _i32, _sz]),
     "nhip_stream_create": (_i32, [C.POINTER(_vp)]),
     "nhip_stream_destroy": (_i32, [_vp]),

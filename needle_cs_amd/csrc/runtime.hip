@@ -1,5 +1,6 @@
 // runtime.hip -- error channel, device selection, memory/stream/event
 // plumbing and the synthetic workload generators of libneedle_hip.so.
+#include <algorithm>
 #include <cmath>
 #include <cstdarg>
 #include <cstring>
@@ -110,6 +111,21 @@ static uint16_t single_to_half_rne(float f)
 
 using namespace nhip;
 
+namespace {
+
+__global__ void copy_kernel(uint8_t* dst, const uint8_t* src, size_t n16, size_t tail)
+{
+    const size_t stride = (size_t)gridDim.x * blockDim.x;
+    const size_t tid = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    uint4* d4 = reinterpret_cast<uint4*>(dst);
+    const uint4* s4 = reinterpret_cast<const uint4*>(src);
+    for (size_t i = tid; i < n16; i += stride) d4[i] = s4[i];
+    const size_t base = n16 * 16;
+    for (size_t i = tid; i < tail; i += stride) dst[base + i] = src[base + i];
+}
+
+}  // namespace
+
 extern "C" {
 
 const char* nhip_last_error(void) { return g_error; }
@@ -185,6 +201,27 @@ int32_t nhip_memcpy_dtod(void* dst, const void* src, size_t bytes, void* stream)
     int32_t rc = ensure_device();
     if (rc) return rc;
     NHIP_CHECK_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, as_stream(stream)));
+    return NHIP_OK;
+}
+
+// Plain device copy as a kernel on the given stream (capturable in a graph,
+// unlike a DMA copy); 16-byte vectors where both pointers allow, bytes else.
+int32_t nhip_copy_dev(void* dst, const void* src, size_t bytes, void* stream)
+{
+    if (bytes == 0) return NHIP_OK;
+    NHIP_REQUIRE(dst && src, "copy: null pointer");
+    int32_t rc = ensure_device();
+    if (rc) return rc;
+    const bool vec = ((reinterpret_cast<uintptr_t>(dst) | reinterpret_cast<uintptr_t>(src)) & 15) == 0;
+    const size_t n16 = vec ? bytes / 16 : 0;
+    const size_t tail = bytes - n16 * 16;
+    const size_t work = std::max(n16, tail);
+    const int block = 256;
+    const size_t want = (work + block - 1) / block;
+    const int grid = (int)std::min<size_t>(std::max<size_t>(want, 1), 4096);
+    hipLaunchKernelGGL(copy_kernel, dim3(grid), dim3(block), 0, as_stream(stream), static_cast<uint8_t*>(dst),
+                       static_cast<const uint8_t*>(src), n16, tail);
+    NHIP_CHECK_HIP(hipGetLastError());
     return NHIP_OK;
 }
 

@@ -313,3 +313,17 @@ def test_int8_special_scale_patterns(hip, orc, tokens):
     want = np.zeros((tokens, rows), dtype=np.float32)
     orc.matmul_rows_i8(w, scales, q, qs, tokens, want, rows, 0, rows)
     assert np.array_equal(y.view(np.uint32), want.view(np.uint32))
+
+
+@pytest.mark.parametrize("nbytes,off", [(1 << 20, 0), (4096 + 7, 0), (3000, 3), (16, 0), (1, 0)])
+def test_copy_dev(hip, nbytes, off):
+    src = np.random.default_rng(nbytes).integers(0, 256, nbytes + 32, dtype=np.uint8)
+    ds = hip.DeviceBuffer.from_array(src)
+    dd = hip.DeviceBuffer(nbytes + 32)
+    dd.zero()
+    hip.check(hip.lib().nhip_copy_dev(dd.ptr + off, ds.ptr + off, nbytes, None))
+    hip.check(hip.lib().nhip_device_sync())
+    got = dd.download(np.uint8)
+    want = np.zeros(nbytes + 32, dtype=np.uint8)
+    want[off:off + nbytes] = src[off:off + nbytes]
+    assert np.array_equal(got, want)
