@@ -213,6 +213,42 @@ int32_t nhip_group_dots_cq_dev(const nhip_weights* w, const int8_t* d_values, in
                                int32_t row_start, int32_t row_end, int32_t* d_dots,
                                void* stream);
 
+/* ------------------------------------------ decode attention (KV cache) -- */
+
+/* Ragged decode attention over a pooled int8 KV cache (one launch for a
+ * batch of rows from independent slots).  Replaces the per-row
+ * AttentionBatch.Run / ExecuteChunk + MergePartials path
+ * (src/Needle/Blocks.cs:849-966, 750-817) that EngineCore.RunAttentionBatch
+ * drives (src/Needle/Engine.cs:2480-2596).  Layout per layer, as the
+ * reference's KV cache (src/Needle/Engine.cs:127-136, 184-187) with one
+ * region per slot:
+ *   keys   int8 [slots][capacity][kv_heads*qk_dim], key_scales   fp32 [slots][capacity][kv_heads]
+ *   values int8 [slots][capacity][kv_heads*64],     value_scales fp32 [slots][capacity][kv_heads]
+ *   q int8 [rows][heads][qk_dim] with q_scales [rows][heads] (QuantizeInt8
+ *   per head), out fp32 [rows][heads][64].
+ * Row r attends positions row_first[r] .. row_first[r]+row_count[r]-1 of
+ * slot row_slot[r] (device arrays, so a captured graph can be replayed with
+ * new spans); query head h reads kv head h / (heads/kv_heads).  Each (row,
+ * head) is split into at most max_chunks chunks by the reference's plan
+ * (8 reproduces the reference; 64 fills the GPU), each chunk is the
+ * reference tile in partial form and the chunks are merged in
+ * MergePartials' order, with the polynomial Ops.Exp.  Rows whose slot or
+ * span is out of range produce zeros.  qk_dim is 48 or 64, v dim 64,
+ * heads/kv_heads <= 16; q, keys, values and out 16-byte aligned.
+ * The workspace (nhip_attention_decode_workspace bytes) must be zeroed once
+ * with nhip_attention_decode_workspace_init; the kernel leaves it reusable.
+ * Calls that share a workspace must not overlap. */
+size_t nhip_attention_decode_workspace(int32_t rows, int32_t heads, int32_t max_chunks);
+int32_t nhip_attention_decode_workspace_init(void* d_workspace, size_t bytes, void* stream);
+int32_t nhip_attention_decode_dev(const int8_t* d_q, const float* d_q_scales, int32_t rows,
+                                  int32_t heads, int32_t kv_heads, int32_t qk_dim,
+                                  const int8_t* d_keys, const float* d_key_scales,
+                                  const int8_t* d_values, const float* d_value_scales,
+                                  int32_t slots, int32_t capacity, const int32_t* d_row_slot,
+                                  const int32_t* d_row_first, const int32_t* d_row_count,
+                                  int32_t max_chunks, void* d_workspace, size_t workspace_bytes,
+                                  float* d_out, void* stream);
+
 /* ------------------------------------------ synthetic workload inputs -- */
 
 /* Deterministic host-side generators for the benchmark workloads: one

@@ -73,6 +73,10 @@ _PROTOS = {
     "nhip_memcpy_dtoh": (_i32, [_vp, _vp, _sz]),
     "nhip_memcpy_dtod": (_i32, [_vp, _vp, _sz, _vp]),
     "nhip_copy_dev": (_i32, [_vp, _vp, _sz, _vp]),
+    "nhip_attention_decode_workspace": (_sz, [_i32, _i32, _i32]),
+    "nhip_attention_decode_workspace_init": (_i32, [_vp, _sz, _vp]),
+    "nhip_attention_decode_dev": (_i32, [_vp, _vp, _i32, _i32, _i32, _i32, _vp, _vp, _vp, _vp, _i32, _i32, _vp, _vp,
+                                         _vp, _i32, _vp, _sz, _vp, _vp]),
     "nhip_memset": (_i32, [_vp, _i32, _sz]),
     "nhip_stream_create": (_i32, [C.POINTER(_vp)]),
     "nhip_stream_destroy": (_i32, [_vp]),

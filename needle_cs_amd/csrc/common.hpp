@@ -94,4 +94,23 @@ __device__ __forceinline__ float ref_max(float a, float b)
     return a > b ? a : (b > a ? b : (__float_as_uint(a) == 0x80000000u ? b : a));
 }
 
+// Ops.Exp (src/Needle/Ops.cs:16-31), one lane: the reference's polynomial
+// exponential, shared bit-for-bit with the CPU restatement.
+__device__ __forceinline__ float exp_poly(float x)
+{
+    x = fminf(fmaxf(x, -87.3f), 88.7f);
+    const float n = __builtin_rintf(x * 1.44269504f);
+    float r = __builtin_fmaf(-n, 0.693359375f, x);
+    r = __builtin_fmaf(-n, -2.12194440e-4f, r);
+    float p = 1.9875691500e-4f;
+    p = __builtin_fmaf(p, r, 1.3981999507e-3f);
+    p = __builtin_fmaf(p, r, 8.3334519073e-3f);
+    p = __builtin_fmaf(p, r, 4.1665795894e-2f);
+    p = __builtin_fmaf(p, r, 1.6666665459e-1f);
+    p = __builtin_fmaf(p, r, 5.0000001201e-1f);
+    const float y = __builtin_fmaf(p, r * r, r + 1.0f);
+    const float scale = __uint_as_float((uint32_t)((int)n + 127) << 23);
+    return y * scale;
+}
+
 }  // namespace nhip

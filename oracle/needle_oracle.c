@@ -31,6 +31,7 @@
 #include "needle_oracle.h"
 
 #include <math.h>
+#include <stdlib.h>
 #include <string.h>
 #include <float.h>
 
@@ -616,6 +617,86 @@ void or_attention_span(int position, int window, int frames, int* first, int* co
 {
     *first = window == 0 ? 0 : (position - window + 1 > 0 ? position - window + 1 : 0);
     *count = (frames > 0 ? frames - 1 : position) - *first + 1;
+}
+
+/* src/Needle/Blocks.cs:934-938 */
+int or_attention_plan(int count, int max_chunks, int* length)
+{
+    int needed = count / 16;
+    if (needed < 1) needed = 1;
+    if (needed > max_chunks) needed = max_chunks;
+    int len = ((count + needed - 1) / needed + 3) & ~3;
+    *length = len;
+    return (count + len - 1) / len;
+}
+
+/* src/Needle/Blocks.cs:760-815, non-SIMD branch, any count */
+void or_merge_head(const float* outs, int out_stride, const float* peaks, const float* sums,
+                   int stride, int count, float* output, int use_poly)
+{
+    if (count == 2) {
+        float peak0 = peaks[0], peak1 = peaks[stride];
+        float pk = fmax_ref(peak0, peak1);
+        float w0 = exp_sel(peak0 - pk, use_poly);
+        float w1 = exp_sel(peak1 - pk, use_poly);
+        float tot = 0.0f;
+        tot += w0 * sums[0];
+        tot += w1 * sums[stride];
+        float inv = 1.0f / tot;
+        for (int d = 0; d < 64; d++) output[d] = (w0 * outs[d] + w1 * outs[out_stride + d]) * inv;
+        return;
+    }
+    float peak = -INFINITY;
+    for (int c = 0; c < count; c++) peak = fmax_ref(peak, peaks[(long)c * stride]);
+    float total = 0.0f;
+    for (int c = 0; c < count; c++) total += exp_sel(peaks[(long)c * stride] - peak, use_poly) * sums[(long)c * stride];
+    float inverse = 1.0f / total;
+    for (int d = 0; d < 64; d++) {
+        float sum = 0.0f;
+        for (int c = 0; c < count; c++)
+            sum += exp_sel(peaks[(long)c * stride] - peak, use_poly) * outs[(long)c * out_stride + d];
+        output[d] = sum * inverse;
+    }
+}
+
+/* src/Needle/Blocks.cs:927-966 (ExecuteChunk + MergePartials) over a ragged
+ * batch with pooled per-slot caches */
+void or_attention_decode(const int8_t* q, const float* q_scales, int rows, int heads, int kv_heads,
+                         int qk_dim, const int8_t* keys, const float* key_scales,
+                         const int8_t* values, const float* value_scales, int capacity,
+                         const int* row_slot, const int* row_first, const int* row_count,
+                         int max_chunks, float* out)
+{
+    int group = heads / kv_heads;
+    if (max_chunks > 256) max_chunks = 256;
+    float* outs = (float*)malloc(sizeof(float) * 64 * (size_t)max_chunks);
+    float peaks[256], sums[256];
+    for (int r = 0; r < rows; r++) {
+        int count = row_count[r];
+        size_t base = (size_t)row_slot[r] * capacity;
+        for (int h = 0; h < heads; h++) {
+            float* dst = out + ((size_t)r * heads + h) * 64;
+            if (count <= 0) {
+                for (int d = 0; d < 64; d++) dst[d] = 0.0f;
+                continue;
+            }
+            int kv = h / group, length;
+            int chunks = or_attention_plan(count, max_chunks, &length);
+            for (int c = 0; c < chunks; c++) {
+                int begin = c * length;
+                int n = count - begin < length ? count - begin : length;
+                or_attention_partial(q + ((size_t)r * heads + h) * qk_dim, q_scales[(size_t)r * heads + h],
+                                     keys + base * kv_heads * qk_dim + (size_t)kv * qk_dim,
+                                     key_scales + base * kv_heads + kv,
+                                     values + base * kv_heads * 64 + (size_t)kv * 64,
+                                     value_scales + base * kv_heads + kv, kv_heads * qk_dim,
+                                     kv_heads * 64, kv_heads, row_first[r] + begin, n, qk_dim, 1,
+                                     outs + (size_t)c * 64, &peaks[c], &sums[c]);
+            }
+            or_merge_head(outs, 64, peaks, sums, 1, chunks, dst, 1);
+        }
+    }
+    free(outs);
 }
 
 /* ---------------------------------------------------------- selection -- */

@@ -180,6 +180,32 @@ void or_merge_partials_double(const float* partials, int count, int heads, float
 /* src/Needle/Blocks.cs:973-978 */
 void or_attention_span(int position, int window, int frames, int* first, int* count);
 
+/* Position-split plan of AttentionBatch.ExecuteChunk (Blocks.cs:934-938)
+ * with the chunk cap as a parameter (the reference's MaxChunks is 8,
+ * MinChunkPositions 16, Blocks.cs:832-833): returns the chunk count, sets
+ * the chunk length (a multiple of 4). */
+int or_attention_plan(int count, int max_chunks, int* length);
+/* One head's merge of `count` partials in the order of
+ * Attention.MergePartials' non-SIMD branch (Blocks.cs:760-815), any count:
+ * outs [count][out_stride] (64 used), peaks/sums [count] at their strides. */
+void or_merge_head(const float* outs, int out_stride, const float* peaks, const float* sums,
+                   int stride, int count, float* output, int use_poly);
+/* Ragged decode attention over a pooled int8 KV cache:
+ *   keys   int8 [slots][capacity][kv_heads*qk_dim], key_scales   [slots][capacity][kv_heads]
+ *   values int8 [slots][capacity][kv_heads*64],     value_scales [slots][capacity][kv_heads]
+ *   q int8 [rows][heads][qk_dim], q_scales [rows][heads], out [rows][heads][64].
+ * Row r attends positions row_first[r] .. +row_count[r]-1 of slot
+ * row_slot[r]; query head h reads kv head h / (heads/kv_heads).  Each
+ * (row, head) is split by or_attention_plan, every chunk is
+ * or_attention_partial with the polynomial exp, and the chunks are merged by
+ * or_merge_head -- AttentionBatch.ExecuteChunk + MergePartials
+ * (Blocks.cs:927-966) for every row of a ragged batch. */
+void or_attention_decode(const int8_t* q, const float* q_scales, int rows, int heads, int kv_heads,
+                         int qk_dim, const int8_t* keys, const float* key_scales,
+                         const int8_t* values, const float* value_scales, int capacity,
+                         const int* row_slot, const int* row_first, const int* row_count,
+                         int max_chunks, float* out);
+
 /* src/Needle/Ops.cs:1086-1089 (first index of the maximum) */
 int or_argmax(const float* x, int n);
 /* src/Needle/Ops.cs:1092-1221, scalar branch (the double log-sum-exp) */

@@ -78,6 +78,9 @@ _PROTOS = {
     "or_merge_partials": (None, [_vp, _i, _i, _vp, _i]),
     "or_merge_partials_double": (None, [_vp, _i, _i, _vp]),
     "or_attention_span": (None, [_i, _i, _i, C.POINTER(_i), C.POINTER(_i)]),
+    "or_attention_plan": (_i, [_i, _i, C.POINTER(_i)]),
+    "or_merge_head": (None, [_vp, _i, _vp, _vp, _i, _i, _vp, _i]),
+    "or_attention_decode": (None, [_vp, _vp, _i, _i, _i, _i, _vp, _vp, _vp, _vp, _i, _vp, _vp, _vp, _i, _vp]),
     "or_argmax": (_i, [_vp, _i]),
     "or_topk_log_softmax": (None, [_vp, _i, _i, _vp, _vp, _vp, _i]),
     "or_baseline_start": (_i, [_i]),
@@ -192,3 +195,34 @@ def synth_half_uniform(st: C.c_uint64, n: int, lo: float, hi: float) -> np.ndarr
 def half_to_single_array(h: np.ndarray) -> np.ndarray:
     f = lib().or_half_to_single
     return np.array([f(int(v)) for v in h.ravel()], dtype=np.float32).reshape(h.shape)
+
+
+def attention_plan(count: int, max_chunks: int):
+    length = C.c_int(0)
+    chunks = lib().or_attention_plan(count, max_chunks, C.byref(length))
+    return chunks, length.value
+
+
+def attention_decode(q, q_scales, heads, kv_heads, qk, keys, key_scales, values, value_scales, capacity,
+                     row_slot, row_first, row_count, max_chunks):
+    rows = len(row_count)
+    out = np.zeros((rows, heads, 64), dtype=np.float32)
+    arrs = [np.ascontiguousarray(a) for a in (q, q_scales, keys, key_scales, values, value_scales)]
+    ints = [np.ascontiguousarray(a, dtype=np.int32) for a in (row_slot, row_first, row_count)]
+    lib().or_attention_decode(p(arrs[0]), p(arrs[1]), rows, heads, kv_heads, qk, p(arrs[2]), p(arrs[3]),
+                              p(arrs[4]), p(arrs[5]), capacity, p(ints[0]), p(ints[1]), p(ints[2]), max_chunks,
+                              p(out))
+    return out
+
+
+def kv_cache(st, slots: int, capacity: int, kv_heads: int, qk: int):
+    """Pooled int8 KV cache filled from N(0,1) values quantized per (position,
+    kv head) with QuantizeInt8, as Engine.cs:1376-1384 writes it."""
+    kf = np.zeros(slots * capacity * kv_heads * qk, dtype=np.float32)
+    vf = np.zeros(slots * capacity * kv_heads * 64, dtype=np.float32)
+    lib().or_synth_normal(p(kf), kf.size, C.byref(st))
+    lib().or_synth_normal(p(vf), vf.size, C.byref(st))
+    kq, ks = quantize_rows(kf.reshape(-1, qk))
+    vq, vs = quantize_rows(vf.reshape(-1, 64))
+    return (kq.reshape(slots, capacity, kv_heads * qk), ks.reshape(slots, capacity, kv_heads),
+            vq.reshape(slots, capacity, kv_heads * 64), vs.reshape(slots, capacity, kv_heads))

@@ -1,0 +1,131 @@
+"""GPU parity of the ragged decode attention over a pooled int8 KV cache
+(nhip_attention_decode_dev) against the oracle's restatement of
+AttentionBatch.ExecuteChunk + MergePartials (src/Needle/Blocks.cs:927-966,
+750-817): bit-exact, because the chunk plan, the per-chunk sums (ascending
+positions), the merge order and the polynomial exp are the same."""
+import ctypes as C
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+
+class Cache:
+    def __init__(self, orc, hip, seed, slots, capacity, kv_heads, qk):
+        st = orc.state(seed)
+        self.slots, self.capacity, self.kv_heads, self.qk = slots, capacity, kv_heads, qk
+        self.keys, self.ks, self.values, self.vs = orc.kv_cache(st, slots, capacity, kv_heads, qk)
+        self.st = st
+        self.d = [hip.DeviceBuffer.from_array(a) for a in (self.keys, self.ks, self.values, self.vs)]
+
+
+def run_decode(hip, cache, q, qs, heads, rows_spec, max_chunks, ws=None, out=None):
+    slot, first, count = (np.array(x, dtype=np.int32) for x in zip(*rows_spec))
+    rows = len(rows_spec)
+    dq, dqs = hip.DeviceBuffer.from_array(q), hip.DeviceBuffer.from_array(qs)
+    dsl, dfi, dco = (hip.DeviceBuffer.from_array(a) for a in (slot, first, count))
+    if ws is None:
+        nbytes = hip.lib().nhip_attention_decode_workspace(rows, heads, max_chunks)
+        ws = hip.DeviceBuffer(nbytes)
+        hip.check(hip.lib().nhip_attention_decode_workspace_init(ws.ptr, ws.nbytes, None))
+    if out is None:
+        out = hip.DeviceBuffer(rows * heads * 64 * 4)
+    k, ks, v, vs = cache.d
+    hip.check(hip.lib().nhip_attention_decode_dev(dq.ptr, dqs.ptr, rows, heads, cache.kv_heads, cache.qk, k.ptr, ks.ptr,
+                                                  v.ptr, vs.ptr, cache.slots, cache.capacity, dsl.ptr, dfi.ptr,
+                                                  dco.ptr, max_chunks, ws.ptr, ws.nbytes, out.ptr, None))
+    return out.download(np.float32).reshape(rows, heads, 64), ws
+
+
+def oracle_decode(orc, cache, q, qs, heads, rows_spec, max_chunks):
+    slot, first, count = (np.array(x, dtype=np.int32) for x in zip(*rows_spec))
+    return orc.attention_decode(q, qs, heads, cache.kv_heads, cache.qk, cache.keys, cache.ks, cache.values, cache.vs,
+                                cache.capacity, slot, first, count, max_chunks)
+
+
+def queries(orc, st, rows, heads, qk):
+    qf = orc.synth_normal(st, rows * heads * qk).reshape(rows * heads, qk)
+    q, qs = orc.quantize_rows(qf)
+    return q, qs
+
+
+def bit_equal(a, b):
+    return np.array_equal(a.view(np.uint32), b.view(np.uint32))
+
+
+@pytest.mark.parametrize("heads,kv_heads,qk", [(16, 16, 64), (12, 2, 48), (4, 1, 64), (8, 8, 48)])
+@pytest.mark.parametrize("max_chunks", [8, 64])
+def test_decode_attention_bit_exact(hip, orc, heads, kv_heads, qk, max_chunks):
+    cache = Cache(orc, hip, 1000 + heads + kv_heads + qk, 4, 2048, kv_heads, qk)
+    spec = [(0, 0, 1), (1, 0, 2), (2, 5, 3), (3, 0, 16), (0, 7, 17), (1, 100, 31), (2, 0, 32), (3, 0, 33),
+            (0, 1000, 100), (1, 0, 257), (2, 1048, 1000), (3, 0, 2048), (1, 2047, 1), (0, 64, 64)]
+    q, qs = queries(orc, cache.st, len(spec), heads, qk)
+    got, _ = run_decode(hip, cache, q, qs, heads, spec, max_chunks)
+    want = oracle_decode(orc, cache, q, qs, heads, spec, max_chunks)
+    assert bit_equal(got, want)
+
+
+def test_decode_attention_invalid_rows_are_zero(hip, orc):
+    cache = Cache(orc, hip, 42, 2, 256, 2, 64)
+    heads = 4
+    spec = [(0, 0, 10), (5, 0, 10), (1, 250, 10), (1, -1, 5), (0, 0, 0), (1, 0, 256)]
+    q, qs = queries(orc, cache.st, len(spec), heads, 64)
+    got, _ = run_decode(hip, cache, q, qs, heads, spec, 64)
+    want = oracle_decode(orc, cache, q, qs, heads, [(0, 0, 10), (0, 0, 0), (0, 0, 0), (0, 0, 0), (0, 0, 0),
+                                                    (1, 0, 256)], 64)
+    assert bit_equal(got[[0, 5]], want[[0, 5]])
+    assert np.all(got[1:5] == 0.0)
+
+
+def test_decode_attention_workspace_reuse(hip, orc):
+    """The merge resets its arrival counters: repeated calls on one workspace
+    stay exact, also with new spans."""
+    cache = Cache(orc, hip, 7, 3, 1024, 4, 64)
+    heads = 8
+    rng = np.random.default_rng(5)
+    ws = out = None
+    for it in range(4):
+        spec = [(int(rng.integers(0, 3)), 0, int(rng.integers(1, 1025))) for _ in range(9)]
+        q, qs = queries(orc, cache.st, len(spec), heads, 64)
+        got, ws = run_decode(hip, cache, q, qs, heads, spec, 64, ws=ws)
+        assert bit_equal(got, oracle_decode(orc, cache, q, qs, heads, spec, 64)), it
+
+
+def test_decode_attention_graph_replays(hip, orc):
+    """Captured once, replayed with new spans written to the device arrays
+    between replays (the decode loop's pattern); every replay is exact."""
+    cache = Cache(orc, hip, 99, 4, 512, 2, 48)
+    heads, rows, mc = 12, 6, 64
+    q, qs = queries(orc, cache.st, rows, heads, 48)
+    dq, dqs = hip.DeviceBuffer.from_array(q), hip.DeviceBuffer.from_array(qs)
+    dsl, dfi, dco = (hip.DeviceBuffer(rows * 4) for _ in range(3))
+    ws = hip.DeviceBuffer(hip.lib().nhip_attention_decode_workspace(rows, heads, mc))
+    hip.check(hip.lib().nhip_attention_decode_workspace_init(ws.ptr, ws.nbytes, None))
+    out = hip.DeviceBuffer(rows * heads * 64 * 4)
+    k, ks, v, vs = cache.d
+    stream = hip.Stream()
+    with hip.Graph.capture(stream) as g:
+        hip.check(hip.lib().nhip_attention_decode_dev(dq.ptr, dqs.ptr, rows, heads, 2, 48, k.ptr, ks.ptr, v.ptr, vs.ptr,
+                                                      4, 512, dsl.ptr, dfi.ptr, dco.ptr, mc, ws.ptr, ws.nbytes,
+                                                      out.ptr, stream.ptr))
+    for rep in range(4):
+        spec = [(r % 4, 0, 20 + 83 * rep + 37 * r) for r in range(rows)]
+        for buf, col in zip((dsl, dfi, dco), zip(*spec)):
+            buf.upload(np.array(col, dtype=np.int32))
+        g.launch()
+        stream.sync()
+        got = out.download(np.float32).reshape(rows, heads, 64)
+        assert bit_equal(got, oracle_decode(orc, cache, q, qs, heads, spec, mc)), rep
+    g.close()
+
+
+def test_decode_attention_rejects_bad_shapes(hip, orc):
+    lib = hip.lib()
+    buf = hip.DeviceBuffer(1 << 16)
+    p = buf.ptr
+    assert lib.nhip_attention_decode_dev(p, p, 1, 6, 4, 64, p, p, p, p, 1, 16, p, p, p, 8, p, buf.nbytes, p, None) != 0
+    assert lib.nhip_attention_decode_dev(p, p, 1, 4, 4, 32, p, p, p, p, 1, 16, p, p, p, 8, p, buf.nbytes, p, None) != 0
+    assert lib.nhip_attention_decode_dev(p, p, 1, 4, 4, 64, p, p, p, p, 1, 8192, p, p, p, 8, p, buf.nbytes, p,
+                                         None) != 0
+    assert "max_chunks" in hip.last_error()

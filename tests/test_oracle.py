@@ -383,6 +383,69 @@ def test_split_partials_merge_to_whole(orc, pieces):
     assert np.max(np.abs(merged_libm - ref)) <= 1e-6 * max(1.0, np.max(np.abs(ref)))
 
 
+def test_attention_plan_known_values_and_invariants(orc):
+    """AttentionBatch.ExecuteChunk's split (src/Needle/Blocks.cs:934-938)."""
+    assert orc.attention_plan(2048, 8) == (8, 256)
+    assert orc.attention_plan(40, 8) == (2, 20)
+    assert orc.attention_plan(17, 8) == (1, 20)
+    assert orc.attention_plan(33, 8) == (2, 20)
+    assert orc.attention_plan(1, 8) == (1, 4)
+    for count in range(1, 3000, 7):
+        for cap in (1, 8, 64):
+            chunks, length = orc.attention_plan(count, cap)
+            assert length % 4 == 0 and 1 <= chunks <= cap
+            assert (chunks - 1) * length < count <= chunks * length
+
+
+@pytest.mark.parametrize("count", [1, 2, 3, 5, 8])
+def test_merge_head_equals_merge_partials(orc, count):
+    """The any-count merge keeps MergePartials' arithmetic for counts <= 8."""
+    st = orc.state(77 + count)
+    PF, heads = 6 * 64 + 16, 3
+    partials = np.zeros(count * PF, dtype=np.float32)
+    for c in range(count):
+        partials[c * PF:c * PF + heads * 64] = orc.synth_normal(st, heads * 64)
+        partials[c * PF + 384:c * PF + 384 + heads] = orc.synth_normal(st, heads) * 3
+        partials[c * PF + 392:c * PF + 392 + heads] = np.abs(orc.synth_normal(st, heads)) * 10 + 1
+    want = np.zeros(heads * 64, dtype=np.float32)
+    orc.lib().or_merge_partials(orc.p(partials), count, heads, orc.p(want), 1)
+    for h in range(heads):
+        got = np.zeros(64, dtype=np.float32)
+        orc.lib().or_merge_head(orc.p(partials[h * 64:]), PF, orc.p(partials[384 + h:]), orc.p(partials[392 + h:]),
+                                PF, count, orc.p(got), 1)
+        assert np.array_equal(got.view(np.uint32), want[h * 64:(h + 1) * 64].view(np.uint32))
+
+
+@pytest.mark.parametrize("heads,kv_heads,qk,max_chunks", [(4, 4, 64, 8), (6, 2, 48, 64), (4, 1, 64, 1)])
+def test_attention_decode_against_float64(orc, heads, kv_heads, qk, max_chunks):
+    """Ragged decode attention: softmax((q.k) * scales / sqrt(qk)) . v in
+    float64 from the same int8 values, per row of a pooled cache."""
+    st = orc.state(heads * 100 + qk + max_chunks)
+    slots, capacity = 3, 300
+    keys, ks, values, vs = orc.kv_cache(st, slots, capacity, kv_heads, qk)
+    rows = 5
+    row_slot = np.array([0, 2, 1, 2, 0], dtype=np.int32)
+    row_first = np.array([0, 10, 0, 250, 3], dtype=np.int32)
+    row_count = np.array([1, 37, 300, 50, 129], dtype=np.int32)
+    qf = orc.synth_normal(st, rows * heads * qk).reshape(rows * heads, qk)
+    q, qs = orc.quantize_rows(qf)
+    out = orc.attention_decode(q, qs, heads, kv_heads, qk, keys, ks, values, vs, capacity, row_slot, row_first,
+                               row_count, max_chunks)
+    group = heads // kv_heads
+    for r in range(rows):
+        sl, f, n = row_slot[r], row_first[r], row_count[r]
+        for h in range(heads):
+            kv = h // group
+            K = keys[sl, f:f + n, kv * qk:(kv + 1) * qk].astype(np.float64)
+            V = values[sl, f:f + n, kv * 64:(kv + 1) * 64].astype(np.float64)
+            dots = K @ q[r * heads + h].astype(np.float64)
+            sc = dots * ks[sl, f:f + n, kv] * qs[r * heads + h] / np.sqrt(qk)
+            p = np.exp(sc - sc.max())
+            p /= p.sum()
+            want = (p * vs[sl, f:f + n, kv]) @ V
+            assert np.max(np.abs(out[r, h] - want)) <= 2e-5 * max(1e-3, np.max(np.abs(want)))
+
+
 def test_attention_span(orc):
     f, c = C.c_int(), C.c_int()
     for pos, window, frames, want in [(10, 0, 0, (0, 11)), (10, 4, 0, (7, 4)), (2, 4, 0, (0, 3)),
