@@ -109,6 +109,66 @@ class GemvCase:
             w.close()
 
 
+class AttnCase:
+    """Ragged decode attention: 16 sequences, context lengths U[32, 2048]
+    (seeded), 16 heads x 64 (qk 64, MHA), int8 KV cache quantized per
+    (position, head) from N(0,1), scale 1/sqrt(64), fp32 output [16,16,64].
+    `copies` pooled caches are cycled so that every launch reads HBM."""
+
+    def __init__(self, seed: int, rows: int = 16, heads: int = 16, qk: int = 64, capacity: int = 2048,
+                 copies: int = 4, max_chunks: int = 64):
+        self.rows, self.heads, self.qk, self.capacity, self.max_chunks = rows, heads, qk, capacity, max_chunks
+        st = C.c_uint64(seed)
+        counts = []
+        for _ in range(rows):
+            u = N.synth_uniform(st, 1, 0.0, 1.0)[0]
+            counts.append(32 + min(int(u * (2048 - 32 + 1)), 2048 - 32))
+        self.counts = np.array(counts, dtype=np.int32)
+        slots = rows
+        per_pos = heads * qk + heads * 4 + heads * 64 + heads * 4
+        n_k, n_v = slots * capacity * heads * qk, slots * capacity * heads * 64
+        self.caches = []
+        kf = N.DeviceBuffer.from_array(N.synth_normal(st, n_k))
+        vf = N.DeviceBuffer.from_array(N.synth_normal(st, n_v))
+        for c in range(copies):
+            k, ks = N.DeviceBuffer(n_k), N.DeviceBuffer(n_k // qk * 4)
+            v, vs = N.DeviceBuffer(n_v), N.DeviceBuffer(n_v // 64 * 4)
+            if c == 0:
+                N.check(N.lib().nhip_quantize_rows_dev(kf.ptr, n_k // qk, qk, k.ptr, ks.ptr, None))
+                N.check(N.lib().nhip_quantize_rows_dev(vf.ptr, n_v // 64, 64, v.ptr, vs.ptr, None))
+            else:
+                for dst, src in zip((k, ks, v, vs), self.caches[0]):
+                    N.check(N.lib().nhip_copy_dev(dst.ptr, src.ptr, src.nbytes, None))
+            self.caches.append((k, ks, v, vs))
+        kf.close()
+        vf.close()
+        qf = N.DeviceBuffer.from_array(N.synth_normal(st, rows * heads * qk))
+        self.dq, self.dqs = N.DeviceBuffer(rows * heads * qk), N.DeviceBuffer(rows * heads * 4)
+        N.check(N.lib().nhip_quantize_rows_dev(qf.ptr, rows * heads, qk, self.dq.ptr, self.dqs.ptr, None))
+        self.slot = N.DeviceBuffer.from_array(np.arange(rows, dtype=np.int32))
+        self.first = N.DeviceBuffer.from_array(np.zeros(rows, dtype=np.int32))
+        self.count = N.DeviceBuffer.from_array(self.counts)
+        self.ws = N.DeviceBuffer(N.lib().nhip_attention_decode_workspace(rows, heads, max_chunks))
+        N.check(N.lib().nhip_attention_decode_workspace_init(self.ws.ptr, self.ws.nbytes, None))
+        self.out = N.DeviceBuffer(rows * heads * 64 * 4)
+        self.copies = copies
+        self.bytes = int(self.counts.sum()) * per_pos + rows * heads * (qk + 4) + rows * heads * 64 * 4
+
+    def launch(self, i: int) -> None:
+        k, ks, v, vs = self.caches[i % self.copies]
+        N.check(N.lib().nhip_attention_decode_dev(self.dq.ptr, self.dqs.ptr, self.rows, self.heads, self.heads,
+                                                  self.qk, k.ptr, ks.ptr, v.ptr, vs.ptr, self.rows, self.capacity,
+                                                  self.slot.ptr, self.first.ptr, self.count.ptr, self.max_chunks,
+                                                  self.ws.ptr, self.ws.nbytes, self.out.ptr, None))
+
+    time = GemvCase.time
+
+    def close(self) -> None:
+        for c in self.caches:
+            for b in c:
+                b.close()
+
+
 def physical_cores() -> int:
     try:
         import subprocess
@@ -207,6 +267,18 @@ def main() -> int:
             print(f"# GEMV M={m} K={k} N={n}: {t * 1e3:.2f} us/launch, {g:.0f} GB/s", file=sys.stderr, flush=True)
             case.close()
 
+    attention = None
+    if not args.no_secondary:
+        case = AttnCase(seed=0x3003)
+        t = case.time(max(200, args.steps // 4), args.warmup)
+        g = case.bytes / (t * 1e-3) / 1e9
+        attention = {"workload": "ragged decode attention, 16 seqs ctx U[32,2048] (sum %d), 16 heads x 64, int8 KV"
+                                 % int(case.counts.sum()),
+                     "us_per_launch": round(t * 1e3, 3), "GB/s": round(g, 1), "frac_hbm_peak": round(g / HBM_PEAK_GBS, 4),
+                     "bytes_per_launch": case.bytes, "max_chunks": case.max_chunks}
+        print(f"# attention: {t * 1e3:.2f} us/launch, {g:.0f} GB/s over {case.bytes} B", file=sys.stderr, flush=True)
+        case.close()
+
     cpu = None
     if not args.no_cpu:
         cpu = cpu_baseline(main_case, args.cpu_seconds)
@@ -233,6 +305,7 @@ def main() -> int:
                      "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": measured_traffic()},
         "cpu_baseline": cpu,
         "secondary": secondary,
+        "attention": attention,
     }
     main_case.close()
     print(json.dumps(line), flush=True)

@@ -235,9 +235,10 @@ int32_t nhip_group_dots_cq_dev(const nhip_weights* w, const int8_t* d_values, in
  * MergePartials' order, with the polynomial Ops.Exp.  Rows whose slot or
  * span is out of range produce zeros.  qk_dim is 48 or 64, v dim 64,
  * heads/kv_heads <= 16; q, keys, values and out 16-byte aligned.
- * The workspace (nhip_attention_decode_workspace bytes) must be zeroed once
- * with nhip_attention_decode_workspace_init; the kernel leaves it reusable.
- * Calls that share a workspace must not overlap. */
+ * The workspace (nhip_attention_decode_workspace bytes) holds the chunk
+ * partials; it needs no initialisation (nhip_attention_decode_workspace_init
+ * zeroes it, for callers that want defined contents).  Calls that share a
+ * workspace must not overlap. */
 size_t nhip_attention_decode_workspace(int32_t rows, int32_t heads, int32_t max_chunks);
 int32_t nhip_attention_decode_workspace_init(void* d_workspace, size_t bytes, void* stream);
 int32_t nhip_attention_decode_dev(const int8_t* d_q, const float* d_q_scales, int32_t rows,

@@ -20,10 +20,11 @@
 // and forms the int32 dots of every query head of the group with v_dot4.
 // Phase 4 gives one thread per (head, 4 value dims), which walks the chunk's
 // positions in order, reading one value dword per position (a wave covers 4
-// heads x 64 dims = 256 contiguous bytes of a cache row).  The last
-// workgroup of a (row, head block) to finish merges the partials; its
-// arrival counter is reset to zero by the merger, so the workspace needs
-// zeroing only once.
+// heads x 64 dims = 256 contiguous bytes of a cache row).  A second kernel
+// merges each (row, head block)'s partials with one thread per (head, dim);
+// the kernel boundary makes the partials visible across XCDs (an in-kernel
+// last-arrival merge would need an L2 writeback and invalidate per
+// workgroup).
 #include <algorithm>
 
 #include "common.hpp"
@@ -44,7 +45,6 @@ struct DecodeAttnParams {
     const int32_t* row_slot;
     const int32_t* row_first;
     const int32_t* row_count;
-    int32_t* arrivals;      // [rows][head_blocks]
     float* peaks;           // [rows][max_chunks][heads]
     float* sums;            // [rows][max_chunks][heads]
     float* partials;        // [rows][max_chunks][heads][64]
@@ -62,10 +62,29 @@ __device__ __forceinline__ int plan(int count, int max_chunks, int* length)
     return (count + len - 1) / len;
 }
 
+// n / d for d in [1, 256] and n < 2^24, with mag = magic(d): multiply-high
+// by ceil(2^32 / d) (d == 1, whose multiplier does not fit, passes n through)
+__device__ __forceinline__ uint32_t magic(uint32_t d) { return d == 1 ? 0u : 0xFFFFFFFFu / d + 1u; }
+__device__ __forceinline__ int fast_div(int n, uint32_t mag) { return mag ? (int)__umulhi((uint32_t)n, mag) : n; }
+
+// Unsigned keys in the order of the floats (-0 below +0, as MathF.Max
+// prefers +0): max over keys is max over values, in any order.
+__device__ __forceinline__ uint32_t order_key(float x)
+{
+    const uint32_t u = __float_as_uint(x);
+    return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+__device__ __forceinline__ float order_value(uint32_t k)
+{
+    return __uint_as_float((k & 0x80000000u) ? (k & 0x7FFFFFFFu) : ~k);
+}
+
 __device__ __forceinline__ float sx8(uint32_t v, int b)
 {
     return static_cast<float>(static_cast<int32_t>(v << (24 - 8 * b)) >> 24);
 }
+
+constexpr int kVBlock = 32;  // value dwords per thread loaded together
 
 __global__ __launch_bounds__(kThreads) void decode_attention_kernel(DecodeAttnParams p)
 {
@@ -82,25 +101,18 @@ __global__ __launch_bounds__(kThreads) void decode_attention_kernel(DecodeAttnPa
     const int lmax = p.lmax;
 
     int8_t* q_lds = reinterpret_cast<int8_t*>(lds);                        // [16][64]
-    float* score = reinterpret_cast<float*>(lds + kMaxHeadsPerBlock * 64);  // [16][lmax]
-    float* ew = score + kMaxHeadsPerBlock * lmax;                           // [16][lmax]
-    float* ww = ew + kMaxHeadsPerBlock * lmax;                              // [16][lmax]
-    float* peak_lds = ww + kMaxHeadsPerBlock * lmax;                        // [16]
-    __shared__ int last_flag;
+    float* score = reinterpret_cast<float*>(lds + kMaxHeadsPerBlock * 64);  // [16][lmax], then e_s
+    float* vsc = score + kMaxHeadsPerBlock * lmax;                          // [16 kv][lmax]
+    float* wl = vsc + kMaxHeadsPerBlock * lmax;                             // [16][lmax] e_s * valueScale_s
+    float* qs_lds = wl + kMaxHeadsPerBlock * lmax;                          // [16]
+    uint32_t* peak_key = reinterpret_cast<uint32_t*>(qs_lds + kMaxHeadsPerBlock);  // [16]
 
     const int slot = p.row_slot[row];
     const int first = p.row_first[row];
-    int count = p.row_count[row];
+    const int count = p.row_count[row];
     // rows with an invalid slot or span produce zeros (no out-of-range reads)
     const bool valid = slot >= 0 && slot < p.slots && first >= 0 && count >= 1 && count <= p.capacity - first;
-    if (!valid) {
-        if (chunk == 0 && tid < nh * 16) {
-            const int h = h0 + tid / 16;
-            float4* o = reinterpret_cast<float4*>(p.out + ((size_t)row * p.heads + h) * 64 + 4 * (tid % 16));
-            *o = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-        }
-        return;
-    }
+    if (!valid) return;  // the merge writes zeros
     int length;
     const int needed = plan(count, p.max_chunks, &length);
     if (chunk >= needed) return;
@@ -110,164 +122,225 @@ __global__ __launch_bounds__(kThreads) void decode_attention_kernel(DecodeAttnPa
     const int qk = p.qk;
     const int q4 = qk / 4;
 
-    // stage the query heads of this block (nh * qk bytes, dword-granular)
-    {
-        const uint32_t* src = reinterpret_cast<const uint32_t*>(p.q + ((size_t)row * p.heads + h0) * qk);
-        uint32_t* dst = reinterpret_cast<uint32_t*>(q_lds);
-        for (int i = tid; i < nh * q4; i += kThreads) dst[(i / q4) * 16 + (i % q4)] = src[i];
-    }
-    __syncthreads();
+    // Loads are issued oldest-first in the order they are consumed (the
+    // vector memory counter retires in order): the query heads and scales,
+    // this thread's value dwords of the first kVBlock positions (phase 4),
+    // then the first pass of key rows and scales (phase 1).
+    const uint32_t qword = tid < nh * q4
+        ? reinterpret_cast<const uint32_t*>(p.q + ((size_t)row * p.heads + h0) * qk)[tid] : 0u;
+    const float qsc = tid < nh ? p.qscale[(size_t)row * p.heads + h0 + tid] : 0.0f;
 
-    // phase 1: scores, one thread per (kv head, position)
-    for (int it = tid; it < nkv * L; it += kThreads) {
-        const int kvl = it / L;
-        const int s = it - kvl * L;
-        const int kv = kv0 + kvl;
-        const uint4* krow = reinterpret_cast<const uint4*>(p.keys + ((pos0 + s) * p.kv_heads + kv) * qk);
-        uint4 kr[4];
-        kr[0] = krow[0];
-        kr[1] = krow[1];
-        kr[2] = krow[2];
-        kr[3] = qk == 64 ? krow[3] : make_uint4(0, 0, 0, 0);
-        const float ks = p.kscale[(pos0 + s) * p.kv_heads + kv];
-        for (int g = 0; g < group; g++) {
-            const int hl = kvl * group + g;
-            const uint4* qv = reinterpret_cast<const uint4*>(q_lds + hl * 64);
-            int dot = 0;
+    const bool vthread = tid < nh * 16;
+    const int vhl = vthread ? tid >> 4 : 0;
+    const int vqd = tid & 15;
+    const size_t vstride4 = (size_t)p.kv_heads * 16;  // dwords per cache position
+    const uint32_t* vp = reinterpret_cast<const uint32_t*>(p.values) +
+                         (pos0 * p.kv_heads + kv0 + vhl / group) * 16 + vqd;
+    uint32_t vreg[kVBlock];
 #pragma unroll
-            for (int j = 0; j < 4; j++) {
-                const uint4 a = j < 3 || qk == 64 ? qv[j] : make_uint4(0, 0, 0, 0);
-                dot = __builtin_amdgcn_sdot4((int)a.x, (int)kr[j].x, dot, false);
-                dot = __builtin_amdgcn_sdot4((int)a.y, (int)kr[j].y, dot, false);
-                dot = __builtin_amdgcn_sdot4((int)a.z, (int)kr[j].z, dot, false);
-                dot = __builtin_amdgcn_sdot4((int)a.w, (int)kr[j].w, dot, false);
+    for (int j = 0; j < kVBlock; j++) vreg[j] = vp[(size_t)min(j, L - 1) * vstride4];
+
+    // phase 1: scores.  The chunk's key rows for this head block are read as
+    // 16-byte units, four consecutive lanes per (position, kv head) -- a wave
+    // instruction covers 1 KB of consecutive cache rows (768 B for qk 48,
+    // whose fourth lane idles).  Each lane dots its 16 bytes with the query
+    // heads of the group (v_dot4) and the four partial int32 sums are added
+    // across the lanes (exact).
+    const int units = L * nkv * 4;
+    const int pieces = qk / 16;
+    const int lslot = tid & 3;
+    const int qslot = min(lslot, pieces - 1);
+    const uint32_t mag_kv = magic((uint32_t)nkv);
+    const uint32_t mag_l = magic((uint32_t)L);
+    constexpr int KU = 8;  // units per thread per pass, loads issued together
+    auto pass = [&](int base) {
+        uint4 kw[KU];
+        float ksv[KU], vsv[KU];
+#pragma unroll
+        for (int k = 0; k < KU; k++) {
+            const int u = min(base + k * kThreads + tid, units - 1);
+            const int w = u >> 2;
+            const int s = fast_div(w, mag_kv);
+            const int kvl = w - s * nkv;
+            const size_t cell = (pos0 + s) * p.kv_heads + kv0 + kvl;
+            kw[k] = *reinterpret_cast<const uint4*>(p.keys + cell * qk + 16 * qslot);
+            ksv[k] = p.kscale[cell];
+            vsv[k] = p.vscale[cell];
+        }
+        if (base == 0) {  // stage the query heads and scales behind the first loads
+            if (tid < nh * q4) reinterpret_cast<uint32_t*>(q_lds)[(tid / q4) * 16 + (tid % q4)] = qword;
+            if (tid < nh) {
+                qs_lds[tid] = qsc * p.inv_sqrt;
+                peak_key[tid] = order_key(-INFINITY);
             }
-            const float scale = p.qscale[(size_t)row * p.heads + h0 + hl] * p.inv_sqrt;
-            score[hl * lmax + s] = (static_cast<float>(dot) * ks) * scale;
+            __syncthreads();
         }
-    }
+#pragma unroll
+        for (int k = 0; k < KU; k++) {
+            const int u = base + k * kThreads + tid;
+            if (base + k * kThreads >= units) break;  // uniform
+            const bool ok = u < units;  // whole aligned 4-lane groups
+            const int w = min(u, units - 1) >> 2;
+            const int s = fast_div(w, mag_kv);
+            const int kvl = w - s * nkv;
+            for (int g = 0; g < group; g++) {
+                const int hl = kvl * group + g;
+                const uint4 qv = *reinterpret_cast<const uint4*>(q_lds + hl * 64 + 16 * qslot);
+                int part = 0;
+                part = __builtin_amdgcn_sdot4((int)qv.x, (int)kw[k].x, part, false);
+                part = __builtin_amdgcn_sdot4((int)qv.y, (int)kw[k].y, part, false);
+                part = __builtin_amdgcn_sdot4((int)qv.z, (int)kw[k].z, part, false);
+                part = __builtin_amdgcn_sdot4((int)qv.w, (int)kw[k].w, part, false);
+                part = lslot < pieces ? part : 0;
+                // sum over the aligned 4-lane group: quad permutations [1,0,3,2]
+                // and [2,3,0,1] (DPP, no LDS round trip)
+                part += __builtin_amdgcn_mov_dpp(part, 0xB1, 0xF, 0xF, false);
+                part += __builtin_amdgcn_mov_dpp(part, 0x4E, 0xF, 0xF, false);
+                if (ok && lslot == 0) {
+                    const float sc = (static_cast<float>(part) * ksv[k]) * qs_lds[hl];
+                    score[hl * lmax + s] = sc;
+                    atomicMax(&peak_key[hl], order_key(sc));  // the chunk peak (max is order-free)
+                }
+            }
+            if (ok && lslot == 1) vsc[kvl * lmax + s] = vsv[k];
+        }
+    };
+    pass(0);  // peeled: the common case (units <= KU * 256) is straight-line code
+    for (int base = KU * kThreads; base < units; base += KU * kThreads) pass(base);
     __syncthreads();
 
-    // phase 2: per-head peak (max is order-independent; +0 preferred over -0)
-    {
-        const int wave = tid >> 6, lane = tid & 63;
-        for (int hl = wave; hl < nh; hl += kThreads / 64) {
-            float m = -INFINITY;
-            for (int s = lane; s < L; s += 64) m = ref_max(m, score[hl * lmax + s]);
-            for (int off = 32; off > 0; off >>= 1) m = ref_max(m, __shfl_xor(m, off));
-            if (lane == 0) peak_lds[hl] = m;
-        }
-    }
-    __syncthreads();
-
-    // phase 3: e_s and e_s * valueScale_s
+    // phase 3: e_s = Exp(score_s - peak) and e_s * valueScale_s
     for (int it = tid; it < nh * L; it += kThreads) {
-        const int hl = it / L;
+        const int hl = fast_div(it, mag_l);
         const int s = it - hl * L;
-        const int kv = kv0 + hl / group;
-        const float e = exp_poly(score[hl * lmax + s] - peak_lds[hl]);
-        ew[hl * lmax + s] = e;
-        ww[hl * lmax + s] = e * p.vscale[(pos0 + s) * p.kv_heads + kv];
+        const float e = exp_poly(score[hl * lmax + s] - order_value(peak_key[hl]));
+        score[hl * lmax + s] = e;
+        wl[hl * lmax + s] = e * vsc[(hl / group) * lmax + s];
     }
     __syncthreads();
 
     // phase 4: one thread per (head, 4 dims), positions in ascending order
     const size_t pbase = ((size_t)row * p.max_chunks + chunk) * p.heads;
-    if (tid < nh * 16) {
-        const int hl = tid >> 4;
-        const int qd = tid & 15;
-        const int kv = kv0 + hl / group;
-        const size_t vstride = (size_t)p.kv_heads * 64;
-        const uint32_t* vp = reinterpret_cast<const uint32_t*>(p.values + (pos0 * p.kv_heads + kv) * 64 + 4 * qd);
+    if (vthread) {
+        const int hl = vhl;
         float o0 = 0.0f, o1 = 0.0f, o2 = 0.0f, o3 = 0.0f, total = 0.0f;
-        int s = 0;
-        for (; s + 8 <= L; s += 8) {
-            uint32_t v[8];
-#pragma unroll
-            for (int j = 0; j < 8; j++) v[j] = vp[(size_t)(s + j) * (vstride / 4)];
-#pragma unroll
-            for (int j = 0; j < 8; j++) {
-                const float w = ww[hl * lmax + s + j];
-                total = total + ew[hl * lmax + s + j];
-                o0 = o0 + w * sx8(v[j], 0);
-                o1 = o1 + w * sx8(v[j], 1);
-                o2 = o2 + w * sx8(v[j], 2);
-                o3 = o3 + w * sx8(v[j], 3);
-            }
-        }
-        for (; s < L; s++) {
-            const uint32_t v = vp[(size_t)s * (vstride / 4)];
-            const float w = ww[hl * lmax + s];
-            total = total + ew[hl * lmax + s];
+        auto step = [&](float e, float w, uint32_t v) {
+            total = total + e;
             o0 = o0 + w * sx8(v, 0);
             o1 = o1 + w * sx8(v, 1);
             o2 = o2 + w * sx8(v, 2);
             o3 = o3 + w * sx8(v, 3);
+        };
+        for (int s0 = 0; s0 < L; s0 += kVBlock) {
+            if (s0 > 0) {
+#pragma unroll
+                for (int j = 0; j < kVBlock; j++) vreg[j] = vp[(size_t)min(s0 + j, L - 1) * vstride4];
+            }
+#pragma unroll
+            for (int j4 = 0; j4 < kVBlock; j4 += 4) {
+                if (s0 + j4 >= L) break;  // uniform
+                const float4 e4 = *reinterpret_cast<const float4*>(score + hl * lmax + s0 + j4);
+                const float4 w4 = *reinterpret_cast<const float4*>(wl + hl * lmax + s0 + j4);
+                const int rem = L - (s0 + j4);
+                step(e4.x, w4.x, vreg[j4]);
+                if (rem > 1) step(e4.y, w4.y, vreg[j4 + 1]);
+                if (rem > 2) step(e4.z, w4.z, vreg[j4 + 2]);
+                if (rem > 3) step(e4.w, w4.w, vreg[j4 + 3]);
+            }
         }
         const int h = h0 + hl;
-        *reinterpret_cast<float4*>(p.partials + (pbase + h) * 64 + 4 * qd) = make_float4(o0, o1, o2, o3);
-        if (qd == 0) {
-            p.peaks[pbase + h] = peak_lds[hl];
+        *reinterpret_cast<float4*>(p.partials + (pbase + h) * 64 + 4 * vqd) = make_float4(o0, o1, o2, o3);
+        if (vqd == 0) {
+            p.peaks[pbase + h] = order_value(peak_key[hl]);
             p.sums[pbase + h] = total;
         }
     }
 
-    // arrival: the last workgroup of this (row, head block) merges
-    __threadfence();
-    __syncthreads();
-    int32_t* counter = p.arrivals + (size_t)row * gridDim.z + hb;
-    if (tid == 0) {
-        const int old = __hip_atomic_fetch_add(counter, 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
-        last_flag = old == needed - 1;
+}
+
+// Merge of a (row, head)'s chunk partials, one workgroup of 64 threads
+// (one per dim): MergePartials' non-SIMD order (Blocks.cs:760-815); the
+// thread's chunk values are loaded together before the ascending-order chain.
+constexpr int kMergeBatch = 64;
+
+__global__ __launch_bounds__(64) void decode_merge_kernel(DecodeAttnParams p)
+{
+    __shared__ float mpk[256];
+    __shared__ float msm[256];
+    __shared__ float wts[256];
+    __shared__ float inv_lds;
+    const int row = blockIdx.x;
+    const int h = blockIdx.y;
+    const int d = threadIdx.x;
+    const int slot = p.row_slot[row];
+    const int first = p.row_first[row];
+    const int count = p.row_count[row];
+    const bool valid = slot >= 0 && slot < p.slots && first >= 0 && count >= 1 && count <= p.capacity - first;
+    float* dst = p.out + ((size_t)row * p.heads + h) * 64 + d;
+    if (!valid) {  // uniform over the block
+        *dst = 0.0f;
+        return;
+    }
+    int length;
+    const int needed = plan(count, p.max_chunks, &length);
+    const size_t rbase = (size_t)row * p.max_chunks * p.heads + h;  // + c * heads
+    const float* part = p.partials + rbase * 64 + d;
+    const size_t cstride = (size_t)p.heads * 64;
+    float a[kMergeBatch];
+#pragma unroll
+    for (int j = 0; j < kMergeBatch; j++) a[j] = part[(size_t)min(j, needed - 1) * cstride];
+    for (int c = d; c < needed; c += 64) {
+        mpk[c] = p.peaks[rbase + (size_t)c * p.heads];
+        msm[c] = p.sums[rbase + (size_t)c * p.heads];
     }
     __syncthreads();
-    if (!last_flag) return;
-    __threadfence();
-    if (tid < nh * 16) {
-        const int hl = tid >> 4;
-        const int qd = tid & 15;
-        const int h = h0 + hl;
-        const size_t rb = (size_t)row * p.max_chunks * p.heads + h;  // + c * heads
-        const size_t hs = p.heads;
-        float r0, r1, r2, r3;
-        if (needed == 2) {
-            const float peak0 = p.peaks[rb], peak1 = p.peaks[rb + hs];
-            const float pk = ref_max(peak0, peak1);
-            const float w0 = exp_poly(peak0 - pk);
-            const float w1 = exp_poly(peak1 - pk);
-            float tot = 0.0f;
-            tot = tot + w0 * p.sums[rb];
-            tot = tot + w1 * p.sums[rb + hs];
-            const float inv = 1.0f / tot;
-            const float4 a = *reinterpret_cast<const float4*>(p.partials + rb * 64 + 4 * qd);
-            const float4 b = *reinterpret_cast<const float4*>(p.partials + (rb + hs) * 64 + 4 * qd);
-            r0 = (w0 * a.x + w1 * b.x) * inv;
-            r1 = (w0 * a.y + w1 * b.y) * inv;
-            r2 = (w0 * a.z + w1 * b.z) * inv;
-            r3 = (w0 * a.w + w1 * b.w) * inv;
-        } else {
-            float peak = -INFINITY;
-            for (int c = 0; c < needed; c++) peak = ref_max(peak, p.peaks[rb + c * hs]);
-            float total = 0.0f;
-            for (int c = 0; c < needed; c++) total = total + exp_poly(p.peaks[rb + c * hs] - peak) * p.sums[rb + c * hs];
-            const float inverse = 1.0f / total;
-            float s0 = 0.0f, s1 = 0.0f, s2 = 0.0f, s3 = 0.0f;
-            for (int c = 0; c < needed; c++) {
-                const float w = exp_poly(p.peaks[rb + c * hs] - peak);
-                const float4 a = *reinterpret_cast<const float4*>(p.partials + (rb + c * hs) * 64 + 4 * qd);
-                s0 = s0 + w * a.x;
-                s1 = s1 + w * a.y;
-                s2 = s2 + w * a.z;
-                s3 = s3 + w * a.w;
+    if (needed == 2) {  // uniform over the block
+        const float peak0 = mpk[0], peak1 = mpk[1];
+        const float pk = ref_max(peak0, peak1);
+        const float w0 = exp_poly(peak0 - pk);
+        const float w1 = exp_poly(peak1 - pk);
+        float tot = 0.0f;
+        tot = tot + w0 * msm[0];
+        tot = tot + w1 * msm[1];
+        const float inv = 1.0f / tot;
+        *dst = (w0 * a[0] + w1 * a[1]) * inv;
+        return;
+    }
+    // w_c = Exp(peak_c - peak); the peak by a wave reduction (max is
+    // order-independent), the total in ascending c by thread 0
+    float peak = -INFINITY;
+    for (int c = d; c < needed; c += 64) peak = ref_max(peak, mpk[c]);
+    for (int off = 32; off > 0; off >>= 1) peak = ref_max(peak, __shfl_xor(peak, off));
+    for (int c = d; c < needed; c += 64) wts[c] = exp_poly(mpk[c] - peak);
+    __syncthreads();
+    if (d == 0) {
+        float total = 0.0f;
+        for (int c0 = 0; c0 < needed; c0 += 8) {
+            float w8[8], s8[8];
+#pragma unroll
+            for (int j = 0; j < 8; j++) {
+                const int c = min(c0 + j, needed - 1);
+                w8[j] = wts[c];
+                s8[j] = msm[c];
             }
-            r0 = s0 * inverse;
-            r1 = s1 * inverse;
-            r2 = s2 * inverse;
-            r3 = s3 * inverse;
+#pragma unroll
+            for (int j = 0; j < 8; j++)
+                if (c0 + j < needed) total = total + w8[j] * s8[j];
         }
-        *reinterpret_cast<float4*>(p.out + ((size_t)row * p.heads + h) * 64 + 4 * qd) = make_float4(r0, r1, r2, r3);
+        inv_lds = 1.0f / total;
     }
-    if (tid == 0) __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __syncthreads();
+    float sum = 0.0f;
+    for (int c0 = 0; c0 < needed; c0 += kMergeBatch) {
+        if (c0 > 0) {
+#pragma unroll
+            for (int j = 0; j < kMergeBatch; j++) a[j] = part[(size_t)min(c0 + j, needed - 1) * cstride];
+        }
+#pragma unroll
+        for (int j = 0; j < kMergeBatch; j++)
+            if (c0 + j < needed) sum = sum + wts[c0 + j] * a[j];
+    }
+    *dst = sum * inv_lds;
 }
 
 __global__ void zero_kernel(uint32_t* p, size_t n)
@@ -279,16 +352,14 @@ __global__ void zero_kernel(uint32_t* p, size_t n)
 inline size_t a256(size_t x) { return (x + 255) & ~size_t(255); }
 
 struct WorkspaceLayout {
-    size_t arrivals, peaks, sums, partials, total;
+    size_t peaks, sums, partials, total;
 };
 
 WorkspaceLayout layout(int rows, int heads, int max_chunks)
 {
-    const int head_blocks = heads;  // upper bound on head blocks per row
     WorkspaceLayout w{};
     const size_t pc = (size_t)rows * max_chunks * heads;
-    w.arrivals = 0;
-    w.peaks = a256((size_t)rows * head_blocks * sizeof(int32_t));
+    w.peaks = 0;
     w.sums = w.peaks + a256(pc * sizeof(float));
     w.partials = w.sums + a256(pc * sizeof(float));
     w.total = w.partials + a256(pc * 64 * sizeof(float));
@@ -351,7 +422,7 @@ int32_t nhip_attention_decode_dev(const int8_t* d_q, const float* d_qscale, int3
     // longest chunk: <= 32 below 16*max_chunks positions, else ceil(capacity/max_chunks) rounded up to 4
     const int lmax = std::max(32, ((capacity + max_chunks - 1) / max_chunks + 3) & ~3);
     const size_t lds = kMaxHeadsPerBlock * 64 + (size_t)3 * kMaxHeadsPerBlock * lmax * sizeof(float) +
-                       kMaxHeadsPerBlock * sizeof(float);
+                       2 * kMaxHeadsPerBlock * sizeof(float);
     NHIP_REQUIRE(lds <= 64 * 1024, "attention: chunks of up to %d positions need %zu bytes of LDS; raise "
                  "max_chunks", lmax, lds);
     int32_t rc = ensure_device();
@@ -367,7 +438,6 @@ int32_t nhip_attention_decode_dev(const int8_t* d_q, const float* d_qscale, int3
     p.row_first = d_row_first;
     p.row_count = d_row_count;
     uint8_t* ws = static_cast<uint8_t*>(d_workspace);
-    p.arrivals = reinterpret_cast<int32_t*>(ws + wl.arrivals);
     p.peaks = reinterpret_cast<float*>(ws + wl.peaks);
     p.sums = reinterpret_cast<float*>(ws + wl.sums);
     p.partials = reinterpret_cast<float*>(ws + wl.partials);
@@ -385,6 +455,8 @@ int32_t nhip_attention_decode_dev(const int8_t* d_q, const float* d_qscale, int3
     const int head_blocks = (kv_heads + p.kv_per_block - 1) / p.kv_per_block;
     hipLaunchKernelGGL(decode_attention_kernel, dim3(max_chunks, rows, head_blocks), dim3(kThreads), lds,
                        as_stream(stream), p);
+    NHIP_CHECK_HIP(hipGetLastError());
+    hipLaunchKernelGGL(decode_merge_kernel, dim3(rows, heads), dim3(64), 0, as_stream(stream), p);
     NHIP_CHECK_HIP(hipGetLastError());
     return NHIP_OK;
 }
