@@ -32,6 +32,7 @@ sys.path.insert(0, ROOT)
 import needle_cs_amd as N  # noqa: E402
 
 HBM_PEAK_GBS = 8000.0
+INT8_PEAK_TOPS = 5000.0  # dense int8 MFMA
 METRIC = "int8 decode GEMV GB/s (% HBM peak); beam-3 batched decode tokens/sec"
 
 
@@ -107,6 +108,21 @@ class GemvCase:
     def close(self) -> None:
         for w in self.weights:
             w.close()
+
+
+class GemmCase(GemvCase):
+    """Prefill int8 GEMM: M=512 tokens, K=2048, N=8192, per-token int8
+    activations; `fused` selects the fused-epilogue entry point."""
+
+    def __init__(self, m: int, k: int, n: int, seed: int, fused: bool):
+        super().__init__(m, k, n, seed, min_bytes=64 << 20)
+        self.fused = fused
+        self.ops = 2 * m * n * k
+
+    def launch(self, i: int) -> None:
+        w = self.weights[i % self.copies]
+        fn = N.lib().nhip_matmul_i8_fused_dev if self.fused else N.lib().nhip_matmul_i8_dev
+        N.check(fn(w.handle, self.dq.ptr, self.ds.ptr, self.m, self.dy.ptr, self.n, 0, self.n, None))
 
 
 class AttnCase:
@@ -267,6 +283,20 @@ def main() -> int:
             print(f"# GEMV M={m} K={k} N={n}: {t * 1e3:.2f} us/launch, {g:.0f} GB/s", file=sys.stderr, flush=True)
             case.close()
 
+    prefill = []
+    if not args.no_secondary:
+        for fused in (True, False):
+            case = GemmCase(512, 2048, 8192, seed=0x4004, fused=fused)
+            t = case.time(max(50, args.steps // 20), max(5, args.warmup // 10))
+            tops = case.ops / (t * 1e-3) / 1e12
+            prefill.append({"workload": "prefill int8 GEMM M=512 K=2048 N=8192 (%s epilogue)" %
+                                        ("fused fma, 1e-4 RMS" if fused else "reference-order, bit-exact"),
+                            "us_per_launch": round(t * 1e3, 2), "TOPS": round(tops, 1),
+                            "frac_int8_mfma_peak": round(tops / INT8_PEAK_TOPS, 4)})
+            print(f"# prefill GEMM ({'fused' if fused else 'exact'}): {t * 1e3:.1f} us, {tops:.0f} TOPS",
+                  file=sys.stderr, flush=True)
+            case.close()
+
     attention = None
     if not args.no_secondary:
         case = AttnCase(seed=0x3003)
@@ -305,6 +335,7 @@ def main() -> int:
                      "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": measured_traffic()},
         "cpu_baseline": cpu,
         "secondary": secondary,
+        "prefill": prefill,
         "attention": attention,
     }
     main_case.close()

@@ -198,6 +198,16 @@ int32_t nhip_matmul_i8_dev(const nhip_weights* w, const int8_t* d_q, const float
                            int32_t tokens, float* d_y, int32_t ldy, int32_t row_start,
                            int32_t row_end, void* stream);
 
+/* Prefill form of nhip_matmul_i8_dev with a fused epilogue: the same exact
+ * int32 group sums D_g, accumulated as acc = fma(h(scale[n][g]), D_g, acc)
+ * and scaled once, y = acc * qscale[t] -- two VALU operations per (token,
+ * row, group) instead of the reference's four, so the fp32 outputs agree with
+ * Scalar.MatMulRows to 1e-4 of RMS(y), not bit for bit.  For prefill
+ * throughput; nhip_matmul_i8_dev stays bit-exact for every token count. */
+int32_t nhip_matmul_i8_fused_dev(const nhip_weights* w, const int8_t* d_q, const float* d_qscale,
+                                 int32_t tokens, float* d_y, int32_t ldy, int32_t row_start,
+                                 int32_t row_end, void* stream);
+
 /* Scalar.MatMulRows on device for codebook weights (Scalar.cs:146-192):
  * activations as produced by nhip_prepare_dev. */
 int32_t nhip_matmul_cq_dev(const nhip_weights* w, const int8_t* d_values, const float* d_scales,

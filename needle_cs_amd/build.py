@@ -4,6 +4,8 @@ Every HIP source under csrc/ is compiled for gfx950 only, with
   -ffp-contract=off   no implicit FMA contraction: every float operation of
                       the reference-order epilogues is one IEEE operation
   -packed-fp32-ops    off: no v_pk_* fp32 instructions are generated
+  -amdgpu-mfma-vgpr-form  MFMA results in VGPRs (no AGPR copies before the
+                      VALU epilogues)
 and linked into needle_cs_amd/libneedle_hip.so next to this file.
 """
 from __future__ import annotations
@@ -28,6 +30,7 @@ FLAGS = [
     "-fPIC",
     "-ffp-contract=off",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-mllvm", "-amdgpu-mfma-vgpr-form",
     "-Wall",
     "-Wno-unused-function",
     "-I", INCLUDE,

@@ -67,6 +67,15 @@ struct DeviceWeights {
 struct nhip_weights : nhip::DeviceWeights {};
 
 namespace nhip {
+// Prefill matmul of the literal int8 format (gemm.hip): exact = Scalar
+// order (bit-identical with the decode kernels), else the fused epilogue.
+int32_t launch_gemm_i8(const DeviceWeights* w, const int8_t* q, const float* qscale, int32_t tokens, float* y,
+                       int32_t ldy, int32_t row_start, int32_t row_end, bool exact, hipStream_t stream);
+// Token count from which literal int8 matmuls use the prefill kernel.
+constexpr int32_t kGemmMinTokens = 32;
+}  // namespace nhip
+
+namespace nhip {
 
 // ------------------------------------------------ exact device arithmetic --
 

@@ -849,6 +849,8 @@ int32_t run_matmul(const DeviceWeights* w, const int8_t* q, const float* scales,
     const int waves = waves_override ? waves_override : (tiles * ((tokens + 15) / 16) >= 512 ? 4 : 8);
     const int m = std::min(16, tokens);
     if (w->format == WeightFormat::Int8G32) {
+        if (!dots && tokens >= kGemmMinTokens)
+            return launch_gemm_i8(w, q, scales, tokens, y, ldy, row_start, row_end, true, stream);
         const int32_t drc = try_i8_decode(w, p, stream);
         if (drc <= 0) return drc;
         // LDS per phase: staged operands gph*32*m + products m*16*ldd*4 + a
