@@ -212,6 +212,76 @@ int or_argmax(const float* x, int n);
 void or_topk_log_softmax(const float* x, int n, int k, int* indices, float* log_probs,
                          float* probs, int mask_special_023);
 
+/* ---- threaded CPU baseline (cpu_baseline.c) ---- */
+
+int or_baseline_start(int members);
+void or_baseline_stop(void);
+/* or_matmul_rows_i8 split over the pool's members (bit-identical results). */
+void or_baseline_matmul_i8(const int8_t* w, const uint16_t* scales, int rows, int cols, int group,
+                           const int8_t* q, const float* qscale, int tokens, float* y, int ldy,
+                           int row_start, int row_end);
+
+/* ---- synthetic int8 decoder (decoder.c) ---- */
+
+/* Canonical element-wise operations of the decoder (no reference
+ * counterpart; the GPU kernels repeat them operation for operation). */
+float or_log_poly(float x);
+float or_add_rmsnorm_quant(float* x, const float* delta, const float* gain, int d, float eps, float* h,
+                           int8_t* q);
+void or_rope_table(int positions, int dim, double theta, float* cos_t, float* sin_t);
+void or_rope_head(float* v, const float* c, const float* s);
+float or_swiglu_quant(const float* g, const float* u, int n, float* a, int8_t* q);
+void or_topk_lse(const float* x, int n, int k, int mask, int* idx, float* lp);
+
+typedef struct or_decoder_dims {
+    int layers, d, heads, kv_heads, head_dim, ffn, vocab, capacity, slots, max_chunks;
+    double theta;
+    float eps;
+} or_decoder_dims;
+
+/* int8 weights [rows][cols] with fp16 group-32 scales [rows][cols/32]:
+ * wqkv [(heads+2*kv_heads)*head_dim][d], wo [d][heads*head_dim],
+ * wgu [2*ffn][d] (gate rows, then up rows), wd [d][ffn]. */
+typedef struct or_layer_weights {
+    const int8_t* wqkv;
+    const uint16_t* sqkv;
+    const int8_t* wo;
+    const uint16_t* so;
+    const int8_t* wgu;
+    const uint16_t* sgu;
+    const int8_t* wd;
+    const uint16_t* sd;
+    const float* attn_norm;
+    const float* ffn_norm;
+} or_layer_weights;
+
+typedef struct or_decoder {
+    or_decoder_dims dims;
+    const or_layer_weights* layers;
+    const float* embedding;  /* [vocab][d] */
+    const float* final_norm; /* [d] */
+    const int8_t* wlm;       /* [vocab][d] */
+    const uint16_t* slm;
+    int threads;             /* > 1: linears on the baseline pool */
+    float* rope_cos;         /* owned: [capacity][head_dim/2] */
+    float* rope_sin;
+    int8_t* keys;            /* owned: [layer][slot][capacity][kv_heads*head_dim] */
+    int8_t* values;
+    float* key_scales;       /* owned: [layer][slot][capacity][kv_heads] */
+    float* value_scales;
+} or_decoder;
+
+int or_decoder_init(or_decoder* m);
+void or_decoder_free(or_decoder* m);
+/* One forward over `rows` rows (token, slot, position each): writes every
+ * layer's K/V at the row's position, fills logits [rows][vocab] if given
+ * and the top-k (masked ids 0,2,3) ids/log-probabilities if k > 0. */
+void or_decoder_forward(or_decoder* m, const int* tokens, const int* slots, const int* positions, int rows,
+                        float* logits, int k, int* topk_idx, float* topk_lp);
+void or_decoder_copy_slot(or_decoder* m, int dst, int src, int length);
+int or_beam_search(or_decoder* m, const int* prompt, int prompt_len, int width, int max_new, int eos,
+                   int* out_tokens, float* out_score, long* fed_rows);
+
 #ifdef __cplusplus
 }
 #endif

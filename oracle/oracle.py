@@ -37,6 +37,24 @@ class AttnTile(C.Structure):
                 ("probability_stride", C.c_int), ("peaks", C.c_void_p), ("sums", C.c_void_p)]
 
 
+class DecoderDims(C.Structure):
+    _fields_ = [("layers", C.c_int), ("d", C.c_int), ("heads", C.c_int), ("kv_heads", C.c_int),
+                ("head_dim", C.c_int), ("ffn", C.c_int), ("vocab", C.c_int), ("capacity", C.c_int),
+                ("slots", C.c_int), ("max_chunks", C.c_int), ("theta", C.c_double), ("eps", C.c_float)]
+
+
+class LayerWeights(C.Structure):
+    _fields_ = [(n, C.c_void_p) for n in ("wqkv", "sqkv", "wo", "so", "wgu", "sgu", "wd", "sd", "attn_norm",
+                                          "ffn_norm")]
+
+
+class Decoder(C.Structure):
+    _fields_ = [("dims", DecoderDims), ("layers", C.POINTER(LayerWeights)), ("embedding", C.c_void_p),
+                ("final_norm", C.c_void_p), ("wlm", C.c_void_p), ("slm", C.c_void_p), ("threads", C.c_int),
+                ("rope_cos", C.c_void_p), ("rope_sin", C.c_void_p), ("keys", C.c_void_p), ("values", C.c_void_p),
+                ("key_scales", C.c_void_p), ("value_scales", C.c_void_p)]
+
+
 _u64p, _vp, _i, _f, _sz = C.POINTER(C.c_uint64), C.c_void_p, C.c_int, C.c_float, C.c_size_t
 _PROTOS = {
     "or_xs_seed": (C.c_uint64, [C.c_uint64]),
@@ -81,6 +99,17 @@ _PROTOS = {
     "or_attention_plan": (_i, [_i, _i, C.POINTER(_i)]),
     "or_merge_head": (None, [_vp, _i, _vp, _vp, _i, _i, _vp, _i]),
     "or_attention_decode": (None, [_vp, _vp, _i, _i, _i, _i, _vp, _vp, _vp, _vp, _i, _vp, _vp, _vp, _i, _vp]),
+    "or_log_poly": (_f, [_f]),
+    "or_add_rmsnorm_quant": (_f, [_vp, _vp, _vp, _i, _f, _vp, _vp]),
+    "or_rope_table": (None, [_i, _i, C.c_double, _vp, _vp]),
+    "or_rope_head": (None, [_vp, _vp, _vp]),
+    "or_swiglu_quant": (_f, [_vp, _vp, _i, _vp, _vp]),
+    "or_topk_lse": (None, [_vp, _i, _i, _i, _vp, _vp]),
+    "or_decoder_init": (_i, [C.POINTER(Decoder)]),
+    "or_decoder_free": (None, [C.POINTER(Decoder)]),
+    "or_decoder_forward": (None, [C.POINTER(Decoder), _vp, _vp, _vp, _i, _vp, _i, _vp, _vp]),
+    "or_decoder_copy_slot": (None, [C.POINTER(Decoder), _i, _i, _i]),
+    "or_beam_search": (_i, [C.POINTER(Decoder), _vp, _i, _i, _i, _i, _vp, C.POINTER(_f), C.POINTER(C.c_long)]),
     "or_argmax": (_i, [_vp, _i]),
     "or_topk_log_softmax": (None, [_vp, _i, _i, _vp, _vp, _vp, _i]),
     "or_baseline_start": (_i, [_i]),
@@ -226,3 +255,53 @@ def kv_cache(st, slots: int, capacity: int, kv_heads: int, qk: int):
     vq, vs = quantize_rows(vf.reshape(-1, 64))
     return (kq.reshape(slots, capacity, kv_heads * qk), ks.reshape(slots, capacity, kv_heads),
             vq.reshape(slots, capacity, kv_heads * 64), vs.reshape(slots, capacity, kv_heads))
+
+
+class CpuDecoder:
+    """The oracle's decoder over a synthetic model's numpy arrays (see
+    needle_cs_amd.decoder.synthetic_model for the layout)."""
+
+    def __init__(self, model: dict, slots: int, capacity: int, max_chunks: int = 64, threads: int = 1):
+        dm = model["dims"]
+        self._keep = model
+        self.layers = (LayerWeights * dm["layers"])()
+        for l, lw in enumerate(model["layers"]):
+            for name in ("wqkv", "sqkv", "wo", "so", "wgu", "sgu", "wd", "sd", "attn_norm", "ffn_norm"):
+                setattr(self.layers[l], name, p(lw[name]))
+        self.dec = Decoder()
+        self.dec.dims = DecoderDims(dm["layers"], dm["d"], dm["heads"], dm["kv_heads"], dm["head_dim"], dm["ffn"],
+                                    dm["vocab"], capacity, slots, max_chunks, dm["theta"], dm["eps"])
+        self.dec.layers = C.cast(self.layers, C.POINTER(LayerWeights))
+        self.dec.embedding = p(model["embedding"])
+        self.dec.final_norm = p(model["final_norm"])
+        self.dec.wlm = p(model["wlm"])
+        self.dec.slm = p(model["slm"])
+        self.dec.threads = threads
+        assert lib().or_decoder_init(C.byref(self.dec)) == 0
+        self.vocab = dm["vocab"]
+
+    def forward(self, tokens, slots, positions, k=0, logits=True):
+        rows = len(tokens)
+        t, s, ps = (np.ascontiguousarray(a, dtype=np.int32) for a in (tokens, slots, positions))
+        lg = np.zeros((rows, self.vocab), dtype=np.float32) if logits else None
+        idx = np.zeros((rows, max(k, 1)), dtype=np.int32)
+        lp = np.zeros((rows, max(k, 1)), dtype=np.float32)
+        lib().or_decoder_forward(C.byref(self.dec), p(t), p(s), p(ps), rows, p(lg) if logits else None, k, p(idx),
+                                 p(lp))
+        return lg, idx[:, :k], lp[:, :k]
+
+    def copy_slot(self, dst, src, length):
+        lib().or_decoder_copy_slot(C.byref(self.dec), dst, src, length)
+
+    def beam_search(self, prompt, width, max_new, eos):
+        pr = np.ascontiguousarray(prompt, dtype=np.int32)
+        out = np.zeros(max_new + 1, dtype=np.int32)
+        score = C.c_float()
+        fed = C.c_long()
+        n = lib().or_beam_search(C.byref(self.dec), p(pr), len(pr), width, max_new, eos, p(out), C.byref(score),
+                                 C.byref(fed))
+        return out[:n].copy(), score.value, fed.value
+
+    def close(self):
+        if self.dec.keys:
+            lib().or_decoder_free(C.byref(self.dec))
