@@ -260,6 +260,64 @@ int32_t nhip_attention_decode_dev(const int8_t* d_q, const float* d_q_scales, in
                                   int32_t max_chunks, void* d_workspace, size_t workspace_bytes,
                                   float* d_out, void* stream);
 
+/* ---------------------------------------------- decode loop (engine) -- */
+
+/* The beam/ragged-batched decode step of a pre-norm int8 decoder (RMSNorm,
+ * fused QKV, rotary positions, int8 KV cache per slot, SwiGLU FFN, LM head)
+ * with every linear in the literal int8 format.  One forward packs `rows`
+ * rows from independent cache slots, as EngineCore.ForwardBatch does
+ * (src/Needle/Engine.cs:2303-2350, 2480-2596); beam search drives it as
+ * Whistle.BeamSearch does (src/Needle/Whistle.Decode.cs:226-350) but with
+ * the beams batched into one forward per step, which is the step API of the
+ * performance path (nhip_step / slot copy).  Element-wise operations follow
+ * the canonical order the CPU restatement shares, so logits and token streams
+ * are bit-identical with it. */
+typedef struct nhip_decoder nhip_decoder;
+
+typedef struct nhip_decoder_dims {
+    int32_t layers, d, heads, kv_heads, head_dim, ffn, vocab;
+    int32_t capacity;   /* positions per cache slot */
+    int32_t slots;      /* cache slots (beams, sequences) */
+    int32_t max_rows;   /* rows per forward (prompt length for prefill) */
+    int32_t max_chunks; /* attention position-split cap (64 fills the GPU) */
+    double theta;       /* RoPE base */
+    float eps;          /* RMSNorm epsilon */
+} nhip_decoder_dims;
+
+typedef struct nhip_decode_stats {
+    double prefill_seconds, decode_seconds;
+    int64_t fed_rows; /* rows fed after the prompt (row-tokens) */
+    int32_t steps;
+} nhip_decode_stats;
+
+int32_t nhip_decoder_create(const nhip_decoder_dims* dims, nhip_decoder** out);
+/* Host weights of one layer, uploaded and re-tiled: wqkv [(heads+2kv)*64][d],
+ * wo [d][heads*64], wgu [2*ffn][d] (gate rows then up rows), wd [d][ffn],
+ * each int8 with fp16 group-32 scales; RMSNorm gains [d]. */
+int32_t nhip_decoder_set_layer(nhip_decoder* m, int32_t layer, const int8_t* wqkv, const uint16_t* sqkv,
+                               const int8_t* wo, const uint16_t* so, const int8_t* wgu, const uint16_t* sgu,
+                               const int8_t* wd, const uint16_t* sd, const float* attn_norm,
+                               const float* ffn_norm);
+/* Embedding fp32 [vocab][d], final RMSNorm gain [d], LM head [vocab][d]. */
+int32_t nhip_decoder_set_head(nhip_decoder* m, const float* embedding, const float* final_norm,
+                              const int8_t* wlm, const uint16_t* slm);
+/* One synchronous forward of `rows` rows (host token/slot/position arrays):
+ * writes each layer's K/V at the row's position in its slot, returns logits
+ * [rows][vocab] if non-NULL and the top-k ids / log-probabilities
+ * (TopKLogSoftmax, ids 0,2,3 masked) if k > 0 (k <= 8). */
+int32_t nhip_decoder_forward(nhip_decoder* m, const int32_t* tokens, const int32_t* slots,
+                             const int32_t* positions, int32_t rows, float* logits, int32_t k,
+                             int32_t* topk_idx, float* topk_lp);
+/* Engine.CopyFrom: positions [0, length) of slot src into slot dst. */
+int32_t nhip_decoder_copy_slot(nhip_decoder* m, int32_t dst, int32_t src, int32_t length);
+/* Prefill `prompt` into slot 0, then beam search of `width` beams for up to
+ * max_new tokens (length penalty 1, EOS `eos`); writes the winner's tokens
+ * (without the prompt), its length and normalised score. */
+int32_t nhip_decoder_beam_search(nhip_decoder* m, const int32_t* prompt, int32_t prompt_len, int32_t width,
+                                 int32_t max_new, int32_t eos, int32_t* out_tokens, int32_t* out_len,
+                                 float* out_score, nhip_decode_stats* stats);
+int32_t nhip_decoder_destroy(nhip_decoder* m);
+
 /* ------------------------------------------ synthetic workload inputs -- */
 
 /* Deterministic host-side generators for the benchmark workloads: one

@@ -73,6 +73,13 @@ _PROTOS = {
     "nhip_memcpy_dtoh": (_i32, [_vp, _vp, _sz]),
     "nhip_memcpy_dtod": (_i32, [_vp, _vp, _sz, _vp]),
     "nhip_copy_dev": (_i32, [_vp, _vp, _sz, _vp]),
+    "nhip_decoder_create": (_i32, [_vp, _vp]),
+    "nhip_decoder_set_layer": (_i32, [_vp, _i32] + [_vp] * 10),
+    "nhip_decoder_set_head": (_i32, [_vp, _vp, _vp, _vp, _vp]),
+    "nhip_decoder_forward": (_i32, [_vp, _vp, _vp, _vp, _i32, _vp, _i32, _vp, _vp]),
+    "nhip_decoder_copy_slot": (_i32, [_vp, _i32, _i32, _i32]),
+    "nhip_decoder_beam_search": (_i32, [_vp, _vp, _i32, _i32, _i32, _i32, _vp, _vp, _vp, _vp]),
+    "nhip_decoder_destroy": (_i32, [_vp]),
     "nhip_matmul_i8_fused_dev": (_i32, [_vp, _vp, _vp, _i32, _vp, _i32, _i32, _i32, _vp]),
     "nhip_attention_decode_workspace": (_sz, [_i32, _i32, _i32]),
     "nhip_attention_decode_workspace_init": (_i32, [_vp, _sz, _vp]),

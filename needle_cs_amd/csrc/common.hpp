@@ -97,6 +97,13 @@ __device__ __forceinline__ float ref_round_even(float x)
     return (x + 12582912.0f) - 12582912.0f;
 }
 
+// One element of Scalar.QuantizeInt8 (Scalar.cs:67-74): clamp(RoundEven(x * inverse)).
+__device__ __forceinline__ int ref_quantize_one(float x, float inverse)
+{
+    const float r = ref_round_even(x * inverse);
+    return static_cast<int>(fminf(fmaxf(r, -128.0f), 127.0f));
+}
+
 // MathF.Max for the non-NaN operands used here (+0 preferred over -0).
 __device__ __forceinline__ float ref_max(float a, float b)
 {

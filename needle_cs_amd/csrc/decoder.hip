@@ -1,0 +1,854 @@
+// decoder.hip -- the beam/ragged-batched decode step of an int8 decoder on
+// gfx950, and the beam-search driver around it.
+//
+// One forward runs `rows` packed rows (tokens of independent sequences or
+// beams), each in its own KV-cache slot at its own position: embedding ->
+// per layer [RMSNorm+quantize -> QKV matmul -> RoPE + per-head quantize +
+// KV write -> ragged attention -> quantize -> output matmul -> residual +
+// RMSNorm + quantize -> gate/up matmul -> SwiGLU + quantize -> down matmul]
+// -> residual + final RMSNorm + quantize -> LM head -> top-k log-softmax.
+// This is EngineCore.ForwardBatch's packing (src/Needle/Engine.cs:2303-2350,
+// 2480-2596: rows from several slots in one pass, each attending its own
+// cache) applied to the benchmark's plain pre-norm decoder; the matmuls are
+// the literal int8 kernels (Scalar.MatMulRows' order), the attention is the
+// AttentionBatch + MergePartials order, and the element-wise kernels below
+// follow one canonical operation order (written out at each kernel) that
+// the CPU path repeats exactly, so token streams are bit-identical.
+// Beam search follows Whistle.BeamSearch (src/Needle/Whistle.Decode.cs:
+// 226-350) with the beams batched into one forward per step instead of one
+// Engine.Feed per beam; the last child of a parent keeps the parent's cache
+// slot, other children get a copy (Engine.CopyFrom, Engine.cs:367-379).
+// Decode steps replay a HIP graph per row count.
+#include <algorithm>
+#include <chrono>
+#include <cmath>
+#include <cstring>
+#include <vector>
+
+#include "common.hpp"
+
+namespace nhip {
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kMaxPerThread = 16;  // d and ffn up to 4096 elements per row
+constexpr int kMaxTopK = 8;
+
+__device__ __forceinline__ float block_max_abs(float v, float* red)
+{
+    for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off));
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+    __syncthreads();
+    return fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+}
+
+// Canonical 256-lane sum: lane t holds its elements t, t+256, ... summed in
+// ascending order; lanes fold pairwise with strides 128, 64, ..., 1.
+__device__ __forceinline__ float block_fold(float s, float* red)
+{
+    __syncthreads();
+    red[threadIdx.x] = s;
+    __syncthreads();
+    for (int stride = 128; stride > 0; stride >>= 1) {
+        if ((int)threadIdx.x < stride) red[threadIdx.x] = red[threadIdx.x] + red[threadIdx.x + stride];
+        __syncthreads();
+    }
+    return red[0];
+}
+
+// Natural log for normal x > 0: x = m 2^e, m in [sqrt(1/2), sqrt(2)),
+// log m = 2 atanh(s), s = (m-1)/(m+1), odd series to s^9; e*ln2 split as in
+// Ops.Exp.
+__device__ __forceinline__ float log_poly(float x)
+{
+    const uint32_t u = __float_as_uint(x);
+    int e = (int)(u >> 23) - 127;
+    float m = __uint_as_float((u & 0x7FFFFFu) | 0x3F800000u);
+    if (m > 1.41421356f) {
+        m = m * 0.5f;
+        e = e + 1;
+    }
+    const float f = m - 1.0f;
+    const float s = f / (2.0f + f);
+    const float z = s * s;
+    float p = 0.11111111f;
+    p = __builtin_fmaf(p, z, 0.14285715f);
+    p = __builtin_fmaf(p, z, 0.2f);
+    p = __builtin_fmaf(p, z, 0.33333334f);
+    p = __builtin_fmaf(p, z, 1.0f);
+    const float r = (2.0f * s) * p;
+    const float fe = (float)e;
+    return __builtin_fmaf(fe, 0.693359375f, __builtin_fmaf(fe, -2.12194440e-4f, r));
+}
+
+__global__ __launch_bounds__(kThreads) void embed_kernel(const int32_t* tokens, const float* emb, int d, float* x)
+{
+    const float* src = emb + (size_t)tokens[blockIdx.x] * d;
+    float* dst = x + (size_t)blockIdx.x * d;
+    for (int i = threadIdx.x; i < d; i += kThreads) dst[i] = src[i];
+}
+
+// x += delta (when given); ss = sum x^2 (canonical sum); inv = 1 / sqrt(ss /
+// d + eps); h = (x * inv) * gain; QuantizeInt8(h) -> q, scale.
+__global__ __launch_bounds__(kThreads) void add_rmsnorm_quant_kernel(float* x, const float* delta, const float* gain,
+                                                                     int d, float eps, int8_t* q, float* qscale)
+{
+    __shared__ float red[kThreads];
+    const int t = threadIdx.x;
+    float* xr = x + (size_t)blockIdx.x * d;
+    const float* dr = delta ? delta + (size_t)blockIdx.x * d : nullptr;
+    float v[kMaxPerThread];
+    float s = 0.0f;
+#pragma unroll
+    for (int j = 0; j < kMaxPerThread; j++) {
+        const int i = t + j * kThreads;
+        if (i < d) {
+            float a = xr[i];
+            if (dr) {
+                a = a + dr[i];
+                xr[i] = a;
+            }
+            v[j] = a;
+            s = s + a * a;
+        }
+    }
+    const float ss = block_fold(s, red);
+    const float inv = 1.0f / sqrtf(ss / (float)d + eps);
+    float peak = 0.0f;
+#pragma unroll
+    for (int j = 0; j < kMaxPerThread; j++) {
+        const int i = t + j * kThreads;
+        if (i < d) {
+            v[j] = (v[j] * inv) * gain[i];
+            peak = fmaxf(peak, fabsf(v[j]));
+        }
+    }
+    peak = block_max_abs(peak, red);
+    const float scale = peak > 0.0f ? peak / 127.0f : 1.0f;
+    const float inverse = 1.0f / scale;
+    int8_t* qr = q + (size_t)blockIdx.x * d;
+#pragma unroll
+    for (int j = 0; j < kMaxPerThread; j++) {
+        const int i = t + j * kThreads;
+        if (i < d) qr[i] = static_cast<int8_t>(ref_quantize_one(v[j], inverse));
+    }
+    if (t == 0) qscale[blockIdx.x] = scale;
+}
+
+struct PostParams {
+    const float* qkv;  // [rows][(H + 2 KV) * 64]
+    const int32_t* slots;
+    const int32_t* positions;
+    const float* rope_cos;  // [capacity][32]
+    const float* rope_sin;
+    int8_t* q8;  // [rows][H][64]
+    float* qs;   // [rows][H]
+    int8_t* keys;
+    float* key_scales;
+    int8_t* values;
+    float* value_scales;  // this layer's pools: [slots][capacity][KV(*64)]
+    int heads, kv_heads, capacity;
+};
+
+// One wave per (row, head unit): query heads get RoPE and QuantizeInt8;
+// key heads RoPE, QuantizeInt8 and the cache write at the row's position;
+// value heads QuantizeInt8 and the cache write.  RoPE (rotate-half): x_i' =
+// x_i c_i - x_{i+32} s_i, x_{i+32}' = x_{i+32} c_i + x_i s_i.
+__global__ __launch_bounds__(64) void qkv_post_kernel(PostParams p)
+{
+    const int row = blockIdx.x;
+    const int u = blockIdx.y;
+    const int e = threadIdx.x;
+    const int units = p.heads + 2 * p.kv_heads;
+    const int pos = p.positions[row];
+    float v = p.qkv[((size_t)row * units + u) * 64 + e];
+    if (u < p.heads + p.kv_heads) {
+        const int i = e & 31;
+        const float c = p.rope_cos[(size_t)pos * 32 + i];
+        const float s = p.rope_sin[(size_t)pos * 32 + i];
+        const float other = __shfl_xor(v, 32);
+        v = e < 32 ? v * c - other * s : v * c + other * s;
+    }
+    float peak = fabsf(v);
+    for (int off = 32; off > 0; off >>= 1) peak = fmaxf(peak, __shfl_xor(peak, off));
+    const float scale = peak > 0.0f ? peak / 127.0f : 1.0f;
+    const float inverse = 1.0f / scale;
+    const int8_t qv = static_cast<int8_t>(ref_quantize_one(v, inverse));
+    if (u < p.heads) {
+        p.q8[((size_t)row * p.heads + u) * 64 + e] = qv;
+        if (e == 0) p.qs[(size_t)row * p.heads + u] = scale;
+        return;
+    }
+    const bool key = u < p.heads + p.kv_heads;
+    const int kv = key ? u - p.heads : u - p.heads - p.kv_heads;
+    const size_t cell = ((size_t)p.slots[row] * p.capacity + pos) * p.kv_heads + kv;
+    (key ? p.keys : p.values)[cell * 64 + e] = qv;
+    if (e == 0) (key ? p.key_scales : p.value_scales)[cell] = scale;
+}
+
+// a = (g / (1 + Exp(-g))) * u, then QuantizeInt8(a).
+__global__ __launch_bounds__(kThreads) void swiglu_quant_kernel(const float* gu, int ffn, int8_t* q, float* qscale)
+{
+    __shared__ float red[kThreads];
+    const int t = threadIdx.x;
+    const float* g = gu + (size_t)blockIdx.x * 2 * ffn;
+    const float* up = g + ffn;
+    float v[kMaxPerThread];
+    float peak = 0.0f;
+#pragma unroll
+    for (int j = 0; j < kMaxPerThread; j++) {
+        const int i = t + j * kThreads;
+        if (i < ffn) {
+            const float gi = g[i];
+            v[j] = (gi / (1.0f + exp_poly(-gi))) * up[i];
+            peak = fmaxf(peak, fabsf(v[j]));
+        }
+    }
+    peak = block_max_abs(peak, red);
+    const float scale = peak > 0.0f ? peak / 127.0f : 1.0f;
+    const float inverse = 1.0f / scale;
+    int8_t* qr = q + (size_t)blockIdx.x * ffn;
+#pragma unroll
+    for (int j = 0; j < kMaxPerThread; j++) {
+        const int i = t + j * kThreads;
+        if (i < ffn) qr[i] = static_cast<int8_t>(ref_quantize_one(v[j], inverse));
+    }
+    if (t == 0) qscale[blockIdx.x] = scale;
+}
+
+// (value, id) order of TopKLogSoftmax: larger value first, equal values by
+// the lower id.
+__device__ __forceinline__ bool before(float va, int ia, float vb, int ib)
+{
+    return va > vb || (va == vb && ia < ib);
+}
+
+__device__ __forceinline__ bool masked(int i) { return i == 0 || i == 2 || i == 3; }
+
+// TopKLogSoftmax (src/Needle/Ops.cs:1092-1221) in the canonical float form:
+// top k of the ids except 0, 2, 3 (the set is unique under the order above,
+// so the tree merge equals the reference's sequential insertion);
+// log_shift = peak + log(sum_i Exp(v_i - peak)), masked v_i = -1e30, the sum
+// by the canonical 256-lane reduction; lp = v - log_shift.
+__global__ __launch_bounds__(kThreads) void topk_lse_kernel(const float* logits, int n, int k, int32_t* idx, float* lp)
+{
+    __shared__ float tv[kThreads][kMaxTopK];
+    __shared__ int ti[kThreads][kMaxTopK];
+    __shared__ float red[kThreads];
+    const int t = threadIdx.x;
+    const float* x = logits + (size_t)blockIdx.x * n;
+    float bv[kMaxTopK];
+    int bi[kMaxTopK];
+    for (int m = 0; m < k; m++) {
+        bv[m] = -INFINITY;
+        bi[m] = 0x7FFFFFFF;
+    }
+    for (int i = t; i < n; i += kThreads) {
+        if (masked(i)) continue;
+        const float v = x[i];
+        if (!before(v, i, bv[k - 1], bi[k - 1])) continue;
+        int pos = k - 1;
+        while (pos > 0 && before(v, i, bv[pos - 1], bi[pos - 1])) {
+            bv[pos] = bv[pos - 1];
+            bi[pos] = bi[pos - 1];
+            pos--;
+        }
+        bv[pos] = v;
+        bi[pos] = i;
+    }
+    for (int m = 0; m < k; m++) {
+        tv[t][m] = bv[m];
+        ti[t][m] = bi[m];
+    }
+    __syncthreads();
+    for (int stride = 128; stride > 0; stride >>= 1) {
+        if (t < stride) {
+            float mv[kMaxTopK];
+            int mi[kMaxTopK];
+            int a = 0, b = 0;
+            for (int m = 0; m < k; m++) {
+                if (before(tv[t][a], ti[t][a], tv[t + stride][b], ti[t + stride][b])) {
+                    mv[m] = tv[t][a];
+                    mi[m] = ti[t][a];
+                    a++;
+                } else {
+                    mv[m] = tv[t + stride][b];
+                    mi[m] = ti[t + stride][b];
+                    b++;
+                }
+            }
+            for (int m = 0; m < k; m++) {
+                tv[t][m] = mv[m];
+                ti[t][m] = mi[m];
+            }
+        }
+        __syncthreads();
+    }
+    const float peak = tv[0][0];
+    float s = 0.0f;
+    for (int i = t; i < n; i += kThreads) s = s + exp_poly((masked(i) ? -1e30f : x[i]) - peak);
+    const float total = block_fold(s, red);
+    const float log_shift = peak + log_poly(total);
+    if (t < k) {
+        idx[(size_t)blockIdx.x * k + t] = ti[0][t];
+        lp[(size_t)blockIdx.x * k + t] = tv[0][t] - log_shift;
+    }
+}
+
+// Copies positions [0, length) of slot src to slot dst in every layer's
+// four cache pools (Engine.CopyFrom).
+__global__ void kv_copy_kernel(int8_t* keys, int8_t* values, float* key_scales, float* value_scales, int slots,
+                               int capacity, int kv_heads, int dst, int src, int length)
+{
+    const int layer = blockIdx.y;
+    const size_t base = (size_t)layer * slots * capacity;
+    const size_t a = (base + (size_t)dst * capacity) * kv_heads;
+    const size_t b = (base + (size_t)src * capacity) * kv_heads;
+    const size_t cells = (size_t)length * kv_heads;
+    const size_t n16 = cells * 64 / 16;
+    const size_t stride = (size_t)gridDim.x * blockDim.x;
+    const size_t tid = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const uint4* ks = reinterpret_cast<const uint4*>(keys + b * 64);
+    const uint4* vs = reinterpret_cast<const uint4*>(values + b * 64);
+    uint4* kd = reinterpret_cast<uint4*>(keys + a * 64);
+    uint4* vd = reinterpret_cast<uint4*>(values + a * 64);
+    for (size_t i = tid; i < n16; i += stride) {
+        kd[i] = ks[i];
+        vd[i] = vs[i];
+    }
+    for (size_t i = tid; i < cells; i += stride) {
+        key_scales[a + i] = key_scales[b + i];
+        value_scales[a + i] = value_scales[b + i];
+    }
+}
+
+}  // namespace
+}  // namespace nhip
+
+using namespace nhip;
+
+struct nhip_decoder {
+    nhip_decoder_dims dims{};
+    int qkv_n = 0;
+    std::vector<nhip_weights*> wqkv, wo, wgu, wd;
+    nhip_weights* wlm = nullptr;
+    std::vector<float*> attn_norm, ffn_norm;
+    float* final_norm = nullptr;
+    float* emb = nullptr;
+    float* rope_cos = nullptr;
+    float* rope_sin = nullptr;
+    int8_t* keys = nullptr;
+    int8_t* values = nullptr;
+    float* key_scales = nullptr;
+    float* value_scales = nullptr;
+    // activations for up to max_rows rows
+    float* x = nullptr;
+    float* delta = nullptr;
+    int8_t* q8 = nullptr;
+    float* qs = nullptr;
+    float* qkv = nullptr;
+    int8_t* qh = nullptr;
+    float* qhs = nullptr;
+    float* att = nullptr;
+    float* gu = nullptr;
+    float* logits = nullptr;
+    int32_t* d_in = nullptr;  // tokens, slots, positions, first (0), count: 5 x max_rows
+    int32_t* d_topk_idx = nullptr;
+    float* d_topk_lp = nullptr;
+    int32_t* h_in = nullptr;  // pinned host mirror of d_in
+    int32_t* h_topk_idx = nullptr;
+    float* h_topk_lp = nullptr;
+    void* attn_ws = nullptr;
+    size_t attn_ws_bytes = 0;
+    hipStream_t stream = nullptr;
+    hipGraphExec_t graphs[kMaxTopK + 1] = {};
+    int graph_k[kMaxTopK + 1] = {};
+    std::vector<void*> allocations;
+};
+
+namespace {
+
+template <typename T>
+int32_t dalloc(nhip_decoder* m, T** p, size_t count)
+{
+    void* v = nullptr;
+    NHIP_CHECK_HIP(hipMalloc(&v, std::max<size_t>(count * sizeof(T), 256)));
+    m->allocations.push_back(v);
+    *p = static_cast<T*>(v);
+    return NHIP_OK;
+}
+
+int32_t* in_tokens(nhip_decoder* m, int32_t* base) { return base; }
+int32_t* in_slots(nhip_decoder* m, int32_t* base) { return base + m->dims.max_rows; }
+int32_t* in_positions(nhip_decoder* m, int32_t* base) { return base + 2 * m->dims.max_rows; }
+int32_t* in_first(nhip_decoder* m, int32_t* base) { return base + 3 * m->dims.max_rows; }
+int32_t* in_count(nhip_decoder* m, int32_t* base) { return base + 4 * m->dims.max_rows; }
+
+// Enqueues the forward of `rows` rows whose inputs are already in d_in.
+int32_t enqueue_forward(nhip_decoder* m, int rows, int k)
+{
+    const nhip_decoder_dims& D = m->dims;
+    const int d = D.d, H = D.heads, KV = D.kv_heads, F = D.ffn;
+    hipStream_t s = m->stream;
+    int32_t rc;
+    hipLaunchKernelGGL(embed_kernel, dim3(rows), dim3(kThreads), 0, s, in_tokens(m, m->d_in), m->emb, d, m->x);
+    NHIP_CHECK_HIP(hipGetLastError());
+    const size_t layer_cells = (size_t)D.slots * D.capacity * KV;
+    for (int l = 0; l < D.layers; l++) {
+        hipLaunchKernelGGL(add_rmsnorm_quant_kernel, dim3(rows), dim3(kThreads), 0, s, m->x,
+                           l == 0 ? nullptr : m->delta, m->attn_norm[l], d, D.eps, m->q8, m->qs);
+        NHIP_CHECK_HIP(hipGetLastError());
+        rc = nhip_matmul_i8_dev(m->wqkv[l], m->q8, m->qs, rows, m->qkv, m->qkv_n, 0, m->qkv_n, s);
+        if (rc) return rc;
+        PostParams pp{};
+        pp.qkv = m->qkv;
+        pp.slots = in_slots(m, m->d_in);
+        pp.positions = in_positions(m, m->d_in);
+        pp.rope_cos = m->rope_cos;
+        pp.rope_sin = m->rope_sin;
+        pp.q8 = m->qh;
+        pp.qs = m->qhs;
+        pp.keys = m->keys + (size_t)l * layer_cells * 64;
+        pp.values = m->values + (size_t)l * layer_cells * 64;
+        pp.key_scales = m->key_scales + (size_t)l * layer_cells;
+        pp.value_scales = m->value_scales + (size_t)l * layer_cells;
+        pp.heads = H;
+        pp.kv_heads = KV;
+        pp.capacity = D.capacity;
+        hipLaunchKernelGGL(qkv_post_kernel, dim3(rows, H + 2 * KV), dim3(64), 0, s, pp);
+        NHIP_CHECK_HIP(hipGetLastError());
+        rc = nhip_attention_decode_dev(m->qh, m->qhs, rows, H, KV, 64, pp.keys, pp.key_scales, pp.values,
+                                       pp.value_scales, D.slots, D.capacity, in_slots(m, m->d_in),
+                                       in_first(m, m->d_in), in_count(m, m->d_in), D.max_chunks, m->attn_ws,
+                                       m->attn_ws_bytes, m->att, s);
+        if (rc) return rc;
+        rc = nhip_quantize_rows_dev(m->att, rows, H * 64, m->q8, m->qs, s);
+        if (rc) return rc;
+        rc = nhip_matmul_i8_dev(m->wo[l], m->q8, m->qs, rows, m->delta, d, 0, d, s);
+        if (rc) return rc;
+        hipLaunchKernelGGL(add_rmsnorm_quant_kernel, dim3(rows), dim3(kThreads), 0, s, m->x, m->delta,
+                           m->ffn_norm[l], d, D.eps, m->q8, m->qs);
+        NHIP_CHECK_HIP(hipGetLastError());
+        rc = nhip_matmul_i8_dev(m->wgu[l], m->q8, m->qs, rows, m->gu, 2 * F, 0, 2 * F, s);
+        if (rc) return rc;
+        hipLaunchKernelGGL(swiglu_quant_kernel, dim3(rows), dim3(kThreads), 0, s, m->gu, F, m->q8, m->qs);
+        NHIP_CHECK_HIP(hipGetLastError());
+        rc = nhip_matmul_i8_dev(m->wd[l], m->q8, m->qs, rows, m->delta, d, 0, d, s);
+        if (rc) return rc;
+    }
+    hipLaunchKernelGGL(add_rmsnorm_quant_kernel, dim3(rows), dim3(kThreads), 0, s, m->x, m->delta, m->final_norm, d,
+                       D.eps, m->q8, m->qs);
+    NHIP_CHECK_HIP(hipGetLastError());
+    rc = nhip_matmul_i8_dev(m->wlm, m->q8, m->qs, rows, m->logits, D.vocab, 0, D.vocab, s);
+    if (rc) return rc;
+    if (k > 0) {
+        hipLaunchKernelGGL(topk_lse_kernel, dim3(rows), dim3(kThreads), 0, s, m->logits, D.vocab, k, m->d_topk_idx,
+                           m->d_topk_lp);
+        NHIP_CHECK_HIP(hipGetLastError());
+    }
+    return NHIP_OK;
+}
+
+int32_t stage_inputs(nhip_decoder* m, const int32_t* tokens, const int32_t* slots, const int32_t* positions,
+                     int rows)
+{
+    const nhip_decoder_dims& D = m->dims;
+    for (int r = 0; r < rows; r++) {
+        NHIP_REQUIRE(tokens[r] >= 0 && tokens[r] < D.vocab, "token %d out of range", tokens[r]);
+        NHIP_REQUIRE(slots[r] >= 0 && slots[r] < D.slots, "slot %d out of range", slots[r]);
+        NHIP_REQUIRE(positions[r] >= 0 && positions[r] < D.capacity, "position %d outside the cache capacity %d",
+                     positions[r], D.capacity);
+        in_tokens(m, m->h_in)[r] = tokens[r];
+        in_slots(m, m->h_in)[r] = slots[r];
+        in_positions(m, m->h_in)[r] = positions[r];
+        in_first(m, m->h_in)[r] = 0;
+        in_count(m, m->h_in)[r] = positions[r] + 1;
+    }
+    NHIP_CHECK_HIP(hipMemcpyAsync(m->d_in, m->h_in, sizeof(int32_t) * 5 * D.max_rows, hipMemcpyHostToDevice,
+                                  m->stream));
+    return NHIP_OK;
+}
+
+// Forward with the results of the top-k copied to the pinned mirrors; decode
+// row counts up to kMaxTopK replay a graph captured on first use.
+int32_t forward_step(nhip_decoder* m, const int32_t* tokens, const int32_t* slots, const int32_t* positions,
+                     int rows, int k, bool use_graph)
+{
+    int32_t rc = stage_inputs(m, tokens, slots, positions, rows);
+    if (rc) return rc;
+    if (use_graph && rows <= kMaxTopK) {
+        if (!m->graphs[rows] || m->graph_k[rows] != k) {
+            if (m->graphs[rows]) (void)hipGraphExecDestroy(m->graphs[rows]);
+            m->graphs[rows] = nullptr;
+            hipGraph_t g;
+            NHIP_CHECK_HIP(hipStreamBeginCapture(m->stream, hipStreamCaptureModeThreadLocal));
+            rc = enqueue_forward(m, rows, k);
+            hipError_t e = hipStreamEndCapture(m->stream, &g);
+            if (rc) {
+                if (e == hipSuccess) (void)hipGraphDestroy(g);
+                return rc;
+            }
+            NHIP_CHECK_HIP(e);
+            e = hipGraphInstantiate(&m->graphs[rows], g, nullptr, nullptr, 0);
+            (void)hipGraphDestroy(g);
+            NHIP_CHECK_HIP(e);
+            m->graph_k[rows] = k;
+        }
+        NHIP_CHECK_HIP(hipGraphLaunch(m->graphs[rows], m->stream));
+    } else {
+        rc = enqueue_forward(m, rows, k);
+        if (rc) return rc;
+    }
+    if (k > 0) {
+        NHIP_CHECK_HIP(hipMemcpyAsync(m->h_topk_idx, m->d_topk_idx, sizeof(int32_t) * rows * k, hipMemcpyDeviceToHost,
+                                      m->stream));
+        NHIP_CHECK_HIP(hipMemcpyAsync(m->h_topk_lp, m->d_topk_lp, sizeof(float) * rows * k, hipMemcpyDeviceToHost,
+                                      m->stream));
+    }
+    NHIP_CHECK_HIP(hipStreamSynchronize(m->stream));
+    return NHIP_OK;
+}
+
+int32_t copy_slot(nhip_decoder* m, int dst, int src, int length)
+{
+    const nhip_decoder_dims& D = m->dims;
+    NHIP_REQUIRE(dst >= 0 && dst < D.slots && src >= 0 && src < D.slots, "slot out of range");
+    NHIP_REQUIRE(length >= 0 && length <= D.capacity, "length %d outside [0, %d]", length, D.capacity);
+    if (length == 0 || dst == src) return NHIP_OK;
+    const size_t cells = (size_t)length * D.kv_heads;
+    const int grid = (int)std::min<size_t>((cells * 4 + 255) / 256, 1024);
+    hipLaunchKernelGGL(kv_copy_kernel, dim3(std::max(grid, 1), D.layers), dim3(256), 0, m->stream, m->keys, m->values,
+                       m->key_scales, m->value_scales, D.slots, D.capacity, D.kv_heads, dst, src, length);
+    NHIP_CHECK_HIP(hipGetLastError());
+    return NHIP_OK;
+}
+
+int32_t upload(nhip_decoder* m, float** dst, const float* src, size_t count)
+{
+    int32_t rc = dalloc(m, dst, count);
+    if (rc) return rc;
+    NHIP_CHECK_HIP(hipMemcpy(*dst, src, count * sizeof(float), hipMemcpyHostToDevice));
+    return NHIP_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int32_t nhip_decoder_create(const nhip_decoder_dims* dims, nhip_decoder** out)
+{
+    clear_error();
+    NHIP_REQUIRE(dims && out, "null argument");
+    const nhip_decoder_dims& D = *dims;
+    NHIP_REQUIRE(D.layers > 0 && D.d > 0 && D.d % 32 == 0 && D.d <= kMaxPerThread * kThreads,
+                 "d_model %d must be a positive multiple of 32 up to %d", D.d, kMaxPerThread * kThreads);
+    NHIP_REQUIRE(D.head_dim == 64, "head_dim must be 64");
+    NHIP_REQUIRE(D.heads > 0 && D.kv_heads > 0 && D.heads % D.kv_heads == 0 && D.heads / D.kv_heads <= 16,
+                 "heads/kv_heads");
+    NHIP_REQUIRE(D.heads * 64 % 32 == 0 && D.ffn > 0 && D.ffn % 32 == 0 && D.ffn <= kMaxPerThread * kThreads,
+                 "ffn %d must be a positive multiple of 32 up to %d", D.ffn, kMaxPerThread * kThreads);
+    NHIP_REQUIRE(D.vocab > 4 && D.capacity > 0 && D.slots > 0 && D.max_rows > 0 && D.max_chunks > 0,
+                 "vocab, capacity, slots, max_rows, max_chunks");
+    int32_t rc = ensure_device();
+    if (rc) return rc;
+    nhip_decoder* m = new nhip_decoder();
+    m->dims = D;
+    m->qkv_n = (D.heads + 2 * D.kv_heads) * 64;
+    m->wqkv.assign(D.layers, nullptr);
+    m->wo.assign(D.layers, nullptr);
+    m->wgu.assign(D.layers, nullptr);
+    m->wd.assign(D.layers, nullptr);
+    m->attn_norm.assign(D.layers, nullptr);
+    m->ffn_norm.assign(D.layers, nullptr);
+    const size_t cells = (size_t)D.layers * D.slots * D.capacity * D.kv_heads;
+    const int R = D.max_rows;
+    auto fail = [&](int32_t code) {
+        nhip_decoder_destroy(m);
+        return code;
+    };
+    if ((rc = dalloc(m, &m->keys, cells * 64)) || (rc = dalloc(m, &m->values, cells * 64)) ||
+        (rc = dalloc(m, &m->key_scales, cells)) || (rc = dalloc(m, &m->value_scales, cells)) ||
+        (rc = dalloc(m, &m->x, (size_t)R * D.d)) || (rc = dalloc(m, &m->delta, (size_t)R * D.d)) ||
+        (rc = dalloc(m, &m->q8, (size_t)R * std::max({D.d, D.ffn, D.heads * 64}))) || (rc = dalloc(m, &m->qs, (size_t)R)) ||
+        (rc = dalloc(m, &m->qkv, (size_t)R * m->qkv_n)) || (rc = dalloc(m, &m->qh, (size_t)R * D.heads * 64)) ||
+        (rc = dalloc(m, &m->qhs, (size_t)R * D.heads)) || (rc = dalloc(m, &m->att, (size_t)R * D.heads * 64)) ||
+        (rc = dalloc(m, &m->gu, (size_t)R * 2 * D.ffn)) || (rc = dalloc(m, &m->logits, (size_t)R * D.vocab)) ||
+        (rc = dalloc(m, &m->d_in, (size_t)5 * R)) || (rc = dalloc(m, &m->d_topk_idx, (size_t)R * kMaxTopK)) ||
+        (rc = dalloc(m, &m->d_topk_lp, (size_t)R * kMaxTopK)))
+        return fail(rc);
+    m->attn_ws_bytes = nhip_attention_decode_workspace(R, D.heads, D.max_chunks);
+    void* ws = nullptr;
+    if (hipMalloc(&ws, m->attn_ws_bytes) != hipSuccess) {
+        set_error("hipMalloc of %zu bytes for the attention workspace failed", m->attn_ws_bytes);
+        return fail(NHIP_ERR_HIP);
+    }
+    m->allocations.push_back(ws);
+    m->attn_ws = ws;
+    if (hipHostMalloc(reinterpret_cast<void**>(&m->h_in), sizeof(int32_t) * 5 * R, hipHostMallocDefault) !=
+            hipSuccess ||
+        hipHostMalloc(reinterpret_cast<void**>(&m->h_topk_idx), sizeof(int32_t) * R * kMaxTopK,
+                      hipHostMallocDefault) != hipSuccess ||
+        hipHostMalloc(reinterpret_cast<void**>(&m->h_topk_lp), sizeof(float) * R * kMaxTopK, hipHostMallocDefault) !=
+            hipSuccess) {
+        set_error("hipHostMalloc failed");
+        return fail(NHIP_ERR_HIP);
+    }
+    if (hipStreamCreateWithFlags(&m->stream, hipStreamNonBlocking) != hipSuccess) {
+        set_error("hipStreamCreate failed");
+        return fail(NHIP_ERR_HIP);
+    }
+    // RoPE table: cos/sin of p * theta^(-2i/64) in double, rounded to float
+    std::vector<float> c((size_t)D.capacity * 32), sn((size_t)D.capacity * 32);
+    for (int p = 0; p < D.capacity; p++)
+        for (int i = 0; i < 32; i++) {
+            const double angle = (double)p * std::pow(D.theta, -2.0 * i / 64);
+            c[(size_t)p * 32 + i] = (float)std::cos(angle);
+            sn[(size_t)p * 32 + i] = (float)std::sin(angle);
+        }
+    if ((rc = upload(m, &m->rope_cos, c.data(), c.size())) || (rc = upload(m, &m->rope_sin, sn.data(), sn.size())))
+        return fail(rc);
+    if (hipMemset(m->keys, 0, cells * 64) != hipSuccess || hipMemset(m->values, 0, cells * 64) != hipSuccess ||
+        hipMemset(m->key_scales, 0, cells * 4) != hipSuccess || hipMemset(m->value_scales, 0, cells * 4) != hipSuccess) {
+        set_error("hipMemset failed");
+        return fail(NHIP_ERR_HIP);
+    }
+    *out = m;
+    return NHIP_OK;
+}
+
+int32_t nhip_decoder_set_layer(nhip_decoder* m, int32_t layer, const int8_t* wqkv, const uint16_t* sqkv,
+                               const int8_t* wo, const uint16_t* so, const int8_t* wgu, const uint16_t* sgu,
+                               const int8_t* wd, const uint16_t* sd, const float* attn_norm, const float* ffn_norm)
+{
+    clear_error();
+    NHIP_REQUIRE(m && layer >= 0 && layer < m->dims.layers, "bad decoder or layer %d", layer);
+    NHIP_REQUIRE(wqkv && sqkv && wo && so && wgu && sgu && wd && sd && attn_norm && ffn_norm, "null weights");
+    const nhip_decoder_dims& D = m->dims;
+    int32_t rc;
+    nhip_weights** slots[4] = {&m->wqkv[layer], &m->wo[layer], &m->wgu[layer], &m->wd[layer]};
+    const int8_t* ws[4] = {wqkv, wo, wgu, wd};
+    const uint16_t* ss[4] = {sqkv, so, sgu, sd};
+    const int rows[4] = {m->qkv_n, D.d, 2 * D.ffn, D.d};
+    const int cols[4] = {D.d, D.heads * 64, D.d, D.ffn};
+    for (int i = 0; i < 4; i++) {
+        if (*slots[i]) nhip_weights_destroy(*slots[i]);
+        *slots[i] = nullptr;
+        if ((rc = nhip_weights_i8_create(ws[i], ss[i], rows[i], cols[i], slots[i]))) return rc;
+    }
+    if (!m->attn_norm[layer] && (rc = dalloc(m, &m->attn_norm[layer], D.d))) return rc;
+    if (!m->ffn_norm[layer] && (rc = dalloc(m, &m->ffn_norm[layer], D.d))) return rc;
+    NHIP_CHECK_HIP(hipMemcpy(m->attn_norm[layer], attn_norm, sizeof(float) * D.d, hipMemcpyHostToDevice));
+    NHIP_CHECK_HIP(hipMemcpy(m->ffn_norm[layer], ffn_norm, sizeof(float) * D.d, hipMemcpyHostToDevice));
+    return NHIP_OK;
+}
+
+int32_t nhip_decoder_set_head(nhip_decoder* m, const float* embedding, const float* final_norm, const int8_t* wlm,
+                              const uint16_t* slm)
+{
+    clear_error();
+    NHIP_REQUIRE(m && embedding && final_norm && wlm && slm, "null argument");
+    const nhip_decoder_dims& D = m->dims;
+    int32_t rc;
+    if (!m->emb && (rc = dalloc(m, &m->emb, (size_t)D.vocab * D.d))) return rc;
+    if (!m->final_norm && (rc = dalloc(m, &m->final_norm, D.d))) return rc;
+    NHIP_CHECK_HIP(hipMemcpy(m->emb, embedding, sizeof(float) * D.vocab * D.d, hipMemcpyHostToDevice));
+    NHIP_CHECK_HIP(hipMemcpy(m->final_norm, final_norm, sizeof(float) * D.d, hipMemcpyHostToDevice));
+    if (m->wlm) nhip_weights_destroy(m->wlm);
+    m->wlm = nullptr;
+    return nhip_weights_i8_create(wlm, slm, D.vocab, D.d, &m->wlm);
+}
+
+static int32_t ready(const nhip_decoder* m)
+{
+    NHIP_REQUIRE(m, "null decoder");
+    NHIP_REQUIRE(m->wlm && m->emb, "decoder head not set");
+    for (int l = 0; l < m->dims.layers; l++) NHIP_REQUIRE(m->wqkv[l], "decoder layer %d not set", l);
+    return NHIP_OK;
+}
+
+int32_t nhip_decoder_forward(nhip_decoder* m, const int32_t* tokens, const int32_t* slots, const int32_t* positions,
+                             int32_t rows, float* logits, int32_t k, int32_t* topk_idx, float* topk_lp)
+{
+    clear_error();
+    int32_t rc = ready(m);
+    if (rc) return rc;
+    NHIP_REQUIRE(rows > 0 && rows <= m->dims.max_rows, "rows %d outside [1, %d]", rows, m->dims.max_rows);
+    NHIP_REQUIRE(k >= 0 && k <= kMaxTopK && (k == 0 || (topk_idx && topk_lp)), "k %d outside [0, %d]", k, kMaxTopK);
+    NHIP_REQUIRE(tokens && slots && positions, "null inputs");
+    rc = forward_step(m, tokens, slots, positions, rows, k, false);
+    if (rc) return rc;
+    if (k > 0) {
+        std::memcpy(topk_idx, m->h_topk_idx, sizeof(int32_t) * rows * k);
+        std::memcpy(topk_lp, m->h_topk_lp, sizeof(float) * rows * k);
+    }
+    if (logits)
+        NHIP_CHECK_HIP(hipMemcpy(logits, m->logits, sizeof(float) * rows * m->dims.vocab, hipMemcpyDeviceToHost));
+    return NHIP_OK;
+}
+
+int32_t nhip_decoder_copy_slot(nhip_decoder* m, int32_t dst, int32_t src, int32_t length)
+{
+    clear_error();
+    NHIP_REQUIRE(m, "null decoder");
+    int32_t rc = copy_slot(m, dst, src, length);
+    if (rc) return rc;
+    NHIP_CHECK_HIP(hipStreamSynchronize(m->stream));
+    return NHIP_OK;
+}
+
+int32_t nhip_decoder_beam_search(nhip_decoder* m, const int32_t* prompt, int32_t prompt_len, int32_t width,
+                                 int32_t max_new, int32_t eos, int32_t* out_tokens, int32_t* out_len, float* out_score,
+                                 nhip_decode_stats* stats)
+{
+    clear_error();
+    int32_t rc = ready(m);
+    if (rc) return rc;
+    const nhip_decoder_dims& D = m->dims;
+    NHIP_REQUIRE(prompt && prompt_len > 0 && prompt_len <= D.max_rows, "prompt length %d outside [1, %d]", prompt_len,
+                 D.max_rows);
+    NHIP_REQUIRE(width >= 1 && width <= kMaxTopK && width <= D.slots && width <= D.max_rows,
+                 "beam width %d needs width <= %d, slots and max_rows", width, kMaxTopK);
+    NHIP_REQUIRE(max_new >= 0 && prompt_len + max_new <= D.capacity, "prompt + new tokens exceed the capacity %d",
+                 D.capacity);
+    NHIP_REQUIRE(out_tokens && out_len && out_score, "null outputs");
+    const int W = width;
+    using clock = std::chrono::steady_clock;
+    const auto t0 = clock::now();
+    // prefill the prompt into slot 0; its last row's top-k starts the search
+    std::vector<int32_t> pos(prompt_len), sl(prompt_len, 0);
+    for (int i = 0; i < prompt_len; i++) pos[i] = i;
+    rc = forward_step(m, prompt, sl.data(), pos.data(), prompt_len, W, false);
+    if (rc) return rc;
+    std::vector<int32_t> top_idx(m->h_topk_idx + (size_t)(prompt_len - 1) * W, m->h_topk_idx + (size_t)prompt_len * W);
+    std::vector<float> top_lp(m->h_topk_lp + (size_t)(prompt_len - 1) * W, m->h_topk_lp + (size_t)prompt_len * W);
+    const auto t1 = clock::now();
+
+    struct Cand {
+        float score;
+        int parent, token;
+    };
+    struct Fin {
+        float score;
+        std::vector<int32_t> tokens;
+    };
+    std::vector<std::vector<int32_t>> live_tok(1), next_tok;
+    std::vector<float> live_score(1, 0.0f);
+    std::vector<int> live_slot(1, 0);
+    std::vector<Fin> finished;
+    int live_count = 1;
+    long fed = 0;
+    int steps = 0;
+    for (int step = 0; step < max_new; step++) {
+        std::vector<Cand> cand;
+        for (int i = 0; i < live_count; i++)
+            for (int k = 0; k < W; k++) cand.push_back({live_score[i] + top_lp[(size_t)i * W + k], i, top_idx[(size_t)i * W + k]});
+        std::stable_sort(cand.begin(), cand.end(), [](const Cand& a, const Cand& b) { return a.score > b.score; });
+        std::vector<int> parents, picks;
+        std::vector<float> pick_scores;
+        for (const Cand& c : cand) {
+            if (c.token == eos)
+                finished.push_back({c.score, live_tok[c.parent]});
+            else {
+                parents.push_back(c.parent);
+                picks.push_back(c.token);
+                pick_scores.push_back(c.score);
+            }
+            if ((int)parents.size() >= W) break;
+        }
+        const int kept = (int)parents.size();
+        if (kept == 0) break;
+        if ((int)finished.size() >= W) {
+            float best_fin = -INFINITY, best_live = -INFINITY;
+            for (const Fin& f : finished) best_fin = std::max(best_fin, f.score / (float)(f.tokens.size() + 1));
+            for (int j = 0; j < kept; j++)
+                best_live = std::max(best_live, pick_scores[j] / (float)(live_tok[parents[j]].size() + 1));
+            if (best_fin >= best_live) break;
+        }
+        std::vector<int> last_child(live_count, -1), next_slot(kept);
+        for (int j = 0; j < kept; j++) last_child[parents[j]] = j;
+        std::vector<char> used(D.slots, 0);
+        for (int j = 0; j < kept; j++)
+            if (j == last_child[parents[j]]) used[live_slot[parents[j]]] = 1;
+        next_tok.assign(kept, {});
+        std::vector<int32_t> feed_tok(kept), feed_slot(kept), feed_pos(kept);
+        for (int j = 0; j < kept; j++) {
+            const int p = parents[j];
+            if (j == last_child[p]) {
+                next_slot[j] = live_slot[p];
+            } else {
+                int f = 0;
+                while (used[f]) f++;
+                used[f] = 1;
+                rc = copy_slot(m, f, live_slot[p], prompt_len + (int)live_tok[p].size());
+                if (rc) return rc;
+                next_slot[j] = f;
+            }
+            next_tok[j] = live_tok[p];
+            next_tok[j].push_back(picks[j]);
+            feed_tok[j] = picks[j];
+            feed_slot[j] = next_slot[j];
+            feed_pos[j] = prompt_len + (int)live_tok[p].size();
+        }
+        rc = forward_step(m, feed_tok.data(), feed_slot.data(), feed_pos.data(), kept, W, true);
+        if (rc) return rc;
+        fed += kept;
+        steps++;
+        top_idx.assign(m->h_topk_idx, m->h_topk_idx + (size_t)kept * W);
+        top_lp.assign(m->h_topk_lp, m->h_topk_lp + (size_t)kept * W);
+        live_tok.swap(next_tok);
+        live_slot = next_slot;
+        live_score = pick_scores;
+        live_count = kept;
+    }
+    const auto t2 = clock::now();
+    const std::vector<int32_t>* winner = nullptr;
+    float winner_score = -INFINITY;
+    for (const Fin& f : finished) {
+        const float sc = f.score / (float)(f.tokens.size() + 1);
+        if (sc > winner_score) {
+            winner_score = sc;
+            winner = &f.tokens;
+        }
+    }
+    if (!winner)
+        for (int j = 0; j < live_count; j++) {
+            const float sc = live_score[j] / (float)live_tok[j].size();
+            if (sc > winner_score) {
+                winner_score = sc;
+                winner = &live_tok[j];
+            }
+        }
+    *out_len = winner ? (int32_t)winner->size() : 0;
+    if (winner) std::copy(winner->begin(), winner->end(), out_tokens);
+    *out_score = winner_score;
+    if (stats) {
+        stats->prefill_seconds = std::chrono::duration<double>(t1 - t0).count();
+        stats->decode_seconds = std::chrono::duration<double>(t2 - t1).count();
+        stats->fed_rows = fed;
+        stats->steps = steps;
+    }
+    return NHIP_OK;
+}
+
+int32_t nhip_decoder_destroy(nhip_decoder* m)
+{
+    if (!m) return NHIP_OK;
+    if (m->stream) (void)hipStreamSynchronize(m->stream);
+    for (auto& g : m->graphs)
+        if (g) (void)hipGraphExecDestroy(g);
+    for (auto* w : m->wqkv) nhip_weights_destroy(w);
+    for (auto* w : m->wo) nhip_weights_destroy(w);
+    for (auto* w : m->wgu) nhip_weights_destroy(w);
+    for (auto* w : m->wd) nhip_weights_destroy(w);
+    nhip_weights_destroy(m->wlm);
+    for (void* p : m->allocations) (void)hipFree(p);
+    if (m->h_in) (void)hipHostFree(m->h_in);
+    if (m->h_topk_idx) (void)hipHostFree(m->h_topk_idx);
+    if (m->h_topk_lp) (void)hipHostFree(m->h_topk_lp);
+    if (m->stream) (void)hipStreamDestroy(m->stream);
+    delete m;
+    return NHIP_OK;
+}
+
+}  // extern "C"

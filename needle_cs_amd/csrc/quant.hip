@@ -27,12 +27,6 @@ __device__ __forceinline__ int wave_sum(int v)
     return v;
 }
 
-__device__ __forceinline__ int quantize_one(float x, float inverse)
-{
-    const float r = ref_round_even(x * inverse);
-    return static_cast<int>(fminf(fmaxf(r, -128.0f), 127.0f));
-}
-
 // One block of 256 threads per row.
 __global__ __launch_bounds__(256) void quantize_rows_kernel(const float* __restrict__ x, int cols,
                                                            int8_t* __restrict__ q, float* __restrict__ scales)
@@ -48,7 +42,7 @@ __global__ __launch_bounds__(256) void quantize_rows_kernel(const float* __restr
     const float scale = peak > 0.0f ? peak / 127.0f : 1.0f;
     const float inverse = 1.0f / scale;
     int8_t* out = q + (size_t)blockIdx.x * cols;
-    for (int i = threadIdx.x; i < cols; i += 256) out[i] = static_cast<int8_t>(quantize_one(row[i], inverse));
+    for (int i = threadIdx.x; i < cols; i += 256) out[i] = static_cast<int8_t>(ref_quantize_one(row[i], inverse));
     if (threadIdx.x == 0) scales[blockIdx.x] = scale;
 }
 
@@ -86,8 +80,8 @@ __global__ __launch_bounds__(256) void prepare_kernel(const float* __restrict__ 
     const float peak = wave_max(fmaxf(fabsf(v0), fabsf(v1)));
     const float scale = peak > 0.0f ? peak / 127.0f : 1.0f;
     const float inverse = 1.0f / scale;
-    const int q0 = quantize_one(v0, inverse);
-    const int q1 = quantize_one(v1, inverse);
+    const int q0 = ref_quantize_one(v0, inverse);
+    const int q1 = ref_quantize_one(v1, inverse);
     const int sum = wave_sum(q0 + q1);
     // Planes (Scalar.cs:91-111): destination d takes quantized[src(d)].
     int8_t* dst = values + (size_t)t * cols + g * 128;

@@ -14,7 +14,7 @@ import ctypes as C
 
 import numpy as np
 
-from . import synth_half_uniform, synth_int8, synth_normal, synth_uniform
+from . import check, lib, synth_half_uniform, synth_int8, synth_normal, synth_uniform
 
 CONFIG4 = dict(layers=12, d=1024, heads=16, kv_heads=16, head_dim=64, ffn=4096, vocab=32000, theta=10000.0,
                eps=1e-5)
@@ -53,3 +53,73 @@ def random_prompt(seed: int, length: int, vocab: int) -> np.ndarray:
     st = C.c_uint64(seed)
     v = synth_uniform(st, length, 0.0, 1.0).astype(np.float64)
     return (4 + np.minimum((v * (vocab - 4)).astype(np.int64), vocab - 5)).astype(np.int32)
+
+
+class DecoderDims(C.Structure):
+    _fields_ = [("layers", C.c_int32), ("d", C.c_int32), ("heads", C.c_int32), ("kv_heads", C.c_int32),
+                ("head_dim", C.c_int32), ("ffn", C.c_int32), ("vocab", C.c_int32), ("capacity", C.c_int32),
+                ("slots", C.c_int32), ("max_rows", C.c_int32), ("max_chunks", C.c_int32), ("theta", C.c_double),
+                ("eps", C.c_float)]
+
+
+class DecodeStats(C.Structure):
+    _fields_ = [("prefill_seconds", C.c_double), ("decode_seconds", C.c_double), ("fed_rows", C.c_int64),
+                ("steps", C.c_int32)]
+
+
+def _p(a: np.ndarray) -> int:
+    assert a.flags["C_CONTIGUOUS"]
+    return a.ctypes.data
+
+
+class GpuDecoder:
+    """libneedle_hip's decoder engine holding a synthetic model in HBM."""
+
+    def __init__(self, model: dict, slots: int, capacity: int, max_rows: int, max_chunks: int = 64):
+        dm = model["dims"]
+        self.dims = DecoderDims(dm["layers"], dm["d"], dm["heads"], dm["kv_heads"], dm["head_dim"], dm["ffn"],
+                                dm["vocab"], capacity, slots, max_rows, max_chunks, dm["theta"], dm["eps"])
+        h = C.c_void_p()
+        check(lib().nhip_decoder_create(C.byref(self.dims), C.byref(h)))
+        self.h = h.value
+        for l, lw in enumerate(model["layers"]):
+            check(lib().nhip_decoder_set_layer(self.h, l, *[_p(lw[n]) for n in ("wqkv", "sqkv", "wo", "so", "wgu",
+                                                                                "sgu", "wd", "sd", "attn_norm",
+                                                                                "ffn_norm")]))
+        check(lib().nhip_decoder_set_head(self.h, _p(model["embedding"]), _p(model["final_norm"]), _p(model["wlm"]),
+                                          _p(model["slm"])))
+        self.vocab = dm["vocab"]
+
+    def forward(self, tokens, slots, positions, k=0, logits=True):
+        rows = len(tokens)
+        t, s, ps = (np.ascontiguousarray(a, dtype=np.int32) for a in (tokens, slots, positions))
+        lg = np.zeros((rows, self.vocab), dtype=np.float32) if logits else None
+        idx = np.zeros((rows, max(k, 1)), dtype=np.int32)
+        lp = np.zeros((rows, max(k, 1)), dtype=np.float32)
+        check(lib().nhip_decoder_forward(self.h, _p(t), _p(s), _p(ps), rows, _p(lg) if logits else None, k, _p(idx),
+                                         _p(lp)))
+        return lg, idx[:, :k], lp[:, :k]
+
+    def copy_slot(self, dst, src, length):
+        check(lib().nhip_decoder_copy_slot(self.h, dst, src, length))
+
+    def beam_search(self, prompt, width, max_new, eos):
+        pr = np.ascontiguousarray(prompt, dtype=np.int32)
+        out = np.zeros(max_new + 1, dtype=np.int32)
+        n = C.c_int32()
+        score = C.c_float()
+        stats = DecodeStats()
+        check(lib().nhip_decoder_beam_search(self.h, _p(pr), len(pr), width, max_new, eos, _p(out), C.byref(n),
+                                             C.byref(score), C.byref(stats)))
+        return out[:n.value].copy(), score.value, stats
+
+    def close(self):
+        if self.h:
+            lib().nhip_decoder_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass

@@ -199,7 +199,9 @@ void or_decoder_forward(or_decoder* m, const int* tokens, const int* slots, cons
     int qkv_n = (H + 2 * KV) * hd;
     float* x = (float*)malloc(sizeof(float) * (size_t)rows * d);
     float* h = (float*)malloc(sizeof(float) * (size_t)(d > F ? d : F));
-    int8_t* q8 = (int8_t*)malloc((size_t)rows * (F > d ? F : d));
+    int qw = F > d ? F : d;
+    if (H * hd > qw) qw = H * hd;
+    int8_t* q8 = (int8_t*)malloc((size_t)rows * qw);
     float* qs = (float*)malloc(sizeof(float) * rows);
     float* qkv = (float*)malloc(sizeof(float) * (size_t)rows * qkv_n);
     int8_t* qh = (int8_t*)malloc((size_t)rows * H * hd);
@@ -245,7 +247,7 @@ void or_decoder_forward(or_decoder* m, const int* tokens, const int* slots, cons
                             count, D->max_chunks, att);
         free(slot_rel);
         for (int r = 0; r < rows; r++)
-            qs[r] = or_quantize_int8(att + (size_t)r * H * hd, H * hd, q8 + (size_t)r * d);
+            qs[r] = or_quantize_int8(att + (size_t)r * H * hd, H * hd, q8 + (size_t)r * H * hd);
         linear(m, W->wo, W->so, d, H * hd, q8, qs, rows, delta);
         for (int r = 0; r < rows; r++)
             qs[r] = or_add_rmsnorm_quant(x + (size_t)r * d, delta + (size_t)r * d, W->ffn_norm, d, D->eps, h,

@@ -54,7 +54,7 @@ def bit_equal(a, b):
     return np.array_equal(a.view(np.uint32), b.view(np.uint32))
 
 
-@pytest.mark.parametrize("heads,kv_heads,qk", [(16, 16, 64), (12, 2, 48), (4, 1, 64), (8, 8, 48)])
+@pytest.mark.parametrize("heads,kv_heads,qk", [(16, 16, 64), (12, 2, 48), (4, 1, 64), (8, 8, 48), (6, 2, 64)])
 @pytest.mark.parametrize("max_chunks", [8, 64])
 def test_decode_attention_bit_exact(hip, orc, heads, kv_heads, qk, max_chunks):
     cache = Cache(orc, hip, 1000 + heads + kv_heads + qk, 4, 2048, kv_heads, qk)

@@ -18,7 +18,7 @@ def run_fused(hip, weights, q, qs, tokens, ldy, r0, r1):
 
 
 SHAPES = [(32, 64, 64), (64, 256, 512), (100, 80, 96), (65, 48, 32), (128, 1024, 2048), (512, 512, 2048),
-          (200, 130, 4096)]
+          (200, 130, 4096), (33, 256, 384), (40, 1000, 256), (33, 640, 256)]
 
 
 @pytest.mark.parametrize("tokens,rows,cols", SHAPES)

@@ -15,6 +15,7 @@ import pytest
 from needle_cs_amd.decoder import random_prompt, synthetic_model
 
 TINY = dict(layers=2, d=128, heads=2, kv_heads=2, head_dim=64, ffn=256, vocab=300, theta=10000.0, eps=1e-5)
+GQA = dict(layers=2, d=256, heads=6, kv_heads=2, head_dim=64, ffn=512, vocab=1000, theta=10000.0, eps=1e-5)
 
 
 def test_log_poly_against_log(orc):
@@ -98,11 +99,12 @@ def tiny(orc):
     dec.close()
 
 
-def test_decoder_batched_equals_single(orc, tiny):
-    model, _ = tiny
+@pytest.mark.parametrize("dims", [TINY, GQA], ids=["tiny", "gqa"])
+def test_decoder_batched_equals_single(orc, dims):
+    model = synthetic_model(dims, 4243)
     a = orc.CpuDecoder(model, slots=3, capacity=32)
     b = orc.CpuDecoder(model, slots=3, capacity=32)
-    prompts = [random_prompt(s, 6, TINY["vocab"]) for s in (1, 2, 3)]
+    prompts = [random_prompt(s, 6, dims["vocab"]) for s in (1, 2, 3)]
     for i, pr in enumerate(prompts):  # prefill each slot alone in both
         for dec in (a, b):
             dec.forward(pr, [i] * 6, np.arange(6))
