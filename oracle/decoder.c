@@ -16,9 +16,11 @@
  * reference; their order (written out in each function) is the canonical
  * one that the GPU kernels reproduce operation for operation.
  */
+#define _POSIX_C_SOURCE 199309L
 #include <math.h>
 #include <stdlib.h>
 #include <string.h>
+#include <time.h>
 
 #include "needle_oracle.h"
 
@@ -295,9 +297,17 @@ typedef struct { float score; int parent, token; } cand_t;
  * score with ties in insertion order (a stable sort; List.Sort leaves ties
  * unspecified).  Returns the winner's length; tokens[], score, and the
  * number of forward rows fed after the prompt (for tokens/s). */
-int or_beam_search(or_decoder* m, const int* prompt, int prompt_len, int width, int max_new, int eos,
-                   int* out_tokens, float* out_score, long* fed_rows)
+static double now_s(void)
 {
+    struct timespec ts;
+    clock_gettime(CLOCK_MONOTONIC, &ts);
+    return (double)ts.tv_sec + 1e-9 * (double)ts.tv_nsec;
+}
+
+int or_beam_search(or_decoder* m, const int* prompt, int prompt_len, int width, int max_new, int eos,
+                   int* out_tokens, float* out_score, long* fed_rows, double* seconds)
+{
+    double t0 = now_s();
     int W = width, V = m->dims.vocab;
     int slots_live[16], slots_next[16];
     int* live_tok = (int*)malloc(sizeof(int) * W * (max_new + 1));
@@ -323,6 +333,7 @@ int or_beam_search(or_decoder* m, const int* prompt, int prompt_len, int width, 
         or_topk_lse(lg + (size_t)(prompt_len - 1) * m->dims.vocab, m->dims.vocab, W, 1, topk_idx, topk_lp);
         free(lg);
     }
+    double t1 = now_s();
     int live_count = 1;
     slots_live[0] = 0;
     live_len[0] = 0;
@@ -410,6 +421,11 @@ int or_beam_search(or_decoder* m, const int* prompt, int prompt_len, int width, 
         }
         int* t = live_tok; live_tok = next_tok; next_tok = t;
         live_count = kept;
+    }
+    double t2 = now_s();
+    if (seconds) {
+        seconds[0] = t1 - t0;
+        seconds[1] = t2 - t1;
     }
     int winner_len = 0;
     float winner_score = -INFINITY;

@@ -279,8 +279,9 @@ void or_decoder_free(or_decoder* m);
 void or_decoder_forward(or_decoder* m, const int* tokens, const int* slots, const int* positions, int rows,
                         float* logits, int k, int* topk_idx, float* topk_lp);
 void or_decoder_copy_slot(or_decoder* m, int dst, int src, int length);
+/* seconds (if given): [prefill, decode] wall time. */
 int or_beam_search(or_decoder* m, const int* prompt, int prompt_len, int width, int max_new, int eos,
-                   int* out_tokens, float* out_score, long* fed_rows);
+                   int* out_tokens, float* out_score, long* fed_rows, double* seconds);
 
 #ifdef __cplusplus
 }

@@ -109,7 +109,7 @@ _PROTOS = {
     "or_decoder_free": (None, [C.POINTER(Decoder)]),
     "or_decoder_forward": (None, [C.POINTER(Decoder), _vp, _vp, _vp, _i, _vp, _i, _vp, _vp]),
     "or_decoder_copy_slot": (None, [C.POINTER(Decoder), _i, _i, _i]),
-    "or_beam_search": (_i, [C.POINTER(Decoder), _vp, _i, _i, _i, _i, _vp, C.POINTER(_f), C.POINTER(C.c_long)]),
+    "or_beam_search": (_i, [C.POINTER(Decoder), _vp, _i, _i, _i, _i, _vp, C.POINTER(_f), C.POINTER(C.c_long), _vp]),
     "or_argmax": (_i, [_vp, _i]),
     "or_topk_log_softmax": (None, [_vp, _i, _i, _vp, _vp, _vp, _i]),
     "or_baseline_start": (_i, [_i]),
@@ -298,8 +298,9 @@ class CpuDecoder:
         out = np.zeros(max_new + 1, dtype=np.int32)
         score = C.c_float()
         fed = C.c_long()
+        self.seconds = np.zeros(2, dtype=np.float64)
         n = lib().or_beam_search(C.byref(self.dec), p(pr), len(pr), width, max_new, eos, p(out), C.byref(score),
-                                 C.byref(fed))
+                                 C.byref(fed), p(self.seconds))
         return out[:n].copy(), score.value, fed.value
 
     def close(self):
