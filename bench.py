@@ -198,7 +198,7 @@ def decode_loop(args, threads: int) -> dict:
     prompt = random_prompt(0x6006, 128, CONFIG4["vocab"])
     gen_s = time.perf_counter() - t0
     width, max_new, eos = 3, 64, 1
-    gpu = GpuDecoder(model, slots=width, capacity=256, max_rows=128)
+    gpu = GpuDecoder(model, slots=width, capacity=256, max_rows=128, max_chunks=args.decode_chunks)
     gpu.beam_search(prompt, width, max_new, eos)  # captures the per-row-count graphs
     runs = []
     for _ in range(3):
@@ -221,7 +221,7 @@ def decode_loop(args, threads: int) -> dict:
     if not args.no_cpu:
         from oracle import oracle as O  # the CPU path, timed as the baseline and compared token for token
 
-        cpu = O.CpuDecoder(model, slots=width, capacity=256, threads=threads)
+        cpu = O.CpuDecoder(model, slots=width, capacity=256, threads=threads, max_chunks=args.decode_chunks)
         ctoks, cscore, cfed = cpu.beam_search(prompt, width, max_new, eos)
         cpre, cdec = float(cpu.seconds[0]), float(cpu.seconds[1])
         cpu.close()
@@ -306,6 +306,8 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-secondary", action="store_true")
     ap.add_argument("--no-decode-loop", action="store_true")
+    ap.add_argument("--decode-chunks", type=int, default=64,
+                    help="attention position-split cap of the decode loop (1: one chunk per row with the output quantize fused)")
     ap.add_argument("--pmc-run", type=int, default=0, metavar="LAUNCHES",
                     help="counter-collection mode: a 64 MiB device copy (the calibration kernel of known size), "
                          "then LAUNCHES eager headline GEMVs; prints no JSON line")

@@ -49,6 +49,8 @@ struct DecodeAttnParams {
     float* sums;            // [rows][max_chunks][heads]
     float* partials;        // [rows][max_chunks][heads][64]
     float* out;             // [rows][heads][64]
+    int8_t* q_out;          // optional: QuantizeInt8 of each output row [rows][heads*64]
+    float* qs_out;          //   and its scale [rows] (single-chunk plans, one head block)
     int32_t rows, heads, kv_heads, qk, slots, capacity, max_chunks, lmax, kv_per_block;
     float inv_sqrt;
 };
@@ -112,7 +114,15 @@ __global__ __launch_bounds__(kThreads) void decode_attention_kernel(DecodeAttnPa
     const int count = p.row_count[row];
     // rows with an invalid slot or span produce zeros (no out-of-range reads)
     const bool valid = slot >= 0 && slot < p.slots && first >= 0 && count >= 1 && count <= p.capacity - first;
-    if (!valid) return;  // the merge writes zeros
+    if (!valid) {
+        if (chunk == 0 && tid < nh * 16) {
+            *reinterpret_cast<float4*>(p.out + ((size_t)row * p.heads + h0 + (tid >> 4)) * 64 + 4 * (tid & 15)) =
+                make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            if (p.q_out) *reinterpret_cast<uint32_t*>(p.q_out + (size_t)row * p.heads * 64 + 4 * tid) = 0u;
+        }
+        if (chunk == 0 && tid == 0 && p.q_out) p.qs_out[row] = 1.0f;
+        return;
+    }
     int length;
     const int needed = plan(count, p.max_chunks, &length);
     if (chunk >= needed) return;
@@ -221,6 +231,7 @@ __global__ __launch_bounds__(kThreads) void decode_attention_kernel(DecodeAttnPa
 
     // phase 4: one thread per (head, 4 dims), positions in ascending order
     const size_t pbase = ((size_t)row * p.max_chunks + chunk) * p.heads;
+    float vout[4] = {0.0f, 0.0f, 0.0f, 0.0f};
     if (vthread) {
         const int hl = vhl;
         float o0 = 0.0f, o1 = 0.0f, o2 = 0.0f, o3 = 0.0f, total = 0.0f;
@@ -249,13 +260,51 @@ __global__ __launch_bounds__(kThreads) void decode_attention_kernel(DecodeAttnPa
             }
         }
         const int h = h0 + hl;
-        *reinterpret_cast<float4*>(p.partials + (pbase + h) * 64 + 4 * vqd) = make_float4(o0, o1, o2, o3);
-        if (vqd == 0) {
-            p.peaks[pbase + h] = order_value(peak_key[hl]);
-            p.sums[pbase + h] = total;
+        if (needed == 1) {
+            // the merge of a single partial, in MergePartials' order with
+            // w = Exp(peak - peak)
+            const float pk = order_value(peak_key[hl]);
+            const float w = exp_poly(pk - pk);
+            float tot = 0.0f;
+            tot = tot + w * total;
+            const float inverse = 1.0f / tot;
+            o0 = (0.0f + w * o0) * inverse;
+            o1 = (0.0f + w * o1) * inverse;
+            o2 = (0.0f + w * o2) * inverse;
+            o3 = (0.0f + w * o3) * inverse;
+            *reinterpret_cast<float4*>(p.out + ((size_t)row * p.heads + h) * 64 + 4 * vqd) =
+                make_float4(o0, o1, o2, o3);
+        } else {
+            *reinterpret_cast<float4*>(p.partials + (pbase + h) * 64 + 4 * vqd) = make_float4(o0, o1, o2, o3);
+            if (vqd == 0) {
+                p.peaks[pbase + h] = order_value(peak_key[hl]);
+                p.sums[pbase + h] = total;
+            }
         }
+        vout[0] = o0;
+        vout[1] = o1;
+        vout[2] = o2;
+        vout[3] = o3;
     }
-
+    if (needed == 1 && p.q_out) {
+        __shared__ float qred[kThreads / 64];
+        float m = vthread ? fmaxf(fmaxf(fabsf(vout[0]), fabsf(vout[1])), fmaxf(fabsf(vout[2]), fabsf(vout[3]))) : 0.0f;
+        for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
+        if ((tid & 63) == 0) qred[tid >> 6] = m;
+        __syncthreads();
+        const float peak = fmaxf(fmaxf(qred[0], qred[1]), fmaxf(qred[2], qred[3]));
+        const float scale = peak > 0.0f ? peak / 127.0f : 1.0f;
+        const float inverse = 1.0f / scale;
+        if (vthread) {
+            const uint32_t b0 = (uint32_t)(uint8_t)ref_quantize_one(vout[0], inverse);
+            const uint32_t b1 = (uint32_t)(uint8_t)ref_quantize_one(vout[1], inverse);
+            const uint32_t b2 = (uint32_t)(uint8_t)ref_quantize_one(vout[2], inverse);
+            const uint32_t b3 = (uint32_t)(uint8_t)ref_quantize_one(vout[3], inverse);
+            *reinterpret_cast<uint32_t*>(p.q_out + (size_t)row * p.heads * 64 + (h0 + vhl) * 64 + 4 * vqd) =
+                b0 | (b1 << 8) | (b2 << 16) | (b3 << 24);
+        }
+        if (tid == 0) p.qs_out[row] = scale;
+    }
 }
 
 // Merge of a (row, head)'s chunk partials, one workgroup of 64 threads
@@ -277,12 +326,10 @@ __global__ __launch_bounds__(64) void decode_merge_kernel(DecodeAttnParams p)
     const int count = p.row_count[row];
     const bool valid = slot >= 0 && slot < p.slots && first >= 0 && count >= 1 && count <= p.capacity - first;
     float* dst = p.out + ((size_t)row * p.heads + h) * 64 + d;
-    if (!valid) {  // uniform over the block
-        *dst = 0.0f;
-        return;
-    }
+    if (!valid) return;  // uniform over the block; the chunk kernel wrote zeros
     int length;
     const int needed = plan(count, p.max_chunks, &length);
+    if (needed == 1) return;  // the chunk kernel finished the row
     const size_t rbase = (size_t)row * p.max_chunks * p.heads + h;  // + c * heads
     const float* part = p.partials + rbase * 64 + d;
     const size_t cstride = (size_t)p.heads * 64;
@@ -371,34 +418,15 @@ WorkspaceLayout layout(int rows, int heads, int max_chunks)
 
 using namespace nhip;
 
-extern "C" {
+namespace nhip {
 
-size_t nhip_attention_decode_workspace(int32_t rows, int32_t heads, int32_t max_chunks)
-{
-    if (rows <= 0 || heads <= 0 || max_chunks <= 0) return 0;
-    return layout(rows, heads, max_chunks).total;
-}
-
-int32_t nhip_attention_decode_workspace_init(void* d_workspace, size_t bytes, void* stream)
-{
-    NHIP_REQUIRE(d_workspace && bytes % 4 == 0, "attention workspace: null or size not a multiple of 4");
-    int32_t rc = ensure_device();
-    if (rc) return rc;
-    const size_t n = bytes / 4;
-    const int grid = (int)std::min<size_t>((n + 255) / 256, 1024);
-    hipLaunchKernelGGL(zero_kernel, dim3(std::max(grid, 1)), dim3(256), 0, as_stream(stream),
-                       static_cast<uint32_t*>(d_workspace), n);
-    NHIP_CHECK_HIP(hipGetLastError());
-    return NHIP_OK;
-}
-
-int32_t nhip_attention_decode_dev(const int8_t* d_q, const float* d_qscale, int32_t rows, int32_t heads,
-                                  int32_t kv_heads, int32_t qk_dim, const int8_t* d_keys,
-                                  const float* d_key_scales, const int8_t* d_values,
-                                  const float* d_value_scales, int32_t slots, int32_t capacity,
-                                  const int32_t* d_row_slot, const int32_t* d_row_first,
-                                  const int32_t* d_row_count, int32_t max_chunks, void* d_workspace,
-                                  size_t workspace_bytes, float* d_out, void* stream)
+int32_t attention_decode_impl(const int8_t* d_q, const float* d_qscale, int32_t rows, int32_t heads,
+                              int32_t kv_heads, int32_t qk_dim, const int8_t* d_keys, const float* d_key_scales,
+                              const int8_t* d_values, const float* d_value_scales, int32_t slots,
+                              int32_t capacity, const int32_t* d_row_slot, const int32_t* d_row_first,
+                              const int32_t* d_row_count, int32_t max_chunks, void* d_workspace,
+                              size_t workspace_bytes, float* d_out, int8_t* d_q_out, float* d_qs_out,
+                              hipStream_t stream)
 {
     clear_error();
     if (rows == 0) return NHIP_OK;
@@ -442,6 +470,8 @@ int32_t nhip_attention_decode_dev(const int8_t* d_q, const float* d_qscale, int3
     p.sums = reinterpret_cast<float*>(ws + wl.sums);
     p.partials = reinterpret_cast<float*>(ws + wl.partials);
     p.out = d_out;
+    p.q_out = d_q_out;
+    p.qs_out = d_qs_out;
     p.rows = rows;
     p.heads = heads;
     p.kv_heads = kv_heads;
@@ -453,12 +483,51 @@ int32_t nhip_attention_decode_dev(const int8_t* d_q, const float* d_qscale, int3
     p.kv_per_block = std::max(1, kMaxHeadsPerBlock / group);
     p.inv_sqrt = static_cast<float>(1.0 / std::sqrt(static_cast<double>(qk_dim)));
     const int head_blocks = (kv_heads + p.kv_per_block - 1) / p.kv_per_block;
-    hipLaunchKernelGGL(decode_attention_kernel, dim3(max_chunks, rows, head_blocks), dim3(kThreads), lds,
-                       as_stream(stream), p);
+    NHIP_REQUIRE(!d_q_out || (d_qs_out && max_chunks == 1 && head_blocks == 1),
+                 "attention: a quantized output needs max_chunks 1 and all heads in one block");
+    hipLaunchKernelGGL(decode_attention_kernel, dim3(max_chunks, rows, head_blocks), dim3(kThreads), lds, stream, p);
     NHIP_CHECK_HIP(hipGetLastError());
-    hipLaunchKernelGGL(decode_merge_kernel, dim3(rows, heads), dim3(64), 0, as_stream(stream), p);
+    if (max_chunks > 1) {  // single-chunk plans are finished by the chunk kernel
+        hipLaunchKernelGGL(decode_merge_kernel, dim3(rows, heads), dim3(64), 0, stream, p);
+        NHIP_CHECK_HIP(hipGetLastError());
+    }
+    return NHIP_OK;
+}
+
+}  // namespace nhip
+
+extern "C" {
+
+size_t nhip_attention_decode_workspace(int32_t rows, int32_t heads, int32_t max_chunks)
+{
+    if (rows <= 0 || heads <= 0 || max_chunks <= 0) return 0;
+    return layout(rows, heads, max_chunks).total;
+}
+
+int32_t nhip_attention_decode_workspace_init(void* d_workspace, size_t bytes, void* stream)
+{
+    NHIP_REQUIRE(d_workspace && bytes % 4 == 0, "attention workspace: null or size not a multiple of 4");
+    int32_t rc = ensure_device();
+    if (rc) return rc;
+    const size_t n = bytes / 4;
+    const int grid = (int)std::min<size_t>((n + 255) / 256, 1024);
+    hipLaunchKernelGGL(zero_kernel, dim3(std::max(grid, 1)), dim3(256), 0, as_stream(stream),
+                       static_cast<uint32_t*>(d_workspace), n);
     NHIP_CHECK_HIP(hipGetLastError());
     return NHIP_OK;
+}
+
+int32_t nhip_attention_decode_dev(const int8_t* d_q, const float* d_qscale, int32_t rows, int32_t heads,
+                                  int32_t kv_heads, int32_t qk_dim, const int8_t* d_keys,
+                                  const float* d_key_scales, const int8_t* d_values,
+                                  const float* d_value_scales, int32_t slots, int32_t capacity,
+                                  const int32_t* d_row_slot, const int32_t* d_row_first,
+                                  const int32_t* d_row_count, int32_t max_chunks, void* d_workspace,
+                                  size_t workspace_bytes, float* d_out, void* stream)
+{
+    return attention_decode_impl(d_q, d_qscale, rows, heads, kv_heads, qk_dim, d_keys, d_key_scales, d_values,
+                                 d_value_scales, slots, capacity, d_row_slot, d_row_first, d_row_count, max_chunks,
+                                 d_workspace, workspace_bytes, d_out, nullptr, nullptr, as_stream(stream));
 }
 
 }  // extern "C"

@@ -71,6 +71,16 @@ namespace nhip {
 // order (bit-identical with the decode kernels), else the fused epilogue.
 int32_t launch_gemm_i8(const DeviceWeights* w, const int8_t* q, const float* qscale, int32_t tokens, float* y,
                        int32_t ldy, int32_t row_start, int32_t row_end, bool exact, hipStream_t stream);
+// Ragged decode attention (attention_decode.hip); with d_q_out the output
+// rows are also quantized (QuantizeInt8 per row), which needs max_chunks 1
+// and every head in one block.
+int32_t attention_decode_impl(const int8_t* d_q, const float* d_qscale, int32_t rows, int32_t heads,
+                              int32_t kv_heads, int32_t qk_dim, const int8_t* d_keys, const float* d_key_scales,
+                              const int8_t* d_values, const float* d_value_scales, int32_t slots,
+                              int32_t capacity, const int32_t* d_row_slot, const int32_t* d_row_first,
+                              const int32_t* d_row_count, int32_t max_chunks, void* d_workspace,
+                              size_t workspace_bytes, float* d_out, int8_t* d_q_out, float* d_qs_out,
+                              hipStream_t stream);
 // Token count from which literal int8 matmuls use the prefill kernel.
 constexpr int32_t kGemmMinTokens = 32;
 }  // namespace nhip

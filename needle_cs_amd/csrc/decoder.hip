@@ -22,6 +22,7 @@
 #include <algorithm>
 #include <chrono>
 #include <cmath>
+#include <cstdlib>
 #include <cstring>
 #include <vector>
 
@@ -227,60 +228,77 @@ __device__ __forceinline__ bool before(float va, int ia, float vb, int ib)
 __device__ __forceinline__ bool masked(int i) { return i == 0 || i == 2 || i == 3; }
 
 // TopKLogSoftmax (src/Needle/Ops.cs:1092-1221) in the canonical float form:
-// top k of the ids except 0, 2, 3 (the set is unique under the order above,
+// top K of the ids except 0, 2, 3 (the set is unique under the order above,
 // so the tree merge equals the reference's sequential insertion);
 // log_shift = peak + log(sum_i Exp(v_i - peak)), masked v_i = -1e30, the sum
-// by the canonical 256-lane reduction; lp = v - log_shift.
-__global__ __launch_bounds__(kThreads) void topk_lse_kernel(const float* logits, int n, int k, int32_t* idx, float* lp)
+// by the canonical 256-lane reduction; lp = v - log_shift.  K is a template
+// parameter so that the per-thread lists stay in registers.
+template <int K>
+__global__ __launch_bounds__(kThreads) void topk_lse_kernel(const float* logits, int n, int32_t* idx, float* lp)
 {
-    __shared__ float tv[kThreads][kMaxTopK];
-    __shared__ int ti[kThreads][kMaxTopK];
+    __shared__ float tv[K][kThreads];
+    __shared__ int ti[K][kThreads];
     __shared__ float red[kThreads];
     const int t = threadIdx.x;
     const float* x = logits + (size_t)blockIdx.x * n;
-    float bv[kMaxTopK];
-    int bi[kMaxTopK];
-    for (int m = 0; m < k; m++) {
+    float bv[K];
+    int bi[K];
+#pragma unroll
+    for (int m = 0; m < K; m++) {
         bv[m] = -INFINITY;
         bi[m] = 0x7FFFFFFF;
     }
     for (int i = t; i < n; i += kThreads) {
-        if (masked(i)) continue;
         const float v = x[i];
-        if (!before(v, i, bv[k - 1], bi[k - 1])) continue;
-        int pos = k - 1;
-        while (pos > 0 && before(v, i, bv[pos - 1], bi[pos - 1])) {
-            bv[pos] = bv[pos - 1];
-            bi[pos] = bi[pos - 1];
-            pos--;
+        if (masked(i) || !before(v, i, bv[K - 1], bi[K - 1])) continue;
+        bv[K - 1] = v;
+        bi[K - 1] = i;
+#pragma unroll
+        for (int m = K - 1; m > 0; m--) {
+            if (before(bv[m], bi[m], bv[m - 1], bi[m - 1])) {
+                const float fv = bv[m];
+                const int fi = bi[m];
+                bv[m] = bv[m - 1];
+                bi[m] = bi[m - 1];
+                bv[m - 1] = fv;
+                bi[m - 1] = fi;
+            }
         }
-        bv[pos] = v;
-        bi[pos] = i;
     }
-    for (int m = 0; m < k; m++) {
-        tv[t][m] = bv[m];
-        ti[t][m] = bi[m];
+#pragma unroll
+    for (int m = 0; m < K; m++) {
+        tv[m][t] = bv[m];
+        ti[m][t] = bi[m];
     }
     __syncthreads();
     for (int stride = 128; stride > 0; stride >>= 1) {
         if (t < stride) {
-            float mv[kMaxTopK];
-            int mi[kMaxTopK];
-            int a = 0, b = 0;
-            for (int m = 0; m < k; m++) {
-                if (before(tv[t][a], ti[t][a], tv[t + stride][b], ti[t + stride][b])) {
-                    mv[m] = tv[t][a];
-                    mi[m] = ti[t][a];
-                    a++;
-                } else {
-                    mv[m] = tv[t + stride][b];
-                    mi[m] = ti[t + stride][b];
-                    b++;
-                }
+            float av[K], cv[K];
+            int ai[K], ci[K];
+#pragma unroll
+            for (int m = 0; m < K; m++) {
+                av[m] = tv[m][t];
+                ai[m] = ti[m][t];
+                cv[m] = tv[m][t + stride];
+                ci[m] = ti[m][t + stride];
             }
-            for (int m = 0; m < k; m++) {
-                tv[t][m] = mv[m];
-                ti[t][m] = mi[m];
+            // merge two sorted lists, keeping the first K (compile-time indices)
+#pragma unroll
+            for (int m = 0; m < K; m++) {
+                const bool take_a = before(av[0], ai[0], cv[0], ci[0]);
+                tv[m][t] = take_a ? av[0] : cv[0];
+                ti[m][t] = take_a ? ai[0] : ci[0];
+#pragma unroll
+                for (int q = 0; q < K - 1; q++) {
+                    av[q] = take_a ? av[q + 1] : av[q];
+                    ai[q] = take_a ? ai[q + 1] : ai[q];
+                    cv[q] = take_a ? cv[q] : cv[q + 1];
+                    ci[q] = take_a ? ci[q] : ci[q + 1];
+                }
+                av[K - 1] = take_a ? -INFINITY : av[K - 1];
+                ai[K - 1] = take_a ? 0x7FFFFFFF : ai[K - 1];
+                cv[K - 1] = take_a ? cv[K - 1] : -INFINITY;
+                ci[K - 1] = take_a ? ci[K - 1] : 0x7FFFFFFF;
             }
         }
         __syncthreads();
@@ -290,10 +308,34 @@ __global__ __launch_bounds__(kThreads) void topk_lse_kernel(const float* logits,
     for (int i = t; i < n; i += kThreads) s = s + exp_poly((masked(i) ? -1e30f : x[i]) - peak);
     const float total = block_fold(s, red);
     const float log_shift = peak + log_poly(total);
-    if (t < k) {
-        idx[(size_t)blockIdx.x * k + t] = ti[0][t];
-        lp[(size_t)blockIdx.x * k + t] = tv[0][t] - log_shift;
+    if (t < K) {
+        idx[(size_t)blockIdx.x * K + t] = ti[t][0];
+        lp[(size_t)blockIdx.x * K + t] = tv[t][0] - log_shift;
     }
+}
+
+int32_t launch_topk(const float* logits, int rows, int n, int k, int32_t* idx, float* lp, hipStream_t s)
+{
+    switch (k) {
+#define NHIP_TOPK_CASE(K)                                                                                  \
+    case K:                                                                                                \
+        hipLaunchKernelGGL(topk_lse_kernel<K>, dim3(rows), dim3(kThreads), 0, s, logits, n, idx, lp);      \
+        break;
+        NHIP_TOPK_CASE(1)
+        NHIP_TOPK_CASE(2)
+        NHIP_TOPK_CASE(3)
+        NHIP_TOPK_CASE(4)
+        NHIP_TOPK_CASE(5)
+        NHIP_TOPK_CASE(6)
+        NHIP_TOPK_CASE(7)
+        NHIP_TOPK_CASE(8)
+#undef NHIP_TOPK_CASE
+        default:
+            set_error("top-k %d outside [1, 8]", k);
+            return NHIP_ERR_ARG;
+    }
+    NHIP_CHECK_HIP(hipGetLastError());
+    return NHIP_OK;
 }
 
 // Copies positions [0, length) of slot src to slot dst in every layer's
@@ -418,13 +460,17 @@ int32_t enqueue_forward(nhip_decoder* m, int rows, int k)
         pp.capacity = D.capacity;
         hipLaunchKernelGGL(qkv_post_kernel, dim3(rows, H + 2 * KV), dim3(64), 0, s, pp);
         NHIP_CHECK_HIP(hipGetLastError());
-        rc = nhip_attention_decode_dev(m->qh, m->qhs, rows, H, KV, 64, pp.keys, pp.key_scales, pp.values,
-                                       pp.value_scales, D.slots, D.capacity, in_slots(m, m->d_in),
-                                       in_first(m, m->d_in), in_count(m, m->d_in), D.max_chunks, m->attn_ws,
-                                       m->attn_ws_bytes, m->att, s);
+        // single-chunk attention over all heads also quantizes its output rows
+        const bool fused_quant = D.max_chunks == 1 && H <= 16;
+        rc = attention_decode_impl(m->qh, m->qhs, rows, H, KV, 64, pp.keys, pp.key_scales, pp.values,
+                                   pp.value_scales, D.slots, D.capacity, in_slots(m, m->d_in), in_first(m, m->d_in),
+                                   in_count(m, m->d_in), D.max_chunks, m->attn_ws, m->attn_ws_bytes, m->att,
+                                   fused_quant ? m->q8 : nullptr, fused_quant ? m->qs : nullptr, s);
         if (rc) return rc;
-        rc = nhip_quantize_rows_dev(m->att, rows, H * 64, m->q8, m->qs, s);
-        if (rc) return rc;
+        if (!fused_quant) {
+            rc = nhip_quantize_rows_dev(m->att, rows, H * 64, m->q8, m->qs, s);
+            if (rc) return rc;
+        }
         rc = nhip_matmul_i8_dev(m->wo[l], m->q8, m->qs, rows, m->delta, d, 0, d, s);
         if (rc) return rc;
         hipLaunchKernelGGL(add_rmsnorm_quant_kernel, dim3(rows), dim3(kThreads), 0, s, m->x, m->delta,
@@ -443,9 +489,8 @@ int32_t enqueue_forward(nhip_decoder* m, int rows, int k)
     rc = nhip_matmul_i8_dev(m->wlm, m->q8, m->qs, rows, m->logits, D.vocab, 0, D.vocab, s);
     if (rc) return rc;
     if (k > 0) {
-        hipLaunchKernelGGL(topk_lse_kernel, dim3(rows), dim3(kThreads), 0, s, m->logits, D.vocab, k, m->d_topk_idx,
-                           m->d_topk_lp);
-        NHIP_CHECK_HIP(hipGetLastError());
+        rc = launch_topk(m->logits, rows, D.vocab, k, m->d_topk_idx, m->d_topk_lp, s);
+        if (rc) return rc;
     }
     return NHIP_OK;
 }
@@ -475,6 +520,12 @@ int32_t stage_inputs(nhip_decoder* m, const int32_t* tokens, const int32_t* slot
 int32_t forward_step(nhip_decoder* m, const int32_t* tokens, const int32_t* slots, const int32_t* positions,
                      int rows, int k, bool use_graph)
 {
+    // NHIP_DECODER_GRAPHS=0 launches decode steps eagerly (for kernel tracers)
+    static const bool graphs_enabled = [] {
+        const char* e = getenv("NHIP_DECODER_GRAPHS");
+        return !(e && e[0] == '0');
+    }();
+    use_graph = use_graph && graphs_enabled;
     int32_t rc = stage_inputs(m, tokens, slots, positions, rows);
     if (rc) return rc;
     if (use_graph && rows <= kMaxTopK) {

@@ -66,6 +66,17 @@ def test_decode_attention_bit_exact(hip, orc, heads, kv_heads, qk, max_chunks):
     assert bit_equal(got, want)
 
 
+@pytest.mark.parametrize("heads,kv_heads,qk", [(16, 16, 64), (6, 2, 48)])
+def test_decode_attention_single_chunk_plan(hip, orc, heads, kv_heads, qk):
+    """max_chunks 1: every row is one chunk finished by the chunk kernel (the
+    merge of one partial), no merge launch."""
+    cache = Cache(orc, hip, 31 + heads, 3, 256, kv_heads, qk)
+    spec = [(0, 0, 1), (1, 3, 17), (2, 0, 256), (0, 100, 99), (1, 0, 192)]
+    q, qs = queries(orc, cache.st, len(spec), heads, qk)
+    got, _ = run_decode(hip, cache, q, qs, heads, spec, 1)
+    assert bit_equal(got, oracle_decode(orc, cache, q, qs, heads, spec, 1))
+
+
 def test_decode_attention_invalid_rows_are_zero(hip, orc):
     cache = Cache(orc, hip, 42, 2, 256, 2, 64)
     heads = 4

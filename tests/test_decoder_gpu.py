@@ -17,11 +17,12 @@ def bits(a):
     return np.ascontiguousarray(a).view(np.uint32)
 
 
+@pytest.mark.parametrize("max_chunks", [1, 64])
 @pytest.mark.parametrize("dims", [TINY, GQA], ids=["tiny", "gqa"])
-def test_forward_bit_identical(hip, orc, dims):
+def test_forward_bit_identical(hip, orc, dims, max_chunks):
     model = synthetic_model(dims, 7001)
-    gpu = GpuDecoder(model, slots=4, capacity=64, max_rows=40)
-    cpu = orc.CpuDecoder(model, slots=4, capacity=64)
+    gpu = GpuDecoder(model, slots=4, capacity=64, max_rows=40, max_chunks=max_chunks)
+    cpu = orc.CpuDecoder(model, slots=4, capacity=64, max_chunks=max_chunks)
     prompts = [random_prompt(10 + s, n, dims["vocab"]) for s, n in zip(range(3), (33, 5, 12))]
     for slot, pr in enumerate(prompts):  # prefill (32+ rows use the prefill matmul)
         pos = np.arange(len(pr))
@@ -45,12 +46,13 @@ def test_forward_bit_identical(hip, orc, dims):
     cpu.close()
 
 
+@pytest.mark.parametrize("max_chunks", [1, 64])
 @pytest.mark.parametrize("eos", [1, 7])
-def test_beam_search_identical_tokens(hip, orc, eos):
+def test_beam_search_identical_tokens(hip, orc, eos, max_chunks):
     model = synthetic_model(TINY, 7002)
     prompt = random_prompt(5, 20, TINY["vocab"])
-    gpu = GpuDecoder(model, slots=3, capacity=64, max_rows=20)
-    cpu = orc.CpuDecoder(model, slots=3, capacity=64)
+    gpu = GpuDecoder(model, slots=3, capacity=64, max_rows=20, max_chunks=max_chunks)
+    cpu = orc.CpuDecoder(model, slots=3, capacity=64, max_chunks=max_chunks)
     tg, sg, stats = gpu.beam_search(prompt, 3, 24, eos)
     tc, sc, fed = cpu.beam_search(prompt, 3, 24, eos)
     assert np.array_equal(tg, tc)
