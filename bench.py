@@ -306,6 +306,8 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-secondary", action="store_true")
     ap.add_argument("--no-decode-loop", action="store_true")
+    ap.add_argument("--only", choices=["prefill", "attention", "decode_loop"],
+                    help="run one secondary workload alone (for kernel tracing); prints no JSON line")
     ap.add_argument("--decode-chunks", type=int, default=64,
                     help="attention position-split cap of the decode loop (1: one chunk per row with the output quantize fused)")
     ap.add_argument("--pmc-run", type=int, default=0, metavar="LAUNCHES",
@@ -319,6 +321,22 @@ def main() -> int:
     N.check(N.lib().nhip_init(0))
     print(f"# {N.lib().nhip_describe().decode()}", file=sys.stderr, flush=True)
 
+    if args.only:
+        threads = int(os.environ.get("NEEDLE_THREADS", "0")) or min(physical_cores(), 16)
+        if args.only == "decode_loop":
+            print(json.dumps(decode_loop(args, threads)), file=sys.stderr)
+        elif args.only == "prefill":
+            for fused in (True, False):
+                case = GemmCase(512, 2048, 8192, seed=0x4004, fused=fused)
+                t = case.time(max(50, args.steps // 20), max(5, args.warmup // 10))
+                print(f"# prefill GEMM ({'fused' if fused else 'exact'}): {t * 1e3:.1f} us", file=sys.stderr)
+                case.close()
+        else:
+            case = AttnCase(seed=0x3003)
+            t = case.time(max(200, args.steps // 4), args.warmup)
+            print(f"# attention: {t * 1e3:.2f} us/launch", file=sys.stderr)
+            case.close()
+        return 0
     main_case = GemvCase(3, 2048, 8192, seed=0x1001)
     if args.pmc_run:
         return pmc_run(main_case, args.pmc_run)

@@ -92,26 +92,29 @@ __global__ __launch_bounds__(kThreads) void embed_kernel(const int32_t* tokens, 
 
 // x += delta (when given); ss = sum x^2 (canonical sum); inv = 1 / sqrt(ss /
 // d + eps); h = (x * inv) * gain; QuantizeInt8(h) -> q, scale.
+template <bool DELTA>
 __global__ __launch_bounds__(kThreads) void add_rmsnorm_quant_kernel(float* x, const float* delta, const float* gain,
                                                                      int d, float eps, int8_t* q, float* qscale)
 {
     __shared__ float red[kThreads];
     const int t = threadIdx.x;
     float* xr = x + (size_t)blockIdx.x * d;
-    const float* dr = delta ? delta + (size_t)blockIdx.x * d : nullptr;
-    float v[kMaxPerThread];
+    const float* dr = DELTA ? delta + (size_t)blockIdx.x * d : nullptr;
+    float v[kMaxPerThread], gv[kMaxPerThread];
+#pragma unroll
+    for (int j = 0; j < kMaxPerThread; j++) {  // every load first
+        const int i = min(t + j * kThreads, d - 1);
+        v[j] = xr[i];
+        gv[j] = gain[i];
+        if constexpr (DELTA) v[j] = v[j] + dr[i];
+    }
     float s = 0.0f;
 #pragma unroll
     for (int j = 0; j < kMaxPerThread; j++) {
         const int i = t + j * kThreads;
         if (i < d) {
-            float a = xr[i];
-            if (dr) {
-                a = a + dr[i];
-                xr[i] = a;
-            }
-            v[j] = a;
-            s = s + a * a;
+            if constexpr (DELTA) xr[i] = v[j];
+            s = s + v[j] * v[j];
         }
     }
     const float ss = block_fold(s, red);
@@ -121,7 +124,7 @@ __global__ __launch_bounds__(kThreads) void add_rmsnorm_quant_kernel(float* x, c
     for (int j = 0; j < kMaxPerThread; j++) {
         const int i = t + j * kThreads;
         if (i < d) {
-            v[j] = (v[j] * inv) * gain[i];
+            v[j] = (v[j] * inv) * gv[j];
             peak = fmaxf(peak, fabsf(v[j]));
         }
     }
@@ -195,14 +198,20 @@ __global__ __launch_bounds__(kThreads) void swiglu_quant_kernel(const float* gu,
     const int t = threadIdx.x;
     const float* g = gu + (size_t)blockIdx.x * 2 * ffn;
     const float* up = g + ffn;
-    float v[kMaxPerThread];
+    float v[kMaxPerThread], uv[kMaxPerThread];
+#pragma unroll
+    for (int j = 0; j < kMaxPerThread; j++) {  // every load first
+        const int i = min(t + j * kThreads, ffn - 1);
+        v[j] = g[i];
+        uv[j] = up[i];
+    }
     float peak = 0.0f;
 #pragma unroll
     for (int j = 0; j < kMaxPerThread; j++) {
         const int i = t + j * kThreads;
         if (i < ffn) {
-            const float gi = g[i];
-            v[j] = (gi / (1.0f + exp_poly(-gi))) * up[i];
+            const float gi = v[j];
+            v[j] = (gi / (1.0f + exp_poly(-gi))) * uv[j];
             peak = fmaxf(peak, fabsf(v[j]));
         }
     }
@@ -248,20 +257,29 @@ __global__ __launch_bounds__(kThreads) void topk_lse_kernel(const float* logits,
         bv[m] = -INFINITY;
         bi[m] = 0x7FFFFFFF;
     }
-    for (int i = t; i < n; i += kThreads) {
-        const float v = x[i];
-        if (masked(i) || !before(v, i, bv[K - 1], bi[K - 1])) continue;
-        bv[K - 1] = v;
-        bi[K - 1] = i;
+    // ids i = t + 256 j in ascending j, loaded eight at a time
+    constexpr int kBatch = 8;
+    for (int i0 = t; i0 < n; i0 += kBatch * kThreads) {
+        float xv[kBatch];
 #pragma unroll
-        for (int m = K - 1; m > 0; m--) {
-            if (before(bv[m], bi[m], bv[m - 1], bi[m - 1])) {
-                const float fv = bv[m];
-                const int fi = bi[m];
-                bv[m] = bv[m - 1];
-                bi[m] = bi[m - 1];
-                bv[m - 1] = fv;
-                bi[m - 1] = fi;
+        for (int j = 0; j < kBatch; j++) xv[j] = x[min(i0 + j * kThreads, n - 1)];
+#pragma unroll
+        for (int j = 0; j < kBatch; j++) {
+            const int i = i0 + j * kThreads;
+            const float v = xv[j];
+            if (i >= n || masked(i) || !before(v, i, bv[K - 1], bi[K - 1])) continue;
+            bv[K - 1] = v;
+            bi[K - 1] = i;
+#pragma unroll
+            for (int m = K - 1; m > 0; m--) {
+                if (before(bv[m], bi[m], bv[m - 1], bi[m - 1])) {
+                    const float fv = bv[m];
+                    const int fi = bi[m];
+                    bv[m] = bv[m - 1];
+                    bi[m] = bi[m - 1];
+                    bv[m - 1] = fv;
+                    bi[m - 1] = fi;
+                }
             }
         }
     }
@@ -305,7 +323,16 @@ __global__ __launch_bounds__(kThreads) void topk_lse_kernel(const float* logits,
     }
     const float peak = tv[0][0];
     float s = 0.0f;
-    for (int i = t; i < n; i += kThreads) s = s + exp_poly((masked(i) ? -1e30f : x[i]) - peak);
+    for (int i0 = t; i0 < n; i0 += kBatch * kThreads) {
+        float xv[kBatch];
+#pragma unroll
+        for (int j = 0; j < kBatch; j++) xv[j] = x[min(i0 + j * kThreads, n - 1)];
+#pragma unroll
+        for (int j = 0; j < kBatch; j++) {
+            const int i = i0 + j * kThreads;
+            if (i < n) s = s + exp_poly((masked(i) ? -1e30f : xv[j]) - peak);
+        }
+    }
     const float total = block_fold(s, red);
     const float log_shift = peak + log_poly(total);
     if (t < K) {
@@ -438,8 +465,12 @@ int32_t enqueue_forward(nhip_decoder* m, int rows, int k)
     NHIP_CHECK_HIP(hipGetLastError());
     const size_t layer_cells = (size_t)D.slots * D.capacity * KV;
     for (int l = 0; l < D.layers; l++) {
-        hipLaunchKernelGGL(add_rmsnorm_quant_kernel, dim3(rows), dim3(kThreads), 0, s, m->x,
-                           l == 0 ? nullptr : m->delta, m->attn_norm[l], d, D.eps, m->q8, m->qs);
+        if (l == 0)
+            hipLaunchKernelGGL(add_rmsnorm_quant_kernel<false>, dim3(rows), dim3(kThreads), 0, s, m->x, nullptr,
+                               m->attn_norm[l], d, D.eps, m->q8, m->qs);
+        else
+            hipLaunchKernelGGL(add_rmsnorm_quant_kernel<true>, dim3(rows), dim3(kThreads), 0, s, m->x, m->delta,
+                               m->attn_norm[l], d, D.eps, m->q8, m->qs);
         NHIP_CHECK_HIP(hipGetLastError());
         rc = nhip_matmul_i8_dev(m->wqkv[l], m->q8, m->qs, rows, m->qkv, m->qkv_n, 0, m->qkv_n, s);
         if (rc) return rc;
@@ -473,7 +504,7 @@ int32_t enqueue_forward(nhip_decoder* m, int rows, int k)
         }
         rc = nhip_matmul_i8_dev(m->wo[l], m->q8, m->qs, rows, m->delta, d, 0, d, s);
         if (rc) return rc;
-        hipLaunchKernelGGL(add_rmsnorm_quant_kernel, dim3(rows), dim3(kThreads), 0, s, m->x, m->delta,
+        hipLaunchKernelGGL(add_rmsnorm_quant_kernel<true>, dim3(rows), dim3(kThreads), 0, s, m->x, m->delta,
                            m->ffn_norm[l], d, D.eps, m->q8, m->qs);
         NHIP_CHECK_HIP(hipGetLastError());
         rc = nhip_matmul_i8_dev(m->wgu[l], m->q8, m->qs, rows, m->gu, 2 * F, 0, 2 * F, s);
@@ -483,8 +514,8 @@ int32_t enqueue_forward(nhip_decoder* m, int rows, int k)
         rc = nhip_matmul_i8_dev(m->wd[l], m->q8, m->qs, rows, m->delta, d, 0, d, s);
         if (rc) return rc;
     }
-    hipLaunchKernelGGL(add_rmsnorm_quant_kernel, dim3(rows), dim3(kThreads), 0, s, m->x, m->delta, m->final_norm, d,
-                       D.eps, m->q8, m->qs);
+    hipLaunchKernelGGL(add_rmsnorm_quant_kernel<true>, dim3(rows), dim3(kThreads), 0, s, m->x, m->delta,
+                       m->final_norm, d, D.eps, m->q8, m->qs);
     NHIP_CHECK_HIP(hipGetLastError());
     rc = nhip_matmul_i8_dev(m->wlm, m->q8, m->qs, rows, m->logits, D.vocab, 0, D.vocab, s);
     if (rc) return rc;
