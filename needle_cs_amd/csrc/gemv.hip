@@ -93,6 +93,7 @@ struct MatmulParams {
     int32_t d_bytes;          // LDS bytes of the D buffer of one phase
     int32_t ldd;              // LDS row stride (int32) of D and scales: roundup4(gph) + 4
     int32_t st_bytes;         // int8 path: LDS bytes of the staged activation operands
+    int32_t swz;              // decode path, 5..16 tokens: float4-column swizzle mask of the products
     uint32_t t0, t1, t2, t3;  // codebook bytes 0..15
     float byte_scale;
 };
@@ -532,134 +533,169 @@ __global__ __launch_bounds__(512) void matmul_i8_kernel(MatmulParams p)
     }
 }
 
-// Decode path of the literal int8 format for M <= 4 tokens (beam rows).
-// Each of the S waves of a tile owns `per` weight blocks (2*per groups),
-// computes its products p_g = (hs * scale[t]) * D_g (Scalar.cs:185-186) and
-// leaves them in LDS as [t][r][g]; after one barrier the lanes (t, r) of wave
-// 0 add them in ascending group order, so each y[t][n] is exactly
-// (((0 + p_0) + p_1) + ... + p_{G-1}).  Preconditions (checked on the host):
-// every wave owns per == CB blocks with per % 4 == 0 (its scales are 16-byte
-// aligned in the padded scale rows).
-template <int CB, int TI, int NS, bool EXACT>
+// Decode path of the literal int8 format for M <= 16 tokens (beam rows,
+// packed sequences).  Each of the S waves of a 16-row tile owns CB weight
+// blocks (2*CB groups) and loads its A operands (its K range of the M rows)
+// straight from memory; it computes the products p_g = (hs * scale[t]) * D_g
+// (Scalar.cs:185-186) and leaves them in LDS as [t][r][g]; after one barrier
+// the lanes (t, r) add them in ascending group order, so each y[t][n] is
+// exactly (((0 + p_0) + p_1) + ... + p_{G-1}).
+//   TI <= 4: four groups g..g+3 share one D.  MFMA j of a set holds group
+//            g+j's activations in A rows 4j..4j+3 (zero elsewhere) and
+//            accumulates into the previous result; the row blocks are
+//            disjoint, so D rows 4j+i are exactly D_{g+j} of token i, and
+//            lane (r, kq) ends up holding the M tokens of group g+kq: every
+//            lane's products are useful.  Product rows are padded (stride
+//            GS = roundup4(2*blocks) + 4).
+//   TI == 16: one group per MFMA; lane (r, kq) holds tokens 4kq..4kq+3 of
+//            row r; the products are M*16 rows of GS = roundup4(2*blocks)
+//            floats, the float4 column c of product row x stored at column
+//            c ^ (x & swz), which keeps both the writes and the chain's
+//            reads free of bank conflicts without padding.
+// Preconditions (checked on the host): CB is 4 or 8 and every wave owns CB
+// blocks (its scales are 16-byte aligned in the padded scale rows).
+template <int CB, int TI, bool EXACT>
 __global__ __launch_bounds__(512) void matmul_i8_decode_kernel(MatmulParams p)
 {
+    constexpr bool WIDE = TI > 4;
+    constexpr int TL = WIDE ? 4 : TI;  // tokens per lane
+    constexpr int SETS = 2 * CB / 4;   // TI <= 4: sets of four groups per wave
     extern __shared__ __align__(16) uint8_t lds[];
-    uint2* st = reinterpret_cast<uint2*>(lds);
-    float* pl = reinterpret_cast<float*>(lds + p.st_bytes);  // [t][r][GS]
+    float* pl = reinterpret_cast<float*>(lds);  // products [t][r][GS]
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
     const int tile = p.tile_begin + blockIdx.x;
-    const int M = p.tokens;  // <= 4 == TI
+    const int M = p.tokens;  // <= TI
     const int G = p.groups;
     const int GS = p.ldd;    // product row stride (floats), multiple of 4
     const int r = lane & 15;
     const int kq = lane >> 4;
     const int n = tile * 16 + r;
-    const int ra = min(r, M - 1);
     const int mb0 = wave * CB;
     const int g_first = mb0 * 2;
     const u4* wbase = reinterpret_cast<const u4*>(p.tiles) + (size_t)tile * p.blocks * 64 + lane;
     const uint16_t* nrow = p.norms + (size_t)n * p.groups_pad8 + g_first;
 
-    // 1. activation rows (all K): unit u = (token, 16-byte offset)
-    const int units = M * G * 2;
-    uint4 sv[NS];
+    // 1. activation operands, 2. activation scales, 3. weight scales,
+    // 4. weight blocks -- in this order, all in flight together
+    constexpr int NA = WIDE ? 2 * CB : SETS;
+    long av[NA];
+    float qraw[TL];
+    if constexpr (WIDE) {
+        // 8 bytes (k-slice kq) of token r per group
+        const int8_t* qrow = p.q + (size_t)min(r, M - 1) * p.cols + kq * 8;
 #pragma unroll
-    for (int j = 0; j < NS; j++) {
-        const int u = min((int)threadIdx.x + j * (int)blockDim.x, units - 1);
-        const int t = u / (2 * G);
-        const int o = (u - t * 2 * G) * 16;
-        sv[j] = *reinterpret_cast<const uint4*>(p.q + (size_t)t * p.cols + o);
+        for (int k = 0; k < NA; k++)
+            av[k] = *reinterpret_cast<const long*>(qrow + (size_t)min(g_first + k, G - 1) * 32);
+#pragma unroll
+        for (int i = 0; i < 4; i++) qraw[i] = p.qscale[min(4 * kq + i, M - 1)];
+    } else {
+        // lane (r, kq) feeds A row r of MFMA r/4: token r%4, group
+        // g + r/4, k-slice kq
+        const int8_t* qrow = p.q + (size_t)min(r & 3, M - 1) * p.cols + kq * 8;
+#pragma unroll
+        for (int c = 0; c < NA; c++)
+            av[c] = *reinterpret_cast<const long*>(qrow + (size_t)min(g_first + 4 * c + (r >> 2), G - 1) * 32);
+#pragma unroll
+        for (int i = 0; i < TI; i++) qraw[i] = p.qscale[min(i, M - 1)];
     }
-    // 2. activation scales, 3. this wave's weight scales (8 per 16-byte load),
-    // 4. its weight blocks -- in this order, all in flight together
-    float qraw[TI];
+    constexpr int SJ = WIDE ? CB / 4 : SETS;
+    uint4 sraw[WIDE ? SJ : 1];
+    uint16_t hraw[WIDE ? 1 : SJ];
+    if constexpr (WIDE) {
+        // 8 groups per 16-byte load
 #pragma unroll
-    for (int i = 0; i < TI; i++) qraw[i] = p.qscale[min(i, M - 1)];
-    constexpr int SJ = CB / 4;  // 16-byte scale loads covering 2*CB groups
-    uint4 sraw[SJ];
+        for (int j = 0; j < SJ; j++) sraw[j] = *reinterpret_cast<const uint4*>(nrow + 8 * j);
+    } else {
+        // the scale of this lane's group g + kq in each set
 #pragma unroll
-    for (int j = 0; j < SJ; j++) sraw[j] = *reinterpret_cast<const uint4*>(nrow + 8 * j);
+        for (int c = 0; c < SJ; c++) hraw[c] = nrow[4 * c + kq];
+    }
     u4 w[CB];
 #pragma unroll
     for (int c = 0; c < CB; c++) w[c] = __builtin_nontemporal_load(wbase + (size_t)(mb0 + c) * 64);
     __builtin_amdgcn_sched_barrier(0);
-    // 5. staged operands: bytes o..o+15 of a row are kq = (o%32)/8 and kq+1
-#pragma unroll
-    for (int j = 0; j < NS; j++) {
-        const int u = (int)threadIdx.x + j * (int)blockDim.x;
-        const int uc = min(u, units - 1);
-        const int t = uc / (2 * G);
-        const int o = (uc - t * 2 * G) * 16;
-        const int g = o >> 5;
-        const int k0 = (o & 31) >> 3;
-        if (u < units) {
-            st[(g * 4 + k0) * M + t] = make_uint2(sv[j].x, sv[j].y);
-            st[(g * 4 + k0 + 1) * M + t] = make_uint2(sv[j].z, sv[j].w);
-        }
-    }
-    __syncthreads();
-    long av[2 * CB];
-#pragma unroll
-    for (int k = 0; k < 2 * CB; k++) {
-        const int g = min(g_first + k, G - 1);
-        const long araw = *reinterpret_cast<const long*>(st + (g * 4 + kq) * M + ra);
-        av[k] = r < M ? araw : 0;
-    }
-    float qs[TI];
-#pragma unroll
-    for (int i = 0; i < TI; i++) qs[i] = i < M ? qraw[i] : 0.0f;
-    float pr[2 * CB][TI];
-#pragma unroll
-    for (int k = 0; k < 2 * CB; k++) {
-        const u4& wc = w[k >> 1];
-        const long b = (k & 1) ? (long)(((uint64_t)wc.w << 32) | wc.z) : (long)(((uint64_t)wc.y << 32) | wc.x);
-        const v4i zero = {0, 0, 0, 0};
-        const v4i d = __builtin_amdgcn_mfma_i32_16x16x32_i8(av[k], b, zero, 0, 0, 0);
-        const uint4 s4 = sraw[k >> 3];
-        const int kk = k & 7;
-        const uint32_t word = kk < 4 ? (kk < 2 ? s4.x : s4.y) : (kk < 6 ? s4.z : s4.w);
-        const uint32_t h = (kk & 1) ? (word >> 16) : (word & 0xFFFFu);
-        float hs;
+
+    auto decode_scale = [](uint32_t h) -> float {
         if constexpr (EXACT) {
-            hs = ref_half_to_single(h);
+            return ref_half_to_single(h);
         } else {
             // binary16 -> binary32 is exact; a -0 scale gives a +-0 product,
             // which cannot change an accumulator that starts at +0.
-            hs = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(h)));
+            return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(h)));
         }
+    };
+    const v4i zero = {0, 0, 0, 0};
+    if constexpr (WIDE) {
+        const int tq = 4 * kq;  // first token of this lane's MFMA results
+        float qs[4];
 #pragma unroll
-        for (int i = 0; i < TI; i++) pr[k][i] = (hs * qs[i]) * static_cast<float>(d[i]);
-    }
-    // lanes kq == 0 hold D rows 0..3 (the tokens); groups >= G are never read
-    if (kq == 0) {
+        for (int i = 0; i < 4; i++) qs[i] = tq + i < M ? qraw[i] : 0.0f;
+        float pr[2 * CB][4];
 #pragma unroll
-        for (int i = 0; i < TI; i++) {
-            float4* dst = reinterpret_cast<float4*>(pl + (size_t)(i * 16 + r) * GS + g_first);
+        for (int k = 0; k < 2 * CB; k++) {
+            const u4& wc = w[k >> 1];
+            const long b = (k & 1) ? (long)(((uint64_t)wc.w << 32) | wc.z) : (long)(((uint64_t)wc.y << 32) | wc.x);
+            const long a = r < M ? av[k] : 0;
+            const v4i d = __builtin_amdgcn_mfma_i32_16x16x32_i8(a, b, zero, 0, 0, 0);
+            const uint4 s4 = sraw[k >> 3];
+            const int kk = k & 7;
+            const uint32_t word = kk < 4 ? (kk < 2 ? s4.x : s4.y) : (kk < 6 ? s4.z : s4.w);
+            const float hs = decode_scale((kk & 1) ? (word >> 16) : (word & 0xFFFFu));
 #pragma unroll
-            for (int k4 = 0; k4 < 2 * CB; k4 += 4)
-                dst[k4 >> 2] = make_float4(pr[k4][i], pr[k4 + 1][i], pr[k4 + 2][i], pr[k4 + 3][i]);
+            for (int i = 0; i < 4; i++) pr[k][i] = (hs * qs[i]) * static_cast<float>(d[i]);
+        }
+        // groups >= G are written (inside the row) but never read
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int x = (tq + i) * 16 + r;  // product row
+            if (tq + i < M) {
+                float4* dst = reinterpret_cast<float4*>(pl + (size_t)x * GS);
+#pragma unroll
+                for (int k4 = 0; k4 < 2 * CB; k4 += 4)
+                    dst[((g_first + k4) >> 2) ^ (x & p.swz)] =
+                        make_float4(pr[k4][i], pr[k4 + 1][i], pr[k4 + 2][i], pr[k4 + 3][i]);
+            }
+        }
+    } else {
+        const bool feeds = (r & 3) < M;  // A rows of tokens >= M stay zero
+        float* prow = pl + (size_t)r * GS + g_first + kq;
+#pragma unroll
+        for (int c = 0; c < SETS; c++) {
+            const long a = feeds ? av[c] : 0;
+            v4i d = zero;
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const u4& wc = w[2 * c + (j >> 1)];
+                const long b = (j & 1) ? (long)(((uint64_t)wc.w << 32) | wc.z) : (long)(((uint64_t)wc.y << 32) | wc.x);
+                d = __builtin_amdgcn_mfma_i32_16x16x32_i8((r >> 2) == j ? a : 0, b, d, 0, 0, 0);
+            }
+            const float hs = decode_scale(hraw[c]);
+            // groups >= G are written (inside the row) but never read
+#pragma unroll
+            for (int i = 0; i < TI; i++)
+                if (i < M) prow[(size_t)i * 16 * GS + 4 * c] = (hs * qraw[i]) * static_cast<float>(d[i]);
         }
     }
     __syncthreads();
-    if (threadIdx.x < M * 16) {
-        const int t = threadIdx.x >> 4;
-        const int rr = threadIdx.x & 15;
+    for (int x = threadIdx.x; x < M * 16; x += blockDim.x) {
+        const int t = x >> 4;
+        const int rr = x & 15;
         const int nn = tile * 16 + rr;
-        const float4* row = reinterpret_cast<const float4*>(pl + (size_t)(t * 16 + rr) * GS);
+        const float4* row = reinterpret_cast<const float4*>(pl + (size_t)x * GS);
+        const int sw = WIDE ? (x & p.swz) : 0;
         float acc = 0.0f;
-        int c = 0;
         float4 v[4];
         const int full = G >> 4;  // chunks of 16 groups
         if (full > 0) {
 #pragma unroll
-            for (int j = 0; j < 4; j++) v[j] = row[j];
+            for (int j = 0; j < 4; j++) v[j] = row[j ^ sw];
         }
         for (int ch = 0; ch < full; ch++) {
             float4 nx[4];
             const int nb = min(ch + 1, full - 1) * 4;
 #pragma unroll
-            for (int j = 0; j < 4; j++) nx[j] = row[nb + j];
+            for (int j = 0; j < 4; j++) nx[j] = row[(nb + j) ^ sw];
 #pragma unroll
             for (int j = 0; j < 4; j++) {
                 acc = acc + v[j].x;
@@ -670,38 +706,30 @@ __global__ __launch_bounds__(512) void matmul_i8_decode_kernel(MatmulParams p)
 #pragma unroll
             for (int j = 0; j < 4; j++) v[j] = nx[j];
         }
-        c = full * 16;
         const float* rowf = reinterpret_cast<const float*>(row);
-        for (; c < G; c++) acc = acc + rowf[c];
+        for (int c = full * 16; c < G; c++) acc = acc + rowf[(((c >> 2) ^ sw) << 2) | (c & 3)];
         if (nn >= p.row_start && nn < p.row_end) p.y[(size_t)t * p.ldy + nn] = acc;
     }
 }
 
-template <int CB, int TI, int NS, bool EXACT>
+template <int CB, int TI, bool EXACT>
 int32_t launch_dec_tpl(const MatmulParams& p, int waves, size_t lds, hipStream_t stream)
 {
     const int tiles = p.tile_end - p.tile_begin;
-    hipLaunchKernelGGL((matmul_i8_decode_kernel<CB, TI, NS, EXACT>), dim3(tiles), dim3(64 * waves), lds, stream, p);
+    hipLaunchKernelGGL((matmul_i8_decode_kernel<CB, TI, EXACT>), dim3(tiles), dim3(64 * waves), lds, stream, p);
     NHIP_CHECK_HIP(hipGetLastError());
     return NHIP_OK;
 }
 
-template <int CB, int TI, bool EXACT>
-int32_t launch_dec_ns(const MatmulParams& p, int waves, int ns, size_t lds, hipStream_t s)
-{
-    if (ns <= 1) return launch_dec_tpl<CB, TI, 1, EXACT>(p, waves, lds, s);
-    if (ns <= 2) return launch_dec_tpl<CB, TI, 2, EXACT>(p, waves, lds, s);
-    return launch_dec_tpl<CB, TI, 4, EXACT>(p, waves, lds, s);
-}
-
 template <int CB, bool EXACT>
-int32_t launch_dec_ti(const MatmulParams& p, int waves, int ns, size_t lds, hipStream_t s)
+int32_t launch_dec_ti(const MatmulParams& p, int waves, size_t lds, hipStream_t s)
 {
     switch (p.tokens) {
-        case 1: return launch_dec_ns<CB, 1, EXACT>(p, waves, ns, lds, s);
-        case 2: return launch_dec_ns<CB, 2, EXACT>(p, waves, ns, lds, s);
-        case 3: return launch_dec_ns<CB, 3, EXACT>(p, waves, ns, lds, s);
-        default: return launch_dec_ns<CB, 4, EXACT>(p, waves, ns, lds, s);
+        case 1: return launch_dec_tpl<CB, 1, EXACT>(p, waves, lds, s);
+        case 2: return launch_dec_tpl<CB, 2, EXACT>(p, waves, lds, s);
+        case 3: return launch_dec_tpl<CB, 3, EXACT>(p, waves, lds, s);
+        case 4: return launch_dec_tpl<CB, 4, EXACT>(p, waves, lds, s);
+        default: return launch_dec_tpl<CB, 16, EXACT>(p, waves, lds, s);
     }
 }
 
@@ -709,7 +737,7 @@ int32_t launch_dec_ti(const MatmulParams& p, int waves, int ns, size_t lds, hipS
 // not apply (the caller falls back to the general kernel).
 int32_t try_i8_decode(const DeviceWeights* w, MatmulParams& p, hipStream_t stream)
 {
-    if (p.tokens > 4 || p.dots) return 1;
+    if (p.tokens > 16 || p.dots) return 1;
     static const int waves_override = [] {
         // tuning knob: 2, 4 or 8 waves per tile, or 1 to use the general kernel
         const char* e = getenv("NHIP_DECODE_WAVES");
@@ -718,7 +746,8 @@ int32_t try_i8_decode(const DeviceWeights* w, MatmulParams& p, hipStream_t strea
     }();
     if (waves_override == 1) return 1;
     int waves = 0;
-    const int cands[3] = {4, 8, 2};
+    // 5..16 tokens: more waves split the larger per-tile product work
+    const int cands[3] = {p.tokens > 4 ? 8 : 4, p.tokens > 4 ? 4 : 8, 2};
     for (int c : cands) {
         if (waves_override && c != waves_override) continue;
         if (w->blocks % c == 0 && (w->blocks / c == 4 || w->blocks / c == 8)) {
@@ -729,21 +758,25 @@ int32_t try_i8_decode(const DeviceWeights* w, MatmulParams& p, hipStream_t strea
     if (!waves) return 1;
     const int per = w->blocks / waves;
     const int m = p.tokens;
-    p.st_bytes = (w->groups * 32 * m + 15) & ~15;
-    p.ldd = ((2 * w->blocks + 3) & ~3) + 4;  // product row stride: every group a wave writes
-    const size_t lds = (size_t)p.st_bytes + (size_t)m * 16 * p.ldd * sizeof(float);
+    size_t lds;
+    if (m <= 4) {
+        p.ldd = ((2 * w->blocks + 3) & ~3) + 4;  // product row stride: every group a wave writes
+        p.swz = 0;
+    } else {
+        // the swizzle mask is the largest power of two (<= 16) dividing the
+        // float4 columns, less 1
+        p.ldd = (2 * w->blocks + 3) & ~3;
+        const int cols4 = p.ldd / 4;
+        p.swz = std::min(cols4 & -cols4, 16) - 1;
+    }
+    lds = (size_t)m * 16 * p.ldd * sizeof(float);
     if (lds > kMaxLds) return 1;
-    const int ns = (m * w->groups * 2 + 64 * waves - 1) / (64 * waves);
-    if (ns > 4) return 1;
-    int32_t rc;
     // the kernel's CB must equal per (4 or 8)
     if (per == 4)
-        rc = w->special_scales ? launch_dec_ti<4, true>(p, waves, ns, lds, stream)
-                               : launch_dec_ti<4, false>(p, waves, ns, lds, stream);
-    else
-        rc = w->special_scales ? launch_dec_ti<8, true>(p, waves, ns, lds, stream)
-                               : launch_dec_ti<8, false>(p, waves, ns, lds, stream);
-    return rc;
+        return w->special_scales ? launch_dec_ti<4, true>(p, waves, lds, stream)
+                                 : launch_dec_ti<4, false>(p, waves, lds, stream);
+    return w->special_scales ? launch_dec_ti<8, true>(p, waves, lds, stream)
+                             : launch_dec_ti<8, false>(p, waves, lds, stream);
 }
 
 template <int CB, int NS, bool DOTS>

@@ -277,7 +277,7 @@ def test_kernel_table_prepare_and_quantize(hip, orc):
     assert abs(scale - 0.03149606) <= 1e-6 and list(q) == [-127, 0, 127, 0, 0, 0, 0, 0]
 
 
-# ------------------------------------------ decode kernel (M <= 4) edges --
+# ----------------------------------------- decode kernel (M <= 16) edges --
 
 @pytest.mark.parametrize("tokens", [1, 2, 3, 4])
 @pytest.mark.parametrize("r0,r1", [(0, 37), (5, 29), (16, 17)])
@@ -292,6 +292,23 @@ def test_int8_decode_path_row_ranges(hip, orc, tokens, r0, r1):
         want = np.full((tokens, ldy), SENTINEL, dtype=np.float32)
         orc.matmul_rows_i8(w, scales, q, qs, tokens, want, ldy, r0, r1)
         assert np.array_equal(y.view(np.uint32), want.view(np.uint32))
+
+
+@pytest.mark.parametrize("tokens", [5, 8, 13, 16])
+@pytest.mark.parametrize("r0,r1", [(0, 64), (5, 29), (16, 17)])
+def test_int8_wide_decode_path_row_ranges(hip, orc, tokens, r0, r1):
+    """5..16 rows: lanes hold four tokens each and the swizzled products
+    overwrite the staged activations (K = 1024 and 2048; K = 4096 up to 8
+    rows, beyond which the general kernel runs)."""
+    for cols in (1024, 2048, 4096):
+        rows = 64
+        w, scales, x, q, qs = int8_case(orc, 5000 + tokens * 10 + r0 + cols, rows, cols, tokens)
+        weights = hip.Weights.int8(w, scales)
+        ldy = rows + 3
+        y = run_i8(hip, weights, q, qs, tokens, ldy, r0, r1)
+        want = np.full((tokens, ldy), SENTINEL, dtype=np.float32)
+        orc.matmul_rows_i8(w, scales, q, qs, tokens, want, ldy, r0, r1)
+        assert np.array_equal(y.view(np.uint32), want.view(np.uint32)), cols
 
 
 @pytest.mark.parametrize("tokens", [3, 7])
