@@ -81,6 +81,25 @@ int32_t attention_decode_impl(const int8_t* d_q, const float* d_qscale, int32_t 
                               const int32_t* d_row_count, int32_t max_chunks, void* d_workspace,
                               size_t workspace_bytes, float* d_out, int8_t* d_q_out, float* d_qs_out,
                               hipStream_t stream);
+// Decode matmul (1..4 tokens, literal int8 format, all rows) whose int8
+// activation rows are computed in the kernel's prologue from fp32 inputs
+// (gemv.hip): kProNorm = x (+ delta) -> RMSNorm * gain -> QuantizeInt8,
+// workgroup 0 writing x + delta to x_out when both are given; kProQuant =
+// QuantizeInt8(x); kProSwiglu = QuantizeInt8((g / (1 + Exp(-g))) * u) with
+// x = [g | u] rows of 2K.  Returns 1 (nothing launched) when the shape does
+// not fit the kernel; the caller then runs the element-wise kernel and the
+// plain matmul.
+enum : int32_t { kProNorm = 1, kProQuant = 2, kProSwiglu = 3 };
+struct DecodePrologue {
+    int32_t kind;
+    const float* x;
+    const float* delta;
+    float* x_out;
+    const float* gain;
+    float eps;
+};
+int32_t launch_decode_fused(const DeviceWeights* w, const DecodePrologue& f, int32_t tokens, float* y, int32_t ldy,
+                            hipStream_t stream);
 // Token count from which literal int8 matmuls use the prefill kernel.
 constexpr int32_t kGemmMinTokens = 32;
 }  // namespace nhip
@@ -118,6 +137,71 @@ __device__ __forceinline__ int ref_quantize_one(float x, float inverse)
 __device__ __forceinline__ float ref_max(float a, float b)
 {
     return a > b ? a : (b > a ? b : (__float_as_uint(a) == 0x80000000u ? b : a));
+}
+
+// ------------------------------------------- canonical row reductions --
+// The decoder's element-wise kernels reduce a row of n terms (squares for
+// RMSNorm, exponentials for the top-k log-sum-exp) in one canonical order
+// that the CPU path repeats:
+//   p[t], t < 256: the terms of elements i with (i / 4) % 256 == t, added
+//                  in ascending i starting from +0 (lane t loads the float4
+//                  groups at 4t, 4t + 1024, ...);
+//   q[m], m < 16:  p[16m] + p[16m+1] + ... + p[16m+15], left to right;
+//   total:         q folded with strides 8, 4, 2, 1 (q[m] = q[m] + q[m+s]).
+// The last two levels run in the 16 lanes of one DPP row.
+__device__ __forceinline__ float dpp_row_shl(float v, int n)
+{
+    // lane l of a 16-lane row receives lane l + n (row_shl:n; invalid lanes get 0)
+    switch (n) {
+        case 8: return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x108, 0xF, 0xF, false));
+        case 4: return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x104, 0xF, 0xF, false));
+        case 2: return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x102, 0xF, 0xF, false));
+        default: return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x101, 0xF, 0xF, false));
+    }
+}
+
+// Levels 2 and 3 of the canonical sum for the 256 partials p[] of one row in
+// LDS; called by a whole wave, the total lands in lane 0 (lanes 16, 32 and 48
+// hold the same value).
+__device__ __forceinline__ float canonical_finish(const float* p, int lane)
+{
+    const float4* p4 = reinterpret_cast<const float4*>(p + 16 * (lane & 15));
+    const float4 a = p4[0], b = p4[1], c = p4[2], d = p4[3];
+    float q = a.x;
+    q = q + a.y;
+    q = q + a.z;
+    q = q + a.w;
+    q = q + b.x;
+    q = q + b.y;
+    q = q + b.z;
+    q = q + b.w;
+    q = q + c.x;
+    q = q + c.y;
+    q = q + c.z;
+    q = q + c.w;
+    q = q + d.x;
+    q = q + d.y;
+    q = q + d.z;
+    q = q + d.w;
+    q = q + dpp_row_shl(q, 8);
+    q = q + dpp_row_shl(q, 4);
+    q = q + dpp_row_shl(q, 2);
+    q = q + dpp_row_shl(q, 1);
+    return q;
+}
+
+// Maximum over the 64 lanes of a wave (order-free), in every lane.
+__device__ __forceinline__ float wave_max(float v)
+{
+    v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xF, 0xF, false)));
+    v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4E, 0xF, 0xF, false)));
+    v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x141, 0xF, 0xF, false)));
+    v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x140, 0xF, 0xF, false)));
+    const float a = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+    const float b = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
+    const float c = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+    const float d = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
+    return fmaxf(fmaxf(a, b), fmaxf(c, d));
 }
 
 // Ops.Exp (src/Needle/Ops.cs:16-31), one lane: the reference's polynomial

@@ -35,27 +35,43 @@ constexpr int kThreads = 256;
 constexpr int kMaxPerThread = 16;  // d and ffn up to 4096 elements per row
 constexpr int kMaxTopK = 8;
 
-__device__ __forceinline__ float block_max_abs(float v, float* red)
+constexpr int kGroups4 = 4;        // float4 groups per thread: rows up to 4096 elements
+
+// Maximum over the block (4 waves, order-free) through wmax[4].
+__device__ __forceinline__ float block_max(float v, float* wmax)
 {
-    for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off));
+    v = wave_max(v);
+    if ((threadIdx.x & 63) == 0) wmax[threadIdx.x >> 6] = v;
     __syncthreads();
-    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
-    __syncthreads();
-    return fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    return fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
 }
 
-// Canonical 256-lane sum: lane t holds its elements t, t+256, ... summed in
-// ascending order; lanes fold pairwise with strides 128, 64, ..., 1.
-__device__ __forceinline__ float block_fold(float s, float* red)
+// The canonical row sum (common.hpp) of the partials p[t] held by the 256
+// threads, broadcast to every thread through red[256 + 1].
+__device__ __forceinline__ float block_canonical_sum(float p, float* red)
 {
+    red[threadIdx.x] = p;
     __syncthreads();
-    red[threadIdx.x] = s;
-    __syncthreads();
-    for (int stride = 128; stride > 0; stride >>= 1) {
-        if ((int)threadIdx.x < stride) red[threadIdx.x] = red[threadIdx.x] + red[threadIdx.x + stride];
-        __syncthreads();
+    if (threadIdx.x < 64) {
+        const float total = canonical_finish(red, threadIdx.x);
+        if (threadIdx.x == 0) red[kThreads] = total;
     }
-    return red[0];
+    __syncthreads();
+    return red[kThreads];
+}
+
+__device__ __forceinline__ uint32_t pack_q4(float4 h, float inverse)
+{
+    const uint32_t a = (uint32_t)(ref_quantize_one(h.x, inverse) & 0xFF);
+    const uint32_t b = (uint32_t)(ref_quantize_one(h.y, inverse) & 0xFF);
+    const uint32_t c = (uint32_t)(ref_quantize_one(h.z, inverse) & 0xFF);
+    const uint32_t d = (uint32_t)(ref_quantize_one(h.w, inverse) & 0xFF);
+    return a | (b << 8) | (c << 16) | (d << 24);
+}
+
+__device__ __forceinline__ float max_abs4(float m, float4 v)
+{
+    return fmaxf(fmaxf(m, fmaxf(fabsf(v.x), fabsf(v.y))), fmaxf(fabsf(v.z), fabsf(v.w)));
 }
 
 // Natural log for normal x > 0: x = m 2^e, m in [sqrt(1/2), sqrt(2)),
@@ -91,51 +107,58 @@ __global__ __launch_bounds__(kThreads) void embed_kernel(const int32_t* tokens, 
 }
 
 // x += delta (when given); ss = sum x^2 (canonical sum); inv = 1 / sqrt(ss /
-// d + eps); h = (x * inv) * gain; QuantizeInt8(h) -> q, scale.
+// d + eps); h = (x * inv) * gain; QuantizeInt8(h) -> q, scale.  Thread t
+// holds the float4 groups at 4t + 1024j (d a multiple of 4, at most 4096).
 template <bool DELTA>
 __global__ __launch_bounds__(kThreads) void add_rmsnorm_quant_kernel(float* x, const float* delta, const float* gain,
                                                                      int d, float eps, int8_t* q, float* qscale)
 {
-    __shared__ float red[kThreads];
+    __shared__ __align__(16) float red[kThreads + 4];
     const int t = threadIdx.x;
     float* xr = x + (size_t)blockIdx.x * d;
     const float* dr = DELTA ? delta + (size_t)blockIdx.x * d : nullptr;
-    float v[kMaxPerThread], gv[kMaxPerThread];
+    float4 v[kGroups4], gv[kGroups4];
 #pragma unroll
-    for (int j = 0; j < kMaxPerThread; j++) {  // every load first
-        const int i = min(t + j * kThreads, d - 1);
-        v[j] = xr[i];
-        gv[j] = gain[i];
-        if constexpr (DELTA) v[j] = v[j] + dr[i];
+    for (int j = 0; j < kGroups4; j++) {  // every load first
+        const int i = min(4 * t + 1024 * j, d - 4);
+        v[j] = *reinterpret_cast<const float4*>(xr + i);
+        gv[j] = *reinterpret_cast<const float4*>(gain + i);
+        if constexpr (DELTA) {
+            const float4 e = *reinterpret_cast<const float4*>(dr + i);
+            v[j] = make_float4(v[j].x + e.x, v[j].y + e.y, v[j].z + e.z, v[j].w + e.w);
+        }
     }
     float s = 0.0f;
 #pragma unroll
-    for (int j = 0; j < kMaxPerThread; j++) {
-        const int i = t + j * kThreads;
+    for (int j = 0; j < kGroups4; j++) {
+        const int i = 4 * t + 1024 * j;
         if (i < d) {
-            if constexpr (DELTA) xr[i] = v[j];
-            s = s + v[j] * v[j];
+            if constexpr (DELTA) *reinterpret_cast<float4*>(xr + i) = v[j];
+            s = s + v[j].x * v[j].x;
+            s = s + v[j].y * v[j].y;
+            s = s + v[j].z * v[j].z;
+            s = s + v[j].w * v[j].w;
         }
     }
-    const float ss = block_fold(s, red);
+    const float ss = block_canonical_sum(s, red);
     const float inv = 1.0f / sqrtf(ss / (float)d + eps);
     float peak = 0.0f;
 #pragma unroll
-    for (int j = 0; j < kMaxPerThread; j++) {
-        const int i = t + j * kThreads;
-        if (i < d) {
-            v[j] = (v[j] * inv) * gv[j];
-            peak = fmaxf(peak, fabsf(v[j]));
+    for (int j = 0; j < kGroups4; j++) {
+        if (4 * t + 1024 * j < d) {
+            v[j] = make_float4((v[j].x * inv) * gv[j].x, (v[j].y * inv) * gv[j].y, (v[j].z * inv) * gv[j].z,
+                               (v[j].w * inv) * gv[j].w);
+            peak = max_abs4(peak, v[j]);
         }
     }
-    peak = block_max_abs(peak, red);
+    peak = block_max(peak, red + kThreads);
     const float scale = peak > 0.0f ? peak / 127.0f : 1.0f;
     const float inverse = 1.0f / scale;
     int8_t* qr = q + (size_t)blockIdx.x * d;
 #pragma unroll
-    for (int j = 0; j < kMaxPerThread; j++) {
-        const int i = t + j * kThreads;
-        if (i < d) qr[i] = static_cast<int8_t>(ref_quantize_one(v[j], inverse));
+    for (int j = 0; j < kGroups4; j++) {
+        const int i = 4 * t + 1024 * j;
+        if (i < d) *reinterpret_cast<uint32_t*>(qr + i) = pack_q4(v[j], inverse);
     }
     if (t == 0) qscale[blockIdx.x] = scale;
 }
@@ -191,38 +214,39 @@ __global__ __launch_bounds__(64) void qkv_post_kernel(PostParams p)
     if (e == 0) (key ? p.key_scales : p.value_scales)[cell] = scale;
 }
 
-// a = (g / (1 + Exp(-g))) * u, then QuantizeInt8(a).
+// a = (g / (1 + Exp(-g))) * u, then QuantizeInt8(a).  Thread t holds the
+// float4 groups at 4t + 1024j (ffn a multiple of 4, at most 4096).
 __global__ __launch_bounds__(kThreads) void swiglu_quant_kernel(const float* gu, int ffn, int8_t* q, float* qscale)
 {
-    __shared__ float red[kThreads];
+    __shared__ float wmax[4];
     const int t = threadIdx.x;
     const float* g = gu + (size_t)blockIdx.x * 2 * ffn;
     const float* up = g + ffn;
-    float v[kMaxPerThread], uv[kMaxPerThread];
+    float4 v[kGroups4], uv[kGroups4];
 #pragma unroll
-    for (int j = 0; j < kMaxPerThread; j++) {  // every load first
-        const int i = min(t + j * kThreads, ffn - 1);
-        v[j] = g[i];
-        uv[j] = up[i];
+    for (int j = 0; j < kGroups4; j++) {  // every load first
+        const int i = min(4 * t + 1024 * j, ffn - 4);
+        v[j] = *reinterpret_cast<const float4*>(g + i);
+        uv[j] = *reinterpret_cast<const float4*>(up + i);
     }
     float peak = 0.0f;
 #pragma unroll
-    for (int j = 0; j < kMaxPerThread; j++) {
-        const int i = t + j * kThreads;
-        if (i < ffn) {
-            const float gi = v[j];
-            v[j] = (gi / (1.0f + exp_poly(-gi))) * uv[j];
-            peak = fmaxf(peak, fabsf(v[j]));
+    for (int j = 0; j < kGroups4; j++) {
+        if (4 * t + 1024 * j < ffn) {
+            const float4 gi = v[j];
+            v[j] = make_float4((gi.x / (1.0f + exp_poly(-gi.x))) * uv[j].x, (gi.y / (1.0f + exp_poly(-gi.y))) * uv[j].y,
+                               (gi.z / (1.0f + exp_poly(-gi.z))) * uv[j].z, (gi.w / (1.0f + exp_poly(-gi.w))) * uv[j].w);
+            peak = max_abs4(peak, v[j]);
         }
     }
-    peak = block_max_abs(peak, red);
+    peak = block_max(peak, wmax);
     const float scale = peak > 0.0f ? peak / 127.0f : 1.0f;
     const float inverse = 1.0f / scale;
     int8_t* qr = q + (size_t)blockIdx.x * ffn;
 #pragma unroll
-    for (int j = 0; j < kMaxPerThread; j++) {
-        const int i = t + j * kThreads;
-        if (i < ffn) qr[i] = static_cast<int8_t>(ref_quantize_one(v[j], inverse));
+    for (int j = 0; j < kGroups4; j++) {
+        const int i = 4 * t + 1024 * j;
+        if (i < ffn) *reinterpret_cast<uint32_t*>(qr + i) = pack_q4(v[j], inverse);
     }
     if (t == 0) qscale[blockIdx.x] = scale;
 }
@@ -240,14 +264,14 @@ __device__ __forceinline__ bool masked(int i) { return i == 0 || i == 2 || i == 
 // top K of the ids except 0, 2, 3 (the set is unique under the order above,
 // so the tree merge equals the reference's sequential insertion);
 // log_shift = peak + log(sum_i Exp(v_i - peak)), masked v_i = -1e30, the sum
-// by the canonical 256-lane reduction; lp = v - log_shift.  K is a template
+// by the canonical row reduction; lp = v - log_shift.  K is a template
 // parameter so that the per-thread lists stay in registers.
 template <int K>
 __global__ __launch_bounds__(kThreads) void topk_lse_kernel(const float* logits, int n, int32_t* idx, float* lp)
 {
     __shared__ float tv[K][kThreads];
     __shared__ int ti[K][kThreads];
-    __shared__ float red[kThreads];
+    __shared__ __align__(16) float red[kThreads + 4];
     const int t = threadIdx.x;
     const float* x = logits + (size_t)blockIdx.x * n;
     float bv[K];
@@ -257,15 +281,33 @@ __global__ __launch_bounds__(kThreads) void topk_lse_kernel(const float* logits,
         bv[m] = -INFINITY;
         bi[m] = 0x7FFFFFFF;
     }
-    // ids i = t + 256 j in ascending j, loaded eight at a time
+    // ids i = 4t + 1024 j + e (the canonical lane's elements), two float4
+    // groups at a time (n % 4 == 0: whole groups; else the tail group by
+    // clamped scalar loads)
     constexpr int kBatch = 8;
-    for (int i0 = t; i0 < n; i0 += kBatch * kThreads) {
-        float xv[kBatch];
+    const bool whole = (n & 3) == 0;
+    auto load8 = [&](float (&xv)[kBatch], int i0) {
 #pragma unroll
-        for (int j = 0; j < kBatch; j++) xv[j] = x[min(i0 + j * kThreads, n - 1)];
+        for (int h = 0; h < 2; h++) {
+            const int g = i0 + h * 1024;
+            if (whole) {
+                const float4 v = *reinterpret_cast<const float4*>(x + min(g, n - 4));
+                xv[4 * h] = v.x;
+                xv[4 * h + 1] = v.y;
+                xv[4 * h + 2] = v.z;
+                xv[4 * h + 3] = v.w;
+            } else {
+#pragma unroll
+                for (int e = 0; e < 4; e++) xv[4 * h + e] = x[min(g + e, n - 1)];
+            }
+        }
+    };
+    for (int i0 = 4 * t; i0 < n; i0 += 2 * 1024) {
+        float xv[kBatch];
+        load8(xv, i0);
 #pragma unroll
         for (int j = 0; j < kBatch; j++) {
-            const int i = i0 + j * kThreads;
+            const int i = i0 + (j >> 2) * 1024 + (j & 3);
             const float v = xv[j];
             if (i >= n || masked(i) || !before(v, i, bv[K - 1], bi[K - 1])) continue;
             bv[K - 1] = v;
@@ -323,17 +365,16 @@ __global__ __launch_bounds__(kThreads) void topk_lse_kernel(const float* logits,
     }
     const float peak = tv[0][0];
     float s = 0.0f;
-    for (int i0 = t; i0 < n; i0 += kBatch * kThreads) {
+    for (int i0 = 4 * t; i0 < n; i0 += 2 * 1024) {
         float xv[kBatch];
-#pragma unroll
-        for (int j = 0; j < kBatch; j++) xv[j] = x[min(i0 + j * kThreads, n - 1)];
+        load8(xv, i0);
 #pragma unroll
         for (int j = 0; j < kBatch; j++) {
-            const int i = i0 + j * kThreads;
+            const int i = i0 + (j >> 2) * 1024 + (j & 3);
             if (i < n) s = s + exp_poly((masked(i) ? -1e30f : xv[j]) - peak);
         }
     }
-    const float total = block_fold(s, red);
+    const float total = block_canonical_sum(s, red);
     const float log_shift = peak + log_poly(total);
     if (t < K) {
         idx[(size_t)blockIdx.x * K + t] = ti[t][0];
@@ -413,6 +454,7 @@ struct nhip_decoder {
     float* value_scales = nullptr;
     // activations for up to max_rows rows
     float* x = nullptr;
+    float* x2 = nullptr;  // the other residual buffer of the fused forward
     float* delta = nullptr;
     int8_t* q8 = nullptr;
     float* qs = nullptr;
@@ -454,25 +496,55 @@ int32_t* in_positions(nhip_decoder* m, int32_t* base) { return base + 2 * m->dim
 int32_t* in_first(nhip_decoder* m, int32_t* base) { return base + 3 * m->dims.max_rows; }
 int32_t* in_count(nhip_decoder* m, int32_t* base) { return base + 4 * m->dims.max_rows; }
 
+// Residual + RMSNorm + quantize feeding a matmul.  For up to four rows one
+// fused launch computes the normalised rows in the matmul's prologue, reading
+// *x and the pending delta and writing their sum to the other residual
+// buffer (which then becomes *x); otherwise the element-wise kernel updates
+// *x in place and the plain matmul follows.  Either way the residual ends in
+// *x with the delta added.
+int32_t norm_matmul(nhip_decoder* m, int rows, float** x, bool pending, const float* gain, nhip_weights* w,
+                    float* y, int ldy, bool fuse)
+{
+    const nhip_decoder_dims& D = m->dims;
+    hipStream_t s = m->stream;
+    if (fuse) {
+        float* other = *x == m->x ? m->x2 : m->x;
+        DecodePrologue f{kProNorm, *x, pending ? m->delta : nullptr, pending ? other : nullptr, gain, D.eps};
+        const int32_t rc = launch_decode_fused(w, f, rows, y, ldy, s);
+        if (rc <= 0) {
+            if (rc == 0 && pending) *x = other;
+            return rc;
+        }
+    }
+    if (pending)
+        hipLaunchKernelGGL(add_rmsnorm_quant_kernel<true>, dim3(rows), dim3(kThreads), 0, s, *x, m->delta, gain, D.d,
+                           D.eps, m->q8, m->qs);
+    else
+        hipLaunchKernelGGL(add_rmsnorm_quant_kernel<false>, dim3(rows), dim3(kThreads), 0, s, *x, nullptr, gain, D.d,
+                           D.eps, m->q8, m->qs);
+    NHIP_CHECK_HIP(hipGetLastError());
+    return nhip_matmul_i8_dev(w, m->q8, m->qs, rows, y, ldy, 0, w->rows, s);
+}
+
 // Enqueues the forward of `rows` rows whose inputs are already in d_in.
 int32_t enqueue_forward(nhip_decoder* m, int rows, int k)
 {
+    // NHIP_DECODER_FUSED=0 keeps the element-wise kernels separate (for A/B timing)
+    static const bool fused_enabled = [] {
+        const char* e = getenv("NHIP_DECODER_FUSED");
+        return !(e && e[0] == '0');
+    }();
+    const bool fuse = fused_enabled && rows <= 4;
     const nhip_decoder_dims& D = m->dims;
     const int d = D.d, H = D.heads, KV = D.kv_heads, F = D.ffn;
     hipStream_t s = m->stream;
     int32_t rc;
-    hipLaunchKernelGGL(embed_kernel, dim3(rows), dim3(kThreads), 0, s, in_tokens(m, m->d_in), m->emb, d, m->x);
+    float* x = m->x;
+    hipLaunchKernelGGL(embed_kernel, dim3(rows), dim3(kThreads), 0, s, in_tokens(m, m->d_in), m->emb, d, x);
     NHIP_CHECK_HIP(hipGetLastError());
     const size_t layer_cells = (size_t)D.slots * D.capacity * KV;
     for (int l = 0; l < D.layers; l++) {
-        if (l == 0)
-            hipLaunchKernelGGL(add_rmsnorm_quant_kernel<false>, dim3(rows), dim3(kThreads), 0, s, m->x, nullptr,
-                               m->attn_norm[l], d, D.eps, m->q8, m->qs);
-        else
-            hipLaunchKernelGGL(add_rmsnorm_quant_kernel<true>, dim3(rows), dim3(kThreads), 0, s, m->x, m->delta,
-                               m->attn_norm[l], d, D.eps, m->q8, m->qs);
-        NHIP_CHECK_HIP(hipGetLastError());
-        rc = nhip_matmul_i8_dev(m->wqkv[l], m->q8, m->qs, rows, m->qkv, m->qkv_n, 0, m->qkv_n, s);
+        rc = norm_matmul(m, rows, &x, l > 0, m->attn_norm[l], m->wqkv[l], m->qkv, m->qkv_n, fuse);
         if (rc) return rc;
         PostParams pp{};
         pp.qkv = m->qkv;
@@ -492,33 +564,55 @@ int32_t enqueue_forward(nhip_decoder* m, int rows, int k)
         hipLaunchKernelGGL(qkv_post_kernel, dim3(rows, H + 2 * KV), dim3(64), 0, s, pp);
         NHIP_CHECK_HIP(hipGetLastError());
         // single-chunk attention over all heads also quantizes its output rows
-        const bool fused_quant = D.max_chunks == 1 && H <= 16;
+        const bool attn_quant = D.max_chunks == 1 && H <= 16;
         rc = attention_decode_impl(m->qh, m->qhs, rows, H, KV, 64, pp.keys, pp.key_scales, pp.values,
                                    pp.value_scales, D.slots, D.capacity, in_slots(m, m->d_in), in_first(m, m->d_in),
                                    in_count(m, m->d_in), D.max_chunks, m->attn_ws, m->attn_ws_bytes, m->att,
-                                   fused_quant ? m->q8 : nullptr, fused_quant ? m->qs : nullptr, s);
+                                   attn_quant ? m->q8 : nullptr, attn_quant ? m->qs : nullptr, s);
         if (rc) return rc;
-        if (!fused_quant) {
-            rc = nhip_quantize_rows_dev(m->att, rows, H * 64, m->q8, m->qs, s);
+        rc = 1;
+        if (!attn_quant && fuse) {
+            DecodePrologue f{kProQuant, m->att, nullptr, nullptr, nullptr, 0.0f};
+            rc = launch_decode_fused(m->wo[l], f, rows, m->delta, d, s);
+            if (rc < 0) return rc;
+        }
+        if (rc) {
+            if (!attn_quant) {
+                rc = nhip_quantize_rows_dev(m->att, rows, H * 64, m->q8, m->qs, s);
+                if (rc) return rc;
+            }
+            rc = nhip_matmul_i8_dev(m->wo[l], m->q8, m->qs, rows, m->delta, d, 0, d, s);
             if (rc) return rc;
         }
-        rc = nhip_matmul_i8_dev(m->wo[l], m->q8, m->qs, rows, m->delta, d, 0, d, s);
+        rc = norm_matmul(m, rows, &x, true, m->ffn_norm[l], m->wgu[l], m->gu, 2 * F, fuse);
         if (rc) return rc;
-        hipLaunchKernelGGL(add_rmsnorm_quant_kernel<true>, dim3(rows), dim3(kThreads), 0, s, m->x, m->delta,
-                           m->ffn_norm[l], d, D.eps, m->q8, m->qs);
+        rc = 1;
+        if (fuse) {
+            DecodePrologue f{kProSwiglu, m->gu, nullptr, nullptr, nullptr, 0.0f};
+            rc = launch_decode_fused(m->wd[l], f, rows, m->delta, d, s);
+            if (rc < 0) return rc;
+        }
+        if (rc) {
+            hipLaunchKernelGGL(swiglu_quant_kernel, dim3(rows), dim3(kThreads), 0, s, m->gu, F, m->q8, m->qs);
+            NHIP_CHECK_HIP(hipGetLastError());
+            rc = nhip_matmul_i8_dev(m->wd[l], m->q8, m->qs, rows, m->delta, d, 0, d, s);
+            if (rc) return rc;
+        }
+    }
+    // the final residual is not needed again: no x_out
+    rc = 1;
+    if (fuse) {
+        DecodePrologue f{kProNorm, x, m->delta, nullptr, m->final_norm, D.eps};
+        rc = launch_decode_fused(m->wlm, f, rows, m->logits, D.vocab, s);
+        if (rc < 0) return rc;
+    }
+    if (rc) {
+        hipLaunchKernelGGL(add_rmsnorm_quant_kernel<true>, dim3(rows), dim3(kThreads), 0, s, x, m->delta,
+                           m->final_norm, d, D.eps, m->q8, m->qs);
         NHIP_CHECK_HIP(hipGetLastError());
-        rc = nhip_matmul_i8_dev(m->wgu[l], m->q8, m->qs, rows, m->gu, 2 * F, 0, 2 * F, s);
-        if (rc) return rc;
-        hipLaunchKernelGGL(swiglu_quant_kernel, dim3(rows), dim3(kThreads), 0, s, m->gu, F, m->q8, m->qs);
-        NHIP_CHECK_HIP(hipGetLastError());
-        rc = nhip_matmul_i8_dev(m->wd[l], m->q8, m->qs, rows, m->delta, d, 0, d, s);
+        rc = nhip_matmul_i8_dev(m->wlm, m->q8, m->qs, rows, m->logits, D.vocab, 0, D.vocab, s);
         if (rc) return rc;
     }
-    hipLaunchKernelGGL(add_rmsnorm_quant_kernel<true>, dim3(rows), dim3(kThreads), 0, s, m->x, m->delta,
-                       m->final_norm, d, D.eps, m->q8, m->qs);
-    NHIP_CHECK_HIP(hipGetLastError());
-    rc = nhip_matmul_i8_dev(m->wlm, m->q8, m->qs, rows, m->logits, D.vocab, 0, D.vocab, s);
-    if (rc) return rc;
     if (k > 0) {
         rc = launch_topk(m->logits, rows, D.vocab, k, m->d_topk_idx, m->d_topk_lp, s);
         if (rc) return rc;
@@ -651,7 +745,8 @@ int32_t nhip_decoder_create(const nhip_decoder_dims* dims, nhip_decoder** out)
     };
     if ((rc = dalloc(m, &m->keys, cells * 64)) || (rc = dalloc(m, &m->values, cells * 64)) ||
         (rc = dalloc(m, &m->key_scales, cells)) || (rc = dalloc(m, &m->value_scales, cells)) ||
-        (rc = dalloc(m, &m->x, (size_t)R * D.d)) || (rc = dalloc(m, &m->delta, (size_t)R * D.d)) ||
+        (rc = dalloc(m, &m->x, (size_t)R * D.d)) || (rc = dalloc(m, &m->x2, (size_t)R * D.d)) ||
+        (rc = dalloc(m, &m->delta, (size_t)R * D.d)) ||
         (rc = dalloc(m, &m->q8, (size_t)R * std::max({D.d, D.ffn, D.heads * 64}))) || (rc = dalloc(m, &m->qs, (size_t)R)) ||
         (rc = dalloc(m, &m->qkv, (size_t)R * m->qkv_n)) || (rc = dalloc(m, &m->qh, (size_t)R * D.heads * 64)) ||
         (rc = dalloc(m, &m->qhs, (size_t)R * D.heads)) || (rc = dalloc(m, &m->att, (size_t)R * D.heads * 64)) ||

@@ -533,6 +533,85 @@ __global__ __launch_bounds__(512) void matmul_i8_kernel(MatmulParams p)
     }
 }
 
+__device__ __forceinline__ float decode_scale_fast(uint32_t h)
+{
+    // binary16 -> binary32 is exact; a -0 scale gives a +-0 product, which
+    // cannot change an accumulator that starts at +0.
+    return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(h)));
+}
+
+// M <= 4 tokens: four groups g..g+3 share one D.  MFMA j of a set holds group
+// g+j's activations in A rows 4j..4j+3 (zero elsewhere) and accumulates into
+// the previous result; the row blocks are disjoint, so D rows 4j+i are
+// exactly D_{g+j} of token i, and lane (r, kq) ends up holding the M tokens
+// of group g+kq.  Each product (hs * scale[t]) * D_g goes to LDS at
+// pl[(t*16 + r)*GS + g].  av[c]: this lane's A operand of set c (token r%4,
+// group g + r/4, k-slice kq; zero for tokens >= M); hraw[c]: the scale of
+// (row r, group g + kq).
+template <int CB, int TI, bool EXACT>
+__device__ __forceinline__ void narrow_products(const long (&av)[2 * CB / 4], const float (&qs)[TI],
+                                                const uint16_t (&hraw)[2 * CB / 4], const u4 (&w)[CB], float* pl,
+                                                int GS, int M, int g_first, int r, int kq)
+{
+    const v4i zero = {0, 0, 0, 0};
+    float* prow = pl + (size_t)r * GS + g_first + kq;
+#pragma unroll
+    for (int c = 0; c < 2 * CB / 4; c++) {
+        v4i d = zero;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const u4& wc = w[2 * c + (j >> 1)];
+            const long b = (j & 1) ? (long)(((uint64_t)wc.w << 32) | wc.z) : (long)(((uint64_t)wc.y << 32) | wc.x);
+            d = __builtin_amdgcn_mfma_i32_16x16x32_i8((r >> 2) == j ? av[c] : 0, b, d, 0, 0, 0);
+        }
+        const float hs = EXACT ? ref_half_to_single(hraw[c]) : decode_scale_fast(hraw[c]);
+        // groups >= G are written (inside the row) but never read
+#pragma unroll
+        for (int i = 0; i < TI; i++)
+            if (i < M) prow[(size_t)i * 16 * GS + 4 * c] = (hs * qs[i]) * static_cast<float>(d[i]);
+    }
+}
+
+// The lanes (t, r) of the first M*16 threads add row (t, r)'s products in
+// ascending group order and store y[t][n].  Float4 column c of product row
+// x sits at column c ^ (x & swz).
+__device__ __forceinline__ void chain_products(const float* pl, int GS, int swz, int M, int G, int tile,
+                                               const MatmulParams& p)
+{
+    for (int x = threadIdx.x; x < M * 16; x += blockDim.x) {
+        const int t = x >> 4;
+        const int rr = x & 15;
+        const int nn = tile * 16 + rr;
+        const float4* row = reinterpret_cast<const float4*>(pl + (size_t)x * GS);
+        const int sw = x & swz;
+        float acc = 0.0f;
+        float4 v[4];
+        const int full = G >> 4;  // chunks of 16 groups
+        if (full > 0) {
+#pragma unroll
+            for (int j = 0; j < 4; j++) v[j] = row[j ^ sw];
+        }
+        for (int ch = 0; ch < full; ch++) {
+            float4 nx[4];
+            const int nb = min(ch + 1, full - 1) * 4;
+#pragma unroll
+            for (int j = 0; j < 4; j++) nx[j] = row[(nb + j) ^ sw];
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                acc = acc + v[j].x;
+                acc = acc + v[j].y;
+                acc = acc + v[j].z;
+                acc = acc + v[j].w;
+            }
+#pragma unroll
+            for (int j = 0; j < 4; j++) v[j] = nx[j];
+        }
+        const float* rowf = reinterpret_cast<const float*>(row);
+        for (int c = full * 16; c < G; c++) acc = acc + rowf[(((c >> 2) ^ sw) << 2) | (c & 3)];
+        if (nn >= p.row_start && nn < p.row_end) p.y[(size_t)t * p.ldy + nn] = acc;
+    }
+}
+
 // Decode path of the literal int8 format for M <= 16 tokens (beam rows,
 // packed sequences).  Each of the S waves of a 16-row tile owns CB weight
 // blocks (2*CB groups) and loads its A operands (its K range of the M rows)
@@ -540,12 +619,8 @@ __global__ __launch_bounds__(512) void matmul_i8_kernel(MatmulParams p)
 // (Scalar.cs:185-186) and leaves them in LDS as [t][r][g]; after one barrier
 // the lanes (t, r) add them in ascending group order, so each y[t][n] is
 // exactly (((0 + p_0) + p_1) + ... + p_{G-1}).
-//   TI <= 4: four groups g..g+3 share one D.  MFMA j of a set holds group
-//            g+j's activations in A rows 4j..4j+3 (zero elsewhere) and
-//            accumulates into the previous result; the row blocks are
-//            disjoint, so D rows 4j+i are exactly D_{g+j} of token i, and
-//            lane (r, kq) ends up holding the M tokens of group g+kq: every
-//            lane's products are useful.  Product rows are padded (stride
+//   TI <= 4: narrow_products (four groups per MFMA set, every lane's
+//            products useful); product rows are padded (stride
 //            GS = roundup4(2*blocks) + 4).
 //   TI == 16: one group per MFMA; lane (r, kq) holds tokens 4kq..4kq+3 of
 //            row r; the products are M*16 rows of GS = roundup4(2*blocks)
@@ -558,8 +633,7 @@ template <int CB, int TI, bool EXACT>
 __global__ __launch_bounds__(512) void matmul_i8_decode_kernel(MatmulParams p)
 {
     constexpr bool WIDE = TI > 4;
-    constexpr int TL = WIDE ? 4 : TI;  // tokens per lane
-    constexpr int SETS = 2 * CB / 4;   // TI <= 4: sets of four groups per wave
+    constexpr int SETS = 2 * CB / 4;  // TI <= 4: sets of four groups per wave
     extern __shared__ __align__(16) uint8_t lds[];
     float* pl = reinterpret_cast<float*>(lds);  // products [t][r][GS]
     const int lane = threadIdx.x & 63;
@@ -579,6 +653,7 @@ __global__ __launch_bounds__(512) void matmul_i8_decode_kernel(MatmulParams p)
     // 1. activation operands, 2. activation scales, 3. weight scales,
     // 4. weight blocks -- in this order, all in flight together
     constexpr int NA = WIDE ? 2 * CB : SETS;
+    constexpr int TL = WIDE ? 4 : TI;  // tokens per lane
     long av[NA];
     float qraw[TL];
     if constexpr (WIDE) {
@@ -616,17 +691,8 @@ __global__ __launch_bounds__(512) void matmul_i8_decode_kernel(MatmulParams p)
     for (int c = 0; c < CB; c++) w[c] = __builtin_nontemporal_load(wbase + (size_t)(mb0 + c) * 64);
     __builtin_amdgcn_sched_barrier(0);
 
-    auto decode_scale = [](uint32_t h) -> float {
-        if constexpr (EXACT) {
-            return ref_half_to_single(h);
-        } else {
-            // binary16 -> binary32 is exact; a -0 scale gives a +-0 product,
-            // which cannot change an accumulator that starts at +0.
-            return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(h)));
-        }
-    };
-    const v4i zero = {0, 0, 0, 0};
     if constexpr (WIDE) {
+        const v4i zero = {0, 0, 0, 0};
         const int tq = 4 * kq;  // first token of this lane's MFMA results
         float qs[4];
 #pragma unroll
@@ -641,7 +707,8 @@ __global__ __launch_bounds__(512) void matmul_i8_decode_kernel(MatmulParams p)
             const uint4 s4 = sraw[k >> 3];
             const int kk = k & 7;
             const uint32_t word = kk < 4 ? (kk < 2 ? s4.x : s4.y) : (kk < 6 ? s4.z : s4.w);
-            const float hs = decode_scale((kk & 1) ? (word >> 16) : (word & 0xFFFFu));
+            const uint32_t h = (kk & 1) ? (word >> 16) : (word & 0xFFFFu);
+            const float hs = EXACT ? ref_half_to_single(h) : decode_scale_fast(h);
 #pragma unroll
             for (int i = 0; i < 4; i++) pr[k][i] = (hs * qs[i]) * static_cast<float>(d[i]);
         }
@@ -659,57 +726,196 @@ __global__ __launch_bounds__(512) void matmul_i8_decode_kernel(MatmulParams p)
         }
     } else {
         const bool feeds = (r & 3) < M;  // A rows of tokens >= M stay zero
-        float* prow = pl + (size_t)r * GS + g_first + kq;
 #pragma unroll
-        for (int c = 0; c < SETS; c++) {
-            const long a = feeds ? av[c] : 0;
-            v4i d = zero;
+        for (int c = 0; c < NA; c++) av[c] = feeds ? av[c] : 0;
+        narrow_products<CB, TI, EXACT>(av, qraw, hraw, w, pl, GS, M, g_first, r, kq);
+    }
+    __syncthreads();
+    chain_products(pl, GS, WIDE ? p.swz : 0, M, G, tile, p);
+}
+
+// The decode kernel for M <= 4 with its activation rows computed in the
+// prologue from fp32 inputs instead of read as int8 (one launch instead of
+// an element-wise kernel and a matmul).  Every workgroup loads the inputs
+// first, then its scales and weight blocks, and computes the M quantized
+// rows (all K) into LDS while the weights are in flight; the rows are
+// bit-identical with the element-wise kernels they replace:
+//   kProNorm    x (+ delta) -> RMSNorm (canonical row sum of squares) *
+//               gain -> QuantizeInt8; workgroup 0 also writes x + delta to
+//               x_out;
+//   kProQuant   QuantizeInt8 of x;
+//   kProSwiglu  a = (g / (1 + Exp(-g))) * u for x = [g | u] (2K per row) ->
+//               QuantizeInt8.
+// Thread t of the prologue holds the float4 groups at 4t + 4*nt*j, j < G4
+// (nt = 256 for the norm, whose lanes are the canonical sum's, else the
+// whole block).  Four rows are always computed (rows past M repeat the
+// last), so every load is unconditional and the weight loads stay in
+// flight across the prologue.
+template <int CB, int KIND, bool DELTA, int G4>
+__global__ __launch_bounds__(512) void matmul_i8_decode_fused_kernel(MatmulParams p, DecodePrologue f)
+{
+    constexpr int TI = 4;
+    constexpr int SETS = 2 * CB / 4;
+    extern __shared__ __align__(16) uint8_t lds[];
+    float* pl = reinterpret_cast<float*>(lds);                            // products [t][r][GS]
+    int8_t* qa = reinterpret_cast<int8_t*>(lds + p.d_bytes);              // quantized rows [TI][K]
+    float* red = reinterpret_cast<float*>(lds + p.d_bytes + p.st_bytes);  // [TI][256] partial sums
+    float* sums = red + TI * 256;                                         // [TI]
+    float* wmax = sums + TI;                                              // [TI][8]
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int nwaves = blockDim.x >> 6;
+    const int tile = p.tile_begin + blockIdx.x;
+    const int M = p.tokens;
+    const int K = p.cols;
+    const int G = p.groups;
+    const int GS = p.ldd;
+    const int r = lane & 15;
+    const int kq = lane >> 4;
+    const int n = tile * 16 + r;
+    const bool active = wave * CB < p.blocks;  // waves past the tile's blocks only run the prologue
+    const int mb0 = active ? wave * CB : 0;
+    const int g_first = mb0 * 2;
+    const u4* wbase = reinterpret_cast<const u4*>(p.tiles) + (size_t)tile * p.blocks * 64 + lane;
+    const uint16_t* nrow = p.norms + (size_t)n * p.groups_pad8 + g_first;
+    constexpr bool NORM = KIND == kProNorm;
+    const int nt = NORM ? 256 : (int)blockDim.x;
+
+    // 1. prologue inputs
+    float4 xv[TI][G4], dv[TI][G4], gv[G4];
 #pragma unroll
-            for (int j = 0; j < 4; j++) {
-                const u4& wc = w[2 * c + (j >> 1)];
-                const long b = (j & 1) ? (long)(((uint64_t)wc.w << 32) | wc.z) : (long)(((uint64_t)wc.y << 32) | wc.x);
-                d = __builtin_amdgcn_mfma_i32_16x16x32_i8((r >> 2) == j ? a : 0, b, d, 0, 0, 0);
+    for (int j = 0; j < G4; j++) {
+        const int i = min(4 * (tid + nt * j), K - 4);
+        if constexpr (NORM) gv[j] = *reinterpret_cast<const float4*>(f.gain + i);
+#pragma unroll
+        for (int t = 0; t < TI; t++) {
+            const size_t row = (size_t)min(t, M - 1);
+            if constexpr (KIND == kProSwiglu) {
+                xv[t][j] = *reinterpret_cast<const float4*>(f.x + row * 2 * K + i);
+                dv[t][j] = *reinterpret_cast<const float4*>(f.x + row * 2 * K + K + i);
+            } else {
+                xv[t][j] = *reinterpret_cast<const float4*>(f.x + row * K + i);
+                if constexpr (DELTA) dv[t][j] = *reinterpret_cast<const float4*>(f.delta + row * K + i);
             }
-            const float hs = decode_scale(hraw[c]);
-            // groups >= G are written (inside the row) but never read
+        }
+    }
+    // 2. weight scales, 3. weight blocks
+    uint16_t hraw[SETS];
 #pragma unroll
-            for (int i = 0; i < TI; i++)
-                if (i < M) prow[(size_t)i * 16 * GS + 4 * c] = (hs * qraw[i]) * static_cast<float>(d[i]);
+    for (int c = 0; c < SETS; c++) hraw[c] = nrow[4 * c + kq];
+    u4 w[CB];
+#pragma unroll
+    for (int c = 0; c < CB; c++) w[c] = __builtin_nontemporal_load(wbase + (size_t)(mb0 + c) * 64);
+    __builtin_amdgcn_sched_barrier(0);
+
+    // 4. the quantized rows, while the weights arrive
+    float peak[TI];
+#pragma unroll
+    for (int t = 0; t < TI; t++) peak[t] = 0.0f;
+    if constexpr (NORM) {
+        const bool pt = tid < 256;
+#pragma unroll
+        for (int t = 0; t < TI; t++) {
+            float s = 0.0f;
+#pragma unroll
+            for (int j = 0; j < G4; j++) {
+                if (pt && 4 * (tid + 256 * j) < K) {
+                    float4 v = xv[t][j];
+                    if constexpr (DELTA) v = make_float4(v.x + dv[t][j].x, v.y + dv[t][j].y, v.z + dv[t][j].z, v.w + dv[t][j].w);
+                    xv[t][j] = v;
+                    s = s + v.x * v.x;
+                    s = s + v.y * v.y;
+                    s = s + v.z * v.z;
+                    s = s + v.w * v.w;
+                }
+            }
+            if (pt) red[t * 256 + tid] = s;
+        }
+        __syncthreads();
+        if (wave < TI) {
+            const float total = canonical_finish(red + wave * 256, lane);
+            if (lane == 0) sums[wave] = total;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int t = 0; t < TI; t++) {
+            const float inv = 1.0f / sqrtf(sums[t] / (float)K + f.eps);
+#pragma unroll
+            for (int j = 0; j < G4; j++) {
+                const int i = 4 * (tid + 256 * j);
+                if (pt && i < K) {
+                    if (DELTA && f.x_out && blockIdx.x == 0 && t < M)
+                        *reinterpret_cast<float4*>(f.x_out + (size_t)t * K + i) = xv[t][j];
+                    const float4 v = xv[t][j];
+                    xv[t][j] = make_float4((v.x * inv) * gv[j].x, (v.y * inv) * gv[j].y, (v.z * inv) * gv[j].z,
+                                           (v.w * inv) * gv[j].w);
+                    peak[t] = fmaxf(fmaxf(peak[t], fmaxf(fabsf(xv[t][j].x), fabsf(xv[t][j].y))),
+                                    fmaxf(fabsf(xv[t][j].z), fabsf(xv[t][j].w)));
+                }
+            }
+        }
+    } else {
+#pragma unroll
+        for (int t = 0; t < TI; t++) {
+#pragma unroll
+            for (int j = 0; j < G4; j++) {
+                if (4 * (tid + nt * j) < K) {
+                    if constexpr (KIND == kProSwiglu) {
+                        const float4 g = xv[t][j];
+                        const float4 u = dv[t][j];
+                        xv[t][j] = make_float4((g.x / (1.0f + exp_poly(-g.x))) * u.x, (g.y / (1.0f + exp_poly(-g.y))) * u.y,
+                                               (g.z / (1.0f + exp_poly(-g.z))) * u.z, (g.w / (1.0f + exp_poly(-g.w))) * u.w);
+                    }
+                    peak[t] = fmaxf(fmaxf(peak[t], fmaxf(fabsf(xv[t][j].x), fabsf(xv[t][j].y))),
+                                    fmaxf(fabsf(xv[t][j].z), fabsf(xv[t][j].w)));
+                }
+            }
+        }
+    }
+    // block max per row (order-free)
+#pragma unroll
+    for (int t = 0; t < TI; t++) {
+        const float v = wave_max(peak[t]);
+        if (lane == 0) wmax[t * 8 + wave] = v;
+    }
+    __syncthreads();
+    float qs[TI];
+#pragma unroll
+    for (int t = 0; t < TI; t++) {
+        float pk = wmax[t * 8];
+        for (int wv = 1; wv < nwaves; wv++) pk = fmaxf(pk, wmax[t * 8 + wv]);
+        const float scale = pk > 0.0f ? pk / 127.0f : 1.0f;
+        const float inverse = 1.0f / scale;
+        qs[t] = scale;
+#pragma unroll
+        for (int j = 0; j < G4; j++) {
+            const int i = 4 * (tid + nt * j);
+            if (tid < nt && i < K) {
+                const float4 h = xv[t][j];
+                const uint32_t b0 = (uint32_t)(ref_quantize_one(h.x, inverse) & 0xFF);
+                const uint32_t b1 = (uint32_t)(ref_quantize_one(h.y, inverse) & 0xFF);
+                const uint32_t b2 = (uint32_t)(ref_quantize_one(h.z, inverse) & 0xFF);
+                const uint32_t b3 = (uint32_t)(ref_quantize_one(h.w, inverse) & 0xFF);
+                *reinterpret_cast<uint32_t*>(qa + (size_t)t * K + i) = b0 | (b1 << 8) | (b2 << 16) | (b3 << 24);
+            }
         }
     }
     __syncthreads();
-    for (int x = threadIdx.x; x < M * 16; x += blockDim.x) {
-        const int t = x >> 4;
-        const int rr = x & 15;
-        const int nn = tile * 16 + rr;
-        const float4* row = reinterpret_cast<const float4*>(pl + (size_t)x * GS);
-        const int sw = WIDE ? (x & p.swz) : 0;
-        float acc = 0.0f;
-        float4 v[4];
-        const int full = G >> 4;  // chunks of 16 groups
-        if (full > 0) {
+    // 5. A operands from the quantized rows (token r%4, group g + r/4, k-slice kq)
+    if (active) {
+        long av[SETS];
+        const bool feeds = (r & 3) < M;
 #pragma unroll
-            for (int j = 0; j < 4; j++) v[j] = row[j ^ sw];
+        for (int c = 0; c < SETS; c++) {
+            const int g = min(g_first + 4 * c + (r >> 2), G - 1);
+            const long a = *reinterpret_cast<const long*>(qa + (size_t)(r & 3) * K + g * 32 + kq * 8);
+            av[c] = feeds ? a : 0;
         }
-        for (int ch = 0; ch < full; ch++) {
-            float4 nx[4];
-            const int nb = min(ch + 1, full - 1) * 4;
-#pragma unroll
-            for (int j = 0; j < 4; j++) nx[j] = row[(nb + j) ^ sw];
-#pragma unroll
-            for (int j = 0; j < 4; j++) {
-                acc = acc + v[j].x;
-                acc = acc + v[j].y;
-                acc = acc + v[j].z;
-                acc = acc + v[j].w;
-            }
-#pragma unroll
-            for (int j = 0; j < 4; j++) v[j] = nx[j];
-        }
-        const float* rowf = reinterpret_cast<const float*>(row);
-        for (int c = full * 16; c < G; c++) acc = acc + rowf[(((c >> 2) ^ sw) << 2) | (c & 3)];
-        if (nn >= p.row_start && nn < p.row_end) p.y[(size_t)t * p.ldy + nn] = acc;
+        narrow_products<CB, TI, false>(av, qs, hraw, w, pl, GS, M, g_first, r, kq);
     }
+    __syncthreads();
+    chain_products(pl, GS, 0, M, G, tile, p);
 }
 
 template <int CB, int TI, bool EXACT>
@@ -777,6 +983,34 @@ int32_t try_i8_decode(const DeviceWeights* w, MatmulParams& p, hipStream_t strea
                                  : launch_dec_ti<4, false>(p, waves, lds, stream);
     return w->special_scales ? launch_dec_ti<8, true>(p, waves, lds, stream)
                              : launch_dec_ti<8, false>(p, waves, lds, stream);
+}
+
+template <int CB, int KIND, bool DELTA, int G4>
+int32_t launch_fused_tpl(const MatmulParams& p, const DecodePrologue& f, int waves, size_t lds, hipStream_t stream)
+{
+    const int tiles = p.tile_end - p.tile_begin;
+    hipLaunchKernelGGL((matmul_i8_decode_fused_kernel<CB, KIND, DELTA, G4>), dim3(tiles), dim3(64 * waves), lds,
+                       stream, p, f);
+    NHIP_CHECK_HIP(hipGetLastError());
+    return NHIP_OK;
+}
+
+template <int CB, int G4>
+int32_t launch_fused_kind(const MatmulParams& p, const DecodePrologue& f, int waves, size_t lds, hipStream_t s)
+{
+    switch (f.kind) {
+        case kProNorm:
+            return f.delta ? launch_fused_tpl<CB, kProNorm, true, G4>(p, f, waves, lds, s)
+                           : launch_fused_tpl<CB, kProNorm, false, G4>(p, f, waves, lds, s);
+        case kProQuant: return launch_fused_tpl<CB, kProQuant, false, G4>(p, f, waves, lds, s);
+        default: return launch_fused_tpl<CB, kProSwiglu, false, G4>(p, f, waves, lds, s);
+    }
+}
+
+template <int CB>
+int32_t launch_fused_g4(const MatmulParams& p, const DecodePrologue& f, int waves, int g4, size_t lds, hipStream_t s)
+{
+    return g4 == 1 ? launch_fused_kind<CB, 1>(p, f, waves, lds, s) : launch_fused_kind<CB, 2>(p, f, waves, lds, s);
 }
 
 template <int CB, int NS, bool DOTS>
@@ -1094,6 +1328,54 @@ int32_t matmul_cq_internal(const DeviceWeights* w, const int8_t* values, const f
                            int32_t row_end, hipStream_t stream)
 {
     return run_matmul(w, values, scales, offsets, stride, tokens, y, ldy, row_start, row_end, nullptr, stream);
+}
+
+int32_t launch_decode_fused(const DeviceWeights* w, const DecodePrologue& f, int32_t tokens, float* y, int32_t ldy,
+                            hipStream_t stream)
+{
+    NHIP_REQUIRE(w && w->format == WeightFormat::Int8G32, "weights are not in the int8 format");
+    NHIP_REQUIRE(f.x && y && ldy >= w->rows, "fused matmul: null input/output or ldy %d < rows", ldy);
+    if (tokens < 1 || tokens > 4 || w->special_scales) return 1;
+    const int K = w->cols;
+    // waves: 4, or 8 when the (non-norm) prologue needs more threads; CB in
+    // {2, 4, 8} dividing the tile's blocks with at most `waves` waves busy
+    int waves = 4;
+    if (f.kind != kProNorm && K > 4 * 256 * 2) waves = 8;
+    const int nt = f.kind == kProNorm ? 256 : 64 * waves;
+    const int g4 = (K + 4 * nt - 1) / (4 * nt);
+    if (g4 > 2) return 1;
+    int cb = 0;
+    for (int c : {2, 4, 8}) {
+        if (w->blocks % c == 0 && w->blocks <= waves * c) {
+            cb = c;
+            break;
+        }
+    }
+    if (!cb) return 1;
+    MatmulParams p{};
+    p.tiles = w->tiles;
+    p.norms = w->norms;
+    p.y = y;
+    p.tokens = tokens;
+    p.cols = K;
+    p.groups = w->groups;
+    p.blocks = w->blocks;
+    p.groups_pad8 = w->groups_pad8;
+    p.ldy = ldy;
+    p.row_start = 0;
+    p.row_end = w->rows;
+    p.tile_begin = 0;
+    p.tile_end = w->tiles_n;
+    p.ldd = ((2 * w->blocks + 3) & ~3) + 4;
+    p.d_bytes = tokens * 16 * p.ldd * (int)sizeof(float);
+    p.st_bytes = (4 * K + 15) & ~15;
+    const size_t lds = (size_t)p.d_bytes + p.st_bytes + (4 * 256 + 4 + 4 * 8) * sizeof(float);
+    if (lds > kMaxLds) return 1;
+    int32_t rc = ensure_device();
+    if (rc) return rc;
+    if (cb == 2) return launch_fused_g4<2>(p, f, waves, g4, lds, stream);
+    if (cb == 4) return launch_fused_g4<4>(p, f, waves, g4, lds, stream);
+    return launch_fused_g4<8>(p, f, waves, g4, lds, stream);
 }
 
 int32_t weights_cq_create_internal(const nhip_cq* cq, nhip_weights** out)

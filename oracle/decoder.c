@@ -52,14 +52,24 @@ float or_log_poly(float x)
     return fmaf(fe, 0.693359375f, fmaf(fe, -2.12194440e-4f, r));
 }
 
-/* The canonical 256-way reduction: lane t adds its elements i = t, t+256,
- * ... in ascending i, then lanes are folded pairwise with strides 128, 64,
- * ..., 1 (s[t] = s[t] + s[t + stride]). */
-static float tree_fold(float* s)
+/* The canonical 256-way reduction of a row's terms: partial p[t] (t < 256)
+ * adds the terms of the elements i with (i / 4) % 256 == t in ascending i
+ * from +0 (CANON_LANE); q[m] (m < 16) = p[16m] + p[16m+1] + ... + p[16m+15]
+ * left to right; the total is q folded with strides 8, 4, 2, 1
+ * (q[m] = q[m] + q[m + stride]).  On the GPU lane t of a 256-thread block
+ * holds p[t], and the last two levels run in one 16-lane DPP row. */
+#define CANON_LANE(i) (((i) >> 2) & 255)
+
+static float tree_fold(const float* p)
 {
-    for (int stride = 128; stride > 0; stride >>= 1)
-        for (int t = 0; t < stride; t++) s[t] = s[t] + s[t + stride];
-    return s[0];
+    float q[16];
+    for (int m = 0; m < 16; m++) {
+        q[m] = p[16 * m];
+        for (int k = 1; k < 16; k++) q[m] = q[m] + p[16 * m + k];
+    }
+    for (int stride = 8; stride > 0; stride >>= 1)
+        for (int m = 0; m < stride; m++) q[m] = q[m] + q[m + stride];
+    return q[0];
 }
 
 /* x += delta (if given); h = (x * inv) * gain with inv = 1 / sqrt(ss / d +
@@ -71,7 +81,7 @@ float or_add_rmsnorm_quant(float* x, const float* delta, const float* gain, int 
     for (int t = 0; t < 256; t++) s[t] = 0.0f;
     if (delta)
         for (int i = 0; i < d; i++) x[i] = x[i] + delta[i];
-    for (int i = 0; i < d; i++) s[i & 255] = s[i & 255] + x[i] * x[i];
+    for (int i = 0; i < d; i++) s[CANON_LANE(i)] = s[CANON_LANE(i)] + x[i] * x[i];
     float ss = tree_fold(s);
     float inv = 1.0f / sqrtf(ss / (float)d + eps);
     for (int i = 0; i < d; i++) h[i] = (x[i] * inv) * gain[i];
@@ -137,7 +147,7 @@ void or_topk_lse(const float* x, int n, int k, int mask, int* idx, float* lp)
     for (int t = 0; t < 256; t++) s[t] = 0.0f;
     for (int i = 0; i < n; i++) {
         float v = mask && (i == 0 || i == 2 || i == 3) ? -1e30f : x[i];
-        s[i & 255] = s[i & 255] + or_exp_poly(v - peak);
+        s[CANON_LANE(i)] = s[CANON_LANE(i)] + or_exp_poly(v - peak);
     }
     float log_shift = peak + or_log_poly(tree_fold(s));
     for (int m = 0; m < k; m++) {

@@ -10,6 +10,7 @@ pytestmark = pytest.mark.gpu
 
 TINY = dict(layers=2, d=128, heads=2, kv_heads=2, head_dim=64, ffn=256, vocab=300, theta=10000.0, eps=1e-5)
 GQA = dict(layers=2, d=256, heads=6, kv_heads=2, head_dim=64, ffn=512, vocab=1000, theta=10000.0, eps=1e-5)
+ODD = dict(layers=1, d=96, heads=1, kv_heads=1, head_dim=64, ffn=160, vocab=301, theta=10000.0, eps=1e-5)
 WIDE = dict(layers=2, d=1024, heads=16, kv_heads=16, head_dim=64, ffn=4096, vocab=32000, theta=10000.0, eps=1e-5)
 
 
@@ -18,7 +19,7 @@ def bits(a):
 
 
 @pytest.mark.parametrize("max_chunks", [1, 64])
-@pytest.mark.parametrize("dims", [TINY, GQA], ids=["tiny", "gqa"])
+@pytest.mark.parametrize("dims", [TINY, GQA, ODD], ids=["tiny", "gqa", "odd"])
 def test_forward_bit_identical(hip, orc, dims, max_chunks):
     model = synthetic_model(dims, 7001)
     gpu = GpuDecoder(model, slots=4, capacity=64, max_rows=40, max_chunks=max_chunks)
