@@ -13,18 +13,22 @@
 //   fused  acc = fma(h(scale[n][g]), D_g, acc), y = acc * qscale[t] -- two
 //          VALU operations per (token, row, group) instead of four, within
 //          1e-4 of RMS(y) of the exact result.
-// The epilogue is VALU work on every (token, row, group) triple, which bounds
-// this kernel below the MFMA peak: the int8 MFMAs need 2*M*N*K / 5 POPS,
-// the epilogue M*N*K/32 triples x (2 or 4) operations at the VALU rate.
+// Two format limits bound this kernel below the int8 MFMA peak: a group of
+// 32 is one v_mfma_i32_16x16x32_i8 (16 cycles on gfx950, half the rate of
+// the K=64 int8 instruction, whose sum would span two groups of different
+// scales), and the epilogue is VALU work on every (token, row, group)
+// triple, M*N*K/32 x (2 or 4) operations at the VALU rate.  Each stage is
+// software-pipelined: group k+1's MFMAs and group k+2's LDS reads are in
+// flight while group k's epilogue runs.
 // Weights are the same re-tiled 1 KB blocks as the decode kernels (one
 // dwordx4 per lane is the B operand of two groups), loaded by each wave for
 // its own tiles.  Activations go through LDS: per stage of 4 blocks (256 K
-// elements) the 256 threads load 64 tokens x 256 bytes with row-contiguous
-// 16-byte loads (1 KB per wave instruction) and store them in MFMA fragment
-// order, so every A operand is one conflict-free ds_read_b64 (8-byte A
-// fragments loaded straight from rows 2 KB apart were the bottleneck).  The
-// LDS stage is double-buffered: the next stage's activations, weights and
-// scales are in flight while the current one is multiplied.
+// elements) the threads load 64 tokens x 256 bytes in 16-byte units and
+// store each unit with one 16-byte write into an order in which every MFMA
+// A operand is one conflict-free ds_read_b64 and every wave's writes are
+// contiguous.  The LDS stage is double-buffered: the next stage's
+// activations, weights and scales are in flight while the current one is
+// multiplied.
 #include <algorithm>
 
 #include "common.hpp"
@@ -38,7 +42,8 @@ typedef unsigned int u4 __attribute__((ext_vector_type(4)));
 constexpr int kTokensPerBlock = 64;
 constexpr int kTilesPerBlock = 8;  // 16-row tiles per workgroup (2 per wave)
 constexpr int kStage = 4;          // weight blocks (2 groups each) per pipeline stage
-constexpr int kStageLds = kStage * 2 * 4 * 64 * 8;  // A fragments of one stage: 16 KB
+constexpr int kSubtileSlots = 66;  // 8-byte slots per (group, subtile) block: 64 + 2 of padding
+constexpr int kStageLds = kStage * 2 * 4 * kSubtileSlots * 8;  // A fragments of one stage (16.5 KB)
 
 struct GemmParams {
     const uint8_t* tiles;
@@ -50,28 +55,35 @@ struct GemmParams {
     int32_t row_start, row_end, tile_begin, tile_end;
 };
 
+template <int TPW>
 struct WStage {
-    u4 w[kStage][2];  // weight blocks of the wave's two tiles
-    uint4 s[2];       // fp16 scales of the stage's 8 groups, per tile row
+    u4 w[kStage][TPW];  // weight blocks of the wave's tiles
+    uint4 s[TPW];       // fp16 scales of the stage's 8 groups, per tile row
 };
 
-template <bool EXACT, bool SPECIAL>
-__global__ __launch_bounds__(256) void gemm_i8_kernel(GemmParams p)
+// WAVES waves per workgroup, each owning TPW = 8 / WAVES 16-row tiles (four
+// waves of two tiles measured fastest: eight waves of one tile read the
+// A operands twice as often).
+template <bool EXACT, bool SPECIAL, int WAVES>
+__device__ __forceinline__ void gemm_i8_body(const GemmParams& p)
 {
-    __shared__ __align__(16) uint2 afrag[2][kStageLds / 8];  // [buf][block][h][subtile][lane]
+    constexpr int TPW = kTilesPerBlock / WAVES;
+    constexpr int NT = 64 * WAVES;           // threads
+    constexpr int AU = 1024 / NT;            // 16-byte activation units per thread and stage
+    __shared__ __align__(16) uint2 afrag[2][kStageLds / 8];  // [buf][group][subtile][token][kq]
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
     const int r = lane & 15;
     const int kq = lane >> 4;
     const int t0 = blockIdx.y * kTokensPerBlock;
-    const int tile0 = p.tile_begin + blockIdx.x * kTilesPerBlock + wave * 2;
+    const int tile0 = p.tile_begin + blockIdx.x * kTilesPerBlock + wave * TPW;
     const int stages = (p.blocks + kStage - 1) / kStage;
 
-    const u4* wbase[2];
-    const uint16_t* nrow[2];
+    const u4* wbase[TPW];
+    const uint16_t* nrow[TPW];
 #pragma unroll
-    for (int j = 0; j < 2; j++) {
+    for (int j = 0; j < TPW; j++) {
         const int tj = min(tile0 + j, p.tile_end - 1);
         wbase[j] = reinterpret_cast<const u4*>(p.tiles) + (size_t)tj * p.blocks * 64 + lane;
         nrow[j] = p.norms + (size_t)(tj * 16 + r) * p.groups_pad8;
@@ -82,114 +94,130 @@ __global__ __launch_bounds__(256) void gemm_i8_kernel(GemmParams p)
 #pragma unroll
         for (int e = 0; e < 4; e++) qs[i][e] = p.qscale[min(t0 + 16 * i + 4 * kq + e, p.tokens - 1)];
 
-    // activation staging: 16-byte unit u = j*256 + tid of a stage is token
-    // u/16, bytes 16*(u%16) .. of the stage's 256-byte K slice
-    auto load_a = [&](uint4 (&av)[4], int st) {
+    // activation staging: 16-byte unit u = j*NT + tid of a stage is token
+    // 16*i + t16 (t16 = u%16, i = (u/32)%4), bytes 32*gs + 16*p (p = (u/16)%2,
+    // gs = u/128: group within the stage) of the stage's 256-byte K slice.
+    // LDS order [gs][i][t16][kq] (8 bytes each, each (gs, i) block padded to
+    // 528 bytes so that the paired reads of subtiles i and i+1 fall on
+    // different banks): the unit is k-slices 2p and 2p+1, one 16-byte write,
+    // and lane (t16, kq) of an MFMA reads its A operand from 512 contiguous
+    // bytes.
+    auto load_a = [&](uint4 (&av)[AU], int st) {
 #pragma unroll
-        for (int j = 0; j < 4; j++) {
-            const int u = j * 256 + tid;
-            const int t = min(t0 + (u >> 4), p.tokens - 1);
-            const int kb = min(st * kStage * 64 + 16 * (u & 15), p.cols - 16);  // past K only in the padded group
+        for (int j = 0; j < AU; j++) {
+            const int u = j * NT + tid;
+            const int t = min(t0 + ((u >> 5) & 3) * 16 + (u & 15), p.tokens - 1);
+            const int kb = min(st * kStage * 64 + 32 * (u >> 7) + 16 * ((u >> 4) & 1), p.cols - 16);  // past K only in the padded group
             av[j] = *reinterpret_cast<const uint4*>(p.q + (size_t)t * p.cols + kb);
         }
     };
-    auto store_a = [&](const uint4 (&av)[4], int buf) {
+    auto store_a = [&](const uint4 (&av)[AU], int buf) {
 #pragma unroll
-        for (int j = 0; j < 4; j++) {
-            const int u = j * 256 + tid;
-            const int tl = u >> 4;  // token within the block of 64
-            const int c = u & 15;   // 16-byte chunk: block c/4, group (c%4)/2, kq 2*(c%2), +1
-            const int base = (((c >> 2) * 2 + ((c & 3) >> 1)) * 4 + (tl >> 4)) * 64 + (tl & 15);
-            const int k0 = 2 * (c & 1);
-            afrag[buf][base + 16 * k0] = make_uint2(av[j].x, av[j].y);
-            afrag[buf][base + 16 * (k0 + 1)] = make_uint2(av[j].z, av[j].w);
+        for (int j = 0; j < AU; j++) {
+            const int u = j * NT + tid;
+            const int slot = ((u >> 7) * 4 + ((u >> 5) & 3)) * kSubtileSlots + (u & 15) * 4 + 2 * ((u >> 4) & 1);
+            *reinterpret_cast<uint4*>(&afrag[buf][slot]) = av[j];
         }
     };
-    auto load_w = [&](WStage& ws, int st) {
+    auto load_w = [&](WStage<TPW>& ws, int st) {
 #pragma unroll
         for (int b = 0; b < kStage; b++)
 #pragma unroll
-            for (int j = 0; j < 2; j++)
+            for (int j = 0; j < TPW; j++)
                 ws.w[b][j] = wbase[j][(size_t)min(st * kStage + b, p.blocks - 1) * 64];  // cached: 8 token blocks share it
 #pragma unroll
-        for (int j = 0; j < 2; j++) ws.s[j] = *reinterpret_cast<const uint4*>(nrow[j] + st * kStage * 2);
+        for (int j = 0; j < TPW; j++) ws.s[j] = *reinterpret_cast<const uint4*>(nrow[j] + st * kStage * 2);
     };
 
-    float acc[2][4][4];
+    float acc[TPW][4][4];
 #pragma unroll
-    for (int j = 0; j < 2; j++)
+    for (int j = 0; j < TPW; j++)
 #pragma unroll
         for (int i = 0; i < 4; i++)
 #pragma unroll
             for (int e = 0; e < 4; e++) acc[j][i][e] = 0.0f;
 
-    auto compute = [&](const WStage& ws, int buf, int st) {
+    // one stage: group k's A operands (four 16-token subtiles), its MFMAs
+    // and its epilogue, software-pipelined so that group k+1's MFMAs and
+    // group k+2's LDS reads are in flight during group k's epilogue
+    auto read_a = [&](long (&av)[4], int buf, int k) {
 #pragma unroll
-        for (int b = 0; b < kStage; b++) {
-            if (st * kStage + b >= p.blocks) break;  // uniform
+        for (int i = 0; i < 4; i++) {
+            const uint2 f = afrag[buf][(k * 4 + i) * kSubtileSlots + r * 4 + kq];
+            av[i] = (long)(((uint64_t)f.y << 32) | f.x);
+        }
+    };
+    auto issue = [&](v4i (&d)[TPW][4], const long (&av)[4], const WStage<TPW>& ws, int k) {
+        const v4i zero = {0, 0, 0, 0};
 #pragma unroll
-            for (int h = 0; h < 2; h++) {
-                long av[4];
+        for (int j = 0; j < TPW; j++) {
+            const u4& wc = ws.w[k >> 1][j];
+            const long bop = (k & 1) ? (long)(((uint64_t)wc.w << 32) | wc.z) : (long)(((uint64_t)wc.y << 32) | wc.x);
 #pragma unroll
-                for (int i = 0; i < 4; i++) {
-                    const uint2 f = afrag[buf][((b * 2 + h) * 4 + i) * 64 + lane];
-                    av[i] = (long)(((uint64_t)f.y << 32) | f.x);
-                }
-                const int g8 = b * 2 + h;  // group within the stage's 8
+            for (int i = 0; i < 4; i++) d[j][i] = __builtin_amdgcn_mfma_i32_16x16x32_i8(av[i], bop, zero, 0, 0, 0);
+        }
+    };
+    auto epilogue = [&](const v4i (&d)[TPW][4], const WStage<TPW>& ws, int k) {
 #pragma unroll
-                for (int j = 0; j < 2; j++) {
-                    const u4& wc = ws.w[b][j];
-                    const long bop = h ? (long)(((uint64_t)wc.w << 32) | wc.z) : (long)(((uint64_t)wc.y << 32) | wc.x);
-                    const uint4 s4 = ws.s[j];
-                    const uint32_t word = g8 < 4 ? (g8 < 2 ? s4.x : s4.y) : (g8 < 6 ? s4.z : s4.w);
-                    const uint32_t hbits = (g8 & 1) ? (word >> 16) : (word & 0xFFFFu);
-                    float hs;
-                    if constexpr (SPECIAL)
-                        hs = ref_half_to_single(hbits);
+        for (int j = 0; j < TPW; j++) {
+            const uint4 s4 = ws.s[j];
+            const uint32_t word = k < 4 ? (k < 2 ? s4.x : s4.y) : (k < 6 ? s4.z : s4.w);
+            const uint32_t hbits = (k & 1) ? (word >> 16) : (word & 0xFFFFu);
+            float hs;
+            if constexpr (SPECIAL)
+                hs = ref_half_to_single(hbits);
+            else
+                hs = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(hbits)));
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    const float df = static_cast<float>(d[j][i][e]);
+                    if constexpr (EXACT)
+                        acc[j][i][e] = acc[j][i][e] + (hs * qs[i][e]) * df;
                     else
-                        hs = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(hbits)));
-#pragma unroll
-                    for (int i = 0; i < 4; i++) {
-                        const v4i zero = {0, 0, 0, 0};
-                        const v4i d = __builtin_amdgcn_mfma_i32_16x16x32_i8(av[i], bop, zero, 0, 0, 0);
-#pragma unroll
-                        for (int e = 0; e < 4; e++) {
-                            const float df = static_cast<float>(d[e]);
-                            if constexpr (EXACT)
-                                acc[j][i][e] = acc[j][i][e] + (hs * qs[i][e]) * df;
-                            else
-                                acc[j][i][e] = __builtin_fmaf(hs, df, acc[j][i][e]);
-                        }
-                    }
+                        acc[j][i][e] = __builtin_fmaf(hs, df, acc[j][i][e]);
                 }
-            }
+        }
+    };
+    constexpr int KG = 2 * kStage;  // groups per stage
+    auto compute = [&](const WStage<TPW>& ws, int buf, int st) {
+        long aa[2][4];
+        v4i dd[2][TPW][4];
+        read_a(aa[0], buf, 0);
+        read_a(aa[1], buf, 1);
+        issue(dd[0], aa[0], ws, 0);
+#pragma unroll
+        for (int k = 0; k < KG; k++) {
+            if (k + 1 < KG) issue(dd[(k + 1) & 1], aa[(k + 1) & 1], ws, k + 1);
+            if (k + 2 < KG) read_a(aa[k & 1], buf, k + 2);
+            // groups past the last block (a partial last stage) are computed
+            // on clamped operands and dropped here
+            if (st * kStage + (k >> 1) < p.blocks) epilogue(dd[k & 1], ws, k);
         }
     };
 
-    // pipeline: stage st+1's loads are in flight while stage st is multiplied
-    uint4 areg[4];
-    WStage wcur, wnext;
+    // pipeline: stage st+1's loads are in flight while stage st is
+    // multiplied (the last iteration reloads the last stage, unused)
+    uint4 areg[AU];
+    WStage<TPW> wcur, wnext;
     load_a(areg, 0);
     load_w(wcur, 0);
     store_a(areg, 0);
     __syncthreads();
     for (int st = 0; st < stages; st++) {
         const int buf = st & 1;
-        const bool more = st + 1 < stages;
-        if (more) {
-            load_a(areg, st + 1);
-            load_w(wnext, st + 1);
-        }
+        const int nst = min(st + 1, stages - 1);
+        load_a(areg, nst);
+        load_w(wnext, nst);
         compute(wcur, buf, st);
-        if (more) {
-            store_a(areg, buf ^ 1);  // that buffer was last read two stages ago
-            wcur = wnext;
-        }
+        store_a(areg, buf ^ 1);  // that buffer was last read two stages ago
+        wcur = wnext;
         __syncthreads();
     }
 
 #pragma unroll
-    for (int j = 0; j < 2; j++) {
+    for (int j = 0; j < TPW; j++) {
         const int n = (tile0 + j) * 16 + r;
         if (tile0 + j >= p.tile_end || n < p.row_start || n >= p.row_end) continue;
 #pragma unroll
@@ -200,6 +228,12 @@ __global__ __launch_bounds__(256) void gemm_i8_kernel(GemmParams p)
                 if (t < p.tokens) p.y[(size_t)t * p.ldy + n] = EXACT ? acc[j][i][e] : acc[j][i][e] * qs[i][e];
             }
     }
+}
+
+template <bool EXACT, bool SPECIAL>
+__global__ __launch_bounds__(256) void gemm_i8_kernel(GemmParams p)
+{
+    gemm_i8_body<EXACT, SPECIAL, 4>(p);
 }
 
 template <bool EXACT>
