@@ -55,6 +55,34 @@ struct DecodeAttnParams {
     float inv_sqrt;
 };
 
+}  // namespace
+
+// Longest chunk of the plan: at most 32 positions below 16*max_chunks
+// positions, else ceil(capacity/max_chunks) rounded up to 4.
+int decode_attention_lmax(int capacity, int max_chunks)
+{
+    return std::max(32, ((capacity + max_chunks - 1) / max_chunks + 3) & ~3);
+}
+
+// LDS of the chunk kernel: query heads, scores / weights / value scales per
+// head and position of a block, its peaks and query scales.
+size_t decode_attention_lds(int lmax, int kv_per_block, int group)
+{
+    return kMaxHeadsPerBlock * 64 + (size_t)3 * kv_per_block * group * lmax * sizeof(float) +
+           2 * kMaxHeadsPerBlock * sizeof(float);
+}
+
+// KV heads per workgroup: whole groups of at most 16 query heads, fewer when
+// a block's scores would not fit in 64 KB of LDS (0: none fit).
+int decode_attention_kv_per_block(int group, int kv_heads, int lmax)
+{
+    int kv = std::min(std::max(1, kMaxHeadsPerBlock / group), kv_heads);
+    while (kv > 0 && decode_attention_lds(lmax, kv, group) > 64 * 1024) kv--;
+    return kv;
+}
+
+namespace {
+
 // The reference's chunk plan (Blocks.cs:934-938).
 __device__ __forceinline__ int plan(int count, int max_chunks, int* length)
 {
@@ -102,11 +130,12 @@ __global__ __launch_bounds__(kThreads) void decode_attention_kernel(DecodeAttnPa
     const int nh = nkv * group;  // <= 16
     const int lmax = p.lmax;
 
+    const int hmax = p.kv_per_block * group;                                // heads of a full block
     int8_t* q_lds = reinterpret_cast<int8_t*>(lds);                        // [16][64]
-    float* score = reinterpret_cast<float*>(lds + kMaxHeadsPerBlock * 64);  // [16][lmax], then e_s
-    float* vsc = score + kMaxHeadsPerBlock * lmax;                          // [16 kv][lmax]
-    float* wl = vsc + kMaxHeadsPerBlock * lmax;                             // [16][lmax] e_s * valueScale_s
-    float* qs_lds = wl + kMaxHeadsPerBlock * lmax;                          // [16]
+    float* score = reinterpret_cast<float*>(lds + kMaxHeadsPerBlock * 64);  // [hmax][lmax], then e_s
+    float* vsc = score + hmax * lmax;                                       // [kv][lmax]
+    float* wl = vsc + hmax * lmax;                                          // [hmax][lmax] e_s * valueScale_s
+    float* qs_lds = wl + hmax * lmax;                                       // [16]
     uint32_t* peak_key = reinterpret_cast<uint32_t*>(qs_lds + kMaxHeadsPerBlock);  // [16]
 
     const int slot = p.row_slot[row];
@@ -162,20 +191,21 @@ __global__ __launch_bounds__(kThreads) void decode_attention_kernel(DecodeAttnPa
     const int qslot = min(lslot, pieces - 1);
     const uint32_t mag_kv = magic((uint32_t)nkv);
     const uint32_t mag_l = magic((uint32_t)L);
+    const float* sbase = (lslot & 1) ? p.vscale : p.kscale;  // slot 0 the key scale, slot 1 the value scale
     constexpr int KU = 8;  // units per thread per pass, loads issued together
     auto pass = [&](int base) {
         uint4 kw[KU];
-        float ksv[KU], vsv[KU];
+        float sv[KU];
 #pragma unroll
         for (int k = 0; k < KU; k++) {
+            if (base + k * kThreads >= units) break;  // uniform: no duplicate loads
             const int u = min(base + k * kThreads + tid, units - 1);
             const int w = u >> 2;
             const int s = fast_div(w, mag_kv);
             const int kvl = w - s * nkv;
             const size_t cell = (pos0 + s) * p.kv_heads + kv0 + kvl;
             kw[k] = *reinterpret_cast<const uint4*>(p.keys + cell * qk + 16 * qslot);
-            ksv[k] = p.kscale[cell];
-            vsv[k] = p.vscale[cell];
+            sv[k] = sbase[cell];
         }
         if (base == 0) {  // stage the query heads and scales behind the first loads
             if (tid < nh * q4) reinterpret_cast<uint32_t*>(q_lds)[(tid / q4) * 16 + (tid % q4)] = qword;
@@ -207,12 +237,12 @@ __global__ __launch_bounds__(kThreads) void decode_attention_kernel(DecodeAttnPa
                 part += __builtin_amdgcn_mov_dpp(part, 0xB1, 0xF, 0xF, false);
                 part += __builtin_amdgcn_mov_dpp(part, 0x4E, 0xF, 0xF, false);
                 if (ok && lslot == 0) {
-                    const float sc = (static_cast<float>(part) * ksv[k]) * qs_lds[hl];
+                    const float sc = (static_cast<float>(part) * sv[k]) * qs_lds[hl];
                     score[hl * lmax + s] = sc;
                     atomicMax(&peak_key[hl], order_key(sc));  // the chunk peak (max is order-free)
                 }
             }
-            if (ok && lslot == 1) vsc[kvl * lmax + s] = vsv[k];
+            if (ok && lslot == 1) vsc[kvl * lmax + s] = sv[k];
         }
     };
     pass(0);  // peeled: the common case (units <= KU * 256) is straight-line code
@@ -308,16 +338,17 @@ __global__ __launch_bounds__(kThreads) void decode_attention_kernel(DecodeAttnPa
 }
 
 // Merge of a (row, head)'s chunk partials, one workgroup of 64 threads
-// (one per dim): MergePartials' non-SIMD order (Blocks.cs:760-815); the
-// thread's chunk values are loaded together before the ascending-order chain.
+// (one per dim): MergePartials' non-SIMD order (Blocks.cs:760-815).  Every
+// load is issued first; thread c (< needed) holds chunk c's peak and sum;
+// after one barrier every thread walks the chunks in ascending order with
+// two independent chains, the total (the same in every thread) and its own
+// dim's weighted sum.
 constexpr int kMergeBatch = 64;
 
 __global__ __launch_bounds__(64) void decode_merge_kernel(DecodeAttnParams p)
 {
-    __shared__ float mpk[256];
     __shared__ float msm[256];
     __shared__ float wts[256];
-    __shared__ float inv_lds;
     const int row = blockIdx.x;
     const int h = blockIdx.y;
     const int d = threadIdx.x;
@@ -333,61 +364,74 @@ __global__ __launch_bounds__(64) void decode_merge_kernel(DecodeAttnParams p)
     const size_t rbase = (size_t)row * p.max_chunks * p.heads + h;  // + c * heads
     const float* part = p.partials + rbase * 64 + d;
     const size_t cstride = (size_t)p.heads * 64;
+    // this thread's chunks' peaks and sums (c = d, d + 64, ...; needed <= 256)
+    float pk[4], sm[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const int c = min(d + 64 * j, needed - 1);
+        pk[j] = p.peaks[rbase + (size_t)c * p.heads];
+        sm[j] = p.sums[rbase + (size_t)c * p.heads];
+    }
     float a[kMergeBatch];
 #pragma unroll
     for (int j = 0; j < kMergeBatch; j++) a[j] = part[(size_t)min(j, needed - 1) * cstride];
-    for (int c = d; c < needed; c += 64) {
-        mpk[c] = p.peaks[rbase + (size_t)c * p.heads];
-        msm[c] = p.sums[rbase + (size_t)c * p.heads];
-    }
-    __syncthreads();
-    if (needed == 2) {  // uniform over the block
-        const float peak0 = mpk[0], peak1 = mpk[1];
-        const float pk = ref_max(peak0, peak1);
-        const float w0 = exp_poly(peak0 - pk);
-        const float w1 = exp_poly(peak1 - pk);
+    if (needed == 2) {  // uniform over the block: MergePartials' two-chunk branch
+        const float peak0 = __shfl(pk[0], 0), peak1 = __shfl(pk[0], 1);
+        const float sum0 = __shfl(sm[0], 0), sum1 = __shfl(sm[0], 1);
+        const float peak = ref_max(peak0, peak1);
+        const float w0 = exp_poly(peak0 - peak);
+        const float w1 = exp_poly(peak1 - peak);
         float tot = 0.0f;
-        tot = tot + w0 * msm[0];
-        tot = tot + w1 * msm[1];
+        tot = tot + w0 * sum0;
+        tot = tot + w1 * sum1;
         const float inv = 1.0f / tot;
         *dst = (w0 * a[0] + w1 * a[1]) * inv;
         return;
     }
-    // w_c = Exp(peak_c - peak); the peak by a wave reduction (max is
-    // order-independent), the total in ascending c by thread 0
+    // peak = the largest chunk peak (order-free)
     float peak = -INFINITY;
-    for (int c = d; c < needed; c += 64) peak = ref_max(peak, mpk[c]);
-    for (int off = 32; off > 0; off >>= 1) peak = ref_max(peak, __shfl_xor(peak, off));
-    for (int c = d; c < needed; c += 64) wts[c] = exp_poly(mpk[c] - peak);
-    __syncthreads();
-    if (d == 0) {
-        float total = 0.0f;
-        for (int c0 = 0; c0 < needed; c0 += 8) {
-            float w8[8], s8[8];
 #pragma unroll
-            for (int j = 0; j < 8; j++) {
-                const int c = min(c0 + j, needed - 1);
-                w8[j] = wts[c];
-                s8[j] = msm[c];
-            }
+    for (int j = 0; j < 4; j++)
+        if (d + 64 * j < needed) peak = ref_max(peak, pk[j]);
+    peak = wave_max(peak);
 #pragma unroll
-            for (int j = 0; j < 8; j++)
-                if (c0 + j < needed) total = total + w8[j] * s8[j];
+    for (int j = 0; j < 4; j++) {
+        const int c = d + 64 * j;
+        if (c < needed) {
+            wts[c] = exp_poly(pk[j] - peak);
+            msm[c] = sm[j];
         }
-        inv_lds = 1.0f / total;
     }
     __syncthreads();
-    float sum = 0.0f;
+    float total = 0.0f, sum = 0.0f;
     for (int c0 = 0; c0 < needed; c0 += kMergeBatch) {
         if (c0 > 0) {
 #pragma unroll
             for (int j = 0; j < kMergeBatch; j++) a[j] = part[(size_t)min(c0 + j, needed - 1) * cstride];
         }
 #pragma unroll
-        for (int j = 0; j < kMergeBatch; j++)
-            if (c0 + j < needed) sum = sum + wts[c0 + j] * a[j];
+        for (int j = 0; j < kMergeBatch; j += 4) {
+            if (c0 + j >= needed) break;  // uniform
+            const float4 w4 = *reinterpret_cast<const float4*>(wts + c0 + j);
+            const float4 s4 = *reinterpret_cast<const float4*>(msm + c0 + j);
+            const int rem = needed - (c0 + j);
+            total = total + w4.x * s4.x;
+            sum = sum + w4.x * a[j];
+            if (rem > 1) {
+                total = total + w4.y * s4.y;
+                sum = sum + w4.y * a[j + 1];
+            }
+            if (rem > 2) {
+                total = total + w4.z * s4.z;
+                sum = sum + w4.z * a[j + 2];
+            }
+            if (rem > 3) {
+                total = total + w4.w * s4.w;
+                sum = sum + w4.w * a[j + 3];
+            }
+        }
     }
-    *dst = sum * inv_lds;
+    *dst = sum * (1.0f / total);
 }
 
 __global__ void zero_kernel(uint32_t* p, size_t n)
@@ -447,12 +491,11 @@ int32_t attention_decode_impl(const int8_t* d_q, const float* d_qscale, int32_t 
     const WorkspaceLayout wl = layout(rows, heads, max_chunks);
     NHIP_REQUIRE(workspace_bytes >= wl.total, "attention: workspace of %zu bytes, need %zu", workspace_bytes,
                  wl.total);
-    // longest chunk: <= 32 below 16*max_chunks positions, else ceil(capacity/max_chunks) rounded up to 4
-    const int lmax = std::max(32, ((capacity + max_chunks - 1) / max_chunks + 3) & ~3);
-    const size_t lds = kMaxHeadsPerBlock * 64 + (size_t)3 * kMaxHeadsPerBlock * lmax * sizeof(float) +
-                       2 * kMaxHeadsPerBlock * sizeof(float);
-    NHIP_REQUIRE(lds <= 64 * 1024, "attention: chunks of up to %d positions need %zu bytes of LDS; raise "
-                 "max_chunks", lmax, lds);
+    const int lmax = decode_attention_lmax(capacity, max_chunks);
+    const int kv_per_block = decode_attention_kv_per_block(group, kv_heads, lmax);
+    NHIP_REQUIRE(kv_per_block > 0, "attention: chunks of up to %d positions do not fit in LDS; raise max_chunks",
+                 lmax);
+    const size_t lds = decode_attention_lds(lmax, kv_per_block, group);
     int32_t rc = ensure_device();
     if (rc) return rc;
     DecodeAttnParams p{};
@@ -480,7 +523,7 @@ int32_t attention_decode_impl(const int8_t* d_q, const float* d_qscale, int32_t 
     p.capacity = capacity;
     p.max_chunks = max_chunks;
     p.lmax = lmax;
-    p.kv_per_block = std::max(1, kMaxHeadsPerBlock / group);
+    p.kv_per_block = kv_per_block;
     p.inv_sqrt = static_cast<float>(1.0 / std::sqrt(static_cast<double>(qk_dim)));
     const int head_blocks = (kv_heads + p.kv_per_block - 1) / p.kv_per_block;
     NHIP_REQUIRE(!d_q_out || (d_qs_out && max_chunks == 1 && head_blocks == 1),

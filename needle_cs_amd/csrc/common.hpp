@@ -100,6 +100,11 @@ struct DecodePrologue {
 };
 int32_t launch_decode_fused(const DeviceWeights* w, const DecodePrologue& f, int32_t tokens, float* y, int32_t ldy,
                             hipStream_t stream);
+// Chunk-kernel geometry of attention_decode_impl: the longest chunk of the
+// plan, and the kv heads per workgroup (0 when a chunk does not fit in LDS);
+// a quantized output needs every head in one workgroup.
+int decode_attention_lmax(int capacity, int max_chunks);
+int decode_attention_kv_per_block(int group, int kv_heads, int lmax);
 // Token count from which literal int8 matmuls use the prefill kernel.
 constexpr int32_t kGemmMinTokens = 32;
 }  // namespace nhip

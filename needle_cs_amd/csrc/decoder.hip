@@ -563,8 +563,11 @@ int32_t enqueue_forward(nhip_decoder* m, int rows, int k)
         pp.capacity = D.capacity;
         hipLaunchKernelGGL(qkv_post_kernel, dim3(rows, H + 2 * KV), dim3(64), 0, s, pp);
         NHIP_CHECK_HIP(hipGetLastError());
-        // single-chunk attention over all heads also quantizes its output rows
-        const bool attn_quant = D.max_chunks == 1 && H <= 16;
+        // single-chunk attention with every head in one workgroup also
+        // quantizes its output rows
+        const bool attn_quant =
+            D.max_chunks == 1 &&
+            decode_attention_kv_per_block(H / KV, KV, decode_attention_lmax(D.capacity, D.max_chunks)) >= KV;
         rc = attention_decode_impl(m->qh, m->qhs, rows, H, KV, 64, pp.keys, pp.key_scales, pp.values,
                                    pp.value_scales, D.slots, D.capacity, in_slots(m, m->d_in), in_first(m, m->d_in),
                                    in_count(m, m->d_in), D.max_chunks, m->attn_ws, m->attn_ws_bytes, m->att,

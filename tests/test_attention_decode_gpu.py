@@ -137,6 +137,8 @@ def test_decode_attention_rejects_bad_shapes(hip, orc):
     p = buf.ptr
     assert lib.nhip_attention_decode_dev(p, p, 1, 6, 4, 64, p, p, p, p, 1, 16, p, p, p, 8, p, buf.nbytes, p, None) != 0
     assert lib.nhip_attention_decode_dev(p, p, 1, 4, 4, 32, p, p, p, p, 1, 16, p, p, p, 8, p, buf.nbytes, p, None) != 0
-    assert lib.nhip_attention_decode_dev(p, p, 1, 4, 4, 64, p, p, p, p, 1, 8192, p, p, p, 8, p, buf.nbytes, p,
+    # chunks of 8192 positions: even one kv head per workgroup exceeds LDS,
+    # so the call is rejected before any launch
+    assert lib.nhip_attention_decode_dev(p, p, 1, 4, 4, 64, p, p, p, p, 1, 65536, p, p, p, 8, p, buf.nbytes, p,
                                          None) != 0
     assert "max_chunks" in hip.last_error()
