@@ -85,11 +85,10 @@ int32_t attention_decode_impl(const int8_t* d_q, const float* d_qscale, int32_t 
 // activation rows are computed in the kernel's prologue from fp32 inputs
 // (gemv.hip): kProNorm = x (+ delta) -> RMSNorm * gain -> QuantizeInt8,
 // workgroup 0 writing x + delta to x_out when both are given; kProQuant =
-// QuantizeInt8(x); kProSwiglu = QuantizeInt8((g / (1 + Exp(-g))) * u) with
-// x = [g | u] rows of 2K.  Returns 1 (nothing launched) when the shape does
-// not fit the kernel; the caller then runs the element-wise kernel and the
+// QuantizeInt8(x).  Returns 1 (nothing launched) when the shape does not
+// fit the kernel; the caller then runs the element-wise kernel and the
 // plain matmul.
-enum : int32_t { kProNorm = 1, kProQuant = 2, kProSwiglu = 3 };
+enum : int32_t { kProNorm = 1, kProQuant = 2 };
 struct DecodePrologue {
     int32_t kind;
     const float* x;
@@ -97,6 +96,10 @@ struct DecodePrologue {
     float* x_out;
     const float* gain;
     float eps;
+    // nonzero: the weight rows are (8 gate rows, the 8 matching up rows) per
+    // 16-row tile and the kernel stores a = (g / (1 + Exp(-g))) * u at
+    // y[t][8*tile + r] (rows/2 outputs per token) instead of the rows
+    int32_t swiglu;
 };
 int32_t launch_decode_fused(const DeviceWeights* w, const DecodePrologue& f, int32_t tokens, float* y, int32_t ldy,
                             hipStream_t stream);

@@ -214,20 +214,22 @@ __global__ __launch_bounds__(64) void qkv_post_kernel(PostParams p)
     if (e == 0) (key ? p.key_scales : p.value_scales)[cell] = scale;
 }
 
-// a = (g / (1 + Exp(-g))) * u, then QuantizeInt8(a).  Thread t holds the
-// float4 groups at 4t + 1024j (ffn a multiple of 4, at most 4096).
+// a = (g / (1 + Exp(-g))) * u, then QuantizeInt8(a).  The gate/up outputs
+// are tile-interleaved (gate j at 16*(j/8) + j%8, up j eight further on).
+// Thread t holds the float4 groups at 4t + 1024j (ffn a multiple of 8, at
+// most 4096).
 __global__ __launch_bounds__(kThreads) void swiglu_quant_kernel(const float* gu, int ffn, int8_t* q, float* qscale)
 {
     __shared__ float wmax[4];
     const int t = threadIdx.x;
-    const float* g = gu + (size_t)blockIdx.x * 2 * ffn;
-    const float* up = g + ffn;
+    const float* row = gu + (size_t)blockIdx.x * 2 * ffn;
     float4 v[kGroups4], uv[kGroups4];
 #pragma unroll
     for (int j = 0; j < kGroups4; j++) {  // every load first
         const int i = min(4 * t + 1024 * j, ffn - 4);
-        v[j] = *reinterpret_cast<const float4*>(g + i);
-        uv[j] = *reinterpret_cast<const float4*>(up + i);
+        const int gi = 16 * (i >> 3) + (i & 7);
+        v[j] = *reinterpret_cast<const float4*>(row + gi);
+        uv[j] = *reinterpret_cast<const float4*>(row + gi + 8);
     }
     float peak = 0.0f;
 #pragma unroll
@@ -463,6 +465,7 @@ struct nhip_decoder {
     float* qhs = nullptr;
     float* att = nullptr;
     float* gu = nullptr;
+    float* act = nullptr;  // SwiGLU activations [rows][ffn] of the fused gate/up matmul
     float* logits = nullptr;
     int32_t* d_in = nullptr;  // tokens, slots, positions, first (0), count: 5 x max_rows
     int32_t* d_topk_idx = nullptr;
@@ -502,17 +505,23 @@ int32_t* in_count(nhip_decoder* m, int32_t* base) { return base + 4 * m->dims.ma
 // buffer (which then becomes *x); otherwise the element-wise kernel updates
 // *x in place and the plain matmul follows.  Either way the residual ends in
 // *x with the delta added.
+// With `act` (the gate/up matmul) the fused launch applies SwiGLU to the
+// tile-interleaved rows and writes the activations to act[rows][ffn],
+// setting *fused; the fallback writes the interleaved rows to y.
 int32_t norm_matmul(nhip_decoder* m, int rows, float** x, bool pending, const float* gain, nhip_weights* w,
-                    float* y, int ldy, bool fuse)
+                    float* y, int ldy, bool fuse, float* act = nullptr, bool* fused = nullptr)
 {
     const nhip_decoder_dims& D = m->dims;
     hipStream_t s = m->stream;
+    if (fused) *fused = false;
     if (fuse) {
         float* other = *x == m->x ? m->x2 : m->x;
-        DecodePrologue f{kProNorm, *x, pending ? m->delta : nullptr, pending ? other : nullptr, gain, D.eps};
-        const int32_t rc = launch_decode_fused(w, f, rows, y, ldy, s);
+        DecodePrologue f{kProNorm, *x, pending ? m->delta : nullptr, pending ? other : nullptr, gain, D.eps,
+                         act ? 1 : 0};
+        const int32_t rc = act ? launch_decode_fused(w, f, rows, act, D.ffn, s) : launch_decode_fused(w, f, rows, y, ldy, s);
         if (rc <= 0) {
             if (rc == 0 && pending) *x = other;
+            if (rc == 0 && fused) *fused = true;
             return rc;
         }
     }
@@ -575,7 +584,7 @@ int32_t enqueue_forward(nhip_decoder* m, int rows, int k)
         if (rc) return rc;
         rc = 1;
         if (!attn_quant && fuse) {
-            DecodePrologue f{kProQuant, m->att, nullptr, nullptr, nullptr, 0.0f};
+            DecodePrologue f{kProQuant, m->att, nullptr, nullptr, nullptr, 0.0f, 0};
             rc = launch_decode_fused(m->wo[l], f, rows, m->delta, d, s);
             if (rc < 0) return rc;
         }
@@ -587,15 +596,20 @@ int32_t enqueue_forward(nhip_decoder* m, int rows, int k)
             rc = nhip_matmul_i8_dev(m->wo[l], m->q8, m->qs, rows, m->delta, d, 0, d, s);
             if (rc) return rc;
         }
-        rc = norm_matmul(m, rows, &x, true, m->ffn_norm[l], m->wgu[l], m->gu, 2 * F, fuse);
+        bool act_ready = false;  // SwiGLU applied by the gate/up matmul (into m->act)
+        rc = norm_matmul(m, rows, &x, true, m->ffn_norm[l], m->wgu[l], m->gu, 2 * F, fuse, m->act, &act_ready);
         if (rc) return rc;
-        rc = 1;
-        if (fuse) {
-            DecodePrologue f{kProSwiglu, m->gu, nullptr, nullptr, nullptr, 0.0f};
+        if (act_ready) {  // quantize the activations in the down matmul's prologue
+            DecodePrologue f{kProQuant, m->act, nullptr, nullptr, nullptr, 0.0f, 0};
             rc = launch_decode_fused(m->wd[l], f, rows, m->delta, d, s);
             if (rc < 0) return rc;
-        }
-        if (rc) {
+            if (rc) {
+                rc = nhip_quantize_rows_dev(m->act, rows, F, m->q8, m->qs, s);
+                if (rc) return rc;
+                rc = nhip_matmul_i8_dev(m->wd[l], m->q8, m->qs, rows, m->delta, d, 0, d, s);
+                if (rc) return rc;
+            }
+        } else {  // interleaved gate/up rows -> SwiGLU + quantize -> down matmul
             hipLaunchKernelGGL(swiglu_quant_kernel, dim3(rows), dim3(kThreads), 0, s, m->gu, F, m->q8, m->qs);
             NHIP_CHECK_HIP(hipGetLastError());
             rc = nhip_matmul_i8_dev(m->wd[l], m->q8, m->qs, rows, m->delta, d, 0, d, s);
@@ -605,7 +619,7 @@ int32_t enqueue_forward(nhip_decoder* m, int rows, int k)
     // the final residual is not needed again: no x_out
     rc = 1;
     if (fuse) {
-        DecodePrologue f{kProNorm, x, m->delta, nullptr, m->final_norm, D.eps};
+        DecodePrologue f{kProNorm, x, m->delta, nullptr, m->final_norm, D.eps, 0};
         rc = launch_decode_fused(m->wlm, f, rows, m->logits, D.vocab, s);
         if (rc < 0) return rc;
     }
@@ -753,7 +767,7 @@ int32_t nhip_decoder_create(const nhip_decoder_dims* dims, nhip_decoder** out)
         (rc = dalloc(m, &m->q8, (size_t)R * std::max({D.d, D.ffn, D.heads * 64}))) || (rc = dalloc(m, &m->qs, (size_t)R)) ||
         (rc = dalloc(m, &m->qkv, (size_t)R * m->qkv_n)) || (rc = dalloc(m, &m->qh, (size_t)R * D.heads * 64)) ||
         (rc = dalloc(m, &m->qhs, (size_t)R * D.heads)) || (rc = dalloc(m, &m->att, (size_t)R * D.heads * 64)) ||
-        (rc = dalloc(m, &m->gu, (size_t)R * 2 * D.ffn)) || (rc = dalloc(m, &m->logits, (size_t)R * D.vocab)) ||
+        (rc = dalloc(m, &m->gu, (size_t)R * 2 * D.ffn)) || (rc = dalloc(m, &m->act, (size_t)R * D.ffn)) || (rc = dalloc(m, &m->logits, (size_t)R * D.vocab)) ||
         (rc = dalloc(m, &m->d_in, (size_t)5 * R)) || (rc = dalloc(m, &m->d_topk_idx, (size_t)R * kMaxTopK)) ||
         (rc = dalloc(m, &m->d_topk_lp, (size_t)R * kMaxTopK)))
         return fail(rc);
@@ -807,8 +821,19 @@ int32_t nhip_decoder_set_layer(nhip_decoder* m, int32_t layer, const int8_t* wqk
     const nhip_decoder_dims& D = m->dims;
     int32_t rc;
     nhip_weights** slots[4] = {&m->wqkv[layer], &m->wo[layer], &m->wgu[layer], &m->wd[layer]};
-    const int8_t* ws[4] = {wqkv, wo, wgu, wd};
-    const uint16_t* ss[4] = {sqkv, so, sgu, sd};
+    // the gate/up rows are uploaded tile-interleaved: rows 16b..16b+7 are
+    // gate rows 8b..8b+7, rows 16b+8..16b+15 the matching up rows
+    const int F = D.ffn, G = D.d / 32;
+    std::vector<int8_t> wgu_i((size_t)2 * F * D.d);
+    std::vector<uint16_t> sgu_i((size_t)2 * F * G);
+    for (int n = 0; n < 2 * F; n++) {
+        const int b = n >> 4, e = n & 15;
+        const int src = e < 8 ? 8 * b + e : F + 8 * b + (e - 8);
+        std::memcpy(&wgu_i[(size_t)n * D.d], wgu + (size_t)src * D.d, D.d);
+        std::memcpy(&sgu_i[(size_t)n * G], sgu + (size_t)src * G, sizeof(uint16_t) * G);
+    }
+    const int8_t* ws[4] = {wqkv, wo, wgu_i.data(), wd};
+    const uint16_t* ss[4] = {sqkv, so, sgu_i.data(), sd};
     const int rows[4] = {m->qkv_n, D.d, 2 * D.ffn, D.d};
     const int cols[4] = {D.d, D.heads * 64, D.d, D.ffn};
     for (int i = 0; i < 4; i++) {

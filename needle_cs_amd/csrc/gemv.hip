@@ -94,6 +94,7 @@ struct MatmulParams {
     int32_t ldd;              // LDS row stride (int32) of D and scales: roundup4(gph) + 4
     int32_t st_bytes;         // int8 path: LDS bytes of the staged activation operands
     int32_t swz;              // decode path, 5..16 tokens: float4-column swizzle mask of the products
+    int32_t swiglu;           // fused decode path: rows are (8 gate, 8 up) pairs per tile, store SwiGLU
     uint32_t t0, t1, t2, t3;  // codebook bytes 0..15
     float byte_scale;
 };
@@ -574,7 +575,10 @@ __device__ __forceinline__ void narrow_products(const long (&av)[2 * CB / 4], co
 
 // The lanes (t, r) of the first M*16 threads add row (t, r)'s products in
 // ascending group order and store y[t][n].  Float4 column c of product row
-// x sits at column c ^ (x & swz).
+// x sits at column c ^ (x & swz).  With p.swiglu the tile's rows are gate
+// rows j = 8*tile + r (r < 8) followed by the matching up rows: lane r < 8
+// takes lane r + 8's sum (DPP row_shl:8 within the token's 16-lane row) and
+// stores a = (g / (1 + Exp(-g))) * u at y[t][j].
 __device__ __forceinline__ void chain_products(const float* pl, int GS, int swz, int M, int G, int tile,
                                                const MatmulParams& p)
 {
@@ -608,7 +612,12 @@ __device__ __forceinline__ void chain_products(const float* pl, int GS, int swz,
         }
         const float* rowf = reinterpret_cast<const float*>(row);
         for (int c = full * 16; c < G; c++) acc = acc + rowf[(((c >> 2) ^ sw) << 2) | (c & 3)];
-        if (nn >= p.row_start && nn < p.row_end) p.y[(size_t)t * p.ldy + nn] = acc;
+        if (p.swiglu) {
+            const float u = dpp_row_shl(acc, 8);
+            if (rr < 8) p.y[(size_t)t * p.ldy + tile * 8 + rr] = (acc / (1.0f + exp_poly(-acc))) * u;
+        } else if (nn >= p.row_start && nn < p.row_end) {
+            p.y[(size_t)t * p.ldy + nn] = acc;
+        }
     }
 }
 
@@ -743,9 +752,7 @@ __global__ __launch_bounds__(512) void matmul_i8_decode_kernel(MatmulParams p)
 //   kProNorm    x (+ delta) -> RMSNorm (canonical row sum of squares) *
 //               gain -> QuantizeInt8; workgroup 0 also writes x + delta to
 //               x_out;
-//   kProQuant   QuantizeInt8 of x;
-//   kProSwiglu  a = (g / (1 + Exp(-g))) * u for x = [g | u] (2K per row) ->
-//               QuantizeInt8.
+//   kProQuant   QuantizeInt8 of x.
 // Thread t of the prologue holds the float4 groups at 4t + 4*nt*j, j < G4
 // (nt = 256 for the norm, whose lanes are the canonical sum's, else the
 // whole block).  Four rows are always computed (rows past M repeat the
@@ -783,7 +790,7 @@ __global__ __launch_bounds__(512) void matmul_i8_decode_fused_kernel(MatmulParam
     const int nt = NORM ? 256 : (int)blockDim.x;
 
     // 1. prologue inputs
-    float4 xv[TI][G4], dv[TI][G4], gv[G4];
+    float4 xv[TI][G4], dv[TI][G4], gv[G4];  // dv: the delta of the norm
 #pragma unroll
     for (int j = 0; j < G4; j++) {
         const int i = min(4 * (tid + nt * j), K - 4);
@@ -791,13 +798,8 @@ __global__ __launch_bounds__(512) void matmul_i8_decode_fused_kernel(MatmulParam
 #pragma unroll
         for (int t = 0; t < TI; t++) {
             const size_t row = (size_t)min(t, M - 1);
-            if constexpr (KIND == kProSwiglu) {
-                xv[t][j] = *reinterpret_cast<const float4*>(f.x + row * 2 * K + i);
-                dv[t][j] = *reinterpret_cast<const float4*>(f.x + row * 2 * K + K + i);
-            } else {
-                xv[t][j] = *reinterpret_cast<const float4*>(f.x + row * K + i);
-                if constexpr (DELTA) dv[t][j] = *reinterpret_cast<const float4*>(f.delta + row * K + i);
-            }
+            xv[t][j] = *reinterpret_cast<const float4*>(f.x + row * K + i);
+            if constexpr (DELTA) dv[t][j] = *reinterpret_cast<const float4*>(f.delta + row * K + i);
         }
     }
     // 2. weight scales, 3. weight blocks
@@ -861,12 +863,6 @@ __global__ __launch_bounds__(512) void matmul_i8_decode_fused_kernel(MatmulParam
 #pragma unroll
             for (int j = 0; j < G4; j++) {
                 if (4 * (tid + nt * j) < K) {
-                    if constexpr (KIND == kProSwiglu) {
-                        const float4 g = xv[t][j];
-                        const float4 u = dv[t][j];
-                        xv[t][j] = make_float4((g.x / (1.0f + exp_poly(-g.x))) * u.x, (g.y / (1.0f + exp_poly(-g.y))) * u.y,
-                                               (g.z / (1.0f + exp_poly(-g.z))) * u.z, (g.w / (1.0f + exp_poly(-g.w))) * u.w);
-                    }
                     peak[t] = fmaxf(fmaxf(peak[t], fmaxf(fabsf(xv[t][j].x), fabsf(xv[t][j].y))),
                                     fmaxf(fabsf(xv[t][j].z), fabsf(xv[t][j].w)));
                 }
@@ -1002,8 +998,7 @@ int32_t launch_fused_kind(const MatmulParams& p, const DecodePrologue& f, int wa
         case kProNorm:
             return f.delta ? launch_fused_tpl<CB, kProNorm, true, G4>(p, f, waves, lds, s)
                            : launch_fused_tpl<CB, kProNorm, false, G4>(p, f, waves, lds, s);
-        case kProQuant: return launch_fused_tpl<CB, kProQuant, false, G4>(p, f, waves, lds, s);
-        default: return launch_fused_tpl<CB, kProSwiglu, false, G4>(p, f, waves, lds, s);
+        default: return launch_fused_tpl<CB, kProQuant, false, G4>(p, f, waves, lds, s);
     }
 }
 
@@ -1334,7 +1329,9 @@ int32_t launch_decode_fused(const DeviceWeights* w, const DecodePrologue& f, int
                             hipStream_t stream)
 {
     NHIP_REQUIRE(w && w->format == WeightFormat::Int8G32, "weights are not in the int8 format");
-    NHIP_REQUIRE(f.x && y && ldy >= w->rows, "fused matmul: null input/output or ldy %d < rows", ldy);
+    NHIP_REQUIRE(f.x && y && ldy >= (f.swiglu ? w->rows / 2 : w->rows), "fused matmul: null input/output or ldy %d "
+                 "too small", ldy);
+    NHIP_REQUIRE(!f.swiglu || w->rows % 16 == 0, "fused matmul: SwiGLU pairs need whole 16-row tiles");
     if (tokens < 1 || tokens > 4 || w->special_scales) return 1;
     const int K = w->cols;
     // waves: 4, or 8 when the (non-norm) prologue needs more threads; CB in
@@ -1366,6 +1363,7 @@ int32_t launch_decode_fused(const DeviceWeights* w, const DecodePrologue& f, int
     p.row_end = w->rows;
     p.tile_begin = 0;
     p.tile_end = w->tiles_n;
+    p.swiglu = f.swiglu;
     p.ldd = ((2 * w->blocks + 3) & ~3) + 4;
     p.d_bytes = tokens * 16 * p.ldd * (int)sizeof(float);
     p.st_bytes = (4 * K + 15) & ~15;
