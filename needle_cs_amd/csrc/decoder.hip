@@ -47,7 +47,8 @@ __device__ __forceinline__ float block_max(float v, float* wmax)
 }
 
 // The canonical row sum (common.hpp) of the partials p[t] held by the 256
-// threads, broadcast to every thread through red[256 + 1].
+// threads, broadcast to every thread through red[256] (red holds 257 floats;
+// other reductions of the same kernel must not reuse red[256]).
 __device__ __forceinline__ float block_canonical_sum(float p, float* red)
 {
     red[threadIdx.x] = p;
@@ -113,7 +114,7 @@ template <bool DELTA>
 __global__ __launch_bounds__(kThreads) void add_rmsnorm_quant_kernel(float* x, const float* delta, const float* gain,
                                                                      int d, float eps, int8_t* q, float* qscale)
 {
-    __shared__ __align__(16) float red[kThreads + 4];
+    __shared__ __align__(16) float red[kThreads + 8];  // partials, the broadcast sum, 4 wave maxima
     const int t = threadIdx.x;
     float* xr = x + (size_t)blockIdx.x * d;
     const float* dr = DELTA ? delta + (size_t)blockIdx.x * d : nullptr;
@@ -151,7 +152,7 @@ __global__ __launch_bounds__(kThreads) void add_rmsnorm_quant_kernel(float* x, c
             peak = max_abs4(peak, v[j]);
         }
     }
-    peak = block_max(peak, red + kThreads);
+    peak = block_max(peak, red + kThreads + 4);
     const float scale = peak > 0.0f ? peak / 127.0f : 1.0f;
     const float inverse = 1.0f / scale;
     int8_t* qr = q + (size_t)blockIdx.x * d;
@@ -264,18 +265,44 @@ __device__ __forceinline__ bool masked(int i) { return i == 0 || i == 2 || i == 
 
 // TopKLogSoftmax (src/Needle/Ops.cs:1092-1221) in the canonical float form:
 // top K of the ids except 0, 2, 3 (the set is unique under the order above,
-// so the tree merge equals the reference's sequential insertion);
-// log_shift = peak + log(sum_i Exp(v_i - peak)), masked v_i = -1e30, the sum
-// by the canonical row reduction; lp = v - log_shift.  K is a template
-// parameter so that the per-thread lists stay in registers.
+// so merging per-thread and per-block lists equals the reference's
+// sequential insertion); log_shift = peak + log(S), masked v_i = -1e30, with
+// S over blocks of kTopkBlock ids: S_b = sum Exp(v_i - m_b) (m_b the block
+// maximum, the canonical row reduction over the block's ids) and S = sum_b
+// Exp(m_b - peak) * S_b in ascending b; lp = v - log_shift.  One workgroup
+// per (block, row) computes the block's top K, m_b and S_b; a second kernel
+// merges a row's blocks.  K is a template parameter so that the per-thread
+// lists stay in registers.
+constexpr int kTopkBlock = 2048;
+
 template <int K>
-__global__ __launch_bounds__(kThreads) void topk_lse_kernel(const float* logits, int n, int32_t* idx, float* lp)
+__global__ __launch_bounds__(kThreads) void topk_block_kernel(const float* logits, int n, int blocks, float* bvals,
+                                                             int32_t* bids, float* bmax, float* bsum)
 {
     __shared__ float tv[K][kThreads];
     __shared__ int ti[K][kThreads];
-    __shared__ __align__(16) float red[kThreads + 4];
+    __shared__ __align__(16) float red[kThreads + 8];  // partials, the broadcast sum, 4 wave maxima
     const int t = threadIdx.x;
-    const float* x = logits + (size_t)blockIdx.x * n;
+    const int b = blockIdx.x;
+    const int row = blockIdx.y;
+    const float* x = logits + (size_t)row * n;
+    const int b0 = b * kTopkBlock;
+    // ids b0 + 4t + 1024h + e (h < 2): the block's canonical lane t
+    float xv[8];
+#pragma unroll
+    for (int h = 0; h < 2; h++) {
+        const int g = b0 + 4 * t + 1024 * h;
+        if ((n & 3) == 0) {
+            const float4 v = *reinterpret_cast<const float4*>(x + min(g, n - 4));
+            xv[4 * h] = v.x;
+            xv[4 * h + 1] = v.y;
+            xv[4 * h + 2] = v.z;
+            xv[4 * h + 3] = v.w;
+        } else {
+#pragma unroll
+            for (int e = 0; e < 4; e++) xv[4 * h + e] = x[min(g + e, n - 1)];
+        }
+    }
     float bv[K];
     int bi[K];
 #pragma unroll
@@ -283,50 +310,36 @@ __global__ __launch_bounds__(kThreads) void topk_lse_kernel(const float* logits,
         bv[m] = -INFINITY;
         bi[m] = 0x7FFFFFFF;
     }
-    // ids i = 4t + 1024 j + e (the canonical lane's elements), two float4
-    // groups at a time (n % 4 == 0: whole groups; else the tail group by
-    // clamped scalar loads)
-    constexpr int kBatch = 8;
-    const bool whole = (n & 3) == 0;
-    auto load8 = [&](float (&xv)[kBatch], int i0) {
+    float mloc = -INFINITY;
 #pragma unroll
-        for (int h = 0; h < 2; h++) {
-            const int g = i0 + h * 1024;
-            if (whole) {
-                const float4 v = *reinterpret_cast<const float4*>(x + min(g, n - 4));
-                xv[4 * h] = v.x;
-                xv[4 * h + 1] = v.y;
-                xv[4 * h + 2] = v.z;
-                xv[4 * h + 3] = v.w;
-            } else {
+    for (int j = 0; j < 8; j++) {
+        const int i = b0 + 4 * t + 1024 * (j >> 2) + (j & 3);
+        if (i >= n) continue;
+        xv[j] = masked(i) ? -1e30f : xv[j];
+        mloc = fmaxf(mloc, xv[j]);
+        if (masked(i) || !before(xv[j], i, bv[K - 1], bi[K - 1])) continue;
+        bv[K - 1] = xv[j];
+        bi[K - 1] = i;
 #pragma unroll
-                for (int e = 0; e < 4; e++) xv[4 * h + e] = x[min(g + e, n - 1)];
-            }
-        }
-    };
-    for (int i0 = 4 * t; i0 < n; i0 += 2 * 1024) {
-        float xv[kBatch];
-        load8(xv, i0);
-#pragma unroll
-        for (int j = 0; j < kBatch; j++) {
-            const int i = i0 + (j >> 2) * 1024 + (j & 3);
-            const float v = xv[j];
-            if (i >= n || masked(i) || !before(v, i, bv[K - 1], bi[K - 1])) continue;
-            bv[K - 1] = v;
-            bi[K - 1] = i;
-#pragma unroll
-            for (int m = K - 1; m > 0; m--) {
-                if (before(bv[m], bi[m], bv[m - 1], bi[m - 1])) {
-                    const float fv = bv[m];
-                    const int fi = bi[m];
-                    bv[m] = bv[m - 1];
-                    bi[m] = bi[m - 1];
-                    bv[m - 1] = fv;
-                    bi[m - 1] = fi;
-                }
+        for (int m = K - 1; m > 0; m--) {
+            if (before(bv[m], bi[m], bv[m - 1], bi[m - 1])) {
+                const float fv = bv[m];
+                const int fi = bi[m];
+                bv[m] = bv[m - 1];
+                bi[m] = bi[m - 1];
+                bv[m - 1] = fv;
+                bi[m - 1] = fi;
             }
         }
     }
+    const float mb = block_max(mloc, red + kThreads + 4);
+    float s = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+        const int i = b0 + 4 * t + 1024 * (j >> 2) + (j & 3);
+        if (i < n) s = s + exp_poly(xv[j] - mb);
+    }
+    const float sb = block_canonical_sum(s, red);
 #pragma unroll
     for (int m = 0; m < K; m++) {
         tv[m][t] = bv[m];
@@ -365,31 +378,82 @@ __global__ __launch_bounds__(kThreads) void topk_lse_kernel(const float* logits,
         }
         __syncthreads();
     }
-    const float peak = tv[0][0];
-    float s = 0.0f;
-    for (int i0 = 4 * t; i0 < n; i0 += 2 * 1024) {
-        float xv[kBatch];
-        load8(xv, i0);
-#pragma unroll
-        for (int j = 0; j < kBatch; j++) {
-            const int i = i0 + (j >> 2) * 1024 + (j & 3);
-            if (i < n) s = s + exp_poly((masked(i) ? -1e30f : xv[j]) - peak);
-        }
-    }
-    const float total = block_canonical_sum(s, red);
-    const float log_shift = peak + log_poly(total);
+    const size_t slot = (size_t)row * blocks + b;
     if (t < K) {
-        idx[(size_t)blockIdx.x * K + t] = ti[t][0];
-        lp[(size_t)blockIdx.x * K + t] = tv[t][0] - log_shift;
+        bvals[slot * K + t] = tv[t][0];
+        bids[slot * K + t] = ti[t][0];
+    }
+    if (t == 0) {
+        bmax[slot] = mb;
+        bsum[slot] = sb;
     }
 }
 
-int32_t launch_topk(const float* logits, int rows, int n, int k, int32_t* idx, float* lp, hipStream_t s)
+// Merge of a row's block lists (sequential insertion in the (value, id)
+// order) and S = sum_b Exp(m_b - peak) * S_b in ascending b.
+template <int K>
+__global__ __launch_bounds__(64) void topk_final_kernel(const float* bvals, const int32_t* bids, const float* bmax,
+                                                         const float* bsum, int blocks, int32_t* idx, float* lp)
 {
+    if (threadIdx.x != 0) return;
+    const int row = blockIdx.x;
+    float bv[K];
+    int bi[K];
+#pragma unroll
+    for (int m = 0; m < K; m++) {
+        bv[m] = -INFINITY;
+        bi[m] = 0x7FFFFFFF;
+    }
+    const size_t base = (size_t)row * blocks;
+    for (int c = 0; c < blocks * K; c++) {
+        const float v = bvals[base * K + c];
+        const int i = bids[base * K + c];
+        if (!before(v, i, bv[K - 1], bi[K - 1])) continue;
+        bv[K - 1] = v;
+        bi[K - 1] = i;
+#pragma unroll
+        for (int m = K - 1; m > 0; m--) {
+            if (before(bv[m], bi[m], bv[m - 1], bi[m - 1])) {
+                const float fv = bv[m];
+                const int fi = bi[m];
+                bv[m] = bv[m - 1];
+                bi[m] = bi[m - 1];
+                bv[m - 1] = fv;
+                bi[m - 1] = fi;
+            }
+        }
+    }
+    const float peak = bv[0];
+    float total = 0.0f;
+    for (int b = 0; b < blocks; b++) total = total + exp_poly(bmax[base + b] - peak) * bsum[base + b];
+    const float log_shift = peak + log_poly(total);
+#pragma unroll
+    for (int m = 0; m < K; m++) {
+        idx[(size_t)row * K + m] = bi[m];
+        lp[(size_t)row * K + m] = bv[m] - log_shift;
+    }
+}
+
+// Scratch of the top-k: per (row, block) K values and ids, the block maximum
+// and sum.
+struct TopkScratch {
+    float* vals;
+    int32_t* ids;
+    float* bmax;
+    float* bsum;
+};
+
+int32_t launch_topk(const float* logits, int rows, int n, int k, const TopkScratch& ts, int32_t* idx, float* lp,
+                    hipStream_t s)
+{
+    const int blocks = (n + kTopkBlock - 1) / kTopkBlock;
     switch (k) {
-#define NHIP_TOPK_CASE(K)                                                                                  \
-    case K:                                                                                                \
-        hipLaunchKernelGGL(topk_lse_kernel<K>, dim3(rows), dim3(kThreads), 0, s, logits, n, idx, lp);      \
+#define NHIP_TOPK_CASE(K)                                                                                        \
+    case K:                                                                                                      \
+        hipLaunchKernelGGL(topk_block_kernel<K>, dim3(blocks, rows), dim3(kThreads), 0, s, logits, n, blocks,    \
+                           ts.vals, ts.ids, ts.bmax, ts.bsum);                                                   \
+        hipLaunchKernelGGL(topk_final_kernel<K>, dim3(rows), dim3(64), 0, s, ts.vals, ts.ids, ts.bmax, ts.bsum,   \
+                           blocks, idx, lp);                                                                     \
         break;
         NHIP_TOPK_CASE(1)
         NHIP_TOPK_CASE(2)
@@ -469,6 +533,7 @@ struct nhip_decoder {
     float* logits = nullptr;
     int32_t* d_in = nullptr;  // tokens, slots, positions, first (0), count: 5 x max_rows
     int32_t* d_topk_idx = nullptr;
+    TopkScratch topk{};  // per (row, block) partial top-k lists, maxima and sums
     float* d_topk_lp = nullptr;
     int32_t* h_in = nullptr;  // pinned host mirror of d_in
     int32_t* h_topk_idx = nullptr;
@@ -631,7 +696,7 @@ int32_t enqueue_forward(nhip_decoder* m, int rows, int k)
         if (rc) return rc;
     }
     if (k > 0) {
-        rc = launch_topk(m->logits, rows, D.vocab, k, m->d_topk_idx, m->d_topk_lp, s);
+        rc = launch_topk(m->logits, rows, D.vocab, k, m->topk, m->d_topk_idx, m->d_topk_lp, s);
         if (rc) return rc;
     }
     return NHIP_OK;
@@ -769,7 +834,11 @@ int32_t nhip_decoder_create(const nhip_decoder_dims* dims, nhip_decoder** out)
         (rc = dalloc(m, &m->qhs, (size_t)R * D.heads)) || (rc = dalloc(m, &m->att, (size_t)R * D.heads * 64)) ||
         (rc = dalloc(m, &m->gu, (size_t)R * 2 * D.ffn)) || (rc = dalloc(m, &m->act, (size_t)R * D.ffn)) || (rc = dalloc(m, &m->logits, (size_t)R * D.vocab)) ||
         (rc = dalloc(m, &m->d_in, (size_t)5 * R)) || (rc = dalloc(m, &m->d_topk_idx, (size_t)R * kMaxTopK)) ||
-        (rc = dalloc(m, &m->d_topk_lp, (size_t)R * kMaxTopK)))
+        (rc = dalloc(m, &m->d_topk_lp, (size_t)R * kMaxTopK)) ||
+        (rc = dalloc(m, &m->topk.vals, (size_t)R * ((D.vocab + kTopkBlock - 1) / kTopkBlock) * kMaxTopK)) ||
+        (rc = dalloc(m, &m->topk.ids, (size_t)R * ((D.vocab + kTopkBlock - 1) / kTopkBlock) * kMaxTopK)) ||
+        (rc = dalloc(m, &m->topk.bmax, (size_t)R * ((D.vocab + kTopkBlock - 1) / kTopkBlock))) ||
+        (rc = dalloc(m, &m->topk.bsum, (size_t)R * ((D.vocab + kTopkBlock - 1) / kTopkBlock))))
         return fail(rc);
     m->attn_ws_bytes = nhip_attention_decode_workspace(R, D.heads, D.max_chunks);
     void* ws = nullptr;

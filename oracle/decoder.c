@@ -121,8 +121,14 @@ float or_swiglu_quant(const float* g, const float* u, int n, float* a, int8_t* q
 
 /* TopKLogSoftmax (src/Needle/Ops.cs:1092-1221) in the canonical float form:
  * the top k of the allowed ids (0, 2, 3 masked when mask is set) by value,
- * ties to the lower id; log_shift = peak + log(sum_i Exp(v_i - peak)) with
- * masked v_i = -1e30, the sum by the canonical reduction. */
+ * ties to the lower id; log_shift = peak + log(S) with peak the top value
+ * and S summed over blocks of OR_TOPK_BLOCK ids: for block b with masked
+ * values v_i = -1e30 and block maximum m_b, S_b = sum_i Exp(v_i - m_b) by
+ * the canonical reduction over the block's ids (relative to its start),
+ * and S = sum_b Exp(m_b - peak) * S_b in ascending b.  The blocks let the
+ * GPU reduce one block per workgroup. */
+#define OR_TOPK_BLOCK 2048
+
 void or_topk_lse(const float* x, int n, int k, int mask, int* idx, float* lp)
 {
     float top_val[16];
@@ -143,13 +149,23 @@ void or_topk_lse(const float* x, int n, int k, int mask, int* idx, float* lp)
         }
     }
     float peak = top_val[0];
-    float s[256];
-    for (int t = 0; t < 256; t++) s[t] = 0.0f;
-    for (int i = 0; i < n; i++) {
-        float v = mask && (i == 0 || i == 2 || i == 3) ? -1e30f : x[i];
-        s[CANON_LANE(i)] = s[CANON_LANE(i)] + or_exp_poly(v - peak);
+    float total = 0.0f;
+    for (int b0 = 0; b0 < n; b0 += OR_TOPK_BLOCK) {
+        int b1 = b0 + OR_TOPK_BLOCK < n ? b0 + OR_TOPK_BLOCK : n;
+        float mb = -INFINITY;
+        for (int i = b0; i < b1; i++) {
+            float v = mask && (i == 0 || i == 2 || i == 3) ? -1e30f : x[i];
+            mb = fmaxf(mb, v);
+        }
+        float s[256];
+        for (int t = 0; t < 256; t++) s[t] = 0.0f;
+        for (int i = b0; i < b1; i++) {
+            float v = mask && (i == 0 || i == 2 || i == 3) ? -1e30f : x[i];
+            s[CANON_LANE(i - b0)] = s[CANON_LANE(i - b0)] + or_exp_poly(v - mb);
+        }
+        total = total + or_exp_poly(mb - peak) * tree_fold(s);
     }
-    float log_shift = peak + or_log_poly(tree_fold(s));
+    float log_shift = peak + or_log_poly(total);
     for (int m = 0; m < k; m++) {
         idx[m] = top_idx[m];
         lp[m] = top_val[m] - log_shift;
