@@ -125,6 +125,51 @@ class GemmCase(GemvCase):
         N.check(fn(w.handle, self.dq.ptr, self.ds.ptr, self.m, self.dy.ptr, self.n, 0, self.n, None))
 
 
+class CqGemvCase(GemvCase):
+    """Reference-native GEMV (the .cact weight format): 4- or 2-bit codebook
+    indices (uniform bytes), a codebook of levels U(-1, 1) from the seeded
+    stream with Codebook.Fill's bytes (round-half-even of level / ByteScale
+    + 63, ByteScale = max |level| / 63), fp16 norms U(0.002, 0.02) per
+    128-column group, and N(0,1) activations through the Hadamard prepare
+    (nhip_prepare_dev) outside the timed region."""
+
+    def __init__(self, m: int, k: int, n: int, bits: int, seed: int, min_bytes: int = 300 << 20):
+        self.m, self.k, self.n, self.bits = m, k, n, bits
+        st = C.c_uint64(seed)
+        count = 16 if bits == 4 else 4
+        book = N.Codebook()
+        levels = N.synth_uniform(st, 16, -1.0, 1.0).astype(np.float32)
+        bscale = np.float32(np.max(np.abs(levels[:count])) / np.float32(63.0))
+        for i in range(16):
+            book.levels[i] = float(levels[i])
+        for i in range(32):
+            book.bytes[i] = int(np.rint(levels[i % 16] / bscale)) + 63 if i % 16 < count else 0
+        book.byte_scale = float(bscale)
+        self.book = book
+        per = n * k * bits // 8 + n * (k // 128) * 2
+        self.copies = max(2, -(-min_bytes // per))
+        self.weights = []
+        for _ in range(self.copies):
+            idx = N.synth_int8(st, n * k * bits // 8).view(np.uint8)
+            norms = N.synth_half_uniform(st, n * (k // 128), 0.002, 0.02)
+            self.weights.append(N.Weights.codebook(idx, norms, book, n, k, bits))
+        self.stride = ((k // 128) + 7) // 8 * 8
+        x = N.synth_normal(st, m * k)
+        dx = N.DeviceBuffer.from_array(x)
+        self.dv = N.DeviceBuffer(m * k)
+        self.dsc = N.DeviceBuffer(m * self.stride * 4)
+        self.doff = N.DeviceBuffer(m * self.stride * 4)
+        N.check(N.lib().nhip_prepare_dev(dx.ptr, m, k, bits, self.dv.ptr, self.dsc.ptr, self.doff.ptr, self.stride,
+                                         None))
+        self.dy = N.DeviceBuffer(m * n * 4)
+        self.bytes = per + m * k + 2 * m * self.stride * 4 + m * n * 4
+
+    def launch(self, i: int) -> None:
+        w = self.weights[i % self.copies]
+        N.check(N.lib().nhip_matmul_cq_dev(w.handle, self.dv.ptr, self.dsc.ptr, self.doff.ptr, self.stride, self.m,
+                                           self.dy.ptr, self.n, 0, self.n, None))
+
+
 class AttnCase:
     """Ragged decode attention: 16 sequences, context lengths U[32, 2048]
     (seeded), 16 heads x 64 (qk 64, MHA), int8 KV cache quantized per
@@ -354,6 +399,16 @@ def main() -> int:
                               "GB/s": round(g, 1), "frac_hbm_peak": round(g / HBM_PEAK_GBS, 4),
                               "bytes_per_launch": case.bytes})
             print(f"# GEMV M={m} K={k} N={n}: {t * 1e3:.2f} us/launch, {g:.0f} GB/s", file=sys.stderr, flush=True)
+            case.close()
+        for bits, (m, k, n) in [(4, (1, 1024, 4096)), (4, (3, 2048, 8192)), (2, (3, 2048, 8192))]:
+            case = CqGemvCase(m, k, n, bits, seed=0x2800 + bits + m)
+            t = case.time(max(200, args.steps // 2), args.warmup)
+            g = case.bytes / (t * 1e-3) / 1e9
+            secondary.append({"workload": f"Cq{bits} (reference-native codebook, g128) GEMV M={m} K={k} N={n}",
+                              "us_per_launch": round(t * 1e3, 3), "GB/s": round(g, 1),
+                              "frac_hbm_peak": round(g / HBM_PEAK_GBS, 4), "bytes_per_launch": case.bytes})
+            print(f"# Cq{bits} GEMV M={m} K={k} N={n}: {t * 1e3:.2f} us/launch, {g:.0f} GB/s", file=sys.stderr,
+                  flush=True)
             case.close()
 
     prefill = []
