@@ -318,6 +318,43 @@ int32_t nhip_decoder_beam_search(nhip_decoder* m, const int32_t* prompt, int32_t
                                  float* out_score, nhip_decode_stats* stats);
 int32_t nhip_decoder_destroy(nhip_decoder* m);
 
+/* ------------------------------------------------- .cact archives (Model) -- */
+
+/* Model.Open / Model.FromMemory (src/Needle/Model.cs:307-389, 400-411): the
+ * archive is parsed in place and every tensor is uploaded to HBM once.  The
+ * layout is the reference's (Model.cs:190-276 Record / Reader;
+ * ModelInfo.cs:7-8 magic 0x05E12A84 and the 196-byte header): 48 uint32
+ * header words + the RoPE theta float, header[2] codebook floats, header[1]
+ * packed 44-byte records, then the data.  Malformed archives (Model.cs:372-389's
+ * checks, plus each record's data inside the archive) give NHIP_ERR_FORMAT
+ * before any device work.  Codebook-quantized records become weights for
+ * nhip_matmul_cq_dev (2-bit book = Codebook.Fill(levels 0..3), 4-bit =
+ * Codebook.Fill(levels 12..27)); fp16 / fp32 records become fp32 device
+ * arrays (fp16 by Scalar.HalfToSingle); raw records (the tokenizer blob)
+ * stay in the caller's bytes at record.offset.  The model holds no pointer
+ * into the archive after nhip_open returns. */
+enum { NHIP_CACT_FP16 = 1, NHIP_CACT_FP32 = 2, NHIP_CACT_CQ = 3, NHIP_CACT_RAW = 4 };
+
+typedef struct nhip_record_info {
+    int32_t dtype, ndim;
+    uint32_t shape[4];
+    uint64_t offset, bytes; /* in the archive */
+    uint32_t group, bits;   /* codebook-quantized records: 128, 2 or 4 */
+} nhip_record_info;
+
+typedef struct nhip_model nhip_model;
+
+int32_t nhip_open(const uint8_t* cact, size_t length, nhip_model** out);
+/* header words [48] (geometry: Model.cs:65-105), RoPE theta, record count;
+ * any output may be NULL */
+int32_t nhip_model_info(const nhip_model* m, uint32_t* header48, float* rope_theta, int32_t* records);
+int32_t nhip_model_record(const nhip_model* m, int32_t index, nhip_record_info* info);
+/* the device weights of a codebook-quantized record, else NULL */
+nhip_weights* nhip_model_weights(const nhip_model* m, int32_t index);
+/* the fp32 device array of an fp16 / fp32 record, else NULL */
+const float* nhip_model_dense(const nhip_model* m, int32_t index);
+int32_t nhip_model_close(nhip_model* m);
+
 /* ------------------------------------------ synthetic workload inputs -- */
 
 /* Deterministic host-side generators for the benchmark workloads: one

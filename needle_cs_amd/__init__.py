@@ -16,7 +16,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libneedle_hip.so")
 
 __all__ = [
-    "LIB_PATH", "NeedleHipError", "lib", "check", "Codebook", "Cq", "Activations", "AttnTile",
+    "LIB_PATH", "NeedleHipError", "lib", "check", "Codebook", "Cq", "Activations", "AttnTile", "RecordInfo",
     "DeviceBuffer", "Weights", "Stream", "Event", "Graph", "synth_normal", "synth_uniform", "synth_int8",
     "synth_half_uniform", "available",
 ]
@@ -55,6 +55,12 @@ class AttnTile(C.Structure):
                 ("probability_stride", C.c_int32), ("peaks", C.c_void_p), ("sums", C.c_void_p)]
 
 
+class RecordInfo(C.Structure):
+    """nhip_record_info: one .cact record (src/Needle/Model.cs:190-197)."""
+    _fields_ = [("dtype", C.c_int32), ("ndim", C.c_int32), ("shape", C.c_uint32 * 4), ("offset", C.c_uint64),
+                ("bytes", C.c_uint64), ("group", C.c_uint32), ("bits", C.c_uint32)]
+
+
 _i32, _u64p, _vp, _sz = C.c_int32, C.POINTER(C.c_uint64), C.c_void_p, C.c_size_t
 _PROTOS = {
     "nhip_last_error": (C.c_char_p, []),
@@ -80,6 +86,12 @@ _PROTOS = {
     "nhip_decoder_copy_slot": (_i32, [_vp, _i32, _i32, _i32]),
     "nhip_decoder_beam_search": (_i32, [_vp, _vp, _i32, _i32, _i32, _i32, _vp, _vp, _vp, _vp]),
     "nhip_decoder_destroy": (_i32, [_vp]),
+    "nhip_open": (_i32, [_vp, _sz, C.POINTER(_vp)]),
+    "nhip_model_info": (_i32, [_vp, C.POINTER(C.c_uint32), C.POINTER(C.c_float), C.POINTER(_i32)]),
+    "nhip_model_record": (_i32, [_vp, _i32, C.POINTER(RecordInfo)]),
+    "nhip_model_weights": (_vp, [_vp, _i32]),
+    "nhip_model_dense": (_vp, [_vp, _i32]),
+    "nhip_model_close": (_i32, [_vp]),
     "nhip_matmul_i8_fused_dev": (_i32, [_vp, _vp, _vp, _i32, _vp, _i32, _i32, _i32, _vp]),
     "nhip_attention_decode_workspace": (_sz, [_i32, _i32, _i32]),
     "nhip_attention_decode_workspace_init": (_i32, [_vp, _sz, _vp]),
