@@ -782,6 +782,19 @@ int32_t copy_slot(nhip_decoder* m, int dst, int src, int length)
     return NHIP_OK;
 }
 
+// Captured decode graphs hold the weights' device pointers: weights that
+// change (set_layer / set_head) drop them, and the next decode step
+// captures again.  The stream is drained first so that no replay is running.
+void drop_graphs(nhip_decoder* m)
+{
+    if (m->stream) (void)hipStreamSynchronize(m->stream);
+    for (int i = 0; i <= kMaxTopK; i++) {
+        if (m->graphs[i]) (void)hipGraphExecDestroy(m->graphs[i]);
+        m->graphs[i] = nullptr;
+        m->graph_k[i] = 0;
+    }
+}
+
 int32_t upload(nhip_decoder* m, float** dst, const float* src, size_t count)
 {
     int32_t rc = dalloc(m, dst, count);
@@ -889,6 +902,7 @@ int32_t nhip_decoder_set_layer(nhip_decoder* m, int32_t layer, const int8_t* wqk
     NHIP_REQUIRE(wqkv && sqkv && wo && so && wgu && sgu && wd && sd && attn_norm && ffn_norm, "null weights");
     const nhip_decoder_dims& D = m->dims;
     int32_t rc;
+    drop_graphs(m);
     nhip_weights** slots[4] = {&m->wqkv[layer], &m->wo[layer], &m->wgu[layer], &m->wd[layer]};
     // the gate/up rows are uploaded tile-interleaved: rows 16b..16b+7 are
     // gate rows 8b..8b+7, rows 16b+8..16b+15 the matching up rows
@@ -924,6 +938,7 @@ int32_t nhip_decoder_set_head(nhip_decoder* m, const float* embedding, const flo
     NHIP_REQUIRE(m && embedding && final_norm && wlm && slm, "null argument");
     const nhip_decoder_dims& D = m->dims;
     int32_t rc;
+    drop_graphs(m);
     if (!m->emb && (rc = dalloc(m, &m->emb, (size_t)D.vocab * D.d))) return rc;
     if (!m->final_norm && (rc = dalloc(m, &m->final_norm, D.d))) return rc;
     NHIP_CHECK_HIP(hipMemcpy(m->emb, embedding, sizeof(float) * D.vocab * D.d, hipMemcpyHostToDevice));

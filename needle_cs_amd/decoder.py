@@ -82,13 +82,17 @@ class GpuDecoder:
         h = C.c_void_p()
         check(lib().nhip_decoder_create(C.byref(self.dims), C.byref(h)))
         self.h = h.value
+        self.set_model(model)
+        self.vocab = dm["vocab"]
+
+    def set_model(self, model: dict) -> None:
+        """Uploads (or replaces) every layer's weights and the head."""
         for l, lw in enumerate(model["layers"]):
             check(lib().nhip_decoder_set_layer(self.h, l, *[_p(lw[n]) for n in ("wqkv", "sqkv", "wo", "so", "wgu",
                                                                                 "sgu", "wd", "sd", "attn_norm",
                                                                                 "ffn_norm")]))
         check(lib().nhip_decoder_set_head(self.h, _p(model["embedding"]), _p(model["final_norm"]), _p(model["wlm"]),
                                           _p(model["slm"])))
-        self.vocab = dm["vocab"]
 
     def forward(self, tokens, slots, positions, k=0, logits=True):
         rows = len(tokens)

@@ -82,3 +82,21 @@ def test_wide_layers_prefill_and_beam(hip, orc):
     assert np.array_equal(tg, tc) and np.float32(sg) == np.float32(sc)
     gpu.close()
     cpu.close()
+
+
+def test_replacing_weights_after_graph_capture(hip, orc):
+    """Beam-search decode steps replay a captured graph per row count;
+    weights replaced afterwards (set_layer / set_head) must be the ones the
+    next search reads (the graphs holding the old pointers are dropped)."""
+    model_a = synthetic_model(TINY, 7101)
+    model_b = synthetic_model(TINY, 7102)
+    prompt = random_prompt(8, 12, TINY["vocab"])
+    gpu = GpuDecoder(model_a, slots=3, capacity=64, max_rows=16)
+    gpu.beam_search(prompt, 3, 10, 1)  # captures the 1..3-row graphs
+    gpu.set_model(model_b)
+    cpu = orc.CpuDecoder(model_b, slots=3, capacity=64)
+    tg, sg, _ = gpu.beam_search(prompt, 3, 10, 1)
+    tc, sc, _ = cpu.beam_search(prompt, 3, 10, 1)
+    assert np.array_equal(tg, tc) and np.float32(sg) == np.float32(sc)
+    gpu.close()
+    cpu.close()
