@@ -342,6 +342,23 @@ def pmc_run(case: GemvCase, launches: int) -> int:
     return 0
 
 
+def codebook_lines(args) -> list:
+    """The reference-native form of the GEMV configs: Cq4/Cq2 codebook
+    weights, g128 norms, Hadamard-prepared activations."""
+    out = []
+    for bits, (m, k, n) in [(4, (1, 1024, 4096)), (4, (3, 2048, 8192)), (2, (3, 2048, 8192))]:
+        case = CqGemvCase(m, k, n, bits, seed=0x2800 + bits + m)
+        t = case.time(max(200, args.steps // 2), args.warmup)
+        g = case.bytes / (t * 1e-3) / 1e9
+        out.append({"workload": f"Cq{bits} (reference-native codebook, g128) GEMV M={m} K={k} N={n}",
+                    "us_per_launch": round(t * 1e3, 3), "GB/s": round(g, 1),
+                    "frac_hbm_peak": round(g / HBM_PEAK_GBS, 4), "bytes_per_launch": case.bytes})
+        print(f"# Cq{bits} GEMV M={m} K={k} N={n}: {t * 1e3:.2f} us/launch, {g:.0f} GB/s", file=sys.stderr,
+              flush=True)
+        case.close()
+    return out
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -351,7 +368,7 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-secondary", action="store_true")
     ap.add_argument("--no-decode-loop", action="store_true")
-    ap.add_argument("--only", choices=["prefill", "attention", "decode_loop"],
+    ap.add_argument("--only", choices=["prefill", "attention", "decode_loop", "codebook"],
                     help="run one secondary workload alone (for kernel tracing); prints no JSON line")
     ap.add_argument("--decode-chunks", type=int, default=64,
                     help="attention position-split cap of the decode loop (1: one chunk per row with the output quantize fused)")
@@ -370,6 +387,8 @@ def main() -> int:
         threads = int(os.environ.get("NEEDLE_THREADS", "0")) or min(physical_cores(), 16)
         if args.only == "decode_loop":
             print(json.dumps(decode_loop(args, threads)), file=sys.stderr)
+        elif args.only == "codebook":
+            codebook_lines(args)
         elif args.only == "prefill":
             for fused in (True, False):
                 case = GemmCase(512, 2048, 8192, seed=0x4004, fused=fused)
@@ -400,16 +419,7 @@ def main() -> int:
                               "bytes_per_launch": case.bytes})
             print(f"# GEMV M={m} K={k} N={n}: {t * 1e3:.2f} us/launch, {g:.0f} GB/s", file=sys.stderr, flush=True)
             case.close()
-        for bits, (m, k, n) in [(4, (1, 1024, 4096)), (4, (3, 2048, 8192)), (2, (3, 2048, 8192))]:
-            case = CqGemvCase(m, k, n, bits, seed=0x2800 + bits + m)
-            t = case.time(max(200, args.steps // 2), args.warmup)
-            g = case.bytes / (t * 1e-3) / 1e9
-            secondary.append({"workload": f"Cq{bits} (reference-native codebook, g128) GEMV M={m} K={k} N={n}",
-                              "us_per_launch": round(t * 1e3, 3), "GB/s": round(g, 1),
-                              "frac_hbm_peak": round(g / HBM_PEAK_GBS, 4), "bytes_per_launch": case.bytes})
-            print(f"# Cq{bits} GEMV M={m} K={k} N={n}: {t * 1e3:.2f} us/launch, {g:.0f} GB/s", file=sys.stderr,
-                  flush=True)
-            case.close()
+        secondary += codebook_lines(args)
 
     prefill = []
     if not args.no_secondary:

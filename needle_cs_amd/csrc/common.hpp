@@ -55,6 +55,7 @@ struct DeviceWeights {
     int32_t blocks;       // 1 KB blocks per tile
     int32_t groups_pad8;  // scale row stride (halves)
     uint32_t table[4];    // codebook bytes 0..15 (Cq formats)
+    uint32_t split_table[4];  // the same bytes as the decode kernel's split lookup tables
     float byte_scale;     // codebook ByteScale (1 for the literal format)
     uint8_t* tiles;
     uint16_t* norms;

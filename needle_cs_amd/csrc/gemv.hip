@@ -96,6 +96,7 @@ struct MatmulParams {
     int32_t swz;              // decode path, 5..16 tokens: float4-column swizzle mask of the products
     int32_t swiglu;           // fused decode path: rows are (8 gate, 8 up) pairs per tile, store SwiGLU
     uint32_t t0, t1, t2, t3;  // codebook bytes 0..15
+    uint32_t x0, x1, x2, x3;  // the split tables of lut4x (TA, TB)
     float byte_scale;
 };
 
@@ -112,6 +113,26 @@ __device__ __forceinline__ uint32_t lut4(uint32_t idx, uint32_t t0, uint32_t t1,
     const uint32_t b3 = (idx >> 3) & 0x01010101u;
     const uint32_t mask = (b3 << 8) - b3;  // 0xFF in every byte whose index has bit 3 set
     return (hi & mask) | (lo & ~mask);
+}
+
+// The same lookup in three operations, for tables whose 16 bytes are all
+// below 128 (codebook bytes are in [0, 126]).  v_perm_b32's selector byte s
+// picks byte s of its 8-byte source for s < 8, the sign of source byte 1, 3,
+// 5 or 7 (0x00 or 0xFF) for s = 8..11, 0x00 for 12 and 0xFF for 13..15.
+// With
+//   A = perm(TA, c),  B = perm(TB, c ^ 8),
+//   TA = table bytes 0..7, TB = bytes 8..15, every byte but byte 4 of each
+//        stored complemented,
+// one of A, B is the stored byte (TA[c] for c < 8, TB[c - 8] for c >= 8)
+// and the other is 0x00 for c = 4, 12 (selector 12; stored plain) and 0xFF
+// for every other c (selectors 8..11 read the complemented, sign-set bytes
+// 1, 3, 5, 7, and 13..15 give 0xFF), so A ^ B is the table byte.
+// c: four codes 0..15, one per byte.
+__device__ __forceinline__ uint32_t lut4x(uint32_t c, uint32_t a0, uint32_t a1, uint32_t b0, uint32_t b1)
+{
+    const uint32_t a = __builtin_amdgcn_perm(a1, a0, c);
+    const uint32_t b = __builtin_amdgcn_perm(b1, b0, c ^ 0x08080808u);
+    return a ^ b;
 }
 
 // The MFMA A operand(s) one lane supplies for one group: activation bytes of
@@ -157,11 +178,13 @@ __device__ __forceinline__ Operand<F> load_operand(const int8_t* qrow, bool vali
     return o;
 }
 
-// D_g for group `h` (0/1) of the loaded weight block `w`.
-template <int F>
-__device__ __forceinline__ v4i group_dot(const u4& w, int h, const Operand<F>& a, const MatmulParams& p)
+// d + the MFMA products of group `h` (0/1) of the loaded weight block `w`:
+// D_g itself when d is zero.
+// SPLIT: Cq4 codes go through lut4x and the split tables x0..x3.
+template <int F, bool SPLIT = false>
+__device__ __forceinline__ v4i group_dot(const u4& w, int h, const Operand<F>& a, const MatmulParams& p,
+                                         v4i d = v4i{0, 0, 0, 0})
 {
-    v4i d = {0, 0, 0, 0};
     if constexpr (F == kI8) {
         const long b = h ? (long)(((uint64_t)w.w << 32) | w.z) : (long)(((uint64_t)w.y << 32) | w.x);
         d = __builtin_amdgcn_mfma_i32_16x16x32_i8(a.a, b, d, 0, 0, 0);
@@ -179,14 +202,39 @@ __device__ __forceinline__ v4i group_dot(const u4& w, int h, const Operand<F>& a
         for (int s = 0; s < 2; s++) {
             const int sh = 4 * s;
             v4i b;
-            b.x = (int)lut4((w.x >> sh) & 0x0F0F0F0Fu, p.t0, p.t1, p.t2, p.t3);
-            b.y = (int)lut4((w.y >> sh) & 0x0F0F0F0Fu, p.t0, p.t1, p.t2, p.t3);
-            b.z = (int)lut4((w.z >> sh) & 0x0F0F0F0Fu, p.t0, p.t1, p.t2, p.t3);
-            b.w = (int)lut4((w.w >> sh) & 0x0F0F0F0Fu, p.t0, p.t1, p.t2, p.t3);
+            if constexpr (SPLIT) {
+                b.x = (int)lut4x((w.x >> sh) & 0x0F0F0F0Fu, p.x0, p.x1, p.x2, p.x3);
+                b.y = (int)lut4x((w.y >> sh) & 0x0F0F0F0Fu, p.x0, p.x1, p.x2, p.x3);
+                b.z = (int)lut4x((w.z >> sh) & 0x0F0F0F0Fu, p.x0, p.x1, p.x2, p.x3);
+                b.w = (int)lut4x((w.w >> sh) & 0x0F0F0F0Fu, p.x0, p.x1, p.x2, p.x3);
+            } else {
+                b.x = (int)lut4((w.x >> sh) & 0x0F0F0F0Fu, p.t0, p.t1, p.t2, p.t3);
+                b.y = (int)lut4((w.y >> sh) & 0x0F0F0F0Fu, p.t0, p.t1, p.t2, p.t3);
+                b.z = (int)lut4((w.z >> sh) & 0x0F0F0F0Fu, p.t0, p.t1, p.t2, p.t3);
+                b.w = (int)lut4((w.w >> sh) & 0x0F0F0F0Fu, p.t0, p.t1, p.t2, p.t3);
+            }
             d = __builtin_amdgcn_mfma_i32_16x16x64_i8(a.a[s], b, d, 0, 0, 0);
         }
     }
     return d;
+}
+
+// The operand itself, or zeros (an A row block that must not contribute).
+template <int F>
+__device__ __forceinline__ Operand<F> operand_if(const Operand<F>& o, bool keep)
+{
+    Operand<F> z;
+    if constexpr (F == kI8) {
+        z.a = keep ? o.a : 0;
+    } else if constexpr (F == kCq2) {
+#pragma unroll
+        for (int s = 0; s < 4; s++) z.a[s] = keep ? o.a[s] : 0;
+    } else {
+        const v4i zero = {0, 0, 0, 0};
+#pragma unroll
+        for (int s = 0; s < 2; s++) z.a[s] = keep ? o.a[s] : zero;
+    }
+    return z;
 }
 
 // One block per (16-row tile, 16-token block); S = blockDim.x/64 waves split
@@ -743,6 +791,116 @@ __global__ __launch_bounds__(512) void matmul_i8_decode_kernel(MatmulParams p)
     chain_products(pl, GS, WIDE ? p.swz : 0, M, G, tile, p);
 }
 
+// Codebook formats, M <= 4 tokens: the four-group MFMA sets of
+// narrow_products with the codebook epilogue.  Wave w owns the GPW groups
+// from g_first = GPW*w (groups past G run on clamped operands and are
+// dropped).  Set c covers groups g_first + 4c + j, j < 4: group j's MFMAs
+// take A rows 4j..4j+3 (tokens 0..3) and that group's weights, so lane
+// (r, kq) ends up holding D_g of row r, g = g_first + 4c + kq, for tokens
+// 0..3.  The lane leaves
+//     scaled     = (HalfToSingle(norm[n][g]) * ByteScale) * scale[t][g]
+//     pa[t][r][g] = scaled * D_g,   pb[t][r][g] = scaled * offset[t][g]
+// in LDS; after one barrier lane (t, r) adds both rows in ascending g and
+// stores acc - bias, Scalar.MatMulRows' operations in its order
+// (Scalar.cs:185-189).
+template <int F, int GPW, bool EXACT>
+__global__ __launch_bounds__(512) void matmul_cq_decode_kernel(MatmulParams p)
+{
+    using T = Traits<F>;
+    constexpr int SETS = GPW / 4;
+    constexpr int CB = GPW / T::GPB;  // weight blocks per wave
+    extern __shared__ __align__(16) uint8_t lds[];
+    const int M = p.tokens;  // 1..4
+    const int G = p.groups;
+    const int GS = p.ldd;    // product row stride (floats), a multiple of 4
+    float* pa = reinterpret_cast<float*>(lds);
+    float* pb = pa + (size_t)M * 16 * GS;
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int tile = p.tile_begin + blockIdx.x;
+    const int r = lane & 15;
+    const int kq = lane >> 4;
+    const int n = tile * 16 + r;
+    const int g_first = wave * GPW;
+    const u4* wbase = reinterpret_cast<const u4*>(p.tiles) + (size_t)tile * p.blocks * 64 + lane;
+    const uint16_t* nrow = p.norms + (size_t)n * p.groups_pad8;
+
+    // 1. A operands: lane (r, kq) feeds A row r of every set, token r%4
+    //    (rows of tokens >= M repeat token M-1; their D rows are never
+    //    read) of group g_first + 4c + r/4; 2. activation scales and
+    //    offsets and 3. weight scales of the lane's groups g_first + 4c + kq;
+    //    4. weight blocks -- all in flight together
+    const int8_t* qrow = p.q + (size_t)min(r & 3, M - 1) * p.cols;
+    Operand<F> av[SETS];
+#pragma unroll
+    for (int c = 0; c < SETS; c++) av[c] = load_operand<F>(qrow, true, min(g_first + 4 * c + (r >> 2), G - 1), kq);
+    float sc[SETS][4], of[SETS][4];
+    uint16_t hraw[SETS];
+#pragma unroll
+    for (int c = 0; c < SETS; c++) {
+        const int g = min(g_first + 4 * c + kq, G - 1);
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const size_t at = (size_t)min(i, M - 1) * p.stride + g;
+            sc[c][i] = p.qscale[at];
+            of[c][i] = p.offsets[at];
+        }
+        hraw[c] = nrow[g];
+    }
+    u4 w[CB];
+#pragma unroll
+    for (int c = 0; c < CB; c++)
+        w[c] = __builtin_nontemporal_load(wbase + (size_t)min(wave * CB + c, p.blocks - 1) * 64);
+    __builtin_amdgcn_sched_barrier(0);
+
+#pragma unroll
+    for (int c = 0; c < SETS; c++) {
+        v4i d = {0, 0, 0, 0};
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const int gl = 4 * c + j;  // group within the wave
+            d = group_dot<F, true>(w[gl / T::GPB], gl % T::GPB, operand_if<F>(av[c], (r >> 2) == j), p, d);
+        }
+        const float hs = EXACT ? ref_half_to_single(hraw[c]) : decode_scale_fast(hraw[c]);
+        const float hb = hs * p.byte_scale;
+        // groups >= G are written (inside the row) but never read
+        const size_t at = (size_t)r * GS + g_first + 4 * c + kq;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            if (i < M) {
+                const float scaled = hb * sc[c][i];
+                pa[at + (size_t)i * 16 * GS] = scaled * static_cast<float>(d[i]);
+                pb[at + (size_t)i * 16 * GS] = scaled * of[c][i];
+            }
+        }
+    }
+    __syncthreads();
+    for (int x = threadIdx.x; x < M * 16; x += blockDim.x) {
+        const int nn = tile * 16 + (x & 15);
+        const float* ra = pa + (size_t)x * GS;
+        const float* rb = pb + (size_t)x * GS;
+        float acc = 0.0f, bias = 0.0f;
+        int g = 0;
+        for (; g + 4 <= G; g += 4) {
+            const float4 a = *reinterpret_cast<const float4*>(ra + g);
+            const float4 b = *reinterpret_cast<const float4*>(rb + g);
+            acc = acc + a.x;
+            bias = bias + b.x;
+            acc = acc + a.y;
+            bias = bias + b.y;
+            acc = acc + a.z;
+            bias = bias + b.z;
+            acc = acc + a.w;
+            bias = bias + b.w;
+        }
+        for (; g < G; g++) {
+            acc = acc + ra[g];
+            bias = bias + rb[g];
+        }
+        if (nn >= p.row_start && nn < p.row_end) p.y[(size_t)(x >> 4) * p.ldy + nn] = acc - bias;
+    }
+}
+
 // The decode kernel for M <= 4 with its activation rows computed in the
 // prologue from fp32 inputs instead of read as int8 (one launch instead of
 // an element-wise kernel and a matmul).  Every workgroup loads the inputs
@@ -981,6 +1139,54 @@ int32_t try_i8_decode(const DeviceWeights* w, MatmulParams& p, hipStream_t strea
                              : launch_dec_ti<8, false>(p, waves, lds, stream);
 }
 
+template <int F, int GPW>
+int32_t launch_cq_decode_tpl(const MatmulParams& p, bool exact, int waves, size_t lds, hipStream_t stream)
+{
+    const int tiles = p.tile_end - p.tile_begin;
+    if (exact)
+        hipLaunchKernelGGL((matmul_cq_decode_kernel<F, GPW, true>), dim3(tiles), dim3(64 * waves), lds, stream, p);
+    else
+        hipLaunchKernelGGL((matmul_cq_decode_kernel<F, GPW, false>), dim3(tiles), dim3(64 * waves), lds, stream, p);
+    NHIP_CHECK_HIP(hipGetLastError());
+    return NHIP_OK;
+}
+
+template <int F>
+int32_t launch_cq_decode_gpw(const MatmulParams& p, int gpw, bool exact, int waves, size_t lds, hipStream_t s)
+{
+    switch (gpw) {
+        case 4: return launch_cq_decode_tpl<F, 4>(p, exact, waves, lds, s);
+        case 8: return launch_cq_decode_tpl<F, 8>(p, exact, waves, lds, s);
+        default: return launch_cq_decode_tpl<F, 16>(p, exact, waves, lds, s);
+    }
+}
+
+// Codebook formats, 1..4 tokens: runs matmul_cq_decode_kernel with GPW
+// groups per wave (4, one set, by default, more when that would take over 8
+// waves; NHIP_CQ_DECODE_GPW = 4, 8 or 16 overrides it for tuning) and one
+// wave per GPW groups.  Returns 1 when it does not apply
+// (more than 4 tokens, group sums requested, or K over 16*8 groups).
+int32_t try_cq_decode(const DeviceWeights* w, MatmulParams& p, hipStream_t stream)
+{
+    if (p.tokens > 4 || p.dots) return 1;
+    static const int gpw_override = [] {
+        const char* e = getenv("NHIP_CQ_DECODE_GPW");
+        const int v = e ? atoi(e) : 0;
+        return (v == 4 || v == 8 || v == 16) ? v : 0;
+    }();
+    const bool cq4 = w->format == WeightFormat::Cq4;
+    int gpw = gpw_override ? gpw_override : 4;
+    while (gpw < 16 && (w->groups + gpw - 1) / gpw > 8) gpw *= 2;
+    const int waves = (w->groups + gpw - 1) / gpw;
+    if (waves > 8) return 1;
+    p.ldd = waves * gpw + 4;  // every group a wave writes, + 4: conflict-free product writes
+    const size_t lds = (size_t)2 * p.tokens * 16 * p.ldd * sizeof(float);
+    if (lds > kMaxLds) return 1;
+    const bool exact = w->special_scales != 0;
+    return cq4 ? launch_cq_decode_gpw<kCq4>(p, gpw, exact, waves, lds, stream)
+               : launch_cq_decode_gpw<kCq2>(p, gpw, exact, waves, lds, stream);
+}
+
 template <int CB, int KIND, bool DELTA, int G4>
 int32_t launch_fused_tpl(const MatmulParams& p, const DecodePrologue& f, int waves, size_t lds, hipStream_t stream)
 {
@@ -1098,6 +1304,10 @@ int32_t run_matmul(const DeviceWeights* w, const int8_t* q, const float* scales,
     p.t1 = w->table[1];
     p.t2 = w->table[2];
     p.t3 = w->table[3];
+    p.x0 = w->split_table[0];
+    p.x1 = w->split_table[1];
+    p.x2 = w->split_table[2];
+    p.x3 = w->split_table[3];
     p.byte_scale = w->byte_scale;
 
     // Waves per 16-row tile (each loads 1/waves of the tile's weight blocks).
@@ -1135,6 +1345,10 @@ int32_t run_matmul(const DeviceWeights* w, const int8_t* q, const float* scales,
             return NHIP_ERR_UNSUPPORTED;
         }
         return dots ? launch_i8<true>(p, waves, ns, lds, stream) : launch_i8<false>(p, waves, ns, lds, stream);
+    }
+    {
+        const int32_t drc = try_cq_decode(w, p, stream);
+        if (drc <= 0) return drc;
     }
     // Codebook formats.  Groups per phase: the int32 D buffer [gph][M][16]
     // plus the decoded scales [gph][16] stay within 64 KB of LDS, and no
@@ -1234,6 +1448,12 @@ int32_t create_weights(WeightFormat fmt, const uint8_t* d_src, const uint16_t* d
     if (book) {
         std::memcpy(w->table, book->bytes, 16);
         w->byte_scale = book->byte_scale;
+        // lut4x's split tables: bytes 0..7 and 8..15, every byte but the
+        // fifth of each complemented (the codebook bytes are below 128)
+        uint8_t split[16];
+        for (int i = 0; i < 16; i++)
+            split[i] = (i & 7) == 4 ? book->bytes[i] : static_cast<uint8_t>(~book->bytes[i]);
+        std::memcpy(w->split_table, split, 16);
     }
     const size_t units = (size_t)w->tiles_n * w->blocks * 64;
     const size_t norm_elems = (size_t)w->tiles_n * 16 * w->groups_pad8;
@@ -1380,6 +1600,10 @@ int32_t weights_cq_create_internal(const nhip_cq* cq, nhip_weights** out)
 {
     NHIP_REQUIRE(cq && cq->indices && cq->norms && cq->book, "Cq view is incomplete");
     NHIP_REQUIRE(cq->bits == 2 || cq->bits == 4, "bits %d is not 2 or 4", cq->bits);
+    // the kernels multiply codebook bytes as signed int8 MFMA operands
+    for (int i = 0; i < (1 << cq->bits); i++)
+        NHIP_REQUIRE(cq->book->bytes[i] < 128, "codebook byte %d is %d: the matmul takes codebook bytes in [0, 127] "
+                     "(Codebook.Fill makes [0, 126])", i, cq->book->bytes[i]);
     return create_from_host(cq->bits == 2 ? WeightFormat::Cq2 : WeightFormat::Cq4, cq->indices, cq->norms, cq->rows,
                             cq->cols, cq->book, out);
 }

@@ -237,6 +237,71 @@ def test_prepare_bit_exact(hip, orc, bits, cols, tokens):
     assert np.array_equal(do.download(np.float32), off)
 
 
+def run_cq(hip, c, rows, cols, bits, tokens, ldy, r0, r1):
+    weights = hip.Weights.codebook(c["indices"], c["norms"], hip_book(hip, c["book"]), rows, cols, bits)
+    dv = hip.DeviceBuffer.from_array(c["values"])
+    ds = hip.DeviceBuffer.from_array(c["scales"])
+    do = hip.DeviceBuffer.from_array(c["offsets"])
+    dy = hip.DeviceBuffer.from_array(np.full(tokens * ldy, SENTINEL, dtype=np.float32))
+    hip.check(hip.lib().nhip_matmul_cq_dev(weights.handle, dv.ptr, ds.ptr, do.ptr, c["act"].stride, tokens, dy.ptr,
+                                           ldy, r0, r1, None))
+    return dy.download(np.float32)
+
+
+@pytest.mark.parametrize("bits", [2, 4])
+@pytest.mark.parametrize("tokens", [1, 2, 3, 4])
+@pytest.mark.parametrize("r0,r1", [(0, 37), (5, 29), (16, 17)])
+def test_cq_decode_path_row_ranges(hip, orc, bits, tokens, r0, r1):
+    """1..4 tokens run the codebook decode kernel: K = 640 (5 groups, a
+    partial set of four), 2048, 8192 (64 groups) and 16384 (128 groups, the
+    most it takes: 16 per wave)."""
+    rows = 37
+    ldy = rows + 5
+    for cols in (640, 2048, 8192, 16384):
+        c = cq_case(orc, 6000 + tokens * 10 + r0 + cols + bits, rows, cols, bits, tokens)
+        got = run_cq(hip, c, rows, cols, bits, tokens, ldy, r0, r1)
+        want = np.full(tokens * ldy, SENTINEL, dtype=np.float32)
+        orc.matmul_rows(c["cq"], c["act"], tokens, want, ldy, r0, r1)
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), cols
+
+
+@pytest.mark.parametrize("bits", [2, 4])
+@pytest.mark.parametrize("tokens", [3, 9])
+def test_cq_special_norm_patterns(hip, orc, bits, tokens):
+    """Zero, negative-zero, subnormal and exponent-31 fp16 norms decode as
+    Scalar.HalfToSingle does (Scalar.cs:121-128), in the decode kernel (3
+    tokens) and the general one (9)."""
+    rows, cols = 64, 2048
+    c = cq_case(orc, 777 + tokens + bits, rows, cols, bits, tokens)
+    flat = c["norms"]
+    flat[::7] = 0x8000
+    flat[::11] = 0x0000
+    flat[::13] = 0x0001
+    flat[::17] = 0x83FF
+    flat[::19] = 0x7C00
+    flat[::23] = 0xFC01
+    got = run_cq(hip, c, rows, cols, bits, tokens, rows, 0, rows)
+    want = np.full(tokens * rows, SENTINEL, dtype=np.float32)
+    orc.matmul_rows(c["cq"], c["act"], tokens, want, rows, 0, rows)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+@pytest.mark.parametrize("bits", [2, 4])
+def test_codebook_bytes_above_127_are_rejected(hip, orc, bits):
+    """The kernels multiply codebook bytes as signed int8 MFMA operands, so
+    a codebook byte of 128 or more (Codebook.Fill makes [0, 126]) is refused
+    when the weights are created, before anything is uploaded; bytes the
+    format never indexes (4..15 of a 2-bit book) are not checked."""
+    rows, cols = 16, 256
+    c = cq_case(orc, 991 + bits, rows, cols, bits, 1)
+    c["book"].bytes[7] = 200
+    if bits == 2:
+        hip.Weights.codebook(c["indices"], c["norms"], hip_book(hip, c["book"]), rows, cols, bits).close()
+        c["book"].bytes[3] = 128
+    with pytest.raises(hip.NeedleHipError, match="codebook byte"):
+        hip.Weights.codebook(c["indices"], c["norms"], hip_book(hip, c["book"]), rows, cols, bits)
+
+
 # ------------------------------------------------- kernel-table entries --
 
 @pytest.mark.parametrize("bits,rows,cols,tokens,r0,r1", [
