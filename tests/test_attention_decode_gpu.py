@@ -77,6 +77,19 @@ def test_decode_attention_single_chunk_plan(hip, orc, heads, kv_heads, qk):
     assert bit_equal(got, oracle_decode(orc, cache, q, qs, heads, spec, 1))
 
 
+def test_decode_attention_several_head_blocks(hip, orc):
+    """Chunks of up to 1024 positions (capacity 8192, max_chunks 8) leave LDS
+    for 5 of 16 kv heads per workgroup: 4 head blocks per row."""
+    heads = 16
+    cache = Cache(orc, hip, 4242, 2, 8192, heads, 64)
+    spec = [(0, 0, 8192), (1, 17, 5000), (0, 3, 40), (1, 0, 1), (1, 4000, 2049), (0, 8000, 192)]
+    q, qs = queries(orc, cache.st, len(spec), heads, 64)
+    assert hip.lib().nhip_attention_decode_workspace(len(spec), heads, 8) > 0
+    for rep in range(2):
+        got, _ = run_decode(hip, cache, q, qs, heads, spec, 8)
+        assert bit_equal(got, oracle_decode(orc, cache, q, qs, heads, spec, 8)), rep
+
+
 def test_decode_attention_invalid_rows_are_zero(hip, orc):
     cache = Cache(orc, hip, 42, 2, 256, 2, 64)
     heads = 4
