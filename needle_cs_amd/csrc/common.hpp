@@ -104,6 +104,15 @@ struct DecodePrologue {
 };
 int32_t launch_decode_fused(const DeviceWeights* w, const DecodePrologue& f, int32_t tokens, float* y, int32_t ldy,
                             hipStream_t stream);
+// The decode matmul of int8 rows q (scales qscale) over tile-interleaved
+// gate/up weights, storing the SwiGLU activations at act[t][0 .. rows/2);
+// returns 1 when the decode kernel does not take the shape.
+int32_t launch_decode_swiglu(const DeviceWeights* w, const int8_t* q, const float* qscale, int32_t tokens,
+                             float* act, int32_t ldy, hipStream_t stream);
+// Fused prologues pay for their input rows in every workgroup; beyond this
+// many 16-row tiles a separate element-wise launch and the plain matmul are
+// faster.
+constexpr int kFusedPrologueMaxTiles = 256;
 // Chunk-kernel geometry of attention_decode_impl: the longest chunk of the
 // plan, and the kv heads per workgroup (0 when a chunk does not fit in LDS);
 // a quantized output needs every head in one workgroup.

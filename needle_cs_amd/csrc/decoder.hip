@@ -564,22 +564,22 @@ int32_t* in_positions(nhip_decoder* m, int32_t* base) { return base + 2 * m->dim
 int32_t* in_first(nhip_decoder* m, int32_t* base) { return base + 3 * m->dims.max_rows; }
 int32_t* in_count(nhip_decoder* m, int32_t* base) { return base + 4 * m->dims.max_rows; }
 
-// Residual + RMSNorm + quantize feeding a matmul.  For up to four rows one
-// fused launch computes the normalised rows in the matmul's prologue, reading
-// *x and the pending delta and writing their sum to the other residual
-// buffer (which then becomes *x); otherwise the element-wise kernel updates
-// *x in place and the plain matmul follows.  Either way the residual ends in
-// *x with the delta added.
-// With `act` (the gate/up matmul) the fused launch applies SwiGLU to the
-// tile-interleaved rows and writes the activations to act[rows][ffn],
-// setting *fused; the fallback writes the interleaved rows to y.
+// Residual + RMSNorm + quantize feeding a matmul.  For up to four rows and
+// at most kFusedPrologueMaxTiles row tiles one fused launch computes the
+// normalised rows in the matmul's prologue, reading *x and the pending delta
+// and writing their sum to the other residual buffer (which then becomes
+// *x); otherwise the element-wise kernel updates *x in place and the plain
+// matmul follows.  Either way the residual ends in *x with the delta added.
+// With `act` (the gate/up matmul) and up to four rows the matmul's chain
+// applies SwiGLU to the tile-interleaved rows and writes the activations to
+// act[rows][ffn], setting *fused; otherwise the interleaved rows go to y.
 int32_t norm_matmul(nhip_decoder* m, int rows, float** x, bool pending, const float* gain, nhip_weights* w,
                     float* y, int ldy, bool fuse, float* act = nullptr, bool* fused = nullptr)
 {
     const nhip_decoder_dims& D = m->dims;
     hipStream_t s = m->stream;
     if (fused) *fused = false;
-    if (fuse) {
+    if (fuse && w->tiles_n <= kFusedPrologueMaxTiles) {
         float* other = *x == m->x ? m->x2 : m->x;
         DecodePrologue f{kProNorm, *x, pending ? m->delta : nullptr, pending ? other : nullptr, gain, D.eps,
                          act ? 1 : 0};
@@ -597,6 +597,13 @@ int32_t norm_matmul(nhip_decoder* m, int rows, float** x, bool pending, const fl
         hipLaunchKernelGGL(add_rmsnorm_quant_kernel<false>, dim3(rows), dim3(kThreads), 0, s, *x, nullptr, gain, D.d,
                            D.eps, m->q8, m->qs);
     NHIP_CHECK_HIP(hipGetLastError());
+    if (act && fuse) {
+        const int32_t rc = launch_decode_swiglu(w, m->q8, m->qs, rows, act, D.ffn, s);
+        if (rc <= 0) {
+            if (rc == 0) *fused = true;
+            return rc;
+        }
+    }
     return nhip_matmul_i8_dev(w, m->q8, m->qs, rows, y, ldy, 0, w->rows, s);
 }
 
@@ -683,7 +690,7 @@ int32_t enqueue_forward(nhip_decoder* m, int rows, int k)
     }
     // the final residual is not needed again: no x_out
     rc = 1;
-    if (fuse) {
+    if (fuse && m->wlm->tiles_n <= kFusedPrologueMaxTiles) {
         DecodePrologue f{kProNorm, x, m->delta, nullptr, m->final_norm, D.eps, 0};
         rc = launch_decode_fused(m->wlm, f, rows, m->logits, D.vocab, s);
         if (rc < 0) return rc;

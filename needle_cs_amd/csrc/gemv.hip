@@ -1264,23 +1264,10 @@ int32_t launch_fmt(const MatmulParams& p, int waves, size_t lds, hipStream_t s)
 }
 
 
-int32_t run_matmul(const DeviceWeights* w, const int8_t* q, const float* scales, const float* offsets,
-                   int32_t stride, int32_t tokens, float* y, int32_t ldy, int32_t row_start,
-                   int32_t row_end, int32_t* dots, hipStream_t stream)
+MatmulParams matmul_params(const DeviceWeights* w, const int8_t* q, const float* scales, const float* offsets,
+                           int32_t stride, int32_t tokens, float* y, int32_t ldy, int32_t row_start, int32_t row_end,
+                           int32_t* dots)
 {
-    NHIP_REQUIRE(w, "weights are NULL");
-    NHIP_REQUIRE(tokens >= 0, "tokens %d < 0", tokens);
-    NHIP_REQUIRE(row_start >= 0 && row_start <= row_end && row_end <= w->rows,
-                 "row range [%d,%d) outside [0,%d)", row_start, row_end, w->rows);
-    if (tokens == 0 || row_start == row_end) return NHIP_OK;
-    NHIP_REQUIRE(q && (scales || dots), "activations are NULL");
-    NHIP_REQUIRE(dots || (y && ldy > 0), "output NULL or ldy %d <= 0", ldy);
-    const bool cq = w->format != WeightFormat::Int8G32;
-    if (cq && !dots)
-        NHIP_REQUIRE(offsets && stride >= w->groups, "offsets NULL or stride %d < groups %d", stride, w->groups);
-    int32_t rc = ensure_device();
-    if (rc) return rc;
-
     MatmulParams p{};
     p.tiles = w->tiles;
     p.norms = w->norms;
@@ -1309,6 +1296,27 @@ int32_t run_matmul(const DeviceWeights* w, const int8_t* q, const float* scales,
     p.x2 = w->split_table[2];
     p.x3 = w->split_table[3];
     p.byte_scale = w->byte_scale;
+    return p;
+}
+
+int32_t run_matmul(const DeviceWeights* w, const int8_t* q, const float* scales, const float* offsets,
+                   int32_t stride, int32_t tokens, float* y, int32_t ldy, int32_t row_start,
+                   int32_t row_end, int32_t* dots, hipStream_t stream)
+{
+    NHIP_REQUIRE(w, "weights are NULL");
+    NHIP_REQUIRE(tokens >= 0, "tokens %d < 0", tokens);
+    NHIP_REQUIRE(row_start >= 0 && row_start <= row_end && row_end <= w->rows,
+                 "row range [%d,%d) outside [0,%d)", row_start, row_end, w->rows);
+    if (tokens == 0 || row_start == row_end) return NHIP_OK;
+    NHIP_REQUIRE(q && (scales || dots), "activations are NULL");
+    NHIP_REQUIRE(dots || (y && ldy > 0), "output NULL or ldy %d <= 0", ldy);
+    const bool cq = w->format != WeightFormat::Int8G32;
+    if (cq && !dots)
+        NHIP_REQUIRE(offsets && stride >= w->groups, "offsets NULL or stride %d < groups %d", stride, w->groups);
+    int32_t rc = ensure_device();
+    if (rc) return rc;
+
+    MatmulParams p = matmul_params(w, q, scales, offsets, stride, tokens, y, ldy, row_start, row_end, dots);
 
     // Waves per 16-row tile (each loads 1/waves of the tile's weight blocks).
     // NHIP_MATMUL_WAVES (4 or 8) overrides the default for tuning.
@@ -1543,6 +1551,21 @@ int32_t matmul_cq_internal(const DeviceWeights* w, const int8_t* values, const f
                            int32_t row_end, hipStream_t stream)
 {
     return run_matmul(w, values, scales, offsets, stride, tokens, y, ldy, row_start, row_end, nullptr, stream);
+}
+
+int32_t launch_decode_swiglu(const DeviceWeights* w, const int8_t* q, const float* qscale, int32_t tokens,
+                             float* act, int32_t ldy, hipStream_t stream)
+{
+    NHIP_REQUIRE(w && w->format == WeightFormat::Int8G32, "weights are not in the int8 format");
+    NHIP_REQUIRE(w->rows % 16 == 0, "SwiGLU pairs need whole 16-row tiles");
+    NHIP_REQUIRE(q && qscale && act && ldy >= w->rows / 2, "SwiGLU matmul: null input/output or ldy %d too small",
+                 ldy);
+    if (tokens < 1 || tokens > 16) return 1;
+    int32_t rc = ensure_device();
+    if (rc) return rc;
+    MatmulParams p = matmul_params(w, q, qscale, nullptr, 0, tokens, act, ldy, 0, w->rows, nullptr);
+    p.swiglu = 1;
+    return try_i8_decode(w, p, stream);
 }
 
 int32_t launch_decode_fused(const DeviceWeights* w, const DecodePrologue& f, int32_t tokens, float* y, int32_t ldy,

@@ -73,6 +73,20 @@ def test_wide_layers_prefill_and_beam(hip, orc):
     lg_c, ic, lpc = cpu.forward(prompt, [0] * 16, np.arange(16), k=3)
     assert np.array_equal(bits(lg_g), bits(lg_c))
     assert np.array_equal(ig, ic)
+    # three decode rows: the gate/up (512 tiles) and head (2000 tiles)
+    # matmuls take the separate norm launch and the plain kernel, the gate/up
+    # one with the SwiGLU chain epilogue; the others fuse their prologues
+    gpu.copy_slot(1, 0, 16)
+    cpu.copy_slot(1, 0, 16)
+    gpu.copy_slot(2, 0, 16)
+    cpu.copy_slot(2, 0, 16)
+    toks = np.array([ig[-1, 0], ig[-1, 1], ig[-1, 2]], dtype=np.int32)
+    for step in range(2):
+        lg_g, ig2, lpg = gpu.forward(toks, [0, 1, 2], [16 + step] * 3, k=3)
+        lg_c, ic2, lpc = cpu.forward(toks, [0, 1, 2], [16 + step] * 3, k=3)
+        assert np.array_equal(bits(lg_g), bits(lg_c)), step
+        assert np.array_equal(ig2, ic2) and np.array_equal(bits(lpg), bits(lpc))
+        toks = ic2[:, 0].copy()
     gpu.close()
     cpu.close()
     gpu = GpuDecoder(model, slots=3, capacity=32, max_rows=16)
