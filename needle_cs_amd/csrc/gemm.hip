@@ -23,12 +23,14 @@
 // Weights are the same re-tiled 1 KB blocks as the decode kernels (one
 // dwordx4 per lane is the B operand of two groups), loaded by each wave for
 // its own tiles.  Activations go through LDS: per stage of 4 blocks (256 K
-// elements) the threads load 64 tokens x 256 bytes in 16-byte units and
-// store each unit with one 16-byte write into an order in which every MFMA
-// A operand is one conflict-free ds_read_b64 and every wave's writes are
-// contiguous.  The LDS stage is double-buffered: the next stage's
-// activations, weights and scales are in flight while the current one is
-// multiplied.
+// elements) 64 tokens x 256 bytes are copied straight from memory into LDS
+// (global_load_lds, 16 bytes per lane, no registers) in an order in which
+// every MFMA A operand is one conflict-free ds_read_b64.  The LDS stage is
+// double-buffered: the next stage's activations, weights and scales are
+// issued at the top of a stage and in flight while the current one is
+// multiplied; one wait and one barrier end the stage.  (Staged through
+// registers, the compiler sank the activation loads to the end of the stage
+// to save registers and exposed their latency every stage.)
 #include <algorithm>
 
 #include "common.hpp"
@@ -42,8 +44,9 @@ typedef unsigned int u4 __attribute__((ext_vector_type(4)));
 constexpr int kTokensPerBlock = 64;
 constexpr int kTilesPerBlock = 8;  // 16-row tiles per workgroup (2 per wave)
 constexpr int kStage = 4;          // weight blocks (2 groups each) per pipeline stage
-constexpr int kSubtileSlots = 66;  // 8-byte slots per (group, subtile) block: 64 + 2 of padding
-constexpr int kStageLds = kStage * 2 * 4 * kSubtileSlots * 8;  // A fragments of one stage (16.5 KB)
+constexpr int kStageLds = kStage * 2 * 4 * 512;  // A fragments of one stage (16 KB)
+// s_waitcnt immediate (gfx9 encoding): vmcnt 0, expcnt and lgkmcnt not waited on
+constexpr int kWaitVmcnt0 = 0x0F70;
 
 struct GemmParams {
     const uint8_t* tiles;
@@ -70,7 +73,7 @@ __device__ __forceinline__ void gemm_i8_body(const GemmParams& p)
     constexpr int TPW = kTilesPerBlock / WAVES;
     constexpr int NT = 64 * WAVES;           // threads
     constexpr int AU = 1024 / NT;            // 16-byte activation units per thread and stage
-    __shared__ __align__(16) uint2 afrag[2][kStageLds / 8];  // [buf][group][subtile][token][kq]
+    __shared__ __align__(16) uint8_t afrag[2][kStageLds];  // [buf][group][subtile] blocks of 512 bytes
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
@@ -94,29 +97,29 @@ __device__ __forceinline__ void gemm_i8_body(const GemmParams& p)
 #pragma unroll
         for (int e = 0; e < 4; e++) qs[i][e] = p.qscale[min(t0 + 16 * i + 4 * kq + e, p.tokens - 1)];
 
-    // activation staging: 16-byte unit u = j*NT + tid of a stage is token
-    // 16*i + t16 (t16 = u%16, i = (u/32)%4), bytes 32*gs + 16*p (p = (u/16)%2,
-    // gs = u/128: group within the stage) of the stage's 256-byte K slice.
-    // LDS order [gs][i][t16][kq] (8 bytes each, each (gs, i) block padded to
-    // 528 bytes so that the paired reads of subtiles i and i+1 fall on
-    // different banks): the unit is k-slices 2p and 2p+1, one 16-byte write,
-    // and lane (t16, kq) of an MFMA reads its A operand from 512 contiguous
-    // bytes.
-    auto load_a = [&](uint4 (&av)[AU], int st) {
+    // Activation staging, straight from memory into LDS (global_load_lds,
+    // no registers): per stage 32 blocks (group gs of the stage, 16-token
+    // subtile i) of 512 bytes, block b = 4*gs + i.  Position x (0..31) of a
+    // block holds the 16 bytes of token 16i + x/2, k-slices 2p and 2p + 1 of
+    // the group, with p = (x & 1) ^ bit 3 of the token ^ (i & 1): the MFMA
+    // A reads (lane (t16, kq): 8 bytes at position 2*t16 + (kq/2 ^ ...),
+    // half kq & 1) then cover all 64 banks in each half-wave, and the paired
+    // reads of subtiles i and i + 1 fall on different banks.  Wave
+    // instruction j of wave w fills blocks 2R and 2R + 1, R = AU*w + j, one
+    // contiguous KB: lane l writes its 16 bytes at 16*l.
+    auto load_a = [&](int buf, int st) {
 #pragma unroll
         for (int j = 0; j < AU; j++) {
-            const int u = j * NT + tid;
-            const int t = min(t0 + ((u >> 5) & 3) * 16 + (u & 15), p.tokens - 1);
-            const int kb = min(st * kStage * 64 + 32 * (u >> 7) + 16 * ((u >> 4) & 1), p.cols - 16);  // past K only in the padded group
-            av[j] = *reinterpret_cast<const uint4*>(p.q + (size_t)t * p.cols + kb);
-        }
-    };
-    auto store_a = [&](const uint4 (&av)[AU], int buf) {
-#pragma unroll
-        for (int j = 0; j < AU; j++) {
-            const int u = j * NT + tid;
-            const int slot = ((u >> 7) * 4 + ((u >> 5) & 3)) * kSubtileSlots + (u & 15) * 4 + 2 * ((u >> 4) & 1);
-            *reinterpret_cast<uint4*>(&afrag[buf][slot]) = av[j];
+            const int R = AU * wave + j;
+            const int b = 2 * R + (lane >> 5);
+            const int gs = b >> 2;
+            const int i = b & 3;
+            const int x = lane & 31;
+            const int rr = x >> 1;
+            const int pp = (x & 1) ^ ((rr >> 3) & 1) ^ (i & 1);
+            const int t = min(t0 + 16 * i + rr, p.tokens - 1);
+            const int kb = min(st * kStage * 64 + 32 * gs + 16 * pp, p.cols - 16);  // past K only in padded groups
+            __builtin_amdgcn_global_load_lds(p.q + (size_t)t * p.cols + kb, &afrag[buf][R * 1024], 16, 0, 0);
         }
     };
     auto load_w = [&](WStage<TPW>& ws, int st) {
@@ -143,8 +146,8 @@ __device__ __forceinline__ void gemm_i8_body(const GemmParams& p)
     auto read_a = [&](long (&av)[4], int buf, int k) {
 #pragma unroll
         for (int i = 0; i < 4; i++) {
-            const uint2 f = afrag[buf][(k * 4 + i) * kSubtileSlots + r * 4 + kq];
-            av[i] = (long)(((uint64_t)f.y << 32) | f.x);
+            const int x = 2 * r + ((kq >> 1) ^ ((r >> 3) & 1) ^ (i & 1));
+            av[i] = *reinterpret_cast<const long*>(&afrag[buf][(k * 4 + i) * 512 + x * 16 + (kq & 1) * 8]);
         }
     };
     auto issue = [&](v4i (&d)[TPW][4], const long (&av)[4], const WStage<TPW>& ws, int k) {
@@ -168,6 +171,7 @@ __device__ __forceinline__ void gemm_i8_body(const GemmParams& p)
                 hs = ref_half_to_single(hbits);
             else
                 hs = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(hbits)));
+            asm volatile("" : "+v"(hs));  // one conversion per scale, then full-rate v_fma_f32
 #pragma unroll
             for (int i = 0; i < 4; i++)
 #pragma unroll
@@ -191,28 +195,27 @@ __device__ __forceinline__ void gemm_i8_body(const GemmParams& p)
         for (int k = 0; k < KG; k++) {
             if (k + 1 < KG) issue(dd[(k + 1) & 1], aa[(k + 1) & 1], ws, k + 1);
             if (k + 2 < KG) read_a(aa[k & 1], buf, k + 2);
-            // groups past the last block (a partial last stage) are computed
-            // on clamped operands and dropped here
-            if (st * kStage + (k >> 1) < p.blocks) epilogue(dd[k & 1], ws, k);
+            // groups past the last block (a partial last stage) run on
+            // clamped operands with the zero scales of the padded scale rows
+            epilogue(dd[k & 1], ws, k);
         }
     };
 
     // pipeline: stage st+1's loads are in flight while stage st is
     // multiplied (the last iteration reloads the last stage, unused)
-    uint4 areg[AU];
     WStage<TPW> wcur, wnext;
-    load_a(areg, 0);
+    load_a(0, 0);
     load_w(wcur, 0);
-    store_a(areg, 0);
+    __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
     __syncthreads();
     for (int st = 0; st < stages; st++) {
         const int buf = st & 1;
         const int nst = min(st + 1, stages - 1);
-        load_a(areg, nst);
+        load_a(buf ^ 1, nst);  // that buffer was last read in the previous stage, before the barrier
         load_w(wnext, nst);
         compute(wcur, buf, st);
-        store_a(areg, buf ^ 1);  // that buffer was last read two stages ago
         wcur = wnext;
+        __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);  // this wave's LDS writes of the next stage have landed
         __syncthreads();
     }
 
