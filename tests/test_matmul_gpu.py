@@ -249,12 +249,12 @@ def run_cq(hip, c, rows, cols, bits, tokens, ldy, r0, r1):
 
 
 @pytest.mark.parametrize("bits", [2, 4])
-@pytest.mark.parametrize("tokens", [1, 2, 3, 4])
+@pytest.mark.parametrize("tokens", [1, 2, 3, 4, 5, 8, 13, 16])
 @pytest.mark.parametrize("r0,r1", [(0, 37), (5, 29), (16, 17)])
 def test_cq_decode_path_row_ranges(hip, orc, bits, tokens, r0, r1):
-    """1..4 tokens run the codebook decode kernel: K = 640 (5 groups, a
-    partial set of four), 2048, 8192 (64 groups) and 16384 (128 groups, the
-    most it takes: 16 per wave)."""
+    """1..4 tokens run the codebook decode kernel, 5..16 the general one: K =
+    640 (5 groups, a partial set of four), 2048, 8192 (64 groups) and 16384
+    (128 groups, 16 per wave, the most the decode kernel takes)."""
     rows = 37
     ldy = rows + 5
     for cols in (640, 2048, 8192, 16384):
@@ -266,11 +266,11 @@ def test_cq_decode_path_row_ranges(hip, orc, bits, tokens, r0, r1):
 
 
 @pytest.mark.parametrize("bits", [2, 4])
-@pytest.mark.parametrize("tokens", [3, 9])
+@pytest.mark.parametrize("tokens", [3, 9, 20])
 def test_cq_special_norm_patterns(hip, orc, bits, tokens):
     """Zero, negative-zero, subnormal and exponent-31 fp16 norms decode as
     Scalar.HalfToSingle does (Scalar.cs:121-128), in the decode kernel (3
-    tokens) and the general one (9)."""
+    tokens) and the general kernel (9 and 20: one and two token blocks)."""
     rows, cols = 64, 2048
     c = cq_case(orc, 777 + tokens + bits, rows, cols, bits, tokens)
     flat = c["norms"]
@@ -284,6 +284,31 @@ def test_cq_special_norm_patterns(hip, orc, bits, tokens):
     want = np.full(tokens * rows, SENTINEL, dtype=np.float32)
     orc.matmul_rows(c["cq"], c["act"], tokens, want, rows, 0, rows)
     assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+@pytest.mark.parametrize("bits", [2, 4])
+@pytest.mark.parametrize("extra", [1, 4])
+def test_cq_wide_tokens_any_stride(hip, orc, bits, extra):
+    """Activation scale rows of any stride >= G (here G + 1, not a multiple
+    of 4, and G + 4) give the reference's bits."""
+    rows, cols, tokens = 48, 2048, 7
+    g = cols // 128
+    c = cq_case(orc, 313 + bits + extra, rows, cols, bits, tokens)
+    stride = g + extra
+    sc = np.zeros((tokens, stride), dtype=np.float32)
+    of = np.zeros((tokens, stride), dtype=np.float32)
+    sc[:, :g] = c["scales"].reshape(tokens, -1)[:, :g]
+    of[:, :g] = c["offsets"].reshape(tokens, -1)[:, :g]
+    weights = hip.Weights.codebook(c["indices"], c["norms"], hip_book(hip, c["book"]), rows, cols, bits)
+    dv = hip.DeviceBuffer.from_array(c["values"])
+    ds = hip.DeviceBuffer.from_array(sc)
+    do = hip.DeviceBuffer.from_array(of)
+    dy = hip.DeviceBuffer.from_array(np.full(tokens * rows, SENTINEL, dtype=np.float32))
+    hip.check(hip.lib().nhip_matmul_cq_dev(weights.handle, dv.ptr, ds.ptr, do.ptr, stride, tokens, dy.ptr, rows, 0,
+                                           rows, None))
+    want = np.full(tokens * rows, SENTINEL, dtype=np.float32)
+    orc.matmul_rows(c["cq"], c["act"], tokens, want, rows, 0, rows)
+    assert np.array_equal(dy.download(np.float32).view(np.uint32), want.view(np.uint32))
 
 
 @pytest.mark.parametrize("bits", [2, 4])
