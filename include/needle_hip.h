@@ -308,6 +308,25 @@ int32_t nhip_decoder_set_head(nhip_decoder* m, const float* embedding, const flo
 int32_t nhip_decoder_forward(nhip_decoder* m, const int32_t* tokens, const int32_t* slots,
                              const int32_t* positions, int32_t rows, float* logits, int32_t k,
                              int32_t* topk_idx, float* topk_lp);
+/* Grammar-constrained greedy step: one forward whose LM head computes only
+ * the 16-row vocab tiles that hold an id allowed by some row's mask
+ * (Engine.LogitsForRows' sparse head, src/Needle/Engine.cs:2191-2195,
+ * 2683-2700), then Ops.ArgMaxMasked per row (src/Needle/Ops.cs:1223-1266):
+ * best[r] = the lowest allowed id holding row r's largest allowed logit
+ * above -inf, or -1.  masks: host [rows][words] bitsets, bit id%32 of word
+ * id/32 (ids from vocab on are ignored); best_logit optional.  rows <= 16.
+ * The allowed logits are bit-identical with the dense head's. */
+int32_t nhip_decoder_forward_masked(nhip_decoder* m, const int32_t* tokens, const int32_t* slots,
+                                    const int32_t* positions, int32_t rows, const uint32_t* masks,
+                                    int32_t words, int32_t* best, float* best_logit);
+/* Ops.ArgMaxMasked (src/Needle/Ops.cs:1223-1266; kernel-table slot 25's
+ * operation) over `rows` device rows: row r reads d_x + r*ldx and the mask
+ * d_mask + r*mask_ld ([words] bitsets, ids >= length ignored) and writes the
+ * chosen id (or -1) to d_index[r] and, if d_value is non-NULL, its value
+ * (-inf for -1).  Asynchronous on `stream`. */
+int32_t nhip_argmax_masked_dev(const float* d_x, int32_t ldx, const uint32_t* d_mask, int32_t mask_ld,
+                               int32_t words, int32_t length, int32_t rows, int32_t* d_index, float* d_value,
+                               void* stream);
 /* Engine.CopyFrom: positions [0, length) of slot src into slot dst. */
 int32_t nhip_decoder_copy_slot(nhip_decoder* m, int32_t dst, int32_t src, int32_t length);
 /* Prefill `prompt` into slot 0, then beam search of `width` beams for up to

@@ -104,6 +104,12 @@ struct DecodePrologue {
 };
 int32_t launch_decode_fused(const DeviceWeights* w, const DecodePrologue& f, int32_t tokens, float* y, int32_t ldy,
                             hipStream_t stream);
+// The decode matmul of int8 rows q restricted to the 16-row tiles holding a
+// row set in some token's mask ([tokens][mask_words] bitsets, bit id%32 of
+// word id/32); the other outputs are left untouched (Engine.LogitsForRows'
+// sparse head, src/Needle/Engine.cs:2683-2700).
+int32_t launch_decode_masked(const DeviceWeights* w, const int8_t* q, const float* qscale, int32_t tokens, float* y,
+                             int32_t ldy, const uint32_t* mask, int32_t mask_words, hipStream_t stream);
 // The decode matmul of int8 rows q (scales qscale) over tile-interleaved
 // gate/up weights, storing the SwiGLU activations at act[t][0 .. rows/2);
 // returns 1 when the decode kernel does not take the shape.

@@ -34,6 +34,7 @@ namespace {
 constexpr int kThreads = 256;
 constexpr int kMaxPerThread = 16;  // d and ffn up to 4096 elements per row
 constexpr int kMaxTopK = 8;
+constexpr int kMaxMaskedRows = 16;  // rows of a masked (sparse-head) forward
 
 constexpr int kGroups4 = 4;        // float4 groups per thread: rows up to 4096 elements
 
@@ -472,6 +473,70 @@ int32_t launch_topk(const float* logits, int rows, int n, int k, const TopkScrat
     return NHIP_OK;
 }
 
+// Ops.ArgMaxMasked per row (src/Needle/Ops.cs:1223-1266): the scalar form
+// scans the allowed ids in ascending order and takes a value only when it is
+// strictly above the best so far (from -inf), so the result is the lowest id
+// holding the largest allowed value above -inf (NaN never is), or -1.  Here
+// each thread keeps the best (value, id) of the ids tid, tid + 256, ...
+// (ascending, strict >), and the block reduces the pairs with "larger value,
+// then lower id", which gives the same id.
+__global__ __launch_bounds__(kThreads) void argmax_masked_kernel(const float* x, int ldx, const uint32_t* mask,
+                                                                 int mask_ld, int words, int length, int32_t* index,
+                                                                 float* value)
+{
+    __shared__ float sv[kThreads / 64];
+    __shared__ int si[kThreads / 64];
+    const int row = blockIdx.x;
+    const int tid = threadIdx.x;
+    const float* xr = x + (size_t)row * ldx;
+    const uint32_t* mr = mask + (size_t)row * mask_ld;
+    const int n = min(length, words * 32);
+    float bv = -INFINITY;
+    int bi = 0x7FFFFFFF;
+    for (int i = tid; i < n; i += kThreads) {
+        if ((mr[i >> 5] >> (i & 31)) & 1u) {
+            const float v = xr[i];
+            if (v > bv) {
+                bv = v;
+                bi = i;
+            }
+        }
+    }
+    auto better = [](float v, int i, float bv2, int bi2) { return v > bv2 || (v == bv2 && i < bi2); };
+    for (int off = 32; off > 0; off >>= 1) {
+        const float ov = __shfl_xor(bv, off);
+        const int oi = __shfl_xor(bi, off);
+        if (better(ov, oi, bv, bi)) {
+            bv = ov;
+            bi = oi;
+        }
+    }
+    if ((tid & 63) == 0) {
+        sv[tid >> 6] = bv;
+        si[tid >> 6] = bi;
+    }
+    __syncthreads();
+    if (tid == 0) {
+        for (int w = 1; w < kThreads / 64; w++)
+            if (better(sv[w], si[w], bv, bi)) {
+                bv = sv[w];
+                bi = si[w];
+            }
+        const bool found = bi != 0x7FFFFFFF;
+        index[row] = found ? bi : -1;
+        if (value) value[row] = found ? bv : -INFINITY;
+    }
+}
+
+int32_t launch_argmax_masked(const float* x, int ldx, const uint32_t* mask, int mask_ld, int words, int length,
+                             int rows, int32_t* index, float* value, hipStream_t s)
+{
+    hipLaunchKernelGGL(argmax_masked_kernel, dim3(rows), dim3(kThreads), 0, s, x, ldx, mask, mask_ld, words, length,
+                       index, value);
+    NHIP_CHECK_HIP(hipGetLastError());
+    return NHIP_OK;
+}
+
 // Copies positions [0, length) of slot src to slot dst in every layer's
 // four cache pools (Engine.CopyFrom).
 __global__ void kv_copy_kernel(int8_t* keys, int8_t* values, float* key_scales, float* value_scales, int slots,
@@ -532,6 +597,14 @@ struct nhip_decoder {
     float* act = nullptr;  // SwiGLU activations [rows][ffn] of the fused gate/up matmul
     float* logits = nullptr;
     int32_t* d_in = nullptr;  // tokens, slots, positions, first (0), count: 5 x max_rows
+    // masked (grammar) head: id bitsets [rows][mask_words] and the chosen ids
+    int32_t mask_words = 0;
+    uint32_t* d_mask = nullptr;
+    int32_t* d_best = nullptr;
+    float* d_best_val = nullptr;
+    uint32_t* h_mask = nullptr;
+    int32_t* h_best = nullptr;
+    float* h_best_val = nullptr;
     int32_t* d_topk_idx = nullptr;
     TopkScratch topk{};  // per (row, block) partial top-k lists, maxima and sums
     float* d_topk_lp = nullptr;
@@ -608,7 +681,7 @@ int32_t norm_matmul(nhip_decoder* m, int rows, float** x, bool pending, const fl
 }
 
 // Enqueues the forward of `rows` rows whose inputs are already in d_in.
-int32_t enqueue_forward(nhip_decoder* m, int rows, int k)
+int32_t enqueue_forward(nhip_decoder* m, int rows, int k, bool masked = false)
 {
     // NHIP_DECODER_FUSED=0 keeps the element-wise kernels separate (for A/B timing)
     static const bool fused_enabled = [] {
@@ -687,6 +760,17 @@ int32_t enqueue_forward(nhip_decoder* m, int rows, int k)
             rc = nhip_matmul_i8_dev(m->wd[l], m->q8, m->qs, rows, m->delta, d, 0, d, s);
             if (rc) return rc;
         }
+    }
+    if (masked) {
+        // the sparse head: the final norm, the LM head over the vocab tiles
+        // that hold an allowed id of some row, and ArgMaxMasked per row
+        hipLaunchKernelGGL(add_rmsnorm_quant_kernel<true>, dim3(rows), dim3(kThreads), 0, s, x, m->delta,
+                           m->final_norm, d, D.eps, m->q8, m->qs);
+        NHIP_CHECK_HIP(hipGetLastError());
+        rc = launch_decode_masked(m->wlm, m->q8, m->qs, rows, m->logits, D.vocab, m->d_mask, m->mask_words, s);
+        if (rc) return rc;
+        return launch_argmax_masked(m->logits, D.vocab, m->d_mask, m->mask_words, m->mask_words, D.vocab, rows,
+                                    m->d_best, m->d_best_val, s);
     }
     // the final residual is not needed again: no x_out
     rc = 1;
@@ -855,6 +939,8 @@ int32_t nhip_decoder_create(const nhip_decoder_dims* dims, nhip_decoder** out)
         (rc = dalloc(m, &m->gu, (size_t)R * 2 * D.ffn)) || (rc = dalloc(m, &m->act, (size_t)R * D.ffn)) || (rc = dalloc(m, &m->logits, (size_t)R * D.vocab)) ||
         (rc = dalloc(m, &m->d_in, (size_t)5 * R)) || (rc = dalloc(m, &m->d_topk_idx, (size_t)R * kMaxTopK)) ||
         (rc = dalloc(m, &m->d_topk_lp, (size_t)R * kMaxTopK)) ||
+        (rc = dalloc(m, &m->d_mask, (size_t)kMaxMaskedRows * ((D.vocab + 31) / 32))) ||
+        (rc = dalloc(m, &m->d_best, (size_t)kMaxMaskedRows)) || (rc = dalloc(m, &m->d_best_val, (size_t)kMaxMaskedRows)) ||
         (rc = dalloc(m, &m->topk.vals, (size_t)R * ((D.vocab + kTopkBlock - 1) / kTopkBlock) * kMaxTopK)) ||
         (rc = dalloc(m, &m->topk.ids, (size_t)R * ((D.vocab + kTopkBlock - 1) / kTopkBlock) * kMaxTopK)) ||
         (rc = dalloc(m, &m->topk.bmax, (size_t)R * ((D.vocab + kTopkBlock - 1) / kTopkBlock))) ||
@@ -868,12 +954,19 @@ int32_t nhip_decoder_create(const nhip_decoder_dims* dims, nhip_decoder** out)
     }
     m->allocations.push_back(ws);
     m->attn_ws = ws;
+    m->mask_words = (D.vocab + 31) / 32;
     if (hipHostMalloc(reinterpret_cast<void**>(&m->h_in), sizeof(int32_t) * 5 * R, hipHostMallocDefault) !=
             hipSuccess ||
         hipHostMalloc(reinterpret_cast<void**>(&m->h_topk_idx), sizeof(int32_t) * R * kMaxTopK,
                       hipHostMallocDefault) != hipSuccess ||
         hipHostMalloc(reinterpret_cast<void**>(&m->h_topk_lp), sizeof(float) * R * kMaxTopK, hipHostMallocDefault) !=
-            hipSuccess) {
+            hipSuccess ||
+        hipHostMalloc(reinterpret_cast<void**>(&m->h_mask), sizeof(uint32_t) * kMaxMaskedRows * ((D.vocab + 31) / 32),
+                      hipHostMallocDefault) != hipSuccess ||
+        hipHostMalloc(reinterpret_cast<void**>(&m->h_best), sizeof(int32_t) * kMaxMaskedRows, hipHostMallocDefault) !=
+            hipSuccess ||
+        hipHostMalloc(reinterpret_cast<void**>(&m->h_best_val), sizeof(float) * kMaxMaskedRows,
+                      hipHostMallocDefault) != hipSuccess) {
         set_error("hipHostMalloc failed");
         return fail(NHIP_ERR_HIP);
     }
@@ -981,6 +1074,55 @@ int32_t nhip_decoder_forward(nhip_decoder* m, const int32_t* tokens, const int32
     if (logits)
         NHIP_CHECK_HIP(hipMemcpy(logits, m->logits, sizeof(float) * rows * m->dims.vocab, hipMemcpyDeviceToHost));
     return NHIP_OK;
+}
+
+int32_t nhip_decoder_forward_masked(nhip_decoder* m, const int32_t* tokens, const int32_t* slots,
+                                    const int32_t* positions, int32_t rows, const uint32_t* masks, int32_t words,
+                                    int32_t* best, float* best_logit)
+{
+    clear_error();
+    int32_t rc = ready(m);
+    if (rc) return rc;
+    NHIP_REQUIRE(rows > 0 && rows <= std::min(m->dims.max_rows, kMaxMaskedRows), "rows %d outside [1, %d]", rows,
+                 std::min(m->dims.max_rows, kMaxMaskedRows));
+    NHIP_REQUIRE(tokens && slots && positions && masks && best && words > 0, "null inputs or words %d <= 0", words);
+    rc = stage_inputs(m, tokens, slots, positions, rows);
+    if (rc) return rc;
+    // ids from vocab on (and words past the caller's) are not allowed
+    const int MW = m->mask_words;
+    const int keep = std::min(words, MW);
+    for (int r = 0; r < rows; r++) {
+        uint32_t* dst = m->h_mask + (size_t)r * MW;
+        std::memcpy(dst, masks + (size_t)r * words, sizeof(uint32_t) * keep);
+        for (int w = keep; w < MW; w++) dst[w] = 0u;
+        const int tail = m->dims.vocab - 32 * (MW - 1);  // valid bits of the last word
+        if (keep == MW && tail < 32) dst[MW - 1] &= (1u << tail) - 1u;
+    }
+    NHIP_CHECK_HIP(hipMemcpyAsync(m->d_mask, m->h_mask, sizeof(uint32_t) * rows * MW, hipMemcpyHostToDevice,
+                                  m->stream));
+    rc = enqueue_forward(m, rows, 0, true);
+    if (rc) return rc;
+    NHIP_CHECK_HIP(hipMemcpyAsync(m->h_best, m->d_best, sizeof(int32_t) * rows, hipMemcpyDeviceToHost, m->stream));
+    NHIP_CHECK_HIP(
+        hipMemcpyAsync(m->h_best_val, m->d_best_val, sizeof(float) * rows, hipMemcpyDeviceToHost, m->stream));
+    NHIP_CHECK_HIP(hipStreamSynchronize(m->stream));
+    std::memcpy(best, m->h_best, sizeof(int32_t) * rows);
+    if (best_logit) std::memcpy(best_logit, m->h_best_val, sizeof(float) * rows);
+    return NHIP_OK;
+}
+
+int32_t nhip_argmax_masked_dev(const float* d_x, int32_t ldx, const uint32_t* d_mask, int32_t mask_ld, int32_t words,
+                               int32_t length, int32_t rows, int32_t* d_index, float* d_value, void* stream)
+{
+    clear_error();
+    NHIP_REQUIRE(rows >= 0 && words >= 0 && length >= 0 && ldx >= 0 && mask_ld >= 0, "negative size");
+    if (rows == 0) return NHIP_OK;
+    NHIP_REQUIRE(d_x && d_mask && d_index, "null pointer");
+    NHIP_REQUIRE(rows == 1 || (ldx >= length && mask_ld >= words),
+                 "row strides (%d floats, %d words) shorter than a row (%d, %d)", ldx, mask_ld, length, words);
+    int32_t rc = ensure_device();
+    if (rc) return rc;
+    return launch_argmax_masked(d_x, ldx, d_mask, mask_ld, words, length, rows, d_index, d_value, as_stream(stream));
 }
 
 int32_t nhip_decoder_copy_slot(nhip_decoder* m, int32_t dst, int32_t src, int32_t length)
@@ -1142,6 +1284,9 @@ int32_t nhip_decoder_destroy(nhip_decoder* m)
     if (m->h_in) (void)hipHostFree(m->h_in);
     if (m->h_topk_idx) (void)hipHostFree(m->h_topk_idx);
     if (m->h_topk_lp) (void)hipHostFree(m->h_topk_lp);
+    if (m->h_mask) (void)hipHostFree(m->h_mask);
+    if (m->h_best) (void)hipHostFree(m->h_best);
+    if (m->h_best_val) (void)hipHostFree(m->h_best_val);
     if (m->stream) (void)hipStreamDestroy(m->stream);
     delete m;
     return NHIP_OK;

@@ -95,6 +95,8 @@ struct MatmulParams {
     int32_t st_bytes;         // int8 path: LDS bytes of the staged activation operands
     int32_t swz;              // decode path, 5..16 tokens: float4-column swizzle mask of the products
     int32_t swiglu;           // fused decode path: rows are (8 gate, 8 up) pairs per tile, store SwiGLU
+    const uint32_t* tile_mask;  // decode kernel: [mask_rows][mask_words] id bitsets; tiles with no set bit
+    int32_t mask_words, mask_rows;  // in any row are skipped (their outputs are left untouched)
     uint32_t t0, t1, t2, t3;  // codebook bytes 0..15
     uint32_t x0, x1, x2, x3;  // the split tables of lut4x (TA, TB)
     float byte_scale;
@@ -706,6 +708,13 @@ __global__ __launch_bounds__(512) void matmul_i8_decode_kernel(MatmulParams p)
     const int g_first = mb0 * 2;
     const u4* wbase = reinterpret_cast<const u4*>(p.tiles) + (size_t)tile * p.blocks * 64 + lane;
     const uint16_t* nrow = p.norms + (size_t)n * p.groups_pad8 + g_first;
+    if (p.tile_mask) {
+        // sparse rows: the tile's 16 ids are bits 16*(tile&1).. of word tile/2
+        uint32_t live = 0;
+        for (int t = 0; t < p.mask_rows; t++)
+            live |= (p.tile_mask[(size_t)t * p.mask_words + (tile >> 1)] >> (16 * (tile & 1))) & 0xFFFFu;
+        if (!live) return;  // uniform over the workgroup
+    }
 
     // 1. activation operands, 2. activation scales, 3. weight scales,
     // 4. weight blocks -- in this order, all in flight together
@@ -1551,6 +1560,26 @@ int32_t matmul_cq_internal(const DeviceWeights* w, const int8_t* values, const f
                            int32_t row_end, hipStream_t stream)
 {
     return run_matmul(w, values, scales, offsets, stride, tokens, y, ldy, row_start, row_end, nullptr, stream);
+}
+
+int32_t launch_decode_masked(const DeviceWeights* w, const int8_t* q, const float* qscale, int32_t tokens, float* y,
+                             int32_t ldy, const uint32_t* mask, int32_t mask_words, hipStream_t stream)
+{
+    NHIP_REQUIRE(w && w->format == WeightFormat::Int8G32, "weights are not in the int8 format");
+    NHIP_REQUIRE(q && qscale && y && mask && ldy >= w->rows, "masked matmul: null pointer or ldy %d too small", ldy);
+    NHIP_REQUIRE(mask_words >= (w->rows + 31) / 32, "masked matmul: %d mask words for %d rows", mask_words, w->rows);
+    int32_t rc = ensure_device();
+    if (rc) return rc;
+    if (tokens >= 1 && tokens <= 16) {
+        MatmulParams p = matmul_params(w, q, qscale, nullptr, 0, tokens, y, ldy, 0, w->rows, nullptr);
+        p.tile_mask = mask;
+        p.mask_words = mask_words;
+        p.mask_rows = tokens;
+        rc = try_i8_decode(w, p, stream);
+        if (rc <= 0) return rc;
+    }
+    // shapes the decode kernel does not take: every row (a superset)
+    return run_matmul(w, q, qscale, nullptr, 0, tokens, y, ldy, 0, w->rows, nullptr, stream);
 }
 
 int32_t launch_decode_swiglu(const DeviceWeights* w, const int8_t* q, const float* qscale, int32_t tokens,

@@ -104,6 +104,19 @@ class GpuDecoder:
                                          _p(lp)))
         return lg, idx[:, :k], lp[:, :k]
 
+    def forward_masked(self, tokens, slots, positions, masks):
+        """One forward with the sparse, masked head: masks [rows][words]
+        uint32 id bitsets; returns the chosen ids (-1: none) and their
+        logits."""
+        rows = len(tokens)
+        t, s, ps = (np.ascontiguousarray(a, dtype=np.int32) for a in (tokens, slots, positions))
+        m = np.ascontiguousarray(masks, dtype=np.uint32).reshape(rows, -1)
+        best = np.zeros(rows, dtype=np.int32)
+        val = np.zeros(rows, dtype=np.float32)
+        check(lib().nhip_decoder_forward_masked(self.h, _p(t), _p(s), _p(ps), rows, _p(m), m.shape[1], _p(best),
+                                                _p(val)))
+        return best, val
+
     def copy_slot(self, dst, src, length):
         check(lib().nhip_decoder_copy_slot(self.h, dst, src, length))
 

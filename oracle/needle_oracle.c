@@ -709,6 +709,27 @@ int or_argmax(const float* x, int n)
     return best;
 }
 
+/* src/Needle/Ops.cs:1236-1266 (ArgMaxMaskedScalar): ids in ascending order,
+ * bit id%32 of mask word id/32, ids >= length skipped; a value replaces the
+ * best only when strictly greater (the first id of the maximum wins, -inf
+ * and NaN never do); -1 when nothing is selected. */
+int or_argmax_masked(const float* x, const uint32_t* mask, int words, int length)
+{
+    int best = -1;
+    float peak = -INFINITY;
+    for (int w = 0; w < words; w++) {
+        uint32_t bits = mask[w];
+        while (bits != 0) {
+            int id = w * 32 + __builtin_ctz(bits);
+            bits &= bits - 1;
+            if (id >= length) continue;
+            float value = x[id];
+            if (value > peak) { peak = value; best = id; }
+        }
+    }
+    return best;
+}
+
 /* src/Needle/Ops.cs:1092-1221, scalar branch (k <= 16) */
 void or_topk_log_softmax(const float* x, int n, int k, int* indices, float* log_probs,
                          float* probs, int mask_special_023)

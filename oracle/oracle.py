@@ -111,6 +111,7 @@ _PROTOS = {
     "or_decoder_copy_slot": (None, [C.POINTER(Decoder), _i, _i, _i]),
     "or_beam_search": (_i, [C.POINTER(Decoder), _vp, _i, _i, _i, _i, _vp, C.POINTER(_f), C.POINTER(C.c_long), _vp]),
     "or_argmax": (_i, [_vp, _i]),
+    "or_argmax_masked": (_i, [_vp, _vp, _i, _i]),
     "or_topk_log_softmax": (None, [_vp, _i, _i, _vp, _vp, _vp, _i]),
     "or_baseline_start": (_i, [_i]),
     "or_baseline_stop": (None, []),

@@ -465,6 +465,53 @@ def test_argmax_first_index(orc):
         assert orc.lib().or_argmax(orc.p(x), 300) == int(np.argmax(x))
 
 
+def masked_argmax_brute(x, mask, words, length):
+    """The largest allowed value that exceeds -inf (NaN never does), then its
+    lowest id: the closed form of Ops.ArgMaxMaskedScalar's ascending scan."""
+    ids = [w * 32 + b for w in range(words) for b in range(32) if (int(mask[w]) >> b) & 1]
+    ids = [i for i in ids if i < length and x[i] > -np.inf]
+    if not ids:
+        return -1
+    peak = max(x[i] for i in ids)
+    return min(i for i in ids if x[i] == peak)
+
+
+def test_argmax_masked_cases(orc):
+    """src/Needle/Ops.cs:1236-1266: ties to the first id, +0 and -0 tie, NaN
+    and -inf never win, ids past length and cleared bits are skipped, an
+    empty selection gives -1."""
+    f = orc.lib().or_argmax_masked
+    x = np.array([1, 7, 7, 3, -0.0, 0.0, np.nan, -np.inf] + [0] * 56, dtype=np.float32)
+    m = np.array([0xFFFFFFFF, 0xFFFFFFFF], dtype=np.uint32)
+    assert f(orc.p(x), orc.p(m), 2, 8) == 1
+    m = np.array([0b11110000, 0], dtype=np.uint32)   # -0, +0, NaN, -inf
+    assert f(orc.p(x), orc.p(m), 2, 8) == 4
+    m = np.array([0b11000000, 0], dtype=np.uint32)   # NaN, -inf only
+    assert f(orc.p(x), orc.p(m), 2, 8) == -1
+    m = np.array([0b1000, 0], dtype=np.uint32)
+    assert f(orc.p(x), orc.p(m), 2, 3) == -1           # id 3 >= length
+    assert f(orc.p(x), orc.p(np.zeros(2, dtype=np.uint32)), 2, 64) == -1
+    y = np.full(64, -np.inf, dtype=np.float32)
+    y[40] = np.inf
+    m = np.array([0, 1 << 8], dtype=np.uint32)
+    assert f(orc.p(y), orc.p(m), 2, 64) == 40
+
+
+def test_argmax_masked_against_brute_force(orc):
+    rng = np.random.default_rng(77)
+    for trial in range(200):
+        n = int(rng.integers(1, 300))
+        words = (n + 31) // 32 + int(rng.integers(0, 2))
+        x = rng.integers(-4, 4, words * 32).astype(np.float32)
+        x[rng.random(x.size) < 0.05] = np.nan
+        x[rng.random(x.size) < 0.05] = -np.inf
+        density = [0.0, 0.01, 0.2, 1.0][trial % 4]
+        bits = rng.random(words * 32) < density
+        mask = np.packbits(bits.reshape(words, 32)[:, ::-1], axis=1).view(">u4").reshape(words).astype(np.uint32)
+        got = orc.lib().or_argmax_masked(orc.p(x), orc.p(mask), words, n)
+        assert got == masked_argmax_brute(x, mask, words, n), trial
+
+
 @pytest.mark.parametrize("mask", [0, 1])
 def test_topk_log_softmax_against_numpy(orc, mask):
     rng = np.random.default_rng(11 + mask)
