@@ -477,15 +477,20 @@ int32_t launch_topk(const float* logits, int rows, int n, int k, const TopkScrat
 // scans the allowed ids in ascending order and takes a value only when it is
 // strictly above the best so far (from -inf), so the result is the lowest id
 // holding the largest allowed value above -inf (NaN never is), or -1.  Here
-// each thread keeps the best (value, id) of the ids tid, tid + 256, ...
-// (ascending, strict >), and the block reduces the pairs with "larger value,
-// then lower id", which gives the same id.
-__global__ __launch_bounds__(kThreads) void argmax_masked_kernel(const float* x, int ldx, const uint32_t* mask,
-                                                                 int mask_ld, int words, int length, int32_t* index,
-                                                                 float* value)
+// each of 1024 threads keeps the best (value, id) of the ids tid, tid + 1024,
+// ... (ascending, strict >; eight ids' mask words and values loaded
+// together), and the block reduces the pairs with "larger value, then lower
+// id", which gives the same id.  Values of ids that are not allowed are
+// loaded but never compared.
+constexpr int kArgmaxThreads = 1024;
+constexpr int kArgmaxBatch = 8;
+
+__global__ __launch_bounds__(kArgmaxThreads) void argmax_masked_kernel(const float* x, int ldx, const uint32_t* mask,
+                                                                       int mask_ld, int words, int length,
+                                                                       int32_t* index, float* value)
 {
-    __shared__ float sv[kThreads / 64];
-    __shared__ int si[kThreads / 64];
+    __shared__ float sv[kArgmaxThreads / 64];
+    __shared__ int si[kArgmaxThreads / 64];
     const int row = blockIdx.x;
     const int tid = threadIdx.x;
     const float* xr = x + (size_t)row * ldx;
@@ -493,11 +498,20 @@ __global__ __launch_bounds__(kThreads) void argmax_masked_kernel(const float* x,
     const int n = min(length, words * 32);
     float bv = -INFINITY;
     int bi = 0x7FFFFFFF;
-    for (int i = tid; i < n; i += kThreads) {
-        if ((mr[i >> 5] >> (i & 31)) & 1u) {
-            const float v = xr[i];
-            if (v > bv) {
-                bv = v;
+    for (int base = tid; base < n; base += kArgmaxThreads * kArgmaxBatch) {
+        uint32_t mw[kArgmaxBatch];
+        float v[kArgmaxBatch];
+#pragma unroll
+        for (int j = 0; j < kArgmaxBatch; j++) {
+            const int i = min(base + j * kArgmaxThreads, n - 1);
+            mw[j] = mr[i >> 5];
+            v[j] = xr[i];
+        }
+#pragma unroll
+        for (int j = 0; j < kArgmaxBatch; j++) {
+            const int i = base + j * kArgmaxThreads;
+            if (i < n && ((mw[j] >> (i & 31)) & 1u) && v[j] > bv) {
+                bv = v[j];
                 bi = i;
             }
         }
@@ -517,7 +531,7 @@ __global__ __launch_bounds__(kThreads) void argmax_masked_kernel(const float* x,
     }
     __syncthreads();
     if (tid == 0) {
-        for (int w = 1; w < kThreads / 64; w++)
+        for (int w = 1; w < kArgmaxThreads / 64; w++)
             if (better(sv[w], si[w], bv, bi)) {
                 bv = sv[w];
                 bi = si[w];
@@ -531,8 +545,8 @@ __global__ __launch_bounds__(kThreads) void argmax_masked_kernel(const float* x,
 int32_t launch_argmax_masked(const float* x, int ldx, const uint32_t* mask, int mask_ld, int words, int length,
                              int rows, int32_t* index, float* value, hipStream_t s)
 {
-    hipLaunchKernelGGL(argmax_masked_kernel, dim3(rows), dim3(kThreads), 0, s, x, ldx, mask, mask_ld, words, length,
-                       index, value);
+    hipLaunchKernelGGL(argmax_masked_kernel, dim3(rows), dim3(kArgmaxThreads), 0, s, x, ldx, mask, mask_ld, words,
+                       length, index, value);
     NHIP_CHECK_HIP(hipGetLastError());
     return NHIP_OK;
 }
@@ -940,7 +954,7 @@ int32_t nhip_decoder_create(const nhip_decoder_dims* dims, nhip_decoder** out)
         (rc = dalloc(m, &m->d_in, (size_t)5 * R)) || (rc = dalloc(m, &m->d_topk_idx, (size_t)R * kMaxTopK)) ||
         (rc = dalloc(m, &m->d_topk_lp, (size_t)R * kMaxTopK)) ||
         (rc = dalloc(m, &m->d_mask, (size_t)kMaxMaskedRows * ((D.vocab + 31) / 32))) ||
-        (rc = dalloc(m, &m->d_best, (size_t)kMaxMaskedRows)) || (rc = dalloc(m, &m->d_best_val, (size_t)kMaxMaskedRows)) ||
+        (rc = dalloc(m, &m->d_best, (size_t)2 * kMaxMaskedRows)) ||
         (rc = dalloc(m, &m->topk.vals, (size_t)R * ((D.vocab + kTopkBlock - 1) / kTopkBlock) * kMaxTopK)) ||
         (rc = dalloc(m, &m->topk.ids, (size_t)R * ((D.vocab + kTopkBlock - 1) / kTopkBlock) * kMaxTopK)) ||
         (rc = dalloc(m, &m->topk.bmax, (size_t)R * ((D.vocab + kTopkBlock - 1) / kTopkBlock))) ||
@@ -955,6 +969,7 @@ int32_t nhip_decoder_create(const nhip_decoder_dims* dims, nhip_decoder** out)
     m->allocations.push_back(ws);
     m->attn_ws = ws;
     m->mask_words = (D.vocab + 31) / 32;
+    m->d_best_val = reinterpret_cast<float*>(m->d_best + kMaxMaskedRows);  // one copy returns both
     if (hipHostMalloc(reinterpret_cast<void**>(&m->h_in), sizeof(int32_t) * 5 * R, hipHostMallocDefault) !=
             hipSuccess ||
         hipHostMalloc(reinterpret_cast<void**>(&m->h_topk_idx), sizeof(int32_t) * R * kMaxTopK,
@@ -963,13 +978,12 @@ int32_t nhip_decoder_create(const nhip_decoder_dims* dims, nhip_decoder** out)
             hipSuccess ||
         hipHostMalloc(reinterpret_cast<void**>(&m->h_mask), sizeof(uint32_t) * kMaxMaskedRows * ((D.vocab + 31) / 32),
                       hipHostMallocDefault) != hipSuccess ||
-        hipHostMalloc(reinterpret_cast<void**>(&m->h_best), sizeof(int32_t) * kMaxMaskedRows, hipHostMallocDefault) !=
-            hipSuccess ||
-        hipHostMalloc(reinterpret_cast<void**>(&m->h_best_val), sizeof(float) * kMaxMaskedRows,
+        hipHostMalloc(reinterpret_cast<void**>(&m->h_best), sizeof(int32_t) * 2 * kMaxMaskedRows,
                       hipHostMallocDefault) != hipSuccess) {
         set_error("hipHostMalloc failed");
         return fail(NHIP_ERR_HIP);
     }
+    m->h_best_val = reinterpret_cast<float*>(m->h_best + kMaxMaskedRows);
     if (hipStreamCreateWithFlags(&m->stream, hipStreamNonBlocking) != hipSuccess) {
         set_error("hipStreamCreate failed");
         return fail(NHIP_ERR_HIP);
@@ -1102,9 +1116,8 @@ int32_t nhip_decoder_forward_masked(nhip_decoder* m, const int32_t* tokens, cons
                                   m->stream));
     rc = enqueue_forward(m, rows, 0, true);
     if (rc) return rc;
-    NHIP_CHECK_HIP(hipMemcpyAsync(m->h_best, m->d_best, sizeof(int32_t) * rows, hipMemcpyDeviceToHost, m->stream));
-    NHIP_CHECK_HIP(
-        hipMemcpyAsync(m->h_best_val, m->d_best_val, sizeof(float) * rows, hipMemcpyDeviceToHost, m->stream));
+    NHIP_CHECK_HIP(hipMemcpyAsync(m->h_best, m->d_best, sizeof(int32_t) * 2 * kMaxMaskedRows, hipMemcpyDeviceToHost,
+                                  m->stream));
     NHIP_CHECK_HIP(hipStreamSynchronize(m->stream));
     std::memcpy(best, m->h_best, sizeof(int32_t) * rows);
     if (best_logit) std::memcpy(best_logit, m->h_best_val, sizeof(float) * rows);
@@ -1286,7 +1299,6 @@ int32_t nhip_decoder_destroy(nhip_decoder* m)
     if (m->h_topk_lp) (void)hipHostFree(m->h_topk_lp);
     if (m->h_mask) (void)hipHostFree(m->h_mask);
     if (m->h_best) (void)hipHostFree(m->h_best);
-    if (m->h_best_val) (void)hipHostFree(m->h_best_val);
     if (m->stream) (void)hipStreamDestroy(m->stream);
     delete m;
     return NHIP_OK;
