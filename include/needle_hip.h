@@ -260,6 +260,38 @@ int32_t nhip_attention_decode_dev(const int8_t* d_q, const float* d_q_scales, in
                                   int32_t max_chunks, void* d_workspace, size_t workspace_bytes,
                                   float* d_out, void* stream);
 
+/* ------------------------------------ Needle 3 attention inputs (rows) -- */
+
+/* Needle 3's step from a row's raw Q/K/V projections to its int8 query heads
+ * and KV-cache row (EngineCore.TapsAndAttentionHeadsSingle,
+ * src/Needle/Engine.cs:1302-1387, and Scalar.Taps3's multi-frame form,
+ * src/Needle/Scalar.cs:285-288): for every query, key and value head the
+ * three-tap convolution over time with the slot's two previous frames
+ * (taps [3][width] per part: current, previous, two back), then for queries
+ * and keys ZeroCenteredRms (q_norm / k_norm [qk_dim], shared by the heads),
+ * Rope at the row's position (cos / sin tables [capacity][qk_dim/2]) and
+ * QuantizeInt8 per head; values QuantizeInt8 per head.  Queries go to
+ * d_q [rows][heads*qk_dim] / d_q_scales [rows][heads]; keys and values to the
+ * cache at (slot, position): keys [slots][capacity][kv_heads*qk_dim],
+ * values [slots][capacity][kv_heads*v_dim], scales [slots][capacity][kv_heads].
+ * d_raw: [rows][qw + kw + vw] (qw = heads*qk_dim, kw = kv_heads*qk_dim,
+ * vw = kv_heads*v_dim); d_history: [slots] x ([2][qw], [2][kw], [2][vw]),
+ * frame 1 the latest, moved on to each slot's last two frames.  The rows of a
+ * slot must be one contiguous run of consecutive positions (a row takes its
+ * previous frames from the rows before it in the run); rows with an
+ * out-of-range slot or position get q = 0, scale 1 and touch nothing.
+ * qk_dim even and <= 64, v_dim <= 64.  Bit-identical with the reference's
+ * scalar row-by-row step on the same tables. */
+int32_t nhip_needle3_attention_inputs_dev(const float* d_raw, int32_t rows, int32_t heads, int32_t kv_heads,
+                                          int32_t qk_dim, int32_t v_dim, const float* d_q_taps,
+                                          const float* d_k_taps, const float* d_v_taps, const float* d_q_norm,
+                                          const float* d_k_norm, const float* d_rope_cos,
+                                          const float* d_rope_sin, float* d_history,
+                                          const int32_t* d_row_slot, const int32_t* d_row_pos, int32_t slots,
+                                          int32_t capacity, int8_t* d_q, float* d_q_scales, int8_t* d_keys,
+                                          float* d_key_scales, int8_t* d_values, float* d_value_scales,
+                                          void* stream);
+
 /* ---------------------------------------------- decode loop (engine) -- */
 
 /* The beam/ragged-batched decode step of a pre-norm int8 decoder (RMSNorm,

@@ -699,6 +699,106 @@ void or_attention_decode(const int8_t* q, const float* q_scales, int rows, int h
     free(outs);
 }
 
+/* ----------------------------------- Needle 3 attention inputs (rows) -- */
+
+/* Scalar.SumOfSquares (src/Needle/Scalar.cs:206-211) and Ops.InverseRms /
+ * ZeroCenteredRms's scalar branch (src/Needle/Ops.cs:209, 233-244):
+ * destination = ((1 + scale) * x) * (1 / sqrt(sum x^2 / n + 1e-6)). */
+void or_zero_centered_rms(const float* x, const float* scale, int n, float* destination)
+{
+    float sum = 0.0f;
+    for (int i = 0; i < n; i++) sum += x[i] * x[i];
+    float inverse = 1.0f / sqrtf(sum / (float)n + 1e-6f);
+    for (int i = 0; i < n; i++) destination[i] = (1.0f + scale[i]) * x[i] * inverse;
+}
+
+/* Scalar.Rope for one head (src/Needle/Scalar.cs:233-248): rotate-half
+ * pairs (i, i + n/2) by the table's cos / sin of the position. */
+void or_rope_rotate(float* x, int n, const float* cos_row, const float* sin_row)
+{
+    int half = n / 2;
+    for (int i = 0; i < half; i++) {
+        float a = x[i], b = x[half + i];
+        x[i] = a * cos_row[i] - b * sin_row[i];
+        x[half + i] = b * cos_row[i] + a * sin_row[i];
+    }
+}
+
+/* EngineCore.TapsAndAttentionHeadsSingle (src/Needle/Engine.cs:1332-1387)
+ * with TapsHead (:1302-1330, scalar branch), one row at a time in order:
+ * for each query head, key head and value head the three-tap convolution of
+ * the current raw frame with the slot's two previous frames
+ *   conv = taps[c] * x_t + taps[W + c] * x_{t-1} + taps[2W + c] * x_{t-2}
+ * (W = the part's width), then for queries and keys ZeroCenteredRms (QNorm /
+ * KNorm, shared by the heads), Rope at the row's position and QuantizeInt8
+ * per head -- queries to q / q_scales, keys to the slot's cache row -- and
+ * for values QuantizeInt8 per head to the cache; then the slot's history
+ * moves on one frame (frame 0 <- frame 1, frame 1 <- the raw row).
+ * raw: [rows][qw + kw + vw]; history: [slots][2][qw], [2][kw], [2][vw]
+ * (frame 1 the latest); rope tables [capacity][qk/2].  Rows whose slot or
+ * position is out of range get q = 0, scale 1 and touch nothing. */
+void or_needle3_attention_inputs(const float* raw, int rows, int heads, int kv_heads, int qk, int vd,
+                                 const float* q_taps, const float* k_taps, const float* v_taps,
+                                 const float* q_norm, const float* k_norm, const float* rope_cos,
+                                 const float* rope_sin, float* history, const int* row_slot, const int* row_pos,
+                                 int slots, int capacity, int8_t* q, float* q_scales, int8_t* keys,
+                                 float* key_scales, int8_t* values, float* value_scales)
+{
+    int qw = heads * qk, kw = kv_heads * qk, vw = kv_heads * vd, all = qw + kw + vw, half = qk / 2;
+    float buf[256];
+    for (int r = 0; r < rows; r++) {
+        int slot = row_slot[r], pos = row_pos[r];
+        const float* x = raw + (long)r * all;
+        if (slot < 0 || slot >= slots || pos < 0 || pos >= capacity) {
+            memset(q + (long)r * qw, 0, (size_t)qw);
+            for (int h = 0; h < heads; h++) q_scales[(long)r * heads + h] = 1.0f;
+            continue;
+        }
+        float* hist = history + (long)slot * 2 * all;
+        const float* cs = rope_cos + (long)pos * half;
+        const float* sn = rope_sin + (long)pos * half;
+        int parts[3] = {qw, kw, vw};
+        const float* taps[3] = {q_taps, k_taps, v_taps};
+        int base = 0;
+        for (int part = 0; part < 3; part++) {
+            int W = parts[part], n = part == 2 ? vd : qk, count = W / n;
+            const float* cur = x + base;
+            const float* f0 = hist + 2 * base;
+            const float* f1 = f0 + W;
+            for (int h = 0; h < count; h++) {
+                int off = h * n;
+                for (int c = 0; c < n; c++)
+                    buf[c] = taps[part][off + c] * cur[off + c] + taps[part][W + off + c] * f1[off + c] +
+                             taps[part][2 * W + off + c] * f0[off + c];
+                if (part == 0) {
+                    or_zero_centered_rms(buf, q_norm, n, buf);
+                    or_rope_rotate(buf, n, cs, sn);
+                    q_scales[(long)r * heads + h] = or_quantize_int8(buf, n, q + (long)r * qw + off);
+                } else if (part == 1) {
+                    or_zero_centered_rms(buf, k_norm, n, buf);
+                    or_rope_rotate(buf, n, cs, sn);
+                    long cell = (long)slot * capacity + pos;
+                    key_scales[cell * kv_heads + h] = or_quantize_int8(buf, n, keys + cell * kw + off);
+                } else {
+                    long cell = (long)slot * capacity + pos;
+                    value_scales[cell * kv_heads + h] = or_quantize_int8(buf, n, values + cell * vw + off);
+                }
+            }
+            base += W;
+        }
+        /* the history moves on one frame */
+        base = 0;
+        for (int part = 0; part < 3; part++) {
+            int W = parts[part];
+            float* f0 = hist + 2 * base;
+            float* f1 = f0 + W;
+            memcpy(f0, f1, sizeof(float) * W);
+            memcpy(f1, x + base, sizeof(float) * W);
+            base += W;
+        }
+    }
+}
+
 /* ---------------------------------------------------------- selection -- */
 
 /* src/Needle/Ops.cs:1086-1089 */

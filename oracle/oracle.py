@@ -111,6 +111,10 @@ _PROTOS = {
     "or_decoder_copy_slot": (None, [C.POINTER(Decoder), _i, _i, _i]),
     "or_beam_search": (_i, [C.POINTER(Decoder), _vp, _i, _i, _i, _i, _vp, C.POINTER(_f), C.POINTER(C.c_long), _vp]),
     "or_argmax": (_i, [_vp, _i]),
+    "or_zero_centered_rms": (None, [_vp, _vp, _i, _vp]),
+    "or_rope_rotate": (None, [_vp, _i, _vp, _vp]),
+    "or_needle3_attention_inputs": (None, [_vp, _i, _i, _i, _i, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
+                                           _vp, _i, _i, _vp, _vp, _vp, _vp, _vp, _vp]),
     "or_argmax_masked": (_i, [_vp, _vp, _i, _i]),
     "or_topk_log_softmax": (None, [_vp, _i, _i, _vp, _vp, _vp, _i]),
     "or_baseline_start": (_i, [_i]),

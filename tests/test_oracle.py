@@ -465,6 +465,91 @@ def test_argmax_first_index(orc):
         assert orc.lib().or_argmax(orc.p(x), 300) == int(np.argmax(x))
 
 
+def test_zero_centered_rms_against_float64(orc):
+    """Ops.ZeroCenteredRms (src/Needle/Ops.cs:209, 233-244): (1 + scale) * x /
+    sqrt(mean(x^2) + 1e-6), within a few float32 roundings of float64."""
+    rng = np.random.default_rng(21)
+    for n in (48, 64, 7):
+        x = (rng.standard_normal(n) * 3).astype(np.float32)
+        sc = (rng.standard_normal(n) * 0.2).astype(np.float32)
+        out = np.zeros(n, np.float32)
+        orc.lib().or_zero_centered_rms(orc.p(x), orc.p(sc), n, orc.p(out))
+        x64 = x.astype(np.float64)
+        want = (1 + sc.astype(np.float64)) * x64 / np.sqrt(np.mean(x64 * x64) + 1e-6)
+        assert np.max(np.abs(out - want)) <= 4e-7 * np.max(np.abs(want))
+
+
+def test_rope_rotate_is_a_rotation(orc):
+    """Scalar.Rope (src/Needle/Scalar.cs:233-248): pairs (i, i + n/2) rotate by
+    the table's angle (float64 check), and the pair norms are kept."""
+    rng = np.random.default_rng(22)
+    n = 48
+    x = rng.standard_normal(n).astype(np.float32)
+    ang = rng.uniform(0, 6.3, n // 2)
+    cs, sn = np.cos(ang).astype(np.float32), np.sin(ang).astype(np.float32)
+    y = x.copy()
+    orc.lib().or_rope_rotate(orc.p(y), n, orc.p(cs), orc.p(sn))
+    z = (x[:24] + 1j * x[24:]).astype(np.complex128) * (cs.astype(np.float64) + 1j * sn.astype(np.float64))
+    assert np.allclose(y[:24], z.real, atol=1e-6) and np.allclose(y[24:], z.imag, atol=1e-6)
+    assert np.allclose(np.hypot(y[:24], y[24:]), np.hypot(x[:24], x[24:]), rtol=1e-5)
+
+
+def test_needle3_attention_inputs_against_float64(orc):
+    """The row step (src/Needle/Engine.cs:1302-1387): taps over the history,
+    norm, rotation and per-head quantization match a float64 computation to
+    one int8 step, and the history moves on one frame."""
+    rng = np.random.default_rng(23)
+    heads, kv, qk, vd, slots, cap = 4, 2, 48, 64, 2, 8
+    qw, kw, vw = heads * qk, kv * qk, kv * vd
+    allw = qw + kw + vw
+    f = lambda *s: rng.standard_normal(s).astype(np.float32)
+    taps = [f(3, qw), f(3, kw), f(3, vw)]
+    qn, kn = f(qk) * 0.1, f(qk) * 0.1
+    ang = rng.uniform(0, 6.3, (cap, qk // 2))
+    cs, sn = np.cos(ang).astype(np.float32), np.sin(ang).astype(np.float32)
+    hist = f(slots, 2 * allw)
+    raw = f(1, allw)
+    q = np.zeros((1, qw), np.int8)
+    qs = np.zeros((1, heads), np.float32)
+    keys, values = np.zeros((slots, cap, kw), np.int8), np.zeros((slots, cap, vw), np.int8)
+    ks, vs = np.zeros((slots, cap, kv), np.float32), np.zeros((slots, cap, kv), np.float32)
+    h0 = hist.copy()
+    rsl, rps = np.array([1], np.int32), np.array([3], np.int32)
+    orc.lib().or_needle3_attention_inputs(orc.p(raw), 1, heads, kv, qk, vd, orc.p(taps[0]), orc.p(taps[1]),
+                                          orc.p(taps[2]), orc.p(qn), orc.p(kn), orc.p(cs), orc.p(sn), orc.p(hist),
+                                          orc.p(rsl), orc.p(rps), slots, cap, orc.p(q), orc.p(qs), orc.p(keys),
+                                          orc.p(ks), orc.p(values), orc.p(vs))
+    d = lambda a: a.astype(np.float64)
+    hs = d(h0[1])
+    def conv(part_base, W, t):
+        f0, f1 = hs[2 * part_base:2 * part_base + W], hs[2 * part_base + W:2 * part_base + 2 * W]
+        cur = d(raw[0, part_base:part_base + W])
+        return d(t[0]) * cur + d(t[1]) * f1 + d(t[2]) * f0
+    def norm_rope(x, sc):
+        y = (1 + d(sc)) * x / np.sqrt(np.mean(x * x) + 1e-6)
+        a, b = y[:qk // 2], y[qk // 2:]
+        c_, s_ = d(cs[3]), d(sn[3])
+        return np.concatenate([a * c_ - b * s_, b * c_ + a * s_])
+    def check(x, qv, scale):
+        want = np.clip(np.round(x / (np.max(np.abs(x)) / 127)), -128, 127)
+        assert np.max(np.abs(qv.astype(np.int32) - want)) <= 1
+        assert abs(scale - np.max(np.abs(x)) / 127) <= 1e-5 * abs(scale)
+    cq = conv(0, qw, taps[0])
+    for h in range(heads):
+        check(norm_rope(cq[h * qk:(h + 1) * qk], qn), q[0, h * qk:(h + 1) * qk], qs[0, h])
+    ck = conv(qw, kw, taps[1])
+    for h in range(kv):
+        check(norm_rope(ck[h * qk:(h + 1) * qk], kn), keys[1, 3, h * qk:(h + 1) * qk], ks[1, 3, h])
+    cv = conv(qw + kw, vw, taps[2])
+    for h in range(kv):
+        check(cv[h * vd:(h + 1) * vd], values[1, 3, h * vd:(h + 1) * vd], vs[1, 3, h])
+    new = hist[1]
+    for base, W in ((0, qw), (qw, kw), (qw + kw, vw)):
+        assert np.array_equal(new[2 * base:2 * base + W], h0[1, 2 * base + W:2 * base + 2 * W])
+        assert np.array_equal(new[2 * base + W:2 * base + 2 * W], raw[0, base:base + W])
+    assert np.array_equal(hist[0], h0[0])
+
+
 def masked_argmax_brute(x, mask, words, length):
     """The largest allowed value that exceeds -inf (NaN never does), then its
     lowest id: the closed form of Ops.ArgMaxMaskedScalar's ascending scan."""
