@@ -1,7 +1,7 @@
 """GPU parity of the prefill matmul (literal int8, 32+ tokens) against the
 oracle: the exact path (nhip_matmul_i8_dev) is bit-identical with
 Scalar.MatMulRows' order; the fused epilogue (nhip_matmul_i8_fused_dev) is
-within the north-star tolerance, max|y - y_ref| <= 1e-4 * RMS(y_ref)."""
+within the required tolerance, max|y - y_ref| <= 1e-4 * RMS(y_ref)."""
 import numpy as np
 import pytest
 

@@ -2,7 +2,7 @@
 and multi-block token counts) through the C ABI against the oracle.
 
 Bar: the int32 group sums are bit-exact; the fp32 outputs are bit-exact too,
-because the kernel keeps Scalar.MatMulRows' epilogue order (the north-star
+because the kernel keeps Scalar.MatMulRows' epilogue order (the required
 tolerance, max-abs-error <= 1e-4 * RMS(y), is asserted as well)."""
 import ctypes as C
 
