@@ -396,7 +396,12 @@ template <int K>
 __global__ __launch_bounds__(64) void topk_final_kernel(const float* bvals, const int32_t* bids, const float* bmax,
                                                          const float* bsum, int blocks, int32_t* idx, float* lp)
 {
-    if (threadIdx.x != 0) return;
+    // the 64 threads stage the row's candidates (and below the block maxima
+    // and sums) in LDS, 256 at a time; thread 0 walks them in order
+    constexpr int kChunk = 256;
+    __shared__ float sv[kChunk];
+    __shared__ int si[kChunk];
+    const int tid = threadIdx.x;
     const int row = blockIdx.x;
     float bv[K];
     int bi[K];
@@ -406,27 +411,49 @@ __global__ __launch_bounds__(64) void topk_final_kernel(const float* bvals, cons
         bi[m] = 0x7FFFFFFF;
     }
     const size_t base = (size_t)row * blocks;
-    for (int c = 0; c < blocks * K; c++) {
-        const float v = bvals[base * K + c];
-        const int i = bids[base * K + c];
-        if (!before(v, i, bv[K - 1], bi[K - 1])) continue;
-        bv[K - 1] = v;
-        bi[K - 1] = i;
+    const int n = blocks * K;
+    for (int c0 = 0; c0 < n; c0 += kChunk) {
+        const int cnt = min(kChunk, n - c0);
+        for (int j = tid; j < cnt; j += 64) {
+            sv[j] = bvals[base * K + c0 + j];
+            si[j] = bids[base * K + c0 + j];
+        }
+        __syncthreads();
+        for (int c = 0; tid == 0 && c < cnt; c++) {
+            const float v = sv[c];
+            const int i = si[c];
+            if (!before(v, i, bv[K - 1], bi[K - 1])) continue;
+            bv[K - 1] = v;
+            bi[K - 1] = i;
 #pragma unroll
-        for (int m = K - 1; m > 0; m--) {
-            if (before(bv[m], bi[m], bv[m - 1], bi[m - 1])) {
-                const float fv = bv[m];
-                const int fi = bi[m];
-                bv[m] = bv[m - 1];
-                bi[m] = bi[m - 1];
-                bv[m - 1] = fv;
-                bi[m - 1] = fi;
+            for (int m = K - 1; m > 0; m--) {
+                if (before(bv[m], bi[m], bv[m - 1], bi[m - 1])) {
+                    const float fv = bv[m];
+                    const int fi = bi[m];
+                    bv[m] = bv[m - 1];
+                    bi[m] = bi[m - 1];
+                    bv[m - 1] = fv;
+                    bi[m - 1] = fi;
+                }
             }
         }
+        __syncthreads();
     }
-    const float peak = bv[0];
+    // log-sum-exp over the blocks in ascending order (sv: maxima, si: sums)
     float total = 0.0f;
-    for (int b = 0; b < blocks; b++) total = total + exp_poly(bmax[base + b] - peak) * bsum[base + b];
+    for (int b0 = 0; b0 < blocks; b0 += kChunk) {
+        const int cnt = min(kChunk, blocks - b0);
+        for (int j = tid; j < cnt; j += 64) {
+            sv[j] = bmax[base + b0 + j];
+            si[j] = __float_as_int(bsum[base + b0 + j]);
+        }
+        __syncthreads();
+        const float peak = bv[0];
+        for (int b = 0; tid == 0 && b < cnt; b++) total = total + exp_poly(sv[b] - peak) * __int_as_float(si[b]);
+        __syncthreads();
+    }
+    if (tid != 0) return;
+    const float peak = bv[0];
     const float log_shift = peak + log_poly(total);
 #pragma unroll
     for (int m = 0; m < K; m++) {
