@@ -434,6 +434,206 @@ __global__ __launch_bounds__(64) void decode_merge_kernel(DecodeAttnParams p)
     *dst = sum * (1.0f / total);
 }
 
+// Whole-row attention for caches of at most kRowMaxCapacity positions: one
+// workgroup per (row, query head) runs every chunk of the row's plan and then
+// merges them itself, with the chunk kernel's per-chunk arithmetic and
+// decode_merge_kernel's merge, so the results are the same bits.  For short
+// contexts the chunk kernel's grid is small (a few chunks per row, all heads
+// in one workgroup) and the merge is a second launch; here the (row, head)
+// grid is wider and there is one launch.
+//   phase 1: thread per (position, 16-byte key piece), v_dot4 + quad DPP sum;
+//            chunk peaks by LDS atomicMax on order keys
+//   phase 3: e_s and e_s * valueScale_s
+//   phase 4: thread per (chunk, 4 value dims) walks the chunk's positions
+//   merge:   wave 0, one lane per dim, chunks in ascending order
+constexpr int kRowMaxCapacity = 512;
+constexpr int kRowMaxChunks = kRowMaxCapacity / 16;  // the plan makes at most count/16 chunks
+constexpr int kRowUnits = kRowMaxCapacity * 4 / kThreads;  // key pieces per thread
+
+__global__ __launch_bounds__(kThreads) void decode_attention_row_kernel(DecodeAttnParams p)
+{
+    __shared__ __align__(16) float score[kRowMaxCapacity];  // scores, then e_s
+    __shared__ __align__(16) float wl[kRowMaxCapacity];     // e_s * valueScale_s
+    __shared__ float vsc[kRowMaxCapacity];
+    __shared__ __align__(16) float part[kRowMaxChunks * 64];
+    __shared__ uint32_t peak_key[kRowMaxChunks];
+    __shared__ float csum[kRowMaxChunks];
+    __shared__ float cwt[kRowMaxChunks];
+    __shared__ __align__(16) uint32_t q_lds[16];
+
+    const int row = blockIdx.x;
+    const int h = blockIdx.y;
+    const int tid = threadIdx.x;
+    const int kv = h / (p.heads / p.kv_heads);
+    const int slot = p.row_slot[row];
+    const int first = p.row_first[row];
+    const int count = p.row_count[row];
+    float* dst = p.out + ((size_t)row * p.heads + h) * 64;
+    const bool valid = slot >= 0 && slot < p.slots && first >= 0 && count >= 1 && count <= p.capacity - first;
+    if (!valid) {
+        if (tid < 16) *reinterpret_cast<float4*>(dst + 4 * tid) = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        return;
+    }
+    int length;
+    const int needed = plan(count, p.max_chunks, &length);  // count <= capacity <= 512: needed <= 32
+    const uint32_t mag_len = magic((uint32_t)length);       // s < 512: s / length is exact
+    const size_t pos0 = (size_t)slot * p.capacity + first;
+    const int qk = p.qk;
+    const int pieces = qk / 16;
+
+    const uint32_t qword = tid < qk / 4 ? reinterpret_cast<const uint32_t*>(p.q + ((size_t)row * p.heads + h) * qk)[tid]
+                                        : 0u;
+    const float qsc = p.qscale[(size_t)row * p.heads + h] * p.inv_sqrt;
+
+    // phase 4's value dwords of the first kVBlock positions of this thread's
+    // chunk, issued ahead of the key rows
+    const int vj = tid & 15;
+    const size_t vstride4 = (size_t)p.kv_heads * 16;  // dwords per cache position
+    auto vbase = [&](int c) {
+        return reinterpret_cast<const uint32_t*>(p.values) + ((pos0 + (size_t)c * length) * p.kv_heads + kv) * 16 + vj;
+    };
+    uint32_t vreg[kVBlock];
+    {
+        const int c = tid >> 4;
+        if (c < needed) {
+            const int L = min(length, count - c * length);
+            const uint32_t* vp = vbase(c);
+#pragma unroll
+            for (int j = 0; j < kVBlock; j++) vreg[j] = vp[(size_t)min(j, L - 1) * vstride4];
+        }
+    }
+
+    // phase 1: scores
+    const int units = count * 4;
+    const int lslot = tid & 3;
+    const int qslot = min(lslot, pieces - 1);
+    const float* sbase = (lslot & 1) ? p.vscale : p.kscale;  // slot 0 the key scale, slot 1 the value scale
+    uint4 kw[kRowUnits];
+    float sv[kRowUnits];
+#pragma unroll
+    for (int k = 0; k < kRowUnits; k++) {
+        if (k * kThreads >= units) break;  // uniform
+        const int u = min(k * kThreads + tid, units - 1);
+        const size_t cell = (pos0 + (u >> 2)) * p.kv_heads + kv;
+        kw[k] = *reinterpret_cast<const uint4*>(p.keys + cell * qk + 16 * qslot);
+        sv[k] = sbase[cell];
+    }
+    if (tid < 16) q_lds[tid] = qword;
+    if (tid < kRowMaxChunks) peak_key[tid] = order_key(-INFINITY);
+    __syncthreads();
+    const uint4 qv = *reinterpret_cast<const uint4*>(q_lds + 4 * qslot);
+#pragma unroll
+    for (int k = 0; k < kRowUnits; k++) {
+        if (k * kThreads >= units) break;  // uniform
+        const int u = k * kThreads + tid;
+        const bool ok = u < units;  // whole aligned 4-lane groups
+        const int s = min(u, units - 1) >> 2;
+        int d4 = 0;
+        d4 = __builtin_amdgcn_sdot4((int)qv.x, (int)kw[k].x, d4, false);
+        d4 = __builtin_amdgcn_sdot4((int)qv.y, (int)kw[k].y, d4, false);
+        d4 = __builtin_amdgcn_sdot4((int)qv.z, (int)kw[k].z, d4, false);
+        d4 = __builtin_amdgcn_sdot4((int)qv.w, (int)kw[k].w, d4, false);
+        d4 = lslot < pieces ? d4 : 0;
+        d4 += __builtin_amdgcn_mov_dpp(d4, 0xB1, 0xF, 0xF, false);
+        d4 += __builtin_amdgcn_mov_dpp(d4, 0x4E, 0xF, 0xF, false);
+        if (ok && lslot == 0) {
+            const float sc = (static_cast<float>(d4) * sv[k]) * qsc;
+            score[s] = sc;
+            atomicMax(&peak_key[fast_div(s, mag_len)], order_key(sc));
+        }
+        if (ok && lslot == 1) vsc[s] = sv[k];
+    }
+    __syncthreads();
+
+    // phase 3
+    for (int s = tid; s < count; s += kThreads) {
+        const float e = exp_poly(score[s] - order_value(peak_key[fast_div(s, mag_len)]));
+        score[s] = e;
+        wl[s] = e * vsc[s];
+    }
+    __syncthreads();
+
+    // phase 4: chunk c's sums in ascending positions
+    for (int c0 = 0; c0 < needed; c0 += kThreads / 16) {
+        const int c = c0 + (tid >> 4);
+        if (c >= needed) break;
+        const int b = c * length;
+        const int L = min(length, count - b);
+        const uint32_t* vp = vbase(c);
+        float o0 = 0.0f, o1 = 0.0f, o2 = 0.0f, o3 = 0.0f, total = 0.0f;
+        auto step = [&](float e, float w, uint32_t v) {
+            total = total + e;
+            o0 = o0 + w * sx8(v, 0);
+            o1 = o1 + w * sx8(v, 1);
+            o2 = o2 + w * sx8(v, 2);
+            o3 = o3 + w * sx8(v, 3);
+        };
+        for (int s0 = 0; s0 < L; s0 += kVBlock) {
+            if (s0 > 0 || c0 > 0) {
+#pragma unroll
+                for (int j = 0; j < kVBlock; j++) vreg[j] = vp[(size_t)min(s0 + j, L - 1) * vstride4];
+            }
+#pragma unroll
+            for (int j4 = 0; j4 < kVBlock; j4 += 4) {
+                if (s0 + j4 >= L) break;
+                const float4 e4 = *reinterpret_cast<const float4*>(score + b + s0 + j4);
+                const float4 w4 = *reinterpret_cast<const float4*>(wl + b + s0 + j4);
+                const int rem = L - (s0 + j4);
+                step(e4.x, w4.x, vreg[j4]);
+                if (rem > 1) step(e4.y, w4.y, vreg[j4 + 1]);
+                if (rem > 2) step(e4.z, w4.z, vreg[j4 + 2]);
+                if (rem > 3) step(e4.w, w4.w, vreg[j4 + 3]);
+            }
+        }
+        if (needed == 1) {
+            // the merge of a single partial, as in the chunk kernel
+            const float pk = order_value(peak_key[0]);
+            const float w = exp_poly(pk - pk);
+            float tot = 0.0f;
+            tot = tot + w * total;
+            const float inverse = 1.0f / tot;
+            *reinterpret_cast<float4*>(dst + 4 * vj) =
+                make_float4((0.0f + w * o0) * inverse, (0.0f + w * o1) * inverse, (0.0f + w * o2) * inverse,
+                            (0.0f + w * o3) * inverse);
+        } else {
+            *reinterpret_cast<float4*>(part + c * 64 + 4 * vj) = make_float4(o0, o1, o2, o3);
+            if (vj == 0) csum[c] = total;
+        }
+    }
+    if (needed == 1) return;  // uniform
+    __syncthreads();
+
+    // merge: decode_merge_kernel's arithmetic.  Every wave finds the same
+    // peak; thread c < needed writes chunk c's weight.
+    const int d = tid & 63;
+    const float pkd = d < needed ? order_value(peak_key[d]) : -INFINITY;
+    float peak = -INFINITY;
+    if (d < needed) peak = ref_max(peak, pkd);
+    peak = wave_max(peak);
+    if (tid < needed) cwt[tid] = exp_poly(pkd - peak);
+    __syncthreads();
+    if (tid >= 64) return;
+    if (needed == 2) {  // MergePartials' two-chunk branch
+        const float peak0 = __shfl(pkd, 0), peak1 = __shfl(pkd, 1);
+        const float pk2 = ref_max(peak0, peak1);
+        const float w0 = exp_poly(peak0 - pk2);
+        const float w1 = exp_poly(peak1 - pk2);
+        float tot = 0.0f;
+        tot = tot + w0 * csum[0];
+        tot = tot + w1 * csum[1];
+        const float inv = 1.0f / tot;
+        dst[d] = (w0 * part[d] + w1 * part[64 + d]) * inv;
+        return;
+    }
+    float total = 0.0f, sum = 0.0f;
+    for (int c = 0; c < needed; c++) {
+        const float w = cwt[c];
+        total = total + w * csum[c];
+        sum = sum + w * part[c * 64 + d];
+    }
+    dst[d] = sum * (1.0f / total);
+}
+
 __global__ void zero_kernel(uint32_t* p, size_t n)
 {
     for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)
@@ -528,6 +728,11 @@ int32_t attention_decode_impl(const int8_t* d_q, const float* d_qscale, int32_t 
     const int head_blocks = (kv_heads + p.kv_per_block - 1) / p.kv_per_block;
     NHIP_REQUIRE(!d_q_out || (d_qs_out && max_chunks == 1 && head_blocks == 1),
                  "attention: a quantized output needs max_chunks 1 and all heads in one block");
+    if (!d_q_out && capacity <= kRowMaxCapacity) {  // every count <= capacity: one workgroup per (row, head)
+        hipLaunchKernelGGL(decode_attention_row_kernel, dim3(rows, heads), dim3(kThreads), 0, stream, p);
+        NHIP_CHECK_HIP(hipGetLastError());
+        return NHIP_OK;
+    }
     hipLaunchKernelGGL(decode_attention_kernel, dim3(max_chunks, rows, head_blocks), dim3(kThreads), lds, stream, p);
     NHIP_CHECK_HIP(hipGetLastError());
     if (max_chunks > 1) {  // single-chunk plans are finished by the chunk kernel

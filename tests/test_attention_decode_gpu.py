@@ -66,15 +66,33 @@ def test_decode_attention_bit_exact(hip, orc, heads, kv_heads, qk, max_chunks):
     assert bit_equal(got, want)
 
 
+@pytest.mark.parametrize("capacity", [256, 600])
 @pytest.mark.parametrize("heads,kv_heads,qk", [(16, 16, 64), (6, 2, 48)])
-def test_decode_attention_single_chunk_plan(hip, orc, heads, kv_heads, qk):
-    """max_chunks 1: every row is one chunk finished by the chunk kernel (the
-    merge of one partial), no merge launch."""
-    cache = Cache(orc, hip, 31 + heads, 3, 256, kv_heads, qk)
+def test_decode_attention_single_chunk_plan(hip, orc, heads, kv_heads, qk, capacity):
+    """max_chunks 1: every row is one chunk, finished with the merge of one
+    partial, no merge launch (capacity 256: the whole-row kernel; 600: the
+    chunk kernel)."""
+    cache = Cache(orc, hip, 31 + heads, 3, capacity, kv_heads, qk)
     spec = [(0, 0, 1), (1, 3, 17), (2, 0, 256), (0, 100, 99), (1, 0, 192)]
     q, qs = queries(orc, cache.st, len(spec), heads, qk)
     got, _ = run_decode(hip, cache, q, qs, heads, spec, 1)
     assert bit_equal(got, oracle_decode(orc, cache, q, qs, heads, spec, 1))
+
+
+@pytest.mark.parametrize("heads,kv_heads,qk", [(16, 16, 64), (12, 2, 48), (4, 1, 64), (8, 8, 48)])
+@pytest.mark.parametrize("capacity,max_chunks", [(512, 1), (512, 2), (512, 8), (512, 64), (192, 64), (513, 64)])
+def test_decode_attention_short_cache_bit_exact(hip, orc, heads, kv_heads, qk, capacity, max_chunks):
+    """Caches of at most 512 positions take the whole-row kernel (one
+    workgroup per (row, head) runs every chunk and the merge); 513 takes the
+    chunk kernel and its merge launch.  Counts cover one chunk, the two-chunk
+    merge branch, uneven last chunks and the full cache."""
+    cache = Cache(orc, hip, 77 + heads + qk + capacity + max_chunks, 3, capacity, kv_heads, qk)
+    spec = [(0, 0, 1), (1, 0, 2), (2, 5, 15), (0, 0, 16), (1, 7, 17), (2, 0, 31), (0, 1, 32), (1, 0, 33),
+            (2, 0, 47), (0, 10, 48), (1, 0, 100), (2, 3, 129), (0, 0, 160), (1, 0, 191), (2, 0, capacity),
+            (0, capacity - 1, 1), (1, capacity // 2, capacity - capacity // 2)]
+    q, qs = queries(orc, cache.st, len(spec), heads, qk)
+    got, _ = run_decode(hip, cache, q, qs, heads, spec, max_chunks)
+    assert bit_equal(got, oracle_decode(orc, cache, q, qs, heads, spec, max_chunks))
 
 
 def test_decode_attention_several_head_blocks(hip, orc):
@@ -103,8 +121,7 @@ def test_decode_attention_invalid_rows_are_zero(hip, orc):
 
 
 def test_decode_attention_workspace_reuse(hip, orc):
-    """The merge resets its arrival counters: repeated calls on one workspace
-    stay exact, also with new spans."""
+    """Repeated calls on one workspace stay exact, also with new spans."""
     cache = Cache(orc, hip, 7, 3, 1024, 4, 64)
     heads = 8
     rng = np.random.default_rng(5)
