@@ -51,6 +51,16 @@ struct DecodeAttnParams {
     float* out;             // [rows][heads][64]
     int8_t* q_out;          // optional: QuantizeInt8 of each output row [rows][heads*64]
     float* qs_out;          //   and its scale [rows] (single-chunk plans, one head block)
+    // the whole-row kernel's POST form: fp32 QKV rows [rows][(heads + 2 kv_heads) * 64],
+    // each row's position, RoPE tables [capacity][32], and the cache it writes
+    const float* qkv;
+    const int32_t* positions;
+    const float* rope_cos;
+    const float* rope_sin;
+    int8_t* wkeys;
+    float* wkscale;
+    int8_t* wvalues;
+    float* wvscale;
     int32_t rows, heads, kv_heads, qk, slots, capacity, max_chunks, lmax, kv_per_block;
     float inv_sqrt;
 };
@@ -446,10 +456,22 @@ __global__ __launch_bounds__(64) void decode_merge_kernel(DecodeAttnParams p)
 //   phase 3: e_s and e_s * valueScale_s
 //   phase 4: thread per (chunk, 4 value dims) walks the chunk's positions
 //   merge:   wave 0, one lane per dim, chunks in ascending order
+//
+// POST (the decoder's step, at most kPostRows rows, qk 64): the workgroup
+// first builds its inputs from the fp32 QKV rows, as qkv_post_kernel in
+// decoder.hip does: RoPE (rotate-half) on its query head and QuantizeInt8
+// into the query; RoPE and QuantizeInt8 of the key head and QuantizeInt8 of
+// the value head of every row of the batch that writes a position of this
+// row's span (same slot) -- those positions are taken from the workgroup's
+// own results, not from the cache, since other workgroups of the launch
+// write them.  The workgroups of the group's first query head write their
+// row's key and value heads and scales to the cache.
 constexpr int kRowMaxCapacity = 512;
 constexpr int kRowMaxChunks = kRowMaxCapacity / 16;  // the plan makes at most count/16 chunks
 constexpr int kRowUnits = kRowMaxCapacity * 4 / kThreads;  // key pieces per thread
+constexpr int kPostRows = 4;
 
+template <bool POST>
 __global__ __launch_bounds__(kThreads) void decode_attention_row_kernel(DecodeAttnParams p)
 {
     __shared__ __align__(16) float score[kRowMaxCapacity];  // scores, then e_s
@@ -460,11 +482,15 @@ __global__ __launch_bounds__(kThreads) void decode_attention_row_kernel(DecodeAt
     __shared__ float csum[kRowMaxChunks];
     __shared__ float cwt[kRowMaxChunks];
     __shared__ __align__(16) uint32_t q_lds[16];
+    __shared__ __align__(16) uint32_t sub_k[POST ? kPostRows : 1][16];  // POST: key / value heads of the
+    __shared__ __align__(16) uint32_t sub_v[POST ? kPostRows : 1][16];  // positions written in this launch
+    __shared__ float sub_ks[POST ? kPostRows : 1], sub_vs[POST ? kPostRows : 1], q_scale[1];
 
     const int row = blockIdx.x;
     const int h = blockIdx.y;
     const int tid = threadIdx.x;
-    const int kv = h / (p.heads / p.kv_heads);
+    const int group = p.heads / p.kv_heads;
+    const int kv = h / group;
     const int slot = p.row_slot[row];
     const int first = p.row_first[row];
     const int count = p.row_count[row];
@@ -481,9 +507,55 @@ __global__ __launch_bounds__(kThreads) void decode_attention_row_kernel(DecodeAt
     const int qk = p.qk;
     const int pieces = qk / 16;
 
-    const uint32_t qword = tid < qk / 4 ? reinterpret_cast<const uint32_t*>(p.q + ((size_t)row * p.heads + h) * qk)[tid]
-                                        : 0u;
-    const float qsc = p.qscale[(size_t)row * p.heads + h] * p.inv_sqrt;
+    // POST: the rows r of the batch that write a position of this row's span
+    // (bit r of `subs`, at span position rel[r]); the same in every thread.
+    // Every row's position and slot are loaded together (clamped indexes),
+    // one memory round trip.
+    uint32_t subs = 0u;
+    int rel[kPostRows], rpos[kPostRows];
+    int pos_row = 0;
+    float post_x[3] = {0.0f, 0.0f, 0.0f}, post_c[3] = {0.0f, 0.0f, 0.0f}, post_sn[3] = {0.0f, 0.0f, 0.0f};
+    if constexpr (POST) {
+        int rslot[kPostRows];
+#pragma unroll
+        for (int r = 0; r < kPostRows; r++) {
+            const int rr = min(r, p.rows - 1);
+            rpos[r] = p.positions[rr];
+            rslot[r] = p.row_slot[rr];
+        }
+#pragma unroll
+        for (int r = 0; r < kPostRows; r++) {  // branch-free: the loads stay together
+            rel[r] = rpos[r] - first;
+            subs |= (uint32_t)((r < p.rows) & (rslot[r] == slot) & (rel[r] >= 0) & (rel[r] < count)) << r;
+            pos_row = r == row ? rpos[r] : pos_row;
+        }
+        // unit 0 is the query head, unit 1 + 2r (+1) row r's key (value)
+        // head; wave w takes units w, w + 4, w + 8.  Their loads go first:
+        // they are L2 hits and the vector memory counter retires in order.
+        const int e = tid & 63;
+        const int units_all = p.heads + 2 * p.kv_heads;
+#pragma unroll
+        for (int k = 0; k < 3; k++) {  // unconditional, clamped loads (no waits at a join)
+            const int u = (tid >> 6) + 4 * k;
+            const int r = u == 0 ? row : min((u - 1) >> 1, p.rows - 1);
+            const bool value = u > 0 && ((u - 1) & 1);
+            const int col = u == 0 ? h : (value ? p.heads + p.kv_heads + kv : p.heads + kv);
+            int at = pos_row;
+#pragma unroll
+            for (int q = 0; q < kPostRows; q++) at = (u > 0 && q == r) ? rpos[q] : at;
+            const size_t t = (size_t)at * 32 + (e & 31);
+            post_x[k] = p.qkv[((size_t)r * units_all + col) * 64 + e];
+            post_c[k] = p.rope_cos[t];
+            post_sn[k] = p.rope_sin[t];
+        }
+    }
+
+    uint32_t qword = 0u;
+    float qsc = 0.0f;
+    if constexpr (!POST) {
+        qword = tid < qk / 4 ? reinterpret_cast<const uint32_t*>(p.q + ((size_t)row * p.heads + h) * qk)[tid] : 0u;
+        qsc = p.qscale[(size_t)row * p.heads + h] * p.inv_sqrt;
+    }
 
     // phase 4's value dwords of the first kVBlock positions of this thread's
     // chunk, issued ahead of the key rows
@@ -518,9 +590,43 @@ __global__ __launch_bounds__(kThreads) void decode_attention_row_kernel(DecodeAt
         kw[k] = *reinterpret_cast<const uint4*>(p.keys + cell * qk + 16 * qslot);
         sv[k] = sbase[cell];
     }
-    if (tid < 16) q_lds[tid] = qword;
+    if constexpr (POST) {
+        // RoPE, then QuantizeInt8 per head, in qkv_post_kernel's arithmetic
+        const int e = tid & 63;
+#pragma unroll
+        for (int k = 0; k < 3; k++) {
+            const int u = (tid >> 6) + 4 * k;
+            const int r = u == 0 ? row : (u - 1) >> 1;
+            if (u > 2 * kPostRows || (u > 0 && !((subs >> r) & 1u))) continue;  // uniform per wave
+            const bool value = u > 0 && ((u - 1) & 1);
+            float v = post_x[k];
+            const float other = __shfl_xor(v, 32);
+            if (!value) v = e < 32 ? v * post_c[k] - other * post_sn[k] : v * post_c[k] + other * post_sn[k];
+            // max |v| over the head (order-free: any reduction order gives
+            // the same maximum)
+            const float peak = wave_max(fabsf(v));
+            const float scale = peak > 0.0f ? peak / 127.0f : 1.0f;
+            const float inverse = 1.0f / scale;
+            const int8_t qv = static_cast<int8_t>(ref_quantize_one(v, inverse));
+            if (u == 0) {
+                reinterpret_cast<int8_t*>(q_lds)[e] = qv;
+                if (e == 0) q_scale[0] = scale;
+                continue;
+            }
+            reinterpret_cast<int8_t*>(value ? sub_v[r] : sub_k[r])[e] = qv;
+            if (e == 0) (value ? sub_vs : sub_ks)[r] = scale;
+            if (r == row && h % group == 0) {  // this row's cache write, once per kv head
+                const size_t cell = ((size_t)slot * p.capacity + pos_row) * p.kv_heads + kv;
+                (value ? p.wvalues : p.wkeys)[cell * 64 + e] = qv;
+                if (e == 0) (value ? p.wvscale : p.wkscale)[cell] = scale;
+            }
+        }
+    } else {
+        if (tid < 16) q_lds[tid] = qword;
+    }
     if (tid < kRowMaxChunks) peak_key[tid] = order_key(-INFINITY);
     __syncthreads();
+    if constexpr (POST) qsc = q_scale[0] * p.inv_sqrt;
     const uint4 qv = *reinterpret_cast<const uint4*>(q_lds + 4 * qslot);
 #pragma unroll
     for (int k = 0; k < kRowUnits; k++) {
@@ -528,6 +634,15 @@ __global__ __launch_bounds__(kThreads) void decode_attention_row_kernel(DecodeAt
         const int u = k * kThreads + tid;
         const bool ok = u < units;  // whole aligned 4-lane groups
         const int s = min(u, units - 1) >> 2;
+        if constexpr (POST) {
+#pragma unroll
+            for (int r = 0; r < kPostRows; r++) {
+                if (((subs >> r) & 1u) && s == rel[r]) {
+                    kw[k] = *reinterpret_cast<const uint4*>(&sub_k[r][4 * qslot]);
+                    sv[k] = (lslot & 1) ? sub_vs[r] : sub_ks[r];
+                }
+            }
+        }
         int d4 = 0;
         d4 = __builtin_amdgcn_sdot4((int)qv.x, (int)kw[k].x, d4, false);
         d4 = __builtin_amdgcn_sdot4((int)qv.y, (int)kw[k].y, d4, false);
@@ -572,6 +687,17 @@ __global__ __launch_bounds__(kThreads) void decode_attention_row_kernel(DecodeAt
             if (s0 > 0 || c0 > 0) {
 #pragma unroll
                 for (int j = 0; j < kVBlock; j++) vreg[j] = vp[(size_t)min(s0 + j, L - 1) * vstride4];
+            }
+            if constexpr (POST) {
+#pragma unroll
+                for (int r = 0; r < kPostRows; r++) {
+                    const int jj = rel[r] - (b + s0);
+                    if (((subs >> r) & 1u) && jj >= 0 && jj < kVBlock) {
+                        const uint32_t w = sub_v[r][vj];
+#pragma unroll
+                        for (int j = 0; j < kVBlock; j++) vreg[j] = j == jj ? w : vreg[j];
+                    }
+                }
             }
 #pragma unroll
             for (int j4 = 0; j4 < kVBlock; j4 += 4) {
@@ -664,6 +790,48 @@ using namespace nhip;
 
 namespace nhip {
 
+int32_t attention_decode_post_impl(const AttnPostInputs& in, int32_t rows, int32_t heads, int32_t kv_heads,
+                                   int8_t* d_keys, float* d_key_scales, int8_t* d_values, float* d_value_scales,
+                                   int32_t slots, int32_t capacity, const int32_t* d_row_slot,
+                                   const int32_t* d_row_first, const int32_t* d_row_count, int32_t max_chunks,
+                                   float* d_out, hipStream_t stream)
+{
+    if (rows < 1 || rows > kPostRows || capacity > kRowMaxCapacity) return 1;
+    NHIP_REQUIRE(heads > 0 && kv_heads > 0 && heads % kv_heads == 0 && slots > 0 && capacity > 0 && max_chunks >= 1,
+                 "attention: bad shape");
+    NHIP_REQUIRE(in.qkv && in.positions && in.rope_cos && in.rope_sin && d_keys && d_key_scales && d_values &&
+                     d_value_scales && d_row_slot && d_row_first && d_row_count && d_out,
+                 "attention: null pointer");
+    DecodeAttnParams p{};
+    p.keys = d_keys;
+    p.kscale = d_key_scales;
+    p.values = d_values;
+    p.vscale = d_value_scales;
+    p.wkeys = d_keys;
+    p.wkscale = d_key_scales;
+    p.wvalues = d_values;
+    p.wvscale = d_value_scales;
+    p.row_slot = d_row_slot;
+    p.row_first = d_row_first;
+    p.row_count = d_row_count;
+    p.qkv = in.qkv;
+    p.positions = in.positions;
+    p.rope_cos = in.rope_cos;
+    p.rope_sin = in.rope_sin;
+    p.out = d_out;
+    p.rows = rows;
+    p.heads = heads;
+    p.kv_heads = kv_heads;
+    p.qk = 64;
+    p.slots = slots;
+    p.capacity = capacity;
+    p.max_chunks = max_chunks;
+    p.inv_sqrt = static_cast<float>(1.0 / std::sqrt(64.0));
+    hipLaunchKernelGGL(decode_attention_row_kernel<true>, dim3(rows, heads), dim3(kThreads), 0, stream, p);
+    NHIP_CHECK_HIP(hipGetLastError());
+    return NHIP_OK;
+}
+
 int32_t attention_decode_impl(const int8_t* d_q, const float* d_qscale, int32_t rows, int32_t heads,
                               int32_t kv_heads, int32_t qk_dim, const int8_t* d_keys, const float* d_key_scales,
                               const int8_t* d_values, const float* d_value_scales, int32_t slots,
@@ -729,7 +897,7 @@ int32_t attention_decode_impl(const int8_t* d_q, const float* d_qscale, int32_t 
     NHIP_REQUIRE(!d_q_out || (d_qs_out && max_chunks == 1 && head_blocks == 1),
                  "attention: a quantized output needs max_chunks 1 and all heads in one block");
     if (!d_q_out && capacity <= kRowMaxCapacity) {  // every count <= capacity: one workgroup per (row, head)
-        hipLaunchKernelGGL(decode_attention_row_kernel, dim3(rows, heads), dim3(kThreads), 0, stream, p);
+        hipLaunchKernelGGL(decode_attention_row_kernel<false>, dim3(rows, heads), dim3(kThreads), 0, stream, p);
         NHIP_CHECK_HIP(hipGetLastError());
         return NHIP_OK;
     }

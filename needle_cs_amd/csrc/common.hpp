@@ -119,6 +119,23 @@ int32_t launch_decode_swiglu(const DeviceWeights* w, const int8_t* q, const floa
 // many 16-row tiles a separate element-wise launch and the plain matmul are
 // faster.
 constexpr int kFusedPrologueMaxTiles = 256;
+// The decoder's step attention with its input post-processing folded in:
+// RoPE on the query and key heads of the fp32 QKV rows, per-head
+// QuantizeInt8, and each row's key and value write to the cache at its
+// position (qk 64).  Rows of the batch that write positions of another row's
+// span are read from the launch's own results.  Returns 1 without launching
+// when it does not apply: more than 4 rows or caches over 512 positions.
+struct AttnPostInputs {
+    const float* qkv;          // [rows][(heads + 2 kv_heads) * 64]
+    const int32_t* positions;  // [rows]
+    const float* rope_cos;     // [capacity][32]
+    const float* rope_sin;
+};
+int32_t attention_decode_post_impl(const AttnPostInputs& in, int32_t rows, int32_t heads, int32_t kv_heads,
+                                   int8_t* d_keys, float* d_key_scales, int8_t* d_values, float* d_value_scales,
+                                   int32_t slots, int32_t capacity, const int32_t* d_row_slot,
+                                   const int32_t* d_row_first, const int32_t* d_row_count, int32_t max_chunks,
+                                   float* d_out, hipStream_t stream);
 // Chunk-kernel geometry of attention_decode_impl: the longest chunk of the
 // plan, and the kv heads per workgroup (0 when a chunk does not fit in LDS);
 // a quantized output needs every head in one workgroup.

@@ -756,18 +756,28 @@ int32_t enqueue_forward(nhip_decoder* m, int rows, int k, bool masked = false)
         pp.heads = H;
         pp.kv_heads = KV;
         pp.capacity = D.capacity;
-        hipLaunchKernelGGL(qkv_post_kernel, dim3(rows, H + 2 * KV), dim3(64), 0, s, pp);
-        NHIP_CHECK_HIP(hipGetLastError());
         // single-chunk attention with every head in one workgroup also
         // quantizes its output rows
         const bool attn_quant =
             D.max_chunks == 1 &&
             decode_attention_kv_per_block(H / KV, KV, decode_attention_lmax(D.capacity, D.max_chunks)) >= KV;
-        rc = attention_decode_impl(m->qh, m->qhs, rows, H, KV, 64, pp.keys, pp.key_scales, pp.values,
-                                   pp.value_scales, D.slots, D.capacity, in_slots(m, m->d_in), in_first(m, m->d_in),
-                                   in_count(m, m->d_in), D.max_chunks, m->attn_ws, m->attn_ws_bytes, m->att,
-                                   attn_quant ? m->q8 : nullptr, attn_quant ? m->qs : nullptr, s);
-        if (rc) return rc;
+        rc = 1;
+        if (fuse && !attn_quant) {  // RoPE, quantize and the KV write inside the attention launch
+            const AttnPostInputs in{m->qkv, pp.positions, m->rope_cos, m->rope_sin};
+            rc = attention_decode_post_impl(in, rows, H, KV, pp.keys, pp.key_scales, pp.values, pp.value_scales,
+                                            D.slots, D.capacity, pp.slots, in_first(m, m->d_in),
+                                            in_count(m, m->d_in), D.max_chunks, m->att, s);
+            if (rc < 0) return rc;
+        }
+        if (rc) {
+            hipLaunchKernelGGL(qkv_post_kernel, dim3(rows, H + 2 * KV), dim3(64), 0, s, pp);
+            NHIP_CHECK_HIP(hipGetLastError());
+            rc = attention_decode_impl(m->qh, m->qhs, rows, H, KV, 64, pp.keys, pp.key_scales, pp.values,
+                                       pp.value_scales, D.slots, D.capacity, pp.slots, in_first(m, m->d_in),
+                                       in_count(m, m->d_in), D.max_chunks, m->attn_ws, m->attn_ws_bytes, m->att,
+                                       attn_quant ? m->q8 : nullptr, attn_quant ? m->qs : nullptr, s);
+            if (rc) return rc;
+        }
         rc = 1;
         if (!attn_quant && fuse) {
             DecodePrologue f{kProQuant, m->att, nullptr, nullptr, nullptr, 0.0f, 0};

@@ -47,6 +47,43 @@ def test_forward_bit_identical(hip, orc, dims, max_chunks):
     cpu.close()
 
 
+@pytest.mark.parametrize("max_chunks", [8, 64])
+@pytest.mark.parametrize("dims", [TINY, GQA], ids=["tiny", "gqa"])
+def test_small_batches_sharing_slots(hip, orc, dims, max_chunks):
+    """Forwards of at most 4 rows write their key/value rows inside the
+    attention launch; rows of one slot at consecutive positions attend to
+    each other's new positions, which the launch takes from its own results.
+    Chunked prefills of 4, 3, 4 and 2 rows, then mixed batches of two slots."""
+    model = synthetic_model(dims, 7004)
+    gpu = GpuDecoder(model, slots=3, capacity=64, max_rows=8, max_chunks=max_chunks)
+    cpu = orc.CpuDecoder(model, slots=3, capacity=64, max_chunks=max_chunks)
+    prompt = random_prompt(12, 13, dims["vocab"])
+    start = 0
+    for n in (4, 3, 4, 2):
+        for slot in (0, 1):
+            toks = prompt[start:start + n]
+            pos = np.arange(start, start + n)
+            lg_g, ig, lpg = gpu.forward(toks, [slot] * n, pos, k=2)
+            lg_c, ic, lpc = cpu.forward(toks, [slot] * n, pos, k=2)
+            assert np.array_equal(bits(lg_g), bits(lg_c)), (start, slot)
+            assert np.array_equal(ig, ic) and np.array_equal(bits(lpg), bits(lpc))
+        start += n
+    toks = np.array([5, 9, 11, 13], dtype=np.int32)
+    for step in range(3):  # [slot 0, slot 0, slot 1, slot 2] and the reverse order
+        p0 = 13 + 2 * step
+        spec = [(0, p0), (0, p0 + 1), (1, 13 + step), (2, step)]
+        if step == 1:
+            spec = spec[::-1]
+        slots, pos = [x[0] for x in spec], [x[1] for x in spec]
+        lg_g, ig, lpg = gpu.forward(toks, slots, pos, k=2)
+        lg_c, ic, lpc = cpu.forward(toks, slots, pos, k=2)
+        assert np.array_equal(bits(lg_g), bits(lg_c)), step
+        assert np.array_equal(ig, ic) and np.array_equal(bits(lpg), bits(lpc))
+        toks = ic[:, 0].copy()
+    gpu.close()
+    cpu.close()
+
+
 @pytest.mark.parametrize("max_chunks", [1, 64])
 @pytest.mark.parametrize("eos", [1, 7])
 def test_beam_search_identical_tokens(hip, orc, eos, max_chunks):
