@@ -359,6 +359,17 @@ int32_t nhip_decoder_forward_masked(nhip_decoder* m, const int32_t* tokens, cons
 int32_t nhip_argmax_masked_dev(const float* d_x, int32_t ldx, const uint32_t* d_mask, int32_t mask_ld,
                                int32_t words, int32_t length, int32_t rows, int32_t* d_index, float* d_value,
                                void* stream);
+/* Ops.TopKLogSoftmax (src/Needle/Ops.cs:1092-1221) as the decoder's head
+ * runs it, over `rows` device rows of n logits (row r at d_logits + r*n):
+ * the k (1..8) best ids by value, ties to the lower id, ids 0, 2 and 3
+ * excluded, and their log-probabilities v - (peak + log S), with S summed
+ * over blocks of 2048 ids in the canonical order.  d_idx / d_lp: [rows][k].
+ * n <= 524288.  The workspace (nhip_topk_lse_workspace bytes) holds the
+ * per-block partial lists; nothing needs clearing.  Asynchronous on
+ * `stream`. */
+size_t nhip_topk_lse_workspace(int32_t rows, int32_t n);
+int32_t nhip_topk_lse_dev(const float* d_logits, int32_t rows, int32_t n, int32_t k, void* d_workspace,
+                          size_t workspace_bytes, int32_t* d_idx, float* d_lp, void* stream);
 /* Engine.CopyFrom: positions [0, length) of slot src into slot dst. */
 int32_t nhip_decoder_copy_slot(nhip_decoder* m, int32_t dst, int32_t src, int32_t length);
 /* Prefill `prompt` into slot 0, then beam search of `width` beams for up to

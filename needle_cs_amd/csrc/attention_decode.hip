@@ -126,6 +126,15 @@ __device__ __forceinline__ float sx8(uint32_t v, int b)
 
 constexpr int kVBlock = 32;  // value dwords per thread loaded together
 
+// A uniform load of data that no kernel of the launch writes, through the
+// scalar cache.  Kernels that store to global memory would otherwise load
+// such arrays with vector loads (the compiler cannot rule out aliasing),
+// which costs a memory round trip of its own ahead of the dependent loads.
+__device__ __forceinline__ int32_t uniform_load(const int32_t* a, int i)
+{
+    return ((const __attribute__((address_space(4))) int32_t*)a)[i];
+}
+
 __global__ __launch_bounds__(kThreads) void decode_attention_kernel(DecodeAttnParams p)
 {
     extern __shared__ __align__(16) uint8_t lds[];
@@ -491,15 +500,46 @@ __global__ __launch_bounds__(kThreads) void decode_attention_row_kernel(DecodeAt
     const int tid = threadIdx.x;
     const int group = p.heads / p.kv_heads;
     const int kv = h / group;
-    const int slot = p.row_slot[row];
-    const int first = p.row_first[row];
-    const int count = p.row_count[row];
-    float* dst = p.out + ((size_t)row * p.heads + h) * 64;
-    const bool valid = slot >= 0 && slot < p.slots && first >= 0 && count >= 1 && count <= p.capacity - first;
-    if (!valid) {
-        if (tid < 16) *reinterpret_cast<float4*>(dst + 4 * tid) = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-        return;
+    // The first round trip: this row's span (scalar loads), and for POST the
+    // fp32 QKV heads of the workgroup's units (they depend on nothing) and
+    // every row's position and slot, one per lane (vector loads, read back
+    // with v_readlane).  Nothing branches on them, so the loads issue
+    // together.  A row with an invalid slot or span runs on the span (slot
+    // 0, first 0, count 1), writes zeros and no cache row.
+    const int slot_in = uniform_load(p.row_slot, row);
+    const int first_in = uniform_load(p.row_first, row);
+    const int count_in = uniform_load(p.row_count, row);
+    const int e = tid & 63;
+    const int units_all = p.heads + 2 * p.kv_heads;
+    // POST units: unit 0 is the query head, unit 1 + 2r (+1) row r's key
+    // (value) head; wave w takes units w, w + 4, w + 8 (clamped rows: the
+    // loads are unconditional, so no wait gathers them at a join)
+    float post_x[3] = {0.0f, 0.0f, 0.0f}, post_c[3] = {0.0f, 0.0f, 0.0f}, post_sn[3] = {0.0f, 0.0f, 0.0f};
+    int rpos[kPostRows], rslot[kPostRows];
+    if constexpr (POST) {
+#pragma unroll
+        for (int k = 0; k < 3; k++) {
+            const int u = (tid >> 6) + 4 * k;
+            const int r = u == 0 ? row : min((u - 1) >> 1, p.rows - 1);
+            const bool value = u > 0 && ((u - 1) & 1);
+            const int col = u == 0 ? h : (value ? p.heads + p.kv_heads + kv : p.heads + kv);
+            post_x[k] = p.qkv[((size_t)r * units_all + col) * 64 + e];
+        }
+        const int lr = min(e, p.rows - 1);
+        const int mpos = p.positions[lr];
+        const int mslot = p.row_slot[lr];
+#pragma unroll
+        for (int r = 0; r < kPostRows; r++) {
+            rpos[r] = __builtin_amdgcn_readlane(mpos, r);
+            rslot[r] = __builtin_amdgcn_readlane(mslot, r);
+        }
     }
+    float* dst = p.out + ((size_t)row * p.heads + h) * 64;
+    const bool valid = (slot_in >= 0) & (slot_in < p.slots) & (first_in >= 0) & (count_in >= 1) &
+                       (count_in <= p.capacity - first_in);
+    const int slot = valid ? slot_in : 0;
+    const int first = valid ? first_in : 0;
+    const int count = valid ? count_in : 1;
     int length;
     const int needed = plan(count, p.max_chunks, &length);  // count <= capacity <= 512: needed <= 32
     const uint32_t mag_len = magic((uint32_t)length);       // s < 512: s / length is exact
@@ -509,42 +549,25 @@ __global__ __launch_bounds__(kThreads) void decode_attention_row_kernel(DecodeAt
 
     // POST: the rows r of the batch that write a position of this row's span
     // (bit r of `subs`, at span position rel[r]); the same in every thread.
-    // Every row's position and slot are loaded together (clamped indexes),
-    // one memory round trip.
+    // Then the RoPE factors of the query and key units.
     uint32_t subs = 0u;
-    int rel[kPostRows], rpos[kPostRows];
+    int rel[kPostRows];
     int pos_row = 0;
-    float post_x[3] = {0.0f, 0.0f, 0.0f}, post_c[3] = {0.0f, 0.0f, 0.0f}, post_sn[3] = {0.0f, 0.0f, 0.0f};
     if constexpr (POST) {
-        int rslot[kPostRows];
 #pragma unroll
         for (int r = 0; r < kPostRows; r++) {
-            const int rr = min(r, p.rows - 1);
-            rpos[r] = p.positions[rr];
-            rslot[r] = p.row_slot[rr];
-        }
-#pragma unroll
-        for (int r = 0; r < kPostRows; r++) {  // branch-free: the loads stay together
             rel[r] = rpos[r] - first;
             subs |= (uint32_t)((r < p.rows) & (rslot[r] == slot) & (rel[r] >= 0) & (rel[r] < count)) << r;
             pos_row = r == row ? rpos[r] : pos_row;
         }
-        // unit 0 is the query head, unit 1 + 2r (+1) row r's key (value)
-        // head; wave w takes units w, w + 4, w + 8.  Their loads go first:
-        // they are L2 hits and the vector memory counter retires in order.
-        const int e = tid & 63;
-        const int units_all = p.heads + 2 * p.kv_heads;
 #pragma unroll
-        for (int k = 0; k < 3; k++) {  // unconditional, clamped loads (no waits at a join)
+        for (int k = 0; k < 3; k++) {
             const int u = (tid >> 6) + 4 * k;
-            const int r = u == 0 ? row : min((u - 1) >> 1, p.rows - 1);
-            const bool value = u > 0 && ((u - 1) & 1);
-            const int col = u == 0 ? h : (value ? p.heads + p.kv_heads + kv : p.heads + kv);
+            const int r = min((u - 1) >> 1, p.rows - 1);
             int at = pos_row;
 #pragma unroll
             for (int q = 0; q < kPostRows; q++) at = (u > 0 && q == r) ? rpos[q] : at;
             const size_t t = (size_t)at * 32 + (e & 31);
-            post_x[k] = p.qkv[((size_t)r * units_all + col) * 64 + e];
             post_c[k] = p.rope_cos[t];
             post_sn[k] = p.rope_sin[t];
         }
@@ -592,7 +615,6 @@ __global__ __launch_bounds__(kThreads) void decode_attention_row_kernel(DecodeAt
     }
     if constexpr (POST) {
         // RoPE, then QuantizeInt8 per head, in qkv_post_kernel's arithmetic
-        const int e = tid & 63;
 #pragma unroll
         for (int k = 0; k < 3; k++) {
             const int u = (tid >> 6) + 4 * k;
@@ -615,7 +637,7 @@ __global__ __launch_bounds__(kThreads) void decode_attention_row_kernel(DecodeAt
             }
             reinterpret_cast<int8_t*>(value ? sub_v[r] : sub_k[r])[e] = qv;
             if (e == 0) (value ? sub_vs : sub_ks)[r] = scale;
-            if (r == row && h % group == 0) {  // this row's cache write, once per kv head
+            if (valid && r == row && h % group == 0) {  // this row's cache write, once per kv head
                 const size_t cell = ((size_t)slot * p.capacity + pos_row) * p.kv_heads + kv;
                 (value ? p.wvalues : p.wkeys)[cell * 64 + e] = qv;
                 if (e == 0) (value ? p.wvscale : p.wkscale)[cell] = scale;
@@ -719,8 +741,9 @@ __global__ __launch_bounds__(kThreads) void decode_attention_row_kernel(DecodeAt
             tot = tot + w * total;
             const float inverse = 1.0f / tot;
             *reinterpret_cast<float4*>(dst + 4 * vj) =
-                make_float4((0.0f + w * o0) * inverse, (0.0f + w * o1) * inverse, (0.0f + w * o2) * inverse,
-                            (0.0f + w * o3) * inverse);
+                valid ? make_float4((0.0f + w * o0) * inverse, (0.0f + w * o1) * inverse, (0.0f + w * o2) * inverse,
+                                    (0.0f + w * o3) * inverse)
+                      : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
         } else {
             *reinterpret_cast<float4*>(part + c * 64 + 4 * vj) = make_float4(o0, o1, o2, o3);
             if (vj == 0) csum[c] = total;

@@ -275,6 +275,8 @@ __device__ __forceinline__ bool masked(int i) { return i == 0 || i == 2 || i == 
 // merges a row's blocks.  K is a template parameter so that the per-thread
 // lists stay in registers.
 constexpr int kTopkBlock = 2048;
+constexpr int kTopkMaxBlocks = 256;                           // vocab <= 524288
+constexpr int kTopkMaxCandidates = kTopkMaxBlocks * kMaxTopK;  // the final merge's LDS
 
 template <int K>
 __global__ __launch_bounds__(kThreads) void topk_block_kernel(const float* logits, int n, int blocks, float* bvals,
@@ -396,69 +398,59 @@ template <int K>
 __global__ __launch_bounds__(64) void topk_final_kernel(const float* bvals, const int32_t* bids, const float* bmax,
                                                          const float* bsum, int blocks, int32_t* idx, float* lp)
 {
-    // the 64 threads stage the row's candidates (and below the block maxima
-    // and sums) in LDS, 256 at a time; thread 0 walks them in order
-    constexpr int kChunk = 256;
-    __shared__ float sv[kChunk];
-    __shared__ int si[kChunk];
+    // The row's top K of the blocks' candidates under `before` (value, then
+    // the lower id).  That order is total on the candidates (never NaN; the
+    // blocks' (-inf, INT_MAX) placeholders are identical to each other), so
+    // the result is the K first candidates in that order, whatever the
+    // sequence of comparisons: every thread ranks its candidates against all
+    // others in parallel (equal candidates by their index) and rank m goes to
+    // slot m.
+    __shared__ float sv[kTopkMaxCandidates];
+    __shared__ int si[kTopkMaxCandidates];
+    __shared__ float best_v[K];
+    __shared__ int best_i[K];
+    __shared__ float prod[kTopkMaxBlocks];
     const int tid = threadIdx.x;
     const int row = blockIdx.x;
-    float bv[K];
-    int bi[K];
-#pragma unroll
-    for (int m = 0; m < K; m++) {
-        bv[m] = -INFINITY;
-        bi[m] = 0x7FFFFFFF;
-    }
     const size_t base = (size_t)row * blocks;
     const int n = blocks * K;
-    for (int c0 = 0; c0 < n; c0 += kChunk) {
-        const int cnt = min(kChunk, n - c0);
-        for (int j = tid; j < cnt; j += 64) {
-            sv[j] = bvals[base * K + c0 + j];
-            si[j] = bids[base * K + c0 + j];
-        }
-        __syncthreads();
-        for (int c = 0; tid == 0 && c < cnt; c++) {
-            const float v = sv[c];
-            const int i = si[c];
-            if (!before(v, i, bv[K - 1], bi[K - 1])) continue;
-            bv[K - 1] = v;
-            bi[K - 1] = i;
-#pragma unroll
-            for (int m = K - 1; m > 0; m--) {
-                if (before(bv[m], bi[m], bv[m - 1], bi[m - 1])) {
-                    const float fv = bv[m];
-                    const int fi = bi[m];
-                    bv[m] = bv[m - 1];
-                    bi[m] = bi[m - 1];
-                    bv[m - 1] = fv;
-                    bi[m - 1] = fi;
-                }
-            }
-        }
-        __syncthreads();
+    for (int j = tid; j < n; j += 64) {
+        sv[j] = bvals[base * K + j];
+        si[j] = bids[base * K + j];
     }
-    // log-sum-exp over the blocks in ascending order (sv: maxima, si: sums)
-    float total = 0.0f;
-    for (int b0 = 0; b0 < blocks; b0 += kChunk) {
-        const int cnt = min(kChunk, blocks - b0);
-        for (int j = tid; j < cnt; j += 64) {
-            sv[j] = bmax[base + b0 + j];
-            si[j] = __float_as_int(bsum[base + b0 + j]);
-        }
-        __syncthreads();
-        const float peak = bv[0];
-        for (int b = 0; tid == 0 && b < cnt; b++) total = total + exp_poly(sv[b] - peak) * __int_as_float(si[b]);
-        __syncthreads();
+    if (tid < K) {
+        best_v[tid] = -INFINITY;
+        best_i[tid] = 0x7FFFFFFF;
     }
+    __syncthreads();
+    for (int c = tid; c < n; c += 64) {
+        const float v = sv[c];
+        const int i = si[c];
+        int rank = 0;
+        for (int o = 0; o < n; o++) {
+            const float ov = sv[o];
+            const int oi = si[o];
+            rank += (before(ov, oi, v, i) || (ov == v && oi == i && o < c)) ? 1 : 0;
+        }
+        if (rank < K && v == v) {
+            best_v[rank] = v;
+            best_i[rank] = i;
+        }
+    }
+    __syncthreads();
+    // log-sum-exp over the blocks in ascending order: the terms
+    // Exp(max_b - peak) * sum_b in parallel, then their sum in order
+    const float peak = best_v[0];
+    for (int b = tid; b < blocks; b += 64) prod[b] = exp_poly(bmax[base + b] - peak) * bsum[base + b];
+    __syncthreads();
     if (tid != 0) return;
-    const float peak = bv[0];
+    float total = 0.0f;
+    for (int b = 0; b < blocks; b++) total = total + prod[b];
     const float log_shift = peak + log_poly(total);
 #pragma unroll
     for (int m = 0; m < K; m++) {
-        idx[(size_t)row * K + m] = bi[m];
-        lp[(size_t)row * K + m] = bv[m] - log_shift;
+        idx[(size_t)row * K + m] = best_i[m];
+        lp[(size_t)row * K + m] = best_v[m] - log_shift;
     }
 }
 
@@ -475,6 +467,7 @@ int32_t launch_topk(const float* logits, int rows, int n, int k, const TopkScrat
                     hipStream_t s)
 {
     const int blocks = (n + kTopkBlock - 1) / kTopkBlock;
+    NHIP_REQUIRE(blocks <= kTopkMaxBlocks, "top-k: at most %d ids per row (got %d)", kTopkMaxBlocks * kTopkBlock, n);
     switch (k) {
 #define NHIP_TOPK_CASE(K)                                                                                        \
     case K:                                                                                                      \
@@ -963,6 +956,8 @@ int32_t nhip_decoder_create(const nhip_decoder_dims* dims, nhip_decoder** out)
                  "ffn %d must be a positive multiple of 32 up to %d", D.ffn, kMaxPerThread * kThreads);
     NHIP_REQUIRE(D.vocab > 4 && D.capacity > 0 && D.slots > 0 && D.max_rows > 0 && D.max_chunks > 0,
                  "vocab, capacity, slots, max_rows, max_chunks");
+    NHIP_REQUIRE(D.vocab <= kTopkMaxBlocks * kTopkBlock, "vocab %d above the top-k's %d", D.vocab,
+                 kTopkMaxBlocks * kTopkBlock);
     int32_t rc = ensure_device();
     if (rc) return rc;
     nhip_decoder* m = new nhip_decoder();
@@ -1173,6 +1168,49 @@ int32_t nhip_argmax_masked_dev(const float* d_x, int32_t ldx, const uint32_t* d_
     int32_t rc = ensure_device();
     if (rc) return rc;
     return launch_argmax_masked(d_x, ldx, d_mask, mask_ld, words, length, rows, d_index, d_value, as_stream(stream));
+}
+
+// Workspace of nhip_topk_lse_dev: the decoder's TopkScratch arrays, each
+// 256-byte aligned.
+static size_t topk_ws_layout(int32_t rows, int32_t n, TopkScratch* ts, uint8_t* base)
+{
+    const size_t blocks = ((size_t)n + kTopkBlock - 1) / kTopkBlock;
+    const size_t lists = (size_t)rows * blocks * kMaxTopK, per = (size_t)rows * blocks;
+    auto a256 = [](size_t x) { return (x + 255) & ~size_t(255); };
+    const size_t o_ids = a256(lists * sizeof(float));
+    const size_t o_max = o_ids + a256(lists * sizeof(int32_t));
+    const size_t o_sum = o_max + a256(per * sizeof(float));
+    if (ts) {
+        ts->vals = reinterpret_cast<float*>(base);
+        ts->ids = reinterpret_cast<int32_t*>(base + o_ids);
+        ts->bmax = reinterpret_cast<float*>(base + o_max);
+        ts->bsum = reinterpret_cast<float*>(base + o_sum);
+    }
+    return o_sum + a256(per * sizeof(float));
+}
+
+size_t nhip_topk_lse_workspace(int32_t rows, int32_t n)
+{
+    if (rows <= 0 || n <= 0) return 0;
+    return topk_ws_layout(rows, n, nullptr, nullptr);
+}
+
+int32_t nhip_topk_lse_dev(const float* d_logits, int32_t rows, int32_t n, int32_t k, void* d_workspace,
+                          size_t workspace_bytes, int32_t* d_idx, float* d_lp, void* stream)
+{
+    clear_error();
+    NHIP_REQUIRE(rows >= 0 && n >= 1 && k >= 1 && k <= kMaxTopK, "rows %d, n %d, k %d (1..%d)", rows, n, k, kMaxTopK);
+    NHIP_REQUIRE(n <= kTopkMaxBlocks * kTopkBlock, "at most %d logits per row", kTopkMaxBlocks * kTopkBlock);
+    if (rows == 0) return NHIP_OK;
+    NHIP_REQUIRE(d_logits && d_workspace && d_idx && d_lp, "null pointer");
+    NHIP_REQUIRE((reinterpret_cast<uintptr_t>(d_logits) & 15) == 0 && (reinterpret_cast<uintptr_t>(d_workspace) & 255) == 0,
+                 "logits must be 16-byte aligned and the workspace 256-byte aligned");
+    TopkScratch ts{};
+    const size_t need = topk_ws_layout(rows, n, &ts, static_cast<uint8_t*>(d_workspace));
+    NHIP_REQUIRE(workspace_bytes >= need, "workspace of %zu bytes, need %zu", workspace_bytes, need);
+    int32_t rc = ensure_device();
+    if (rc) return rc;
+    return launch_topk(d_logits, rows, n, k, ts, d_idx, d_lp, as_stream(stream));
 }
 
 int32_t nhip_decoder_copy_slot(nhip_decoder* m, int32_t dst, int32_t src, int32_t length)

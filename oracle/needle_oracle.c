@@ -449,10 +449,18 @@ void or_quantize_rows(const float* x, int tokens, int cols, int8_t* q, float* sc
 
 /* ----------------------------------------------------------- softmax -- */
 
-/* src/Needle/Ops.cs:16-31 (one lane; Fma.MultiplyAddNegated(a,b,c) = c - a*b fused) */
+/* x86 MAXPS / MINPS on one lane (Avx.Max / Avx.Min): the first operand when
+ * it compares greater (less), else the second -- so a NaN first operand
+ * gives the second. */
+static inline float max_ps(float a, float b) { return a > b ? a : b; }
+static inline float min_ps(float a, float b) { return a < b ? a : b; }
+
+/* src/Needle/Ops.cs:16-31 (one lane; Fma.MultiplyAddNegated(a,b,c) = c - a*b
+ * fused).  The clamp is Avx.Min(Avx.Max(x, -87.3), 88.7) (Ops.cs:18): a NaN
+ * argument becomes -87.3. */
 float or_exp_poly(float x)
 {
-    x = fmin_ref(fmax_ref(x, -87.3f), 88.7f);
+    x = min_ps(max_ps(x, -87.3f), 88.7f);
     float n = rintf(x * 1.44269504f);
     float r = fmaf(-n, 0.693359375f, x);
     r = fmaf(-n, -2.12194440e-4f, r);

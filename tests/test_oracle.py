@@ -305,6 +305,19 @@ def test_exp_poly_against_exp(orc):
     assert orc.lib().or_exp_poly(0.0) == 1.0
 
 
+def test_exp_poly_clamps_like_avx_max_min(orc):
+    """Ops.Exp clamps with Avx.Min(Avx.Max(x, -87.3), 88.7) (src/Needle/Ops.cs:18):
+    MAXPS returns its second operand when the first is NaN, so a NaN argument
+    (e.g. -inf - -inf) is exp(-87.3), and +-inf land on the clamp bounds.  At
+    88.7 the power-of-two scale 2^128 overflows to +inf, as in the reference."""
+    e = orc.lib().or_exp_poly
+    lo, hi = e(-87.3), e(88.7)
+    assert 1.17e-38 < lo < 1.3e-38 and hi == float("inf")
+    assert e(float("nan")) == lo
+    assert e(float("-inf")) == lo and e(-1e30) == lo
+    assert e(float("inf")) == hi and e(1e30) == hi
+
+
 # --------------------------------------------------------- attention --
 
 def _attention_inputs(seed, positions, kv_heads, heads, qk):
