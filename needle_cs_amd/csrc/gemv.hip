@@ -629,6 +629,16 @@ __device__ __forceinline__ void narrow_products(const long (&av)[2 * CB / 4], co
 // rows j = 8*tile + r (r < 8) followed by the matching up rows: lane r < 8
 // takes lane r + 8's sum (DPP row_shl:8 within the token's 16-lane row) and
 // stores a = (g / (1 + Exp(-g))) * u at y[t][j].
+__device__ __forceinline__ void store_chain(float acc, int t, int rr, int nn, int tile, const MatmulParams& p)
+{
+    if (p.swiglu) {
+        const float u = dpp_row_shl(acc, 8);
+        if (rr < 8) p.y[(size_t)t * p.ldy + tile * 8 + rr] = (acc / (1.0f + exp_poly(-acc))) * u;
+    } else if (nn >= p.row_start && nn < p.row_end) {
+        p.y[(size_t)t * p.ldy + nn] = acc;
+    }
+}
+
 __device__ __forceinline__ void chain_products(const float* pl, int GS, int swz, int M, int G, int tile,
                                                const MatmulParams& p)
 {
@@ -662,12 +672,7 @@ __device__ __forceinline__ void chain_products(const float* pl, int GS, int swz,
         }
         const float* rowf = reinterpret_cast<const float*>(row);
         for (int c = full * 16; c < G; c++) acc = acc + rowf[(((c >> 2) ^ sw) << 2) | (c & 3)];
-        if (p.swiglu) {
-            const float u = dpp_row_shl(acc, 8);
-            if (rr < 8) p.y[(size_t)t * p.ldy + tile * 8 + rr] = (acc / (1.0f + exp_poly(-acc))) * u;
-        } else if (nn >= p.row_start && nn < p.row_end) {
-            p.y[(size_t)t * p.ldy + nn] = acc;
-        }
+        store_chain(acc, t, rr, nn, tile, p);
     }
 }
 
