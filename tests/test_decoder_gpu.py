@@ -18,12 +18,16 @@ def bits(a):
     return np.ascontiguousarray(a).view(np.uint32)
 
 
+@pytest.mark.parametrize("capacity", [64, 600])
 @pytest.mark.parametrize("max_chunks", [1, 64])
 @pytest.mark.parametrize("dims", [TINY, GQA, ODD], ids=["tiny", "gqa", "odd"])
-def test_forward_bit_identical(hip, orc, dims, max_chunks):
+def test_forward_bit_identical(hip, orc, dims, max_chunks, capacity):
+    """Capacity 64: decode steps run the whole-row attention with the
+    RoPE/quantize/KV write folded in; 600 (over 512 positions): the separate
+    post-processing kernel, the chunk kernel and the merge."""
     model = synthetic_model(dims, 7001)
-    gpu = GpuDecoder(model, slots=4, capacity=64, max_rows=40, max_chunks=max_chunks)
-    cpu = orc.CpuDecoder(model, slots=4, capacity=64, max_chunks=max_chunks)
+    gpu = GpuDecoder(model, slots=4, capacity=capacity, max_rows=40, max_chunks=max_chunks)
+    cpu = orc.CpuDecoder(model, slots=4, capacity=capacity, max_chunks=max_chunks)
     prompts = [random_prompt(10 + s, n, dims["vocab"]) for s, n in zip(range(3), (33, 5, 12))]
     for slot, pr in enumerate(prompts):  # prefill (32+ rows use the prefill matmul)
         pos = np.arange(len(pr))
