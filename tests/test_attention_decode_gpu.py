@@ -95,6 +95,22 @@ def test_decode_attention_short_cache_bit_exact(hip, orc, heads, kv_heads, qk, c
     assert bit_equal(got, oracle_decode(orc, cache, q, qs, heads, spec, max_chunks))
 
 
+@pytest.mark.parametrize("heads,kv_heads,qk,rows", [(16, 16, 64, 17), (32, 4, 64, 9), (16, 2, 48, 16)])
+@pytest.mark.parametrize("capacity,max_chunks", [(2048, 64), (2048, 8), (4096, 64), (600, 2), (1024, 1)])
+def test_decode_attention_long_rows_bit_exact(hip, orc, heads, kv_heads, qk, rows, capacity, max_chunks):
+    """Caches of 600..4096 positions and at least 256 (row, head) pairs, in
+    groups of 1, 8 and 8 query heads per kv head: the chunk kernel and its
+    merge, bit-exact, with full-cache, single-position and random spans."""
+    cache = Cache(orc, hip, 500 + heads + qk + capacity + max_chunks, 4, capacity, kv_heads, qk)
+    rng = np.random.default_rng(capacity + max_chunks + heads)
+    fixed = [(0, 0, capacity), (1, capacity - 1, 1), (2, 0, 2), (3, 5, 33), (0, 100, 17), (1, 0, capacity // 2 + 3)]
+    spec = fixed + [(int(rng.integers(0, 4)), 0, int(rng.integers(1, capacity + 1))) for _ in range(rows - len(fixed))]
+    assert len(spec) * heads >= 256
+    q, qs = queries(orc, cache.st, len(spec), heads, qk)
+    got, _ = run_decode(hip, cache, q, qs, heads, spec, max_chunks)
+    assert bit_equal(got, oracle_decode(orc, cache, q, qs, heads, spec, max_chunks))
+
+
 def test_decode_attention_several_head_blocks(hip, orc):
     """Chunks of up to 1024 positions (capacity 8192, max_chunks 8) leave LDS
     for 5 of 16 kv heads per workgroup: 4 head blocks per row."""
