@@ -96,7 +96,7 @@ def test_decode_attention_short_cache_bit_exact(hip, orc, heads, kv_heads, qk, c
 
 
 @pytest.mark.parametrize("heads,kv_heads,qk,rows", [(16, 16, 64, 17), (32, 4, 64, 9), (16, 2, 48, 16)])
-@pytest.mark.parametrize("capacity,max_chunks", [(2048, 64), (2048, 8), (4096, 64), (600, 2), (1024, 1)])
+@pytest.mark.parametrize("capacity,max_chunks", [(2048, 64), (2048, 8), (4096, 64), (600, 2), (1024, 4)])
 def test_decode_attention_long_rows_bit_exact(hip, orc, heads, kv_heads, qk, rows, capacity, max_chunks):
     """Caches of 600..4096 positions and at least 256 (row, head) pairs, in
     groups of 1, 8 and 8 query heads per kv head: the chunk kernel and its
