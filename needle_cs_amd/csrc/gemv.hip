@@ -713,6 +713,10 @@ __global__ __launch_bounds__(512) void matmul_i8_decode_kernel(MatmulParams p)
     const int g_first = mb0 * 2;
     const u4* wbase = reinterpret_cast<const u4*>(p.tiles) + (size_t)tile * p.blocks * 64 + lane;
     const uint16_t* nrow = p.norms + (size_t)n * p.groups_pad8 + g_first;
+    // every kernel argument the loads need, read before the mask branch: one
+    // round trip to the argument segment instead of one per side of it
+    asm volatile("" ::"s"(p.tiles), "s"(p.norms), "s"(p.q), "s"(p.qscale), "s"(p.cols), "s"(p.blocks),
+                 "s"(p.groups_pad8), "s"(p.tile_mask));
     if (p.tile_mask) {
         // sparse rows: the tile's 16 ids are bits 16*(tile&1).. of word tile/2
         uint32_t live = 0;
@@ -1665,11 +1669,56 @@ int32_t weights_cq_create_internal(const nhip_cq* cq, nhip_weights** out)
                             cq->cols, cq->book, out);
 }
 
+// A pure read with the decode GEMV's access pattern, the bandwidth ceiling
+// one launch of that many bytes can reach: 256-thread workgroups over 32 KB,
+// wave w over 8 KB of them, eight 16-byte non-temporal loads per lane, each
+// wave instruction 1 KB contiguous.  The loaded words are folded by XOR and
+// each workgroup stores its fold (so no load is dead).
+constexpr int kReadChunk = 32 * 1024;
+
+__global__ __launch_bounds__(256) void read_stream_kernel(const u4* src, size_t n16, uint32_t* sink)
+{
+    __shared__ uint32_t wf[4];
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const size_t base = (size_t)blockIdx.x * (kReadChunk / 16) + (size_t)wave * 512 + lane;
+    u4 v[8];
+#pragma unroll
+    for (int c = 0; c < 8; c++) {
+        const size_t i = base + (size_t)c * 64;
+        v[c] = i < n16 ? __builtin_nontemporal_load(src + i) : u4{0u, 0u, 0u, 0u};
+    }
+    uint32_t f = 0u;
+#pragma unroll
+    for (int c = 0; c < 8; c++) f ^= v[c].x ^ v[c].y ^ v[c].z ^ v[c].w;
+    for (int off = 32; off > 0; off >>= 1) f ^= __shfl_xor(f, off);
+    if (lane == 0) wf[wave] = f;
+    __syncthreads();
+    if (threadIdx.x == 0) sink[blockIdx.x] = wf[0] ^ wf[1] ^ wf[2] ^ wf[3];
+}
+
 }  // namespace nhip
 
 using namespace nhip;
 
 extern "C" {
+
+int32_t nhip_read_stream_dev(const void* d_src, size_t bytes, uint32_t* d_sink, void* stream)
+{
+    clear_error();
+    NHIP_REQUIRE(bytes % 16 == 0 && (reinterpret_cast<uintptr_t>(d_src) & 15) == 0,
+                 "read stream: 16-byte aligned source and a multiple of 16 bytes");
+    if (bytes == 0) return NHIP_OK;
+    NHIP_REQUIRE(d_src && d_sink, "read stream: null pointer");
+    int32_t rc = ensure_device();
+    if (rc) return rc;
+    const size_t grid = (bytes + kReadChunk - 1) / kReadChunk;
+    NHIP_REQUIRE(grid <= 0x7FFFFFFF, "read stream: too many bytes");
+    hipLaunchKernelGGL(read_stream_kernel, dim3((unsigned)grid), dim3(256), 0, as_stream(stream),
+                       static_cast<const u4*>(d_src), bytes / 16, d_sink);
+    NHIP_CHECK_HIP(hipGetLastError());
+    return NHIP_OK;
+}
 
 int32_t nhip_weights_i8_create(const int8_t* w, const uint16_t* scales, int32_t rows, int32_t cols,
                                nhip_weights** out)
