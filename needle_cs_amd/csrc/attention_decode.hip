@@ -157,6 +157,10 @@ __global__ __launch_bounds__(kThreads) void decode_attention_kernel(DecodeAttnPa
     float* qs_lds = wl + hmax * lmax;                                       // [16]
     uint32_t* peak_key = reinterpret_cast<uint32_t*>(qs_lds + kMaxHeadsPerBlock);  // [16]
 
+    // the arguments of every load, read together: one round trip to the
+    // argument segment
+    asm volatile("" ::"s"(p.row_slot), "s"(p.row_first), "s"(p.row_count), "s"(p.q), "s"(p.qscale), "s"(p.keys),
+                 "s"(p.kscale), "s"(p.values), "s"(p.vscale), "s"(p.capacity), "s"(p.max_chunks));
     const int slot = p.row_slot[row];
     const int first = p.row_first[row];
     const int count = p.row_count[row];
@@ -371,6 +375,8 @@ __global__ __launch_bounds__(64) void decode_merge_kernel(DecodeAttnParams p)
     const int row = blockIdx.x;
     const int h = blockIdx.y;
     const int d = threadIdx.x;
+    asm volatile("" ::"s"(p.row_slot), "s"(p.row_first), "s"(p.row_count), "s"(p.peaks), "s"(p.sums),
+                 "s"(p.partials), "s"(p.out), "s"(p.capacity), "s"(p.max_chunks), "s"(p.heads));
     const int slot = p.row_slot[row];
     const int first = p.row_first[row];
     const int count = p.row_count[row];
@@ -506,6 +512,12 @@ __global__ __launch_bounds__(kThreads) void decode_attention_row_kernel(DecodeAt
     // with v_readlane).  Nothing branches on them, so the loads issue
     // together.  A row with an invalid slot or span runs on the span (slot
     // 0, first 0, count 1), writes zeros and no cache row.
+    asm volatile("" ::"s"(p.row_slot), "s"(p.row_first), "s"(p.row_count), "s"(p.keys), "s"(p.kscale),
+                 "s"(p.values), "s"(p.vscale), "s"(p.capacity), "s"(p.max_chunks), "s"(p.heads), "s"(p.kv_heads));
+    if constexpr (POST)
+        asm volatile("" ::"s"(p.qkv), "s"(p.positions), "s"(p.rope_cos), "s"(p.rope_sin), "s"(p.rows));
+    else
+        asm volatile("" ::"s"(p.q), "s"(p.qscale));
     const int slot_in = uniform_load(p.row_slot, row);
     const int first_in = uniform_load(p.row_first, row);
     const int count_in = uniform_load(p.row_count, row);

@@ -103,6 +103,7 @@ __device__ __forceinline__ float log_poly(float x)
 
 __global__ __launch_bounds__(kThreads) void embed_kernel(const int32_t* tokens, const float* emb, int d, float* x)
 {
+    asm volatile("" ::"s"(tokens), "s"(emb), "s"(d), "s"(x));  // one round trip to the arguments
     const float* src = emb + (size_t)tokens[blockIdx.x] * d;
     float* dst = x + (size_t)blockIdx.x * d;
     for (int i = threadIdx.x; i < d; i += kThreads) dst[i] = src[i];

@@ -842,6 +842,10 @@ __global__ __launch_bounds__(512) void matmul_cq_decode_kernel(MatmulParams p)
     const int g_first = wave * GPW;
     const u4* wbase = reinterpret_cast<const u4*>(p.tiles) + (size_t)tile * p.blocks * 64 + lane;
     const uint16_t* nrow = p.norms + (size_t)n * p.groups_pad8;
+    // the arguments of every load, read together: one round trip to the
+    // argument segment
+    asm volatile("" ::"s"(p.tiles), "s"(p.norms), "s"(p.q), "s"(p.qscale), "s"(p.offsets), "s"(p.cols),
+                 "s"(p.stride), "s"(p.blocks), "s"(p.groups_pad8), "s"(p.tile_mask));
 
     // 1. A operands: lane (r, kq) feeds A row r of every set, token r%4
     //    (rows of tokens >= M repeat token M-1; their D rows are never
@@ -962,6 +966,10 @@ __global__ __launch_bounds__(512) void matmul_i8_decode_fused_kernel(MatmulParam
     const int g_first = mb0 * 2;
     const u4* wbase = reinterpret_cast<const u4*>(p.tiles) + (size_t)tile * p.blocks * 64 + lane;
     const uint16_t* nrow = p.norms + (size_t)n * p.groups_pad8 + g_first;
+    // the arguments of every load, read together: one round trip to the
+    // argument segment
+    asm volatile("" ::"s"(p.tiles), "s"(p.norms), "s"(p.blocks), "s"(p.groups_pad8), "s"(f.x), "s"(f.delta),
+                 "s"(f.gain));
     constexpr bool NORM = KIND == kProNorm;
     const int nt = NORM ? 256 : (int)blockDim.x;
 
