@@ -110,6 +110,32 @@ class GemvCase:
             w.close()
 
 
+class ReadCase:
+    """The read ceiling of one launch: nhip_read_stream_dev over `nbytes`
+    (the GEMV's weight and scale bytes) with the GEMV's access pattern,
+    cycling as many distinct buffers as the GEMV cycles weight copies."""
+
+    def __init__(self, nbytes: int, copies: int):
+        self.nbytes = nbytes - nbytes % 16
+        self.bufs = []
+        for _ in range(copies):
+            b = N.DeviceBuffer(self.nbytes)
+            N.check(N.lib().nhip_memset(b.ptr, 0x5A, b.nbytes))
+            self.bufs.append(b)
+        self.sink = N.DeviceBuffer(-(-self.nbytes // 32768) * 4)
+
+    def launch(self, i: int) -> None:
+        b = self.bufs[i % len(self.bufs)]
+        N.check(N.lib().nhip_read_stream_dev(b.ptr, self.nbytes, self.sink.ptr, None))
+
+    time = GemvCase.time
+
+    def close(self) -> None:
+        for b in self.bufs:
+            b.close()
+        self.sink.close()
+
+
 class GemmCase(GemvCase):
     """Prefill int8 GEMM: M=512 tokens, K=2048, N=8192, per-token int8
     activations; `fused` selects the fused-epilogue entry point."""
@@ -407,6 +433,17 @@ def main() -> int:
     ms = main_case.time(args.steps, args.warmup)
     gbs = main_case.bytes / (ms * 1e-3) / 1e9
     print(f"# headline GEMV M=3 K=2048 N=8192: {ms * 1e3:.2f} us/launch, {gbs:.0f} GB/s", file=sys.stderr, flush=True)
+    rcase = ReadCase(main_case.bytes - (main_case.m * main_case.k + main_case.m * 4 + main_case.m * main_case.n * 4),
+                     main_case.copies)
+    rms = rcase.time(args.steps, args.warmup)
+    rgbs = rcase.nbytes / (rms * 1e-3) / 1e9
+    read_ceiling = {"workload": "pure read of the GEMV's weight and scale bytes, the GEMV's load pattern "
+                                "(nhip_read_stream_dev), same copies cycled",
+                    "bytes_per_launch": rcase.nbytes, "us_per_launch": round(rms * 1e3, 3), "GB/s": round(rgbs, 1),
+                    "frac_hbm_peak": round(rgbs / HBM_PEAK_GBS, 4),
+                    "gemv_frac_of_read_ceiling": round(rms / ms, 4)}
+    print(f"# read ceiling {rcase.nbytes} B: {rms * 1e3:.2f} us/launch, {rgbs:.0f} GB/s", file=sys.stderr, flush=True)
+    rcase.close()
 
     secondary = []
     if not args.no_secondary:
@@ -477,6 +514,7 @@ def main() -> int:
         "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": measured_traffic()},
         "cpu_baseline": cpu,
+        "read_ceiling": read_ceiling,
         "secondary": secondary,
         "prefill": prefill,
         "attention": attention,

@@ -198,6 +198,14 @@ int32_t nhip_matmul_i8_dev(const nhip_weights* w, const int8_t* d_q, const float
                            int32_t tokens, float* d_y, int32_t ldy, int32_t row_start,
                            int32_t row_end, void* stream);
 
+/* Bandwidth calibration, no reference counterpart: reads `bytes` (a multiple
+ * of 16) from d_src with the decode GEMV's access pattern (16-byte
+ * non-temporal loads, 1 KB per wave instruction, 32 KB per 256-thread
+ * workgroup) and writes each workgroup's XOR of the words it read to
+ * d_sink[ceil(bytes / 32768)].  The time of one launch is the read ceiling
+ * of a GEMV over the same bytes. */
+int32_t nhip_read_stream_dev(const void* d_src, size_t bytes, uint32_t* d_sink, void* stream);
+
 /* Prefill form of nhip_matmul_i8_dev with a fused epilogue: the same exact
  * int32 group sums D_g, accumulated as acc = fma(h(scale[n][g]), D_g, acc)
  * and scaled once, y = acc * qscale[t] -- two VALU operations per (token,

@@ -85,6 +85,7 @@ _PROTOS = {
     "nhip_decoder_forward": (_i32, [_vp, _vp, _vp, _vp, _i32, _vp, _i32, _vp, _vp]),
     "nhip_decoder_forward_masked": (_i32, [_vp, _vp, _vp, _vp, _i32, _vp, _i32, _vp, _vp]),
     "nhip_argmax_masked_dev": (_i32, [_vp, _i32, _vp, _i32, _i32, _i32, _i32, _vp, _vp, _vp]),
+    "nhip_read_stream_dev": (_i32, [_vp, C.c_size_t, _vp, _vp]),
     "nhip_topk_lse_workspace": (C.c_size_t, [_i32, _i32]),
     "nhip_topk_lse_dev": (_i32, [_vp, _i32, _i32, _i32, _vp, C.c_size_t, _vp, _vp, _vp]),
     "nhip_needle3_attention_inputs_dev": (_i32, [_vp, _i32, _i32, _i32, _i32, _i32] + [_vp] * 10 +
