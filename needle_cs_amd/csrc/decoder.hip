@@ -428,7 +428,8 @@ __global__ __launch_bounds__(64) void topk_final_kernel(const float* bvals, cons
         const float v = sv[c];
         const int i = si[c];
         int rank = 0;
-        for (int o = 0; o < n; o++) {
+#pragma unroll 8
+        for (int o = 0; o < n; o++) {  // unrolled: the LDS reads of 8 candidates issue together
             const float ov = sv[o];
             const int oi = si[o];
             rank += (before(ov, oi, v, i) || (ov == v && oi == i && o < c)) ? 1 : 0;
@@ -446,6 +447,7 @@ __global__ __launch_bounds__(64) void topk_final_kernel(const float* bvals, cons
     __syncthreads();
     if (tid != 0) return;
     float total = 0.0f;
+#pragma unroll 8
     for (int b = 0; b < blocks; b++) total = total + prod[b];
     const float log_shift = peak + log_poly(total);
 #pragma unroll
