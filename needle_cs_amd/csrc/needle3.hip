@@ -40,22 +40,37 @@ struct Needle3Params {
     int32_t rows, heads, kv_heads, qk, vd, slots, capacity;
 };
 
-__device__ __forceinline__ bool row_valid(const Needle3Params& p, int r)
+// Row r's run flags from the (slot, position) of rows r - 2 .. r + 1, all
+// loaded up front (clamped indexes) so they take one round trip: what
+// row_valid and continues compute, without their chain of dependent loads.
+struct RunFlags {
+    bool valid, run1, run2, next_continues;
+    int slot, pos;
+};
+// A uniform load through the scalar cache (the kernels store to global
+// memory, so the compiler would otherwise use vector loads for these
+// arrays, which no kernel of the launch writes).
+__device__ __forceinline__ int32_t uniform_load(const int32_t* a, int i)
 {
-    const int slot = p.row_slot[r], pos = p.row_pos[r];
-    return slot >= 0 && slot < p.slots && pos >= 0 && pos < p.capacity;
+    return ((const __attribute__((address_space(4))) int32_t*)a)[i];
 }
 
-// rows r - back .. r are one run: valid, one slot, consecutive positions
-__device__ __forceinline__ bool continues(const Needle3Params& p, int r, int back)
+__device__ __forceinline__ RunFlags run_flags(const Needle3Params& p, int r)
 {
-    if (!row_valid(p, r)) return false;
-    for (int b = 1; b <= back; b++) {
-        if (r - b < 0 || !row_valid(p, r - b) || p.row_slot[r - b] != p.row_slot[r] ||
-            p.row_pos[r - b] != p.row_pos[r] - b)
-            return false;
-    }
-    return true;
+    const int ra = max(r - 2, 0), rb = max(r - 1, 0), rc = min(r + 1, p.rows - 1);
+    const int s2 = uniform_load(p.row_slot, ra), q2 = uniform_load(p.row_pos, ra);
+    const int s1 = uniform_load(p.row_slot, rb), q1 = uniform_load(p.row_pos, rb);
+    const int s0 = uniform_load(p.row_slot, r), q0 = uniform_load(p.row_pos, r);
+    const int sn = uniform_load(p.row_slot, rc), qn = uniform_load(p.row_pos, rc);
+    auto ok = [&](int s, int q) { return (s >= 0) & (s < p.slots) & (q >= 0) & (q < p.capacity); };
+    RunFlags f;
+    f.valid = ok(s0, q0);
+    f.run1 = f.valid & (r >= 1) & ok(s1, q1) & (s1 == s0) & (q1 == q0 - 1);
+    f.run2 = f.run1 & (r >= 2) & ok(s2, q2) & (s2 == s0) & (q2 == q0 - 2);
+    f.next_continues = (r + 1 < p.rows) & ok(sn, qn) & f.valid & (sn == s0) & (qn == q0 + 1);
+    f.slot = s0;
+    f.pos = q0;
+    return f;
 }
 
 __global__ __launch_bounds__(64) void needle3_inputs_kernel(Needle3Params p)
@@ -73,16 +88,17 @@ __global__ __launch_bounds__(64) void needle3_inputs_kernel(Needle3Params p)
     const int W = part == 0 ? qw : (part == 1 ? kw : vw);
     const int base = part == 0 ? 0 : (part == 1 ? qw : qw + kw);
     const int off = head * n;
-    if (!row_valid(p, r)) {  // q = 0 with scale 1; nothing else is touched
+    const RunFlags rf = run_flags(p, r);
+    if (!rf.valid) {  // q = 0 with scale 1; nothing else is touched
         if (part == 0) {
             if (c < n) p.q[(size_t)r * qw + off + c] = 0;
             if (c == 0) p.q_scales[(size_t)r * p.heads + head] = 1.0f;
         }
         return;
     }
-    const int slot = p.row_slot[r], pos = p.row_pos[r];
-    const bool run1 = continues(p, r, 1);
-    const bool run2 = run1 && continues(p, r, 2);
+    const int slot = rf.slot, pos = rf.pos;
+    const bool run1 = rf.run1;
+    const bool run2 = rf.run2;
     const float* hist = p.history + (size_t)slot * 2 * all + 2 * base;  // frame 0, then frame 1 (latest)
     const float* taps = p.taps[part] + off;
     float x = 0.0f;
@@ -98,7 +114,8 @@ __global__ __launch_bounds__(64) void needle3_inputs_kernel(Needle3Params p)
         red[c] = x * x;
         __syncthreads();
         float sum = 0.0f;
-        for (int i = 0; i < n; i++) sum = sum + red[i];
+#pragma unroll 8
+        for (int i = 0; i < n; i++) sum = sum + red[i];  // ascending; the reads issue 8 at a time
         const float inverse = 1.0f / sqrtf(sum / (float)n + 1e-6f);
         const float* scale = part == 0 ? p.q_norm : p.k_norm;
         x = c < n ? (1.0f + scale[c]) * x * inverse : 0.0f;
@@ -137,12 +154,13 @@ __global__ __launch_bounds__(64) void needle3_inputs_kernel(Needle3Params p)
 __global__ __launch_bounds__(256) void needle3_history_kernel(Needle3Params p)
 {
     const int r = blockIdx.x;
-    if (!row_valid(p, r)) return;
-    if (r + 1 < p.rows && continues(p, r + 1, 1)) return;  // not the run's last row
+    const RunFlags rf = run_flags(p, r);
+    if (!rf.valid) return;
+    if (rf.next_continues) return;  // not the run's last row
     const int qw = p.heads * p.qk, kw = p.kv_heads * p.qk, vw = p.kv_heads * p.vd;
     const int all = qw + kw + vw;
-    const bool run1 = continues(p, r, 1);
-    float* hist = p.history + (size_t)p.row_slot[r] * 2 * all;
+    const bool run1 = rf.run1;
+    float* hist = p.history + (size_t)rf.slot * 2 * all;
     for (int e = threadIdx.x; e < all; e += blockDim.x) {
         const int part = e < qw ? 0 : (e < qw + kw ? 1 : 2);
         const int base = part == 0 ? 0 : (part == 1 ? qw : qw + kw);
