@@ -136,6 +136,48 @@ class ReadCase:
         self.sink.close()
 
 
+class Needle3Case:
+    """Needle 3 attention inputs (nhip_needle3_attention_inputs_dev) for `rows`
+    rows of one geometry: three-tap convolution over the slot history,
+    ZeroCenteredRms, Rope and QuantizeInt8 into the queries and the KV cache.
+    Rows of a slot are consecutive positions (a run per slot)."""
+
+    def __init__(self, seed: int, rows: int, slots: int, heads: int = 16, kv: int = 16, qk: int = 64, vd: int = 64,
+                 capacity: int = 256):
+        st = C.c_uint64(seed)
+        self.rows, self.g, self.slots, self.capacity = rows, (heads, kv, qk, vd), slots, capacity
+        qw, kw, vw = heads * qk, kv * qk, kv * vd
+        allw = qw + kw + vw
+        D = N.DeviceBuffer.from_array
+        f = lambda n, sc=1.0: N.synth_normal(st, n) * np.float32(sc)
+        self.bufs = [D(f(rows * allw))]
+        self.bufs += [D(f(3 * w, 0.5)) for w in (qw, kw, vw)]
+        self.bufs += [D(f(qk, 0.1)), D(f(qk, 0.1))]
+        ang = N.synth_uniform(st, capacity * qk // 2, 0.0, 6.28)
+        self.bufs += [D(np.cos(ang).astype(np.float32)), D(np.sin(ang).astype(np.float32)), D(f(slots * 2 * allw))]
+        per = -(-rows // slots)
+        assert 100 + per < capacity
+        slot = np.repeat(np.arange(slots, dtype=np.int32), per)[:rows]
+        pos = np.concatenate([100 + np.arange(per, dtype=np.int32)] * slots)[:rows]
+        self.bufs += [D(slot), D(pos)]
+        self.bufs += [N.DeviceBuffer(rows * qw), N.DeviceBuffer(rows * heads * 4),
+                      N.DeviceBuffer(slots * capacity * kw), N.DeviceBuffer(slots * capacity * kv * 4),
+                      N.DeviceBuffer(slots * capacity * vw), N.DeviceBuffer(slots * capacity * kv * 4)]
+
+    def launch(self, i: int) -> None:
+        heads, kv, qk, vd = self.g
+        b = [x.ptr for x in self.bufs]
+        N.check(N.lib().nhip_needle3_attention_inputs_dev(
+            b[0], self.rows, heads, kv, qk, vd, b[1], b[2], b[3], b[4], b[5], b[6], b[7], b[8], b[9], b[10],
+            self.slots, self.capacity, b[11], b[12], b[13], b[14], b[15], b[16], None))
+
+    time = GemvCase.time
+
+    def close(self) -> None:
+        for x in self.bufs:
+            x.close()
+
+
 class GemmCase(GemvCase):
     """Prefill int8 GEMM: M=512 tokens, K=2048, N=8192, per-token int8
     activations; `fused` selects the fused-epilogue entry point."""
@@ -484,6 +526,17 @@ def main() -> int:
         print(f"# attention: {t * 1e3:.2f} us/launch, {g:.0f} GB/s over {case.bytes} B", file=sys.stderr, flush=True)
         case.close()
 
+    needle3 = []
+    if not args.no_secondary:
+        for rows, slots, what in ((3, 3, "one decode step of 3 rows in 3 slots"),
+                                  (128, 1, "a 128-row prefill chunk of one slot")):
+            case = Needle3Case(seed=0x5005 + rows, rows=rows, slots=slots)
+            t = case.time(max(200, args.steps // 4), args.warmup)
+            needle3.append({"workload": f"Needle 3 attention inputs, 16 heads x 64, {what}", "rows": rows,
+                            "us_per_launch": round(t * 1e3, 3)})
+            print(f"# needle3 attention inputs, {rows} rows: {t * 1e3:.2f} us/launch", file=sys.stderr, flush=True)
+            case.close()
+
     threads = int(os.environ.get("NEEDLE_THREADS", "0")) or min(physical_cores(), int(os.environ.get("OMP_NUM_THREADS", "16") or 16))
     loop = None
     if not args.no_decode_loop:
@@ -518,6 +571,7 @@ def main() -> int:
         "secondary": secondary,
         "prefill": prefill,
         "attention": attention,
+        "needle3_inputs": needle3,
         "decode_loop": loop,
     }
     main_case.close()
