@@ -378,8 +378,49 @@ int32_t nhip_argmax_masked_dev(const float* d_x, int32_t ldx, const uint32_t* d_
 size_t nhip_topk_lse_workspace(int32_t rows, int32_t n);
 int32_t nhip_topk_lse_dev(const float* d_logits, int32_t rows, int32_t n, int32_t k, void* d_workspace,
                           size_t workspace_bytes, int32_t* d_idx, float* d_lp, void* stream);
-/* Engine.CopyFrom: positions [0, length) of slot src into slot dst. */
+/* Ops.ArgMax (src/Needle/Ops.cs:1052-1090; Engine.Greedy, Engine.cs:103)
+ * over `rows` device rows of n values (row r at d_x + r*ldx): d_index[r] =
+ * the lowest id holding the row's largest non-NaN value, 0 when x[0] is NaN
+ * (the scalar loop's `x[i] > x[best]` from best = 0: +0 and -0 are equal, an
+ * all -inf row gives 0; the AVX path gives the same ids on NaN-free rows);
+ * d_value[r] (optional) = that value.  Asynchronous on `stream`. */
+int32_t nhip_argmax_dev(const float* d_x, int32_t ldx, int32_t n, int32_t rows, int32_t* d_index, float* d_value,
+                        void* stream);
+/* Engine.CopyFrom (src/Needle/Engine.cs:367-379): positions [0, length) of
+ * slot src into slot dst, whose length (for nhip_decoder_step) becomes
+ * `length`. */
 int32_t nhip_decoder_copy_slot(nhip_decoder* m, int32_t dst, int32_t src, int32_t length);
+/* The step API of the batched engine: BatchedEngine.ForwardBatch /
+ * EngineCore.ForwardBatch (src/Needle/BatchEngine.cs:38-39,
+ * src/Needle/Engine.cs:2303-2350).  Rows carry tokens[r] into slot
+ * row_slots[r]; the rows of a slot form one contiguous run and sit at the
+ * slot's length + their offset in the run (Engine.cs:2655-2661), and every
+ * slot's length grows by its run (NHIP_ERR_ARG past the capacity, before any
+ * device work).  The LM head runs only over head_rows[0..heads) (rows of
+ * this call): row i of the outputs is row head_rows[i] -- logits [heads][vocab]
+ * (BatchLogitsRow), the top-k ids / log-probabilities [heads][k] if k > 0,
+ * Ops.ArgMax of each head row into argmax[heads] if non-NULL.  rows <= 16
+ * replay a graph captured per (rows, heads, k, argmax).  Synchronous.
+ * nhip_decoder_forward (explicit positions) leaves the lengths alone. */
+int32_t nhip_decoder_step(nhip_decoder* m, const int32_t* tokens, const int32_t* row_slots, int32_t rows,
+                          const int32_t* head_rows, int32_t heads, float* logits, int32_t k, int32_t* topk_idx,
+                          float* topk_lp, int32_t* argmax);
+/* BatchedEngine.ResetSlot / MarkSlot / RewindSlot / SlotLength
+ * (src/Needle/BatchEngine.cs:25-30): reset sets a slot's length (and mark) to
+ * 0, mark records its length, rewind returns to the mark; the next step
+ * overwrites the cache from there. */
+int32_t nhip_decoder_slot_reset(nhip_decoder* m, int32_t slot);
+int32_t nhip_decoder_slot_mark(nhip_decoder* m, int32_t slot);
+int32_t nhip_decoder_slot_rewind(nhip_decoder* m, int32_t slot);
+int32_t nhip_decoder_slot_length(const nhip_decoder* m, int32_t slot, int32_t* length);
+/* Greedy decoding, ToolCaller.Complete's loop (src/Needle/ToolCaller.cs:
+ * 59-77) on slot 0: reset it, feed the prompt (chunks of max_rows rows, the
+ * head on the last row only), then up to max_new times take Ops.ArgMax of
+ * the last logits on the device, stop before a token equal to `stop` (-1:
+ * none), otherwise record it and feed it.  Writes the tokens (without the
+ * prompt) and their count. */
+int32_t nhip_decoder_greedy(nhip_decoder* m, const int32_t* prompt, int32_t prompt_len, int32_t max_new,
+                            int32_t stop, int32_t* out_tokens, int32_t* out_len, nhip_decode_stats* stats);
 /* Prefill `prompt` into slot 0, then beam search of `width` beams for up to
  * max_new tokens (length penalty 1, EOS `eos`); writes the winner's tokens
  * (without the prompt), its length and normalised score. */

@@ -91,6 +91,13 @@ _PROTOS = {
     "nhip_needle3_attention_inputs_dev": (_i32, [_vp, _i32, _i32, _i32, _i32, _i32] + [_vp] * 10 +
                                           [_i32, _i32] + [_vp] * 7),
     "nhip_decoder_copy_slot": (_i32, [_vp, _i32, _i32, _i32]),
+    "nhip_argmax_dev": (_i32, [_vp, _i32, _i32, _i32, _vp, _vp, _vp]),
+    "nhip_decoder_step": (_i32, [_vp, _vp, _vp, _i32, _vp, _i32, _vp, _i32, _vp, _vp, _vp]),
+    "nhip_decoder_slot_reset": (_i32, [_vp, _i32]),
+    "nhip_decoder_slot_mark": (_i32, [_vp, _i32]),
+    "nhip_decoder_slot_rewind": (_i32, [_vp, _i32]),
+    "nhip_decoder_slot_length": (_i32, [_vp, _i32, _vp]),
+    "nhip_decoder_greedy": (_i32, [_vp, _vp, _i32, _i32, _i32, _vp, _vp, _vp]),
     "nhip_decoder_beam_search": (_i32, [_vp, _vp, _i32, _i32, _i32, _i32, _vp, _vp, _vp, _vp]),
     "nhip_decoder_destroy": (_i32, [_vp]),
     "nhip_open": (_i32, [_vp, _sz, C.POINTER(_vp)]),

@@ -112,14 +112,18 @@ __global__ __launch_bounds__(kThreads) void embed_kernel(const int32_t* tokens, 
 // x += delta (when given); ss = sum x^2 (canonical sum); inv = 1 / sqrt(ss /
 // d + eps); h = (x * inv) * gain; QuantizeInt8(h) -> q, scale.  Thread t
 // holds the float4 groups at 4t + 1024j (d a multiple of 4, at most 4096).
+// Block b reads row row_map[b] of x and delta (row b without a map) and
+// writes row b of q and qscale: the LM head's rows of a forward.
 template <bool DELTA>
 __global__ __launch_bounds__(kThreads) void add_rmsnorm_quant_kernel(float* x, const float* delta, const float* gain,
-                                                                     int d, float eps, int8_t* q, float* qscale)
+                                                                     int d, float eps, int8_t* q, float* qscale,
+                                                                     const int32_t* row_map)
 {
     __shared__ __align__(16) float red[kThreads + 8];  // partials, the broadcast sum, 4 wave maxima
     const int t = threadIdx.x;
-    float* xr = x + (size_t)blockIdx.x * d;
-    const float* dr = DELTA ? delta + (size_t)blockIdx.x * d : nullptr;
+    const int src = row_map ? row_map[blockIdx.x] : (int)blockIdx.x;
+    float* xr = x + (size_t)src * d;
+    const float* dr = DELTA ? delta + (size_t)src * d : nullptr;
     float4 v[kGroups4], gv[kGroups4];
 #pragma unroll
     for (int j = 0; j < kGroups4; j++) {  // every load first
@@ -265,10 +269,15 @@ __device__ __forceinline__ bool before(float va, int ia, float vb, int ib)
 
 __device__ __forceinline__ bool masked(int i) { return i == 0 || i == 2 || i == 3; }
 
-// TopKLogSoftmax (src/Needle/Ops.cs:1092-1221) in the canonical float form:
-// top K of the ids except 0, 2, 3 (the set is unique under the order above,
-// so merging per-thread and per-block lists equals the reference's
-// sequential insertion); log_shift = peak + log(S), masked v_i = -1e30, with
+// TopKLogSoftmax (src/Needle/Ops.cs:1092-1221) in the canonical float form.
+// The ids are the reference's selection (Ops.cs:1094-1166) for NaN-free
+// rows: id 1 (always) and every id from 4 on holding a value above -inf are
+// candidates, the top K of them under the order above fill the slots (the
+// set is unique under that order, so merging per-thread and per-block lists
+// equals the sequential insertion), slots left over hold (-inf, -1), and when
+// no id from 4 on is above -inf while x[4] is -inf, the last slot, if left
+// over, holds (-inf, 4): the reference's scan admits its first value even at
+// -inf and drops it at the next entry.  log_shift = peak + log(S), masked v_i = -1e30, with
 // S over blocks of kTopkBlock ids: S_b = sum Exp(v_i - m_b) (m_b the block
 // maximum, the canonical row reduction over the block's ids) and S = sum_b
 // Exp(m_b - peak) * S_b in ascending b; lp = v - log_shift.  One workgroup
@@ -321,7 +330,10 @@ __global__ __launch_bounds__(kThreads) void topk_block_kernel(const float* logit
         if (i >= n) continue;
         xv[j] = masked(i) ? -1e30f : xv[j];
         mloc = fmaxf(mloc, xv[j]);
-        if (masked(i) || !before(xv[j], i, bv[K - 1], bi[K - 1])) continue;
+        // the reference's scan admits a value only above -inf (its first
+        // scanned id aside, which the final merge restores), except id 1,
+        // which it places first whatever its value
+        if (masked(i) || (!(xv[j] > -INFINITY) && i != 1) || !before(xv[j], i, bv[K - 1], bi[K - 1])) continue;
         bv[K - 1] = xv[j];
         bi[K - 1] = i;
 #pragma unroll
@@ -396,8 +408,9 @@ __global__ __launch_bounds__(kThreads) void topk_block_kernel(const float* logit
 // Merge of a row's block lists (sequential insertion in the (value, id)
 // order) and S = sum_b Exp(m_b - peak) * S_b in ascending b.
 template <int K>
-__global__ __launch_bounds__(64) void topk_final_kernel(const float* bvals, const int32_t* bids, const float* bmax,
-                                                         const float* bsum, int blocks, int32_t* idx, float* lp)
+__global__ __launch_bounds__(64) void topk_final_kernel(const float* logits, int width, const float* bvals,
+                                                         const int32_t* bids, const float* bmax, const float* bsum,
+                                                         int blocks, int32_t* idx, float* lp)
 {
     // The row's top K of the blocks' candidates under `before` (value, then
     // the lower id).  That order is total on the candidates (never NaN; the
@@ -440,6 +453,15 @@ __global__ __launch_bounds__(64) void topk_final_kernel(const float* bvals, cons
         }
     }
     __syncthreads();
+    if (tid == 0 && best_i[K - 1] == 0x7FFFFFFF && width > 4) {
+        // fewer than K candidates: the reference keeps its first scanned id
+        // (4) in the last slot when it was -inf and no later id entered
+        bool later = false;
+#pragma unroll
+        for (int m = 0; m < K; m++) later = later || (best_i[m] != 1 && best_i[m] != 0x7FFFFFFF);
+        if (!later && logits[(size_t)row * width + 4] == -INFINITY) best_i[K - 1] = 4;
+    }
+    __syncthreads();
     // log-sum-exp over the blocks in ascending order: the terms
     // Exp(max_b - peak) * sum_b in parallel, then their sum in order
     const float peak = best_v[0];
@@ -452,7 +474,7 @@ __global__ __launch_bounds__(64) void topk_final_kernel(const float* bvals, cons
     const float log_shift = peak + log_poly(total);
 #pragma unroll
     for (int m = 0; m < K; m++) {
-        idx[(size_t)row * K + m] = best_i[m];
+        idx[(size_t)row * K + m] = best_i[m] == 0x7FFFFFFF ? -1 : best_i[m];
         lp[(size_t)row * K + m] = best_v[m] - log_shift;
     }
 }
@@ -476,8 +498,8 @@ int32_t launch_topk(const float* logits, int rows, int n, int k, const TopkScrat
     case K:                                                                                                      \
         hipLaunchKernelGGL(topk_block_kernel<K>, dim3(blocks, rows), dim3(kThreads), 0, s, logits, n, blocks,    \
                            ts.vals, ts.ids, ts.bmax, ts.bsum);                                                   \
-        hipLaunchKernelGGL(topk_final_kernel<K>, dim3(rows), dim3(64), 0, s, ts.vals, ts.ids, ts.bmax, ts.bsum,   \
-                           blocks, idx, lp);                                                                     \
+        hipLaunchKernelGGL(topk_final_kernel<K>, dim3(rows), dim3(64), 0, s, logits, n, ts.vals, ts.ids, ts.bmax, \
+                           ts.bsum, blocks, idx, lp);                                                            \
         break;
         NHIP_TOPK_CASE(1)
         NHIP_TOPK_CASE(2)
@@ -574,6 +596,74 @@ int32_t launch_argmax_masked(const float* x, int ldx, const uint32_t* mask, int 
     return NHIP_OK;
 }
 
+// Ops.ArgMax per row (src/Needle/Ops.cs:1052-1090).  The scalar loop starts
+// at id 0 and moves to id i only when x[i] > x[best], so: 0 when x[0] is
+// NaN, otherwise the lowest id holding the largest non-NaN value (+0 and -0
+// are equal, every -inf row gives 0).  The AVX path (first id equal to the
+// maximum) gives the same id on every NaN-free row.  Each of 1024 threads
+// keeps the best (value, id) of ids tid, tid + 1024, ... ("larger value,
+// then lower id", NaN never taken) and the block reduces the pairs in the
+// same order.
+__global__ __launch_bounds__(kArgmaxThreads) void argmax_kernel(const float* x, int ldx, int n, int32_t* index,
+                                                                float* value)
+{
+    __shared__ float sv[kArgmaxThreads / 64];
+    __shared__ int si[kArgmaxThreads / 64];
+    const int row = blockIdx.x;
+    const int tid = threadIdx.x;
+    const float* xr = x + (size_t)row * ldx;
+    auto better = [](float v, int i, float bv2, int bi2) { return v > bv2 || (v == bv2 && i < bi2); };
+    float bv = -INFINITY;
+    int bi = 0x7FFFFFFF;
+    for (int base = tid; base < n; base += kArgmaxThreads * kArgmaxBatch) {
+        float v[kArgmaxBatch];
+#pragma unroll
+        for (int j = 0; j < kArgmaxBatch; j++) v[j] = xr[min(base + j * kArgmaxThreads, n - 1)];
+#pragma unroll
+        for (int j = 0; j < kArgmaxBatch; j++) {
+            const int i = base + j * kArgmaxThreads;
+            if (i < n && better(v[j], i, bv, bi)) {
+                bv = v[j];
+                bi = i;
+            }
+        }
+    }
+    for (int off = 32; off > 0; off >>= 1) {
+        const float ov = __shfl_xor(bv, off);
+        const int oi = __shfl_xor(bi, off);
+        if (better(ov, oi, bv, bi)) {
+            bv = ov;
+            bi = oi;
+        }
+    }
+    if ((tid & 63) == 0) {
+        sv[tid >> 6] = bv;
+        si[tid >> 6] = bi;
+    }
+    __syncthreads();
+    if (tid == 0) {
+        for (int w = 1; w < kArgmaxThreads / 64; w++)
+            if (better(sv[w], si[w], bv, bi)) {
+                bv = sv[w];
+                bi = si[w];
+            }
+        const float x0 = xr[0];
+        if (x0 != x0 || bi == 0x7FFFFFFF) {  // NaN at id 0 (or every value NaN with it)
+            bi = 0;
+            bv = x0;
+        }
+        index[row] = bi;
+        if (value) value[row] = bv;
+    }
+}
+
+int32_t launch_argmax(const float* x, int ldx, int n, int rows, int32_t* index, float* value, hipStream_t s)
+{
+    hipLaunchKernelGGL(argmax_kernel, dim3(rows), dim3(kArgmaxThreads), 0, s, x, ldx, n, index, value);
+    NHIP_CHECK_HIP(hipGetLastError());
+    return NHIP_OK;
+}
+
 // Copies positions [0, length) of slot src to slot dst in every layer's
 // four cache pools (Engine.CopyFrom).
 __global__ void kv_copy_kernel(int8_t* keys, int8_t* values, float* key_scales, float* value_scales, int slots,
@@ -606,6 +696,29 @@ __global__ void kv_copy_kernel(int8_t* keys, int8_t* values, float* key_scales, 
 
 using namespace nhip;
 
+// What a forward computes after its layers: the LM head over `heads` of its
+// rows (all of them, in order, when `all_rows`), then the top-k (k > 0) or
+// Ops.ArgMax (`argmax`) of each head row.
+struct HeadPlan {
+    int heads = 0;
+    bool all_rows = true;
+    int k = 0;
+    bool argmax = false;
+    bool operator==(const HeadPlan& o) const
+    {
+        return heads == o.heads && all_rows == o.all_rows && k == o.k && argmax == o.argmax;
+    }
+};
+
+// A decode step captured as a graph: its row count and head plan.  Replays
+// read the step's inputs (tokens, slots, positions, spans, head rows) from
+// device memory the host refreshes before each launch.
+struct StepGraph {
+    int rows;
+    HeadPlan head;
+    hipGraphExec_t exec;
+};
+
 struct nhip_decoder {
     nhip_decoder_dims dims{};
     int qkv_n = 0;
@@ -633,10 +746,11 @@ struct nhip_decoder {
     float* gu = nullptr;
     float* act = nullptr;  // SwiGLU activations [rows][ffn] of the fused gate/up matmul
     float* logits = nullptr;
-    int32_t* d_in = nullptr;  // tokens, slots, positions, first (0), count: 5 x max_rows
+    int32_t* d_in = nullptr;  // tokens, slots, positions, first (0), count, head rows: 6 x max_rows
     // masked (grammar) head: id bitsets [rows][mask_words] and the chosen ids
     int32_t mask_words = 0;
     uint32_t* d_mask = nullptr;
+    int32_t best_rows = 0;  // rows of d_best / d_best_val: max(max_rows, kMaxMaskedRows)
     int32_t* d_best = nullptr;
     float* d_best_val = nullptr;
     uint32_t* h_mask = nullptr;
@@ -651,8 +765,8 @@ struct nhip_decoder {
     void* attn_ws = nullptr;
     size_t attn_ws_bytes = 0;
     hipStream_t stream = nullptr;
-    hipGraphExec_t graphs[kMaxTopK + 1] = {};
-    int graph_k[kMaxTopK + 1] = {};
+    std::vector<StepGraph> graphs;  // captured decode steps, by their shape
+    std::vector<int32_t> slot_len, slot_mark;  // the step API's slot lengths and marks
     std::vector<void*> allocations;
 };
 
@@ -673,6 +787,7 @@ int32_t* in_slots(nhip_decoder* m, int32_t* base) { return base + m->dims.max_ro
 int32_t* in_positions(nhip_decoder* m, int32_t* base) { return base + 2 * m->dims.max_rows; }
 int32_t* in_first(nhip_decoder* m, int32_t* base) { return base + 3 * m->dims.max_rows; }
 int32_t* in_count(nhip_decoder* m, int32_t* base) { return base + 4 * m->dims.max_rows; }
+int32_t* in_heads(nhip_decoder* m, int32_t* base) { return base + 5 * m->dims.max_rows; }
 
 // Residual + RMSNorm + quantize feeding a matmul.  For up to four rows and
 // at most kFusedPrologueMaxTiles row tiles one fused launch computes the
@@ -702,10 +817,10 @@ int32_t norm_matmul(nhip_decoder* m, int rows, float** x, bool pending, const fl
     }
     if (pending)
         hipLaunchKernelGGL(add_rmsnorm_quant_kernel<true>, dim3(rows), dim3(kThreads), 0, s, *x, m->delta, gain, D.d,
-                           D.eps, m->q8, m->qs);
+                           D.eps, m->q8, m->qs, nullptr);
     else
         hipLaunchKernelGGL(add_rmsnorm_quant_kernel<false>, dim3(rows), dim3(kThreads), 0, s, *x, nullptr, gain, D.d,
-                           D.eps, m->q8, m->qs);
+                           D.eps, m->q8, m->qs, nullptr);
     NHIP_CHECK_HIP(hipGetLastError());
     if (act && fuse) {
         const int32_t rc = launch_decode_swiglu(w, m->q8, m->qs, rows, act, D.ffn, s);
@@ -717,8 +832,9 @@ int32_t norm_matmul(nhip_decoder* m, int rows, float** x, bool pending, const fl
     return nhip_matmul_i8_dev(w, m->q8, m->qs, rows, y, ldy, 0, w->rows, s);
 }
 
-// Enqueues the forward of `rows` rows whose inputs are already in d_in.
-int32_t enqueue_forward(nhip_decoder* m, int rows, int k, bool masked = false)
+// Enqueues the forward of `rows` rows whose inputs are already in d_in,
+// with the head of `hp` (ignored by the masked head).
+int32_t enqueue_forward(nhip_decoder* m, int rows, const HeadPlan& hp, bool masked = false)
 {
     // NHIP_DECODER_FUSED=0 keeps the element-wise kernels separate (for A/B timing)
     static const bool fused_enabled = [] {
@@ -812,36 +928,42 @@ int32_t enqueue_forward(nhip_decoder* m, int rows, int k, bool masked = false)
         // the sparse head: the final norm, the LM head over the vocab tiles
         // that hold an allowed id of some row, and ArgMaxMasked per row
         hipLaunchKernelGGL(add_rmsnorm_quant_kernel<true>, dim3(rows), dim3(kThreads), 0, s, x, m->delta,
-                           m->final_norm, d, D.eps, m->q8, m->qs);
+                           m->final_norm, d, D.eps, m->q8, m->qs, nullptr);
         NHIP_CHECK_HIP(hipGetLastError());
         rc = launch_decode_masked(m->wlm, m->q8, m->qs, rows, m->logits, D.vocab, m->d_mask, m->mask_words, s);
         if (rc) return rc;
         return launch_argmax_masked(m->logits, D.vocab, m->d_mask, m->mask_words, m->mask_words, D.vocab, rows,
                                     m->d_best, m->d_best_val, s);
     }
-    // the final residual is not needed again: no x_out
+    // the final residual is not needed again: no x_out.  The head runs over
+    // the plan's rows only (EngineCore.ForwardBatch's headRows,
+    // src/Needle/Engine.cs:2341-2348): row i of the logits is row
+    // head_rows[i] of the forward.
+    const int heads = hp.all_rows ? rows : hp.heads;
+    if (heads == 0) return NHIP_OK;
     rc = 1;
-    if (fuse && m->wlm->tiles_n <= kFusedPrologueMaxTiles) {
+    if (hp.all_rows && fuse && m->wlm->tiles_n <= kFusedPrologueMaxTiles) {
         DecodePrologue f{kProNorm, x, m->delta, nullptr, m->final_norm, D.eps, 0};
         rc = launch_decode_fused(m->wlm, f, rows, m->logits, D.vocab, s);
         if (rc < 0) return rc;
     }
     if (rc) {
-        hipLaunchKernelGGL(add_rmsnorm_quant_kernel<true>, dim3(rows), dim3(kThreads), 0, s, x, m->delta,
-                           m->final_norm, d, D.eps, m->q8, m->qs);
+        hipLaunchKernelGGL(add_rmsnorm_quant_kernel<true>, dim3(heads), dim3(kThreads), 0, s, x, m->delta,
+                           m->final_norm, d, D.eps, m->q8, m->qs, hp.all_rows ? nullptr : in_heads(m, m->d_in));
         NHIP_CHECK_HIP(hipGetLastError());
-        rc = nhip_matmul_i8_dev(m->wlm, m->q8, m->qs, rows, m->logits, D.vocab, 0, D.vocab, s);
+        rc = nhip_matmul_i8_dev(m->wlm, m->q8, m->qs, heads, m->logits, D.vocab, 0, D.vocab, s);
         if (rc) return rc;
     }
-    if (k > 0) {
-        rc = launch_topk(m->logits, rows, D.vocab, k, m->topk, m->d_topk_idx, m->d_topk_lp, s);
+    if (hp.k > 0) {
+        rc = launch_topk(m->logits, heads, D.vocab, hp.k, m->topk, m->d_topk_idx, m->d_topk_lp, s);
         if (rc) return rc;
     }
+    if (hp.argmax) return launch_argmax(m->logits, D.vocab, D.vocab, heads, m->d_best, m->d_best_val, s);
     return NHIP_OK;
 }
 
 int32_t stage_inputs(nhip_decoder* m, const int32_t* tokens, const int32_t* slots, const int32_t* positions,
-                     int rows)
+                     int rows, const int32_t* head_rows = nullptr, int heads = 0)
 {
     const nhip_decoder_dims& D = m->dims;
     for (int r = 0; r < rows; r++) {
@@ -855,55 +977,82 @@ int32_t stage_inputs(nhip_decoder* m, const int32_t* tokens, const int32_t* slot
         in_first(m, m->h_in)[r] = 0;
         in_count(m, m->h_in)[r] = positions[r] + 1;
     }
-    NHIP_CHECK_HIP(hipMemcpyAsync(m->d_in, m->h_in, sizeof(int32_t) * 5 * D.max_rows, hipMemcpyHostToDevice,
+    for (int i = 0; i < heads; i++) {
+        NHIP_REQUIRE(head_rows[i] >= 0 && head_rows[i] < rows, "head row %d outside [0, %d)", head_rows[i], rows);
+        in_heads(m, m->h_in)[i] = head_rows[i];
+    }
+    NHIP_CHECK_HIP(hipMemcpyAsync(m->d_in, m->h_in, sizeof(int32_t) * 6 * D.max_rows, hipMemcpyHostToDevice,
                                   m->stream));
     return NHIP_OK;
 }
 
-// Forward with the results of the top-k copied to the pinned mirrors; decode
-// row counts up to kMaxTopK replay a graph captured on first use.
-int32_t forward_step(nhip_decoder* m, const int32_t* tokens, const int32_t* slots, const int32_t* positions,
-                     int rows, int k, bool use_graph)
+// Forward of staged inputs with the results of the top-k / argmax copied
+// to the pinned mirrors; steps of up to kMaxGraphRows rows replay a graph
+// captured on first use for their (rows, head plan).
+constexpr int kMaxGraphRows = 16;
+constexpr size_t kMaxGraphs = 64;
+
+int32_t run_staged(nhip_decoder* m, int rows, const HeadPlan& hp, bool use_graph)
 {
     // NHIP_DECODER_GRAPHS=0 launches decode steps eagerly (for kernel tracers)
     static const bool graphs_enabled = [] {
         const char* e = getenv("NHIP_DECODER_GRAPHS");
         return !(e && e[0] == '0');
     }();
-    use_graph = use_graph && graphs_enabled;
-    int32_t rc = stage_inputs(m, tokens, slots, positions, rows);
-    if (rc) return rc;
-    if (use_graph && rows <= kMaxTopK) {
-        if (!m->graphs[rows] || m->graph_k[rows] != k) {
-            if (m->graphs[rows]) (void)hipGraphExecDestroy(m->graphs[rows]);
-            m->graphs[rows] = nullptr;
+    int32_t rc;
+    use_graph = use_graph && graphs_enabled && rows <= kMaxGraphRows;
+    if (use_graph) {
+        hipGraphExec_t exec = nullptr;
+        for (const StepGraph& g : m->graphs)
+            if (g.rows == rows && g.head == hp) exec = g.exec;
+        if (!exec) {
+            if (m->graphs.size() >= kMaxGraphs) {  // drop the oldest
+                NHIP_CHECK_HIP(hipStreamSynchronize(m->stream));
+                (void)hipGraphExecDestroy(m->graphs.front().exec);
+                m->graphs.erase(m->graphs.begin());
+            }
             hipGraph_t g;
             NHIP_CHECK_HIP(hipStreamBeginCapture(m->stream, hipStreamCaptureModeThreadLocal));
-            rc = enqueue_forward(m, rows, k);
+            rc = enqueue_forward(m, rows, hp);
             hipError_t e = hipStreamEndCapture(m->stream, &g);
             if (rc) {
                 if (e == hipSuccess) (void)hipGraphDestroy(g);
                 return rc;
             }
             NHIP_CHECK_HIP(e);
-            e = hipGraphInstantiate(&m->graphs[rows], g, nullptr, nullptr, 0);
+            e = hipGraphInstantiate(&exec, g, nullptr, nullptr, 0);
             (void)hipGraphDestroy(g);
             NHIP_CHECK_HIP(e);
-            m->graph_k[rows] = k;
+            m->graphs.push_back(StepGraph{rows, hp, exec});
         }
-        NHIP_CHECK_HIP(hipGraphLaunch(m->graphs[rows], m->stream));
+        NHIP_CHECK_HIP(hipGraphLaunch(exec, m->stream));
     } else {
-        rc = enqueue_forward(m, rows, k);
+        rc = enqueue_forward(m, rows, hp);
         if (rc) return rc;
     }
-    if (k > 0) {
-        NHIP_CHECK_HIP(hipMemcpyAsync(m->h_topk_idx, m->d_topk_idx, sizeof(int32_t) * rows * k, hipMemcpyDeviceToHost,
+    const int heads = hp.all_rows ? rows : hp.heads;
+    if (hp.k > 0 && heads > 0) {
+        NHIP_CHECK_HIP(hipMemcpyAsync(m->h_topk_idx, m->d_topk_idx, sizeof(int32_t) * heads * hp.k,
+                                      hipMemcpyDeviceToHost, m->stream));
+        NHIP_CHECK_HIP(hipMemcpyAsync(m->h_topk_lp, m->d_topk_lp, sizeof(float) * heads * hp.k, hipMemcpyDeviceToHost,
                                       m->stream));
-        NHIP_CHECK_HIP(hipMemcpyAsync(m->h_topk_lp, m->d_topk_lp, sizeof(float) * rows * k, hipMemcpyDeviceToHost,
+    }
+    if (hp.argmax && heads > 0) {
+        NHIP_CHECK_HIP(hipMemcpyAsync(m->h_best, m->d_best, sizeof(int32_t) * 2 * m->best_rows, hipMemcpyDeviceToHost,
                                       m->stream));
     }
     NHIP_CHECK_HIP(hipStreamSynchronize(m->stream));
     return NHIP_OK;
+}
+
+int32_t forward_step(nhip_decoder* m, const int32_t* tokens, const int32_t* slots, const int32_t* positions,
+                     int rows, int k, bool use_graph)
+{
+    int32_t rc = stage_inputs(m, tokens, slots, positions, rows);
+    if (rc) return rc;
+    HeadPlan hp;
+    hp.k = k;
+    return run_staged(m, rows, hp, use_graph);
 }
 
 int32_t copy_slot(nhip_decoder* m, int dst, int src, int length)
@@ -926,11 +1075,8 @@ int32_t copy_slot(nhip_decoder* m, int dst, int src, int length)
 void drop_graphs(nhip_decoder* m)
 {
     if (m->stream) (void)hipStreamSynchronize(m->stream);
-    for (int i = 0; i <= kMaxTopK; i++) {
-        if (m->graphs[i]) (void)hipGraphExecDestroy(m->graphs[i]);
-        m->graphs[i] = nullptr;
-        m->graph_k[i] = 0;
-    }
+    for (StepGraph& g : m->graphs) (void)hipGraphExecDestroy(g.exec);
+    m->graphs.clear();
 }
 
 int32_t upload(nhip_decoder* m, float** dst, const float* src, size_t count)
@@ -974,6 +1120,9 @@ int32_t nhip_decoder_create(const nhip_decoder_dims* dims, nhip_decoder** out)
     m->ffn_norm.assign(D.layers, nullptr);
     const size_t cells = (size_t)D.layers * D.slots * D.capacity * D.kv_heads;
     const int R = D.max_rows;
+    m->best_rows = std::max(R, kMaxMaskedRows);
+    m->slot_len.assign(D.slots, 0);
+    m->slot_mark.assign(D.slots, 0);
     auto fail = [&](int32_t code) {
         nhip_decoder_destroy(m);
         return code;
@@ -986,10 +1135,10 @@ int32_t nhip_decoder_create(const nhip_decoder_dims* dims, nhip_decoder** out)
         (rc = dalloc(m, &m->qkv, (size_t)R * m->qkv_n)) || (rc = dalloc(m, &m->qh, (size_t)R * D.heads * 64)) ||
         (rc = dalloc(m, &m->qhs, (size_t)R * D.heads)) || (rc = dalloc(m, &m->att, (size_t)R * D.heads * 64)) ||
         (rc = dalloc(m, &m->gu, (size_t)R * 2 * D.ffn)) || (rc = dalloc(m, &m->act, (size_t)R * D.ffn)) || (rc = dalloc(m, &m->logits, (size_t)R * D.vocab)) ||
-        (rc = dalloc(m, &m->d_in, (size_t)5 * R)) || (rc = dalloc(m, &m->d_topk_idx, (size_t)R * kMaxTopK)) ||
+        (rc = dalloc(m, &m->d_in, (size_t)6 * R)) || (rc = dalloc(m, &m->d_topk_idx, (size_t)R * kMaxTopK)) ||
         (rc = dalloc(m, &m->d_topk_lp, (size_t)R * kMaxTopK)) ||
         (rc = dalloc(m, &m->d_mask, (size_t)kMaxMaskedRows * ((D.vocab + 31) / 32))) ||
-        (rc = dalloc(m, &m->d_best, (size_t)2 * kMaxMaskedRows)) ||
+        (rc = dalloc(m, &m->d_best, (size_t)2 * m->best_rows)) ||
         (rc = dalloc(m, &m->topk.vals, (size_t)R * ((D.vocab + kTopkBlock - 1) / kTopkBlock) * kMaxTopK)) ||
         (rc = dalloc(m, &m->topk.ids, (size_t)R * ((D.vocab + kTopkBlock - 1) / kTopkBlock) * kMaxTopK)) ||
         (rc = dalloc(m, &m->topk.bmax, (size_t)R * ((D.vocab + kTopkBlock - 1) / kTopkBlock))) ||
@@ -1004,8 +1153,8 @@ int32_t nhip_decoder_create(const nhip_decoder_dims* dims, nhip_decoder** out)
     m->allocations.push_back(ws);
     m->attn_ws = ws;
     m->mask_words = (D.vocab + 31) / 32;
-    m->d_best_val = reinterpret_cast<float*>(m->d_best + kMaxMaskedRows);  // one copy returns both
-    if (hipHostMalloc(reinterpret_cast<void**>(&m->h_in), sizeof(int32_t) * 5 * R, hipHostMallocDefault) !=
+    m->d_best_val = reinterpret_cast<float*>(m->d_best + m->best_rows);  // one copy returns both
+    if (hipHostMalloc(reinterpret_cast<void**>(&m->h_in), sizeof(int32_t) * 6 * R, hipHostMallocDefault) !=
             hipSuccess ||
         hipHostMalloc(reinterpret_cast<void**>(&m->h_topk_idx), sizeof(int32_t) * R * kMaxTopK,
                       hipHostMallocDefault) != hipSuccess ||
@@ -1013,12 +1162,12 @@ int32_t nhip_decoder_create(const nhip_decoder_dims* dims, nhip_decoder** out)
             hipSuccess ||
         hipHostMalloc(reinterpret_cast<void**>(&m->h_mask), sizeof(uint32_t) * kMaxMaskedRows * ((D.vocab + 31) / 32),
                       hipHostMallocDefault) != hipSuccess ||
-        hipHostMalloc(reinterpret_cast<void**>(&m->h_best), sizeof(int32_t) * 2 * kMaxMaskedRows,
+        hipHostMalloc(reinterpret_cast<void**>(&m->h_best), sizeof(int32_t) * 2 * m->best_rows,
                       hipHostMallocDefault) != hipSuccess) {
         set_error("hipHostMalloc failed");
         return fail(NHIP_ERR_HIP);
     }
-    m->h_best_val = reinterpret_cast<float*>(m->h_best + kMaxMaskedRows);
+    m->h_best_val = reinterpret_cast<float*>(m->h_best + m->best_rows);
     if (hipStreamCreateWithFlags(&m->stream, hipStreamNonBlocking) != hipSuccess) {
         set_error("hipStreamCreate failed");
         return fail(NHIP_ERR_HIP);
@@ -1149,9 +1298,9 @@ int32_t nhip_decoder_forward_masked(nhip_decoder* m, const int32_t* tokens, cons
     }
     NHIP_CHECK_HIP(hipMemcpyAsync(m->d_mask, m->h_mask, sizeof(uint32_t) * rows * MW, hipMemcpyHostToDevice,
                                   m->stream));
-    rc = enqueue_forward(m, rows, 0, true);
+    rc = enqueue_forward(m, rows, HeadPlan{}, true);
     if (rc) return rc;
-    NHIP_CHECK_HIP(hipMemcpyAsync(m->h_best, m->d_best, sizeof(int32_t) * 2 * kMaxMaskedRows, hipMemcpyDeviceToHost,
+    NHIP_CHECK_HIP(hipMemcpyAsync(m->h_best, m->d_best, sizeof(int32_t) * 2 * m->best_rows, hipMemcpyDeviceToHost,
                                   m->stream));
     NHIP_CHECK_HIP(hipStreamSynchronize(m->stream));
     std::memcpy(best, m->h_best, sizeof(int32_t) * rows);
@@ -1222,8 +1371,157 @@ int32_t nhip_decoder_copy_slot(nhip_decoder* m, int32_t dst, int32_t src, int32_
     NHIP_REQUIRE(m, "null decoder");
     int32_t rc = copy_slot(m, dst, src, length);
     if (rc) return rc;
+    m->slot_len[dst] = length;  // Engine.CopyFrom takes the source's length
     NHIP_CHECK_HIP(hipStreamSynchronize(m->stream));
     return NHIP_OK;
+}
+
+// EngineCore.ForwardBatch (src/Needle/Engine.cs:2303-2350): positions from
+// the slots' lengths (row t of a run of slot s sits at len[s] + t - run
+// start, Engine.cs:2655-2661), lengths advanced by the runs afterwards.
+int32_t nhip_decoder_step(nhip_decoder* m, const int32_t* tokens, const int32_t* row_slots, int32_t rows,
+                          const int32_t* head_rows, int32_t heads, float* logits, int32_t k, int32_t* topk_idx,
+                          float* topk_lp, int32_t* argmax)
+{
+    clear_error();
+    int32_t rc = ready(m);
+    if (rc) return rc;
+    const nhip_decoder_dims& D = m->dims;
+    NHIP_REQUIRE(rows > 0 && rows <= D.max_rows, "rows %d outside [1, %d]", rows, D.max_rows);
+    NHIP_REQUIRE(heads >= 0 && heads <= rows, "heads %d outside [0, %d]", heads, rows);
+    NHIP_REQUIRE(tokens && row_slots && (heads == 0 || head_rows), "null inputs");
+    NHIP_REQUIRE(k >= 0 && k <= kMaxTopK && (k == 0 || (topk_idx && topk_lp)), "k %d outside [0, %d]", k, kMaxTopK);
+    std::vector<int32_t> pos(rows);
+    std::vector<char> seen(D.slots, 0);
+    for (int rs = 0; rs < rows;) {
+        const int slot = row_slots[rs];
+        NHIP_REQUIRE(slot >= 0 && slot < D.slots, "slot %d out of range", slot);
+        NHIP_REQUIRE(!seen[slot], "the rows of slot %d must be one contiguous run", slot);
+        seen[slot] = 1;
+        int rk = rs;
+        while (rk + 1 < rows && row_slots[rk + 1] == slot) rk++;
+        NHIP_REQUIRE(m->slot_len[slot] + (rk - rs + 1) <= D.capacity, "slot %d: context capacity %d exceeded", slot,
+                     D.capacity);
+        for (int t = rs; t <= rk; t++) pos[t] = m->slot_len[slot] + t - rs;
+        rs = rk + 1;
+    }
+    rc = stage_inputs(m, tokens, row_slots, pos.data(), rows, head_rows, heads);
+    if (rc) return rc;
+    HeadPlan hp;
+    hp.heads = heads;
+    hp.all_rows = false;
+    hp.k = heads > 0 ? k : 0;
+    hp.argmax = heads > 0 && argmax != nullptr;
+    rc = run_staged(m, rows, hp, true);
+    if (rc) return rc;
+    for (int t = 0; t < rows; t++) m->slot_len[row_slots[t]] = std::max(m->slot_len[row_slots[t]], pos[t] + 1);
+    if (heads > 0 && k > 0) {
+        std::memcpy(topk_idx, m->h_topk_idx, sizeof(int32_t) * heads * k);
+        std::memcpy(topk_lp, m->h_topk_lp, sizeof(float) * heads * k);
+    }
+    if (hp.argmax) std::memcpy(argmax, m->h_best, sizeof(int32_t) * heads);
+    if (logits && heads > 0)
+        NHIP_CHECK_HIP(hipMemcpy(logits, m->logits, sizeof(float) * heads * D.vocab, hipMemcpyDeviceToHost));
+    return NHIP_OK;
+}
+
+// BatchedEngine.ResetSlot / MarkSlot / RewindSlot / SlotLength
+// (src/Needle/BatchEngine.cs:25-30; Engine.cs:2227-2276).  The cache rows
+// past a slot's length are never read, so a reset or a rewind only moves the
+// length; a mark records it.
+int32_t nhip_decoder_slot_reset(nhip_decoder* m, int32_t slot)
+{
+    clear_error();
+    NHIP_REQUIRE(m && slot >= 0 && slot < m->dims.slots, "slot %d out of range", slot);
+    m->slot_len[slot] = 0;
+    m->slot_mark[slot] = 0;
+    return NHIP_OK;
+}
+
+int32_t nhip_decoder_slot_mark(nhip_decoder* m, int32_t slot)
+{
+    clear_error();
+    NHIP_REQUIRE(m && slot >= 0 && slot < m->dims.slots, "slot %d out of range", slot);
+    m->slot_mark[slot] = m->slot_len[slot];
+    return NHIP_OK;
+}
+
+int32_t nhip_decoder_slot_rewind(nhip_decoder* m, int32_t slot)
+{
+    clear_error();
+    NHIP_REQUIRE(m && slot >= 0 && slot < m->dims.slots, "slot %d out of range", slot);
+    m->slot_len[slot] = m->slot_mark[slot];
+    return NHIP_OK;
+}
+
+int32_t nhip_decoder_slot_length(const nhip_decoder* m, int32_t slot, int32_t* length)
+{
+    clear_error();
+    NHIP_REQUIRE(m && slot >= 0 && slot < m->dims.slots && length, "slot %d out of range", slot);
+    *length = m->slot_len[slot];
+    return NHIP_OK;
+}
+
+// ToolCaller.Complete's loop (src/Needle/ToolCaller.cs:59-77) on slot 0:
+// reset, feed the prompt in chunks of max_rows rows with the head on its
+// last row only (BatchedEngine.FeedSlot, Engine.cs:2286-2301), then per
+// step Ops.ArgMax of the head row (Engine.Greedy, Engine.cs:103) on the
+// device; stop before a token equal to `stop` (-1: none), otherwise record
+// it and feed it as a one-row step (a replayed graph).
+int32_t nhip_decoder_greedy(nhip_decoder* m, const int32_t* prompt, int32_t prompt_len, int32_t max_new,
+                            int32_t stop, int32_t* out_tokens, int32_t* out_len, nhip_decode_stats* stats)
+{
+    clear_error();
+    int32_t rc = ready(m);
+    if (rc) return rc;
+    const nhip_decoder_dims& D = m->dims;
+    NHIP_REQUIRE(prompt && prompt_len > 0 && max_new >= 0 && out_len && (max_new == 0 || out_tokens),
+                 "prompt length %d, max_new %d", prompt_len, max_new);
+    NHIP_REQUIRE(prompt_len + max_new <= D.capacity, "prompt + new tokens exceed the capacity %d", D.capacity);
+    using clock = std::chrono::steady_clock;
+    const auto t0 = clock::now();
+    m->slot_len[0] = 0;
+    std::vector<int32_t> sl(std::min(prompt_len, D.max_rows), 0);
+    int32_t next = 0;
+    for (int start = 0; start < prompt_len; start += D.max_rows) {
+        const int count = std::min(D.max_rows, prompt_len - start);
+        const bool last = start + count == prompt_len;
+        const int32_t head = count - 1;
+        rc = nhip_decoder_step(m, prompt + start, sl.data(), count, &head, last ? 1 : 0, nullptr, 0, nullptr, nullptr,
+                               last ? &next : nullptr);
+        if (rc) return rc;
+    }
+    const auto t1 = clock::now();
+    int n = 0;
+    const int32_t zero = 0;
+    for (int step = 0; step < max_new; step++) {
+        if (next == stop) break;
+        out_tokens[n++] = next;
+        rc = nhip_decoder_step(m, &next, &zero, 1, &zero, 1, nullptr, 0, nullptr, nullptr, &next);
+        if (rc) return rc;
+    }
+    const auto t2 = clock::now();
+    *out_len = n;
+    if (stats) {
+        stats->prefill_seconds = std::chrono::duration<double>(t1 - t0).count();
+        stats->decode_seconds = std::chrono::duration<double>(t2 - t1).count();
+        stats->fed_rows = n;
+        stats->steps = n;
+    }
+    return NHIP_OK;
+}
+
+int32_t nhip_argmax_dev(const float* d_x, int32_t ldx, int32_t n, int32_t rows, int32_t* d_index, float* d_value,
+                        void* stream)
+{
+    clear_error();
+    NHIP_REQUIRE(rows >= 0 && n >= 1 && ldx >= 0, "rows %d, n %d", rows, n);
+    if (rows == 0) return NHIP_OK;
+    NHIP_REQUIRE(d_x && d_index, "null pointer");
+    NHIP_REQUIRE(rows == 1 || ldx >= n, "row stride %d shorter than a row (%d)", ldx, n);
+    int32_t rc = ensure_device();
+    if (rc) return rc;
+    return launch_argmax(d_x, ldx, n, rows, d_index, d_value, as_stream(stream));
 }
 
 int32_t nhip_decoder_beam_search(nhip_decoder* m, const int32_t* prompt, int32_t prompt_len, int32_t width,
@@ -1244,13 +1542,21 @@ int32_t nhip_decoder_beam_search(nhip_decoder* m, const int32_t* prompt, int32_t
     const int W = width;
     using clock = std::chrono::steady_clock;
     const auto t0 = clock::now();
-    // prefill the prompt into slot 0; its last row's top-k starts the search
+    // prefill the prompt into slot 0; the top-k of its last row (the only
+    // head row) starts the search
     std::vector<int32_t> pos(prompt_len), sl(prompt_len, 0);
     for (int i = 0; i < prompt_len; i++) pos[i] = i;
-    rc = forward_step(m, prompt, sl.data(), pos.data(), prompt_len, W, false);
+    const int32_t last = prompt_len - 1;
+    rc = stage_inputs(m, prompt, sl.data(), pos.data(), prompt_len, &last, 1);
     if (rc) return rc;
-    std::vector<int32_t> top_idx(m->h_topk_idx + (size_t)(prompt_len - 1) * W, m->h_topk_idx + (size_t)prompt_len * W);
-    std::vector<float> top_lp(m->h_topk_lp + (size_t)(prompt_len - 1) * W, m->h_topk_lp + (size_t)prompt_len * W);
+    HeadPlan prefill_head;
+    prefill_head.heads = 1;
+    prefill_head.all_rows = false;
+    prefill_head.k = W;
+    rc = run_staged(m, prompt_len, prefill_head, false);
+    if (rc) return rc;
+    std::vector<int32_t> top_idx(m->h_topk_idx, m->h_topk_idx + W);
+    std::vector<float> top_lp(m->h_topk_lp, m->h_topk_lp + W);
     const auto t1 = clock::now();
 
     struct Cand {
@@ -1364,8 +1670,7 @@ int32_t nhip_decoder_destroy(nhip_decoder* m)
 {
     if (!m) return NHIP_OK;
     if (m->stream) (void)hipStreamSynchronize(m->stream);
-    for (auto& g : m->graphs)
-        if (g) (void)hipGraphExecDestroy(g);
+    for (StepGraph& g : m->graphs) (void)hipGraphExecDestroy(g.exec);
     for (auto* w : m->wqkv) nhip_weights_destroy(w);
     for (auto* w : m->wo) nhip_weights_destroy(w);
     for (auto* w : m->wgu) nhip_weights_destroy(w);

@@ -120,6 +120,45 @@ class GpuDecoder:
     def copy_slot(self, dst, src, length):
         check(lib().nhip_decoder_copy_slot(self.h, dst, src, length))
 
+    def step(self, tokens, row_slots, head_rows, k=0, logits=True, argmax=False):
+        """BatchedEngine.ForwardBatch: positions from the slots' lengths;
+        returns the head rows' logits [heads][vocab] (or None), top-k ids and
+        log-probabilities [heads][k], and Ops.ArgMax ids [heads] (or None)."""
+        rows, heads = len(tokens), len(head_rows)
+        t, s = (np.ascontiguousarray(a, dtype=np.int32) for a in (tokens, row_slots))
+        hr = np.ascontiguousarray(head_rows, dtype=np.int32).reshape(-1)
+        lg = np.zeros((heads, self.vocab), dtype=np.float32) if logits else None
+        idx = np.zeros((max(heads, 1), max(k, 1)), dtype=np.int32)
+        lp = np.zeros((max(heads, 1), max(k, 1)), dtype=np.float32)
+        am = np.zeros(max(heads, 1), dtype=np.int32)
+        check(lib().nhip_decoder_step(self.h, _p(t), _p(s), rows, _p(hr) if heads else None, heads,
+                                      _p(lg) if logits and heads else None, k, _p(idx), _p(lp),
+                                      _p(am) if argmax else None))
+        return lg, idx[:heads, :k], lp[:heads, :k], (am[:heads] if argmax else None)
+
+    def slot_reset(self, slot):
+        check(lib().nhip_decoder_slot_reset(self.h, slot))
+
+    def slot_mark(self, slot):
+        check(lib().nhip_decoder_slot_mark(self.h, slot))
+
+    def slot_rewind(self, slot):
+        check(lib().nhip_decoder_slot_rewind(self.h, slot))
+
+    def slot_length(self, slot) -> int:
+        n = C.c_int32()
+        check(lib().nhip_decoder_slot_length(self.h, slot, C.byref(n)))
+        return n.value
+
+    def greedy(self, prompt, max_new, stop=-1):
+        pr = np.ascontiguousarray(prompt, dtype=np.int32)
+        out = np.zeros(max(max_new, 1), dtype=np.int32)
+        n = C.c_int32()
+        stats = DecodeStats()
+        check(lib().nhip_decoder_greedy(self.h, _p(pr), len(pr), max_new, stop, _p(out), C.byref(n),
+                                        C.byref(stats)))
+        return out[:n.value].copy(), stats
+
     def beam_search(self, prompt, width, max_new, eos):
         pr = np.ascontiguousarray(prompt, dtype=np.int32)
         out = np.zeros(max_new + 1, dtype=np.int32)

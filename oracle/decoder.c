@@ -120,8 +120,9 @@ float or_swiglu_quant(const float* g, const float* u, int n, float* a, int8_t* q
 }
 
 /* TopKLogSoftmax (src/Needle/Ops.cs:1092-1221) in the canonical float form:
- * the top k of the allowed ids (0, 2, 3 masked when mask is set) by value,
- * ties to the lower id; log_shift = peak + log(S) with peak the top value
+ * the reference's own selection (or_topk_select: the top k of the allowed
+ * ids by value, ties to the lower id, one -inf id at most, (-inf, -1) for
+ * slots left over); log_shift = peak + log(S) with peak the top value
  * and S summed over blocks of OR_TOPK_BLOCK ids: for block b with masked
  * values v_i = -1e30 and block maximum m_b, S_b = sum_i Exp(v_i - m_b) by
  * the canonical reduction over the block's ids (relative to its start),
@@ -133,21 +134,7 @@ void or_topk_lse(const float* x, int n, int k, int mask, int* idx, float* lp)
 {
     float top_val[16];
     int top_idx[16];
-    for (int m = 0; m < k; m++) { top_val[m] = -INFINITY; top_idx[m] = 0x7FFFFFFF; }
-    for (int i = 0; i < n; i++) {
-        if (mask && (i == 0 || i == 2 || i == 3)) continue;
-        float v = x[i];
-        if (v > top_val[k - 1] || (v == top_val[k - 1] && i < top_idx[k - 1])) {
-            int pos = k - 1;
-            while (pos > 0 && (v > top_val[pos - 1] || (v == top_val[pos - 1] && i < top_idx[pos - 1]))) {
-                top_val[pos] = top_val[pos - 1];
-                top_idx[pos] = top_idx[pos - 1];
-                pos--;
-            }
-            top_val[pos] = v;
-            top_idx[pos] = i;
-        }
-    }
+    or_topk_select(x, n, k, mask, top_idx, top_val);
     float peak = top_val[0];
     float total = 0.0f;
     for (int b0 = 0; b0 < n; b0 += OR_TOPK_BLOCK) {
@@ -312,6 +299,46 @@ void or_decoder_copy_slot(or_decoder* m, int dst, int src, int length)
     }
 }
 
+/* ------------------------------------------------------------ greedy -- */
+
+static double now_s(void)
+{
+    struct timespec ts;
+    clock_gettime(CLOCK_MONOTONIC, &ts);
+    return (double)ts.tv_sec + 1e-9 * (double)ts.tv_nsec;
+}
+
+
+int or_greedy(or_decoder* m, const int* prompt, int prompt_len, int max_new, int stop, int* out_tokens,
+              double* seconds)
+{
+    double t0 = now_s();
+    int V = m->dims.vocab;
+    float* lg = (float*)malloc(sizeof(float) * (size_t)prompt_len * V);
+    int* pos = (int*)malloc(sizeof(int) * prompt_len);
+    int* sl = (int*)calloc(prompt_len, sizeof(int));
+    for (int i = 0; i < prompt_len; i++) pos[i] = i;
+    or_decoder_forward(m, prompt, sl, pos, prompt_len, lg, 0, NULL, NULL);
+    double t1 = now_s();
+    const float* last = lg + (size_t)(prompt_len - 1) * V;
+    int n = 0;
+    for (int step = 0; step < max_new; step++) {
+        int next = or_argmax(last, V);
+        if (next == stop) break;
+        out_tokens[n++] = next;
+        int slot = 0, p = prompt_len + step;
+        or_decoder_forward(m, &next, &slot, &p, 1, lg, 0, NULL, NULL);
+        last = lg;
+    }
+    double t2 = now_s();
+    if (seconds) {
+        seconds[0] = t1 - t0;
+        seconds[1] = t2 - t1;
+    }
+    free(lg); free(pos); free(sl);
+    return n;
+}
+
 /* ------------------------------------------------------- beam search -- */
 
 typedef struct { float score; int parent, token; } cand_t;
@@ -323,12 +350,6 @@ typedef struct { float score; int parent, token; } cand_t;
  * score with ties in insertion order (a stable sort; List.Sort leaves ties
  * unspecified).  Returns the winner's length; tokens[], score, and the
  * number of forward rows fed after the prompt (for tokens/s). */
-static double now_s(void)
-{
-    struct timespec ts;
-    clock_gettime(CLOCK_MONOTONIC, &ts);
-    return (double)ts.tv_sec + 1e-9 * (double)ts.tv_nsec;
-}
 
 int or_beam_search(or_decoder* m, const int* prompt, int prompt_len, int width, int max_new, int eos,
                    int* out_tokens, float* out_score, long* fed_rows, double* seconds)

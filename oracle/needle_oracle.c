@@ -839,11 +839,16 @@ int or_argmax_masked(const float* x, const uint32_t* mask, int words, int length
 }
 
 /* src/Needle/Ops.cs:1092-1221, scalar branch (k <= 16) */
-void or_topk_log_softmax(const float* x, int n, int k, int* indices, float* log_probs,
-                         float* probs, int mask_special_023)
+/* The selection of src/Needle/Ops.cs:1094-1166 (scalar loop; the AVX loop
+ * selects the same ids for NaN-free rows): slots start as (-inf, -1); with
+ * the mask and n > 1, id 1 is placed in slot 0 whatever its value and the
+ * scan starts at id 4; a value enters when it is above the last slot's
+ * value, or equal to it with a lower id than the last slot's (INT_MAX
+ * before the first entry), and moves up past larger-or-equal-with-higher-id
+ * entries.  So the first scanned value enters even at -inf, later -inf
+ * values never do, and slots left over keep (-inf, -1). */
+void or_topk_select(const float* x, int n, int k, int mask_special_023, int* top_idx, float* top_val)
 {
-    float top_val[16];
-    int top_idx[16];
     for (int i = 0; i < k; i++) { top_val[i] = -INFINITY; top_idx[i] = -1; }
     float min_val = -INFINITY;
     int min_idx = 0x7FFFFFFF;
@@ -870,6 +875,14 @@ void or_topk_log_softmax(const float* x, int n, int k, int* indices, float* log_
             min_idx = top_idx[k - 1];
         }
     }
+}
+
+void or_topk_log_softmax(const float* x, int n, int k, int* indices, float* log_probs,
+                         float* probs, int mask_special_023)
+{
+    float top_val[16];
+    int top_idx[16];
+    or_topk_select(x, n, k, mask_special_023, top_idx, top_val);
     float peak = top_val[0];
     double total = 0;
     for (int i = 0; i < n; i++) {

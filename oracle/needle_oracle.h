@@ -208,6 +208,9 @@ void or_attention_decode(const int8_t* q, const float* q_scales, int rows, int h
 
 /* src/Needle/Ops.cs:1086-1089 (first index of the maximum) */
 int or_argmax(const float* x, int n);
+/* src/Needle/Ops.cs:1094-1166: the ids and values TopKLogSoftmax selects
+ * (slots left over: (-inf, -1)) */
+void or_topk_select(const float* x, int n, int k, int mask_special_023, int* top_idx, float* top_val);
 /* src/Needle/Ops.cs:1092-1221, scalar branch (the double log-sum-exp) */
 void or_topk_log_softmax(const float* x, int n, int k, int* indices, float* log_probs,
                          float* probs, int mask_special_023);
@@ -279,6 +282,12 @@ void or_decoder_free(or_decoder* m);
 void or_decoder_forward(or_decoder* m, const int* tokens, const int* slots, const int* positions, int rows,
                         float* logits, int k, int* topk_idx, float* topk_lp);
 void or_decoder_copy_slot(or_decoder* m, int dst, int src, int length);
+/* ToolCaller.Complete's loop (src/Needle/ToolCaller.cs:59-77) on this
+ * decoder: prefill the prompt into slot 0, then up to max_new times take
+ * Ops.ArgMax of the last logits (or_argmax), stop before a token equal to
+ * `stop` (-1: none), record it and feed it.  Returns the number of tokens. */
+int or_greedy(or_decoder* m, const int* prompt, int prompt_len, int max_new, int stop, int* out_tokens,
+              double* seconds);
 /* seconds (if given): [prefill, decode] wall time. */
 int or_beam_search(or_decoder* m, const int* prompt, int prompt_len, int width, int max_new, int eos,
                    int* out_tokens, float* out_score, long* fed_rows, double* seconds);

@@ -111,6 +111,8 @@ _PROTOS = {
     "or_decoder_copy_slot": (None, [C.POINTER(Decoder), _i, _i, _i]),
     "or_beam_search": (_i, [C.POINTER(Decoder), _vp, _i, _i, _i, _i, _vp, C.POINTER(_f), C.POINTER(C.c_long), _vp]),
     "or_argmax": (_i, [_vp, _i]),
+    "or_topk_select": (None, [_vp, _i, _i, _i, _vp, _vp]),
+    "or_greedy": (_i, [C.POINTER(Decoder), _vp, _i, _i, _i, _vp, _vp]),
     "or_zero_centered_rms": (None, [_vp, _vp, _i, _vp]),
     "or_rope_rotate": (None, [_vp, _i, _vp, _vp]),
     "or_needle3_attention_inputs": (None, [_vp, _i, _i, _i, _i, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
@@ -307,6 +309,13 @@ class CpuDecoder:
         n = lib().or_beam_search(C.byref(self.dec), p(pr), len(pr), width, max_new, eos, p(out), C.byref(score),
                                  C.byref(fed), p(self.seconds))
         return out[:n].copy(), score.value, fed.value
+
+    def greedy(self, prompt, max_new, stop=-1):
+        pr = np.ascontiguousarray(prompt, dtype=np.int32)
+        out = np.zeros(max(max_new, 1), dtype=np.int32)
+        self.seconds = np.zeros(2, dtype=np.float64)
+        n = lib().or_greedy(C.byref(self.dec), p(pr), len(pr), max_new, stop, p(out), p(self.seconds))
+        return out[:n].copy()
 
     def close(self):
         if self.dec.keys:

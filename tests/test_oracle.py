@@ -478,6 +478,79 @@ def test_argmax_first_index(orc):
         assert orc.lib().or_argmax(orc.p(x), 300) == int(np.argmax(x))
 
 
+def test_argmax_special_values(orc):
+    """Ops.ArgMax's scalar loop (src/Needle/Ops.cs:1086-1089): NaN-free rows
+    give numpy's argmax (first index of the maximum; +0 and -0 equal; all
+    -inf gives 0); a NaN at id 0 gives 0, NaN elsewhere is skipped
+    (np.nanargmax)."""
+    f = orc.lib().or_argmax
+    inf, nan = np.inf, np.nan
+    cases = [([-inf, -inf, -inf], 0), ([-0.0, 0.0, -0.0], 0), ([0.0, -0.0, 1e-45], 2), ([nan, 5.0, 7.0], 0),
+             ([1.0, nan, 3.0, 3.0], 2), ([-inf, nan, -inf], 0), ([2.0, inf, inf, nan], 1), ([7.0], 0)]
+    for vals, want in cases:
+        x = np.array(vals, dtype=np.float32)
+        assert f(orc.p(x), len(x)) == want, vals
+    rng = np.random.default_rng(6)
+    for _ in range(50):
+        n = int(rng.integers(1, 3000))
+        x = rng.integers(-4, 4, n).astype(np.float32)
+        x[rng.random(n) < 0.05] = -inf
+        assert f(orc.p(x), n) == int(np.argmax(x))
+        x[1 + rng.integers(0, n, 3) % max(n - 1, 1)] = nan
+        if n > 1:
+            assert f(orc.p(x), n) == int(np.nanargmax(x))
+
+
+def topk_select(orc, vals, k, mask=1):
+    x = np.array(vals, dtype=np.float32)
+    idx = np.zeros(k, dtype=np.int32)
+    val = np.zeros(k, dtype=np.float32)
+    orc.lib().or_topk_select(orc.p(x), len(x), k, mask, orc.p(idx), orc.p(val))
+    return list(idx), list(val)
+
+
+def test_topk_select_fewer_values_than_k(orc):
+    """Known answers traced by hand through Ops.TopKLogSoftmax's selection
+    loop (src/Needle/Ops.cs:1094-1166): slots start (-inf, -1), min = (-inf,
+    INT_MAX); with the mask id 1 is put in slot 0 (and becomes the minimum
+    only when k == 1) and the scan starts at id 4; a value enters when v >
+    min or (v == min and id < min id), then min = the last slot."""
+    inf = np.inf
+    # x[4] = -inf enters first (-inf == min, 4 < INT_MAX) into the last slot;
+    # 5 and 6 (-inf, ids above 4) never enter
+    assert topk_select(orc, [0, 1, 0, 0, -inf, -inf, -inf], 3)[0] == [1, -1, 4]
+    # the finite x[5] enters after x[4] and pushes it out of the last slot
+    assert topk_select(orc, [0, 1, 0, 0, -inf, 2, -inf], 3)[0] == [5, 1, -1]
+    # x[1] = -inf stays in slot 0 until a larger value moves it down
+    assert topk_select(orc, [0, -inf, 0, 0, -inf, -inf], 2)[0] == [1, 4]
+    assert topk_select(orc, [0, -inf, 0, 0, 3, -inf], 3)[0] == [4, 1, -1]
+    # k == 1: min starts at (x[1], 1): -inf ids never enter
+    assert topk_select(orc, [0, -inf, 0, 0, -inf, -inf], 1)[0] == [1]
+    # n == 1 with the mask: id 0 is masked, nothing is selected
+    assert topk_select(orc, [5.0], 2)[0] == [-1, -1]
+    # without the mask the first value enters at -inf, later ones do not
+    assert topk_select(orc, [-inf, -inf, -inf], 2, mask=0)[0] == [-1, 0]
+    assert topk_select(orc, [-inf, 4.0, -inf], 3, mask=0)[0] == [1, -1, -1]
+
+
+def test_topk_select_against_brute_force(orc):
+    """With at least k values above -inf among the allowed ids, the
+    selection is the k first allowed ids by (larger value, then lower id)."""
+    rng = np.random.default_rng(17)
+    for trial in range(200):
+        n = int(rng.integers(12, 400))
+        k = int(rng.integers(1, 9))
+        mask = trial % 2
+        x = rng.integers(-6, 6, n).astype(np.float32)
+        x[rng.random(n) < 0.3] = -np.inf
+        allowed = [i for i in range(n) if not (mask and i in (0, 2, 3))]
+        finite = [i for i in allowed if x[i] > -np.inf]
+        if len(finite) < k:
+            continue
+        want = sorted(finite, key=lambda i: (-float(x[i]), i))[:k]
+        assert topk_select(orc, x, k, mask)[0] == want, trial
+
+
 def test_zero_centered_rms_against_float64(orc):
     """Ops.ZeroCenteredRms (src/Needle/Ops.cs:209, 233-244): (1 + scale) * x /
     sqrt(mean(x^2) + 1e-6), within a few float32 roundings of float64."""

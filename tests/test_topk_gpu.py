@@ -51,13 +51,48 @@ def test_topk_lse_matches_oracle(hip, orc, n, k, kind):
 
 def test_topk_lse_fewer_allowed_ids_than_k(hip, orc):
     """n = 5: ids 1 and 4 are the only allowed ones; the remaining slots are
-    the (-inf, INT_MAX) placeholders of both restatements."""
+    the reference's (-inf, -1) (Ops.cs:1096)."""
     x = np.array([[3.0, 1.0, 9.0, 9.0, 2.0], [-1.0, -np.inf, 4.0, 4.0, 2.0]], dtype=np.float32)
     for k in (2, 3, 4):
         got = run(hip, x, k)
         want = oracle(orc, x, k)
         assert np.array_equal(got[0], want[0]), k
         assert np.array_equal(got[1].view(np.uint32), want[1].view(np.uint32)), k
+        assert np.all(got[0][:, 2:] == -1)
+
+
+@pytest.mark.parametrize("n", [6, 300, 4100])
+def test_topk_lse_few_values_above_minus_inf(hip, orc, n):
+    """Rows with fewer than k values above -inf: the reference's selection
+    admits its first scanned id (4) at -inf and drops it at the next entry,
+    never admits a later -inf, and leaves (-inf, -1) in the slots left over
+    (tests/test_oracle.py traces these cases by hand).  Ids equal; the
+    log-probabilities bit-identical, or NaN on both sides for rows whose
+    peak is -inf."""
+    inf = np.inf
+    rows = np.full((8, n), -inf, dtype=np.float32)
+    rows[1, 1] = 2.5                      # only id 1 (x[4] = -inf stays in the last slot for k >= 2)
+    rows[2, 5] = 1.0                      # one finite id after x[4] = -inf
+    rows[3, n - 1] = 0.5                  # the last id only
+    rows[4, [1, 4]] = [3.0, 3.0]          # a tie of id 1 and id 4
+    rows[5, 4] = 7.0                      # x[4] finite
+    rows[6, [1, n - 2, n - 1]] = [1.0, 1.0, 0.0]
+    # row 0 and row 7: all -inf (peak -inf: NaN log-probabilities)
+    rows[7, 0] = 9.0  # a masked id only
+    for k in (1, 2, 3, 8):
+        got = run(hip, rows, k)
+        want = oracle(orc, rows, k)
+        assert np.array_equal(got[0], want[0]), k
+        g, w = got[1], want[1]
+        assert np.array_equal(np.isnan(g), np.isnan(w)), k
+        ok = ~np.isnan(w)
+        assert np.array_equal(g[ok].view(np.uint32), w[ok].view(np.uint32)), k
+        for r in range(rows.shape[0]):
+            ref_idx = np.zeros(k, dtype=np.int32)
+            ref_lp = np.zeros(k, dtype=np.float32)
+            xr = np.ascontiguousarray(rows[r])
+            orc.lib().or_topk_log_softmax(orc.p(xr), n, k, orc.p(ref_idx), orc.p(ref_lp), None, 1)
+            assert np.array_equal(got[0][r], ref_idx), (k, r)
 
 
 def test_topk_lse_rejects_bad_arguments(hip, orc):
