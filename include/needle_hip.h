@@ -268,6 +268,25 @@ int32_t nhip_attention_decode_dev(const int8_t* d_q, const float* d_q_scales, in
                                   int32_t max_chunks, void* d_workspace, size_t workspace_bytes,
                                   float* d_out, void* stream);
 
+/* No counterpart in the reference: nhip_attention_decode_dev for callers
+ * that cannot allocate (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  Same arguments, semantics and results,
+ * without the workspace: the chunk partials go to a fixed 8 MiB device
+ * scratch array that the library holds on each GPU until the process ends
+ * (its address is looked up at nhip_init, which must have been called).
+ * Calls whose partials (nhip_attention_decode_workspace(rows, heads,
+ * max_chunks) bytes) exceed 8 MiB fail with NHIP_ERR_ARG.  No allocation
+ * happens in the call.  Every call on a GPU shares that GPU's scratch:
+ * calls that overlap on one GPU (other streams or threads) race, so
+ * serialise them. */
+int32_t nhip_attention_decode_noalloc_dev(const int8_t* d_q, const float* d_q_scales, int32_t rows,
+                                          int32_t heads, int32_t kv_heads, int32_t qk_dim,
+                                          const int8_t* d_keys, const float* d_key_scales,
+                                          const int8_t* d_values, const float* d_value_scales,
+                                          int32_t slots, int32_t capacity, const int32_t* d_row_slot,
+                                          const int32_t* d_row_first, const int32_t* d_row_count,
+                                          int32_t max_chunks, float* d_out, void* stream);
+
 /* ------------------------------------ Needle 3 attention inputs (rows) -- */
 
 /* Needle 3's step from a row's raw Q/K/V projections to its int8 query heads

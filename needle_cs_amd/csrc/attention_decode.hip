@@ -26,8 +26,17 @@
 // last-arrival merge would need an L2 writeback and invalidate per
 // workgroup).
 #include <algorithm>
+#include <mutex>
 
 #include "common.hpp"
+
+// Scratch of nhip_attention_decode_noalloc_dev: room for the chunk partials
+// (peaks, sums and per-chunk outputs) of one call, in a file-scope device
+// array that every GPU the library runs on holds until the process ends.  In
+// host code this name is only a stand-in for the symbol; host code uses the
+// per-device address that attention_scratch_setup() looks up.
+constexpr size_t kAttentionScratchBytes = size_t(8) << 20;
+static __device__ __align__(256) uint8_t scratch[kAttentionScratchBytes];
 
 namespace nhip {
 namespace {
@@ -825,6 +834,41 @@ using namespace nhip;
 
 namespace nhip {
 
+namespace {
+constexpr int kMaxScratchDevices = 64;
+std::mutex g_scratch_mutex;
+void* g_scratch[kMaxScratchDevices] = {};  // the scratch array's address on each device
+}  // namespace
+
+int32_t attention_scratch_setup()
+{
+    int dev = -1;
+    NHIP_CHECK_HIP(hipGetDevice(&dev));
+    NHIP_REQUIRE(dev >= 0 && dev < kMaxScratchDevices, "device %d above %d", dev, kMaxScratchDevices);
+    std::lock_guard<std::mutex> lock(g_scratch_mutex);
+    if (g_scratch[dev]) return NHIP_OK;
+    void* p = nullptr;
+    NHIP_CHECK_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+    NHIP_REQUIRE(p != nullptr, "no device address for the attention scratch on device %d", dev);
+    g_scratch[dev] = p;
+    return NHIP_OK;
+}
+
+// The scratch address on the current device (looked up there if this
+// device was not the one initialised).
+int32_t attention_scratch_address(void** out)
+{
+    int dev = -1;
+    NHIP_CHECK_HIP(hipGetDevice(&dev));
+    NHIP_REQUIRE(dev >= 0 && dev < kMaxScratchDevices, "device %d above %d", dev, kMaxScratchDevices);
+    if (!g_scratch[dev]) {
+        int32_t rc = attention_scratch_setup();
+        if (rc) return rc;
+    }
+    *out = g_scratch[dev];
+    return NHIP_OK;
+}
+
 int32_t attention_decode_post_impl(const AttnPostInputs& in, int32_t rows, int32_t heads, int32_t kv_heads,
                                    int8_t* d_keys, float* d_key_scales, int8_t* d_values, float* d_value_scales,
                                    int32_t slots, int32_t capacity, const int32_t* d_row_slot,
@@ -979,6 +1023,33 @@ int32_t nhip_attention_decode_dev(const int8_t* d_q, const float* d_qscale, int3
     return attention_decode_impl(d_q, d_qscale, rows, heads, kv_heads, qk_dim, d_keys, d_key_scales, d_values,
                                  d_value_scales, slots, capacity, d_row_slot, d_row_first, d_row_count, max_chunks,
                                  d_workspace, workspace_bytes, d_out, nullptr, nullptr, as_stream(stream));
+}
+
+int32_t nhip_attention_decode_noalloc_dev(const int8_t* d_q, const float* d_qscale, int32_t rows, int32_t heads,
+                                          int32_t kv_heads, int32_t qk_dim, const int8_t* d_keys,
+                                          const float* d_key_scales, const int8_t* d_values,
+                                          const float* d_value_scales, int32_t slots, int32_t capacity,
+                                          const int32_t* d_row_slot, const int32_t* d_row_first,
+                                          const int32_t* d_row_count, int32_t max_chunks, float* d_out, void* stream)
+{
+    clear_error();
+    NHIP_REQUIRE(device_ready(), "attention (no allocation): call nhip_init first");
+    int32_t rc = ensure_device();
+    if (rc) return rc;
+    if (rows == 0) return NHIP_OK;
+    NHIP_REQUIRE(rows > 0 && heads > 0 && max_chunks >= 1 && max_chunks <= 256,
+                 "attention (no allocation): rows %d, heads %d, max_chunks %d", rows, heads, max_chunks);
+    const size_t need = layout(rows, heads, max_chunks).total;
+    NHIP_REQUIRE(need <= kAttentionScratchBytes,
+                 "attention (no allocation): %d rows x %d heads x %d chunks need %zu bytes of partials, above the "
+                 "%zu-byte scratch; use nhip_attention_decode_dev with a workspace",
+                 rows, heads, max_chunks, need, kAttentionScratchBytes);
+    void* ws = nullptr;
+    rc = attention_scratch_address(&ws);
+    if (rc) return rc;
+    return attention_decode_impl(d_q, d_qscale, rows, heads, kv_heads, qk_dim, d_keys, d_key_scales, d_values,
+                                 d_value_scales, slots, capacity, d_row_slot, d_row_first, d_row_count, max_chunks, ws,
+                                 kAttentionScratchBytes, d_out, nullptr, nullptr, as_stream(stream));
 }
 
 }  // extern "C"

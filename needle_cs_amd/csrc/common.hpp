@@ -37,6 +37,12 @@ void clear_error();
 
 // Initialises the device on first use (device 0 unless nhip_init chose one).
 int32_t ensure_device();
+// True once a device has been initialised (by nhip_init or a first use).
+bool device_ready();
+// Looks up, once per device and with that device current, the address of
+// the no-allocation attention entry's scratch array (attention_decode.hip);
+// called by the device initialisation.
+int32_t attention_scratch_setup();
 hipStream_t default_stream();
 inline hipStream_t as_stream(void* s) { return s ? static_cast<hipStream_t>(s) : default_stream(); }
 

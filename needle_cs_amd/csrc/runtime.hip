@@ -47,6 +47,8 @@ static int32_t init_locked(int32_t device)
         return NHIP_ERR_NODEV;
     }
     NHIP_CHECK_HIP(hipSetDevice(device));
+    int32_t rc = attention_scratch_setup();
+    if (rc) return rc;
     if (g_stream == nullptr) NHIP_CHECK_HIP(hipStreamCreateWithFlags(&g_stream, hipStreamNonBlocking));
     g_device = device;
     snprintf(g_describe, sizeof(g_describe), "needle_hip 0.1 %s (%d CUs, %.0f GiB HBM)", prop.gcnArchName,
@@ -66,6 +68,8 @@ int32_t ensure_device()
     if (g_device >= 0) return NHIP_OK;
     return init_locked(0);
 }
+
+bool device_ready() { return g_device >= 0; }
 
 hipStream_t default_stream() { return g_stream; }
 
