@@ -222,6 +222,19 @@ int32_t nhip_matmul_cq_dev(const nhip_weights* w, const int8_t* d_values, const 
                            const float* d_offsets, int32_t stride, int32_t tokens, float* d_y,
                            int32_t ldy, int32_t row_start, int32_t row_end, void* stream);
 
+/* Quant.MatMulBatch (src/Needle/Quant.cs:679-816): `count` (1..4) weight
+ * matrices of one format and one K that share the activations (Needle 3's
+ * Q, K, V and Gate projections), each job j computing all of its rows into
+ * d_y[j] with row stride ldy[j] (>= its rows), as nhip_matmul_i8_dev
+ * (literal: d_scales [tokens], d_offsets and stride unused) or
+ * nhip_matmul_cq_dev (codebook) would.  Decode sizes (literal up to 16
+ * tokens, codebook up to 4) run as one launch over every job's row tiles;
+ * other token counts run the jobs in turn.  Bit-identical with the
+ * single-matrix calls.  w and d_y / ldy are host arrays of `count` entries. */
+int32_t nhip_matmul_batch_dev(const nhip_weights* const* w, int32_t count, const int8_t* d_q,
+                              const float* d_scales, const float* d_offsets, int32_t stride,
+                              int32_t tokens, float* const* d_y, const int32_t* ldy, void* stream);
+
 /* The int32 group sums D[t][n-row_start][g] (Scalar.cs:162-184) that the
  * matmuls accumulate, for checking them bit-exactly.  Literal / codebook. */
 int32_t nhip_group_dots_i8_dev(const nhip_weights* w, const int8_t* d_q, int32_t tokens,

@@ -694,7 +694,7 @@ __device__ __forceinline__ void chain_products(const float* pl, int GS, int swz,
 // Preconditions (checked on the host): CB is 4 or 8 and every wave owns CB
 // blocks (its scales are 16-byte aligned in the padded scale rows).
 template <int CB, int TI, bool EXACT>
-__global__ __launch_bounds__(512) void matmul_i8_decode_kernel(MatmulParams p)
+__device__ __forceinline__ void i8_decode_tile(const MatmulParams& p, const int tile)
 {
     constexpr bool WIDE = TI > 4;
     constexpr int SETS = 2 * CB / 4;  // TI <= 4: sets of four groups per wave
@@ -702,7 +702,6 @@ __global__ __launch_bounds__(512) void matmul_i8_decode_kernel(MatmulParams p)
     float* pl = reinterpret_cast<float*>(lds);  // products [t][r][GS]
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
-    const int tile = p.tile_begin + blockIdx.x;
     const int M = p.tokens;  // <= TI
     const int G = p.groups;
     const int GS = p.ldd;    // product row stride (floats), multiple of 4
@@ -809,6 +808,41 @@ __global__ __launch_bounds__(512) void matmul_i8_decode_kernel(MatmulParams p)
     chain_products(pl, GS, WIDE ? p.swz : 0, M, G, tile, p);
 }
 
+template <int CB, int TI, bool EXACT>
+__global__ __launch_bounds__(512) void matmul_i8_decode_kernel(MatmulParams p)
+{
+    i8_decode_tile<CB, TI, EXACT>(p, p.tile_begin + blockIdx.x);
+}
+
+// Quant.MatMulBatch (src/Needle/Quant.cs:679-816): up to four weight
+// matrices with the same K that share one set of activations, in one launch.
+// Job j owns the workgroups [first[j], first[j+1]), one per 16-row tile of
+// its rows; every job has the same tile shape (blocks, waves, LDS), so one
+// kernel instance serves them all.
+constexpr int kMaxBatchJobs = 4;
+
+struct MatmulBatch {
+    MatmulParams job[kMaxBatchJobs];
+    int32_t first[kMaxBatchJobs + 1];
+    int32_t count;
+};
+
+__device__ __forceinline__ int batch_job(const MatmulBatch& b)
+{
+    int j = 0;
+#pragma unroll
+    for (int i = 1; i < kMaxBatchJobs; i++) j += (i < b.count && (int)blockIdx.x >= b.first[i]) ? 1 : 0;
+    return j;
+}
+
+template <int CB, int TI, bool EXACT>
+__global__ __launch_bounds__(512) void matmul_i8_decode_batch_kernel(MatmulBatch b)
+{
+    const int j = batch_job(b);
+    const MatmulParams& p = b.job[j];
+    i8_decode_tile<CB, TI, EXACT>(p, p.tile_begin + (int)blockIdx.x - b.first[j]);
+}
+
 // Codebook formats, M <= 4 tokens: the four-group MFMA sets of
 // narrow_products with the codebook epilogue.  Wave w owns the GPW groups
 // from g_first = GPW*w (groups past G run on clamped operands and are
@@ -822,7 +856,7 @@ __global__ __launch_bounds__(512) void matmul_i8_decode_kernel(MatmulParams p)
 // stores acc - bias, Scalar.MatMulRows' operations in its order
 // (Scalar.cs:185-189).
 template <int F, int GPW, bool EXACT>
-__global__ __launch_bounds__(512) void matmul_cq_decode_kernel(MatmulParams p)
+__device__ __forceinline__ void cq_decode_tile(const MatmulParams& p, const int tile)
 {
     using T = Traits<F>;
     constexpr int SETS = GPW / 4;
@@ -835,7 +869,6 @@ __global__ __launch_bounds__(512) void matmul_cq_decode_kernel(MatmulParams p)
     float* pb = pa + (size_t)M * 16 * GS;
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
-    const int tile = p.tile_begin + blockIdx.x;
     const int r = lane & 15;
     const int kq = lane >> 4;
     const int n = tile * 16 + r;
@@ -921,6 +954,20 @@ __global__ __launch_bounds__(512) void matmul_cq_decode_kernel(MatmulParams p)
         }
         if (nn >= p.row_start && nn < p.row_end) p.y[(size_t)(x >> 4) * p.ldy + nn] = acc - bias;
     }
+}
+
+template <int F, int GPW, bool EXACT>
+__global__ __launch_bounds__(512) void matmul_cq_decode_kernel(MatmulParams p)
+{
+    cq_decode_tile<F, GPW, EXACT>(p, p.tile_begin + blockIdx.x);
+}
+
+template <int F, int GPW, bool EXACT>
+__global__ __launch_bounds__(512) void matmul_cq_decode_batch_kernel(MatmulBatch b)
+{
+    const int j = batch_job(b);
+    const MatmulParams& p = b.job[j];
+    cq_decode_tile<F, GPW, EXACT>(p, p.tile_begin + (int)blockIdx.x - b.first[j]);
 }
 
 // The decode kernel for M <= 4 with its activation rows computed in the
@@ -1119,18 +1166,19 @@ int32_t launch_dec_ti(const MatmulParams& p, int waves, size_t lds, hipStream_t 
     }
 }
 
-// Runs the decode kernel when its preconditions hold; returns 1 when it did
-// not apply (the caller falls back to the general kernel).
-int32_t try_i8_decode(const DeviceWeights* w, MatmulParams& p, hipStream_t stream)
+// The int8 decode kernel's launch shape for these weights and p.tokens:
+// sets p.ldd and p.swz, the waves per tile and the LDS bytes; false when the
+// kernel does not apply (the caller falls back to the general kernel).
+bool plan_i8_decode(const DeviceWeights* w, MatmulParams& p, int* waves_out, size_t* lds_out)
 {
-    if (p.tokens > 16 || p.dots) return 1;
+    if (p.tokens > 16 || p.dots) return false;
     static const int waves_override = [] {
         // tuning knob: 2, 4 or 8 waves per tile, or 1 to use the general kernel
         const char* e = getenv("NHIP_DECODE_WAVES");
         const int v = e ? atoi(e) : 0;
         return (v == 1 || v == 2 || v == 4 || v == 8) ? v : 0;
     }();
-    if (waves_override == 1) return 1;
+    if (waves_override == 1) return false;
     int waves = 0;
     // 5..16 tokens: more waves split the larger per-tile product work
     const int cands[3] = {p.tokens > 4 ? 8 : 4, p.tokens > 4 ? 4 : 8, 2};
@@ -1141,8 +1189,7 @@ int32_t try_i8_decode(const DeviceWeights* w, MatmulParams& p, hipStream_t strea
             break;
         }
     }
-    if (!waves) return 1;
-    const int per = w->blocks / waves;
+    if (!waves) return false;
     const int m = p.tokens;
     size_t lds;
     if (m <= 4) {
@@ -1156,9 +1203,21 @@ int32_t try_i8_decode(const DeviceWeights* w, MatmulParams& p, hipStream_t strea
         p.swz = std::min(cols4 & -cols4, 16) - 1;
     }
     lds = (size_t)m * 16 * p.ldd * sizeof(float);
-    if (lds > kMaxLds) return 1;
-    // the kernel's CB must equal per (4 or 8)
-    if (per == 4)
+    if (lds > kMaxLds) return false;
+    *waves_out = waves;
+    *lds_out = lds;
+    return true;
+}
+
+// Runs the decode kernel when its preconditions hold; returns 1 when it did
+// not apply (the caller falls back to the general kernel).
+int32_t try_i8_decode(const DeviceWeights* w, MatmulParams& p, hipStream_t stream)
+{
+    int waves = 0;
+    size_t lds = 0;
+    if (!plan_i8_decode(w, p, &waves, &lds)) return 1;
+    // the kernel's CB must equal the blocks per wave (4 or 8)
+    if (w->blocks / waves == 4)
         return w->special_scales ? launch_dec_ti<4, true>(p, waves, lds, stream)
                                  : launch_dec_ti<4, false>(p, waves, lds, stream);
     return w->special_scales ? launch_dec_ti<8, true>(p, waves, lds, stream)
@@ -1192,22 +1251,33 @@ int32_t launch_cq_decode_gpw(const MatmulParams& p, int gpw, bool exact, int wav
 // waves; NHIP_CQ_DECODE_GPW = 4, 8 or 16 overrides it for tuning) and one
 // wave per GPW groups.  Returns 1 when it does not apply
 // (more than 4 tokens, group sums requested, or K over 16*8 groups).
-int32_t try_cq_decode(const DeviceWeights* w, MatmulParams& p, hipStream_t stream)
+bool plan_cq_decode(const DeviceWeights* w, MatmulParams& p, int* gpw_out, int* waves_out, size_t* lds_out)
 {
-    if (p.tokens > 4 || p.dots) return 1;
+    if (p.tokens > 4 || p.dots) return false;
     static const int gpw_override = [] {
         const char* e = getenv("NHIP_CQ_DECODE_GPW");
         const int v = e ? atoi(e) : 0;
         return (v == 4 || v == 8 || v == 16) ? v : 0;
     }();
-    const bool cq4 = w->format == WeightFormat::Cq4;
     int gpw = gpw_override ? gpw_override : 4;
     while (gpw < 16 && (w->groups + gpw - 1) / gpw > 8) gpw *= 2;
     const int waves = (w->groups + gpw - 1) / gpw;
-    if (waves > 8) return 1;
+    if (waves > 8) return false;
     p.ldd = waves * gpw + 4;  // every group a wave writes, + 4: conflict-free product writes
     const size_t lds = (size_t)2 * p.tokens * 16 * p.ldd * sizeof(float);
-    if (lds > kMaxLds) return 1;
+    if (lds > kMaxLds) return false;
+    *gpw_out = gpw;
+    *waves_out = waves;
+    *lds_out = lds;
+    return true;
+}
+
+int32_t try_cq_decode(const DeviceWeights* w, MatmulParams& p, hipStream_t stream)
+{
+    int gpw = 0, waves = 0;
+    size_t lds = 0;
+    if (!plan_cq_decode(w, p, &gpw, &waves, &lds)) return 1;
+    const bool cq4 = w->format == WeightFormat::Cq4;
     const bool exact = w->special_scales != 0;
     return cq4 ? launch_cq_decode_gpw<kCq4>(p, gpw, exact, waves, lds, stream)
                : launch_cq_decode_gpw<kCq2>(p, gpw, exact, waves, lds, stream);
@@ -1408,6 +1478,105 @@ int32_t run_matmul(const DeviceWeights* w, const int8_t* q, const float* scales,
             return dots ? launch_fmt<kCq4, true>(p, waves, lds, stream) : launch_fmt<kCq4, false>(p, waves, lds, stream);
     }
     return NHIP_ERR_ARG;
+}
+
+// ------------------------------------------------------ batched matmuls --
+
+template <int CB, int TI, bool EXACT>
+int32_t launch_dec_batch_tpl(const MatmulBatch& b, int waves, size_t lds, hipStream_t s)
+{
+    hipLaunchKernelGGL((matmul_i8_decode_batch_kernel<CB, TI, EXACT>), dim3(b.first[b.count]), dim3(64 * waves), lds,
+                       s, b);
+    NHIP_CHECK_HIP(hipGetLastError());
+    return NHIP_OK;
+}
+
+template <int CB, bool EXACT>
+int32_t launch_dec_batch_ti(const MatmulBatch& b, int waves, size_t lds, hipStream_t s)
+{
+    switch (b.job[0].tokens) {
+        case 1: return launch_dec_batch_tpl<CB, 1, EXACT>(b, waves, lds, s);
+        case 2: return launch_dec_batch_tpl<CB, 2, EXACT>(b, waves, lds, s);
+        case 3: return launch_dec_batch_tpl<CB, 3, EXACT>(b, waves, lds, s);
+        case 4: return launch_dec_batch_tpl<CB, 4, EXACT>(b, waves, lds, s);
+        default: return launch_dec_batch_tpl<CB, 16, EXACT>(b, waves, lds, s);
+    }
+}
+
+template <int F, int GPW>
+int32_t launch_cq_batch_tpl(const MatmulBatch& b, bool exact, int waves, size_t lds, hipStream_t s)
+{
+    if (exact)
+        hipLaunchKernelGGL((matmul_cq_decode_batch_kernel<F, GPW, true>), dim3(b.first[b.count]), dim3(64 * waves),
+                           lds, s, b);
+    else
+        hipLaunchKernelGGL((matmul_cq_decode_batch_kernel<F, GPW, false>), dim3(b.first[b.count]), dim3(64 * waves),
+                           lds, s, b);
+    NHIP_CHECK_HIP(hipGetLastError());
+    return NHIP_OK;
+}
+
+template <int F>
+int32_t launch_cq_batch_gpw(const MatmulBatch& b, int gpw, bool exact, int waves, size_t lds, hipStream_t s)
+{
+    switch (gpw) {
+        case 4: return launch_cq_batch_tpl<F, 4>(b, exact, waves, lds, s);
+        case 8: return launch_cq_batch_tpl<F, 8>(b, exact, waves, lds, s);
+        default: return launch_cq_batch_tpl<F, 16>(b, exact, waves, lds, s);
+    }
+}
+
+// Quant.MatMulBatch.Run (src/Needle/Quant.cs:697-706, 753-772): every job's
+// MatMulRows over all its rows with the shared activations.  The decode
+// sizes (int8 up to 16 tokens, codebook up to 4) run as one launch over the
+// row tiles of every job; other token counts run the jobs one after another
+// (the same kernels as nhip_matmul_*_dev, so the same bits either way).
+int32_t run_matmul_batch(const DeviceWeights* const* w, int32_t count, const int8_t* q, const float* scales,
+                         const float* offsets, int32_t stride, int32_t tokens, float* const* y, const int32_t* ldy,
+                         hipStream_t stream)
+{
+    NHIP_REQUIRE(w && y && ldy && count >= 1 && count <= kMaxBatchJobs, "batch of %d jobs outside [1, %d]", count,
+                 kMaxBatchJobs);
+    NHIP_REQUIRE(tokens >= 0, "tokens %d < 0", tokens);
+    for (int j = 0; j < count; j++) {
+        NHIP_REQUIRE(w[j] && y[j], "job %d: null weights or output", j);
+        NHIP_REQUIRE(w[j]->format == w[0]->format && w[j]->cols == w[0]->cols,
+                     "job %d: every job needs the format and K of job 0", j);
+        NHIP_REQUIRE(ldy[j] >= w[j]->rows, "job %d: ldy %d below its %d rows", j, ldy[j], w[j]->rows);
+    }
+    if (tokens == 0) return NHIP_OK;
+    NHIP_REQUIRE(q && scales, "activations are NULL");
+    const bool cq = w[0]->format != WeightFormat::Int8G32;
+    if (cq) NHIP_REQUIRE(offsets && stride >= w[0]->groups, "offsets NULL or stride %d < groups %d", stride, w[0]->groups);
+    int32_t rc = ensure_device();
+    if (rc) return rc;
+    MatmulBatch b{};
+    b.count = count;
+    bool exact = false;
+    for (int j = 0; j < count; j++) {
+        b.job[j] = matmul_params(w[j], q, scales, offsets, stride, tokens, y[j], ldy[j], 0, w[j]->rows, nullptr);
+        b.first[j + 1] = b.first[j] + (b.job[j].tile_end - b.job[j].tile_begin);
+        exact = exact || w[j]->special_scales;
+    }
+    int waves = 0, gpw = 0;
+    size_t lds = 0;
+    bool planned = true;
+    for (int j = 0; j < count && planned; j++)  // the same shape for every job (same K and tokens)
+        planned = cq ? plan_cq_decode(w[j], b.job[j], &gpw, &waves, &lds) : plan_i8_decode(w[j], b.job[j], &waves, &lds);
+    if (planned) {
+        if (!cq)
+            return w[0]->blocks / waves == 4 ? (exact ? launch_dec_batch_ti<4, true>(b, waves, lds, stream)
+                                                      : launch_dec_batch_ti<4, false>(b, waves, lds, stream))
+                                             : (exact ? launch_dec_batch_ti<8, true>(b, waves, lds, stream)
+                                                      : launch_dec_batch_ti<8, false>(b, waves, lds, stream));
+        return w[0]->format == WeightFormat::Cq4 ? launch_cq_batch_gpw<kCq4>(b, gpw, exact, waves, lds, stream)
+                                                 : launch_cq_batch_gpw<kCq2>(b, gpw, exact, waves, lds, stream);
+    }
+    for (int j = 0; j < count; j++) {
+        rc = run_matmul(w[j], q, scales, offsets, stride, tokens, y[j], ldy[j], 0, w[j]->rows, nullptr, stream);
+        if (rc) return rc;
+    }
+    return NHIP_OK;
 }
 
 // ------------------------------------------------------------ re-tiling --
@@ -1776,6 +1945,17 @@ int32_t nhip_matmul_i8_dev(const nhip_weights* w, const int8_t* d_q, const float
     NHIP_REQUIRE(ldy >= row_end, "ldy %d < row_end %d", ldy, row_end);
     return run_matmul(w, d_q, d_qscale, nullptr, 0, tokens, d_y, ldy, row_start, row_end, nullptr,
                       as_stream(stream));
+}
+
+int32_t nhip_matmul_batch_dev(const nhip_weights* const* w, int32_t count, const int8_t* d_q, const float* d_scales,
+                              const float* d_offsets, int32_t stride, int32_t tokens, float* const* d_y,
+                              const int32_t* ldy, void* stream)
+{
+    clear_error();
+    NHIP_REQUIRE(w && count >= 1 && count <= kMaxBatchJobs, "batch of %d jobs outside [1, %d]", count, kMaxBatchJobs);
+    const DeviceWeights* dw[kMaxBatchJobs] = {};
+    for (int j = 0; j < count; j++) dw[j] = w[j];
+    return run_matmul_batch(dw, count, d_q, d_scales, d_offsets, stride, tokens, d_y, ldy, as_stream(stream));
 }
 
 int32_t nhip_matmul_cq_dev(const nhip_weights* w, const int8_t* d_values, const float* d_scales,
