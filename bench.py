@@ -238,6 +238,70 @@ class CqGemvCase(GemvCase):
                                            self.dy.ptr, self.n, 0, self.n, None))
 
 
+class BatchCase(CqGemvCase):
+    """Quant.MatMulBatch at Needle 3's attention projections: Q, K, V and
+    Gate (576, 96, 128, 768 rows x 768 columns, Cq2 codebook, g128 norms)
+    sharing one prepared activation set; `copies` sets of the four weights
+    are cycled past the MALL.  launch() runs the grouped launch
+    (nhip_matmul_batch_dev); launch_separate() the four single-matrix
+    launches it replaces."""
+
+    ROWS = (576, 96, 128, 768)
+
+    def __init__(self, m: int, seed: int, min_bytes: int = 300 << 20):
+        k, bits = 768, 2
+        super().__init__(m, k, self.ROWS[0], bits, seed, min_bytes=1)  # activations, codebook, one weight set
+        st = C.c_uint64(seed + 1)
+        per = sum(n * k * bits // 8 + n * (k // 128) * 2 for n in self.ROWS)
+        self.copies = max(2, -(-min_bytes // per))
+        for w in self.weights:
+            w.close()
+        self.sets = []
+        for _ in range(self.copies):
+            ws = []
+            for n in self.ROWS:
+                idx = N.synth_int8(st, n * k * bits // 8).view(np.uint8)
+                norms = N.synth_half_uniform(st, n * (k // 128), 0.002, 0.02)
+                ws.append(N.Weights.codebook(idx, norms, self.book, n, k, bits))
+            self.sets.append(ws)
+        self.weights = [w for ws in self.sets for w in ws]
+        self.outs = [N.DeviceBuffer(m * n * 4) for n in self.ROWS]
+        self.Y = (C.c_void_p * 4)(*[o.ptr for o in self.outs])
+        self.L = (C.c_int32 * 4)(*self.ROWS)
+        self.handles = [(C.c_void_p * 4)(*[w.handle for w in ws]) for ws in self.sets]
+        self.bytes = per + m * k + 2 * m * self.stride * 4 + m * sum(self.ROWS) * 4
+        self.separate = False
+
+    def launch(self, i: int) -> None:
+        if self.separate:
+            for w, o, n in zip(self.sets[i % self.copies], self.outs, self.ROWS):
+                N.check(N.lib().nhip_matmul_cq_dev(w.handle, self.dv.ptr, self.dsc.ptr, self.doff.ptr, self.stride,
+                                                   self.m, o.ptr, n, 0, n, None))
+            return
+        N.check(N.lib().nhip_matmul_batch_dev(self.handles[i % self.copies], 4, self.dv.ptr, self.dsc.ptr,
+                                              self.doff.ptr, self.stride, self.m, self.Y, self.L, None))
+
+
+def batch_lines(args) -> list:
+    """MatMulBatch at Needle 3's Q/K/V/Gate shapes: one grouped launch against
+    the four launches it replaces."""
+    out = []
+    for m in (1, 3):
+        case = BatchCase(m, seed=0x6006 + m)
+        t = case.time(max(200, args.steps // 4), args.warmup)
+        case.separate = True
+        t4 = case.time(max(200, args.steps // 4), args.warmup)
+        g = case.bytes / (t * 1e-3) / 1e9
+        out.append({"workload": f"Needle 3 Q/K/V/Gate MatMulBatch, Cq2 K=768 rows 576+96+128+768, M={m}",
+                    "us_per_launch": round(t * 1e3, 3), "GB/s": round(g, 1),
+                    "frac_hbm_peak": round(g / HBM_PEAK_GBS, 4), "bytes_per_launch": case.bytes,
+                    "us_four_separate_launches": round(t4 * 1e3, 3)})
+        print(f"# MatMulBatch QKVG M={m}: {t * 1e3:.2f} us/launch ({g:.0f} GB/s); four launches {t4 * 1e3:.2f} us",
+              file=sys.stderr, flush=True)
+        case.close()
+    return out
+
+
 class AttnCase:
     """Ragged decode attention: 16 sequences, context lengths U[32, 2048]
     (seeded), 16 heads x 64 (qk 64, MHA), int8 KV cache quantized per
@@ -436,7 +500,7 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-secondary", action="store_true")
     ap.add_argument("--no-decode-loop", action="store_true")
-    ap.add_argument("--only", choices=["prefill", "attention", "decode_loop", "codebook"],
+    ap.add_argument("--only", choices=["prefill", "attention", "decode_loop", "codebook", "batch"],
                     help="run one secondary workload alone (for kernel tracing); prints no JSON line")
     ap.add_argument("--decode-chunks", type=int, default=64,
                     help="attention position-split cap of the decode loop (1: one chunk per row with the output quantize fused)")
@@ -457,6 +521,8 @@ def main() -> int:
             print(json.dumps(decode_loop(args, threads)), file=sys.stderr)
         elif args.only == "codebook":
             codebook_lines(args)
+        elif args.only == "batch":
+            batch_lines(args)
         elif args.only == "prefill":
             for fused in (True, False):
                 case = GemmCase(512, 2048, 8192, seed=0x4004, fused=fused)
@@ -499,6 +565,7 @@ def main() -> int:
             print(f"# GEMV M={m} K={k} N={n}: {t * 1e3:.2f} us/launch, {g:.0f} GB/s", file=sys.stderr, flush=True)
             case.close()
         secondary += codebook_lines(args)
+        secondary += batch_lines(args)
 
     prefill = []
     if not args.no_secondary:
