@@ -12,8 +12,9 @@ region) and timed with HIP events on the stream the kernels run on.
 
 Printed: one JSON line with the metric, a roofline object for the GEMV
 kernel (algorithmic bytes / average launch time vs 8 TB/s) and the CPU
-baseline (the oracle's restatement of the reference CPU MatMulRows, row-
-parallel over NEEDLE_THREADS host threads, on a bounded sample).
+baseline (a restatement of the reference CPU MatMulRows in the SIMD tier the
+reference picks on the host, row-parallel over NEEDLE_THREADS = the physical
+core count, on a bounded sample).
 """
 from __future__ import annotations
 
@@ -366,8 +367,10 @@ def decode_loop(args, threads: int) -> dict:
     """Beam-3 batched decode on the 12-layer d1024 int8 decoder: prompt of
     128 seeded ids (prefill), then up to 64 new tokens with beam width 3.
     row-tokens/s = rows fed after the prompt / decode wall time (beams are
-    rows); the CPU path (the oracle's restatement, linears on `threads`
-    host threads) runs the same search and its token stream is compared."""
+    rows); the CPU path runs the same search twice on `threads` host
+    threads: in the oracle's scalar order (its token stream must equal the
+    GPU's) and with every linear in the reference's SIMD tier (the timed
+    baseline)."""
     from needle_cs_amd.decoder import CONFIG4, GpuDecoder, random_prompt, synthetic_model
 
     t0 = time.perf_counter()
@@ -396,25 +399,41 @@ def decode_loop(args, threads: int) -> dict:
     print(f"# decode loop: {out['row_tokens_per_s']} row-tokens/s, {out['ms_per_step']} ms/step, "
           f"prefill {out['prefill_ms']} ms", file=sys.stderr, flush=True)
     if not args.no_cpu:
-        from oracle import oracle as O  # the CPU path, timed as the baseline and compared token for token
+        from oracle import oracle as O  # the CPU path: checked token for token, and timed as the baseline
 
+        # the oracle's canonical order (the checker of the GPU's token stream)
         cpu = O.CpuDecoder(model, slots=width, capacity=256, threads=threads, max_chunks=args.decode_chunks)
         ctoks, cscore, cfed = cpu.beam_search(prompt, width, max_new, eos)
-        cpre, cdec = float(cpu.seconds[0]), float(cpu.seconds[1])
+        spre, sdec = float(cpu.seconds[0]), float(cpu.seconds[1])
         cpu.close()
         same = bool(np.array_equal(ctoks, toks) and np.float32(cscore) == np.float32(score))
+        # the reference's SIMD tier for every linear (the timed baseline)
+        tier = O.lib().or_simd_tier()
+        cpu = O.CpuDecoder(model, slots=width, capacity=256, threads=threads, max_chunks=args.decode_chunks,
+                           simd=tier)
+        vtoks, vscore, vfed = cpu.beam_search(prompt, width, max_new, eos)
+        cpre, cdec = float(cpu.seconds[0]), float(cpu.seconds[1])
+        cpu.close()
         out["tokens_identical_to_cpu_path"] = same
-        out["cpu_path"] = {"row_tokens_per_s": round(cfed / cdec, 2), "prefill_ms": round(cpre * 1e3, 1),
-                           "threads": threads, "kind": "port",
-                           "sample": "the same prompt and 64-token beam-3 search through the oracle's restatement "
-                                     "(int8 linears row-parallel)"}
+        out["tokens_identical_to_simd_cpu_path"] = bool(np.array_equal(vtoks, toks))
+        common = int(np.argmax(np.append(vtoks[:len(toks)] != toks[:len(vtoks)], True)))
+        out["simd_cpu_path_matching_prefix"] = min(common, len(toks), len(vtoks))
+        out["cpu_path"] = {"row_tokens_per_s": round(vfed / cdec, 2), "prefill_ms": round(cpre * 1e3, 1),
+                           "threads": threads, "kind": "port", "tier": TIER_NAMES[tier],
+                           "scalar_order_row_tokens_per_s": round(cfed / sdec, 2),
+                           "sample": "the same prompt and 64-token beam-3 search on the host: every int8 linear in "
+                                     f"the reference's {TIER_NAMES[tier]} tier (oracle/cpu_simd.c) row-parallel over "
+                                     f"{threads} threads; the token stream is also checked against the oracle's "
+                                     "scalar order, timed as scalar_order_row_tokens_per_s"}
         out["speedup_vs_cpu_path"] = round(out["row_tokens_per_s"] / out["cpu_path"]["row_tokens_per_s"], 1)
-        print(f"# decode loop CPU path: {out['cpu_path']['row_tokens_per_s']} row-tokens/s; identical tokens: "
-              f"{same}", file=sys.stderr, flush=True)
+        print(f"# decode loop CPU path ({TIER_NAMES[tier]}): {out['cpu_path']['row_tokens_per_s']} row-tokens/s "
+              f"(scalar order {out['cpu_path']['scalar_order_row_tokens_per_s']}); identical tokens: {same} "
+              f"(SIMD path: {out['tokens_identical_to_simd_cpu_path']})", file=sys.stderr, flush=True)
     return out
 
 
 def physical_cores() -> int:
+    """lscpu's distinct (core, socket) pairs: cores per socket x sockets."""
     try:
         import subprocess
         out = subprocess.run(["lscpu", "-p=CORE,SOCKET"], capture_output=True, text=True).stdout
@@ -424,13 +443,26 @@ def physical_cores() -> int:
         return max(1, (os.cpu_count() or 2) // 2)
 
 
-def cpu_baseline(case: GemvCase, budget_s: float) -> dict:
-    """The oracle's MatMulRows restatement (row-parallel as MatMulBatch.RunShard)
-    on the host cores, same shape, bounded to about `budget_s` seconds."""
-    from oracle import oracle as O  # the checker, timed here as the CPU baseline
+def host_threads() -> int:
+    """NEEDLE_THREADS when set, else the host's physical core count (the
+    reference CLI's NEEDLE_THREADS setting for a whole host)."""
+    return int(os.environ.get("NEEDLE_THREADS", "0")) or physical_cores()
 
-    threads = int(os.environ.get("NEEDLE_THREADS", "0")) or min(physical_cores(), int(os.environ.get("OMP_NUM_THREADS", "16") or 16))
-    threads = O.lib().or_baseline_start(threads)
+
+TIER_NAMES = {0: "scalar", 1: "AVX2", 2: "AVX-VNNI"}
+
+
+def cpu_baseline(case: GemvCase, budget_s: float) -> dict:
+    """The reference CPU path's GEMV on the host cores, same shape: the SIMD
+    tier Tiers.Best picks on this CPU (oracle/cpu_simd.c: Gemv.Tile4 / Tile2
+    / Rows with the AVX-VNNI or AVX2 group dot), row-parallel as
+    MatMulBatch.RunShard over the physical cores, bounded to about
+    `budget_s` seconds; the scalar restatement of Scalar.MatMulRows is timed
+    beside it on a shorter sample."""
+    from oracle import oracle as O  # the checker's library, timed here as the CPU baseline
+
+    threads = O.lib().or_baseline_start(host_threads())
+    tier = O.lib().or_simd_tier()
     m, k, n = case.m, case.k, case.n
     st = C.c_uint64(0xC0FFEE)
     copies = 4
@@ -438,21 +470,34 @@ def cpu_baseline(case: GemvCase, budget_s: float) -> dict:
     ss = [N.synth_half_uniform(st, n * (k // 32), 0.002, 0.02).reshape(n, k // 32) for _ in range(copies)]
     q, qs = O.quantize_rows(case.x)
     y = np.zeros((m, n), dtype=np.float32)
-    times = []
-    t_end = time.perf_counter() + budget_s
-    i = 0
-    while time.perf_counter() < t_end or i < 3:
-        t0 = time.perf_counter()
-        O.lib().or_baseline_matmul_i8(O.p(ws[i % copies]), O.p(ss[i % copies]), n, k, 32, O.p(q), O.p(qs), m,
-                                      O.p(y), n, 0, n)
-        times.append(time.perf_counter() - t0)
-        i += 1
+
+    def sample(simd: bool, seconds: float):
+        times = []
+        t_end = time.perf_counter() + seconds
+        i = 0
+        while time.perf_counter() < t_end or i < 3:
+            t0 = time.perf_counter()
+            if simd:
+                O.lib().or_baseline_simd_matmul_i8(tier, O.p(ws[i % copies]), O.p(ss[i % copies]), n, k, O.p(q),
+                                                   O.p(qs), m, O.p(y), n, 0, n)
+            else:
+                O.lib().or_baseline_matmul_i8(O.p(ws[i % copies]), O.p(ss[i % copies]), n, k, 32, O.p(q), O.p(qs),
+                                              m, O.p(y), n, 0, n)
+            times.append(time.perf_counter() - t0)
+            i += 1
+        return times
+
+    times = sample(True, budget_s)
+    scalar = sample(False, max(1.0, budget_s / 5))
     O.lib().or_baseline_stop()
-    med = float(np.median(times))
+    med, smed = float(np.median(times)), float(np.median(scalar))
     return {"value": round(case.bytes / med / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+            "tier": TIER_NAMES[tier], "physical_cores": physical_cores(),
+            "scalar_port_GBps": round(case.bytes / smed / 1e9, 3),
             "sample": f"{len(times)} GEMVs M={m} K={k} N={n} cycling {copies} weight copies in {sum(times):.1f} s "
-                      f"(median {med * 1e3:.2f} ms/GEMV); oracle restatement of Scalar.MatMulRows, row-parallel "
-                      f"over {threads} threads"}
+                      f"(median {med * 1e3:.3f} ms/GEMV); restatement of the reference's {TIER_NAMES[tier]} tier "
+                      f"(Gemv.Tile2 + Rows, VnniDot / Avx2Dot), row-parallel over {threads} threads; the scalar "
+                      f"MatMulRows restatement: median {smed * 1e3:.2f} ms/GEMV over {len(scalar)} GEMVs"}
 
 
 def pmc_run(case: GemvCase, launches: int) -> int:
@@ -516,7 +561,7 @@ def main() -> int:
     print(f"# {N.lib().nhip_describe().decode()}", file=sys.stderr, flush=True)
 
     if args.only:
-        threads = int(os.environ.get("NEEDLE_THREADS", "0")) or min(physical_cores(), 16)
+        threads = host_threads()
         if args.only == "decode_loop":
             print(json.dumps(decode_loop(args, threads)), file=sys.stderr)
         elif args.only == "codebook":
@@ -604,7 +649,7 @@ def main() -> int:
             print(f"# needle3 attention inputs, {rows} rows: {t * 1e3:.2f} us/launch", file=sys.stderr, flush=True)
             case.close()
 
-    threads = int(os.environ.get("NEEDLE_THREADS", "0")) or min(physical_cores(), int(os.environ.get("OMP_NUM_THREADS", "16") or 16))
+    threads = host_threads()
     loop = None
     if not args.no_decode_loop:
         loop = decode_loop(args, threads)
@@ -612,7 +657,8 @@ def main() -> int:
     cpu = None
     if not args.no_cpu:
         cpu = cpu_baseline(main_case, args.cpu_seconds)
-        print(f"# cpu baseline: {cpu['value']} GB/s on {cpu['cores']} threads", file=sys.stderr, flush=True)
+        print(f"# cpu baseline ({cpu['tier']}): {cpu['value']} GB/s on {cpu['cores']} threads (scalar port "
+              f"{cpu['scalar_port_GBps']} GB/s)", file=sys.stderr, flush=True)
 
     line = {
         "metric": METRIC,

@@ -7,7 +7,8 @@
  * [m*B/M, (m+1)*B/M).  Workers are a persistent spin pool, as
  * src/Needle/Pool.cs keeps its team spinning between calls.  Every member
  * runs or_matmul_rows_i8 on its rows, so results are bit-identical to the
- * single-threaded oracle.
+ * single-threaded oracle; or_baseline_simd_matmul_i8 runs the SIMD tier
+ * (cpu_simd.c) on each member's rows instead.
  */
 #define _GNU_SOURCE
 #include <pthread.h>
@@ -18,6 +19,7 @@
 #include "needle_oracle.h"
 
 typedef struct {
+    int tier; /* OR_TIER_SCALAR: or_matmul_rows_i8, else or_simd_matmul_i8 */
     const int8_t* w;
     const uint16_t* scales;
     int rows, cols, group;
@@ -46,7 +48,10 @@ static void run_member(int m)
     int r0 = j->row_start + first * 4;
     int r1 = j->row_start + end * 4;
     if (r1 > j->row_end) r1 = j->row_end;
-    if (r0 < r1)
+    if (r0 < r1 && j->tier != OR_TIER_SCALAR)
+        or_simd_matmul_i8(j->tier, j->w, j->scales, j->rows, j->cols, j->q, j->qscale, j->tokens, j->y, j->ldy, r0,
+                          r1);
+    else if (r0 < r1)
         or_matmul_rows_i8(j->w, j->scales, j->rows, j->cols, j->group, j->q, j->qscale, j->tokens, j->y, j->ldy,
                           r0, r1);
 }
@@ -94,6 +99,15 @@ void or_baseline_stop(void)
     }
 }
 
+static void run_pool(const job_t* j)
+{
+    pool.job = *j;
+    atomic_store(&pool.done, 0);
+    atomic_fetch_add_explicit(&pool.generation, 1, memory_order_release);
+    run_member(0);
+    while (atomic_load_explicit(&pool.done, memory_order_acquire) < pool.members - 1) sched_yield();
+}
+
 void or_baseline_matmul_i8(const int8_t* w, const uint16_t* scales, int rows, int cols, int group, const int8_t* q,
                            const float* qscale, int tokens, float* y, int ldy, int row_start, int row_end)
 {
@@ -101,10 +115,18 @@ void or_baseline_matmul_i8(const int8_t* w, const uint16_t* scales, int rows, in
         or_matmul_rows_i8(w, scales, rows, cols, group, q, qscale, tokens, y, ldy, row_start, row_end);
         return;
     }
-    job_t j = {w, scales, rows, cols, group, q, qscale, tokens, y, ldy, row_start, row_end};
-    pool.job = j;
-    atomic_store(&pool.done, 0);
-    atomic_fetch_add_explicit(&pool.generation, 1, memory_order_release);
-    run_member(0);
-    while (atomic_load_explicit(&pool.done, memory_order_acquire) < pool.members - 1) sched_yield();
+    job_t j = {OR_TIER_SCALAR, w, scales, rows, cols, group, q, qscale, tokens, y, ldy, row_start, row_end};
+    run_pool(&j);
+}
+
+void or_baseline_simd_matmul_i8(int tier, const int8_t* w, const uint16_t* scales, int rows, int cols,
+                                const int8_t* q, const float* qscale, int tokens, float* y, int ldy, int row_start,
+                                int row_end)
+{
+    if (pool.members <= 1) {
+        or_simd_matmul_i8(tier, w, scales, rows, cols, q, qscale, tokens, y, ldy, row_start, row_end);
+        return;
+    }
+    job_t j = {tier, w, scales, rows, cols, 32, q, qscale, tokens, y, ldy, row_start, row_end};
+    run_pool(&j);
 }

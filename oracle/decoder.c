@@ -8,7 +8,8 @@
  * fused QKV -> RoPE -> int8 KV cache -> ragged attention -> output
  * projection -> residual, RMSNorm -> gate/up -> SwiGLU -> down -> residual,
  * final RMSNorm -> LM head -> TopKLogSoftmax -> beam search.  Every linear is
- * the literal int8 matmul (or_matmul_rows_i8, Scalar.MatMulRows' order) on
+ * the literal int8 matmul (or_matmul_rows_i8, Scalar.MatMulRows' order; or,
+ * for the timed CPU path only, the SIMD tier of cpu_simd.c) on
  * activations quantized per row with QuantizeInt8 (Scalar.cs:67-74);
  * attention is or_attention_decode (AttentionBatch + MergePartials order);
  * the beam driver follows Whistle.BeamSearch (src/Needle/Whistle.Decode.cs:
@@ -164,7 +165,9 @@ void or_topk_lse(const float* x, int n, int k, int mask, int* idx, float* lp)
 static void linear(const or_decoder* m, const int8_t* w, const uint16_t* s, int rows, int cols, const int8_t* q,
                    const float* qs, int tokens, float* y)
 {
-    if (m->threads > 1)
+    if (m->simd != OR_TIER_SCALAR)
+        or_baseline_simd_matmul_i8(m->simd, w, s, rows, cols, q, qs, tokens, y, rows, 0, rows);
+    else if (m->threads > 1)
         or_baseline_matmul_i8(w, s, rows, cols, 32, q, qs, tokens, y, rows, 0, rows);
     else
         or_matmul_rows_i8(w, s, rows, cols, 32, q, qs, tokens, y, rows, 0, rows);

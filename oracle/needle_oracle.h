@@ -224,6 +224,22 @@ void or_baseline_matmul_i8(const int8_t* w, const uint16_t* scales, int rows, in
                            const int8_t* q, const float* qscale, int tokens, float* y, int ldy,
                            int row_start, int row_end);
 
+/* ---- SIMD tier of the CPU matmul (cpu_simd.c): the timed baseline ---- */
+
+enum { OR_TIER_SCALAR = 0, OR_TIER_AVX2 = 1, OR_TIER_AVX_VNNI = 2 };
+/* Tiers.Best on this CPU (src/Needle/Tiers.cs:127-138): AVX-VNNI, else
+ * AVX2 + FMA (+ F16C), else scalar. */
+int or_simd_tier(void);
+/* Quant.MatMulRows' SIMD branch (Quant.cs:627-632, Gemv.cs Tile4 / Tile2 /
+ * Rows) for the literal int8 format (group 32): exact int32 group sums, the
+ * SIMD tier's float association. */
+void or_simd_matmul_i8(int tier, const int8_t* w, const uint16_t* scales, int rows, int cols, const int8_t* q,
+                       const float* qscale, int tokens, float* y, int ldy, int row_start, int row_end);
+/* or_simd_matmul_i8 split over the pool's members (4-row blocks). */
+void or_baseline_simd_matmul_i8(int tier, const int8_t* w, const uint16_t* scales, int rows, int cols,
+                                const int8_t* q, const float* qscale, int tokens, float* y, int ldy,
+                                int row_start, int row_end);
+
 /* ---- synthetic int8 decoder (decoder.c) ---- */
 
 /* Canonical element-wise operations of the decoder (no reference
@@ -266,6 +282,7 @@ typedef struct or_decoder {
     const int8_t* wlm;       /* [vocab][d] */
     const uint16_t* slm;
     int threads;             /* > 1: linears on the baseline pool */
+    int simd;                /* OR_TIER_*: linears in the SIMD tier (the timed CPU path), 0: the scalar order */
     float* rope_cos;         /* owned: [capacity][head_dim/2] */
     float* rope_sin;
     int8_t* keys;            /* owned: [layer][slot][capacity][kv_heads*head_dim] */

@@ -51,6 +51,7 @@ class LayerWeights(C.Structure):
 class Decoder(C.Structure):
     _fields_ = [("dims", DecoderDims), ("layers", C.POINTER(LayerWeights)), ("embedding", C.c_void_p),
                 ("final_norm", C.c_void_p), ("wlm", C.c_void_p), ("slm", C.c_void_p), ("threads", C.c_int),
+                ("simd", C.c_int),
                 ("rope_cos", C.c_void_p), ("rope_sin", C.c_void_p), ("keys", C.c_void_p), ("values", C.c_void_p),
                 ("key_scales", C.c_void_p), ("value_scales", C.c_void_p)]
 
@@ -122,6 +123,9 @@ _PROTOS = {
     "or_baseline_start": (_i, [_i]),
     "or_baseline_stop": (None, []),
     "or_baseline_matmul_i8": (None, [_vp, _vp, _i, _i, _i, _vp, _vp, _i, _vp, _i, _i, _i]),
+    "or_simd_tier": (_i, []),
+    "or_simd_matmul_i8": (None, [_i, _vp, _vp, _i, _i, _vp, _vp, _i, _vp, _i, _i, _i]),
+    "or_baseline_simd_matmul_i8": (None, [_i, _vp, _vp, _i, _i, _vp, _vp, _i, _vp, _i, _i, _i]),
 }
 
 _LIB = None
@@ -268,7 +272,7 @@ class CpuDecoder:
     """The oracle's decoder over a synthetic model's numpy arrays (see
     needle_cs_amd.decoder.synthetic_model for the layout)."""
 
-    def __init__(self, model: dict, slots: int, capacity: int, max_chunks: int = 64, threads: int = 1):
+    def __init__(self, model: dict, slots: int, capacity: int, max_chunks: int = 64, threads: int = 1, simd: int = 0):
         dm = model["dims"]
         self._keep = model
         self.layers = (LayerWeights * dm["layers"])()
@@ -284,6 +288,7 @@ class CpuDecoder:
         self.dec.wlm = p(model["wlm"])
         self.dec.slm = p(model["slm"])
         self.dec.threads = threads
+        self.dec.simd = simd
         assert lib().or_decoder_init(C.byref(self.dec)) == 0
         self.vocab = dm["vocab"]
 
