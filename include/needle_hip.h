@@ -121,6 +121,20 @@ void nhip_merge_partials(const float* partials, int32_t count, int32_t heads, fl
  * scalar src/Needle/Scalar.cs:67-74).  Returns the scale. */
 float nhip_quantize_int8(const float* x, int32_t n, int8_t* destination);
 
+/* The kernel-table entries above return void, as the reference's do: a
+ * failure (no device, a HIP error, an argument the reference's caller would
+ * have rejected) leaves the outputs untouched and sets nhip_last_error(), so
+ * a host installs the table only after a probe call leaves nhip_last_error()
+ * empty.  Weights are looked up in a cache by their view's host pointers and
+ * shape; nhip_table_release drops every cached device copy whose index
+ * pointer lies in [base, base + bytes) (all of them when base is NULL) and
+ * frees its HBM -- call it when the host disposes of the model that owns
+ * those bytes (Model.Dispose), with no entry running on its weights, so that
+ * a later model mapped at the same addresses is uploaded afresh.
+ * nhip_table_cached reports the cached entries and their HBM bytes. */
+int32_t nhip_table_release(const void* base, size_t bytes, int32_t* released);
+int32_t nhip_table_cached(int32_t* entries, size_t* device_bytes);
+
 /* Mirror of Net10KernelExports.Fill (src/Needle/Kernels/Net10KernelExports.cs:118-150):
  * writes this library's entries into a 27-slot KernelTable (slots 0, 1, 3, 4,
  * 22; every other slot is set to NULL so the reference falls back to its own

@@ -111,6 +111,8 @@ _PROTOS = {
     "nhip_attention_decode_workspace_init": (_i32, [_vp, _sz, _vp]),
     "nhip_attention_decode_dev": (_i32, [_vp, _vp, _i32, _i32, _i32, _i32, _vp, _vp, _vp, _vp, _i32, _i32, _vp, _vp,
                                          _vp, _i32, _vp, _sz, _vp, _vp]),
+    "nhip_table_release": (_i32, [_vp, _sz, _vp]),
+    "nhip_table_cached": (_i32, [_vp, _vp]),
     "nhip_matmul_batch_dev": (_i32, [_vp, _i32, _vp, _vp, _vp, _i32, _i32, _vp, _vp, _vp]),
     "nhip_attention_decode_noalloc_dev": (_i32, [_vp, _vp, _i32, _i32, _i32, _i32, _vp, _vp, _vp, _vp, _i32, _i32,
                                                  _vp, _vp, _vp, _i32, _vp, _vp]),

@@ -4,8 +4,10 @@
 // The reference calls these from its thread pool concurrently on disjoint
 // row ranges (src/Needle/Quant.cs:725-771), so every entry is re-entrant:
 // per-thread staging buffers and stream, and a mutex-guarded cache mapping a
-// weight view's host pointers to its HBM copy (uploaded once, kept for the
-// life of the process, as the reference keeps the mapped model).
+// weight view's host pointers to its HBM copy (uploaded on first use, kept
+// until nhip_table_release drops the entries of a model's host range, which
+// the host calls when it disposes of the model: a later model mapped at the
+// same addresses must not find the old weights).
 #include <cstring>
 #include <map>
 #include <mutex>
@@ -204,6 +206,44 @@ float nhip_quantize_int8(const float* x, int32_t n, int8_t* destination)
     if (n <= 0) return scale;
     if (quantize_impl(x, n, destination, &scale) != NHIP_OK) return 1.0f;
     return scale;
+}
+
+int32_t nhip_table_release(const void* base, size_t bytes, int32_t* released)
+{
+    clear_error();
+    int32_t n = 0;
+    {
+        std::lock_guard<std::mutex> lock(g_cache_mutex);
+        const uintptr_t lo = reinterpret_cast<uintptr_t>(base);
+        for (auto it = g_cache.begin(); it != g_cache.end();) {
+            const uintptr_t idx = reinterpret_cast<uintptr_t>(std::get<0>(it->first));
+            if (!base || (idx >= lo && idx - lo < bytes)) {
+                if (device_ready()) (void)hipDeviceSynchronize();  // no kernel still reads them
+                nhip_weights_destroy(it->second);
+                it = g_cache.erase(it);
+                n++;
+            } else {
+                ++it;
+            }
+        }
+    }
+    if (released) *released = n;
+    return NHIP_OK;
+}
+
+int32_t nhip_table_cached(int32_t* entries, size_t* device_bytes)
+{
+    clear_error();
+    std::lock_guard<std::mutex> lock(g_cache_mutex);
+    size_t total = 0;
+    for (const auto& kv : g_cache) {
+        size_t b = 0;
+        (void)nhip_weights_info(kv.second, nullptr, nullptr, nullptr, &b);
+        total += b;
+    }
+    if (entries) *entries = (int32_t)g_cache.size();
+    if (device_bytes) *device_bytes = total;
+    return NHIP_OK;
 }
 
 int32_t nhip_fill_kernel_table(void** table, int32_t count)

@@ -73,3 +73,26 @@ def test_gemm_special_scales_exact(hip, orc):
     want = np.zeros((tokens, rows), dtype=np.float32)
     orc.matmul_rows_i8(w, scales, q, qs, tokens, want, rows, 0, rows)
     assert np.array_equal(y.view(np.uint32), want.view(np.uint32))
+
+
+def test_gemm_prefill_config_full_size(hip, orc):
+    """The prefill configuration at full size: M = 512 tokens, K = 2048,
+    N = 8192.  Exact path bit-identical with Scalar.MatMulRows' order, fused
+    path within 1e-4 * RMS; the oracle runs row-parallel on its pool (the
+    same bits as one thread)."""
+    tokens, rows, cols = 512, 8192, 2048
+    w, scales, x, q, qs = int8_case(orc, 0x512, rows, cols, tokens)
+    weights = hip.Weights.int8(w, scales)
+    want = np.zeros((tokens, rows), dtype=np.float32)
+    members = orc.lib().or_baseline_start(8)
+    try:
+        orc.lib().or_baseline_matmul_i8(orc.p(w), orc.p(scales), rows, cols, 32, orc.p(q), orc.p(qs), tokens,
+                                        orc.p(want), rows, 0, rows)
+    finally:
+        orc.lib().or_baseline_stop()
+    assert members == 8
+    y = run_i8(hip, weights, q, qs, tokens, rows, 0, rows)
+    assert np.array_equal(y.view(np.uint32), want.view(np.uint32))
+    yf = run_fused(hip, weights, q, qs, tokens, rows, 0, rows)
+    rms = float(np.sqrt(np.mean(want.astype(np.float64) ** 2)))
+    assert np.max(np.abs(yf.astype(np.float64) - want)) <= 1e-4 * rms
