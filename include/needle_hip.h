@@ -510,7 +510,59 @@ int32_t nhip_model_record(const nhip_model* m, int32_t index, nhip_record_info* 
 nhip_weights* nhip_model_weights(const nhip_model* m, int32_t index);
 /* the fp32 device array of an fp16 / fp32 record, else NULL */
 const float* nhip_model_dense(const nhip_model* m, int32_t index);
+/* the record's bytes (indices, then fp16 norms) on the device, for row
+ * gathers (Quant.GatherRow, src/Needle/Quant.cs:566-575), of a
+ * codebook-quantized record, else NULL */
+const uint8_t* nhip_model_raw(const nhip_model* m, int32_t index);
+/* the archive's 2-bit and 4-bit codebooks (Model.cs:318-321); either may be NULL */
+int32_t nhip_model_codebooks(const nhip_model* m, nhip_codebook* book2, nhip_codebook* book4);
 int32_t nhip_model_close(nhip_model* m);
+
+/* ----------------------------------- Needle 3 batched engine (step API) -- */
+
+/* BatchedEngine over an opened Needle 3 archive (src/Needle/BatchEngine.cs:5-50,
+ * EngineCore.ForwardBatch, src/Needle/Engine.cs:2285-2350): `slots` (1..16)
+ * independent sequences of up to `capacity` positions each, steps of up to
+ * `chunk` rows (0: the reference's default 64).  Attention splits a row's
+ * span into at most `max_chunks` chunks by the reference's plan (0: 8, the
+ * reference's MaxChunks, Blocks.cs:832).  The model must stay open while the
+ * context lives.  One context is single-threaded; it owns a HIP stream and
+ * its device state (KV cache, convolution and engram histories, snapshots). */
+typedef struct nhip_ctx nhip_ctx;
+
+int32_t nhip_ctx_create(const nhip_model* model, int32_t capacity, int32_t slots, int32_t chunk,
+                        int32_t max_chunks, nhip_ctx** out);
+int32_t nhip_ctx_destroy(nhip_ctx* c);
+/* any output may be NULL */
+int32_t nhip_ctx_info(const nhip_ctx* c, int32_t* vocab, int32_t* slots, int32_t* capacity, int32_t* chunk);
+/* ForwardBatch (Engine.cs:2303-2350): row r feeds tokens[r] to slot
+ * row_slots[r]; a slot's rows form one contiguous run at the slot's length +
+ * their offset in it, and every slot's length grows by its run (NHIP_ERR_ARG
+ * past the capacity, before any device work).  The LM head runs only over
+ * head_rows[0..heads): output row i is row head_rows[i] -- logits
+ * [heads][vocab] if non-NULL (BatchLogitsRow), the top-k ids and
+ * log-probabilities [heads][k] if k > 0 (Ops.TopKLogSoftmax as
+ * nhip_topk_lse_dev), Ops.ArgMax of each head row into argmax[heads] if
+ * non-NULL.  Synchronous.  After a failed step the slots it named must be
+ * reset. */
+int32_t nhip_step(nhip_ctx* c, const int32_t* tokens, const int32_t* row_slots, int32_t rows,
+                  const int32_t* head_rows, int32_t heads, float* logits, int32_t k, int32_t* topk_idx,
+                  float* topk_lp, int32_t* argmax);
+/* FeedSlot (Engine.cs:2285-2301): `count` tokens into one slot in steps of
+ * `chunk` rows; logits [vocab] of the last token if non-NULL. */
+int32_t nhip_slot_feed(nhip_ctx* c, int32_t slot, const int32_t* tokens, int32_t count, float* logits);
+/* ResetSlot / MarkSlot / RewindSlot / SlotLength (BatchEngine.cs:24-29,
+ * Engine.cs:2224-2283): reset clears the slot's histories and sets its length
+ * and mark to 0; mark snapshots the histories and records the length; rewind
+ * restores the snapshot and the length. */
+int32_t nhip_slot_reset(nhip_ctx* c, int32_t slot);
+int32_t nhip_slot_mark(nhip_ctx* c, int32_t slot);
+int32_t nhip_slot_rewind(nhip_ctx* c, int32_t slot);
+int32_t nhip_slot_length(const nhip_ctx* c, int32_t slot, int32_t* length);
+/* Engine.CopyFrom (Engine.cs:367-379) between two slots of one context (a
+ * beam reorder): dst becomes a clone of src -- KV positions [0, length of
+ * src), histories, snapshot, previous tokens, length and mark. */
+int32_t nhip_slot_copy(nhip_ctx* c, int32_t dst, int32_t src);
 
 /* ------------------------------------------ synthetic workload inputs -- */
 

@@ -106,6 +106,18 @@ _PROTOS = {
     "nhip_model_weights": (_vp, [_vp, _i32]),
     "nhip_model_dense": (_vp, [_vp, _i32]),
     "nhip_model_close": (_i32, [_vp]),
+    "nhip_model_raw": (_vp, [_vp, _i32]),
+    "nhip_model_codebooks": (_i32, [_vp, C.POINTER(Codebook), C.POINTER(Codebook)]),
+    "nhip_ctx_create": (_i32, [_vp, _i32, _i32, _i32, _i32, C.POINTER(_vp)]),
+    "nhip_ctx_destroy": (_i32, [_vp]),
+    "nhip_ctx_info": (_i32, [_vp, _vp, _vp, _vp, _vp]),
+    "nhip_step": (_i32, [_vp, _vp, _vp, _i32, _vp, _i32, _vp, _i32, _vp, _vp, _vp]),
+    "nhip_slot_feed": (_i32, [_vp, _i32, _vp, _i32, _vp]),
+    "nhip_slot_reset": (_i32, [_vp, _i32]),
+    "nhip_slot_mark": (_i32, [_vp, _i32]),
+    "nhip_slot_rewind": (_i32, [_vp, _i32]),
+    "nhip_slot_length": (_i32, [_vp, _i32, _vp]),
+    "nhip_slot_copy": (_i32, [_vp, _i32, _i32]),
     "nhip_matmul_i8_fused_dev": (_i32, [_vp, _vp, _vp, _i32, _vp, _i32, _i32, _i32, _vp]),
     "nhip_attention_decode_workspace": (_sz, [_i32, _i32, _i32]),
     "nhip_attention_decode_workspace_init": (_i32, [_vp, _sz, _vp]),

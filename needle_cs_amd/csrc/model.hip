@@ -14,9 +14,14 @@
 //   CQ data  rows x cols*bits/8 index bytes, then fp16 norms [rows][cols/128].
 // The well-formedness checks are Model.RequireWellFormed's, done on the host
 // before any device work.  CQ tensors become device weights (the matmul
-// kernels' re-tiled layout); fp16 / fp32 tensors become fp32 device arrays
-// (fp16 by Scalar.HalfToSingle, the exact decode of non-audio archives); raw
-// tensors (the tokenizer blob) stay in the caller's bytes.
+// kernels' re-tiled layout) and also keep their raw bytes on the device (for
+// row gathers: Quant.GatherRow of the embedding and the engram tables);
+// fp16 / fp32 tensors become fp32 device arrays.  fp16 records decode with
+// Scalar.HalfToSingle, except in archives that carry audio weights (a
+// 13-element fp32 record, Model.cs:343, 391-397): there the records before
+// the audio block decode with HalfToSingleUpstream, as Model.Open's reader
+// does (ExactHalves = !HasAudioWeights, Model.cs:334, 346).  Raw tensors
+// (the tokenizer blob) stay in the caller's bytes.
 #include <cstring>
 #include <vector>
 
@@ -43,6 +48,18 @@ float half_to_single(uint16_t half)
         return (half & 0x8000u) ? -sub : sub;
     }
     const uint32_t bits = ((mag << 13) + 0x38000000u) | ((half & 0x8000u) << 16);
+    float f;
+    std::memcpy(&f, &bits, 4);
+    return f;
+}
+
+// Scalar.HalfToSingleUpstream (src/Needle/Scalar.cs:113-119): the exponent
+// rebias without the subnormal case.
+float half_to_single_upstream(uint16_t half)
+{
+    const uint32_t mag = half & 0x7FFFu;
+    if (mag == 0) return 0.0f;
+    const uint32_t bits = ((mag << 13) + 0x38000000u) | ((uint32_t)(half & 0x8000u) << 16);
     float f;
     std::memcpy(&f, &bits, 4);
     return f;
@@ -83,6 +100,7 @@ struct nhip_model {
     nhip_codebook book2{}, book4{};
     std::vector<nhip_record_info> info;
     std::vector<nhip_weights*> weights;  // CQ records
+    std::vector<uint8_t*> raw;           // CQ records: their bytes (indices, then norms) on the device
     std::vector<float*> dense;           // fp16 / fp32 records, fp32 on the device
 };
 
@@ -183,7 +201,12 @@ int32_t nhip_open(const uint8_t* cact, size_t length, nhip_model** out)
     }
     const size_t count = m->info.size();
     m->weights.assign(count, nullptr);
+    m->raw.assign(count, nullptr);
     m->dense.assign(count, nullptr);
+    // HasAudioWeights: the audio block starts at a 13-element fp32 record
+    size_t audio_at = count;
+    for (size_t i = 0; i < count && audio_at == count; i++)
+        if (m->info[i].dtype == NHIP_CACT_FP32 && m->info[i].ndim == 1 && m->info[i].shape[0] == 13) audio_at = i;
     std::vector<float> host;
     for (size_t i = 0; i < count && rc == NHIP_OK; i++) {
         const nhip_record_info& ri = m->info[i];
@@ -196,6 +219,16 @@ int32_t nhip_open(const uint8_t* cact, size_t length, nhip_model** out)
             nhip_cq cq{src, norms.data(), ri.bits == 2 ? &m->book2 : &m->book4, (int32_t)ri.shape[0],
                        (int32_t)ri.shape[1], (int32_t)ri.bits};
             rc = weights_cq_create_internal(&cq, &m->weights[i]);
+            if (rc == NHIP_OK) {
+                void* d = nullptr;
+                hipError_t e = hipMalloc(&d, std::max<size_t>(ri.bytes, 1));
+                if (e == hipSuccess) e = hipMemcpy(d, src, ri.bytes, hipMemcpyHostToDevice);
+                if (e != hipSuccess) {
+                    set_error("codebook tensor %zu raw upload failed: %s", i, hipGetErrorString(e));
+                    rc = NHIP_ERR_HIP;
+                }
+                m->raw[i] = static_cast<uint8_t*>(d);
+            }
         } else if (ri.dtype == NHIP_CACT_FP16 || ri.dtype == NHIP_CACT_FP32) {
             const size_t n = (size_t)elements(ri);
             host.resize(std::max<size_t>(n, 1));
@@ -203,7 +236,7 @@ int32_t nhip_open(const uint8_t* cact, size_t length, nhip_model** out)
                 for (size_t e = 0; e < n; e++) {
                     uint16_t h;
                     std::memcpy(&h, src + 2 * e, 2);
-                    host[e] = half_to_single(h);
+                    host[e] = audio_at < count && i < audio_at ? half_to_single_upstream(h) : half_to_single(h);
                 }
             } else {
                 std::memcpy(host.data(), src, n * 4);
@@ -245,6 +278,21 @@ int32_t nhip_model_record(const nhip_model* m, int32_t index, nhip_record_info* 
     return NHIP_OK;
 }
 
+const uint8_t* nhip_model_raw(const nhip_model* m, int32_t index)
+{
+    if (!m || index < 0 || (size_t)index >= m->raw.size()) return nullptr;
+    return m->raw[index];
+}
+
+int32_t nhip_model_codebooks(const nhip_model* m, nhip_codebook* book2, nhip_codebook* book4)
+{
+    clear_error();
+    NHIP_REQUIRE(m, "model is NULL");
+    if (book2) *book2 = m->book2;
+    if (book4) *book4 = m->book4;
+    return NHIP_OK;
+}
+
 nhip_weights* nhip_model_weights(const nhip_model* m, int32_t index)
 {
     if (!m || index < 0 || (size_t)index >= m->weights.size()) return nullptr;
@@ -263,6 +311,8 @@ int32_t nhip_model_close(nhip_model* m)
     for (nhip_weights* w : m->weights)
         if (w) nhip_weights_destroy(w);
     for (float* d : m->dense)
+        if (d) (void)hipFree(d);
+    for (uint8_t* d : m->raw)
         if (d) (void)hipFree(d);
     delete m;
     return NHIP_OK;

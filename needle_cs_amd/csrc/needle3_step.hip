@@ -1,0 +1,1320 @@
+// needle3_step.hip -- Needle 3's batched decode step on gfx950, driven from an
+// opened .cact archive: the step API of the batched engine (nhip_ctx_*,
+// nhip_step, nhip_slot_*).
+//
+// One step is EngineCore.ForwardBatch (src/Needle/Engine.cs:2303-2350): rows
+// from up to `slots` independent sequences, each slot's rows one contiguous
+// run at the slot's length + their offset, through
+//   embedding (Quant.GatherRow of the 4-bit table, times sqrt(dim), copied to
+//   the four hyper-connection lanes),
+//   per layer (RunLayerBatch, :2352-2398)
+//     RmsFakeA8 of the 4-lane stream, Prepare 4-bit, the phi matmuls,
+//     sigmoid gates, Mix4 and Sinkhorn4x4 (the hyper-connection mix),
+//     the engram at its layers (ApplyEngramBatch, :2399-2463),
+//     attention (RunAttentionBatch, :2480-2596): CenteredRmsFakeA8, Prepare
+//     2-bit, the Q/K/V/Gate MatMulBatch, the three-tap convolution +
+//     ZeroCenteredRms + RoPE + QuantizeInt8 into the KV cache, ragged
+//     attention over the window (global layers: the whole span), GateFakeA8,
+//     Prepare, the output matmul and PostNormAdd,
+//     the Kronecker-Hadamard MLP (HadamardMlp.Apply, Blocks.cs:1067-1101),
+//     CombineDiff4x4 into the next stream;
+//   the head rows: Mix4 of the lanes, ZeroCenteredRms, FakeA8, Prepare 4-bit
+//   and the tied embedding (PrepareHeadVectors, :920-928).
+// Every row kernel below follows its scalar kernel's operation order
+// (src/Needle/Scalar.cs) with the polynomial Ops.Exp where that code calls
+// MathF.Exp; sums are sequential chains (one lane over the row staged in
+// LDS), maxima are order-free, element-wise work runs in parallel with the
+// same per-element arithmetic.  The results are bit-identical with the CPU
+// restatement.
+#include <algorithm>
+#include <cmath>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "common.hpp"
+
+namespace nhip {
+
+int32_t attention_decode_impl(const int8_t* d_q, const float* d_qscale, int32_t rows, int32_t heads,
+                              int32_t kv_heads, int32_t qk_dim, const int8_t* d_keys, const float* d_key_scales,
+                              const int8_t* d_values, const float* d_value_scales, int32_t slots, int32_t capacity,
+                              const int32_t* d_row_slot, const int32_t* d_row_first, const int32_t* d_row_count,
+                              int32_t max_chunks, void* d_workspace, size_t workspace_bytes, float* d_out,
+                              int8_t* d_q_out, float* d_qs_out, hipStream_t stream);
+
+namespace {
+
+constexpr int kLanes = 4;
+constexpr int kEngramHistory = 9;
+constexpr int kEngramTaps = 4;
+constexpr int kThreads = 256;
+constexpr int kMaxStream = 4096;  // 4 * dim floats staged in LDS (dim <= 1024)
+
+__device__ __forceinline__ float sigmoid_poly(float x) { return 1.0f / (1.0f + exp_poly(-x)); }
+
+__device__ __forceinline__ float clamp_q(float v)
+{
+    return fminf(fmaxf(ref_round_even(v), -128.0f), 127.0f);
+}
+
+// Scalar.SumOfSquares over n floats of LDS (one lane, ascending), then
+// Ops.InverseRms: 1 / sqrt(sum / n + 1e-6).
+__device__ __forceinline__ float inverse_rms_lane(const float* x, int n)
+{
+    float sum = 0.0f;
+    for (int i = 0; i < n; i++) sum = sum + x[i] * x[i];
+    return 1.0f / sqrtf(sum / (float)n + 1e-6f);
+}
+
+// Maximum of |v| over the block (order-free).
+__device__ __forceinline__ float block_peak(float v, float* red)
+{
+    v = wave_max(v);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+    __syncthreads();
+    float m = red[0];
+    for (int w = 1; w < (int)(blockDim.x >> 6); w++) m = fmaxf(m, red[w]);
+    __syncthreads();
+    return m;
+}
+
+// ---------------------------------------------------------- gathers --
+
+struct Book {
+    float levels[16];
+};
+
+// Scalar.DecodeRow of one 128-group into LDS g[128] (thread i < 128 takes
+// element i), then Scalar.Hadamard's butterflies (strides 1..64, each an
+// exact pair a + b, a - b) and the scale.
+__device__ __forceinline__ void gather_group(const uint8_t* raw, int rows, int cols, int bits, const Book& book, int row,
+                                             int group, float* g)
+{
+    const int i = threadIdx.x;
+    if (i < 128) {
+        const int groups = cols / 128;
+        const uint8_t* idx = raw + (size_t)row * cols * bits / 8;
+        const uint16_t* norms = reinterpret_cast<const uint16_t*>(raw + (size_t)rows * cols * bits / 8);
+        const float norm = ref_half_to_single(norms[(size_t)row * groups + group]);
+        const int code = bits == 2 ? (idx[group * 32 + i / 4] >> (i % 4 * 2)) & 3 : (idx[group * 64 + i / 2] >> (i % 2 * 4)) & 15;
+        g[i] = book.levels[code] * norm;
+    }
+    __syncthreads();
+    for (int stride = 1; stride < 128; stride <<= 1) {
+        if (i < 64) {
+            const int block = (i / stride) * stride * 2, k = block + i % stride;
+            const float a = g[k], b = g[k + stride];
+            g[k] = a + b;
+            g[k + stride] = a - b;
+        }
+        __syncthreads();
+    }
+    if (i < 128) g[i] = g[i] * 0.08838834764831845f;
+    __syncthreads();
+}
+
+// Embedding (ForwardBatch, Engine.cs:2310-2316): GatherRow of the token's
+// row, x += (sqrt(dim) - 1) * x, copied to the four lanes of the stream.
+__global__ __launch_bounds__(128) void n3_embed_kernel(const uint8_t* raw, int rows, int dim, int bits, Book book,
+                                                       const int32_t* tokens, float scale_m1, float* stream)
+{
+    __shared__ float g[128];
+    const int t = blockIdx.x;
+    const int token = tokens[t];
+    float* row = stream + (size_t)t * kLanes * dim;
+    for (int grp = 0; grp < dim / 128; grp++) {
+        gather_group(raw, rows, dim, bits, book, token, grp, g);
+        const float v = g[threadIdx.x];
+        const float x = v + scale_m1 * v;
+        for (int lane = 0; lane < kLanes; lane++) row[lane * dim + grp * 128 + threadIdx.x] = x;
+        __syncthreads();
+    }
+}
+
+// The engram input of ApplyEngramBatch (Engine.cs:2404-2414): every table's
+// GatherRow (zeros for row -1), then Quant.FakeA8 of the row.
+__global__ __launch_bounds__(128) void n3_engram_gather_kernel(const uint8_t* raw, int rows, int sub, int bits, Book book,
+                                                               const int32_t* erows, int tables, int dim, float* out)
+{
+    __shared__ float g[128];
+    __shared__ float red[4];
+    const int t = blockIdx.x;
+    float* row = out + (size_t)t * dim;
+    for (int table = 0; table < tables; table++) {
+        const int r = erows[t * tables + table];
+        for (int grp = 0; grp < sub / 128; grp++) {
+            if (r < 0) {
+                row[table * sub + grp * 128 + threadIdx.x] = 0.0f;
+                continue;
+            }
+            gather_group(raw, rows, sub, bits, book, r, grp, g);
+            row[table * sub + grp * 128 + threadIdx.x] = g[threadIdx.x];
+            __syncthreads();
+        }
+    }
+    __syncthreads();
+    float peak = 0.0f;
+    for (int i = threadIdx.x; i < dim; i += 128) peak = fmaxf(peak, fabsf(row[i]));
+    peak = block_peak(peak, red);
+    const float scale = peak > 0.0f ? peak / 127.0f : 1.0f;
+    const float inverse = 1.0f / scale;
+    for (int i = threadIdx.x; i < dim; i += 128) row[i] = clamp_q(row[i] * inverse) * scale;
+}
+
+// ---------------------------------------------------- normalisations --
+
+enum NormMode { kRmsFake = 0, kCenteredFake = 1, kHeadFake = 2 };
+
+// kRmsFake      Scalar.RmsFakeA8 of x[row] (n floats);
+// kCenteredFake Scalar.CenteredRmsFakeA8 of x[row] with scale s;
+// kHeadFake     PrepareHeadVectors: Mix4 of the row's four lanes by 0.25,
+//               ZeroCenteredRms with s, Quant.FakeA8 (the same operations
+//               as CenteredRmsFakeA8 of the mix).
+// Row b reads row map[b] (row b without a map) and writes row b of out.
+template <int MODE>
+__global__ __launch_bounds__(kThreads) void n3_norm_fake_kernel(const float* x, int n, const float* s,
+                                                                const int32_t* map, float* out)
+{
+    __shared__ float v[kMaxStream];
+    __shared__ float red[8];
+    __shared__ float inv_s;
+    const int b = blockIdx.x;
+    const int src = map ? map[b] : b;
+    if (MODE == kHeadFake) {
+        const float* r = x + (size_t)src * kLanes * n;
+        for (int c = threadIdx.x; c < n; c += kThreads)
+            v[c] = 0.25f * r[c] + 0.25f * r[n + c] + 0.25f * r[2 * n + c] + 0.25f * r[3 * n + c];
+    } else {
+        const float* r = x + (size_t)src * n;
+        for (int c = threadIdx.x; c < n; c += kThreads) v[c] = r[c];
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) inv_s = inverse_rms_lane(v, n);
+    __syncthreads();
+    const float inverse = inv_s;
+    float peak = 0.0f;
+    for (int c = threadIdx.x; c < n; c += kThreads) {
+        const float d = MODE == kRmsFake ? v[c] * inverse : (1.0f + s[c]) * v[c] * inverse;
+        v[c] = d;
+        peak = fmaxf(peak, fabsf(d));
+    }
+    peak = block_peak(peak, red);
+    const float scale = peak > 0.0f ? peak / 127.0f : 1.0f;
+    const float round = 1.0f / scale;
+    float* o = out + (size_t)b * n;
+    for (int c = threadIdx.x; c < n; c += kThreads) o[c] = clamp_q(v[c] * round) * scale;
+}
+
+// ----------------------------------------------- hyper-connection mix --
+
+struct HyperArgs {
+    const float* stream;
+    const float* pre_out;   // row t at t * ld4 (the layer's 4 outputs)
+    const float* post_out;  // row t at t * ld4
+    const float* res_out;   // row t at t * ld16 (the layer's 16 outputs)
+    int ld4, ld16;
+    const float *a_pre, *a_post, *a_res, *b_pre, *b_post, *b_res;  // the layer's entries
+    int lane, dim;
+    float* input;
+    float* residual;
+    float* post_gate;  // [rows][4]
+    float* mix;        // [rows][16]
+};
+
+// RunLayerBatch's per-row mix (Engine.cs:2366-2381): hpre / postGate by
+// Sigmoid, Mix4 of the lanes into input and residual, Sinkhorn4x4 of the
+// residual-mix logits.
+__global__ __launch_bounds__(kThreads) void n3_hyper_kernel(HyperArgs a)
+{
+    __shared__ float hpre[4];
+    const int t = blockIdx.x;
+    const int i = threadIdx.x;
+    if (i < 4) {
+        hpre[i] = sigmoid_poly(a.a_pre[0] * a.pre_out[t * a.ld4 + i] + a.b_pre[i] + (i == a.lane ? 4.0f : -4.0f));
+        a.post_gate[t * 4 + i] =
+            2.0f * sigmoid_poly(a.a_post[0] * a.post_out[t * a.ld4 + i] + a.b_post[i] + (i == a.lane ? 0.0f : -4.0f));
+    }
+    if (i == 64) {  // Scalar.Sinkhorn4x4
+        float lg[16], r[16];
+        for (int k = 0; k < 16; k++) lg[k] = a.a_res[0] * a.res_out[t * a.ld16 + k] + a.b_res[k];
+        for (int row = 0; row < 4; row++) {
+            const float peak = fmaxf(fmaxf(lg[row * 4], lg[row * 4 + 1]), fmaxf(lg[row * 4 + 2], lg[row * 4 + 3]));
+            for (int c = 0; c < 4; c++) r[row * 4 + c] = exp_poly(lg[row * 4 + c] - peak);
+        }
+        for (int it = 0; it < 20; it++) {
+            for (int row = 0; row < 4; row++) {
+                const float sum = r[row * 4] + r[row * 4 + 1] + r[row * 4 + 2] + r[row * 4 + 3];
+                for (int c = 0; c < 4; c++) r[row * 4 + c] = r[row * 4 + c] / sum;
+            }
+            for (int c = 0; c < 4; c++) {
+                const float sum = r[c] + r[4 + c] + r[8 + c] + r[12 + c];
+                if (sum > 0.0f)
+                    for (int row = 0; row < 4; row++) r[row * 4 + c] = r[row * 4 + c] / sum;
+            }
+        }
+        for (int k = 0; k < 16; k++) a.mix[t * 16 + k] = r[k];
+    }
+    __syncthreads();
+    const int dim = a.dim;
+    const float* s = a.stream + (size_t)t * kLanes * dim;
+    for (int c = i; c < dim; c += kThreads) {
+        const float u = hpre[0] * s[c] + hpre[1] * s[dim + c] + hpre[2] * s[2 * dim + c] + hpre[3] * s[3 * dim + c];
+        a.input[(size_t)t * dim + c] = u;
+        a.residual[(size_t)t * dim + c] = u;
+    }
+}
+
+// ----------------------------------------------------------- engram --
+
+struct EngramArgs {
+    const float* stage;        // [rows][10][dim]: row 9 the new value projection
+    float* history;            // [slots][9][dim] of this site
+    const int32_t* row_slot;
+    const int32_t* run_start;  // first row of each row's run
+    const float* taps;         // [4][dim]
+    int dilation, dim;
+    const float* input;
+    const float* key;
+    float* residual;
+    float inverse_root;        // 1 / sqrt(dim)
+};
+
+// Row t's convolution input j (0..9): the slot's history followed by the
+// value rows of its run (Engine.cs:2430-2437): sequence index (t - rs) + j.
+__device__ __forceinline__ const float* engram_frame(const EngramArgs& a, int t, int j)
+{
+    const int rs = a.run_start[t];
+    const int idx = (t - rs) + j;
+    if (j == kEngramHistory) return a.stage + ((size_t)t * (kEngramHistory + 1) + kEngramHistory) * a.dim;
+    if (idx < kEngramHistory) return a.history + ((size_t)a.row_slot[t] * kEngramHistory + idx) * a.dim;
+    return a.stage + ((size_t)(rs + idx - kEngramHistory) * (kEngramHistory + 1) + kEngramHistory) * a.dim;
+}
+
+// The engram's convolution, RmsUnit of the input and the key, their Dot,
+// alpha = Sigmoid(dot / sqrt(dim)) and residual += alpha * conv
+// (Engine.cs:2437-2462).
+__global__ __launch_bounds__(kThreads) void n3_engram_mix_kernel(EngramArgs a)
+{
+    __shared__ float ua[1024];
+    __shared__ float ub[1024];
+    __shared__ float cv[1024];
+    __shared__ float alpha_s;
+    const int t = blockIdx.x;
+    const int dim = a.dim;
+    const float* f[kEngramTaps];
+    for (int j = 0; j < kEngramTaps; j++) f[j] = engram_frame(a, t, kEngramHistory - j * a.dilation);
+    for (int c = threadIdx.x; c < dim; c += kThreads) {
+        float o = 0.0f;
+        for (int j = 0; j < kEngramTaps; j++) o = o + a.taps[(size_t)j * dim + c] * f[j][c];
+        cv[c] = o;
+        ua[c] = a.input[(size_t)t * dim + c];
+        ub[c] = a.key[(size_t)t * dim + c];
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const float ia = inverse_rms_lane(ua, dim);
+        const float ib = inverse_rms_lane(ub, dim);
+        float dot = 0.0f;
+        for (int c = 0; c < dim; c++) dot = dot + (ua[c] * ia) * (ub[c] * ib);
+        alpha_s = sigmoid_poly(dot * a.inverse_root);
+    }
+    __syncthreads();
+    const float alpha = alpha_s;
+    for (int c = threadIdx.x; c < dim; c += kThreads) {
+        float* r = a.residual + (size_t)t * dim + c;
+        *r = *r + alpha * cv[c];
+    }
+}
+
+// The slot's engram history after its run (Engine.cs:2439): the nine frames
+// before the sequence's end.  Launched after the mix (which reads the old
+// history); a block per run end, each thread owns whole columns.
+__global__ __launch_bounds__(kThreads) void n3_engram_history_kernel(EngramArgs a, const int32_t* run_end)
+{
+    const int t = blockIdx.x;
+    if (!run_end[t]) return;
+    const int n = t - a.run_start[t] + 1;  // the run's length
+    float* hist = a.history + (size_t)a.row_slot[t] * kEngramHistory * a.dim;
+    for (int c = threadIdx.x; c < a.dim; c += kThreads) {
+        float v[kEngramHistory];
+        for (int j = 0; j < kEngramHistory; j++) {
+            const int idx = n + j;  // sequence index of the new frame j
+            v[j] = idx < kEngramHistory
+                       ? hist[(size_t)idx * a.dim + c]
+                       : a.stage[((size_t)(a.run_start[t] + idx - kEngramHistory) * (kEngramHistory + 1) + kEngramHistory) * a.dim + c];
+        }
+        for (int j = 0; j < kEngramHistory; j++) hist[(size_t)j * a.dim + c] = v[j];
+    }
+}
+
+// ------------------------------------------------- attention epilogue --
+
+// Scalar.GateFakeA8 on each row of x (in place): x *= Sigmoid(gate), then
+// the fake int8 round trip at the row's peak.
+__global__ __launch_bounds__(kThreads) void n3_gate_fake_kernel(float* x, const float* gate, int n)
+{
+    __shared__ float red[8];
+    const int t = blockIdx.x;
+    float* r = x + (size_t)t * n;
+    const float* g = gate + (size_t)t * n;
+    float peak = 0.0f;
+    for (int c = threadIdx.x; c < n; c += kThreads) {
+        const float v = r[c] * sigmoid_poly(g[c]);
+        r[c] = v;
+        peak = fmaxf(peak, fabsf(v));
+    }
+    peak = block_peak(peak, red);
+    const float scale = peak > 0.0f ? peak / 127.0f : 1.0f;
+    const float round = 1.0f / scale;
+    for (int c = threadIdx.x; c < n; c += kThreads) r[c] = clamp_q(r[c] * round) * scale;
+}
+
+// Scalar.PostNormAdd: residual += gate * ((1 + s) * x * (1 / rms(x))).
+__global__ __launch_bounds__(kThreads) void n3_post_norm_add_kernel(float* residual, const float* x, const float* s,
+                                                                    float gate, int n)
+{
+    __shared__ float v[1024];
+    __shared__ float inv_s;
+    const int t = blockIdx.x;
+    for (int c = threadIdx.x; c < n; c += kThreads) v[c] = x[(size_t)t * n + c];
+    __syncthreads();
+    if (threadIdx.x == 0) inv_s = inverse_rms_lane(v, n);
+    __syncthreads();
+    const float inverse = inv_s;
+    for (int c = threadIdx.x; c < n; c += kThreads) {
+        float* r = residual + (size_t)t * n + c;
+        *r = *r + gate * ((1.0f + s[c]) * v[c] * inverse);
+    }
+}
+
+// -------------------------------------------------------------- MLP --
+
+struct MlpArgs {
+    float* residual;
+    const float* pre_norm;
+    const int32_t *perm_a, *perm_b;
+    const float *d1, *d2, *b2, *d3, *d4, *w1a, *w1b, *w2a, *w2b, *w3a, *w3b, *cond_v, *cond_u;
+    int dim, rows, cols;
+};
+
+// Scalar.Kron in LDS: scratch[k][c] = sum_{i < active} left[i][k] z[i][c]
+// (a chain over i per (k, c)), then result[k][c] = sum_j scratch[k][j]
+// right[j][c] (a chain over j), for k < result_rows.
+__device__ __forceinline__ void kron_lds(const float* z, int active, const float* left, const float* right, int rows,
+                                         int cols, int result_rows, float* scratch, float* result)
+{
+    for (int e = threadIdx.x; e < result_rows * cols; e += kThreads) {
+        const int k = e / cols, c = e % cols;
+        float sum = 0.0f;
+        for (int i = 0; i < active; i++) sum = sum + left[i * rows + k] * z[i * cols + c];
+        scratch[e] = sum;
+    }
+    __syncthreads();
+    for (int e = threadIdx.x; e < result_rows * cols; e += kThreads) {
+        const int k = e / cols, c = e % cols;
+        float sum = 0.0f;
+        for (int j = 0; j < cols; j++) sum = sum + scratch[k * cols + j] * right[j * cols + c];
+        result[e] = sum;
+    }
+    __syncthreads();
+}
+
+// HadamardMlp.Apply (Blocks.cs:1067-1101) with its scalar kernels, Scale 1,
+// one row per workgroup; front, back and the Kron scratch live in LDS.
+__global__ __launch_bounds__(kThreads) void n3_mlp_kernel(MlpArgs a)
+{
+    extern __shared__ float lds[];
+    const int width = a.rows * a.cols, dim = a.dim;
+    float* front = lds;             // width (>= the padded input)
+    float* back = front + width;    // width
+    float* scratch = back + width;  // width
+    float* norm = scratch + width;  // dim
+    __shared__ float weights[8];
+    __shared__ float inv_s;
+    const int t = blockIdx.x;
+    float* res = a.residual + (size_t)t * dim;
+    const int input_rows = (dim + a.cols - 1) / a.cols;
+    const int output_rows = min(a.rows, (input_rows + 3) / 4 * 4);
+    for (int c = threadIdx.x; c < dim; c += kThreads) norm[c] = res[c];
+    __syncthreads();
+    if (threadIdx.x == 0) inv_s = inverse_rms_lane(norm, dim);
+    __syncthreads();
+    for (int c = threadIdx.x; c < dim; c += kThreads) norm[c] = (1.0f + a.pre_norm[c]) * norm[c] * inv_s;
+    __syncthreads();
+    if (threadIdx.x < 8) {  // Scalar.ConditionWeights: eight chains over dim
+        const int j = threadIdx.x;
+        float sum = 0.0f;
+        for (int i = 0; i < dim; i++) sum = sum + norm[i] * a.cond_v[i * 8 + j];
+        weights[j] = sum;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {  // Scalar.Softmax over the eight weights
+        float peak = -INFINITY;
+        for (int j = 0; j < 8; j++) peak = fmaxf(peak, weights[j]);
+        float total = 0.0f;
+        for (int j = 0; j < 8; j++) {
+            weights[j] = exp_poly(weights[j] - peak);
+            total = total + weights[j];
+        }
+        for (int j = 0; j < 8; j++) weights[j] = weights[j] / total;
+    }
+    for (int c = threadIdx.x; c < input_rows * a.cols; c += kThreads) front[c] = c < dim ? norm[c] * a.d1[c] : 0.0f;
+    __syncthreads();
+    kron_lds(front, input_rows, a.w1a, a.w1b, a.rows, a.cols, a.rows, scratch, back);
+    for (int n = threadIdx.x; n < width; n += kThreads) {  // Scalar.PermuteModulateActivate
+        float condition = 1.0f;
+        for (int j = 0; j < 8; j++) condition = condition + weights[j] * a.cond_u[j * width + n];
+        const float v = a.d2[n] * condition * back[a.perm_a[n]] + a.b2[n];
+        front[n] = v * sigmoid_poly(v);
+    }
+    __syncthreads();
+    kron_lds(front, a.rows, a.w2a, a.w2b, a.rows, a.cols, a.rows, scratch, back);
+    for (int n = threadIdx.x; n < width; n += kThreads) front[n] = back[a.perm_b[n]] * a.d3[n];
+    __syncthreads();
+    kron_lds(front, a.rows, a.w3a, a.w3b, a.rows, a.cols, output_rows, scratch, back);
+    for (int c = threadIdx.x; c < dim; c += kThreads) res[c] = res[c] + 1.0f * (back[c] * a.d4[c]);
+}
+
+// Ops.CombineDiff4x4's scalar branch (Ops.cs:800-812): lane i of the next
+// stream = postGate[i] * (x - u) + sum_j mix[i][j] * s_j, left to right.
+__global__ __launch_bounds__(kThreads) void n3_combine_kernel(const float* stream, const float* mix, const float* x,
+                                                              const float* u, const float* post_gate, int dim,
+                                                              float* next)
+{
+    const int t = blockIdx.x;
+    const float* s = stream + (size_t)t * kLanes * dim;
+    const float* m = mix + t * 16;
+    const float* xr = x + (size_t)t * dim;
+    const float* ur = u + (size_t)t * dim;
+    float* o = next + (size_t)t * kLanes * dim;
+    for (int e = threadIdx.x; e < kLanes * dim; e += kThreads) {
+        const int i = e / dim, c = e % dim;
+        const float* w = m + 4 * i;
+        o[e] = post_gate[t * 4 + i] * (xr[c] - ur[c]) + w[0] * s[c] + w[1] * s[dim + c] + w[2] * s[2 * dim + c] +
+               w[3] * s[3 * dim + c];
+    }
+}
+
+}  // namespace
+}  // namespace nhip
+
+using namespace nhip;
+
+// ------------------------------------------------------------- model --
+
+namespace {
+
+struct N3Layer {
+    const float *norm_in = nullptr, *q_taps = nullptr, *k_taps = nullptr, *v_taps = nullptr, *q_norm = nullptr,
+                *k_norm = nullptr, *post_norm = nullptr, *pre_hada = nullptr;
+    nhip_weights *q = nullptr, *k = nullptr, *v = nullptr, *gate = nullptr, *out = nullptr;
+    float attn_gate = 0.0f;
+    const float *d1 = nullptr, *d2 = nullptr, *b2 = nullptr, *d3 = nullptr, *d4 = nullptr, *w1a = nullptr,
+                *w1b = nullptr, *w2a = nullptr, *w2b = nullptr, *w3a = nullptr, *w3b = nullptr, *cond_v = nullptr,
+                *cond_u = nullptr;
+};
+
+struct N3Site {
+    const uint8_t* tables = nullptr;
+    int table_rows = 0, table_cols = 0, table_bits = 0;
+    nhip_weights *key = nullptr, *value = nullptr;
+    const float* taps = nullptr;
+};
+
+}  // namespace
+
+struct nhip_ctx {
+    const nhip_model* model = nullptr;
+    // geometry (Model.cs:65-121)
+    int vocab = 0, dim = 0, heads = 0, kv = 0, layers = 0, qk = 0, vd = 0, hada_rows = 0, hada_cols = 0, window = 0;
+    int engram_slots = 0, engram_sub = 0, engram_tables = 0, dilation = 0, order_count = 0, orders[4] = {};
+    int site_count = 0, sites[16] = {};
+    uint64_t global_mask = 0;
+    int slots = 0, capacity = 0, max_rows = 0, max_chunks = 0;
+    // weights
+    nhip_weights* embedding = nullptr;
+    const uint8_t* embedding_raw = nullptr;
+    int embedding_bits = 4;
+    Book book2{}, book4{};
+    std::vector<N3Layer> layer;
+    const float *a_pre = nullptr, *a_post = nullptr, *a_res = nullptr, *b_pre = nullptr, *b_post = nullptr,
+                *b_res = nullptr;
+    nhip_weights *phi_pre = nullptr, *phi_post = nullptr, *phi_res = nullptr;
+    int32_t *perm_a = nullptr, *perm_b = nullptr;
+    std::vector<N3Site> site;
+    const float* final_norm = nullptr;
+    // per-slot state
+    int8_t *keys = nullptr, *values = nullptr;
+    float *key_scales = nullptr, *value_scales = nullptr;
+    float *qkv_hist = nullptr, *engram_hist = nullptr, *snap_qkv = nullptr, *snap_engram = nullptr;
+    std::vector<int32_t> len, marked, prev, snap_prev;
+    float *rope_cos = nullptr, *rope_sin = nullptr;
+    // scratch for max_rows rows
+    float *stream = nullptr, *next = nullptr, *normed = nullptr, *input = nullptr, *residual = nullptr,
+          *raw = nullptr, *gate = nullptr, *att = nullptr, *proj = nullptr, *key = nullptr, *stage = nullptr,
+          *ein = nullptr, *pre_out = nullptr, *post_out = nullptr, *res_out = nullptr, *post_gate = nullptr,
+          *mix = nullptr, *qs = nullptr, *logits = nullptr, *act_s = nullptr, *act_o = nullptr;
+    int8_t *act_v = nullptr, *q8 = nullptr;
+    int32_t* d_in = nullptr;  // the per-row inputs of a step, kInSections x max_rows, then the engram rows
+    int32_t* h_in = nullptr;  // their pinned host staging
+    void* attn_ws = nullptr;
+    size_t attn_ws_bytes = 0;
+    void* topk_ws = nullptr;
+    size_t topk_ws_bytes = 0;
+    int32_t *d_topk_idx = nullptr, *d_argmax = nullptr;
+    float* d_topk_lp = nullptr;
+    size_t mlp_lds = 0;
+    hipStream_t stream_h = nullptr;
+    std::vector<void*> allocations;
+};
+
+namespace {
+
+// per-row step inputs: token, slot, position, attention span of the global
+// layers (first, count) and of the sliding-window layers, head rows, the
+// first row of the row's run, whether the row ends its run
+enum { kInTokens, kInSlots, kInPos, kInFirst, kInCount, kInFirstW, kInCountW, kInHeads, kInRunStart, kInRunEnd, kInSections };
+
+int32_t* in(nhip_ctx* c, int32_t* base, int section) { return base + (size_t)section * c->max_rows; }
+int32_t* in_erows(nhip_ctx* c, int32_t* base) { return base + (size_t)kInSections * c->max_rows; }
+
+template <typename T>
+int32_t ctx_alloc(nhip_ctx* c, T** p, size_t count)
+{
+    void* v = nullptr;
+    NHIP_CHECK_HIP(hipMalloc(&v, std::max<size_t>(count * sizeof(T), 256)));
+    NHIP_CHECK_HIP(hipMemset(v, 0, std::max<size_t>(count * sizeof(T), 256)));
+    c->allocations.push_back(v);
+    *p = static_cast<T*>(v);
+    return NHIP_OK;
+}
+
+// Model.Open's reader over the archive's records, in order (Model.cs:307-371).
+struct RecordCursor {
+    const nhip_model* m;
+    int next = 0, count = 0;
+    int32_t status = NHIP_OK;
+    nhip_record_info info(int i)
+    {
+        nhip_record_info r{};
+        nhip_model_record(m, i, &r);
+        return r;
+    }
+    int take(int dtype_a, int dtype_b, const char* what)
+    {
+        if (status) return -1;
+        if (next >= count) {
+            set_error("archive ends before its %s", what);
+            status = NHIP_ERR_FORMAT;
+            return -1;
+        }
+        const nhip_record_info r = info(next);
+        if (r.dtype != dtype_a && r.dtype != dtype_b) {
+            set_error("record %d: %s expected (dtype %d)", next, what, r.dtype);
+            status = NHIP_ERR_FORMAT;
+            return -1;
+        }
+        return next++;
+    }
+    nhip_weights* quant(int bits, int rows, int cols, const char* what)
+    {
+        const int i = take(NHIP_CACT_CQ, NHIP_CACT_CQ, what);
+        if (i < 0) return nullptr;
+        const nhip_record_info r = info(i);
+        if ((bits && (int)r.bits != bits) || (rows && (int)r.shape[0] != rows) || (cols && (int)r.shape[1] != cols)) {
+            set_error("record %d (%s): %ux%u %u-bit, expected %dx%d %d-bit", i, what, r.shape[0], r.shape[1], r.bits, rows,
+                      cols, bits);
+            status = NHIP_ERR_FORMAT;
+            return nullptr;
+        }
+        return nhip_model_weights(m, i);
+    }
+    const float* dense(size_t elements, const char* what)
+    {
+        const int i = take(NHIP_CACT_FP16, NHIP_CACT_FP32, what);
+        if (i < 0) return nullptr;
+        const nhip_record_info r = info(i);
+        size_t n = 1;
+        for (int d = 0; d < r.ndim; d++) n *= r.shape[d];
+        if (elements && n != elements) {
+            set_error("record %d (%s): %zu elements, expected %zu", i, what, n, elements);
+            status = NHIP_ERR_FORMAT;
+            return nullptr;
+        }
+        return nhip_model_dense(m, i);
+    }
+};
+
+int32_t load_model(nhip_ctx* c)
+{
+    uint32_t h[48];
+    float theta = 0.0f;
+    int32_t records = 0;
+    int32_t rc = nhip_model_info(c->model, h, &theta, &records);
+    if (rc) return rc;
+    c->vocab = (int)h[5];
+    c->dim = (int)h[7];
+    c->heads = (int)h[8];
+    c->kv = (int)h[9];
+    c->layers = (int)h[10];
+    c->qk = (int)h[11];
+    c->vd = (int)h[12];
+    const int hada_n = (int)h[14];
+    int bl = 0;
+    for (uint32_t v = (uint32_t)(hada_n - 1); v; v >>= 1) bl++;
+    c->hada_rows = hada_n > 0 ? 1 << (bl / 2) : 0;
+    c->hada_cols = c->hada_rows ? hada_n / c->hada_rows : 0;
+    c->window = (int)h[16];
+    c->global_mask = (uint64_t)h[17] | ((uint64_t)h[18] << 32);
+    c->engram_slots = (int)h[20];
+    c->engram_sub = (int)h[21];
+    c->engram_tables = (int)h[22];
+    c->dilation = (int)h[24];
+    c->order_count = (int)h[26];
+    for (int i = 0; i < 4; i++) c->orders[i] = (int)h[27 + i];
+    c->site_count = (int)h[31];
+    for (int i = 0; i < 16; i++) c->sites[i] = (int)h[32 + i];
+    // Model.Open's geometry requirements (Model.cs:326-331), plus this
+    // engine's limits
+    NHIP_REQUIRE(c->qk == 48 && c->vd == 64 && h[15] == 4, "head geometry qk %d v %d lanes %u; needs 48 / 64 / 4", c->qk,
+                 c->vd, h[15]);
+    NHIP_REQUIRE(h[19] == 3 && (c->site_count == 0 || h[23] == 4) && c->dim % 128 == 0 && c->dim <= 1024,
+                 "conv taps %u, engram taps %u, dim %d (a multiple of 128 up to 1024)", h[19], h[23], c->dim);
+    NHIP_REQUIRE(c->hada_cols % 8 == 0 && c->hada_rows * c->hada_cols == hada_n && hada_n >= c->dim,
+                 "MLP size %d must split into rows x cols (cols divisible by 8) covering dim %d", hada_n, c->dim);
+    NHIP_REQUIRE(c->heads > 0 && c->kv > 0 && c->heads % c->kv == 0 && c->heads * c->vd <= 1024, "heads %d / kv %d",
+                 c->heads, c->kv);
+    NHIP_REQUIRE(c->site_count >= 0 && c->site_count <= 16 && c->order_count >= 0 && c->order_count <= 4,
+                 "engram sites %d, orders %d", c->site_count, c->order_count);
+    NHIP_REQUIRE(c->site_count == 0 || (c->engram_tables % std::max(c->order_count, 1) == 0 &&
+                                       c->engram_tables * c->engram_sub == c->dim && c->engram_sub % 128 == 0 &&
+                                       c->engram_slots > 0 && c->dilation >= 1 && 3 * c->dilation <= kEngramHistory),
+                 "engram geometry: %d tables x %d columns, %d slots, dilation %d", c->engram_tables, c->engram_sub,
+                 c->engram_slots, c->dilation);
+    nhip_codebook b2, b4;
+    nhip_model_codebooks(c->model, &b2, &b4);
+    std::memcpy(c->book2.levels, b2.levels, sizeof(b2.levels));
+    std::memcpy(c->book4.levels, b4.levels, sizeof(b4.levels));
+    const int d = c->dim, qw = c->heads * c->qk, kw = c->kv * c->qk, vw = c->kv * c->vd, ow = c->heads * c->vd;
+    const size_t width = (size_t)c->hada_rows * c->hada_cols;
+    RecordCursor r{c->model, 0, records};
+    {
+        const int i = r.take(NHIP_CACT_CQ, NHIP_CACT_CQ, "embedding");
+        if (i >= 0) {
+            nhip_record_info ri = r.info(i);
+            NHIP_REQUIRE(ri.bits == 4 && (int)ri.shape[1] == d && (int)ri.shape[0] == c->vocab,
+                         "embedding %ux%u %u-bit, expected %dx%d 4-bit", ri.shape[0], ri.shape[1], ri.bits, c->vocab, d);
+            c->embedding = nhip_model_weights(c->model, i);
+            c->embedding_raw = nhip_model_raw(c->model, i);
+        }
+    }
+    c->layer.resize(c->layers);
+    for (int l = 0; l < c->layers && !r.status; l++) {
+        N3Layer& w = c->layer[l];
+        w.norm_in = r.dense(d, "NormIn");
+        w.q = r.quant(2, qw, d, "Q");
+        w.k = r.quant(2, kw, d, "K");
+        w.v = r.quant(2, vw, d, "V");
+        w.q_taps = r.dense((size_t)3 * qw, "QTaps");
+        w.k_taps = r.dense((size_t)3 * kw, "KTaps");
+        w.v_taps = r.dense((size_t)3 * vw, "VTaps");
+        w.q_norm = r.dense(c->qk, "QNorm");
+        w.k_norm = r.dense(c->qk, "KNorm");
+        w.gate = r.quant(2, ow, d, "Gate");
+        w.out = r.quant(2, d, ow, "Out");
+        w.post_norm = r.dense(d, "PostNorm");
+        const float* g = r.dense(1, "AttnGate");
+        if (g) {  // LayerWeights: AttnGate = 1 / (1 + MathF.Exp(-x)), once, with the host libm
+            float x = 0.0f;
+            NHIP_CHECK_HIP(hipMemcpy(&x, g, sizeof(float), hipMemcpyDeviceToHost));
+            w.attn_gate = 1.0f / (1.0f + std::exp(-x));
+        }
+        w.pre_hada = r.dense(d, "PreHada");
+        w.d1 = r.dense(d, "D1");
+        w.d2 = r.dense(width, "D2");
+        w.b2 = r.dense(width, "B2");
+        w.d3 = r.dense(width, "D3");
+        w.d4 = r.dense(d, "D4");
+        w.w1a = r.dense((size_t)c->hada_rows * c->hada_rows, "W1A");
+        w.w1b = r.dense((size_t)c->hada_cols * c->hada_cols, "W1B");
+        w.w2a = r.dense((size_t)c->hada_rows * c->hada_rows, "W2A");
+        w.w2b = r.dense((size_t)c->hada_cols * c->hada_cols, "W2B");
+        w.w3a = r.dense((size_t)c->hada_rows * c->hada_rows, "W3A");
+        w.w3b = r.dense((size_t)c->hada_cols * c->hada_cols, "W3B");
+        w.cond_v = r.dense((size_t)d * 8, "CondV");
+        w.cond_u = r.dense(8 * width, "CondU");
+    }
+    c->a_pre = r.dense(c->layers, "APre");
+    c->a_post = r.dense(c->layers, "APost");
+    c->a_res = r.dense(c->layers, "ARes");
+    c->b_pre = r.dense((size_t)c->layers * 4, "BPre");
+    c->b_post = r.dense((size_t)c->layers * 4, "BPost");
+    c->b_res = r.dense((size_t)c->layers * 16, "BRes");
+    c->phi_pre = r.quant(4, c->layers * 4, 4 * d, "PhiPre");
+    c->phi_post = r.quant(4, c->layers * 4, 4 * d, "PhiPost");
+    c->phi_res = r.quant(4, c->layers * 16, 4 * d, "PhiRes");
+    const float* pa = r.dense(width, "PermA");
+    const float* pb = r.dense(width, "PermB");
+    c->site.resize(c->site_count);
+    for (int s = 0; s < c->site_count && !r.status; s++) {
+        N3Site& st = c->site[s];
+        const int i = r.take(NHIP_CACT_CQ, NHIP_CACT_CQ, "engram tables");
+        if (i >= 0) {
+            const nhip_record_info ri = r.info(i);
+            st.tables = nhip_model_raw(c->model, i);
+            st.table_rows = (int)ri.shape[0];
+            st.table_cols = (int)ri.shape[1];
+            st.table_bits = (int)ri.bits;
+            NHIP_REQUIRE(st.table_cols == c->engram_sub && st.table_rows >= c->engram_tables * c->engram_slots,
+                         "engram tables %ux%u for %d tables of %d slots x %d", ri.shape[0], ri.shape[1], c->engram_tables,
+                         c->engram_slots, c->engram_sub);
+        }
+        st.key = r.quant(2, d, d, "engram Key");
+        st.value = r.quant(2, d, d, "engram Value");
+        st.taps = r.dense((size_t)kEngramTaps * d, "engram Taps");
+    }
+    c->final_norm = r.dense(d, "FinalNorm");
+    if (r.status) return r.status;
+    int32_t rc2;
+    if ((rc2 = ctx_alloc(c, &c->perm_a, width)) || (rc2 = ctx_alloc(c, &c->perm_b, width))) return rc2;
+    // HyperConnections' permutations (stored as floats, Model.cs:168-169):
+    // every index must address the MLP's width
+    std::vector<float> pf(width);
+    std::vector<int32_t> pi(width);
+    for (int k = 0; k < 2; k++) {
+        NHIP_CHECK_HIP(hipMemcpy(pf.data(), k ? pb : pa, width * sizeof(float), hipMemcpyDeviceToHost));
+        for (size_t i = 0; i < width; i++) {
+            NHIP_REQUIRE(pf[i] >= 0.0f && pf[i] < (float)width && pf[i] == (float)(int32_t)pf[i],
+                         "permutation %c entry %zu (%g) outside [0, %zu)", k ? 'B' : 'A', i, (double)pf[i], width);
+            pi[i] = (int32_t)pf[i];
+        }
+        NHIP_CHECK_HIP(hipMemcpy(k ? c->perm_b : c->perm_a, pi.data(), width * sizeof(int32_t), hipMemcpyHostToDevice));
+    }
+    return NHIP_OK;
+}
+
+int32_t alloc_state(nhip_ctx* c)
+{
+    const int d = c->dim, R = c->max_rows, qw = c->heads * c->qk, kw = c->kv * c->qk, vw = c->kv * c->vd,
+              ow = c->heads * c->vd, all = qw + kw + vw, sw = kLanes * d;
+    const size_t cells = (size_t)c->layers * c->slots * c->capacity;
+    const size_t hist = (size_t)c->layers * c->slots * 2 * all;
+    const size_t ehist = (size_t)std::max(c->site_count, 1) * c->slots * kEngramHistory * d;
+    const int stride4 = (sw / 128 + 7) / 8 * 8;
+    int32_t rc;
+    if ((rc = ctx_alloc(c, &c->keys, cells * kw)) || (rc = ctx_alloc(c, &c->values, cells * vw)) ||
+        (rc = ctx_alloc(c, &c->key_scales, cells * c->kv)) || (rc = ctx_alloc(c, &c->value_scales, cells * c->kv)) ||
+        (rc = ctx_alloc(c, &c->qkv_hist, hist)) || (rc = ctx_alloc(c, &c->snap_qkv, hist)) ||
+        (rc = ctx_alloc(c, &c->engram_hist, ehist)) || (rc = ctx_alloc(c, &c->snap_engram, ehist)) ||
+        (rc = ctx_alloc(c, &c->rope_cos, (size_t)c->capacity * c->qk / 2)) ||
+        (rc = ctx_alloc(c, &c->rope_sin, (size_t)c->capacity * c->qk / 2)) ||
+        (rc = ctx_alloc(c, &c->stream, (size_t)R * sw)) || (rc = ctx_alloc(c, &c->next, (size_t)R * sw)) ||
+        (rc = ctx_alloc(c, &c->normed, (size_t)R * sw)) || (rc = ctx_alloc(c, &c->input, (size_t)R * d)) ||
+        (rc = ctx_alloc(c, &c->residual, (size_t)R * d)) || (rc = ctx_alloc(c, &c->raw, (size_t)R * all)) ||
+        (rc = ctx_alloc(c, &c->gate, (size_t)R * ow)) || (rc = ctx_alloc(c, &c->att, (size_t)R * ow)) ||
+        (rc = ctx_alloc(c, &c->proj, (size_t)R * d)) || (rc = ctx_alloc(c, &c->key, (size_t)R * d)) ||
+        (rc = ctx_alloc(c, &c->stage, (size_t)R * (kEngramHistory + 1) * d)) ||
+        (rc = ctx_alloc(c, &c->ein, (size_t)R * d)) || (rc = ctx_alloc(c, &c->pre_out, (size_t)R * 4 * c->layers)) ||
+        (rc = ctx_alloc(c, &c->post_out, (size_t)R * 4 * c->layers)) ||
+        (rc = ctx_alloc(c, &c->res_out, (size_t)R * 16 * c->layers)) ||
+        (rc = ctx_alloc(c, &c->post_gate, (size_t)R * 4)) || (rc = ctx_alloc(c, &c->mix, (size_t)R * 16)) ||
+        (rc = ctx_alloc(c, &c->q8, (size_t)R * qw)) || (rc = ctx_alloc(c, &c->qs, (size_t)R * c->heads)) ||
+        (rc = ctx_alloc(c, &c->logits, (size_t)R * c->vocab)) || (rc = ctx_alloc(c, &c->act_v, (size_t)R * sw)) ||
+        (rc = ctx_alloc(c, &c->d_topk_idx, (size_t)R * 8)) || (rc = ctx_alloc(c, &c->d_topk_lp, (size_t)R * 8)) ||
+        (rc = ctx_alloc(c, &c->d_argmax, (size_t)R)) ||
+        (rc = ctx_alloc(c, &c->act_s, (size_t)R * stride4)) || (rc = ctx_alloc(c, &c->act_o, (size_t)R * stride4)) ||
+        (rc = ctx_alloc(c, &c->d_in, (size_t)R * (kInSections + std::max(c->engram_tables, 1)))))
+        return rc;
+    NHIP_CHECK_HIP(hipHostMalloc(reinterpret_cast<void**>(&c->h_in),
+                                 sizeof(int32_t) * (size_t)R * (kInSections + std::max(c->engram_tables, 1)),
+                                 hipHostMallocDefault));
+    c->attn_ws_bytes = nhip_attention_decode_workspace(R, c->heads, c->max_chunks);
+    NHIP_CHECK_HIP(hipMalloc(&c->attn_ws, c->attn_ws_bytes));
+    c->allocations.push_back(c->attn_ws);
+    c->topk_ws_bytes = nhip_topk_lse_workspace(R, c->vocab);
+    NHIP_CHECK_HIP(hipMalloc(&c->topk_ws, c->topk_ws_bytes));
+    c->allocations.push_back(c->topk_ws);
+    // EngineCore.RopeFrequencies + BuildRopeTables (Engine.cs:336-356):
+    // float powf / cosf / sinf on the host, as MathF on Linux
+    const int half = c->qk / 2;
+    uint32_t hdr[48];
+    float theta = 0.0f;
+    nhip_model_info(c->model, hdr, &theta, nullptr);
+    std::vector<float> freq(half), cs((size_t)c->capacity * half), sn((size_t)c->capacity * half);
+    for (int i = 0; i < half; i++) freq[i] = 1.0f / std::pow(theta, 2.0f * (float)i / (float)c->qk);
+    for (int p = 0; p < c->capacity; p++)
+        for (int i = 0; i < half; i++) {
+            const float angle = (float)p * freq[i];
+            cs[(size_t)p * half + i] = std::cos(angle);
+            sn[(size_t)p * half + i] = std::sin(angle);
+        }
+    NHIP_CHECK_HIP(hipMemcpy(c->rope_cos, cs.data(), cs.size() * 4, hipMemcpyHostToDevice));
+    NHIP_CHECK_HIP(hipMemcpy(c->rope_sin, sn.data(), sn.size() * 4, hipMemcpyHostToDevice));
+    c->len.assign(c->slots, 0);
+    c->marked.assign(c->slots, 0);
+    c->prev.assign(2 * c->slots, 0);
+    c->snap_prev.assign(2 * c->slots, 0);
+    const size_t width = (size_t)c->hada_rows * c->hada_cols;
+    c->mlp_lds = (3 * width + d) * sizeof(float);
+    NHIP_REQUIRE(c->mlp_lds <= 160 * 1024, "the MLP's %zu bytes of LDS exceed the CU's", c->mlp_lds);
+    if (c->mlp_lds > 64 * 1024)
+        NHIP_CHECK_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(n3_mlp_kernel),
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)c->mlp_lds));
+    return NHIP_OK;
+}
+
+int32_t prepare(nhip_ctx* c, const float* x, int rows, int cols, int bits)
+{
+    const int stride = (cols / 128 + 7) / 8 * 8;
+    return nhip_prepare_dev(x, rows, cols, bits, c->act_v, c->act_s, c->act_o, stride, c->stream_h);
+}
+
+// Rows [row0, row0 + count) of w over the prepared activations of `rows`
+// rows: y[t * ldy + n] for those n.
+int32_t matmul(nhip_ctx* c, const nhip_weights* w, int rows, int cols, int row0, int count, float* y, int ldy)
+{
+    const int stride = (cols / 128 + 7) / 8 * 8;
+    return nhip_matmul_cq_dev(w, c->act_v, c->act_s, c->act_o, stride, rows, y, ldy, row0, row0 + count, c->stream_h);
+}
+
+// EngineCore.EngramHashRowsBatch (Engine.cs:2631-2656) on the host.
+void engram_rows(const nhip_ctx* c, const int32_t* tokens, const int32_t* row_slots, int rows, int32_t* out)
+{
+    const int heads = c->engram_tables / c->order_count;
+    int run_start = 0;
+    for (int t = 0; t < rows; t++) {
+        if (t == 0 || row_slots[t] != row_slots[t - 1]) run_start = t;
+        const int slot = row_slots[t], position = c->len[slot] + t - run_start;
+        const int32_t* pv = &c->prev[2 * slot];
+        for (int o = 0; o < c->order_count; o++)
+            for (int h = 0; h < heads; h++) {
+                const int table = o * heads + h, order = c->orders[o];
+                if (position < order - 1) {
+                    out[t * c->engram_tables + table] = -1;
+                    continue;
+                }
+                uint32_t acc = 0x9E3779B9u * (uint32_t)(table + 1);
+                for (int j = 0; j < order; j++) {
+                    const int back = t - run_start - j;
+                    const int token = back >= 0 ? tokens[run_start + back] : pv[back + 2];
+                    acc = (acc ^ (uint32_t)token) * 0x01000193u;
+                }
+                acc ^= acc >> 15;
+                out[t * c->engram_tables + table] = table * c->engram_slots + (int)(acc % (uint32_t)c->engram_slots);
+            }
+    }
+}
+
+
+int32_t enqueue_step(nhip_ctx* c, int rows, int heads, int k, bool argmax)
+{
+    hipStream_t s = c->stream_h;
+    const int d = c->dim, sw = kLanes * d, L = c->layers, H = c->heads, KV = c->kv, qw = H * c->qk,
+              kw = KV * c->qk, vw = KV * c->vd, ow = H * c->vd, all = qw + kw + vw;
+    const int stride_d = (d / 128 + 7) / 8 * 8;
+    int32_t rc;
+    // EngineCore's embeddingScale = sqrt(dim) (Engine.cs:123), host sqrtf
+    const float emb_scale_m1 = std::sqrt((float)d) - 1.0f;
+    hipLaunchKernelGGL(n3_embed_kernel, dim3(rows), dim3(128), 0, s, c->embedding_raw, c->vocab, d, c->embedding_bits,
+                       c->book4, in(c, c->d_in, kInTokens), emb_scale_m1, c->stream);
+    NHIP_CHECK_HIP(hipGetLastError());
+    for (int l = 0; l < L; l++) {
+        const N3Layer& w = c->layer[l];
+        // hyper-connection phi (RunLayerBatch, Engine.cs:2356-2364)
+        hipLaunchKernelGGL(n3_norm_fake_kernel<kRmsFake>, dim3(rows), dim3(kThreads), 0, s, c->stream, sw, nullptr,
+                           nullptr, c->normed);
+        NHIP_CHECK_HIP(hipGetLastError());
+        if ((rc = prepare(c, c->normed, rows, sw, 4)) ||
+            (rc = matmul(c, c->phi_pre, rows, sw, l * 4, 4, c->pre_out, 4 * L)) ||
+            (rc = matmul(c, c->phi_post, rows, sw, l * 4, 4, c->post_out, 4 * L)) ||
+            (rc = matmul(c, c->phi_res, rows, sw, l * 16, 16, c->res_out, 16 * L)))
+            return rc;
+        HyperArgs ha{c->stream, c->pre_out + l * 4, c->post_out + l * 4, c->res_out + l * 16, 4 * L, 16 * L,
+                     c->a_pre + l, c->a_post + l, c->a_res + l, c->b_pre + 4 * l, c->b_post + 4 * l,
+                     c->b_res + 16 * l, l % kLanes, d, c->input, c->residual, c->post_gate, c->mix};
+        hipLaunchKernelGGL(n3_hyper_kernel, dim3(rows), dim3(kThreads), 0, s, ha);
+        NHIP_CHECK_HIP(hipGetLastError());
+        // engram (ApplyEngramBatch, Engine.cs:2399-2463)
+        int site = -1;
+        for (int k2 = 0; k2 < c->site_count; k2++)
+            if (c->sites[k2] == l) site = k2;
+        if (site >= 0) {
+            const N3Site& st = c->site[site];
+            hipLaunchKernelGGL(n3_engram_gather_kernel, dim3(rows), dim3(128), 0, s, st.tables, st.table_rows,
+                               st.table_cols, st.table_bits, st.table_bits == 2 ? c->book2 : c->book4,
+                               in_erows(c, c->d_in), c->engram_tables, d, c->ein);
+            NHIP_CHECK_HIP(hipGetLastError());
+            if ((rc = prepare(c, c->ein, rows, d, 2))) return rc;
+            const nhip_weights* jw[2] = {st.key, st.value};
+            float* jy[2] = {c->key, c->stage + (size_t)kEngramHistory * d};
+            const int32_t jl[2] = {d, (kEngramHistory + 1) * d};
+            if ((rc = nhip_matmul_batch_dev(jw, 2, c->act_v, c->act_s, c->act_o, stride_d, rows, jy, jl, s))) return rc;
+            EngramArgs ea{c->stage,
+                          c->engram_hist + (size_t)site * c->slots * kEngramHistory * d,
+                          in(c, c->d_in, kInSlots),
+                          in(c, c->d_in, kInRunStart),
+                          st.taps,
+                          c->dilation,
+                          d,
+                          c->input,
+                          c->key,
+                          c->residual,
+                          1.0f / std::sqrt((float)d)};
+            hipLaunchKernelGGL(n3_engram_mix_kernel, dim3(rows), dim3(kThreads), 0, s, ea);
+            hipLaunchKernelGGL(n3_engram_history_kernel, dim3(rows), dim3(kThreads), 0, s, ea,
+                               in(c, c->d_in, kInRunEnd));
+            NHIP_CHECK_HIP(hipGetLastError());
+        }
+        // attention (RunAttentionBatch, Engine.cs:2480-2596)
+        hipLaunchKernelGGL(n3_norm_fake_kernel<kCenteredFake>, dim3(rows), dim3(kThreads), 0, s, c->residual, d,
+                           w.norm_in, nullptr, c->normed);
+        NHIP_CHECK_HIP(hipGetLastError());
+        if ((rc = prepare(c, c->normed, rows, d, 2))) return rc;
+        const nhip_weights* pw[4] = {w.q, w.k, w.v, w.gate};
+        float* py[4] = {c->raw, c->raw + qw, c->raw + qw + kw, c->gate};
+        const int32_t pl[4] = {all, all, all, ow};
+        if ((rc = nhip_matmul_batch_dev(pw, 4, c->act_v, c->act_s, c->act_o, stride_d, rows, py, pl, s))) return rc;
+        const size_t lcell = (size_t)l * c->slots * c->capacity;
+        int8_t* keys = c->keys + lcell * kw;
+        int8_t* values = c->values + lcell * vw;
+        float* kscale = c->key_scales + lcell * KV;
+        float* vscale = c->value_scales + lcell * KV;
+        if ((rc = nhip_needle3_attention_inputs_dev(
+                 c->raw, rows, H, KV, c->qk, c->vd, w.q_taps, w.k_taps, w.v_taps, w.q_norm, w.k_norm, c->rope_cos,
+                 c->rope_sin, c->qkv_hist + (size_t)l * c->slots * 2 * all, in(c, c->d_in, kInSlots),
+                 in(c, c->d_in, kInPos), c->slots, c->capacity, c->q8, c->qs, keys, kscale, values, vscale, s)))
+            return rc;
+        // the layer's span (Blocks.cs:973-978): global layers from 0, the
+        // others over the window ending at the row
+        const bool global = ((c->global_mask >> l) & 1) || c->window == 0;
+        if ((rc = attention_decode_impl(c->q8, c->qs, rows, H, KV, c->qk, keys, kscale, values, vscale, c->slots,
+                                        c->capacity, in(c, c->d_in, kInSlots),
+                                        in(c, c->d_in, global ? kInFirst : kInFirstW),
+                                        in(c, c->d_in, global ? kInCount : kInCountW), c->max_chunks, c->attn_ws,
+                                        c->attn_ws_bytes, c->att, nullptr, nullptr, s)))
+            return rc;
+        hipLaunchKernelGGL(n3_gate_fake_kernel, dim3(rows), dim3(kThreads), 0, s, c->att, c->gate, ow);
+        NHIP_CHECK_HIP(hipGetLastError());
+        if ((rc = prepare(c, c->att, rows, ow, 2)) || (rc = matmul(c, w.out, rows, ow, 0, d, c->proj, d))) return rc;
+        hipLaunchKernelGGL(n3_post_norm_add_kernel, dim3(rows), dim3(kThreads), 0, s, c->residual, c->proj,
+                           w.post_norm, w.attn_gate, d);
+        // the Kronecker-Hadamard MLP (RunMlp, Engine.cs:2146-2156)
+        MlpArgs ma{c->residual, w.pre_hada, c->perm_a, c->perm_b, w.d1, w.d2, w.b2, w.d3, w.d4, w.w1a, w.w1b,
+                   w.w2a, w.w2b, w.w3a, w.w3b, w.cond_v, w.cond_u, d, c->hada_rows, c->hada_cols};
+        hipLaunchKernelGGL(n3_mlp_kernel, dim3(rows), dim3(kThreads), c->mlp_lds, s, ma);
+        hipLaunchKernelGGL(n3_combine_kernel, dim3(rows), dim3(kThreads), 0, s, c->stream, c->mix, c->residual,
+                           c->input, c->post_gate, d, c->next);
+        NHIP_CHECK_HIP(hipGetLastError());
+        std::swap(c->stream, c->next);
+    }
+    if (heads == 0) return NHIP_OK;
+    // the head rows (PrepareHeadVectors, Engine.cs:920-928) and the tied
+    // 4-bit embedding
+    hipLaunchKernelGGL(n3_norm_fake_kernel<kHeadFake>, dim3(heads), dim3(kThreads), 0, s, c->stream, d,
+                       c->final_norm, in(c, c->d_in, kInHeads), c->normed);
+    NHIP_CHECK_HIP(hipGetLastError());
+    if ((rc = prepare(c, c->normed, heads, d, 4)) ||
+        (rc = matmul(c, c->embedding, heads, d, 0, c->vocab, c->logits, c->vocab)))
+        return rc;
+    if (k > 0 && (rc = nhip_topk_lse_dev(c->logits, heads, c->vocab, k, c->topk_ws, c->topk_ws_bytes, c->d_topk_idx,
+                                         c->d_topk_lp, s)))
+        return rc;
+    if (argmax && (rc = nhip_argmax_dev(c->logits, c->vocab, c->vocab, heads, c->d_argmax, nullptr, s))) return rc;
+    return NHIP_OK;
+}
+
+// The live histories of a slot (convolution frames of every layer, engram
+// frames of every site) to or from its snapshot; MarkView / RewindView
+// (Engine.cs:2235-2255) with the rewind restoring eagerly.
+int32_t snapshot_slot(nhip_ctx* c, int slot, bool to_snapshot)
+{
+    const size_t all = (size_t)c->heads * c->qk + (size_t)c->kv * c->qk + (size_t)c->kv * c->vd;
+    int32_t rc;
+    for (int l = 0; l < c->layers; l++) {
+        const size_t o = ((size_t)l * c->slots + slot) * 2 * all;
+        float* live = c->qkv_hist + o;
+        float* snap = c->snap_qkv + o;
+        if ((rc = nhip_copy_dev(to_snapshot ? snap : live, to_snapshot ? live : snap, sizeof(float) * 2 * all,
+                                c->stream_h)))
+            return rc;
+    }
+    const size_t eh = (size_t)kEngramHistory * c->dim;
+    for (int k = 0; k < c->site_count; k++) {
+        const size_t o = ((size_t)k * c->slots + slot) * eh;
+        float* live = c->engram_hist + o;
+        float* snap = c->snap_engram + o;
+        if ((rc = nhip_copy_dev(to_snapshot ? snap : live, to_snapshot ? live : snap, sizeof(float) * eh, c->stream_h)))
+            return rc;
+    }
+    for (int i = 0; i < 2; i++) {
+        if (to_snapshot) c->snap_prev[2 * slot + i] = c->prev[2 * slot + i];
+        else c->prev[2 * slot + i] = c->snap_prev[2 * slot + i];
+    }
+    NHIP_CHECK_HIP(hipStreamSynchronize(c->stream_h));
+    return NHIP_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int32_t nhip_ctx_destroy(nhip_ctx* c)
+{
+    clear_error();
+    if (!c) return NHIP_OK;
+    if (c->stream_h) (void)hipStreamSynchronize(c->stream_h);
+    for (void* p : c->allocations) (void)hipFree(p);
+    if (c->h_in) (void)hipHostFree(c->h_in);
+    if (c->stream_h) (void)hipStreamDestroy(c->stream_h);
+    delete c;
+    return NHIP_OK;
+}
+
+int32_t nhip_ctx_create(const nhip_model* model, int32_t capacity, int32_t slots, int32_t chunk, int32_t max_chunks,
+                        nhip_ctx** out)
+{
+    clear_error();
+    NHIP_REQUIRE(model && out, "null argument");
+    *out = nullptr;
+    if (chunk <= 0) chunk = 64;
+    if (max_chunks <= 0) max_chunks = 8;
+    // BatchedEngine's limits (BatchEngine.cs:11-12): 1..16 slots
+    NHIP_REQUIRE(capacity > 0 && slots >= 1 && slots <= 16 && chunk <= 4096 && max_chunks <= 256,
+                 "capacity %d, slots %d (1..16), chunk %d (<= 4096), max_chunks %d (<= 256)", capacity, slots, chunk,
+                 max_chunks);
+    int32_t rc = ensure_device();
+    if (rc) return rc;
+    nhip_ctx* c = new nhip_ctx();
+    c->model = model;
+    c->slots = slots;
+    c->capacity = capacity;
+    c->max_rows = chunk;
+    c->max_chunks = max_chunks;
+    if (hipStreamCreateWithFlags(&c->stream_h, hipStreamNonBlocking) != hipSuccess) {
+        delete c;
+        set_error("hipStreamCreateWithFlags failed");
+        return NHIP_ERR_HIP;
+    }
+    if ((rc = load_model(c)) || (rc = alloc_state(c))) {
+        const std::string why = nhip_last_error();
+        nhip_ctx_destroy(c);
+        set_error("%s", why.c_str());
+        return rc;
+    }
+    if (hipStreamSynchronize(c->stream_h) != hipSuccess || hipDeviceSynchronize() != hipSuccess) {
+        nhip_ctx_destroy(c);
+        set_error("context set-up failed");
+        return NHIP_ERR_HIP;
+    }
+    *out = c;
+    return NHIP_OK;
+}
+
+int32_t nhip_ctx_info(const nhip_ctx* c, int32_t* vocab, int32_t* slots, int32_t* capacity, int32_t* chunk)
+{
+    clear_error();
+    NHIP_REQUIRE(c, "null context");
+    if (vocab) *vocab = c->vocab;
+    if (slots) *slots = c->slots;
+    if (capacity) *capacity = c->capacity;
+    if (chunk) *chunk = c->max_rows;
+    return NHIP_OK;
+}
+
+int32_t nhip_step(nhip_ctx* c, const int32_t* tokens, const int32_t* row_slots, int32_t rows, const int32_t* head_rows,
+                  int32_t heads, float* logits, int32_t k, int32_t* topk_idx, float* topk_lp, int32_t* argmax)
+{
+    clear_error();
+    NHIP_REQUIRE(c && tokens && row_slots, "null argument");
+    // ForwardBatch's checks (Engine.cs:2305-2307)
+    NHIP_REQUIRE(rows >= 1 && rows <= c->max_rows, "rows %d outside [1, %d]", rows, c->max_rows);
+    NHIP_REQUIRE(heads >= 0 && heads <= rows && (heads == 0 || head_rows), "heads %d outside [0, %d]", heads, rows);
+    NHIP_REQUIRE(k >= 0 && k <= 8 && (k == 0 || (topk_idx && topk_lp)), "k %d outside [0, 8] or null top-k output", k);
+    const int R = c->max_rows;
+    int32_t* h = c->h_in;
+    std::vector<char> seen(c->slots, 0);
+    for (int rs = 0; rs < rows;) {
+        const int slot = row_slots[rs];
+        NHIP_REQUIRE(slot >= 0 && slot < c->slots, "row %d: slot %d outside [0, %d)", rs, slot, c->slots);
+        NHIP_REQUIRE(!seen[slot], "the rows of slot %d must form one contiguous run", slot);
+        seen[slot] = 1;
+        int rk = rs;
+        while (rk + 1 < rows && row_slots[rk + 1] == slot) rk++;
+        NHIP_REQUIRE(c->len[slot] + (rk - rs + 1) <= c->capacity, "slot %d: context capacity %d exceeded", slot,
+                     c->capacity);
+        for (int t = rs; t <= rk; t++) {
+            NHIP_REQUIRE(tokens[t] >= 0 && tokens[t] < c->vocab, "row %d: token %d outside [0, %d)", t, tokens[t],
+                         c->vocab);
+            const int pos = c->len[slot] + t - rs;
+            const int first_w = c->window > 0 ? std::max(pos - c->window + 1, 0) : 0;
+            h[kInTokens * R + t] = tokens[t];
+            h[kInSlots * R + t] = slot;
+            h[kInPos * R + t] = pos;
+            h[kInFirst * R + t] = 0;
+            h[kInCount * R + t] = pos + 1;
+            h[kInFirstW * R + t] = first_w;
+            h[kInCountW * R + t] = pos - first_w + 1;
+            h[kInRunStart * R + t] = rs;
+            h[kInRunEnd * R + t] = t == rk ? 1 : 0;
+        }
+        rs = rk + 1;
+    }
+    for (int i = 0; i < heads; i++) {
+        NHIP_REQUIRE(head_rows[i] >= 0 && head_rows[i] < rows, "head row %d outside [0, %d)", head_rows[i], rows);
+        h[kInHeads * R + i] = head_rows[i];
+    }
+    if (c->site_count > 0) engram_rows(c, tokens, row_slots, rows, in_erows(c, h));
+    const size_t words = (size_t)R * (kInSections + std::max(c->engram_tables, 1));
+    hipStream_t s = c->stream_h;
+    int32_t rc = NHIP_OK;
+    if (hipMemcpyAsync(c->d_in, h, words * sizeof(int32_t), hipMemcpyHostToDevice, s) != hipSuccess) {
+        set_error("step input upload failed");
+        rc = NHIP_ERR_HIP;
+    }
+    if (rc == NHIP_OK) rc = enqueue_step(c, rows, heads, k, argmax != nullptr);
+    if (rc == NHIP_OK && heads > 0) {
+        const size_t hv = (size_t)heads;
+        hipError_t e = hipSuccess;
+        if (logits) e = hipMemcpyAsync(logits, c->logits, hv * c->vocab * sizeof(float), hipMemcpyDeviceToHost, s);
+        if (e == hipSuccess && k > 0) {
+            // the device lists are [heads][k] with stride k
+            e = hipMemcpyAsync(topk_idx, c->d_topk_idx, hv * k * sizeof(int32_t), hipMemcpyDeviceToHost, s);
+            if (e == hipSuccess)
+                e = hipMemcpyAsync(topk_lp, c->d_topk_lp, hv * k * sizeof(float), hipMemcpyDeviceToHost, s);
+        }
+        if (e == hipSuccess && argmax)
+            e = hipMemcpyAsync(argmax, c->d_argmax, hv * sizeof(int32_t), hipMemcpyDeviceToHost, s);
+        if (e != hipSuccess) {
+            set_error("step output download failed: %s", hipGetErrorString(e));
+            rc = NHIP_ERR_HIP;
+        }
+    }
+    // the staging buffer is reused by the next call: drain the stream first
+    const hipError_t done = hipStreamSynchronize(s);
+    if (rc != NHIP_OK) return rc;
+    if (done != hipSuccess) {
+        set_error("step failed: %s", hipGetErrorString(done));
+        return NHIP_ERR_HIP;
+    }
+    // the slots' lengths and previous tokens (ForwardBatch, Engine.cs:2326-2340)
+    for (int rs = 0; rs < rows;) {
+        const int slot = row_slots[rs];
+        int rk = rs;
+        while (rk + 1 < rows && row_slots[rk + 1] == slot) rk++;
+        int32_t* pv = &c->prev[2 * slot];
+        pv[0] = rk > rs ? tokens[rk - 1] : pv[1];
+        pv[1] = tokens[rk];
+        c->len[slot] += rk - rs + 1;
+        rs = rk + 1;
+    }
+    return NHIP_OK;
+}
+
+int32_t nhip_slot_feed(nhip_ctx* c, int32_t slot, const int32_t* tokens, int32_t count, float* logits)
+{
+    clear_error();
+    NHIP_REQUIRE(c && (tokens || count == 0), "null argument");
+    NHIP_REQUIRE(slot >= 0 && slot < c->slots, "slot %d outside [0, %d)", slot, c->slots);
+    NHIP_REQUIRE(count >= 0, "count %d", count);
+    // FeedSlot (Engine.cs:2285-2301): the capacity is checked before any work
+    NHIP_REQUIRE(c->len[slot] + count <= c->capacity, "slot %d: context capacity %d exceeded", slot, c->capacity);
+    std::vector<int32_t> row_slots(c->max_rows, slot);
+    for (int start = 0; start < count; start += c->max_rows) {
+        const int n = std::min(c->max_rows, count - start);
+        const bool last = start + n == count;
+        const int32_t head = n - 1;
+        const int heads = last && logits ? 1 : 0;
+        const int32_t rc = nhip_step(c, tokens + start, row_slots.data(), n, heads ? &head : nullptr, heads,
+                                     heads ? logits : nullptr, 0, nullptr, nullptr, nullptr);
+        if (rc) return rc;
+    }
+    return NHIP_OK;
+}
+
+int32_t nhip_slot_reset(nhip_ctx* c, int32_t slot)
+{
+    clear_error();
+    NHIP_REQUIRE(c && slot >= 0 && slot < c->slots, "slot %d outside the context's slots", slot);
+    const size_t all = (size_t)c->heads * c->qk + (size_t)c->kv * c->qk + (size_t)c->kv * c->vd;
+    for (int l = 0; l < c->layers; l++)
+        NHIP_CHECK_HIP(hipMemsetAsync(c->qkv_hist + ((size_t)l * c->slots + slot) * 2 * all, 0, sizeof(float) * 2 * all,
+                                      c->stream_h));
+    const size_t eh = (size_t)kEngramHistory * c->dim;
+    for (int k = 0; k < c->site_count; k++)
+        NHIP_CHECK_HIP(
+            hipMemsetAsync(c->engram_hist + ((size_t)k * c->slots + slot) * eh, 0, sizeof(float) * eh, c->stream_h));
+    NHIP_CHECK_HIP(hipStreamSynchronize(c->stream_h));
+    c->prev[2 * slot] = c->prev[2 * slot + 1] = 0;
+    c->len[slot] = 0;
+    c->marked[slot] = 0;
+    return NHIP_OK;
+}
+
+int32_t nhip_slot_mark(nhip_ctx* c, int32_t slot)
+{
+    clear_error();
+    NHIP_REQUIRE(c && slot >= 0 && slot < c->slots, "slot %d outside the context's slots", slot);
+    const int32_t rc = snapshot_slot(c, slot, true);
+    if (rc) return rc;
+    c->marked[slot] = c->len[slot];
+    return NHIP_OK;
+}
+
+int32_t nhip_slot_rewind(nhip_ctx* c, int32_t slot)
+{
+    clear_error();
+    NHIP_REQUIRE(c && slot >= 0 && slot < c->slots, "slot %d outside the context's slots", slot);
+    const int32_t rc = snapshot_slot(c, slot, false);
+    if (rc) return rc;
+    c->len[slot] = c->marked[slot];
+    return NHIP_OK;
+}
+
+int32_t nhip_slot_length(const nhip_ctx* c, int32_t slot, int32_t* length)
+{
+    clear_error();
+    NHIP_REQUIRE(c && length && slot >= 0 && slot < c->slots, "slot %d outside the context's slots", slot);
+    *length = c->len[slot];
+    return NHIP_OK;
+}
+
+int32_t nhip_slot_copy(nhip_ctx* c, int32_t dst, int32_t src)
+{
+    clear_error();
+    NHIP_REQUIRE(c && dst >= 0 && dst < c->slots && src >= 0 && src < c->slots, "slots %d <- %d outside [0, %d)", dst,
+                 src, c ? c->slots : 0);
+    if (dst == src) return NHIP_OK;
+    const size_t qw = (size_t)c->heads * c->qk, kw = (size_t)c->kv * c->qk, vw = (size_t)c->kv * c->vd,
+                 all = qw + kw + vw, n = (size_t)c->len[src], KV = c->kv;
+    hipStream_t s = c->stream_h;
+    int32_t rc;
+    for (int l = 0; l < c->layers; l++) {
+        const size_t cs = ((size_t)l * c->slots + src) * c->capacity, cd = ((size_t)l * c->slots + dst) * c->capacity;
+        const size_t hs = ((size_t)l * c->slots + src) * 2 * all, hd = ((size_t)l * c->slots + dst) * 2 * all;
+        if ((rc = nhip_copy_dev(c->keys + cd * kw, c->keys + cs * kw, n * kw, s)) ||
+            (rc = nhip_copy_dev(c->values + cd * vw, c->values + cs * vw, n * vw, s)) ||
+            (rc = nhip_copy_dev(c->key_scales + cd * KV, c->key_scales + cs * KV, n * KV * sizeof(float), s)) ||
+            (rc = nhip_copy_dev(c->value_scales + cd * KV, c->value_scales + cs * KV, n * KV * sizeof(float), s)) ||
+            (rc = nhip_copy_dev(c->qkv_hist + hd, c->qkv_hist + hs, 2 * all * sizeof(float), s)) ||
+            (rc = nhip_copy_dev(c->snap_qkv + hd, c->snap_qkv + hs, 2 * all * sizeof(float), s)))
+            return rc;
+    }
+    const size_t eh = (size_t)kEngramHistory * c->dim;
+    for (int k = 0; k < c->site_count; k++) {
+        const size_t os = ((size_t)k * c->slots + src) * eh, od = ((size_t)k * c->slots + dst) * eh;
+        if ((rc = nhip_copy_dev(c->engram_hist + od, c->engram_hist + os, eh * sizeof(float), s)) ||
+            (rc = nhip_copy_dev(c->snap_engram + od, c->snap_engram + os, eh * sizeof(float), s)))
+            return rc;
+    }
+    NHIP_CHECK_HIP(hipStreamSynchronize(s));
+    for (int i = 0; i < 2; i++) {
+        c->prev[2 * dst + i] = c->prev[2 * src + i];
+        c->snap_prev[2 * dst + i] = c->snap_prev[2 * src + i];
+    }
+    c->len[dst] = c->len[src];
+    c->marked[dst] = c->marked[src];
+    return NHIP_OK;
+}
+
+}  // extern "C"

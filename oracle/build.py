@@ -1,7 +1,7 @@
 """Build the oracle (test infrastructure) with gcc.
 
 Produces oracle/_build/libneedle_oracle.so from needle_oracle.c,
-cpu_baseline.c, cpu_simd.c and decoder.c.  Flags keep every float operation an IEEE binary32 operation
+cpu_baseline.c, cpu_simd.c, decoder.c and needle3_model.c.  Flags keep every float operation an IEEE binary32 operation
 in source order (-ffp-contract=off, no -ffast-math); -O2 -mavx2 only lets gcc
 vectorise the integer group dots and the row loops.  cpu_simd.c's SIMD tier
 (the timed baseline) takes its AVX2 / AVX-VNNI instructions from function
@@ -16,7 +16,7 @@ import sys
 HERE = os.path.dirname(os.path.abspath(__file__))
 OUT = os.path.join(HERE, "_build")
 LIB = os.path.join(OUT, "libneedle_oracle.so")
-SOURCES = ["needle_oracle.c", "cpu_baseline.c", "cpu_simd.c", "decoder.c"]
+SOURCES = ["needle_oracle.c", "cpu_baseline.c", "cpu_simd.c", "decoder.c", "needle3_model.c"]
 FLAGS = ["-O2", "-std=c11", "-fPIC", "-shared", "-ffp-contract=off", "-fno-fast-math", "-mavx2",
          "-Wall", "-Wextra", "-pthread"]
 

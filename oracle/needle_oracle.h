@@ -309,6 +309,102 @@ int or_greedy(or_decoder* m, const int* prompt, int prompt_len, int max_new, int
 int or_beam_search(or_decoder* m, const int* prompt, int prompt_len, int width, int max_new, int eos,
                    int* out_tokens, float* out_score, long* fed_rows, double* seconds);
 
+/* ---- Needle 3's batched decode step (needle3_model.c) ---- */
+
+/* Needle 3 row kernels in the scalar order (src/Needle/Scalar.cs), the
+ * polynomial Ops.Exp in place of MathF.Exp. */
+float or_sigmoid(float x);
+float or_n3_attn_gate(float x);                                                       /* Model.cs:147 */
+void or_rms_fake_a8(const float* x, int n, float* d);                                 /* Scalar.RmsFakeA8 */
+void or_centered_rms_fake_a8(const float* x, const float* s, int n, float* d);        /* Scalar.CenteredRmsFakeA8 */
+void or_gate_fake_a8(float* x, const float* gate, int n);                             /* Scalar.GateFakeA8 */
+float or_fake_a8(float* x, int n);                                                    /* Quant.FakeA8 (Quant.cs:69-79) */
+void or_post_norm_add(float* residual, const float* x, const float* s, float gate, int n); /* Scalar.PostNormAdd */
+void or_mix4(const float* s, int dim, float w0, float w1, float w2, float w3, float* d);  /* Scalar.Mix4 */
+void or_combine_diff4x4(const float* s, int dim, const float* mix, const float* x, const float* u,
+                        const float* post_gate, float* d);                            /* Ops.CombineDiff4x4 */
+void or_sinkhorn4x4(const float* logits, float* r);                                   /* Scalar.Sinkhorn4x4 */
+void or_rms_unit(const float* x, int n, float* d);                                    /* Ops.RmsUnit (scalar) */
+float or_dot(const float* a, const float* b, int n);                                  /* Scalar.Dot */
+void or_gather_row(const or_cq* w, int row, float* d);                                /* Quant.GatherRow */
+
+/* Geometry (src/Needle/Model.cs:65-121) */
+typedef struct or_n3_dims {
+    int vocab, dim, heads, kv_heads, layers, qk, vd, hada_n, hada_rows, hada_cols, window;
+    int engram_slots, engram_sub, engram_tables, engram_dilation, order_count, orders[4];
+    int site_count, sites[16];
+    uint64_t global_mask;
+    float rope_theta;
+} or_n3_dims;
+
+/* MlpWeights (src/Needle/Audio.cs:5-27) */
+typedef struct or_n3_mlp {
+    const float *d1, *d2, *b2, *d3, *d4, *w1a, *w1b, *w2a, *w2b, *w3a, *w3b, *cond_v, *cond_u;
+} or_n3_mlp;
+
+/* LayerWeights (src/Needle/Model.cs:123-152); attn_gate already the
+ * sigmoid of the stored value */
+typedef struct or_n3_layer {
+    const float* norm_in;
+    or_cq q, k, v;
+    const float *q_taps, *k_taps, *v_taps, *q_norm, *k_norm;
+    or_cq gate, out;
+    const float* post_norm;
+    float attn_gate;
+    const float* pre_hada;
+    or_n3_mlp mlp;
+} or_n3_layer;
+
+/* EngramSite (src/Needle/Model.cs:176-188) */
+typedef struct or_n3_site {
+    or_cq tables, key, value;
+    const float* taps; /* [4][dim] */
+} or_n3_site;
+
+typedef struct or_n3_model {
+    or_n3_dims g;
+    or_cq embedding;                                   /* [vocab][dim], 4-bit (the tied head) */
+    const or_n3_layer* layer;                          /* [layers] */
+    const float *a_pre, *a_post, *a_res, *b_pre, *b_post, *b_res;
+    or_cq phi_pre, phi_post, phi_res;                  /* [L*4|L*4|L*16][4*dim], 4-bit */
+    const int *perm_a, *perm_b;                        /* [hada_n] */
+    const or_n3_site* site;                            /* [site_count] */
+    const float* final_norm;
+} or_n3_model;
+
+/* A batched engine's state (EngineCore with slots, Engine.cs:2197-2283):
+ * per slot the KV caches of every layer, the three-tap histories, the
+ * engram histories, the two previous tokens, the length and the mark. */
+typedef struct or_n3_engine {
+    const or_n3_model* m;
+    int slots, capacity, max_chunks;
+    float *rope_cos, *rope_sin;                        /* [capacity][qk/2] */
+    int8_t *keys, *values;                             /* [layers][slots][capacity][kv*qk | kv*vd] */
+    float *key_scales, *value_scales;                  /* [layers][slots][capacity][kv] */
+    float* qkv_hist;                                   /* [layers][slots][2*(qw+kw+vw)] */
+    float* engram_hist;                                /* [sites][slots][9][dim] */
+    float *snap_qkv, *snap_engram;
+    int *length, *marked, *prev, *snap_prev;
+} or_n3_engine;
+
+/* HadamardMlp.Apply (Blocks.cs:1067-1101), scalar kernels, Scale 1 */
+void or_hadamard_mlp(const or_n3_mlp* w, const float* pre_norm, const int* perm_a, const int* perm_b, int dim,
+                     int rows, int cols, float* residual);
+/* EngineCore.EngramHashRowsBatch (Engine.cs:2631-2656) */
+void or_n3_engram_rows(const or_n3_dims* g, const int* tokens, const int* row_slots, int rows, const int* lengths,
+                       const int* prev, int* out);
+/* EngineCore.RopeFrequencies + BuildRopeTables (Engine.cs:336-356) */
+void or_n3_rope_tables(float theta, int qk, int capacity, float* cos_t, float* sin_t);
+int or_n3_init(or_n3_engine* e);
+void or_n3_free(or_n3_engine* e);
+void or_n3_reset(or_n3_engine* e, int slot);
+void or_n3_mark(or_n3_engine* e, int slot);
+void or_n3_rewind(or_n3_engine* e, int slot);
+/* EngineCore.ForwardBatch (Engine.cs:2303-2350): logits [heads][vocab] of
+ * the head rows. */
+void or_n3_forward(or_n3_engine* e, const int* tokens, const int* row_slots, int rows, const int* head_rows,
+                   int heads, float* logits);
+
 #ifdef __cplusplus
 }
 #endif

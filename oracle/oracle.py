@@ -56,6 +56,51 @@ class Decoder(C.Structure):
                 ("key_scales", C.c_void_p), ("value_scales", C.c_void_p)]
 
 
+class _N3:
+    """ctypes mirrors of needle_oracle.h's Needle 3 structs."""
+
+    class Dims(C.Structure):
+        _fields_ = [(n, C.c_int) for n in ("vocab", "dim", "heads", "kv_heads", "layers", "qk", "vd", "hada_n",
+                                            "hada_rows", "hada_cols", "window", "engram_slots", "engram_sub",
+                                            "engram_tables", "engram_dilation", "order_count")] + \
+                   [("orders", C.c_int * 4), ("site_count", C.c_int), ("sites", C.c_int * 16),
+                    ("global_mask", C.c_uint64), ("rope_theta", C.c_float)]
+
+    class Mlp(C.Structure):
+        _fields_ = [(n, C.c_void_p) for n in ("d1", "d2", "b2", "d3", "d4", "w1a", "w1b", "w2a", "w2b", "w3a", "w3b",
+                                               "cond_v", "cond_u")]
+
+    class Layer(C.Structure):
+        pass
+
+    class Site(C.Structure):
+        pass
+
+    class Model(C.Structure):
+        pass
+
+    class Engine(C.Structure):
+        pass
+
+
+_N3.Layer._fields_ = [("norm_in", C.c_void_p), ("q", Cq), ("k", Cq), ("v", Cq), ("q_taps", C.c_void_p),
+                      ("k_taps", C.c_void_p), ("v_taps", C.c_void_p), ("q_norm", C.c_void_p), ("k_norm", C.c_void_p),
+                      ("gate", Cq), ("out", Cq), ("post_norm", C.c_void_p), ("attn_gate", C.c_float),
+                      ("pre_hada", C.c_void_p), ("mlp", _N3.Mlp)]
+_N3.Site._fields_ = [("tables", Cq), ("key", Cq), ("value", Cq), ("taps", C.c_void_p)]
+_N3.Model._fields_ = [("g", _N3.Dims), ("embedding", Cq), ("layer", C.POINTER(_N3.Layer))] + \
+                     [(n, C.c_void_p) for n in ("a_pre", "a_post", "a_res", "b_pre", "b_post", "b_res")] + \
+                     [("phi_pre", Cq), ("phi_post", Cq), ("phi_res", Cq), ("perm_a", C.c_void_p),
+                      ("perm_b", C.c_void_p), ("site", C.POINTER(_N3.Site)), ("final_norm", C.c_void_p)]
+_N3.Engine._fields_ = [("m", C.POINTER(_N3.Model)), ("slots", C.c_int), ("capacity", C.c_int),
+                       ("max_chunks", C.c_int)] + \
+                      [(n, C.c_void_p) for n in ("rope_cos", "rope_sin", "keys", "values", "key_scales",
+                                                  "value_scales", "qkv_hist", "engram_hist", "snap_qkv",
+                                                  "snap_engram")] + \
+                      [("length", C.POINTER(C.c_int)), ("marked", C.POINTER(C.c_int)), ("prev", C.POINTER(C.c_int)),
+                       ("snap_prev", C.POINTER(C.c_int))]
+N3 = _N3
+
 _u64p, _vp, _i, _f, _sz = C.POINTER(C.c_uint64), C.c_void_p, C.c_int, C.c_float, C.c_size_t
 _PROTOS = {
     "or_xs_seed": (C.c_uint64, [C.c_uint64]),
@@ -124,6 +169,28 @@ _PROTOS = {
     "or_baseline_stop": (None, []),
     "or_baseline_matmul_i8": (None, [_vp, _vp, _i, _i, _i, _vp, _vp, _i, _vp, _i, _i, _i]),
     "or_simd_tier": (_i, []),
+    "or_sigmoid": (_f, [_f]),
+    "or_n3_attn_gate": (_f, [_f]),
+    "or_rms_fake_a8": (None, [_vp, _i, _vp]),
+    "or_centered_rms_fake_a8": (None, [_vp, _vp, _i, _vp]),
+    "or_gate_fake_a8": (None, [_vp, _vp, _i]),
+    "or_fake_a8": (_f, [_vp, _i]),
+    "or_post_norm_add": (None, [_vp, _vp, _vp, _f, _i]),
+    "or_mix4": (None, [_vp, _i, _f, _f, _f, _f, _vp]),
+    "or_combine_diff4x4": (None, [_vp, _i, _vp, _vp, _vp, _vp, _vp]),
+    "or_sinkhorn4x4": (None, [_vp, _vp]),
+    "or_rms_unit": (None, [_vp, _i, _vp]),
+    "or_dot": (_f, [_vp, _vp, _i]),
+    "or_gather_row": (None, [C.POINTER(Cq), _i, _vp]),
+    "or_hadamard_mlp": (None, [C.POINTER(_N3.Mlp), _vp, _vp, _vp, _i, _i, _i, _vp]),
+    "or_n3_engram_rows": (None, [C.POINTER(_N3.Dims), _vp, _vp, _i, _vp, _vp, _vp]),
+    "or_n3_rope_tables": (None, [_f, _i, _i, _vp, _vp]),
+    "or_n3_init": (_i, [C.POINTER(_N3.Engine)]),
+    "or_n3_free": (None, [C.POINTER(_N3.Engine)]),
+    "or_n3_reset": (None, [C.POINTER(_N3.Engine), _i]),
+    "or_n3_mark": (None, [C.POINTER(_N3.Engine), _i]),
+    "or_n3_rewind": (None, [C.POINTER(_N3.Engine), _i]),
+    "or_n3_forward": (None, [C.POINTER(_N3.Engine), _vp, _vp, _i, _vp, _i, _vp]),
     "or_simd_matmul_i8": (None, [_i, _vp, _vp, _i, _i, _vp, _vp, _i, _vp, _i, _i, _i]),
     "or_baseline_simd_matmul_i8": (None, [_i, _vp, _vp, _i, _i, _vp, _vp, _i, _vp, _i, _i, _i]),
 }
