@@ -432,6 +432,99 @@ def decode_loop(args, threads: int) -> dict:
     return out
 
 
+def needle3_step_bytes(archive: bytes, geometry: dict) -> int:
+    """Weight bytes one decode step reads: every codebook record but the
+    engram tables (a few gathered rows), the tied embedding once for the head,
+    and the dense records as the fp32 arrays they become on the device."""
+    from needle_cs_amd.archive import parse
+    _, _, _, recs = parse(archive)
+    first_site = 1 + geometry["layers"] * 27 + 11  # Model.Open's record order
+    tables = {first_site + 4 * s for s in range(len(geometry["sites"]))}
+    total = 0
+    for i, r in enumerate(recs):
+        dtype, nbytes = r[0], r[8]
+        if dtype == 3 and i not in tables:
+            total += nbytes
+        elif dtype in (1, 2):
+            total += nbytes * (2 if dtype == 1 else 1)
+    return total
+
+
+def needle3_loop(args, threads: int) -> dict:
+    """Batched greedy decode of three slots on a random-init archive of
+    Needle 3's geometry (20 layers, hidden 768, 12/2 heads, 5 engram sites,
+    vocab 8192) through the step API: a 64-token prompt per slot (63 fed with
+    FeedSlot, the last in the first 3-row step), then 63 decode steps of 3
+    rows with the head's ArgMax as the next tokens.  The CPU leg runs the
+    oracle's scalar engine (one thread) on the same prompts for a bounded
+    number of steps: its tokens must match the GPU's, its step time is the
+    port baseline."""
+    from needle_cs_amd.archive import NEEDLE3, needle3_archive
+    from needle_cs_amd.engine import BatchedEngine, Model
+
+    g3 = NEEDLE3
+    archive = needle3_archive(g3, 0x7007)
+    slots, prompt_len, new = 3, 64, 64
+    prompts = np.random.default_rng(0x7008).integers(0, g3["vocab"], (slots, prompt_len)).astype(np.int32)
+    step_bytes = needle3_step_bytes(archive, g3)
+    lanes = np.arange(slots, dtype=np.int32)
+    with Model(archive) as model, BatchedEngine(model, context_length=prompt_len + new, chunk_size=64, slots=slots,
+                                                max_chunks=8) as eng:
+        def run():
+            for s in range(slots):
+                eng.reset_slot(s)
+            t0 = time.perf_counter()
+            for s in range(slots):
+                eng.feed_slot(s, prompts[s, :-1], compute_logits=False)
+            _, _, _, toks = eng.forward_batch(prompts[:, -1], lanes, lanes, logits=False, argmax=True)
+            pre = time.perf_counter() - t0
+            out = [toks]
+            t1 = time.perf_counter()
+            for _ in range(new - 1):
+                _, _, _, toks = eng.forward_batch(toks, lanes, lanes, logits=False, argmax=True)
+                out.append(toks)
+            return pre, time.perf_counter() - t1, np.stack(out, 1)
+
+        run()  # captures the step graphs
+        pre, dec, toks = min((run() for _ in range(3)), key=lambda r: r[1])
+    steps = new - 1
+    ms = dec / steps * 1e3
+    out = {"workload": "greedy decode of 3 slots, Needle 3 geometry (20 layers, hidden 768, 12/2 heads x 48/64, "
+                       "MLP 32x32, 5 engram sites, vocab 8192), random-init archive; prompt 64 per slot, 63 steps",
+           "row_tokens_per_s": round(slots * steps / dec, 1), "ms_per_step": round(ms, 4),
+           "prefill_ms": round(pre * 1e3, 2), "weight_bytes_per_step": step_bytes,
+           "weights_GBps_per_step": round(step_bytes / (ms * 1e-3) / 1e9, 2),
+           "frac_hbm_peak": round(step_bytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 5)}
+    print(f"# needle3 decode: {out['row_tokens_per_s']} row-tokens/s, {ms:.3f} ms/step, prefill {pre * 1e3:.1f} ms",
+          file=sys.stderr, flush=True)
+    if not args.no_cpu:
+        from oracle import needle3 as M
+        from oracle import oracle as O
+
+        check_steps = 6
+        cpu = M.OracleEngine(O, M.OracleModel(O, archive), slots=slots, capacity=prompt_len + new, max_chunks=8)
+        for s in range(slots):
+            cpu.step(prompts[s, :-1], [s] * (prompt_len - 1), [])
+        lg = cpu.step(prompts[:, -1], lanes, lanes)
+        ctoks = [np.argmax(lg, axis=1)]
+        t0 = time.perf_counter()
+        for _ in range(check_steps):
+            lg = cpu.step(ctoks[-1].astype(np.int32), lanes, lanes)
+            ctoks.append(np.argmax(lg, axis=1))
+        cdec = time.perf_counter() - t0
+        cpu.close()
+        ctoks = np.stack(ctoks, 1)
+        out["tokens_identical_to_cpu_path"] = bool(np.array_equal(ctoks, toks[:, :check_steps + 1]))
+        out["cpu_path"] = {"row_tokens_per_s": round(slots * check_steps / cdec, 2), "threads": 1, "kind": "port",
+                           "sample": f"the oracle's scalar Needle 3 engine (oracle/needle3_model.c, one thread) on "
+                                     f"the same prompts, {check_steps} decode steps of 3 rows after the prefill; "
+                                     f"tokens compared over those {check_steps + 1} per slot"}
+        out["speedup_vs_cpu_path"] = round(out["row_tokens_per_s"] / out["cpu_path"]["row_tokens_per_s"], 1)
+        print(f"# needle3 CPU path: {out['cpu_path']['row_tokens_per_s']} row-tokens/s; identical tokens: "
+              f"{out['tokens_identical_to_cpu_path']}", file=sys.stderr, flush=True)
+    return out
+
+
 def physical_cores() -> int:
     """lscpu's distinct (core, socket) pairs: cores per socket x sockets."""
     try:
@@ -545,7 +638,7 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-secondary", action="store_true")
     ap.add_argument("--no-decode-loop", action="store_true")
-    ap.add_argument("--only", choices=["prefill", "attention", "decode_loop", "codebook", "batch"],
+    ap.add_argument("--only", choices=["prefill", "attention", "decode_loop", "codebook", "batch", "needle3"],
                     help="run one secondary workload alone (for kernel tracing); prints no JSON line")
     ap.add_argument("--decode-chunks", type=int, default=64,
                     help="attention position-split cap of the decode loop (1: one chunk per row with the output quantize fused)")
@@ -564,6 +657,8 @@ def main() -> int:
         threads = host_threads()
         if args.only == "decode_loop":
             print(json.dumps(decode_loop(args, threads)), file=sys.stderr)
+        elif args.only == "needle3":
+            print(json.dumps(needle3_loop(args, threads)), file=sys.stderr)
         elif args.only == "codebook":
             codebook_lines(args)
         elif args.only == "batch":
@@ -654,6 +749,10 @@ def main() -> int:
     if not args.no_decode_loop:
         loop = decode_loop(args, threads)
 
+    n3 = None
+    if not args.no_decode_loop:
+        n3 = needle3_loop(args, threads)
+
     cpu = None
     if not args.no_cpu:
         cpu = cpu_baseline(main_case, args.cpu_seconds)
@@ -686,6 +785,7 @@ def main() -> int:
         "attention": attention,
         "needle3_inputs": needle3,
         "decode_loop": loop,
+        "needle3_decode": n3,
     }
     main_case.close()
     print(json.dumps(line), flush=True)

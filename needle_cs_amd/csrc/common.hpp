@@ -270,4 +270,66 @@ __device__ __forceinline__ float exp_poly(float x)
     return y * scale;
 }
 
+// Sum of an int over the 64 lanes of a wave (exact), in every lane.
+__device__ __forceinline__ int wave_sum_i32(int v)
+{
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
+    return v;
+}
+
+// Scalar.Hadamard (Scalar.cs:76-89) of one 128-element group held by a wave:
+// lane e holds elements e (v0) and e + 64 (v1).  Butterfly stage s < 64
+// pairs lanes e and e ^ s, stage 64 pairs v0 with v1; the lower element of a
+// pair becomes a + b, the upper a - b, exactly as the scalar loop computes
+// them (the pairs of a stage are independent), then the 1/sqrt(128) scale.
+__device__ __forceinline__ void hadamard_wave(float& v0, float& v1)
+{
+    const int lane = threadIdx.x & 63;
+    for (int s = 1; s < 64; s <<= 1) {
+        const float p0 = __shfl_xor(v0, s);
+        const float p1 = __shfl_xor(v1, s);
+        const bool upper = (lane & s) != 0;
+        v0 = upper ? p0 - v0 : v0 + p0;
+        v1 = upper ? p1 - v1 : v1 + p1;
+    }
+    const float a = v0, b = v1;
+    v0 = (a + b) * 0.08838834764831845f;
+    v1 = (a - b) * 0.08838834764831845f;
+}
+
+// The rest of Quant.Prepare's scalar branch (Quant.cs:473-488) for one
+// Hadamard-rotated group held by a wave (as hadamard_wave leaves it):
+// QuantizeInt8 (absmax / 127), the Planes permutation (Scalar.cs:91-111:
+// destination d takes quantized[src(d)]) into dst[128], and lane 0 writes the
+// group's scale and offset 63 * sum(q).
+__device__ __forceinline__ void prepare_group_wave(float v0, float v1, int bits, int8_t* dst, float* scale_out,
+                                                   float* offset_out)
+{
+    const int lane = threadIdx.x & 63;
+    const float peak = wave_max(fmaxf(fabsf(v0), fabsf(v1)));
+    const float scale = peak > 0.0f ? peak / 127.0f : 1.0f;
+    const float inverse = 1.0f / scale;
+    const int q0 = ref_quantize_one(v0, inverse);
+    const int q1 = ref_quantize_one(v1, inverse);
+    const int sum = wave_sum_i32(q0 + q1);
+#pragma unroll
+    for (int k = 0; k < 2; k++) {
+        const int d = lane + 64 * k;
+        int sidx;
+        if (bits == 2) {
+            sidx = 4 * (d & 31) + (d >> 5);              // p*32 + j <- 4j + p
+        } else {
+            const int half = d >> 6, r = d & 63;
+            sidx = half * 64 + 2 * (r & 31) + (r >> 5);  // half*64 + p*32 + j <- half*64 + 2j + p
+        }
+        const int a = __shfl(q0, sidx & 63);
+        const int b = __shfl(q1, sidx & 63);
+        dst[d] = static_cast<int8_t>(sidx < 64 ? a : b);
+    }
+    if (lane == 0) {
+        *scale_out = scale;
+        *offset_out = 63.0f * (float)sum;
+    }
+}
+
 }  // namespace nhip

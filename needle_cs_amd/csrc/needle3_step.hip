@@ -28,6 +28,7 @@
 // restatement.
 #include <algorithm>
 #include <cmath>
+#include <cstdlib>
 #include <cstring>
 #include <string>
 #include <vector>
@@ -49,7 +50,11 @@ constexpr int kLanes = 4;
 constexpr int kEngramHistory = 9;
 constexpr int kEngramTaps = 4;
 constexpr int kThreads = 256;
-constexpr int kMaxStream = 4096;  // 4 * dim floats staged in LDS (dim <= 1024)
+constexpr int kWaves = kThreads / 64;
+constexpr int kMaxDim = 1024;
+constexpr int kPer = kMaxDim / kThreads;    // elements of a dim-row per thread: c = threadIdx.x + kThreads * q
+constexpr int kMaxStream = kLanes * kMaxDim;
+constexpr int kCondPer = 8 * kMaxDim / kThreads;  // condition-weight entries per thread
 
 __device__ __forceinline__ float sigmoid_poly(float x) { return 1.0f / (1.0f + exp_poly(-x)); }
 
@@ -58,14 +63,49 @@ __device__ __forceinline__ float clamp_q(float v)
     return fminf(fmaxf(ref_round_even(v), -128.0f), 127.0f);
 }
 
-// Scalar.SumOfSquares over n floats of LDS (one lane, ascending), then
-// Ops.InverseRms: 1 / sqrt(sum / n + 1e-6).
-__device__ __forceinline__ float inverse_rms_lane(const float* x, int n)
+__device__ __forceinline__ int col_of(int q) { return (int)threadIdx.x + kThreads * q; }
+
+// The sequential sum ((0 + v[0]) + v[1]) + ... + v[n-1] of n floats in LDS,
+// run by one lane: the scalar reductions' order (Scalar.SumOfSquares /
+// Scalar.Dot with the products formed beforehand -- each product is rounded
+// before it is added, as in `sum += x[i] * y[i]` without contraction).  n is
+// a multiple of 64 and v is 16-byte aligned with kChainPad readable floats
+// past n: the loads run one 32-float batch ahead of the dependent adds.
+// Different lanes may run different chains at once.
+constexpr int kChainPad = 32;
+
+__device__ __forceinline__ float chain_sum(const float* v, int n)
 {
+    const float4* p = reinterpret_cast<const float4*>(v);
     float sum = 0.0f;
-    for (int i = 0; i < n; i++) sum = sum + x[i] * x[i];
-    return 1.0f / sqrtf(sum / (float)n + 1e-6f);
+    float4 a[8], b[8];
+#pragma unroll
+    for (int j = 0; j < 8; j++) a[j] = p[j];
+    for (int k = 0; k < (n >> 2); k += 16) {
+#pragma unroll
+        for (int j = 0; j < 8; j++) b[j] = p[k + 8 + j];
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            sum = sum + a[j].x;
+            sum = sum + a[j].y;
+            sum = sum + a[j].z;
+            sum = sum + a[j].w;
+        }
+#pragma unroll
+        for (int j = 0; j < 8; j++) a[j] = p[k + 16 + j];  // the last round reads the padding
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            sum = sum + b[j].x;
+            sum = sum + b[j].y;
+            sum = sum + b[j].z;
+            sum = sum + b[j].w;
+        }
+    }
+    return sum;
 }
+
+// Ops.InverseRms of a sum of squares over n elements
+__device__ __forceinline__ float inverse_rms_of(float sum, int n) { return 1.0f / sqrtf(sum / (float)n + 1e-6f); }
 
 // Maximum of |v| over the block (order-free).
 __device__ __forceinline__ float block_peak(float v, float* red)
@@ -74,9 +114,55 @@ __device__ __forceinline__ float block_peak(float v, float* red)
     if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
     __syncthreads();
     float m = red[0];
-    for (int w = 1; w < (int)(blockDim.x >> 6); w++) m = fmaxf(m, red[w]);
+    for (int w = 1; w < kWaves; w++) m = fmaxf(m, red[w]);
     __syncthreads();
     return m;
+}
+
+// The int8 round trip of the fused norms and of Quant.FakeA8 on an LDS row
+// d[0..n): peak = max |d|, scale = peak > 0 ? peak / 127 : 1, then
+// d = clamp(RoundEven(d * (1 / scale))) * scale (Scalar.cs:55-65).
+__device__ __forceinline__ void fake_row(float* d, int n, float* red)
+{
+    float peak = 0.0f;
+    for (int c = threadIdx.x; c < n; c += kThreads) peak = fmaxf(peak, fabsf(d[c]));
+    peak = block_peak(peak, red);
+    const float scale = peak > 0.0f ? peak / 127.0f : 1.0f;
+    const float round = 1.0f / scale;
+    for (int c = threadIdx.x; c < n; c += kThreads) d[c] = clamp_q(d[c] * round) * scale;
+    __syncthreads();
+}
+
+// Prepared activations (Quant.Activations): row t's values at values + t * cols,
+// its group scales and offsets at scales / offsets + t * stride.
+struct Act {
+    int8_t* values;
+    float* scales;
+    float* offsets;
+};
+
+// Quant.Prepare (Quant.cs:473-488) of an LDS row of `cols` floats into row t
+// of act: wave w takes groups w, w + 4, ...
+__device__ __forceinline__ void prepare_row(const float* v, int cols, int bits, const Act& act, int stride, int t)
+{
+    const int lane = threadIdx.x & 63;
+    for (int g = threadIdx.x >> 6; g < cols / 128; g += kWaves) {
+        float v0 = v[g * 128 + lane], v1 = v[g * 128 + 64 + lane];
+        hadamard_wave(v0, v1);
+        prepare_group_wave(v0, v1, bits, act.values + (size_t)t * cols + g * 128, act.scales + (size_t)t * stride + g,
+                           act.offsets + (size_t)t * stride + g);
+    }
+}
+
+// Sum of squares of an LDS row by one lane, as Ops.InverseRms needs it; the
+// squares go to sq first (all threads), then lane 0 chains them.
+__device__ __forceinline__ float row_inverse_rms(const float* x, float* sq, int n, float* slot)
+{
+    for (int c = threadIdx.x; c < n; c += kThreads) sq[c] = x[c] * x[c];
+    __syncthreads();
+    if (threadIdx.x == 0) *slot = inverse_rms_of(chain_sum(sq, n), n);
+    __syncthreads();
+    return *slot;
 }
 
 // ---------------------------------------------------------- gathers --
@@ -85,125 +171,63 @@ struct Book {
     float levels[16];
 };
 
-// Scalar.DecodeRow of one 128-group into LDS g[128] (thread i < 128 takes
-// element i), then Scalar.Hadamard's butterflies (strides 1..64, each an
-// exact pair a + b, a - b) and the scale.
-__device__ __forceinline__ void gather_group(const uint8_t* raw, int rows, int cols, int bits, const Book& book, int row,
-                                             int group, float* g)
+// Quant.GatherRow of group `group` of row `row` (Scalar.DecodeRow, then
+// Scalar.Hadamard), held by a wave as hadamard_wave leaves it.
+__device__ __forceinline__ void gather_group_wave(const uint8_t* raw, int rows, int cols, int bits, const Book& book,
+                                                  int row, int group, float& v0, float& v1)
 {
-    const int i = threadIdx.x;
-    if (i < 128) {
-        const int groups = cols / 128;
-        const uint8_t* idx = raw + (size_t)row * cols * bits / 8;
-        const uint16_t* norms = reinterpret_cast<const uint16_t*>(raw + (size_t)rows * cols * bits / 8);
-        const float norm = ref_half_to_single(norms[(size_t)row * groups + group]);
-        const int code = bits == 2 ? (idx[group * 32 + i / 4] >> (i % 4 * 2)) & 3 : (idx[group * 64 + i / 2] >> (i % 2 * 4)) & 15;
-        g[i] = book.levels[code] * norm;
+    const int lane = threadIdx.x & 63;
+    const int groups = cols / 128;
+    const uint8_t* idx = raw + (size_t)row * cols * bits / 8;
+    const uint16_t* norms = reinterpret_cast<const uint16_t*>(raw + (size_t)rows * cols * bits / 8);
+    const float norm = ref_half_to_single(norms[(size_t)row * groups + group]);
+    int c0, c1;
+    if (bits == 2) {
+        c0 = (idx[group * 32 + lane / 4] >> (lane % 4 * 2)) & 3;
+        c1 = (idx[group * 32 + (lane + 64) / 4] >> (lane % 4 * 2)) & 3;
+    } else {
+        c0 = (idx[group * 64 + lane / 2] >> (lane % 2 * 4)) & 15;
+        c1 = (idx[group * 64 + (lane + 64) / 2] >> (lane % 2 * 4)) & 15;
     }
-    __syncthreads();
-    for (int stride = 1; stride < 128; stride <<= 1) {
-        if (i < 64) {
-            const int block = (i / stride) * stride * 2, k = block + i % stride;
-            const float a = g[k], b = g[k + stride];
-            g[k] = a + b;
-            g[k + stride] = a - b;
-        }
-        __syncthreads();
-    }
-    if (i < 128) g[i] = g[i] * 0.08838834764831845f;
-    __syncthreads();
+    v0 = book.levels[c0] * norm;
+    v1 = book.levels[c1] * norm;
+    hadamard_wave(v0, v1);
 }
 
 // Embedding (ForwardBatch, Engine.cs:2310-2316): GatherRow of the token's
-// row, x += (sqrt(dim) - 1) * x, copied to the four lanes of the stream.
-__global__ __launch_bounds__(128) void n3_embed_kernel(const uint8_t* raw, int rows, int dim, int bits, Book book,
-                                                       const int32_t* tokens, float scale_m1, float* stream)
+// row, x += (sqrt(dim) - 1) * x, copied to the four lanes of the stream; then
+// the first layer's RmsFakeA8 of the stream and its 4-bit Prepare.
+__global__ __launch_bounds__(kThreads) void n3_embed_kernel(const uint8_t* raw, int rows, int dim, int bits, Book book,
+                                                            const int32_t* tokens, float scale_m1, float* stream,
+                                                            Act act, int stride)
 {
-    __shared__ float g[128];
+    __shared__ __align__(16) float s[kMaxStream];
+    __shared__ __align__(16) float sq[kMaxStream + kChainPad];
+    __shared__ float red[kWaves];
+    __shared__ float inv_s;
     const int t = blockIdx.x;
+    const int lane = threadIdx.x & 63;
     const int token = tokens[t];
     float* row = stream + (size_t)t * kLanes * dim;
-    for (int grp = 0; grp < dim / 128; grp++) {
-        gather_group(raw, rows, dim, bits, book, token, grp, g);
-        const float v = g[threadIdx.x];
-        const float x = v + scale_m1 * v;
-        for (int lane = 0; lane < kLanes; lane++) row[lane * dim + grp * 128 + threadIdx.x] = x;
-        __syncthreads();
-    }
-}
-
-// The engram input of ApplyEngramBatch (Engine.cs:2404-2414): every table's
-// GatherRow (zeros for row -1), then Quant.FakeA8 of the row.
-__global__ __launch_bounds__(128) void n3_engram_gather_kernel(const uint8_t* raw, int rows, int sub, int bits, Book book,
-                                                               const int32_t* erows, int tables, int dim, float* out)
-{
-    __shared__ float g[128];
-    __shared__ float red[4];
-    const int t = blockIdx.x;
-    float* row = out + (size_t)t * dim;
-    for (int table = 0; table < tables; table++) {
-        const int r = erows[t * tables + table];
-        for (int grp = 0; grp < sub / 128; grp++) {
-            if (r < 0) {
-                row[table * sub + grp * 128 + threadIdx.x] = 0.0f;
-                continue;
-            }
-            gather_group(raw, rows, sub, bits, book, r, grp, g);
-            row[table * sub + grp * 128 + threadIdx.x] = g[threadIdx.x];
-            __syncthreads();
+    for (int g = threadIdx.x >> 6; g < dim / 128; g += kWaves) {
+        float v0, v1;
+        gather_group_wave(raw, rows, dim, bits, book, token, g, v0, v1);
+        const float x0 = v0 + scale_m1 * v0, x1 = v1 + scale_m1 * v1;
+        for (int l = 0; l < kLanes; l++) {
+            const int c = l * dim + g * 128 + lane;
+            row[c] = x0;
+            row[c + 64] = x1;
+            s[c] = x0;
+            s[c + 64] = x1;
         }
     }
     __syncthreads();
-    float peak = 0.0f;
-    for (int i = threadIdx.x; i < dim; i += 128) peak = fmaxf(peak, fabsf(row[i]));
-    peak = block_peak(peak, red);
-    const float scale = peak > 0.0f ? peak / 127.0f : 1.0f;
-    const float inverse = 1.0f / scale;
-    for (int i = threadIdx.x; i < dim; i += 128) row[i] = clamp_q(row[i] * inverse) * scale;
-}
-
-// ---------------------------------------------------- normalisations --
-
-enum NormMode { kRmsFake = 0, kCenteredFake = 1, kHeadFake = 2 };
-
-// kRmsFake      Scalar.RmsFakeA8 of x[row] (n floats);
-// kCenteredFake Scalar.CenteredRmsFakeA8 of x[row] with scale s;
-// kHeadFake     PrepareHeadVectors: Mix4 of the row's four lanes by 0.25,
-//               ZeroCenteredRms with s, Quant.FakeA8 (the same operations
-//               as CenteredRmsFakeA8 of the mix).
-// Row b reads row map[b] (row b without a map) and writes row b of out.
-template <int MODE>
-__global__ __launch_bounds__(kThreads) void n3_norm_fake_kernel(const float* x, int n, const float* s,
-                                                                const int32_t* map, float* out)
-{
-    __shared__ float v[kMaxStream];
-    __shared__ float red[8];
-    __shared__ float inv_s;
-    const int b = blockIdx.x;
-    const int src = map ? map[b] : b;
-    if (MODE == kHeadFake) {
-        const float* r = x + (size_t)src * kLanes * n;
-        for (int c = threadIdx.x; c < n; c += kThreads)
-            v[c] = 0.25f * r[c] + 0.25f * r[n + c] + 0.25f * r[2 * n + c] + 0.25f * r[3 * n + c];
-    } else {
-        const float* r = x + (size_t)src * n;
-        for (int c = threadIdx.x; c < n; c += kThreads) v[c] = r[c];
-    }
+    const int n = kLanes * dim;
+    const float inverse = row_inverse_rms(s, sq, n, &inv_s);
+    for (int c = threadIdx.x; c < n; c += kThreads) s[c] = s[c] * inverse;
     __syncthreads();
-    if (threadIdx.x == 0) inv_s = inverse_rms_lane(v, n);
-    __syncthreads();
-    const float inverse = inv_s;
-    float peak = 0.0f;
-    for (int c = threadIdx.x; c < n; c += kThreads) {
-        const float d = MODE == kRmsFake ? v[c] * inverse : (1.0f + s[c]) * v[c] * inverse;
-        v[c] = d;
-        peak = fmaxf(peak, fabsf(d));
-    }
-    peak = block_peak(peak, red);
-    const float scale = peak > 0.0f ? peak / 127.0f : 1.0f;
-    const float round = 1.0f / scale;
-    float* o = out + (size_t)b * n;
-    for (int c = threadIdx.x; c < n; c += kThreads) o[c] = clamp_q(v[c] * round) * scale;
+    fake_row(s, n, red);
+    prepare_row(s, n, 4, act, stride, t);
 }
 
 // ----------------------------------------------- hyper-connection mix --
@@ -220,49 +244,102 @@ struct HyperArgs {
     float* residual;
     float* post_gate;  // [rows][4]
     float* mix;        // [rows][16]
+    const float* norm_in;
+    // engram layers: the gathered engram input instead of the attention norm
+    const uint8_t* tables;
+    int table_rows, table_cols, table_bits, tables_count;
+    Book book;
+    const int32_t* erows;
+    Act act;
+    int stride;
 };
 
 // RunLayerBatch's per-row mix (Engine.cs:2366-2381): hpre / postGate by
 // Sigmoid, Mix4 of the lanes into input and residual, Sinkhorn4x4 of the
-// residual-mix logits.
+// residual-mix logits.  Wave 0 runs Sinkhorn4x4 with one lane per matrix
+// entry (lane e = 4a + c, repeated across the wave): every lane of a row or
+// column forms the same left-to-right sum of its four entries, so each
+// normalisation is Scalar.Sinkhorn4x4's.  Then, on layers without an engram,
+// RunAttentionBatch's CenteredRmsFakeA8 of the residual and its 2-bit Prepare
+// (Engine.cs:2487-2490); on engram layers, ApplyEngramBatch's input
+// (Engine.cs:2404-2414): every table's GatherRow (zeros for row -1),
+// Quant.FakeA8 and the 2-bit Prepare.
 __global__ __launch_bounds__(kThreads) void n3_hyper_kernel(HyperArgs a)
 {
+    __shared__ __align__(16) float x[kMaxDim];
+    __shared__ __align__(16) float sq[kMaxDim + kChainPad];
     __shared__ float hpre[4];
+    __shared__ float red[kWaves];
+    __shared__ float inv_s;
     const int t = blockIdx.x;
     const int i = threadIdx.x;
-    if (i < 4) {
-        hpre[i] = sigmoid_poly(a.a_pre[0] * a.pre_out[t * a.ld4 + i] + a.b_pre[i] + (i == a.lane ? 4.0f : -4.0f));
-        a.post_gate[t * 4 + i] =
-            2.0f * sigmoid_poly(a.a_post[0] * a.post_out[t * a.ld4 + i] + a.b_post[i] + (i == a.lane ? 0.0f : -4.0f));
-    }
-    if (i == 64) {  // Scalar.Sinkhorn4x4
-        float lg[16], r[16];
-        for (int k = 0; k < 16; k++) lg[k] = a.a_res[0] * a.res_out[t * a.ld16 + k] + a.b_res[k];
-        for (int row = 0; row < 4; row++) {
-            const float peak = fmaxf(fmaxf(lg[row * 4], lg[row * 4 + 1]), fmaxf(lg[row * 4 + 2], lg[row * 4 + 3]));
-            for (int c = 0; c < 4; c++) r[row * 4 + c] = exp_poly(lg[row * 4 + c] - peak);
-        }
-        for (int it = 0; it < 20; it++) {
-            for (int row = 0; row < 4; row++) {
-                const float sum = r[row * 4] + r[row * 4 + 1] + r[row * 4 + 2] + r[row * 4 + 3];
-                for (int c = 0; c < 4; c++) r[row * 4 + c] = r[row * 4 + c] / sum;
-            }
-            for (int c = 0; c < 4; c++) {
-                const float sum = r[c] + r[4 + c] + r[8 + c] + r[12 + c];
-                if (sum > 0.0f)
-                    for (int row = 0; row < 4; row++) r[row * 4 + c] = r[row * 4 + c] / sum;
-            }
-        }
-        for (int k = 0; k < 16; k++) a.mix[t * 16 + k] = r[k];
-    }
-    __syncthreads();
     const int dim = a.dim;
     const float* s = a.stream + (size_t)t * kLanes * dim;
-    for (int c = i; c < dim; c += kThreads) {
-        const float u = hpre[0] * s[c] + hpre[1] * s[dim + c] + hpre[2] * s[2 * dim + c] + hpre[3] * s[3 * dim + c];
-        a.input[(size_t)t * dim + c] = u;
-        a.residual[(size_t)t * dim + c] = u;
+    float sv[kPer][kLanes], sn[kPer];
+#pragma unroll
+    for (int q = 0; q < kPer; q++) {
+        const int c = col_of(q);
+        if (c < dim) {
+#pragma unroll
+            for (int l = 0; l < kLanes; l++) sv[q][l] = s[l * dim + c];
+            sn[q] = a.norm_in[c];
+        }
     }
+    if (i < 64) {
+        const int e = i & 15, row = e >> 2, col = e & 3;
+        const float lg = a.a_res[0] * a.res_out[t * a.ld16 + e] + a.b_res[e];
+        const float l0 = __shfl(lg, row * 4), l1 = __shfl(lg, row * 4 + 1), l2 = __shfl(lg, row * 4 + 2),
+                    l3 = __shfl(lg, row * 4 + 3);
+        float r = exp_poly(lg - fmaxf(fmaxf(l0, l1), fmaxf(l2, l3)));
+        for (int it = 0; it < 20; it++) {
+            const float rs = __shfl(r, row * 4) + __shfl(r, row * 4 + 1) + __shfl(r, row * 4 + 2) + __shfl(r, row * 4 + 3);
+            r = r / rs;
+            const float cs = __shfl(r, col) + __shfl(r, 4 + col) + __shfl(r, 8 + col) + __shfl(r, 12 + col);
+            if (cs > 0.0f) r = r / cs;
+        }
+        if (i < 16) a.mix[t * 16 + e] = r;
+        if (i < 4) {
+            hpre[i] = sigmoid_poly(a.a_pre[0] * a.pre_out[t * a.ld4 + i] + a.b_pre[i] + (i == a.lane ? 4.0f : -4.0f));
+            a.post_gate[t * 4 + i] =
+                2.0f * sigmoid_poly(a.a_post[0] * a.post_out[t * a.ld4 + i] + a.b_post[i] + (i == a.lane ? 0.0f : -4.0f));
+        }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int q = 0; q < kPer; q++) {
+        const int c = col_of(q);
+        if (c < dim) {
+            const float u = hpre[0] * sv[q][0] + hpre[1] * sv[q][1] + hpre[2] * sv[q][2] + hpre[3] * sv[q][3];
+            a.input[(size_t)t * dim + c] = u;
+            a.residual[(size_t)t * dim + c] = u;
+            x[c] = u;
+        }
+    }
+    __syncthreads();
+    if (a.tables) {
+        const int sub = a.table_cols, per = sub / 128;
+        for (int unit = i >> 6; unit < a.tables_count * per; unit += kWaves) {
+            const int table = unit / per, g = unit % per;
+            const int r = a.erows[t * a.tables_count + table];
+            float v0 = 0.0f, v1 = 0.0f;
+            if (r >= 0) gather_group_wave(a.tables, a.table_rows, sub, a.table_bits, a.book, r, g, v0, v1);
+            sq[table * sub + g * 128 + (i & 63)] = v0;
+            sq[table * sub + g * 128 + 64 + (i & 63)] = v1;
+        }
+        __syncthreads();
+        fake_row(sq, dim, red);
+        prepare_row(sq, dim, 2, a.act, a.stride, t);
+        return;
+    }
+    const float inverse = row_inverse_rms(x, sq, dim, &inv_s);
+#pragma unroll
+    for (int q = 0; q < kPer; q++) {
+        const int c = col_of(q);
+        if (c < dim) x[c] = (1.0f + sn[q]) * x[c] * inverse;
+    }
+    __syncthreads();
+    fake_row(x, dim, red);
+    prepare_row(x, dim, 2, a.act, a.stride, t);
 }
 
 // ----------------------------------------------------------- engram --
@@ -272,12 +349,16 @@ struct EngramArgs {
     float* history;            // [slots][9][dim] of this site
     const int32_t* row_slot;
     const int32_t* run_start;  // first row of each row's run
+    const int32_t* run_end;    // whether the row ends its run
     const float* taps;         // [4][dim]
     int dilation, dim;
     const float* input;
     const float* key;
     float* residual;
     float inverse_root;        // 1 / sqrt(dim)
+    const float* norm_in;
+    Act act;
+    int stride;
 };
 
 // Row t's convolution input j (0..9): the slot's history followed by the
@@ -293,161 +374,361 @@ __device__ __forceinline__ const float* engram_frame(const EngramArgs& a, int t,
 
 // The engram's convolution, RmsUnit of the input and the key, their Dot,
 // alpha = Sigmoid(dot / sqrt(dim)) and residual += alpha * conv
-// (Engine.cs:2437-2462).
+// (Engine.cs:2437-2462), then RunAttentionBatch's CenteredRmsFakeA8 of the
+// residual and its 2-bit Prepare.  Lanes 0 and 1 run the two sums of squares
+// at once.
 __global__ __launch_bounds__(kThreads) void n3_engram_mix_kernel(EngramArgs a)
 {
-    __shared__ float ua[1024];
-    __shared__ float ub[1024];
-    __shared__ float cv[1024];
+    __shared__ __align__(16) float ua[kMaxDim];
+    __shared__ __align__(16) float ub[kMaxDim];
+    __shared__ __align__(16) float sq[2][kMaxDim + kChainPad];
+    __shared__ float inv[2];
+    __shared__ float red[kWaves];
     __shared__ float alpha_s;
     const int t = blockIdx.x;
     const int dim = a.dim;
     const float* f[kEngramTaps];
+#pragma unroll
     for (int j = 0; j < kEngramTaps; j++) f[j] = engram_frame(a, t, kEngramHistory - j * a.dilation);
-    for (int c = threadIdx.x; c < dim; c += kThreads) {
-        float o = 0.0f;
-        for (int j = 0; j < kEngramTaps; j++) o = o + a.taps[(size_t)j * dim + c] * f[j][c];
-        cv[c] = o;
-        ua[c] = a.input[(size_t)t * dim + c];
-        ub[c] = a.key[(size_t)t * dim + c];
+    float tp[kPer][kEngramTaps], fr[kPer][kEngramTaps], xv[kPer], kv[kPer], rv[kPer], sn[kPer];
+#pragma unroll
+    for (int q = 0; q < kPer; q++) {
+        const int c = col_of(q);
+        if (c < dim) {
+#pragma unroll
+            for (int j = 0; j < kEngramTaps; j++) {
+                tp[q][j] = a.taps[(size_t)j * dim + c];
+                fr[q][j] = f[j][c];
+            }
+            xv[q] = a.input[(size_t)t * dim + c];
+            kv[q] = a.key[(size_t)t * dim + c];
+            rv[q] = a.residual[(size_t)t * dim + c];
+            sn[q] = a.norm_in[c];
+        }
+    }
+    float cv[kPer];
+#pragma unroll
+    for (int q = 0; q < kPer; q++) {
+        const int c = col_of(q);
+        if (c < dim) {
+            float o = 0.0f;
+#pragma unroll
+            for (int j = 0; j < kEngramTaps; j++) o = o + tp[q][j] * fr[q][j];
+            cv[q] = o;
+            ua[c] = xv[q];
+            ub[c] = kv[q];
+            sq[0][c] = xv[q] * xv[q];
+            sq[1][c] = kv[q] * kv[q];
+        }
     }
     __syncthreads();
-    if (threadIdx.x == 0) {
-        const float ia = inverse_rms_lane(ua, dim);
-        const float ib = inverse_rms_lane(ub, dim);
-        float dot = 0.0f;
-        for (int c = 0; c < dim; c++) dot = dot + (ua[c] * ia) * (ub[c] * ib);
-        alpha_s = sigmoid_poly(dot * a.inverse_root);
-    }
+    if (threadIdx.x < 2) inv[threadIdx.x] = inverse_rms_of(chain_sum(sq[threadIdx.x], dim), dim);
+    __syncthreads();
+    const float ia = inv[0], ib = inv[1];
+    for (int c = threadIdx.x; c < dim; c += kThreads) sq[0][c] = (ua[c] * ia) * (ub[c] * ib);
+    __syncthreads();
+    if (threadIdx.x == 0) alpha_s = sigmoid_poly(chain_sum(sq[0], dim) * a.inverse_root);
     __syncthreads();
     const float alpha = alpha_s;
-    for (int c = threadIdx.x; c < dim; c += kThreads) {
-        float* r = a.residual + (size_t)t * dim + c;
-        *r = *r + alpha * cv[c];
-    }
-}
-
-// The slot's engram history after its run (Engine.cs:2439): the nine frames
-// before the sequence's end.  Launched after the mix (which reads the old
-// history); a block per run end, each thread owns whole columns.
-__global__ __launch_bounds__(kThreads) void n3_engram_history_kernel(EngramArgs a, const int32_t* run_end)
-{
-    const int t = blockIdx.x;
-    if (!run_end[t]) return;
-    const int n = t - a.run_start[t] + 1;  // the run's length
-    float* hist = a.history + (size_t)a.row_slot[t] * kEngramHistory * a.dim;
-    for (int c = threadIdx.x; c < a.dim; c += kThreads) {
-        float v[kEngramHistory];
-        for (int j = 0; j < kEngramHistory; j++) {
-            const int idx = n + j;  // sequence index of the new frame j
-            v[j] = idx < kEngramHistory
-                       ? hist[(size_t)idx * a.dim + c]
-                       : a.stage[((size_t)(a.run_start[t] + idx - kEngramHistory) * (kEngramHistory + 1) + kEngramHistory) * a.dim + c];
+#pragma unroll
+    for (int q = 0; q < kPer; q++) {
+        const int c = col_of(q);
+        if (c < dim) {
+            const float r = rv[q] + alpha * cv[q];
+            a.residual[(size_t)t * dim + c] = r;
+            ua[c] = r;
         }
-        for (int j = 0; j < kEngramHistory; j++) hist[(size_t)j * a.dim + c] = v[j];
     }
+    __syncthreads();
+    const float inverse = row_inverse_rms(ua, sq[1], dim, &inv[0]);
+#pragma unroll
+    for (int q = 0; q < kPer; q++) {
+        const int c = col_of(q);
+        if (c < dim) ua[c] = (1.0f + sn[q]) * ua[c] * inverse;
+    }
+    __syncthreads();
+    fake_row(ua, dim, red);
+    prepare_row(ua, dim, 2, a.act, a.stride, t);
 }
 
 // ------------------------------------------------- attention epilogue --
 
-// Scalar.GateFakeA8 on each row of x (in place): x *= Sigmoid(gate), then
-// the fake int8 round trip at the row's peak.
-__global__ __launch_bounds__(kThreads) void n3_gate_fake_kernel(float* x, const float* gate, int n)
+// Scalar.GateFakeA8 on row t of the attention output: x *= Sigmoid(gate),
+// the fake int8 round trip at the row's peak, and the 2-bit Prepare of the
+// output matmul.  On engram layers the run-end rows also move their slot's
+// engram history on (Engine.cs:2439): the nine frames before the sequence's
+// end.  This runs after every row's engram mix has read the old history.
+__global__ __launch_bounds__(kThreads) void n3_gate_kernel(const float* att, const float* gate, int n, Act act,
+                                                           int stride, EngramArgs e)
 {
-    __shared__ float red[8];
+    __shared__ __align__(16) float x[kMaxDim];
+    __shared__ float red[kWaves];
     const int t = blockIdx.x;
-    float* r = x + (size_t)t * n;
-    const float* g = gate + (size_t)t * n;
-    float peak = 0.0f;
-    for (int c = threadIdx.x; c < n; c += kThreads) {
-        const float v = r[c] * sigmoid_poly(g[c]);
-        r[c] = v;
-        peak = fmaxf(peak, fabsf(v));
+    float av[kPer], gv[kPer];
+#pragma unroll
+    for (int q = 0; q < kPer; q++) {
+        const int c = col_of(q);
+        if (c < n) {
+            av[q] = att[(size_t)t * n + c];
+            gv[q] = gate[(size_t)t * n + c];
+        }
     }
-    peak = block_peak(peak, red);
-    const float scale = peak > 0.0f ? peak / 127.0f : 1.0f;
-    const float round = 1.0f / scale;
-    for (int c = threadIdx.x; c < n; c += kThreads) r[c] = clamp_q(r[c] * round) * scale;
+#pragma unroll
+    for (int q = 0; q < kPer; q++) {
+        const int c = col_of(q);
+        if (c < n) x[c] = av[q] * sigmoid_poly(gv[q]);
+    }
+    __syncthreads();
+    fake_row(x, n, red);
+    prepare_row(x, n, 2, act, stride, t);
+    if (e.history && e.run_end[t]) {
+        const int len = t - e.run_start[t] + 1;  // the run's length
+        float* hist = e.history + (size_t)e.row_slot[t] * kEngramHistory * e.dim;
+        for (int c = threadIdx.x; c < e.dim; c += kThreads) {
+            float v[kEngramHistory];
+#pragma unroll
+            for (int j = 0; j < kEngramHistory; j++) {
+                const int idx = len + j;  // sequence index of the new frame j
+                v[j] = idx < kEngramHistory
+                           ? hist[(size_t)idx * e.dim + c]
+                           : e.stage[((size_t)(e.run_start[t] + idx - kEngramHistory) * (kEngramHistory + 1) +
+                                      kEngramHistory) * e.dim + c];
+            }
+#pragma unroll
+            for (int j = 0; j < kEngramHistory; j++) hist[(size_t)j * e.dim + c] = v[j];
+        }
+    }
 }
 
-// Scalar.PostNormAdd: residual += gate * ((1 + s) * x * (1 / rms(x))).
-__global__ __launch_bounds__(kThreads) void n3_post_norm_add_kernel(float* residual, const float* x, const float* s,
-                                                                    float gate, int n)
-{
-    __shared__ float v[1024];
-    __shared__ float inv_s;
-    const int t = blockIdx.x;
-    for (int c = threadIdx.x; c < n; c += kThreads) v[c] = x[(size_t)t * n + c];
-    __syncthreads();
-    if (threadIdx.x == 0) inv_s = inverse_rms_lane(v, n);
-    __syncthreads();
-    const float inverse = inv_s;
-    for (int c = threadIdx.x; c < n; c += kThreads) {
-        float* r = residual + (size_t)t * n + c;
-        *r = *r + gate * ((1.0f + s[c]) * v[c] * inverse);
-    }
-}
+// -------------------------------------------------------------- tail --
 
-// -------------------------------------------------------------- MLP --
-
-struct MlpArgs {
+struct TailArgs {
     float* residual;
+    const float* proj;
+    const float* post_norm;
+    float attn_gate;
     const float* pre_norm;
     const int32_t *perm_a, *perm_b;
     const float *d1, *d2, *b2, *d3, *d4, *w1a, *w1b, *w2a, *w2b, *w3a, *w3b, *cond_v, *cond_u;
     int dim, rows, cols;
+    const float* stream;     // this layer's stream
+    const float* mix;        // [rows][16]
+    const float* input;      // u
+    const float* post_gate;  // [rows][4]
+    float* next;             // the next stream
+    // the next layer's RmsFakeA8 + 4-bit Prepare (head_of == NULL), or the
+    // head rows' PrepareHeadVectors + 4-bit Prepare into row head_of[t]
+    const int32_t* head_of;
+    const float* final_norm;
+    Act act;
+    int stride;
 };
+
+// Bytes of LDS n3_tail_kernel takes for a geometry.
+size_t tail_lds_bytes(int dim, int rows, int cols)
+{
+    const size_t width = (size_t)rows * cols;
+    return sizeof(float) * (3 * width + 32 + 2 * (size_t)dim + 8 * ((size_t)dim + 4) + kChainPad + 3 * (size_t)rows * rows +
+                            3 * (size_t)cols * cols + 2 * (size_t)kLanes * dim + kChainPad);
+}
 
 // Scalar.Kron in LDS: scratch[k][c] = sum_{i < active} left[i][k] z[i][c]
 // (a chain over i per (k, c)), then result[k][c] = sum_j scratch[k][j]
-// right[j][c] (a chain over j), for k < result_rows.
+// right[j][c] (a chain over j), for k < result_rows.  Thread u owns the four
+// elements 4u .. 4u+3 (one k, four consecutive c; cols % 4 == 0) and runs
+// their chains together; each step's operands are loaded 8 steps at a time.
+// scratch rows are cols + 1 apart (kron_scratch floats in all).
+__device__ __forceinline__ int kron_scratch(int rows, int cols) { return rows * cols + 32; }
+
 __device__ __forceinline__ void kron_lds(const float* z, int active, const float* left, const float* right, int rows,
                                          int cols, int result_rows, float* scratch, float* result)
 {
-    for (int e = threadIdx.x; e < result_rows * cols; e += kThreads) {
-        const int k = e / cols, c = e % cols;
-        float sum = 0.0f;
-        for (int i = 0; i < active; i++) sum = sum + left[i * rows + k] * z[i * cols + c];
-        scratch[e] = sum;
+    const int e0 = 4 * (int)threadIdx.x;
+    const bool on = e0 < result_rows * cols;
+    const int k = on ? e0 / cols : 0, c = e0 - k * cols, ss = cols + 1;
+    float4 sum = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    if (on) {
+        for (int i0 = 0; i0 < active; i0 += 8) {
+            float lv[8];
+            float4 zv[8];
+#pragma unroll
+            for (int u = 0; u < 8; u++)
+                if (i0 + u < active) {
+                    lv[u] = left[(i0 + u) * rows + k];
+                    zv[u] = *reinterpret_cast<const float4*>(z + (i0 + u) * cols + c);
+                }
+#pragma unroll
+            for (int u = 0; u < 8; u++)
+                if (i0 + u < active) {
+                    sum.x = sum.x + lv[u] * zv[u].x;
+                    sum.y = sum.y + lv[u] * zv[u].y;
+                    sum.z = sum.z + lv[u] * zv[u].z;
+                    sum.w = sum.w + lv[u] * zv[u].w;
+                }
+        }
+        float* srow = scratch + k * ss + c;
+        srow[0] = sum.x;
+        srow[1] = sum.y;
+        srow[2] = sum.z;
+        srow[3] = sum.w;
     }
     __syncthreads();
-    for (int e = threadIdx.x; e < result_rows * cols; e += kThreads) {
-        const int k = e / cols, c = e % cols;
-        float sum = 0.0f;
-        for (int j = 0; j < cols; j++) sum = sum + scratch[k * cols + j] * right[j * cols + c];
-        result[e] = sum;
+    if (on) {
+        sum = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        for (int j0 = 0; j0 < cols; j0 += 8) {
+            float sv[8];
+            float4 rv[8];
+#pragma unroll
+            for (int u = 0; u < 8; u++) {
+                sv[u] = scratch[k * ss + j0 + u];
+                rv[u] = *reinterpret_cast<const float4*>(right + (j0 + u) * cols + c);
+            }
+#pragma unroll
+            for (int u = 0; u < 8; u++) {
+                sum.x = sum.x + sv[u] * rv[u].x;
+                sum.y = sum.y + sv[u] * rv[u].y;
+                sum.z = sum.z + sv[u] * rv[u].z;
+                sum.w = sum.w + sv[u] * rv[u].w;
+            }
+        }
+        *reinterpret_cast<float4*>(result + e0) = sum;
     }
     __syncthreads();
 }
 
-// HadamardMlp.Apply (Blocks.cs:1067-1101) with its scalar kernels, Scale 1,
-// one row per workgroup; front, back and the Kron scratch live in LDS.
-__global__ __launch_bounds__(kThreads) void n3_mlp_kernel(MlpArgs a)
+// The end of a layer for one row, in RunLayerBatch's order
+// (Engine.cs:2382-2397): Scalar.PostNormAdd of the attention output into the
+// residual, HadamardMlp.Apply (Blocks.cs:1067-1101, scalar kernels, Scale 1),
+// CombineDiff4x4's scalar branch (Ops.cs:800-812) into the next stream; then
+// the next layer's RmsFakeA8 + 4-bit Prepare of that stream, or after the
+// last layer PrepareHeadVectors (Engine.cs:920-928: Mix4 by 0.25,
+// ZeroCenteredRms, FakeA8) + 4-bit Prepare for the head rows.  The Kronecker
+// factors are staged in LDS; the condition weights' products are formed in
+// parallel and summed by eight lanes at once, each in ascending i.
+__global__ __launch_bounds__(kThreads) void n3_tail_kernel(TailArgs a)
 {
-    extern __shared__ float lds[];
-    const int width = a.rows * a.cols, dim = a.dim;
-    float* front = lds;             // width (>= the padded input)
-    float* back = front + width;    // width
-    float* scratch = back + width;  // width
-    float* norm = scratch + width;  // dim
+    extern __shared__ __align__(16) float lds[];
+    const int width = a.rows * a.cols, dim = a.dim, rr = a.rows * a.rows, cc = a.cols * a.cols, n4 = kLanes * dim;
+    const int pstride = dim + 4;      // condition products: row j at j * pstride (banks apart)
+    float* front = lds;               // width (>= the padded input)
+    float* back = front + width;      // width
+    float* scratch = back + width;    // kron_scratch
+    float* res = scratch + kron_scratch(a.rows, a.cols);  // dim
+    float* norm = res + dim;          // dim
+    float* prod = norm + dim;         // 8 * pstride (also the squares)
+    float* wl = prod + 8 * pstride + kChainPad;  // W1A, W2A, W3A
+    float* wr = wl + 3 * rr;          // W1B, W2B, W3B
+    float* ns = wr + 3 * cc;          // the next stream row, 4 * dim
+    float* nsq = ns + n4;             // its squares
     __shared__ float weights[8];
+    __shared__ float red[kWaves];
     __shared__ float inv_s;
     const int t = blockIdx.x;
-    float* res = a.residual + (size_t)t * dim;
+    // every global load of the row up front
+    float rv[kPer], pv[kPer], psv[kPer], prv[kPer], d1v[kPer], d4v[kPer], uv[kPer], sv[kPer][kLanes];
+#pragma unroll
+    for (int q = 0; q < kPer; q++) {
+        const int c = col_of(q);
+        if (c < dim) {
+            rv[q] = a.residual[(size_t)t * dim + c];
+            pv[q] = a.proj[(size_t)t * dim + c];
+            psv[q] = a.post_norm[c];
+            prv[q] = a.pre_norm[c];
+            d1v[q] = a.d1[c];
+            d4v[q] = a.d4[c];
+            uv[q] = a.input[(size_t)t * dim + c];
+#pragma unroll
+            for (int l = 0; l < kLanes; l++) sv[q][l] = a.stream[(size_t)t * n4 + l * dim + c];
+        }
+    }
+    float cu[kPer][8], d2v[kPer], b2v[kPer], d3v[kPer];
+    int pa[kPer], pb[kPer];
+#pragma unroll
+    for (int q = 0; q < kPer; q++) {
+        const int n = col_of(q);
+        if (n < width) {
+#pragma unroll
+            for (int j = 0; j < 8; j++) cu[q][j] = a.cond_u[j * width + n];
+            d2v[q] = a.d2[n];
+            b2v[q] = a.b2[n];
+            d3v[q] = a.d3[n];
+            pa[q] = a.perm_a[n];
+            pb[q] = a.perm_b[n];
+        }
+    }
+    float cvv[kCondPer], wv[kPer][6];
+#pragma unroll
+    for (int q = 0; q < kCondPer; q++) {
+        const int e = col_of(q);
+        if (e < dim * 8) cvv[q] = a.cond_v[e];
+    }
+#pragma unroll
+    for (int q = 0; q < kPer; q++) {
+        const int e = col_of(q);
+        if (e < rr) {
+            wv[q][0] = a.w1a[e];
+            wv[q][1] = a.w2a[e];
+            wv[q][2] = a.w3a[e];
+        }
+        if (e < cc) {
+            wv[q][3] = a.w1b[e];
+            wv[q][4] = a.w2b[e];
+            wv[q][5] = a.w3b[e];
+        }
+    }
+#pragma unroll
+    for (int q = 0; q < kPer; q++) {
+        const int e = col_of(q);
+        if (e < rr) {
+            wl[e] = wv[q][0];
+            wl[rr + e] = wv[q][1];
+            wl[2 * rr + e] = wv[q][2];
+        }
+        if (e < cc) {
+            wr[e] = wv[q][3];
+            wr[cc + e] = wv[q][4];
+            wr[2 * cc + e] = wv[q][5];
+        }
+    }
+    // Scalar.PostNormAdd: residual += gate * ((1 + s) * x * (1 / rms(x))), x = the attention projection
+#pragma unroll
+    for (int q = 0; q < kPer; q++) {
+        const int c = col_of(q);
+        if (c < dim) norm[c] = pv[q];
+    }
+    __syncthreads();
+    float inverse = row_inverse_rms(norm, prod, dim, &inv_s);
+#pragma unroll
+    for (int q = 0; q < kPer; q++) {
+        const int c = col_of(q);
+        if (c < dim) {
+            rv[q] = rv[q] + a.attn_gate * ((1.0f + psv[q]) * pv[q] * inverse);
+            res[c] = rv[q];
+        }
+    }
+    __syncthreads();
+    // HadamardMlp.Apply
+    inverse = row_inverse_rms(res, prod, dim, &inv_s);
+#pragma unroll
+    for (int q = 0; q < kPer; q++) {
+        const int c = col_of(q);
+        if (c < dim) norm[c] = (1.0f + prv[q]) * rv[q] * inverse;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int q = 0; q < kCondPer; q++) {  // Scalar.ConditionWeights' products
+        const int e = col_of(q);
+        if (e < dim * 8) prod[(e & 7) * pstride + (e >> 3)] = norm[e >> 3] * cvv[q];
+    }
     const int input_rows = (dim + a.cols - 1) / a.cols;
     const int output_rows = min(a.rows, (input_rows + 3) / 4 * 4);
-    for (int c = threadIdx.x; c < dim; c += kThreads) norm[c] = res[c];
-    __syncthreads();
-    if (threadIdx.x == 0) inv_s = inverse_rms_lane(norm, dim);
-    __syncthreads();
-    for (int c = threadIdx.x; c < dim; c += kThreads) norm[c] = (1.0f + a.pre_norm[c]) * norm[c] * inv_s;
-    __syncthreads();
-    if (threadIdx.x < 8) {  // Scalar.ConditionWeights: eight chains over dim
-        const int j = threadIdx.x;
-        float sum = 0.0f;
-        for (int i = 0; i < dim; i++) sum = sum + norm[i] * a.cond_v[i * 8 + j];
-        weights[j] = sum;
+#pragma unroll
+    for (int q = 0; q < kPer; q++) {
+        const int c = col_of(q);
+        if (c < input_rows * a.cols) front[c] = c < dim ? norm[c] * d1v[q] : 0.0f;
     }
+    __syncthreads();
+    if (threadIdx.x < 8) weights[threadIdx.x] = chain_sum(prod + threadIdx.x * pstride, dim);
     __syncthreads();
     if (threadIdx.x == 0) {  // Scalar.Softmax over the eight weights
         float peak = -INFINITY;
@@ -459,41 +740,75 @@ __global__ __launch_bounds__(kThreads) void n3_mlp_kernel(MlpArgs a)
         }
         for (int j = 0; j < 8; j++) weights[j] = weights[j] / total;
     }
-    for (int c = threadIdx.x; c < input_rows * a.cols; c += kThreads) front[c] = c < dim ? norm[c] * a.d1[c] : 0.0f;
-    __syncthreads();
-    kron_lds(front, input_rows, a.w1a, a.w1b, a.rows, a.cols, a.rows, scratch, back);
-    for (int n = threadIdx.x; n < width; n += kThreads) {  // Scalar.PermuteModulateActivate
-        float condition = 1.0f;
-        for (int j = 0; j < 8; j++) condition = condition + weights[j] * a.cond_u[j * width + n];
-        const float v = a.d2[n] * condition * back[a.perm_a[n]] + a.b2[n];
-        front[n] = v * sigmoid_poly(v);
+    kron_lds(front, input_rows, wl, wr, a.rows, a.cols, a.rows, scratch, back);
+#pragma unroll
+    for (int q = 0; q < kPer; q++) {  // Scalar.PermuteModulateActivate
+        const int n = col_of(q);
+        if (n < width) {
+            float condition = 1.0f;
+#pragma unroll
+            for (int j = 0; j < 8; j++) condition = condition + weights[j] * cu[q][j];
+            const float v = d2v[q] * condition * back[pa[q]] + b2v[q];
+            front[n] = v * sigmoid_poly(v);
+        }
     }
     __syncthreads();
-    kron_lds(front, a.rows, a.w2a, a.w2b, a.rows, a.cols, a.rows, scratch, back);
-    for (int n = threadIdx.x; n < width; n += kThreads) front[n] = back[a.perm_b[n]] * a.d3[n];
-    __syncthreads();
-    kron_lds(front, a.rows, a.w3a, a.w3b, a.rows, a.cols, output_rows, scratch, back);
-    for (int c = threadIdx.x; c < dim; c += kThreads) res[c] = res[c] + 1.0f * (back[c] * a.d4[c]);
-}
-
-// Ops.CombineDiff4x4's scalar branch (Ops.cs:800-812): lane i of the next
-// stream = postGate[i] * (x - u) + sum_j mix[i][j] * s_j, left to right.
-__global__ __launch_bounds__(kThreads) void n3_combine_kernel(const float* stream, const float* mix, const float* x,
-                                                              const float* u, const float* post_gate, int dim,
-                                                              float* next)
-{
-    const int t = blockIdx.x;
-    const float* s = stream + (size_t)t * kLanes * dim;
-    const float* m = mix + t * 16;
-    const float* xr = x + (size_t)t * dim;
-    const float* ur = u + (size_t)t * dim;
-    float* o = next + (size_t)t * kLanes * dim;
-    for (int e = threadIdx.x; e < kLanes * dim; e += kThreads) {
-        const int i = e / dim, c = e % dim;
-        const float* w = m + 4 * i;
-        o[e] = post_gate[t * 4 + i] * (xr[c] - ur[c]) + w[0] * s[c] + w[1] * s[dim + c] + w[2] * s[2 * dim + c] +
-               w[3] * s[3 * dim + c];
+    kron_lds(front, a.rows, wl + rr, wr + cc, a.rows, a.cols, a.rows, scratch, back);
+#pragma unroll
+    for (int q = 0; q < kPer; q++) {  // Scalar.PermuteScale
+        const int n = col_of(q);
+        if (n < width) front[n] = back[pb[q]] * d3v[q];
     }
+    __syncthreads();
+    kron_lds(front, a.rows, wl + 2 * rr, wr + 2 * cc, a.rows, a.cols, output_rows, scratch, back);
+    // Scalar.AccumulateOutput, then CombineDiff4x4 into the next stream
+    const float* m = a.mix + t * 16;
+    const float* pg = a.post_gate + t * 4;
+#pragma unroll
+    for (int q = 0; q < kPer; q++) {
+        const int c = col_of(q);
+        if (c < dim) {
+            const float x = rv[q] + 1.0f * (back[c] * d4v[q]);
+            const float y = x - uv[q];
+#pragma unroll
+            for (int l = 0; l < kLanes; l++) {
+                const float o = pg[l] * y + m[4 * l] * sv[q][0] + m[4 * l + 1] * sv[q][1] + m[4 * l + 2] * sv[q][2] +
+                                m[4 * l + 3] * sv[q][3];
+                a.next[(size_t)t * n4 + l * dim + c] = o;
+                ns[l * dim + c] = o;
+            }
+        }
+    }
+    __syncthreads();
+    if (!a.head_of) {  // the next layer's RmsFakeA8 and 4-bit Prepare
+        inverse = row_inverse_rms(ns, nsq, n4, &inv_s);
+        for (int c = threadIdx.x; c < n4; c += kThreads) ns[c] = ns[c] * inverse;
+        __syncthreads();
+        fake_row(ns, n4, red);
+        prepare_row(ns, n4, 4, a.act, a.stride, t);
+        return;
+    }
+    const int head = a.head_of[t];
+    if (head < 0) return;
+    float fv[kPer];
+#pragma unroll
+    for (int q = 0; q < kPer; q++) {
+        const int c = col_of(q);
+        if (c < dim) {
+            fv[q] = a.final_norm[c];
+            norm[c] = 0.25f * ns[c] + 0.25f * ns[dim + c] + 0.25f * ns[2 * dim + c] + 0.25f * ns[3 * dim + c];
+        }
+    }
+    __syncthreads();
+    inverse = row_inverse_rms(norm, nsq, dim, &inv_s);
+#pragma unroll
+    for (int q = 0; q < kPer; q++) {
+        const int c = col_of(q);
+        if (c < dim) norm[c] = (1.0f + fv[q]) * norm[c] * inverse;
+    }
+    __syncthreads();
+    fake_row(norm, dim, red);
+    prepare_row(norm, dim, 4, a.act, a.stride, head);
 }
 
 }  // namespace
@@ -550,8 +865,9 @@ struct nhip_ctx {
     float *qkv_hist = nullptr, *engram_hist = nullptr, *snap_qkv = nullptr, *snap_engram = nullptr;
     std::vector<int32_t> len, marked, prev, snap_prev;
     float *rope_cos = nullptr, *rope_sin = nullptr;
-    // scratch for max_rows rows
-    float *stream = nullptr, *next = nullptr, *normed = nullptr, *input = nullptr, *residual = nullptr,
+    // scratch for max_rows rows (stream_a holds the embedding, the layers
+    // alternate between the two stream buffers)
+    float *stream_a = nullptr, *stream_b = nullptr, *normed = nullptr, *input = nullptr, *residual = nullptr,
           *raw = nullptr, *gate = nullptr, *att = nullptr, *proj = nullptr, *key = nullptr, *stage = nullptr,
           *ein = nullptr, *pre_out = nullptr, *post_out = nullptr, *res_out = nullptr, *post_gate = nullptr,
           *mix = nullptr, *qs = nullptr, *logits = nullptr, *act_s = nullptr, *act_o = nullptr;
@@ -564,17 +880,27 @@ struct nhip_ctx {
     size_t topk_ws_bytes = 0;
     int32_t *d_topk_idx = nullptr, *d_argmax = nullptr;
     float* d_topk_lp = nullptr;
-    size_t mlp_lds = 0;
+    size_t tail_lds = 0;
     hipStream_t stream_h = nullptr;
+    struct Graph {
+        int rows, heads, k;
+        bool argmax;
+        hipGraphExec_t exec;
+    };
+    std::vector<Graph> graphs;  // captured steps, by their shape
     std::vector<void*> allocations;
 };
 
 namespace {
 
 // per-row step inputs: token, slot, position, attention span of the global
-// layers (first, count) and of the sliding-window layers, head rows, the
-// first row of the row's run, whether the row ends its run
-enum { kInTokens, kInSlots, kInPos, kInFirst, kInCount, kInFirstW, kInCountW, kInHeads, kInRunStart, kInRunEnd, kInSections };
+// layers (first, count) and of the sliding-window layers, the row's index
+// among the head rows (-1: none), the first row of the row's run, whether
+// the row ends its run
+enum {
+    kInTokens, kInSlots, kInPos, kInFirst, kInCount, kInFirstW, kInCountW, kInHeadOf, kInRunStart, kInRunEnd,
+    kInSections
+};
 
 int32_t* in(nhip_ctx* c, int32_t* base, int section) { return base + (size_t)section * c->max_rows; }
 int32_t* in_erows(nhip_ctx* c, int32_t* base) { return base + (size_t)kInSections * c->max_rows; }
@@ -683,8 +1009,9 @@ int32_t load_model(nhip_ctx* c)
                  "conv taps %u, engram taps %u, dim %d (a multiple of 128 up to 1024)", h[19], h[23], c->dim);
     NHIP_REQUIRE(c->hada_cols % 8 == 0 && c->hada_rows * c->hada_cols == hada_n && hada_n >= c->dim,
                  "MLP size %d must split into rows x cols (cols divisible by 8) covering dim %d", hada_n, c->dim);
-    NHIP_REQUIRE(c->heads > 0 && c->kv > 0 && c->heads % c->kv == 0 && c->heads * c->vd <= 1024, "heads %d / kv %d",
-                 c->heads, c->kv);
+    NHIP_REQUIRE(c->heads > 0 && c->kv > 0 && c->heads % c->kv == 0 && c->heads * c->vd <= 1024 &&
+                     (c->heads * c->vd) % 128 == 0,
+                 "heads %d / kv %d (heads * 64 a multiple of 128 up to 1024)", c->heads, c->kv);
     NHIP_REQUIRE(c->site_count >= 0 && c->site_count <= 16 && c->order_count >= 0 && c->order_count <= 4,
                  "engram sites %d, orders %d", c->site_count, c->order_count);
     NHIP_REQUIRE(c->site_count == 0 || (c->engram_tables % std::max(c->order_count, 1) == 0 &&
@@ -809,7 +1136,7 @@ int32_t alloc_state(nhip_ctx* c)
         (rc = ctx_alloc(c, &c->engram_hist, ehist)) || (rc = ctx_alloc(c, &c->snap_engram, ehist)) ||
         (rc = ctx_alloc(c, &c->rope_cos, (size_t)c->capacity * c->qk / 2)) ||
         (rc = ctx_alloc(c, &c->rope_sin, (size_t)c->capacity * c->qk / 2)) ||
-        (rc = ctx_alloc(c, &c->stream, (size_t)R * sw)) || (rc = ctx_alloc(c, &c->next, (size_t)R * sw)) ||
+        (rc = ctx_alloc(c, &c->stream_a, (size_t)R * sw)) || (rc = ctx_alloc(c, &c->stream_b, (size_t)R * sw)) ||
         (rc = ctx_alloc(c, &c->normed, (size_t)R * sw)) || (rc = ctx_alloc(c, &c->input, (size_t)R * d)) ||
         (rc = ctx_alloc(c, &c->residual, (size_t)R * d)) || (rc = ctx_alloc(c, &c->raw, (size_t)R * all)) ||
         (rc = ctx_alloc(c, &c->gate, (size_t)R * ow)) || (rc = ctx_alloc(c, &c->att, (size_t)R * ow)) ||
@@ -856,26 +1183,23 @@ int32_t alloc_state(nhip_ctx* c)
     c->prev.assign(2 * c->slots, 0);
     c->snap_prev.assign(2 * c->slots, 0);
     const size_t width = (size_t)c->hada_rows * c->hada_cols;
-    c->mlp_lds = (3 * width + d) * sizeof(float);
-    NHIP_REQUIRE(c->mlp_lds <= 160 * 1024, "the MLP's %zu bytes of LDS exceed the CU's", c->mlp_lds);
-    if (c->mlp_lds > 64 * 1024)
-        NHIP_CHECK_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(n3_mlp_kernel),
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)c->mlp_lds));
+    NHIP_REQUIRE(width <= 4 * kThreads, "MLP size %zu above %d", width, 4 * kThreads);
+    c->tail_lds = tail_lds_bytes(d, c->hada_rows, c->hada_cols);
+    NHIP_REQUIRE(c->tail_lds <= 160 * 1024, "the layer tail's %zu bytes of LDS exceed the CU's", c->tail_lds);
+    if (c->tail_lds > 64 * 1024)
+        NHIP_CHECK_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(n3_tail_kernel),
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)c->tail_lds));
     return NHIP_OK;
 }
 
-int32_t prepare(nhip_ctx* c, const float* x, int rows, int cols, int bits)
-{
-    const int stride = (cols / 128 + 7) / 8 * 8;
-    return nhip_prepare_dev(x, rows, cols, bits, c->act_v, c->act_s, c->act_o, stride, c->stream_h);
-}
+int stride_of(int cols) { return (cols / 128 + 7) / 8 * 8; }
 
 // Rows [row0, row0 + count) of w over the prepared activations of `rows`
 // rows: y[t * ldy + n] for those n.
 int32_t matmul(nhip_ctx* c, const nhip_weights* w, int rows, int cols, int row0, int count, float* y, int ldy)
 {
-    const int stride = (cols / 128 + 7) / 8 * 8;
-    return nhip_matmul_cq_dev(w, c->act_v, c->act_s, c->act_o, stride, rows, y, ldy, row0, row0 + count, c->stream_h);
+    return nhip_matmul_cq_dev(w, c->act_v, c->act_s, c->act_o, stride_of(cols), rows, y, ldy, row0, row0 + count,
+                              c->stream_h);
 }
 
 // EngineCore.EngramHashRowsBatch (Engine.cs:2631-2656) on the host.
@@ -907,70 +1231,75 @@ void engram_rows(const nhip_ctx* c, const int32_t* tokens, const int32_t* row_sl
 }
 
 
+// One step over `rows` rows whose inputs are on the device; `heads` distinct
+// head rows.  Per layer: the phi matmuls (one launch), the hyper-connection
+// mix with the attention norm (or the engram input) and its Prepare, on
+// engram layers the key / value matmuls and the engram blend with the
+// attention norm, the Q/K/V/Gate matmuls, the attention inputs, attention,
+// the gate with the output matmul's Prepare, the output matmul, and the
+// layer tail (PostNormAdd, MLP, CombineDiff4x4, the next layer's norm and
+// Prepare -- or the head rows' after the last layer).
 int32_t enqueue_step(nhip_ctx* c, int rows, int heads, int k, bool argmax)
 {
     hipStream_t s = c->stream_h;
     const int d = c->dim, sw = kLanes * d, L = c->layers, H = c->heads, KV = c->kv, qw = H * c->qk,
               kw = KV * c->qk, vw = KV * c->vd, ow = H * c->vd, all = qw + kw + vw;
-    const int stride_d = (d / 128 + 7) / 8 * 8;
+    const int stride4 = stride_of(sw), stride_d = stride_of(d), stride_o = stride_of(ow);
+    const Act act{c->act_v, c->act_s, c->act_o};
     int32_t rc;
+    float* cur = c->stream_a;
+    float* nxt = c->stream_b;
     // EngineCore's embeddingScale = sqrt(dim) (Engine.cs:123), host sqrtf
     const float emb_scale_m1 = std::sqrt((float)d) - 1.0f;
-    hipLaunchKernelGGL(n3_embed_kernel, dim3(rows), dim3(128), 0, s, c->embedding_raw, c->vocab, d, c->embedding_bits,
-                       c->book4, in(c, c->d_in, kInTokens), emb_scale_m1, c->stream);
+    hipLaunchKernelGGL(n3_embed_kernel, dim3(rows), dim3(kThreads), 0, s, c->embedding_raw, c->vocab, d,
+                       c->embedding_bits, c->book4, in(c, c->d_in, kInTokens), emb_scale_m1, cur, act, stride4);
     NHIP_CHECK_HIP(hipGetLastError());
     for (int l = 0; l < L; l++) {
         const N3Layer& w = c->layer[l];
-        // hyper-connection phi (RunLayerBatch, Engine.cs:2356-2364)
-        hipLaunchKernelGGL(n3_norm_fake_kernel<kRmsFake>, dim3(rows), dim3(kThreads), 0, s, c->stream, sw, nullptr,
-                           nullptr, c->normed);
-        NHIP_CHECK_HIP(hipGetLastError());
-        if ((rc = prepare(c, c->normed, rows, sw, 4)) ||
-            (rc = matmul(c, c->phi_pre, rows, sw, l * 4, 4, c->pre_out, 4 * L)) ||
-            (rc = matmul(c, c->phi_post, rows, sw, l * 4, 4, c->post_out, 4 * L)) ||
-            (rc = matmul(c, c->phi_res, rows, sw, l * 16, 16, c->res_out, 16 * L)))
-            return rc;
-        HyperArgs ha{c->stream, c->pre_out + l * 4, c->post_out + l * 4, c->res_out + l * 16, 4 * L, 16 * L,
-                     c->a_pre + l, c->a_post + l, c->a_res + l, c->b_pre + 4 * l, c->b_post + 4 * l,
-                     c->b_res + 16 * l, l % kLanes, d, c->input, c->residual, c->post_gate, c->mix};
-        hipLaunchKernelGGL(n3_hyper_kernel, dim3(rows), dim3(kThreads), 0, s, ha);
-        NHIP_CHECK_HIP(hipGetLastError());
-        // engram (ApplyEngramBatch, Engine.cs:2399-2463)
+        // hyper-connection phi (RunLayerBatch, Engine.cs:2356-2364): the
+        // three matrices in one launch (every layer's rows; this layer's are
+        // read back)
+        const nhip_weights* phw[3] = {c->phi_pre, c->phi_post, c->phi_res};
+        float* phy[3] = {c->pre_out, c->post_out, c->res_out};
+        const int32_t phl[3] = {4 * L, 4 * L, 16 * L};
+        if ((rc = nhip_matmul_batch_dev(phw, 3, c->act_v, c->act_s, c->act_o, stride4, rows, phy, phl, s))) return rc;
         int site = -1;
         for (int k2 = 0; k2 < c->site_count; k2++)
             if (c->sites[k2] == l) site = k2;
-        if (site >= 0) {
-            const N3Site& st = c->site[site];
-            hipLaunchKernelGGL(n3_engram_gather_kernel, dim3(rows), dim3(128), 0, s, st.tables, st.table_rows,
-                               st.table_cols, st.table_bits, st.table_bits == 2 ? c->book2 : c->book4,
-                               in_erows(c, c->d_in), c->engram_tables, d, c->ein);
-            NHIP_CHECK_HIP(hipGetLastError());
-            if ((rc = prepare(c, c->ein, rows, d, 2))) return rc;
-            const nhip_weights* jw[2] = {st.key, st.value};
+        const N3Site* st = site >= 0 ? &c->site[site] : nullptr;
+        HyperArgs ha{cur, c->pre_out + l * 4, c->post_out + l * 4, c->res_out + l * 16, 4 * L, 16 * L,
+                     c->a_pre + l, c->a_post + l, c->a_res + l, c->b_pre + 4 * l, c->b_post + 4 * l,
+                     c->b_res + 16 * l, l % kLanes, d, c->input, c->residual, c->post_gate, c->mix, w.norm_in,
+                     st ? st->tables : nullptr, st ? st->table_rows : 0, st ? st->table_cols : 0,
+                     st ? st->table_bits : 0, c->engram_tables, st && st->table_bits == 2 ? c->book2 : c->book4,
+                     in_erows(c, c->d_in), act, stride_d};
+        hipLaunchKernelGGL(n3_hyper_kernel, dim3(rows), dim3(kThreads), 0, s, ha);
+        NHIP_CHECK_HIP(hipGetLastError());
+        EngramArgs ea{};
+        if (st) {  // engram (ApplyEngramBatch, Engine.cs:2399-2463)
+            const nhip_weights* jw[2] = {st->key, st->value};
             float* jy[2] = {c->key, c->stage + (size_t)kEngramHistory * d};
             const int32_t jl[2] = {d, (kEngramHistory + 1) * d};
             if ((rc = nhip_matmul_batch_dev(jw, 2, c->act_v, c->act_s, c->act_o, stride_d, rows, jy, jl, s))) return rc;
-            EngramArgs ea{c->stage,
-                          c->engram_hist + (size_t)site * c->slots * kEngramHistory * d,
-                          in(c, c->d_in, kInSlots),
-                          in(c, c->d_in, kInRunStart),
-                          st.taps,
-                          c->dilation,
-                          d,
-                          c->input,
-                          c->key,
-                          c->residual,
-                          1.0f / std::sqrt((float)d)};
+            ea = EngramArgs{c->stage,
+                            c->engram_hist + (size_t)site * c->slots * kEngramHistory * d,
+                            in(c, c->d_in, kInSlots),
+                            in(c, c->d_in, kInRunStart),
+                            in(c, c->d_in, kInRunEnd),
+                            st->taps,
+                            c->dilation,
+                            d,
+                            c->input,
+                            c->key,
+                            c->residual,
+                            1.0f / std::sqrt((float)d),
+                            w.norm_in,
+                            act,
+                            stride_d};
             hipLaunchKernelGGL(n3_engram_mix_kernel, dim3(rows), dim3(kThreads), 0, s, ea);
-            hipLaunchKernelGGL(n3_engram_history_kernel, dim3(rows), dim3(kThreads), 0, s, ea,
-                               in(c, c->d_in, kInRunEnd));
             NHIP_CHECK_HIP(hipGetLastError());
         }
         // attention (RunAttentionBatch, Engine.cs:2480-2596)
-        hipLaunchKernelGGL(n3_norm_fake_kernel<kCenteredFake>, dim3(rows), dim3(kThreads), 0, s, c->residual, d,
-                           w.norm_in, nullptr, c->normed);
-        NHIP_CHECK_HIP(hipGetLastError());
-        if ((rc = prepare(c, c->normed, rows, d, 2))) return rc;
         const nhip_weights* pw[4] = {w.q, w.k, w.v, w.gate};
         float* py[4] = {c->raw, c->raw + qw, c->raw + qw + kw, c->gate};
         const int32_t pl[4] = {all, all, all, ow};
@@ -994,33 +1323,68 @@ int32_t enqueue_step(nhip_ctx* c, int rows, int heads, int k, bool argmax)
                                         in(c, c->d_in, global ? kInCount : kInCountW), c->max_chunks, c->attn_ws,
                                         c->attn_ws_bytes, c->att, nullptr, nullptr, s)))
             return rc;
-        hipLaunchKernelGGL(n3_gate_fake_kernel, dim3(rows), dim3(kThreads), 0, s, c->att, c->gate, ow);
+        hipLaunchKernelGGL(n3_gate_kernel, dim3(rows), dim3(kThreads), 0, s, c->att, c->gate, ow, act, stride_o, ea);
         NHIP_CHECK_HIP(hipGetLastError());
-        if ((rc = prepare(c, c->att, rows, ow, 2)) || (rc = matmul(c, w.out, rows, ow, 0, d, c->proj, d))) return rc;
-        hipLaunchKernelGGL(n3_post_norm_add_kernel, dim3(rows), dim3(kThreads), 0, s, c->residual, c->proj,
-                           w.post_norm, w.attn_gate, d);
-        // the Kronecker-Hadamard MLP (RunMlp, Engine.cs:2146-2156)
-        MlpArgs ma{c->residual, w.pre_hada, c->perm_a, c->perm_b, w.d1, w.d2, w.b2, w.d3, w.d4, w.w1a, w.w1b,
-                   w.w2a, w.w2b, w.w3a, w.w3b, w.cond_v, w.cond_u, d, c->hada_rows, c->hada_cols};
-        hipLaunchKernelGGL(n3_mlp_kernel, dim3(rows), dim3(kThreads), c->mlp_lds, s, ma);
-        hipLaunchKernelGGL(n3_combine_kernel, dim3(rows), dim3(kThreads), 0, s, c->stream, c->mix, c->residual,
-                           c->input, c->post_gate, d, c->next);
+        if ((rc = matmul(c, w.out, rows, ow, 0, d, c->proj, d))) return rc;
+        const bool last = l == L - 1;
+        TailArgs ta{c->residual, c->proj, w.post_norm, w.attn_gate, w.pre_hada, c->perm_a, c->perm_b, w.d1, w.d2,
+                    w.b2, w.d3, w.d4, w.w1a, w.w1b, w.w2a, w.w2b, w.w3a, w.w3b, w.cond_v, w.cond_u, d, c->hada_rows,
+                    c->hada_cols, cur, c->mix, c->input, c->post_gate, nxt,
+                    last ? in(c, c->d_in, kInHeadOf) : nullptr, c->final_norm, act, last ? stride_d : stride4};
+        hipLaunchKernelGGL(n3_tail_kernel, dim3(rows), dim3(kThreads), c->tail_lds, s, ta);
         NHIP_CHECK_HIP(hipGetLastError());
-        std::swap(c->stream, c->next);
+        std::swap(cur, nxt);
     }
     if (heads == 0) return NHIP_OK;
-    // the head rows (PrepareHeadVectors, Engine.cs:920-928) and the tied
-    // 4-bit embedding
-    hipLaunchKernelGGL(n3_norm_fake_kernel<kHeadFake>, dim3(heads), dim3(kThreads), 0, s, c->stream, d,
-                       c->final_norm, in(c, c->d_in, kInHeads), c->normed);
-    NHIP_CHECK_HIP(hipGetLastError());
-    if ((rc = prepare(c, c->normed, heads, d, 4)) ||
-        (rc = matmul(c, c->embedding, heads, d, 0, c->vocab, c->logits, c->vocab)))
-        return rc;
+    // the head rows' logits: the tied 4-bit embedding (PrepareHead,
+    // Engine.cs:2188-2189)
+    if ((rc = matmul(c, c->embedding, heads, d, 0, c->vocab, c->logits, c->vocab))) return rc;
     if (k > 0 && (rc = nhip_topk_lse_dev(c->logits, heads, c->vocab, k, c->topk_ws, c->topk_ws_bytes, c->d_topk_idx,
                                          c->d_topk_lp, s)))
         return rc;
     if (argmax && (rc = nhip_argmax_dev(c->logits, c->vocab, c->vocab, heads, c->d_argmax, nullptr, s))) return rc;
+    return NHIP_OK;
+}
+
+// Steps of up to kMaxGraphRows rows replay a graph captured on first use for
+// their (rows, heads, k, argmax): every per-step input lives in device
+// arrays uploaded before the launch, so the captured kernels and arguments
+// stay valid.  NHIP_ENGINE_GRAPHS=0 launches every step eagerly (for kernel
+// tracers).
+constexpr int kMaxGraphRows = 16;
+constexpr size_t kMaxGraphs = 64;
+
+int32_t run_step(nhip_ctx* c, int rows, int heads, int k, bool argmax)
+{
+    static const bool graphs_enabled = [] {
+        const char* e = getenv("NHIP_ENGINE_GRAPHS");
+        return !(e && e[0] == '0');
+    }();
+    if (!graphs_enabled || rows > kMaxGraphRows) return enqueue_step(c, rows, heads, k, argmax);
+    hipGraphExec_t exec = nullptr;
+    for (const nhip_ctx::Graph& g : c->graphs)
+        if (g.rows == rows && g.heads == heads && g.k == k && g.argmax == argmax) exec = g.exec;
+    if (!exec) {
+        if (c->graphs.size() >= kMaxGraphs) {  // drop the oldest
+            NHIP_CHECK_HIP(hipStreamSynchronize(c->stream_h));
+            (void)hipGraphExecDestroy(c->graphs.front().exec);
+            c->graphs.erase(c->graphs.begin());
+        }
+        hipGraph_t g;
+        NHIP_CHECK_HIP(hipStreamBeginCapture(c->stream_h, hipStreamCaptureModeThreadLocal));
+        const int32_t rc = enqueue_step(c, rows, heads, k, argmax);
+        hipError_t e = hipStreamEndCapture(c->stream_h, &g);
+        if (rc) {
+            if (e == hipSuccess) (void)hipGraphDestroy(g);
+            return rc;
+        }
+        NHIP_CHECK_HIP(e);
+        e = hipGraphInstantiate(&exec, g, nullptr, nullptr, 0);
+        (void)hipGraphDestroy(g);
+        NHIP_CHECK_HIP(e);
+        c->graphs.push_back(nhip_ctx::Graph{rows, heads, k, argmax, exec});
+    }
+    NHIP_CHECK_HIP(hipGraphLaunch(exec, c->stream_h));
     return NHIP_OK;
 }
 
@@ -1064,6 +1428,7 @@ int32_t nhip_ctx_destroy(nhip_ctx* c)
     clear_error();
     if (!c) return NHIP_OK;
     if (c->stream_h) (void)hipStreamSynchronize(c->stream_h);
+    for (nhip_ctx::Graph& g : c->graphs) (void)hipGraphExecDestroy(g.exec);
     for (void* p : c->allocations) (void)hipFree(p);
     if (c->h_in) (void)hipHostFree(c->h_in);
     if (c->stream_h) (void)hipStreamDestroy(c->stream_h);
@@ -1160,9 +1525,16 @@ int32_t nhip_step(nhip_ctx* c, const int32_t* tokens, const int32_t* row_slots, 
         }
         rs = rk + 1;
     }
+    // the head runs once per distinct head row, in order of first mention;
+    // repeated rows are copied out again
+    for (int t = 0; t < rows; t++) h[kInHeadOf * R + t] = -1;
+    std::vector<int> head_map(heads);
+    int distinct = 0;
     for (int i = 0; i < heads; i++) {
-        NHIP_REQUIRE(head_rows[i] >= 0 && head_rows[i] < rows, "head row %d outside [0, %d)", head_rows[i], rows);
-        h[kInHeads * R + i] = head_rows[i];
+        const int t = head_rows[i];
+        NHIP_REQUIRE(t >= 0 && t < rows, "head row %d outside [0, %d)", t, rows);
+        if (h[kInHeadOf * R + t] < 0) h[kInHeadOf * R + t] = distinct++;
+        head_map[i] = h[kInHeadOf * R + t];
     }
     if (c->site_count > 0) engram_rows(c, tokens, row_slots, rows, in_erows(c, h));
     const size_t words = (size_t)R * (kInSections + std::max(c->engram_tables, 1));
@@ -1172,19 +1544,36 @@ int32_t nhip_step(nhip_ctx* c, const int32_t* tokens, const int32_t* row_slots, 
         set_error("step input upload failed");
         rc = NHIP_ERR_HIP;
     }
-    if (rc == NHIP_OK) rc = enqueue_step(c, rows, heads, k, argmax != nullptr);
+    if (rc == NHIP_OK) rc = run_step(c, rows, distinct, k, argmax != nullptr);
+    const bool repeats = distinct < heads;
+    std::vector<float> lg_h, lp_h;
+    std::vector<int32_t> idx_h, am_h;
     if (rc == NHIP_OK && heads > 0) {
-        const size_t hv = (size_t)heads;
+        const size_t hv = (size_t)distinct, V = (size_t)c->vocab;
+        float* lg_dst = logits;
+        float* lp_dst = topk_lp;
+        int32_t* idx_dst = topk_idx;
+        int32_t* am_dst = argmax;
+        if (repeats) {  // download the distinct rows, expand below
+            lg_h.resize(hv * V);
+            lp_h.resize(hv * 8);
+            idx_h.resize(hv * 8);
+            am_h.resize(hv);
+            lg_dst = lg_h.data();
+            lp_dst = lp_h.data();
+            idx_dst = idx_h.data();
+            am_dst = am_h.data();
+        }
         hipError_t e = hipSuccess;
-        if (logits) e = hipMemcpyAsync(logits, c->logits, hv * c->vocab * sizeof(float), hipMemcpyDeviceToHost, s);
+        if (logits) e = hipMemcpyAsync(lg_dst, c->logits, hv * V * sizeof(float), hipMemcpyDeviceToHost, s);
         if (e == hipSuccess && k > 0) {
             // the device lists are [heads][k] with stride k
-            e = hipMemcpyAsync(topk_idx, c->d_topk_idx, hv * k * sizeof(int32_t), hipMemcpyDeviceToHost, s);
+            e = hipMemcpyAsync(idx_dst, c->d_topk_idx, hv * k * sizeof(int32_t), hipMemcpyDeviceToHost, s);
             if (e == hipSuccess)
-                e = hipMemcpyAsync(topk_lp, c->d_topk_lp, hv * k * sizeof(float), hipMemcpyDeviceToHost, s);
+                e = hipMemcpyAsync(lp_dst, c->d_topk_lp, hv * k * sizeof(float), hipMemcpyDeviceToHost, s);
         }
         if (e == hipSuccess && argmax)
-            e = hipMemcpyAsync(argmax, c->d_argmax, hv * sizeof(int32_t), hipMemcpyDeviceToHost, s);
+            e = hipMemcpyAsync(am_dst, c->d_argmax, hv * sizeof(int32_t), hipMemcpyDeviceToHost, s);
         if (e != hipSuccess) {
             set_error("step output download failed: %s", hipGetErrorString(e));
             rc = NHIP_ERR_HIP;
@@ -1197,6 +1586,16 @@ int32_t nhip_step(nhip_ctx* c, const int32_t* tokens, const int32_t* row_slots, 
         set_error("step failed: %s", hipGetErrorString(done));
         return NHIP_ERR_HIP;
     }
+    if (repeats)
+        for (int i = 0; i < heads; i++) {
+            const size_t u = (size_t)head_map[i], V = (size_t)c->vocab;
+            if (logits) std::memcpy(logits + i * V, lg_h.data() + u * V, V * sizeof(float));
+            if (k > 0) {
+                std::memcpy(topk_idx + (size_t)i * k, idx_h.data() + u * k, k * sizeof(int32_t));
+                std::memcpy(topk_lp + (size_t)i * k, lp_h.data() + u * k, k * sizeof(float));
+            }
+            if (argmax) argmax[i] = am_h[u];
+        }
     // the slots' lengths and previous tokens (ForwardBatch, Engine.cs:2326-2340)
     for (int rs = 0; rs < rows;) {
         const int slot = row_slots[rs];

@@ -21,12 +21,6 @@ __device__ __forceinline__ float wave_max(float v)
     return v;
 }
 
-__device__ __forceinline__ int wave_sum(int v)
-{
-    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
-    return v;
-}
-
 // One block of 256 threads per row.
 __global__ __launch_bounds__(256) void quantize_rows_kernel(const float* __restrict__ x, int cols,
                                                            int8_t* __restrict__ q, float* __restrict__ scales)
@@ -46,10 +40,8 @@ __global__ __launch_bounds__(256) void quantize_rows_kernel(const float* __restr
     if (threadIdx.x == 0) scales[blockIdx.x] = scale;
 }
 
-// One wave per (token, group): lane e holds elements e (v0) and e + 64 (v1).
-// Butterfly stage s < 64 pairs lanes e and e ^ s; stage 64 pairs v0 with v1.
-// The lower element of a pair becomes a + b, the upper a - b, exactly as
-// Scalar.Hadamard computes them.
+// One wave per (token, group): lane e holds elements e and e + 64
+// (hadamard_wave, prepare_group_wave).
 __global__ __launch_bounds__(256) void prepare_kernel(const float* __restrict__ x, int tokens, int cols, int bits,
                                                      int8_t* __restrict__ values, float* __restrict__ scales,
                                                      float* __restrict__ offsets, int stride)
@@ -63,46 +55,9 @@ __global__ __launch_bounds__(256) void prepare_kernel(const float* __restrict__ 
     const float* src = x + (size_t)t * cols + g * 128;
     float v0 = src[lane];
     float v1 = src[lane + 64];
-    for (int s = 1; s < 64; s <<= 1) {
-        const float p0 = __shfl_xor(v0, s);
-        const float p1 = __shfl_xor(v1, s);
-        const bool upper = (lane & s) != 0;
-        v0 = upper ? p0 - v0 : v0 + p0;
-        v1 = upper ? p1 - v1 : v1 + p1;
-    }
-    {
-        const float a = v0, b = v1;
-        v0 = a + b;
-        v1 = a - b;
-    }
-    v0 = v0 * 0.08838834764831845f;
-    v1 = v1 * 0.08838834764831845f;
-    const float peak = wave_max(fmaxf(fabsf(v0), fabsf(v1)));
-    const float scale = peak > 0.0f ? peak / 127.0f : 1.0f;
-    const float inverse = 1.0f / scale;
-    const int q0 = ref_quantize_one(v0, inverse);
-    const int q1 = ref_quantize_one(v1, inverse);
-    const int sum = wave_sum(q0 + q1);
-    // Planes (Scalar.cs:91-111): destination d takes quantized[src(d)].
-    int8_t* dst = values + (size_t)t * cols + g * 128;
-#pragma unroll
-    for (int k = 0; k < 2; k++) {
-        const int d = lane + 64 * k;
-        int sidx;
-        if (bits == 2) {
-            sidx = 4 * (d & 31) + (d >> 5);                      // p*32 + j <- 4j + p
-        } else {
-            const int half = d >> 6, r = d & 63;
-            sidx = half * 64 + 2 * (r & 31) + (r >> 5);          // half*64 + p*32 + j <- half*64 + 2j + p
-        }
-        const int a = __shfl(q0, sidx & 63);
-        const int b = __shfl(q1, sidx & 63);
-        dst[d] = static_cast<int8_t>(sidx < 64 ? a : b);
-    }
-    if (lane == 0) {
-        scales[(size_t)t * stride + g] = scale;
-        offsets[(size_t)t * stride + g] = 63.0f * (float)sum;
-    }
+    hadamard_wave(v0, v1);
+    prepare_group_wave(v0, v1, bits, values + (size_t)t * cols + g * 128, scales + (size_t)t * stride + g,
+                       offsets + (size_t)t * stride + g);
 }
 
 }  // namespace

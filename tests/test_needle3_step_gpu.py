@@ -234,3 +234,29 @@ def test_errors_leave_the_slots_untouched(hip, model):
         assert np.isfinite(lg).all() and g.slot_length(0) == 20
     finally:
         g.close()
+
+
+def test_needle3_geometry_matches_the_oracle(hip, orc):
+    """Needle 3's own geometry (768 hidden, 20 layers, 12/2 heads, 5 engram
+    sites, 1024-wide MLP, 8192 vocab): a mixed prefill step and decode steps
+    of three slots, bit for bit."""
+    from needle_cs_amd.engine import BatchedEngine, Model
+    print("needle3 full geometry parity", flush=True)
+    archive = M.write_archive(M.NEEDLE3, 7)
+    om = M.OracleModel(orc, archive)
+    o = M.OracleEngine(orc, om, slots=3, capacity=64, max_chunks=MAX_CHUNKS)
+    with Model(archive) as model, BatchedEngine(model, context_length=64, chunk_size=16, slots=3,
+                                                max_chunks=MAX_CHUNKS) as g:
+        rng = np.random.default_rng(8)
+        t = rng.integers(0, M.NEEDLE3["vocab"], 16).astype(np.int32)
+        s = [0] * 8 + [1] * 5 + [2] * 3
+        lg, _, _, am = g.forward_batch(t, s, [7, 12, 15], argmax=True)
+        want = o.step(t, s, [7, 12, 15])
+        assert same_bits(lg, want)
+        for step in range(3):
+            t = am.astype(np.int32)
+            lg, _, _, am = g.forward_batch(t, [0, 1, 2], [0, 1, 2], argmax=True)
+            want = o.step(t, [0, 1, 2], [0, 1, 2])
+            assert same_bits(lg, want), f"decode step {step}"
+            assert np.array_equal(am, np.argmax(want, axis=1))
+    o.close()
