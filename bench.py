@@ -487,6 +487,25 @@ def needle3_loop(args, threads: int) -> dict:
 
         run()  # captures the step graphs
         pre, dec, toks = min((run() for _ in range(3)), key=lambda r: r[1])
+        # the same loop with all 16 slots of a BatchedEngine busy: the step's
+        # row kernels run side by side, so rows cost little more than one
+        wide = 16
+        wide_prompts = np.random.default_rng(0x7009).integers(0, g3["vocab"], (wide, prompt_len)).astype(np.int32)
+        wlanes = np.arange(wide, dtype=np.int32)
+        with BatchedEngine(model, context_length=prompt_len + new, chunk_size=64, slots=wide, max_chunks=8) as eng16:
+            def run16():
+                for s in range(wide):
+                    eng16.reset_slot(s)
+                for s in range(wide):
+                    eng16.feed_slot(s, wide_prompts[s, :-1], compute_logits=False)
+                _, _, _, t16 = eng16.forward_batch(wide_prompts[:, -1], wlanes, wlanes, logits=False, argmax=True)
+                t1 = time.perf_counter()
+                for _ in range(new - 1):
+                    _, _, _, t16 = eng16.forward_batch(t16, wlanes, wlanes, logits=False, argmax=True)
+                return time.perf_counter() - t1
+
+            run16()
+            dec16 = min(run16() for _ in range(3))
     steps = new - 1
     ms = dec / steps * 1e3
     out = {"workload": "greedy decode of 3 slots, Needle 3 geometry (20 layers, hidden 768, 12/2 heads x 48/64, "
@@ -494,8 +513,11 @@ def needle3_loop(args, threads: int) -> dict:
            "row_tokens_per_s": round(slots * steps / dec, 1), "ms_per_step": round(ms, 4),
            "prefill_ms": round(pre * 1e3, 2), "weight_bytes_per_step": step_bytes,
            "weights_GBps_per_step": round(step_bytes / (ms * 1e-3) / 1e9, 2),
-           "frac_hbm_peak": round(step_bytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 5)}
-    print(f"# needle3 decode: {out['row_tokens_per_s']} row-tokens/s, {ms:.3f} ms/step, prefill {pre * 1e3:.1f} ms",
+           "frac_hbm_peak": round(step_bytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 5),
+           "slots16": {"row_tokens_per_s": round(wide * steps / dec16, 1),
+                       "ms_per_step": round(dec16 / steps * 1e3, 4)}}
+    print(f"# needle3 decode: {out['row_tokens_per_s']} row-tokens/s, {ms:.3f} ms/step, prefill {pre * 1e3:.1f} ms; "
+          f"16 slots: {out['slots16']['row_tokens_per_s']} row-tokens/s, {out['slots16']['ms_per_step']} ms/step",
           file=sys.stderr, flush=True)
     if not args.no_cpu:
         from oracle import needle3 as M
