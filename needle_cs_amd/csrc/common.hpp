@@ -142,6 +142,17 @@ int32_t attention_decode_post_impl(const AttnPostInputs& in, int32_t rows, int32
                                    int32_t slots, int32_t capacity, const int32_t* d_row_slot,
                                    const int32_t* d_row_first, const int32_t* d_row_count, int32_t max_chunks,
                                    float* d_out, hipStream_t stream);
+// nhip_needle3_attention_inputs_dev; with_history false leaves the slots'
+// Q/K/V frames to the caller, which moves them on after every row of the
+// step has read them.
+int32_t needle3_attention_inputs_impl(const float* d_raw, int32_t rows, int32_t heads, int32_t kv_heads,
+                                      int32_t qk_dim, int32_t v_dim, const float* d_q_taps, const float* d_k_taps,
+                                      const float* d_v_taps, const float* d_q_norm, const float* d_k_norm,
+                                      const float* d_rope_cos, const float* d_rope_sin, float* d_history,
+                                      const int32_t* d_row_slot, const int32_t* d_row_pos, int32_t slots,
+                                      int32_t capacity, int8_t* d_q, float* d_q_scales, int8_t* d_keys,
+                                      float* d_key_scales, int8_t* d_values, float* d_value_scales, bool with_history,
+                                      hipStream_t s);
 // Chunk-kernel geometry of attention_decode_impl: the longest chunk of the
 // plan, and the kv heads per workgroup (0 when a chunk does not fit in LDS);
 // a quantized output needs every head in one workgroup.

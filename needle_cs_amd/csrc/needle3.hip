@@ -174,18 +174,19 @@ __global__ __launch_bounds__(256) void needle3_history_kernel(Needle3Params p)
 }
 
 }  // namespace
-}  // namespace nhip
 
-using namespace nhip;
-
-extern "C" int32_t nhip_needle3_attention_inputs_dev(
-    const float* d_raw, int32_t rows, int32_t heads, int32_t kv_heads, int32_t qk_dim, int32_t v_dim,
-    const float* d_q_taps, const float* d_k_taps, const float* d_v_taps, const float* d_q_norm,
-    const float* d_k_norm, const float* d_rope_cos, const float* d_rope_sin, float* d_history,
-    const int32_t* d_row_slot, const int32_t* d_row_pos, int32_t slots, int32_t capacity, int8_t* d_q,
-    float* d_q_scales, int8_t* d_keys, float* d_key_scales, int8_t* d_values, float* d_value_scales, void* stream)
+// The attention inputs; with_history false leaves the slots' frames to the
+// caller, which must move them on (as needle3_history_kernel does) after
+// every row of the step has read them.
+int32_t needle3_attention_inputs_impl(const float* d_raw, int32_t rows, int32_t heads, int32_t kv_heads,
+                                      int32_t qk_dim, int32_t v_dim, const float* d_q_taps, const float* d_k_taps,
+                                      const float* d_v_taps, const float* d_q_norm, const float* d_k_norm,
+                                      const float* d_rope_cos, const float* d_rope_sin, float* d_history,
+                                      const int32_t* d_row_slot, const int32_t* d_row_pos, int32_t slots,
+                                      int32_t capacity, int8_t* d_q, float* d_q_scales, int8_t* d_keys,
+                                      float* d_key_scales, int8_t* d_values, float* d_value_scales, bool with_history,
+                                      hipStream_t s)
 {
-    clear_error();
     NHIP_REQUIRE(rows >= 0, "rows %d < 0", rows);
     if (rows == 0) return NHIP_OK;
     NHIP_REQUIRE(heads > 0 && kv_heads > 0 && slots > 0 && capacity > 0, "heads, kv_heads, slots and capacity must be "
@@ -223,10 +224,27 @@ extern "C" int32_t nhip_needle3_attention_inputs_dev(
     p.vd = v_dim;
     p.slots = slots;
     p.capacity = capacity;
-    hipStream_t s = as_stream(stream);
     hipLaunchKernelGGL(needle3_inputs_kernel, dim3(rows, heads + 2 * kv_heads), dim3(64), 0, s, p);
     NHIP_CHECK_HIP(hipGetLastError());
-    hipLaunchKernelGGL(needle3_history_kernel, dim3(rows), dim3(256), 0, s, p);
-    NHIP_CHECK_HIP(hipGetLastError());
+    if (with_history) {
+        hipLaunchKernelGGL(needle3_history_kernel, dim3(rows), dim3(256), 0, s, p);
+        NHIP_CHECK_HIP(hipGetLastError());
+    }
     return NHIP_OK;
+}
+
+}  // namespace nhip
+
+extern "C" int32_t nhip_needle3_attention_inputs_dev(
+    const float* d_raw, int32_t rows, int32_t heads, int32_t kv_heads, int32_t qk_dim, int32_t v_dim,
+    const float* d_q_taps, const float* d_k_taps, const float* d_v_taps, const float* d_q_norm,
+    const float* d_k_norm, const float* d_rope_cos, const float* d_rope_sin, float* d_history,
+    const int32_t* d_row_slot, const int32_t* d_row_pos, int32_t slots, int32_t capacity, int8_t* d_q,
+    float* d_q_scales, int8_t* d_keys, float* d_key_scales, int8_t* d_values, float* d_value_scales, void* stream)
+{
+    nhip::clear_error();
+    return nhip::needle3_attention_inputs_impl(d_raw, rows, heads, kv_heads, qk_dim, v_dim, d_q_taps, d_k_taps,
+                                               d_v_taps, d_q_norm, d_k_norm, d_rope_cos, d_rope_sin, d_history,
+                                               d_row_slot, d_row_pos, slots, capacity, d_q, d_q_scales, d_keys,
+                                               d_key_scales, d_values, d_value_scales, true, nhip::as_stream(stream));
 }

@@ -55,6 +55,7 @@ constexpr int kMaxDim = 1024;
 constexpr int kPer = kMaxDim / kThreads;    // elements of a dim-row per thread: c = threadIdx.x + kThreads * q
 constexpr int kMaxStream = kLanes * kMaxDim;
 constexpr int kCondPer = 8 * kMaxDim / kThreads;  // condition-weight entries per thread
+constexpr int kHistPer = 10;                       // Q/K/V frame entries per thread (qw + kw + vw <= 2560)
 
 __device__ __forceinline__ float sigmoid_poly(float x) { return 1.0f / (1.0f + exp_poly(-x)); }
 
@@ -458,12 +459,43 @@ __global__ __launch_bounds__(kThreads) void n3_engram_mix_kernel(EngramArgs a)
 // output matmul.  On engram layers the run-end rows also move their slot's
 // engram history on (Engine.cs:2439): the nine frames before the sequence's
 // end.  This runs after every row's engram mix has read the old history.
+// The slots' Q/K/V frames (the three-tap convolution's history) of a layer.
+struct QkvHistArgs {
+    float* history;  // [slots] x ([2][qw], [2][kw], [2][vw]), frame 1 the latest
+    const float* raw;  // [rows][qw + kw + vw]: this step's projections
+    const int32_t* row_slot;
+    const int32_t* run_start;
+    const int32_t* run_end;
+    int qw, kw, vw;
+};
+
 __global__ __launch_bounds__(kThreads) void n3_gate_kernel(const float* att, const float* gate, int n, Act act,
-                                                           int stride, EngramArgs e)
+                                                           int stride, EngramArgs e, QkvHistArgs h)
 {
     __shared__ __align__(16) float x[kMaxDim];
     __shared__ float red[kWaves];
     const int t = blockIdx.x;
+    // the run's last row moves its slot's Q/K/V frames on: frame 0 takes the
+    // row before it (the old frame 1 for a one-row run), frame 1 the row
+    // itself (Scalar.Taps3's history, TapsAndAttentionHeadsSingle); the loads
+    // go out with the row's own
+    const bool hist_end = h.run_end[t] != 0;
+    const int all = h.qw + h.kw + h.vw;
+    float* hist = h.history + (size_t)h.row_slot[t] * 2 * all;
+    float hv0[kHistPer], hv1[kHistPer];
+    if (hist_end) {
+        const bool run1 = t > h.run_start[t];
+#pragma unroll
+        for (int q = 0; q < kHistPer; q++) {
+            const int c = col_of(q);
+            if (c < all) {
+                const int base = c < h.qw ? 0 : (c < h.qw + h.kw ? h.qw : h.qw + h.kw);
+                const int width = c < h.qw ? h.qw : (c < h.qw + h.kw ? h.kw : h.vw);
+                hv0[q] = run1 ? h.raw[(size_t)(t - 1) * all + c] : hist[2 * base + (c - base) + width];
+                hv1[q] = h.raw[(size_t)t * all + c];
+            }
+        }
+    }
     float av[kPer], gv[kPer];
 #pragma unroll
     for (int q = 0; q < kPer; q++) {
@@ -481,6 +513,18 @@ __global__ __launch_bounds__(kThreads) void n3_gate_kernel(const float* att, con
     __syncthreads();
     fake_row(x, n, red);
     prepare_row(x, n, 2, act, stride, t);
+    if (hist_end) {
+#pragma unroll
+        for (int q = 0; q < kHistPer; q++) {
+            const int c = col_of(q);
+            if (c < all) {
+                const int base = c < h.qw ? 0 : (c < h.qw + h.kw ? h.qw : h.qw + h.kw);
+                const int width = c < h.qw ? h.qw : (c < h.qw + h.kw ? h.kw : h.vw);
+                hist[2 * base + (c - base)] = hv0[q];
+                hist[2 * base + (c - base) + width] = hv1[q];
+            }
+        }
+    }
     if (e.history && e.run_end[t]) {
         const int len = t - e.run_start[t] + 1;  // the run's length
         float* hist = e.history + (size_t)e.row_slot[t] * kEngramHistory * e.dim;
@@ -1009,6 +1053,8 @@ int32_t load_model(nhip_ctx* c)
                  "conv taps %u, engram taps %u, dim %d (a multiple of 128 up to 1024)", h[19], h[23], c->dim);
     NHIP_REQUIRE(c->hada_cols % 8 == 0 && c->hada_rows * c->hada_cols == hada_n && hada_n >= c->dim,
                  "MLP size %d must split into rows x cols (cols divisible by 8) covering dim %d", hada_n, c->dim);
+    NHIP_REQUIRE(c->heads * c->qk + c->kv * (c->qk + c->vd) <= kHistPer * kThreads, "Q/K/V width %d above %d",
+                 c->heads * c->qk + c->kv * (c->qk + c->vd), kHistPer * kThreads);
     NHIP_REQUIRE(c->heads > 0 && c->kv > 0 && c->heads % c->kv == 0 && c->heads * c->vd <= 1024 &&
                      (c->heads * c->vd) % 128 == 0,
                  "heads %d / kv %d (heads * 64 a multiple of 128 up to 1024)", c->heads, c->kv);
@@ -1309,10 +1355,11 @@ int32_t enqueue_step(nhip_ctx* c, int rows, int heads, int k, bool argmax)
         int8_t* values = c->values + lcell * vw;
         float* kscale = c->key_scales + lcell * KV;
         float* vscale = c->value_scales + lcell * KV;
-        if ((rc = nhip_needle3_attention_inputs_dev(
-                 c->raw, rows, H, KV, c->qk, c->vd, w.q_taps, w.k_taps, w.v_taps, w.q_norm, w.k_norm, c->rope_cos,
-                 c->rope_sin, c->qkv_hist + (size_t)l * c->slots * 2 * all, in(c, c->d_in, kInSlots),
-                 in(c, c->d_in, kInPos), c->slots, c->capacity, c->q8, c->qs, keys, kscale, values, vscale, s)))
+        float* qkv_hist = c->qkv_hist + (size_t)l * c->slots * 2 * all;
+        if ((rc = needle3_attention_inputs_impl(c->raw, rows, H, KV, c->qk, c->vd, w.q_taps, w.k_taps, w.v_taps,
+                                                w.q_norm, w.k_norm, c->rope_cos, c->rope_sin, qkv_hist,
+                                                in(c, c->d_in, kInSlots), in(c, c->d_in, kInPos), c->slots,
+                                                c->capacity, c->q8, c->qs, keys, kscale, values, vscale, false, s)))
             return rc;
         // the layer's span (Blocks.cs:973-978): global layers from 0, the
         // others over the window ending at the row
@@ -1323,7 +1370,11 @@ int32_t enqueue_step(nhip_ctx* c, int rows, int heads, int k, bool argmax)
                                         in(c, c->d_in, global ? kInCount : kInCountW), c->max_chunks, c->attn_ws,
                                         c->attn_ws_bytes, c->att, nullptr, nullptr, s)))
             return rc;
-        hipLaunchKernelGGL(n3_gate_kernel, dim3(rows), dim3(kThreads), 0, s, c->att, c->gate, ow, act, stride_o, ea);
+        // the gate also moves the slots' Q/K/V frames on, after attention's
+        // inputs have read them
+        const QkvHistArgs qh{qkv_hist, c->raw, in(c, c->d_in, kInSlots), in(c, c->d_in, kInRunStart),
+                             in(c, c->d_in, kInRunEnd), qw, kw, vw};
+        hipLaunchKernelGGL(n3_gate_kernel, dim3(rows), dim3(kThreads), 0, s, c->att, c->gate, ow, act, stride_o, ea, qh);
         NHIP_CHECK_HIP(hipGetLastError());
         if ((rc = matmul(c, w.out, rows, ow, 0, d, c->proj, d))) return rc;
         const bool last = l == L - 1;
