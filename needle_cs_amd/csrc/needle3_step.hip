@@ -592,23 +592,23 @@ __device__ __forceinline__ void kron_lds(const float* z, int active, const float
     const int k = on ? e0 / cols : 0, c = e0 - k * cols, ss = cols + 1;
     float4 sum = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     if (on) {
+        // active is a multiple of 8 (the caller zero-fills z's rows up to it:
+        // a zero product leaves a sum that starts at +0 unchanged)
         for (int i0 = 0; i0 < active; i0 += 8) {
             float lv[8];
             float4 zv[8];
 #pragma unroll
-            for (int u = 0; u < 8; u++)
-                if (i0 + u < active) {
-                    lv[u] = left[(i0 + u) * rows + k];
-                    zv[u] = *reinterpret_cast<const float4*>(z + (i0 + u) * cols + c);
-                }
+            for (int u = 0; u < 8; u++) {
+                lv[u] = left[(i0 + u) * rows + k];
+                zv[u] = *reinterpret_cast<const float4*>(z + (i0 + u) * cols + c);
+            }
 #pragma unroll
-            for (int u = 0; u < 8; u++)
-                if (i0 + u < active) {
-                    sum.x = sum.x + lv[u] * zv[u].x;
-                    sum.y = sum.y + lv[u] * zv[u].y;
-                    sum.z = sum.z + lv[u] * zv[u].z;
-                    sum.w = sum.w + lv[u] * zv[u].w;
-                }
+            for (int u = 0; u < 8; u++) {
+                sum.x = sum.x + lv[u] * zv[u].x;
+                sum.y = sum.y + lv[u] * zv[u].y;
+                sum.z = sum.z + lv[u] * zv[u].z;
+                sum.w = sum.w + lv[u] * zv[u].w;
+            }
         }
         float* srow = scratch + k * ss + c;
         srow[0] = sum.x;
@@ -766,10 +766,11 @@ __global__ __launch_bounds__(kThreads) void n3_tail_kernel(TailArgs a)
     }
     const int input_rows = (dim + a.cols - 1) / a.cols;
     const int output_rows = min(a.rows, (input_rows + 3) / 4 * 4);
+    const int active_rows = (input_rows + 7) / 8 * 8;  // <= rows (rows % 8 == 0): zero rows past the input
 #pragma unroll
     for (int q = 0; q < kPer; q++) {
         const int c = col_of(q);
-        if (c < input_rows * a.cols) front[c] = c < dim ? norm[c] * d1v[q] : 0.0f;
+        if (c < active_rows * a.cols) front[c] = c < dim ? norm[c] * d1v[q] : 0.0f;
     }
     __syncthreads();
     if (threadIdx.x < 8) weights[threadIdx.x] = chain_sum(prod + threadIdx.x * pstride, dim);
@@ -784,7 +785,7 @@ __global__ __launch_bounds__(kThreads) void n3_tail_kernel(TailArgs a)
         }
         for (int j = 0; j < 8; j++) weights[j] = weights[j] / total;
     }
-    kron_lds(front, input_rows, wl, wr, a.rows, a.cols, a.rows, scratch, back);
+    kron_lds(front, active_rows, wl, wr, a.rows, a.cols, a.rows, scratch, back);
 #pragma unroll
     for (int q = 0; q < kPer; q++) {  // Scalar.PermuteModulateActivate
         const int n = col_of(q);
@@ -1051,7 +1052,8 @@ int32_t load_model(nhip_ctx* c)
                  c->vd, h[15]);
     NHIP_REQUIRE(h[19] == 3 && (c->site_count == 0 || h[23] == 4) && c->dim % 128 == 0 && c->dim <= 1024,
                  "conv taps %u, engram taps %u, dim %d (a multiple of 128 up to 1024)", h[19], h[23], c->dim);
-    NHIP_REQUIRE(c->hada_cols % 8 == 0 && c->hada_rows * c->hada_cols == hada_n && hada_n >= c->dim,
+    NHIP_REQUIRE(c->hada_cols % 8 == 0 && c->hada_rows % 8 == 0 && c->hada_rows * c->hada_cols == hada_n &&
+                     hada_n >= c->dim,
                  "MLP size %d must split into rows x cols (cols divisible by 8) covering dim %d", hada_n, c->dim);
     NHIP_REQUIRE(c->heads * c->qk + c->kv * (c->qk + c->vd) <= kHistPer * kThreads, "Q/K/V width %d above %d",
                  c->heads * c->qk + c->kv * (c->qk + c->vd), kHistPer * kThreads);
