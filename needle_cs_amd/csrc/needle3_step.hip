@@ -720,20 +720,6 @@ __global__ __launch_bounds__(kThreads) void n3_tail_kernel(TailArgs a)
             wv[q][5] = a.w3b[e];
         }
     }
-#pragma unroll
-    for (int q = 0; q < kPer; q++) {
-        const int e = col_of(q);
-        if (e < rr) {
-            wl[e] = wv[q][0];
-            wl[rr + e] = wv[q][1];
-            wl[2 * rr + e] = wv[q][2];
-        }
-        if (e < cc) {
-            wr[e] = wv[q][3];
-            wr[cc + e] = wv[q][4];
-            wr[2 * cc + e] = wv[q][5];
-        }
-    }
     // Scalar.PostNormAdd: residual += gate * ((1 + s) * x * (1 / rms(x))), x = the attention projection
 #pragma unroll
     for (int q = 0; q < kPer; q++) {
@@ -763,6 +749,22 @@ __global__ __launch_bounds__(kThreads) void n3_tail_kernel(TailArgs a)
     for (int q = 0; q < kCondPer; q++) {  // Scalar.ConditionWeights' products
         const int e = col_of(q);
         if (e < dim * 8) prod[(e & 7) * pstride + (e >> 3)] = norm[e >> 3] * cvv[q];
+    }
+    // the Kronecker factors into LDS only now: stored earlier, their loads
+    // (issued last) would hold up the two norm chains above
+#pragma unroll
+    for (int q = 0; q < kPer; q++) {
+        const int e = col_of(q);
+        if (e < rr) {
+            wl[e] = wv[q][0];
+            wl[rr + e] = wv[q][1];
+            wl[2 * rr + e] = wv[q][2];
+        }
+        if (e < cc) {
+            wr[e] = wv[q][3];
+            wr[cc + e] = wv[q][4];
+            wr[2 * cc + e] = wv[q][5];
+        }
     }
     const int input_rows = (dim + a.cols - 1) / a.cols;
     const int output_rows = min(a.rows, (input_rows + 3) / 4 * 4);
