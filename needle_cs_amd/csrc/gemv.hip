@@ -956,18 +956,144 @@ __device__ __forceinline__ void cq_decode_tile(const MatmulParams& p, const int 
     }
 }
 
+// Codebook formats, 5..16 tokens: one group per MFMA set, whose A rows are
+// the 16 tokens (rows of tokens >= M zero), so lane (r, kq) holds D_g of
+// row r for tokens 4kq..4kq+3.  Wave w owns the GPW groups from
+// g_first = GPW*w (groups past G run on clamped operands; their columns are
+// never read).  The lane leaves, per group and token,
+//     scaled = (HalfToSingle(norm[n][g]) * ByteScale) * scale[t][g]
+//     pa[t][r][g] = scaled * D_g,   pb[t][r][g] = scaled * offset[t][g]
+// in LDS as float4 columns of four groups, column c of product row x at
+// c ^ (x & swz) (the int8 decode path's swizzle); after one barrier lane
+// (t, r) adds both rows in ascending g and stores acc - bias, Scalar.MatMulRows'
+// operations in its order (Scalar.cs:185-189), as cq_decode_tile does.
 template <int F, int GPW, bool EXACT>
-__global__ __launch_bounds__(512) void matmul_cq_decode_kernel(MatmulParams p)
+__device__ __forceinline__ void cq_decode_wide_tile(const MatmulParams& p, const int tile)
 {
-    cq_decode_tile<F, GPW, EXACT>(p, p.tile_begin + blockIdx.x);
+    using T = Traits<F>;
+    static_assert(GPW % 4 == 0, "products are stored four groups at a time");
+    constexpr int CB = GPW / T::GPB;  // weight blocks per wave
+    extern __shared__ __align__(16) uint8_t lds[];
+    const int M = p.tokens;  // 5..16
+    const int G = p.groups;
+    const int GS = p.ldd;    // product row stride (floats): every group a wave writes, a multiple of 4
+    float4* pa = reinterpret_cast<float4*>(lds);
+    float4* pb = pa + (size_t)M * 16 * (GS / 4);
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int r = lane & 15;
+    const int kq = lane >> 4;
+    const int n = tile * 16 + r;
+    const int g_first = wave * GPW;
+    const u4* wbase = reinterpret_cast<const u4*>(p.tiles) + (size_t)tile * p.blocks * 64 + lane;
+    const uint16_t* nrow = p.norms + (size_t)n * p.groups_pad8;
+    asm volatile("" ::"s"(p.tiles), "s"(p.norms), "s"(p.q), "s"(p.qscale), "s"(p.offsets), "s"(p.cols),
+                 "s"(p.stride), "s"(p.blocks), "s"(p.groups_pad8));
+
+    // 1. A operands of token r, 2. activation scales and offsets of tokens
+    // 4kq..4kq+3, 3. weight scales of row n, 4. weight blocks -- all in flight
+    // together
+    const int8_t* qrow = p.q + (size_t)min(r, M - 1) * p.cols;
+    Operand<F> av[GPW];
+#pragma unroll
+    for (int c = 0; c < GPW; c++) av[c] = load_operand<F>(qrow, r < M, min(g_first + c, G - 1), kq);
+    float sc[GPW][4], of[GPW][4];
+#pragma unroll
+    for (int c = 0; c < GPW; c++) {
+        const int g = min(g_first + c, G - 1);
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const size_t at = (size_t)min(4 * kq + i, M - 1) * p.stride + g;
+            sc[c][i] = p.qscale[at];
+            of[c][i] = p.offsets[at];
+        }
+    }
+    uint16_t hraw[GPW];
+#pragma unroll
+    for (int c = 0; c < GPW; c++) hraw[c] = nrow[min(g_first + c, G - 1)];
+    u4 w[CB];
+#pragma unroll
+    for (int c = 0; c < CB; c++)
+        w[c] = __builtin_nontemporal_load(wbase + (size_t)min(wave * CB + c, p.blocks - 1) * 64);
+    __builtin_amdgcn_sched_barrier(0);
+
+    const int tq = 4 * kq;  // first token of this lane's MFMA results
+#pragma unroll
+    for (int c4 = 0; c4 < GPW / 4; c4++) {
+        float ra[4][4], rb[4][4];  // [token i][group j of the column]
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const int gl = 4 * c4 + j;
+            const v4i d = group_dot<F, true>(w[gl / T::GPB], gl % T::GPB, av[gl], p);
+            const float hs = EXACT ? ref_half_to_single(hraw[gl]) : decode_scale_fast(hraw[gl]);
+            const float hb = hs * p.byte_scale;
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const float scaled = hb * sc[gl][i];
+                ra[i][j] = scaled * static_cast<float>(d[i]);
+                rb[i][j] = scaled * of[gl][i];
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int x = (tq + i) * 16 + r;  // product row
+            if (tq + i < M) {
+                const int col = ((g_first >> 2) + c4) ^ (x & p.swz);
+                pa[(size_t)x * (GS / 4) + col] = make_float4(ra[i][0], ra[i][1], ra[i][2], ra[i][3]);
+                pb[(size_t)x * (GS / 4) + col] = make_float4(rb[i][0], rb[i][1], rb[i][2], rb[i][3]);
+            }
+        }
+    }
+    __syncthreads();
+    for (int x = threadIdx.x; x < M * 16; x += blockDim.x) {
+        const int nn = tile * 16 + (x & 15);
+        const float4* row_a = pa + (size_t)x * (GS / 4);
+        const float4* row_b = pb + (size_t)x * (GS / 4);
+        const int sw = x & p.swz;
+        float acc = 0.0f, bias = 0.0f;
+        for (int c = 0; c < (G >> 2); c++) {
+            const float4 a = row_a[c ^ sw];
+            const float4 b = row_b[c ^ sw];
+            acc = acc + a.x;
+            bias = bias + b.x;
+            acc = acc + a.y;
+            bias = bias + b.y;
+            acc = acc + a.z;
+            bias = bias + b.z;
+            acc = acc + a.w;
+            bias = bias + b.w;
+        }
+        if (G & 3) {
+            const float4 a = row_a[(G >> 2) ^ sw];
+            const float4 b = row_b[(G >> 2) ^ sw];
+            const float av4[4] = {a.x, a.y, a.z, a.w}, bv4[4] = {b.x, b.y, b.z, b.w};
+            for (int j = 0; j < (G & 3); j++) {
+                acc = acc + av4[j];
+                bias = bias + bv4[j];
+            }
+        }
+        if (nn >= p.row_start && nn < p.row_end) p.y[(size_t)(x >> 4) * p.ldy + nn] = acc - bias;
+    }
 }
 
-template <int F, int GPW, bool EXACT>
+template <int F, int GPW, bool EXACT, bool WIDE>
+__global__ __launch_bounds__(512) void matmul_cq_decode_kernel(MatmulParams p)
+{
+    if constexpr (WIDE)
+        cq_decode_wide_tile<F, GPW, EXACT>(p, p.tile_begin + blockIdx.x);
+    else
+        cq_decode_tile<F, GPW, EXACT>(p, p.tile_begin + blockIdx.x);
+}
+
+template <int F, int GPW, bool EXACT, bool WIDE>
 __global__ __launch_bounds__(512) void matmul_cq_decode_batch_kernel(MatmulBatch b)
 {
     const int j = batch_job(b);
     const MatmulParams& p = b.job[j];
-    cq_decode_tile<F, GPW, EXACT>(p, p.tile_begin + (int)blockIdx.x - b.first[j]);
+    if constexpr (WIDE)
+        cq_decode_wide_tile<F, GPW, EXACT>(p, p.tile_begin + (int)blockIdx.x - b.first[j]);
+    else
+        cq_decode_tile<F, GPW, EXACT>(p, p.tile_begin + (int)blockIdx.x - b.first[j]);
 }
 
 // The decode kernel for M <= 4 with its activation rows computed in the
@@ -1224,14 +1350,29 @@ int32_t try_i8_decode(const DeviceWeights* w, MatmulParams& p, hipStream_t strea
                              : launch_dec_ti<8, false>(p, waves, lds, stream);
 }
 
-template <int F, int GPW>
-int32_t launch_cq_decode_tpl(const MatmulParams& p, bool exact, int waves, size_t lds, hipStream_t stream)
+template <int F, int GPW, bool WIDE>
+void launch_cq_decode_w(const MatmulParams& p, bool exact, int waves, size_t lds, hipStream_t stream)
 {
     const int tiles = p.tile_end - p.tile_begin;
     if (exact)
-        hipLaunchKernelGGL((matmul_cq_decode_kernel<F, GPW, true>), dim3(tiles), dim3(64 * waves), lds, stream, p);
+        hipLaunchKernelGGL((matmul_cq_decode_kernel<F, GPW, true, WIDE>), dim3(tiles), dim3(64 * waves), lds, stream,
+                           p);
     else
-        hipLaunchKernelGGL((matmul_cq_decode_kernel<F, GPW, false>), dim3(tiles), dim3(64 * waves), lds, stream, p);
+        hipLaunchKernelGGL((matmul_cq_decode_kernel<F, GPW, false, WIDE>), dim3(tiles), dim3(64 * waves), lds, stream,
+                           p);
+}
+
+template <int F, int GPW>
+int32_t launch_cq_decode_tpl(const MatmulParams& p, bool exact, int waves, size_t lds, hipStream_t stream)
+{
+    if constexpr (GPW <= 8) {  // the planner takes 5..16 tokens only up to 8 groups per wave
+        if (p.tokens > 4) {
+            launch_cq_decode_w<F, GPW, true>(p, exact, waves, lds, stream);
+            NHIP_CHECK_HIP(hipGetLastError());
+            return NHIP_OK;
+        }
+    }
+    launch_cq_decode_w<F, GPW, false>(p, exact, waves, lds, stream);
     NHIP_CHECK_HIP(hipGetLastError());
     return NHIP_OK;
 }
@@ -1246,14 +1387,16 @@ int32_t launch_cq_decode_gpw(const MatmulParams& p, int gpw, bool exact, int wav
     }
 }
 
-// Codebook formats, 1..4 tokens: runs matmul_cq_decode_kernel with GPW
-// groups per wave (4, one set, by default, more when that would take over 8
+// Codebook formats, 1..16 tokens: runs matmul_cq_decode_kernel (the
+// four-group sets for up to 4 tokens, one group per MFMA set for 5..16) with
+// GPW groups per wave (4 by default, more when that would take over 8
 // waves; NHIP_CQ_DECODE_GPW = 4, 8 or 16 overrides it for tuning) and one
-// wave per GPW groups.  Returns 1 when it does not apply
-// (more than 4 tokens, group sums requested, or K over 16*8 groups).
+// wave per GPW groups.  Returns false when it does not apply (more than 16
+// tokens, group sums requested, K over 16*8 groups, or products over 64 KB
+// of LDS).
 bool plan_cq_decode(const DeviceWeights* w, MatmulParams& p, int* gpw_out, int* waves_out, size_t* lds_out)
 {
-    if (p.tokens > 4 || p.dots) return false;
+    if (p.tokens > 16 || p.dots) return false;
     static const int gpw_override = [] {
         const char* e = getenv("NHIP_CQ_DECODE_GPW");
         const int v = e ? atoi(e) : 0;
@@ -1262,8 +1405,17 @@ bool plan_cq_decode(const DeviceWeights* w, MatmulParams& p, int* gpw_out, int* 
     int gpw = gpw_override ? gpw_override : 4;
     while (gpw < 16 && (w->groups + gpw - 1) / gpw > 8) gpw *= 2;
     const int waves = (w->groups + gpw - 1) / gpw;
-    if (waves > 8) return false;
-    p.ldd = waves * gpw + 4;  // every group a wave writes, + 4: conflict-free product writes
+    if (waves > 8 || (p.tokens > 4 && gpw > 8)) return false;
+    if (p.tokens <= 4) {
+        p.ldd = waves * gpw + 4;  // every group a wave writes, + 4: conflict-free product writes
+        p.swz = 0;
+    } else {
+        // every group a wave writes, in float4 columns swizzled within the
+        // largest power-of-two block (<= 16) that divides them
+        p.ldd = waves * gpw;
+        const int cols4 = p.ldd / 4;
+        p.swz = std::min(cols4 & -cols4, 16) - 1;
+    }
     const size_t lds = (size_t)2 * p.tokens * 16 * p.ldd * sizeof(float);
     if (lds > kMaxLds) return false;
     *gpw_out = gpw;
@@ -1503,15 +1655,28 @@ int32_t launch_dec_batch_ti(const MatmulBatch& b, int waves, size_t lds, hipStre
     }
 }
 
+template <int F, int GPW, bool WIDE>
+void launch_cq_batch_w(const MatmulBatch& b, bool exact, int waves, size_t lds, hipStream_t s)
+{
+    if (exact)
+        hipLaunchKernelGGL((matmul_cq_decode_batch_kernel<F, GPW, true, WIDE>), dim3(b.first[b.count]),
+                           dim3(64 * waves), lds, s, b);
+    else
+        hipLaunchKernelGGL((matmul_cq_decode_batch_kernel<F, GPW, false, WIDE>), dim3(b.first[b.count]),
+                           dim3(64 * waves), lds, s, b);
+}
+
 template <int F, int GPW>
 int32_t launch_cq_batch_tpl(const MatmulBatch& b, bool exact, int waves, size_t lds, hipStream_t s)
 {
-    if (exact)
-        hipLaunchKernelGGL((matmul_cq_decode_batch_kernel<F, GPW, true>), dim3(b.first[b.count]), dim3(64 * waves),
-                           lds, s, b);
-    else
-        hipLaunchKernelGGL((matmul_cq_decode_batch_kernel<F, GPW, false>), dim3(b.first[b.count]), dim3(64 * waves),
-                           lds, s, b);
+    if constexpr (GPW <= 8) {
+        if (b.job[0].tokens > 4) {
+            launch_cq_batch_w<F, GPW, true>(b, exact, waves, lds, s);
+            NHIP_CHECK_HIP(hipGetLastError());
+            return NHIP_OK;
+        }
+    }
+    launch_cq_batch_w<F, GPW, false>(b, exact, waves, lds, s);
     NHIP_CHECK_HIP(hipGetLastError());
     return NHIP_OK;
 }
@@ -1528,7 +1693,7 @@ int32_t launch_cq_batch_gpw(const MatmulBatch& b, int gpw, bool exact, int waves
 
 // Quant.MatMulBatch.Run (src/Needle/Quant.cs:697-706, 753-772): every job's
 // MatMulRows over all its rows with the shared activations.  The decode
-// sizes (int8 up to 16 tokens, codebook up to 4) run as one launch over the
+// sizes (up to 16 tokens) run as one launch over the
 // row tiles of every job; other token counts run the jobs one after another
 // (the same kernels as nhip_matmul_*_dev, so the same bits either way).
 int32_t run_matmul_batch(const DeviceWeights* const* w, int32_t count, const int8_t* q, const float* scales,

@@ -33,7 +33,7 @@ def run_batch(hip, handles, rows, q, scales, offsets, stride, tokens, pad=3):
 
 
 @pytest.mark.parametrize("bits", [2, 4])
-@pytest.mark.parametrize("tokens", [1, 3, 4, 7, 40])
+@pytest.mark.parametrize("tokens", [1, 3, 4, 7, 12, 16, 40])
 @pytest.mark.parametrize("jobs", [4, 1, 3])
 def test_codebook_batch_bit_exact(hip, orc, bits, tokens, jobs):
     rows = NEEDLE3_QKVG[:jobs]
