@@ -638,7 +638,8 @@ def codebook_lines(args) -> list:
     """The reference-native form of the GEMV configs: Cq4/Cq2 codebook
     weights, g128 norms, Hadamard-prepared activations."""
     out = []
-    for bits, (m, k, n) in [(4, (1, 1024, 4096)), (4, (3, 2048, 8192)), (2, (3, 2048, 8192))]:
+    for bits, (m, k, n) in [(4, (1, 1024, 4096)), (4, (3, 2048, 8192)), (2, (3, 2048, 8192)), (4, (16, 2048, 8192)),
+                            (2, (16, 2048, 8192))]:
         case = CqGemvCase(m, k, n, bits, seed=0x2800 + bits + m)
         t = case.time(max(200, args.steps // 2), args.warmup)
         g = case.bytes / (t * 1e-3) / 1e9
