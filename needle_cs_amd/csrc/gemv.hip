@@ -1392,8 +1392,8 @@ int32_t launch_cq_decode_gpw(const MatmulParams& p, int gpw, bool exact, int wav
 // GPW groups per wave (4 by default, more when that would take over 8
 // waves; NHIP_CQ_DECODE_GPW = 4, 8 or 16 overrides it for tuning) and one
 // wave per GPW groups.  Returns false when it does not apply (more than 16
-// tokens, group sums requested, K over 16*8 groups, or products over 64 KB
-// of LDS).
+// tokens, group sums requested, K over 16*8 groups, products over 64 KB of
+// LDS, or 5..16 tokens over more than 256 row tiles).
 bool plan_cq_decode(const DeviceWeights* w, MatmulParams& p, int* gpw_out, int* waves_out, size_t* lds_out)
 {
     if (p.tokens > 16 || p.dots) return false;
@@ -1406,6 +1406,10 @@ bool plan_cq_decode(const DeviceWeights* w, MatmulParams& p, int* gpw_out, int* 
     while (gpw < 16 && (w->groups + gpw - 1) / gpw > 8) gpw *= 2;
     const int waves = (w->groups + gpw - 1) / gpw;
     if (waves > 8 || (p.tokens > 4 && gpw > 8)) return false;
+    // 5..16 tokens over more than 256 tiles measured faster on the general kernel
+    // (Cq4 16 x 2048 x 8192: 6.46 against 5.71 us), fewer faster here (Cq2
+    // 16 x 768 x 2560: 4.13 against 7.10 us)
+    if (p.tokens > 4 && p.tile_end - p.tile_begin > 256) return false;
     if (p.tokens <= 4) {
         p.ldd = waves * gpw + 4;  // every group a wave writes, + 4: conflict-free product writes
         p.swz = 0;
