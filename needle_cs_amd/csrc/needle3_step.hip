@@ -166,6 +166,20 @@ __device__ __forceinline__ float row_inverse_rms(const float* x, float* sq, int 
     return *slot;
 }
 
+// The same, with `beside()` run by the other threads while lane 0 chains.
+template <typename F>
+__device__ __forceinline__ float row_inverse_rms_beside(const float* x, float* sq, int n, float* slot, F&& beside)
+{
+    for (int c = threadIdx.x; c < n; c += kThreads) sq[c] = x[c] * x[c];
+    __syncthreads();
+    if (threadIdx.x == 0)
+        *slot = inverse_rms_of(chain_sum(sq, n), n);
+    else
+        beside();
+    __syncthreads();
+    return *slot;
+}
+
 // ---------------------------------------------------------- gathers --
 
 struct Book {
@@ -257,10 +271,12 @@ struct HyperArgs {
 
 // RunLayerBatch's per-row mix (Engine.cs:2366-2381): hpre / postGate by
 // Sigmoid, Mix4 of the lanes into input and residual, Sinkhorn4x4 of the
-// residual-mix logits.  Wave 0 runs Sinkhorn4x4 with one lane per matrix
+// residual-mix logits.  Wave 1 runs Sinkhorn4x4 with one lane per matrix
 // entry (lane e = 4a + c, repeated across the wave): every lane of a row or
 // column forms the same left-to-right sum of its four entries, so each
-// normalisation is Scalar.Sinkhorn4x4's.  Then, on layers without an engram,
+// normalisation is Scalar.Sinkhorn4x4's.  Only the layer's tail reads the
+// mix matrix, so Sinkhorn runs beside the norm's sum of squares (or before
+// the engram gathers).  Then, on layers without an engram,
 // RunAttentionBatch's CenteredRmsFakeA8 of the residual and its 2-bit Prepare
 // (Engine.cs:2487-2490); on engram layers, ApplyEngramBatch's input
 // (Engine.cs:2404-2414): every table's GatherRow (zeros for row -1),
@@ -286,9 +302,17 @@ __global__ __launch_bounds__(kThreads) void n3_hyper_kernel(HyperArgs a)
             sn[q] = a.norm_in[c];
         }
     }
-    if (i < 64) {
-        const int e = i & 15, row = e >> 2, col = e & 3;
-        const float lg = a.a_res[0] * a.res_out[t * a.ld16 + e] + a.b_res[e];
+    const int e = i & 15;
+    const bool sink = (i >> 6) == 1;  // wave 1
+    const float lg = sink ? a.a_res[0] * a.res_out[t * a.ld16 + e] + a.b_res[e] : 0.0f;
+    if (i < 4) {
+        hpre[i] = sigmoid_poly(a.a_pre[0] * a.pre_out[t * a.ld4 + i] + a.b_pre[i] + (i == a.lane ? 4.0f : -4.0f));
+        a.post_gate[t * 4 + i] =
+            2.0f * sigmoid_poly(a.a_post[0] * a.post_out[t * a.ld4 + i] + a.b_post[i] + (i == a.lane ? 0.0f : -4.0f));
+    }
+    auto sinkhorn = [&]() {
+        if (!sink) return;
+        const int row = e >> 2, col = e & 3;
         const float l0 = __shfl(lg, row * 4), l1 = __shfl(lg, row * 4 + 1), l2 = __shfl(lg, row * 4 + 2),
                     l3 = __shfl(lg, row * 4 + 3);
         float r = exp_poly(lg - fmaxf(fmaxf(l0, l1), fmaxf(l2, l3)));
@@ -298,13 +322,8 @@ __global__ __launch_bounds__(kThreads) void n3_hyper_kernel(HyperArgs a)
             const float cs = __shfl(r, col) + __shfl(r, 4 + col) + __shfl(r, 8 + col) + __shfl(r, 12 + col);
             if (cs > 0.0f) r = r / cs;
         }
-        if (i < 16) a.mix[t * 16 + e] = r;
-        if (i < 4) {
-            hpre[i] = sigmoid_poly(a.a_pre[0] * a.pre_out[t * a.ld4 + i] + a.b_pre[i] + (i == a.lane ? 4.0f : -4.0f));
-            a.post_gate[t * 4 + i] =
-                2.0f * sigmoid_poly(a.a_post[0] * a.post_out[t * a.ld4 + i] + a.b_post[i] + (i == a.lane ? 0.0f : -4.0f));
-        }
-    }
+        if (i < 80) a.mix[t * 16 + e] = r;
+    };
     __syncthreads();
 #pragma unroll
     for (int q = 0; q < kPer; q++) {
@@ -318,6 +337,7 @@ __global__ __launch_bounds__(kThreads) void n3_hyper_kernel(HyperArgs a)
     }
     __syncthreads();
     if (a.tables) {
+        sinkhorn();
         const int sub = a.table_cols, per = sub / 128;
         for (int unit = i >> 6; unit < a.tables_count * per; unit += kWaves) {
             const int table = unit / per, g = unit % per;
@@ -332,7 +352,7 @@ __global__ __launch_bounds__(kThreads) void n3_hyper_kernel(HyperArgs a)
         prepare_row(sq, dim, 2, a.act, a.stride, t);
         return;
     }
-    const float inverse = row_inverse_rms(x, sq, dim, &inv_s);
+    const float inverse = row_inverse_rms_beside(x, sq, dim, &inv_s, sinkhorn);
 #pragma unroll
     for (int q = 0; q < kPer; q++) {
         const int c = col_of(q);
