@@ -848,10 +848,28 @@ __global__ __launch_bounds__(kThreads) void n3_tail_kernel(TailArgs a)
     }
     __syncthreads();
     if (!a.head_of) {  // the next layer's RmsFakeA8 and 4-bit Prepare
-        inverse = row_inverse_rms(ns, nsq, n4, &inv_s);
-        for (int c = threadIdx.x; c < n4; c += kThreads) ns[c] = ns[c] * inverse;
+        // RmsUnit then FakeA8 with one barrier: the peak of x * inverse is
+        // RoundNearest(max |x| * inverse) (inverse > 0 and rounding is
+        // monotone), so the row's max |x| is taken with the squares, before
+        // the chain, and the scaling and the int8 round trip run in one pass
+        float peak_x = 0.0f;
+        for (int c = threadIdx.x; c < n4; c += kThreads) {
+            nsq[c] = ns[c] * ns[c];
+            peak_x = fmaxf(peak_x, fabsf(ns[c]));
+        }
+        peak_x = wave_max(peak_x);
+        if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = peak_x;
         __syncthreads();
-        fake_row(ns, n4, red);
+        if (threadIdx.x == 0) inv_s = inverse_rms_of(chain_sum(nsq, n4), n4);
+        __syncthreads();
+        inverse = inv_s;
+        float m = red[0];
+        for (int w = 1; w < kWaves; w++) m = fmaxf(m, red[w]);
+        const float peak = m * inverse;
+        const float scale = peak > 0.0f ? peak / 127.0f : 1.0f;
+        const float round = 1.0f / scale;
+        for (int c = threadIdx.x; c < n4; c += kThreads) ns[c] = clamp_q((ns[c] * inverse) * round) * scale;
+        __syncthreads();
         prepare_row(ns, n4, 4, a.act, a.stride, t);
         return;
     }
