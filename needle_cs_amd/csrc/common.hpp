@@ -281,11 +281,61 @@ __device__ __forceinline__ float exp_poly(float x)
     return y * scale;
 }
 
+// The value lane (lane ^ S) of the wave holds, S = 1..32, without an LDS
+// round trip: DPP quad permutations [1,0,3,2] (1) and [2,3,0,1] (2), a row
+// half-mirror then the quad reversal [3,2,1,0] (4: 7 - l, then 3 - that
+// within the quad, is l ^ 4), a row rotation by 8 (8), and gfx950's
+// permlane16 / permlane32 swaps of a register with itself (16, 32: the swap
+// returns the lower rows' values in its first result and the upper rows' in
+// its second).
+template <int S>
+__device__ __forceinline__ uint32_t lane_xor(uint32_t v)
+{
+    if constexpr (S == 1) {
+        return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0xB1, 0xF, 0xF, false);
+    } else if constexpr (S == 2) {
+        return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x4E, 0xF, 0xF, false);
+    } else if constexpr (S == 4) {
+        const int m = __builtin_amdgcn_update_dpp(0, (int)v, 0x141, 0xF, 0xF, false);
+        return (uint32_t)__builtin_amdgcn_update_dpp(0, m, 0x1B, 0xF, 0xF, false);
+    } else if constexpr (S == 8) {
+        return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x128, 0xF, 0xF, false);
+    } else if constexpr (S == 16) {
+        const auto r = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+        return (threadIdx.x & 16) ? r[0] : r[1];
+    } else {
+        static_assert(S == 32, "lane_xor: S is a power of two below 64");
+        const auto r = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+        return (threadIdx.x & 32) ? r[0] : r[1];
+    }
+}
+template <int S>
+__device__ __forceinline__ float lane_xor(float v)
+{
+    return __uint_as_float(lane_xor<S>(__float_as_uint(v)));
+}
+
 // Sum of an int over the 64 lanes of a wave (exact), in every lane.
 __device__ __forceinline__ int wave_sum_i32(int v)
 {
-    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
+    v += (int)lane_xor<32>((uint32_t)v);
+    v += (int)lane_xor<16>((uint32_t)v);
+    v += (int)lane_xor<8>((uint32_t)v);
+    v += (int)lane_xor<4>((uint32_t)v);
+    v += (int)lane_xor<2>((uint32_t)v);
+    v += (int)lane_xor<1>((uint32_t)v);
     return v;
+}
+
+// One butterfly stage of hadamard_wave: lanes e and e ^ S pair up.
+template <int S>
+__device__ __forceinline__ void hadamard_stage(float& v0, float& v1)
+{
+    const float p0 = lane_xor<S>(v0);
+    const float p1 = lane_xor<S>(v1);
+    const bool upper = (threadIdx.x & S) != 0;
+    v0 = upper ? p0 - v0 : v0 + p0;
+    v1 = upper ? p1 - v1 : v1 + p1;
 }
 
 // Scalar.Hadamard (Scalar.cs:76-89) of one 128-element group held by a wave:
@@ -295,14 +345,12 @@ __device__ __forceinline__ int wave_sum_i32(int v)
 // them (the pairs of a stage are independent), then the 1/sqrt(128) scale.
 __device__ __forceinline__ void hadamard_wave(float& v0, float& v1)
 {
-    const int lane = threadIdx.x & 63;
-    for (int s = 1; s < 64; s <<= 1) {
-        const float p0 = __shfl_xor(v0, s);
-        const float p1 = __shfl_xor(v1, s);
-        const bool upper = (lane & s) != 0;
-        v0 = upper ? p0 - v0 : v0 + p0;
-        v1 = upper ? p1 - v1 : v1 + p1;
-    }
+    hadamard_stage<1>(v0, v1);
+    hadamard_stage<2>(v0, v1);
+    hadamard_stage<4>(v0, v1);
+    hadamard_stage<8>(v0, v1);
+    hadamard_stage<16>(v0, v1);
+    hadamard_stage<32>(v0, v1);
     const float a = v0, b = v1;
     v0 = (a + b) * 0.08838834764831845f;
     v1 = (a - b) * 0.08838834764831845f;
