@@ -604,60 +604,85 @@ size_t tail_lds_bytes(int dim, int rows, int cols)
 // scratch rows are cols + 1 apart (kron_scratch floats in all).
 __device__ __forceinline__ int kron_scratch(int rows, int cols) { return rows * cols + 32; }
 
+// The two chains of output element e0..e0+3 (row k = e0 / cols, columns c..c+3).
+// active is a multiple of 8 (the caller zero-fills z's rows up to it: a
+// zero product leaves a sum that starts at +0 unchanged).
+__device__ __forceinline__ void kron_first(const float* z, int active, const float* left, int rows, int cols, int e0,
+                                           float* scratch)
+{
+    const int k = e0 / cols, c = e0 - k * cols, ss = cols + 1;
+    float4 sum = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    for (int i0 = 0; i0 < active; i0 += 8) {
+        float lv[8];
+        float4 zv[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            lv[u] = left[(i0 + u) * rows + k];
+            zv[u] = *reinterpret_cast<const float4*>(z + (i0 + u) * cols + c);
+        }
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            sum.x = sum.x + lv[u] * zv[u].x;
+            sum.y = sum.y + lv[u] * zv[u].y;
+            sum.z = sum.z + lv[u] * zv[u].z;
+            sum.w = sum.w + lv[u] * zv[u].w;
+        }
+    }
+    float* srow = scratch + k * ss + c;
+    srow[0] = sum.x;
+    srow[1] = sum.y;
+    srow[2] = sum.z;
+    srow[3] = sum.w;
+}
+
+__device__ __forceinline__ void kron_second(const float* right, int cols, int e0, const float* scratch, float* result)
+{
+    const int k = e0 / cols, c = e0 - k * cols, ss = cols + 1;
+    float4 sum = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    for (int j0 = 0; j0 < cols; j0 += 8) {
+        float sv[8];
+        float4 rv[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            sv[u] = scratch[k * ss + j0 + u];
+            rv[u] = *reinterpret_cast<const float4*>(right + (j0 + u) * cols + c);
+        }
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            sum.x = sum.x + sv[u] * rv[u].x;
+            sum.y = sum.y + sv[u] * rv[u].y;
+            sum.z = sum.z + sv[u] * rv[u].z;
+            sum.w = sum.w + sv[u] * rv[u].w;
+        }
+    }
+    *reinterpret_cast<float4*>(result + e0) = sum;
+}
+
 __device__ __forceinline__ void kron_lds(const float* z, int active, const float* left, const float* right, int rows,
                                          int cols, int result_rows, float* scratch, float* result)
 {
     const int e0 = 4 * (int)threadIdx.x;
     const bool on = e0 < result_rows * cols;
-    const int k = on ? e0 / cols : 0, c = e0 - k * cols, ss = cols + 1;
-    float4 sum = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-    if (on) {
-        // active is a multiple of 8 (the caller zero-fills z's rows up to it:
-        // a zero product leaves a sum that starts at +0 unchanged)
-        for (int i0 = 0; i0 < active; i0 += 8) {
-            float lv[8];
-            float4 zv[8];
-#pragma unroll
-            for (int u = 0; u < 8; u++) {
-                lv[u] = left[(i0 + u) * rows + k];
-                zv[u] = *reinterpret_cast<const float4*>(z + (i0 + u) * cols + c);
-            }
-#pragma unroll
-            for (int u = 0; u < 8; u++) {
-                sum.x = sum.x + lv[u] * zv[u].x;
-                sum.y = sum.y + lv[u] * zv[u].y;
-                sum.z = sum.z + lv[u] * zv[u].z;
-                sum.w = sum.w + lv[u] * zv[u].w;
-            }
-        }
-        float* srow = scratch + k * ss + c;
-        srow[0] = sum.x;
-        srow[1] = sum.y;
-        srow[2] = sum.z;
-        srow[3] = sum.w;
-    }
+    if (on) kron_first(z, active, left, rows, cols, e0, scratch);
     __syncthreads();
-    if (on) {
-        sum = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-        for (int j0 = 0; j0 < cols; j0 += 8) {
-            float sv[8];
-            float4 rv[8];
-#pragma unroll
-            for (int u = 0; u < 8; u++) {
-                sv[u] = scratch[k * ss + j0 + u];
-                rv[u] = *reinterpret_cast<const float4*>(right + (j0 + u) * cols + c);
-            }
-#pragma unroll
-            for (int u = 0; u < 8; u++) {
-                sum.x = sum.x + sv[u] * rv[u].x;
-                sum.y = sum.y + sv[u] * rv[u].y;
-                sum.z = sum.z + sv[u] * rv[u].z;
-                sum.w = sum.w + sv[u] * rv[u].w;
-            }
-        }
-        *reinterpret_cast<float4*>(result + e0) = sum;
-    }
+    if (on) kron_second(right, cols, e0, scratch, result);
     __syncthreads();
+}
+
+// kron_lds by the first `nthreads` threads (a multiple of 64) with no block
+// barrier: thread u owns the outputs 4f.. for f = u, u + nthreads, ...  A
+// row's cols / 4 outputs are consecutive f in one wave (cols / 4 divides
+// 64), which writes that row of scratch and then reads it, so a wave-scope
+// fence orders the passes.  The caller synchronises before result is read.
+__device__ __forceinline__ void kron_rows(const float* z, int active, const float* left, const float* right,
+                                          int rows, int cols, int result_rows, float* scratch, float* result,
+                                          int nthreads)
+{
+    const int total4 = result_rows * cols / 4;
+    for (int f = threadIdx.x; f < total4; f += nthreads) kron_first(z, active, left, rows, cols, 4 * f, scratch);
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    for (int f = threadIdx.x; f < total4; f += nthreads) kron_second(right, cols, 4 * f, scratch, result);
 }
 
 // The end of a layer for one row, in RunLayerBatch's order
@@ -795,19 +820,27 @@ __global__ __launch_bounds__(kThreads) void n3_tail_kernel(TailArgs a)
         if (c < active_rows * a.cols) front[c] = c < dim ? norm[c] * d1v[q] : 0.0f;
     }
     __syncthreads();
-    if (threadIdx.x < 8) weights[threadIdx.x] = chain_sum(prod + threadIdx.x * pstride, dim);
-    __syncthreads();
-    if (threadIdx.x == 0) {  // Scalar.Softmax over the eight weights
-        float peak = -INFINITY;
-        for (int j = 0; j < 8; j++) peak = fmaxf(peak, weights[j]);
-        float total = 0.0f;
-        for (int j = 0; j < 8; j++) {
-            weights[j] = exp_poly(weights[j] - peak);
-            total = total + weights[j];
+    // wave 3 sums the condition weights and takes their softmax while waves
+    // 0-2 run the first Kronecker product, which does not depend on them
+    if (threadIdx.x >= 3 * 64) {
+        const int lane = threadIdx.x - 3 * 64;
+        if (lane < 8) weights[lane] = chain_sum(prod + lane * pstride, dim);
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        if (lane == 0) {  // Scalar.Softmax over the eight weights
+            float peak = -INFINITY;
+            for (int j = 0; j < 8; j++) peak = fmaxf(peak, weights[j]);
+            float total = 0.0f;
+            for (int j = 0; j < 8; j++) {
+                weights[j] = exp_poly(weights[j] - peak);
+                total = total + weights[j];
+            }
+            for (int j = 0; j < 8; j++) weights[j] = weights[j] / total;
         }
-        for (int j = 0; j < 8; j++) weights[j] = weights[j] / total;
+    } else {
+        kron_rows(front, active_rows, wl, wr, a.rows, a.cols, a.rows, scratch, back, 3 * 64);
     }
-    kron_lds(front, active_rows, wl, wr, a.rows, a.cols, a.rows, scratch, back);
+    __syncthreads();
 #pragma unroll
     for (int q = 0; q < kPer; q++) {  // Scalar.PermuteModulateActivate
         const int n = col_of(q);
@@ -1092,8 +1125,8 @@ int32_t load_model(nhip_ctx* c)
                  c->vd, h[15]);
     NHIP_REQUIRE(h[19] == 3 && (c->site_count == 0 || h[23] == 4) && c->dim % 128 == 0 && c->dim <= 1024,
                  "conv taps %u, engram taps %u, dim %d (a multiple of 128 up to 1024)", h[19], h[23], c->dim);
-    NHIP_REQUIRE(c->hada_cols % 8 == 0 && c->hada_rows % 8 == 0 && c->hada_rows * c->hada_cols == hada_n &&
-                     hada_n >= c->dim,
+    NHIP_REQUIRE(c->hada_cols % 8 == 0 && 64 % (c->hada_cols / 4) == 0 && c->hada_rows % 8 == 0 &&
+                     c->hada_rows * c->hada_cols == hada_n && hada_n >= c->dim,
                  "MLP size %d must split into rows x cols (cols divisible by 8) covering dim %d", hada_n, c->dim);
     NHIP_REQUIRE(c->heads * c->qk + c->kv * (c->qk + c->vd) <= kHistPer * kThreads, "Q/K/V width %d above %d",
                  c->heads * c->qk + c->kv * (c->qk + c->vd), kHistPer * kThreads);
