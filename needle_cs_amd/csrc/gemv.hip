@@ -253,7 +253,7 @@ __device__ __forceinline__ Operand<F> operand_if(const Operand<F>& o, bool keep)
 //     which is Scalar.MatMulRows' exact operation order (Scalar.cs:185-189);
 //     phases continue the same accumulators, so the order spans all of K.
 template <int F, int CB, bool DOTS>
-__global__ __launch_bounds__(512) void matmul_kernel(MatmulParams p)
+__device__ __forceinline__ void matmul_tile(const MatmulParams& p, const int tile)
 {
     using T = Traits<F>;
     extern __shared__ __align__(16) uint8_t lds[];
@@ -266,7 +266,6 @@ __global__ __launch_bounds__(512) void matmul_kernel(MatmulParams p)
     const int S = blockDim.x >> 6;
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
-    const int tile = p.tile_begin + blockIdx.x;
     const int tb = blockIdx.y * 16;
     const int M = min(16, p.tokens - tb);
     const int G = p.groups;
@@ -409,6 +408,12 @@ __global__ __launch_bounds__(512) void matmul_kernel(MatmulParams p)
         const int nc = tile * 16 + cr;
         if (nc >= p.row_start && nc < p.row_end) p.y[(size_t)(tb + ct) * p.ldy + nc] = acc - bias;
     }
+}
+
+template <int F, int CB, bool DOTS>
+__global__ __launch_bounds__(512) void matmul_kernel(MatmulParams p)
+{
+    matmul_tile<F, CB, DOTS>(p, p.tile_begin + blockIdx.x);
 }
 
 // Literal int8 path.  Same phases and epilogue as matmul_kernel, but the
@@ -833,6 +838,16 @@ __device__ __forceinline__ int batch_job(const MatmulBatch& b)
 #pragma unroll
     for (int i = 1; i < kMaxBatchJobs; i++) j += (i < b.count && (int)blockIdx.x >= b.first[i]) ? 1 : 0;
     return j;
+}
+
+// MatMulBatch over more tokens than the decode kernels take: the general
+// kernel's tiles of every job (same K, tokens and phase plan) in one launch.
+template <int F, int CB>
+__global__ __launch_bounds__(512) void matmul_batch_kernel(MatmulBatch b)
+{
+    const int j = batch_job(b);
+    const MatmulParams& p = b.job[j];
+    matmul_tile<F, CB, false>(p, p.tile_begin + (int)blockIdx.x - b.first[j]);
 }
 
 template <int CB, int TI, bool EXACT>
@@ -1551,6 +1566,37 @@ MatmulParams matmul_params(const DeviceWeights* w, const int8_t* q, const float*
     return p;
 }
 
+// Waves per 16-row tile of the general kernels (each loads 1/waves of the
+// tile's weight blocks) for `tiles` row tiles; NHIP_MATMUL_WAVES (4 or 8)
+// overrides the default for tuning.
+int general_waves(int tiles, int tokens)
+{
+    static const int waves_override = [] {
+        const char* e = getenv("NHIP_MATMUL_WAVES");
+        const int v = e ? atoi(e) : 0;
+        return (v == 4 || v == 8) ? v : 0;
+    }();
+    return waves_override ? waves_override : (tiles * ((tokens + 15) / 16) >= 512 ? 4 : 8);
+}
+
+// Codebook formats, general kernel.  Groups per phase: the int32 D buffer
+// [gph][M][16] plus the decoded scales [gph][16] stay within 64 KB of LDS,
+// and no wave holds more than 8 weight blocks.  False (and the bytes needed
+// in *lds) when it does not fit.
+bool plan_general_cq(const DeviceWeights* w, MatmulParams& p, int waves, size_t* lds)
+{
+    const int m = std::min(16, p.tokens);
+    const int gpb = w->format == WeightFormat::Cq4 ? 1 : 2;
+    int gph = std::min(std::min(w->groups, 1024 / (m + 1) - 12), 8 * waves * gpb);
+    gph -= gph % gpb;
+    if (gph < gpb) gph = gpb;
+    p.gph = gph;
+    p.ldd = ((gph + 3) & ~3) + 4;
+    p.d_bytes = m * 16 * p.ldd * 4;
+    *lds = (size_t)p.d_bytes + (size_t)16 * p.ldd * 4 + 64 * 4;
+    return *lds <= kMaxLds;
+}
+
 int32_t run_matmul(const DeviceWeights* w, const int8_t* q, const float* scales, const float* offsets,
                    int32_t stride, int32_t tokens, float* y, int32_t ldy, int32_t row_start,
                    int32_t row_end, int32_t* dots, hipStream_t stream)
@@ -1570,15 +1616,8 @@ int32_t run_matmul(const DeviceWeights* w, const int8_t* q, const float* scales,
 
     MatmulParams p = matmul_params(w, q, scales, offsets, stride, tokens, y, ldy, row_start, row_end, dots);
 
-    // Waves per 16-row tile (each loads 1/waves of the tile's weight blocks).
-    // NHIP_MATMUL_WAVES (4 or 8) overrides the default for tuning.
     const int tiles = p.tile_end - p.tile_begin;
-    static const int waves_override = [] {
-        const char* e = getenv("NHIP_MATMUL_WAVES");
-        const int v = e ? atoi(e) : 0;
-        return (v == 4 || v == 8) ? v : 0;
-    }();
-    const int waves = waves_override ? waves_override : (tiles * ((tokens + 15) / 16) >= 512 ? 4 : 8);
+    const int waves = general_waves(tiles, tokens);
     const int m = std::min(16, tokens);
     if (w->format == WeightFormat::Int8G32) {
         if (!dots && tokens >= kGemmMinTokens)
@@ -1610,18 +1649,8 @@ int32_t run_matmul(const DeviceWeights* w, const int8_t* q, const float* scales,
         const int32_t drc = try_cq_decode(w, p, stream);
         if (drc <= 0) return drc;
     }
-    // Codebook formats.  Groups per phase: the int32 D buffer [gph][M][16]
-    // plus the decoded scales [gph][16] stay within 64 KB of LDS, and no
-    // wave holds more than 8 weight blocks.
-    const int gpb = w->format == WeightFormat::Cq4 ? 1 : 2;
-    int gph = std::min(std::min(w->groups, 1024 / (m + 1) - 12), 8 * waves * gpb);
-    gph -= gph % gpb;
-    if (gph < gpb) gph = gpb;
-    p.gph = gph;
-    p.ldd = ((gph + 3) & ~3) + 4;
-    p.d_bytes = m * 16 * p.ldd * 4;
-    const size_t lds = (size_t)p.d_bytes + (size_t)16 * p.ldd * 4 + 64 * 4;
-    if (lds > kMaxLds) {
+    size_t lds = 0;
+    if (!plan_general_cq(w, p, waves, &lds)) {
         set_error("matmul needs %zu bytes of LDS (max %zu)", lds, kMaxLds);
         return NHIP_ERR_UNSUPPORTED;
     }
@@ -1695,11 +1724,29 @@ int32_t launch_cq_batch_gpw(const MatmulBatch& b, int gpw, bool exact, int waves
     }
 }
 
+template <int F, int CB>
+int32_t launch_gen_batch(const MatmulBatch& b, int waves, size_t lds, hipStream_t s)
+{
+    hipLaunchKernelGGL((matmul_batch_kernel<F, CB>), dim3(b.first[b.count], (b.job[0].tokens + 15) / 16),
+                       dim3(64 * waves), lds, s, b);
+    NHIP_CHECK_HIP(hipGetLastError());
+    return NHIP_OK;
+}
+
+template <int F>
+int32_t launch_gen_batch_fmt(const MatmulBatch& b, int per, int waves, size_t lds, hipStream_t s)
+{
+    if (per <= 2) return launch_gen_batch<F, 2>(b, waves, lds, s);
+    if (per <= 4) return launch_gen_batch<F, 4>(b, waves, lds, s);
+    return launch_gen_batch<F, 8>(b, waves, lds, s);
+}
+
 // Quant.MatMulBatch.Run (src/Needle/Quant.cs:697-706, 753-772): every job's
 // MatMulRows over all its rows with the shared activations.  The decode
-// sizes (up to 16 tokens) run as one launch over the
-// row tiles of every job; other token counts run the jobs one after another
-// (the same kernels as nhip_matmul_*_dev, so the same bits either way).
+// sizes (up to 16 tokens), and the codebook formats at any token count (the
+// general kernel), run as one launch over the row tiles of every job; the
+// literal format past 16 tokens runs the jobs one after another (the same
+// kernels as nhip_matmul_*_dev, so the same bits either way).
 int32_t run_matmul_batch(const DeviceWeights* const* w, int32_t count, const int8_t* q, const float* scales,
                          const float* offsets, int32_t stride, int32_t tokens, float* const* y, const int32_t* ldy,
                          hipStream_t stream)
@@ -1740,6 +1787,18 @@ int32_t run_matmul_batch(const DeviceWeights* const* w, int32_t count, const int
                                                       : launch_dec_batch_ti<8, false>(b, waves, lds, stream));
         return w[0]->format == WeightFormat::Cq4 ? launch_cq_batch_gpw<kCq4>(b, gpw, exact, waves, lds, stream)
                                                  : launch_cq_batch_gpw<kCq2>(b, gpw, exact, waves, lds, stream);
+    }
+    if (cq) {  // the general kernel over every job's tiles, one launch
+        const int waves2 = general_waves(b.first[count], tokens);
+        size_t lds2 = 0;
+        bool fits = true;
+        for (int j = 0; j < count && fits; j++) fits = plan_general_cq(w[j], b.job[j], waves2, &lds2);
+        if (fits) {
+            const int gpb = w[0]->format == WeightFormat::Cq4 ? 1 : 2;
+            const int per = ((b.job[0].gph + gpb - 1) / gpb + waves2 - 1) / waves2;
+            return w[0]->format == WeightFormat::Cq4 ? launch_gen_batch_fmt<kCq4>(b, per, waves2, lds2, stream)
+                                                     : launch_gen_batch_fmt<kCq2>(b, per, waves2, lds2, stream);
+        }
     }
     for (int j = 0; j < count; j++) {
         rc = run_matmul(w[j], q, scales, offsets, stride, tokens, y[j], ldy[j], 0, w[j]->rows, nullptr, stream);
