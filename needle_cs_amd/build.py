@@ -6,6 +6,10 @@ Every HIP source under csrc/ is compiled for gfx950 only, with
   -packed-fp32-ops    off: no v_pk_* fp32 instructions are generated
   -amdgpu-mfma-vgpr-form  MFMA results in VGPRs (no AGPR copies before the
                       VALU epilogues)
+  -amdgpu-kernarg-preload-count=16  leading scalar kernel arguments are
+                      preloaded into SGPRs (no argument-segment round trip
+                      before a kernel's first loads; see ArgHead in
+                      csrc/common.hpp)
 and linked into needle_cs_amd/libneedle_hip.so next to this file.
 """
 from __future__ import annotations
@@ -31,6 +35,7 @@ FLAGS = [
     "-ffp-contract=off",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-mllvm", "-amdgpu-mfma-vgpr-form",
+    "-mllvm", "-amdgpu-kernarg-preload-count=16",
     "-Wall",
     "-Wno-unused-function",
     "-I", INCLUDE,

@@ -46,6 +46,22 @@ int32_t attention_scratch_setup();
 hipStream_t default_stream();
 inline hipStream_t as_stream(void* s) { return s ? static_cast<hipStream_t>(s) : default_stream(); }
 
+// ------------------------------------------------ preloaded arguments --
+
+// gfx950 loads a kernel's leading scalar arguments into SGPRs before its
+// first instruction (kernarg preload, built with
+// -amdgpu-kernarg-preload-count; 14 SGPRs at most), while a struct argument
+// is read from the argument segment with a scalar memory round trip.  A
+// kernel whose first loads need fields of its parameter struct takes those
+// fields again as leading pointer and 64-bit arguments (a "head", at most
+// seven 8-byte words) and overwrites the struct's copies with them: its
+// first loads then issue without waiting for the argument segment (about
+// 0.25 us per launch).  Pointers travel as pointers, so that the compiler
+// still knows them to be global memory; 32-bit fields travel in pairs.
+inline uint64_t head_pair(int32_t lo, int32_t hi) { return (uint64_t)(uint32_t)lo | ((uint64_t)(uint32_t)hi << 32); }
+__device__ __forceinline__ int32_t head_lo(uint64_t v) { return (int32_t)(uint32_t)v; }
+__device__ __forceinline__ int32_t head_hi(uint64_t v) { return (int32_t)(uint32_t)(v >> 32); }
+
 // ------------------------------------------------------- device weights --
 
 enum class WeightFormat : int32_t { Int8G32 = 8, Cq2 = 2, Cq4 = 4 };

@@ -80,15 +80,20 @@ __device__ __host__ __forceinline__ int act_pos(int slot, int kq)
 }
 
 struct MatmulParams {
+    // tiles .. mask_rows: what the decode kernels' first loads need, also
+    // passed as their preloaded leading arguments (MATMUL_HEAD_PARAMS)
     const uint8_t* tiles;
     const uint16_t* norms;
     const int8_t* q;          // [tokens][cols]
     const float* qscale;      // int8: [tokens]; Cq: [tokens][stride]
+    int32_t tokens, cols, groups, blocks;
+    int32_t tile_begin;
+    int32_t mask_rows;        // > 0: tile_mask is set (see below)
     const float* offsets;     // Cq: [tokens][stride]
     float* y;
     int32_t* dots;
-    int32_t tokens, cols, groups, blocks, groups_pad8, stride, ldy;
-    int32_t row_start, row_end, tile_begin, tile_end;
+    int32_t groups_pad8, stride, ldy;  // groups_pad8 = (groups + 7) & ~7
+    int32_t row_start, row_end, tile_end;
     int32_t gph;              // groups per phase (a multiple of Traits::GPB)
     int32_t d_bytes;          // LDS bytes of the D buffer of one phase
     int32_t ldd;              // LDS row stride (int32) of D and scales: roundup4(gph) + 4
@@ -96,11 +101,30 @@ struct MatmulParams {
     int32_t swz;              // decode path, 5..16 tokens: float4-column swizzle mask of the products
     int32_t swiglu;           // fused decode path: rows are (8 gate, 8 up) pairs per tile, store SwiGLU
     const uint32_t* tile_mask;  // decode kernel: [mask_rows][mask_words] id bitsets; tiles with no set bit
-    int32_t mask_words, mask_rows;  // in any row are skipped (their outputs are left untouched)
+    int32_t mask_words;         // in any row are skipped (their outputs are left untouched)
     uint32_t t0, t1, t2, t3;  // codebook bytes 0..15
     uint32_t x0, x1, x2, x3;  // the split tables of lut4x (TA, TB)
     float byte_scale;
 };
+
+// The decode kernels' head (see head_pair): the fields of their first loads.
+#define MATMUL_HEAD_PARAMS const uint8_t *h_tiles, const uint16_t *h_norms, const int8_t *h_q, const float *h_qscale, \
+                           uint64_t h_tokens_cols, uint64_t h_groups_blocks, uint64_t h_begin_mask
+#define MATMUL_HEAD_ARGS(p) (p).tiles, (p).norms, (p).q, (p).qscale, head_pair((p).tokens, (p).cols), \
+                            head_pair((p).groups, (p).blocks), head_pair((p).tile_begin, (p).mask_rows)
+#define MATMUL_TAKE_HEAD(p)                    \
+    do {                                       \
+        (p).tiles = h_tiles;                   \
+        (p).norms = h_norms;                   \
+        (p).q = h_q;                           \
+        (p).qscale = h_qscale;                 \
+        (p).tokens = head_lo(h_tokens_cols);   \
+        (p).cols = head_hi(h_tokens_cols);     \
+        (p).groups = head_lo(h_groups_blocks); \
+        (p).blocks = head_hi(h_groups_blocks); \
+        (p).tile_begin = head_lo(h_begin_mask); \
+        (p).mask_rows = head_hi(h_begin_mask); \
+    } while (0)
 
 __device__ __forceinline__ uint32_t lut2(uint32_t idx, uint32_t t0)
 {
@@ -716,13 +740,11 @@ __device__ __forceinline__ void i8_decode_tile(const MatmulParams& p, const int 
     const int mb0 = wave * CB;
     const int g_first = mb0 * 2;
     const u4* wbase = reinterpret_cast<const u4*>(p.tiles) + (size_t)tile * p.blocks * 64 + lane;
-    const uint16_t* nrow = p.norms + (size_t)n * p.groups_pad8 + g_first;
-    // every kernel argument the loads need, read before the mask branch: one
-    // round trip to the argument segment instead of one per side of it
-    asm volatile("" ::"s"(p.tiles), "s"(p.norms), "s"(p.q), "s"(p.qscale), "s"(p.cols), "s"(p.blocks),
-                 "s"(p.groups_pad8), "s"(p.tile_mask));
-    if (p.tile_mask) {
+    const uint16_t* nrow = p.norms + (size_t)n * ((G + 7) & ~7) + g_first;
+    if (p.mask_rows > 0) {
         // sparse rows: the tile's 16 ids are bits 16*(tile&1).. of word tile/2
+        // (the mask and its word count are read from the argument segment
+        // only on this path)
         uint32_t live = 0;
         for (int t = 0; t < p.mask_rows; t++)
             live |= (p.tile_mask[(size_t)t * p.mask_words + (tile >> 1)] >> (16 * (tile & 1))) & 0xFFFFu;
@@ -814,8 +836,9 @@ __device__ __forceinline__ void i8_decode_tile(const MatmulParams& p, const int 
 }
 
 template <int CB, int TI, bool EXACT>
-__global__ __launch_bounds__(512) void matmul_i8_decode_kernel(MatmulParams p)
+__global__ __launch_bounds__(512) void matmul_i8_decode_kernel(MATMUL_HEAD_PARAMS, MatmulParams p)
 {
+    MATMUL_TAKE_HEAD(p);
     i8_decode_tile<CB, TI, EXACT>(p, p.tile_begin + blockIdx.x);
 }
 
@@ -889,23 +912,27 @@ __device__ __forceinline__ void cq_decode_tile(const MatmulParams& p, const int 
     const int n = tile * 16 + r;
     const int g_first = wave * GPW;
     const u4* wbase = reinterpret_cast<const u4*>(p.tiles) + (size_t)tile * p.blocks * 64 + lane;
-    const uint16_t* nrow = p.norms + (size_t)n * p.groups_pad8;
-    // the arguments of every load, read together: one round trip to the
-    // argument segment
-    asm volatile("" ::"s"(p.tiles), "s"(p.norms), "s"(p.q), "s"(p.qscale), "s"(p.offsets), "s"(p.cols),
-                 "s"(p.stride), "s"(p.blocks), "s"(p.groups_pad8), "s"(p.tile_mask));
+    const uint16_t* nrow = p.norms + (size_t)n * ((G + 7) & ~7);
 
     // 1. A operands: lane (r, kq) feeds A row r of every set, token r%4
     //    (rows of tokens >= M repeat token M-1; their D rows are never
-    //    read) of group g_first + 4c + r/4; 2. activation scales and
-    //    offsets and 3. weight scales of the lane's groups g_first + 4c + kq;
-    //    4. weight blocks -- all in flight together
+    //    read) of group g_first + 4c + r/4; 2. weight scales of the lane's
+    //    groups g_first + 4c + kq; 3. weight blocks; 4. the activation
+    //    scales and offsets of those groups -- all in flight together (the
+    //    first three from the preloaded arguments, the last after the
+    //    argument segment's stride and offsets arrive)
     const int8_t* qrow = p.q + (size_t)min(r & 3, M - 1) * p.cols;
     Operand<F> av[SETS];
 #pragma unroll
     for (int c = 0; c < SETS; c++) av[c] = load_operand<F>(qrow, true, min(g_first + 4 * c + (r >> 2), G - 1), kq);
-    float sc[SETS][4], of[SETS][4];
     uint16_t hraw[SETS];
+#pragma unroll
+    for (int c = 0; c < SETS; c++) hraw[c] = nrow[min(g_first + 4 * c + kq, G - 1)];
+    u4 w[CB];
+#pragma unroll
+    for (int c = 0; c < CB; c++)
+        w[c] = __builtin_nontemporal_load(wbase + (size_t)min(wave * CB + c, p.blocks - 1) * 64);
+    float sc[SETS][4], of[SETS][4];
 #pragma unroll
     for (int c = 0; c < SETS; c++) {
         const int g = min(g_first + 4 * c + kq, G - 1);
@@ -915,12 +942,7 @@ __device__ __forceinline__ void cq_decode_tile(const MatmulParams& p, const int 
             sc[c][i] = p.qscale[at];
             of[c][i] = p.offsets[at];
         }
-        hraw[c] = nrow[g];
     }
-    u4 w[CB];
-#pragma unroll
-    for (int c = 0; c < CB; c++)
-        w[c] = __builtin_nontemporal_load(wbase + (size_t)min(wave * CB + c, p.blocks - 1) * 64);
     __builtin_amdgcn_sched_barrier(0);
 
 #pragma unroll
@@ -1001,17 +1023,22 @@ __device__ __forceinline__ void cq_decode_wide_tile(const MatmulParams& p, const
     const int n = tile * 16 + r;
     const int g_first = wave * GPW;
     const u4* wbase = reinterpret_cast<const u4*>(p.tiles) + (size_t)tile * p.blocks * 64 + lane;
-    const uint16_t* nrow = p.norms + (size_t)n * p.groups_pad8;
-    asm volatile("" ::"s"(p.tiles), "s"(p.norms), "s"(p.q), "s"(p.qscale), "s"(p.offsets), "s"(p.cols),
-                 "s"(p.stride), "s"(p.blocks), "s"(p.groups_pad8));
+    const uint16_t* nrow = p.norms + (size_t)n * ((G + 7) & ~7);
 
-    // 1. A operands of token r, 2. activation scales and offsets of tokens
-    // 4kq..4kq+3, 3. weight scales of row n, 4. weight blocks -- all in flight
-    // together
+    // 1. A operands of token r, 2. weight scales of row n, 3. weight blocks,
+    // 4. activation scales and offsets of tokens 4kq..4kq+3 (their stride
+    // and offsets come from the argument segment) -- all in flight together
     const int8_t* qrow = p.q + (size_t)min(r, M - 1) * p.cols;
     Operand<F> av[GPW];
 #pragma unroll
     for (int c = 0; c < GPW; c++) av[c] = load_operand<F>(qrow, r < M, min(g_first + c, G - 1), kq);
+    uint16_t hraw[GPW];
+#pragma unroll
+    for (int c = 0; c < GPW; c++) hraw[c] = nrow[min(g_first + c, G - 1)];
+    u4 w[CB];
+#pragma unroll
+    for (int c = 0; c < CB; c++)
+        w[c] = __builtin_nontemporal_load(wbase + (size_t)min(wave * CB + c, p.blocks - 1) * 64);
     float sc[GPW][4], of[GPW][4];
 #pragma unroll
     for (int c = 0; c < GPW; c++) {
@@ -1023,13 +1050,6 @@ __device__ __forceinline__ void cq_decode_wide_tile(const MatmulParams& p, const
             of[c][i] = p.offsets[at];
         }
     }
-    uint16_t hraw[GPW];
-#pragma unroll
-    for (int c = 0; c < GPW; c++) hraw[c] = nrow[min(g_first + c, G - 1)];
-    u4 w[CB];
-#pragma unroll
-    for (int c = 0; c < CB; c++)
-        w[c] = __builtin_nontemporal_load(wbase + (size_t)min(wave * CB + c, p.blocks - 1) * 64);
     __builtin_amdgcn_sched_barrier(0);
 
     const int tq = 4 * kq;  // first token of this lane's MFMA results
@@ -1092,8 +1112,9 @@ __device__ __forceinline__ void cq_decode_wide_tile(const MatmulParams& p, const
 }
 
 template <int F, int GPW, bool EXACT, bool WIDE>
-__global__ __launch_bounds__(512) void matmul_cq_decode_kernel(MatmulParams p)
+__global__ __launch_bounds__(512) void matmul_cq_decode_kernel(MATMUL_HEAD_PARAMS, MatmulParams p)
 {
+    MATMUL_TAKE_HEAD(p);
     if constexpr (WIDE)
         cq_decode_wide_tile<F, GPW, EXACT>(p, p.tile_begin + blockIdx.x);
     else
@@ -1290,7 +1311,8 @@ template <int CB, int TI, bool EXACT>
 int32_t launch_dec_tpl(const MatmulParams& p, int waves, size_t lds, hipStream_t stream)
 {
     const int tiles = p.tile_end - p.tile_begin;
-    hipLaunchKernelGGL((matmul_i8_decode_kernel<CB, TI, EXACT>), dim3(tiles), dim3(64 * waves), lds, stream, p);
+    hipLaunchKernelGGL((matmul_i8_decode_kernel<CB, TI, EXACT>), dim3(tiles), dim3(64 * waves), lds, stream,
+                       MATMUL_HEAD_ARGS(p), p);
     NHIP_CHECK_HIP(hipGetLastError());
     return NHIP_OK;
 }
@@ -1371,10 +1393,10 @@ void launch_cq_decode_w(const MatmulParams& p, bool exact, int waves, size_t lds
     const int tiles = p.tile_end - p.tile_begin;
     if (exact)
         hipLaunchKernelGGL((matmul_cq_decode_kernel<F, GPW, true, WIDE>), dim3(tiles), dim3(64 * waves), lds, stream,
-                           p);
+                           MATMUL_HEAD_ARGS(p), p);
     else
         hipLaunchKernelGGL((matmul_cq_decode_kernel<F, GPW, false, WIDE>), dim3(tiles), dim3(64 * waves), lds, stream,
-                           p);
+                           MATMUL_HEAD_ARGS(p), p);
 }
 
 template <int F, int GPW>
