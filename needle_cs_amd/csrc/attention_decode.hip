@@ -74,6 +74,28 @@ struct DecodeAttnParams {
     float inv_sqrt;
 };
 
+// The attention kernels' preloaded head (head_pair, common.hpp): the span
+// arrays, the two pointers of the kernel's first other loads (A, B: the
+// chunk and row kernels' q and qscale, the POST row kernel's qkv and
+// positions, the merge kernel's peaks and sums), (heads, kv_heads) and
+// (kv_per_block, rows).
+#define ATTN_HEAD_PARAMS const int32_t *h_slot, const int32_t *h_first, const int32_t *h_count, const void *h_a, \
+                         const void *h_b, uint64_t h_heads, uint64_t h_blocks_rows
+#define ATTN_HEAD_ARGS(p, A, B) (p).row_slot, (p).row_first, (p).row_count, (const void*)(A), (const void*)(B), \
+                                head_pair((p).heads, (p).kv_heads), head_pair((p).kv_per_block, (p).rows)
+#define ATTN_TAKE_HEAD(p, A, B)                                              \
+    do {                                                                     \
+        (p).row_slot = h_slot;                                               \
+        (p).row_first = h_first;                                             \
+        (p).row_count = h_count;                                             \
+        (p).A = (decltype((p).A))(h_a);                                      \
+        (p).B = (decltype((p).B))(h_b);                                      \
+        (p).heads = head_lo(h_heads);                                        \
+        (p).kv_heads = head_hi(h_heads);                                     \
+        (p).kv_per_block = head_lo(h_blocks_rows);                           \
+        (p).rows = head_hi(h_blocks_rows);                                   \
+    } while (0)
+
 }  // namespace
 
 // Longest chunk of the plan: at most 32 positions below 16*max_chunks
@@ -144,8 +166,9 @@ __device__ __forceinline__ int32_t uniform_load(const int32_t* a, int i)
     return ((const __attribute__((address_space(4))) int32_t*)a)[i];
 }
 
-__global__ __launch_bounds__(kThreads) void decode_attention_kernel(DecodeAttnParams p)
+__global__ __launch_bounds__(kThreads) void decode_attention_kernel(ATTN_HEAD_PARAMS, DecodeAttnParams p)
 {
+    ATTN_TAKE_HEAD(p, q, qscale);
     extern __shared__ __align__(16) uint8_t lds[];
     const int hb = blockIdx.z;
     const int row = blockIdx.y;
@@ -166,15 +189,13 @@ __global__ __launch_bounds__(kThreads) void decode_attention_kernel(DecodeAttnPa
     float* qs_lds = wl + hmax * lmax;                                       // [16]
     uint32_t* peak_key = reinterpret_cast<uint32_t*>(qs_lds + kMaxHeadsPerBlock);  // [16]
 
-    // the arguments of every load, read together: one round trip to the
-    // argument segment
-    asm volatile("" ::"s"(p.row_slot), "s"(p.row_first), "s"(p.row_count), "s"(p.q), "s"(p.qscale), "s"(p.keys),
-                 "s"(p.kscale), "s"(p.values), "s"(p.vscale), "s"(p.capacity), "s"(p.max_chunks));
-    const int slot = p.row_slot[row];
-    const int first = p.row_first[row];
-    const int count = p.row_count[row];
+    // the span in one round trip (scalar loads; non-short-circuit tests, so
+    // no branch separates them)
+    const int slot = uniform_load(p.row_slot, row);
+    const int first = uniform_load(p.row_first, row);
+    const int count = uniform_load(p.row_count, row);
     // rows with an invalid slot or span produce zeros (no out-of-range reads)
-    const bool valid = slot >= 0 && slot < p.slots && first >= 0 && count >= 1 && count <= p.capacity - first;
+    const bool valid = (slot >= 0) & (slot < p.slots) & (first >= 0) & (count >= 1) & (count <= p.capacity - first);
     if (!valid) {
         if (chunk == 0 && tid < nh * 16) {
             *reinterpret_cast<float4*>(p.out + ((size_t)row * p.heads + h0 + (tid >> 4)) * 64 + 4 * (tid & 15)) =
@@ -377,19 +398,21 @@ __global__ __launch_bounds__(kThreads) void decode_attention_kernel(DecodeAttnPa
 // dim's weighted sum.
 constexpr int kMergeBatch = 64;
 
-__global__ __launch_bounds__(64) void decode_merge_kernel(DecodeAttnParams p)
+__global__ __launch_bounds__(64) void decode_merge_kernel(ATTN_HEAD_PARAMS, DecodeAttnParams p)
 {
+    ATTN_TAKE_HEAD(p, peaks, sums);
     __shared__ float msm[256];
     __shared__ float wts[256];
     const int row = blockIdx.x;
     const int h = blockIdx.y;
     const int d = threadIdx.x;
-    asm volatile("" ::"s"(p.row_slot), "s"(p.row_first), "s"(p.row_count), "s"(p.peaks), "s"(p.sums),
-                 "s"(p.partials), "s"(p.out), "s"(p.capacity), "s"(p.max_chunks), "s"(p.heads));
-    const int slot = p.row_slot[row];
-    const int first = p.row_first[row];
-    const int count = p.row_count[row];
-    const bool valid = slot >= 0 && slot < p.slots && first >= 0 && count >= 1 && count <= p.capacity - first;
+    const int slot = uniform_load(p.row_slot, row);
+    const int first = uniform_load(p.row_first, row);
+    const int count = uniform_load(p.row_count, row);
+    // the argument-segment fields of the partial loads, read in the same
+    // round trip as the span
+    asm volatile("" ::"s"(p.partials), "s"(p.out), "s"(p.max_chunks), "s"(p.capacity), "s"(p.slots));
+    const bool valid = (slot >= 0) & (slot < p.slots) & (first >= 0) & (count >= 1) & (count <= p.capacity - first);
     float* dst = p.out + ((size_t)row * p.heads + h) * 64 + d;
     if (!valid) return;  // uniform over the block; the chunk kernel wrote zeros
     int length;
@@ -496,8 +519,12 @@ constexpr int kRowUnits = kRowMaxCapacity * 4 / kThreads;  // key pieces per thr
 constexpr int kPostRows = 4;
 
 template <bool POST>
-__global__ __launch_bounds__(kThreads) void decode_attention_row_kernel(DecodeAttnParams p)
+__global__ __launch_bounds__(kThreads) void decode_attention_row_kernel(ATTN_HEAD_PARAMS, DecodeAttnParams p)
 {
+    if constexpr (POST)
+        ATTN_TAKE_HEAD(p, qkv, positions);
+    else
+        ATTN_TAKE_HEAD(p, q, qscale);
     __shared__ __align__(16) float score[kRowMaxCapacity];  // scores, then e_s
     __shared__ __align__(16) float wl[kRowMaxCapacity];     // e_s * valueScale_s
     __shared__ float vsc[kRowMaxCapacity];
@@ -521,12 +548,6 @@ __global__ __launch_bounds__(kThreads) void decode_attention_row_kernel(DecodeAt
     // with v_readlane).  Nothing branches on them, so the loads issue
     // together.  A row with an invalid slot or span runs on the span (slot
     // 0, first 0, count 1), writes zeros and no cache row.
-    asm volatile("" ::"s"(p.row_slot), "s"(p.row_first), "s"(p.row_count), "s"(p.keys), "s"(p.kscale),
-                 "s"(p.values), "s"(p.vscale), "s"(p.capacity), "s"(p.max_chunks), "s"(p.heads), "s"(p.kv_heads));
-    if constexpr (POST)
-        asm volatile("" ::"s"(p.qkv), "s"(p.positions), "s"(p.rope_cos), "s"(p.rope_sin), "s"(p.rows));
-    else
-        asm volatile("" ::"s"(p.q), "s"(p.qscale));
     const int slot_in = uniform_load(p.row_slot, row);
     const int first_in = uniform_load(p.row_first, row);
     const int count_in = uniform_load(p.row_count, row);
@@ -906,7 +927,8 @@ int32_t attention_decode_post_impl(const AttnPostInputs& in, int32_t rows, int32
     p.capacity = capacity;
     p.max_chunks = max_chunks;
     p.inv_sqrt = static_cast<float>(1.0 / std::sqrt(64.0));
-    hipLaunchKernelGGL(decode_attention_row_kernel<true>, dim3(rows, heads), dim3(kThreads), 0, stream, p);
+    hipLaunchKernelGGL(decode_attention_row_kernel<true>, dim3(rows, heads), dim3(kThreads), 0, stream,
+                       ATTN_HEAD_ARGS(p, p.qkv, p.positions), p);
     NHIP_CHECK_HIP(hipGetLastError());
     return NHIP_OK;
 }
@@ -976,14 +998,17 @@ int32_t attention_decode_impl(const int8_t* d_q, const float* d_qscale, int32_t 
     NHIP_REQUIRE(!d_q_out || (d_qs_out && max_chunks == 1 && head_blocks == 1),
                  "attention: a quantized output needs max_chunks 1 and all heads in one block");
     if (!d_q_out && capacity <= kRowMaxCapacity) {  // every count <= capacity: one workgroup per (row, head)
-        hipLaunchKernelGGL(decode_attention_row_kernel<false>, dim3(rows, heads), dim3(kThreads), 0, stream, p);
+        hipLaunchKernelGGL(decode_attention_row_kernel<false>, dim3(rows, heads), dim3(kThreads), 0, stream,
+                           ATTN_HEAD_ARGS(p, p.q, p.qscale), p);
         NHIP_CHECK_HIP(hipGetLastError());
         return NHIP_OK;
     }
-    hipLaunchKernelGGL(decode_attention_kernel, dim3(max_chunks, rows, head_blocks), dim3(kThreads), lds, stream, p);
+    hipLaunchKernelGGL(decode_attention_kernel, dim3(max_chunks, rows, head_blocks), dim3(kThreads), lds, stream,
+                       ATTN_HEAD_ARGS(p, p.q, p.qscale), p);
     NHIP_CHECK_HIP(hipGetLastError());
     if (max_chunks > 1) {  // single-chunk plans are finished by the chunk kernel
-        hipLaunchKernelGGL(decode_merge_kernel, dim3(rows, heads), dim3(64), 0, stream, p);
+        hipLaunchKernelGGL(decode_merge_kernel, dim3(rows, heads), dim3(64), 0, stream,
+                           ATTN_HEAD_ARGS(p, p.peaks, p.sums), p);
         NHIP_CHECK_HIP(hipGetLastError());
     }
     return NHIP_OK;

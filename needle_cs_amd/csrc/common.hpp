@@ -123,6 +123,10 @@ struct DecodePrologue {
     // 16-row tile and the kernel stores a = (g / (1 + Exp(-g))) * u at
     // y[t][8*tile + r] (rows/2 outputs per token) instead of the rows
     int32_t swiglu;
+    // set: the kernel stores residual[t][n] + the row's sum at y[t][n]
+    // (residual laid out like y): the residual stream's update in the
+    // producing matmul
+    const float* residual;
 };
 int32_t launch_decode_fused(const DeviceWeights* w, const DecodePrologue& f, int32_t tokens, float* y, int32_t ldy,
                             hipStream_t stream);
@@ -139,8 +143,9 @@ int32_t launch_decode_swiglu(const DeviceWeights* w, const int8_t* q, const floa
                              float* act, int32_t ldy, hipStream_t stream);
 // Fused prologues pay for their input rows in every workgroup; beyond this
 // many 16-row tiles a separate element-wise launch and the plain matmul are
-// faster.
-constexpr int kFusedPrologueMaxTiles = 256;
+// faster (at 512 tiles of K = 1024 and 3 rows the fused launch still wins
+// by about 0.4 us; an LM head of 2,000 tiles gains nothing either way).
+constexpr int kFusedPrologueMaxTiles = 512;
 // The decoder's step attention with its input post-processing folded in:
 // RoPE on the query and key heads of the fp32 QKV rows, per-head
 // QuantizeInt8, and each row's key and value write to the cache at its

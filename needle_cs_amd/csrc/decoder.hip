@@ -847,11 +847,17 @@ int32_t enqueue_forward(nhip_decoder* m, int rows, const HeadPlan& hp, bool mask
     hipStream_t s = m->stream;
     int32_t rc;
     float* x = m->x;
+    // pending: m->delta holds an output not yet added to the residual x (the
+    // fused output and down matmuls add it in their own chain instead and
+    // write the new residual to the other buffer)
+    bool pending = false;
+    auto other_of = [m](const float* cur) { return cur == m->x ? m->x2 : m->x; };
     hipLaunchKernelGGL(embed_kernel, dim3(rows), dim3(kThreads), 0, s, in_tokens(m, m->d_in), m->emb, d, x);
     NHIP_CHECK_HIP(hipGetLastError());
     const size_t layer_cells = (size_t)D.slots * D.capacity * KV;
     for (int l = 0; l < D.layers; l++) {
-        rc = norm_matmul(m, rows, &x, l > 0, m->attn_norm[l], m->wqkv[l], m->qkv, m->qkv_n, fuse);
+        rc = norm_matmul(m, rows, &x, pending, m->attn_norm[l], m->wqkv[l], m->qkv, m->qkv_n, fuse);
+        pending = false;
         if (rc) return rc;
         PostParams pp{};
         pp.qkv = m->qkv;
@@ -892,11 +898,13 @@ int32_t enqueue_forward(nhip_decoder* m, int rows, const HeadPlan& hp, bool mask
         }
         rc = 1;
         if (!attn_quant && fuse) {
-            DecodePrologue f{kProQuant, m->att, nullptr, nullptr, nullptr, 0.0f, 0};
-            rc = launch_decode_fused(m->wo[l], f, rows, m->delta, d, s);
+            DecodePrologue f{kProQuant, m->att, nullptr, nullptr, nullptr, 0.0f, 0, x};
+            rc = launch_decode_fused(m->wo[l], f, rows, other_of(x), d, s);
             if (rc < 0) return rc;
+            if (rc == 0) x = other_of(x);
         }
         if (rc) {
+            pending = true;
             if (!attn_quant) {
                 rc = nhip_quantize_rows_dev(m->att, rows, H * 64, m->q8, m->qs, s);
                 if (rc) return rc;
@@ -905,13 +913,17 @@ int32_t enqueue_forward(nhip_decoder* m, int rows, const HeadPlan& hp, bool mask
             if (rc) return rc;
         }
         bool act_ready = false;  // SwiGLU applied by the gate/up matmul (into m->act)
-        rc = norm_matmul(m, rows, &x, true, m->ffn_norm[l], m->wgu[l], m->gu, 2 * F, fuse, m->act, &act_ready);
+        rc = norm_matmul(m, rows, &x, pending, m->ffn_norm[l], m->wgu[l], m->gu, 2 * F, fuse, m->act, &act_ready);
         if (rc) return rc;
+        pending = true;
         if (act_ready) {  // quantize the activations in the down matmul's prologue
-            DecodePrologue f{kProQuant, m->act, nullptr, nullptr, nullptr, 0.0f, 0};
-            rc = launch_decode_fused(m->wd[l], f, rows, m->delta, d, s);
+            DecodePrologue f{kProQuant, m->act, nullptr, nullptr, nullptr, 0.0f, 0, x};
+            rc = launch_decode_fused(m->wd[l], f, rows, other_of(x), d, s);
             if (rc < 0) return rc;
-            if (rc) {
+            if (rc == 0) {
+                x = other_of(x);
+                pending = false;
+            } else {
                 rc = nhip_quantize_rows_dev(m->act, rows, F, m->q8, m->qs, s);
                 if (rc) return rc;
                 rc = nhip_matmul_i8_dev(m->wd[l], m->q8, m->qs, rows, m->delta, d, 0, d, s);
@@ -927,8 +939,12 @@ int32_t enqueue_forward(nhip_decoder* m, int rows, const HeadPlan& hp, bool mask
     if (masked) {
         // the sparse head: the final norm, the LM head over the vocab tiles
         // that hold an allowed id of some row, and ArgMaxMasked per row
-        hipLaunchKernelGGL(add_rmsnorm_quant_kernel<true>, dim3(rows), dim3(kThreads), 0, s, x, m->delta,
-                           m->final_norm, d, D.eps, m->q8, m->qs, nullptr);
+        if (pending)
+            hipLaunchKernelGGL(add_rmsnorm_quant_kernel<true>, dim3(rows), dim3(kThreads), 0, s, x, m->delta,
+                               m->final_norm, d, D.eps, m->q8, m->qs, nullptr);
+        else
+            hipLaunchKernelGGL(add_rmsnorm_quant_kernel<false>, dim3(rows), dim3(kThreads), 0, s, x, nullptr,
+                               m->final_norm, d, D.eps, m->q8, m->qs, nullptr);
         NHIP_CHECK_HIP(hipGetLastError());
         rc = launch_decode_masked(m->wlm, m->q8, m->qs, rows, m->logits, D.vocab, m->d_mask, m->mask_words, s);
         if (rc) return rc;
@@ -943,13 +959,17 @@ int32_t enqueue_forward(nhip_decoder* m, int rows, const HeadPlan& hp, bool mask
     if (heads == 0) return NHIP_OK;
     rc = 1;
     if (hp.all_rows && fuse && m->wlm->tiles_n <= kFusedPrologueMaxTiles) {
-        DecodePrologue f{kProNorm, x, m->delta, nullptr, m->final_norm, D.eps, 0};
+        DecodePrologue f{kProNorm, x, pending ? m->delta : nullptr, nullptr, m->final_norm, D.eps, 0};
         rc = launch_decode_fused(m->wlm, f, rows, m->logits, D.vocab, s);
         if (rc < 0) return rc;
     }
     if (rc) {
-        hipLaunchKernelGGL(add_rmsnorm_quant_kernel<true>, dim3(heads), dim3(kThreads), 0, s, x, m->delta,
-                           m->final_norm, d, D.eps, m->q8, m->qs, hp.all_rows ? nullptr : in_heads(m, m->d_in));
+        if (pending)
+            hipLaunchKernelGGL(add_rmsnorm_quant_kernel<true>, dim3(heads), dim3(kThreads), 0, s, x, m->delta,
+                               m->final_norm, d, D.eps, m->q8, m->qs, hp.all_rows ? nullptr : in_heads(m, m->d_in));
+        else
+            hipLaunchKernelGGL(add_rmsnorm_quant_kernel<false>, dim3(heads), dim3(kThreads), 0, s, x, nullptr,
+                               m->final_norm, d, D.eps, m->q8, m->qs, hp.all_rows ? nullptr : in_heads(m, m->d_in));
         NHIP_CHECK_HIP(hipGetLastError());
         rc = nhip_matmul_i8_dev(m->wlm, m->q8, m->qs, heads, m->logits, D.vocab, 0, D.vocab, s);
         if (rc) return rc;

@@ -100,6 +100,7 @@ struct MatmulParams {
     int32_t st_bytes;         // int8 path: LDS bytes of the staged activation operands
     int32_t swz;              // decode path, 5..16 tokens: float4-column swizzle mask of the products
     int32_t swiglu;           // fused decode path: rows are (8 gate, 8 up) pairs per tile, store SwiGLU
+    const float* residual;    // fused decode path: y[t][n] = residual[t][n] + the row's sum (same ldy)
     const uint32_t* tile_mask;  // decode kernel: [mask_rows][mask_words] id bitsets; tiles with no set bit
     int32_t mask_words;         // in any row are skipped (their outputs are left untouched)
     uint32_t t0, t1, t2, t3;  // codebook bytes 0..15
@@ -658,18 +659,21 @@ __device__ __forceinline__ void narrow_products(const long (&av)[2 * CB / 4], co
 // rows j = 8*tile + r (r < 8) followed by the matching up rows: lane r < 8
 // takes lane r + 8's sum (DPP row_shl:8 within the token's 16-lane row) and
 // stores a = (g / (1 + Exp(-g))) * u at y[t][j].
-__device__ __forceinline__ void store_chain(float acc, int t, int rr, int nn, int tile, const MatmulParams& p)
+// res: this lane's residual value when p.residual is set (the stored value
+// is then res + acc)
+__device__ __forceinline__ void store_chain(float acc, int t, int rr, int nn, int tile, const MatmulParams& p,
+                                            float res = 0.0f)
 {
     if (p.swiglu) {
         const float u = dpp_row_shl(acc, 8);
         if (rr < 8) p.y[(size_t)t * p.ldy + tile * 8 + rr] = (acc / (1.0f + exp_poly(-acc))) * u;
     } else if (nn >= p.row_start && nn < p.row_end) {
-        p.y[(size_t)t * p.ldy + nn] = acc;
+        p.y[(size_t)t * p.ldy + nn] = p.residual ? res + acc : acc;
     }
 }
 
 __device__ __forceinline__ void chain_products(const float* pl, int GS, int swz, int M, int G, int tile,
-                                               const MatmulParams& p)
+                                               const MatmulParams& p, float res = 0.0f)
 {
     for (int x = threadIdx.x; x < M * 16; x += blockDim.x) {
         const int t = x >> 4;
@@ -701,7 +705,7 @@ __device__ __forceinline__ void chain_products(const float* pl, int GS, int swz,
         }
         const float* rowf = reinterpret_cast<const float*>(row);
         for (int c = full * 16; c < G; c++) acc = acc + rowf[(((c >> 2) ^ sw) << 2) | (c & 3)];
-        store_chain(acc, t, rr, nn, tile, p);
+        store_chain(acc, t, rr, nn, tile, p, res);
     }
 }
 
@@ -1135,22 +1139,38 @@ __global__ __launch_bounds__(512) void matmul_cq_decode_batch_kernel(MatmulBatch
 // The decode kernel for M <= 4 with its activation rows computed in the
 // prologue from fp32 inputs instead of read as int8 (one launch instead of
 // an element-wise kernel and a matmul).  Every workgroup loads the inputs
-// first, then its scales and weight blocks, and computes the M quantized
-// rows (all K) into LDS while the weights are in flight; the rows are
-// bit-identical with the element-wise kernels they replace:
+// first, then its scales and weight blocks, and computes the M = TI
+// quantized rows (all K) into LDS while the weights are in flight; the rows
+// are bit-identical with the element-wise kernels they replace:
 //   kProNorm    x (+ delta) -> RMSNorm (canonical row sum of squares) *
 //               gain -> QuantizeInt8; workgroup 0 also writes x + delta to
 //               x_out;
 //   kProQuant   QuantizeInt8 of x.
+// With p.residual the chain stores residual + y (the residual stream's
+// update, x + delta in Engine's order of operands: one IEEE addition, so the
+// same bits) instead of y.
 // Thread t of the prologue holds the float4 groups at 4t + 4*nt*j, j < G4
 // (nt = 256 for the norm, whose lanes are the canonical sum's, else the
-// whole block).  Four rows are always computed (rows past M repeat the
-// last), so every load is unconditional and the weight loads stay in
-// flight across the prologue.
-template <int CB, int KIND, bool DELTA, int G4>
-__global__ __launch_bounds__(512) void matmul_i8_decode_fused_kernel(MatmulParams p, DecodePrologue f)
+// whole block).  Every prologue load is unconditional, so the weight loads
+// stay in flight across the prologue.  The first loads' arguments come
+// preloaded (the head: x, delta, gain, tiles, norms, (waves, K), (G,
+// blocks)); tile_begin is 0 (every row).
+template <int CB, int KIND, bool DELTA, int G4, int TI>
+__global__ __launch_bounds__(512) void matmul_i8_decode_fused_kernel(const float* h_x, const float* h_delta,
+                                                                     const float* h_gain, const uint8_t* h_tiles,
+                                                                     const uint16_t* h_norms, uint64_t h_waves_cols,
+                                                                     uint64_t h_groups_blocks, MatmulParams p,
+                                                                     DecodePrologue f)
 {
-    constexpr int TI = 4;
+    f.x = h_x;
+    f.delta = h_delta;
+    f.gain = h_gain;
+    p.tiles = h_tiles;
+    p.norms = h_norms;
+    p.tokens = TI;
+    p.cols = head_hi(h_waves_cols);
+    p.groups = head_lo(h_groups_blocks);
+    p.blocks = head_hi(h_groups_blocks);
     constexpr int SETS = 2 * CB / 4;
     extern __shared__ __align__(16) uint8_t lds[];
     float* pl = reinterpret_cast<float*>(lds);                            // products [t][r][GS]
@@ -1161,9 +1181,9 @@ __global__ __launch_bounds__(512) void matmul_i8_decode_fused_kernel(MatmulParam
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
-    const int nwaves = blockDim.x >> 6;
-    const int tile = p.tile_begin + blockIdx.x;
-    const int M = p.tokens;
+    const int nwaves = head_lo(h_waves_cols);
+    const int tile = blockIdx.x;
+    constexpr int M = TI;
     const int K = p.cols;
     const int G = p.groups;
     const int GS = p.ldd;
@@ -1174,13 +1194,9 @@ __global__ __launch_bounds__(512) void matmul_i8_decode_fused_kernel(MatmulParam
     const int mb0 = active ? wave * CB : 0;
     const int g_first = mb0 * 2;
     const u4* wbase = reinterpret_cast<const u4*>(p.tiles) + (size_t)tile * p.blocks * 64 + lane;
-    const uint16_t* nrow = p.norms + (size_t)n * p.groups_pad8 + g_first;
-    // the arguments of every load, read together: one round trip to the
-    // argument segment
-    asm volatile("" ::"s"(p.tiles), "s"(p.norms), "s"(p.blocks), "s"(p.groups_pad8), "s"(f.x), "s"(f.delta),
-                 "s"(f.gain));
+    const uint16_t* nrow = p.norms + (size_t)n * ((G + 7) & ~7) + g_first;
     constexpr bool NORM = KIND == kProNorm;
-    const int nt = NORM ? 256 : (int)blockDim.x;
+    const int nt = NORM ? 256 : 64 * nwaves;
 
     // 1. prologue inputs
     float4 xv[TI][G4], dv[TI][G4], gv[G4];  // dv: the delta of the norm
@@ -1202,9 +1218,13 @@ __global__ __launch_bounds__(512) void matmul_i8_decode_fused_kernel(MatmulParam
     u4 w[CB];
 #pragma unroll
     for (int c = 0; c < CB; c++) w[c] = __builtin_nontemporal_load(wbase + (size_t)(mb0 + c) * 64);
+    // 4. the residual value of chain lane (t, r) = (tid / 16, tid % 16)
+    float res = 0.0f;
+    if (p.residual)
+        res = p.residual[(size_t)min(tid >> 4, M - 1) * p.ldy + min(tile * 16 + (tid & 15), p.row_end - 1)];
     __builtin_amdgcn_sched_barrier(0);
 
-    // 4. the quantized rows, while the weights arrive
+    // 5. the quantized rows, while the weights arrive
     float peak[TI];
 #pragma unroll
     for (int t = 0; t < TI; t++) peak[t] = 0.0f;
@@ -1291,20 +1311,20 @@ __global__ __launch_bounds__(512) void matmul_i8_decode_fused_kernel(MatmulParam
         }
     }
     __syncthreads();
-    // 5. A operands from the quantized rows (token r%4, group g + r/4, k-slice kq)
+    // 6. A operands from the quantized rows (token r%4, group g + r/4, k-slice kq)
     if (active) {
         long av[SETS];
         const bool feeds = (r & 3) < M;
 #pragma unroll
         for (int c = 0; c < SETS; c++) {
             const int g = min(g_first + 4 * c + (r >> 2), G - 1);
-            const long a = *reinterpret_cast<const long*>(qa + (size_t)(r & 3) * K + g * 32 + kq * 8);
+            const long a = *reinterpret_cast<const long*>(qa + (size_t)min(r & 3, M - 1) * K + g * 32 + kq * 8);
             av[c] = feeds ? a : 0;
         }
         narrow_products<CB, TI, false>(av, qs, hraw, w, pl, GS, M, g_first, r, kq);
     }
     __syncthreads();
-    chain_products(pl, GS, 0, M, G, tile, p);
+    chain_products(pl, GS, 0, M, G, tile, p, res);
 }
 
 template <int CB, int TI, bool EXACT>
@@ -1476,14 +1496,26 @@ int32_t try_cq_decode(const DeviceWeights* w, MatmulParams& p, hipStream_t strea
                : launch_cq_decode_gpw<kCq2>(p, gpw, exact, waves, lds, stream);
 }
 
-template <int CB, int KIND, bool DELTA, int G4>
-int32_t launch_fused_tpl(const MatmulParams& p, const DecodePrologue& f, int waves, size_t lds, hipStream_t stream)
+template <int CB, int KIND, bool DELTA, int G4, int TI>
+int32_t launch_fused_ti(const MatmulParams& p, const DecodePrologue& f, int waves, size_t lds, hipStream_t stream)
 {
     const int tiles = p.tile_end - p.tile_begin;
-    hipLaunchKernelGGL((matmul_i8_decode_fused_kernel<CB, KIND, DELTA, G4>), dim3(tiles), dim3(64 * waves), lds,
-                       stream, p, f);
+    hipLaunchKernelGGL((matmul_i8_decode_fused_kernel<CB, KIND, DELTA, G4, TI>), dim3(tiles), dim3(64 * waves), lds,
+                       stream, f.x, f.delta, f.gain, p.tiles, p.norms, head_pair(waves, p.cols),
+                       head_pair(p.groups, p.blocks), p, f);
     NHIP_CHECK_HIP(hipGetLastError());
     return NHIP_OK;
+}
+
+template <int CB, int KIND, bool DELTA, int G4>
+int32_t launch_fused_tpl(const MatmulParams& p, const DecodePrologue& f, int waves, size_t lds, hipStream_t s)
+{
+    switch (p.tokens) {
+        case 1: return launch_fused_ti<CB, KIND, DELTA, G4, 1>(p, f, waves, lds, s);
+        case 2: return launch_fused_ti<CB, KIND, DELTA, G4, 2>(p, f, waves, lds, s);
+        case 3: return launch_fused_ti<CB, KIND, DELTA, G4, 3>(p, f, waves, lds, s);
+        default: return launch_fused_ti<CB, KIND, DELTA, G4, 4>(p, f, waves, lds, s);
+    }
 }
 
 template <int CB, int G4>
@@ -2069,9 +2101,10 @@ int32_t launch_decode_fused(const DeviceWeights* w, const DecodePrologue& f, int
     p.ldy = ldy;
     p.row_start = 0;
     p.row_end = w->rows;
-    p.tile_begin = 0;
+    p.tile_begin = 0;  // the kernel runs every row from tile 0
     p.tile_end = w->tiles_n;
     p.swiglu = f.swiglu;
+    p.residual = f.residual;
     p.ldd = ((2 * w->blocks + 3) & ~3) + 4;
     p.d_bytes = tokens * 16 * p.ldd * (int)sizeof(float);
     p.st_bytes = (4 * K + 15) & ~15;
