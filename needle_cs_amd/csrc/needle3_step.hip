@@ -71,20 +71,37 @@ __device__ __forceinline__ int col_of(int q) { return (int)threadIdx.x + kThread
 // Scalar.Dot with the products formed beforehand -- each product is rounded
 // before it is added, as in `sum += x[i] * y[i]` without contraction).  n is
 // a multiple of 64 and v is 16-byte aligned with kChainPad readable floats
-// past n: the loads run one 32-float batch ahead of the dependent adds.
-// Different lanes may run different chains at once.
+// past n.  The reads run one 32-float batch ahead of the dependent adds:
+// they are issued by inline ds_read_b128 (the compiler, given plain loads,
+// moved every batch's reads to the top of its own loop iteration and exposed
+// the LDS latency once per 64 adds), and an s_waitcnt that takes the batch's
+// registers as operands orders their use after the wait -- LDS reads return
+// in order, so lgkmcnt(8) means the older batch has landed.  Different
+// lanes may run different chains at once.
 constexpr int kChainPad = 32;
+
+typedef float chain4 __attribute__((ext_vector_type(4)));
+#define CHAIN_READ8(x, base, off)                                                                                  \
+    asm volatile("ds_read_b128 %0, %8 offset:" #off "\n\tds_read_b128 %1, %8 offset:" #off "+16\n\t"                 \
+                 "ds_read_b128 %2, %8 offset:" #off "+32\n\tds_read_b128 %3, %8 offset:" #off "+48\n\t"                \
+                 "ds_read_b128 %4, %8 offset:" #off "+64\n\tds_read_b128 %5, %8 offset:" #off "+80\n\t"                \
+                 "ds_read_b128 %6, %8 offset:" #off "+96\n\tds_read_b128 %7, %8 offset:" #off "+112"                    \
+                 : "=v"(x[0]), "=v"(x[1]), "=v"(x[2]), "=v"(x[3]), "=v"(x[4]), "=v"(x[5]), "=v"(x[6]), "=v"(x[7]) \
+                 : "v"(base))
+#define CHAIN_WAIT(n, x)                                                                                           \
+    asm volatile("s_waitcnt lgkmcnt(" #n ")"                                                                       \
+                 : "+v"(x[0]), "+v"(x[1]), "+v"(x[2]), "+v"(x[3]), "+v"(x[4]), "+v"(x[5]), "+v"(x[6]), "+v"(x[7]))
 
 __device__ __forceinline__ float chain_sum(const float* v, int n)
 {
-    const float4* p = reinterpret_cast<const float4*>(v);
+    const uint32_t base = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const float*)v;
     float sum = 0.0f;
-    float4 a[8], b[8];
-#pragma unroll
-    for (int j = 0; j < 8; j++) a[j] = p[j];
+    chain4 a[8], b[8];
+    CHAIN_READ8(a, base, 0);
     for (int k = 0; k < (n >> 2); k += 16) {
-#pragma unroll
-        for (int j = 0; j < 8; j++) b[j] = p[k + 8 + j];
+        const uint32_t at = base + (uint32_t)k * 16u;
+        CHAIN_READ8(b, at, 128);
+        CHAIN_WAIT(8, a);
 #pragma unroll
         for (int j = 0; j < 8; j++) {
             sum = sum + a[j].x;
@@ -92,8 +109,8 @@ __device__ __forceinline__ float chain_sum(const float* v, int n)
             sum = sum + a[j].z;
             sum = sum + a[j].w;
         }
-#pragma unroll
-        for (int j = 0; j < 8; j++) a[j] = p[k + 16 + j];  // the last round reads the padding
+        CHAIN_READ8(a, at, 256);  // the last round reads the padding
+        CHAIN_WAIT(8, b);
 #pragma unroll
         for (int j = 0; j < 8; j++) {
             sum = sum + b[j].x;
@@ -102,6 +119,7 @@ __device__ __forceinline__ float chain_sum(const float* v, int n)
             sum = sum + b[j].w;
         }
     }
+    CHAIN_WAIT(0, a);  // no read is left in flight
     return sum;
 }
 
