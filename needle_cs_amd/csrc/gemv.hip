@@ -108,6 +108,13 @@ struct MatmulParams {
     float byte_scale;
 };
 
+// The argument-segment fields the products and the chain use, read once the
+// first loads are in flight: used only after a barrier, the compiler would
+// load them there, one more round trip on the kernel's critical path.
+#define MATMUL_TAIL_FIELDS(p)                                                                                   \
+    asm volatile("" ::"s"((p).y), "s"((p).ldy), "s"((p).row_start), "s"((p).row_end), "s"((p).swiglu),          \
+                 "s"((p).residual), "s"((p).ldd), "s"((p).swz), "s"(blockDim.x))
+
 // The decode kernels' head (see head_pair): the fields of their first loads.
 #define MATMUL_HEAD_PARAMS const uint8_t *h_tiles, const uint16_t *h_norms, const int8_t *h_q, const float *h_qscale, \
                            uint64_t h_tokens_cols, uint64_t h_groups_blocks, uint64_t h_begin_mask
@@ -795,6 +802,7 @@ __device__ __forceinline__ void i8_decode_tile(const MatmulParams& p, const int 
 #pragma unroll
     for (int c = 0; c < CB; c++) w[c] = __builtin_nontemporal_load(wbase + (size_t)(mb0 + c) * 64);
     __builtin_amdgcn_sched_barrier(0);
+    MATMUL_TAIL_FIELDS(p);
 
     if constexpr (WIDE) {
         const v4i zero = {0, 0, 0, 0};
@@ -948,6 +956,7 @@ __device__ __forceinline__ void cq_decode_tile(const MatmulParams& p, const int 
         }
     }
     __builtin_amdgcn_sched_barrier(0);
+    MATMUL_TAIL_FIELDS(p);
 
 #pragma unroll
     for (int c = 0; c < SETS; c++) {
@@ -1055,6 +1064,7 @@ __device__ __forceinline__ void cq_decode_wide_tile(const MatmulParams& p, const
         }
     }
     __builtin_amdgcn_sched_barrier(0);
+    MATMUL_TAIL_FIELDS(p);
 
     const int tq = 4 * kq;  // first token of this lane's MFMA results
 #pragma unroll
@@ -1223,6 +1233,8 @@ __global__ __launch_bounds__(512) void matmul_i8_decode_fused_kernel(const float
     if (p.residual)
         res = p.residual[(size_t)min(tid >> 4, M - 1) * p.ldy + min(tile * 16 + (tid & 15), p.row_end - 1)];
     __builtin_amdgcn_sched_barrier(0);
+    MATMUL_TAIL_FIELDS(p);
+    asm volatile("" ::"s"(f.eps), "s"(f.x_out), "s"(p.d_bytes), "s"(p.st_bytes));
 
     // 5. the quantized rows, while the weights arrive
     float peak[TI];
