@@ -62,6 +62,44 @@ inline uint64_t head_pair(int32_t lo, int32_t hi) { return (uint64_t)(uint32_t)l
 __device__ __forceinline__ int32_t head_lo(uint64_t v) { return (int32_t)(uint32_t)v; }
 __device__ __forceinline__ int32_t head_hi(uint64_t v) { return (int32_t)(uint32_t)(v >> 32); }
 
+// ------------------------------------------------- ordered LDS chains --
+
+// Sequential sums over LDS (the reference's scalar order: one lane adds one
+// value after another) are bound by the dependent adds only if the reads run
+// ahead of them.  Given plain loads, the compiler moved each batch's reads to
+// the top of its own loop iteration, exposing the LDS latency once per batch.
+// These read batches with inline ds_read_b128 and wait with an s_waitcnt
+// that takes the batch's registers as operands, so no use of them is placed
+// before the wait; LDS reads complete in order, so lgkmcnt(n) with n reads
+// issued after a batch means that batch has landed.
+typedef float chain4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ uint32_t lds_address(const void* p)
+{
+    return (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const void*)p;
+}
+
+// eight 16-byte reads at base + off, base + off + 16, ...
+#define CHAIN_READ8(x, base, off)                                                                                  \
+    asm volatile("ds_read_b128 %0, %8 offset:" #off "\n\tds_read_b128 %1, %8 offset:" #off "+16\n\t"                 \
+                 "ds_read_b128 %2, %8 offset:" #off "+32\n\tds_read_b128 %3, %8 offset:" #off "+48\n\t"                \
+                 "ds_read_b128 %4, %8 offset:" #off "+64\n\tds_read_b128 %5, %8 offset:" #off "+80\n\t"                \
+                 "ds_read_b128 %6, %8 offset:" #off "+96\n\tds_read_b128 %7, %8 offset:" #off "+112"                    \
+                 : "=v"(x[0]), "=v"(x[1]), "=v"(x[2]), "=v"(x[3]), "=v"(x[4]), "=v"(x[5]), "=v"(x[6]), "=v"(x[7]) \
+                 : "v"(base))
+#define CHAIN_WAIT(n, x)                                                                                           \
+    asm volatile("s_waitcnt lgkmcnt(" #n ")"                                                                       \
+                 : "+v"(x[0]), "+v"(x[1]), "+v"(x[2]), "+v"(x[3]), "+v"(x[4]), "+v"(x[5]), "+v"(x[6]), "+v"(x[7]))
+// four 16-byte reads at four addresses
+#define CHAIN_READ4(x, a0, a1, a2, a3)                                                                             \
+    asm volatile("ds_read_b128 %0, %4\n\tds_read_b128 %1, %5\n\tds_read_b128 %2, %6\n\tds_read_b128 %3, %7"          \
+                 : "=v"(x[0]), "=v"(x[1]), "=v"(x[2]), "=v"(x[3])                                                   \
+                 : "v"(a0), "v"(a1), "v"(a2), "v"(a3))
+#define CHAIN_WAIT4(n, x) asm volatile("s_waitcnt lgkmcnt(" #n ")" : "+v"(x[0]), "+v"(x[1]), "+v"(x[2]), "+v"(x[3]))
+#define CHAIN_WAIT44(n, x, y)                                                                                      \
+    asm volatile("s_waitcnt lgkmcnt(" #n ")"                                                                       \
+                 : "+v"(x[0]), "+v"(x[1]), "+v"(x[2]), "+v"(x[3]), "+v"(y[0]), "+v"(y[1]), "+v"(y[2]), "+v"(y[3]))
+
 // ------------------------------------------------------- device weights --
 
 enum class WeightFormat : int32_t { Int8G32 = 8, Cq2 = 2, Cq4 = 4 };

@@ -689,17 +689,29 @@ __device__ __forceinline__ void chain_products(const float* pl, int GS, int swz,
         const float4* row = reinterpret_cast<const float4*>(pl + (size_t)x * GS);
         const int sw = x & swz;
         float acc = 0.0f;
-        float4 v[4];
-        const int full = G >> 4;  // chunks of 16 groups
-        if (full > 0) {
+        // the float4 columns in batches of 16 (64 groups), then 4: every read
+        // of a batch is issued before its first add, so the LDS latency is
+        // exposed once per batch (a one-batch-ahead prefetch of 4 columns,
+        // which the compiler served only after the current batch's wait,
+        // exposed it every 16 groups)
+        const int G4 = G >> 2;
+        int c4 = 0;
+        for (; c4 + 16 <= G4; c4 += 16) {
+            float4 v[16];
 #pragma unroll
-            for (int j = 0; j < 4; j++) v[j] = row[j ^ sw];
+            for (int j = 0; j < 16; j++) v[j] = row[(c4 + j) ^ sw];
+#pragma unroll
+            for (int j = 0; j < 16; j++) {
+                acc = acc + v[j].x;
+                acc = acc + v[j].y;
+                acc = acc + v[j].z;
+                acc = acc + v[j].w;
+            }
         }
-        for (int ch = 0; ch < full; ch++) {
-            float4 nx[4];
-            const int nb = min(ch + 1, full - 1) * 4;
+        for (; c4 + 4 <= G4; c4 += 4) {
+            float4 v[4];
 #pragma unroll
-            for (int j = 0; j < 4; j++) nx[j] = row[(nb + j) ^ sw];
+            for (int j = 0; j < 4; j++) v[j] = row[(c4 + j) ^ sw];
 #pragma unroll
             for (int j = 0; j < 4; j++) {
                 acc = acc + v[j].x;
@@ -707,9 +719,8 @@ __device__ __forceinline__ void chain_products(const float* pl, int GS, int swz,
                 acc = acc + v[j].z;
                 acc = acc + v[j].w;
             }
-#pragma unroll
-            for (int j = 0; j < 4; j++) v[j] = nx[j];
         }
+        const int full = c4 >> 2;  // chunks of 16 groups done
         const float* rowf = reinterpret_cast<const float*>(row);
         for (int c = full * 16; c < G; c++) acc = acc + rowf[(((c >> 2) ^ sw) << 2) | (c & 3)];
         store_chain(acc, t, rr, nn, tile, p, res);

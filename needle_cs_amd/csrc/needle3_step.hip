@@ -80,21 +80,9 @@ __device__ __forceinline__ int col_of(int q) { return (int)threadIdx.x + kThread
 // lanes may run different chains at once.
 constexpr int kChainPad = 32;
 
-typedef float chain4 __attribute__((ext_vector_type(4)));
-#define CHAIN_READ8(x, base, off)                                                                                  \
-    asm volatile("ds_read_b128 %0, %8 offset:" #off "\n\tds_read_b128 %1, %8 offset:" #off "+16\n\t"                 \
-                 "ds_read_b128 %2, %8 offset:" #off "+32\n\tds_read_b128 %3, %8 offset:" #off "+48\n\t"                \
-                 "ds_read_b128 %4, %8 offset:" #off "+64\n\tds_read_b128 %5, %8 offset:" #off "+80\n\t"                \
-                 "ds_read_b128 %6, %8 offset:" #off "+96\n\tds_read_b128 %7, %8 offset:" #off "+112"                    \
-                 : "=v"(x[0]), "=v"(x[1]), "=v"(x[2]), "=v"(x[3]), "=v"(x[4]), "=v"(x[5]), "=v"(x[6]), "=v"(x[7]) \
-                 : "v"(base))
-#define CHAIN_WAIT(n, x)                                                                                           \
-    asm volatile("s_waitcnt lgkmcnt(" #n ")"                                                                       \
-                 : "+v"(x[0]), "+v"(x[1]), "+v"(x[2]), "+v"(x[3]), "+v"(x[4]), "+v"(x[5]), "+v"(x[6]), "+v"(x[7]))
-
 __device__ __forceinline__ float chain_sum(const float* v, int n)
 {
-    const uint32_t base = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const float*)v;
+    const uint32_t base = lds_address(v);
     float sum = 0.0f;
     chain4 a[8], b[8];
     CHAIN_READ8(a, base, 0);
