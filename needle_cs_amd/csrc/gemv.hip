@@ -997,6 +997,27 @@ __device__ __forceinline__ void cq_decode_tile(const MatmulParams& p, const int 
         const float* rb = pb + (size_t)x * GS;
         float acc = 0.0f, bias = 0.0f;
         int g = 0;
+        // 16 groups per batch, every read of a batch issued before its
+        // first add (one exposed LDS latency per batch)
+        for (; g + 16 <= G; g += 16) {
+            float4 a[4], b[4];
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                a[j] = *reinterpret_cast<const float4*>(ra + g + 4 * j);
+                b[j] = *reinterpret_cast<const float4*>(rb + g + 4 * j);
+            }
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                acc = acc + a[j].x;
+                bias = bias + b[j].x;
+                acc = acc + a[j].y;
+                bias = bias + b[j].y;
+                acc = acc + a[j].z;
+                bias = bias + b[j].z;
+                acc = acc + a[j].w;
+                bias = bias + b[j].w;
+            }
+        }
         for (; g + 4 <= G; g += 4) {
             const float4 a = *reinterpret_cast<const float4*>(ra + g);
             const float4 b = *reinterpret_cast<const float4*>(rb + g);
@@ -1111,7 +1132,27 @@ __device__ __forceinline__ void cq_decode_wide_tile(const MatmulParams& p, const
         const float4* row_b = pb + (size_t)x * (GS / 4);
         const int sw = x & p.swz;
         float acc = 0.0f, bias = 0.0f;
-        for (int c = 0; c < (G >> 2); c++) {
+        int c = 0;
+        for (; c + 4 <= (G >> 2); c += 4) {  // 16 groups per batch, reads first
+            float4 a[4], b[4];
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                a[j] = row_a[(c + j) ^ sw];
+                b[j] = row_b[(c + j) ^ sw];
+            }
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                acc = acc + a[j].x;
+                bias = bias + b[j].x;
+                acc = acc + a[j].y;
+                bias = bias + b[j].y;
+                acc = acc + a[j].z;
+                bias = bias + b[j].z;
+                acc = acc + a[j].w;
+                bias = bias + b[j].w;
+            }
+        }
+        for (; c < (G >> 2); c++) {
             const float4 a = row_a[c ^ sw];
             const float4 b = row_b[c ^ sw];
             acc = acc + a.x;
