@@ -525,8 +525,10 @@ __global__ __launch_bounds__(kThreads) void decode_attention_row_kernel(ATTN_HEA
         ATTN_TAKE_HEAD(p, qkv, positions);
     else
         ATTN_TAKE_HEAD(p, q, qscale);
-    __shared__ __align__(16) float score[kRowMaxCapacity];  // scores, then e_s
-    __shared__ __align__(16) float wl[kRowMaxCapacity];     // e_s * valueScale_s
+    // scores, then e_s; e_s * valueScale_s (each padded by kVBlock floats:
+    // phase 4 reads the last chunk's rows up to the chunk length)
+    __shared__ __align__(16) float score[kRowMaxCapacity + kVBlock];
+    __shared__ __align__(16) float wl[kRowMaxCapacity + kVBlock];
     __shared__ float vsc[kRowMaxCapacity];
     __shared__ __align__(16) float part[kRowMaxChunks * 64];
     __shared__ uint32_t peak_key[kRowMaxChunks];
@@ -747,11 +749,9 @@ __global__ __launch_bounds__(kThreads) void decode_attention_row_kernel(ATTN_HEA
             o2 = o2 + w * sx8(v, 2);
             o3 = o3 + w * sx8(v, 3);
         };
-        for (int s0 = 0; s0 < L; s0 += kVBlock) {
-            if (s0 > 0 || c0 > 0) {
-#pragma unroll
-                for (int j = 0; j < kVBlock; j++) vreg[j] = vp[(size_t)min(s0 + j, L - 1) * vstride4];
-            }
+        // POST: the positions this launch writes come from the workgroup's
+        // own rows, not from the cache
+        auto substitute = [&](int s0) {
             if constexpr (POST) {
 #pragma unroll
                 for (int r = 0; r < kPostRows; r++) {
@@ -763,16 +763,47 @@ __global__ __launch_bounds__(kThreads) void decode_attention_row_kernel(ATTN_HEA
                     }
                 }
             }
+        };
+        if (length <= kVBlock) {  // uniform: every chunk in one pass
+            if (c0 > 0) {
+#pragma unroll
+                for (int j = 0; j < kVBlock; j++) vreg[j] = vp[(size_t)min(j, L - 1) * vstride4];
+            }
+            substitute(0);
+            // Positions past L (the last chunk's tail, up to `length`) run as
+            // steps of weight 0, so that every thread of the pass runs the
+            // same instructions: total + 0 and o + 0 * v leave the sums
+            // unchanged, since no partial sum is -0 (they start at +0, and a
+            // rounded sum is -0 only when both operands are).  The LDS rows
+            // are padded for the reads past the last position.
 #pragma unroll
             for (int j4 = 0; j4 < kVBlock; j4 += 4) {
-                if (s0 + j4 >= L) break;
-                const float4 e4 = *reinterpret_cast<const float4*>(score + b + s0 + j4);
-                const float4 w4 = *reinterpret_cast<const float4*>(wl + b + s0 + j4);
-                const int rem = L - (s0 + j4);
-                step(e4.x, w4.x, vreg[j4]);
-                if (rem > 1) step(e4.y, w4.y, vreg[j4 + 1]);
-                if (rem > 2) step(e4.z, w4.z, vreg[j4 + 2]);
-                if (rem > 3) step(e4.w, w4.w, vreg[j4 + 3]);
+                if (j4 >= length) break;  // uniform
+                const float4 e4 = *reinterpret_cast<const float4*>(score + b + j4);
+                const float4 w4 = *reinterpret_cast<const float4*>(wl + b + j4);
+                step(j4 < L ? e4.x : 0.0f, j4 < L ? w4.x : 0.0f, vreg[j4]);
+                step(j4 + 1 < L ? e4.y : 0.0f, j4 + 1 < L ? w4.y : 0.0f, vreg[j4 + 1]);
+                step(j4 + 2 < L ? e4.z : 0.0f, j4 + 2 < L ? w4.z : 0.0f, vreg[j4 + 2]);
+                step(j4 + 3 < L ? e4.w : 0.0f, j4 + 3 < L ? w4.w : 0.0f, vreg[j4 + 3]);
+            }
+        } else {
+            for (int s0 = 0; s0 < L; s0 += kVBlock) {
+                if (s0 > 0 || c0 > 0) {
+#pragma unroll
+                    for (int j = 0; j < kVBlock; j++) vreg[j] = vp[(size_t)min(s0 + j, L - 1) * vstride4];
+                }
+                substitute(s0);
+#pragma unroll
+                for (int j4 = 0; j4 < kVBlock; j4 += 4) {
+                    if (s0 + j4 >= L) break;
+                    const float4 e4 = *reinterpret_cast<const float4*>(score + b + s0 + j4);
+                    const float4 w4 = *reinterpret_cast<const float4*>(wl + b + s0 + j4);
+                    const int rem = L - (s0 + j4);
+                    step(e4.x, w4.x, vreg[j4]);
+                    if (rem > 1) step(e4.y, w4.y, vreg[j4 + 1]);
+                    if (rem > 2) step(e4.z, w4.z, vreg[j4 + 2]);
+                    if (rem > 3) step(e4.w, w4.w, vreg[j4 + 3]);
+                }
             }
         }
         if (needed == 1) {
