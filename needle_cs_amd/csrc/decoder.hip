@@ -1052,10 +1052,11 @@ int32_t run_staged(nhip_decoder* m, int rows, const HeadPlan& hp, bool use_graph
     }
     const int heads = hp.all_rows ? rows : hp.heads;
     if (hp.k > 0 && heads > 0) {
-        NHIP_CHECK_HIP(hipMemcpyAsync(m->h_topk_idx, m->d_topk_idx, sizeof(int32_t) * heads * hp.k,
-                                      hipMemcpyDeviceToHost, m->stream));
-        NHIP_CHECK_HIP(hipMemcpyAsync(m->h_topk_lp, m->d_topk_lp, sizeof(float) * heads * hp.k, hipMemcpyDeviceToHost,
-                                      m->stream));
+        // ids and log-probabilities in one copy (the log-probabilities follow
+        // the ids' region of max_rows * kMaxTopK entries)
+        const size_t span = reinterpret_cast<const char*>(m->d_topk_lp + (size_t)heads * hp.k) -
+                            reinterpret_cast<const char*>(m->d_topk_idx);
+        NHIP_CHECK_HIP(hipMemcpyAsync(m->h_topk_idx, m->d_topk_idx, span, hipMemcpyDeviceToHost, m->stream));
     }
     if (hp.argmax && heads > 0) {
         NHIP_CHECK_HIP(hipMemcpyAsync(m->h_best, m->d_best, sizeof(int32_t) * 2 * m->best_rows, hipMemcpyDeviceToHost,
@@ -1155,8 +1156,7 @@ int32_t nhip_decoder_create(const nhip_decoder_dims* dims, nhip_decoder** out)
         (rc = dalloc(m, &m->qkv, (size_t)R * m->qkv_n)) || (rc = dalloc(m, &m->qh, (size_t)R * D.heads * 64)) ||
         (rc = dalloc(m, &m->qhs, (size_t)R * D.heads)) || (rc = dalloc(m, &m->att, (size_t)R * D.heads * 64)) ||
         (rc = dalloc(m, &m->gu, (size_t)R * 2 * D.ffn)) || (rc = dalloc(m, &m->act, (size_t)R * D.ffn)) || (rc = dalloc(m, &m->logits, (size_t)R * D.vocab)) ||
-        (rc = dalloc(m, &m->d_in, (size_t)6 * R)) || (rc = dalloc(m, &m->d_topk_idx, (size_t)R * kMaxTopK)) ||
-        (rc = dalloc(m, &m->d_topk_lp, (size_t)R * kMaxTopK)) ||
+        (rc = dalloc(m, &m->d_in, (size_t)6 * R)) || (rc = dalloc(m, &m->d_topk_idx, (size_t)2 * R * kMaxTopK)) ||
         (rc = dalloc(m, &m->d_mask, (size_t)kMaxMaskedRows * ((D.vocab + 31) / 32))) ||
         (rc = dalloc(m, &m->d_best, (size_t)2 * m->best_rows)) ||
         (rc = dalloc(m, &m->topk.vals, (size_t)R * ((D.vocab + kTopkBlock - 1) / kTopkBlock) * kMaxTopK)) ||
@@ -1174,12 +1174,12 @@ int32_t nhip_decoder_create(const nhip_decoder_dims* dims, nhip_decoder** out)
     m->attn_ws = ws;
     m->mask_words = (D.vocab + 31) / 32;
     m->d_best_val = reinterpret_cast<float*>(m->d_best + m->best_rows);  // one copy returns both
+    // the top-k ids, then their log-probabilities: one copy returns both
+    m->d_topk_lp = reinterpret_cast<float*>(m->d_topk_idx + (size_t)R * kMaxTopK);
     if (hipHostMalloc(reinterpret_cast<void**>(&m->h_in), sizeof(int32_t) * 6 * R, hipHostMallocDefault) !=
             hipSuccess ||
-        hipHostMalloc(reinterpret_cast<void**>(&m->h_topk_idx), sizeof(int32_t) * R * kMaxTopK,
+        hipHostMalloc(reinterpret_cast<void**>(&m->h_topk_idx), sizeof(int32_t) * 2 * R * kMaxTopK,
                       hipHostMallocDefault) != hipSuccess ||
-        hipHostMalloc(reinterpret_cast<void**>(&m->h_topk_lp), sizeof(float) * R * kMaxTopK, hipHostMallocDefault) !=
-            hipSuccess ||
         hipHostMalloc(reinterpret_cast<void**>(&m->h_mask), sizeof(uint32_t) * kMaxMaskedRows * ((D.vocab + 31) / 32),
                       hipHostMallocDefault) != hipSuccess ||
         hipHostMalloc(reinterpret_cast<void**>(&m->h_best), sizeof(int32_t) * 2 * m->best_rows,
@@ -1188,6 +1188,7 @@ int32_t nhip_decoder_create(const nhip_decoder_dims* dims, nhip_decoder** out)
         return fail(NHIP_ERR_HIP);
     }
     m->h_best_val = reinterpret_cast<float*>(m->h_best + m->best_rows);
+    m->h_topk_lp = reinterpret_cast<float*>(m->h_topk_idx + (size_t)R * kMaxTopK);
     if (hipStreamCreateWithFlags(&m->stream, hipStreamNonBlocking) != hipSuccess) {
         set_error("hipStreamCreate failed");
         return fail(NHIP_ERR_HIP);
@@ -1699,7 +1700,6 @@ int32_t nhip_decoder_destroy(nhip_decoder* m)
     for (void* p : m->allocations) (void)hipFree(p);
     if (m->h_in) (void)hipHostFree(m->h_in);
     if (m->h_topk_idx) (void)hipHostFree(m->h_topk_idx);
-    if (m->h_topk_lp) (void)hipHostFree(m->h_topk_lp);
     if (m->h_mask) (void)hipHostFree(m->h_mask);
     if (m->h_best) (void)hipHostFree(m->h_best);
     if (m->stream) (void)hipStreamDestroy(m->stream);
