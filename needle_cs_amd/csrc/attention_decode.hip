@@ -64,8 +64,7 @@ struct DecodeAttnParams {
     // each row's position, RoPE tables [capacity][32], and the cache it writes
     const float* qkv;
     const int32_t* positions;
-    const float* rope_cos;
-    const float* rope_sin;
+    const float* rope_rows;  // [rows][64]: cos then sin of each row's position (32 each)
     int8_t* wkeys;
     float* wkscale;
     int8_t* wvalues;
@@ -568,6 +567,12 @@ __global__ __launch_bounds__(kThreads) void decode_attention_row_kernel(ATTN_HEA
             const bool value = u > 0 && ((u - 1) & 1);
             const int col = u == 0 ? h : (value ? p.heads + p.kv_heads + kv : p.heads + kv);
             post_x[k] = p.qkv[((size_t)r * units_all + col) * 64 + e];
+            // the RoPE factors of the unit's row (the query's row, or the
+            // row whose key this is), staged per row: no dependence on the
+            // position, so they arrive with this first round trip
+            const float* rope = p.rope_rows + (size_t)r * 64 + (e & 31);
+            post_c[k] = rope[0];
+            post_sn[k] = rope[32];
         }
         const int lr = min(e, p.rows - 1);
         const int mpos = p.positions[lr];
@@ -603,17 +608,6 @@ __global__ __launch_bounds__(kThreads) void decode_attention_row_kernel(ATTN_HEA
             rel[r] = rpos[r] - first;
             subs |= (uint32_t)((r < p.rows) & (rslot[r] == slot) & (rel[r] >= 0) & (rel[r] < count)) << r;
             pos_row = r == row ? rpos[r] : pos_row;
-        }
-#pragma unroll
-        for (int k = 0; k < 3; k++) {
-            const int u = (tid >> 6) + 4 * k;
-            const int r = min((u - 1) >> 1, p.rows - 1);
-            int at = pos_row;
-#pragma unroll
-            for (int q = 0; q < kPostRows; q++) at = (u > 0 && q == r) ? rpos[q] : at;
-            const size_t t = (size_t)at * 32 + (e & 31);
-            post_c[k] = p.rope_cos[t];
-            post_sn[k] = p.rope_sin[t];
         }
     }
 
@@ -930,7 +924,7 @@ int32_t attention_decode_post_impl(const AttnPostInputs& in, int32_t rows, int32
     if (rows < 1 || rows > kPostRows || capacity > kRowMaxCapacity) return 1;
     NHIP_REQUIRE(heads > 0 && kv_heads > 0 && heads % kv_heads == 0 && slots > 0 && capacity > 0 && max_chunks >= 1,
                  "attention: bad shape");
-    NHIP_REQUIRE(in.qkv && in.positions && in.rope_cos && in.rope_sin && d_keys && d_key_scales && d_values &&
+    NHIP_REQUIRE(in.qkv && in.positions && in.rope_rows && d_keys && d_key_scales && d_values &&
                      d_value_scales && d_row_slot && d_row_first && d_row_count && d_out,
                  "attention: null pointer");
     DecodeAttnParams p{};
@@ -947,8 +941,7 @@ int32_t attention_decode_post_impl(const AttnPostInputs& in, int32_t rows, int32
     p.row_count = d_row_count;
     p.qkv = in.qkv;
     p.positions = in.positions;
-    p.rope_cos = in.rope_cos;
-    p.rope_sin = in.rope_sin;
+    p.rope_rows = in.rope_rows;
     p.out = d_out;
     p.rows = rows;
     p.heads = heads;

@@ -193,8 +193,7 @@ constexpr int kFusedPrologueMaxTiles = 512;
 struct AttnPostInputs {
     const float* qkv;          // [rows][(heads + 2 kv_heads) * 64]
     const int32_t* positions;  // [rows]
-    const float* rope_cos;     // [capacity][32]
-    const float* rope_sin;
+    const float* rope_rows;    // [rows][64]: cos then sin (32 each) of each row's position
 };
 int32_t attention_decode_post_impl(const AttnPostInputs& in, int32_t rows, int32_t heads, int32_t kv_heads,
                                    int8_t* d_keys, float* d_key_scales, int8_t* d_values, float* d_value_scales,

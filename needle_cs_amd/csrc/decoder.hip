@@ -729,6 +729,7 @@ struct nhip_decoder {
     float* emb = nullptr;
     float* rope_cos = nullptr;
     float* rope_sin = nullptr;
+    std::vector<float> rope_cos_h, rope_sin_h;  // host copies of the tables
     int8_t* keys = nullptr;
     int8_t* values = nullptr;
     float* key_scales = nullptr;
@@ -788,6 +789,10 @@ int32_t* in_positions(nhip_decoder* m, int32_t* base) { return base + 2 * m->dim
 int32_t* in_first(nhip_decoder* m, int32_t* base) { return base + 3 * m->dims.max_rows; }
 int32_t* in_count(nhip_decoder* m, int32_t* base) { return base + 4 * m->dims.max_rows; }
 int32_t* in_heads(nhip_decoder* m, int32_t* base) { return base + 5 * m->dims.max_rows; }
+// [max_rows][64]: the RoPE table's cos then sin row (32 each) of each row's
+// position, staged with the step so that the attention reads them without a
+// load that depends on the position
+float* in_rope(nhip_decoder* m, int32_t* base) { return reinterpret_cast<float*>(base + 6 * m->dims.max_rows); }
 
 // Residual + RMSNorm + quantize feeding a matmul.  For up to four rows and
 // at most kFusedPrologueMaxTiles row tiles one fused launch computes the
@@ -881,7 +886,7 @@ int32_t enqueue_forward(nhip_decoder* m, int rows, const HeadPlan& hp, bool mask
             decode_attention_kv_per_block(H / KV, KV, decode_attention_lmax(D.capacity, D.max_chunks)) >= KV;
         rc = 1;
         if (fuse && !attn_quant) {  // RoPE, quantize and the KV write inside the attention launch
-            const AttnPostInputs in{m->qkv, pp.positions, m->rope_cos, m->rope_sin};
+            const AttnPostInputs in{m->qkv, pp.positions, in_rope(m, m->d_in)};
             rc = attention_decode_post_impl(in, rows, H, KV, pp.keys, pp.key_scales, pp.values, pp.value_scales,
                                             D.slots, D.capacity, pp.slots, in_first(m, m->d_in),
                                             in_count(m, m->d_in), D.max_chunks, m->att, s);
@@ -996,13 +1001,17 @@ int32_t stage_inputs(nhip_decoder* m, const int32_t* tokens, const int32_t* slot
         in_positions(m, m->h_in)[r] = positions[r];
         in_first(m, m->h_in)[r] = 0;
         in_count(m, m->h_in)[r] = positions[r] + 1;
+        float* rope = in_rope(m, m->h_in) + (size_t)r * 64;
+        std::memcpy(rope, m->rope_cos_h.data() + (size_t)positions[r] * 32, 32 * sizeof(float));
+        std::memcpy(rope + 32, m->rope_sin_h.data() + (size_t)positions[r] * 32, 32 * sizeof(float));
     }
     for (int i = 0; i < heads; i++) {
         NHIP_REQUIRE(head_rows[i] >= 0 && head_rows[i] < rows, "head row %d outside [0, %d)", head_rows[i], rows);
         in_heads(m, m->h_in)[i] = head_rows[i];
     }
-    NHIP_CHECK_HIP(hipMemcpyAsync(m->d_in, m->h_in, sizeof(int32_t) * 6 * D.max_rows, hipMemcpyHostToDevice,
-                                  m->stream));
+    // the id arrays and the RoPE rows of the staged rows, in one copy
+    NHIP_CHECK_HIP(hipMemcpyAsync(m->d_in, m->h_in, sizeof(int32_t) * 6 * D.max_rows + sizeof(float) * 64 * rows,
+                                  hipMemcpyHostToDevice, m->stream));
     return NHIP_OK;
 }
 
@@ -1156,7 +1165,7 @@ int32_t nhip_decoder_create(const nhip_decoder_dims* dims, nhip_decoder** out)
         (rc = dalloc(m, &m->qkv, (size_t)R * m->qkv_n)) || (rc = dalloc(m, &m->qh, (size_t)R * D.heads * 64)) ||
         (rc = dalloc(m, &m->qhs, (size_t)R * D.heads)) || (rc = dalloc(m, &m->att, (size_t)R * D.heads * 64)) ||
         (rc = dalloc(m, &m->gu, (size_t)R * 2 * D.ffn)) || (rc = dalloc(m, &m->act, (size_t)R * D.ffn)) || (rc = dalloc(m, &m->logits, (size_t)R * D.vocab)) ||
-        (rc = dalloc(m, &m->d_in, (size_t)6 * R)) || (rc = dalloc(m, &m->d_topk_idx, (size_t)2 * R * kMaxTopK)) ||
+        (rc = dalloc(m, &m->d_in, (size_t)(6 + 64) * R)) || (rc = dalloc(m, &m->d_topk_idx, (size_t)2 * R * kMaxTopK)) ||
         (rc = dalloc(m, &m->d_mask, (size_t)kMaxMaskedRows * ((D.vocab + 31) / 32))) ||
         (rc = dalloc(m, &m->d_best, (size_t)2 * m->best_rows)) ||
         (rc = dalloc(m, &m->topk.vals, (size_t)R * ((D.vocab + kTopkBlock - 1) / kTopkBlock) * kMaxTopK)) ||
@@ -1176,7 +1185,7 @@ int32_t nhip_decoder_create(const nhip_decoder_dims* dims, nhip_decoder** out)
     m->d_best_val = reinterpret_cast<float*>(m->d_best + m->best_rows);  // one copy returns both
     // the top-k ids, then their log-probabilities: one copy returns both
     m->d_topk_lp = reinterpret_cast<float*>(m->d_topk_idx + (size_t)R * kMaxTopK);
-    if (hipHostMalloc(reinterpret_cast<void**>(&m->h_in), sizeof(int32_t) * 6 * R, hipHostMallocDefault) !=
+    if (hipHostMalloc(reinterpret_cast<void**>(&m->h_in), sizeof(int32_t) * (6 + 64) * R, hipHostMallocDefault) !=
             hipSuccess ||
         hipHostMalloc(reinterpret_cast<void**>(&m->h_topk_idx), sizeof(int32_t) * 2 * R * kMaxTopK,
                       hipHostMallocDefault) != hipSuccess ||
@@ -1203,6 +1212,8 @@ int32_t nhip_decoder_create(const nhip_decoder_dims* dims, nhip_decoder** out)
         }
     if ((rc = upload(m, &m->rope_cos, c.data(), c.size())) || (rc = upload(m, &m->rope_sin, sn.data(), sn.size())))
         return fail(rc);
+    m->rope_cos_h = std::move(c);
+    m->rope_sin_h = std::move(sn);
     if (hipMemset(m->keys, 0, cells * 64) != hipSuccess || hipMemset(m->values, 0, cells * 64) != hipSuccess ||
         hipMemset(m->key_scales, 0, cells * 4) != hipSuccess || hipMemset(m->value_scales, 0, cells * 4) != hipSuccess) {
         set_error("hipMemset failed");
