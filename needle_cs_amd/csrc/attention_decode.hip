@@ -193,6 +193,11 @@ __global__ __launch_bounds__(kThreads) void decode_attention_kernel(ATTN_HEAD_PA
     const int slot = uniform_load(p.row_slot, row);
     const int first = uniform_load(p.row_first, row);
     const int count = uniform_load(p.row_count, row);
+    // the cache pointers and sizes in the same round trip: left to itself the
+    // compiler loads them from the argument segment only after the plan, a
+    // second round trip ahead of the first cache load
+    asm volatile("" ::"s"(p.keys), "s"(p.kscale), "s"(p.values), "s"(p.vscale), "s"(p.lmax), "s"(p.qk),
+                 "s"(p.inv_sqrt));
     // rows with an invalid slot or span produce zeros (no out-of-range reads)
     const bool valid = (slot >= 0) & (slot < p.slots) & (first >= 0) & (count >= 1) & (count <= p.capacity - first);
     if (!valid) {
@@ -221,15 +226,22 @@ __global__ __launch_bounds__(kThreads) void decode_attention_kernel(ATTN_HEAD_PA
         ? reinterpret_cast<const uint32_t*>(p.q + ((size_t)row * p.heads + h0) * qk)[tid] : 0u;
     const float qsc = tid < nh ? p.qscale[(size_t)row * p.heads + h0 + tid] : 0.0f;
 
+    // Cache addresses: a uniform base at the chunk's first (position, kv
+    // head) cell plus a 32-bit lane offset (one add per load; the launch
+    // checks that a chunk's cells span less than 2 GB)
+    const size_t cell0 = pos0 * p.kv_heads + kv0;
     const bool vthread = tid < nh * 16;
     const int vhl = vthread ? tid >> 4 : 0;
     const int vqd = tid & 15;
-    const size_t vstride4 = (size_t)p.kv_heads * 16;  // dwords per cache position
-    const uint32_t* vp = reinterpret_cast<const uint32_t*>(p.values) +
-                         (pos0 * p.kv_heads + kv0 + vhl / group) * 16 + vqd;
+    const uint32_t vrow = (uint32_t)p.kv_heads * 64u;  // value bytes per cache position
+    const uint8_t* vbase = reinterpret_cast<const uint8_t*>(p.values) + cell0 * 64;
+    const uint32_t voff = (uint32_t)(vhl / group) * 64u + 4u * (uint32_t)vqd;
+    auto vload = [&](int s) {
+        return *reinterpret_cast<const uint32_t*>(vbase + (voff + (uint32_t)min(s, L - 1) * vrow));
+    };
     uint32_t vreg[kVBlock];
 #pragma unroll
-    for (int j = 0; j < kVBlock; j++) vreg[j] = vp[(size_t)min(j, L - 1) * vstride4];
+    for (int j = 0; j < kVBlock; j++) vreg[j] = vload(j);
 
     // phase 1: scores.  The chunk's key rows for this head block are read as
     // 16-byte units, four consecutive lanes per (position, kv head) -- a wave
@@ -243,7 +255,10 @@ __global__ __launch_bounds__(kThreads) void decode_attention_kernel(ATTN_HEAD_PA
     const int qslot = min(lslot, pieces - 1);
     const uint32_t mag_kv = magic((uint32_t)nkv);
     const uint32_t mag_l = magic((uint32_t)L);
-    const float* sbase = (lslot & 1) ? p.vscale : p.kscale;  // slot 0 the key scale, slot 1 the value scale
+    // slot 0 the key scale, slot 1 the value scale
+    const float* sbase = ((lslot & 1) ? p.vscale : p.kscale) + cell0;
+    const int8_t* kbase = p.keys + cell0 * qk;
+    const uint32_t kgap = (uint32_t)(p.kv_heads - nkv);  // cells of other blocks per position
     constexpr int KU = 8;  // units per thread per pass, loads issued together
     auto pass = [&](int base) {
         uint4 kw[KU];
@@ -251,13 +266,11 @@ __global__ __launch_bounds__(kThreads) void decode_attention_kernel(ATTN_HEAD_PA
 #pragma unroll
         for (int k = 0; k < KU; k++) {
             if (base + k * kThreads >= units) break;  // uniform: no duplicate loads
-            const int u = min(base + k * kThreads + tid, units - 1);
-            const int w = u >> 2;
-            const int s = fast_div(w, mag_kv);
-            const int kvl = w - s * nkv;
-            const size_t cell = (pos0 + s) * p.kv_heads + kv0 + kvl;
-            kw[k] = *reinterpret_cast<const uint4*>(p.keys + cell * qk + 16 * qslot);
-            sv[k] = sbase[cell];
+            const uint32_t w = (uint32_t)min(base + k * kThreads + tid, units - 1) >> 2;
+            // cell offset (s * kv_heads + kvl) of unit w = s * nkv + kvl
+            const uint32_t cw = kgap ? w + (uint32_t)fast_div((int)w, mag_kv) * kgap : w;
+            kw[k] = *reinterpret_cast<const uint4*>(kbase + (cw * (uint32_t)qk + 16u * (uint32_t)qslot));
+            sv[k] = sbase[cw];
         }
         if (base == 0) {  // stage the query heads and scales behind the first loads
             if (tid < nh * q4) reinterpret_cast<uint32_t*>(q_lds)[(tid / q4) * 16 + (tid % q4)] = qword;
@@ -327,7 +340,7 @@ __global__ __launch_bounds__(kThreads) void decode_attention_kernel(ATTN_HEAD_PA
         for (int s0 = 0; s0 < L; s0 += kVBlock) {
             if (s0 > 0) {
 #pragma unroll
-                for (int j = 0; j < kVBlock; j++) vreg[j] = vp[(size_t)min(s0 + j, L - 1) * vstride4];
+                for (int j = 0; j < kVBlock; j++) vreg[j] = vload(s0 + j);
             }
 #pragma unroll
             for (int j4 = 0; j4 < kVBlock; j4 += 4) {
@@ -988,6 +1001,8 @@ int32_t attention_decode_impl(const int8_t* d_q, const float* d_qscale, int32_t 
     const int kv_per_block = decode_attention_kv_per_block(group, kv_heads, lmax);
     NHIP_REQUIRE(kv_per_block > 0, "attention: chunks of up to %d positions do not fit in LDS; raise max_chunks",
                  lmax);
+    NHIP_REQUIRE((int64_t)lmax * kv_heads * 64 < (int64_t(1) << 31),
+                 "attention: a chunk of %d positions x %d kv heads spans 2 GB of the cache or more", lmax, kv_heads);
     const size_t lds = decode_attention_lds(lmax, kv_per_block, group);
     int32_t rc = ensure_device();
     if (rc) return rc;
