@@ -71,6 +71,8 @@ struct DecodeAttnParams {
     float* wvscale;
     int32_t rows, heads, kv_heads, qk, slots, capacity, max_chunks, lmax, kv_per_block;
     float inv_sqrt;
+    int32_t cus;         // compute units of the device (the chunk kernel's placement period)
+    uint32_t cus_magic;  // magic(cus) for fast_div
 };
 
 // The attention kernels' preloaded head (head_pair, common.hpp): the span
@@ -165,13 +167,83 @@ __device__ __forceinline__ int32_t uniform_load(const int32_t* a, int i)
     return ((const __attribute__((address_space(4))) int32_t*)a)[i];
 }
 
+// Placement of the chunk kernel's (row, chunk) units on compute units, for
+// batches of up to kPlacedRows rows.  A launch's workgroups are dealt to the
+// CUs in turn (workgroup g to CU g mod P, P CUs, all resident at once), and a
+// CU's time grows with the positions of its units, so the units are ordered
+// by chunk length, longest first (ties: lower row first), and unit j goes to
+// workgroup g whose round g / P runs forward on even rounds and backward on
+// odd ones: each CU's long and short units pair up.  Every lane of a wave
+// takes one row (span, plan); lane r's units are j in [before_r, before_r +
+// needed_r), before_r summing the units of the rows ordered ahead of it, a
+// quarter of the rows per wave, combined through LDS.  Rows with an invalid
+// span count as one unit of length 0 (its workgroup writes the zeros).
+// Returns false, uniformly over the workgroup, when workgroup g has no unit.
+constexpr int kPlacedRows = 64;
+
+struct PlacedUnit {
+    int row, chunk, slot, first, count, needed, length;
+    bool valid;
+};
+
+__device__ __forceinline__ bool place_unit(const DecodeAttnParams& p, int g, PlacedUnit& u)
+{
+    __shared__ int quarter_sums[4][64];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform, so the loop below is
+    const bool live = lane < p.rows;
+    int s = 0, f = 0, c = 0;
+    if (live) {
+        s = p.row_slot[lane];
+        f = p.row_first[lane];
+        c = p.row_count[lane];
+    }
+    // the cache pointers and sizes in the same round trip (left to itself the
+    // compiler loads them from the argument segment after the placement)
+    asm volatile("" ::"s"(p.keys), "s"(p.kscale), "s"(p.values), "s"(p.vscale), "s"(p.lmax), "s"(p.qk),
+                 "s"(p.inv_sqrt), "s"(p.slots), "s"(p.capacity), "s"(p.max_chunks), "s"(p.cus), "s"(p.cus_magic),
+                 "s"(p.out), "s"(p.partials), "s"(p.q_out));
+    const bool ok = live & (s >= 0) & (s < p.slots) & (f >= 0) & (c >= 1) & (c <= p.capacity - f);
+    // the reference's plan (as plan()) in unsigned arithmetic, count >= 1
+    const uint32_t cu = ok ? (uint32_t)c : 16u;
+    const uint32_t want = min(max(cu >> 4, 1u), (uint32_t)p.max_chunks);
+    const uint32_t len = (((cu + want - 1) / want) + 3) & ~3u;
+    const int need = ok ? (int)((cu + len - 1) / len) : (live ? 1 : 0);
+    const int key = live ? (ok ? (int)len : 0) * 64 + (63 - lane) : -1;
+    const int per = (p.rows + 3) >> 2;
+    const int r_end = min(p.rows, (wave + 1) * per);
+    int before = 0;
+    for (int r = wave * per; r < r_end; r++) {  // uniform bounds
+        const int kr = __builtin_amdgcn_readlane(key, r);
+        const int nr = __builtin_amdgcn_readlane(need, r);
+        before += kr > key ? nr : 0;
+    }
+    quarter_sums[wave][lane] = before;
+    __syncthreads();
+    before = quarter_sums[0][lane] + quarter_sums[1][lane] + quarter_sums[2][lane] + quarter_sums[3][lane];
+    const int P = p.cus;
+    const int round = fast_div(g, p.cus_magic);
+    const int at = g - round * P;
+    const int j = round * P + ((round & 1) ? P - 1 - at : at);
+    const uint64_t hit = __ballot(live && before <= j && j < before + need);
+    if (hit == 0) return false;
+    const int r = __builtin_ctzll(hit);
+    u.row = r;
+    u.chunk = j - __builtin_amdgcn_readlane(before, r);
+    u.slot = __builtin_amdgcn_readlane(s, r);
+    u.first = __builtin_amdgcn_readlane(f, r);
+    u.count = __builtin_amdgcn_readlane(c, r);
+    u.needed = __builtin_amdgcn_readlane(need, r);
+    u.length = __builtin_amdgcn_readlane((int)len, r);
+    u.valid = __builtin_amdgcn_readlane((int)ok, r) != 0;
+    return true;
+}
+
 __global__ __launch_bounds__(kThreads) void decode_attention_kernel(ATTN_HEAD_PARAMS, DecodeAttnParams p)
 {
     ATTN_TAKE_HEAD(p, q, qscale);
     extern __shared__ __align__(16) uint8_t lds[];
     const int hb = blockIdx.z;
-    const int row = blockIdx.y;
-    const int chunk = blockIdx.x;
     const int tid = threadIdx.x;
     const int group = p.heads / p.kv_heads;
     const int kv0 = hb * p.kv_per_block;
@@ -188,19 +260,28 @@ __global__ __launch_bounds__(kThreads) void decode_attention_kernel(ATTN_HEAD_PA
     float* qs_lds = wl + hmax * lmax;                                       // [16]
     uint32_t* peak_key = reinterpret_cast<uint32_t*>(qs_lds + kMaxHeadsPerBlock);  // [16]
 
-    // the span in one round trip (scalar loads; non-short-circuit tests, so
-    // no branch separates them)
-    const int slot = uniform_load(p.row_slot, row);
-    const int first = uniform_load(p.row_first, row);
-    const int count = uniform_load(p.row_count, row);
-    // the cache pointers and sizes in the same round trip: left to itself the
-    // compiler loads them from the argument segment only after the plan, a
-    // second round trip ahead of the first cache load
-    asm volatile("" ::"s"(p.keys), "s"(p.kscale), "s"(p.values), "s"(p.vscale), "s"(p.lmax), "s"(p.qk),
-                 "s"(p.inv_sqrt));
-    // rows with an invalid slot or span produce zeros (no out-of-range reads)
-    const bool valid = (slot >= 0) & (slot < p.slots) & (first >= 0) & (count >= 1) & (count <= p.capacity - first);
-    if (!valid) {
+    // the unit, its row's span and plan in one round trip
+    PlacedUnit u;
+    if (p.rows <= kPlacedRows) {
+        if (!place_unit(p, blockIdx.x, u)) return;
+    } else {  // one workgroup per (chunk, row): scalar loads, no branch between them
+        u.row = blockIdx.y;
+        u.chunk = blockIdx.x;
+        u.slot = uniform_load(p.row_slot, u.row);
+        u.first = uniform_load(p.row_first, u.row);
+        u.count = uniform_load(p.row_count, u.row);
+        // the cache pointers and sizes in the same round trip: left to itself
+        // the compiler loads them from the argument segment only after the
+        // plan, a second round trip ahead of the first cache load
+        asm volatile("" ::"s"(p.keys), "s"(p.kscale), "s"(p.values), "s"(p.vscale), "s"(p.lmax), "s"(p.qk),
+                     "s"(p.inv_sqrt));
+        // rows with an invalid slot or span produce zeros (no out-of-range reads)
+        u.valid = (u.slot >= 0) & (u.slot < p.slots) & (u.first >= 0) & (u.count >= 1) &
+                  (u.count <= p.capacity - u.first);
+        u.needed = u.valid ? plan(u.count, p.max_chunks, &u.length) : 1;
+    }
+    const int row = u.row, chunk = u.chunk, slot = u.slot, first = u.first, count = u.count;
+    if (!u.valid) {
         if (chunk == 0 && tid < nh * 16) {
             *reinterpret_cast<float4*>(p.out + ((size_t)row * p.heads + h0 + (tid >> 4)) * 64 + 4 * (tid & 15)) =
                 make_float4(0.0f, 0.0f, 0.0f, 0.0f);
@@ -209,8 +290,7 @@ __global__ __launch_bounds__(kThreads) void decode_attention_kernel(ATTN_HEAD_PA
         if (chunk == 0 && tid == 0 && p.q_out) p.qs_out[row] = 1.0f;
         return;
     }
-    int length;
-    const int needed = plan(count, p.max_chunks, &length);
+    const int needed = u.needed, length = u.length;
     if (chunk >= needed) return;
     const int begin = first + chunk * length;
     const int L = min(length, count - chunk * length);
@@ -220,8 +300,9 @@ __global__ __launch_bounds__(kThreads) void decode_attention_kernel(ATTN_HEAD_PA
 
     // Loads are issued oldest-first in the order they are consumed (the
     // vector memory counter retires in order): the query heads and scales,
-    // this thread's value dwords of the first kVBlock positions (phase 4),
-    // then the first pass of key rows and scales (phase 1).
+    // the first pass of key rows and scales (phase 1), then this thread's
+    // value dwords of the first kVBlock positions (phase 4), which arrive
+    // while the scores are formed.
     const uint32_t qword = tid < nh * q4
         ? reinterpret_cast<const uint32_t*>(p.q + ((size_t)row * p.heads + h0) * qk)[tid] : 0u;
     const float qsc = tid < nh ? p.qscale[(size_t)row * p.heads + h0 + tid] : 0.0f;
@@ -240,8 +321,6 @@ __global__ __launch_bounds__(kThreads) void decode_attention_kernel(ATTN_HEAD_PA
         return *reinterpret_cast<const uint32_t*>(vbase + (voff + (uint32_t)min(s, L - 1) * vrow));
     };
     uint32_t vreg[kVBlock];
-#pragma unroll
-    for (int j = 0; j < kVBlock; j++) vreg[j] = vload(j);
 
     // phase 1: scores.  The chunk's key rows for this head block are read as
     // 16-byte units, four consecutive lanes per (position, kv head) -- a wave
@@ -272,7 +351,9 @@ __global__ __launch_bounds__(kThreads) void decode_attention_kernel(ATTN_HEAD_PA
             kw[k] = *reinterpret_cast<const uint4*>(kbase + (cw * (uint32_t)qk + 16u * (uint32_t)qslot));
             sv[k] = sbase[cw];
         }
-        if (base == 0) {  // stage the query heads and scales behind the first loads
+        if (base == 0) {  // the value loads, then stage the query heads and scales
+#pragma unroll
+            for (int j = 0; j < kVBlock; j++) vreg[j] = vload(j);
             if (tid < nh * q4) reinterpret_cast<uint32_t*>(q_lds)[(tid / q4) * 16 + (tid % q4)] = qword;
             if (tid < nh) {
                 qs_lds[tid] = qsc * p.inv_sqrt;
@@ -1042,8 +1123,16 @@ int32_t attention_decode_impl(const int8_t* d_q, const float* d_qscale, int32_t 
         NHIP_CHECK_HIP(hipGetLastError());
         return NHIP_OK;
     }
-    hipLaunchKernelGGL(decode_attention_kernel, dim3(max_chunks, rows, head_blocks), dim3(kThreads), lds, stream,
-                       ATTN_HEAD_ARGS(p, p.q, p.qscale), p);
+    p.cus = std::max(device_cus(), 1);
+    p.cus_magic = p.cus == 1 ? 0u : 0xFFFFFFFFu / (uint32_t)p.cus + 1u;  // as magic(): exact for g < 2^16
+    dim3 grid(max_chunks, rows, head_blocks);
+    if (rows <= kPlacedRows) {  // placed units: whole rounds of p.cus workgroups
+        grid.x = rows * max_chunks;
+        if ((int)grid.x > p.cus) grid.x = (grid.x + p.cus - 1) / p.cus * p.cus;
+        grid.y = 1;
+    }
+    hipLaunchKernelGGL(decode_attention_kernel, grid, dim3(kThreads), lds, stream, ATTN_HEAD_ARGS(p, p.q, p.qscale),
+                       p);
     NHIP_CHECK_HIP(hipGetLastError());
     if (max_chunks > 1) {  // single-chunk plans are finished by the chunk kernel
         hipLaunchKernelGGL(decode_merge_kernel, dim3(rows, heads), dim3(64), 0, stream,

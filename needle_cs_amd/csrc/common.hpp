@@ -39,6 +39,8 @@ void clear_error();
 int32_t ensure_device();
 // True once a device has been initialised (by nhip_init or a first use).
 bool device_ready();
+// Compute units of the initialised device.
+int device_cus();
 // Looks up, once per device and with that device current, the address of
 // the no-allocation attention entry's scratch array (attention_decode.hip);
 // called by the device initialisation.

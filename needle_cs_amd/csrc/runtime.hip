@@ -14,6 +14,7 @@ namespace {
 thread_local char g_error[1024] = "";
 std::mutex g_init_mutex;
 int g_device = -1;
+int g_cus = 0;
 hipStream_t g_stream = nullptr;
 char g_describe[256] = "";
 }  // namespace
@@ -51,6 +52,7 @@ static int32_t init_locked(int32_t device)
     if (rc) return rc;
     if (g_stream == nullptr) NHIP_CHECK_HIP(hipStreamCreateWithFlags(&g_stream, hipStreamNonBlocking));
     g_device = device;
+    g_cus = prop.multiProcessorCount;
     snprintf(g_describe, sizeof(g_describe), "needle_hip 0.1 %s (%d CUs, %.0f GiB HBM)", prop.gcnArchName,
              prop.multiProcessorCount, prop.totalGlobalMem / 1073741824.0);
     return NHIP_OK;
@@ -70,6 +72,8 @@ int32_t ensure_device()
 }
 
 bool device_ready() { return g_device >= 0; }
+
+int device_cus() { return g_cus; }
 
 hipStream_t default_stream() { return g_stream; }
 

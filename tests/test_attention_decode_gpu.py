@@ -136,6 +136,28 @@ def test_decode_attention_invalid_rows_are_zero(hip, orc):
     assert np.all(got[1:5] == 0.0)
 
 
+@pytest.mark.parametrize("rows", [6, 64, 70])
+def test_decode_attention_chunk_kernel_invalid_and_many_rows(hip, orc, rows):
+    """The chunk kernel (capacity 1024) with invalid spans among valid ones:
+    up to 64 rows the units are placed in length order over the compute
+    units, beyond that one workgroup per (chunk, row); either way the valid
+    rows are bit-exact and the invalid ones zero."""
+    heads, kv_heads, capacity, max_chunks = 8, 4, 1024, 16
+    cache = Cache(orc, hip, 7000 + rows, 3, capacity, kv_heads, 64)
+    rng = np.random.default_rng(rows)
+    spec = [(int(rng.integers(0, 3)), 0, int(rng.integers(1, capacity + 1))) for _ in range(rows)]
+    bad = {1: (3, 0, 10), 2: (1, -1, 5), 3: (0, 0, 0), 4: (2, 1000, 25)}
+    for k, v in bad.items():
+        spec[k] = v
+    q, qs = queries(orc, cache.st, rows, heads, 64)
+    got, _ = run_decode(hip, cache, q, qs, heads, spec, max_chunks)
+    good = [k for k in range(rows) if k not in bad]
+    want = oracle_decode(orc, cache, q, qs, heads, [spec[k] if k not in bad else (0, 0, 0) for k in range(rows)],
+                         max_chunks)
+    assert bit_equal(got[good], want[good])
+    assert np.all(got[list(bad)] == 0.0)
+
+
 def test_decode_attention_workspace_reuse(hip, orc):
     """Repeated calls on one workspace stay exact, also with new spans."""
     cache = Cache(orc, hip, 7, 3, 1024, 4, 64)
