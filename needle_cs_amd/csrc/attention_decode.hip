@@ -494,8 +494,8 @@ constexpr int kMergeBatch = 64;
 __global__ __launch_bounds__(64) void decode_merge_kernel(ATTN_HEAD_PARAMS, DecodeAttnParams p)
 {
     ATTN_TAKE_HEAD(p, peaks, sums);
-    __shared__ float msm[256];
-    __shared__ float wts[256];
+    __shared__ __align__(16) float msm[256];
+    __shared__ __align__(16) float wts[256];
     const int row = blockIdx.x;
     const int h = blockIdx.y;
     const int d = threadIdx.x;
@@ -511,20 +511,26 @@ __global__ __launch_bounds__(64) void decode_merge_kernel(ATTN_HEAD_PARAMS, Deco
     int length;
     const int needed = plan(count, p.max_chunks, &length);
     if (needed == 1) return;  // the chunk kernel finished the row
-    const size_t rbase = (size_t)row * p.max_chunks * p.heads + h;  // + c * heads
-    const float* part = p.partials + rbase * 64 + d;
-    const size_t cstride = (size_t)p.heads * 64;
+    // uniform bases at the (row, head)'s first chunk, 32-bit lane offsets
+    // (chunk c at + c * heads for the peaks and sums, + c * heads * 64 for
+    // the partials; the workspace layout keeps them below 4 GB)
+    const size_t rbase = (size_t)row * p.max_chunks * p.heads + h;
+    const float* kbase = p.peaks + rbase;
+    const float* sbase = p.sums + rbase;
+    const float* pbase = p.partials + rbase * 64;
+    const uint32_t heads = (uint32_t)p.heads;
+    const uint32_t cstride = heads * 64u;
     // this thread's chunks' peaks and sums (c = d, d + 64, ...; needed <= 256)
     float pk[4], sm[4];
 #pragma unroll
     for (int j = 0; j < 4; j++) {
-        const int c = min(d + 64 * j, needed - 1);
-        pk[j] = p.peaks[rbase + (size_t)c * p.heads];
-        sm[j] = p.sums[rbase + (size_t)c * p.heads];
+        const uint32_t c = (uint32_t)min(d + 64 * j, needed - 1);
+        pk[j] = kbase[c * heads];
+        sm[j] = sbase[c * heads];
     }
     float a[kMergeBatch];
 #pragma unroll
-    for (int j = 0; j < kMergeBatch; j++) a[j] = part[(size_t)min(j, needed - 1) * cstride];
+    for (int j = 0; j < kMergeBatch; j++) a[j] = pbase[(uint32_t)d + (uint32_t)min(j, needed - 1) * cstride];
     if (needed == 2) {  // uniform over the block: MergePartials' two-chunk branch
         const float peak0 = __shfl(pk[0], 0), peak1 = __shfl(pk[0], 1);
         const float sum0 = __shfl(sm[0], 0), sum1 = __shfl(sm[0], 1);
@@ -544,12 +550,17 @@ __global__ __launch_bounds__(64) void decode_merge_kernel(ATTN_HEAD_PARAMS, Deco
     for (int j = 0; j < 4; j++)
         if (d + 64 * j < needed) peak = ref_max(peak, pk[j]);
     peak = wave_max(peak);
+    // chunk weights and sums, zero from `needed` to the end of its batch of
+    // kMergeBatch: the walk below then runs whole batches without branches,
+    // and its extra steps add +0 to sums that start at +0 (never -0 under
+    // round-to-nearest), which leaves them unchanged
+    const int padded = (needed + kMergeBatch - 1) / kMergeBatch * kMergeBatch;
 #pragma unroll
     for (int j = 0; j < 4; j++) {
         const int c = d + 64 * j;
-        if (c < needed) {
-            wts[c] = exp_poly(pk[j] - peak);
-            msm[c] = sm[j];
+        if (c < padded) {
+            wts[c] = c < needed ? exp_poly(pk[j] - peak) : 0.0f;
+            msm[c] = c < needed ? sm[j] : 0.0f;
         }
     }
     __syncthreads();
@@ -557,28 +568,26 @@ __global__ __launch_bounds__(64) void decode_merge_kernel(ATTN_HEAD_PARAMS, Deco
     for (int c0 = 0; c0 < needed; c0 += kMergeBatch) {
         if (c0 > 0) {
 #pragma unroll
-            for (int j = 0; j < kMergeBatch; j++) a[j] = part[(size_t)min(c0 + j, needed - 1) * cstride];
+            for (int j = 0; j < kMergeBatch; j++)
+                a[j] = pbase[(uint32_t)d + (uint32_t)min(c0 + j, needed - 1) * cstride];
         }
+        float4 w4[kMergeBatch / 4], s4[kMergeBatch / 4];
 #pragma unroll
-        for (int j = 0; j < kMergeBatch; j += 4) {
-            if (c0 + j >= needed) break;  // uniform
-            const float4 w4 = *reinterpret_cast<const float4*>(wts + c0 + j);
-            const float4 s4 = *reinterpret_cast<const float4*>(msm + c0 + j);
-            const int rem = needed - (c0 + j);
-            total = total + w4.x * s4.x;
-            sum = sum + w4.x * a[j];
-            if (rem > 1) {
-                total = total + w4.y * s4.y;
-                sum = sum + w4.y * a[j + 1];
-            }
-            if (rem > 2) {
-                total = total + w4.z * s4.z;
-                sum = sum + w4.z * a[j + 2];
-            }
-            if (rem > 3) {
-                total = total + w4.w * s4.w;
-                sum = sum + w4.w * a[j + 3];
-            }
+        for (int i = 0; i < kMergeBatch / 4; i++) {
+            w4[i] = *reinterpret_cast<const float4*>(wts + c0 + 4 * i);
+            s4[i] = *reinterpret_cast<const float4*>(msm + c0 + 4 * i);
+        }
+        const int rem = needed - c0;
+        auto step = [&](float w, float sv, float av, int j) {
+            total = total + w * sv;
+            sum = sum + w * (j < rem ? av : 0.0f);
+        };
+#pragma unroll
+        for (int i = 0; i < kMergeBatch / 4; i++) {
+            step(w4[i].x, s4[i].x, a[4 * i], 4 * i);
+            step(w4[i].y, s4[i].y, a[4 * i + 1], 4 * i + 1);
+            step(w4[i].z, s4[i].z, a[4 * i + 2], 4 * i + 2);
+            step(w4[i].w, s4[i].w, a[4 * i + 3], 4 * i + 3);
         }
     }
     *dst = sum * (1.0f / total);

@@ -158,6 +158,18 @@ def test_decode_attention_chunk_kernel_invalid_and_many_rows(hip, orc, rows):
     assert np.all(got[list(bad)] == 0.0)
 
 
+@pytest.mark.parametrize("max_chunks", [100, 256])
+def test_decode_attention_merge_of_many_chunks(hip, orc, max_chunks):
+    """Rows of up to 8192 positions in up to 256 chunks: the merge walks its
+    chunks in batches of 64 (the last one partly filled), bit-exact."""
+    heads = 8
+    cache = Cache(orc, hip, 9100 + max_chunks, 2, 8192, heads, 64)
+    spec = [(0, 0, 8192), (1, 5, 4100), (0, 100, 1700), (1, 0, 1040), (0, 7000, 1190), (1, 3, 33)]
+    q, qs = queries(orc, cache.st, len(spec), heads, 64)
+    got, _ = run_decode(hip, cache, q, qs, heads, spec, max_chunks)
+    assert bit_equal(got, oracle_decode(orc, cache, q, qs, heads, spec, max_chunks))
+
+
 def test_decode_attention_workspace_reuse(hip, orc):
     """Repeated calls on one workspace stay exact, also with new spans."""
     cache = Cache(orc, hip, 7, 3, 1024, 4, 64)
