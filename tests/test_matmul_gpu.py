@@ -343,6 +343,12 @@ def test_kernel_table_matmul_rows_leaves_rows_untouched(hip, orc, bits, rows, co
     got = np.full(tokens * ldy, SENTINEL, dtype=np.float32)
     hip.lib().nhip_matmul_rows(C.byref(cq), C.byref(act), tokens, got.ctypes.data, ldy, r0, r1)
     assert hip.last_error() == ""
+    # the entry caches the weights' device copy by host address; drop it as
+    # the reference's host does when it disposes of a model, so that a later
+    # case whose arrays reuse these addresses uploads its own weights
+    released = C.c_int32(0)
+    hip.check(hip.lib().nhip_table_release(c["indices"].ctypes.data, c["indices"].nbytes, C.byref(released)))
+    assert released.value == 1
     want = np.full(tokens * ldy, SENTINEL, dtype=np.float32)
     orc.matmul_rows(c["cq"], c["act"], tokens, want, ldy, r0, r1)
     assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
