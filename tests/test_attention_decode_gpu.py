@@ -136,12 +136,13 @@ def test_decode_attention_invalid_rows_are_zero(hip, orc):
     assert np.all(got[1:5] == 0.0)
 
 
-@pytest.mark.parametrize("rows", [6, 64, 70])
+@pytest.mark.parametrize("rows", [6, 20, 64, 70])
 def test_decode_attention_chunk_kernel_invalid_and_many_rows(hip, orc, rows):
     """The chunk kernel (capacity 1024) with invalid spans among valid ones:
     up to 64 rows the units are placed in length order over the compute
-    units, beyond that one workgroup per (chunk, row); either way the valid
-    rows are bit-exact and the invalid ones zero."""
+    units (20 rows x 16 chunks: a second, backward round of 256 workgroups,
+    partly used), beyond that one workgroup per (chunk, row); either way the
+    valid rows are bit-exact and the invalid ones zero."""
     heads, kv_heads, capacity, max_chunks = 8, 4, 1024, 16
     cache = Cache(orc, hip, 7000 + rows, 3, capacity, kv_heads, 64)
     rng = np.random.default_rng(rows)
