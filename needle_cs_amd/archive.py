@@ -16,6 +16,15 @@ FinalNorm and the tokenizer blob; header words as Geometry reads them
 (Model.cs:75-104).  Values are seeded random draws scaled to keep every
 activation finite and in range: the reference ships no Needle 3 weights
 offline, so these archives drive the engine's parity tests and benchmarks.
+
+Record shapes follow the real archive where the reference's numpy forward
+reads them (tools/golden.py): D1 and D4 span the MLP width (it multiplies
+them with the zero-padded width, golden.py:186-195; the engine reads their
+first `dim` entries, Blocks.cs:1135 and :1216), BPre / BPost are [layers][4]
+and BRes [layers][4][4] (golden.py:258-263).  The engram value weights and
+the MLP's output scale D4 are drawn large enough that the engram and the MLP
+move each layer's output by well over the engine's int8 activation noise, so
+a misplaced engram site or MLP shows against that forward.
 """
 from __future__ import annotations
 
@@ -142,11 +151,11 @@ def needle3_archive(g: dict, seed: int) -> bytes:
         dense((d,), rng.uniform(-0.2, 0.2, d))                                  # PostNorm
         dense((1,), rng.uniform(-1, 1, 1))                                      # AttnGate (logit)
         dense((d,), rng.uniform(-0.2, 0.2, d))                                  # PreHada
-        dense((d,), rng.uniform(0.5, 1.5, d))                                   # D1
+        dense((width,), np.r_[rng.uniform(0.5, 1.5, d), np.ones(width - d)])    # D1
         dense((width,), rng.uniform(0.5, 1.5, width))                           # D2
         dense((width,), rng.uniform(-0.1, 0.1, width))                          # B2
         dense((width,), rng.uniform(0.5, 1.5, width))                           # D3
-        dense((d,), rng.uniform(0.05, 0.2, d))                                  # D4
+        dense((width,), np.r_[rng.uniform(0.2, 0.8, d), np.ones(width - d)])    # D4
         for n in (rows, cols, rows, cols, rows, cols):                          # W1A, W1B, W2A, W2B, W3A, W3B
             dense((n, n), rng.standard_normal(n * n) / math.sqrt(n))
         dense((d, 8), rng.standard_normal(d * 8) * 0.05)                        # CondV
@@ -154,9 +163,9 @@ def needle3_archive(g: dict, seed: int) -> bytes:
     dense((L,), rng.uniform(0.5, 1.5, L))                                       # APre
     dense((L,), rng.uniform(0.5, 1.5, L))                                       # APost
     dense((L,), rng.uniform(0.5, 1.5, L))                                       # ARes
-    dense((L * 4,), rng.uniform(-1, 1, L * 4))                                  # BPre
-    dense((L * 4,), rng.uniform(-1, 1, L * 4))                                  # BPost
-    dense((L * 16,), rng.uniform(-1, 1, L * 16))                                # BRes
+    dense((L, 4), rng.uniform(-1, 1, L * 4))                                    # BPre
+    dense((L, 4), rng.uniform(-1, 1, L * 4))                                    # BPost
+    dense((L, 4, 4), rng.uniform(-1, 1, L * 16))                                # BRes
     cq(L * 4, 4 * d, 4)                                                         # PhiPre
     cq(L * 4, 4 * d, 4)                                                         # PhiPost
     cq(L * 16, 4 * d, 4)                                                        # PhiRes
@@ -165,7 +174,7 @@ def needle3_archive(g: dict, seed: int) -> bytes:
     for _ in g["sites"]:
         cq(g["engram_tables"] * g["engram_slots"], g["engram_sub"], 2, 0.05, 0.3)  # Tables
         cq(d, d, 2)                                                             # Key
-        cq(d, d, 2)                                                             # Value
+        cq(d, d, 2, 0.02, 0.2)                                                  # Value
         dense((4, d), rng.uniform(-0.5, 0.5, 4 * d))                            # Taps
     dense((d,), rng.uniform(-0.2, 0.2, d))                                      # FinalNorm
     tensors.append((RAW, (16,), bytes(range(16)), 0))                           # tokenizer blob

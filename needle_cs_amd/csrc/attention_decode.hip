@@ -1010,10 +1010,16 @@ int32_t attention_scratch_address(void** out)
     int dev = -1;
     NHIP_CHECK_HIP(hipGetDevice(&dev));
     NHIP_REQUIRE(dev >= 0 && dev < kMaxScratchDevices, "device %d above %d", dev, kMaxScratchDevices);
-    if (!g_scratch[dev]) {
-        int32_t rc = attention_scratch_setup();
-        if (rc) return rc;
+    {
+        std::lock_guard<std::mutex> lock(g_scratch_mutex);
+        if (g_scratch[dev]) {
+            *out = g_scratch[dev];
+            return NHIP_OK;
+        }
     }
+    int32_t rc = attention_scratch_setup();  // takes the mutex itself
+    if (rc) return rc;
+    std::lock_guard<std::mutex> lock(g_scratch_mutex);
     *out = g_scratch[dev];
     return NHIP_OK;
 }

@@ -1512,7 +1512,8 @@ int32_t nhip_decoder_greedy(nhip_decoder* m, const int32_t* prompt, int32_t prom
     NHIP_REQUIRE(prompt_len + max_new <= D.capacity, "prompt + new tokens exceed the capacity %d", D.capacity);
     using clock = std::chrono::steady_clock;
     const auto t0 = clock::now();
-    m->slot_len[0] = 0;
+    m->slot_len[0] = 0;  // slot 0 starts over, as nhip_decoder_slot_reset leaves it
+    m->slot_mark[0] = 0;
     std::vector<int32_t> sl(std::min(prompt_len, D.max_rows), 0);
     int32_t next = 0;
     for (int start = 0; start < prompt_len; start += D.max_rows) {

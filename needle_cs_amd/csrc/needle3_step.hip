@@ -1094,6 +1094,25 @@ struct RecordCursor {
         }
         return nhip_model_dense(m, i);
     }
+
+    // A dense record of `first` or `second` elements, of which the engine
+    // reads the first `first` (D1 and D4 are stored MLP-width in Needle 3
+    // archives, tools/golden.py:186-195, and read over the hidden width,
+    // Blocks.cs:1135 ScaleInput and :1216 AccumulateOutput).
+    const float* dense_either(size_t first, size_t second, const char* what)
+    {
+        const int i = take(NHIP_CACT_FP16, NHIP_CACT_FP32, what);
+        if (i < 0) return nullptr;
+        const nhip_record_info r = info(i);
+        size_t n = 1;
+        for (int d = 0; d < r.ndim; d++) n *= r.shape[d];
+        if (n != first && n != second) {
+            set_error("record %d (%s): %zu elements, expected %zu or %zu", i, what, n, first, second);
+            status = NHIP_ERR_FORMAT;
+            return nullptr;
+        }
+        return nhip_model_dense(m, i);
+    }
 };
 
 int32_t load_model(nhip_ctx* c)
@@ -1141,6 +1160,11 @@ int32_t load_model(nhip_ctx* c)
                  "heads %d / kv %d (heads * 64 a multiple of 128 up to 1024)", c->heads, c->kv);
     NHIP_REQUIRE(c->site_count >= 0 && c->site_count <= 16 && c->order_count >= 0 && c->order_count <= 4,
                  "engram sites %d, orders %d", c->site_count, c->order_count);
+    // EngramHashRowsBatch reads an n-gram's tokens from the run and the slot's
+    // two carried tokens, so orders run 1..3; every site needs an order.
+    NHIP_REQUIRE(c->site_count == 0 || c->order_count >= 1, "engram sites %d with no n-gram orders", c->site_count);
+    for (int o = 0; o < c->order_count; o++)
+        NHIP_REQUIRE(c->orders[o] >= 1 && c->orders[o] <= 3, "engram order %d is %d (1..3)", o, c->orders[o]);
     NHIP_REQUIRE(c->site_count == 0 || (c->engram_tables % std::max(c->order_count, 1) == 0 &&
                                        c->engram_tables * c->engram_sub == c->dim && c->engram_sub % 128 == 0 &&
                                        c->engram_slots > 0 && c->dilation >= 1 && 3 * c->dilation <= kEngramHistory),
@@ -1185,11 +1209,11 @@ int32_t load_model(nhip_ctx* c)
             w.attn_gate = 1.0f / (1.0f + std::exp(-x));
         }
         w.pre_hada = r.dense(d, "PreHada");
-        w.d1 = r.dense(d, "D1");
+        w.d1 = r.dense_either(d, width, "D1");
         w.d2 = r.dense(width, "D2");
         w.b2 = r.dense(width, "B2");
         w.d3 = r.dense(width, "D3");
-        w.d4 = r.dense(d, "D4");
+        w.d4 = r.dense_either(d, width, "D4");
         w.w1a = r.dense((size_t)c->hada_rows * c->hada_rows, "W1A");
         w.w1b = r.dense((size_t)c->hada_cols * c->hada_cols, "W1B");
         w.w2a = r.dense((size_t)c->hada_rows * c->hada_rows, "W2A");

@@ -97,7 +97,12 @@ class BatchedEngine:
         ids and log-probabilities [heads][k], Ops.ArgMax ids [heads] (or None)."""
         t = np.ascontiguousarray(tokens, dtype=np.int32).reshape(-1)
         s = np.ascontiguousarray(row_slots, dtype=np.int32).reshape(-1)
-        hr = np.ascontiguousarray(head_rows, dtype=np.int32).reshape(-1)
+        if len(s) != len(t):
+            raise ValueError(f"{len(t)} tokens but {len(s)} row slots")
+        hr_in = np.asarray(head_rows).reshape(-1)
+        if hr_in.size and not np.issubdtype(hr_in.dtype, np.integer):
+            raise ValueError("head_rows must be integers")
+        hr = np.ascontiguousarray(hr_in, dtype=np.int32)
         heads = len(hr)
         lg = np.zeros((heads, self.vocab_size), dtype=np.float32) if logits else None
         idx = np.zeros((max(heads, 1), max(k, 1)), dtype=np.int32)

@@ -18,7 +18,7 @@ OUT = os.path.join(HERE, "_build")
 LIB = os.path.join(OUT, "libneedle_oracle.so")
 SOURCES = ["needle_oracle.c", "cpu_baseline.c", "cpu_simd.c", "decoder.c", "needle3_model.c"]
 FLAGS = ["-O2", "-std=c11", "-fPIC", "-shared", "-ffp-contract=off", "-fno-fast-math", "-mavx2",
-         "-Wall", "-Wextra", "-pthread"]
+         "-Wall", "-Wextra", "-pthread", "-fopenmp"]
 
 
 def build() -> str:

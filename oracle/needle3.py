@@ -122,14 +122,20 @@ class OracleEngine:
         assert orc.lib().or_n3_init(C.byref(self.e)) == 0
         self.vocab = om.dims.vocab
 
-    def step(self, tokens, row_slots, head_rows):
+    def step(self, tokens, row_slots, head_rows, trace=False):
+        """Logits [heads][vocab] of the head rows; with trace=True also the
+        stream [layers + 1][rows][4][dim] after the embedding and each layer."""
         t = np.ascontiguousarray(tokens, dtype=np.int32)
         s = np.ascontiguousarray(row_slots, dtype=np.int32)
         h = np.ascontiguousarray(head_rows, dtype=np.int32).reshape(-1)
         lg = np.zeros((len(h), self.vocab), dtype=np.float32)
+        g = self.om.dims
+        states = np.zeros((g.layers + 1, len(t), 4, g.dim), dtype=np.float32) if trace else None
+        self.e.trace = states.ctypes.data if trace else None
         self.orc.lib().or_n3_forward(C.byref(self.e), self.orc.p(t), self.orc.p(s), len(t),
                                      self.orc.p(h) if len(h) else None, len(h), self.orc.p(lg) if len(h) else None)
-        return lg
+        self.e.trace = None
+        return (lg, states) if trace else lg
 
     def reset(self, slot):
         self.orc.lib().or_n3_reset(C.byref(self.e), slot)

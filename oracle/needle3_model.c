@@ -355,6 +355,12 @@ void or_n3_rewind(or_n3_engine* e, int slot)
     e->length[slot] = e->marked[slot];
 }
 
+/* Threads of or_n3_forward's matmuls, attention rows and MLP rows (1 by
+ * default).  Every output element is still computed by one thread in the
+ * scalar order, so the results do not depend on the count. */
+static int n3_threads = 1;
+void or_n3_set_threads(int n) { n3_threads = n > 0 ? n : 1; }
+
 static void matmul(const or_cq* w, int row0, int rows, const float* x, int tokens, float* y, int ldy, int bits)
 {
     int cols = w->cols, groups = cols / 128, stride = (groups + 7) / 8 * 8;
@@ -370,11 +376,24 @@ static void matmul(const or_cq* w, int row0, int rows, const float* x, int token
     slice.indices = w->indices + (size_t)row0 * cols * w->bits / 8;
     slice.norms = w->norms + (size_t)row0 * groups;
     slice.rows = rows;
-    or_matmul_rows(&slice, &a, tokens, y, ldy, 0, rows);
+    int blocks = rows < 64 * n3_threads ? 1 : n3_threads;
+#pragma omp parallel for num_threads(blocks) schedule(static)
+    for (int b = 0; b < blocks; b++)
+        or_matmul_rows(&slice, &a, tokens, y, ldy, (int)((long)rows * b / blocks), (int)((long)rows * (b + 1) / blocks));
     free(a.values);
     free(a.scales);
     free(a.offsets);
 }
+
+/* Planted composition mistakes, the controls of the tests that hold this
+ * forward to the reference's own numpy forward (0, the default: none):
+ *   1  hpre's +4 lane bias on lane (l + 1) % 4 instead of l % 4
+ *   2  every engram site applied one layer late
+ *   3  the MLP run before PostNormAdd instead of after it
+ *   4  the Sinkhorn mix applied transposed
+ *   5  PostNorm and PreHada exchanged (each layer's records read one slot off) */
+static int plant;
+void or_n3_set_plant(int which) { plant = which; }
 
 void or_n3_forward(or_n3_engine* e, const int* tokens, const int* row_slots, int rows, const int* head_rows,
                    int heads, float* logits)
@@ -424,9 +443,10 @@ void or_n3_forward(or_n3_engine* e, const int* tokens, const int* row_slots, int
         for (int i = 0; i < dim; i++) buf[i] += emb_scale * buf[i];
         for (int lane = 0; lane < N3_LANES; lane++) memcpy(stream + (size_t)t * sw + lane * dim, buf, sizeof(float) * dim);
     }
+    if (e->trace) memcpy(e->trace, stream, sizeof(float) * (size_t)rows * sw);
     for (int l = 0; l < g->layers; l++) {
         const or_n3_layer* w = &m->layer[l];
-        int lane = l % N3_LANES;
+        int lane = l % N3_LANES, bias_lane = plant == 1 ? (l + 1) % N3_LANES : lane;
         /* hyper-connection phi (RunLayerBatch, Engine.cs:2356-2364) */
         for (int t = 0; t < rows; t++) or_rms_fake_a8(stream + (size_t)t * sw, sw, normed + (size_t)t * sw);
         matmul(&m->phi_pre, l * 4, 4, normed, rows, pre_out, 4, 4);
@@ -435,19 +455,26 @@ void or_n3_forward(or_n3_engine* e, const int* tokens, const int* row_slots, int
         for (int t = 0; t < rows; t++) {
             float hpre[4], logits_mix[16];
             for (int i = 0; i < 4; i++) {
-                hpre[i] = or_sigmoid(m->a_pre[l] * pre_out[t * 4 + i] + m->b_pre[l * 4 + i] + (i == lane ? 4.0f : -4.0f));
+                hpre[i] = or_sigmoid(m->a_pre[l] * pre_out[t * 4 + i] + m->b_pre[l * 4 + i] + (i == bias_lane ? 4.0f : -4.0f));
                 post_gate[t * 4 + i] =
                     2.0f * or_sigmoid(m->a_post[l] * post_out[t * 4 + i] + m->b_post[l * 4 + i] + (i == lane ? 0.0f : -4.0f));
             }
             or_mix4(stream + (size_t)t * sw, dim, hpre[0], hpre[1], hpre[2], hpre[3], input + (size_t)t * dim);
             for (int i = 0; i < 16; i++) logits_mix[i] = m->a_res[l] * res_out[t * 16 + i] + m->b_res[l * 16 + i];
             or_sinkhorn4x4(logits_mix, mix + t * 16);
+            if (plant == 4)
+                for (int i = 0; i < 4; i++)
+                    for (int j = i + 1; j < 4; j++) {
+                        float a = mix[t * 16 + i * 4 + j];
+                        mix[t * 16 + i * 4 + j] = mix[t * 16 + j * 4 + i];
+                        mix[t * 16 + j * 4 + i] = a;
+                    }
             memcpy(residual + (size_t)t * dim, input + (size_t)t * dim, sizeof(float) * dim);
         }
         /* engram (ApplyEngramBatch, Engine.cs:2399-2463) */
         int site = -1;
         for (int s = 0; s < g->site_count; s++)
-            if (g->sites[s] == l) site = s;
+            if (g->sites[s] + (plant == 2) == l) site = s;
         if (site >= 0) {
             const or_n3_site* S = &m->site[site];
             int sub = g->engram_sub, stride = N3_ENGRAM_HISTORY + 1;
@@ -508,16 +535,24 @@ void or_n3_forward(or_n3_engine* e, const int* tokens, const int* row_slots, int
             first[t] = window == 0 ? 0 : (pos[t] - window + 1 > 0 ? pos[t] - window + 1 : 0);
             count[t] = pos[t] - first[t] + 1;
         }
-        or_attention_decode(q8, qs, rows, H, KV, qk, e->keys + lcell * kw, e->key_scales + lcell * KV,
-                            e->values + lcell * vw, e->value_scales + lcell * KV, e->capacity, row_slots, first, count,
-                            e->max_chunks, att);
+#pragma omp parallel for num_threads(n3_threads) schedule(dynamic, 1)
+        for (int t = 0; t < rows; t++)
+            or_attention_decode(q8 + (size_t)t * qw, qs + (size_t)t * H, 1, H, KV, qk, e->keys + lcell * kw,
+                                e->key_scales + lcell * KV, e->values + lcell * vw, e->value_scales + lcell * KV,
+                                e->capacity, row_slots + t, first + t, count + t, e->max_chunks, att + (size_t)t * ow);
         for (int t = 0; t < rows; t++) or_gate_fake_a8(att + (size_t)t * ow, gate + (size_t)t * ow, ow);
         matmul(&w->out, 0, dim, att, rows, proj, dim, 2);
+        const float* post_norm = plant == 5 ? w->pre_hada : w->post_norm;
+        const float* pre_hada = plant == 5 ? w->post_norm : w->pre_hada;
+        for (int t = 0; t < rows && plant == 3; t++)
+            or_hadamard_mlp(&w->mlp, pre_hada, m->perm_a, m->perm_b, dim, g->hada_rows, g->hada_cols,
+                            residual + (size_t)t * dim);
         for (int t = 0; t < rows; t++)
-            or_post_norm_add(residual + (size_t)t * dim, proj + (size_t)t * dim, w->post_norm, w->attn_gate, dim);
+            or_post_norm_add(residual + (size_t)t * dim, proj + (size_t)t * dim, post_norm, w->attn_gate, dim);
         /* Kronecker-Hadamard MLP (RunMlp) */
-        for (int t = 0; t < rows; t++)
-            or_hadamard_mlp(&w->mlp, w->pre_hada, m->perm_a, m->perm_b, dim, g->hada_rows, g->hada_cols,
+#pragma omp parallel for num_threads(n3_threads) schedule(static)
+        for (int t = 0; t < (plant != 3 ? rows : 0); t++)
+            or_hadamard_mlp(&w->mlp, pre_hada, m->perm_a, m->perm_b, dim, g->hada_rows, g->hada_cols,
                             residual + (size_t)t * dim);
         /* the four lanes of the next stream */
         for (int t = 0; t < rows; t++)
@@ -526,6 +561,7 @@ void or_n3_forward(or_n3_engine* e, const int* tokens, const int* row_slots, int
         float* swap = stream;
         stream = next;
         next = swap;
+        if (e->trace) memcpy(e->trace + (size_t)(l + 1) * rows * sw, stream, sizeof(float) * (size_t)rows * sw);
     }
     /* the slots' lengths and previous tokens (ForwardBatch, Engine.cs:2326-2340) */
     for (int rs = 0; rs < rows;) {

@@ -385,6 +385,10 @@ typedef struct or_n3_engine {
     float* engram_hist;                                /* [sites][slots][9][dim] */
     float *snap_qkv, *snap_engram;
     int *length, *marked, *prev, *snap_prev;
+    /* optional: when set, or_n3_forward copies the stream [rows][4][dim]
+     * after the embedding to trace[0] and after layer l to trace[l + 1]
+     * (the states tools/golden.py:253-267 dumps as x0 and streamNN) */
+    float* trace;
 } or_n3_engine;
 
 /* HadamardMlp.Apply (Blocks.cs:1067-1101), scalar kernels, Scale 1 */
@@ -404,6 +408,10 @@ void or_n3_rewind(or_n3_engine* e, int slot);
  * the head rows. */
 void or_n3_forward(or_n3_engine* e, const int* tokens, const int* row_slots, int rows, const int* head_rows,
                    int heads, float* logits);
+/* A planted composition mistake for the tests' controls (0: none). */
+void or_n3_set_plant(int which);
+/* Threads of or_n3_forward's row-parallel loops (results do not depend on it). */
+void or_n3_set_threads(int n);
 
 #ifdef __cplusplus
 }

@@ -98,7 +98,7 @@ _N3.Engine._fields_ = [("m", C.POINTER(_N3.Model)), ("slots", C.c_int), ("capaci
                                                   "value_scales", "qkv_hist", "engram_hist", "snap_qkv",
                                                   "snap_engram")] + \
                       [("length", C.POINTER(C.c_int)), ("marked", C.POINTER(C.c_int)), ("prev", C.POINTER(C.c_int)),
-                       ("snap_prev", C.POINTER(C.c_int))]
+                       ("snap_prev", C.POINTER(C.c_int)), ("trace", C.c_void_p)]
 N3 = _N3
 
 _u64p, _vp, _i, _f, _sz = C.POINTER(C.c_uint64), C.c_void_p, C.c_int, C.c_float, C.c_size_t
@@ -191,6 +191,8 @@ _PROTOS = {
     "or_n3_mark": (None, [C.POINTER(_N3.Engine), _i]),
     "or_n3_rewind": (None, [C.POINTER(_N3.Engine), _i]),
     "or_n3_forward": (None, [C.POINTER(_N3.Engine), _vp, _vp, _i, _vp, _i, _vp]),
+    "or_n3_set_plant": (None, [_i]),
+    "or_n3_set_threads": (None, [_i]),
     "or_simd_matmul_i8": (None, [_i, _vp, _vp, _i, _i, _vp, _vp, _i, _vp, _i, _i, _i]),
     "or_baseline_simd_matmul_i8": (None, [_i, _vp, _vp, _i, _i, _vp, _vp, _i, _vp, _i, _i, _i]),
 }

@@ -155,3 +155,33 @@ def test_replacing_weights_after_graph_capture(hip, orc):
     assert np.array_equal(tg, tc) and np.float32(sg) == np.float32(sc)
     gpu.close()
     cpu.close()
+
+
+def test_config4_beam3_decode_loop_as_specified(hip, orc):
+    """The benchmark decode loop as specified: 12 layers, d_model 1024, 16
+    heads x 64, SwiGLU 4096, vocab 32000, int8 g32 linears, a 128-token
+    prompt, beam width 3, 64 new tokens (Whistle.BeamSearch,
+    src/Needle/Whistle.Decode.cs:226-350) - the same model, prompt and search
+    bench.py times.  Token stream and score identical to the oracle's scalar
+    order; then 64 greedy tokens from the same prompt (Engine.Greedy)."""
+    from needle_cs_amd.decoder import CONFIG4
+    assert CONFIG4["layers"] == 12 and CONFIG4["d"] == 1024 and CONFIG4["vocab"] == 32000
+    print("config 4: model", flush=True)
+    model = synthetic_model(CONFIG4, 0x5005)
+    prompt = random_prompt(0x6006, 128, CONFIG4["vocab"])
+    gpu = GpuDecoder(model, slots=3, capacity=256, max_rows=128)
+    cpu = orc.CpuDecoder(model, slots=3, capacity=256, threads=16)
+    try:
+        print("config 4: beam search", flush=True)
+        tg, sg, stats = gpu.beam_search(prompt, 3, 64, 1)
+        tc, sc, fed = cpu.beam_search(prompt, 3, 64, 1)
+        assert len(tg) == 64
+        assert np.array_equal(tg, tc) and np.float32(sg) == np.float32(sc)
+        assert stats.fed_rows == fed
+        print("config 4: greedy", flush=True)
+        g1, gs = gpu.greedy(prompt, 64)
+        c1 = cpu.greedy(prompt, 64)
+        assert len(g1) == 64 and np.array_equal(g1, c1) and gs.steps == 64
+    finally:
+        gpu.close()
+        cpu.close()

@@ -260,3 +260,46 @@ def test_needle3_geometry_matches_the_oracle(hip, orc):
             assert same_bits(lg, want), f"decode step {step}"
             assert np.array_equal(am, np.argmax(want, axis=1))
     o.close()
+
+
+def test_needle3_window_past_1024_positions(hip, orc):
+    """Needle 3's geometry with the cache past its 1024-position window
+    (windowed layers attend max(0, pos - 1023)..pos, Blocks.cs:973-978;
+    global layers every position, Model.cs:89-90): 1088 prompt tokens fed in
+    128-row chunks, then 12 decode steps to position 1099.  Every decode
+    step's logits equal the oracle's bit for bit, and the last one meets the
+    reference's own numpy forward (tools/golden.py, the `window` vectors of
+    tests/golden/needle3_golden.npz) at cosine >= 0.9995 with the same argmax."""
+    import hashlib
+    import os
+
+    from needle_cs_amd.engine import BatchedEngine, Model
+    fix = np.load(os.path.join(os.path.dirname(__file__), "golden", "needle3_golden.npz"))
+    archive = M.write_archive(M.NEEDLE3, int(fix["window_seed"]))
+    assert hashlib.sha256(archive).hexdigest() == str(fix["window_sha256"])
+    toks = np.ascontiguousarray(fix["window_tokens"], dtype=np.int32)
+    prompt, cap, chunks = 1088, 1152, 64
+    orc.lib().or_n3_set_threads(min(16, os.cpu_count() or 1))
+    om = M.OracleModel(orc, archive)
+    o = M.OracleEngine(orc, om, slots=1, capacity=cap, max_chunks=chunks)
+    try:
+        with Model(archive) as model, BatchedEngine(model, context_length=cap, chunk_size=128, slots=1,
+                                                    max_chunks=chunks) as g:
+            print("needle3 window: GPU prefill of 1088 tokens", flush=True)
+            g.feed_slot(0, toks[:prompt], compute_logits=False)
+            for s in range(0, prompt, 128):
+                part = toks[s:min(s + 128, prompt)]
+                o.step(part, [0] * len(part), [])
+                print(f"needle3 window: oracle prefill {s + len(part)}/{prompt}", flush=True)
+            for pos in range(prompt, len(toks)):
+                lg, _, _, _ = g.forward_batch(toks[pos:pos + 1], [0], [0])
+                want = o.step(toks[pos:pos + 1], [0], [0])
+                assert same_bits(lg, want), f"position {pos}"
+            assert g.slot_length(0) == len(toks)
+        ref = fix["window_logits"].astype(np.float64)
+        last = lg[0].astype(np.float64)
+        assert int(np.argmax(last)) == int(np.argmax(ref))
+        assert last @ ref / np.linalg.norm(last) / np.linalg.norm(ref) >= 0.9995
+    finally:
+        o.close()
+        orc.lib().or_n3_set_threads(1)
