@@ -121,9 +121,15 @@ struct DeviceWeights {
     float byte_scale;     // codebook ByteScale (1 for the literal format)
     uint8_t* tiles;
     uint16_t* norms;
+    // literal int8 matrices of at most kNarrowMaxRows rows: the weights again
+    // in their row-major [rows][cols] order, for the narrow decode kernel
+    // (narrow.hip), which gives a workgroup 4 or 8 whole rows
+    uint8_t* rowmajor;
     size_t device_bytes;
     int32_t special_scales;  // some scale has binary16 exponent 31 (inf/NaN patterns)
 };
+
+constexpr int kNarrowMaxRows = 4096;
 
 }  // namespace nhip
 
@@ -170,6 +176,17 @@ struct DecodePrologue {
 };
 int32_t launch_decode_fused(const DeviceWeights* w, const DecodePrologue& f, int32_t tokens, float* y, int32_t ldy,
                             hipStream_t stream);
+// The narrow decode matmul (narrow.hip) over rows [row_start, row_end):
+// kind 0 takes int8 rows `in` [tokens][cols] with scales qscale, kProNorm /
+// kProQuant compute them from fp32 rows as launch_decode_fused does (delta,
+// gain, x_out, eps as in DecodePrologue); with `residual` it stores
+// residual + y.  Returns 1 (nothing launched) for weights or shapes it does
+// not take: no row-major copy, exponent-31 scales, more than 4 tokens, K not
+// a multiple of 1024 or above 4096.
+int32_t launch_i8_narrow(const DeviceWeights* w, int32_t kind, const void* in, const float* delta,
+                         const float* gain, const float* qscale, float* x_out, float eps, const float* residual,
+                         int32_t tokens, float* y, int32_t ldy, int32_t row_start, int32_t row_end,
+                         hipStream_t stream);
 // The decode matmul of int8 rows q restricted to the 16-row tiles holding a
 // row set in some token's mask ([tokens][mask_words] bitsets, bit id%32 of
 // word id/32); the other outputs are left untouched (Engine.LogitsForRows'

@@ -1740,6 +1740,11 @@ int32_t run_matmul(const DeviceWeights* w, const int8_t* q, const float* scales,
     if (w->format == WeightFormat::Int8G32) {
         if (!dots && tokens >= kGemmMinTokens)
             return launch_gemm_i8(w, q, scales, tokens, y, ldy, row_start, row_end, true, stream);
+        if (!dots) {
+            const int32_t nrc = launch_i8_narrow(w, 0, q, nullptr, nullptr, scales, nullptr, 0.0f, nullptr, tokens,
+                                                 y, ldy, row_start, row_end, stream);
+            if (nrc <= 0) return nrc;
+        }
         const int32_t drc = try_i8_decode(w, p, stream);
         if (drc <= 0) return drc;
         // LDS per phase: staged operands gph*32*m + products m*16*ldd*4 + a
@@ -2052,6 +2057,21 @@ int32_t create_weights(WeightFormat fmt, const uint8_t* d_src, const uint16_t* d
         return NHIP_ERR_HIP;
     }
     w->special_scales = special;
+    if (fmt == WeightFormat::Int8G32 && rows <= kNarrowMaxRows) {
+        // the narrow decode kernel's row-major copy (narrow.hip)
+        e = hipMalloc(&w->rowmajor, (size_t)rows * cols);
+        if (e == hipSuccess) e = hipMemcpyAsync(w->rowmajor, d_src, (size_t)rows * cols, hipMemcpyDeviceToDevice, s);
+        if (e == hipSuccess) e = hipStreamSynchronize(s);
+        if (e != hipSuccess) {
+            set_error("row-major weight copy failed: %s", hipGetErrorString(e));
+            (void)hipFree(w->rowmajor);
+            (void)hipFree(w->tiles);
+            (void)hipFree(w->norms);
+            delete w;
+            return NHIP_ERR_HIP;
+        }
+        w->device_bytes += (size_t)rows * cols;
+    }
     *out = w;
     return NHIP_OK;
 }
@@ -2137,6 +2157,11 @@ int32_t launch_decode_fused(const DeviceWeights* w, const DecodePrologue& f, int
                  "too small", ldy);
     NHIP_REQUIRE(!f.swiglu || w->rows % 16 == 0, "fused matmul: SwiGLU pairs need whole 16-row tiles");
     if (tokens < 1 || tokens > 4 || w->special_scales) return 1;
+    if (!f.swiglu) {
+        const int32_t nrc = launch_i8_narrow(w, f.kind, f.x, f.delta, f.gain, nullptr, f.x_out, f.eps, f.residual,
+                                             tokens, y, ldy, 0, w->rows, stream);
+        if (nrc <= 0) return nrc;
+    }
     const int K = w->cols;
     // waves: 4, or 8 when the (non-norm) prologue needs more threads; CB in
     // {2, 4, 8} dividing the tile's blocks with at most `waves` waves busy
@@ -2271,6 +2296,7 @@ int32_t nhip_weights_destroy(nhip_weights* w)
     if (!w) return NHIP_OK;
     (void)hipFree(w->tiles);
     (void)hipFree(w->norms);
+    (void)hipFree(w->rowmajor);
     delete w;
     return NHIP_OK;
 }

@@ -440,3 +440,25 @@ def test_copy_dev(hip, nbytes, off):
     want = np.zeros(nbytes + 32, dtype=np.uint8)
     want[off:off + nbytes] = src[off:off + nbytes]
     assert np.array_equal(got, want)
+
+
+@pytest.mark.parametrize("tokens", [1, 2, 3, 4])
+@pytest.mark.parametrize("rows,cols,r0,r1", [
+    (1024, 4096, 0, 1024),   # the decoder's down matmul: 4-row workgroups, K = 4096
+    (1000, 1024, 0, 1000),   # 4-row workgroups, rows not a multiple of 4
+    (2048, 2048, 5, 1999),   # a row range cutting workgroups at both ends
+    (3000, 2048, 0, 3000),   # 8-row workgroups, ragged last workgroup
+    (4096, 1024, 1234, 4001),
+    (3072, 4096, 0, 3072),
+])
+def test_int8_narrow_decode_bit_exact(hip, orc, tokens, rows, cols, r0, r1):
+    """Matrices of at most 4096 rows with K a multiple of 1024 and at most 4
+    tokens take the narrow kernel (4 or 8 whole rows per workgroup, from the
+    row-major copy): bit-exact with the oracle, rows outside [r0, r1)
+    untouched."""
+    w, scales, x, q, qs = int8_case(orc, 31 * tokens + rows + 7 * cols, rows, cols, tokens)
+    weights = hip.Weights.int8(w, scales)
+    y = run_i8(hip, weights, q, qs, tokens, rows + 3, r0, r1)
+    want = np.full((tokens, rows + 3), SENTINEL, dtype=np.float32)
+    orc.matmul_rows_i8(w, scales, q, qs, tokens, want, rows + 3, r0, r1)
+    assert np.array_equal(y.view(np.uint32), want.view(np.uint32))
