@@ -472,9 +472,10 @@ def needle3_loop(args, threads: int) -> dict:
     vocab 8192) through the step API: a 64-token prompt per slot (63 fed with
     FeedSlot, the last in the first 3-row step), then 63 decode steps of 3
     rows with the head's ArgMax as the next tokens.  The CPU leg runs the
-    oracle's scalar engine (one thread) on the same prompts for a bounded
-    number of steps: its tokens must match the GPU's, its step time is the
-    port baseline."""
+    oracle's scalar engine on the same prompts for a bounded number of steps,
+    its matmul rows, attention rows and MLP rows spread over `threads` host
+    threads (each output is still one thread's scalar-order sum): its tokens
+    must match the GPU's, its step time is the port baseline."""
     from needle_cs_amd.archive import NEEDLE3, needle3_archive
     from needle_cs_amd.engine import BatchedEngine, Model
 
@@ -539,7 +540,9 @@ def needle3_loop(args, threads: int) -> dict:
         from oracle import needle3 as M
         from oracle import oracle as O
 
-        check_steps = 6
+        check_steps = 12
+        O.lib().or_n3_set_threads(threads)
+        O.lib().or_n3_set_tier(1)  # the engine's row order: the AVX2 tier's sums
         cpu = M.OracleEngine(O, M.OracleModel(O, archive), slots=slots, capacity=prompt_len + new, max_chunks=8)
         for s in range(slots):
             cpu.step(prompts[s, :-1], [s] * (prompt_len - 1), [])
@@ -551,12 +554,16 @@ def needle3_loop(args, threads: int) -> dict:
             ctoks.append(np.argmax(lg, axis=1))
         cdec = time.perf_counter() - t0
         cpu.close()
+        O.lib().or_n3_set_threads(1)
+        O.lib().or_n3_set_tier(0)
         ctoks = np.stack(ctoks, 1)
         out["tokens_identical_to_cpu_path"] = bool(np.array_equal(ctoks, toks[:, :check_steps + 1]))
-        out["cpu_path"] = {"row_tokens_per_s": round(slots * check_steps / cdec, 2), "threads": 1, "kind": "port",
-                           "sample": f"the oracle's scalar Needle 3 engine (oracle/needle3_model.c, one thread) on "
-                                     f"the same prompts, {check_steps} decode steps of 3 rows after the prefill; "
-                                     f"tokens compared over those {check_steps + 1} per slot"}
+        out["cpu_path"] = {"row_tokens_per_s": round(slots * check_steps / cdec, 2),
+                           "ms_per_step": round(cdec / check_steps * 1e3, 2), "threads": threads, "kind": "port",
+                           "sample": f"the oracle's scalar Needle 3 engine (oracle/needle3_model.c) on the same "
+                                     f"prompts, matmul, attention and MLP rows over {threads} threads, "
+                                     f"{check_steps} decode steps of 3 rows after the prefill; tokens compared over "
+                                     f"those {check_steps + 1} per slot"}
         out["speedup_vs_cpu_path"] = round(out["row_tokens_per_s"] / out["cpu_path"]["row_tokens_per_s"], 1)
         print(f"# needle3 CPU path: {out['cpu_path']['row_tokens_per_s']} row-tokens/s; identical tokens: "
               f"{out['tokens_identical_to_cpu_path']}", file=sys.stderr, flush=True)

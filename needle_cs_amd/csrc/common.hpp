@@ -64,44 +64,6 @@ inline uint64_t head_pair(int32_t lo, int32_t hi) { return (uint64_t)(uint32_t)l
 __device__ __forceinline__ int32_t head_lo(uint64_t v) { return (int32_t)(uint32_t)v; }
 __device__ __forceinline__ int32_t head_hi(uint64_t v) { return (int32_t)(uint32_t)(v >> 32); }
 
-// ------------------------------------------------- ordered LDS chains --
-
-// Sequential sums over LDS (the reference's scalar order: one lane adds one
-// value after another) are bound by the dependent adds only if the reads run
-// ahead of them.  Given plain loads, the compiler moved each batch's reads to
-// the top of its own loop iteration, exposing the LDS latency once per batch.
-// These read batches with inline ds_read_b128 and wait with an s_waitcnt
-// that takes the batch's registers as operands, so no use of them is placed
-// before the wait; LDS reads complete in order, so lgkmcnt(n) with n reads
-// issued after a batch means that batch has landed.
-typedef float chain4 __attribute__((ext_vector_type(4)));
-
-__device__ __forceinline__ uint32_t lds_address(const void* p)
-{
-    return (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const void*)p;
-}
-
-// eight 16-byte reads at base + off, base + off + 16, ...
-#define CHAIN_READ8(x, base, off)                                                                                  \
-    asm volatile("ds_read_b128 %0, %8 offset:" #off "\n\tds_read_b128 %1, %8 offset:" #off "+16\n\t"                 \
-                 "ds_read_b128 %2, %8 offset:" #off "+32\n\tds_read_b128 %3, %8 offset:" #off "+48\n\t"                \
-                 "ds_read_b128 %4, %8 offset:" #off "+64\n\tds_read_b128 %5, %8 offset:" #off "+80\n\t"                \
-                 "ds_read_b128 %6, %8 offset:" #off "+96\n\tds_read_b128 %7, %8 offset:" #off "+112"                    \
-                 : "=v"(x[0]), "=v"(x[1]), "=v"(x[2]), "=v"(x[3]), "=v"(x[4]), "=v"(x[5]), "=v"(x[6]), "=v"(x[7]) \
-                 : "v"(base))
-#define CHAIN_WAIT(n, x)                                                                                           \
-    asm volatile("s_waitcnt lgkmcnt(" #n ")"                                                                       \
-                 : "+v"(x[0]), "+v"(x[1]), "+v"(x[2]), "+v"(x[3]), "+v"(x[4]), "+v"(x[5]), "+v"(x[6]), "+v"(x[7]))
-// four 16-byte reads at four addresses
-#define CHAIN_READ4(x, a0, a1, a2, a3)                                                                             \
-    asm volatile("ds_read_b128 %0, %4\n\tds_read_b128 %1, %5\n\tds_read_b128 %2, %6\n\tds_read_b128 %3, %7"          \
-                 : "=v"(x[0]), "=v"(x[1]), "=v"(x[2]), "=v"(x[3])                                                   \
-                 : "v"(a0), "v"(a1), "v"(a2), "v"(a3))
-#define CHAIN_WAIT4(n, x) asm volatile("s_waitcnt lgkmcnt(" #n ")" : "+v"(x[0]), "+v"(x[1]), "+v"(x[2]), "+v"(x[3]))
-#define CHAIN_WAIT44(n, x, y)                                                                                      \
-    asm volatile("s_waitcnt lgkmcnt(" #n ")"                                                                       \
-                 : "+v"(x[0]), "+v"(x[1]), "+v"(x[2]), "+v"(x[3]), "+v"(y[0]), "+v"(y[1]), "+v"(y[2]), "+v"(y[3]))
-
 // ------------------------------------------------------- device weights --
 
 enum class WeightFormat : int32_t { Int8G32 = 8, Cq2 = 2, Cq4 = 4 };
@@ -323,6 +285,54 @@ __device__ __forceinline__ float canonical_finish(const float* p, int lane)
     q = q + dpp_row_shl(q, 2);
     q = q + dpp_row_shl(q, 1);
     return q;
+}
+
+// Ops.SumOfSquares / Ops.Dot in the AVX2 tier's Vector256 order (Ops.cs:
+// 123-205; RmsStats / CenteredRmsStats, :513-630, sum the same way), by one
+// whole wave over LDS rows a and b (b = a for the squares): lane 8k + j
+// (k < 4, j < 8) is lane j of accumulator s_k and takes
+// fma(a[i], b[i], acc) for i = 32m + 8k + j, m ascending, over n & ~31; a
+// remaining 16-block goes to s0 and s1 (lanes 0-15) and an 8-block to s2
+// (lanes 16-23); the rest is a sequential FMA tail.  The total is
+// Vector256.Sum((s0 + s1) + (s2 + s3)) + tail with Vector256.Sum(v) =
+// ((v0 + v1) + (v2 + v3)) + ((v4 + v5) + (v6 + v7)) (.NET's Sum(lower) +
+// Sum(upper)).  Returns the total in every lane; call from wave-uniform code.
+__device__ __forceinline__ float wave_v256_sum(const float* a, const float* b, int n)
+{
+    const int lane = threadIdx.x & 63;
+    const int bulk = n & ~31;
+    float acc = 0.0f;
+    if (lane < 32) {
+        int i = lane;
+        for (; i + 7 * 32 < bulk; i += 8 * 32) {
+            float x[8], y[8];
+#pragma unroll
+            for (int u = 0; u < 8; u++) {
+                x[u] = a[i + 32 * u];
+                y[u] = b[i + 32 * u];
+            }
+#pragma unroll
+            for (int u = 0; u < 8; u++) acc = fmaf(x[u], y[u], acc);
+        }
+        for (; i < bulk; i += 32) acc = fmaf(a[i], b[i], acc);
+    }
+    int i = bulk;
+    if (i + 16 <= n) {
+        if (lane < 16) acc = fmaf(a[i + lane], b[i + lane], acc);
+        i += 16;
+    }
+    if (i + 8 <= n) {
+        if (lane >= 16 && lane < 24) acc = fmaf(a[i + lane - 16], b[i + lane - 16], acc);
+        i += 8;
+    }
+    float tail = 0.0f;
+    for (; i < n; i++) tail = fmaf(a[i], b[i], tail);
+    // lane j < 8: v_j = (s0_j + s1_j) + (s2_j + s3_j), then the pairwise tree
+    const float v = (acc + __shfl(acc, lane + 8)) + (__shfl(acc, lane + 16) + __shfl(acc, lane + 24));
+    const float p2 = v + __shfl(v, lane + 1);
+    const float p4 = p2 + __shfl(p2, lane + 2);
+    const float p8 = p4 + __shfl(p4, lane + 4);
+    return __shfl(p8, 0) + tail;
 }
 
 // Maximum over the 64 lanes of a wave (order-free), in every lane.

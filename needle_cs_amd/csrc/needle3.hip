@@ -6,16 +6,16 @@
 //
 // One wave per (row, head), one lane per element of the head (qk <= 64,
 // vd <= 64): the lane forms its convolution term, the wave's sum of squares
-// runs in the reference's ascending order from LDS, the rotation pairs lanes
+// runs in the AVX2 tier's Vector256 order (wave_v256_sum), the rotation pairs lanes
 // i and i + qk/2, and the int8 row is quantized with the head's absolute
 // maximum.  Rows of one slot with consecutive positions form a run: a row
 // takes its previous frames from the rows before it in the run and, for the
 // run's first rows, from the slot's history; a second launch then moves each
 // slot's history to the run's last two frames.  Precondition (as in
 // EngineCore.ForwardBatch's rows): the rows of a slot are one contiguous run
-// of consecutive positions.  The arithmetic is the
-// reference's scalar order (no contraction), so the outputs are bit-identical
-// with its row-by-row step.
+// of consecutive positions.  Apart from the sum of squares the arithmetic is
+// the reference's scalar order (no contraction), so the outputs are
+// bit-identical with the oracle's row-by-row step in the AVX2 row tier.
 #include "common.hpp"
 
 namespace nhip {
@@ -110,12 +110,10 @@ __global__ __launch_bounds__(64) void needle3_inputs_kernel(Needle3Params p)
         x = taps[c] * x2 + taps[W + c] * x1 + taps[2 * W + c] * x0;
     }
     if (part < 2) {
-        // ZeroCenteredRms: the sum of squares in ascending order
-        red[c] = x * x;
+        // ZeroCenteredRms, its sum of squares in the AVX2 tier's order
+        red[c] = x;
         __syncthreads();
-        float sum = 0.0f;
-#pragma unroll 8
-        for (int i = 0; i < n; i++) sum = sum + red[i];  // ascending; the reads issue 8 at a time
+        const float sum = wave_v256_sum(red, red, n);
         const float inverse = 1.0f / sqrtf(sum / (float)n + 1e-6f);
         const float* scale = part == 0 ? p.q_norm : p.k_norm;
         x = c < n ? (1.0f + scale[c]) * x * inverse : 0.0f;

@@ -66,51 +66,6 @@ __device__ __forceinline__ float clamp_q(float v)
 
 __device__ __forceinline__ int col_of(int q) { return (int)threadIdx.x + kThreads * q; }
 
-// The sequential sum ((0 + v[0]) + v[1]) + ... + v[n-1] of n floats in LDS,
-// run by one lane: the scalar reductions' order (Scalar.SumOfSquares /
-// Scalar.Dot with the products formed beforehand -- each product is rounded
-// before it is added, as in `sum += x[i] * y[i]` without contraction).  n is
-// a multiple of 64 and v is 16-byte aligned with kChainPad readable floats
-// past n.  The reads run one 32-float batch ahead of the dependent adds:
-// they are issued by inline ds_read_b128 (the compiler, given plain loads,
-// moved every batch's reads to the top of its own loop iteration and exposed
-// the LDS latency once per 64 adds), and an s_waitcnt that takes the batch's
-// registers as operands orders their use after the wait -- LDS reads return
-// in order, so lgkmcnt(8) means the older batch has landed.  Different
-// lanes may run different chains at once.
-constexpr int kChainPad = 32;
-
-__device__ __forceinline__ float chain_sum(const float* v, int n)
-{
-    const uint32_t base = lds_address(v);
-    float sum = 0.0f;
-    chain4 a[8], b[8];
-    CHAIN_READ8(a, base, 0);
-    for (int k = 0; k < (n >> 2); k += 16) {
-        const uint32_t at = base + (uint32_t)k * 16u;
-        CHAIN_READ8(b, at, 128);
-        CHAIN_WAIT(8, a);
-#pragma unroll
-        for (int j = 0; j < 8; j++) {
-            sum = sum + a[j].x;
-            sum = sum + a[j].y;
-            sum = sum + a[j].z;
-            sum = sum + a[j].w;
-        }
-        CHAIN_READ8(a, at, 256);  // the last round reads the padding
-        CHAIN_WAIT(8, b);
-#pragma unroll
-        for (int j = 0; j < 8; j++) {
-            sum = sum + b[j].x;
-            sum = sum + b[j].y;
-            sum = sum + b[j].z;
-            sum = sum + b[j].w;
-        }
-    }
-    CHAIN_WAIT(0, a);  // no read is left in flight
-    return sum;
-}
-
 // Ops.InverseRms of a sum of squares over n elements
 __device__ __forceinline__ float inverse_rms_of(float sum, int n) { return 1.0f / sqrtf(sum / (float)n + 1e-6f); }
 
@@ -161,27 +116,28 @@ __device__ __forceinline__ void prepare_row(const float* v, int cols, int bits, 
     }
 }
 
-// Sum of squares of an LDS row by one lane, as Ops.InverseRms needs it; the
-// squares go to sq first (all threads), then lane 0 chains them.
-__device__ __forceinline__ float row_inverse_rms(const float* x, float* sq, int n, float* slot)
+// Ops.InverseRms of an LDS row x[0..n) (written before the call and
+// synchronised), its sum of squares in the AVX2 tier's order by wave 0.
+__device__ __forceinline__ float row_inverse_rms(const float* x, int n, float* slot)
 {
-    for (int c = threadIdx.x; c < n; c += kThreads) sq[c] = x[c] * x[c];
-    __syncthreads();
-    if (threadIdx.x == 0) *slot = inverse_rms_of(chain_sum(sq, n), n);
+    if (threadIdx.x < 64) {
+        const float sum = wave_v256_sum(x, x, n);
+        if (threadIdx.x == 0) *slot = inverse_rms_of(sum, n);
+    }
     __syncthreads();
     return *slot;
 }
 
-// The same, with `beside()` run by the other threads while lane 0 chains.
+// The same, with `beside()` run by waves 1.. while wave 0 sums.
 template <typename F>
-__device__ __forceinline__ float row_inverse_rms_beside(const float* x, float* sq, int n, float* slot, F&& beside)
+__device__ __forceinline__ float row_inverse_rms_beside(const float* x, int n, float* slot, F&& beside)
 {
-    for (int c = threadIdx.x; c < n; c += kThreads) sq[c] = x[c] * x[c];
-    __syncthreads();
-    if (threadIdx.x == 0)
-        *slot = inverse_rms_of(chain_sum(sq, n), n);
-    else
+    if (threadIdx.x < 64) {
+        const float sum = wave_v256_sum(x, x, n);
+        if (threadIdx.x == 0) *slot = inverse_rms_of(sum, n);
+    } else {
         beside();
+    }
     __syncthreads();
     return *slot;
 }
@@ -223,7 +179,6 @@ __global__ __launch_bounds__(kThreads) void n3_embed_kernel(const uint8_t* raw, 
                                                             Act act, int stride)
 {
     __shared__ __align__(16) float s[kMaxStream];
-    __shared__ __align__(16) float sq[kMaxStream + kChainPad];
     __shared__ float red[kWaves];
     __shared__ float inv_s;
     const int t = blockIdx.x;
@@ -244,7 +199,7 @@ __global__ __launch_bounds__(kThreads) void n3_embed_kernel(const uint8_t* raw, 
     }
     __syncthreads();
     const int n = kLanes * dim;
-    const float inverse = row_inverse_rms(s, sq, n, &inv_s);
+    const float inverse = row_inverse_rms(s, n, &inv_s);
     for (int c = threadIdx.x; c < n; c += kThreads) s[c] = s[c] * inverse;
     __syncthreads();
     fake_row(s, n, red);
@@ -290,7 +245,7 @@ struct HyperArgs {
 __global__ __launch_bounds__(kThreads) void n3_hyper_kernel(HyperArgs a)
 {
     __shared__ __align__(16) float x[kMaxDim];
-    __shared__ __align__(16) float sq[kMaxDim + kChainPad];
+    __shared__ __align__(16) float sq[kMaxDim];
     __shared__ float hpre[4];
     __shared__ float red[kWaves];
     __shared__ float inv_s;
@@ -358,7 +313,7 @@ __global__ __launch_bounds__(kThreads) void n3_hyper_kernel(HyperArgs a)
         prepare_row(sq, dim, 2, a.act, a.stride, t);
         return;
     }
-    const float inverse = row_inverse_rms_beside(x, sq, dim, &inv_s, sinkhorn);
+    const float inverse = row_inverse_rms_beside(x, dim, &inv_s, sinkhorn);
 #pragma unroll
     for (int q = 0; q < kPer; q++) {
         const int c = col_of(q);
@@ -402,13 +357,12 @@ __device__ __forceinline__ const float* engram_frame(const EngramArgs& a, int t,
 // The engram's convolution, RmsUnit of the input and the key, their Dot,
 // alpha = Sigmoid(dot / sqrt(dim)) and residual += alpha * conv
 // (Engine.cs:2437-2462), then RunAttentionBatch's CenteredRmsFakeA8 of the
-// residual and its 2-bit Prepare.  Lanes 0 and 1 run the two sums of squares
-// at once.
+// residual and its 2-bit Prepare.  Waves 0 and 1 run the two sums of squares
+// at once; every sum is in the AVX2 tier's order.
 __global__ __launch_bounds__(kThreads) void n3_engram_mix_kernel(EngramArgs a)
 {
     __shared__ __align__(16) float ua[kMaxDim];
     __shared__ __align__(16) float ub[kMaxDim];
-    __shared__ __align__(16) float sq[2][kMaxDim + kChainPad];
     __shared__ float inv[2];
     __shared__ float red[kWaves];
     __shared__ float alpha_s;
@@ -444,17 +398,27 @@ __global__ __launch_bounds__(kThreads) void n3_engram_mix_kernel(EngramArgs a)
             cv[q] = o;
             ua[c] = xv[q];
             ub[c] = kv[q];
-            sq[0][c] = xv[q] * xv[q];
-            sq[1][c] = kv[q] * kv[q];
         }
     }
     __syncthreads();
-    if (threadIdx.x < 2) inv[threadIdx.x] = inverse_rms_of(chain_sum(sq[threadIdx.x], dim), dim);
+    // Ops.RmsUnit of the input (wave 0) and of the key (wave 1)
+    if (threadIdx.x < 128) {
+        const float* v = threadIdx.x < 64 ? ua : ub;
+        const float sum = wave_v256_sum(v, v, dim);
+        if ((threadIdx.x & 63) == 0) inv[threadIdx.x >> 6] = inverse_rms_of(sum, dim);
+    }
     __syncthreads();
     const float ia = inv[0], ib = inv[1];
-    for (int c = threadIdx.x; c < dim; c += kThreads) sq[0][c] = (ua[c] * ia) * (ub[c] * ib);
+    for (int c = threadIdx.x; c < dim; c += kThreads) {
+        ua[c] = ua[c] * ia;
+        ub[c] = ub[c] * ib;
+    }
     __syncthreads();
-    if (threadIdx.x == 0) alpha_s = sigmoid_poly(chain_sum(sq[0], dim) * a.inverse_root);
+    // alpha = Sigmoid(Ops.Dot(unitA, unitB) / sqrt(dim))
+    if (threadIdx.x < 64) {
+        const float dot = wave_v256_sum(ua, ub, dim);
+        if (threadIdx.x == 0) alpha_s = sigmoid_poly(dot * a.inverse_root);
+    }
     __syncthreads();
     const float alpha = alpha_s;
 #pragma unroll
@@ -467,7 +431,7 @@ __global__ __launch_bounds__(kThreads) void n3_engram_mix_kernel(EngramArgs a)
         }
     }
     __syncthreads();
-    const float inverse = row_inverse_rms(ua, sq[1], dim, &inv[0]);
+    const float inverse = row_inverse_rms(ua, dim, &inv[0]);
 #pragma unroll
     for (int q = 0; q < kPer; q++) {
         const int c = col_of(q);
@@ -598,8 +562,50 @@ struct TailArgs {
 size_t tail_lds_bytes(int dim, int rows, int cols)
 {
     const size_t width = (size_t)rows * cols;
-    return sizeof(float) * (3 * width + 32 + 2 * (size_t)dim + 8 * ((size_t)dim + 4) + kChainPad + 3 * (size_t)rows * rows +
-                            3 * (size_t)cols * cols + 2 * (size_t)kLanes * dim + kChainPad);
+    return sizeof(float) * (3 * width + 32 + 2 * (size_t)dim + 8 * (size_t)dim + 3 * (size_t)rows * rows +
+                            3 * (size_t)cols * cols + (size_t)kLanes * dim);
+}
+
+// HadamardMlp.ConditionWeights' Vector256 branch (Blocks.cs:1104-1125) by one
+// wave, from LDS: lane 8k + j (k < 4, j < 8) accumulates
+// fma(input[i], cond_v[8i + j], acc) over i = k (mod 4) ascending (a
+// remainder of dim % 4 goes to k = 0); weight j = (l0 + l1) + (l2 + l3);
+// then Ops.Softmax's 8-wide branch (Ops.cs:269-276): e = Exp(w - max),
+// total = Vector256.Sum(e), w = e * (1 / total).  Lane j < 8 returns
+// weight j.
+__device__ __forceinline__ float wave_condition_weights(const float* input, const float* cond_v, int dim)
+{
+    const int lane = threadIdx.x & 63;
+    const int k = (lane >> 3) & 3, j = lane & 7;
+    const int bulk = dim & ~3;
+    float acc = 0.0f;
+    if (lane < 32) {
+        int i = k;
+        for (; i + 28 < bulk; i += 32) {
+            float x[8], c[8];
+#pragma unroll
+            for (int u = 0; u < 8; u++) {
+                x[u] = input[i + 4 * u];
+                c[u] = cond_v[(i + 4 * u) * 8 + j];
+            }
+#pragma unroll
+            for (int u = 0; u < 8; u++) acc = fmaf(x[u], c[u], acc);
+        }
+        for (; i < bulk; i += 4) acc = fmaf(input[i], cond_v[i * 8 + j], acc);
+        if (k == 0)
+            for (int r = bulk; r < dim; r++) acc = fmaf(input[r], cond_v[r * 8 + j], acc);
+    }
+    const float w = (acc + __shfl(acc, lane + 8)) + (__shfl(acc, lane + 16) + __shfl(acc, lane + 24));
+    float peak = w;
+    peak = fmaxf(peak, __shfl_xor(peak, 1));
+    peak = fmaxf(peak, __shfl_xor(peak, 2));
+    peak = fmaxf(peak, __shfl_xor(peak, 4));
+    const float e = exp_poly(w - peak);
+    const float p2 = e + __shfl(e, lane + 1);
+    const float p4 = p2 + __shfl(p2, lane + 2);
+    const float p8 = p4 + __shfl(p4, lane + 4);
+    const float total = __shfl(p8, 0);
+    return e * (1.0f / total);
 }
 
 // Scalar.Kron in LDS: scratch[k][c] = sum_{i < active} left[i][k] z[i][c]
@@ -698,23 +704,22 @@ __device__ __forceinline__ void kron_rows(const float* z, int active, const floa
 // the next layer's RmsFakeA8 + 4-bit Prepare of that stream, or after the
 // last layer PrepareHeadVectors (Engine.cs:920-928: Mix4 by 0.25,
 // ZeroCenteredRms, FakeA8) + 4-bit Prepare for the head rows.  The Kronecker
-// factors are staged in LDS; the condition weights' products are formed in
-// parallel and summed by eight lanes at once, each in ascending i.
+// factors are staged in LDS.  The sums of PostNormAdd, the norms and the
+// condition weights run in the AVX2 tier's order (wave_v256_sum,
+// wave_condition_weights), and PostNormAdd adds with its Vector256 FMA.
 __global__ __launch_bounds__(kThreads) void n3_tail_kernel(TailArgs a)
 {
     extern __shared__ __align__(16) float lds[];
     const int width = a.rows * a.cols, dim = a.dim, rr = a.rows * a.rows, cc = a.cols * a.cols, n4 = kLanes * dim;
-    const int pstride = dim + 4;      // condition products: row j at j * pstride (banks apart)
     float* front = lds;               // width (>= the padded input)
     float* back = front + width;      // width
     float* scratch = back + width;    // kron_scratch
     float* res = scratch + kron_scratch(a.rows, a.cols);  // dim
     float* norm = res + dim;          // dim
-    float* prod = norm + dim;         // 8 * pstride (also the squares)
-    float* wl = prod + 8 * pstride + kChainPad;  // W1A, W2A, W3A
+    float* cvl = norm + dim;          // CondV [dim][8]
+    float* wl = cvl + 8 * dim;        // W1A, W2A, W3A
     float* wr = wl + 3 * rr;          // W1B, W2B, W3B
     float* ns = wr + 3 * cc;          // the next stream row, 4 * dim
-    float* nsq = ns + n4;             // its squares
     __shared__ float weights[8];
     __shared__ float red[kWaves];
     __shared__ float inv_s;
@@ -778,18 +783,22 @@ __global__ __launch_bounds__(kThreads) void n3_tail_kernel(TailArgs a)
         if (c < dim) norm[c] = pv[q];
     }
     __syncthreads();
-    float inverse = row_inverse_rms(norm, prod, dim, &inv_s);
+    float inverse = row_inverse_rms(norm, dim, &inv_s);
+    // Ops.PostNormAdd's Vector256 branch: fma(gate, ((1 + s) * x) * inverse,
+    // residual) over whole 8-blocks, the scalar expression on the rest
+    const int blocks8 = dim & ~7;
 #pragma unroll
     for (int q = 0; q < kPer; q++) {
         const int c = col_of(q);
         if (c < dim) {
-            rv[q] = rv[q] + a.attn_gate * ((1.0f + psv[q]) * pv[q] * inverse);
+            const float v = (1.0f + psv[q]) * pv[q] * inverse;
+            rv[q] = c < blocks8 ? fmaf(a.attn_gate, v, rv[q]) : rv[q] + a.attn_gate * (1.0f + psv[q]) * pv[q] * inverse;
             res[c] = rv[q];
         }
     }
     __syncthreads();
     // HadamardMlp.Apply
-    inverse = row_inverse_rms(res, prod, dim, &inv_s);
+    inverse = row_inverse_rms(res, dim, &inv_s);
 #pragma unroll
     for (int q = 0; q < kPer; q++) {
         const int c = col_of(q);
@@ -797,9 +806,9 @@ __global__ __launch_bounds__(kThreads) void n3_tail_kernel(TailArgs a)
     }
     __syncthreads();
 #pragma unroll
-    for (int q = 0; q < kCondPer; q++) {  // Scalar.ConditionWeights' products
+    for (int q = 0; q < kCondPer; q++) {  // CondV for the condition weights
         const int e = col_of(q);
-        if (e < dim * 8) prod[(e & 7) * pstride + (e >> 3)] = norm[e >> 3] * cvv[q];
+        if (e < dim * 8) cvl[e] = cvv[q];
     }
     // the Kronecker factors into LDS only now: stored earlier, their loads
     // (issued last) would hold up the two norm chains above
@@ -826,23 +835,11 @@ __global__ __launch_bounds__(kThreads) void n3_tail_kernel(TailArgs a)
         if (c < active_rows * a.cols) front[c] = c < dim ? norm[c] * d1v[q] : 0.0f;
     }
     __syncthreads();
-    // wave 3 sums the condition weights and takes their softmax while waves
-    // 0-2 run the first Kronecker product, which does not depend on them
+    // wave 3 forms the condition weights while waves 0-2 run the first
+    // Kronecker product, which does not depend on them
     if (threadIdx.x >= 3 * 64) {
-        const int lane = threadIdx.x - 3 * 64;
-        if (lane < 8) weights[lane] = chain_sum(prod + lane * pstride, dim);
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-        if (lane == 0) {  // Scalar.Softmax over the eight weights
-            float peak = -INFINITY;
-            for (int j = 0; j < 8; j++) peak = fmaxf(peak, weights[j]);
-            float total = 0.0f;
-            for (int j = 0; j < 8; j++) {
-                weights[j] = exp_poly(weights[j] - peak);
-                total = total + weights[j];
-            }
-            for (int j = 0; j < 8; j++) weights[j] = weights[j] / total;
-        }
+        const float w = wave_condition_weights(norm, cvl, dim);
+        if (threadIdx.x - 3 * 64 < 8) weights[threadIdx.x - 3 * 64] = w;
     } else {
         kron_rows(front, active_rows, wl, wr, a.rows, a.cols, a.rows, scratch, back, 3 * 64);
     }
@@ -892,14 +889,13 @@ __global__ __launch_bounds__(kThreads) void n3_tail_kernel(TailArgs a)
         // monotone), so the row's max |x| is taken with the squares, before
         // the chain, and the scaling and the int8 round trip run in one pass
         float peak_x = 0.0f;
-        for (int c = threadIdx.x; c < n4; c += kThreads) {
-            nsq[c] = ns[c] * ns[c];
-            peak_x = fmaxf(peak_x, fabsf(ns[c]));
-        }
+        for (int c = threadIdx.x; c < n4; c += kThreads) peak_x = fmaxf(peak_x, fabsf(ns[c]));
         peak_x = wave_max(peak_x);
         if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = peak_x;
-        __syncthreads();
-        if (threadIdx.x == 0) inv_s = inverse_rms_of(chain_sum(nsq, n4), n4);
+        if (threadIdx.x < 64) {
+            const float sum = wave_v256_sum(ns, ns, n4);
+            if (threadIdx.x == 0) inv_s = inverse_rms_of(sum, n4);
+        }
         __syncthreads();
         inverse = inv_s;
         float m = red[0];
@@ -924,7 +920,7 @@ __global__ __launch_bounds__(kThreads) void n3_tail_kernel(TailArgs a)
         }
     }
     __syncthreads();
-    inverse = row_inverse_rms(norm, nsq, dim, &inv_s);
+    inverse = row_inverse_rms(norm, dim, &inv_s);
 #pragma unroll
     for (int q = 0; q < kPer; q++) {
         const int c = col_of(q);

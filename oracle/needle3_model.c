@@ -39,12 +39,15 @@ float or_n3_attn_gate(float x) { return 1.0f / (1.0f + expf(-x)); }
 /* Sigmoid (Scalar.cs:193) with the polynomial exp */
 float or_sigmoid(float x) { return 1.0f / (1.0f + or_exp_poly(-x)); }
 
-/* Scalar.SumOfSquares + InverseRms (Scalar.cs:206-211, Ops.cs:209) */
+/* SumOfSquares + InverseRms (Scalar.cs:206-211 or the Vector256 sum, by the
+ * row tier; Ops.cs:209).  RmsFakeA8, CenteredRmsFakeA8, RmsUnit and
+ * ZeroCenteredRms have the same elementwise form on both tiers; on the
+ * Vector256 tier the fused norms take the peak of x (times inverse, which
+ * rounds to the same value as the peak of x * inverse: inverse > 0 and
+ * rounding is monotone), Ops.cs:632-723. */
 static float inverse_rms(const float* x, int n)
 {
-    float sum = 0.0f;
-    for (int i = 0; i < n; i++) sum += x[i] * x[i];
-    return 1.0f / sqrtf(sum / (float)n + 1e-6f);
+    return 1.0f / sqrtf(or_tier_sum_of_squares(x, n) / (float)n + 1e-6f);
 }
 
 /* Scalar.RmsFakeA8 (Scalar.cs:~367-381) */
@@ -92,10 +95,19 @@ float or_fake_a8(float* x, int n)
     return scale;
 }
 
-/* Scalar.PostNormAdd */
+/* Scalar.PostNormAdd, or Ops.PostNormAdd's Vector256 branch (Ops.cs:904-
+ * 928): residual = fma(gate, ((1 + s) * x) * inverse, residual) in 8-blocks,
+ * the tail as ((gate * (1 + s)) * x) * inverse added */
 void or_post_norm_add(float* residual, const float* x, const float* s, float gate, int n)
 {
     float inverse = inverse_rms(x, n);
+    if (or_n3_tier()) {
+        int i = 0;
+        for (; i + 8 <= n; i += 8)
+            for (int j = i; j < i + 8; j++) residual[j] = fmaf(gate, (1.0f + s[j]) * x[j] * inverse, residual[j]);
+        for (; i < n; i++) residual[i] += gate * (1.0f + s[i]) * x[i] * inverse;
+        return;
+    }
     for (int i = 0; i < n; i++) residual[i] += gate * ((1.0f + s[i]) * x[i] * inverse);
 }
 
@@ -146,12 +158,48 @@ void or_rms_unit(const float* x, int n, float* d)
     for (int i = 0; i < n; i++) d[i] = x[i] * inverse;
 }
 
-/* Scalar.Dot */
+/* Scalar.Dot, or Ops.Dot's Vector256 branch (Ops.cs:167-205) */
 float or_dot(const float* a, const float* b, int n)
 {
+    if (or_n3_tier()) return or_v256_sum(a, b, n);
     float sum = 0.0f;
     for (int i = 0; i < n; i++) sum += a[i] * b[i];
     return sum;
+}
+
+/* HadamardMlp.ConditionWeights (Blocks.cs:1104-1125): Scalar.ConditionWeights,
+ * or the Vector256 branch -- accumulator k takes the inputs i = k (mod 4) by
+ * FMA (a remainder of dim % 4 goes to l0), weights = (l0 + l1) + (l2 + l3),
+ * then Ops.Softmax's 8-wide branch (Ops.cs:269-276): e = Exp(v - max),
+ * total = Vector256.Sum(e), weights = e * (1 / total). */
+static void condition_weights(const float* cond_v, const float* input, int dim, float* weights)
+{
+    if (!or_n3_tier()) {
+        for (int j = 0; j < 8; j++) {
+            float sum = 0.0f;
+            for (int i = 0; i < dim; i++) sum += input[i] * cond_v[i * 8 + j];
+            weights[j] = sum;
+        }
+        or_softmax(weights, 8, 1);
+        return;
+    }
+    float l[4][8] = {{0.0f}};
+    int i = 0;
+    for (; i + 4 <= dim; i += 4)
+        for (int k = 0; k < 4; k++)
+            for (int j = 0; j < 8; j++) l[k][j] = fmaf(input[i + k], cond_v[(i + k) * 8 + j], l[k][j]);
+    for (; i < dim; i++)
+        for (int j = 0; j < 8; j++) l[0][j] = fmaf(input[i], cond_v[i * 8 + j], l[0][j]);
+    float peak = -INFINITY;
+    for (int j = 0; j < 8; j++) {
+        weights[j] = (l[0][j] + l[1][j]) + (l[2][j] + l[3][j]);
+        peak = fmax_(peak, weights[j]);
+    }
+    float e[8];
+    for (int j = 0; j < 8; j++) e[j] = or_exp_poly(weights[j] - peak);
+    float total = ((e[0] + e[1]) + (e[2] + e[3])) + ((e[4] + e[5]) + (e[6] + e[7]));
+    float inverse = 1.0f / total;
+    for (int j = 0; j < 8; j++) weights[j] = e[j] * inverse;
 }
 
 /* Quant.GatherRow (Quant.cs:566-575): Scalar.DecodeRow, then Scalar.Hadamard
@@ -195,12 +243,7 @@ void or_hadamard_mlp(const or_n3_mlp* w, const float* pre_norm, const int* perm_
     float* scratch = (float*)malloc(sizeof(float) * cols);
     float weights[8];
     or_zero_centered_rms(residual, pre_norm, dim, normalized);
-    for (int j = 0; j < 8; j++) {
-        float sum = 0.0f;
-        for (int i = 0; i < dim; i++) sum += normalized[i] * w->cond_v[i * 8 + j];
-        weights[j] = sum;
-    }
-    or_softmax(weights, 8, 1);
+    condition_weights(w->cond_v, normalized, dim, weights);
     for (int i = 0; i < dim; i++) front[i] = normalized[i] * w->d1[i];
     for (int i = dim; i < input_rows * cols; i++) front[i] = 0.0f;
     kron(front, input_rows, w->w1a, w->w1b, rows, cols, rows, back, scratch);
@@ -376,7 +419,8 @@ static void matmul(const or_cq* w, int row0, int rows, const float* x, int token
     slice.indices = w->indices + (size_t)row0 * cols * w->bits / 8;
     slice.norms = w->norms + (size_t)row0 * groups;
     slice.rows = rows;
-    int blocks = rows < 64 * n3_threads ? 1 : n3_threads;
+    int blocks = rows / 32 < n3_threads ? rows / 32 : n3_threads;
+    if (blocks < 1) blocks = 1;
 #pragma omp parallel for num_threads(blocks) schedule(static)
     for (int b = 0; b < blocks; b++)
         or_matmul_rows(&slice, &a, tokens, y, ldy, (int)((long)rows * b / blocks), (int)((long)rows * (b + 1) / blocks));

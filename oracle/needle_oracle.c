@@ -712,10 +712,56 @@ void or_attention_decode(const int8_t* q, const float* q_scales, int rows, int h
 /* Scalar.SumOfSquares (src/Needle/Scalar.cs:206-211) and Ops.InverseRms /
  * ZeroCenteredRms's scalar branch (src/Needle/Ops.cs:209, 233-244):
  * destination = ((1 + scale) * x) * (1 / sqrt(sum x^2 / n + 1e-6)). */
-void or_zero_centered_rms(const float* x, const float* scale, int n, float* destination)
+/* The row order of the Needle 3 engine's reductions: 0 (the default) is
+ * Scalar.cs's sequential sums, 1 the AVX2 tier's (Ops.cs, the Vector256
+ * branches that Tiers.Best takes on AVX2 / AVX-VNNI hosts). */
+static int row_tier;
+void or_n3_set_tier(int tier) { row_tier = tier; }
+int or_n3_tier(void) { return row_tier; }
+
+/* Ops.SumOfSquares / Ops.Dot on the Vector256 tier (Ops.cs:123-205; RmsStats
+ * and CenteredRmsStats, :513-630, sum the same way): four 8-lane
+ * accumulators take x[i .. i + 32) by FMA, a remaining 16-block goes to s0
+ * and s1 and an 8-block to s2, the rest to a sequential FMA tail; the result
+ * is Vector256.Sum((s0 + s1) + (s2 + s3)) + tail, where Vector256.Sum(v) =
+ * ((v0 + v1) + (v2 + v3)) + ((v4 + v5) + (v6 + v7)) (.NET's Sum(lower) +
+ * Sum(upper)).  b == NULL: the squares of a. */
+float or_v256_sum(const float* a, const float* b, int n)
 {
+    float s[4][8] = {{0.0f}};
+    int i = 0, bulk = n & ~31;
+    if (!b) b = a;
+    for (; i < bulk; i += 32)
+        for (int k = 0; k < 4; k++)
+            for (int j = 0; j < 8; j++) s[k][j] = fmaf(a[i + 8 * k + j], b[i + 8 * k + j], s[k][j]);
+    for (; i + 16 <= n; i += 16)
+        for (int k = 0; k < 2; k++)
+            for (int j = 0; j < 8; j++) s[k][j] = fmaf(a[i + 8 * k + j], b[i + 8 * k + j], s[k][j]);
+    if (i + 8 <= n) {
+        for (int j = 0; j < 8; j++) s[2][j] = fmaf(a[i + j], b[i + j], s[2][j]);
+        i += 8;
+    }
+    float tail = 0.0f;
+    for (; i < n; i++) tail = fmaf(a[i], b[i], tail);
+    float v[8];
+    for (int j = 0; j < 8; j++) v[j] = (s[0][j] + s[1][j]) + (s[2][j] + s[3][j]);
+    return (((v[0] + v[1]) + (v[2] + v[3])) + ((v[4] + v[5]) + (v[6] + v[7]))) + tail;
+}
+
+/* Ops.SumOfSquares in the row tier: Scalar.SumOfSquares or the Vector256 sum */
+float or_tier_sum_of_squares(const float* x, int n)
+{
+    if (row_tier) return or_v256_sum(x, NULL, n);
     float sum = 0.0f;
     for (int i = 0; i < n; i++) sum += x[i] * x[i];
+    return sum;
+}
+
+/* Ops.ZeroCenteredRms (Ops.cs:233-255): the elementwise form is the same on
+ * both tiers, ((1 + scale) * x) * inverse */
+void or_zero_centered_rms(const float* x, const float* scale, int n, float* destination)
+{
+    float sum = or_tier_sum_of_squares(x, n);
     float inverse = 1.0f / sqrtf(sum / (float)n + 1e-6f);
     for (int i = 0; i < n; i++) destination[i] = (1.0f + scale[i]) * x[i] * inverse;
 }

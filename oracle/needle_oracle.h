@@ -408,6 +408,12 @@ void or_n3_rewind(or_n3_engine* e, int slot);
  * the head rows. */
 void or_n3_forward(or_n3_engine* e, const int* tokens, const int* row_slots, int rows, const int* head_rows,
                    int heads, float* logits);
+/* The Needle 3 row ops' reduction order: 0 Scalar.cs, 1 the AVX2 tier's
+ * Vector256 sums (and the elementwise forms of the ops that own them). */
+void or_n3_set_tier(int tier);
+int or_n3_tier(void);
+float or_v256_sum(const float* a, const float* b, int n);
+float or_tier_sum_of_squares(const float* x, int n);
 /* A planted composition mistake for the tests' controls (0: none). */
 void or_n3_set_plant(int which);
 /* Threads of or_n3_forward's row-parallel loops (results do not depend on it). */

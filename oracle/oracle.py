@@ -193,6 +193,10 @@ _PROTOS = {
     "or_n3_forward": (None, [C.POINTER(_N3.Engine), _vp, _vp, _i, _vp, _i, _vp]),
     "or_n3_set_plant": (None, [_i]),
     "or_n3_set_threads": (None, [_i]),
+    "or_n3_set_tier": (None, [_i]),
+    "or_n3_tier": (_i, []),
+    "or_v256_sum": (C.c_float, [_vp, _vp, _i]),
+    "or_tier_sum_of_squares": (C.c_float, [_vp, _i]),
     "or_simd_matmul_i8": (None, [_i, _vp, _vp, _i, _i, _vp, _vp, _i, _vp, _i, _i, _i]),
     "or_baseline_simd_matmul_i8": (None, [_i, _vp, _vp, _i, _i, _vp, _vp, _i, _vp, _i, _i, _i]),
 }

@@ -17,7 +17,9 @@ logits to cosine 0.9997-0.9999, so the bounds here are:
 Each planted composition mistake (or_n3_set_plant: a lane bias on the wrong
 lane, the engram one layer late, the MLP before PostNormAdd, the Sinkhorn
 mix transposed, PostNorm and PreHada exchanged) moves some layer by 13% or
-more and must fail the layer bound.
+more and must fail the layer bound.  Every check runs in both row orders of
+the oracle (or_n3_set_tier: Scalar.cs's sums, or the AVX2 tier's Vector256
+sums, which the GPU engine runs).
 """
 import ctypes as C
 import hashlib
@@ -46,6 +48,13 @@ def models(orc):
     orc.lib().or_n3_set_threads(min(8, os.cpu_count() or 1))
     yield {case: M.OracleModel(orc, archive_of(case)) for case in STATE_CASES}
     orc.lib().or_n3_set_threads(1)
+
+
+@pytest.fixture(params=[0, 1], ids=["scalar", "avx2"])
+def tier(orc, request):
+    orc.lib().or_n3_set_tier(request.param)
+    yield request.param
+    orc.lib().or_n3_set_tier(0)
 
 
 def feed(orc, om, tokens, chunk):
@@ -111,7 +120,7 @@ def test_engram_rows_equal_the_reference_hash(orc, case):
 
 
 @pytest.mark.parametrize("case,chunk", [("short", 24), ("short", 7), ("prompt", 40), ("prompt", 1)])
-def test_forward_matches_the_reference_forward(orc, models, case, chunk):
+def test_forward_matches_the_reference_forward(orc, models, tier, case, chunk):
     logits, states = feed(orc, models[case], FIX[f"{case}_tokens"], chunk)
     want = FIX[f"{case}_logits"]
     assert int(np.argmax(logits)) == int(np.argmax(want))
@@ -121,7 +130,7 @@ def test_forward_matches_the_reference_forward(orc, models, case, chunk):
 
 
 @pytest.mark.parametrize("plant", [1, 2, 3, 4, 5])
-def test_planted_composition_mistakes_fail(orc, models, plant):
+def test_planted_composition_mistakes_fail(orc, models, tier, plant):
     orc.lib().or_n3_set_plant(plant)
     try:
         _, states = feed(orc, models["short"], FIX["short_tokens"], 24)
@@ -130,7 +139,7 @@ def test_planted_composition_mistakes_fail(orc, models, plant):
     assert layer_errors("short", states).max() > 2 * LAYER_BOUND
 
 
-def test_forward_threads_do_not_change_bits(orc, models):
+def test_forward_threads_do_not_change_bits(orc, models, tier):
     tokens = FIX["short_tokens"]
     orc.lib().or_n3_set_threads(1)
     one = feed(orc, models["short"], tokens, 24)

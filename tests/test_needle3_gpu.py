@@ -9,6 +9,15 @@ import pytest
 pytestmark = pytest.mark.gpu
 
 
+@pytest.fixture(autouse=True, scope="module")
+def avx2_row_tier(orc):
+    """The GPU engine sums its rows in the AVX2 tier's order
+    (or_n3_set_tier(1)); the oracle runs the same order here."""
+    orc.lib().or_n3_set_tier(1)
+    yield
+    orc.lib().or_n3_set_tier(0)
+
+
 class Case:
     def __init__(self, seed, heads, kv, qk, vd, slots, capacity):
         rng = np.random.default_rng(seed)

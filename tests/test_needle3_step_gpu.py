@@ -19,6 +19,15 @@ import needle3_model as M
 
 pytestmark = pytest.mark.gpu
 
+
+@pytest.fixture(autouse=True, scope="module")
+def avx2_row_tier(orc):
+    """The GPU engine sums its rows in the AVX2 tier's order
+    (or_n3_set_tier(1)); the oracle runs the same order here."""
+    orc.lib().or_n3_set_tier(1)
+    yield
+    orc.lib().or_n3_set_tier(0)
+
 GEOM = M.SMALL
 SEED = 3
 MAX_CHUNKS = 8
