@@ -608,9 +608,10 @@ __device__ __forceinline__ float wave_condition_weights(const float* input, cons
     return e * (1.0f / total);
 }
 
-// Scalar.Kron in LDS: scratch[k][c] = sum_{i < active} left[i][k] z[i][c]
-// (a chain over i per (k, c)), then result[k][c] = sum_j scratch[k][j]
-// right[j][c] (a chain over j), for k < result_rows.  Thread u owns the four
+// Kron in LDS in the vectorised tiers' form (Blocks.cs:1243-1700): scratch[k][c]
+// = sum_{i < active} left[i][k] z[i][c] (an FMA chain over i per (k, c)),
+// then result[k][c] = sum_j scratch[k][j] right[j][c] (an FMA chain over j),
+// for k < result_rows.  Thread u owns the four
 // elements 4u .. 4u+3 (one k, four consecutive c; cols % 4 == 0) and runs
 // their chains together; each step's operands are loaded 8 steps at a time.
 // scratch rows are cols + 1 apart (kron_scratch floats in all).
@@ -634,10 +635,10 @@ __device__ __forceinline__ void kron_first(const float* z, int active, const flo
         }
 #pragma unroll
         for (int u = 0; u < 8; u++) {
-            sum.x = sum.x + lv[u] * zv[u].x;
-            sum.y = sum.y + lv[u] * zv[u].y;
-            sum.z = sum.z + lv[u] * zv[u].z;
-            sum.w = sum.w + lv[u] * zv[u].w;
+            sum.x = fmaf(lv[u], zv[u].x, sum.x);
+            sum.y = fmaf(lv[u], zv[u].y, sum.y);
+            sum.z = fmaf(lv[u], zv[u].z, sum.z);
+            sum.w = fmaf(lv[u], zv[u].w, sum.w);
         }
     }
     float* srow = scratch + k * ss + c;
@@ -661,10 +662,10 @@ __device__ __forceinline__ void kron_second(const float* right, int cols, int e0
         }
 #pragma unroll
         for (int u = 0; u < 8; u++) {
-            sum.x = sum.x + sv[u] * rv[u].x;
-            sum.y = sum.y + sv[u] * rv[u].y;
-            sum.z = sum.z + sv[u] * rv[u].z;
-            sum.w = sum.w + sv[u] * rv[u].w;
+            sum.x = fmaf(sv[u], rv[u].x, sum.x);
+            sum.y = fmaf(sv[u], rv[u].y, sum.y);
+            sum.z = fmaf(sv[u], rv[u].z, sum.z);
+            sum.w = fmaf(sv[u], rv[u].w, sum.w);
         }
     }
     *reinterpret_cast<float4*>(result + e0) = sum;

@@ -210,19 +210,26 @@ void or_gather_row(const or_cq* w, int row, float* d)
     for (int g = 0; g < w->cols / 128; g++) or_hadamard(d + g * 128, d + g * 128);
 }
 
-/* Scalar.Kron: result[k][c] = sum_j (sum_i left[i][k] z[i][c]) right[j][c] */
+/* Scalar.Kron: result[k][c] = sum_j (sum_i left[i][k] z[i][c]) right[j][c],
+ * each sum in ascending order from +0.  The vectorised tiers (KronAvx2,
+ * Kron32Avx2Range, Kron32Avx2Range4, KronAvx512Range; Blocks.cs:1243-1700)
+ * form every output's two sums in the same order, each step one FMA: the
+ * row tier's form. */
 static void kron(const float* z, int active_rows, const float* left, const float* right, int rows, int cols,
                  int result_rows, float* result, float* scratch)
 {
+    int fused = or_n3_tier();
     for (int k = 0; k < result_rows; k++) {
         for (int c = 0; c < cols; c++) {
             float sum = 0.0f;
-            for (int i = 0; i < active_rows; i++) sum += left[i * rows + k] * z[i * cols + c];
+            for (int i = 0; i < active_rows; i++)
+                sum = fused ? fmaf(left[i * rows + k], z[i * cols + c], sum) : sum + left[i * rows + k] * z[i * cols + c];
             scratch[c] = sum;
         }
         for (int c = 0; c < cols; c++) {
             float sum = 0.0f;
-            for (int j = 0; j < cols; j++) sum += scratch[j] * right[j * cols + c];
+            for (int j = 0; j < cols; j++)
+                sum = fused ? fmaf(scratch[j], right[j * cols + c], sum) : sum + scratch[j] * right[j * cols + c];
             result[k * cols + c] = sum;
         }
     }
