@@ -89,37 +89,24 @@ class GemvCase:
                                            self.n, None))
 
     def time(self, steps: int, warmup: int) -> float:
-        """Average ms per launch over `steps` launches replayed as one graph
-        and bracketed by two events on their stream.  The untimed warmup
-        launches (at least 20) are queued right before the start event, so
-        the host's submission of the timed graph overlaps them and the GPU
-        runs the timed launches back to back (with only 20 timed launches the
-        replay's own submission would otherwise add about 0.5 us to each).
-        The replay timed from an idle GPU is kept in self.replay_ms."""
+        """Average ms per launch over `steps` launches replayed as one graph,
+        bracketed by two events on the launches' stream (after `warmup` eager
+        launches and one untimed replay)."""
+        for i in range(warmup):
+            self.launch(i)
         N.check(N.lib().nhip_device_sync())
-        with N.Graph.capture() as gw:
-            for i in range(max(warmup, 20)):
-                self.launch(i)
         with N.Graph.capture() as g:
             for i in range(steps):
                 self.launch(i)
-        g.launch()  # first replays carry one-time costs
-        gw.launch()
+        g.launch()  # the first replay carries one-time costs
         N.check(N.lib().nhip_device_sync())
         start, stop = N.Event(), N.Event()
-        start.record()
-        g.launch()
-        stop.record()
-        self.replay_ms = start.elapsed_ms(stop) / steps
-        N.check(N.lib().nhip_device_sync())
-        gw.launch()
         start.record()
         g.launch()
         stop.record()
         ms = start.elapsed_ms(stop)
         N.check(N.lib().nhip_device_sync())
         g.close()
-        gw.close()
         return ms / steps
 
     def close(self) -> None:
@@ -830,8 +817,7 @@ def main() -> int:
         "timing": {"method": "a step is one GEMV on each of the cycled weight matrices (a pass over that many "
                              "layers); the K steps' launches are replayed as one graph between two HIP events on "
                              "their stream",
-                   "us_per_launch": round(ms * 1e3, 4),
-                   "graph_replay_from_idle_us_per_launch": round(main_case.replay_ms * 1e3, 3)},
+                   "us_per_launch": round(ms * 1e3, 4)},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": measured_traffic()},
         "cpu_baseline": cpu,
