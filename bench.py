@@ -3,12 +3,13 @@
 
 Headline workload: the beam/ragged-batched int8 decode GEMV -- M = 3 packed
 rows (beam width 3), K = 2048, N = 8192, int8 weights with one fp16 scale per
-32-element group, activations quantized per row to int8 (absmax/127).  One
-step = one GEMV launch over one weight matrix; successive steps cycle through
-enough distinct weight copies (>= 300 MB) that the 256 MB Infinity Cache
-cannot hold them, so every step streams its weights from HBM.  The K timed
-steps are replayed as one HIP graph (no host launch overhead in the timed
-region) and timed with HIP events on the stream the kernels run on.
+32-element group, activations quantized per row to int8 (absmax/127).  The
+GEMV runs over enough distinct weight copies (>= 300 MB) that the 256 MB
+Infinity Cache cannot hold them, so every launch streams its weights from
+HBM; one step = one GEMV on each copy (a pass over that many layers).  The K
+timed steps' launches are replayed as one HIP graph (no host launch overhead
+in the timed region) and timed with HIP events on the stream the kernels run
+on.
 
 Printed: one JSON line with the metric, a roofline object for the GEMV
 kernel (algorithmic bytes / average launch time vs 8 TB/s) and the CPU
@@ -459,10 +460,11 @@ def needle3_loop(args, threads: int) -> dict:
     vocab 8192) through the step API: a 64-token prompt per slot (63 fed with
     FeedSlot, the last in the first 3-row step), then 63 decode steps of 3
     rows with the head's ArgMax as the next tokens.  The CPU leg runs the
-    oracle's scalar engine on the same prompts for a bounded number of steps,
-    its matmul rows, attention rows and MLP rows spread over `threads` host
-    threads (each output is still one thread's scalar-order sum): its tokens
-    must match the GPU's, its step time is the port baseline."""
+    oracle's engine in the engine's row order (the AVX2 tier's sums) on the
+    same prompts for a bounded number of steps, its matmul rows, attention
+    rows and MLP rows spread over `threads` host threads (each output is still
+    one thread's sum): its tokens must match the GPU's, its step time is the
+    port baseline."""
     from needle_cs_amd.archive import NEEDLE3, needle3_archive
     from needle_cs_amd.engine import BatchedEngine, Model
 
@@ -547,7 +549,7 @@ def needle3_loop(args, threads: int) -> dict:
         out["tokens_identical_to_cpu_path"] = bool(np.array_equal(ctoks, toks[:, :check_steps + 1]))
         out["cpu_path"] = {"row_tokens_per_s": round(slots * check_steps / cdec, 2),
                            "ms_per_step": round(cdec / check_steps * 1e3, 2), "threads": threads, "kind": "port",
-                           "sample": f"the oracle's scalar Needle 3 engine (oracle/needle3_model.c) on the same "
+                           "sample": f"the oracle's Needle 3 engine (oracle/needle3_model.c, AVX2-tier row order) on the same "
                                      f"prompts, matmul, attention and MLP rows over {threads} threads, "
                                      f"{check_steps} decode steps of 3 rows after the prefill; tokens compared over "
                                      f"those {check_steps + 1} per slot"}

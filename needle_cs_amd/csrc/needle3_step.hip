@@ -49,13 +49,13 @@ namespace {
 constexpr int kLanes = 4;
 constexpr int kEngramHistory = 9;
 constexpr int kEngramTaps = 4;
-constexpr int kThreads = 256;
+constexpr int kThreads = 1024;  // one workgroup per row: 16 waves share each row's phases
 constexpr int kWaves = kThreads / 64;
 constexpr int kMaxDim = 1024;
 constexpr int kPer = kMaxDim / kThreads;    // elements of a dim-row per thread: c = threadIdx.x + kThreads * q
 constexpr int kMaxStream = kLanes * kMaxDim;
 constexpr int kCondPer = 8 * kMaxDim / kThreads;  // condition-weight entries per thread
-constexpr int kHistPer = 10;                       // Q/K/V frame entries per thread (qw + kw + vw <= 2560)
+constexpr int kHistPer = (2560 + kThreads - 1) / kThreads;  // Q/K/V frame entries per thread (qw + kw + vw <= 2560)
 
 __device__ __forceinline__ float sigmoid_poly(float x) { return 1.0f / (1.0f + exp_poly(-x)); }
 
@@ -836,13 +836,14 @@ __global__ __launch_bounds__(kThreads) void n3_tail_kernel(TailArgs a)
         if (c < active_rows * a.cols) front[c] = c < dim ? norm[c] * d1v[q] : 0.0f;
     }
     __syncthreads();
-    // wave 3 forms the condition weights while waves 0-2 run the first
-    // Kronecker product, which does not depend on them
-    if (threadIdx.x >= 3 * 64) {
+    // the last wave forms the condition weights while the others run the
+    // first Kronecker product, which does not depend on them
+    constexpr int kKronThreads = (kWaves - 1) * 64;
+    if (threadIdx.x >= kKronThreads) {
         const float w = wave_condition_weights(norm, cvl, dim);
-        if (threadIdx.x - 3 * 64 < 8) weights[threadIdx.x - 3 * 64] = w;
+        if (threadIdx.x - kKronThreads < 8) weights[threadIdx.x - kKronThreads] = w;
     } else {
-        kron_rows(front, active_rows, wl, wr, a.rows, a.cols, a.rows, scratch, back, 3 * 64);
+        kron_rows(front, active_rows, wl, wr, a.rows, a.cols, a.rows, scratch, back, kKronThreads);
     }
     __syncthreads();
 #pragma unroll
@@ -1331,7 +1332,7 @@ int32_t alloc_state(nhip_ctx* c)
     c->prev.assign(2 * c->slots, 0);
     c->snap_prev.assign(2 * c->slots, 0);
     const size_t width = (size_t)c->hada_rows * c->hada_cols;
-    NHIP_REQUIRE(width <= 4 * kThreads, "MLP size %zu above %d", width, 4 * kThreads);
+    NHIP_REQUIRE(width <= (size_t)kPer * kThreads, "MLP size %zu above %d", width, kPer * kThreads);
     c->tail_lds = tail_lds_bytes(d, c->hada_rows, c->hada_cols);
     NHIP_REQUIRE(c->tail_lds <= 160 * 1024, "the layer tail's %zu bytes of LDS exceed the CU's", c->tail_lds);
     if (c->tail_lds > 64 * 1024)
