@@ -335,6 +335,100 @@ __device__ __forceinline__ float wave_v256_sum(const float* a, const float* b, i
     return __shfl(p8, 0) + tail;
 }
 
+// acc = fma(a[m], b[m], acc) for m = 0 .. count-1 in ascending order, over
+// two 16-byte aligned LDS rows (count % 16 == 0).  The batches of 16 steps
+// alternate between two register sets: each batch is read (four 16-byte
+// reads per row) before the previous one is summed, and scheduling barriers
+// keep the compiler from sinking those reads below the sums, so the chain
+// runs behind its reads (at most 8 reads outstanding, within the LDS
+// counter's range; LDS reads return in order).
+template <bool kSquares>
+__device__ __forceinline__ void lds_chain_load(const float4* a4, const float4* b4, int m4, float4 (&x)[4],
+                                               float4 (&y)[4])
+{
+#pragma unroll
+    for (int u = 0; u < 4; u++) {
+        x[u] = a4[m4 + u];
+        if constexpr (!kSquares) y[u] = b4[m4 + u];
+    }
+}
+
+template <bool kSquares>
+__device__ __forceinline__ float lds_chain_sum(const float4 (&x)[4], const float4 (&y)[4], float acc)
+{
+#pragma unroll
+    for (int u = 0; u < 4; u++) {
+        const float4 v = kSquares ? x[u] : y[u];
+        acc = fmaf(x[u].x, v.x, acc);
+        acc = fmaf(x[u].y, v.y, acc);
+        acc = fmaf(x[u].z, v.z, acc);
+        acc = fmaf(x[u].w, v.w, acc);
+    }
+    return acc;
+}
+
+template <bool kSquares>
+__device__ __forceinline__ float lds_chain(const float* a, const float* b, int count, float acc)
+{
+    const float4* a4 = reinterpret_cast<const float4*>(a);
+    const float4* b4 = reinterpret_cast<const float4*>(b);
+    const int batches = count / 16;
+    float4 xa[4], xb[4], ya[4], yb[4];
+    lds_chain_load<kSquares>(a4, b4, 0, xa, xb);
+    int k = 0;
+    for (; k + 2 < batches; k += 2) {
+        lds_chain_load<kSquares>(a4, b4, 4 * (k + 1), ya, yb);
+        __builtin_amdgcn_sched_barrier(0);
+        acc = lds_chain_sum<kSquares>(xa, xb, acc);
+        __builtin_amdgcn_sched_barrier(0);
+        lds_chain_load<kSquares>(a4, b4, 4 * (k + 2), xa, xb);
+        __builtin_amdgcn_sched_barrier(0);
+        acc = lds_chain_sum<kSquares>(ya, yb, acc);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    if (k + 1 < batches) {
+        lds_chain_load<kSquares>(a4, b4, 4 * (k + 1), ya, yb);
+        __builtin_amdgcn_sched_barrier(0);
+        acc = lds_chain_sum<kSquares>(xa, xb, acc);
+        __builtin_amdgcn_sched_barrier(0);
+        acc = lds_chain_sum<kSquares>(ya, yb, acc);
+    } else {
+        acc = lds_chain_sum<kSquares>(xa, xb, acc);
+    }
+    return acc;
+}
+
+__device__ __forceinline__ float lds_fma_chain(const float* a, const float* b, int count, float acc)
+{
+    return lds_chain<false>(a, b, count, acc);
+}
+
+// lds_fma_chain of a row with itself (a sum of squares from +0), one read per step.
+__device__ __forceinline__ float lds_square_chain(const float* a, int count)
+{
+    return lds_chain<true>(a, a, count, 0.0f);
+}
+
+// The padded row stride of a lane-major copy of an n-element LDS row for
+// wave_v256_squares (n % 512 == 0): element i sits at (i % 32) * stride +
+// i / 32, so lane L's chain is one contiguous row; the pad of 4 keeps rows
+// 16-byte aligned and spreads the copy's stores over the banks.
+__host__ __device__ constexpr int v256_stride(int n) { return n / 32 + 4; }
+
+// wave_v256_sum's sum of squares (every element i < n in lane i % 32's chain
+// at step i / 32, then the same tree) from the lane-major copy t of the row.
+__device__ __forceinline__ float wave_v256_squares(const float* t, int n)
+{
+    const int lane = threadIdx.x & 63;
+    float acc = 0.0f;
+    if (lane < 32) acc = lds_square_chain(t + lane * v256_stride(n), n / 32);
+    const float v = (acc + __shfl(acc, lane + 8)) + (__shfl(acc, lane + 16) + __shfl(acc, lane + 24));
+    const float p2 = v + __shfl(v, lane + 1);
+    const float p4 = p2 + __shfl(p2, lane + 2);
+    const float p8 = p4 + __shfl(p4, lane + 4);
+    return __shfl(p8, 0);
+}
+
 // Maximum over the 64 lanes of a wave (order-free), in every lane.
 __device__ __forceinline__ float wave_max(float v)
 {

@@ -228,22 +228,46 @@ struct HyperArgs {
     const int32_t* erows;
     Act act;
     int stride;
+    int rows;
 };
+
+// Sinkhorn4x4 of row t's residual-mix logits (Engine.cs:2374-2378) by one
+// wave, one lane per matrix entry (lane e = 4a + c, repeated across the
+// wave): every lane of a row or column forms the same left-to-right sum of
+// its four entries, so each normalisation is Scalar.Sinkhorn4x4's.
+__device__ __forceinline__ void sinkhorn_wave(const HyperArgs& a, int t)
+{
+    const int lane = threadIdx.x & 63;
+    const int e = lane & 15, row = e >> 2, col = e & 3;
+    const float lg = a.a_res[0] * a.res_out[t * a.ld16 + e] + a.b_res[e];
+    const float l0 = __shfl(lg, row * 4), l1 = __shfl(lg, row * 4 + 1), l2 = __shfl(lg, row * 4 + 2),
+                l3 = __shfl(lg, row * 4 + 3);
+    float r = exp_poly(lg - fmaxf(fmaxf(l0, l1), fmaxf(l2, l3)));
+    for (int it = 0; it < 20; it++) {
+        const float rs = __shfl(r, row * 4) + __shfl(r, row * 4 + 1) + __shfl(r, row * 4 + 2) + __shfl(r, row * 4 + 3);
+        r = r / rs;
+        const float cs = __shfl(r, col) + __shfl(r, 4 + col) + __shfl(r, 8 + col) + __shfl(r, 12 + col);
+        if (cs > 0.0f) r = r / cs;
+    }
+    if (lane < 16) a.mix[t * 16 + e] = r;
+}
 
 // RunLayerBatch's per-row mix (Engine.cs:2366-2381): hpre / postGate by
 // Sigmoid, Mix4 of the lanes into input and residual, Sinkhorn4x4 of the
-// residual-mix logits.  Wave 1 runs Sinkhorn4x4 with one lane per matrix
-// entry (lane e = 4a + c, repeated across the wave): every lane of a row or
-// column forms the same left-to-right sum of its four entries, so each
-// normalisation is Scalar.Sinkhorn4x4's.  Only the layer's tail reads the
-// mix matrix, so Sinkhorn runs beside the norm's sum of squares (or before
-// the engram gathers).  Then, on layers without an engram,
-// RunAttentionBatch's CenteredRmsFakeA8 of the residual and its 2-bit Prepare
-// (Engine.cs:2487-2490); on engram layers, ApplyEngramBatch's input
-// (Engine.cs:2404-2414): every table's GatherRow (zeros for row -1),
-// Quant.FakeA8 and the 2-bit Prepare.
+// residual-mix logits.  Workgroups 0 .. rows-1 take one row each; only the
+// layer's tail reads the mix matrix, so Sinkhorn runs in workgroups of its
+// own after them (one wave per row), beside the rows' work.  Then, on layers
+// without an engram, RunAttentionBatch's CenteredRmsFakeA8 of the residual
+// and its 2-bit Prepare (Engine.cs:2487-2490); on engram layers,
+// ApplyEngramBatch's input (Engine.cs:2404-2414): every table's GatherRow
+// (zeros for row -1), Quant.FakeA8 and the 2-bit Prepare.
 __global__ __launch_bounds__(kThreads) void n3_hyper_kernel(HyperArgs a)
 {
+    if ((int)blockIdx.x >= a.rows) {
+        const int t = ((int)blockIdx.x - a.rows) * kWaves + (int)(threadIdx.x >> 6);
+        if (t < a.rows) sinkhorn_wave(a, t);
+        return;
+    }
     __shared__ __align__(16) float x[kMaxDim];
     __shared__ __align__(16) float sq[kMaxDim];
     __shared__ float hpre[4];
@@ -263,28 +287,11 @@ __global__ __launch_bounds__(kThreads) void n3_hyper_kernel(HyperArgs a)
             sn[q] = a.norm_in[c];
         }
     }
-    const int e = i & 15;
-    const bool sink = (i >> 6) == 1;  // wave 1
-    const float lg = sink ? a.a_res[0] * a.res_out[t * a.ld16 + e] + a.b_res[e] : 0.0f;
     if (i < 4) {
         hpre[i] = sigmoid_poly(a.a_pre[0] * a.pre_out[t * a.ld4 + i] + a.b_pre[i] + (i == a.lane ? 4.0f : -4.0f));
         a.post_gate[t * 4 + i] =
             2.0f * sigmoid_poly(a.a_post[0] * a.post_out[t * a.ld4 + i] + a.b_post[i] + (i == a.lane ? 0.0f : -4.0f));
     }
-    auto sinkhorn = [&]() {
-        if (!sink) return;
-        const int row = e >> 2, col = e & 3;
-        const float l0 = __shfl(lg, row * 4), l1 = __shfl(lg, row * 4 + 1), l2 = __shfl(lg, row * 4 + 2),
-                    l3 = __shfl(lg, row * 4 + 3);
-        float r = exp_poly(lg - fmaxf(fmaxf(l0, l1), fmaxf(l2, l3)));
-        for (int it = 0; it < 20; it++) {
-            const float rs = __shfl(r, row * 4) + __shfl(r, row * 4 + 1) + __shfl(r, row * 4 + 2) + __shfl(r, row * 4 + 3);
-            r = r / rs;
-            const float cs = __shfl(r, col) + __shfl(r, 4 + col) + __shfl(r, 8 + col) + __shfl(r, 12 + col);
-            if (cs > 0.0f) r = r / cs;
-        }
-        if (i < 80) a.mix[t * 16 + e] = r;
-    };
     __syncthreads();
 #pragma unroll
     for (int q = 0; q < kPer; q++) {
@@ -298,7 +305,6 @@ __global__ __launch_bounds__(kThreads) void n3_hyper_kernel(HyperArgs a)
     }
     __syncthreads();
     if (a.tables) {
-        sinkhorn();
         const int sub = a.table_cols, per = sub / 128;
         for (int unit = i >> 6; unit < a.tables_count * per; unit += kWaves) {
             const int table = unit / per, g = unit % per;
@@ -313,7 +319,7 @@ __global__ __launch_bounds__(kThreads) void n3_hyper_kernel(HyperArgs a)
         prepare_row(sq, dim, 2, a.act, a.stride, t);
         return;
     }
-    const float inverse = row_inverse_rms_beside(x, dim, &inv_s, sinkhorn);
+    const float inverse = row_inverse_rms(x, dim, &inv_s);
 #pragma unroll
     for (int q = 0; q < kPer; q++) {
         const int c = col_of(q);
@@ -558,43 +564,33 @@ struct TailArgs {
     int stride;
 };
 
+// The padded row stride of the condition weights' lane-major copies (dim % 64
+// == 0): input[i] at (i % 4) * stride + i / 4, cond_v[8i + j] at
+// ((i % 4) * 8 + j) * stride + i / 4.
+__host__ __device__ constexpr int cond_stride(int dim) { return dim / 4 + 4; }
+
 // Bytes of LDS n3_tail_kernel takes for a geometry.
 size_t tail_lds_bytes(int dim, int rows, int cols)
 {
     const size_t width = (size_t)rows * cols;
-    return sizeof(float) * (3 * width + 32 + 2 * (size_t)dim + 8 * (size_t)dim + 3 * (size_t)rows * rows +
-                            3 * (size_t)cols * cols + (size_t)kLanes * dim);
+    return sizeof(float) * (3 * width + 32 + 2 * (size_t)dim + 36 * (size_t)cond_stride(dim) +
+                            3 * (size_t)rows * rows + 3 * (size_t)cols * cols + (size_t)kLanes * dim +
+                            32 * (size_t)v256_stride(kLanes * dim));
 }
 
 // HadamardMlp.ConditionWeights' Vector256 branch (Blocks.cs:1104-1125) by one
-// wave, from LDS: lane 8k + j (k < 4, j < 8) accumulates
-// fma(input[i], cond_v[8i + j], acc) over i = k (mod 4) ascending (a
-// remainder of dim % 4 goes to k = 0); weight j = (l0 + l1) + (l2 + l3);
-// then Ops.Softmax's 8-wide branch (Ops.cs:269-276): e = Exp(w - max),
-// total = Vector256.Sum(e), w = e * (1 / total).  Lane j < 8 returns
-// weight j.
-__device__ __forceinline__ float wave_condition_weights(const float* input, const float* cond_v, int dim)
+// wave, from the lane-major copies: lane 8k + j (k < 4, j < 8) accumulates
+// fma(input[i], cond_v[8i + j], acc) over i = k (mod 4) ascending (dim % 4
+// == 0: no remainder); weight j = (l0 + l1) + (l2 + l3); then Ops.Softmax's
+// 8-wide branch (Ops.cs:269-276): e = Exp(w - max), total =
+// Vector256.Sum(e), w = e * (1 / total).  Lane j < 8 returns weight j.
+__device__ __forceinline__ float wave_condition_weights(const float* input_t, const float* cond_t, int dim)
 {
     const int lane = threadIdx.x & 63;
-    const int k = (lane >> 3) & 3, j = lane & 7;
-    const int bulk = dim & ~3;
+    const int k = (lane >> 3) & 3;
+    const int stride = cond_stride(dim);
     float acc = 0.0f;
-    if (lane < 32) {
-        int i = k;
-        for (; i + 28 < bulk; i += 32) {
-            float x[8], c[8];
-#pragma unroll
-            for (int u = 0; u < 8; u++) {
-                x[u] = input[i + 4 * u];
-                c[u] = cond_v[(i + 4 * u) * 8 + j];
-            }
-#pragma unroll
-            for (int u = 0; u < 8; u++) acc = fmaf(x[u], c[u], acc);
-        }
-        for (; i < bulk; i += 4) acc = fmaf(input[i], cond_v[i * 8 + j], acc);
-        if (k == 0)
-            for (int r = bulk; r < dim; r++) acc = fmaf(input[r], cond_v[r * 8 + j], acc);
-    }
+    if (lane < 32) acc = lds_fma_chain(input_t + k * stride, cond_t + lane * stride, dim / 4, 0.0f);
     const float w = (acc + __shfl(acc, lane + 8)) + (__shfl(acc, lane + 16) + __shfl(acc, lane + 24));
     float peak = w;
     peak = fmaxf(peak, __shfl_xor(peak, 1));
@@ -717,10 +713,13 @@ __global__ __launch_bounds__(kThreads) void n3_tail_kernel(TailArgs a)
     float* scratch = back + width;    // kron_scratch
     float* res = scratch + kron_scratch(a.rows, a.cols);  // dim
     float* norm = res + dim;          // dim
-    float* cvl = norm + dim;          // CondV [dim][8]
-    float* wl = cvl + 8 * dim;        // W1A, W2A, W3A
+    const int cs = cond_stride(dim), ts = v256_stride(n4);
+    float* cvt = norm + dim;          // CondV, lane-major [32][cs]
+    float* int_ = cvt + 32 * cs;      // the condition input, lane-major [4][cs]
+    float* wl = int_ + 4 * cs;        // W1A, W2A, W3A
     float* wr = wl + 3 * rr;          // W1B, W2B, W3B
     float* ns = wr + 3 * cc;          // the next stream row, 4 * dim
+    float* nst = ns + n4;             // its lane-major copy [32][ts]
     __shared__ float weights[8];
     __shared__ float red[kWaves];
     __shared__ float inv_s;
@@ -803,13 +802,17 @@ __global__ __launch_bounds__(kThreads) void n3_tail_kernel(TailArgs a)
 #pragma unroll
     for (int q = 0; q < kPer; q++) {
         const int c = col_of(q);
-        if (c < dim) norm[c] = (1.0f + prv[q]) * rv[q] * inverse;
+        if (c < dim) {
+            const float v = (1.0f + prv[q]) * rv[q] * inverse;
+            norm[c] = v;
+            int_[(c & 3) * cs + (c >> 2)] = v;
+        }
     }
     __syncthreads();
 #pragma unroll
     for (int q = 0; q < kCondPer; q++) {  // CondV for the condition weights
         const int e = col_of(q);
-        if (e < dim * 8) cvl[e] = cvv[q];
+        if (e < dim * 8) cvt[(((e >> 3) & 3) * 8 + (e & 7)) * cs + (e >> 5)] = cvv[q];
     }
     // the Kronecker factors into LDS only now: stored earlier, their loads
     // (issued last) would hold up the two norm chains above
@@ -840,7 +843,7 @@ __global__ __launch_bounds__(kThreads) void n3_tail_kernel(TailArgs a)
     // first Kronecker product, which does not depend on them
     constexpr int kKronThreads = (kWaves - 1) * 64;
     if (threadIdx.x >= kKronThreads) {
-        const float w = wave_condition_weights(norm, cvl, dim);
+        const float w = wave_condition_weights(int_, cvt, dim);
         if (threadIdx.x - kKronThreads < 8) weights[threadIdx.x - kKronThreads] = w;
     } else {
         kron_rows(front, active_rows, wl, wr, a.rows, a.cols, a.rows, scratch, back, kKronThreads);
@@ -879,8 +882,10 @@ __global__ __launch_bounds__(kThreads) void n3_tail_kernel(TailArgs a)
             for (int l = 0; l < kLanes; l++) {
                 const float o = pg[l] * y + m[4 * l] * sv[q][0] + m[4 * l + 1] * sv[q][1] + m[4 * l + 2] * sv[q][2] +
                                 m[4 * l + 3] * sv[q][3];
-                a.next[(size_t)t * n4 + l * dim + c] = o;
-                ns[l * dim + c] = o;
+                const int i = l * dim + c;
+                a.next[(size_t)t * n4 + i] = o;
+                ns[i] = o;
+                nst[(i & 31) * ts + (i >> 5)] = o;
             }
         }
     }
@@ -895,7 +900,7 @@ __global__ __launch_bounds__(kThreads) void n3_tail_kernel(TailArgs a)
         peak_x = wave_max(peak_x);
         if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = peak_x;
         if (threadIdx.x < 64) {
-            const float sum = wave_v256_sum(ns, ns, n4);
+            const float sum = wave_v256_squares(nst, n4);
             if (threadIdx.x == 0) inv_s = inverse_rms_of(sum, n4);
         }
         __syncthreads();
@@ -1421,8 +1426,8 @@ int32_t enqueue_step(nhip_ctx* c, int rows, int heads, int k, bool argmax)
                      c->b_res + 16 * l, l % kLanes, d, c->input, c->residual, c->post_gate, c->mix, w.norm_in,
                      st ? st->tables : nullptr, st ? st->table_rows : 0, st ? st->table_cols : 0,
                      st ? st->table_bits : 0, c->engram_tables, st && st->table_bits == 2 ? c->book2 : c->book4,
-                     in_erows(c, c->d_in), act, stride_d};
-        hipLaunchKernelGGL(n3_hyper_kernel, dim3(rows), dim3(kThreads), 0, s, ha);
+                     in_erows(c, c->d_in), act, stride_d, rows};
+        hipLaunchKernelGGL(n3_hyper_kernel, dim3(rows + (rows + kWaves - 1) / kWaves), dim3(kThreads), 0, s, ha);
         NHIP_CHECK_HIP(hipGetLastError());
         EngramArgs ea{};
         if (st) {  // engram (ApplyEngramBatch, Engine.cs:2399-2463)
