@@ -287,6 +287,56 @@ __device__ __forceinline__ float canonical_finish(const float* p, int lane)
     return q;
 }
 
+// The value lane (lane ^ S) of the wave holds, S = 1..32, without an LDS
+// round trip: DPP quad permutations [1,0,3,2] (1) and [2,3,0,1] (2), a row
+// half-mirror then the quad reversal [3,2,1,0] (4: 7 - l, then 3 - that
+// within the quad, is l ^ 4), a row rotation by 8 (8), and gfx950's
+// permlane16 / permlane32 swaps of a register with itself (16, 32: the swap
+// returns the lower rows' values in its first result and the upper rows' in
+// its second).
+template <int S>
+__device__ __forceinline__ uint32_t lane_xor(uint32_t v)
+{
+    if constexpr (S == 1) {
+        return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0xB1, 0xF, 0xF, false);
+    } else if constexpr (S == 2) {
+        return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x4E, 0xF, 0xF, false);
+    } else if constexpr (S == 4) {
+        const int m = __builtin_amdgcn_update_dpp(0, (int)v, 0x141, 0xF, 0xF, false);
+        return (uint32_t)__builtin_amdgcn_update_dpp(0, m, 0x1B, 0xF, 0xF, false);
+    } else if constexpr (S == 8) {
+        return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x128, 0xF, 0xF, false);
+    } else if constexpr (S == 16) {
+        const auto r = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+        return (threadIdx.x & 16) ? r[0] : r[1];
+    } else {
+        static_assert(S == 32, "lane_xor: S is a power of two below 64");
+        const auto r = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+        return (threadIdx.x & 32) ? r[0] : r[1];
+    }
+}
+template <int S>
+__device__ __forceinline__ float lane_xor(float v)
+{
+    return __uint_as_float(lane_xor<S>(__float_as_uint(v)));
+}
+
+// The end of a Vector256 sum: lane 8k + j holds lane j of accumulator s_k
+// (k < 4); returns Vector256.Sum((s0 + s1) + (s2 + s3)), with Vector256.Sum(v)
+// = ((v0 + v1) + (v2 + v3)) + ((v4 + v5) + (v6 + v7)), in every lane.  Lanes
+// 0-7 form the vector from their xor-partners 8, 16 and 24 (lanes j + 8,
+// j + 16, j + 24), the tree runs on xor-partners 1, 2, 4, and lane 0's total
+// is read out.
+__device__ __forceinline__ float v256_tree(float acc)
+{
+    const float a16 = lane_xor<16>(acc);
+    const float v = (acc + lane_xor<8>(acc)) + (a16 + lane_xor<8>(a16));
+    const float p2 = v + lane_xor<1>(v);
+    const float p4 = p2 + lane_xor<2>(p2);
+    const float p8 = p4 + lane_xor<4>(p4);
+    return __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(p8)));
+}
+
 // Ops.SumOfSquares / Ops.Dot in the AVX2 tier's Vector256 order (Ops.cs:
 // 123-205; RmsStats / CenteredRmsStats, :513-630, sum the same way), by one
 // whole wave over LDS rows a and b (b = a for the squares): lane 8k + j
@@ -328,11 +378,7 @@ __device__ __forceinline__ float wave_v256_sum(const float* a, const float* b, i
     float tail = 0.0f;
     for (; i < n; i++) tail = fmaf(a[i], b[i], tail);
     // lane j < 8: v_j = (s0_j + s1_j) + (s2_j + s3_j), then the pairwise tree
-    const float v = (acc + __shfl(acc, lane + 8)) + (__shfl(acc, lane + 16) + __shfl(acc, lane + 24));
-    const float p2 = v + __shfl(v, lane + 1);
-    const float p4 = p2 + __shfl(p2, lane + 2);
-    const float p8 = p4 + __shfl(p4, lane + 4);
-    return __shfl(p8, 0) + tail;
+    return v256_tree(acc) + tail;
 }
 
 // acc = fma(a[m], b[m], acc) for m = 0 .. count-1 in ascending order, over
@@ -422,11 +468,7 @@ __device__ __forceinline__ float wave_v256_squares(const float* t, int n)
     const int lane = threadIdx.x & 63;
     float acc = 0.0f;
     if (lane < 32) acc = lds_square_chain(t + lane * v256_stride(n), n / 32);
-    const float v = (acc + __shfl(acc, lane + 8)) + (__shfl(acc, lane + 16) + __shfl(acc, lane + 24));
-    const float p2 = v + __shfl(v, lane + 1);
-    const float p4 = p2 + __shfl(p2, lane + 2);
-    const float p8 = p4 + __shfl(p4, lane + 4);
-    return __shfl(p8, 0);
+    return v256_tree(acc);
 }
 
 // Maximum over the 64 lanes of a wave (order-free), in every lane.
@@ -462,38 +504,24 @@ __device__ __forceinline__ float exp_poly(float x)
     return y * scale;
 }
 
-// The value lane (lane ^ S) of the wave holds, S = 1..32, without an LDS
-// round trip: DPP quad permutations [1,0,3,2] (1) and [2,3,0,1] (2), a row
-// half-mirror then the quad reversal [3,2,1,0] (4: 7 - l, then 3 - that
-// within the quad, is l ^ 4), a row rotation by 8 (8), and gfx950's
-// permlane16 / permlane32 swaps of a register with itself (16, 32: the swap
-// returns the lower rows' values in its first result and the upper rows' in
-// its second).
-template <int S>
-__device__ __forceinline__ uint32_t lane_xor(uint32_t v)
+// A 16-entry byte table lookup of four 4-bit codes in three operations, for
+// tables whose 16 bytes are all below 128 (codebook bytes are in [0, 126]).  v_perm_b32's selector byte s
+// picks byte s of its 8-byte source for s < 8, the sign of source byte 1, 3,
+// 5 or 7 (0x00 or 0xFF) for s = 8..11, 0x00 for 12 and 0xFF for 13..15.
+// With
+//   A = perm(TA, c),  B = perm(TB, c ^ 8),
+//   TA = table bytes 0..7, TB = bytes 8..15, every byte but byte 4 of each
+//        stored complemented,
+// one of A, B is the stored byte (TA[c] for c < 8, TB[c - 8] for c >= 8)
+// and the other is 0x00 for c = 4, 12 (selector 12; stored plain) and 0xFF
+// for every other c (selectors 8..11 read the complemented, sign-set bytes
+// 1, 3, 5, 7, and 13..15 give 0xFF), so A ^ B is the table byte.
+// c: four codes 0..15, one per byte.
+__device__ __forceinline__ uint32_t lut4x(uint32_t c, uint32_t a0, uint32_t a1, uint32_t b0, uint32_t b1)
 {
-    if constexpr (S == 1) {
-        return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0xB1, 0xF, 0xF, false);
-    } else if constexpr (S == 2) {
-        return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x4E, 0xF, 0xF, false);
-    } else if constexpr (S == 4) {
-        const int m = __builtin_amdgcn_update_dpp(0, (int)v, 0x141, 0xF, 0xF, false);
-        return (uint32_t)__builtin_amdgcn_update_dpp(0, m, 0x1B, 0xF, 0xF, false);
-    } else if constexpr (S == 8) {
-        return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x128, 0xF, 0xF, false);
-    } else if constexpr (S == 16) {
-        const auto r = __builtin_amdgcn_permlane16_swap(v, v, false, false);
-        return (threadIdx.x & 16) ? r[0] : r[1];
-    } else {
-        static_assert(S == 32, "lane_xor: S is a power of two below 64");
-        const auto r = __builtin_amdgcn_permlane32_swap(v, v, false, false);
-        return (threadIdx.x & 32) ? r[0] : r[1];
-    }
-}
-template <int S>
-__device__ __forceinline__ float lane_xor(float v)
-{
-    return __uint_as_float(lane_xor<S>(__float_as_uint(v)));
+    const uint32_t a = __builtin_amdgcn_perm(a1, a0, c);
+    const uint32_t b = __builtin_amdgcn_perm(b1, b0, c ^ 0x08080808u);
+    return a ^ b;
 }
 
 // Sum of an int over the 64 lanes of a wave (exact), in every lane.

@@ -149,26 +149,6 @@ __device__ __forceinline__ uint32_t lut4(uint32_t idx, uint32_t t0, uint32_t t1,
     return (hi & mask) | (lo & ~mask);
 }
 
-// The same lookup in three operations, for tables whose 16 bytes are all
-// below 128 (codebook bytes are in [0, 126]).  v_perm_b32's selector byte s
-// picks byte s of its 8-byte source for s < 8, the sign of source byte 1, 3,
-// 5 or 7 (0x00 or 0xFF) for s = 8..11, 0x00 for 12 and 0xFF for 13..15.
-// With
-//   A = perm(TA, c),  B = perm(TB, c ^ 8),
-//   TA = table bytes 0..7, TB = bytes 8..15, every byte but byte 4 of each
-//        stored complemented,
-// one of A, B is the stored byte (TA[c] for c < 8, TB[c - 8] for c >= 8)
-// and the other is 0x00 for c = 4, 12 (selector 12; stored plain) and 0xFF
-// for every other c (selectors 8..11 read the complemented, sign-set bytes
-// 1, 3, 5, 7, and 13..15 give 0xFF), so A ^ B is the table byte.
-// c: four codes 0..15, one per byte.
-__device__ __forceinline__ uint32_t lut4x(uint32_t c, uint32_t a0, uint32_t a1, uint32_t b0, uint32_t b1)
-{
-    const uint32_t a = __builtin_amdgcn_perm(a1, a0, c);
-    const uint32_t b = __builtin_amdgcn_perm(b1, b0, c ^ 0x08080808u);
-    return a ^ b;
-}
-
 // The MFMA A operand(s) one lane supplies for one group: activation bytes of
 // token lane%16 at act_pos(slot, lane/16) inside the group.
 template <int F>

@@ -56,6 +56,7 @@ constexpr int kPer = kMaxDim / kThreads;    // elements of a dim-row per thread:
 constexpr int kMaxStream = kLanes * kMaxDim;
 constexpr int kCondPer = 8 * kMaxDim / kThreads;  // condition-weight entries per thread
 constexpr int kHistPer = (2560 + kThreads - 1) / kThreads;  // Q/K/V frame entries per thread (qw + kw + vw <= 2560)
+constexpr int kMaxPhiGroups = kLanes * kMaxDim / 128;       // groups of a phi row (K = 4 * dim)
 
 __device__ __forceinline__ float sigmoid_poly(float x) { return 1.0f / (1.0f + exp_poly(-x)); }
 
@@ -208,12 +209,23 @@ __global__ __launch_bounds__(kThreads) void n3_embed_kernel(const uint8_t* raw, 
 
 // ----------------------------------------------- hyper-connection mix --
 
+// The layer's hyper-connection phi rows (RunLayerBatch, Engine.cs:2356-2364):
+// 4 pre, 4 post and 16 residual-mix outputs of three Cq4 matrices over the
+// stream's 4-bit prepared activations.  codes[m] points at the layer's first
+// row of matrix m ([rows][K / 2] codes, the archive's row-major bytes),
+// norms[m] at its fp16 group norms ([rows][K / 128]).
+struct PhiRows {
+    const uint8_t* codes[3];
+    const uint16_t* norms[3];
+    uint32_t split[4];  // the 4-bit codebook's split lookup tables (lut4x)
+    float byte_scale;   // its ByteScale
+    Act in;             // the stream's Quant.Prepare rows, K = kLanes * dim
+    int stride;
+};
+
 struct HyperArgs {
     const float* stream;
-    const float* pre_out;   // row t at t * ld4 (the layer's 4 outputs)
-    const float* post_out;  // row t at t * ld4
-    const float* res_out;   // row t at t * ld16 (the layer's 16 outputs)
-    int ld4, ld16;
+    PhiRows phi;
     const float *a_pre, *a_post, *a_res, *b_pre, *b_post, *b_res;  // the layer's entries
     int lane, dim;
     float* input;
@@ -231,41 +243,156 @@ struct HyperArgs {
     int rows;
 };
 
+// Scalar.MatMulRows' exact int32 dot (Scalar.cs:166-184) of one Cq4 row's
+// group (64 code bytes) with a group of 4-bit prepared activations (128
+// int8 in Planes order): code byte j of half h carries activation
+// 2h * 32 + j in its low nibble and (2h + 1) * 32 + j in its high nibble.
+// The codes go through lut4x to their codebook bytes (below 128, so the
+// signed byte dot is exact).
+__device__ __forceinline__ int cq4_group_dot(const uint8_t* codes, const int8_t* x, const uint32_t (&split)[4])
+{
+    const uint4* w4 = reinterpret_cast<const uint4*>(codes);
+    const uint4* x4 = reinterpret_cast<const uint4*>(x);
+    int dot = 0;
+#pragma unroll
+    for (int h = 0; h < 2; h++) {
+        const uint4 wv[2] = {w4[2 * h], w4[2 * h + 1]};
+        const uint4 lo[2] = {x4[4 * h], x4[4 * h + 1]};
+        const uint4 hi[2] = {x4[4 * h + 2], x4[4 * h + 3]};
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            const uint4& w = wv[k >> 2];
+            const uint32_t word = (k & 3) == 0 ? w.x : (k & 3) == 1 ? w.y : (k & 3) == 2 ? w.z : w.w;
+            const uint4& l = lo[k >> 2];
+            const uint4& u = hi[k >> 2];
+            const uint32_t xl = (k & 3) == 0 ? l.x : (k & 3) == 1 ? l.y : (k & 3) == 2 ? l.z : l.w;
+            const uint32_t xh = (k & 3) == 0 ? u.x : (k & 3) == 1 ? u.y : (k & 3) == 2 ? u.z : u.w;
+            const uint32_t bl = lut4x(word & 0x0F0F0F0Fu, split[0], split[1], split[2], split[3]);
+            const uint32_t bh = lut4x((word >> 4) & 0x0F0F0F0Fu, split[0], split[1], split[2], split[3]);
+            dot = __builtin_amdgcn_sdot4((int)bl, (int)xl, dot, false);
+            dot = __builtin_amdgcn_sdot4((int)bh, (int)xh, dot, false);
+        }
+    }
+    return dot;
+}
+
+// `outputs` phi rows of row t: the workgroup's threads take the (output,
+// group) pairs, each forming the group's dot and the two products of
+// Scalar.MatMulRows' chain (Scalar.cs:146-192): scaled = (HalfToSingle(norm)
+// * ByteScale) * scale[g], scaled * dot and scaled * offset[g], into
+// prod[2 * (output * groups + group) + 0 / 1].  After a barrier, lane o <
+// outputs adds them in ascending group order (accumulator += scaled * dot,
+// bias += scaled * offset) and returns accumulator - bias (other lanes
+// return 0).  first[m] is the first output of matrix m (outputs first[m] ..
+// first[m + 1] - 1 read its rows 0, 1, ...).
+__device__ __forceinline__ float phi_outputs(const PhiRows& p, int t, int K, int m0, const int (&first)[4],
+                                             float* prod)
+{
+    const int groups = K / 128, outputs = first[3] - first[0];
+    const int8_t* x = p.in.values + (size_t)t * K;
+    const float* scales = p.in.scales + (size_t)t * p.stride;
+    const float* offsets = p.in.offsets + (size_t)t * p.stride;
+    for (int u = threadIdx.x; u < outputs * groups; u += kThreads) {
+        const int o = u / groups, g = u - o * groups;
+        const int m = m0 + (o >= first[1] - first[0]) + (o >= first[2] - first[0]);
+        const int r = o + first[0] - first[m - m0];
+        const float scaled = ref_half_to_single(p.norms[m][(size_t)r * groups + g]) * p.byte_scale * scales[g];
+        const int dot = cq4_group_dot(p.codes[m] + (size_t)r * (K / 2) + g * 64, x + g * 128, p.split);
+        prod[2 * u] = scaled * (float)dot;
+        prod[2 * u + 1] = scaled * offsets[g];
+    }
+    __syncthreads();
+    float y = 0.0f;
+    const int o = threadIdx.x;
+    if (o < outputs) {
+        const float2* pr = reinterpret_cast<const float2*>(prod) + o * groups;
+        float accumulator = 0.0f, bias = 0.0f;
+        for (int g = 0; g < groups; g++) {
+            const float2 v = pr[g];
+            accumulator += v.x;
+            bias += v.y;
+        }
+        y = accumulator - bias;
+    }
+    return y;
+}
+
+// Lane l of a 16-lane row receives lane l + n (n > 0) or l - n (n < 0) of
+// its row, written only into the lanes of bank `bank` (lanes 4 * bank ..
+// 4 * bank + 3 of each row); the other lanes keep `old`.
+template <int n, int bank>
+__device__ __forceinline__ float dpp_bank_shift(float old, float v)
+{
+    constexpr int ctrl = n > 0 ? 0x100 + n : 0x110 - n;
+    return __int_as_float(
+        __builtin_amdgcn_update_dpp(__float_as_int(old), __float_as_int(v), ctrl, 0xF, 1 << bank, false));
+}
+
+// The entry of column (lane & 3) in row p of the 4 x 4 matrix held by lanes
+// e = 4a + c of each 16-lane row: lane 4p + c, reached from bank a by a row
+// shift of 4 (p - a).
+template <int p>
+__device__ __forceinline__ float column_entry(float r)
+{
+    float v = r;  // bank p holds it itself
+    if constexpr (p != 0) v = dpp_bank_shift<4 * p, 0>(v, r);
+    if constexpr (p != 1) v = dpp_bank_shift<4 * (p - 1), 1>(v, r);
+    if constexpr (p != 2) v = dpp_bank_shift<4 * (p - 2), 2>(v, r);
+    if constexpr (p != 3) v = dpp_bank_shift<4 * (p - 3), 3>(v, r);
+    return v;
+}
+
+// Lane q of the quad of 4 lanes (quad_perm [q, q, q, q]).
+template <int q>
+__device__ __forceinline__ float quad_entry(float r)
+{
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(r), q * 0x55, 0xF, 0xF, false));
+}
+
 // Sinkhorn4x4 of row t's residual-mix logits (Engine.cs:2374-2378) by one
-// wave, one lane per matrix entry (lane e = 4a + c, repeated across the
-// wave): every lane of a row or column forms the same left-to-right sum of
-// its four entries, so each normalisation is Scalar.Sinkhorn4x4's.
-__device__ __forceinline__ void sinkhorn_wave(const HyperArgs& a, int t)
+// wave, one lane per matrix entry (lane e = 4a + c of each 16-lane row, the
+// four rows alike): a matrix row is a quad of lanes and a column the lanes
+// c, 4 + c, 8 + c, 12 + c, reached through DPP.  Every lane of a row or
+// column forms the same left-to-right sum of its four entries, so each
+// normalisation is Scalar.Sinkhorn4x4's.
+__device__ __forceinline__ void sinkhorn_wave(const HyperArgs& a, int t, const float* logits)
 {
     const int lane = threadIdx.x & 63;
-    const int e = lane & 15, row = e >> 2, col = e & 3;
-    const float lg = a.a_res[0] * a.res_out[t * a.ld16 + e] + a.b_res[e];
-    const float l0 = __shfl(lg, row * 4), l1 = __shfl(lg, row * 4 + 1), l2 = __shfl(lg, row * 4 + 2),
-                l3 = __shfl(lg, row * 4 + 3);
-    float r = exp_poly(lg - fmaxf(fmaxf(l0, l1), fmaxf(l2, l3)));
+    const int e = lane & 15;
+    const float lg = logits[e];
+    const float peak = fmaxf(fmaxf(quad_entry<0>(lg), quad_entry<1>(lg)), fmaxf(quad_entry<2>(lg), quad_entry<3>(lg)));
+    float r = exp_poly(lg - peak);
     for (int it = 0; it < 20; it++) {
-        const float rs = __shfl(r, row * 4) + __shfl(r, row * 4 + 1) + __shfl(r, row * 4 + 2) + __shfl(r, row * 4 + 3);
+        const float rs = ((quad_entry<0>(r) + quad_entry<1>(r)) + quad_entry<2>(r)) + quad_entry<3>(r);
         r = r / rs;
-        const float cs = __shfl(r, col) + __shfl(r, 4 + col) + __shfl(r, 8 + col) + __shfl(r, 12 + col);
+        const float cs = ((column_entry<0>(r) + column_entry<1>(r)) + column_entry<2>(r)) + column_entry<3>(r);
         if (cs > 0.0f) r = r / cs;
     }
     if (lane < 16) a.mix[t * 16 + e] = r;
 }
 
-// RunLayerBatch's per-row mix (Engine.cs:2366-2381): hpre / postGate by
-// Sigmoid, Mix4 of the lanes into input and residual, Sinkhorn4x4 of the
-// residual-mix logits.  Workgroups 0 .. rows-1 take one row each; only the
-// layer's tail reads the mix matrix, so Sinkhorn runs in workgroups of its
-// own after them (one wave per row), beside the rows' work.  Then, on layers
-// without an engram, RunAttentionBatch's CenteredRmsFakeA8 of the residual
-// and its 2-bit Prepare (Engine.cs:2487-2490); on engram layers,
-// ApplyEngramBatch's input (Engine.cs:2404-2414): every table's GatherRow
-// (zeros for row -1), Quant.FakeA8 and the 2-bit Prepare.
+// RunLayerBatch's per-row mix (Engine.cs:2356-2381): the phi rows, hpre /
+// postGate by Sigmoid, Mix4 of the lanes into input and residual, Sinkhorn4x4
+// of the residual-mix logits.  Workgroup t < rows takes row t's 4 pre and 4
+// post outputs and the mix; only the layer's tail reads the Sinkhorn matrix,
+// so workgroup rows + t forms row t's 16 residual-mix outputs and its
+// Sinkhorn beside it.  Then, on layers without an engram,
+// RunAttentionBatch's CenteredRmsFakeA8 of the residual and its 2-bit Prepare
+// (Engine.cs:2487-2490); on engram layers, ApplyEngramBatch's input
+// (Engine.cs:2404-2414): every table's GatherRow (zeros for row -1),
+// Quant.FakeA8 and the 2-bit Prepare.
 __global__ __launch_bounds__(kThreads) void n3_hyper_kernel(HyperArgs a)
 {
+    __shared__ __align__(16) float prod[2 * 16 * kMaxPhiGroups];
+    __shared__ float logits[16];
+    const int dim = a.dim, K = kLanes * dim;
     if ((int)blockIdx.x >= a.rows) {
-        const int t = ((int)blockIdx.x - a.rows) * kWaves + (int)(threadIdx.x >> 6);
-        if (t < a.rows) sinkhorn_wave(a, t);
+        const int t = (int)blockIdx.x - a.rows;
+        const int first[4] = {0, 16, 16, 16};
+        const float y = phi_outputs(a.phi, t, K, 2, first, prod);
+        if (threadIdx.x < 16) logits[threadIdx.x] = a.a_res[0] * y + a.b_res[threadIdx.x];
+        __syncthreads();
+        if (threadIdx.x < 64) sinkhorn_wave(a, t, logits);
         return;
     }
     __shared__ __align__(16) float x[kMaxDim];
@@ -275,7 +402,6 @@ __global__ __launch_bounds__(kThreads) void n3_hyper_kernel(HyperArgs a)
     __shared__ float inv_s;
     const int t = blockIdx.x;
     const int i = threadIdx.x;
-    const int dim = a.dim;
     const float* s = a.stream + (size_t)t * kLanes * dim;
     float sv[kPer][kLanes], sn[kPer];
 #pragma unroll
@@ -287,10 +413,13 @@ __global__ __launch_bounds__(kThreads) void n3_hyper_kernel(HyperArgs a)
             sn[q] = a.norm_in[c];
         }
     }
-    if (i < 4) {
-        hpre[i] = sigmoid_poly(a.a_pre[0] * a.pre_out[t * a.ld4 + i] + a.b_pre[i] + (i == a.lane ? 4.0f : -4.0f));
-        a.post_gate[t * 4 + i] =
-            2.0f * sigmoid_poly(a.a_post[0] * a.post_out[t * a.ld4 + i] + a.b_post[i] + (i == a.lane ? 0.0f : -4.0f));
+    {
+        const int first[4] = {0, 4, 8, 8};
+        const float y = phi_outputs(a.phi, t, K, 0, first, prod);
+        if (i < 4) hpre[i] = sigmoid_poly(a.a_pre[0] * y + a.b_pre[i] + (i == a.lane ? 4.0f : -4.0f));
+        if (i >= 4 && i < 8)
+            a.post_gate[t * 4 + i - 4] =
+                2.0f * sigmoid_poly(a.a_post[0] * y + a.b_post[i - 4] + (i - 4 == a.lane ? 0.0f : -4.0f));
     }
     __syncthreads();
 #pragma unroll
@@ -591,16 +720,19 @@ __device__ __forceinline__ float wave_condition_weights(const float* input_t, co
     const int stride = cond_stride(dim);
     float acc = 0.0f;
     if (lane < 32) acc = lds_fma_chain(input_t + k * stride, cond_t + lane * stride, dim / 4, 0.0f);
-    const float w = (acc + __shfl(acc, lane + 8)) + (__shfl(acc, lane + 16) + __shfl(acc, lane + 24));
+    // lanes 0-7: their xor-partners 8, 16, 24 are lanes j + 8, j + 16, j + 24,
+    // and xor-partners 1, 2, 4 span the eight weights
+    const float a16 = lane_xor<16>(acc);
+    const float w = (acc + lane_xor<8>(acc)) + (a16 + lane_xor<8>(a16));
     float peak = w;
-    peak = fmaxf(peak, __shfl_xor(peak, 1));
-    peak = fmaxf(peak, __shfl_xor(peak, 2));
-    peak = fmaxf(peak, __shfl_xor(peak, 4));
+    peak = fmaxf(peak, lane_xor<1>(peak));
+    peak = fmaxf(peak, lane_xor<2>(peak));
+    peak = fmaxf(peak, lane_xor<4>(peak));
     const float e = exp_poly(w - peak);
-    const float p2 = e + __shfl(e, lane + 1);
-    const float p4 = p2 + __shfl(p2, lane + 2);
-    const float p8 = p4 + __shfl(p4, lane + 4);
-    const float total = __shfl(p8, 0);
+    const float p2 = e + lane_xor<1>(e);
+    const float p4 = p2 + lane_xor<2>(p2);
+    const float p8 = p4 + lane_xor<4>(p4);
+    const float total = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(p8)));
     return e * (1.0f / total);
 }
 
@@ -756,6 +888,12 @@ __global__ __launch_bounds__(kThreads) void n3_tail_kernel(TailArgs a)
             pb[q] = a.perm_b[n];
         }
     }
+    // the row's lane mix and post gates (wave-uniform), for CombineDiff4x4
+    float mix[16], pgate[kLanes];
+#pragma unroll
+    for (int e = 0; e < 16; e++) mix[e] = a.mix[t * 16 + e];
+#pragma unroll
+    for (int l = 0; l < kLanes; l++) pgate[l] = a.post_gate[t * kLanes + l];
     float cvv[kCondPer], wv[kPer][6];
 #pragma unroll
     for (int q = 0; q < kCondPer; q++) {
@@ -870,8 +1008,6 @@ __global__ __launch_bounds__(kThreads) void n3_tail_kernel(TailArgs a)
     __syncthreads();
     kron_lds(front, a.rows, wl + 2 * rr, wr + 2 * cc, a.rows, a.cols, output_rows, scratch, back);
     // Scalar.AccumulateOutput, then CombineDiff4x4 into the next stream
-    const float* m = a.mix + t * 16;
-    const float* pg = a.post_gate + t * 4;
 #pragma unroll
     for (int q = 0; q < kPer; q++) {
         const int c = col_of(q);
@@ -880,8 +1016,8 @@ __global__ __launch_bounds__(kThreads) void n3_tail_kernel(TailArgs a)
             const float y = x - uv[q];
 #pragma unroll
             for (int l = 0; l < kLanes; l++) {
-                const float o = pg[l] * y + m[4 * l] * sv[q][0] + m[4 * l + 1] * sv[q][1] + m[4 * l + 2] * sv[q][2] +
-                                m[4 * l + 3] * sv[q][3];
+                const float o = pgate[l] * y + mix[4 * l] * sv[q][0] + mix[4 * l + 1] * sv[q][1] +
+                                mix[4 * l + 2] * sv[q][2] + mix[4 * l + 3] * sv[q][3];
                 const int i = l * dim + c;
                 a.next[(size_t)t * n4 + i] = o;
                 ns[i] = o;
@@ -983,6 +1119,7 @@ struct nhip_ctx {
     const float *a_pre = nullptr, *a_post = nullptr, *a_res = nullptr, *b_pre = nullptr, *b_post = nullptr,
                 *b_res = nullptr;
     nhip_weights *phi_pre = nullptr, *phi_post = nullptr, *phi_res = nullptr;
+    const uint8_t* phi_raw[3] = {nullptr, nullptr, nullptr};  // their archive bytes on the device
     int32_t *perm_a = nullptr, *perm_b = nullptr;
     std::vector<N3Site> site;
     const float* final_norm = nullptr;
@@ -996,9 +1133,9 @@ struct nhip_ctx {
     // alternate between the two stream buffers)
     float *stream_a = nullptr, *stream_b = nullptr, *normed = nullptr, *input = nullptr, *residual = nullptr,
           *raw = nullptr, *gate = nullptr, *att = nullptr, *proj = nullptr, *key = nullptr, *stage = nullptr,
-          *ein = nullptr, *pre_out = nullptr, *post_out = nullptr, *res_out = nullptr, *post_gate = nullptr,
-          *mix = nullptr, *qs = nullptr, *logits = nullptr, *act_s = nullptr, *act_o = nullptr;
-    int8_t *act_v = nullptr, *q8 = nullptr;
+          *ein = nullptr, *post_gate = nullptr, *mix = nullptr, *qs = nullptr, *logits = nullptr, *act_s = nullptr,
+          *act_o = nullptr, *act4_s = nullptr, *act4_o = nullptr;
+    int8_t *act_v = nullptr, *act4_v = nullptr, *q8 = nullptr;  // act4: the stream's 4-bit Prepare (phi input)
     int32_t* d_in = nullptr;  // the per-row inputs of a step, kInSections x max_rows, then the engram rows
     int32_t* h_in = nullptr;  // their pinned host staging
     void* attn_ws = nullptr;
@@ -1233,8 +1370,11 @@ int32_t load_model(nhip_ctx* c)
     c->b_post = r.dense((size_t)c->layers * 4, "BPost");
     c->b_res = r.dense((size_t)c->layers * 16, "BRes");
     c->phi_pre = r.quant(4, c->layers * 4, 4 * d, "PhiPre");
+    c->phi_raw[0] = r.status ? nullptr : nhip_model_raw(c->model, r.next - 1);
     c->phi_post = r.quant(4, c->layers * 4, 4 * d, "PhiPost");
+    c->phi_raw[1] = r.status ? nullptr : nhip_model_raw(c->model, r.next - 1);
     c->phi_res = r.quant(4, c->layers * 16, 4 * d, "PhiRes");
+    c->phi_raw[2] = r.status ? nullptr : nhip_model_raw(c->model, r.next - 1);
     const float* pa = r.dense(width, "PermA");
     const float* pb = r.dense(width, "PermB");
     c->site.resize(c->site_count);
@@ -1296,9 +1436,8 @@ int32_t alloc_state(nhip_ctx* c)
         (rc = ctx_alloc(c, &c->gate, (size_t)R * ow)) || (rc = ctx_alloc(c, &c->att, (size_t)R * ow)) ||
         (rc = ctx_alloc(c, &c->proj, (size_t)R * d)) || (rc = ctx_alloc(c, &c->key, (size_t)R * d)) ||
         (rc = ctx_alloc(c, &c->stage, (size_t)R * (kEngramHistory + 1) * d)) ||
-        (rc = ctx_alloc(c, &c->ein, (size_t)R * d)) || (rc = ctx_alloc(c, &c->pre_out, (size_t)R * 4 * c->layers)) ||
-        (rc = ctx_alloc(c, &c->post_out, (size_t)R * 4 * c->layers)) ||
-        (rc = ctx_alloc(c, &c->res_out, (size_t)R * 16 * c->layers)) ||
+        (rc = ctx_alloc(c, &c->ein, (size_t)R * d)) || (rc = ctx_alloc(c, &c->act4_v, (size_t)R * sw)) ||
+        (rc = ctx_alloc(c, &c->act4_s, (size_t)R * stride4)) || (rc = ctx_alloc(c, &c->act4_o, (size_t)R * stride4)) ||
         (rc = ctx_alloc(c, &c->post_gate, (size_t)R * 4)) || (rc = ctx_alloc(c, &c->mix, (size_t)R * 16)) ||
         (rc = ctx_alloc(c, &c->q8, (size_t)R * qw)) || (rc = ctx_alloc(c, &c->qs, (size_t)R * c->heads)) ||
         (rc = ctx_alloc(c, &c->logits, (size_t)R * c->vocab)) || (rc = ctx_alloc(c, &c->act_v, (size_t)R * sw)) ||
@@ -1400,34 +1539,40 @@ int32_t enqueue_step(nhip_ctx* c, int rows, int heads, int k, bool argmax)
               kw = KV * c->qk, vw = KV * c->vd, ow = H * c->vd, all = qw + kw + vw;
     const int stride4 = stride_of(sw), stride_d = stride_of(d), stride_o = stride_of(ow);
     const Act act{c->act_v, c->act_s, c->act_o};
+    const Act act4{c->act4_v, c->act4_s, c->act4_o};
     int32_t rc;
     float* cur = c->stream_a;
     float* nxt = c->stream_b;
     // EngineCore's embeddingScale = sqrt(dim) (Engine.cs:123), host sqrtf
     const float emb_scale_m1 = std::sqrt((float)d) - 1.0f;
     hipLaunchKernelGGL(n3_embed_kernel, dim3(rows), dim3(kThreads), 0, s, c->embedding_raw, c->vocab, d,
-                       c->embedding_bits, c->book4, in(c, c->d_in, kInTokens), emb_scale_m1, cur, act, stride4);
+                       c->embedding_bits, c->book4, in(c, c->d_in, kInTokens), emb_scale_m1, cur, act4, stride4);
     NHIP_CHECK_HIP(hipGetLastError());
     for (int l = 0; l < L; l++) {
         const N3Layer& w = c->layer[l];
         // hyper-connection phi (RunLayerBatch, Engine.cs:2356-2364): the
-        // three matrices in one launch (every layer's rows; this layer's are
-        // read back)
-        const nhip_weights* phw[3] = {c->phi_pre, c->phi_post, c->phi_res};
-        float* phy[3] = {c->pre_out, c->post_out, c->res_out};
-        const int32_t phl[3] = {4 * L, 4 * L, 16 * L};
-        if ((rc = nhip_matmul_batch_dev(phw, 3, c->act_v, c->act_s, c->act_o, stride4, rows, phy, phl, s))) return rc;
+        // layer's 4 + 4 + 16 rows, formed by the mix kernel itself
+        PhiRows phi{};
+        const int per[3] = {4, 4, 16}, totals[3] = {4 * L, 4 * L, 16 * L};
+        for (int m = 0; m < 3; m++) {
+            phi.codes[m] = c->phi_raw[m] + (size_t)l * per[m] * (sw / 2);
+            phi.norms[m] = reinterpret_cast<const uint16_t*>(c->phi_raw[m] + (size_t)totals[m] * (sw / 2)) +
+                           (size_t)l * per[m] * (sw / 128);
+        }
+        std::memcpy(phi.split, c->phi_pre->split_table, sizeof(phi.split));
+        phi.byte_scale = c->phi_pre->byte_scale;
+        phi.in = act4;
+        phi.stride = stride4;
         int site = -1;
         for (int k2 = 0; k2 < c->site_count; k2++)
             if (c->sites[k2] == l) site = k2;
         const N3Site* st = site >= 0 ? &c->site[site] : nullptr;
-        HyperArgs ha{cur, c->pre_out + l * 4, c->post_out + l * 4, c->res_out + l * 16, 4 * L, 16 * L,
-                     c->a_pre + l, c->a_post + l, c->a_res + l, c->b_pre + 4 * l, c->b_post + 4 * l,
+        HyperArgs ha{cur, phi, c->a_pre + l, c->a_post + l, c->a_res + l, c->b_pre + 4 * l, c->b_post + 4 * l,
                      c->b_res + 16 * l, l % kLanes, d, c->input, c->residual, c->post_gate, c->mix, w.norm_in,
                      st ? st->tables : nullptr, st ? st->table_rows : 0, st ? st->table_cols : 0,
                      st ? st->table_bits : 0, c->engram_tables, st && st->table_bits == 2 ? c->book2 : c->book4,
                      in_erows(c, c->d_in), act, stride_d, rows};
-        hipLaunchKernelGGL(n3_hyper_kernel, dim3(rows + (rows + kWaves - 1) / kWaves), dim3(kThreads), 0, s, ha);
+        hipLaunchKernelGGL(n3_hyper_kernel, dim3(2 * rows), dim3(kThreads), 0, s, ha);
         NHIP_CHECK_HIP(hipGetLastError());
         EngramArgs ea{};
         if (st) {  // engram (ApplyEngramBatch, Engine.cs:2399-2463)
@@ -1489,7 +1634,8 @@ int32_t enqueue_step(nhip_ctx* c, int rows, int heads, int k, bool argmax)
         TailArgs ta{c->residual, c->proj, w.post_norm, w.attn_gate, w.pre_hada, c->perm_a, c->perm_b, w.d1, w.d2,
                     w.b2, w.d3, w.d4, w.w1a, w.w1b, w.w2a, w.w2b, w.w3a, w.w3b, w.cond_v, w.cond_u, d, c->hada_rows,
                     c->hada_cols, cur, c->mix, c->input, c->post_gate, nxt,
-                    last ? in(c, c->d_in, kInHeadOf) : nullptr, c->final_norm, act, last ? stride_d : stride4};
+                    last ? in(c, c->d_in, kInHeadOf) : nullptr, c->final_norm, last ? act : act4,
+                    last ? stride_d : stride4};
         hipLaunchKernelGGL(n3_tail_kernel, dim3(rows), dim3(kThreads), c->tail_lds, s, ta);
         NHIP_CHECK_HIP(hipGetLastError());
         std::swap(cur, nxt);
