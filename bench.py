@@ -512,6 +512,21 @@ def needle3_loop(args, threads: int) -> dict:
 
             run16()
             dec16 = min(run16() for _ in range(3))
+        # one sequence alone: the step's latency, the figure a single user waits per token
+        with BatchedEngine(model, context_length=prompt_len + new, chunk_size=64, slots=1, max_chunks=8) as eng1:
+            one = np.zeros(1, dtype=np.int32)
+
+            def run1():
+                eng1.reset_slot(0)
+                eng1.feed_slot(0, prompts[0, :-1], compute_logits=False)
+                _, _, _, t1 = eng1.forward_batch(prompts[:1, -1], one, one, logits=False, argmax=True)
+                t0 = time.perf_counter()
+                for _ in range(new - 1):
+                    _, _, _, t1 = eng1.forward_batch(t1, one, one, logits=False, argmax=True)
+                return time.perf_counter() - t0
+
+            run1()
+            dec1 = min(run1() for _ in range(3))
     steps = new - 1
     ms = dec / steps * 1e3
     out = {"workload": "greedy decode of 3 slots, Needle 3 geometry (20 layers, hidden 768, 12/2 heads x 48/64, "
@@ -521,9 +536,11 @@ def needle3_loop(args, threads: int) -> dict:
            "weights_GBps_per_step": round(step_bytes / (ms * 1e-3) / 1e9, 2),
            "frac_hbm_peak": round(step_bytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 5),
            "slots16": {"row_tokens_per_s": round(wide * steps / dec16, 1),
-                       "ms_per_step": round(dec16 / steps * 1e3, 4)}}
+                       "ms_per_step": round(dec16 / steps * 1e3, 4)},
+           "slots1": {"row_tokens_per_s": round(steps / dec1, 1), "ms_per_step": round(dec1 / steps * 1e3, 4)}}
     print(f"# needle3 decode: {out['row_tokens_per_s']} row-tokens/s, {ms:.3f} ms/step, prefill {pre * 1e3:.1f} ms; "
-          f"16 slots: {out['slots16']['row_tokens_per_s']} row-tokens/s, {out['slots16']['ms_per_step']} ms/step",
+          f"16 slots: {out['slots16']['row_tokens_per_s']} row-tokens/s, {out['slots16']['ms_per_step']} ms/step; "
+          f"1 slot: {out['slots1']['ms_per_step']} ms/step",
           file=sys.stderr, flush=True)
     if not args.no_cpu:
         from oracle import needle3 as M

@@ -836,8 +836,19 @@ __device__ __forceinline__ void kron_rows(const float* z, int active, const floa
 // factors are staged in LDS.  The sums of PostNormAdd, the norms and the
 // condition weights run in the AVX2 tier's order (wave_v256_sum,
 // wave_condition_weights), and PostNormAdd adds with its Vector256 FMA.
-__global__ __launch_bounds__(kThreads) void n3_tail_kernel(TailArgs a)
+// The first loads' pointers also travel as leading arguments, which gfx950
+// preloads into SGPRs (kernarg preload; a struct argument is never
+// preloaded), so those loads issue without an argument-segment round trip.
+__global__ __launch_bounds__(kThreads) void n3_tail_kernel(const float* h_proj, float* h_residual,
+                                                           const float* h_post_norm, const float* h_pre_norm,
+                                                           const float* h_mix, const float* h_post_gate, TailArgs a)
 {
+    a.proj = h_proj;
+    a.residual = h_residual;
+    a.post_norm = h_post_norm;
+    a.pre_norm = h_pre_norm;
+    a.mix = h_mix;
+    a.post_gate = h_post_gate;
     extern __shared__ __align__(16) float lds[];
     const int width = a.rows * a.cols, dim = a.dim, rr = a.rows * a.rows, cc = a.cols * a.cols, n4 = kLanes * dim;
     float* front = lds;               // width (>= the padded input)
@@ -1636,7 +1647,8 @@ int32_t enqueue_step(nhip_ctx* c, int rows, int heads, int k, bool argmax)
                     c->hada_cols, cur, c->mix, c->input, c->post_gate, nxt,
                     last ? in(c, c->d_in, kInHeadOf) : nullptr, c->final_norm, last ? act : act4,
                     last ? stride_d : stride4};
-        hipLaunchKernelGGL(n3_tail_kernel, dim3(rows), dim3(kThreads), c->tail_lds, s, ta);
+        hipLaunchKernelGGL(n3_tail_kernel, dim3(rows), dim3(kThreads), c->tail_lds, s, ta.proj, ta.residual,
+                           ta.post_norm, ta.pre_norm, ta.mix, ta.post_gate, ta);
         NHIP_CHECK_HIP(hipGetLastError());
         std::swap(cur, nxt);
     }
