@@ -69,6 +69,9 @@ struct DecodeAttnParams {
     float* wkscale;
     int8_t* wvalues;
     float* wvscale;
+    // the whole-row kernel's Needle 3 form: the step's raw Q/K/V projections
+    // and what turns them into the query and the cache row
+    Needle3AttnInputs n3;
     int32_t rows, heads, kv_heads, qk, slots, capacity, max_chunks, lmax, kv_per_block;
     float inv_sqrt;
     int32_t cus;         // compute units of the device (the chunk kernel's placement period)
@@ -619,12 +622,20 @@ constexpr int kRowMaxCapacity = 512;
 constexpr int kRowMaxChunks = kRowMaxCapacity / 16;  // the plan makes at most count/16 chunks
 constexpr int kRowUnits = kRowMaxCapacity * 4 / kThreads;  // key pieces per thread
 constexpr int kPostRows = 4;
+// the row kernel's forms: q given, the decoder's step (POST), Needle 3's step (N3)
+constexpr int kRowPlain = 0, kRowPost = 1, kRowNeedle3 = 2;
 
-template <bool POST>
+template <int MODE>
 __global__ __launch_bounds__(kThreads) void decode_attention_row_kernel(ATTN_HEAD_PARAMS, DecodeAttnParams p)
 {
+    constexpr bool POST = MODE == kRowPost;
+    constexpr bool N3 = MODE == kRowNeedle3;
+    constexpr bool SUB = POST || N3;                 // positions written in this launch come from LDS
+    constexpr int kSub = POST ? kPostRows : 1;       // N3: only the row's own position
     if constexpr (POST)
         ATTN_TAKE_HEAD(p, qkv, positions);
+    else if constexpr (N3)
+        ATTN_TAKE_HEAD(p, n3.raw, positions);
     else
         ATTN_TAKE_HEAD(p, q, qscale);
     // scores, then e_s; e_s * valueScale_s (each padded by kVBlock floats:
@@ -637,9 +648,10 @@ __global__ __launch_bounds__(kThreads) void decode_attention_row_kernel(ATTN_HEA
     __shared__ float csum[kRowMaxChunks];
     __shared__ float cwt[kRowMaxChunks];
     __shared__ __align__(16) uint32_t q_lds[16];
-    __shared__ __align__(16) uint32_t sub_k[POST ? kPostRows : 1][16];  // POST: key / value heads of the
-    __shared__ __align__(16) uint32_t sub_v[POST ? kPostRows : 1][16];  // positions written in this launch
-    __shared__ float sub_ks[POST ? kPostRows : 1], sub_vs[POST ? kPostRows : 1], q_scale[1];
+    __shared__ __align__(16) uint32_t sub_k[kSub][16];  // POST, N3: key / value heads of the
+    __shared__ __align__(16) uint32_t sub_v[kSub][16];  // positions written in this launch
+    __shared__ float sub_ks[kSub], sub_vs[kSub], q_scale[1];
+    __shared__ float n3_red[N3 ? 3 : 1][64], n3_val[N3 ? 3 : 1][64];  // N3: per-unit norm and RoPE rows
 
     const int row = blockIdx.x;
     const int h = blockIdx.y;
@@ -686,12 +698,55 @@ __global__ __launch_bounds__(kThreads) void decode_attention_row_kernel(ATTN_HEA
             rslot[r] = __builtin_amdgcn_readlane(mslot, r);
         }
     }
+    // N3 units: wave 0 the query head h, wave 1 the key head and wave 2 the
+    // value head of the row (the step's rows are one per slot): the row's
+    // projection, the taps and the norm scales load now, the slot's two
+    // previous frames and the RoPE factors once the slot and position are in
+    const int n3_part = tid >> 6;  // 0 query, 1 key, 2 value, 3 none
+    const int n3_n = n3_part == 2 ? 64 : p.qk;
+    const int n3_qw = p.heads * p.qk, n3_kw = p.kv_heads * p.qk;
+    const int n3_all = n3_qw + n3_kw + p.kv_heads * 64;
+    const int n3_W = n3_part == 0 ? n3_qw : (n3_part == 1 ? n3_kw : p.kv_heads * 64);
+    const int n3_base = n3_part == 0 ? 0 : (n3_part == 1 ? n3_qw : n3_qw + n3_kw);
+    const int n3_off = (n3_part == 0 ? h : kv) * n3_n;
+    const bool n3_lane = n3_part < 3 && e < n3_n;
+    float n3_x2 = 0.0f, n3_x1 = 0.0f, n3_x0 = 0.0f, n3_t0 = 0.0f, n3_t1 = 0.0f, n3_t2 = 0.0f, n3_sc = 0.0f;
+    float n3_cs = 0.0f, n3_sn = 0.0f;
+    int n3_pos = 0;
+    if constexpr (N3) {
+        n3_pos = uniform_load(p.positions, row);
+        if (n3_lane) {
+            n3_x2 = p.n3.raw[(size_t)row * n3_all + n3_base + n3_off + e];
+            // (selected, not indexed: a runtime index into the argument's
+            // array would copy it to scratch)
+            const float* taps = (n3_part == 0 ? p.n3.taps[0] : (n3_part == 1 ? p.n3.taps[1] : p.n3.taps[2])) + n3_off + e;
+            n3_t0 = taps[0];
+            n3_t1 = taps[n3_W];
+            n3_t2 = taps[2 * n3_W];
+            if (n3_part < 2) n3_sc = (n3_part == 0 ? p.n3.q_norm : p.n3.k_norm)[e];
+        }
+    }
     float* dst = p.out + ((size_t)row * p.heads + h) * 64;
     const bool valid = (slot_in >= 0) & (slot_in < p.slots) & (first_in >= 0) & (count_in >= 1) &
                        (count_in <= p.capacity - first_in);
     const int slot = valid ? slot_in : 0;
     const int first = valid ? first_in : 0;
     const int count = valid ? count_in : 1;
+    const bool n3_row_ok = (slot_in >= 0) & (slot_in < p.slots) & (n3_pos >= 0) & (n3_pos < p.capacity);
+    if constexpr (N3) {
+        if (n3_lane) {
+            // frame 0, then frame 1 (the latest) of the slot's Q/K/V history
+            const float* hist = p.n3.history + (size_t)slot * 2 * n3_all + 2 * n3_base;
+            n3_x1 = hist[n3_W + n3_off + e];
+            n3_x0 = hist[n3_off + e];
+            if (n3_part < 2) {
+                const int half = n3_n / 2;
+                const size_t rp = (size_t)(n3_row_ok ? n3_pos : 0) * half + (e < half ? e : e - half);
+                n3_cs = p.n3.rope_cos[rp];
+                n3_sn = p.n3.rope_sin[rp];
+            }
+        }
+    }
     int length;
     const int needed = plan(count, p.max_chunks, &length);  // count <= capacity <= 512: needed <= 32
     const uint32_t mag_len = magic((uint32_t)length);       // s < 512: s / length is exact
@@ -703,8 +758,13 @@ __global__ __launch_bounds__(kThreads) void decode_attention_row_kernel(ATTN_HEA
     // (bit r of `subs`, at span position rel[r]); the same in every thread.
     // Then the RoPE factors of the query and key units.
     uint32_t subs = 0u;
-    int rel[kPostRows];
+    int rel[kSub];
     int pos_row = 0;
+    if constexpr (N3) {
+        rel[0] = n3_pos - first;
+        subs = (uint32_t)(n3_row_ok & (slot_in == slot) & (rel[0] >= 0) & (rel[0] < count));
+        pos_row = n3_pos;
+    }
     if constexpr (POST) {
 #pragma unroll
         for (int r = 0; r < kPostRows; r++) {
@@ -716,7 +776,7 @@ __global__ __launch_bounds__(kThreads) void decode_attention_row_kernel(ATTN_HEA
 
     uint32_t qword = 0u;
     float qsc = 0.0f;
-    if constexpr (!POST) {
+    if constexpr (!SUB) {
         qword = tid < qk / 4 ? reinterpret_cast<const uint32_t*>(p.q + ((size_t)row * p.heads + h) * qk)[tid] : 0u;
         qsc = p.qscale[(size_t)row * p.heads + h] * p.inv_sqrt;
     }
@@ -784,12 +844,55 @@ __global__ __launch_bounds__(kThreads) void decode_attention_row_kernel(ATTN_HEA
                 if (e == 0) (value ? p.wvscale : p.wkscale)[cell] = scale;
             }
         }
+    } else if constexpr (N3) {
+        // EngineCore.TapsAndAttentionHeadsSingle (Engine.cs:1302-1387) for
+        // the row's own units, with needle3_inputs_kernel's arithmetic: the
+        // three-tap convolution (Scalar.Taps3), ZeroCenteredRms of query and
+        // key heads (sum of squares in the AVX2 tier's order) and RoPE on
+        // lanes i and i + n/2, then QuantizeInt8 over the head
+        if (n3_part < 3) {  // uniform per wave
+            float x = n3_lane ? n3_t0 * n3_x2 + n3_t1 * n3_x1 + n3_t2 * n3_x0 : 0.0f;
+            if (n3_part < 2) {
+                n3_red[n3_part][e] = x;
+                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+                __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+                const float sum = wave_v256_sum(n3_red[n3_part], n3_red[n3_part], n3_n);
+                const float inverse = 1.0f / sqrtf(sum / (float)n3_n + 1e-6f);
+                x = n3_lane ? (1.0f + n3_sc) * x * inverse : 0.0f;
+                n3_val[n3_part][e] = x;
+                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+                __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+                const int half = n3_n / 2;
+                if (n3_lane) {
+                    const int i = e < half ? e : e - half;
+                    const float a = n3_val[n3_part][i], b = n3_val[n3_part][half + i];
+                    x = e < half ? a * n3_cs - b * n3_sn : b * n3_cs + a * n3_sn;
+                }
+            }
+            const float m = wave_max(n3_lane ? fabsf(x) : 0.0f);
+            const float scale = m > 0.0f ? m / 127.0f : 1.0f;
+            const float inverse = 1.0f / scale;
+            const int8_t qv = static_cast<int8_t>(ref_quantize_one(x, inverse));
+            if (n3_part == 0) {
+                reinterpret_cast<int8_t*>(q_lds)[e] = n3_lane ? qv : static_cast<int8_t>(0);
+                if (e == 0) q_scale[0] = scale;
+            } else {
+                const bool value = n3_part == 2;
+                if (n3_lane) reinterpret_cast<int8_t*>(value ? sub_v[0] : sub_k[0])[e] = qv;
+                if (e == 0) (value ? sub_vs : sub_ks)[0] = scale;
+                if (n3_row_ok && h % group == 0) {  // the row's cache row, once per kv head
+                    const size_t cell = ((size_t)slot_in * p.capacity + n3_pos) * p.kv_heads + kv;
+                    if (n3_lane) (value ? p.wvalues : p.wkeys)[cell * n3_n + e] = qv;
+                    if (e == 0) (value ? p.wvscale : p.wkscale)[cell] = scale;
+                }
+            }
+        }
     } else {
         if (tid < 16) q_lds[tid] = qword;
     }
     if (tid < kRowMaxChunks) peak_key[tid] = order_key(-INFINITY);
     __syncthreads();
-    if constexpr (POST) qsc = q_scale[0] * p.inv_sqrt;
+    if constexpr (SUB) qsc = q_scale[0] * p.inv_sqrt;
     const uint4 qv = *reinterpret_cast<const uint4*>(q_lds + 4 * qslot);
 #pragma unroll
     for (int k = 0; k < kRowUnits; k++) {
@@ -797,9 +900,9 @@ __global__ __launch_bounds__(kThreads) void decode_attention_row_kernel(ATTN_HEA
         const int u = k * kThreads + tid;
         const bool ok = u < units;  // whole aligned 4-lane groups
         const int s = min(u, units - 1) >> 2;
-        if constexpr (POST) {
+        if constexpr (SUB) {
 #pragma unroll
-            for (int r = 0; r < kPostRows; r++) {
+            for (int r = 0; r < kSub; r++) {
                 if (((subs >> r) & 1u) && s == rel[r]) {
                     kw[k] = *reinterpret_cast<const uint4*>(&sub_k[r][4 * qslot]);
                     sv[k] = (lslot & 1) ? sub_vs[r] : sub_ks[r];
@@ -849,9 +952,9 @@ __global__ __launch_bounds__(kThreads) void decode_attention_row_kernel(ATTN_HEA
         // POST: the positions this launch writes come from the workgroup's
         // own rows, not from the cache
         auto substitute = [&](int s0) {
-            if constexpr (POST) {
+            if constexpr (SUB) {
 #pragma unroll
-                for (int r = 0; r < kPostRows; r++) {
+                for (int r = 0; r < kSub; r++) {
                     const int jj = rel[r] - (b + s0);
                     if (((subs >> r) & 1u) && jj >= 0 && jj < kVBlock) {
                         const uint32_t w = sub_v[r][vj];
@@ -1060,8 +1163,52 @@ int32_t attention_decode_post_impl(const AttnPostInputs& in, int32_t rows, int32
     p.capacity = capacity;
     p.max_chunks = max_chunks;
     p.inv_sqrt = static_cast<float>(1.0 / std::sqrt(64.0));
-    hipLaunchKernelGGL(decode_attention_row_kernel<true>, dim3(rows, heads), dim3(kThreads), 0, stream,
+    hipLaunchKernelGGL(decode_attention_row_kernel<kRowPost>, dim3(rows, heads), dim3(kThreads), 0, stream,
                        ATTN_HEAD_ARGS(p, p.qkv, p.positions), p);
+    NHIP_CHECK_HIP(hipGetLastError());
+    return NHIP_OK;
+}
+
+int32_t attention_decode_needle3_impl(const Needle3AttnInputs& in, int32_t rows, int32_t heads, int32_t kv_heads,
+                                      int32_t qk_dim, int32_t v_dim, int8_t* d_keys, float* d_key_scales,
+                                      int8_t* d_values, float* d_value_scales, int32_t slots, int32_t capacity,
+                                      const int32_t* d_row_slot, const int32_t* d_row_pos,
+                                      const int32_t* d_row_first, const int32_t* d_row_count, int32_t max_chunks,
+                                      float* d_out, hipStream_t stream)
+{
+    if (rows < 1 || capacity > kRowMaxCapacity || v_dim != 64) return 1;
+    NHIP_REQUIRE(heads > 0 && kv_heads > 0 && heads % kv_heads == 0 && slots > 0 && capacity > 0 && max_chunks >= 1,
+                 "attention: bad shape");
+    NHIP_REQUIRE(qk_dim == 48 || qk_dim == 64, "attention: qk_dim must be 48 or 64 (got %d)", qk_dim);
+    NHIP_REQUIRE(in.raw && in.taps[0] && in.taps[1] && in.taps[2] && in.q_norm && in.k_norm && in.rope_cos &&
+                     in.rope_sin && in.history && d_keys && d_key_scales && d_values && d_value_scales &&
+                     d_row_slot && d_row_pos && d_row_first && d_row_count && d_out,
+                 "attention: null pointer");
+    DecodeAttnParams p{};
+    p.keys = d_keys;
+    p.kscale = d_key_scales;
+    p.values = d_values;
+    p.vscale = d_value_scales;
+    p.wkeys = d_keys;
+    p.wkscale = d_key_scales;
+    p.wvalues = d_values;
+    p.wvscale = d_value_scales;
+    p.row_slot = d_row_slot;
+    p.row_first = d_row_first;
+    p.row_count = d_row_count;
+    p.positions = d_row_pos;
+    p.n3 = in;
+    p.out = d_out;
+    p.rows = rows;
+    p.heads = heads;
+    p.kv_heads = kv_heads;
+    p.qk = qk_dim;
+    p.slots = slots;
+    p.capacity = capacity;
+    p.max_chunks = max_chunks;
+    p.inv_sqrt = static_cast<float>(1.0 / std::sqrt(static_cast<double>(qk_dim)));
+    hipLaunchKernelGGL(decode_attention_row_kernel<kRowNeedle3>, dim3(rows, heads), dim3(kThreads), 0, stream,
+                       ATTN_HEAD_ARGS(p, p.n3.raw, p.positions), p);
     NHIP_CHECK_HIP(hipGetLastError());
     return NHIP_OK;
 }
@@ -1133,7 +1280,7 @@ int32_t attention_decode_impl(const int8_t* d_q, const float* d_qscale, int32_t 
     NHIP_REQUIRE(!d_q_out || (d_qs_out && max_chunks == 1 && head_blocks == 1),
                  "attention: a quantized output needs max_chunks 1 and all heads in one block");
     if (!d_q_out && capacity <= kRowMaxCapacity) {  // every count <= capacity: one workgroup per (row, head)
-        hipLaunchKernelGGL(decode_attention_row_kernel<false>, dim3(rows, heads), dim3(kThreads), 0, stream,
+        hipLaunchKernelGGL(decode_attention_row_kernel<kRowPlain>, dim3(rows, heads), dim3(kThreads), 0, stream,
                            ATTN_HEAD_ARGS(p, p.q, p.qscale), p);
         NHIP_CHECK_HIP(hipGetLastError());
         return NHIP_OK;

@@ -181,6 +181,32 @@ int32_t attention_decode_post_impl(const AttnPostInputs& in, int32_t rows, int32
                                    int32_t slots, int32_t capacity, const int32_t* d_row_slot,
                                    const int32_t* d_row_first, const int32_t* d_row_count, int32_t max_chunks,
                                    float* d_out, hipStream_t stream);
+// Needle 3's attention inputs and decode attention in one launch (the
+// whole-row kernel's Needle 3 form), for steps whose rows are one per slot
+// and caches of at most 512 positions: each (row, query head) workgroup forms
+// its query head, and the row's key and value heads, from the raw Q/K/V
+// projections as needle3_attention_inputs_impl does (three-tap convolution
+// over the slot's two previous frames, ZeroCenteredRms and RoPE of the query
+// and key heads, QuantizeInt8), attends over its span with its own key and
+// value in place of the cache at the row's position, and the group's first
+// query head writes that key and value to the cache.  The slots' frames are
+// left for the caller to move on.  Returns 1 without launching when it does
+// not apply (caches over 512 positions, value heads other than 64).
+struct Needle3AttnInputs {
+    const float* raw;       // [rows][qw + kw + vw]
+    const float* taps[3];   // query, key, value taps: [3][width] each
+    const float* q_norm;    // [qk]
+    const float* k_norm;    // [qk]
+    const float* rope_cos;  // [capacity][qk / 2]
+    const float* rope_sin;
+    const float* history;   // [slots][2][qw], [2][kw], [2][vw]: frame 0, then frame 1
+};
+int32_t attention_decode_needle3_impl(const Needle3AttnInputs& in, int32_t rows, int32_t heads, int32_t kv_heads,
+                                      int32_t qk_dim, int32_t v_dim, int8_t* d_keys, float* d_key_scales,
+                                      int8_t* d_values, float* d_value_scales, int32_t slots, int32_t capacity,
+                                      const int32_t* d_row_slot, const int32_t* d_row_pos,
+                                      const int32_t* d_row_first, const int32_t* d_row_count, int32_t max_chunks,
+                                      float* d_out, hipStream_t stream);
 // nhip_needle3_attention_inputs_dev; with_history false leaves the slots'
 // Q/K/V frames to the caller, which moves them on after every row of the
 // step has read them.

@@ -1159,7 +1159,7 @@ struct nhip_ctx {
     hipStream_t stream_h = nullptr;
     struct Graph {
         int rows, heads, k;
-        bool argmax;
+        bool argmax, single_runs;
         hipGraphExec_t exec;
     };
     std::vector<Graph> graphs;  // captured steps, by their shape
@@ -1543,7 +1543,7 @@ void engram_rows(const nhip_ctx* c, const int32_t* tokens, const int32_t* row_sl
 // the gate with the output matmul's Prepare, the output matmul, and the
 // layer tail (PostNormAdd, MLP, CombineDiff4x4, the next layer's norm and
 // Prepare -- or the head rows' after the last layer).
-int32_t enqueue_step(nhip_ctx* c, int rows, int heads, int k, bool argmax)
+int32_t enqueue_step(nhip_ctx* c, int rows, int heads, int k, bool argmax, bool single_runs)
 {
     hipStream_t s = c->stream_h;
     const int d = c->dim, sw = kLanes * d, L = c->layers, H = c->heads, KV = c->kv, qw = H * c->qk,
@@ -1620,20 +1620,34 @@ int32_t enqueue_step(nhip_ctx* c, int rows, int heads, int k, bool argmax)
         float* kscale = c->key_scales + lcell * KV;
         float* vscale = c->value_scales + lcell * KV;
         float* qkv_hist = c->qkv_hist + (size_t)l * c->slots * 2 * all;
-        if ((rc = needle3_attention_inputs_impl(c->raw, rows, H, KV, c->qk, c->vd, w.q_taps, w.k_taps, w.v_taps,
-                                                w.q_norm, w.k_norm, c->rope_cos, c->rope_sin, qkv_hist,
-                                                in(c, c->d_in, kInSlots), in(c, c->d_in, kInPos), c->slots,
-                                                c->capacity, c->q8, c->qs, keys, kscale, values, vscale, false, s)))
-            return rc;
         // the layer's span (Blocks.cs:973-978): global layers from 0, the
         // others over the window ending at the row
         const bool global = ((c->global_mask >> l) & 1) || c->window == 0;
-        if ((rc = attention_decode_impl(c->q8, c->qs, rows, H, KV, c->qk, keys, kscale, values, vscale, c->slots,
-                                        c->capacity, in(c, c->d_in, kInSlots),
-                                        in(c, c->d_in, global ? kInFirst : kInFirstW),
-                                        in(c, c->d_in, global ? kInCount : kInCountW), c->max_chunks, c->attn_ws,
-                                        c->attn_ws_bytes, c->att, nullptr, nullptr, s)))
-            return rc;
+        const int32_t* first = in(c, c->d_in, global ? kInFirst : kInFirstW);
+        const int32_t* count = in(c, c->d_in, global ? kInCount : kInCountW);
+        // steps whose rows are one per slot: the attention inputs inside the
+        // attention launch; otherwise (runs of rows, long caches) two launches
+        int32_t fused = 1;
+        if (single_runs) {
+            const Needle3AttnInputs n3in{c->raw, {w.q_taps, w.k_taps, w.v_taps}, w.q_norm, w.k_norm,
+                                         c->rope_cos, c->rope_sin, qkv_hist};
+            fused = attention_decode_needle3_impl(n3in, rows, H, KV, c->qk, c->vd, keys, kscale, values, vscale,
+                                                  c->slots, c->capacity, in(c, c->d_in, kInSlots),
+                                                  in(c, c->d_in, kInPos), first, count, c->max_chunks, c->att, s);
+            if (fused < 0) return fused;
+        }
+        if (fused == 1) {
+            if ((rc = needle3_attention_inputs_impl(c->raw, rows, H, KV, c->qk, c->vd, w.q_taps, w.k_taps, w.v_taps,
+                                                    w.q_norm, w.k_norm, c->rope_cos, c->rope_sin, qkv_hist,
+                                                    in(c, c->d_in, kInSlots), in(c, c->d_in, kInPos), c->slots,
+                                                    c->capacity, c->q8, c->qs, keys, kscale, values, vscale, false,
+                                                    s)))
+                return rc;
+            if ((rc = attention_decode_impl(c->q8, c->qs, rows, H, KV, c->qk, keys, kscale, values, vscale, c->slots,
+                                            c->capacity, in(c, c->d_in, kInSlots), first, count, c->max_chunks,
+                                            c->attn_ws, c->attn_ws_bytes, c->att, nullptr, nullptr, s)))
+                return rc;
+        }
         // the gate also moves the slots' Q/K/V frames on, after attention's
         // inputs have read them
         const QkvHistArgs qh{qkv_hist, c->raw, in(c, c->d_in, kInSlots), in(c, c->d_in, kInRunStart),
@@ -1671,16 +1685,17 @@ int32_t enqueue_step(nhip_ctx* c, int rows, int heads, int k, bool argmax)
 constexpr int kMaxGraphRows = 16;
 constexpr size_t kMaxGraphs = 64;
 
-int32_t run_step(nhip_ctx* c, int rows, int heads, int k, bool argmax)
+int32_t run_step(nhip_ctx* c, int rows, int heads, int k, bool argmax, bool single_runs)
 {
     static const bool graphs_enabled = [] {
         const char* e = getenv("NHIP_ENGINE_GRAPHS");
         return !(e && e[0] == '0');
     }();
-    if (!graphs_enabled || rows > kMaxGraphRows) return enqueue_step(c, rows, heads, k, argmax);
+    if (!graphs_enabled || rows > kMaxGraphRows) return enqueue_step(c, rows, heads, k, argmax, single_runs);
     hipGraphExec_t exec = nullptr;
     for (const nhip_ctx::Graph& g : c->graphs)
-        if (g.rows == rows && g.heads == heads && g.k == k && g.argmax == argmax) exec = g.exec;
+        if (g.rows == rows && g.heads == heads && g.k == k && g.argmax == argmax && g.single_runs == single_runs)
+            exec = g.exec;
     if (!exec) {
         if (c->graphs.size() >= kMaxGraphs) {  // drop the oldest
             NHIP_CHECK_HIP(hipStreamSynchronize(c->stream_h));
@@ -1689,7 +1704,7 @@ int32_t run_step(nhip_ctx* c, int rows, int heads, int k, bool argmax)
         }
         hipGraph_t g;
         NHIP_CHECK_HIP(hipStreamBeginCapture(c->stream_h, hipStreamCaptureModeThreadLocal));
-        const int32_t rc = enqueue_step(c, rows, heads, k, argmax);
+        const int32_t rc = enqueue_step(c, rows, heads, k, argmax, single_runs);
         hipError_t e = hipStreamEndCapture(c->stream_h, &g);
         if (rc) {
             if (e == hipSuccess) (void)hipGraphDestroy(g);
@@ -1699,7 +1714,7 @@ int32_t run_step(nhip_ctx* c, int rows, int heads, int k, bool argmax)
         e = hipGraphInstantiate(&exec, g, nullptr, nullptr, 0);
         (void)hipGraphDestroy(g);
         NHIP_CHECK_HIP(e);
-        c->graphs.push_back(nhip_ctx::Graph{rows, heads, k, argmax, exec});
+        c->graphs.push_back(nhip_ctx::Graph{rows, heads, k, argmax, single_runs, exec});
     }
     NHIP_CHECK_HIP(hipGraphLaunch(exec, c->stream_h));
     return NHIP_OK;
@@ -1816,6 +1831,7 @@ int32_t nhip_step(nhip_ctx* c, const int32_t* tokens, const int32_t* row_slots, 
     const int R = c->max_rows;
     int32_t* h = c->h_in;
     std::vector<char> seen(c->slots, 0);
+    bool single_runs = true;  // every row the only row of its slot
     for (int rs = 0; rs < rows;) {
         const int slot = row_slots[rs];
         NHIP_REQUIRE(slot >= 0 && slot < c->slots, "row %d: slot %d outside [0, %d)", rs, slot, c->slots);
@@ -1823,6 +1839,7 @@ int32_t nhip_step(nhip_ctx* c, const int32_t* tokens, const int32_t* row_slots, 
         seen[slot] = 1;
         int rk = rs;
         while (rk + 1 < rows && row_slots[rk + 1] == slot) rk++;
+        single_runs = single_runs && rk == rs;
         NHIP_REQUIRE(c->len[slot] + (rk - rs + 1) <= c->capacity, "slot %d: context capacity %d exceeded", slot,
                      c->capacity);
         for (int t = rs; t <= rk; t++) {
@@ -1861,7 +1878,7 @@ int32_t nhip_step(nhip_ctx* c, const int32_t* tokens, const int32_t* row_slots, 
         set_error("step input upload failed");
         rc = NHIP_ERR_HIP;
     }
-    if (rc == NHIP_OK) rc = run_step(c, rows, distinct, k, argmax != nullptr);
+    if (rc == NHIP_OK) rc = run_step(c, rows, distinct, k, argmax != nullptr, single_runs);
     const bool repeats = distinct < heads;
     std::vector<float> lg_h, lp_h;
     std::vector<int32_t> idx_h, am_h;
