@@ -620,13 +620,15 @@ __global__ __launch_bounds__(64) void decode_merge_kernel(ATTN_HEAD_PARAMS, Deco
 // row's key and value heads and scales to the cache.
 constexpr int kRowMaxCapacity = 512;
 constexpr int kRowMaxChunks = kRowMaxCapacity / 16;  // the plan makes at most count/16 chunks
-constexpr int kRowUnits = kRowMaxCapacity * 4 / kThreads;  // key pieces per thread
+constexpr int kRowThreads = 512;                             // threads of a (row, head) workgroup
+constexpr int kRowUnits = kRowMaxCapacity * 4 / kRowThreads;  // key pieces per thread
 constexpr int kPostRows = 4;
+constexpr int kPostIters = (2 * kPostRows + 1 + kRowThreads / 64 - 1) / (kRowThreads / 64);  // POST units per wave
 // the row kernel's forms: q given, the decoder's step (POST), Needle 3's step (N3)
 constexpr int kRowPlain = 0, kRowPost = 1, kRowNeedle3 = 2;
 
 template <int MODE>
-__global__ __launch_bounds__(kThreads) void decode_attention_row_kernel(ATTN_HEAD_PARAMS, DecodeAttnParams p)
+__global__ __launch_bounds__(kRowThreads) void decode_attention_row_kernel(ATTN_HEAD_PARAMS, DecodeAttnParams p)
 {
     constexpr bool POST = MODE == kRowPost;
     constexpr bool N3 = MODE == kRowNeedle3;
@@ -672,12 +674,12 @@ __global__ __launch_bounds__(kThreads) void decode_attention_row_kernel(ATTN_HEA
     // POST units: unit 0 is the query head, unit 1 + 2r (+1) row r's key
     // (value) head; wave w takes units w, w + 4, w + 8 (clamped rows: the
     // loads are unconditional, so no wait gathers them at a join)
-    float post_x[3] = {0.0f, 0.0f, 0.0f}, post_c[3] = {0.0f, 0.0f, 0.0f}, post_sn[3] = {0.0f, 0.0f, 0.0f};
+    float post_x[kPostIters], post_c[kPostIters], post_sn[kPostIters];
     int rpos[kPostRows], rslot[kPostRows];
     if constexpr (POST) {
 #pragma unroll
-        for (int k = 0; k < 3; k++) {
-            const int u = (tid >> 6) + 4 * k;
+        for (int k = 0; k < kPostIters; k++) {
+            const int u = (tid >> 6) + (kRowThreads / 64) * k;
             const int r = u == 0 ? row : min((u - 1) >> 1, p.rows - 1);
             const bool value = u > 0 && ((u - 1) & 1);
             const int col = u == 0 ? h : (value ? p.heads + p.kv_heads + kv : p.heads + kv);
@@ -808,8 +810,8 @@ __global__ __launch_bounds__(kThreads) void decode_attention_row_kernel(ATTN_HEA
     float sv[kRowUnits];
 #pragma unroll
     for (int k = 0; k < kRowUnits; k++) {
-        if (k * kThreads >= units) break;  // uniform
-        const int u = min(k * kThreads + tid, units - 1);
+        if (k * kRowThreads >= units) break;  // uniform
+        const int u = min(k * kRowThreads + tid, units - 1);
         const size_t cell = (pos0 + (u >> 2)) * p.kv_heads + kv;
         kw[k] = *reinterpret_cast<const uint4*>(p.keys + cell * qk + 16 * qslot);
         sv[k] = sbase[cell];
@@ -817,8 +819,8 @@ __global__ __launch_bounds__(kThreads) void decode_attention_row_kernel(ATTN_HEA
     if constexpr (POST) {
         // RoPE, then QuantizeInt8 per head, in qkv_post_kernel's arithmetic
 #pragma unroll
-        for (int k = 0; k < 3; k++) {
-            const int u = (tid >> 6) + 4 * k;
+        for (int k = 0; k < kPostIters; k++) {
+            const int u = (tid >> 6) + (kRowThreads / 64) * k;
             const int r = u == 0 ? row : (u - 1) >> 1;
             if (u > 2 * kPostRows || (u > 0 && !((subs >> r) & 1u))) continue;  // uniform per wave
             const bool value = u > 0 && ((u - 1) & 1);
@@ -896,8 +898,8 @@ __global__ __launch_bounds__(kThreads) void decode_attention_row_kernel(ATTN_HEA
     const uint4 qv = *reinterpret_cast<const uint4*>(q_lds + 4 * qslot);
 #pragma unroll
     for (int k = 0; k < kRowUnits; k++) {
-        if (k * kThreads >= units) break;  // uniform
-        const int u = k * kThreads + tid;
+        if (k * kRowThreads >= units) break;  // uniform
+        const int u = k * kRowThreads + tid;
         const bool ok = u < units;  // whole aligned 4-lane groups
         const int s = min(u, units - 1) >> 2;
         if constexpr (SUB) {
@@ -927,7 +929,7 @@ __global__ __launch_bounds__(kThreads) void decode_attention_row_kernel(ATTN_HEA
     __syncthreads();
 
     // phase 3
-    for (int s = tid; s < count; s += kThreads) {
+    for (int s = tid; s < count; s += kRowThreads) {
         const float e = exp_poly(score[s] - order_value(peak_key[fast_div(s, mag_len)]));
         score[s] = e;
         wl[s] = e * vsc[s];
@@ -935,7 +937,7 @@ __global__ __launch_bounds__(kThreads) void decode_attention_row_kernel(ATTN_HEA
     __syncthreads();
 
     // phase 4: chunk c's sums in ascending positions
-    for (int c0 = 0; c0 < needed; c0 += kThreads / 16) {
+    for (int c0 = 0; c0 < needed; c0 += kRowThreads / 16) {
         const int c = c0 + (tid >> 4);
         if (c >= needed) break;
         const int b = c * length;
@@ -1163,7 +1165,7 @@ int32_t attention_decode_post_impl(const AttnPostInputs& in, int32_t rows, int32
     p.capacity = capacity;
     p.max_chunks = max_chunks;
     p.inv_sqrt = static_cast<float>(1.0 / std::sqrt(64.0));
-    hipLaunchKernelGGL(decode_attention_row_kernel<kRowPost>, dim3(rows, heads), dim3(kThreads), 0, stream,
+    hipLaunchKernelGGL(decode_attention_row_kernel<kRowPost>, dim3(rows, heads), dim3(kRowThreads), 0, stream,
                        ATTN_HEAD_ARGS(p, p.qkv, p.positions), p);
     NHIP_CHECK_HIP(hipGetLastError());
     return NHIP_OK;
@@ -1207,7 +1209,7 @@ int32_t attention_decode_needle3_impl(const Needle3AttnInputs& in, int32_t rows,
     p.capacity = capacity;
     p.max_chunks = max_chunks;
     p.inv_sqrt = static_cast<float>(1.0 / std::sqrt(static_cast<double>(qk_dim)));
-    hipLaunchKernelGGL(decode_attention_row_kernel<kRowNeedle3>, dim3(rows, heads), dim3(kThreads), 0, stream,
+    hipLaunchKernelGGL(decode_attention_row_kernel<kRowNeedle3>, dim3(rows, heads), dim3(kRowThreads), 0, stream,
                        ATTN_HEAD_ARGS(p, p.n3.raw, p.positions), p);
     NHIP_CHECK_HIP(hipGetLastError());
     return NHIP_OK;
@@ -1280,7 +1282,7 @@ int32_t attention_decode_impl(const int8_t* d_q, const float* d_qscale, int32_t 
     NHIP_REQUIRE(!d_q_out || (d_qs_out && max_chunks == 1 && head_blocks == 1),
                  "attention: a quantized output needs max_chunks 1 and all heads in one block");
     if (!d_q_out && capacity <= kRowMaxCapacity) {  // every count <= capacity: one workgroup per (row, head)
-        hipLaunchKernelGGL(decode_attention_row_kernel<kRowPlain>, dim3(rows, heads), dim3(kThreads), 0, stream,
+        hipLaunchKernelGGL(decode_attention_row_kernel<kRowPlain>, dim3(rows, heads), dim3(kRowThreads), 0, stream,
                            ATTN_HEAD_ARGS(p, p.q, p.qscale), p);
         NHIP_CHECK_HIP(hipGetLastError());
         return NHIP_OK;
