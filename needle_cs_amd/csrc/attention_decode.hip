@@ -620,16 +620,21 @@ __global__ __launch_bounds__(64) void decode_merge_kernel(ATTN_HEAD_PARAMS, Deco
 // row's key and value heads and scales to the cache.
 constexpr int kRowMaxCapacity = 512;
 constexpr int kRowMaxChunks = kRowMaxCapacity / 16;  // the plan makes at most count/16 chunks
-constexpr int kRowThreads = 512;                             // threads of a (row, head) workgroup
-constexpr int kRowUnits = kRowMaxCapacity * 4 / kRowThreads;  // key pieces per thread
 constexpr int kPostRows = 4;
-constexpr int kPostIters = (2 * kPostRows + 1 + kRowThreads / 64 - 1) / (kRowThreads / 64);  // POST units per wave
 // the row kernel's forms: q given, the decoder's step (POST), Needle 3's step (N3)
 constexpr int kRowPlain = 0, kRowPost = 1, kRowNeedle3 = 2;
+// Threads of a (row, head) workgroup.  The decode forms have a few rows, so
+// a workgroup per (row, head) leaves most of the chip idle and 8 waves finish
+// each row sooner; the plain form also runs prefill chunks of up to 128 rows
+// (thousands of workgroups), where 4 waves keep twice the workgroups resident.
+constexpr int row_threads(int mode) { return mode == kRowPlain ? 256 : 512; }
 
 template <int MODE>
-__global__ __launch_bounds__(kRowThreads) void decode_attention_row_kernel(ATTN_HEAD_PARAMS, DecodeAttnParams p)
+__global__ __launch_bounds__(row_threads(MODE)) void decode_attention_row_kernel(ATTN_HEAD_PARAMS, DecodeAttnParams p)
 {
+    constexpr int kRowThreads = row_threads(MODE);
+    constexpr int kRowUnits = kRowMaxCapacity * 4 / kRowThreads;  // key pieces per thread
+    constexpr int kPostIters = (2 * kPostRows + 1 + kRowThreads / 64 - 1) / (kRowThreads / 64);  // POST units per wave
     constexpr bool POST = MODE == kRowPost;
     constexpr bool N3 = MODE == kRowNeedle3;
     constexpr bool SUB = POST || N3;                 // positions written in this launch come from LDS
@@ -672,8 +677,8 @@ __global__ __launch_bounds__(kRowThreads) void decode_attention_row_kernel(ATTN_
     const int e = tid & 63;
     const int units_all = p.heads + 2 * p.kv_heads;
     // POST units: unit 0 is the query head, unit 1 + 2r (+1) row r's key
-    // (value) head; wave w takes units w, w + 4, w + 8 (clamped rows: the
-    // loads are unconditional, so no wait gathers them at a join)
+    // (value) head; of W waves, wave w takes units w, w + W, ... (clamped
+    // rows: the loads are unconditional, so no wait gathers them at a join)
     float post_x[kPostIters], post_c[kPostIters], post_sn[kPostIters];
     int rpos[kPostRows], rslot[kPostRows];
     if constexpr (POST) {
@@ -1165,7 +1170,7 @@ int32_t attention_decode_post_impl(const AttnPostInputs& in, int32_t rows, int32
     p.capacity = capacity;
     p.max_chunks = max_chunks;
     p.inv_sqrt = static_cast<float>(1.0 / std::sqrt(64.0));
-    hipLaunchKernelGGL(decode_attention_row_kernel<kRowPost>, dim3(rows, heads), dim3(kRowThreads), 0, stream,
+    hipLaunchKernelGGL(decode_attention_row_kernel<kRowPost>, dim3(rows, heads), dim3(row_threads(kRowPost)), 0, stream,
                        ATTN_HEAD_ARGS(p, p.qkv, p.positions), p);
     NHIP_CHECK_HIP(hipGetLastError());
     return NHIP_OK;
@@ -1209,7 +1214,7 @@ int32_t attention_decode_needle3_impl(const Needle3AttnInputs& in, int32_t rows,
     p.capacity = capacity;
     p.max_chunks = max_chunks;
     p.inv_sqrt = static_cast<float>(1.0 / std::sqrt(static_cast<double>(qk_dim)));
-    hipLaunchKernelGGL(decode_attention_row_kernel<kRowNeedle3>, dim3(rows, heads), dim3(kRowThreads), 0, stream,
+    hipLaunchKernelGGL(decode_attention_row_kernel<kRowNeedle3>, dim3(rows, heads), dim3(row_threads(kRowNeedle3)), 0, stream,
                        ATTN_HEAD_ARGS(p, p.n3.raw, p.positions), p);
     NHIP_CHECK_HIP(hipGetLastError());
     return NHIP_OK;
@@ -1282,7 +1287,7 @@ int32_t attention_decode_impl(const int8_t* d_q, const float* d_qscale, int32_t 
     NHIP_REQUIRE(!d_q_out || (d_qs_out && max_chunks == 1 && head_blocks == 1),
                  "attention: a quantized output needs max_chunks 1 and all heads in one block");
     if (!d_q_out && capacity <= kRowMaxCapacity) {  // every count <= capacity: one workgroup per (row, head)
-        hipLaunchKernelGGL(decode_attention_row_kernel<kRowPlain>, dim3(rows, heads), dim3(kRowThreads), 0, stream,
+        hipLaunchKernelGGL(decode_attention_row_kernel<kRowPlain>, dim3(rows, heads), dim3(row_threads(kRowPlain)), 0, stream,
                            ATTN_HEAD_ARGS(p, p.q, p.qscale), p);
         NHIP_CHECK_HIP(hipGetLastError());
         return NHIP_OK;
