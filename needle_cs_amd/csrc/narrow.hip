@@ -34,7 +34,7 @@ struct NarrowParams {
     const float* residual;  // set: y[t][n] = residual[t][n] + the row's sum (same ldy)
     const float* qscale;    // KIND 0: the int8 rows' scales [tokens]
     float* x_out;           // kProNorm with delta: workgroup 0 stores x + delta here
-    int32_t ldy, rows, row_start, row_end, gs, blk0;
+    int32_t ldy, row_start, row_end, gs;
     float eps;
 };
 
@@ -52,7 +52,7 @@ template <int RW, int NL, int WAVES, int TI, int KIND, bool DELTA>
 __global__ __launch_bounds__(64 * WAVES) void matmul_i8_narrow_kernel(const int8_t* h_w, const uint16_t* h_norms,
                                                                          const void* h_in, const float* h_delta,
                                                                          const float* h_gain, uint64_t h_k_gp8,
-                                                                         NarrowParams p)
+                                                                         uint64_t h_rows_blk0, NarrowParams p)
 {
     constexpr int LPR = 64 / RW;          // lanes per row in a wave load
     constexpr int SEG = LPR * 16;         // bytes of a row per wave load
@@ -60,16 +60,19 @@ __global__ __launch_bounds__(64 * WAVES) void matmul_i8_narrow_kernel(const int8
     constexpr int G4 = NL * 4 / RW;       // prologue float4 of a row per thread (K = 4 * NT * G4)
     constexpr bool PRO = KIND != 0;
     constexpr bool NORM = KIND == kProNorm;
+    // every address of the first loads comes from these leading (preloaded)
+    // arguments: no wait on the argument segment before they issue
     const int K = head_lo(h_k_gp8);
     const int GP8 = head_hi(h_k_gp8);
+    const int rows = head_lo(h_rows_blk0);
     const int G = K >> 5;
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
     const int r = lane / LPR;
     const int c = lane % LPR;
-    const int blk = p.blk0 + (int)blockIdx.x;
-    const int nl = min(blk * RW + r, p.rows - 1);  // rows past the end load the last row and store nothing
+    const int blk = head_hi(h_rows_blk0) + (int)blockIdx.x;
+    const int nl = min(blk * RW + r, rows - 1);  // rows past the end load the last row and store nothing
     const int kw0 = wave * (K / WAVES) + c * 16;    // this lane's first weight byte in the row
 
     extern __shared__ __align__(16) uint8_t lds[];
@@ -115,7 +118,7 @@ __global__ __launch_bounds__(64 * WAVES) void matmul_i8_narrow_kernel(const int8
     // 4. the residual value of chain lane (t, rr) = (tid / RW, tid % RW)
     float res = 0.0f;
     if (p.residual && tid < TI * RW)
-        res = p.residual[(size_t)(tid / RW) * p.ldy + min(blk * RW + tid % RW, p.rows - 1)];
+        res = p.residual[(size_t)(tid / RW) * p.ldy + min(blk * RW + tid % RW, rows - 1)];
     if constexpr (!PRO) {
 #pragma unroll
         for (int t = 0; t < TI; t++) qs[t] = p.qscale[t];
@@ -255,7 +258,7 @@ __global__ __launch_bounds__(64 * WAVES) void matmul_i8_narrow_kernel(const int8
             }
         }
         const int n = blk * RW + tid % RW;
-        if (n < p.rows && n >= p.row_start && n < p.row_end)
+        if (n < rows && n >= p.row_start && n < p.row_end)
             p.y[(size_t)(tid / RW) * p.ldy + n] = p.residual ? res + acc : acc;
     }
 }
@@ -267,7 +270,7 @@ int32_t launch_narrow_ti(const DeviceWeights* w, const void* in, const float* de
     static_assert(KIND != kProNorm || WAVES == 4, "the canonical sum of squares takes 256 threads");
     hipLaunchKernelGGL((matmul_i8_narrow_kernel<RW, NL, WAVES, TI, KIND, DELTA>), dim3(blocks), dim3(64 * WAVES), lds,
                        s, reinterpret_cast<const int8_t*>(w->rowmajor), w->norms, in, delta, gain,
-                       head_pair(w->cols, w->groups_pad8), p);
+                       head_pair(w->cols, w->groups_pad8), head_pair(w->rows, p.row_start / RW), p);
     NHIP_CHECK_HIP(hipGetLastError());
     return NHIP_OK;
 }
@@ -356,13 +359,11 @@ int32_t launch_i8_narrow(const DeviceWeights* w, int32_t kind, const void* in, c
     p.qscale = qscale;
     p.x_out = x_out;
     p.ldy = ldy;
-    p.rows = w->rows;
     p.row_start = row_start;
     p.row_end = row_end;
     p.gs = w->groups + 4;
-    p.blk0 = row_start / rw;
     p.eps = eps;
-    const int blocks = (row_end + rw - 1) / rw - p.blk0;
+    const int blocks = (row_end + rw - 1) / rw - row_start / rw;
     if (blocks <= 0) return NHIP_OK;
     const size_t lds = (size_t)tokens * rw * p.gs * 4 + (kind ? (size_t)tokens * K : 0) +
                        (kind == kProNorm ? (size_t)tokens * 256 * 4 : 0) + (size_t)tokens * (1 + waves) * 4;
