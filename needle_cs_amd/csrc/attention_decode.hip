@@ -475,12 +475,8 @@ __global__ __launch_bounds__(kThreads) void decode_attention_kernel(ATTN_HEAD_PA
         const float scale = peak > 0.0f ? peak / 127.0f : 1.0f;
         const float inverse = 1.0f / scale;
         if (vthread) {
-            const uint32_t b0 = (uint32_t)(uint8_t)ref_quantize_one(vout[0], inverse);
-            const uint32_t b1 = (uint32_t)(uint8_t)ref_quantize_one(vout[1], inverse);
-            const uint32_t b2 = (uint32_t)(uint8_t)ref_quantize_one(vout[2], inverse);
-            const uint32_t b3 = (uint32_t)(uint8_t)ref_quantize_one(vout[3], inverse);
             *reinterpret_cast<uint32_t*>(p.q_out + (size_t)row * p.heads * 64 + (h0 + vhl) * 64 + 4 * vqd) =
-                b0 | (b1 << 8) | (b2 << 16) | (b3 << 24);
+                ref_quantize4(make_float4(vout[0], vout[1], vout[2], vout[3]), inverse);
         }
         if (tid == 0) p.qs_out[row] = scale;
     }

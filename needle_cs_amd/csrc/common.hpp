@@ -243,17 +243,30 @@ __device__ __forceinline__ float ref_half_to_single(uint32_t half)
     return mag == 0 ? 0.0f : v;
 }
 
-// Scalar.RoundEven (src/Needle/Scalar.cs:51-53).
-__device__ __forceinline__ float ref_round_even(float x)
-{
-    return (x + 12582912.0f) - 12582912.0f;
-}
+// Scalar.RoundEven (src/Needle/Scalar.cs:51-53): (x + 1.5 * 2^23) - 1.5 * 2^23
+// there, which rounds half to even for |x| < 2^22 -- rint (v_rndne_f32), one
+// instruction.  Every caller clamps to [-128, 127], where the two agree for
+// all x (past 2^22 both keep the sign and clamp to the same end).
+__device__ __forceinline__ float ref_round_even(float x) { return __builtin_rintf(x); }
 
 // One element of Scalar.QuantizeInt8 (Scalar.cs:67-74): clamp(RoundEven(x * inverse)).
 __device__ __forceinline__ int ref_quantize_one(float x, float inverse)
 {
     const float r = ref_round_even(x * inverse);
     return static_cast<int>(fminf(fmaxf(r, -128.0f), 127.0f));
+}
+
+// Four elements of QuantizeInt8 packed little-endian into a dword: the low
+// bytes of the four ints gathered by three v_perm_b32.
+__device__ __forceinline__ uint32_t ref_quantize4(float4 h, float inverse)
+{
+    const uint32_t b0 = (uint32_t)ref_quantize_one(h.x, inverse);
+    const uint32_t b1 = (uint32_t)ref_quantize_one(h.y, inverse);
+    const uint32_t b2 = (uint32_t)ref_quantize_one(h.z, inverse);
+    const uint32_t b3 = (uint32_t)ref_quantize_one(h.w, inverse);
+    const uint32_t lo = __builtin_amdgcn_perm(b1, b0, 0x0c0c0400u);  // [b0, b1, 0, 0]
+    const uint32_t hi = __builtin_amdgcn_perm(b3, b2, 0x0c0c0400u);  // [b2, b3, 0, 0]
+    return __builtin_amdgcn_perm(hi, lo, 0x05040100u);               // [b0, b1, b2, b3]
 }
 
 // MathF.Max for the non-NaN operands used here (+0 preferred over -0).

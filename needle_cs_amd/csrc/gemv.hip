@@ -1345,12 +1345,7 @@ __global__ __launch_bounds__(512) void matmul_i8_decode_fused_kernel(const float
         for (int j = 0; j < G4; j++) {
             const int i = 4 * (tid + nt * j);
             if (tid < nt && i < K) {
-                const float4 h = xv[t][j];
-                const uint32_t b0 = (uint32_t)(ref_quantize_one(h.x, inverse) & 0xFF);
-                const uint32_t b1 = (uint32_t)(ref_quantize_one(h.y, inverse) & 0xFF);
-                const uint32_t b2 = (uint32_t)(ref_quantize_one(h.z, inverse) & 0xFF);
-                const uint32_t b3 = (uint32_t)(ref_quantize_one(h.w, inverse) & 0xFF);
-                *reinterpret_cast<uint32_t*>(qa + (size_t)t * K + i) = b0 | (b1 << 8) | (b2 << 16) | (b3 << 24);
+                *reinterpret_cast<uint32_t*>(qa + (size_t)t * K + i) = ref_quantize4(xv[t][j], inverse);
             }
         }
     }

@@ -86,7 +86,7 @@ __global__ __launch_bounds__(64 * WAVES) void matmul_i8_narrow_kernel(const int8
     float4 xv[PRO ? TI : 1][PRO ? G4 : 1];
     float4 dv[DELTA ? TI : 1][DELTA ? G4 : 1];
     float4 gv[NORM ? G4 : 1];
-    u4 av[PRO ? 1 : TI][PRO ? 1 : NL];
+    u4 av[TI][NL];  // the int8 rows' pieces (PRO: read from LDS after the prologue)
     float qs[TI];
     if constexpr (PRO) {
         const float* x = static_cast<const float*>(h_in);
@@ -192,12 +192,7 @@ __global__ __launch_bounds__(64 * WAVES) void matmul_i8_narrow_kernel(const int8
 #pragma unroll
             for (int j = 0; j < G4; j++) {
                 const int i = 4 * (tid + NT * j);
-                const float4 h = xv[t][j];
-                const uint32_t b0 = (uint32_t)(ref_quantize_one(h.x, inverse) & 0xFF);
-                const uint32_t b1 = (uint32_t)(ref_quantize_one(h.y, inverse) & 0xFF);
-                const uint32_t b2 = (uint32_t)(ref_quantize_one(h.z, inverse) & 0xFF);
-                const uint32_t b3 = (uint32_t)(ref_quantize_one(h.w, inverse) & 0xFF);
-                *reinterpret_cast<uint32_t*>(qa + (size_t)t * K + i) = b0 | (b1 << 8) | (b2 << 16) | (b3 << 24);
+                *reinterpret_cast<uint32_t*>(qa + (size_t)t * K + i) = ref_quantize4(xv[t][j], inverse);
             }
         }
         __syncthreads();
@@ -206,17 +201,21 @@ __global__ __launch_bounds__(64 * WAVES) void matmul_i8_narrow_kernel(const int8
     // 6. the group sums and products: lane (r, c) holds half of group g of
     // row r; the even lane of each pair writes p_g
     float* prow = pl + (size_t)r * p.gs;
+    if constexpr (PRO) {
+        // every piece read before the first product is written: the reads
+        // issue together instead of each waiting behind a write
+#pragma unroll
+        for (int j = 0; j < NL; j++)
+#pragma unroll
+            for (int t = 0; t < TI; t++) av[t][j] = *reinterpret_cast<const u4*>(qa + (size_t)t * K + kw0 + j * SEG);
+    }
 #pragma unroll
     for (int j = 0; j < NL; j++) {
         const int g = (kw0 + j * SEG) >> 5;
         const float hs = narrow_half(hraw[j]);
 #pragma unroll
         for (int t = 0; t < TI; t++) {
-            u4 a;
-            if constexpr (PRO)
-                a = *reinterpret_cast<const u4*>(qa + (size_t)t * K + kw0 + j * SEG);
-            else
-                a = av[t][j];
+            const u4 a = av[t][j];
             int d = __builtin_amdgcn_sdot4((int)a.x, (int)w[j].x, 0, false);
             d = __builtin_amdgcn_sdot4((int)a.y, (int)w[j].y, d, false);
             d = __builtin_amdgcn_sdot4((int)a.z, (int)w[j].z, d, false);
