@@ -698,12 +698,15 @@ struct TailArgs {
 // ((i % 4) * 8 + j) * stride + i / 4.
 __host__ __device__ constexpr int cond_stride(int dim) { return dim / 4 + 4; }
 
+// The row stride of a transposed Kronecker left factor in LDS (16-byte aligned).
+__host__ __device__ constexpr int krows_t(int rows) { return rows + 4; }
+
 // Bytes of LDS n3_tail_kernel takes for a geometry.
 size_t tail_lds_bytes(int dim, int rows, int cols)
 {
     const size_t width = (size_t)rows * cols;
-    return sizeof(float) * (3 * width + 32 + 2 * (size_t)dim + 36 * (size_t)cond_stride(dim) +
-                            3 * (size_t)rows * rows + 3 * (size_t)cols * cols + (size_t)kLanes * dim +
+    return sizeof(float) * (2 * width + (size_t)rows * (cols + 4) + 2 * (size_t)dim + 36 * (size_t)cond_stride(dim) +
+                            3 * (size_t)rows * krows_t(rows) + 3 * (size_t)cols * cols + (size_t)kLanes * dim +
                             32 * (size_t)v256_stride(kLanes * dim));
 }
 
@@ -742,23 +745,29 @@ __device__ __forceinline__ float wave_condition_weights(const float* input_t, co
 // for k < result_rows.  Thread u owns the four
 // elements 4u .. 4u+3 (one k, four consecutive c; cols % 4 == 0) and runs
 // their chains together; each step's operands are loaded 8 steps at a time.
-// scratch rows are cols + 1 apart (kron_scratch floats in all).
-__device__ __forceinline__ int kron_scratch(int rows, int cols) { return rows * cols + 32; }
+// The passes are bound by the LDS reads, so the scalar operand of 4 steps
+// comes in one 16-byte read as well: left is staged transposed (leftT[k][i],
+// rows krows_t(rows) apart) and scratch rows are cols + 4 apart (both
+// 16-byte aligned; kron_scratch floats in all).
+__device__ __forceinline__ int kron_scratch(int rows, int cols) { return rows * (cols + 4); }
 
 // The two chains of output element e0..e0+3 (row k = e0 / cols, columns c..c+3).
 // active is a multiple of 8 (the caller zero-fills z's rows up to it: a
 // zero product leaves a sum that starts at +0 unchanged).
-__device__ __forceinline__ void kron_first(const float* z, int active, const float* left, int rows, int cols, int e0,
+__device__ __forceinline__ void kron_first(const float* z, int active, const float* left, int lt, int cols, int e0,
                                            float* scratch)
 {
-    const int k = e0 / cols, c = e0 - k * cols, ss = cols + 1;
+    const int k = e0 / cols, c = e0 - k * cols, ss = cols + 4;
     float4 sum = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     for (int i0 = 0; i0 < active; i0 += 8) {
         float lv[8];
         float4 zv[8];
+        const float4 l0 = *reinterpret_cast<const float4*>(left + k * lt + i0);
+        const float4 l1 = *reinterpret_cast<const float4*>(left + k * lt + i0 + 4);
+        lv[0] = l0.x; lv[1] = l0.y; lv[2] = l0.z; lv[3] = l0.w;
+        lv[4] = l1.x; lv[5] = l1.y; lv[6] = l1.z; lv[7] = l1.w;
 #pragma unroll
         for (int u = 0; u < 8; u++) {
-            lv[u] = left[(i0 + u) * rows + k];
             zv[u] = *reinterpret_cast<const float4*>(z + (i0 + u) * cols + c);
         }
 #pragma unroll
@@ -778,14 +787,17 @@ __device__ __forceinline__ void kron_first(const float* z, int active, const flo
 
 __device__ __forceinline__ void kron_second(const float* right, int cols, int e0, const float* scratch, float* result)
 {
-    const int k = e0 / cols, c = e0 - k * cols, ss = cols + 1;
+    const int k = e0 / cols, c = e0 - k * cols, ss = cols + 4;
     float4 sum = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     for (int j0 = 0; j0 < cols; j0 += 8) {
         float sv[8];
         float4 rv[8];
+        const float4 s0 = *reinterpret_cast<const float4*>(scratch + k * ss + j0);
+        const float4 s1 = *reinterpret_cast<const float4*>(scratch + k * ss + j0 + 4);
+        sv[0] = s0.x; sv[1] = s0.y; sv[2] = s0.z; sv[3] = s0.w;
+        sv[4] = s1.x; sv[5] = s1.y; sv[6] = s1.z; sv[7] = s1.w;
 #pragma unroll
         for (int u = 0; u < 8; u++) {
-            sv[u] = scratch[k * ss + j0 + u];
             rv[u] = *reinterpret_cast<const float4*>(right + (j0 + u) * cols + c);
         }
 #pragma unroll
@@ -860,7 +872,8 @@ __global__ __launch_bounds__(kThreads) void n3_tail_kernel(const float* h_proj, 
     float* cvt = norm + dim;          // CondV, lane-major [32][cs]
     float* int_ = cvt + 32 * cs;      // the condition input, lane-major [4][cs]
     float* wl = int_ + 4 * cs;        // W1A, W2A, W3A
-    float* wr = wl + 3 * rr;          // W1B, W2B, W3B
+    const int lt = krows_t(a.rows);   // W1A, W2A, W3A transposed ([k][i], rows lt apart)
+    float* wr = wl + 3 * a.rows * lt; // W1B, W2B, W3B
     float* ns = wr + 3 * cc;          // the next stream row, 4 * dim
     float* nst = ns + n4;             // its lane-major copy [32][ts]
     __shared__ float weights[8];
@@ -969,9 +982,10 @@ __global__ __launch_bounds__(kThreads) void n3_tail_kernel(const float* h_proj, 
     for (int q = 0; q < kPer; q++) {
         const int e = col_of(q);
         if (e < rr) {
-            wl[e] = wv[q][0];
-            wl[rr + e] = wv[q][1];
-            wl[2 * rr + e] = wv[q][2];
+            const int et = (e % a.rows) * lt + e / a.rows;
+            wl[et] = wv[q][0];
+            wl[a.rows * lt + et] = wv[q][1];
+            wl[2 * a.rows * lt + et] = wv[q][2];
         }
         if (e < cc) {
             wr[e] = wv[q][3];
@@ -995,7 +1009,7 @@ __global__ __launch_bounds__(kThreads) void n3_tail_kernel(const float* h_proj, 
         const float w = wave_condition_weights(int_, cvt, dim);
         if (threadIdx.x - kKronThreads < 8) weights[threadIdx.x - kKronThreads] = w;
     } else {
-        kron_rows(front, active_rows, wl, wr, a.rows, a.cols, a.rows, scratch, back, kKronThreads);
+        kron_rows(front, active_rows, wl, wr, lt, a.cols, a.rows, scratch, back, kKronThreads);
     }
     __syncthreads();
 #pragma unroll
@@ -1010,14 +1024,14 @@ __global__ __launch_bounds__(kThreads) void n3_tail_kernel(const float* h_proj, 
         }
     }
     __syncthreads();
-    kron_lds(front, a.rows, wl + rr, wr + cc, a.rows, a.cols, a.rows, scratch, back);
+    kron_lds(front, a.rows, wl + a.rows * lt, wr + cc, lt, a.cols, a.rows, scratch, back);
 #pragma unroll
     for (int q = 0; q < kPer; q++) {  // Scalar.PermuteScale
         const int n = col_of(q);
         if (n < width) front[n] = back[pb[q]] * d3v[q];
     }
     __syncthreads();
-    kron_lds(front, a.rows, wl + 2 * rr, wr + 2 * cc, a.rows, a.cols, output_rows, scratch, back);
+    kron_lds(front, a.rows, wl + 2 * a.rows * lt, wr + 2 * cc, lt, a.cols, output_rows, scratch, back);
     // Scalar.AccumulateOutput, then CombineDiff4x4 into the next stream
 #pragma unroll
     for (int q = 0; q < kPer; q++) {
