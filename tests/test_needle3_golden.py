@@ -28,7 +28,8 @@ import os
 import numpy as np
 import pytest
 
-import needle3_model as M
+from needle_cs_amd.archive import NEEDLE3, needle3_archive
+from oracle.needle3 import OracleEngine, OracleModel
 
 FIX = np.load(os.path.join(os.path.dirname(__file__), "golden", "needle3_golden.npz"))
 LAYER_BOUND = 0.06
@@ -37,7 +38,7 @@ STATE_CASES = ("short", "prompt")
 
 
 def archive_of(case):
-    a = M.write_archive(M.NEEDLE3, int(FIX[f"{case}_seed"]))
+    a = needle3_archive(NEEDLE3, int(FIX[f"{case}_seed"]))
     assert hashlib.sha256(a).hexdigest() == str(FIX[f"{case}_sha256"]), \
         "the archive generator drifted from the fixture: rerun tests/golden/make_needle3_golden.py"
     return a
@@ -46,7 +47,7 @@ def archive_of(case):
 @pytest.fixture(scope="module")
 def models(orc):
     orc.lib().or_n3_set_threads(min(8, os.cpu_count() or 1))
-    yield {case: M.OracleModel(orc, archive_of(case)) for case in STATE_CASES}
+    yield {case: OracleModel(orc, archive_of(case)) for case in STATE_CASES}
     orc.lib().or_n3_set_threads(1)
 
 
@@ -60,7 +61,7 @@ def tier(orc, request):
 def feed(orc, om, tokens, chunk):
     """Feeds tokens in steps of `chunk` rows; the last step's logits and the
     last token's stream states [layers + 1][4][dim]."""
-    e = M.OracleEngine(orc, om, slots=1, capacity=64)
+    e = OracleEngine(orc, om, slots=1, capacity=64)
     try:
         for s in range(0, len(tokens), chunk):
             part = tokens[s:s + chunk]
@@ -100,8 +101,8 @@ def test_engram_rows_equal_the_reference_hash(orc, case):
     step: table * slots + engram_indices where the order's n-gram is full,
     -1 before it."""
     g = orc.N3.Dims()
-    g.engram_tables, g.engram_slots, g.order_count = M.NEEDLE3["engram_tables"], M.NEEDLE3["engram_slots"], 2
-    g.orders[0], g.orders[1] = M.NEEDLE3["orders"]
+    g.engram_tables, g.engram_slots, g.order_count = NEEDLE3["engram_tables"], NEEDLE3["engram_slots"], 2
+    g.orders[0], g.orders[1] = NEEDLE3["orders"]
     tokens = np.ascontiguousarray(FIX[f"{case}_tokens"], dtype=np.int32)
     n, tables, slots = len(tokens), g.engram_tables, g.engram_slots
     lengths = np.zeros(1, dtype=np.int32)
@@ -114,7 +115,7 @@ def test_engram_rows_equal_the_reference_hash(orc, case):
     idx = FIX[f"{case}_engram"]
     heads = tables // 2
     for table in range(tables):
-        order = M.NEEDLE3["orders"][table // heads]
+        order = NEEDLE3["orders"][table // heads]
         want = np.where(np.arange(n) >= order - 1, table * slots + idx[:, table], -1)
         assert np.array_equal(out[:, table], want), table
 

@@ -22,7 +22,8 @@ import numpy as np
 import pytest
 from scipy.linalg import hadamard
 
-import needle3_model as M
+from needle_cs_amd.archive import SMALL, needle3_archive
+from oracle.needle3 import OracleEngine, OracleModel
 
 F32 = np.float32
 
@@ -347,15 +348,15 @@ def test_engram_rows_follow_the_whole_sequence_across_steps(orc):
 
 @pytest.fixture(scope="module")
 def small(orc):
-    return M.OracleModel(orc, M.write_archive(M.SMALL, 3))
+    return OracleModel(orc, needle3_archive(SMALL, 3))
 
 
 def toks(seed, n):
-    return np.random.default_rng(seed).integers(0, M.SMALL["vocab"], n).astype(np.int32)
+    return np.random.default_rng(seed).integers(0, SMALL["vocab"], n).astype(np.int32)
 
 
 def engine(orc, om, slots=3):
-    return M.OracleEngine(orc, om, slots=slots, capacity=96, max_chunks=8)
+    return OracleEngine(orc, om, slots=slots, capacity=96, max_chunks=8)
 
 
 def test_oracle_engine_batched_equals_single(orc, small):
@@ -399,7 +400,7 @@ def test_oracle_engine_context_changes_logits(orc, small):
     a = engine(orc, small)
     base = toks(8, 10)
     other = base.copy()
-    other[0] = (other[0] + 1) % M.SMALL["vocab"]  # 9 positions back: outside the window of 6
+    other[0] = (other[0] + 1) % SMALL["vocab"]  # 9 positions back: outside the window of 6
     la = a.step(base, [0] * 10, [9])
     lb = a.step(other, [1] * 10, [9])
     assert not bits_equal(la, lb)

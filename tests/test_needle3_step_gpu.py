@@ -1,7 +1,7 @@
 """The Needle 3 batched engine on the GPU (nhip_ctx_* / nhip_step /
 nhip_slot_*) against the oracle's ForwardBatch restatement, bit for bit.
 
-A random-init archive of Needle 3's layer program (tests/needle3_model.py:
+A random-init archive of Needle 3's layer program (needle_cs_amd/archive.py:
 4-lane hyper-connections, an engram site, a global layer among windowed
 ones, the Kronecker-Hadamard MLP) is opened with nhip_open and stepped like
 BatchedEngine (src/Needle/BatchEngine.cs:5-50, Engine.cs:2285-2350); the
@@ -15,7 +15,8 @@ import ctypes as C
 import numpy as np
 import pytest
 
-import needle3_model as M
+from needle_cs_amd.archive import NEEDLE3, SMALL, needle3_archive
+from oracle.needle3 import OracleEngine, OracleModel
 
 pytestmark = pytest.mark.gpu
 
@@ -28,14 +29,14 @@ def avx2_row_tier(orc):
     yield
     orc.lib().or_n3_set_tier(0)
 
-GEOM = M.SMALL
+GEOM = SMALL
 SEED = 3
 MAX_CHUNKS = 8
 
 
 @pytest.fixture(scope="module")
 def archive():
-    return M.write_archive(GEOM, SEED)
+    return needle3_archive(GEOM, SEED)
 
 
 @pytest.fixture(scope="module")
@@ -48,7 +49,7 @@ def model(hip, archive):
 
 @pytest.fixture(scope="module")
 def omodel(orc, archive):
-    return M.OracleModel(orc, archive)
+    return OracleModel(orc, archive)
 
 
 def gpu_engine(model, slots=3, capacity=96, chunk=16):
@@ -57,7 +58,7 @@ def gpu_engine(model, slots=3, capacity=96, chunk=16):
 
 
 def cpu_engine(orc, omodel, slots=3, capacity=96):
-    return M.OracleEngine(orc, omodel, slots=slots, capacity=capacity, max_chunks=MAX_CHUNKS)
+    return OracleEngine(orc, omodel, slots=slots, capacity=capacity, max_chunks=MAX_CHUNKS)
 
 
 def same_bits(a, b):
@@ -251,13 +252,13 @@ def test_needle3_geometry_matches_the_oracle(hip, orc):
     of three slots, bit for bit."""
     from needle_cs_amd.engine import BatchedEngine, Model
     print("needle3 full geometry parity", flush=True)
-    archive = M.write_archive(M.NEEDLE3, 7)
-    om = M.OracleModel(orc, archive)
-    o = M.OracleEngine(orc, om, slots=3, capacity=64, max_chunks=MAX_CHUNKS)
+    archive = needle3_archive(NEEDLE3, 7)
+    om = OracleModel(orc, archive)
+    o = OracleEngine(orc, om, slots=3, capacity=64, max_chunks=MAX_CHUNKS)
     with Model(archive) as model, BatchedEngine(model, context_length=64, chunk_size=16, slots=3,
                                                 max_chunks=MAX_CHUNKS) as g:
         rng = np.random.default_rng(8)
-        t = rng.integers(0, M.NEEDLE3["vocab"], 16).astype(np.int32)
+        t = rng.integers(0, NEEDLE3["vocab"], 16).astype(np.int32)
         s = [0] * 8 + [1] * 5 + [2] * 3
         lg, _, _, am = g.forward_batch(t, s, [7, 12, 15], argmax=True)
         want = o.step(t, s, [7, 12, 15])
@@ -284,13 +285,13 @@ def test_needle3_window_past_1024_positions(hip, orc):
 
     from needle_cs_amd.engine import BatchedEngine, Model
     fix = np.load(os.path.join(os.path.dirname(__file__), "golden", "needle3_golden.npz"))
-    archive = M.write_archive(M.NEEDLE3, int(fix["window_seed"]))
+    archive = needle3_archive(NEEDLE3, int(fix["window_seed"]))
     assert hashlib.sha256(archive).hexdigest() == str(fix["window_sha256"])
     toks = np.ascontiguousarray(fix["window_tokens"], dtype=np.int32)
     prompt, cap, chunks = 1088, 1152, 64
     orc.lib().or_n3_set_threads(min(16, os.cpu_count() or 1))
-    om = M.OracleModel(orc, archive)
-    o = M.OracleEngine(orc, om, slots=1, capacity=cap, max_chunks=chunks)
+    om = OracleModel(orc, archive)
+    o = OracleEngine(orc, om, slots=1, capacity=cap, max_chunks=chunks)
     try:
         with Model(archive) as model, BatchedEngine(model, context_length=cap, chunk_size=128, slots=1,
                                                     max_chunks=chunks) as g:

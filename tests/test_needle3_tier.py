@@ -21,7 +21,8 @@ import math
 import numpy as np
 import pytest
 
-import needle3_model as M
+from needle_cs_amd.archive import SMALL, needle3_archive
+from oracle.needle3 import OracleEngine, OracleModel
 
 F32 = np.float32
 
@@ -186,11 +187,11 @@ def test_hadamard_mlp_tier_close(tiers):
 
 @pytest.fixture(scope="module")
 def small(orc):
-    return M.OracleModel(orc, M.write_archive(M.SMALL, 3))
+    return OracleModel(orc, needle3_archive(SMALL, 3))
 
 
 def toks(seed, n):
-    return np.random.default_rng(seed).integers(0, M.SMALL["vocab"], n).astype(np.int32)
+    return np.random.default_rng(seed).integers(0, SMALL["vocab"], n).astype(np.int32)
 
 
 def bits_equal(a, b):
@@ -203,8 +204,8 @@ def test_tier_engine_batched_single_chunk_sequential(tiers, small):
     differ from tier 0's only by the tiers' rounding (same argmax here)."""
     orc = tiers
     orc.lib().or_n3_set_tier(1)
-    a = M.OracleEngine(orc, small, slots=2, capacity=96, max_chunks=8)
-    b = M.OracleEngine(orc, small, slots=2, capacity=96, max_chunks=8)
+    a = OracleEngine(orc, small, slots=2, capacity=96, max_chunks=8)
+    b = OracleEngine(orc, small, slots=2, capacity=96, max_chunks=8)
     p0, p1 = toks(1, 7), toks(2, 9)
     both_rows = a.step(np.r_[p0, p1], [0] * 7 + [1] * 9, [6, 15])
     seq = np.concatenate([b.step(p0[i:i + 1], [0], [0]) for i in range(7)])
@@ -213,7 +214,7 @@ def test_tier_engine_batched_single_chunk_sequential(tiers, small):
     a.close()
     b.close()
     orc.lib().or_n3_set_tier(0)
-    c = M.OracleEngine(orc, small, slots=1, capacity=96, max_chunks=8)
+    c = OracleEngine(orc, small, slots=1, capacity=96, max_chunks=8)
     scalar = c.step(p0, [0] * 7, [6])
     c.close()
     assert not bits_equal(scalar, seq[-1:])
