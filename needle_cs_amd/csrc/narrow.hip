@@ -328,11 +328,11 @@ int env_int(const char* name, int fallback)
 // Which launches take the narrow kernel, and its shape.  Measured on the
 // decoder's matmuls (12 layers, d 1024, M = 3; traced per launch against the
 // 16-row fused kernel): down (N 1024, K 4096, quantize prologue) 7.17 ->
-// 5.85 us with 4-row workgroups; output (N 1024, K 1024) 3.78 -> 3.41 us;
-// the QKV matmul with its RMSNorm prologue (N 3072) was slower, 4.87 against
-// 5.37 us with 8-row workgroups, so the norm prologue keeps the 16-row
-// kernel.  NHIP_NARROW_RW (0 off, 4 or 8), NHIP_NARROW_WAVES (4 or 8) and
-// NHIP_NARROW_NORM=1 override the choices for timing.
+// 5.14 us with 4-row workgroups; output (N 1024, K 1024) 3.78 -> 3.22 us;
+// the QKV matmul with its RMSNorm prologue (N 3072) 5.30 -> 5.01 us with
+// 8-row workgroups (5.52 with 4-row ones).  NHIP_NARROW_RW (0 off, 4 or 8),
+// NHIP_NARROW_WAVES (4 or 8) and NHIP_NARROW_NORM=0 (the norm prologue on
+// the 16-row kernel) override the choices for timing.
 int32_t launch_i8_narrow(const DeviceWeights* w, int32_t kind, const void* in, const float* delta,
                          const float* gain, const float* qscale, float* x_out, float eps, const float* residual,
                          int32_t tokens, float* y, int32_t ldy, int32_t row_start, int32_t row_end,
@@ -340,7 +340,7 @@ int32_t launch_i8_narrow(const DeviceWeights* w, int32_t kind, const void* in, c
 {
     static const int forced_rw = env_int("NHIP_NARROW_RW", -1);
     static const int forced_waves = env_int("NHIP_NARROW_WAVES", 0);
-    static const bool norm_ok = env_int("NHIP_NARROW_NORM", 0) == 1;
+    static const bool norm_ok = env_int("NHIP_NARROW_NORM", 1) == 1;
     if (!w || !w->rowmajor || w->format != WeightFormat::Int8G32 || w->special_scales) return 1;
     if (tokens < 1 || tokens > 4 || w->cols % 1024 != 0 || w->cols > 4096) return 1;
     if (kind == kProNorm && !norm_ok) return 1;
