@@ -140,15 +140,14 @@ int32_t launch_decode_fused(const DeviceWeights* w, const DecodePrologue& f, int
                             hipStream_t stream);
 // The narrow decode matmul (narrow.hip) over rows [row_start, row_end):
 // kind 0 takes int8 rows `in` [tokens][cols] with scales qscale, kProNorm /
-// kProQuant compute them from fp32 rows as launch_decode_fused does (delta,
-// gain, x_out, eps as in DecodePrologue); with `residual` it stores
-// residual + y.  Returns 1 (nothing launched) for weights or shapes it does
-// not take: no row-major copy, exponent-31 scales, more than 4 tokens, K not
-// a multiple of 1024 or above 4096.
+// kProQuant compute them from fp32 rows as launch_decode_fused does (gain,
+// eps as in DecodePrologue); with `residual` it stores residual + y.
+// Returns 1 (nothing launched) for weights or shapes it does not take: no
+// row-major copy, exponent-31 scales, more than 4 tokens, K not a multiple
+// of 1024 or above 4096, a pending delta.
 int32_t launch_i8_narrow(const DeviceWeights* w, int32_t kind, const void* in, const float* delta,
-                         const float* gain, const float* qscale, float* x_out, float eps, const float* residual,
-                         int32_t tokens, float* y, int32_t ldy, int32_t row_start, int32_t row_end,
-                         hipStream_t stream);
+                         const float* gain, const float* qscale, float eps, const float* residual, int32_t tokens,
+                         float* y, int32_t ldy, int32_t row_start, int32_t row_end, hipStream_t stream);
 // The decode matmul of int8 rows q restricted to the 16-row tiles holding a
 // row set in some token's mask ([tokens][mask_words] bitsets, bit id%32 of
 // word id/32); the other outputs are left untouched (Engine.LogitsForRows'

@@ -428,6 +428,19 @@ __global__ __launch_bounds__(64) void topk_final_kernel(const float* logits, int
     const int row = blockIdx.x;
     const size_t base = (size_t)row * blocks;
     const int n = blocks * K;
+    // the log-sum-exp's block maxima and sums, and the special case's logit,
+    // load with the candidates: nothing between depends on them
+    constexpr int kPerThread = kTopkMaxBlocks / 64;
+    float bm[kPerThread], bs[kPerThread];
+#pragma unroll
+    for (int q = 0; q < kPerThread; q++) {
+        const int b = tid + 64 * q;
+        if (b < blocks) {
+            bm[q] = bmax[base + b];
+            bs[q] = bsum[base + b];
+        }
+    }
+    const float logit4 = tid == 0 && width > 4 ? logits[(size_t)row * width + 4] : 0.0f;
     for (int j = tid; j < n; j += 64) {
         sv[j] = bvals[base * K + j];
         si[j] = bids[base * K + j];
@@ -459,13 +472,17 @@ __global__ __launch_bounds__(64) void topk_final_kernel(const float* logits, int
         bool later = false;
 #pragma unroll
         for (int m = 0; m < K; m++) later = later || (best_i[m] != 1 && best_i[m] != 0x7FFFFFFF);
-        if (!later && logits[(size_t)row * width + 4] == -INFINITY) best_i[K - 1] = 4;
+        if (!later && logit4 == -INFINITY) best_i[K - 1] = 4;
     }
     __syncthreads();
     // log-sum-exp over the blocks in ascending order: the terms
     // Exp(max_b - peak) * sum_b in parallel, then their sum in order
     const float peak = best_v[0];
-    for (int b = tid; b < blocks; b += 64) prod[b] = exp_poly(bmax[base + b] - peak) * bsum[base + b];
+#pragma unroll
+    for (int q = 0; q < kPerThread; q++) {
+        const int b = tid + 64 * q;
+        if (b < blocks) prod[b] = exp_poly(bm[q] - peak) * bs[q];
+    }
     __syncthreads();
     if (tid != 0) return;
     float total = 0.0f;

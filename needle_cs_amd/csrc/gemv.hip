@@ -1716,8 +1716,8 @@ int32_t run_matmul(const DeviceWeights* w, const int8_t* q, const float* scales,
         if (!dots && tokens >= kGemmMinTokens)
             return launch_gemm_i8(w, q, scales, tokens, y, ldy, row_start, row_end, true, stream);
         if (!dots) {
-            const int32_t nrc = launch_i8_narrow(w, 0, q, nullptr, nullptr, scales, nullptr, 0.0f, nullptr, tokens,
-                                                 y, ldy, row_start, row_end, stream);
+            const int32_t nrc = launch_i8_narrow(w, 0, q, nullptr, nullptr, scales, 0.0f, nullptr, tokens, y, ldy,
+                                                 row_start, row_end, stream);
             if (nrc <= 0) return nrc;
         }
         const int32_t drc = try_i8_decode(w, p, stream);
@@ -2133,8 +2133,8 @@ int32_t launch_decode_fused(const DeviceWeights* w, const DecodePrologue& f, int
     NHIP_REQUIRE(!f.swiglu || w->rows % 16 == 0, "fused matmul: SwiGLU pairs need whole 16-row tiles");
     if (tokens < 1 || tokens > 4 || w->special_scales) return 1;
     if (!f.swiglu) {
-        const int32_t nrc = launch_i8_narrow(w, f.kind, f.x, f.delta, f.gain, nullptr, f.x_out, f.eps, f.residual,
-                                             tokens, y, ldy, 0, w->rows, stream);
+        const int32_t nrc = launch_i8_narrow(w, f.kind, f.x, f.delta, f.gain, nullptr, f.eps, f.residual, tokens, y,
+                                             ldy, 0, w->rows, stream);
         if (nrc <= 0) return nrc;
     }
     const int K = w->cols;

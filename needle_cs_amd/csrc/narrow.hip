@@ -19,9 +19,9 @@
 // sum and the partner lane (c ^ 1, the other half) adds its own through DPP.
 // The activations come either as int8 rows (KIND 0), or are computed from
 // fp32 rows in the prologue exactly as gemv.hip's fused decode kernel does
-// (kProNorm: x (+ delta) -> RMSNorm with the canonical row sum of squares *
-// gain -> QuantizeInt8; kProQuant: QuantizeInt8 of x) into LDS, while the
-// weight loads are in flight.
+// (kProNorm: x -> RMSNorm with the canonical row sum of squares * gain ->
+// QuantizeInt8; kProQuant: QuantizeInt8 of x) into LDS, while the weight
+// loads are in flight.
 #include "common.hpp"
 
 namespace nhip {
@@ -33,7 +33,6 @@ struct NarrowParams {
     float* y;
     const float* residual;  // set: y[t][n] = residual[t][n] + the row's sum (same ldy)
     const float* qscale;    // KIND 0: the int8 rows' scales [tokens]
-    float* x_out;           // kProNorm with delta: workgroup 0 stores x + delta here
     int32_t ldy, row_start, row_end, gs;
     float eps;
 };
@@ -48,10 +47,10 @@ __device__ __forceinline__ float narrow_half(uint32_t h)
 // lane ^ 1's value (DPP quad_perm [1, 0, 3, 2])
 __device__ __forceinline__ int pair_swap(int v) { return __builtin_amdgcn_update_dpp(0, v, 0xB1, 0xF, 0xF, false); }
 
-template <int RW, int NL, int WAVES, int TI, int KIND, bool DELTA>
+template <int RW, int NL, int WAVES, int TI, int KIND>
 __global__ __launch_bounds__(64 * WAVES) void matmul_i8_narrow_kernel(const int8_t* h_w, const uint16_t* h_norms,
-                                                                         const void* h_in, const float* h_delta,
-                                                                         const float* h_gain, uint64_t h_k_gp8,
+                                                                         const void* h_in, const float* h_gain,
+                                                                         uint64_t h_k_gp8,
                                                                          uint64_t h_rows_blk0, NarrowParams p)
 {
     constexpr int LPR = 64 / RW;          // lanes per row in a wave load
@@ -84,7 +83,6 @@ __global__ __launch_bounds__(64 * WAVES) void matmul_i8_narrow_kernel(const int8
 
     // 1. the activations: fp32 prologue rows, or the int8 rows' pieces
     float4 xv[PRO ? TI : 1][PRO ? G4 : 1];
-    float4 dv[DELTA ? TI : 1][DELTA ? G4 : 1];
     float4 gv[NORM ? G4 : 1];
     u4 av[TI][NL];  // the int8 rows' pieces (PRO: read from LDS after the prologue)
     float qs[TI];
@@ -95,10 +93,7 @@ __global__ __launch_bounds__(64 * WAVES) void matmul_i8_narrow_kernel(const int8
             const int i = 4 * (tid + NT * j);
             if constexpr (NORM) gv[j] = *reinterpret_cast<const float4*>(h_gain + i);
 #pragma unroll
-            for (int t = 0; t < TI; t++) {
-                xv[t][j] = *reinterpret_cast<const float4*>(x + (size_t)t * K + i);
-                if constexpr (DELTA) dv[t][j] = *reinterpret_cast<const float4*>(h_delta + (size_t)t * K + i);
-            }
+            for (int t = 0; t < TI; t++) xv[t][j] = *reinterpret_cast<const float4*>(x + (size_t)t * K + i);
         }
     } else {
         const int8_t* q = static_cast<const int8_t*>(h_in);
@@ -137,10 +132,7 @@ __global__ __launch_bounds__(64 * WAVES) void matmul_i8_narrow_kernel(const int8
                 float s = 0.0f;
 #pragma unroll
                 for (int j = 0; j < G4; j++) {
-                    float4 v = xv[t][j];
-                    if constexpr (DELTA)
-                        v = make_float4(v.x + dv[t][j].x, v.y + dv[t][j].y, v.z + dv[t][j].z, v.w + dv[t][j].w);
-                    xv[t][j] = v;
+                    const float4 v = xv[t][j];
                     s = s + v.x * v.x;
                     s = s + v.y * v.y;
                     s = s + v.z * v.z;
@@ -159,9 +151,6 @@ __global__ __launch_bounds__(64 * WAVES) void matmul_i8_narrow_kernel(const int8
                 const float inv = 1.0f / sqrtf(sums[t] / (float)K + p.eps);
 #pragma unroll
                 for (int j = 0; j < G4; j++) {
-                    const int i = 4 * (tid + NT * j);
-                    if (DELTA && p.x_out && blockIdx.x == 0)
-                        *reinterpret_cast<float4*>(p.x_out + (size_t)t * K + i) = xv[t][j];
                     const float4 v = xv[t][j];
                     xv[t][j] = make_float4((v.x * inv) * gv[j].x, (v.y * inv) * gv[j].y, (v.z * inv) * gv[j].z,
                                            (v.w * inv) * gv[j].w);
@@ -262,59 +251,57 @@ __global__ __launch_bounds__(64 * WAVES) void matmul_i8_narrow_kernel(const int8
     }
 }
 
-template <int RW, int NL, int WAVES, int TI, int KIND, bool DELTA>
-int32_t launch_narrow_ti(const DeviceWeights* w, const void* in, const float* delta, const float* gain,
-                         const NarrowParams& p, int blocks, size_t lds, hipStream_t s)
+template <int RW, int NL, int WAVES, int TI, int KIND>
+int32_t launch_narrow_ti(const DeviceWeights* w, const void* in, const float* gain, const NarrowParams& p, int blocks,
+                         size_t lds, hipStream_t s)
 {
     static_assert(KIND != kProNorm || WAVES == 4, "the canonical sum of squares takes 256 threads");
-    hipLaunchKernelGGL((matmul_i8_narrow_kernel<RW, NL, WAVES, TI, KIND, DELTA>), dim3(blocks), dim3(64 * WAVES), lds,
-                       s, reinterpret_cast<const int8_t*>(w->rowmajor), w->norms, in, delta, gain,
+    hipLaunchKernelGGL((matmul_i8_narrow_kernel<RW, NL, WAVES, TI, KIND>), dim3(blocks), dim3(64 * WAVES), lds, s,
+                       reinterpret_cast<const int8_t*>(w->rowmajor), w->norms, in, gain,
                        head_pair(w->cols, w->groups_pad8), head_pair(w->rows, p.row_start / RW), p);
     NHIP_CHECK_HIP(hipGetLastError());
     return NHIP_OK;
 }
 
-template <int RW, int NL, int WAVES, int KIND, bool DELTA>
-int32_t launch_narrow_tokens(const DeviceWeights* w, int tokens, const void* in, const float* delta,
-                             const float* gain, const NarrowParams& p, int blocks, size_t lds, hipStream_t s)
+template <int RW, int NL, int WAVES, int KIND>
+int32_t launch_narrow_tokens(const DeviceWeights* w, int tokens, const void* in, const float* gain,
+                             const NarrowParams& p, int blocks, size_t lds, hipStream_t s)
 {
     switch (tokens) {
-        case 1: return launch_narrow_ti<RW, NL, WAVES, 1, KIND, DELTA>(w, in, delta, gain, p, blocks, lds, s);
-        case 2: return launch_narrow_ti<RW, NL, WAVES, 2, KIND, DELTA>(w, in, delta, gain, p, blocks, lds, s);
-        case 3: return launch_narrow_ti<RW, NL, WAVES, 3, KIND, DELTA>(w, in, delta, gain, p, blocks, lds, s);
-        default: return launch_narrow_ti<RW, NL, WAVES, 4, KIND, DELTA>(w, in, delta, gain, p, blocks, lds, s);
+        case 1: return launch_narrow_ti<RW, NL, WAVES, 1, KIND>(w, in, gain, p, blocks, lds, s);
+        case 2: return launch_narrow_ti<RW, NL, WAVES, 2, KIND>(w, in, gain, p, blocks, lds, s);
+        case 3: return launch_narrow_ti<RW, NL, WAVES, 3, KIND>(w, in, gain, p, blocks, lds, s);
+        default: return launch_narrow_ti<RW, NL, WAVES, 4, KIND>(w, in, gain, p, blocks, lds, s);
     }
 }
 
 // NL = K * RW / (1024 * WAVES) weight loads per lane, for K = 1024 .. 4096
-template <int RW, int WAVES, int KIND, bool DELTA>
-int32_t launch_narrow_nl(const DeviceWeights* w, int tokens, const void* in, const float* delta, const float* gain,
-                         const NarrowParams& p, int blocks, size_t lds, hipStream_t s)
+template <int RW, int WAVES, int KIND>
+int32_t launch_narrow_nl(const DeviceWeights* w, int tokens, const void* in, const float* gain, const NarrowParams& p,
+                         int blocks, size_t lds, hipStream_t s)
 {
     constexpr int NL1 = RW / WAVES > 0 ? RW / WAVES : 1;  // NL at K = 1024 when RW >= WAVES
     const int nl = w->cols * RW / (1024 * WAVES);
     if constexpr (RW >= WAVES) {
-        if (nl == NL1) return launch_narrow_tokens<RW, NL1, WAVES, KIND, DELTA>(w, tokens, in, delta, gain, p, blocks, lds, s);
+        if (nl == NL1) return launch_narrow_tokens<RW, NL1, WAVES, KIND>(w, tokens, in, gain, p, blocks, lds, s);
         if (nl == 2 * NL1)
-            return launch_narrow_tokens<RW, 2 * NL1, WAVES, KIND, DELTA>(w, tokens, in, delta, gain, p, blocks, lds, s);
-        return launch_narrow_tokens<RW, 4 * NL1, WAVES, KIND, DELTA>(w, tokens, in, delta, gain, p, blocks, lds, s);
+            return launch_narrow_tokens<RW, 2 * NL1, WAVES, KIND>(w, tokens, in, gain, p, blocks, lds, s);
+        return launch_narrow_tokens<RW, 4 * NL1, WAVES, KIND>(w, tokens, in, gain, p, blocks, lds, s);
     } else {  // RW 4, 8 waves: NL 1 (K = 2048) or 2 (K = 4096)
-        if (nl == 1) return launch_narrow_tokens<RW, 1, WAVES, KIND, DELTA>(w, tokens, in, delta, gain, p, blocks, lds, s);
-        return launch_narrow_tokens<RW, 2, WAVES, KIND, DELTA>(w, tokens, in, delta, gain, p, blocks, lds, s);
+        if (nl == 1) return launch_narrow_tokens<RW, 1, WAVES, KIND>(w, tokens, in, gain, p, blocks, lds, s);
+        return launch_narrow_tokens<RW, 2, WAVES, KIND>(w, tokens, in, gain, p, blocks, lds, s);
     }
 }
 
 template <int RW, int WAVES>
-int32_t launch_narrow_kind(const DeviceWeights* w, int kind, int tokens, const void* in, const float* delta,
-                           const float* gain, const NarrowParams& p, int blocks, size_t lds, hipStream_t s)
+int32_t launch_narrow_kind(const DeviceWeights* w, int kind, int tokens, const void* in, const float* gain,
+                           const NarrowParams& p, int blocks, size_t lds, hipStream_t s)
 {
     if constexpr (WAVES == 4) {
-        if (kind == kProNorm)
-            return delta ? launch_narrow_nl<RW, 4, kProNorm, true>(w, tokens, in, delta, gain, p, blocks, lds, s)
-                         : launch_narrow_nl<RW, 4, kProNorm, false>(w, tokens, in, delta, gain, p, blocks, lds, s);
+        if (kind == kProNorm) return launch_narrow_nl<RW, 4, kProNorm>(w, tokens, in, gain, p, blocks, lds, s);
     }
-    if (kind == kProQuant) return launch_narrow_nl<RW, WAVES, kProQuant, false>(w, tokens, in, delta, gain, p, blocks, lds, s);
-    return launch_narrow_nl<RW, WAVES, 0, false>(w, tokens, in, delta, gain, p, blocks, lds, s);
+    if (kind == kProQuant) return launch_narrow_nl<RW, WAVES, kProQuant>(w, tokens, in, gain, p, blocks, lds, s);
+    return launch_narrow_nl<RW, WAVES, 0>(w, tokens, in, gain, p, blocks, lds, s);
 }
 
 int env_int(const char* name, int fallback)
@@ -334,7 +321,7 @@ int env_int(const char* name, int fallback)
 // NHIP_NARROW_WAVES (4 or 8) and NHIP_NARROW_NORM=0 (the norm prologue on
 // the 16-row kernel) override the choices for timing.
 int32_t launch_i8_narrow(const DeviceWeights* w, int32_t kind, const void* in, const float* delta,
-                         const float* gain, const float* qscale, float* x_out, float eps, const float* residual,
+                         const float* gain, const float* qscale, float eps, const float* residual,
                          int32_t tokens, float* y, int32_t ldy, int32_t row_start, int32_t row_end,
                          hipStream_t stream)
 {
@@ -343,7 +330,9 @@ int32_t launch_i8_narrow(const DeviceWeights* w, int32_t kind, const void* in, c
     static const bool norm_ok = env_int("NHIP_NARROW_NORM", 1) == 1;
     if (!w || !w->rowmajor || w->format != WeightFormat::Int8G32 || w->special_scales) return 1;
     if (tokens < 1 || tokens > 4 || w->cols % 1024 != 0 || w->cols > 4096) return 1;
-    if (kind == kProNorm && !norm_ok) return 1;
+    // a prologue with a pending delta (a decoder fallback path) keeps the
+    // 16-row kernel, which also stores x + delta
+    if (delta || (kind == kProNorm && !norm_ok)) return 1;
     const int rw = forced_rw >= 0 ? forced_rw : (w->rows <= 2048 ? 4 : 8);
     if (rw != 4 && rw != 8) return 1;
     int waves = forced_waves ? forced_waves : (w->cols >= 2048 ? 8 : 4);
@@ -356,7 +345,6 @@ int32_t launch_i8_narrow(const DeviceWeights* w, int32_t kind, const void* in, c
     p.y = y;
     p.residual = residual;
     p.qscale = qscale;
-    p.x_out = x_out;
     p.ldy = ldy;
     p.row_start = row_start;
     p.row_end = row_end;
@@ -367,10 +355,10 @@ int32_t launch_i8_narrow(const DeviceWeights* w, int32_t kind, const void* in, c
     const size_t lds = (size_t)tokens * rw * p.gs * 4 + (kind ? (size_t)tokens * K : 0) +
                        (kind == kProNorm ? (size_t)tokens * 256 * 4 : 0) + (size_t)tokens * (1 + waves) * 4;
     if (rw == 4)
-        return waves == 8 ? launch_narrow_kind<4, 8>(w, kind, tokens, in, delta, gain, p, blocks, lds, stream)
-                          : launch_narrow_kind<4, 4>(w, kind, tokens, in, delta, gain, p, blocks, lds, stream);
-    return waves == 8 ? launch_narrow_kind<8, 8>(w, kind, tokens, in, delta, gain, p, blocks, lds, stream)
-                      : launch_narrow_kind<8, 4>(w, kind, tokens, in, delta, gain, p, blocks, lds, stream);
+        return waves == 8 ? launch_narrow_kind<4, 8>(w, kind, tokens, in, gain, p, blocks, lds, stream)
+                          : launch_narrow_kind<4, 4>(w, kind, tokens, in, gain, p, blocks, lds, stream);
+    return waves == 8 ? launch_narrow_kind<8, 8>(w, kind, tokens, in, gain, p, blocks, lds, stream)
+                      : launch_narrow_kind<8, 4>(w, kind, tokens, in, gain, p, blocks, lds, stream);
 }
 
 }  // namespace nhip
