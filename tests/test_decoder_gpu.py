@@ -114,9 +114,10 @@ def test_wide_layers_prefill_and_beam(hip, orc):
     lg_c, ic, lpc = cpu.forward(prompt, [0] * 16, np.arange(16), k=3)
     assert np.array_equal(bits(lg_g), bits(lg_c))
     assert np.array_equal(ig, ic)
-    # three decode rows: the gate/up (512 tiles) and head (2000 tiles)
-    # matmuls take the separate norm launch and the plain kernel, the gate/up
-    # one with the SwiGLU chain epilogue; the others fuse their prologues
+    # three decode rows: the QKV, output and down matmuls take the narrow
+    # kernel with their prologues, the gate/up matmul the 16-row kernel with
+    # its norm prologue and SwiGLU chain epilogue, the head (2000 tiles) the
+    # separate norm launch and the plain kernel
     gpu.copy_slot(1, 0, 16)
     cpu.copy_slot(1, 0, 16)
     gpu.copy_slot(2, 0, 16)
@@ -135,6 +136,33 @@ def test_wide_layers_prefill_and_beam(hip, orc):
     tg, sg, _ = gpu.beam_search(prompt, 3, 4, 1)
     tc, sc, _ = cpu.beam_search(prompt, 3, 4, 1)
     assert np.array_equal(tg, tc) and np.float32(sg) == np.float32(sc)
+    gpu.close()
+    cpu.close()
+
+
+@pytest.mark.parametrize("rows", [1, 2, 3, 4])
+def test_wide_decode_rows(hip, orc, rows):
+    """Decode steps of 1-4 rows (one per slot) at d_model 1024: every token
+    count of the narrow kernel's norm and quantize prologues and of the fused
+    gate/up kernel, bit for bit against the oracle."""
+    model = synthetic_model(WIDE, 7004)
+    prompt = random_prompt(9, 8, WIDE["vocab"])
+    gpu = GpuDecoder(model, slots=4, capacity=16, max_rows=8)
+    cpu = orc.CpuDecoder(model, slots=4, capacity=16, threads=8)
+    _, ig, _ = gpu.forward(prompt, [0] * 8, np.arange(8), k=4)
+    _, ic, _ = cpu.forward(prompt, [0] * 8, np.arange(8), k=4)
+    assert np.array_equal(ig, ic)
+    for s in range(1, rows):
+        gpu.copy_slot(s, 0, 8)
+        cpu.copy_slot(s, 0, 8)
+    toks = ig[-1, :rows].astype(np.int32)
+    lanes = list(range(rows))
+    for step in range(2):
+        lg_g, ig2, lpg = gpu.forward(toks, lanes, [8 + step] * rows, k=4)
+        lg_c, ic2, lpc = cpu.forward(toks, lanes, [8 + step] * rows, k=4)
+        assert np.array_equal(bits(lg_g), bits(lg_c)), step
+        assert np.array_equal(ig2, ic2) and np.array_equal(bits(lpg), bits(lpc))
+        toks = ic2[:, 0].copy()
     gpu.close()
     cpu.close()
 
