@@ -143,8 +143,8 @@ int32_t launch_decode_fused(const DeviceWeights* w, const DecodePrologue& f, int
 // kProQuant compute them from fp32 rows as launch_decode_fused does (gain,
 // eps as in DecodePrologue); with `residual` it stores residual + y.
 // Returns 1 (nothing launched) for weights or shapes it does not take: no
-// row-major copy, exponent-31 scales, more than 4 tokens, K not a multiple
-// of 1024 or above 4096, a pending delta.
+// row-major copy, exponent-31 scales, more than 4 tokens, K other than
+// 1024, 2048 or 4096, a pending delta.
 int32_t launch_i8_narrow(const DeviceWeights* w, int32_t kind, const void* in, const float* delta,
                          const float* gain, const float* qscale, float eps, const float* residual, int32_t tokens,
                          float* y, int32_t ldy, int32_t row_start, int32_t row_end, hipStream_t stream);

@@ -275,7 +275,7 @@ int32_t launch_narrow_tokens(const DeviceWeights* w, int tokens, const void* in,
     }
 }
 
-// NL = K * RW / (1024 * WAVES) weight loads per lane, for K = 1024 .. 4096
+// NL = K * RW / (1024 * WAVES) weight loads per lane, for K = 1024, 2048 or 4096
 template <int RW, int WAVES, int KIND>
 int32_t launch_narrow_nl(const DeviceWeights* w, int tokens, const void* in, const float* gain, const NarrowParams& p,
                          int blocks, size_t lds, hipStream_t s)
@@ -329,7 +329,10 @@ int32_t launch_i8_narrow(const DeviceWeights* w, int32_t kind, const void* in, c
     static const int forced_waves = env_int("NHIP_NARROW_WAVES", 0);
     static const bool norm_ok = env_int("NHIP_NARROW_NORM", 1) == 1;
     if (!w || !w->rowmajor || w->format != WeightFormat::Int8G32 || w->special_scales) return 1;
-    if (tokens < 1 || tokens > 4 || w->cols % 1024 != 0 || w->cols > 4096) return 1;
+    // K = 1024, 2048 or 4096: each wave's K range is then a whole number of
+    // NL row segments (NL = K * RW / (1024 * WAVES)) and the prologue's G4
+    // float4 per thread cover K exactly; K = 3072 would leave a remainder
+    if (tokens < 1 || tokens > 4 || (w->cols != 1024 && w->cols != 2048 && w->cols != 4096)) return 1;
     // a prologue with a pending delta (a decoder fallback path) keeps the
     // 16-row kernel, which also stores x + delta
     if (delta || (kind == kProNorm && !norm_ok)) return 1;

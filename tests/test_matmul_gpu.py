@@ -49,6 +49,8 @@ def assert_tolerance(y, want):
     (17, 48, 256),        # two token blocks
     (33, 80, 512),        # three token blocks
     (4, 1024, 4096),      # K = 4096 (two weight chunks)
+    (3, 1024, 3072),      # K = 3072: not a narrow-kernel shape
+    (1, 3072, 3072),
 ])
 def test_int8_matmul_bit_exact(hip, orc, tokens, rows, cols):
     w, scales, x, q, qs = int8_case(orc, tokens * 1000 + rows + cols, rows, cols, tokens)
