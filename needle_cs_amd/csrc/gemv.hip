@@ -106,7 +106,31 @@ struct MatmulParams {
     uint32_t t0, t1, t2, t3;  // codebook bytes 0..15
     uint32_t x0, x1, x2, x3;  // the split tables of lut4x (TA, TB)
     float byte_scale;
+    // codebook decode kernels: rows n >= split_row[k] (k < split_n, rows
+    // ascending) are stored at row n - split_row[k] of split_y[k] (stride
+    // split_ldy[k]) instead of y, so one launch over matrices stacked by rows
+    // (sharing the activations and K) fills each one's own output
+    int32_t split_n;
+    int32_t split_row[3], split_ldy[3];
+    float* split_y[3];
 };
+
+// Row nn of token t's output (the split outputs, and the row range).
+__device__ __forceinline__ void store_row(const MatmulParams& p, int t, int nn, float v)
+{
+    if (nn < p.row_start || nn >= p.row_end) return;
+    float* y = p.y;
+    int ldy = p.ldy, n = nn;
+#pragma unroll
+    for (int k = 0; k < 3; k++) {
+        if (k < p.split_n && nn >= p.split_row[k]) {
+            y = p.split_y[k];
+            ldy = p.split_ldy[k];
+            n = nn - p.split_row[k];
+        }
+    }
+    y[(size_t)t * ldy + n] = v;
+}
 
 // The argument-segment fields the products and the chain use, read once the
 // first loads are in flight: used only after a barrier, the compiler would
@@ -114,6 +138,12 @@ struct MatmulParams {
 #define MATMUL_TAIL_FIELDS(p)                                                                                   \
     asm volatile("" ::"s"((p).y), "s"((p).ldy), "s"((p).row_start), "s"((p).row_end), "s"((p).swiglu),          \
                  "s"((p).residual), "s"((p).ldd), "s"((p).swz), "s"(blockDim.x))
+
+// The split outputs' fields (codebook decode kernels), read at the same time.
+#define MATMUL_SPLIT_FIELDS(p)                                                                                   \
+    asm volatile("" ::"s"((p).split_n), "s"((p).split_row[0]), "s"((p).split_row[1]), "s"((p).split_row[2]),   \
+                 "s"((p).split_ldy[0]), "s"((p).split_ldy[1]), "s"((p).split_ldy[2]), "s"((p).split_y[0]),     \
+                 "s"((p).split_y[1]), "s"((p).split_y[2]))
 
 // The decode kernels' head (see head_pair): the fields of their first loads.
 #define MATMUL_HEAD_PARAMS const uint8_t *h_tiles, const uint16_t *h_norms, const int8_t *h_q, const float *h_qscale, \
@@ -896,7 +926,7 @@ __global__ __launch_bounds__(512) void matmul_i8_decode_batch_kernel(MatmulBatch
 // in LDS; after one barrier lane (t, r) adds both rows in ascending g and
 // stores acc - bias, Scalar.MatMulRows' operations in its order
 // (Scalar.cs:185-189).
-template <int F, int GPW, bool EXACT>
+template <int F, int GPW, bool EXACT, bool SPLIT>
 __device__ __forceinline__ void cq_decode_tile(const MatmulParams& p, const int tile)
 {
     using T = Traits<F>;
@@ -948,6 +978,7 @@ __device__ __forceinline__ void cq_decode_tile(const MatmulParams& p, const int 
     }
     __builtin_amdgcn_sched_barrier(0);
     MATMUL_TAIL_FIELDS(p);
+    if constexpr (SPLIT) MATMUL_SPLIT_FIELDS(p);
 
 #pragma unroll
     for (int c = 0; c < SETS; c++) {
@@ -1014,7 +1045,10 @@ __device__ __forceinline__ void cq_decode_tile(const MatmulParams& p, const int 
             acc = acc + ra[g];
             bias = bias + rb[g];
         }
-        if (nn >= p.row_start && nn < p.row_end) p.y[(size_t)(x >> 4) * p.ldy + nn] = acc - bias;
+        if constexpr (SPLIT)
+            store_row(p, x >> 4, nn, acc - bias);
+        else if (nn >= p.row_start && nn < p.row_end)
+            p.y[(size_t)(x >> 4) * p.ldy + nn] = acc - bias;
     }
 }
 
@@ -1029,7 +1063,7 @@ __device__ __forceinline__ void cq_decode_tile(const MatmulParams& p, const int 
 // c ^ (x & swz) (the int8 decode path's swizzle); after one barrier lane
 // (t, r) adds both rows in ascending g and stores acc - bias, Scalar.MatMulRows'
 // operations in its order (Scalar.cs:185-189), as cq_decode_tile does.
-template <int F, int GPW, bool EXACT>
+template <int F, int GPW, bool EXACT, bool SPLIT>
 __device__ __forceinline__ void cq_decode_wide_tile(const MatmulParams& p, const int tile)
 {
     using T = Traits<F>;
@@ -1153,18 +1187,22 @@ __device__ __forceinline__ void cq_decode_wide_tile(const MatmulParams& p, const
                 bias = bias + bv4[j];
             }
         }
-        if (nn >= p.row_start && nn < p.row_end) p.y[(size_t)(x >> 4) * p.ldy + nn] = acc - bias;
+        if constexpr (SPLIT)
+            store_row(p, x >> 4, nn, acc - bias);
+        else if (nn >= p.row_start && nn < p.row_end)
+            p.y[(size_t)(x >> 4) * p.ldy + nn] = acc - bias;
     }
 }
 
-template <int F, int GPW, bool EXACT, bool WIDE>
+// SPLIT: the split outputs (MatmulParams::split_n), for stacked matrices.
+template <int F, int GPW, bool EXACT, bool WIDE, bool SPLIT = false>
 __global__ __launch_bounds__(512) void matmul_cq_decode_kernel(MATMUL_HEAD_PARAMS, MatmulParams p)
 {
     MATMUL_TAKE_HEAD(p);
     if constexpr (WIDE)
-        cq_decode_wide_tile<F, GPW, EXACT>(p, p.tile_begin + blockIdx.x);
+        cq_decode_wide_tile<F, GPW, EXACT, SPLIT>(p, p.tile_begin + blockIdx.x);
     else
-        cq_decode_tile<F, GPW, EXACT>(p, p.tile_begin + blockIdx.x);
+        cq_decode_tile<F, GPW, EXACT, SPLIT>(p, p.tile_begin + blockIdx.x);
 }
 
 template <int F, int GPW, bool EXACT, bool WIDE>
@@ -1173,9 +1211,9 @@ __global__ __launch_bounds__(512) void matmul_cq_decode_batch_kernel(MatmulBatch
     const int j = batch_job(b);
     const MatmulParams& p = b.job[j];
     if constexpr (WIDE)
-        cq_decode_wide_tile<F, GPW, EXACT>(p, p.tile_begin + (int)blockIdx.x - b.first[j]);
+        cq_decode_wide_tile<F, GPW, EXACT, false>(p, p.tile_begin + (int)blockIdx.x - b.first[j]);
     else
-        cq_decode_tile<F, GPW, EXACT>(p, p.tile_begin + (int)blockIdx.x - b.first[j]);
+        cq_decode_tile<F, GPW, EXACT, false>(p, p.tile_begin + (int)blockIdx.x - b.first[j]);
 }
 
 // The decode kernel for M <= 4 with its activation rows computed in the
@@ -1450,6 +1488,14 @@ template <int F, int GPW, bool WIDE>
 void launch_cq_decode_w(const MatmulParams& p, bool exact, int waves, size_t lds, hipStream_t stream)
 {
     const int tiles = p.tile_end - p.tile_begin;
+    // split launches: 1..4 tokens, never exact (matmul_cq_split_internal)
+    if constexpr (!WIDE) {
+        if (p.split_n) {
+            hipLaunchKernelGGL((matmul_cq_decode_kernel<F, GPW, false, false, true>), dim3(tiles), dim3(64 * waves),
+                               lds, stream, MATMUL_HEAD_ARGS(p), p);
+            return;
+        }
+    }
     if (exact)
         hipLaunchKernelGGL((matmul_cq_decode_kernel<F, GPW, true, WIDE>), dim3(tiles), dim3(64 * waves), lds, stream,
                            MATMUL_HEAD_ARGS(p), p);
@@ -2087,6 +2133,39 @@ int32_t matmul_cq_internal(const DeviceWeights* w, const int8_t* values, const f
                            int32_t row_end, hipStream_t stream)
 {
     return run_matmul(w, values, scales, offsets, stride, tokens, y, ldy, row_start, row_end, nullptr, stream);
+}
+
+// The codebook decode matmul of every row of w, rows [firsts[k], firsts[k+1])
+// into ys[k] (stride ldys[k]) at their row - firsts[k] (firsts[0] == 0,
+// ascending, parts <= 4): MatMulBatch's jobs as one matrix stacked by rows.
+// Returns 1 (nothing launched) for what it does not take: more than 4
+// tokens, exponent-31 norms, or a shape the decode kernel does not take.
+int32_t matmul_cq_split_internal(const DeviceWeights* w, const int8_t* values, const float* scales,
+                                 const float* offsets, int32_t stride, int32_t tokens, float* const* ys,
+                                 const int32_t* ldys, const int32_t* firsts, int32_t parts, hipStream_t stream)
+{
+    NHIP_REQUIRE(w && w->format != WeightFormat::Int8G32, "weights are not in a codebook format");
+    NHIP_REQUIRE(values && scales && offsets && stride >= w->groups, "null activations or stride %d < groups %d",
+                 stride, w->groups);
+    NHIP_REQUIRE(parts >= 1 && parts <= 4 && firsts[0] == 0, "split matmul: %d parts", parts);
+    for (int k = 0; k < parts; k++) {
+        const int end = k + 1 < parts ? firsts[k + 1] : w->rows;
+        NHIP_REQUIRE(ys[k] && firsts[k] < end && ldys[k] >= end - firsts[k], "split matmul: part %d rows [%d, %d), "
+                     "ldy %d", k, firsts[k], end, ldys[k]);
+    }
+    // 1..4 tokens (the four-group-set tile); with 5..16 the wide tile's
+    // schedule put an argument wait ahead of its first loads
+    if (tokens < 1 || tokens > 4 || w->special_scales) return 1;
+    int32_t rc = ensure_device();
+    if (rc) return rc;
+    MatmulParams p = matmul_params(w, values, scales, offsets, stride, tokens, ys[0], ldys[0], 0, w->rows, nullptr);
+    p.split_n = parts - 1;
+    for (int k = 1; k < parts; k++) {
+        p.split_row[k - 1] = firsts[k];
+        p.split_ldy[k - 1] = ldys[k];
+        p.split_y[k - 1] = ys[k];
+    }
+    return try_cq_decode(w, p, stream);
 }
 
 int32_t launch_decode_masked(const DeviceWeights* w, const int8_t* q, const float* qscale, int32_t tokens, float* y,

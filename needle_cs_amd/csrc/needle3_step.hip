@@ -43,6 +43,10 @@ int32_t attention_decode_impl(const int8_t* d_q, const float* d_qscale, int32_t 
                               const int32_t* d_row_slot, const int32_t* d_row_first, const int32_t* d_row_count,
                               int32_t max_chunks, void* d_workspace, size_t workspace_bytes, float* d_out,
                               int8_t* d_q_out, float* d_qs_out, hipStream_t stream);
+int32_t matmul_cq_split_internal(const DeviceWeights* w, const int8_t* values, const float* scales,
+                                 const float* offsets, int32_t stride, int32_t tokens, float* const* ys,
+                                 const int32_t* ldys, const int32_t* firsts, int32_t parts, hipStream_t stream);
+int32_t weights_cq_create_internal(const nhip_cq* cq, nhip_weights** out);
 
 namespace {
 
@@ -1112,6 +1116,7 @@ struct N3Layer {
     const float *norm_in = nullptr, *q_taps = nullptr, *k_taps = nullptr, *v_taps = nullptr, *q_norm = nullptr,
                 *k_norm = nullptr, *post_norm = nullptr, *pre_hada = nullptr;
     nhip_weights *q = nullptr, *k = nullptr, *v = nullptr, *gate = nullptr, *out = nullptr;
+    nhip_weights* qkvg = nullptr;  // Q, K, V and Gate stacked by rows (the context's own)
     float attn_gate = 0.0f;
     const float *d1 = nullptr, *d2 = nullptr, *b2 = nullptr, *d3 = nullptr, *d4 = nullptr, *w1a = nullptr,
                 *w1b = nullptr, *w2a = nullptr, *w2b = nullptr, *w3a = nullptr, *w3b = nullptr, *cond_v = nullptr,
@@ -1122,6 +1127,7 @@ struct N3Site {
     const uint8_t* tables = nullptr;
     int table_rows = 0, table_cols = 0, table_bits = 0;
     nhip_weights *key = nullptr, *value = nullptr;
+    nhip_weights* key_value = nullptr;  // Key and Value stacked by rows (the context's own)
     const float* taps = nullptr;
 };
 
@@ -1178,6 +1184,7 @@ struct nhip_ctx {
     };
     std::vector<Graph> graphs;  // captured steps, by their shape
     std::vector<void*> allocations;
+    std::vector<nhip_weights*> stacked;  // the stacked matrices above
 };
 
 namespace {
@@ -1205,10 +1212,51 @@ int32_t ctx_alloc(nhip_ctx* c, T** p, size_t count)
     return NHIP_OK;
 }
 
+// Codebook records of one format and K stacked by rows into one matrix the
+// context owns (Q, K, V and Gate; an engram site's Key and Value): they
+// share their activations, and each output row keeps its own chain, so one
+// decode launch with split outputs computes what MatMulBatch's jobs do.
+int32_t stack_rows(nhip_ctx* c, const int* records, int parts, nhip_weights** out)
+{
+    nhip_codebook book2{}, book4{};
+    int32_t rc = nhip_model_codebooks(c->model, &book2, &book4);
+    if (rc) return rc;
+    int rows = 0, cols = 0, bits = 0;
+    for (int k = 0; k < parts; k++) {
+        nhip_record_info ri{};
+        if ((rc = nhip_model_record(c->model, records[k], &ri))) return rc;
+        NHIP_REQUIRE(k == 0 || ((int)ri.shape[1] == cols && (int)ri.bits == bits), "stacked records differ in K or "
+                     "format");
+        rows += (int)ri.shape[0];
+        cols = (int)ri.shape[1];
+        bits = (int)ri.bits;
+    }
+    const size_t row_bytes = (size_t)cols * bits / 8, groups = (size_t)cols / 128;
+    std::vector<uint8_t> codes((size_t)rows * row_bytes);
+    std::vector<uint16_t> norms((size_t)rows * groups);
+    size_t r0 = 0;
+    for (int k = 0; k < parts; k++) {
+        nhip_record_info ri{};
+        nhip_model_record(c->model, records[k], &ri);
+        const size_t n = ri.shape[0];
+        const uint8_t* raw = nhip_model_raw(c->model, records[k]);  // the indices, then the fp16 norms
+        NHIP_REQUIRE(raw, "record %d has no raw copy", records[k]);
+        NHIP_CHECK_HIP(hipMemcpy(codes.data() + r0 * row_bytes, raw, n * row_bytes, hipMemcpyDeviceToHost));
+        NHIP_CHECK_HIP(hipMemcpy(norms.data() + r0 * groups, raw + n * row_bytes, n * groups * 2,
+                                 hipMemcpyDeviceToHost));
+        r0 += n;
+    }
+    const nhip_cq cq{codes.data(), norms.data(), bits == 2 ? &book2 : &book4, rows, cols, bits};
+    if ((rc = weights_cq_create_internal(&cq, out))) return rc;
+    c->stacked.push_back(*out);
+    return NHIP_OK;
+}
+
 // Model.Open's reader over the archive's records, in order (Model.cs:307-371).
 struct RecordCursor {
     const nhip_model* m;
     int next = 0, count = 0;
+    int last = -1;  // the record quant() took last
     int32_t status = NHIP_OK;
     nhip_record_info info(int i)
     {
@@ -1243,6 +1291,7 @@ struct RecordCursor {
             status = NHIP_ERR_FORMAT;
             return nullptr;
         }
+        last = i;
         return nhip_model_weights(m, i);
     }
     const float* dense(size_t elements, const char* what)
@@ -1356,15 +1405,21 @@ int32_t load_model(nhip_ctx* c)
     for (int l = 0; l < c->layers && !r.status; l++) {
         N3Layer& w = c->layer[l];
         w.norm_in = r.dense(d, "NormIn");
+        int qkvg_records[4];
         w.q = r.quant(2, qw, d, "Q");
+        qkvg_records[0] = r.last;
         w.k = r.quant(2, kw, d, "K");
+        qkvg_records[1] = r.last;
         w.v = r.quant(2, vw, d, "V");
+        qkvg_records[2] = r.last;
         w.q_taps = r.dense((size_t)3 * qw, "QTaps");
         w.k_taps = r.dense((size_t)3 * kw, "KTaps");
         w.v_taps = r.dense((size_t)3 * vw, "VTaps");
         w.q_norm = r.dense(c->qk, "QNorm");
         w.k_norm = r.dense(c->qk, "KNorm");
         w.gate = r.quant(2, ow, d, "Gate");
+        qkvg_records[3] = r.last;
+        if (!r.status && (rc = stack_rows(c, qkvg_records, 4, &w.qkvg))) return rc;
         w.out = r.quant(2, d, ow, "Out");
         w.post_norm = r.dense(d, "PostNorm");
         const float* g = r.dense(1, "AttnGate");
@@ -1416,8 +1471,12 @@ int32_t load_model(nhip_ctx* c)
                          "engram tables %ux%u for %d tables of %d slots x %d", ri.shape[0], ri.shape[1], c->engram_tables,
                          c->engram_slots, c->engram_sub);
         }
+        int kv_records[2];
         st.key = r.quant(2, d, d, "engram Key");
+        kv_records[0] = r.last;
         st.value = r.quant(2, d, d, "engram Value");
+        kv_records[1] = r.last;
+        if (!r.status && (rc = stack_rows(c, kv_records, 2, &st.key_value))) return rc;
         st.taps = r.dense((size_t)kEngramTaps * d, "engram Taps");
     }
     c->final_norm = r.dense(d, "FinalNorm");
@@ -1604,7 +1663,11 @@ int32_t enqueue_step(nhip_ctx* c, int rows, int heads, int k, bool argmax, bool 
             const nhip_weights* jw[2] = {st->key, st->value};
             float* jy[2] = {c->key, c->stage + (size_t)kEngramHistory * d};
             const int32_t jl[2] = {d, (kEngramHistory + 1) * d};
-            if ((rc = nhip_matmul_batch_dev(jw, 2, c->act_v, c->act_s, c->act_o, stride_d, rows, jy, jl, s))) return rc;
+            const int32_t jf[2] = {0, d};
+            rc = matmul_cq_split_internal(st->key_value, c->act_v, c->act_s, c->act_o, stride_d, rows, jy, jl, jf, 2, s);
+            if (rc < 0) return rc;
+            if (rc && (rc = nhip_matmul_batch_dev(jw, 2, c->act_v, c->act_s, c->act_o, stride_d, rows, jy, jl, s)))
+                return rc;
             ea = EngramArgs{c->stage,
                             c->engram_hist + (size_t)site * c->slots * kEngramHistory * d,
                             in(c, c->d_in, kInSlots),
@@ -1627,7 +1690,11 @@ int32_t enqueue_step(nhip_ctx* c, int rows, int heads, int k, bool argmax, bool 
         const nhip_weights* pw[4] = {w.q, w.k, w.v, w.gate};
         float* py[4] = {c->raw, c->raw + qw, c->raw + qw + kw, c->gate};
         const int32_t pl[4] = {all, all, all, ow};
-        if ((rc = nhip_matmul_batch_dev(pw, 4, c->act_v, c->act_s, c->act_o, stride_d, rows, py, pl, s))) return rc;
+        const int32_t pf[4] = {0, qw, qw + kw, qw + kw + vw};
+        // one launch over the stacked matrix up to 4 rows; MatMulBatch beyond
+        rc = matmul_cq_split_internal(w.qkvg, c->act_v, c->act_s, c->act_o, stride_d, rows, py, pl, pf, 4, s);
+        if (rc < 0) return rc;
+        if (rc && (rc = nhip_matmul_batch_dev(pw, 4, c->act_v, c->act_s, c->act_o, stride_d, rows, py, pl, s))) return rc;
         const size_t lcell = (size_t)l * c->slots * c->capacity;
         int8_t* keys = c->keys + lcell * kw;
         int8_t* values = c->values + lcell * vw;
@@ -1776,6 +1843,7 @@ int32_t nhip_ctx_destroy(nhip_ctx* c)
     if (c->stream_h) (void)hipStreamSynchronize(c->stream_h);
     for (nhip_ctx::Graph& g : c->graphs) (void)hipGraphExecDestroy(g.exec);
     for (void* p : c->allocations) (void)hipFree(p);
+    for (nhip_weights* w : c->stacked) (void)nhip_weights_destroy(w);
     if (c->h_in) (void)hipHostFree(c->h_in);
     if (c->stream_h) (void)hipStreamDestroy(c->stream_h);
     delete c;
