@@ -641,6 +641,14 @@ __global__ __launch_bounds__(row_threads(MODE)) void decode_attention_row_kernel
         ATTN_TAKE_HEAD(p, n3.raw, positions);
     else
         ATTN_TAKE_HEAD(p, q, qscale);
+    if constexpr (N3) {
+        // the extra column of workgroups (launched with n3.mix): the row's
+        // Sinkhorn4x4, by wave 0, beside the attention
+        if ((int)blockIdx.y == p.heads) {
+            if (threadIdx.x < 64) sinkhorn4x4_wave(p.n3.mix_logits + blockIdx.x * 16, p.n3.mix + blockIdx.x * 16);
+            return;
+        }
+    }
     // scores, then e_s; e_s * valueScale_s (each padded by kVBlock floats:
     // phase 4 reads the last chunk's rows up to the chunk length)
     __shared__ __align__(16) float score[kRowMaxCapacity + kVBlock];
@@ -1172,6 +1180,8 @@ int32_t attention_decode_post_impl(const AttnPostInputs& in, int32_t rows, int32
     return NHIP_OK;
 }
 
+bool attention_needle3_fused(int32_t capacity, int32_t v_dim) { return capacity <= kRowMaxCapacity && v_dim == 64; }
+
 int32_t attention_decode_needle3_impl(const Needle3AttnInputs& in, int32_t rows, int32_t heads, int32_t kv_heads,
                                       int32_t qk_dim, int32_t v_dim, int8_t* d_keys, float* d_key_scales,
                                       int8_t* d_values, float* d_value_scales, int32_t slots, int32_t capacity,
@@ -1179,7 +1189,7 @@ int32_t attention_decode_needle3_impl(const Needle3AttnInputs& in, int32_t rows,
                                       const int32_t* d_row_first, const int32_t* d_row_count, int32_t max_chunks,
                                       float* d_out, hipStream_t stream)
 {
-    if (rows < 1 || capacity > kRowMaxCapacity || v_dim != 64) return 1;
+    if (rows < 1 || !attention_needle3_fused(capacity, v_dim)) return 1;
     NHIP_REQUIRE(heads > 0 && kv_heads > 0 && heads % kv_heads == 0 && slots > 0 && capacity > 0 && max_chunks >= 1,
                  "attention: bad shape");
     NHIP_REQUIRE(qk_dim == 48 || qk_dim == 64, "attention: qk_dim must be 48 or 64 (got %d)", qk_dim);
@@ -1210,8 +1220,9 @@ int32_t attention_decode_needle3_impl(const Needle3AttnInputs& in, int32_t rows,
     p.capacity = capacity;
     p.max_chunks = max_chunks;
     p.inv_sqrt = static_cast<float>(1.0 / std::sqrt(static_cast<double>(qk_dim)));
-    hipLaunchKernelGGL(decode_attention_row_kernel<kRowNeedle3>, dim3(rows, heads), dim3(row_threads(kRowNeedle3)), 0, stream,
-                       ATTN_HEAD_ARGS(p, p.n3.raw, p.positions), p);
+    NHIP_REQUIRE(!in.mix == !in.mix_logits, "attention: Sinkhorn logits and output go together");
+    hipLaunchKernelGGL(decode_attention_row_kernel<kRowNeedle3>, dim3(rows, heads + (in.mix ? 1 : 0)),
+                       dim3(row_threads(kRowNeedle3)), 0, stream, ATTN_HEAD_ARGS(p, p.n3.raw, p.positions), p);
     NHIP_CHECK_HIP(hipGetLastError());
     return NHIP_OK;
 }

@@ -199,7 +199,15 @@ struct Needle3AttnInputs {
     const float* rope_cos;  // [capacity][qk / 2]
     const float* rope_sin;
     const float* history;   // [slots][2][qw], [2][kw], [2][vw]: frame 0, then frame 1
+    // when set, one more workgroup per row forms the row's Sinkhorn4x4 of
+    // its residual-mix logits [rows][16] into mix [rows][16] beside the
+    // attention (only the layer's tail reads it)
+    const float* mix_logits;
+    float* mix;
 };
+// Whether attention_decode_needle3_impl takes a step (caches of at most 512
+// positions, value heads of 64).
+bool attention_needle3_fused(int32_t capacity, int32_t v_dim);
 int32_t attention_decode_needle3_impl(const Needle3AttnInputs& in, int32_t rows, int32_t heads, int32_t kv_heads,
                                       int32_t qk_dim, int32_t v_dim, int8_t* d_keys, float* d_key_scales,
                                       int8_t* d_values, float* d_value_scales, int32_t slots, int32_t capacity,
@@ -540,6 +548,60 @@ __device__ __forceinline__ float exp_poly(float x)
     const float y = __builtin_fmaf(p, r * r, r + 1.0f);
     const float scale = __uint_as_float((uint32_t)((int)n + 127) << 23);
     return y * scale;
+}
+
+// Lane l of a 16-lane row receives lane l + n (n > 0) or l - n (n < 0) of
+// its row, written only into the lanes of bank `bank` (lanes 4 * bank ..
+// 4 * bank + 3 of each row); the other lanes keep `old`.
+template <int n, int bank>
+__device__ __forceinline__ float dpp_bank_shift(float old, float v)
+{
+    constexpr int ctrl = n > 0 ? 0x100 + n : 0x110 - n;
+    return __int_as_float(
+        __builtin_amdgcn_update_dpp(__float_as_int(old), __float_as_int(v), ctrl, 0xF, 1 << bank, false));
+}
+
+// The entry of column (lane & 3) in row p of the 4 x 4 matrix held by lanes
+// e = 4a + c of each 16-lane row: lane 4p + c, reached from bank a by a row
+// shift of 4 (p - a).
+template <int p>
+__device__ __forceinline__ float column_entry(float r)
+{
+    float v = r;  // bank p holds it itself
+    if constexpr (p != 0) v = dpp_bank_shift<4 * p, 0>(v, r);
+    if constexpr (p != 1) v = dpp_bank_shift<4 * (p - 1), 1>(v, r);
+    if constexpr (p != 2) v = dpp_bank_shift<4 * (p - 2), 2>(v, r);
+    if constexpr (p != 3) v = dpp_bank_shift<4 * (p - 3), 3>(v, r);
+    return v;
+}
+
+// Lane q of the quad of 4 lanes (quad_perm [q, q, q, q]).
+template <int q>
+__device__ __forceinline__ float quad_entry(float r)
+{
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(r), q * 0x55, 0xF, 0xF, false));
+}
+
+// Scalar.Sinkhorn4x4 of a 4 x 4 logit matrix (row-major, 16 floats) into
+// `mix` by one wave, one lane per matrix entry (lane e = 4a + c of each
+// 16-lane row, the four rows alike): a matrix row is a quad of lanes and a
+// column the lanes c, 4 + c, 8 + c, 12 + c, reached through DPP.  Every lane
+// of a row or column forms the same left-to-right sum of its four entries,
+// so each normalisation is Scalar.Sinkhorn4x4's.
+__device__ __forceinline__ void sinkhorn4x4_wave(const float* logits, float* mix)
+{
+    const int lane = threadIdx.x & 63;
+    const int e = lane & 15;
+    const float lg = logits[e];
+    const float peak = fmaxf(fmaxf(quad_entry<0>(lg), quad_entry<1>(lg)), fmaxf(quad_entry<2>(lg), quad_entry<3>(lg)));
+    float r = exp_poly(lg - peak);
+    for (int it = 0; it < 20; it++) {
+        const float rs = ((quad_entry<0>(r) + quad_entry<1>(r)) + quad_entry<2>(r)) + quad_entry<3>(r);
+        r = r / rs;
+        const float cs = ((column_entry<0>(r) + column_entry<1>(r)) + column_entry<2>(r)) + column_entry<3>(r);
+        if (cs > 0.0f) r = r / cs;
+    }
+    if (lane < 16) mix[e] = r;
 }
 
 // A 16-entry byte table lookup of four 4-bit codes in three operations, for

@@ -245,6 +245,8 @@ struct HyperArgs {
     Act act;
     int stride;
     int rows;
+    float* mix_logits;  // set: the residual-mix logits [rows][16] go here, for
+                        // the attention launch's Sinkhorn workgroups
 };
 
 // Scalar.MatMulRows' exact int32 dot (Scalar.cs:166-184) of one Cq4 row's
@@ -321,66 +323,14 @@ __device__ __forceinline__ float phi_outputs(const PhiRows& p, int t, int K, int
     return y;
 }
 
-// Lane l of a 16-lane row receives lane l + n (n > 0) or l - n (n < 0) of
-// its row, written only into the lanes of bank `bank` (lanes 4 * bank ..
-// 4 * bank + 3 of each row); the other lanes keep `old`.
-template <int n, int bank>
-__device__ __forceinline__ float dpp_bank_shift(float old, float v)
-{
-    constexpr int ctrl = n > 0 ? 0x100 + n : 0x110 - n;
-    return __int_as_float(
-        __builtin_amdgcn_update_dpp(__float_as_int(old), __float_as_int(v), ctrl, 0xF, 1 << bank, false));
-}
-
-// The entry of column (lane & 3) in row p of the 4 x 4 matrix held by lanes
-// e = 4a + c of each 16-lane row: lane 4p + c, reached from bank a by a row
-// shift of 4 (p - a).
-template <int p>
-__device__ __forceinline__ float column_entry(float r)
-{
-    float v = r;  // bank p holds it itself
-    if constexpr (p != 0) v = dpp_bank_shift<4 * p, 0>(v, r);
-    if constexpr (p != 1) v = dpp_bank_shift<4 * (p - 1), 1>(v, r);
-    if constexpr (p != 2) v = dpp_bank_shift<4 * (p - 2), 2>(v, r);
-    if constexpr (p != 3) v = dpp_bank_shift<4 * (p - 3), 3>(v, r);
-    return v;
-}
-
-// Lane q of the quad of 4 lanes (quad_perm [q, q, q, q]).
-template <int q>
-__device__ __forceinline__ float quad_entry(float r)
-{
-    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(r), q * 0x55, 0xF, 0xF, false));
-}
-
-// Sinkhorn4x4 of row t's residual-mix logits (Engine.cs:2374-2378) by one
-// wave, one lane per matrix entry (lane e = 4a + c of each 16-lane row, the
-// four rows alike): a matrix row is a quad of lanes and a column the lanes
-// c, 4 + c, 8 + c, 12 + c, reached through DPP.  Every lane of a row or
-// column forms the same left-to-right sum of its four entries, so each
-// normalisation is Scalar.Sinkhorn4x4's.
-__device__ __forceinline__ void sinkhorn_wave(const HyperArgs& a, int t, const float* logits)
-{
-    const int lane = threadIdx.x & 63;
-    const int e = lane & 15;
-    const float lg = logits[e];
-    const float peak = fmaxf(fmaxf(quad_entry<0>(lg), quad_entry<1>(lg)), fmaxf(quad_entry<2>(lg), quad_entry<3>(lg)));
-    float r = exp_poly(lg - peak);
-    for (int it = 0; it < 20; it++) {
-        const float rs = ((quad_entry<0>(r) + quad_entry<1>(r)) + quad_entry<2>(r)) + quad_entry<3>(r);
-        r = r / rs;
-        const float cs = ((column_entry<0>(r) + column_entry<1>(r)) + column_entry<2>(r)) + column_entry<3>(r);
-        if (cs > 0.0f) r = r / cs;
-    }
-    if (lane < 16) a.mix[t * 16 + e] = r;
-}
-
 // RunLayerBatch's per-row mix (Engine.cs:2356-2381): the phi rows, hpre /
 // postGate by Sigmoid, Mix4 of the lanes into input and residual, Sinkhorn4x4
 // of the residual-mix logits.  Workgroup t < rows takes row t's 4 pre and 4
 // post outputs and the mix; only the layer's tail reads the Sinkhorn matrix,
 // so workgroup rows + t forms row t's 16 residual-mix outputs and its
-// Sinkhorn beside it.  Then, on layers without an engram,
+// Sinkhorn (Engine.cs:2374-2378) beside it -- or, with a.mix_logits, only
+// the logits, for the attention launch's Sinkhorn workgroups (whose time
+// the attention hides).  Then, on layers without an engram,
 // RunAttentionBatch's CenteredRmsFakeA8 of the residual and its 2-bit Prepare
 // (Engine.cs:2487-2490); on engram layers, ApplyEngramBatch's input
 // (Engine.cs:2404-2414): every table's GatherRow (zeros for row -1),
@@ -394,9 +344,14 @@ __global__ __launch_bounds__(kThreads) void n3_hyper_kernel(HyperArgs a)
         const int t = (int)blockIdx.x - a.rows;
         const int first[4] = {0, 16, 16, 16};
         const float y = phi_outputs(a.phi, t, K, 2, first, prod);
-        if (threadIdx.x < 16) logits[threadIdx.x] = a.a_res[0] * y + a.b_res[threadIdx.x];
+        const float lg = a.a_res[0] * y + a.b_res[threadIdx.x & 15];
+        if (a.mix_logits) {
+            if (threadIdx.x < 16) a.mix_logits[t * 16 + threadIdx.x] = lg;
+            return;
+        }
+        if (threadIdx.x < 16) logits[threadIdx.x] = lg;
         __syncthreads();
-        if (threadIdx.x < 64) sinkhorn_wave(a, t, logits);
+        if (threadIdx.x < 64) sinkhorn4x4_wave(logits, a.mix + t * 16);
         return;
     }
     __shared__ __align__(16) float x[kMaxDim];
@@ -1164,7 +1119,7 @@ struct nhip_ctx {
     // alternate between the two stream buffers)
     float *stream_a = nullptr, *stream_b = nullptr, *normed = nullptr, *input = nullptr, *residual = nullptr,
           *raw = nullptr, *gate = nullptr, *att = nullptr, *proj = nullptr, *key = nullptr, *stage = nullptr,
-          *ein = nullptr, *post_gate = nullptr, *mix = nullptr, *qs = nullptr, *logits = nullptr, *act_s = nullptr,
+          *ein = nullptr, *post_gate = nullptr, *mix = nullptr, *mix_logits = nullptr, *qs = nullptr, *logits = nullptr, *act_s = nullptr,
           *act_o = nullptr, *act4_s = nullptr, *act4_o = nullptr;
     int8_t *act_v = nullptr, *act4_v = nullptr, *q8 = nullptr;  // act4: the stream's 4-bit Prepare (phi input)
     int32_t* d_in = nullptr;  // the per-row inputs of a step, kInSections x max_rows, then the engram rows
@@ -1523,6 +1478,7 @@ int32_t alloc_state(nhip_ctx* c)
         (rc = ctx_alloc(c, &c->ein, (size_t)R * d)) || (rc = ctx_alloc(c, &c->act4_v, (size_t)R * sw)) ||
         (rc = ctx_alloc(c, &c->act4_s, (size_t)R * stride4)) || (rc = ctx_alloc(c, &c->act4_o, (size_t)R * stride4)) ||
         (rc = ctx_alloc(c, &c->post_gate, (size_t)R * 4)) || (rc = ctx_alloc(c, &c->mix, (size_t)R * 16)) ||
+        (rc = ctx_alloc(c, &c->mix_logits, (size_t)R * 16)) ||
         (rc = ctx_alloc(c, &c->q8, (size_t)R * qw)) || (rc = ctx_alloc(c, &c->qs, (size_t)R * c->heads)) ||
         (rc = ctx_alloc(c, &c->logits, (size_t)R * c->vocab)) || (rc = ctx_alloc(c, &c->act_v, (size_t)R * sw)) ||
         (rc = ctx_alloc(c, &c->d_topk_idx, (size_t)R * 8)) || (rc = ctx_alloc(c, &c->d_topk_lp, (size_t)R * 8)) ||
@@ -1629,6 +1585,10 @@ int32_t enqueue_step(nhip_ctx* c, int rows, int heads, int k, bool argmax, bool 
     float* nxt = c->stream_b;
     // EngineCore's embeddingScale = sqrt(dim) (Engine.cs:123), host sqrtf
     const float emb_scale_m1 = std::sqrt((float)d) - 1.0f;
+    // steps whose rows are one per slot run the attention in one launch
+    // (attention_decode_needle3_impl), which then also forms Sinkhorn4x4 of
+    // the mix kernel's residual-mix logits
+    const bool sink_in_attention = single_runs && attention_needle3_fused(c->capacity, c->vd);
     hipLaunchKernelGGL(n3_embed_kernel, dim3(rows), dim3(kThreads), 0, s, c->embedding_raw, c->vocab, d,
                        c->embedding_bits, c->book4, in(c, c->d_in, kInTokens), emb_scale_m1, cur, act4, stride4);
     NHIP_CHECK_HIP(hipGetLastError());
@@ -1655,7 +1615,7 @@ int32_t enqueue_step(nhip_ctx* c, int rows, int heads, int k, bool argmax, bool 
                      c->b_res + 16 * l, l % kLanes, d, c->input, c->residual, c->post_gate, c->mix, w.norm_in,
                      st ? st->tables : nullptr, st ? st->table_rows : 0, st ? st->table_cols : 0,
                      st ? st->table_bits : 0, c->engram_tables, st && st->table_bits == 2 ? c->book2 : c->book4,
-                     in_erows(c, c->d_in), act, stride_d, rows};
+                     in_erows(c, c->d_in), act, stride_d, rows, sink_in_attention ? c->mix_logits : nullptr};
         hipLaunchKernelGGL(n3_hyper_kernel, dim3(2 * rows), dim3(kThreads), 0, s, ha);
         NHIP_CHECK_HIP(hipGetLastError());
         EngramArgs ea{};
@@ -1710,12 +1670,20 @@ int32_t enqueue_step(nhip_ctx* c, int rows, int heads, int k, bool argmax, bool 
         // attention launch; otherwise (runs of rows, long caches) two launches
         int32_t fused = 1;
         if (single_runs) {
-            const Needle3AttnInputs n3in{c->raw, {w.q_taps, w.k_taps, w.v_taps}, w.q_norm, w.k_norm,
-                                         c->rope_cos, c->rope_sin, qkv_hist};
+            const Needle3AttnInputs n3in{c->raw,
+                                         {w.q_taps, w.k_taps, w.v_taps},
+                                         w.q_norm,
+                                         w.k_norm,
+                                         c->rope_cos,
+                                         c->rope_sin,
+                                         qkv_hist,
+                                         sink_in_attention ? c->mix_logits : nullptr,
+                                         sink_in_attention ? c->mix : nullptr};
             fused = attention_decode_needle3_impl(n3in, rows, H, KV, c->qk, c->vd, keys, kscale, values, vscale,
                                                   c->slots, c->capacity, in(c, c->d_in, kInSlots),
                                                   in(c, c->d_in, kInPos), first, count, c->max_chunks, c->att, s);
             if (fused < 0) return fused;
+            NHIP_REQUIRE(fused == 0 || !sink_in_attention, "attention launch refused a step it takes");
         }
         if (fused == 1) {
             if ((rc = needle3_attention_inputs_impl(c->raw, rows, H, KV, c->qk, c->vd, w.q_taps, w.k_taps, w.v_taps,
