@@ -636,15 +636,25 @@ __device__ __forceinline__ int wave_sum_i32(int v)
     return v;
 }
 
-// One butterfly stage of hadamard_wave: lanes e and e ^ S pair up.
+// Bytes idx[0..3] (each 0..3) of the four-byte table t0: the 2-bit
+// codebook's levels of four indices.
+__device__ __forceinline__ uint32_t lut2(uint32_t idx, uint32_t t0)
+{
+    return __builtin_amdgcn_perm(t0, t0, idx);
+}
+
+// One butterfly stage of hadamard_wave: lanes e and e ^ S pair up; the lower
+// lane takes a + b, the upper a - b, both as p + (+-v) (p the partner's value;
+// IEEE addition commutes and p - v is p + (-v)), one add per value into
+// which the compiler folds the DPP move.
 template <int S>
 __device__ __forceinline__ void hadamard_stage(float& v0, float& v1)
 {
-    const float p0 = lane_xor<S>(v0);
-    const float p1 = lane_xor<S>(v1);
-    const bool upper = (threadIdx.x & S) != 0;
-    v0 = upper ? p0 - v0 : v0 + p0;
-    v1 = upper ? p1 - v1 : v1 + p1;
+    const uint32_t neg = ((uint32_t)threadIdx.x & S) ? 0x80000000u : 0u;
+    const float n0 = __uint_as_float(__float_as_uint(v0) ^ neg);
+    const float n1 = __uint_as_float(__float_as_uint(v1) ^ neg);
+    v0 = lane_xor<S>(v0) + n0;
+    v1 = lane_xor<S>(v1) + n1;
 }
 
 // Scalar.Hadamard (Scalar.cs:76-89) of one 128-element group held by a wave:
@@ -669,7 +679,11 @@ __device__ __forceinline__ void hadamard_wave(float& v0, float& v1)
 // Hadamard-rotated group held by a wave (as hadamard_wave leaves it):
 // QuantizeInt8 (absmax / 127), the Planes permutation (Scalar.cs:91-111:
 // destination d takes quantized[src(d)]) into dst[128], and lane 0 writes the
-// group's scale and offset 63 * sum(q).
+// group's scale and offset 63 * sum(q).  WORDS (2-bit only): dst takes the
+// planes positions word-interleaved instead, position 32p + j at byte
+// 16 * (j / 4) + 4p + j % 4, so that one 16-byte read finds the four planes'
+// words that pair with index word j / 4 of the group.
+template <bool WORDS = false>
 __device__ __forceinline__ void prepare_group_wave(float v0, float v1, int bits, int8_t* dst, float* scale_out,
                                                    float* offset_out)
 {
@@ -692,7 +706,8 @@ __device__ __forceinline__ void prepare_group_wave(float v0, float v1, int bits,
         }
         const int a = __shfl(q0, sidx & 63);
         const int b = __shfl(q1, sidx & 63);
-        dst[d] = static_cast<int8_t>(sidx < 64 ? a : b);
+        const int at = WORDS ? 16 * ((d & 31) >> 2) + 4 * (d >> 5) + (d & 3) : d;
+        dst[at] = static_cast<int8_t>(sidx < 64 ? a : b);
     }
     if (lane == 0) {
         *scale_out = scale;

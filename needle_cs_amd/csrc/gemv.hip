@@ -164,11 +164,6 @@ __device__ __forceinline__ void store_row(const MatmulParams& p, int t, int nn, 
         (p).mask_rows = head_hi(h_begin_mask); \
     } while (0)
 
-__device__ __forceinline__ uint32_t lut2(uint32_t idx, uint32_t t0)
-{
-    return __builtin_amdgcn_perm(t0, t0, idx);
-}
-
 __device__ __forceinline__ uint32_t lut4(uint32_t idx, uint32_t t0, uint32_t t1, uint32_t t2, uint32_t t3)
 {
     const uint32_t sel = idx & 0x07070707u;

@@ -121,15 +121,30 @@ __device__ __forceinline__ void prepare_row(const float* v, int cols, int bits, 
     }
 }
 
+// A workgroup barrier that orders LDS only: the waves' outstanding global
+// loads and stores stay in flight across it (__syncthreads waits for them),
+// for code whose waves share data through LDS alone.
+__device__ __forceinline__ void lds_barrier()
+{
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 // Ops.InverseRms of an LDS row x[0..n) (written before the call and
 // synchronised), its sum of squares in the AVX2 tier's order by wave 0.
+// LDS: the closing barrier is lds_barrier.
+template <bool LDS = false>
 __device__ __forceinline__ float row_inverse_rms(const float* x, int n, float* slot)
 {
     if (threadIdx.x < 64) {
         const float sum = wave_v256_sum(x, x, n);
         if (threadIdx.x == 0) *slot = inverse_rms_of(sum, n);
     }
-    __syncthreads();
+    if constexpr (LDS)
+        lds_barrier();
+    else
+        __syncthreads();
     return *slot;
 }
 
@@ -255,9 +270,8 @@ struct HyperArgs {
 // 2h * 32 + j in its low nibble and (2h + 1) * 32 + j in its high nibble.
 // The codes go through lut4x to their codebook bytes (below 128, so the
 // signed byte dot is exact).
-__device__ __forceinline__ int cq4_group_dot(const uint8_t* codes, const int8_t* x, const uint32_t (&split)[4])
+__device__ __forceinline__ int cq4_group_dot(const uint4 (&w4)[4], const int8_t* x, const uint32_t (&split)[4])
 {
-    const uint4* w4 = reinterpret_cast<const uint4*>(codes);
     const uint4* x4 = reinterpret_cast<const uint4*>(x);
     int dot = 0;
 #pragma unroll
@@ -282,45 +296,192 @@ __device__ __forceinline__ int cq4_group_dot(const uint8_t* codes, const int8_t*
     return dot;
 }
 
-// `outputs` phi rows of row t: the workgroup's threads take the (output,
-// group) pairs, each forming the group's dot and the two products of
-// Scalar.MatMulRows' chain (Scalar.cs:146-192): scaled = (HalfToSingle(norm)
-// * ByteScale) * scale[g], scaled * dot and scaled * offset[g], into
-// prod[2 * (output * groups + group) + 0 / 1].  After a barrier, lane o <
-// outputs adds them in ascending group order (accumulator += scaled * dot,
-// bias += scaled * offset) and returns accumulator - bias (other lanes
-// return 0).  first[m] is the first output of matrix m (outputs first[m] ..
-// first[m + 1] - 1 read its rows 0, 1, ...).
-__device__ __forceinline__ float phi_outputs(const PhiRows& p, int t, int K, int m0, const int (&first)[4],
-                                             float* prod)
+// Thread u's (output, group) unit of `outputs` phi rows (u < outputs * K /
+// 128, at most kThreads units): its 64 code bytes and fp16 norm, loaded
+// ahead of the activations they meet.  first[m] is the first output of
+// matrix m (outputs first[m] .. first[m + 1] - 1 read its rows 0, 1, ...).
+struct PhiUnit {
+    uint4 w[4];
+    uint32_t norm;
+};
+
+// A global-memory pointer argument held in scalar registers: selecting
+// between such values per lane stays a select, where selecting struct fields
+// per lane becomes a load of the chosen field through a vector address (and a
+// vmcnt(0) wait that also waits for every global load issued before it).
+template <typename T>
+using global_ptr = const __attribute__((address_space(1))) T*;
+template <typename T>
+__device__ __forceinline__ global_ptr<T> scalar_ptr(const T* p)
 {
+    const uint64_t v = reinterpret_cast<uint64_t>(p);
+    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
+    const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+    return (global_ptr<T>)(((uint64_t)hi << 32) | lo);
+}
+
+__device__ __forceinline__ PhiUnit phi_load(const PhiRows& p, int K, int m0, const int (&first)[4])
+{
+    PhiUnit r{};
     const int groups = K / 128, outputs = first[3] - first[0];
-    const int8_t* x = p.in.values + (size_t)t * K;
-    const float* scales = p.in.scales + (size_t)t * p.stride;
-    const float* offsets = p.in.offsets + (size_t)t * p.stride;
-    for (int u = threadIdx.x; u < outputs * groups; u += kThreads) {
+    const int u = threadIdx.x;
+    if (u < outputs * groups) {
         const int o = u / groups, g = u - o * groups;
         const int m = m0 + (o >= first[1] - first[0]) + (o >= first[2] - first[0]);
-        const int r = o + first[0] - first[m - m0];
-        const float scaled = ref_half_to_single(p.norms[m][(size_t)r * groups + g]) * p.byte_scale * scales[g];
-        const int dot = cq4_group_dot(p.codes[m] + (size_t)r * (K / 2) + g * 64, x + g * 128, p.split);
+        const int row = o + first[0] - first[m - m0];
+        const global_ptr<uint8_t> c0 = scalar_ptr(p.codes[0]), c1 = scalar_ptr(p.codes[1]),
+                                  c2 = scalar_ptr(p.codes[2]);
+        const global_ptr<uint16_t> n0 = scalar_ptr(p.norms[0]), n1 = scalar_ptr(p.norms[1]),
+                                   n2 = scalar_ptr(p.norms[2]);
+        const global_ptr<uint8_t> codes = m == 0 ? c0 : (m == 1 ? c1 : c2);
+        const global_ptr<uint16_t> norms = m == 0 ? n0 : (m == 1 ? n1 : n2);
+        typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+        const global_ptr<u32x4> w4 = (global_ptr<u32x4>)(codes + (size_t)row * (K / 2) + g * 64);
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const u32x4 v = w4[k];
+            r.w[k] = make_uint4(v.x, v.y, v.z, v.w);
+        }
+        r.norm = norms[(size_t)row * groups + g];
+    }
+    return r;
+}
+
+// The phi outputs of one row, whose prepared activations are x [K] and its
+// group scales / offsets: thread u forms its unit's group dot and the two
+// products of Scalar.MatMulRows' chain (Scalar.cs:146-192): scaled =
+// (HalfToSingle(norm) * ByteScale) * scale[g], scaled * dot and scaled *
+// offset[g], into prod[2 * u + 0 / 1].  After a barrier, lane o < outputs
+// adds them in ascending group order (accumulator += scaled * dot, bias +=
+// scaled * offset) and returns accumulator - bias (other lanes return 0).
+__device__ __forceinline__ float phi_outputs(const PhiRows& p, const PhiUnit& unit, const int8_t* x,
+                                             const float* scales, const float* offsets, int K,
+                                             const int (&first)[4], float* prod)
+{
+    const int groups = K / 128, outputs = first[3] - first[0];
+    const int u = threadIdx.x;
+    if (u < outputs * groups) {
+        const int g = u % groups;
+        const float scaled = ref_half_to_single(unit.norm) * p.byte_scale * scales[g];
+        const int dot = cq4_group_dot(unit.w, x + g * 128, p.split);
         prod[2 * u] = scaled * (float)dot;
         prod[2 * u + 1] = scaled * offsets[g];
     }
-    __syncthreads();
+    lds_barrier();
     float y = 0.0f;
     const int o = threadIdx.x;
     if (o < outputs) {
-        const float2* pr = reinterpret_cast<const float2*>(prod) + o * groups;
+        // groups % 4 == 0 (K = 4 * dim, dim % 128 == 0): two groups a float4,
+        // eight groups' reads ahead of their adds
+        const float4* pr = reinterpret_cast<const float4*>(prod) + o * (groups / 2);
         float accumulator = 0.0f, bias = 0.0f;
-        for (int g = 0; g < groups; g++) {
-            const float2 v = pr[g];
+        int g = 0;
+        for (; g + 8 <= groups; g += 8) {
+            const float4 v[4] = {pr[g / 2], pr[g / 2 + 1], pr[g / 2 + 2], pr[g / 2 + 3]};
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                accumulator += v[j].x;
+                bias += v[j].y;
+                accumulator += v[j].z;
+                bias += v[j].w;
+            }
+        }
+        for (; g < groups; g += 2) {
+            const float4 v = pr[g / 2];
             accumulator += v.x;
             bias += v.y;
+            accumulator += v.z;
+            bias += v.w;
         }
         y = accumulator - bias;
     }
     return y;
+}
+
+// Thread i < 24's phi output affine map, z = ga * y + gb: i < 4 the pre
+// outputs (a_pre, b_pre[i]), then the post (a_post, b_post[i - 4]) and the
+// residual-mix logits (a_res, b_res[i - 8]).
+__device__ __forceinline__ void phi_affine(const HyperArgs& a, float& ga, float& gb)
+{
+    const int i = threadIdx.x;
+    const global_ptr<float> pa[3] = {scalar_ptr(a.a_pre), scalar_ptr(a.a_post), scalar_ptr(a.a_res)};
+    const global_ptr<float> pb[3] = {scalar_ptr(a.b_pre), scalar_ptr(a.b_post), scalar_ptr(a.b_res)};
+    const int m = i < 4 ? 0 : (i < 8 ? 1 : 2);
+    const global_ptr<float> ap = m == 0 ? pa[0] : (m == 1 ? pa[1] : pa[2]);
+    const global_ptr<float> bp = m == 0 ? pb[0] : (m == 1 ? pb[1] : pb[2]);
+    ga = 0.0f;
+    gb = 0.0f;
+    if (i < 24) {
+        ga = ap[0];
+        gb = bp[i - (m == 0 ? 0 : (m == 1 ? 4 : 8))];
+    }
+}
+
+// The rest of row t's mix once thread i < 8 holds its phi output y (i < 4:
+// pre, else post) and its affine map ga, gb: hpre / postGate by Sigmoid,
+// Mix4 of the stream lanes sv into input and residual, then on layers
+// without an engram the attention input's CenteredRmsFakeA8 and 2-bit
+// Prepare, on engram layers the gathered engram input's FakeA8 and 2-bit
+// Prepare (RunLayerBatch, Engine.cs:2356-2414).  The attention input's
+// FakeA8 peak is taken with the mix, before the norm: with v = (1 + s) * u
+// and inverse > 0, max |v * inverse| is RoundNearest(max |v| * inverse), as
+// rounding is monotone, so the scaling and the int8 round trip run in one
+// pass after the sum of squares.
+__device__ __forceinline__ void hyper_mix_row(const HyperArgs& a, int t, float y, float ga, float gb,
+                                              const float (&sv)[kPer][kLanes], const float (&sn)[kPer], float* x,
+                                              float* sq, float* hpre, float* red, float* inv_s)
+{
+    const int dim = a.dim;
+    const int i = threadIdx.x;
+    if (i < 4) hpre[i] = sigmoid_poly(ga * y + gb + (i == a.lane ? 4.0f : -4.0f));
+    if (i >= 4 && i < 8) a.post_gate[t * 4 + i - 4] = 2.0f * sigmoid_poly(ga * y + gb + (i - 4 == a.lane ? 0.0f : -4.0f));
+    lds_barrier();
+    float uv[kPer], peak = 0.0f;
+#pragma unroll
+    for (int q = 0; q < kPer; q++) {
+        const int c = col_of(q);
+        if (c < dim) {
+            const float u = hpre[0] * sv[q][0] + hpre[1] * sv[q][1] + hpre[2] * sv[q][2] + hpre[3] * sv[q][3];
+            a.input[(size_t)t * dim + c] = u;
+            a.residual[(size_t)t * dim + c] = u;
+            x[c] = u;
+            uv[q] = u;
+            peak = fmaxf(peak, fabsf((1.0f + sn[q]) * u));
+        }
+    }
+    if (!a.tables) {
+        peak = wave_max(peak);
+        if ((i & 63) == 0) red[i >> 6] = peak;
+    }
+    lds_barrier();
+    if (a.tables) {
+        const int sub = a.table_cols, per = sub / 128;
+        for (int unit = i >> 6; unit < a.tables_count * per; unit += kWaves) {
+            const int table = unit / per, g = unit % per;
+            const int r = a.erows[t * a.tables_count + table];
+            float v0 = 0.0f, v1 = 0.0f;
+            if (r >= 0) gather_group_wave(a.tables, a.table_rows, sub, a.table_bits, a.book, r, g, v0, v1);
+            sq[table * sub + g * 128 + (i & 63)] = v0;
+            sq[table * sub + g * 128 + 64 + (i & 63)] = v1;
+        }
+        __syncthreads();
+        fake_row(sq, dim, red);
+        prepare_row(sq, dim, 2, a.act, a.stride, t);
+        return;
+    }
+    const float inverse = row_inverse_rms<true>(x, dim, inv_s);
+    float m = red[0];
+    for (int w = 1; w < kWaves; w++) m = fmaxf(m, red[w]);
+    const float top = m * inverse;
+    const float scale = top > 0.0f ? top / 127.0f : 1.0f;
+    const float round = 1.0f / scale;
+#pragma unroll
+    for (int q = 0; q < kPer; q++) {
+        const int c = col_of(q);
+        if (c < dim) x[c] = clamp_q(((1.0f + sn[q]) * uv[q] * inverse) * round) * scale;
+    }
+    lds_barrier();
+    prepare_row(x, dim, 2, a.act, a.stride, t);
 }
 
 // RunLayerBatch's per-row mix (Engine.cs:2356-2381): the phi rows, hpre /
@@ -343,8 +504,12 @@ __global__ __launch_bounds__(kThreads) void n3_hyper_kernel(HyperArgs a)
     if ((int)blockIdx.x >= a.rows) {
         const int t = (int)blockIdx.x - a.rows;
         const int first[4] = {0, 16, 16, 16};
-        const float y = phi_outputs(a.phi, t, K, 2, first, prod);
-        const float lg = a.a_res[0] * y + a.b_res[threadIdx.x & 15];
+        const PhiUnit unit = phi_load(a.phi, K, 2, first);
+        const float ga = a.a_res[0], gb = a.b_res[threadIdx.x & 15];
+        const float y = phi_outputs(a.phi, unit, a.phi.in.values + (size_t)t * K,
+                                    a.phi.in.scales + (size_t)t * a.phi.stride,
+                                    a.phi.in.offsets + (size_t)t * a.phi.stride, K, first, prod);
+        const float lg = ga * y + gb;
         if (a.mix_logits) {
             if (threadIdx.x < 16) a.mix_logits[t * 16 + threadIdx.x] = lg;
             return;
@@ -360,7 +525,10 @@ __global__ __launch_bounds__(kThreads) void n3_hyper_kernel(HyperArgs a)
     __shared__ float red[kWaves];
     __shared__ float inv_s;
     const int t = blockIdx.x;
-    const int i = threadIdx.x;
+    const int first[4] = {0, 4, 8, 8};
+    const PhiUnit unit = phi_load(a.phi, K, 0, first);
+    float ga, gb;
+    phi_affine(a, ga, gb);
     const float* s = a.stream + (size_t)t * kLanes * dim;
     float sv[kPer][kLanes], sn[kPer];
 #pragma unroll
@@ -372,50 +540,10 @@ __global__ __launch_bounds__(kThreads) void n3_hyper_kernel(HyperArgs a)
             sn[q] = a.norm_in[c];
         }
     }
-    {
-        const int first[4] = {0, 4, 8, 8};
-        const float y = phi_outputs(a.phi, t, K, 0, first, prod);
-        if (i < 4) hpre[i] = sigmoid_poly(a.a_pre[0] * y + a.b_pre[i] + (i == a.lane ? 4.0f : -4.0f));
-        if (i >= 4 && i < 8)
-            a.post_gate[t * 4 + i - 4] =
-                2.0f * sigmoid_poly(a.a_post[0] * y + a.b_post[i - 4] + (i - 4 == a.lane ? 0.0f : -4.0f));
-    }
-    __syncthreads();
-#pragma unroll
-    for (int q = 0; q < kPer; q++) {
-        const int c = col_of(q);
-        if (c < dim) {
-            const float u = hpre[0] * sv[q][0] + hpre[1] * sv[q][1] + hpre[2] * sv[q][2] + hpre[3] * sv[q][3];
-            a.input[(size_t)t * dim + c] = u;
-            a.residual[(size_t)t * dim + c] = u;
-            x[c] = u;
-        }
-    }
-    __syncthreads();
-    if (a.tables) {
-        const int sub = a.table_cols, per = sub / 128;
-        for (int unit = i >> 6; unit < a.tables_count * per; unit += kWaves) {
-            const int table = unit / per, g = unit % per;
-            const int r = a.erows[t * a.tables_count + table];
-            float v0 = 0.0f, v1 = 0.0f;
-            if (r >= 0) gather_group_wave(a.tables, a.table_rows, sub, a.table_bits, a.book, r, g, v0, v1);
-            sq[table * sub + g * 128 + (i & 63)] = v0;
-            sq[table * sub + g * 128 + 64 + (i & 63)] = v1;
-        }
-        __syncthreads();
-        fake_row(sq, dim, red);
-        prepare_row(sq, dim, 2, a.act, a.stride, t);
-        return;
-    }
-    const float inverse = row_inverse_rms(x, dim, &inv_s);
-#pragma unroll
-    for (int q = 0; q < kPer; q++) {
-        const int c = col_of(q);
-        if (c < dim) x[c] = (1.0f + sn[q]) * x[c] * inverse;
-    }
-    __syncthreads();
-    fake_row(x, dim, red);
-    prepare_row(x, dim, 2, a.act, a.stride, t);
+    const float y = phi_outputs(a.phi, unit, a.phi.in.values + (size_t)t * K,
+                                a.phi.in.scales + (size_t)t * a.phi.stride, a.phi.in.offsets + (size_t)t * a.phi.stride,
+                                K, first, prod);
+    hyper_mix_row(a, t, y, ga, gb, sv, sn, x, sq, hpre, red, &inv_s);
 }
 
 // ----------------------------------------------------------- engram --
@@ -538,11 +666,6 @@ __global__ __launch_bounds__(kThreads) void n3_engram_mix_kernel(EngramArgs a)
 
 // ------------------------------------------------- attention epilogue --
 
-// Scalar.GateFakeA8 on row t of the attention output: x *= Sigmoid(gate),
-// the fake int8 round trip at the row's peak, and the 2-bit Prepare of the
-// output matmul.  On engram layers the run-end rows also move their slot's
-// engram history on (Engine.cs:2439): the nine frames before the sequence's
-// end.  This runs after every row's engram mix has read the old history.
 // The slots' Q/K/V frames (the three-tap convolution's history) of a layer.
 struct QkvHistArgs {
     float* history;  // [slots] x ([2][qw], [2][kw], [2][vw]), frame 1 the latest
@@ -553,33 +676,81 @@ struct QkvHistArgs {
     int qw, kw, vw;
 };
 
+// The run's last row moves its slot's Q/K/V frames on: frame 0 takes the row
+// before it (the old frame 1 for a one-row run), frame 1 the row itself
+// (Scalar.Taps3's history, TapsAndAttentionHeadsSingle).  qkv_hist_load reads
+// the new frames (true when row t ends its run), qkv_hist_store writes them.
+__device__ __forceinline__ bool qkv_hist_load(const QkvHistArgs& h, int t, float* hv0, float* hv1)
+{
+    if (h.run_end[t] == 0) return false;
+    const int all = h.qw + h.kw + h.vw;
+    const float* hist = h.history + (size_t)h.row_slot[t] * 2 * all;
+    const bool run1 = t > h.run_start[t];
+#pragma unroll
+    for (int q = 0; q < kHistPer; q++) {
+        const int c = col_of(q);
+        if (c < all) {
+            const int base = c < h.qw ? 0 : (c < h.qw + h.kw ? h.qw : h.qw + h.kw);
+            const int width = c < h.qw ? h.qw : (c < h.qw + h.kw ? h.kw : h.vw);
+            hv0[q] = run1 ? h.raw[(size_t)(t - 1) * all + c] : hist[2 * base + (c - base) + width];
+            hv1[q] = h.raw[(size_t)t * all + c];
+        }
+    }
+    return true;
+}
+
+__device__ __forceinline__ void qkv_hist_store(const QkvHistArgs& h, int t, const float* hv0, const float* hv1)
+{
+    const int all = h.qw + h.kw + h.vw;
+    float* hist = h.history + (size_t)h.row_slot[t] * 2 * all;
+#pragma unroll
+    for (int q = 0; q < kHistPer; q++) {
+        const int c = col_of(q);
+        if (c < all) {
+            const int base = c < h.qw ? 0 : (c < h.qw + h.kw ? h.qw : h.qw + h.kw);
+            const int width = c < h.qw ? h.qw : (c < h.qw + h.kw ? h.kw : h.vw);
+            hist[2 * base + (c - base)] = hv0[q];
+            hist[2 * base + (c - base) + width] = hv1[q];
+        }
+    }
+}
+
+// On engram layers a run-end row moves its slot's engram history on
+// (Engine.cs:2439): the nine frames before the sequence's end.
+__device__ __forceinline__ void engram_hist_move(const EngramArgs& e, int t)
+{
+    if (!e.history || !e.run_end[t]) return;
+    const int len = t - e.run_start[t] + 1;  // the run's length
+    float* hist = e.history + (size_t)e.row_slot[t] * kEngramHistory * e.dim;
+    for (int c = threadIdx.x; c < e.dim; c += kThreads) {
+        float v[kEngramHistory];
+#pragma unroll
+        for (int j = 0; j < kEngramHistory; j++) {
+            const int idx = len + j;  // sequence index of the new frame j
+            v[j] = idx < kEngramHistory
+                       ? hist[(size_t)idx * e.dim + c]
+                       : e.stage[((size_t)(e.run_start[t] + idx - kEngramHistory) * (kEngramHistory + 1) +
+                                  kEngramHistory) * e.dim + c];
+        }
+#pragma unroll
+        for (int j = 0; j < kEngramHistory; j++) hist[(size_t)j * e.dim + c] = v[j];
+    }
+}
+
+// Scalar.GateFakeA8 on row t of the attention output: x *= Sigmoid(gate),
+// the fake int8 round trip at the row's peak, and the 2-bit Prepare of the
+// output matmul.  Row t's Q/K/V frames and, on engram layers, its engram
+// history move on here, after every row's attention and engram mix have read
+// the old ones.
 __global__ __launch_bounds__(kThreads) void n3_gate_kernel(const float* att, const float* gate, int n, Act act,
                                                            int stride, EngramArgs e, QkvHistArgs h)
 {
     __shared__ __align__(16) float x[kMaxDim];
     __shared__ float red[kWaves];
     const int t = blockIdx.x;
-    // the run's last row moves its slot's Q/K/V frames on: frame 0 takes the
-    // row before it (the old frame 1 for a one-row run), frame 1 the row
-    // itself (Scalar.Taps3's history, TapsAndAttentionHeadsSingle); the loads
-    // go out with the row's own
-    const bool hist_end = h.run_end[t] != 0;
-    const int all = h.qw + h.kw + h.vw;
-    float* hist = h.history + (size_t)h.row_slot[t] * 2 * all;
+    // the history's loads go out with the row's own
     float hv0[kHistPer], hv1[kHistPer];
-    if (hist_end) {
-        const bool run1 = t > h.run_start[t];
-#pragma unroll
-        for (int q = 0; q < kHistPer; q++) {
-            const int c = col_of(q);
-            if (c < all) {
-                const int base = c < h.qw ? 0 : (c < h.qw + h.kw ? h.qw : h.qw + h.kw);
-                const int width = c < h.qw ? h.qw : (c < h.qw + h.kw ? h.kw : h.vw);
-                hv0[q] = run1 ? h.raw[(size_t)(t - 1) * all + c] : hist[2 * base + (c - base) + width];
-                hv1[q] = h.raw[(size_t)t * all + c];
-            }
-        }
-    }
+    const bool hist_end = qkv_hist_load(h, t, hv0, hv1);
     float av[kPer], gv[kPer];
 #pragma unroll
     for (int q = 0; q < kPer; q++) {
@@ -597,33 +768,192 @@ __global__ __launch_bounds__(kThreads) void n3_gate_kernel(const float* att, con
     __syncthreads();
     fake_row(x, n, red);
     prepare_row(x, n, 2, act, stride, t);
-    if (hist_end) {
+    if (hist_end) qkv_hist_store(h, t, hv0, hv1);
+    engram_hist_move(e, t);
+}
+
+// n3_gate_kernel and the output matmul in one launch, for steps of up to
+// kGateOutRows rows: workgroup b computes output columns 16b .. 16b + 15 of
+// every row.  Each workgroup forms the prepared activations itself
+// (GateFakeA8 and the 2-bit Prepare, its waves taking the (row, group)
+// pairs); wave g then takes group g of the workgroup's 16 weight rows
+// (row-major 2-bit codes: element 4j + p in byte j, bits 2p) through four
+// i8 MFMAs, one per plane, as the codebook decode kernels do, and the group
+// dots D_g go into Scalar.MatMulRows' chain (Scalar.cs:146-192):
+//   scaled = (HalfToSingle(norm[n][g]) * ByteScale) * scale[t][g]
+//   acc += scaled * D_g;  bias += scaled * offset[t][g]   (g ascending)
+//   y = acc - bias
+// The Q/K/V and engram history moves of n3_gate_kernel are spread over the
+// workgroups, an element each for the last waves' threads.
+constexpr int kGateOutRows = 4;
+constexpr int kMaxGroups = kMaxDim / 128;
+typedef int v4i __attribute__((ext_vector_type(4)));
+
+struct GateOutArgs {
+    const uint16_t* norms;  // [columns][k / 128] fp16: the record's scales
+    float* y;               // [rows][ldy]
+    int ldy;
+    uint32_t table;         // the 2-bit codebook's four level bytes
+    float byte_scale;
+    EngramArgs e;
+    QkvHistArgs h;
+};
+
+__global__ __launch_bounds__(kThreads) void n3_gate_out_kernel(const uint8_t* codes, const float* att,
+                                                               const float* gate, uint64_t h_rows_k, GateOutArgs a)
+{
+    __shared__ __align__(16) int8_t act[kGateOutRows * kMaxDim];  // [t][k], planes order within each group
+    __shared__ float peak_g[kGateOutRows * kMaxGroups];
+    __shared__ float g_scale[kGateOutRows * kMaxGroups], g_offset[kGateOutRows * kMaxGroups];
+    __shared__ __align__(16) float pa[kGateOutRows * 16 * kMaxGroups], pb[kGateOutRows * 16 * kMaxGroups];
+    const int rows = (int)(uint32_t)h_rows_k, k = (int)(h_rows_k >> 32);
+    const int groups = k >> 7;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
+    // wave g < groups: lane l's MFMA B operand, bytes 8 * (l / 16) .. + 7 of
+    // group g of weight row l % 16, and that row's group scale (lanes < 16)
+    const int nr = lane & 15, kq = lane >> 4;
+    const bool dots = wave < groups;
+    uint2 code = make_uint2(0u, 0u);
+    uint32_t norm = 0u;
+    if (dots) {
+        const size_t row = (size_t)blockIdx.x * 16 + nr;
+        code = *reinterpret_cast<const uint2*>(codes + row * (k >> 2) + wave * 32 + kq * 8);
+        if (lane < 16) norm = a.norms[row * groups + wave];
+    }
+    // the gate's (row, group) pairs: wave v takes v and v + kWaves; lane e
+    // holds elements e and e + 64 of the group, as hadamard_wave wants them
+    const int tasks = rows * groups;
+    float x0[2], x1[2], s0[2], s1[2];
 #pragma unroll
-        for (int q = 0; q < kHistPer; q++) {
-            const int c = col_of(q);
-            if (c < all) {
-                const int base = c < h.qw ? 0 : (c < h.qw + h.kw ? h.qw : h.qw + h.kw);
-                const int width = c < h.qw ? h.qw : (c < h.qw + h.kw ? h.kw : h.vw);
-                hist[2 * base + (c - base)] = hv0[q];
-                hist[2 * base + (c - base) + width] = hv1[q];
+    for (int u = 0; u < 2; u++) {
+        const int task = wave + kWaves * u;
+        if (task < tasks) {
+            const int t = task / groups, gg = task - t * groups;
+            const size_t at = (size_t)t * k + gg * 128 + lane;
+            x0[u] = att[at];
+            x1[u] = att[at + 64];
+            s0[u] = gate[at];
+            s1[u] = gate[at + 64];
+        }
+    }
+    // the history moves: row t's element c for flat index t * width + c, a
+    // run of `per` indices for each workgroup, from its last thread down
+    const int hi = kThreads - 1 - (int)threadIdx.x;
+    const int all = a.h.qw + a.h.kw + a.h.vw;
+    const int qkv_per = (rows * all + (int)gridDim.x - 1) / (int)gridDim.x;
+    const int qkv_e = (int)blockIdx.x * qkv_per + hi;
+    const bool qkv_on = hi < qkv_per && qkv_e < rows * all;
+    float hv0 = 0.0f, hv1 = 0.0f;
+    float* qkv_dst = nullptr;
+    int qkv_width = 0;
+    if (qkv_on) {
+        const int t = qkv_e / all, c = qkv_e - t * all;
+        if (a.h.run_end[t] != 0) {
+            const int base = c < a.h.qw ? 0 : (c < a.h.qw + a.h.kw ? a.h.qw : a.h.qw + a.h.kw);
+            qkv_width = c < a.h.qw ? a.h.qw : (c < a.h.qw + a.h.kw ? a.h.kw : a.h.vw);
+            qkv_dst = a.h.history + (size_t)a.h.row_slot[t] * 2 * all + 2 * base + (c - base);
+            hv0 = t > a.h.run_start[t] ? a.h.raw[(size_t)(t - 1) * all + c] : qkv_dst[qkv_width];
+            hv1 = a.h.raw[(size_t)t * all + c];
+        }
+    }
+#pragma unroll
+    for (int u = 0; u < 2; u++) {
+        const int task = wave + kWaves * u;
+        if (task < tasks) {
+            x0[u] = x0[u] * sigmoid_poly(s0[u]);
+            x1[u] = x1[u] * sigmoid_poly(s1[u]);
+            const float m = wave_max(fmaxf(fabsf(x0[u]), fabsf(x1[u])));
+            if (lane == 0) peak_g[task] = m;
+        }
+    }
+    __syncthreads();
+    // Quant.FakeA8 at the row's peak, then the Hadamard and Prepare of the group
+#pragma unroll
+    for (int u = 0; u < 2; u++) {
+        const int task = wave + kWaves * u;
+        if (task < tasks) {
+            const int t = task / groups, gg = task - t * groups;
+            float peak = 0.0f;
+            for (int j = 0; j < groups; j++) peak = fmaxf(peak, peak_g[t * groups + j]);
+            const float scale = peak > 0.0f ? peak / 127.0f : 1.0f;
+            const float round = 1.0f / scale;
+            float v0 = clamp_q(x0[u] * round) * scale;
+            float v1 = clamp_q(x1[u] * round) * scale;
+            hadamard_wave(v0, v1);
+            prepare_group_wave(v0, v1, 2, act + t * k + gg * 128, &g_scale[task], &g_offset[task]);
+        }
+    }
+    __syncthreads();
+    if (dots) {
+        // D_g for tokens 0..3 (MFMA rows; rows of tokens >= rows read nothing)
+        v4i d = {0, 0, 0, 0};
+#pragma unroll
+        for (int pl = 0; pl < 4; pl++) {
+            long av = 0;
+            if (nr < rows) av = *reinterpret_cast<const long*>(act + nr * k + wave * 128 + 32 * pl + 8 * kq);
+            const uint32_t b0 = lut2((code.x >> (2 * pl)) & 0x03030303u, a.table);
+            const uint32_t b1 = lut2((code.y >> (2 * pl)) & 0x03030303u, a.table);
+            d = __builtin_amdgcn_mfma_i32_16x16x32_i8(av, (long)(((uint64_t)b1 << 32) | b0), d, 0, 0, 0);
+        }
+        // lane l < 16 holds D[t][row l] in d[t]
+        if (lane < 16) {
+            const float hb = ref_half_to_single(norm) * a.byte_scale;
+            const int dv[4] = {d.x, d.y, d.z, d.w};
+#pragma unroll
+            for (int t = 0; t < kGateOutRows; t++) {
+                if (t < rows) {
+                    const float scaled = hb * g_scale[t * groups + wave];
+                    pa[(t * 16 + nr) * kMaxGroups + wave] = scaled * static_cast<float>(dv[t]);
+                    pb[(t * 16 + nr) * kMaxGroups + wave] = scaled * g_offset[t * groups + wave];
+                }
             }
         }
     }
-    if (e.history && e.run_end[t]) {
-        const int len = t - e.run_start[t] + 1;  // the run's length
-        float* hist = e.history + (size_t)e.row_slot[t] * kEngramHistory * e.dim;
-        for (int c = threadIdx.x; c < e.dim; c += kThreads) {
-            float v[kEngramHistory];
+    __syncthreads();
+    if ((int)threadIdx.x < rows * 16) {
+        const int i = threadIdx.x;
+        const float4* ra = reinterpret_cast<const float4*>(pa + i * kMaxGroups);
+        const float4* rb = reinterpret_cast<const float4*>(pb + i * kMaxGroups);
+        const float4 a0 = ra[0], a1 = ra[1], b0 = rb[0], b1 = rb[1];
+        const float av[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+        const float bv[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
+        float acc = 0.0f, bias = 0.0f;
 #pragma unroll
-            for (int j = 0; j < kEngramHistory; j++) {
-                const int idx = len + j;  // sequence index of the new frame j
-                v[j] = idx < kEngramHistory
-                           ? hist[(size_t)idx * e.dim + c]
-                           : e.stage[((size_t)(e.run_start[t] + idx - kEngramHistory) * (kEngramHistory + 1) +
-                                      kEngramHistory) * e.dim + c];
+        for (int gg = 0; gg < kMaxGroups; gg++) {
+            if (gg < groups) {
+                acc = acc + av[gg];
+                bias = bias + bv[gg];
             }
+        }
+        a.y[(size_t)(i >> 4) * a.ldy + blockIdx.x * 16 + (i & 15)] = acc - bias;
+    }
+    if (qkv_dst) {
+        qkv_dst[0] = hv0;
+        qkv_dst[qkv_width] = hv1;
+    }
+    // engram: row t's column c, its nine frames
+    const EngramArgs& e = a.e;
+    if (e.history) {
+        const int per = (rows * e.dim + (int)gridDim.x - 1) / (int)gridDim.x;
+        const int f = (int)blockIdx.x * per + hi;
+        if (hi < per && f < rows * e.dim) {
+            const int t = f / e.dim, c = f - t * e.dim;
+            if (e.run_end[t]) {
+                const int len = t - e.run_start[t] + 1;  // the run's length
+                float* hist = e.history + (size_t)e.row_slot[t] * kEngramHistory * e.dim;
+                float v[kEngramHistory];
 #pragma unroll
-            for (int j = 0; j < kEngramHistory; j++) hist[(size_t)j * e.dim + c] = v[j];
+                for (int j = 0; j < kEngramHistory; j++) {
+                    const int idx = len + j;  // sequence index of the new frame j
+                    v[j] = idx < kEngramHistory
+                               ? hist[(size_t)idx * e.dim + c]
+                               : e.stage[((size_t)(e.run_start[t] + idx - kEngramHistory) * (kEngramHistory + 1) +
+                                          kEngramHistory) * e.dim + c];
+                }
+#pragma unroll
+                for (int j = 0; j < kEngramHistory; j++) hist[(size_t)j * e.dim + c] = v[j];
+            }
         }
     }
 }
@@ -810,9 +1140,25 @@ __device__ __forceinline__ void kron_rows(const float* z, int active, const floa
 // The first loads' pointers also travel as leading arguments, which gfx950
 // preloads into SGPRs (kernarg preload; a struct argument is never
 // preloaded), so those loads issue without an argument-segment round trip.
+// LDS the fused tail's next-layer mix adds to tail_lds_bytes: the 4-bit
+// prepared stream row (values, scales, offsets), the phi products of 24
+// outputs and the mix kernel's two dim rows.
+size_t tail_hyper_lds_bytes(int dim)
+{
+    const size_t n4 = (size_t)kLanes * dim, groups = n4 / 128;
+    return 16 + n4 + sizeof(float) * (2 * groups + 2 * 24 * groups + 2 * (size_t)dim);
+}
+
+// HYPER: for a layer l < L - 1 of a step whose rows are one per slot, the
+// workgroup goes on into layer l + 1's mix (h, as n3_hyper_kernel's row
+// part with all 24 phi outputs, the 16 residual-mix logits stored for the
+// attention launch's Sinkhorn): the next stream row stays in registers and
+// its 4-bit prepared activations in LDS.
+template <bool HYPER>
 __global__ __launch_bounds__(kThreads) void n3_tail_kernel(const float* h_proj, float* h_residual,
                                                            const float* h_post_norm, const float* h_pre_norm,
-                                                           const float* h_mix, const float* h_post_gate, TailArgs a)
+                                                           const float* h_mix, const float* h_post_gate, TailArgs a,
+                                                           HyperArgs h)
 {
     a.proj = h_proj;
     a.residual = h_residual;
@@ -835,12 +1181,20 @@ __global__ __launch_bounds__(kThreads) void n3_tail_kernel(const float* h_proj, 
     float* wr = wl + 3 * a.rows * lt; // W1B, W2B, W3B
     float* ns = wr + 3 * cc;          // the next stream row, 4 * dim
     float* nst = ns + n4;             // its lane-major copy [32][ts]
+    const int g4 = n4 / 128;
+    // HYPER: the 4-bit prepared next stream row, 16-byte aligned
+    int8_t* a4v = reinterpret_cast<int8_t*>(lds + ((int)(nst + 32 * ts - lds) + 3) / 4 * 4);
+    float* a4s = reinterpret_cast<float*>(a4v + n4);          // its group scales, then offsets
+    float* hprod = a4s + 2 * g4;                              // phi products [24][g4][2]
+    float* hx = hprod + 2 * 24 * g4;                          // the mix kernel's rows
+    float* hsq = hx + dim;
     __shared__ float weights[8];
     __shared__ float red[kWaves];
     __shared__ float inv_s;
     const int t = blockIdx.x;
     // every global load of the row up front
     float rv[kPer], pv[kPer], psv[kPer], prv[kPer], d1v[kPer], d4v[kPer], uv[kPer], sv[kPer][kLanes];
+    float hsn[kPer], nsv[kPer][kLanes];  // HYPER: layer l + 1's NormIn, the next stream row
 #pragma unroll
     for (int q = 0; q < kPer; q++) {
         const int c = col_of(q);
@@ -854,6 +1208,7 @@ __global__ __launch_bounds__(kThreads) void n3_tail_kernel(const float* h_proj, 
             uv[q] = a.input[(size_t)t * dim + c];
 #pragma unroll
             for (int l = 0; l < kLanes; l++) sv[q][l] = a.stream[(size_t)t * n4 + l * dim + c];
+            if constexpr (HYPER) hsn[q] = h.norm_in[c];
         }
     }
     float cu[kPer][8], d2v[kPer], b2v[kPer], d3v[kPer];
@@ -1004,12 +1359,22 @@ __global__ __launch_bounds__(kThreads) void n3_tail_kernel(const float* h_proj, 
                                 mix[4 * l + 2] * sv[q][2] + mix[4 * l + 3] * sv[q][3];
                 const int i = l * dim + c;
                 a.next[(size_t)t * n4 + i] = o;
+                if constexpr (HYPER) nsv[q][l] = o;
                 ns[i] = o;
                 nst[(i & 31) * ts + (i >> 5)] = o;
             }
         }
     }
     __syncthreads();
+    // HYPER: layer l + 1's phi rows, 4 pre, 4 post, 16 residual-mix; their
+    // codes and affine maps load under the next layer's RmsFakeA8 and Prepare
+    constexpr int kPhiFirst[4] = {0, 4, 8, 24};
+    PhiUnit hunit{};
+    float hga = 0.0f, hgb = 0.0f;
+    if constexpr (HYPER) {
+        hunit = phi_load(h.phi, n4, 0, kPhiFirst);
+        phi_affine(h, hga, hgb);
+    }
     if (!a.head_of) {  // the next layer's RmsFakeA8 and 4-bit Prepare
         // RmsUnit then FakeA8 with one barrier: the peak of x * inverse is
         // RoundNearest(max |x| * inverse) (inverse > 0 and rounding is
@@ -1023,7 +1388,10 @@ __global__ __launch_bounds__(kThreads) void n3_tail_kernel(const float* h_proj, 
             const float sum = wave_v256_squares(nst, n4);
             if (threadIdx.x == 0) inv_s = inverse_rms_of(sum, n4);
         }
-        __syncthreads();
+        if constexpr (HYPER)  // the phi codes stay in flight
+            lds_barrier();
+        else
+            __syncthreads();
         inverse = inv_s;
         float m = red[0];
         for (int w = 1; w < kWaves; w++) m = fmaxf(m, red[w]);
@@ -1031,8 +1399,20 @@ __global__ __launch_bounds__(kThreads) void n3_tail_kernel(const float* h_proj, 
         const float scale = peak > 0.0f ? peak / 127.0f : 1.0f;
         const float round = 1.0f / scale;
         for (int c = threadIdx.x; c < n4; c += kThreads) ns[c] = clamp_q((ns[c] * inverse) * round) * scale;
-        __syncthreads();
-        prepare_row(ns, n4, 4, a.act, a.stride, t);
+        if constexpr (HYPER)
+            lds_barrier();
+        else
+            __syncthreads();
+        if constexpr (HYPER) {
+            prepare_row(ns, n4, 4, Act{a4v, a4s, a4s + g4}, 0, 0);
+            lds_barrier();
+            const float y = phi_outputs(h.phi, hunit, a4v, a4s, a4s + g4, n4, kPhiFirst, hprod);
+            if (threadIdx.x >= 8 && threadIdx.x < 24) h.mix_logits[t * 16 + threadIdx.x - 8] = hga * y + hgb;
+            __shared__ float hpre[4];
+            hyper_mix_row(h, t, y, hga, hgb, nsv, hsn, hx, hsq, hpre, red, &inv_s);
+        } else {
+            prepare_row(ns, n4, 4, a.act, a.stride, t);
+        }
         return;
     }
     const int head = a.head_of[t];
@@ -1072,6 +1452,7 @@ struct N3Layer {
                 *k_norm = nullptr, *post_norm = nullptr, *pre_hada = nullptr;
     nhip_weights *q = nullptr, *k = nullptr, *v = nullptr, *gate = nullptr, *out = nullptr;
     nhip_weights* qkvg = nullptr;  // Q, K, V and Gate stacked by rows (the context's own)
+    const uint8_t* out_raw = nullptr;  // Out's archive bytes on the device: row-major codes, then the norms
     float attn_gate = 0.0f;
     const float *d1 = nullptr, *d2 = nullptr, *b2 = nullptr, *d3 = nullptr, *d4 = nullptr, *w1a = nullptr,
                 *w1b = nullptr, *w2a = nullptr, *w2b = nullptr, *w3a = nullptr, *w3b = nullptr, *cond_v = nullptr,
@@ -1131,6 +1512,7 @@ struct nhip_ctx {
     int32_t *d_topk_idx = nullptr, *d_argmax = nullptr;
     float* d_topk_lp = nullptr;
     size_t tail_lds = 0;
+    size_t tail_hyper_lds = 0;  // 0: the fused tail + next-layer mix does not fit
     hipStream_t stream_h = nullptr;
     struct Graph {
         int rows, heads, k;
@@ -1376,6 +1758,7 @@ int32_t load_model(nhip_ctx* c)
         qkvg_records[3] = r.last;
         if (!r.status && (rc = stack_rows(c, qkvg_records, 4, &w.qkvg))) return rc;
         w.out = r.quant(2, d, ow, "Out");
+        w.out_raw = r.status ? nullptr : nhip_model_raw(c->model, r.last);
         w.post_norm = r.dense(d, "PostNorm");
         const float* g = r.dense(1, "AttnGate");
         if (g) {  // LayerWeights: AttnGate = 1 / (1 + MathF.Exp(-x)), once, with the host libm
@@ -1520,8 +1903,16 @@ int32_t alloc_state(nhip_ctx* c)
     c->tail_lds = tail_lds_bytes(d, c->hada_rows, c->hada_cols);
     NHIP_REQUIRE(c->tail_lds <= 160 * 1024, "the layer tail's %zu bytes of LDS exceed the CU's", c->tail_lds);
     if (c->tail_lds > 64 * 1024)
-        NHIP_CHECK_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(n3_tail_kernel),
+        NHIP_CHECK_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(n3_tail_kernel<false>),
                                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)c->tail_lds));
+    // the fused tail + next-layer mix, where its LDS fits the CU
+    c->tail_hyper_lds = c->tail_lds + tail_hyper_lds_bytes(d);
+    if (c->tail_hyper_lds > 160 * 1024) {
+        c->tail_hyper_lds = 0;
+    } else if (c->tail_hyper_lds > 64 * 1024) {
+        NHIP_CHECK_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(n3_tail_kernel<true>),
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)c->tail_hyper_lds));
+    }
     return NHIP_OK;
 }
 
@@ -1589,13 +1980,15 @@ int32_t enqueue_step(nhip_ctx* c, int rows, int heads, int k, bool argmax, bool 
     // (attention_decode_needle3_impl), which then also forms Sinkhorn4x4 of
     // the mix kernel's residual-mix logits
     const bool sink_in_attention = single_runs && attention_needle3_fused(c->capacity, c->vd);
-    hipLaunchKernelGGL(n3_embed_kernel, dim3(rows), dim3(kThreads), 0, s, c->embedding_raw, c->vocab, d,
-                       c->embedding_bits, c->book4, in(c, c->d_in, kInTokens), emb_scale_m1, cur, act4, stride4);
-    NHIP_CHECK_HIP(hipGetLastError());
-    for (int l = 0; l < L; l++) {
-        const N3Layer& w = c->layer[l];
-        // hyper-connection phi (RunLayerBatch, Engine.cs:2356-2364): the
-        // layer's 4 + 4 + 16 rows, formed by the mix kernel itself
+    auto site_of = [&](int l) -> const N3Site* {
+        for (int k2 = 0; k2 < c->site_count; k2++)
+            if (c->sites[k2] == l) return &c->site[k2];
+        return nullptr;
+    };
+    // layer l's mix kernel arguments, with the hyper-connection phi
+    // (RunLayerBatch, Engine.cs:2356-2364): the layer's 4 + 4 + 16 rows,
+    // formed by the mix kernel itself
+    auto hyper_args = [&](int l, const float* stream) {
         PhiRows phi{};
         const int per[3] = {4, 4, 16}, totals[3] = {4 * L, 4 * L, 16 * L};
         for (int m = 0; m < 3; m++) {
@@ -1607,17 +2000,33 @@ int32_t enqueue_step(nhip_ctx* c, int rows, int heads, int k, bool argmax, bool 
         phi.byte_scale = c->phi_pre->byte_scale;
         phi.in = act4;
         phi.stride = stride4;
-        int site = -1;
-        for (int k2 = 0; k2 < c->site_count; k2++)
-            if (c->sites[k2] == l) site = k2;
-        const N3Site* st = site >= 0 ? &c->site[site] : nullptr;
-        HyperArgs ha{cur, phi, c->a_pre + l, c->a_post + l, c->a_res + l, c->b_pre + 4 * l, c->b_post + 4 * l,
-                     c->b_res + 16 * l, l % kLanes, d, c->input, c->residual, c->post_gate, c->mix, w.norm_in,
-                     st ? st->tables : nullptr, st ? st->table_rows : 0, st ? st->table_cols : 0,
-                     st ? st->table_bits : 0, c->engram_tables, st && st->table_bits == 2 ? c->book2 : c->book4,
-                     in_erows(c, c->d_in), act, stride_d, rows, sink_in_attention ? c->mix_logits : nullptr};
-        hipLaunchKernelGGL(n3_hyper_kernel, dim3(2 * rows), dim3(kThreads), 0, s, ha);
-        NHIP_CHECK_HIP(hipGetLastError());
+        const N3Site* st = site_of(l);
+        return HyperArgs{stream, phi, c->a_pre + l, c->a_post + l, c->a_res + l, c->b_pre + 4 * l,
+                         c->b_post + 4 * l, c->b_res + 16 * l, l % kLanes, d, c->input, c->residual, c->post_gate,
+                         c->mix, c->layer[l].norm_in, st ? st->tables : nullptr, st ? st->table_rows : 0,
+                         st ? st->table_cols : 0, st ? st->table_bits : 0, c->engram_tables,
+                         st && st->table_bits == 2 ? c->book2 : c->book4, in_erows(c, c->d_in), act, stride_d, rows,
+                         sink_in_attention ? c->mix_logits : nullptr};
+    };
+    // for those steps each layer's tail launch also runs the next layer's
+    // mix (n3_tail_kernel<true>); NHIP_N3_TAIL_MIX=0 keeps the mix launches
+    // (for A/B timing)
+    static const bool tail_mix_enabled = [] {
+        const char* e = getenv("NHIP_N3_TAIL_MIX");
+        return !(e && e[0] == '0');
+    }();
+    const bool fuse_tail = tail_mix_enabled && sink_in_attention && c->tail_hyper_lds > 0;
+    hipLaunchKernelGGL(n3_embed_kernel, dim3(rows), dim3(kThreads), 0, s, c->embedding_raw, c->vocab, d,
+                       c->embedding_bits, c->book4, in(c, c->d_in, kInTokens), emb_scale_m1, cur, act4, stride4);
+    NHIP_CHECK_HIP(hipGetLastError());
+    for (int l = 0; l < L; l++) {
+        const N3Layer& w = c->layer[l];
+        const N3Site* st = site_of(l);
+        if (!fuse_tail || l == 0) {  // otherwise layer l - 1's tail launch ran the mix
+            const HyperArgs ha = hyper_args(l, cur);
+            hipLaunchKernelGGL(n3_hyper_kernel, dim3(2 * rows), dim3(kThreads), 0, s, ha);
+            NHIP_CHECK_HIP(hipGetLastError());
+        }
         EngramArgs ea{};
         if (st) {  // engram (ApplyEngramBatch, Engine.cs:2399-2463)
             const nhip_weights* jw[2] = {st->key, st->value};
@@ -1629,7 +2038,7 @@ int32_t enqueue_step(nhip_ctx* c, int rows, int heads, int k, bool argmax, bool 
             if (rc && (rc = nhip_matmul_batch_dev(jw, 2, c->act_v, c->act_s, c->act_o, stride_d, rows, jy, jl, s)))
                 return rc;
             ea = EngramArgs{c->stage,
-                            c->engram_hist + (size_t)site * c->slots * kEngramHistory * d,
+                            c->engram_hist + (size_t)(st - c->site.data()) * c->slots * kEngramHistory * d,
                             in(c, c->d_in, kInSlots),
                             in(c, c->d_in, kInRunStart),
                             in(c, c->d_in, kInRunEnd),
@@ -1701,17 +2110,38 @@ int32_t enqueue_step(nhip_ctx* c, int rows, int heads, int k, bool argmax, bool 
         // inputs have read them
         const QkvHistArgs qh{qkv_hist, c->raw, in(c, c->d_in, kInSlots), in(c, c->d_in, kInRunStart),
                              in(c, c->d_in, kInRunEnd), qw, kw, vw};
-        hipLaunchKernelGGL(n3_gate_kernel, dim3(rows), dim3(kThreads), 0, s, c->att, c->gate, ow, act, stride_o, ea, qh);
-        NHIP_CHECK_HIP(hipGetLastError());
-        if ((rc = matmul(c, w.out, rows, ow, 0, d, c->proj, d))) return rc;
+        // NHIP_N3_GATE_OUT=0 keeps the two launches for every step (for A/B timing)
+        static const bool gate_out_enabled = [] {
+            const char* e = getenv("NHIP_N3_GATE_OUT");
+            return !(e && e[0] == '0');
+        }();
+        // d and ow are multiples of 128 up to 1024 (load_model), so the d / 16
+        // workgroups cover the columns; each takes at most kThreads of the
+        // rows' Q/K/V history elements
+        if (gate_out_enabled && rows <= kGateOutRows && w.out_raw && rows * (qw + kw + vw) <= kThreads * (d / 16)) {
+            const GateOutArgs ga{reinterpret_cast<const uint16_t*>(w.out_raw + (size_t)d * (ow / 4)), c->proj, d,
+                                 w.out->table[0], w.out->byte_scale, ea, qh};
+            hipLaunchKernelGGL(n3_gate_out_kernel, dim3(d / 16), dim3(kThreads), 0, s, w.out_raw, c->att, c->gate,
+                               (uint64_t)(uint32_t)rows | ((uint64_t)(uint32_t)ow << 32), ga);
+            NHIP_CHECK_HIP(hipGetLastError());
+        } else {
+            hipLaunchKernelGGL(n3_gate_kernel, dim3(rows), dim3(kThreads), 0, s, c->att, c->gate, ow, act, stride_o, ea,
+                               qh);
+            NHIP_CHECK_HIP(hipGetLastError());
+            if ((rc = matmul(c, w.out, rows, ow, 0, d, c->proj, d))) return rc;
+        }
         const bool last = l == L - 1;
         TailArgs ta{c->residual, c->proj, w.post_norm, w.attn_gate, w.pre_hada, c->perm_a, c->perm_b, w.d1, w.d2,
                     w.b2, w.d3, w.d4, w.w1a, w.w1b, w.w2a, w.w2b, w.w3a, w.w3b, w.cond_v, w.cond_u, d, c->hada_rows,
                     c->hada_cols, cur, c->mix, c->input, c->post_gate, nxt,
                     last ? in(c, c->d_in, kInHeadOf) : nullptr, c->final_norm, last ? act : act4,
                     last ? stride_d : stride4};
-        hipLaunchKernelGGL(n3_tail_kernel, dim3(rows), dim3(kThreads), c->tail_lds, s, ta.proj, ta.residual,
-                           ta.post_norm, ta.pre_norm, ta.mix, ta.post_gate, ta);
+        if (fuse_tail && !last)
+            hipLaunchKernelGGL(n3_tail_kernel<true>, dim3(rows), dim3(kThreads), c->tail_hyper_lds, s, ta.proj,
+                               ta.residual, ta.post_norm, ta.pre_norm, ta.mix, ta.post_gate, ta, hyper_args(l + 1, nxt));
+        else
+            hipLaunchKernelGGL(n3_tail_kernel<false>, dim3(rows), dim3(kThreads), c->tail_lds, s, ta.proj,
+                               ta.residual, ta.post_norm, ta.pre_norm, ta.mix, ta.post_gate, ta, HyperArgs{});
         NHIP_CHECK_HIP(hipGetLastError());
         std::swap(cur, nxt);
     }
