@@ -643,9 +643,31 @@ __global__ __launch_bounds__(row_threads(MODE)) void decode_attention_row_kernel
         ATTN_TAKE_HEAD(p, q, qscale);
     if constexpr (N3) {
         // the extra column of workgroups (launched with n3.mix): the row's
-        // Sinkhorn4x4, by wave 0, beside the attention
+        // residual-mix logits (RunLayerBatch, Engine.cs:2364-2378: the phi
+        // outputs' Scalar.MatMulRows chains, then a_res * y + b_res[o]) and
+        // their Sinkhorn4x4 by wave 0, beside the attention
         if ((int)blockIdx.y == p.heads) {
-            if (threadIdx.x < 64) sinkhorn4x4_wave(p.n3.mix_logits + blockIdx.x * 16, p.n3.mix + blockIdx.x * 16);
+            __shared__ __align__(16) float phi_prod[2 * 16 * kPhiMaxGroups];
+            __shared__ __align__(16) int8_t phi_x[128 * kPhiMaxGroups];  // the prepared stream row
+            __shared__ float phi_so[2 * kPhiMaxGroups];                   // its group scales, offsets
+            __shared__ float logits[16];
+            const PhiRows& ph = p.n3.res_phi;
+            const int t = blockIdx.x, K = p.n3.res_k, groups = K / 128;
+            const int first[4] = {0, 16, 16, 16};
+            const PhiUnit unit = phi_load(ph, K, 2, first);
+            const float ga = p.n3.a_res[0], gb = p.n3.b_res[threadIdx.x & 15];
+            // the row once into LDS (each unit reads a group of it)
+            for (int e = threadIdx.x; e < K / 16; e += blockDim.x)
+                reinterpret_cast<uint4*>(phi_x)[e] = reinterpret_cast<const uint4*>(ph.in.values + (size_t)t * K)[e];
+            if ((int)threadIdx.x < 2 * groups) {
+                const float* src = (int)threadIdx.x < groups ? ph.in.scales : ph.in.offsets;
+                phi_so[threadIdx.x] = src[(size_t)t * ph.stride + (int)threadIdx.x % groups];
+            }
+            lds_barrier();
+            const float y = phi_outputs(ph, unit, phi_x, phi_so, phi_so + groups, K, first, phi_prod);
+            if (threadIdx.x < 16) logits[threadIdx.x] = ga * y + gb;
+            lds_barrier();
+            if (threadIdx.x < 64) sinkhorn4x4_wave(logits, p.n3.mix + t * 16);
             return;
         }
     }
@@ -1220,7 +1242,9 @@ int32_t attention_decode_needle3_impl(const Needle3AttnInputs& in, int32_t rows,
     p.capacity = capacity;
     p.max_chunks = max_chunks;
     p.inv_sqrt = static_cast<float>(1.0 / std::sqrt(static_cast<double>(qk_dim)));
-    NHIP_REQUIRE(!in.mix == !in.mix_logits, "attention: Sinkhorn logits and output go together");
+    NHIP_REQUIRE(!in.mix || (in.res_phi.codes[2] && in.res_phi.norms[2] && in.a_res && in.b_res && in.res_k > 0 &&
+                             in.res_k % 128 == 0 && in.res_k / 128 <= kPhiMaxGroups),
+                 "attention: the Sinkhorn workgroups need the residual-mix phi rows (K %d)", in.res_k);
     hipLaunchKernelGGL(decode_attention_row_kernel<kRowNeedle3>, dim3(rows, heads + (in.mix ? 1 : 0)),
                        dim3(row_threads(kRowNeedle3)), 0, stream, ATTN_HEAD_ARGS(p, p.n3.raw, p.positions), p);
     NHIP_CHECK_HIP(hipGetLastError());

@@ -191,6 +191,37 @@ int32_t attention_decode_post_impl(const AttnPostInputs& in, int32_t rows, int32
 // query head writes that key and value to the cache.  The slots' frames are
 // left for the caller to move on.  Returns 1 without launching when it does
 // not apply (caches over 512 positions, value heads other than 64).
+// Prepared activations (Quant.Activations): row t's values at values + t * cols,
+// its group scales and offsets at scales / offsets + t * stride.
+struct Act {
+    int8_t* values;
+    float* scales;
+    float* offsets;
+};
+
+// The layer's hyper-connection phi rows (RunLayerBatch, Engine.cs:2356-2364):
+// 4 pre, 4 post and 16 residual-mix outputs of three Cq4 matrices over the
+// stream's 4-bit prepared activations.  codes[m] points at the layer's first
+// row of matrix m ([rows][K / 2] codes, the archive's row-major bytes),
+// norms[m] at its fp16 group norms ([rows][K / 128]).
+constexpr int kPhiMaxGroups = 32;  // phi rows of K up to 4096
+struct PhiRows {
+    const uint8_t* codes[3];
+    const uint16_t* norms[3];
+    uint32_t split[4];  // the 4-bit codebook's split lookup tables (lut4x)
+    float byte_scale;   // its ByteScale
+    Act in;             // the stream's Quant.Prepare rows, K = kLanes * dim
+    int stride;
+};
+
+// Thread u's (output, group) unit of `outputs` phi rows (u < outputs * K /
+// 128, at most one unit a thread): its 64 code bytes and fp16 norm, loaded
+// ahead of the activations they meet (phi_load).
+struct PhiUnit {
+    uint4 w[4];
+    uint32_t norm;
+};
+
 struct Needle3AttnInputs {
     const float* raw;       // [rows][qw + kw + vw]
     const float* taps[3];   // query, key, value taps: [3][width] each
@@ -199,11 +230,15 @@ struct Needle3AttnInputs {
     const float* rope_cos;  // [capacity][qk / 2]
     const float* rope_sin;
     const float* history;   // [slots][2][qw], [2][kw], [2][vw]: frame 0, then frame 1
-    // when set, one more workgroup per row forms the row's Sinkhorn4x4 of
-    // its residual-mix logits [rows][16] into mix [rows][16] beside the
-    // attention (only the layer's tail reads it)
-    const float* mix_logits;
+    // when set, one more workgroup per row forms the row's 16 residual-mix
+    // logits, its phi outputs a_res * y + b_res[o] (res_phi's matrix 2 over
+    // the K = res_k prepared stream row), and their Sinkhorn4x4 into mix
+    // [rows][16] beside the attention (only the layer's tail reads it)
     float* mix;
+    PhiRows res_phi;
+    int res_k;
+    const float* a_res;  // [1]
+    const float* b_res;  // [16]
 };
 // Whether attention_decode_needle3_impl takes a step (caches of at most 512
 // positions, value heads of 64).
@@ -713,6 +748,143 @@ __device__ __forceinline__ void prepare_group_wave(float v0, float v1, int bits,
         *scale_out = scale;
         *offset_out = 63.0f * (float)sum;
     }
+}
+
+// A workgroup barrier that orders LDS only: the waves' outstanding global
+// loads and stores stay in flight across it (__syncthreads waits for them),
+// for code whose waves share data through LDS alone.
+__device__ __forceinline__ void lds_barrier()
+{
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+// Scalar.MatMulRows' exact int32 dot (Scalar.cs:166-184) of one Cq4 row's
+// group (64 code bytes) with a group of 4-bit prepared activations (128
+// int8 in Planes order): code byte j of half h carries activation
+// 2h * 32 + j in its low nibble and (2h + 1) * 32 + j in its high nibble.
+// The codes go through lut4x to their codebook bytes (below 128, so the
+// signed byte dot is exact).
+__device__ __forceinline__ int cq4_group_dot(const uint4 (&w4)[4], const int8_t* x, const uint32_t (&split)[4])
+{
+    const uint4* x4 = reinterpret_cast<const uint4*>(x);
+    int dot = 0;
+#pragma unroll
+    for (int h = 0; h < 2; h++) {
+        const uint4 wv[2] = {w4[2 * h], w4[2 * h + 1]};
+        const uint4 lo[2] = {x4[4 * h], x4[4 * h + 1]};
+        const uint4 hi[2] = {x4[4 * h + 2], x4[4 * h + 3]};
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            const uint4& w = wv[k >> 2];
+            const uint32_t word = (k & 3) == 0 ? w.x : (k & 3) == 1 ? w.y : (k & 3) == 2 ? w.z : w.w;
+            const uint4& l = lo[k >> 2];
+            const uint4& u = hi[k >> 2];
+            const uint32_t xl = (k & 3) == 0 ? l.x : (k & 3) == 1 ? l.y : (k & 3) == 2 ? l.z : l.w;
+            const uint32_t xh = (k & 3) == 0 ? u.x : (k & 3) == 1 ? u.y : (k & 3) == 2 ? u.z : u.w;
+            const uint32_t bl = lut4x(word & 0x0F0F0F0Fu, split[0], split[1], split[2], split[3]);
+            const uint32_t bh = lut4x((word >> 4) & 0x0F0F0F0Fu, split[0], split[1], split[2], split[3]);
+            dot = __builtin_amdgcn_sdot4((int)bl, (int)xl, dot, false);
+            dot = __builtin_amdgcn_sdot4((int)bh, (int)xh, dot, false);
+        }
+    }
+    return dot;
+}
+
+// A global-memory pointer argument held in scalar registers: selecting
+// between such values per lane stays a select, where selecting struct fields
+// per lane becomes a load of the chosen field through a vector address (and a
+// vmcnt(0) wait that also waits for every global load issued before it).
+template <typename T>
+using global_ptr = const __attribute__((address_space(1))) T*;
+template <typename T>
+__device__ __forceinline__ global_ptr<T> scalar_ptr(const T* p)
+{
+    const uint64_t v = reinterpret_cast<uint64_t>(p);
+    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
+    const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+    return (global_ptr<T>)(((uint64_t)hi << 32) | lo);
+}
+
+// first[m] is the first output of matrix m (outputs first[m] .. first[m + 1]
+// - 1 read its rows 0, 1, ...).
+__device__ __forceinline__ PhiUnit phi_load(const PhiRows& p, int K, int m0, const int (&first)[4])
+{
+    PhiUnit r{};
+    const int groups = K / 128, outputs = first[3] - first[0];
+    const int u = threadIdx.x;
+    if (u < outputs * groups) {
+        const int o = u / groups, g = u - o * groups;
+        const int m = m0 + (o >= first[1] - first[0]) + (o >= first[2] - first[0]);
+        const int row = o + first[0] - first[m - m0];
+        const global_ptr<uint8_t> c0 = scalar_ptr(p.codes[0]), c1 = scalar_ptr(p.codes[1]),
+                                  c2 = scalar_ptr(p.codes[2]);
+        const global_ptr<uint16_t> n0 = scalar_ptr(p.norms[0]), n1 = scalar_ptr(p.norms[1]),
+                                   n2 = scalar_ptr(p.norms[2]);
+        const global_ptr<uint8_t> codes = m == 0 ? c0 : (m == 1 ? c1 : c2);
+        const global_ptr<uint16_t> norms = m == 0 ? n0 : (m == 1 ? n1 : n2);
+        typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+        const global_ptr<u32x4> w4 = (global_ptr<u32x4>)(codes + (size_t)row * (K / 2) + g * 64);
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const u32x4 v = w4[k];
+            r.w[k] = make_uint4(v.x, v.y, v.z, v.w);
+        }
+        r.norm = norms[(size_t)row * groups + g];
+    }
+    return r;
+}
+
+// The phi outputs of one row, whose prepared activations are x [K] and its
+// group scales / offsets: thread u forms its unit's group dot and the two
+// products of Scalar.MatMulRows' chain (Scalar.cs:146-192): scaled =
+// (HalfToSingle(norm) * ByteScale) * scale[g], scaled * dot and scaled *
+// offset[g], into prod[2 * u + 0 / 1].  After a barrier, lane o < outputs
+// adds them in ascending group order (accumulator += scaled * dot, bias +=
+// scaled * offset) and returns accumulator - bias (other lanes return 0).
+__device__ __forceinline__ float phi_outputs(const PhiRows& p, const PhiUnit& unit, const int8_t* x,
+                                             const float* scales, const float* offsets, int K,
+                                             const int (&first)[4], float* prod)
+{
+    const int groups = K / 128, outputs = first[3] - first[0];
+    const int u = threadIdx.x;
+    if (u < outputs * groups) {
+        const int g = u % groups;
+        const float scaled = ref_half_to_single(unit.norm) * p.byte_scale * scales[g];
+        const int dot = cq4_group_dot(unit.w, x + g * 128, p.split);
+        prod[2 * u] = scaled * (float)dot;
+        prod[2 * u + 1] = scaled * offsets[g];
+    }
+    lds_barrier();
+    float y = 0.0f;
+    const int o = threadIdx.x;
+    if (o < outputs) {
+        // groups % 4 == 0 (K = 4 * dim, dim % 128 == 0): two groups a float4,
+        // eight groups' reads ahead of their adds
+        const float4* pr = reinterpret_cast<const float4*>(prod) + o * (groups / 2);
+        float accumulator = 0.0f, bias = 0.0f;
+        int g = 0;
+        for (; g + 8 <= groups; g += 8) {
+            const float4 v[4] = {pr[g / 2], pr[g / 2 + 1], pr[g / 2 + 2], pr[g / 2 + 3]};
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                accumulator += v[j].x;
+                bias += v[j].y;
+                accumulator += v[j].z;
+                bias += v[j].w;
+            }
+        }
+        for (; g < groups; g += 2) {
+            const float4 v = pr[g / 2];
+            accumulator += v.x;
+            bias += v.y;
+            accumulator += v.z;
+            bias += v.w;
+        }
+        y = accumulator - bias;
+    }
+    return y;
 }
 
 }  // namespace nhip

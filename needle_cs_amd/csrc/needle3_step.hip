@@ -100,14 +100,6 @@ __device__ __forceinline__ void fake_row(float* d, int n, float* red)
     __syncthreads();
 }
 
-// Prepared activations (Quant.Activations): row t's values at values + t * cols,
-// its group scales and offsets at scales / offsets + t * stride.
-struct Act {
-    int8_t* values;
-    float* scales;
-    float* offsets;
-};
-
 // Quant.Prepare (Quant.cs:473-488) of an LDS row of `cols` floats into row t
 // of act: wave w takes groups w, w + 4, ...
 __device__ __forceinline__ void prepare_row(const float* v, int cols, int bits, const Act& act, int stride, int t)
@@ -119,16 +111,6 @@ __device__ __forceinline__ void prepare_row(const float* v, int cols, int bits, 
         prepare_group_wave(v0, v1, bits, act.values + (size_t)t * cols + g * 128, act.scales + (size_t)t * stride + g,
                            act.offsets + (size_t)t * stride + g);
     }
-}
-
-// A workgroup barrier that orders LDS only: the waves' outstanding global
-// loads and stores stay in flight across it (__syncthreads waits for them),
-// for code whose waves share data through LDS alone.
-__device__ __forceinline__ void lds_barrier()
-{
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
-    __builtin_amdgcn_s_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
 // Ops.InverseRms of an LDS row x[0..n) (written before the call and
@@ -228,20 +210,6 @@ __global__ __launch_bounds__(kThreads) void n3_embed_kernel(const uint8_t* raw, 
 
 // ----------------------------------------------- hyper-connection mix --
 
-// The layer's hyper-connection phi rows (RunLayerBatch, Engine.cs:2356-2364):
-// 4 pre, 4 post and 16 residual-mix outputs of three Cq4 matrices over the
-// stream's 4-bit prepared activations.  codes[m] points at the layer's first
-// row of matrix m ([rows][K / 2] codes, the archive's row-major bytes),
-// norms[m] at its fp16 group norms ([rows][K / 128]).
-struct PhiRows {
-    const uint8_t* codes[3];
-    const uint16_t* norms[3];
-    uint32_t split[4];  // the 4-bit codebook's split lookup tables (lut4x)
-    float byte_scale;   // its ByteScale
-    Act in;             // the stream's Quant.Prepare rows, K = kLanes * dim
-    int stride;
-};
-
 struct HyperArgs {
     const float* stream;
     PhiRows phi;
@@ -260,160 +228,21 @@ struct HyperArgs {
     Act act;
     int stride;
     int rows;
-    float* mix_logits;  // set: the residual-mix logits [rows][16] go here, for
-                        // the attention launch's Sinkhorn workgroups
 };
 
-// Scalar.MatMulRows' exact int32 dot (Scalar.cs:166-184) of one Cq4 row's
-// group (64 code bytes) with a group of 4-bit prepared activations (128
-// int8 in Planes order): code byte j of half h carries activation
-// 2h * 32 + j in its low nibble and (2h + 1) * 32 + j in its high nibble.
-// The codes go through lut4x to their codebook bytes (below 128, so the
-// signed byte dot is exact).
-__device__ __forceinline__ int cq4_group_dot(const uint4 (&w4)[4], const int8_t* x, const uint32_t (&split)[4])
-{
-    const uint4* x4 = reinterpret_cast<const uint4*>(x);
-    int dot = 0;
-#pragma unroll
-    for (int h = 0; h < 2; h++) {
-        const uint4 wv[2] = {w4[2 * h], w4[2 * h + 1]};
-        const uint4 lo[2] = {x4[4 * h], x4[4 * h + 1]};
-        const uint4 hi[2] = {x4[4 * h + 2], x4[4 * h + 3]};
-#pragma unroll
-        for (int k = 0; k < 8; k++) {
-            const uint4& w = wv[k >> 2];
-            const uint32_t word = (k & 3) == 0 ? w.x : (k & 3) == 1 ? w.y : (k & 3) == 2 ? w.z : w.w;
-            const uint4& l = lo[k >> 2];
-            const uint4& u = hi[k >> 2];
-            const uint32_t xl = (k & 3) == 0 ? l.x : (k & 3) == 1 ? l.y : (k & 3) == 2 ? l.z : l.w;
-            const uint32_t xh = (k & 3) == 0 ? u.x : (k & 3) == 1 ? u.y : (k & 3) == 2 ? u.z : u.w;
-            const uint32_t bl = lut4x(word & 0x0F0F0F0Fu, split[0], split[1], split[2], split[3]);
-            const uint32_t bh = lut4x((word >> 4) & 0x0F0F0F0Fu, split[0], split[1], split[2], split[3]);
-            dot = __builtin_amdgcn_sdot4((int)bl, (int)xl, dot, false);
-            dot = __builtin_amdgcn_sdot4((int)bh, (int)xh, dot, false);
-        }
-    }
-    return dot;
-}
-
-// Thread u's (output, group) unit of `outputs` phi rows (u < outputs * K /
-// 128, at most kThreads units): its 64 code bytes and fp16 norm, loaded
-// ahead of the activations they meet.  first[m] is the first output of
-// matrix m (outputs first[m] .. first[m + 1] - 1 read its rows 0, 1, ...).
-struct PhiUnit {
-    uint4 w[4];
-    uint32_t norm;
-};
-
-// A global-memory pointer argument held in scalar registers: selecting
-// between such values per lane stays a select, where selecting struct fields
-// per lane becomes a load of the chosen field through a vector address (and a
-// vmcnt(0) wait that also waits for every global load issued before it).
-template <typename T>
-using global_ptr = const __attribute__((address_space(1))) T*;
-template <typename T>
-__device__ __forceinline__ global_ptr<T> scalar_ptr(const T* p)
-{
-    const uint64_t v = reinterpret_cast<uint64_t>(p);
-    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
-    const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
-    return (global_ptr<T>)(((uint64_t)hi << 32) | lo);
-}
-
-__device__ __forceinline__ PhiUnit phi_load(const PhiRows& p, int K, int m0, const int (&first)[4])
-{
-    PhiUnit r{};
-    const int groups = K / 128, outputs = first[3] - first[0];
-    const int u = threadIdx.x;
-    if (u < outputs * groups) {
-        const int o = u / groups, g = u - o * groups;
-        const int m = m0 + (o >= first[1] - first[0]) + (o >= first[2] - first[0]);
-        const int row = o + first[0] - first[m - m0];
-        const global_ptr<uint8_t> c0 = scalar_ptr(p.codes[0]), c1 = scalar_ptr(p.codes[1]),
-                                  c2 = scalar_ptr(p.codes[2]);
-        const global_ptr<uint16_t> n0 = scalar_ptr(p.norms[0]), n1 = scalar_ptr(p.norms[1]),
-                                   n2 = scalar_ptr(p.norms[2]);
-        const global_ptr<uint8_t> codes = m == 0 ? c0 : (m == 1 ? c1 : c2);
-        const global_ptr<uint16_t> norms = m == 0 ? n0 : (m == 1 ? n1 : n2);
-        typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-        const global_ptr<u32x4> w4 = (global_ptr<u32x4>)(codes + (size_t)row * (K / 2) + g * 64);
-#pragma unroll
-        for (int k = 0; k < 4; k++) {
-            const u32x4 v = w4[k];
-            r.w[k] = make_uint4(v.x, v.y, v.z, v.w);
-        }
-        r.norm = norms[(size_t)row * groups + g];
-    }
-    return r;
-}
-
-// The phi outputs of one row, whose prepared activations are x [K] and its
-// group scales / offsets: thread u forms its unit's group dot and the two
-// products of Scalar.MatMulRows' chain (Scalar.cs:146-192): scaled =
-// (HalfToSingle(norm) * ByteScale) * scale[g], scaled * dot and scaled *
-// offset[g], into prod[2 * u + 0 / 1].  After a barrier, lane o < outputs
-// adds them in ascending group order (accumulator += scaled * dot, bias +=
-// scaled * offset) and returns accumulator - bias (other lanes return 0).
-__device__ __forceinline__ float phi_outputs(const PhiRows& p, const PhiUnit& unit, const int8_t* x,
-                                             const float* scales, const float* offsets, int K,
-                                             const int (&first)[4], float* prod)
-{
-    const int groups = K / 128, outputs = first[3] - first[0];
-    const int u = threadIdx.x;
-    if (u < outputs * groups) {
-        const int g = u % groups;
-        const float scaled = ref_half_to_single(unit.norm) * p.byte_scale * scales[g];
-        const int dot = cq4_group_dot(unit.w, x + g * 128, p.split);
-        prod[2 * u] = scaled * (float)dot;
-        prod[2 * u + 1] = scaled * offsets[g];
-    }
-    lds_barrier();
-    float y = 0.0f;
-    const int o = threadIdx.x;
-    if (o < outputs) {
-        // groups % 4 == 0 (K = 4 * dim, dim % 128 == 0): two groups a float4,
-        // eight groups' reads ahead of their adds
-        const float4* pr = reinterpret_cast<const float4*>(prod) + o * (groups / 2);
-        float accumulator = 0.0f, bias = 0.0f;
-        int g = 0;
-        for (; g + 8 <= groups; g += 8) {
-            const float4 v[4] = {pr[g / 2], pr[g / 2 + 1], pr[g / 2 + 2], pr[g / 2 + 3]};
-#pragma unroll
-            for (int j = 0; j < 4; j++) {
-                accumulator += v[j].x;
-                bias += v[j].y;
-                accumulator += v[j].z;
-                bias += v[j].w;
-            }
-        }
-        for (; g < groups; g += 2) {
-            const float4 v = pr[g / 2];
-            accumulator += v.x;
-            bias += v.y;
-            accumulator += v.z;
-            bias += v.w;
-        }
-        y = accumulator - bias;
-    }
-    return y;
-}
-
-// Thread i < 24's phi output affine map, z = ga * y + gb: i < 4 the pre
-// outputs (a_pre, b_pre[i]), then the post (a_post, b_post[i - 4]) and the
-// residual-mix logits (a_res, b_res[i - 8]).
+// Thread i < 8's phi output affine map, z = ga * y + gb: i < 4 the pre
+// outputs (a_pre, b_pre[i]), then the post ones (a_post, b_post[i - 4]).
 __device__ __forceinline__ void phi_affine(const HyperArgs& a, float& ga, float& gb)
 {
     const int i = threadIdx.x;
-    const global_ptr<float> pa[3] = {scalar_ptr(a.a_pre), scalar_ptr(a.a_post), scalar_ptr(a.a_res)};
-    const global_ptr<float> pb[3] = {scalar_ptr(a.b_pre), scalar_ptr(a.b_post), scalar_ptr(a.b_res)};
-    const int m = i < 4 ? 0 : (i < 8 ? 1 : 2);
-    const global_ptr<float> ap = m == 0 ? pa[0] : (m == 1 ? pa[1] : pa[2]);
-    const global_ptr<float> bp = m == 0 ? pb[0] : (m == 1 ? pb[1] : pb[2]);
+    const global_ptr<float> a0 = scalar_ptr(a.a_pre), a1 = scalar_ptr(a.a_post);
+    const global_ptr<float> b0 = scalar_ptr(a.b_pre), b1 = scalar_ptr(a.b_post);
     ga = 0.0f;
     gb = 0.0f;
-    if (i < 24) {
-        ga = ap[0];
-        gb = bp[i - (m == 0 ? 0 : (m == 1 ? 4 : 8))];
+    if (i < 8) {
+        const bool post = i >= 4;
+        ga = (post ? a1 : a0)[0];
+        gb = (post ? b1 : b0)[i & 3];
     }
 }
 
@@ -488,10 +317,9 @@ __device__ __forceinline__ void hyper_mix_row(const HyperArgs& a, int t, float y
 // postGate by Sigmoid, Mix4 of the lanes into input and residual, Sinkhorn4x4
 // of the residual-mix logits.  Workgroup t < rows takes row t's 4 pre and 4
 // post outputs and the mix; only the layer's tail reads the Sinkhorn matrix,
-// so workgroup rows + t forms row t's 16 residual-mix outputs and its
-// Sinkhorn (Engine.cs:2374-2378) beside it -- or, with a.mix_logits, only
-// the logits, for the attention launch's Sinkhorn workgroups (whose time
-// the attention hides).  Then, on layers without an engram,
+// so workgroup rows + t (launched for steps whose attention launch does not
+// form it) forms row t's 16 residual-mix outputs and its Sinkhorn
+// (Engine.cs:2374-2378) beside it.  Then, on layers without an engram,
 // RunAttentionBatch's CenteredRmsFakeA8 of the residual and its 2-bit Prepare
 // (Engine.cs:2487-2490); on engram layers, ApplyEngramBatch's input
 // (Engine.cs:2404-2414): every table's GatherRow (zeros for row -1),
@@ -509,12 +337,7 @@ __global__ __launch_bounds__(kThreads) void n3_hyper_kernel(HyperArgs a)
         const float y = phi_outputs(a.phi, unit, a.phi.in.values + (size_t)t * K,
                                     a.phi.in.scales + (size_t)t * a.phi.stride,
                                     a.phi.in.offsets + (size_t)t * a.phi.stride, K, first, prod);
-        const float lg = ga * y + gb;
-        if (a.mix_logits) {
-            if (threadIdx.x < 16) a.mix_logits[t * 16 + threadIdx.x] = lg;
-            return;
-        }
-        if (threadIdx.x < 16) logits[threadIdx.x] = lg;
+        if (threadIdx.x < 16) logits[threadIdx.x] = ga * y + gb;
         __syncthreads();
         if (threadIdx.x < 64) sinkhorn4x4_wave(logits, a.mix + t * 16);
         return;
@@ -1141,19 +964,19 @@ __device__ __forceinline__ void kron_rows(const float* z, int active, const floa
 // preloads into SGPRs (kernarg preload; a struct argument is never
 // preloaded), so those loads issue without an argument-segment round trip.
 // LDS the fused tail's next-layer mix adds to tail_lds_bytes: the 4-bit
-// prepared stream row (values, scales, offsets), the phi products of 24
+// prepared stream row (values, scales, offsets), the phi products of 8
 // outputs and the mix kernel's two dim rows.
 size_t tail_hyper_lds_bytes(int dim)
 {
     const size_t n4 = (size_t)kLanes * dim, groups = n4 / 128;
-    return 16 + n4 + sizeof(float) * (2 * groups + 2 * 24 * groups + 2 * (size_t)dim);
+    return 16 + n4 + sizeof(float) * (2 * groups + 2 * 8 * groups + 2 * (size_t)dim);
 }
 
-// HYPER: for a layer l < L - 1 of a step whose rows are one per slot, the
+// HYPER: for a layer l < L - 1 of a step whose rows are one per slot (whose
+// attention launch forms the residual-mix logits and their Sinkhorn), the
 // workgroup goes on into layer l + 1's mix (h, as n3_hyper_kernel's row
-// part with all 24 phi outputs, the 16 residual-mix logits stored for the
-// attention launch's Sinkhorn): the next stream row stays in registers and
-// its 4-bit prepared activations in LDS.
+// part): the next stream row stays in registers and its 4-bit prepared
+// activations in LDS, with a copy in act for the attention launch.
 template <bool HYPER>
 __global__ __launch_bounds__(kThreads) void n3_tail_kernel(const float* h_proj, float* h_residual,
                                                            const float* h_post_norm, const float* h_pre_norm,
@@ -1185,8 +1008,8 @@ __global__ __launch_bounds__(kThreads) void n3_tail_kernel(const float* h_proj, 
     // HYPER: the 4-bit prepared next stream row, 16-byte aligned
     int8_t* a4v = reinterpret_cast<int8_t*>(lds + ((int)(nst + 32 * ts - lds) + 3) / 4 * 4);
     float* a4s = reinterpret_cast<float*>(a4v + n4);          // its group scales, then offsets
-    float* hprod = a4s + 2 * g4;                              // phi products [24][g4][2]
-    float* hx = hprod + 2 * 24 * g4;                          // the mix kernel's rows
+    float* hprod = a4s + 2 * g4;                              // phi products [8][g4][2]
+    float* hx = hprod + 2 * 8 * g4;                           // the mix kernel's rows
     float* hsq = hx + dim;
     __shared__ float weights[8];
     __shared__ float red[kWaves];
@@ -1366,9 +1189,10 @@ __global__ __launch_bounds__(kThreads) void n3_tail_kernel(const float* h_proj, 
         }
     }
     __syncthreads();
-    // HYPER: layer l + 1's phi rows, 4 pre, 4 post, 16 residual-mix; their
-    // codes and affine maps load under the next layer's RmsFakeA8 and Prepare
-    constexpr int kPhiFirst[4] = {0, 4, 8, 24};
+    // HYPER: layer l + 1's phi rows, 4 pre and 4 post (the attention launch
+    // forms the 16 residual-mix ones); their codes and affine maps load under
+    // the next layer's RmsFakeA8 and Prepare
+    constexpr int kPhiFirst[4] = {0, 4, 8, 8};
     PhiUnit hunit{};
     float hga = 0.0f, hgb = 0.0f;
     if constexpr (HYPER) {
@@ -1406,8 +1230,16 @@ __global__ __launch_bounds__(kThreads) void n3_tail_kernel(const float* h_proj, 
         if constexpr (HYPER) {
             prepare_row(ns, n4, 4, Act{a4v, a4s, a4s + g4}, 0, 0);
             lds_barrier();
+            // and into the row's global copy, which layer l + 1's attention
+            // launch reads for the residual-mix logits
+            for (int e = threadIdx.x; e < n4 / 16; e += kThreads)
+                reinterpret_cast<uint4*>(a.act.values + (size_t)t * n4)[e] = reinterpret_cast<const uint4*>(a4v)[e];
+            if ((int)threadIdx.x < 2 * g4) {
+                const int g = (int)threadIdx.x % g4;
+                float* dst = threadIdx.x < g4 ? a.act.scales : a.act.offsets;
+                dst[(size_t)t * a.stride + g] = a4s[threadIdx.x];
+            }
             const float y = phi_outputs(h.phi, hunit, a4v, a4s, a4s + g4, n4, kPhiFirst, hprod);
-            if (threadIdx.x >= 8 && threadIdx.x < 24) h.mix_logits[t * 16 + threadIdx.x - 8] = hga * y + hgb;
             __shared__ float hpre[4];
             hyper_mix_row(h, t, y, hga, hgb, nsv, hsn, hx, hsq, hpre, red, &inv_s);
         } else {
@@ -1500,7 +1332,7 @@ struct nhip_ctx {
     // alternate between the two stream buffers)
     float *stream_a = nullptr, *stream_b = nullptr, *normed = nullptr, *input = nullptr, *residual = nullptr,
           *raw = nullptr, *gate = nullptr, *att = nullptr, *proj = nullptr, *key = nullptr, *stage = nullptr,
-          *ein = nullptr, *post_gate = nullptr, *mix = nullptr, *mix_logits = nullptr, *qs = nullptr, *logits = nullptr, *act_s = nullptr,
+          *ein = nullptr, *post_gate = nullptr, *mix = nullptr, *qs = nullptr, *logits = nullptr, *act_s = nullptr,
           *act_o = nullptr, *act4_s = nullptr, *act4_o = nullptr;
     int8_t *act_v = nullptr, *act4_v = nullptr, *q8 = nullptr;  // act4: the stream's 4-bit Prepare (phi input)
     int32_t* d_in = nullptr;  // the per-row inputs of a step, kInSections x max_rows, then the engram rows
@@ -1861,7 +1693,6 @@ int32_t alloc_state(nhip_ctx* c)
         (rc = ctx_alloc(c, &c->ein, (size_t)R * d)) || (rc = ctx_alloc(c, &c->act4_v, (size_t)R * sw)) ||
         (rc = ctx_alloc(c, &c->act4_s, (size_t)R * stride4)) || (rc = ctx_alloc(c, &c->act4_o, (size_t)R * stride4)) ||
         (rc = ctx_alloc(c, &c->post_gate, (size_t)R * 4)) || (rc = ctx_alloc(c, &c->mix, (size_t)R * 16)) ||
-        (rc = ctx_alloc(c, &c->mix_logits, (size_t)R * 16)) ||
         (rc = ctx_alloc(c, &c->q8, (size_t)R * qw)) || (rc = ctx_alloc(c, &c->qs, (size_t)R * c->heads)) ||
         (rc = ctx_alloc(c, &c->logits, (size_t)R * c->vocab)) || (rc = ctx_alloc(c, &c->act_v, (size_t)R * sw)) ||
         (rc = ctx_alloc(c, &c->d_topk_idx, (size_t)R * 8)) || (rc = ctx_alloc(c, &c->d_topk_lp, (size_t)R * 8)) ||
@@ -2005,8 +1836,7 @@ int32_t enqueue_step(nhip_ctx* c, int rows, int heads, int k, bool argmax, bool 
                          c->b_post + 4 * l, c->b_res + 16 * l, l % kLanes, d, c->input, c->residual, c->post_gate,
                          c->mix, c->layer[l].norm_in, st ? st->tables : nullptr, st ? st->table_rows : 0,
                          st ? st->table_cols : 0, st ? st->table_bits : 0, c->engram_tables,
-                         st && st->table_bits == 2 ? c->book2 : c->book4, in_erows(c, c->d_in), act, stride_d, rows,
-                         sink_in_attention ? c->mix_logits : nullptr};
+                         st && st->table_bits == 2 ? c->book2 : c->book4, in_erows(c, c->d_in), act, stride_d, rows};
     };
     // for those steps each layer's tail launch also runs the next layer's
     // mix (n3_tail_kernel<true>); NHIP_N3_TAIL_MIX=0 keeps the mix launches
@@ -2024,7 +1854,9 @@ int32_t enqueue_step(nhip_ctx* c, int rows, int heads, int k, bool argmax, bool 
         const N3Site* st = site_of(l);
         if (!fuse_tail || l == 0) {  // otherwise layer l - 1's tail launch ran the mix
             const HyperArgs ha = hyper_args(l, cur);
-            hipLaunchKernelGGL(n3_hyper_kernel, dim3(2 * rows), dim3(kThreads), 0, s, ha);
+            // the attention launch forms the residual-mix rows' Sinkhorn for
+            // steps whose rows are one per slot; the mix launch otherwise
+            hipLaunchKernelGGL(n3_hyper_kernel, dim3(sink_in_attention ? rows : 2 * rows), dim3(kThreads), 0, s, ha);
             NHIP_CHECK_HIP(hipGetLastError());
         }
         EngramArgs ea{};
@@ -2079,6 +1911,9 @@ int32_t enqueue_step(nhip_ctx* c, int rows, int heads, int k, bool argmax, bool 
         // attention launch; otherwise (runs of rows, long caches) two launches
         int32_t fused = 1;
         if (single_runs) {
+            // with the Sinkhorn: the layer's residual-mix phi rows over the
+            // stream's 4-bit prepared rows
+            const HyperArgs hl = hyper_args(l, cur);
             const Needle3AttnInputs n3in{c->raw,
                                          {w.q_taps, w.k_taps, w.v_taps},
                                          w.q_norm,
@@ -2086,8 +1921,11 @@ int32_t enqueue_step(nhip_ctx* c, int rows, int heads, int k, bool argmax, bool 
                                          c->rope_cos,
                                          c->rope_sin,
                                          qkv_hist,
-                                         sink_in_attention ? c->mix_logits : nullptr,
-                                         sink_in_attention ? c->mix : nullptr};
+                                         sink_in_attention ? c->mix : nullptr,
+                                         hl.phi,
+                                         sw,
+                                         hl.a_res,
+                                         hl.b_res};
             fused = attention_decode_needle3_impl(n3in, rows, H, KV, c->qk, c->vd, keys, kscale, values, vscale,
                                                   c->slots, c->capacity, in(c, c->d_in, kInSlots),
                                                   in(c, c->d_in, kInPos), first, count, c->max_chunks, c->att, s);
