@@ -663,10 +663,10 @@ __global__ __launch_bounds__(row_threads(MODE)) void decode_attention_row_kernel
                 const float* src = (int)threadIdx.x < groups ? ph.in.scales : ph.in.offsets;
                 phi_so[threadIdx.x] = src[(size_t)t * ph.stride + (int)threadIdx.x % groups];
             }
-            lds_barrier();
+            __syncthreads();
             const float y = phi_outputs(ph, unit, phi_x, phi_so, phi_so + groups, K, first, phi_prod);
             if (threadIdx.x < 16) logits[threadIdx.x] = ga * y + gb;
-            lds_barrier();
+            __syncthreads();
             if (threadIdx.x < 64) sinkhorn4x4_wave(logits, p.n3.mix + t * 16);
             return;
         }

@@ -750,16 +750,6 @@ __device__ __forceinline__ void prepare_group_wave(float v0, float v1, int bits,
     }
 }
 
-// A workgroup barrier that orders LDS only: the waves' outstanding global
-// loads and stores stay in flight across it (__syncthreads waits for them),
-// for code whose waves share data through LDS alone.
-__device__ __forceinline__ void lds_barrier()
-{
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
-    __builtin_amdgcn_s_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
-}
-
 // Scalar.MatMulRows' exact int32 dot (Scalar.cs:166-184) of one Cq4 row's
 // group (64 code bytes) with a group of 4-bit prepared activations (128
 // int8 in Planes order): code byte j of half h carries activation
@@ -856,7 +846,7 @@ __device__ __forceinline__ float phi_outputs(const PhiRows& p, const PhiUnit& un
         prod[2 * u] = scaled * (float)dot;
         prod[2 * u + 1] = scaled * offsets[g];
     }
-    lds_barrier();
+    __syncthreads();
     float y = 0.0f;
     const int o = threadIdx.x;
     if (o < outputs) {

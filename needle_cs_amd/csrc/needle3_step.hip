@@ -115,18 +115,13 @@ __device__ __forceinline__ void prepare_row(const float* v, int cols, int bits, 
 
 // Ops.InverseRms of an LDS row x[0..n) (written before the call and
 // synchronised), its sum of squares in the AVX2 tier's order by wave 0.
-// LDS: the closing barrier is lds_barrier.
-template <bool LDS = false>
 __device__ __forceinline__ float row_inverse_rms(const float* x, int n, float* slot)
 {
     if (threadIdx.x < 64) {
         const float sum = wave_v256_sum(x, x, n);
         if (threadIdx.x == 0) *slot = inverse_rms_of(sum, n);
     }
-    if constexpr (LDS)
-        lds_barrier();
-    else
-        __syncthreads();
+    __syncthreads();
     return *slot;
 }
 
@@ -264,7 +259,7 @@ __device__ __forceinline__ void hyper_mix_row(const HyperArgs& a, int t, float y
     const int i = threadIdx.x;
     if (i < 4) hpre[i] = sigmoid_poly(ga * y + gb + (i == a.lane ? 4.0f : -4.0f));
     if (i >= 4 && i < 8) a.post_gate[t * 4 + i - 4] = 2.0f * sigmoid_poly(ga * y + gb + (i - 4 == a.lane ? 0.0f : -4.0f));
-    lds_barrier();
+    __syncthreads();
     float uv[kPer], peak = 0.0f;
 #pragma unroll
     for (int q = 0; q < kPer; q++) {
@@ -282,7 +277,7 @@ __device__ __forceinline__ void hyper_mix_row(const HyperArgs& a, int t, float y
         peak = wave_max(peak);
         if ((i & 63) == 0) red[i >> 6] = peak;
     }
-    lds_barrier();
+    __syncthreads();
     if (a.tables) {
         const int sub = a.table_cols, per = sub / 128;
         for (int unit = i >> 6; unit < a.tables_count * per; unit += kWaves) {
@@ -298,7 +293,7 @@ __device__ __forceinline__ void hyper_mix_row(const HyperArgs& a, int t, float y
         prepare_row(sq, dim, 2, a.act, a.stride, t);
         return;
     }
-    const float inverse = row_inverse_rms<true>(x, dim, inv_s);
+    const float inverse = row_inverse_rms(x, dim, inv_s);
     float m = red[0];
     for (int w = 1; w < kWaves; w++) m = fmaxf(m, red[w]);
     const float top = m * inverse;
@@ -309,7 +304,7 @@ __device__ __forceinline__ void hyper_mix_row(const HyperArgs& a, int t, float y
         const int c = col_of(q);
         if (c < dim) x[c] = clamp_q(((1.0f + sn[q]) * uv[q] * inverse) * round) * scale;
     }
-    lds_barrier();
+    __syncthreads();
     prepare_row(x, dim, 2, a.act, a.stride, t);
 }
 
@@ -1212,10 +1207,7 @@ __global__ __launch_bounds__(kThreads) void n3_tail_kernel(const float* h_proj, 
             const float sum = wave_v256_squares(nst, n4);
             if (threadIdx.x == 0) inv_s = inverse_rms_of(sum, n4);
         }
-        if constexpr (HYPER)  // the phi codes stay in flight
-            lds_barrier();
-        else
-            __syncthreads();
+        __syncthreads();
         inverse = inv_s;
         float m = red[0];
         for (int w = 1; w < kWaves; w++) m = fmaxf(m, red[w]);
@@ -1223,13 +1215,10 @@ __global__ __launch_bounds__(kThreads) void n3_tail_kernel(const float* h_proj, 
         const float scale = peak > 0.0f ? peak / 127.0f : 1.0f;
         const float round = 1.0f / scale;
         for (int c = threadIdx.x; c < n4; c += kThreads) ns[c] = clamp_q((ns[c] * inverse) * round) * scale;
-        if constexpr (HYPER)
-            lds_barrier();
-        else
-            __syncthreads();
+        __syncthreads();
         if constexpr (HYPER) {
             prepare_row(ns, n4, 4, Act{a4v, a4s, a4s + g4}, 0, 0);
-            lds_barrier();
+            __syncthreads();
             // and into the row's global copy, which layer l + 1's attention
             // launch reads for the residual-mix logits
             for (int e = threadIdx.x; e < n4 / 16; e += kThreads)
