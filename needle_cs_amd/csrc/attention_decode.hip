@@ -625,6 +625,68 @@ constexpr int kRowPlain = 0, kRowPost = 1, kRowNeedle3 = 2;
 // (thousands of workgroups), where 4 waves keep twice the workgroups resident.
 constexpr int row_threads(int mode) { return mode == kRowPlain ? 256 : 512; }
 
+// Needle3Proj's Gate outputs 16 j .. 16 j + 15 of every row t < rows (at
+// most 16): wave g < k / 128 takes group g through four i8 MFMAs, one per
+// plane (A the rows' prepared activations, B the 2-bit codes through the
+// codebook bytes; the codebook decode kernels' operands), then one lane per
+// (row, output) runs Scalar.MatMulRows' chain (Scalar.cs:146-192):
+//   scaled = (HalfToSingle(norm[n][g]) * ByteScale) * scale[t][g]
+//   acc += scaled * D_g;  bias += scaled * offset[t][g]  (g ascending);  y = acc - bias
+// lds: 2 * 16 * 16 * 8 floats.
+typedef int n3_v4i __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ void n3_gate_tile(const Needle3Proj& q, int rows, int j, float* lds)
+{
+    const int groups = q.k >> 7;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int nr = lane & 15, kq = lane >> 4;
+    float* pa = lds;  // [t][n][8]
+    float* pb = lds + 16 * 16 * 8;
+    if (wave < groups) {
+        const size_t n = (size_t)j * 16 + nr;
+        const uint2 code = *reinterpret_cast<const uint2*>(q.codes[3] + n * (q.k >> 2) + wave * 32 + kq * 8);
+        const uint32_t norm = q.norms[3][n * groups + wave];
+        n3_v4i d = {0, 0, 0, 0};
+#pragma unroll
+        for (int pl = 0; pl < 4; pl++) {
+            long av = 0;
+            if (nr < rows) av = *reinterpret_cast<const long*>(q.act + (size_t)nr * q.k + wave * 128 + 32 * pl + 8 * kq);
+            const uint32_t b0 = lut2((code.x >> (2 * pl)) & 0x03030303u, q.table);
+            const uint32_t b1 = lut2((code.y >> (2 * pl)) & 0x03030303u, q.table);
+            d = __builtin_amdgcn_mfma_i32_16x16x32_i8(av, (long)(((uint64_t)b1 << 32) | b0), d, 0, 0, 0);
+        }
+        // lane l holds D[t = 4 (l / 16) + i][output l % 16] in d[i]
+        const float hb = ref_half_to_single(norm) * q.byte_scale;
+        const int dv[4] = {d.x, d.y, d.z, d.w};
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int t = 4 * kq + i;
+            if (t < rows) {
+                const float scaled = hb * q.scales[(size_t)t * q.stride + wave];
+                pa[(t * 16 + nr) * 8 + wave] = scaled * static_cast<float>(dv[i]);
+                pb[(t * 16 + nr) * 8 + wave] = scaled * q.offsets[(size_t)t * q.stride + wave];
+            }
+        }
+    }
+    __syncthreads();
+    const int x = threadIdx.x;
+    if (x < rows * 16) {
+        const float4* ra = reinterpret_cast<const float4*>(pa + x * 8);
+        const float4* rb = reinterpret_cast<const float4*>(pb + x * 8);
+        const float4 a0 = ra[0], a1 = ra[1], b0 = rb[0], b1 = rb[1];
+        const float av[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+        const float bv[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
+        float acc = 0.0f, bias = 0.0f;
+#pragma unroll
+        for (int g = 0; g < 8; g++) {
+            if (g < groups) {
+                acc = acc + av[g];
+                bias = bias + bv[g];
+            }
+        }
+        q.gate[(size_t)(x >> 4) * q.gate_rows + j * 16 + (x & 15)] = acc - bias;
+    }
+}
+
 template <int MODE>
 __global__ __launch_bounds__(row_threads(MODE)) void decode_attention_row_kernel(ATTN_HEAD_PARAMS, DecodeAttnParams p)
 {
@@ -646,7 +708,7 @@ __global__ __launch_bounds__(row_threads(MODE)) void decode_attention_row_kernel
         // residual-mix logits (RunLayerBatch, Engine.cs:2364-2378: the phi
         // outputs' Scalar.MatMulRows chains, then a_res * y + b_res[o]) and
         // their Sinkhorn4x4 by wave 0, beside the attention
-        if ((int)blockIdx.y == p.heads) {
+        if (p.n3.mix && (int)blockIdx.y == p.heads) {
             __shared__ __align__(16) float phi_prod[2 * 16 * kPhiMaxGroups];
             __shared__ __align__(16) int8_t phi_x[128 * kPhiMaxGroups];  // the prepared stream row
             __shared__ float phi_so[2 * kPhiMaxGroups];                   // its group scales, offsets
@@ -670,6 +732,15 @@ __global__ __launch_bounds__(row_threads(MODE)) void decode_attention_row_kernel
             if (threadIdx.x < 64) sinkhorn4x4_wave(logits, p.n3.mix + t * 16);
             return;
         }
+        // the Gate columns of workgroups (launched with n3.proj): 16 Gate
+        // outputs of every row each
+        const int gate_col0 = p.heads + (p.n3.mix ? 1 : 0);
+        if ((int)blockIdx.y >= gate_col0) {
+            __shared__ __align__(16) float gate_lds[2 * 16 * 16 * 8];
+            const int j = ((int)blockIdx.y - gate_col0) * p.rows + (int)blockIdx.x;
+            if (j < p.n3.proj.gate_rows / 16) n3_gate_tile(p.n3.proj, p.rows, j, gate_lds);
+            return;
+        }
     }
     // scores, then e_s; e_s * valueScale_s (each padded by kVBlock floats:
     // phase 4 reads the last chunk's rows up to the chunk length)
@@ -685,6 +756,9 @@ __global__ __launch_bounds__(row_threads(MODE)) void decode_attention_row_kernel
     __shared__ __align__(16) uint32_t sub_v[kSub][16];  // positions written in this launch
     __shared__ float sub_ks[kSub], sub_vs[kSub], q_scale[1];
     __shared__ float n3_red[N3 ? 3 : 1][64], n3_val[N3 ? 3 : 1][64];  // N3: per-unit norm and RoPE rows
+    // N3 with proj: the Q/K/V products [192][8] twice, the heads [192], the
+    // row's group scales and offsets [8 + 8] and its activations [1024 B]
+    __shared__ __align__(16) float n3_proj_lds[N3 ? 2 * 192 * 8 + 192 + 16 + 256 : 1];
 
     const int row = blockIdx.x;
     const int h = blockIdx.y;
@@ -743,13 +817,53 @@ __global__ __launch_bounds__(row_threads(MODE)) void decode_attention_row_kernel
     const int n3_base = n3_part == 0 ? 0 : (n3_part == 1 ? n3_qw : n3_qw + n3_kw);
     const int n3_off = (n3_part == 0 ? h : kv) * n3_n;
     const bool n3_lane = n3_part < 3 && e < n3_n;
+    const bool n3_proj = N3 && p.n3.proj.codes[0] != nullptr;  // the projections formed here
+    // N3 with proj: the loads of this thread's (output, group) units of the
+    // row's Q/K/V heads, its piece of the row's activations and its group
+    // scale or offset, issued before every other vector load of the
+    // workgroup (the memory counter waits in order: loaded after the cache
+    // rows, the products would wait for those too)
+    constexpr int kProjUnits = 3;  // units <= 3 * kRowThreads (host check)
+    typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+    u32x4 pj_cw[kProjUnits][2];
+    uint32_t pj_cn[kProjUnits];
+    uint4 pj_x = make_uint4(0u, 0u, 0u, 0u);
+    float pj_so = 0.0f;
+    if constexpr (N3) {
+        if (n3_proj) {
+            const Needle3Proj& q = p.n3.proj;
+            const int groups = q.k >> 7, nq = p.qk, units_n = (2 * nq + 64) * groups;
+            if (tid < q.k / 16) pj_x = reinterpret_cast<const uint4*>(q.act + (size_t)row * q.k)[tid];
+            const global_ptr<float> gs = scalar_ptr(q.scales), go = scalar_ptr(q.offsets);
+            if (tid < 2 * groups) pj_so = (tid < groups ? gs : go)[(size_t)row * q.stride + tid % groups];
+            const global_ptr<uint8_t> c0 = scalar_ptr(q.codes[0]), c1 = scalar_ptr(q.codes[1]),
+                                      c2 = scalar_ptr(q.codes[2]);
+            const global_ptr<uint16_t> m0 = scalar_ptr(q.norms[0]), m1 = scalar_ptr(q.norms[1]),
+                                       m2 = scalar_ptr(q.norms[2]);
+#pragma unroll
+            for (int k = 0; k < kProjUnits; k++) {
+                const int u = tid + k * kRowThreads;
+                if (u < units_n) {
+                    const int o = u / groups, g = u - o * groups;
+                    const int m = o < nq ? 0 : (o < 2 * nq ? 1 : 2);
+                    const int r = m == 0 ? h * nq + o : (m == 1 ? kv * nq + o - nq : kv * 64 + o - 2 * nq);
+                    const global_ptr<uint8_t> cb = m == 0 ? c0 : (m == 1 ? c1 : c2);
+                    const global_ptr<uint16_t> nb = m == 0 ? m0 : (m == 1 ? m1 : m2);
+                    const global_ptr<u32x4> w4 = (global_ptr<u32x4>)(cb + (size_t)r * (q.k >> 2) + g * 32);
+                    pj_cw[k][0] = w4[0];
+                    pj_cw[k][1] = w4[1];
+                    pj_cn[k] = nb[(size_t)r * groups + g];
+                }
+            }
+        }
+    }
     float n3_x2 = 0.0f, n3_x1 = 0.0f, n3_x0 = 0.0f, n3_t0 = 0.0f, n3_t1 = 0.0f, n3_t2 = 0.0f, n3_sc = 0.0f;
     float n3_cs = 0.0f, n3_sn = 0.0f;
     int n3_pos = 0;
     if constexpr (N3) {
         n3_pos = uniform_load(p.positions, row);
         if (n3_lane) {
-            n3_x2 = p.n3.raw[(size_t)row * n3_all + n3_base + n3_off + e];
+            if (!n3_proj) n3_x2 = p.n3.raw[(size_t)row * n3_all + n3_base + n3_off + e];
             // (selected, not indexed: a runtime index into the argument's
             // array would copy it to scratch)
             const float* taps = (n3_part == 0 ? p.n3.taps[0] : (n3_part == 1 ? p.n3.taps[1] : p.n3.taps[2])) + n3_off + e;
@@ -846,6 +960,73 @@ __global__ __launch_bounds__(row_threads(MODE)) void decode_attention_row_kernel
         const size_t cell = (pos0 + (u >> 2)) * p.kv_heads + kv;
         kw[k] = *reinterpret_cast<const uint4*>(p.keys + cell * qk + 16 * qslot);
         sv[k] = sbase[cell];
+    }
+    if constexpr (N3) {
+        if (n3_proj) {
+            // the row's query head h and its kv head's key and value heads
+            // (Scalar.MatMulRows, Scalar.cs:146-192): thread per (output,
+            // group), the group's exact int32 dot of the 2-bit codes (through
+            // the codebook bytes) with the prepared activations, and
+            //   scaled = (HalfToSingle(norm) * ByteScale) * scale[g]
+            //   acc += scaled * D_g;  bias += scaled * offset[g]  (g ascending)
+            // then one lane per output: y = acc - bias
+            const Needle3Proj& q = p.n3.proj;
+            const int groups = q.k >> 7, nq = p.qk, outs = 2 * nq + 64, units_n = outs * groups;
+            float* ppa = n3_proj_lds;  // [outs][8]
+            float* ppb = ppa + 192 * 8;
+            float* praw = ppb + 192 * 8;  // [outs]
+            float* pso = praw + 192;      // scales [8], offsets [8]
+            int8_t* px = reinterpret_cast<int8_t*>(pso + 16);
+            if (tid < q.k / 16) reinterpret_cast<uint4*>(px)[tid] = pj_x;
+            if (tid < 2 * groups) pso[(tid < groups ? 0 : 8) + tid % groups] = pj_so;
+            __syncthreads();
+#pragma unroll
+            for (int k = 0; k < kProjUnits; k++) {
+                const int u = tid + k * kRowThreads;
+                if (u < units_n) {
+                    const int o = u / groups, g = u - o * groups;
+                    // code word w (bytes 4w..4w+3: elements 4j + plane) meets
+                    // activation word plane * 8 + w (planes order)
+                    const uint4* xa = reinterpret_cast<const uint4*>(px + g * 128);
+                    int dot = 0;
+#pragma unroll
+                    for (int pl = 0; pl < 4; pl++) {
+                        const uint4 xv[2] = {xa[2 * pl], xa[2 * pl + 1]};
+#pragma unroll
+                        for (int w = 0; w < 8; w++) {
+                            const uint32_t cword = w < 4 ? pj_cw[k][0][w] : pj_cw[k][1][w - 4];
+                            const uint4& xq = xv[w >> 2];
+                            const uint32_t xword = (w & 3) == 0 ? xq.x : (w & 3) == 1 ? xq.y : (w & 3) == 2 ? xq.z : xq.w;
+                            dot = __builtin_amdgcn_sdot4((int)lut2((cword >> (2 * pl)) & 0x03030303u, q.table),
+                                                         (int)xword, dot, false);
+                        }
+                    }
+                    const float scaled = (ref_half_to_single(pj_cn[k]) * q.byte_scale) * pso[g];
+                    ppa[o * 8 + g] = scaled * static_cast<float>(dot);
+                    ppb[o * 8 + g] = scaled * pso[8 + g];
+                }
+            }
+            __syncthreads();
+            if (tid < outs) {
+                float acc = 0.0f, bias = 0.0f;
+#pragma unroll
+                for (int g = 0; g < 8; g++) {
+                    if (g < groups) {
+                        acc = acc + ppa[tid * 8 + g];
+                        bias = bias + ppb[tid * 8 + g];
+                    }
+                }
+                const float v = acc - bias;
+                praw[tid] = v;
+                float* rrow = q.raw + (size_t)row * n3_all;
+                if (tid < nq)
+                    rrow[h * nq + tid] = v;
+                else if (h % group == 0)  // once per kv head
+                    rrow[tid < 2 * nq ? n3_qw + kv * nq + tid - nq : n3_qw + n3_kw + kv * 64 + tid - 2 * nq] = v;
+            }
+            __syncthreads();
+            if (n3_lane) n3_x2 = praw[(n3_part == 0 ? 0 : (n3_part == 1 ? nq : 2 * nq)) + e];
+        }
     }
     if constexpr (POST) {
         // RoPE, then QuantizeInt8 per head, in qkv_post_kernel's arithmetic
@@ -1245,7 +1426,18 @@ int32_t attention_decode_needle3_impl(const Needle3AttnInputs& in, int32_t rows,
     NHIP_REQUIRE(!in.mix || (in.res_phi.codes[2] && in.res_phi.norms[2] && in.a_res && in.b_res && in.res_k > 0 &&
                              in.res_k % 128 == 0 && in.res_k / 128 <= kPhiMaxGroups),
                  "attention: the Sinkhorn workgroups need the residual-mix phi rows (K %d)", in.res_k);
-    hipLaunchKernelGGL(decode_attention_row_kernel<kRowNeedle3>, dim3(rows, heads + (in.mix ? 1 : 0)),
+    int gate_cols = 0;
+    if (in.proj.codes[0]) {
+        const Needle3Proj& q = in.proj;
+        NHIP_REQUIRE(q.codes[1] && q.codes[2] && q.codes[3] && q.norms[0] && q.norms[1] && q.norms[2] && q.norms[3] &&
+                         q.act && q.scales && q.offsets && q.raw && q.gate,
+                     "attention: null projection pointer");
+        NHIP_REQUIRE(rows <= 16 && q.k > 0 && q.k % 128 == 0 && q.k <= 1024 && q.gate_rows > 0 &&
+                         q.gate_rows % 16 == 0 && (2 * qk_dim + 64) * (q.k / 128) <= 3 * row_threads(kRowNeedle3),
+                     "attention: projections of %d rows, K %d, %d gate rows", rows, q.k, q.gate_rows);
+        gate_cols = (q.gate_rows / 16 + rows - 1) / rows;
+    }
+    hipLaunchKernelGGL(decode_attention_row_kernel<kRowNeedle3>, dim3(rows, heads + (in.mix ? 1 : 0) + gate_cols),
                        dim3(row_threads(kRowNeedle3)), 0, stream, ATTN_HEAD_ARGS(p, p.n3.raw, p.positions), p);
     NHIP_CHECK_HIP(hipGetLastError());
     return NHIP_OK;

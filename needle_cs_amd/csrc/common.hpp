@@ -222,6 +222,27 @@ struct PhiUnit {
     uint32_t norm;
 };
 
+// The step's Q/K/V/Gate projections formed inside the attention launch (when
+// codes[0] is set), instead of read from a matmul's output: each (row, query
+// head) workgroup forms its query head and its kv head's key and value heads
+// (Scalar.MatMulRows over the row's 2-bit prepared activations and the
+// records' row-major codes and fp16 norms) and stores them into raw (the key
+// and value heads once per kv head, for the Q/K/V history move); gate_rows /
+// 16 more workgroups form 16 Gate outputs each for every row.
+struct Needle3Proj {
+    const uint8_t* codes[4];   // Q, K, V, Gate records: [rows_m][k / 4] 2-bit codes
+    const uint16_t* norms[4];  // [rows_m][k / 128]
+    uint32_t table;            // the 2-bit codebook's four level bytes
+    float byte_scale;
+    const int8_t* act;         // [rows][k] prepared activations (Quant.Prepare, 2-bit planes)
+    const float* scales;       // [rows][stride]
+    const float* offsets;
+    int stride, k;
+    float* raw;                // [rows][qw + kw + vw]
+    float* gate;               // [rows][gate_rows]
+    int gate_rows;
+};
+
 struct Needle3AttnInputs {
     const float* raw;       // [rows][qw + kw + vw]
     const float* taps[3];   // query, key, value taps: [3][width] each
@@ -239,6 +260,7 @@ struct Needle3AttnInputs {
     int res_k;
     const float* a_res;  // [1]
     const float* b_res;  // [16]
+    Needle3Proj proj;
 };
 // Whether attention_decode_needle3_impl takes a step (caches of at most 512
 // positions, value heads of 64).

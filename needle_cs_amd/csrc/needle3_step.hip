@@ -1274,6 +1274,7 @@ struct N3Layer {
     nhip_weights *q = nullptr, *k = nullptr, *v = nullptr, *gate = nullptr, *out = nullptr;
     nhip_weights* qkvg = nullptr;  // Q, K, V and Gate stacked by rows (the context's own)
     const uint8_t* out_raw = nullptr;  // Out's archive bytes on the device: row-major codes, then the norms
+    const uint8_t* qkvg_raw[4] = {};   // Q, K, V and Gate's, the same way
     float attn_gate = 0.0f;
     const float *d1 = nullptr, *d2 = nullptr, *b2 = nullptr, *d3 = nullptr, *d4 = nullptr, *w1a = nullptr,
                 *w1b = nullptr, *w2a = nullptr, *w2b = nullptr, *w3a = nullptr, *w3b = nullptr, *cond_v = nullptr,
@@ -1578,6 +1579,7 @@ int32_t load_model(nhip_ctx* c)
         w.gate = r.quant(2, ow, d, "Gate");
         qkvg_records[3] = r.last;
         if (!r.status && (rc = stack_rows(c, qkvg_records, 4, &w.qkvg))) return rc;
+        for (int m = 0; m < 4 && !r.status; m++) w.qkvg_raw[m] = nhip_model_raw(c->model, qkvg_records[m]);
         w.out = r.quant(2, d, ow, "Out");
         w.out_raw = r.status ? nullptr : nhip_model_raw(c->model, r.last);
         w.post_norm = r.dense(d, "PostNorm");
@@ -1876,15 +1878,31 @@ int32_t enqueue_step(nhip_ctx* c, int rows, int heads, int k, bool argmax, bool 
             hipLaunchKernelGGL(n3_engram_mix_kernel, dim3(rows), dim3(kThreads), 0, s, ea);
             NHIP_CHECK_HIP(hipGetLastError());
         }
-        // attention (RunAttentionBatch, Engine.cs:2480-2596)
-        const nhip_weights* pw[4] = {w.q, w.k, w.v, w.gate};
-        float* py[4] = {c->raw, c->raw + qw, c->raw + qw + kw, c->gate};
-        const int32_t pl[4] = {all, all, all, ow};
-        const int32_t pf[4] = {0, qw, qw + kw, qw + kw + vw};
-        // one launch over the stacked matrix up to 4 rows; MatMulBatch beyond
-        rc = matmul_cq_split_internal(w.qkvg, c->act_v, c->act_s, c->act_o, stride_d, rows, py, pl, pf, 4, s);
-        if (rc < 0) return rc;
-        if (rc && (rc = nhip_matmul_batch_dev(pw, 4, c->act_v, c->act_s, c->act_o, stride_d, rows, py, pl, s))) return rc;
+        // attention (RunAttentionBatch, Engine.cs:2480-2596).  For steps of 5
+        // to 16 rows whose attention launch forms Sinkhorn (rows one per
+        // slot), it forms the Q/K/V/Gate projections too (each workgroup its
+        // heads' rows, more workgroups the Gate's; Needle3Proj): that costs
+        // the attention about as much as the 1-4-row matmul launch but less
+        // than MatMulBatch.  NHIP_N3_ATTN_PROJ=0 keeps the matmul launch (for
+        // A/B timing)
+        static const bool attn_proj_enabled = [] {
+            const char* e = getenv("NHIP_N3_ATTN_PROJ");
+            return !(e && e[0] == '0');
+        }();
+        const bool proj_in_attention = attn_proj_enabled && sink_in_attention && rows > 4 && rows <= 16 &&
+                                       w.qkvg_raw[0] && w.qkvg_raw[1] && w.qkvg_raw[2] && w.qkvg_raw[3] &&
+                                       (2 * c->qk + 64) * (d / 128) <= 3 * 512;
+        if (!proj_in_attention) {
+            const nhip_weights* pw[4] = {w.q, w.k, w.v, w.gate};
+            float* py[4] = {c->raw, c->raw + qw, c->raw + qw + kw, c->gate};
+            const int32_t pl[4] = {all, all, all, ow};
+            const int32_t pf[4] = {0, qw, qw + kw, qw + kw + vw};
+            // one launch over the stacked matrix up to 4 rows; MatMulBatch beyond
+            rc = matmul_cq_split_internal(w.qkvg, c->act_v, c->act_s, c->act_o, stride_d, rows, py, pl, pf, 4, s);
+            if (rc < 0) return rc;
+            if (rc && (rc = nhip_matmul_batch_dev(pw, 4, c->act_v, c->act_s, c->act_o, stride_d, rows, py, pl, s)))
+                return rc;
+        }
         const size_t lcell = (size_t)l * c->slots * c->capacity;
         int8_t* keys = c->keys + lcell * kw;
         int8_t* values = c->values + lcell * vw;
@@ -1903,7 +1921,7 @@ int32_t enqueue_step(nhip_ctx* c, int rows, int heads, int k, bool argmax, bool 
             // with the Sinkhorn: the layer's residual-mix phi rows over the
             // stream's 4-bit prepared rows
             const HyperArgs hl = hyper_args(l, cur);
-            const Needle3AttnInputs n3in{c->raw,
+            Needle3AttnInputs n3in{c->raw,
                                          {w.q_taps, w.k_taps, w.v_taps},
                                          w.q_norm,
                                          w.k_norm,
@@ -1915,6 +1933,24 @@ int32_t enqueue_step(nhip_ctx* c, int rows, int heads, int k, bool argmax, bool 
                                          sw,
                                          hl.a_res,
                                          hl.b_res};
+            if (proj_in_attention) {
+                const int prow[4] = {qw, kw, vw, ow};
+                Needle3Proj& pj = n3in.proj;
+                for (int m = 0; m < 4; m++) {
+                    pj.codes[m] = w.qkvg_raw[m];
+                    pj.norms[m] = reinterpret_cast<const uint16_t*>(w.qkvg_raw[m] + (size_t)prow[m] * (d / 4));
+                }
+                pj.table = w.q->table[0];
+                pj.byte_scale = w.q->byte_scale;
+                pj.act = c->act_v;
+                pj.scales = c->act_s;
+                pj.offsets = c->act_o;
+                pj.stride = stride_d;
+                pj.k = d;
+                pj.raw = c->raw;
+                pj.gate = c->gate;
+                pj.gate_rows = ow;
+            }
             fused = attention_decode_needle3_impl(n3in, rows, H, KV, c->qk, c->vd, keys, kscale, values, vscale,
                                                   c->slots, c->capacity, in(c, c->d_in, kInSlots),
                                                   in(c, c->d_in, kInPos), first, count, c->max_chunks, c->att, s);
