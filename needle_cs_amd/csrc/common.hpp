@@ -821,12 +821,14 @@ __device__ __forceinline__ global_ptr<T> scalar_ptr(const T* p)
 
 // first[m] is the first output of matrix m (outputs first[m] .. first[m + 1]
 // - 1 read its rows 0, 1, ...).
-__device__ __forceinline__ PhiUnit phi_load(const PhiRows& p, int K, int m0, const int (&first)[4])
+// base: thread base + u takes unit u (keeping the units' address work off
+// waves that have other work first).
+__device__ __forceinline__ PhiUnit phi_load(const PhiRows& p, int K, int m0, const int (&first)[4], int base = 0)
 {
     PhiUnit r{};
     const int groups = K / 128, outputs = first[3] - first[0];
-    const int u = threadIdx.x;
-    if (u < outputs * groups) {
+    const int u = (int)threadIdx.x - base;
+    if (u >= 0 && u < outputs * groups) {
         const int o = u / groups, g = u - o * groups;
         const int m = m0 + (o >= first[1] - first[0]) + (o >= first[2] - first[0]);
         const int row = o + first[0] - first[m - m0];
@@ -857,11 +859,11 @@ __device__ __forceinline__ PhiUnit phi_load(const PhiRows& p, int K, int m0, con
 // scaled * offset) and returns accumulator - bias (other lanes return 0).
 __device__ __forceinline__ float phi_outputs(const PhiRows& p, const PhiUnit& unit, const int8_t* x,
                                              const float* scales, const float* offsets, int K,
-                                             const int (&first)[4], float* prod)
+                                             const int (&first)[4], float* prod, int base = 0)
 {
     const int groups = K / 128, outputs = first[3] - first[0];
-    const int u = threadIdx.x;
-    if (u < outputs * groups) {
+    const int u = (int)threadIdx.x - base;  // phi_load's base
+    if (u >= 0 && u < outputs * groups) {
         const int g = u % groups;
         const float scaled = ref_half_to_single(unit.norm) * p.byte_scale * scales[g];
         const int dot = cq4_group_dot(unit.w, x + g * 128, p.split);

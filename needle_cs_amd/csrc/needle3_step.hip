@@ -1188,10 +1188,11 @@ __global__ __launch_bounds__(kThreads) void n3_tail_kernel(const float* h_proj, 
     // forms the 16 residual-mix ones); their codes and affine maps load under
     // the next layer's RmsFakeA8 and Prepare
     constexpr int kPhiFirst[4] = {0, 4, 8, 8};
+    constexpr int kPhiBase = 8 * 64;  // waves 8.. take the units: wave 0 sums the squares first
     PhiUnit hunit{};
     float hga = 0.0f, hgb = 0.0f;
     if constexpr (HYPER) {
-        hunit = phi_load(h.phi, n4, 0, kPhiFirst);
+        hunit = phi_load(h.phi, n4, 0, kPhiFirst, kPhiBase);
         phi_affine(h, hga, hgb);
     }
     if (!a.head_of) {  // the next layer's RmsFakeA8 and 4-bit Prepare
@@ -1228,7 +1229,7 @@ __global__ __launch_bounds__(kThreads) void n3_tail_kernel(const float* h_proj, 
                 float* dst = threadIdx.x < g4 ? a.act.scales : a.act.offsets;
                 dst[(size_t)t * a.stride + g] = a4s[threadIdx.x];
             }
-            const float y = phi_outputs(h.phi, hunit, a4v, a4s, a4s + g4, n4, kPhiFirst, hprod);
+            const float y = phi_outputs(h.phi, hunit, a4v, a4s, a4s + g4, n4, kPhiFirst, hprod, kPhiBase);
             __shared__ float hpre[4];
             hyper_mix_row(h, t, y, hga, hgb, nsv, hsn, hx, hsq, hpre, red, &inv_s);
         } else {
