@@ -563,29 +563,43 @@ __device__ __forceinline__ void engram_hist_move(const EngramArgs& e, int t)
 __global__ __launch_bounds__(kThreads) void n3_gate_kernel(const float* att, const float* gate, int n, Act act,
                                                            int stride, EngramArgs e, QkvHistArgs h)
 {
-    __shared__ __align__(16) float x[kMaxDim];
-    __shared__ float red[kWaves];
+    __shared__ float peak_g[kMaxDim / 128];
     const int t = blockIdx.x;
-    // the history's loads go out with the row's own
+    const int lane = threadIdx.x & 63;
+    const int g = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);  // wave g takes group g
+    const int groups = n >> 7;
+    // lane e holds elements e and e + 64 of the group, as hadamard_wave wants
+    // them; the history's loads go out with the row's own
+    float x0 = 0.0f, x1 = 0.0f, s0 = 0.0f, s1 = 0.0f;
+    if (g < groups) {
+        const size_t at = (size_t)t * n + g * 128 + lane;
+        x0 = att[at];
+        x1 = att[at + 64];
+        s0 = gate[at];
+        s1 = gate[at + 64];
+    }
     float hv0[kHistPer], hv1[kHistPer];
     const bool hist_end = qkv_hist_load(h, t, hv0, hv1);
-    float av[kPer], gv[kPer];
-#pragma unroll
-    for (int q = 0; q < kPer; q++) {
-        const int c = col_of(q);
-        if (c < n) {
-            av[q] = att[(size_t)t * n + c];
-            gv[q] = gate[(size_t)t * n + c];
-        }
-    }
-#pragma unroll
-    for (int q = 0; q < kPer; q++) {
-        const int c = col_of(q);
-        if (c < n) x[c] = av[q] * sigmoid_poly(gv[q]);
+    if (g < groups) {
+        x0 = x0 * sigmoid_poly(s0);
+        x1 = x1 * sigmoid_poly(s1);
+        const float m = wave_max(fmaxf(fabsf(x0), fabsf(x1)));
+        if (lane == 0) peak_g[g] = m;
     }
     __syncthreads();
-    fake_row(x, n, red);
-    prepare_row(x, n, 2, act, stride, t);
+    if (g < groups) {
+        // Quant.FakeA8 at the row's peak (the maximum of the groups' maxima),
+        // then the group's Hadamard and Prepare
+        float peak = 0.0f;
+        for (int j = 0; j < groups; j++) peak = fmaxf(peak, peak_g[j]);
+        const float scale = peak > 0.0f ? peak / 127.0f : 1.0f;
+        const float round = 1.0f / scale;
+        float v0 = clamp_q(x0 * round) * scale;
+        float v1 = clamp_q(x1 * round) * scale;
+        hadamard_wave(v0, v1);
+        prepare_group_wave(v0, v1, 2, act.values + (size_t)t * n + g * 128, act.scales + (size_t)t * stride + g,
+                           act.offsets + (size_t)t * stride + g);
+    }
     if (hist_end) qkv_hist_store(h, t, hv0, hv1);
     engram_hist_move(e, t);
 }
