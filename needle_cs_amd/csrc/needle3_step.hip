@@ -113,6 +113,22 @@ __device__ __forceinline__ void prepare_row(const float* v, int cols, int bits, 
     }
 }
 
+// prepare_row of the row that RmsUnit and Quant.FakeA8 make of the LDS row
+// v: element i is clamp(RoundEven((v[i] * inverse) * round)) * scale, formed
+// by the wave that prepares its group (no pass and barrier of its own).
+__device__ __forceinline__ void prepare_row_fake(const float* v, int cols, int bits, const Act& act, int stride, int t,
+                                                 float inverse, float round, float scale)
+{
+    const int lane = threadIdx.x & 63;
+    for (int g = threadIdx.x >> 6; g < cols / 128; g += kWaves) {
+        float v0 = clamp_q((v[g * 128 + lane] * inverse) * round) * scale;
+        float v1 = clamp_q((v[g * 128 + 64 + lane] * inverse) * round) * scale;
+        hadamard_wave(v0, v1);
+        prepare_group_wave(v0, v1, bits, act.values + (size_t)t * cols + g * 128, act.scales + (size_t)t * stride + g,
+                           act.offsets + (size_t)t * stride + g);
+    }
+}
+
 // Ops.InverseRms of an LDS row x[0..n) (written before the call and
 // synchronised), its sum of squares in the AVX2 tier's order by wave 0.
 __device__ __forceinline__ float row_inverse_rms(const float* x, int n, float* slot)
@@ -249,8 +265,8 @@ __device__ __forceinline__ void phi_affine(const HyperArgs& a, float& ga, float&
 // Prepare (RunLayerBatch, Engine.cs:2356-2414).  The attention input's
 // FakeA8 peak is taken with the mix, before the norm: with v = (1 + s) * u
 // and inverse > 0, max |v * inverse| is RoundNearest(max |v| * inverse), as
-// rounding is monotone, so the scaling and the int8 round trip run in one
-// pass after the sum of squares.
+// rounding is monotone, so the scaling and the int8 round trip run inside
+// the Prepare waves after the sum of squares.
 __device__ __forceinline__ void hyper_mix_row(const HyperArgs& a, int t, float y, float ga, float gb,
                                               const float (&sv)[kPer][kLanes], const float (&sn)[kPer], float* x,
                                               float* sq, float* hpre, float* red, float* inv_s)
@@ -260,7 +276,7 @@ __device__ __forceinline__ void hyper_mix_row(const HyperArgs& a, int t, float y
     if (i < 4) hpre[i] = sigmoid_poly(ga * y + gb + (i == a.lane ? 4.0f : -4.0f));
     if (i >= 4 && i < 8) a.post_gate[t * 4 + i - 4] = 2.0f * sigmoid_poly(ga * y + gb + (i - 4 == a.lane ? 0.0f : -4.0f));
     __syncthreads();
-    float uv[kPer], peak = 0.0f;
+    float peak = 0.0f;
 #pragma unroll
     for (int q = 0; q < kPer; q++) {
         const int c = col_of(q);
@@ -269,8 +285,9 @@ __device__ __forceinline__ void hyper_mix_row(const HyperArgs& a, int t, float y
             a.input[(size_t)t * dim + c] = u;
             a.residual[(size_t)t * dim + c] = u;
             x[c] = u;
-            uv[q] = u;
-            peak = fmaxf(peak, fabsf((1.0f + sn[q]) * u));
+            const float v = (1.0f + sn[q]) * u;
+            sq[c] = v;  // the scaled row, for the Prepare waves (sq serves the engram input otherwise)
+            peak = fmaxf(peak, fabsf(v));
         }
     }
     if (!a.tables) {
@@ -299,13 +316,7 @@ __device__ __forceinline__ void hyper_mix_row(const HyperArgs& a, int t, float y
     const float top = m * inverse;
     const float scale = top > 0.0f ? top / 127.0f : 1.0f;
     const float round = 1.0f / scale;
-#pragma unroll
-    for (int q = 0; q < kPer; q++) {
-        const int c = col_of(q);
-        if (c < dim) x[c] = clamp_q(((1.0f + sn[q]) * uv[q] * inverse) * round) * scale;
-    }
-    __syncthreads();
-    prepare_row(x, dim, 2, a.act, a.stride, t);
+    prepare_row_fake(sq, dim, 2, a.act, a.stride, t, inverse, round, scale);
 }
 
 // RunLayerBatch's per-row mix (Engine.cs:2356-2381): the phi rows, hpre /
@@ -1213,7 +1224,8 @@ __global__ __launch_bounds__(kThreads) void n3_tail_kernel(const float* h_proj, 
         // RmsUnit then FakeA8 with one barrier: the peak of x * inverse is
         // RoundNearest(max |x| * inverse) (inverse > 0 and rounding is
         // monotone), so the row's max |x| is taken with the squares, before
-        // the chain, and the scaling and the int8 round trip run in one pass
+        // the chain, and the scaling and the int8 round trip run inside the
+        // Prepare waves
         float peak_x = 0.0f;
         for (int c = threadIdx.x; c < n4; c += kThreads) peak_x = fmaxf(peak_x, fabsf(ns[c]));
         peak_x = wave_max(peak_x);
@@ -1229,10 +1241,8 @@ __global__ __launch_bounds__(kThreads) void n3_tail_kernel(const float* h_proj, 
         const float peak = m * inverse;
         const float scale = peak > 0.0f ? peak / 127.0f : 1.0f;
         const float round = 1.0f / scale;
-        for (int c = threadIdx.x; c < n4; c += kThreads) ns[c] = clamp_q((ns[c] * inverse) * round) * scale;
-        __syncthreads();
         if constexpr (HYPER) {
-            prepare_row(ns, n4, 4, Act{a4v, a4s, a4s + g4}, 0, 0);
+            prepare_row_fake(ns, n4, 4, Act{a4v, a4s, a4s + g4}, 0, 0, inverse, round, scale);
             __syncthreads();
             // and into the row's global copy, which layer l + 1's attention
             // launch reads for the residual-mix logits
@@ -1247,7 +1257,7 @@ __global__ __launch_bounds__(kThreads) void n3_tail_kernel(const float* h_proj, 
             __shared__ float hpre[4];
             hyper_mix_row(h, t, y, hga, hgb, nsv, hsn, hx, hsq, hpre, red, &inv_s);
         } else {
-            prepare_row(ns, n4, 4, a.act, a.stride, t);
+            prepare_row_fake(ns, n4, 4, a.act, a.stride, t, inverse, round, scale);
         }
         return;
     }
