@@ -296,18 +296,31 @@ __device__ __forceinline__ void hyper_mix_row(const HyperArgs& a, int t, float y
     }
     __syncthreads();
     if (a.tables) {
-        const int sub = a.table_cols, per = sub / 128;
-        for (int unit = i >> 6; unit < a.tables_count * per; unit += kWaves) {
+        // wave u gathers group u of the row (table u / per, its group u %
+        // per; dim <= 1024: at most 8 groups) in the Hadamard's lane layout,
+        // then FakeA8 at the row's peak, Hadamard and Prepare from registers
+        const int sub = a.table_cols, per = sub / 128, units = a.tables_count * per;
+        const int unit = i >> 6;
+        float v0 = 0.0f, v1 = 0.0f;
+        if (unit < units) {
             const int table = unit / per, g = unit % per;
             const int r = a.erows[t * a.tables_count + table];
-            float v0 = 0.0f, v1 = 0.0f;
             if (r >= 0) gather_group_wave(a.tables, a.table_rows, sub, a.table_bits, a.book, r, g, v0, v1);
-            sq[table * sub + g * 128 + (i & 63)] = v0;
-            sq[table * sub + g * 128 + 64 + (i & 63)] = v1;
+            const float m = wave_max(fmaxf(fabsf(v0), fabsf(v1)));
+            if ((i & 63) == 0) red[unit] = m;
         }
         __syncthreads();
-        fake_row(sq, dim, red);
-        prepare_row(sq, dim, 2, a.act, a.stride, t);
+        if (unit < units) {
+            float m = 0.0f;
+            for (int j = 0; j < units; j++) m = fmaxf(m, red[j]);
+            const float scale = m > 0.0f ? m / 127.0f : 1.0f;
+            const float round = 1.0f / scale;
+            v0 = clamp_q(v0 * round) * scale;
+            v1 = clamp_q(v1 * round) * scale;
+            hadamard_wave(v0, v1);
+            prepare_group_wave(v0, v1, 2, a.act.values + (size_t)t * dim + unit * 128,
+                               a.act.scales + (size_t)t * a.stride + unit, a.act.offsets + (size_t)t * a.stride + unit);
+        }
         return;
     }
     const float inverse = row_inverse_rms(x, dim, inv_s);
@@ -472,6 +485,11 @@ __global__ __launch_bounds__(kThreads) void n3_engram_mix_kernel(EngramArgs a)
     }
     __syncthreads();
     const float alpha = alpha_s;
+    // the attention norm's FakeA8 peak with the residual (the scaled row
+    // (1 + s) * r into ub, whose dot is done): max |v * inverse| is
+    // RoundNearest(max |v| * inverse), so the Prepare waves form the int8
+    // round trip themselves
+    float peak = 0.0f;
 #pragma unroll
     for (int q = 0; q < kPer; q++) {
         const int c = col_of(q);
@@ -479,18 +497,21 @@ __global__ __launch_bounds__(kThreads) void n3_engram_mix_kernel(EngramArgs a)
             const float r = rv[q] + alpha * cv[q];
             a.residual[(size_t)t * dim + c] = r;
             ua[c] = r;
+            const float v = (1.0f + sn[q]) * r;
+            ub[c] = v;
+            peak = fmaxf(peak, fabsf(v));
         }
     }
+    peak = wave_max(peak);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = peak;
     __syncthreads();
     const float inverse = row_inverse_rms(ua, dim, &inv[0]);
-#pragma unroll
-    for (int q = 0; q < kPer; q++) {
-        const int c = col_of(q);
-        if (c < dim) ua[c] = (1.0f + sn[q]) * ua[c] * inverse;
-    }
-    __syncthreads();
-    fake_row(ua, dim, red);
-    prepare_row(ua, dim, 2, a.act, a.stride, t);
+    float m = red[0];
+    for (int w = 1; w < kWaves; w++) m = fmaxf(m, red[w]);
+    const float top = m * inverse;
+    const float scale = top > 0.0f ? top / 127.0f : 1.0f;
+    const float round = 1.0f / scale;
+    prepare_row_fake(ub, dim, 2, a.act, a.stride, t, inverse, round, scale);
 }
 
 // ------------------------------------------------- attention epilogue --
