@@ -74,32 +74,6 @@ __device__ __forceinline__ int col_of(int q) { return (int)threadIdx.x + kThread
 // Ops.InverseRms of a sum of squares over n elements
 __device__ __forceinline__ float inverse_rms_of(float sum, int n) { return 1.0f / sqrtf(sum / (float)n + 1e-6f); }
 
-// Maximum of |v| over the block (order-free).
-__device__ __forceinline__ float block_peak(float v, float* red)
-{
-    v = wave_max(v);
-    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
-    __syncthreads();
-    float m = red[0];
-    for (int w = 1; w < kWaves; w++) m = fmaxf(m, red[w]);
-    __syncthreads();
-    return m;
-}
-
-// The int8 round trip of the fused norms and of Quant.FakeA8 on an LDS row
-// d[0..n): peak = max |d|, scale = peak > 0 ? peak / 127 : 1, then
-// d = clamp(RoundEven(d * (1 / scale))) * scale (Scalar.cs:55-65).
-__device__ __forceinline__ void fake_row(float* d, int n, float* red)
-{
-    float peak = 0.0f;
-    for (int c = threadIdx.x; c < n; c += kThreads) peak = fmaxf(peak, fabsf(d[c]));
-    peak = block_peak(peak, red);
-    const float scale = peak > 0.0f ? peak / 127.0f : 1.0f;
-    const float round = 1.0f / scale;
-    for (int c = threadIdx.x; c < n; c += kThreads) d[c] = clamp_q(d[c] * round) * scale;
-    __syncthreads();
-}
-
 // Quant.Prepare (Quant.cs:473-488) of an LDS row of `cols` floats into row t
 // of act: wave w takes groups w, w + 4, ...
 __device__ __forceinline__ void prepare_row(const float* v, int cols, int bits, const Act& act, int stride, int t)
@@ -115,7 +89,10 @@ __device__ __forceinline__ void prepare_row(const float* v, int cols, int bits, 
 
 // prepare_row of the row that RmsUnit and Quant.FakeA8 make of the LDS row
 // v: element i is clamp(RoundEven((v[i] * inverse) * round)) * scale, formed
-// by the wave that prepares its group (no pass and barrier of its own).
+// by the wave that prepares its group (no pass and barrier of its own).  The
+// caller takes FakeA8's scale = peak > 0 ? peak / 127 : 1 and round =
+// 1 / scale (Scalar.cs:55-65) from the row's peak of v * inverse, which is
+// RoundNearest(max |v| * inverse) since inverse > 0 and rounding is monotone.
 __device__ __forceinline__ void prepare_row_fake(const float* v, int cols, int bits, const Act& act, int stride, int t,
                                                  float inverse, float round, float scale)
 {
@@ -209,14 +186,21 @@ __global__ __launch_bounds__(kThreads) void n3_embed_kernel(const uint8_t* raw, 
             s[c] = x0;
             s[c + 64] = x1;
         }
+        // the group's peak (dim <= 1024: one group a wave, at most 8)
+        const float m = wave_max(fmaxf(fabsf(x0), fabsf(x1)));
+        if (lane == 0) red[g] = m;
     }
     __syncthreads();
     const int n = kLanes * dim;
     const float inverse = row_inverse_rms(s, n, &inv_s);
-    for (int c = threadIdx.x; c < n; c += kThreads) s[c] = s[c] * inverse;
-    __syncthreads();
-    fake_row(s, n, red);
-    prepare_row(s, n, 4, act, stride, t);
+    // RmsUnit then FakeA8: the peak of x * inverse is RoundNearest(max |x| *
+    // inverse), so the Prepare waves form the scaled, int8 round-tripped row
+    float m = 0.0f;
+    for (int g = 0; g < dim / 128; g++) m = fmaxf(m, red[g]);
+    const float top = m * inverse;
+    const float scale = top > 0.0f ? top / 127.0f : 1.0f;
+    const float round = 1.0f / scale;
+    prepare_row_fake(s, n, 4, act, stride, t, inverse, round, scale);
 }
 
 // ----------------------------------------------- hyper-connection mix --
@@ -1284,25 +1268,31 @@ __global__ __launch_bounds__(kThreads) void n3_tail_kernel(const float* h_proj, 
     }
     const int head = a.head_of[t];
     if (head < 0) return;
-    float fv[kPer];
+    // the scaled row (1 + s) * x into res with its peak: FakeA8's peak of
+    // v * inverse is RoundNearest(max |v| * inverse), so the Prepare waves
+    // form the int8 round trip themselves
+    float peak_h = 0.0f;
 #pragma unroll
     for (int q = 0; q < kPer; q++) {
         const int c = col_of(q);
         if (c < dim) {
-            fv[q] = a.final_norm[c];
-            norm[c] = 0.25f * ns[c] + 0.25f * ns[dim + c] + 0.25f * ns[2 * dim + c] + 0.25f * ns[3 * dim + c];
+            const float x = 0.25f * ns[c] + 0.25f * ns[dim + c] + 0.25f * ns[2 * dim + c] + 0.25f * ns[3 * dim + c];
+            norm[c] = x;
+            const float v = (1.0f + a.final_norm[c]) * x;
+            res[c] = v;
+            peak_h = fmaxf(peak_h, fabsf(v));
         }
     }
+    peak_h = wave_max(peak_h);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = peak_h;
     __syncthreads();
     inverse = row_inverse_rms(norm, dim, &inv_s);
-#pragma unroll
-    for (int q = 0; q < kPer; q++) {
-        const int c = col_of(q);
-        if (c < dim) norm[c] = (1.0f + fv[q]) * norm[c] * inverse;
-    }
-    __syncthreads();
-    fake_row(norm, dim, red);
-    prepare_row(norm, dim, 4, a.act, a.stride, head);
+    float m = red[0];
+    for (int w = 1; w < kWaves; w++) m = fmaxf(m, red[w]);
+    const float top = m * inverse;
+    const float scale = top > 0.0f ? top / 127.0f : 1.0f;
+    const float round = 1.0f / scale;
+    prepare_row_fake(res, dim, 4, a.act, a.stride, head, inverse, round, scale);
 }
 
 }  // namespace
