@@ -1132,7 +1132,9 @@ __global__ __launch_bounds__(kThreads) void n3_tail_kernel(const float* h_proj, 
             int_[(c & 3) * cs + (c >> 2)] = v;
         }
     }
-    __syncthreads();
+    // no barrier: what follows writes CondV and the Kronecker factors from
+    // registers and the first product's input from the thread's own norm[c];
+    // int_ is read after the next one
 #pragma unroll
     for (int q = 0; q < kCondPer; q++) {  // CondV for the condition weights
         const int e = col_of(q);
