@@ -161,47 +161,6 @@ __device__ __forceinline__ void gather_group_wave(const uint8_t* raw, int rows, 
     hadamard_wave(v0, v1);
 }
 
-// Embedding (ForwardBatch, Engine.cs:2310-2316): GatherRow of the token's
-// row, x += (sqrt(dim) - 1) * x, copied to the four lanes of the stream; then
-// the first layer's RmsFakeA8 of the stream and its 4-bit Prepare.
-__global__ __launch_bounds__(kThreads) void n3_embed_kernel(const uint8_t* raw, int rows, int dim, int bits, Book book,
-                                                            const int32_t* tokens, float scale_m1, float* stream,
-                                                            Act act, int stride)
-{
-    __shared__ __align__(16) float s[kMaxStream];
-    __shared__ float red[kWaves];
-    __shared__ float inv_s;
-    const int t = blockIdx.x;
-    const int lane = threadIdx.x & 63;
-    const int token = tokens[t];
-    float* row = stream + (size_t)t * kLanes * dim;
-    for (int g = threadIdx.x >> 6; g < dim / 128; g += kWaves) {
-        float v0, v1;
-        gather_group_wave(raw, rows, dim, bits, book, token, g, v0, v1);
-        const float x0 = v0 + scale_m1 * v0, x1 = v1 + scale_m1 * v1;
-        for (int l = 0; l < kLanes; l++) {
-            const int c = l * dim + g * 128 + lane;
-            row[c] = x0;
-            row[c + 64] = x1;
-            s[c] = x0;
-            s[c + 64] = x1;
-        }
-        // the group's peak (dim <= 1024: one group a wave, at most 8)
-        const float m = wave_max(fmaxf(fabsf(x0), fabsf(x1)));
-        if (lane == 0) red[g] = m;
-    }
-    __syncthreads();
-    const int n = kLanes * dim;
-    const float inverse = row_inverse_rms(s, n, &inv_s);
-    // RmsUnit then FakeA8: the peak of x * inverse is RoundNearest(max |x| *
-    // inverse), so the Prepare waves form the scaled, int8 round-tripped row
-    float m = 0.0f;
-    for (int g = 0; g < dim / 128; g++) m = fmaxf(m, red[g]);
-    const float top = m * inverse;
-    const float scale = top > 0.0f ? top / 127.0f : 1.0f;
-    const float round = 1.0f / scale;
-    prepare_row_fake(s, n, 4, act, stride, t, inverse, round, scale);
-}
 
 // ----------------------------------------------- hyper-connection mix --
 
@@ -370,6 +329,96 @@ __global__ __launch_bounds__(kThreads) void n3_hyper_kernel(HyperArgs a)
                                 a.phi.in.scales + (size_t)t * a.phi.stride, a.phi.in.offsets + (size_t)t * a.phi.stride,
                                 K, first, prod);
     hyper_mix_row(a, t, y, ga, gb, sv, sn, x, sq, hpre, red, &inv_s);
+}
+
+// Embedding (ForwardBatch, Engine.cs:2310-2316): GatherRow of the token's
+// row, x += (sqrt(dim) - 1) * x, copied to the four lanes of the stream; then
+// the first layer's RmsFakeA8 of the stream and its 4-bit Prepare.
+// HYPER: for a decode step (rows one per slot), the workgroup goes on into
+// layer 0's mix (h, as n3_tail_kernel<true> does for later layers): the
+// stream row stays in LDS and its 4-bit prepared activations too, with a copy
+// in act for the attention launch's residual-mix rows.
+template <bool HYPER>
+__global__ __launch_bounds__(kThreads) void n3_embed_kernel(const uint8_t* raw, int rows, int dim, int bits, Book book,
+                                                            const int32_t* tokens, float scale_m1, float* stream,
+                                                            Act act, int stride, HyperArgs h)
+{
+    __shared__ __align__(16) float s[kMaxStream];
+    __shared__ float red[kWaves];
+    __shared__ float inv_s;
+    __shared__ __align__(16) int8_t a4v[HYPER ? kMaxStream : 16];
+    __shared__ __align__(16) float a4s[HYPER ? 2 * kMaxPhiGroups : 4];
+    __shared__ __align__(16) float hprod[HYPER ? 2 * 8 * kMaxPhiGroups : 4];
+    __shared__ __align__(16) float hx[HYPER ? kMaxDim : 4];
+    __shared__ __align__(16) float hsq[HYPER ? kMaxDim : 4];
+    __shared__ float hpre[4];
+    constexpr int kPhiFirst[4] = {0, 4, 8, 8};
+    constexpr int kPhiBase = 8 * 64;  // waves 8.. take the phi units
+    PhiUnit hunit{};
+    float hga = 0.0f, hgb = 0.0f, hsn[kPer];
+    if constexpr (HYPER) {
+        hunit = phi_load(h.phi, kLanes * dim, 0, kPhiFirst, kPhiBase);
+        phi_affine(h, hga, hgb);
+#pragma unroll
+        for (int q = 0; q < kPer; q++) {
+            const int c = col_of(q);
+            if (c < dim) hsn[q] = h.norm_in[c];
+        }
+    }
+    const int t = blockIdx.x;
+    const int lane = threadIdx.x & 63;
+    const int token = tokens[t];
+    float* row = stream + (size_t)t * kLanes * dim;
+    for (int g = threadIdx.x >> 6; g < dim / 128; g += kWaves) {
+        float v0, v1;
+        gather_group_wave(raw, rows, dim, bits, book, token, g, v0, v1);
+        const float x0 = v0 + scale_m1 * v0, x1 = v1 + scale_m1 * v1;
+        for (int l = 0; l < kLanes; l++) {
+            const int c = l * dim + g * 128 + lane;
+            row[c] = x0;
+            row[c + 64] = x1;
+            s[c] = x0;
+            s[c + 64] = x1;
+        }
+        // the group's peak (dim <= 1024: one group a wave, at most 8)
+        const float m = wave_max(fmaxf(fabsf(x0), fabsf(x1)));
+        if (lane == 0) red[g] = m;
+    }
+    __syncthreads();
+    const int n = kLanes * dim;
+    const float inverse = row_inverse_rms(s, n, &inv_s);
+    // RmsUnit then FakeA8: the peak of x * inverse is RoundNearest(max |x| *
+    // inverse), so the Prepare waves form the scaled, int8 round-tripped row
+    float m = 0.0f;
+    for (int g = 0; g < dim / 128; g++) m = fmaxf(m, red[g]);
+    const float top = m * inverse;
+    const float scale = top > 0.0f ? top / 127.0f : 1.0f;
+    const float round = 1.0f / scale;
+    if constexpr (HYPER) {
+        const int g4 = n / 128;
+        prepare_row_fake(s, n, 4, Act{a4v, a4s, a4s + g4}, 0, 0, inverse, round, scale);
+        __syncthreads();
+        for (int e = threadIdx.x; e < n / 16; e += kThreads)
+            reinterpret_cast<uint4*>(act.values + (size_t)t * n)[e] = reinterpret_cast<const uint4*>(a4v)[e];
+        if ((int)threadIdx.x < 2 * g4) {
+            const int g = (int)threadIdx.x % g4;
+            float* dst = (int)threadIdx.x < g4 ? act.scales : act.offsets;
+            dst[(size_t)t * stride + g] = a4s[threadIdx.x];
+        }
+        const float y = phi_outputs(h.phi, hunit, a4v, a4s, a4s + g4, n, kPhiFirst, hprod, kPhiBase);
+        float sv[kPer][kLanes];
+#pragma unroll
+        for (int q = 0; q < kPer; q++) {
+            const int c = col_of(q);
+            if (c < dim) {
+#pragma unroll
+                for (int l = 0; l < kLanes; l++) sv[q][l] = s[l * dim + c];
+            }
+        }
+        hyper_mix_row(h, t, y, hga, hgb, sv, hsn, hx, hsq, hpre, red, &inv_s);
+    } else {
+        prepare_row_fake(s, n, 4, act, stride, t, inverse, round, scale);
+    }
 }
 
 // ----------------------------------------------------------- engram --
@@ -1875,13 +1924,19 @@ int32_t enqueue_step(nhip_ctx* c, int rows, int heads, int k, bool argmax, bool 
         return !(e && e[0] == '0');
     }();
     const bool fuse_tail = tail_mix_enabled && sink_in_attention && c->tail_hyper_lds > 0;
-    hipLaunchKernelGGL(n3_embed_kernel, dim3(rows), dim3(kThreads), 0, s, c->embedding_raw, c->vocab, d,
-                       c->embedding_bits, c->book4, in(c, c->d_in, kInTokens), emb_scale_m1, cur, act4, stride4);
+    if (fuse_tail)  // the embedding launch also runs layer 0's mix
+        hipLaunchKernelGGL(n3_embed_kernel<true>, dim3(rows), dim3(kThreads), 0, s, c->embedding_raw, c->vocab, d,
+                           c->embedding_bits, c->book4, in(c, c->d_in, kInTokens), emb_scale_m1, cur, act4, stride4,
+                           hyper_args(0, cur));
+    else
+        hipLaunchKernelGGL(n3_embed_kernel<false>, dim3(rows), dim3(kThreads), 0, s, c->embedding_raw, c->vocab, d,
+                           c->embedding_bits, c->book4, in(c, c->d_in, kInTokens), emb_scale_m1, cur, act4, stride4,
+                           HyperArgs{});
     NHIP_CHECK_HIP(hipGetLastError());
     for (int l = 0; l < L; l++) {
         const N3Layer& w = c->layer[l];
         const N3Site* st = site_of(l);
-        if (!fuse_tail || l == 0) {  // otherwise layer l - 1's tail launch ran the mix
+        if (!fuse_tail) {  // otherwise the embedding's or layer l - 1's tail launch ran the mix
             const HyperArgs ha = hyper_args(l, cur);
             // the attention launch forms the residual-mix rows' Sinkhorn for
             // steps whose rows are one per slot; the mix launch otherwise
